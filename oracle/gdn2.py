@@ -1,0 +1,295 @@
+"""GDN2 (Gated DeltaNet-2) oracle: CPU restatement of the reference's WY forms.
+
+Test infrastructure only (see ``oracle/__init__.py``).
+
+Conventions (reference ``atomic_ops/gdn2_wy_reference.py``):
+  q, k, b, g : [B, T, H, K]      (b = per-channel erase gate "beta")
+  v, w       : [B, T, H, V]      (w = per-channel write gate)
+  h          : [B, H, K, V]      fp32 state
+  o          : [B, T, H, V]      returned in the compute dtype (fp32 in the
+                                  reference, ``gdn2_wy_reference.py:151``)
+
+All arithmetic runs in ``dtype`` (float64 by default).  Inputs that arrive in
+bfloat16 are upcast on entry exactly like the reference's ``.astype(f32)``
+(``gdn2_wy_reference.py:75-77``); the one product the reference forms in the
+input dtype before upcasting, ``w_c * v_c`` (``:94``), is formed the same way.
+"""
+from __future__ import annotations
+
+import torch
+
+CLIP_DECAY = 20.0
+CLIP_ACC = 1e4
+
+
+def n2n(x):
+    """``jnp.nan_to_num(x, nan=0, posinf=1e4, neginf=-1e4)`` (gdn2_wy_reference.py:86)."""
+    return torch.nan_to_num(x, nan=0.0, posinf=CLIP_ACC, neginf=-CLIP_ACC)
+
+
+def sanitize(x, c=CLIP_ACC):
+    """clip to [-c, c] then nan_to_num (gdn2_wy_reference.py:141)."""
+    return torch.nan_to_num(torch.clamp(x, -c, c), nan=0.0, posinf=c, neginf=-c)
+
+
+def wy_inverse(Akk):
+    """Row-wise forward substitution ``A[i] = e_i - Akk[i,:] @ A`` for a
+    strictly lower triangular ``Akk`` (gdn2_wy_reference.py:16-30).
+
+    Rows are built one at a time and stacked (no in-place writes) so torch
+    autograd can differentiate through it, as ``jax.vjp`` does through the
+    reference's ``lax.scan``."""
+    C = Akk.shape[-1]
+    eye = torch.eye(C, dtype=Akk.dtype, device=Akk.device)
+    rows = []
+    for i in range(C):
+        if i == 0:
+            rows.append(eye[0].expand(Akk.shape[:-2] + (C,)))
+            continue
+        prev = torch.stack(rows, dim=-2)                      # [..., i, C]
+        contrib = torch.einsum("...j,...jk->...k", Akk[..., i, :i], prev)
+        rows.append(eye[i] - contrib)
+    return torch.stack(rows, dim=-2)
+
+
+def build_chunk_wy(q_c, k_c, v_c, g_c, b_c, w_c, scale, dtype=torch.float64):
+    """Per-chunk WY build (gdn2_wy_reference.py:59-102).
+
+    Inputs are one chunk in [B, H, C, D] layout.  Returns a dict with
+    ``gc, Aqk, Akk, A, w_pseudo, u, kg, qg, gc_last`` (all ``dtype``)."""
+    f = dtype
+    C = q_c.shape[-2]
+    gc = torch.cumsum(g_c.to(f), dim=-2)                                  # :63
+    decay_diff = gc[..., :, None, :] - gc[..., None, :, :]               # :66
+    edecay = torch.exp(torch.clamp(decay_diff, -CLIP_DECAY, CLIP_DECAY))  # :70
+    causal = torch.tril(torch.ones(C, C, dtype=f))                        # :72
+    strict = torch.tril(torch.ones(C, C, dtype=f), diagonal=-1)          # :73
+    q = q_c.to(f)
+    k = k_c.to(f)
+    b = b_c.to(f)
+    Aqk = scale * torch.einsum("...id,...ijd,...jd->...ij", q, edecay, k) * causal   # :79
+    bk = b * k                                                            # :80
+    Akk = torch.einsum("...id,...ijd,...jd->...ij", bk, edecay, k) * strict         # :81
+    Aqk = n2n(Aqk)                                                        # :86
+    Akk = n2n(Akk)                                                        # :87
+    A = n2n(wy_inverse(Akk))                                              # :89-90
+    kb_decayed = bk * torch.exp(gc)                                       # :92
+    wv = (w_c * v_c).to(f)                                                # :94 (product in input dtype)
+    w_pseudo = n2n(A @ kb_decayed)                                        # :93,95
+    u = n2n(A @ wv)                                                       # :94,96
+    gc_last = gc[..., -1, :]                                              # :98
+    kg = k * torch.exp(gc_last[..., None, :] - gc)                        # :99
+    qg = q * torch.exp(gc)                                                # :100
+    return dict(gc=gc, Aqk=Aqk, Akk=Akk, A=A, w_pseudo=w_pseudo, u=u, kg=kg,
+                qg=qg, gc_last=gc_last, wv=wv, kb_decayed=kb_decayed)
+
+
+def _to_chunks(t, C):
+    """[B, T, H, D] -> [NT, B, H, C, D]."""
+    B, T, H, D = t.shape
+    return t.reshape(B, T // C, C, H, D).permute(1, 0, 3, 2, 4)
+
+
+def _from_chunks(t):
+    """[NT, B, H, C, D] -> [B, T, H, D]."""
+    NT, B, H, C, D = t.shape
+    return t.permute(1, 0, 3, 2, 4).reshape(B, NT * C, H, D)
+
+
+def gdn2_chunked_wy_reference(q, k, v, g, b, w, scale, chunk_size, h0=None,
+                              dtype=torch.float64, return_stages=False):
+    """Chunked WY forward (gdn2_wy_reference.py:105-152).
+
+    Argument order follows the reference function (``q,k,v,g,b,w``), not the
+    drop-in wrapper (``q,k,v,w,b,g``, kernel_trainable_B6.py:187)."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    C = chunk_size
+    assert T % C == 0, f"seq_len={T} must be divisible by chunk_size={C}"   # :109
+    f = dtype
+    ch = [_to_chunks(t, C) for t in (q, k, v, g, b, w)]                    # :120
+    h = torch.zeros(B, H, K, V, dtype=f) if h0 is None else h0.to(f)        # :122-123
+    outs, stages = [], []
+    for n in range(T // C):
+        st = build_chunk_wy(*(t[n] for t in ch), scale, dtype=f)            # :127
+        h_pre = h
+        wh = st["w_pseudo"] @ h_pre                                         # :129
+        v_new = st["u"] - wh                                                # :130
+        qh = st["qg"] @ h_pre                                               # :132
+        intra = st["Aqk"] @ v_new                                           # :134
+        o_c = scale * qh + intra                                            # :136
+        decay_h = torch.exp(st["gc_last"])[..., None]                       # :138
+        write = st["kg"].transpose(-1, -2) @ v_new                          # :139
+        h = sanitize(h_pre * decay_h + write)                               # :140-141
+        o_c = n2n(o_c)                                                      # :142
+        outs.append(o_c)
+        if return_stages:
+            st = dict(st, h_pre=h_pre, v_new=v_new, o=o_c)
+            stages.append(st)
+    o = _from_chunks(torch.stack(outs, 0))                                  # :151
+    if return_stages:
+        return o, h, stages
+    return o, h
+
+
+def gdn2_token_serial_reference(q, k, v, g, b, w, scale, h0=None, dtype=torch.float64):
+    """Token-serial recurrence (gdn2_wy_reference.py:33-56), an independent
+    oracle for the chunked form.  Returns o in ``dtype`` (the reference casts
+    to the input dtype at :55; the tests compare in float64)."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    f = dtype
+    alpha = torch.exp(g.to(f))                                               # :38
+    h = torch.zeros(B, H, K, V, dtype=f) if h0 is None else h0.to(f)
+    outs = []
+    for t in range(T):
+        h = h * alpha[:, t, :, :, None]                                      # :45
+        bk = (b[:, t] * k[:, t]).to(f)                                       # :46
+        erase = torch.einsum("bhd,bhdv->bhv", bk, h)                          # :47
+        v_new = (w[:, t] * v[:, t]).to(f) - erase                             # :48
+        h = h + torch.einsum("bhd,bhv->bhdv", k[:, t].to(f), v_new)           # :49
+        outs.append(torch.einsum("bhdv,bhd->bhv", h, (q[:, t] * scale).to(f)))  # :50
+    return torch.stack(outs, 1), h
+
+
+def final_sanitize(x):
+    """``_final_sanitize`` at the custom_vjp boundary (kernel_trainable_B6.py:64-66)."""
+    return sanitize(x, CLIP_ACC)
+
+
+def gdn2_backward_autodiff(q, k, v, w, b, g, scale, chunk_size, do, dh_final=None,
+                           h0=None, dtype=torch.float64):
+    """The GDN2 gradient as the reference defines it: ``jax.vjp`` of the
+    chunked WY reference followed by ``_final_sanitize``
+    (kernel_trainable.py:38-55; argument remap at :42-43).  Takes the
+    drop-in argument order ``q,k,v,w,b,g``.  Returns
+    ``(dq, dk, dv, dw, db, dg, dh0)`` in ``dtype``."""
+    f = dtype
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    leaves = [t.detach().to(f).requires_grad_(True) for t in (q, k, v, w, b, g)]
+    h0_ = torch.zeros(B, H, K, V, dtype=f) if h0 is None else h0.detach().to(f)
+    h0_.requires_grad_(True)
+    # The reference upcasts every input on entry; w*v is the one product it
+    # forms before the upcast.  For float64 leaves the two coincide.
+    qf, kf, vf, wf, bf, gf = leaves
+    o, h_fin = gdn2_chunked_wy_reference(qf, kf, vf, gf, bf, wf, scale, chunk_size,
+                                         h0=h0_, dtype=f)
+    dO = do.to(f)
+    dH = torch.zeros_like(h_fin) if dh_final is None else dh_final.to(f)
+    grads = torch.autograd.grad((o, h_fin), leaves + [h0_], (dO, dH), allow_unused=True)
+    grads = [torch.zeros_like(x) if gr is None else gr for gr, x in zip(grads, leaves + [h0_])]
+    return tuple(final_sanitize(gr) for gr in grads)
+
+
+def gdn2_backward_chain(q, k, v, w, b, g, scale, chunk_size, do, dh_final=None,
+                        h0=None, dtype=torch.float64):
+    """Hand restatement of the B2 -> B1 -> B3 -> B4 -> B5 chain
+    (kernel_trainable_B6.py:97-181) at chunk ``chunk_size``.
+
+    Independent of autograd: used to pin ``gdn2_backward_autodiff`` and to
+    give per-stage intermediates for kernel-level tests.  Returns the final
+    gradients ``(dq, dk, dv, dw, db, dg, dh0)`` and a dict of per-chunk
+    intermediates."""
+    f = dtype
+    C = chunk_size
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    NT = T // C
+    o, h_fin, st = gdn2_chunked_wy_reference(q, k, v, g, b, w, scale, C, h0=h0,
+                                             dtype=f, return_stages=True)
+    do_ch = _to_chunks(do.to(f), C)
+    qc, kc, vc, gc_in, bc, wc = (_to_chunks(t, C) for t in (q, k, v, g, b, w))
+    causal = torch.tril(torch.ones(C, C, dtype=f))
+    strict = torch.tril(torch.ones(C, C, dtype=f), diagonal=-1)
+
+    # B2 (kernel_bwd_b2_dav.py:61-73)
+    dAqk = [n2n((do_ch[n] @ st[n]["v_new"].transpose(-1, -2)) * causal) for n in range(NT)]
+    dv_partial = [n2n(st[n]["Aqk"].transpose(-1, -2) @ do_ch[n]) for n in range(NT)]
+
+    # B1 reverse scan (kernel_bwd_b1_dhu.py:14-44)
+    dh = torch.zeros(B, H, K, V, dtype=f) if dh_final is None else dh_final.to(f)
+    dh = sanitize(dh)                                                        # b1:18
+    dh_next = [None] * NT
+    dv_all = [None] * NT
+    for n in reversed(range(NT)):
+        s = st[n]
+        dh_next[n] = dh
+        decay = torch.exp(s["gc_last"])[..., None]                            # b1:24
+        from_out = s["qg"].transpose(-1, -2) @ (scale * do_ch[n])             # b1:26-27
+        dv_new = sanitize(dv_partial[n] + s["kg"] @ dh)                       # b1:30-32
+        from_vnew = -(s["w_pseudo"].transpose(-1, -2) @ dv_new)               # b1:34
+        dh = sanitize(from_out + dh * decay + from_vnew)                      # b1:36-37
+        dv_all[n] = dv_new
+    dh0 = dh
+
+    outs = {k_: [] for k_ in ("dq", "dk", "db", "dw", "dv", "dg")}
+    for n in range(NT):
+        s = st[n]
+        qf, kf, bf_, wf, vf = (t[n].to(f) for t in (qc, kc, bc, wc, vc))
+        gc = s["gc"]
+        gcl = s["gc_last"]
+        A = s["A"]
+        h_pre = s["h_pre"]
+        v_new = s["v_new"]
+        dO = do_ch[n]
+        dv = dv_all[n]
+        dhn = dh_next[n]
+        # B3 (kernel_bwd_b3_wy_dqkg.py:128-213)
+        egc = torch.exp(gc)
+        kb_dec = bf_ * kf * egc
+        kg = kf * torch.exp(gcl[..., None, :] - gc)
+        qg = qf * egc
+        wv = s["wv"]
+        dqg = (scale * dO) @ h_pre.transpose(-1, -2)
+        dw_pseudo = (-dv) @ h_pre.transpose(-1, -2)
+        dkg = v_new @ dhn.transpose(-1, -2)
+        dA_total = dw_pseudo @ kb_dec.transpose(-1, -2) + dv @ wv.transpose(-1, -2)
+        dkb = A.transpose(-1, -2) @ dw_pseudo
+        dwv = A.transpose(-1, -2) @ dv
+        dA_total = sanitize(dA_total)
+        tmp = sanitize(dA_total @ A.transpose(-1, -2))
+        dAkk = n2n(-(A.transpose(-1, -2) @ tmp) * strict)
+        dk3 = dkb * egc * bf_ + dkg * torch.exp(gcl[..., None, :] - gc)
+        db3 = dkb * egc * kf
+        dx = dkg * kg
+        dgc3 = dkb * kb_dec + dqg * qg - dx
+        dgc_last = dx.sum(-2) + torch.exp(gcl) * (dhn * h_pre).sum(-1)
+        dgc3 = dgc3.clone()
+        dgc3[..., -1, :] = dgc3[..., -1, :] + dgc_last
+        dq3 = dqg * egc
+        dw3 = dwv * vf
+        dv3 = dwv * wf
+        dq3, dk3, db3, dw3, dv3, dgc3 = map(n2n, (dq3, dk3, db3, dw3, dv3, dgc3))
+        # B4 (kernel_bwd_b4_intra.py:57-132), full chunk as one block
+        diff = gc[..., :, None, :] - gc[..., None, :, :]
+        clipmask = ((diff >= -CLIP_DECAY) & (diff <= CLIP_DECAY)).to(f)
+        E = torch.exp(torch.clamp(diff, -CLIP_DECAY, CLIP_DECAY))
+        dMqk = dAqk[n] * causal
+        dMkk = dAkk * strict
+        Lqk = scale * qf
+        bk = bf_ * kf
+        dL_qk = torch.einsum("...ij,...ijd,...jd->...id", dMqk, E, kf)
+        dR_qk = torch.einsum("...ij,...ijd,...id->...jd", dMqk, E, Lqk)
+        wq = dMqk[..., None] * Lqk[..., :, None, :] * kf[..., None, :, :] * E * clipmask
+        dL_kk = torch.einsum("...ij,...ijd,...jd->...id", dMkk, E, kf)
+        dR_kk = torch.einsum("...ij,...ijd,...id->...jd", dMkk, E, bk)
+        wk = dMkk[..., None] * bk[..., :, None, :] * kf[..., None, :, :] * E * clipmask
+        dgc4 = wq.sum(-2) - wq.sum(-3) + wk.sum(-2) - wk.sum(-3)
+        dq4 = sanitize(dL_qk * scale)
+        dk4 = sanitize(dR_qk + dR_kk + dL_kk * bf_)
+        db4 = sanitize(dL_kk * kf)
+        dgc4 = sanitize(dgc4)
+        # combine + B5 reverse cumsum (kernel_bwd_b5_reverse_cumsum.py:17-24)
+        dgc_total = dgc3 + dgc4
+        dg = sanitize(torch.flip(torch.cumsum(torch.flip(dgc_total, [-2]), -2), [-2]))
+        outs["dq"].append(dq3 + dq4)
+        outs["dk"].append(dk3 + dk4)
+        outs["db"].append(db3 + db4)
+        outs["dw"].append(dw3)
+        outs["dv"].append(dv3)
+        outs["dg"].append(dg)
+    res = {k_: final_sanitize(_from_chunks(torch.stack(vv, 0))) for k_, vv in outs.items()}
+    inter = dict(dAqk=dAqk, dv_partial=dv_partial, dh_next=dh_next, dv_new=dv_all, stages=st)
+    return (res["dq"], res["dk"], res["dv"], res["dw"], res["db"], res["dg"],
+            final_sanitize(dh0)), inter

@@ -1,0 +1,227 @@
+"""Mamba2 SSD chunk-scan oracle: CPU restatement of the reference.
+
+Test infrastructure only (see ``oracle/__init__.py``).
+
+Conventions (reference ``atomic_ops/mamba2_ssd_reference.py:152-179``):
+  dt, x : [B, T, H, P]   (dt is per head *and* channel, model.py:427,471)
+  A     : [H]            (negative log-decay rate per unit dt)
+  Bm, Cm: [B, T, N]      (shared by every head, ngroups = 1)
+  state : [B, H, P, N]   fp32 carry
+  y     : [B, T, H, P]   fp32 (mamba2_ssd_reference.py:148,178)
+There is no ``D * x`` skip term in the reference (it takes no D argument,
+mamba2_ssd_reference.py:152).
+"""
+from __future__ import annotations
+
+import torch
+
+CLIP_STEP = 20.0
+CLIP_ACC = 1e4
+
+
+def sanitize(x, c=CLIP_ACC):
+    """``_sanitize`` (mamba2_ssd_reference.py:66-67)."""
+    return torch.nan_to_num(torch.clamp(x, -c, c), nan=0.0, posinf=c, neginf=-c)
+
+
+def clip_mask(x, lo, hi):
+    """Straight-through mask of ``clip`` (mamba2_bwd_reference.py:48-52)."""
+    return ((x >= lo) & (x <= hi)).to(x.dtype)
+
+
+def chunk_ssd(dt_c, A, B_c, C_c, x_c, state_prev, dtype=torch.float64):
+    """One chunk of the SSD forward (mamba2_ssd_reference.py:70-149).
+
+    Layout: dt_c, x_c [b, C, h, p]; B_c, C_c [b, C, n]; state_prev [b, h, p, n].
+    Returns ``(y_c, state_new, parts)``; ``parts`` holds the intermediates
+    the kernel-level tests check (cumdecay, y_diag, state_end, y_off)."""
+    f = dtype
+    Cs = dt_c.shape[1]
+    dA_exponent = sanitize(torch.einsum("bchd,h->bchd", dt_c.to(f), A.to(f)), CLIP_STEP)  # :85-86
+    idx = torch.arange(Cs)
+    tril_ones = (idx[:, None] >= idx[None, :]).to(f)
+    cumdecay = torch.einsum("ij,bjhd->bihd", tril_ones, dA_exponent)                 # :98-100
+    cumdecay = sanitize(cumdecay, CLIP_ACC)                                           # :115
+    decay_diff = cumdecay[:, :, None] - cumdecay[:, None, :]                          # :117
+    causal = (idx[:, None] >= idx[None, :]).to(f)[None, :, :, None, None]             # :118
+    L = torch.exp(torch.clamp(decay_diff, -CLIP_STEP, CLIP_STEP)) * causal            # :119
+    L = sanitize(L, 1e6)                                                              # :120
+    BC_inner = sanitize(torch.einsum("bis,bjs->bij", C_c.to(f), B_c.to(f)))         # :122-123
+    dBx = sanitize(dt_c.to(f) * x_c.to(f))                                            # :125-126
+    weight = L * BC_inner[:, :, :, None, None]                                        # :129
+    y_diag = sanitize(torch.einsum("bijhd,bjhd->bihd", weight, dBx))                  # :130-131
+    decay_to_end = torch.exp(torch.clamp(cumdecay[:, -1:] - cumdecay, -CLIP_STEP, CLIP_STEP))  # :133
+    decay_to_end = sanitize(decay_to_end, 1e6)                                        # :134
+    write = dBx * decay_to_end                                                        # :135
+    state_end = sanitize(torch.einsum("bcs,bchd->bhds", B_c.to(f), write))            # :136-137
+    decay_h = torch.exp(torch.clamp(cumdecay, -CLIP_STEP, 0.0))                       # :139
+    y_off = sanitize(torch.einsum("bis,bhds->bihd", C_c.to(f), state_prev) * decay_h)  # :140-142
+    decay_chunk_end = torch.exp(torch.clamp(cumdecay[:, -1], -CLIP_STEP, 0.0))        # :144
+    state_new = sanitize(state_prev * decay_chunk_end[..., None] + state_end)         # :145-146
+    y_c = sanitize(y_diag + y_off)                                                    # :148
+    parts = dict(cumdecay=cumdecay, y_diag=y_diag, state_end=state_end, y_off=y_off,
+                 CB=BC_inner)
+    return y_c, state_new, parts
+
+
+def _to_chunks(t, C):
+    """[b, l, ...] -> [n_chunks, b, C, ...] (mamba2_ssd_reference.py:161-164)."""
+    b, l = t.shape[:2]
+    return t.reshape(b, l // C, C, *t.shape[2:]).transpose(0, 1)
+
+
+def _from_chunks(t):
+    """[n_chunks, b, C, ...] -> [b, l, ...] (mamba2_bwd_reference.py:249-257)."""
+    t = t.transpose(0, 1)
+    return t.reshape(t.shape[0], t.shape[1] * t.shape[2], *t.shape[3:])
+
+
+def mamba2_ssd_reference(dt, A, Bm, Cm, x, chunk_size, state0=None, dtype=torch.float64,
+                         return_parts=False):
+    """Chunked SSD forward (mamba2_ssd_reference.py:152-179).  Argument
+    order follows the reference function ``(dt, A, B, C, x, ...)``."""
+    f = dtype
+    b, l, h, p = dt.shape
+    n = Bm.shape[-1]
+    assert l % chunk_size == 0                                                        # :158
+    state = torch.zeros(b, h, p, n, dtype=f) if state0 is None else state0.to(f)     # :168-169
+    dtc, Bc, Cc, xc = (_to_chunks(t, chunk_size) for t in (dt, Bm, Cm, x))
+    ys, parts = [], []
+    for c in range(l // chunk_size):
+        y_c, state, pr = chunk_ssd(dtc[c], A, Bc[c], Cc[c], xc[c], state, dtype=f)
+        ys.append(y_c)
+        parts.append(pr)
+    y = _from_chunks(torch.stack(ys, 0))
+    if return_parts:
+        return y, state, parts
+    return y, state
+
+
+def mamba2_token_serial(dt, A, Bm, Cm, x, state0=None, dtype=torch.float64):
+    """Token-serial SSM ``s_t = exp(dt_t A) s_{t-1} + (dt_t x_t) B_t^T``,
+    ``y_t = s_t C_t`` -- the recurrence the chunked form decomposes
+    (mamba2_ssd_reference.py:14-29).  No clipping, so it agrees with the
+    chunked form only while no clip fires."""
+    f = dtype
+    b, l, h, p = dt.shape
+    n = Bm.shape[-1]
+    s = torch.zeros(b, h, p, n, dtype=f) if state0 is None else state0.to(f)
+    ys = []
+    for t in range(l):
+        dtt = dt[:, t].to(f)
+        decay = torch.exp(dtt * A.to(f)[None, :, None])
+        s = s * decay[..., None] + (dtt * x[:, t].to(f))[..., None] * Bm[:, t].to(f)[:, None, None, :]
+        ys.append(torch.einsum("bhpn,bn->bhp", s, Cm[:, t].to(f)))
+    return torch.stack(ys, 1), s
+
+
+def chunk_ssd_bwd(dt_c, A, B_c, C_c, x_c, state_prev, dy_c, dstate_new, dtype=torch.float64):
+    """Hand-derived backward of one chunk: MB0 ``_chunk_ssd_bwd``
+    (mamba2_bwd_reference.py:55-197).  Returns
+    ``(ddt_c, dB_c, dC_c, dx_c, dA, dstate_prev, dcum_total)``; the last one
+    (the combined cumdecay cotangent after the last-row terms) is exposed for
+    kernel-level tests."""
+    f = dtype
+    dt_c, B_c, C_c, x_c, state_prev = (t.to(f) for t in (dt_c, B_c, C_c, x_c, state_prev))
+    dy_c = dy_c.to(f)
+    dstate_new = dstate_new.to(f)
+    A = A.to(f)
+    Cs = dt_c.shape[1]
+    # forward re-run (:76-108)
+    dA_exponent_raw = torch.einsum("bchd,h->bchd", dt_c, A)
+    dA_exponent = sanitize(dA_exponent_raw, CLIP_STEP)
+    idx = torch.arange(Cs)
+    tril_ones = (idx[:, None] >= idx[None, :]).to(f)
+    cumdecay_raw = torch.einsum("ij,bjhd->bihd", tril_ones, dA_exponent)
+    cumdecay = sanitize(cumdecay_raw, CLIP_ACC)
+    decay_diff_raw = cumdecay[:, :, None] - cumdecay[:, None, :]
+    causal = (idx[:, None] >= idx[None, :]).to(f)[None, :, :, None, None]
+    L = sanitize(torch.exp(torch.clamp(decay_diff_raw, -CLIP_STEP, CLIP_STEP)) * causal, 1e6)
+    BC_inner = sanitize(torch.einsum("bis,bjs->bij", C_c, B_c))
+    dBx = sanitize(dt_c * x_c)
+    weight = L * BC_inner[:, :, :, None, None]
+    decay_to_end_raw = cumdecay[:, -1:] - cumdecay
+    decay_to_end = sanitize(torch.exp(torch.clamp(decay_to_end_raw, -CLIP_STEP, CLIP_STEP)), 1e6)
+    write = sanitize(dBx * decay_to_end)
+    decay_h = torch.exp(torch.clamp(cumdecay, -CLIP_STEP, 0.0))
+    y_off_raw = torch.einsum("bis,bhds->bihd", C_c, state_prev)
+    decay_chunk_end = torch.exp(torch.clamp(cumdecay[:, -1], -CLIP_STEP, 0.0))
+    # reverse pass (:111-197)
+    dy_diag = dy_c
+    dy_off = dy_c
+    dstate_prev = dstate_new * decay_chunk_end[..., None]                              # :115
+    d_decay_chunk_end = (dstate_new * state_prev).sum(-1)                              # :116
+    dstate_end = dstate_new
+    d_cum_last_a = d_decay_chunk_end * decay_chunk_end * clip_mask(cumdecay[:, -1], -CLIP_STEP, 0.0)  # :120
+    dy_off_raw = dy_off * decay_h                                                      # :123
+    d_decay_h = dy_off * y_off_raw                                                     # :126
+    dC_1 = torch.einsum("bihd,bhds->bis", dy_off_raw, state_prev)                      # :127
+    dstate_prev = dstate_prev + torch.einsum("bihd,bis->bhds", dy_off_raw, C_c)        # :128
+    d_cum_from_yoff = d_decay_h * decay_h * clip_mask(cumdecay, -CLIP_STEP, 0.0)       # :131
+    dwrite = torch.einsum("bhds,bcs->bchd", dstate_end, B_c)                           # :134
+    dB_1 = torch.einsum("bhds,bchd->bcs", dstate_end, write)                           # :135
+    d_dBx_1 = dwrite * decay_to_end                                                    # :138
+    d_decay_to_end = dwrite * dBx                                                      # :139
+    d_dte_diff = d_decay_to_end * decay_to_end * clip_mask(decay_to_end_raw, -CLIP_STEP, CLIP_STEP)  # :142
+    d_cum_last_b = d_dte_diff.sum(1)                                                   # :143
+    d_cum_from_dte = -d_dte_diff                                                       # :144
+    dweight = torch.einsum("bihd,bjhd->bijhd", dy_diag, dBx)                           # :147
+    d_dBx_2 = torch.einsum("bijhd,bihd->bjhd", weight, dy_diag)                        # :148
+    dL = dweight * BC_inner[:, :, :, None, None]                                       # :151
+    dBC_inner = (dweight * L).sum((-2, -1))                                            # :152
+    dC_2 = torch.einsum("bij,bjs->bis", dBC_inner, B_c)                                # :155
+    dB_2 = torch.einsum("bij,bis->bjs", dBC_inner, C_c)                                # :156
+    d_decay_diff = dL * L * clip_mask(decay_diff_raw, -CLIP_STEP, CLIP_STEP)           # :159
+    d_cum_i = d_decay_diff.sum(2)                                                      # :162
+    d_cum_j = -d_decay_diff.sum(1)                                                     # :163
+    d_dBx_total = sanitize(d_dBx_1 + d_dBx_2)                                          # :166
+    ddt_1 = d_dBx_total * x_c                                                          # :167
+    dx_c = d_dBx_total * dt_c                                                          # :168
+    d_cum_total = sanitize(d_cum_i + d_cum_j + d_cum_from_yoff + d_cum_from_dte)       # :171-173
+    row_mask = (idx == (Cs - 1)).to(f)[None, :, None, None]                            # :176
+    d_cum_total = d_cum_total + row_mask * (d_cum_last_a + d_cum_last_b)[:, None]      # :177
+    d_cum_total = d_cum_total * clip_mask(cumdecay_raw, -CLIP_ACC, CLIP_ACC)           # :181
+    triu_ones = (idx[:, None] <= idx[None, :]).to(f)
+    d_dA_exp = torch.einsum("ij,bjhd->bihd", triu_ones, d_cum_total)                   # :183
+    d_dA_exp = d_dA_exp * clip_mask(dA_exponent_raw, -CLIP_STEP, CLIP_STEP)            # :186
+    ddt_2 = torch.einsum("bchd,h->bchd", d_dA_exp, A)                                  # :187
+    dA = (d_dA_exp * dt_c).sum((0, 1, 3))                                              # :188
+    ddt_c = sanitize(ddt_1 + ddt_2)                                                    # :190
+    dB_c = sanitize(dB_1 + dB_2)                                                       # :191
+    dC_c = sanitize(dC_1 + dC_2)                                                       # :192
+    dx_c = sanitize(dx_c)                                                              # :193
+    dA = sanitize(dA)                                                                  # :194
+    dstate_prev = sanitize(dstate_prev)                                                # :195
+    return ddt_c, dB_c, dC_c, dx_c, dA, dstate_prev, d_cum_total
+
+
+def chunk_ssd_bwd_scan(dt, A, Bm, Cm, x, chunk_size, do, dstate_final=None, state0=None,
+                       dtype=torch.float64):
+    """Full-sequence MB0 backward (mamba2_bwd_reference.py:200-266): forward
+    re-run for ``state_prev`` per chunk, then a reverse scan.  Returns
+    ``(ddt, dB, dC, dx, dA, dstate0)``."""
+    f = dtype
+    b, l, h, p = dt.shape
+    n = Bm.shape[-1]
+    state = torch.zeros(b, h, p, n, dtype=f) if state0 is None else state0.to(f)
+    dtc, Bc, Cc, xc, doc = (_to_chunks(t, chunk_size) for t in (dt, Bm, Cm, x, do))
+    nc = l // chunk_size
+    prevs = []
+    for c in range(nc):                                                               # :229-234
+        prevs.append(state)
+        _, state, _ = chunk_ssd(dtc[c], A, Bc[c], Cc[c], xc[c], state, dtype=f)
+    dstate = torch.zeros(b, h, p, n, dtype=f) if dstate_final is None else dstate_final.to(f)
+    outs = [None] * nc
+    dA = torch.zeros(h, dtype=f)
+    for c in reversed(range(nc)):                                                     # :236-247
+        ddt_c, dB_c, dC_c, dx_c, dA_c, dstate, _ = chunk_ssd_bwd(
+            dtc[c], A, Bc[c], Cc[c], xc[c], prevs[c], doc[c], dstate, dtype=f)
+        outs[c] = (ddt_c, dB_c, dC_c, dx_c)
+        dA = dA + dA_c                                                                # :263
+    ddt, dB, dC, dx = (_from_chunks(torch.stack([o[i] for o in outs], 0)) for i in range(4))
+    return ddt, dB, dC, dx, dA, sanitize(dstate)                                      # :264
+
+
+def final_sanitize(x):
+    """``_final_sanitize`` at the custom_vjp boundary (kernel_mamba2_trainable_B6.py:67-69)."""
+    return sanitize(x, CLIP_ACC)
