@@ -1,0 +1,143 @@
+"""PyTorch host side of the GDN2 WY chunk pipeline (device memory and streams
+come from torch; every computation runs in libatomic_hybrid.so).
+
+Layouts follow the reference (``atomic_ops/kernel_trainable_B6.py:187``):
+q, k, b, g: [B, T, H, K]; v, w: [B, T, H, V]; h0 / h_final: [B, H, K, V];
+o: [B, T, H, V] float32.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+CHUNK = 64
+
+_DT = {torch.float32: _lib.ATOMIC_F32, torch.bfloat16: _lib.ATOMIC_BF16}
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _check_inputs(q, k, v, w, b, g):
+    if not q.is_cuda:
+        raise ValueError("GDN2 inputs must be HIP device tensors")
+    if q.dtype not in _DT:
+        raise TypeError(f"unsupported dtype {q.dtype}")
+    for name, t in (("k", k), ("b", b)):
+        if t.shape != q.shape or t.dtype != q.dtype:
+            raise ValueError(f"{name} must match q in shape and dtype")
+    for name, t in (("v", v), ("w", w)):
+        if t.shape[:3] != q.shape[:3] or t.dtype != q.dtype:
+            raise ValueError(f"{name} must be [B,T,H,V] with q's dtype")
+    if g.shape != q.shape or g.dtype != torch.float32:
+        raise ValueError("g must be float32 with q's shape")
+
+
+def make_args(q, v, scale, *, do_dtype=None, flags=0, chunk=CHUNK):
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if T % chunk != 0:
+        # same constraint the reference asserts (gdn2_wy_reference.py:109-112)
+        raise ValueError(f"seq_len={T} must be divisible by chunk_size={chunk}")
+    return _lib.Gdn2Args(B, T, H, K, V, chunk, _DT[q.dtype],
+                         _DT[do_dtype if do_dtype is not None else q.dtype], float(scale), flags)
+
+
+def workspace_bytes(args):
+    lib = _lib.load()
+    n = lib.atomic_gdn2_workspace_size(ctypes.byref(args))
+    if n == 0:
+        raise _lib.AtomicError("atomic_gdn2_workspace_size: unsupported shape")
+    return n
+
+
+def new_workspace(args, device):
+    return torch.empty(workspace_bytes(args), dtype=torch.uint8, device=device)
+
+
+def workspace_layout(args):
+    lib = _lib.load()
+    lay = _lib.Gdn2Layout()
+    _lib.check(lib.atomic_gdn2_workspace_layout(ctypes.byref(args), ctypes.byref(lay)),
+               "atomic_gdn2_workspace_layout")
+    return lay
+
+
+def forward(q, k, v, w, b, g, scale, h0=None, *, save=False, workspace=None, chunk=CHUNK):
+    """Returns ``(o, h_final, workspace)``.  With ``save`` the workspace keeps
+    the per-chunk intermediates for :func:`backward`."""
+    _check_inputs(q, k, v, w, b, g)
+    lib = _lib.load()
+    q, k, v, w, b, g = (t.contiguous() for t in (q, k, v, w, b, g))
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    args = make_args(q, v, scale, flags=_lib.GDN2_SAVE if save else 0, chunk=chunk)
+    if workspace is None:
+        workspace = new_workspace(args, q.device)
+    if h0 is not None:
+        h0 = h0.to(torch.float32).contiguous()
+    o = torch.empty(B, T, H, V, dtype=torch.float32, device=q.device)
+    h_final = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
+    rc = lib.atomic_gdn2_fwd(ctypes.byref(args), _ptr(q), _ptr(k), _ptr(v), _ptr(w), _ptr(b), _ptr(g),
+                             _ptr(h0), _ptr(o), _ptr(h_final), _ptr(workspace),
+                             ctypes.c_size_t(workspace.numel()), _stream(q.device))
+    _lib.check(rc, "atomic_gdn2_fwd")
+    return o, h_final, workspace
+
+
+def backward(q, k, v, w, b, g, scale, dO, dh_final=None, h0=None, *, workspace=None, reuse=False,
+             chunk=CHUNK):
+    """Gradients ``(dq, dk, dv, dw, db, dg, dh0)`` in the primals' dtypes
+    (dg and dh0 float32).  ``reuse`` declares that ``workspace`` holds the
+    intermediates of a ``forward(..., save=True)`` on the same inputs."""
+    _check_inputs(q, k, v, w, b, g)
+    lib = _lib.load()
+    q, k, v, w, b, g = (t.contiguous() for t in (q, k, v, w, b, g))
+    dO = dO.contiguous()
+    if dO.dtype not in _DT:
+        dO = dO.to(torch.float32)
+    args = make_args(q, v, scale, do_dtype=dO.dtype, flags=_lib.GDN2_REUSE if reuse else 0, chunk=chunk)
+    if workspace is None:
+        workspace = new_workspace(args, q.device)
+    if h0 is not None:
+        h0 = h0.to(torch.float32).contiguous()
+    if dh_final is not None:
+        dh_final = dh_final.to(torch.float32).contiguous()
+    B, T, H, K = q.shape
+    dq, dk, db = (torch.empty_like(q) for _ in range(3))
+    dv, dw = torch.empty_like(v), torch.empty_like(w)
+    dg = torch.empty_like(g)
+    dh0 = torch.empty(B, H, K, v.shape[-1], dtype=torch.float32, device=q.device)
+    rc = lib.atomic_gdn2_bwd(ctypes.byref(args), _ptr(q), _ptr(k), _ptr(v), _ptr(w), _ptr(b), _ptr(g),
+                             _ptr(h0), _ptr(dO), _ptr(dh_final), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dw),
+                             _ptr(db), _ptr(dg), _ptr(dh0), _ptr(workspace),
+                             ctypes.c_size_t(workspace.numel()), _stream(q.device))
+    _lib.check(rc, "atomic_gdn2_bwd")
+    return dq, dk, dv, dw, db, dg, dh0
+
+
+def chunk_views(workspace, args):
+    """Per-chunk intermediates inside ``workspace`` as tensors
+    ``[B, H, NT, rows, cols]`` (for stage-level tests)."""
+    lay = workspace_layout(args)
+    B, H, C, K, V = args.batch, args.heads, args.chunk, args.dk, args.dv
+    NT = args.seqlen // C
+    dt = torch.bfloat16 if args.dtype == _lib.ATOMIC_BF16 else torch.float32
+    es = 2 if dt == torch.bfloat16 else 4
+
+    def view(off, rows, cols, dtype=dt, esz=es):
+        n = B * H * NT * rows * cols
+        return workspace[off:off + n * esz].view(dtype).view(B, H, NT, rows, cols)
+
+    return dict(qg=view(lay.qg, C, K), kg=view(lay.kg, C, K), w_pseudo=view(lay.w_pseudo, C, K),
+                u=view(lay.u, C, V), aqk=view(lay.aqk, C, C), ainv=view(lay.ainv, C, C),
+                gc_last=view(lay.gc_last, 1, K, torch.float32, 4)[..., 0, :],
+                h_pre_t=view(lay.h_pre_t, V, K), v_new_t=view(lay.v_new_t, V, C))

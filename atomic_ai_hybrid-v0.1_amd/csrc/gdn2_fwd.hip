@@ -1,0 +1,531 @@
+// GDN2 WY chunked forward for gfx950.
+//
+// gdn2_fwd_intra  (one workgroup per (batch, head, chunk); fully parallel)
+//   Follows _build_chunk_wy (atomic_ops/gdn2_wy_reference.py:59-102):
+//   gc = cumsum(g); Aqk / Akk intra-chunk scores; A = (I + Akk)^-1;
+//   w_pseudo = A (b k e^gc); u = A (w v); kg, qg; gc_last.
+//   The pairwise decay exp(gc_i - gc_j) is factorised as
+//   (q e^{gc_i}) . (k e^{-gc_j}) so both score matrices are bf16 MFMA GEMMs.
+//   The factorisation is exact while every g <= 0 in the chunk (then
+//   gc_i - gc_j <= 0 on causal pairs, so the reference's +20 clip never
+//   fires) and -gc_last <= kFactorLimit (so k e^{-gc} stays finite).  Pairs
+//   whose decay falls below the reference's -20 floor then carry their true
+//   (smaller) weight instead of e^-20, a difference below 2e-9 |q||k|.  Any
+//   chunk outside those bounds takes an exact pairwise path that applies
+//   exp(clip(gc_i - gc_j, -20, 20)) as the reference does.
+//
+// gdn2_fwd_state  (one workgroup per (batch, head, V tile); sequential over
+//   chunks).  Follows the scan step of gdn2_chunked_wy_reference
+//   (gdn2_wy_reference.py:125-144) / gdn2_inter_chunk_combine
+//   (kernel_d_pipeline.py:94-124): v_new = u - w_pseudo h;
+//   o = scale qg h + Aqk v_new; h = sanitize(h e^{gc_last} + kg^T v_new).
+//   The fp32 state lives in MFMA accumulators for the whole sequence.
+#include "gdn2.hpp"
+
+namespace ah {
+
+constexpr float kFactorLimit = 64.f;
+
+// ------------------------------------------------------------------ layout
+template <typename T, int C, int K, int V>
+struct IntraLds {
+  static constexpr int PAD = Pad<T>::v;
+  static constexpr int LK = K + PAD, LV = V + PAD;
+  static constexpr int LA = C + 4;                 // fp32 score / inverse rows
+  static constexpr int LAB = C + PAD;              // operand-type inverse rows
+  static constexpr int NCG = K / 8, NSEG = 256 / NCG, RS = C / NSEG;
+  static constexpr int NCGV = V / 8, NSEGV = 256 / NCGV, RSV = C / NSEGV;
+  static constexpr int OPK = C * LK * (int)sizeof(T);
+  static constexpr int OPV = C * LV * (int)sizeof(T);
+  static constexpr int AF = C * LA * 4;
+  static constexpr int off_q = 0, off_k = OPK, off_b = 2 * OPK, off_w = 3 * OPK;
+  static constexpr int end_ops = 3 * OPK + OPV;
+  static constexpr bool alias_a = 2 * OPK >= 2 * AF;
+  static constexpr int off_af = alias_a ? 0 : end_ops;      // Akk (then operand-type A)
+  static constexpr int off_x = off_af + AF;                 // fp32 inverse
+  static constexpr int end_a = off_x + AF;
+  static constexpr int off_tot = (end_ops > end_a ? end_ops : end_a);
+  static constexpr int TOT = NSEG * K * 4;                  // cumsum segment totals; solve scratch
+  static constexpr int off_gl = off_tot + (TOT > 4 * 16 * 17 * 4 ? TOT : 4 * 16 * 17 * 4);
+  static constexpr int off_flag = off_gl + K * 4;
+  static constexpr int total = off_flag + 16;
+  static_assert(RS >= 1 && RSV >= 1, "chunk too small for the thread mapping");
+  static_assert(2 * OPK >= C * K * 4, "gc scratch of the exact path must fit in sQ+sK");
+};
+
+// Exact pairwise scores for one chunk (reference form, used when the
+// factorised form could overflow or a positive gate breaks monotonicity).
+template <typename T, int C, int K>
+__device__ void intra_scores_exact(const float* sgc, const T* q, const T* k, const T* b,
+                                   size_t row_stride, float scale, float* out_qk, float* out_kk) {
+  // thread t computes entries e = t, t + 256, ... of the C x C matrices
+  for (int e = threadIdx.x, s = 0; e < C * C; e += 256, ++s) {
+    const int i = e / C, j = e % C;
+    float aqk = 0.f, akk = 0.f;
+    if (j <= i) {
+      const T* qi = q + i * row_stride;
+      const T* ki = k + i * row_stride;
+      const T* bi = b + i * row_stride;
+      const T* kj = k + j * row_stride;
+      for (int d = 0; d < K; ++d) {
+        const float dd = sgc[i * K + d] - sgc[j * K + d];
+        const float ed = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
+        const float kjd = to_f(kj[d]);
+        aqk += to_f(qi[d]) * ed * kjd;
+        akk += to_f(bi[d]) * to_f(ki[d]) * ed * kjd;
+      }
+      aqk *= scale;
+      if (j == i) akk = 0.f;
+    }
+    out_qk[s] = n2n(aqk);
+    out_kk[s] = n2n(akk);
+  }
+}
+
+template <typename T, int C, int K, int V>
+__global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __restrict__ q,
+                                                     const T* __restrict__ k, const T* __restrict__ v,
+                                                     const T* __restrict__ w, const T* __restrict__ b,
+                                                     const float* __restrict__ g, Gdn2Chunks<T> ck) {
+  typedef IntraLds<T, C, K, V> L;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
+  T* sQ = reinterpret_cast<T*>(lds + L::off_q);
+  T* sK = reinterpret_cast<T*>(lds + L::off_k);
+  T* sB = reinterpret_cast<T*>(lds + L::off_b);
+  T* sW = reinterpret_cast<T*>(lds + L::off_w);
+  float* sAf = reinterpret_cast<float*>(lds + L::off_af);
+  float* sX = reinterpret_cast<float*>(lds + L::off_x);
+  float* sTot = reinterpret_cast<float*>(lds + L::off_tot);
+  float* sGl = reinterpret_cast<float*>(lds + L::off_gl);
+  float* sGcExact = reinterpret_cast<float*>(lds + L::off_q);  // exact path only
+
+  const int tid = threadIdx.x;
+  const int bhn = blockIdx.x;
+  const int n = bhn % dm.NT;
+  const int bh = bhn / dm.NT;
+  const int h = bh % dm.H;
+  const int bb = bh / dm.H;
+  const size_t rsK = (size_t)dm.H * K;  // row stride of [B,T,H,K]
+  const size_t rsV = (size_t)dm.H * V;
+  const size_t t0 = (size_t)bb * dm.T + (size_t)n * C;
+  const T* qc = q + (t0 * dm.H + h) * K;
+  const T* kc = k + (t0 * dm.H + h) * K;
+  const T* bc = b + (t0 * dm.H + h) * K;
+  const float* gc_in = g + (t0 * dm.H + h) * K;
+  const T* vc = v + (t0 * dm.H + h) * V;
+  const T* wc = w + (t0 * dm.H + h) * V;
+
+  // ---- phase 0: gc = cumsum(g) over the chunk (gdn2_wy_reference.py:63)
+  const int cg = tid % L::NCG, seg = tid / L::NCG;
+  float gcr[L::RS][8];
+  bool positive = false;
+#pragma unroll
+  for (int rr = 0; rr < L::RS; ++rr) {
+    load8(gc_in + (size_t)(seg * L::RS + rr) * rsK + cg * 8, gcr[rr]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) positive |= gcr[rr][j] > 0.f;
+  }
+#pragma unroll
+  for (int rr = 1; rr < L::RS; ++rr)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) gcr[rr][j] += gcr[rr - 1][j];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sTot[seg * K + cg * 8 + j] = gcr[L::RS - 1][j];
+  __syncthreads();
+  {
+    float off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) off[j] = 0.f;
+    for (int s = 0; s < seg; ++s)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) off[j] += sTot[s * K + cg * 8 + j];
+#pragma unroll
+    for (int rr = 0; rr < L::RS; ++rr)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) gcr[rr][j] += off[j];
+  }
+  bool too_deep = false;
+  if (seg == L::NSEG - 1) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      sGl[cg * 8 + j] = gcr[L::RS - 1][j];
+      too_deep |= gcr[L::RS - 1][j] < -kFactorLimit;
+    }
+  }
+  const bool exact = __syncthreads_or(positive || too_deep);
+  if (tid < K) ck.gcl[(size_t)bhn * K + tid] = sGl[tid];
+
+  // ---- phase 1: elementwise operands (gdn2_wy_reference.py:92-100)
+  T* g_qg = ck.qg + (size_t)bhn * C * K;
+  T* g_kg = ck.kg + (size_t)bhn * C * K;
+#pragma unroll
+  for (int rr = 0; rr < L::RS; ++rr) {
+    const int r = seg * L::RS + rr;
+    float qv[8], kv[8], bv[8], o_qg[8], o_kt[8], o_kb[8], o_kg[8];
+    load8(qc + (size_t)r * rsK + cg * 8, qv);
+    load8(kc + (size_t)r * rsK + cg * 8, kv);
+    load8(bc + (size_t)r * rsK + cg * 8, bv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float gcv = gcr[rr][j];
+      const float e = __expf(gcv);
+      o_qg[j] = qv[j] * e;
+      o_kt[j] = kv[j] * __expf(-gcv);
+      o_kb[j] = (bv[j] * kv[j]) * e;
+      o_kg[j] = kv[j] * __expf(sGl[cg * 8 + j] - gcv);
+    }
+    store8(g_qg + r * K + cg * 8, o_qg);
+    store8(g_kg + r * K + cg * 8, o_kg);
+    store8(sB + r * L::LK + cg * 8, o_kb);
+    if (!exact) {
+      store8(sQ + r * L::LK + cg * 8, o_qg);
+      store8(sK + r * L::LK + cg * 8, o_kt);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sGcExact[r * K + cg * 8 + j] = gcr[rr][j];
+    }
+  }
+  {
+    const int cgv = tid % L::NCGV, segv = tid / L::NCGV;
+#pragma unroll
+    for (int rr = 0; rr < L::RSV; ++rr) {
+      const int r = segv * L::RSV + rr;
+      float vv[8], wv[8];
+      load8(vc + (size_t)r * rsV + cgv * 8, vv);
+      load8(wc + (size_t)r * rsV + cgv * 8, wv);
+      // w * v is formed in the input dtype before the upcast (gdn2_wy_reference.py:94)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) wv[j] = to_f(from_f<T>(wv[j] * vv[j]));
+      store8(sW + r * L::LV + cgv * 8, wv);
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 2: Aqk (causal, scaled) and Akk (strict) (gdn2_wy_reference.py:79-87)
+  constexpr int NB = C / 16;
+  constexpr int NTRI = NB * (NB + 1) / 2;
+  T* g_aqk = ck.aqk + (size_t)bhn * C * C;
+  const int wv_id = wave_id();
+  if (!exact) {
+    constexpr int JPW = (2 * NTRI + 3) / 4;
+    f32x4 res[JPW];
+#pragma unroll
+    for (int cnt = 0; cnt < JPW; ++cnt) {
+      const int job = wv_id + 4 * cnt;
+      if (job >= 2 * NTRI) break;
+      const int which = job / NTRI;  // 0: Aqk, 1: Akk
+      int t = job % NTRI, mi = 0;
+      while (t > mi) { t -= mi + 1; ++mi; }
+      const int ni = t;
+      f32x4 acc = zero4();
+      acc = tile_mma<T, false, false>(acc, which ? sB : sQ, L::LK, sK, L::LK, 16 * mi, 16 * ni, K);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * mi + tile_row(i), c = 16 * ni + tile_col();
+        float x = which ? acc[i] : dm.scale * acc[i];
+        const bool keep = which ? (r > c) : (r >= c);
+        acc[i] = keep ? n2n(x) : 0.f;
+      }
+      res[cnt] = acc;
+    }
+    __syncthreads();  // sQ / sK are dead from here on; sAf may alias them
+#pragma unroll
+    for (int cnt = 0; cnt < JPW; ++cnt) {
+      const int job = wv_id + 4 * cnt;
+      if (job >= 2 * NTRI) break;
+      const int which = job / NTRI;
+      int t = job % NTRI, mi = 0;
+      while (t > mi) { t -= mi + 1; ++mi; }
+      const int ni = t;
+      if (which == 0) store_tile_n(g_aqk, C, 16 * mi, 16 * ni, res[cnt]);
+      else store_tile_n(sAf, L::LA, 16 * mi, 16 * ni, res[cnt]);
+    }
+  } else {
+    constexpr int PER = C * C / 256;
+    float eqk[PER], ekk[PER];
+    intra_scores_exact<T, C, K>(sGcExact, qc, kc, bc, rsK, dm.scale, eqk, ekk);
+    __syncthreads();
+    for (int e = tid, s = 0; e < C * C; e += 256, ++s) {
+      const int i = e / C, j = e % C;
+      g_aqk[i * C + j] = from_f<T>(eqk[s]);
+      sAf[i * L::LA + j] = ekk[s];
+    }
+  }
+  // upper tiles of Aqk / Akk are zero
+  for (int e = tid; e < C * C; e += 256) {
+    const int i = e / C, j = e % C;
+    if ((j >> 4) > (i >> 4)) {
+      if (!exact) g_aqk[i * C + j] = from_f<T>(0.f);
+      sAf[i * L::LA + j] = 0.f;
+    }
+    sX[i * L::LA + j] = 0.f;
+  }
+  __syncthreads();
+
+  // ---- phase 3: A = (I + Akk)^-1 (gdn2_wy_reference.py:16-30,89-90)
+  // Diagonal 16x16 blocks by forward substitution (wave w, lane = column).
+  {
+    const int lane = lane_id();
+    if (wv_id < NB && lane < 16) {
+      const int o = 16 * wv_id;
+      float x[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float s = (i == lane) ? 1.f : 0.f;
+#pragma unroll
+        for (int j = 0; j < i; ++j) s -= sAf[(o + i) * L::LA + o + j] * x[j];
+        x[i] = s;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sX[(o + i) * L::LA + o + lane] = x[i];
+    }
+  }
+  __syncthreads();
+  // Off-diagonal blocks, one column block per wave:
+  //   A_mn = -A_mm (sum_{k=n}^{m-1} T_mk A_kn)
+  {
+    float* scr = sTot + wv_id * 16 * 17;
+    for (int nb = wv_id; nb < NB; nb += 4) {
+      for (int mb = nb + 1; mb < NB; ++mb) {
+        f32x4 acc = zero4();
+        acc = tile_mma<float, false, true>(acc, sAf + 16 * nb, L::LA, sX + 16 * nb * L::LA, L::LA,
+                                           16 * mb, 16 * nb, 16 * (mb - nb));
+        store_tile_n(scr, 17, 0, 0, acc);
+        wave_lds_sync();  // scr is private to this wave
+        f32x4 a2 = zero4();
+        a2 = tile_mma<float, false, true>(a2, sX + 16 * mb * L::LA + 16 * mb, L::LA, scr, 17, 0, 0, 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a2[i] = -a2[i];
+        store_tile_n(sX, L::LA, 16 * mb, 16 * nb, a2);
+      }
+    }
+  }
+  __syncthreads();
+  // n2n, operand-type copy, global A
+  T* g_ainv = ck.ainv + (size_t)bhn * C * C;
+  const T* opA;
+  int ldA;
+  if constexpr (sizeof(T) == 2) {
+    T* sAb = reinterpret_cast<T*>(lds + L::off_af);  // Akk is dead
+    for (int e = tid; e < C * C; e += 256) {
+      const int i = e / C, j = e % C;
+      const float x = n2n(sX[i * L::LA + j]);
+      sAb[i * (C + Pad<T>::v) + j] = from_f<T>(x);
+      g_ainv[i * C + j] = from_f<T>(x);
+    }
+    opA = sAb;
+    ldA = C + Pad<T>::v;
+  } else {
+    for (int e = tid; e < C * C; e += 256) {
+      const int i = e / C, j = e % C;
+      const float x = n2n(sX[i * L::LA + j]);
+      sX[i * L::LA + j] = x;
+      g_ainv[i * C + j] = from_f<T>(x);
+    }
+    opA = reinterpret_cast<const T*>(sX);
+    ldA = L::LA;
+  }
+  __syncthreads();
+
+  // ---- phase 4: w_pseudo = A kb, u = A wv (gdn2_wy_reference.py:92-96)
+  T* g_wt = ck.wt + (size_t)bhn * C * K;
+  T* g_u = ck.u + (size_t)bhn * C * V;
+  constexpr int TW = NB * (K / 16), TU = NB * (V / 16);
+  for (int job = wv_id; job < TW + TU; job += 4) {
+    const bool isu = job >= TW;
+    const int jj = isu ? job - TW : job;
+    const int nbk = isu ? V / 16 : K / 16;
+    const int mi = jj / nbk, ni = jj % nbk;
+    int kr = 16 * (mi + 1);
+    kr = ((kr + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
+    if (kr > C) kr = C;
+    f32x4 acc = zero4();
+    if (isu) acc = tile_mma<T, false, true>(acc, opA, ldA, sW, L::LV, 16 * mi, 16 * ni, kr);
+    else acc = tile_mma<T, false, true>(acc, opA, ldA, sB, L::LK, 16 * mi, 16 * ni, kr);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = n2n(acc[i]);
+    if (isu) store_tile_n(g_u, V, 16 * mi, 16 * ni, acc);
+    else store_tile_n(g_wt, K, 16 * mi, 16 * ni, acc);
+  }
+}
+
+// ------------------------------------------------------------------ state
+template <typename T, int C, int K, int V, int VT>
+struct StateLds {
+  static constexpr int PAD = Pad<T>::v;
+  static constexpr int LK = K + PAD, LC = C + PAD;
+  static constexpr int off_w = 0;
+  static constexpr int off_q = off_w + C * LK * (int)sizeof(T);
+  static constexpr int off_kg = off_q + C * LK * (int)sizeof(T);
+  static constexpr int off_aqk = off_kg + C * LK * (int)sizeof(T);
+  static constexpr int off_ht = off_aqk + C * LC * (int)sizeof(T);
+  static constexpr int off_vn = off_ht + VT * LK * (int)sizeof(T);
+  static constexpr int off_gl = off_vn + VT * LC * (int)sizeof(T);
+  static constexpr int total = off_gl + K * 4;
+};
+
+// Copy a [R][D] block (row stride `src_ld`) into LDS rows of length `dst_ld`.
+template <typename T, int R, int D>
+__device__ __forceinline__ void stage_rows(T* dst, int dst_ld, const T* src, size_t src_ld) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int PER_ROW = D / VEC;
+  for (int e = threadIdx.x; e < R * PER_ROW; e += 256) {
+    const int r = e / PER_ROW, c = (e % PER_ROW) * VEC;
+    *reinterpret_cast<uint4*>(dst + r * dst_ld + c) =
+        *reinterpret_cast<const uint4*>(src + r * src_ld + c);
+  }
+}
+template <typename T, int R, int D>
+__device__ __forceinline__ void unstage_rows(T* dst, size_t dst_ld, const T* src, int src_ld) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int PER_ROW = D / VEC;
+  for (int e = threadIdx.x; e < R * PER_ROW; e += 256) {
+    const int r = e / PER_ROW, c = (e % PER_ROW) * VEC;
+    *reinterpret_cast<uint4*>(dst + r * dst_ld + c) =
+        *reinterpret_cast<const uint4*>(src + r * src_ld + c);
+  }
+}
+
+// Workgroup -> (bh, vt) so that the V tiles of one head share an XCD (and
+// its L2): consecutive workgroup ids are dealt round-robin over 8 XCDs.
+__device__ __forceinline__ void xcd_group_map(int x, int groups, int per_group, int& grp, int& mem) {
+  const int total = groups * per_group;
+  if (per_group > 1 && total % (8 * per_group) == 0) {
+    const int xcd = x % 8, slot = x / 8;
+    grp = xcd * (total / (8 * per_group)) + slot / per_group;
+    mem = slot % per_group;
+  } else {
+    grp = x / per_group;
+    mem = x % per_group;
+  }
+}
+
+template <typename T, int C, int K, int V, int VT>
+__global__ __launch_bounds__(256) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T> ck,
+                                                     const float* __restrict__ h0, float* __restrict__ o,
+                                                     float* __restrict__ h_final, int save) {
+  typedef StateLds<T, C, K, V, VT> L;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
+  T* sW = reinterpret_cast<T*>(lds + L::off_w);
+  T* sQ = reinterpret_cast<T*>(lds + L::off_q);
+  T* sKg = reinterpret_cast<T*>(lds + L::off_kg);
+  T* sAqk = reinterpret_cast<T*>(lds + L::off_aqk);
+  T* sHt = reinterpret_cast<T*>(lds + L::off_ht);
+  T* sVn = reinterpret_cast<T*>(lds + L::off_vn);
+  float* sGl = reinterpret_cast<float*>(lds + L::off_gl);
+
+  constexpr int NVT = V / VT;
+  int bh, vt;
+  xcd_group_map(blockIdx.x, dm.B * dm.H, NVT, bh, vt);
+  const int h = bh % dm.H, bb = bh / dm.H;
+  const int v0 = vt * VT;
+  const int wv_id = wave_id();
+
+  // state tiles h[d][v]: (K/16) x (VT/16), TPW per wave
+  constexpr int NTI = VT / 16;
+  constexpr int NTH = (K / 16) * NTI;
+  constexpr int TPW = NTH / 4;
+  static_assert(NTH % 4 == 0, "state tiles must split evenly over 4 waves");
+  f32x4 hs[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = 16 * mi + tile_row(i), vv = v0 + 16 * ni + tile_col();
+      hs[t][i] = h0 ? h0[((size_t)bh * K + d) * V + vv] : 0.f;
+    }
+    store_tile_t(sHt, L::LK, 16 * mi, 16 * ni, hs[t]);
+  }
+
+  // X tiles: rows [0, C) = w_pseudo h, rows [C, 2C) = qg h; (2C/16) x NTI tiles
+  constexpr int NTX = (2 * C / 16) * NTI;
+  constexpr int XPW = NTX / 4;
+  static_assert(NTX % 4 == 0, "output tiles must split evenly over 4 waves");
+
+  for (int n = 0; n < dm.NT; ++n) {
+    const size_t bhn = (size_t)bh * dm.NT + n;
+    stage_rows<T, C, K>(sW, L::LK, ck.wt + bhn * C * K, K);
+    stage_rows<T, C, K>(sQ, L::LK, ck.qg + bhn * C * K, K);
+    stage_rows<T, C, K>(sKg, L::LK, ck.kg + bhn * C * K, K);
+    stage_rows<T, C, C>(sAqk, L::LC, ck.aqk + bhn * C * C, C);
+    if (threadIdx.x < K) sGl[threadIdx.x] = ck.gcl[bhn * K + threadIdx.x];
+    __syncthreads();
+    if (save) unstage_rows<T, VT, K>(ck.hT + bhn * V * K + (size_t)v0 * K, K, sHt, L::LK);
+
+    // v_new = u - w_pseudo h ; qh = qg h
+    f32x4 xo[XPW];
+#pragma unroll
+    for (int t = 0; t < XPW; ++t) {
+      const int tile = wv_id * XPW + t, mi = tile / NTI, ni = tile % NTI;
+      const bool is_w = mi < C / 16;
+      f32x4 acc = zero4();
+      acc = tile_mma<T, false, false>(acc, is_w ? sW : sQ, L::LK, sHt, L::LK,
+                                      16 * (is_w ? mi : mi - C / 16), 16 * ni, K);
+      if (is_w) {
+        const T* ug = ck.u + bhn * C * V;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = 16 * mi + tile_row(i), vv = v0 + 16 * ni + tile_col();
+          acc[i] = to_f(ug[j * V + vv]) - acc[i];
+        }
+        store_tile_t(sVn, L::LC, 16 * mi, 16 * ni, acc);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] *= dm.scale;
+      }
+      xo[t] = acc;
+    }
+    __syncthreads();
+    if (save) unstage_rows<T, VT, C>(ck.vnT + bhn * V * C + (size_t)v0 * C, C, sVn, L::LC);
+
+    // o = scale qg h + Aqk v_new   (rows of the qg half)
+    float* og = o + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0;
+#pragma unroll
+    for (int t = 0; t < XPW; ++t) {
+      const int tile = wv_id * XPW + t, mi = tile / NTI, ni = tile % NTI;
+      if (mi >= C / 16) {
+        const int mo = mi - C / 16;
+        int kr = 16 * (mo + 1);
+        kr = ((kr + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
+        if (kr > C) kr = C;
+        f32x4 acc = tile_mma<T, false, false>(xo[t], sAqk, L::LC, sVn, L::LC, 16 * mo, 16 * ni, kr);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * mo + tile_row(i), c = 16 * ni + tile_col();
+          og[(size_t)r * dm.H * V + c] = n2n(acc[i]);
+        }
+      }
+    }
+
+    // h = sanitize(h e^{gc_last} + kg^T v_new)
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
+      f32x4 acc = hs[t];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] *= __expf(sGl[16 * mi + tile_row(i)]);
+      acc = tile_mma<T, true, false>(acc, sKg, L::LK, sVn, L::LC, 16 * mi, 16 * ni, C);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = sanitize(acc[i]);
+      hs[t] = acc;
+    }
+    __syncthreads();  // all reads of sHt / sVn / staged chunk done
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
+      store_tile_t(sHt, L::LK, 16 * mi, 16 * ni, hs[t]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = 16 * mi + tile_row(i), vv = v0 + 16 * ni + tile_col();
+      h_final[((size_t)bh * K + d) * V + vv] = hs[t][i];
+    }
+  }
+}
+
+}  // namespace ah

@@ -1,0 +1,134 @@
+// Host side of the GDN2 chunk pipeline: argument checks, workspace layout,
+// template dispatch and the extern "C" entry points of include/atomic_hybrid.h.
+#include "../../include/atomic_hybrid.h"
+#include "gdn2_fwd.hip"
+
+namespace ah {
+
+static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct Gdn2Plan {
+  Gdn2Dims dm;
+  int es;        // operand element size
+  size_t bhn;    // B * H * NT
+  // forward intermediates
+  size_t o_qg, o_kg, o_wt, o_u, o_aqk, o_ainv, o_gcl, o_ht, o_vnt, fwd_end;
+  // backward scratch
+  size_t o_dvn, o_dht, o_dqg, o_dwt, o_dkg, o_daqk, o_rlast, total;
+};
+
+static int gdn2_plan(const atomic_gdn2_args* a, Gdn2Plan* p) {
+  if (!a) return ATOMIC_ERR_NULL;
+  if (a->dtype != ATOMIC_F32 && a->dtype != ATOMIC_BF16) return ATOMIC_ERR_DTYPE;
+  if (a->do_dtype != ATOMIC_F32 && a->do_dtype != ATOMIC_BF16) return ATOMIC_ERR_DTYPE;
+  if (a->batch <= 0 || a->heads <= 0 || a->seqlen <= 0) return ATOMIC_ERR_SHAPE;
+  if (a->chunk != 64) return ATOMIC_ERR_SHAPE;
+  if (a->seqlen % a->chunk != 0) return ATOMIC_ERR_SHAPE;
+  if (!((a->dk == 64 || a->dk == 128) && a->dv == a->dk)) return ATOMIC_ERR_SHAPE;
+  Gdn2Dims d;
+  d.B = a->batch; d.T = a->seqlen; d.H = a->heads; d.K = a->dk; d.V = a->dv; d.C = a->chunk;
+  d.NT = a->seqlen / a->chunk; d.scale = a->scale;
+  p->dm = d;
+  p->es = a->dtype == ATOMIC_BF16 ? 2 : 4;
+  const size_t N = (size_t)d.B * d.H * d.NT;
+  p->bhn = N;
+  const size_t es = p->es, C = d.C, K = d.K, V = d.V;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off += align256(bytes); return o; };
+  p->o_qg = take(N * C * K * es);
+  p->o_kg = take(N * C * K * es);
+  p->o_wt = take(N * C * K * es);
+  p->o_u = take(N * C * V * es);
+  p->o_aqk = take(N * C * C * es);
+  p->o_ainv = take(N * C * C * es);
+  p->o_gcl = take(N * K * 4);
+  p->o_ht = take(N * V * K * es);
+  p->o_vnt = take(N * V * C * es);
+  p->fwd_end = off;
+  p->o_dvn = take(N * C * V * 4);
+  p->o_dht = take(N * V * K * es);
+  p->o_dqg = take(N * C * K * 4);
+  p->o_dwt = take(N * C * K * 4);
+  p->o_dkg = take(N * C * K * 4);
+  p->o_daqk = take(N * C * C * 4);
+  p->o_rlast = take(N * K * 4);
+  p->total = off;
+  return ATOMIC_OK;
+}
+
+template <typename T>
+static Gdn2Chunks<T> gdn2_chunks(const Gdn2Plan& p, void* ws) {
+  char* base = static_cast<char*>(ws);
+  Gdn2Chunks<T> c;
+  c.qg = reinterpret_cast<T*>(base + p.o_qg);
+  c.kg = reinterpret_cast<T*>(base + p.o_kg);
+  c.wt = reinterpret_cast<T*>(base + p.o_wt);
+  c.u = reinterpret_cast<T*>(base + p.o_u);
+  c.aqk = reinterpret_cast<T*>(base + p.o_aqk);
+  c.ainv = reinterpret_cast<T*>(base + p.o_ainv);
+  c.gcl = reinterpret_cast<float*>(base + p.o_gcl);
+  c.hT = reinterpret_cast<T*>(base + p.o_ht);
+  c.vnT = reinterpret_cast<T*>(base + p.o_vnt);
+  return c;
+}
+
+template <typename T, int K>
+static int gdn2_forward_impl(const Gdn2Plan& p, const void* q, const void* k, const void* v,
+                             const void* w, const void* b, const float* g, const float* h0,
+                             float* o, float* h_final, void* ws, int save, hipStream_t st) {
+  constexpr int C = 64, V = K, VT = 32;
+  Gdn2Chunks<T> ck = gdn2_chunks<T>(p, ws);
+  hipLaunchKernelGGL((gdn2_fwd_intra<T, C, K, V>), dim3((unsigned)p.bhn), dim3(256), 0, st, p.dm,
+                     (const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b, g, ck);
+  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
+  const unsigned nwg = (unsigned)(p.dm.B * p.dm.H * (V / VT));
+  hipLaunchKernelGGL((gdn2_fwd_state<T, C, K, V, VT>), dim3(nwg), dim3(256), 0, st, p.dm, ck, h0, o,
+                     h_final, save);
+  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
+  return ATOMIC_OK;
+}
+
+int gdn2_forward(const Gdn2Plan& p, int dtype, const void* q, const void* k, const void* v,
+                 const void* w, const void* b, const float* g, const float* h0, float* o,
+                 float* h_final, void* ws, int save, hipStream_t st) {
+  if (dtype == ATOMIC_BF16) {
+    if (p.dm.K == 128) return gdn2_forward_impl<bf16, 128>(p, q, k, v, w, b, g, h0, o, h_final, ws, save, st);
+    return gdn2_forward_impl<bf16, 64>(p, q, k, v, w, b, g, h0, o, h_final, ws, save, st);
+  }
+  if (p.dm.K == 128) return gdn2_forward_impl<float, 128>(p, q, k, v, w, b, g, h0, o, h_final, ws, save, st);
+  return gdn2_forward_impl<float, 64>(p, q, k, v, w, b, g, h0, o, h_final, ws, save, st);
+}
+
+}  // namespace ah
+
+using namespace ah;
+
+extern "C" size_t atomic_gdn2_workspace_size(const atomic_gdn2_args* a) {
+  Gdn2Plan p;
+  if (gdn2_plan(a, &p) != ATOMIC_OK) return 0;
+  return p.total;
+}
+
+extern "C" int atomic_gdn2_workspace_layout(const atomic_gdn2_args* a, atomic_gdn2_layout* out) {
+  Gdn2Plan p;
+  const int rc = gdn2_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!out) return ATOMIC_ERR_NULL;
+  out->qg = p.o_qg; out->kg = p.o_kg; out->w_pseudo = p.o_wt; out->u = p.o_u;
+  out->aqk = p.o_aqk; out->ainv = p.o_ainv; out->gc_last = p.o_gcl;
+  out->h_pre_t = p.o_ht; out->v_new_t = p.o_vnt; out->total = p.total;
+  return ATOMIC_OK;
+}
+
+extern "C" int atomic_gdn2_fwd(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
+                               const void* w, const void* b, const float* g, const float* h0,
+                               float* o, float* h_final, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  Gdn2Plan p;
+  const int rc = gdn2_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!q || !k || !v || !w || !b || !g || !o || !h_final) return ATOMIC_ERR_NULL;
+  if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
+  return gdn2_forward(p, a->dtype, q, k, v, w, b, g, h0, o, h_final, workspace,
+                      (a->flags & ATOMIC_GDN2_SAVE) ? 1 : 0, (hipStream_t)stream);
+}

@@ -1,0 +1,116 @@
+/*
+ * atomic_hybrid.h -- C ABI of the MI355X (gfx950) GDN2 WY chunk pipeline and
+ * Mamba2 SSD chunk scan.
+ *
+ * Plain pointers and sizes only.  Every tensor is a device pointer to a dense
+ * row-major array; every call is stream-ordered on `stream` (a hipStream_t,
+ * or NULL for the default stream), allocates nothing, never synchronises the
+ * host, and keeps no global mutable state (reentrant).  Scratch memory is a
+ * caller-owned `workspace` of at least the size the matching *_workspace_size
+ * call returns.
+ *
+ * Return value: ATOMIC_OK (0) or a negative ATOMIC_ERR_* code.  The reference
+ * raises shape errors at trace time and has no runtime error channel
+ * (kernel_a_scores.py:71-72, gdn2_wy_reference.py:109-112); here the same
+ * checks return ATOMIC_ERR_SHAPE before anything is launched.  Numerical
+ * faults are absorbed by the same clip / nan_to_num placement as the
+ * reference, never reported.
+ */
+#ifndef ATOMIC_HYBRID_H
+#define ATOMIC_HYBRID_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  ATOMIC_OK = 0,
+  ATOMIC_ERR_SHAPE = -1,      /* unsupported or inconsistent dimensions       */
+  ATOMIC_ERR_DTYPE = -2,      /* unsupported dtype code                       */
+  ATOMIC_ERR_WORKSPACE = -3,  /* workspace NULL or smaller than required      */
+  ATOMIC_ERR_LAUNCH = -4,     /* a kernel launch failed                       */
+  ATOMIC_ERR_NULL = -5        /* a required pointer is NULL                   */
+};
+
+enum { ATOMIC_F32 = 0, ATOMIC_BF16 = 1 };
+
+/* ------------------------------------------------------------------ GDN2 */
+
+/* Flags for atomic_gdn2_args.flags */
+enum {
+  /* forward: keep the per-chunk intermediates (state entering each chunk,
+     v_new) in the workspace so a following atomic_gdn2_bwd on the same
+     inputs and workspace can skip the forward recompute */
+  ATOMIC_GDN2_SAVE = 1,
+  /* backward: the workspace holds the intermediates of an
+     atomic_gdn2_fwd(..., ATOMIC_GDN2_SAVE) call on identical inputs */
+  ATOMIC_GDN2_REUSE = 2
+};
+
+typedef struct atomic_gdn2_args {
+  int32_t batch;     /* B                                                       */
+  int32_t seqlen;    /* T, a multiple of chunk                                  */
+  int32_t heads;     /* H                                                       */
+  int32_t dk;        /* K: 64 or 128                                            */
+  int32_t dv;        /* V: equal to dk                                          */
+  int32_t chunk;     /* C: 64                                                   */
+  int32_t dtype;     /* q, k, v, w, b and their gradients: ATOMIC_F32 / _BF16  */
+  int32_t do_dtype;  /* upstream gradient dO: ATOMIC_F32 / ATOMIC_BF16          */
+  float scale;       /* query scale (the model passes 1.0, model.py:631)        */
+  int32_t flags;     /* ATOMIC_GDN2_*                                           */
+} atomic_gdn2_args;
+
+/* Bytes of workspace atomic_gdn2_fwd / atomic_gdn2_bwd need for these args. */
+size_t atomic_gdn2_workspace_size(const atomic_gdn2_args* a);
+
+/* Byte offsets of the per-chunk intermediates inside the workspace, for
+   stage-level inspection.  Each block is [B][H][NT][rows][cols] in the
+   operand dtype (bf16 for bf16 inputs, fp32 for fp32 inputs) except gc_last
+   (fp32).  Returns ATOMIC_OK or ATOMIC_ERR_SHAPE. */
+typedef struct atomic_gdn2_layout {
+  size_t qg, kg, w_pseudo, u, aqk, ainv, gc_last, h_pre_t, v_new_t;
+  size_t total;
+} atomic_gdn2_layout;
+int atomic_gdn2_workspace_layout(const atomic_gdn2_args* a, atomic_gdn2_layout* out);
+
+/*
+ * GDN2 WY chunked forward.  Replaces gdn2_pallas_forward / the forward of
+ * gdn2_pallas_forward_trainable(q, k, v, w, b, g, scale, h0)
+ * (reference atomic_ops/kernel_trainable_B6.py:187-194,
+ *  atomic_ops/kernel_d_pipeline.py:161-196); numerics follow
+ * gdn2_chunked_wy_reference (atomic_ops/gdn2_wy_reference.py:105-152).
+ *   q, k, b : [B, T, H, K]  dtype        v, w : [B, T, H, V]  dtype
+ *   g       : [B, T, H, K]  fp32 log-decay
+ *   h0      : [B, H, K, V]  fp32, NULL means zeros
+ *   o       : [B, T, H, V]  fp32 (the reference returns fp32, :151)
+ *   h_final : [B, H, K, V]  fp32
+ */
+int atomic_gdn2_fwd(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
+                    const void* w, const void* b, const float* g, const float* h0, float* o,
+                    float* h_final, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * GDN2 chunked backward: the B2 -> B1 -> B3 -> B4 -> B5 chain of
+ * _gdn2_core_bwd (reference atomic_ops/kernel_trainable_B6.py:97-181), whose
+ * result is the gradient of gdn2_chunked_wy_reference (kernel_trainable.py:38-55).
+ *   dO       : [B, T, H, V]  do_dtype
+ *   dh_final : [B, H, K, V]  fp32, NULL means zeros
+ *   dq, dk, db : [B, T, H, K] dtype     dv, dw : [B, T, H, V] dtype
+ *   dg       : [B, T, H, K]  fp32       dh0 : [B, H, K, V] fp32 (may be NULL)
+ * Every gradient passes the final clip(+-1e4) / nan_to_num of
+ * kernel_trainable_B6.py:64-66,173-179 and is cast to its primal's dtype.
+ */
+int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
+                    const void* w, const void* b, const float* g, const float* h0,
+                    const void* dO, const float* dh_final, void* dq, void* dk, void* dv,
+                    void* dw, void* db, float* dg, float* dh0, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATOMIC_HYBRID_H */
