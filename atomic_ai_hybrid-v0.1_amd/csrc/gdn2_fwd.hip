@@ -360,8 +360,37 @@ struct StateLds {
   static constexpr int off_aqk = off_kg + C * LK * (int)sizeof(T);
   static constexpr int off_ht = off_aqk + C * LC * (int)sizeof(T);
   static constexpr int off_vn = off_ht + VT * LK * (int)sizeof(T);
-  static constexpr int off_gl = off_vn + VT * LC * (int)sizeof(T);
+  static constexpr int LU = VT + PAD;
+  static constexpr int off_u = off_vn + VT * LC * (int)sizeof(T);
+  static constexpr int off_gl = off_u + C * LU * (int)sizeof(T);
   static constexpr int total = off_gl + K * 4;
+};
+
+// A [R][D] block moved global -> registers -> LDS in 16-byte pieces, so the
+// next chunk's loads can be in flight while the current chunk computes.
+template <typename T, int R, int D>
+struct RegStage {
+  static constexpr int VEC = 16 / (int)sizeof(T);
+  static constexpr int PER_ROW = D / VEC;
+  static constexpr int N = R * PER_ROW;
+  static constexpr int PT = (N + 255) / 256;
+  uint4 r[PT];
+  __device__ __forceinline__ void load(const T* src, size_t ld) {
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      const int e = threadIdx.x + 256 * i;
+      if (N % 256 == 0 || e < N)
+        r[i] = *reinterpret_cast<const uint4*>(src + (size_t)(e / PER_ROW) * ld + (e % PER_ROW) * VEC);
+    }
+  }
+  __device__ __forceinline__ void store(T* dst, int ld) const {
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      const int e = threadIdx.x + 256 * i;
+      if (N % 256 == 0 || e < N)
+        *reinterpret_cast<uint4*>(dst + (e / PER_ROW) * ld + (e % PER_ROW) * VEC) = r[i];
+    }
+  }
 };
 
 // Copy a [R][D] block (row stride `src_ld`) into LDS rows of length `dst_ld`.
@@ -401,7 +430,7 @@ __device__ __forceinline__ void xcd_group_map(int x, int groups, int per_group, 
 }
 
 template <typename T, int C, int K, int V, int VT>
-__global__ __launch_bounds__(256) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T> ck,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T> ck,
                                                      const float* __restrict__ h0, float* __restrict__ o,
                                                      float* __restrict__ h_final, int save) {
   typedef StateLds<T, C, K, V, VT> L;
@@ -412,6 +441,7 @@ __global__ __launch_bounds__(256) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T>
   T* sAqk = reinterpret_cast<T*>(lds + L::off_aqk);
   T* sHt = reinterpret_cast<T*>(lds + L::off_ht);
   T* sVn = reinterpret_cast<T*>(lds + L::off_vn);
+  T* sU = reinterpret_cast<T*>(lds + L::off_u);
   float* sGl = reinterpret_cast<float*>(lds + L::off_gl);
 
   constexpr int NVT = V / VT;
@@ -443,14 +473,34 @@ __global__ __launch_bounds__(256) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T>
   constexpr int XPW = NTX / 4;
   static_assert(NTX % 4 == 0, "output tiles must split evenly over 4 waves");
 
+  RegStage<T, C, K> pw, pq, pk;
+  RegStage<T, C, C> pa;
+  RegStage<T, C, VT> pu;
+  RegStage<float, 1, K> pg;
+  auto prefetch = [&](int n) {
+    const size_t bhn = (size_t)bh * dm.NT + n;
+    pw.load(ck.wt + bhn * C * K, K);
+    pq.load(ck.qg + bhn * C * K, K);
+    pk.load(ck.kg + bhn * C * K, K);
+    pa.load(ck.aqk + bhn * C * C, C);
+    pu.load(ck.u + bhn * C * V + v0, V);
+    pg.load(ck.gcl + bhn * K, K);
+  };
+  auto commit = [&]() {
+    pw.store(sW, L::LK);
+    pq.store(sQ, L::LK);
+    pk.store(sKg, L::LK);
+    pa.store(sAqk, L::LC);
+    pu.store(sU, L::LU);
+    pg.store(sGl, K);
+  };
+  prefetch(0);
+  commit();
+  __syncthreads();
+
   for (int n = 0; n < dm.NT; ++n) {
     const size_t bhn = (size_t)bh * dm.NT + n;
-    stage_rows<T, C, K>(sW, L::LK, ck.wt + bhn * C * K, K);
-    stage_rows<T, C, K>(sQ, L::LK, ck.qg + bhn * C * K, K);
-    stage_rows<T, C, K>(sKg, L::LK, ck.kg + bhn * C * K, K);
-    stage_rows<T, C, C>(sAqk, L::LC, ck.aqk + bhn * C * C, C);
-    if (threadIdx.x < K) sGl[threadIdx.x] = ck.gcl[bhn * K + threadIdx.x];
-    __syncthreads();
+    if (n + 1 < dm.NT) prefetch(n + 1);
     if (save) unstage_rows<T, VT, K>(ck.hT + bhn * V * K + (size_t)v0 * K, K, sHt, L::LK);
 
     // v_new = u - w_pseudo h ; qh = qg h
@@ -463,11 +513,10 @@ __global__ __launch_bounds__(256) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T>
       acc = tile_mma<T, false, false>(acc, is_w ? sW : sQ, L::LK, sHt, L::LK,
                                       16 * (is_w ? mi : mi - C / 16), 16 * ni, K);
       if (is_w) {
-        const T* ug = ck.u + bhn * C * V;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int j = 16 * mi + tile_row(i), vv = v0 + 16 * ni + tile_col();
-          acc[i] = to_f(ug[j * V + vv]) - acc[i];
+          const int j = 16 * mi + tile_row(i), vv = 16 * ni + tile_col();
+          acc[i] = to_f(sU[j * L::LU + vv]) - acc[i];
         }
         store_tile_t(sVn, L::LC, 16 * mi, 16 * ni, acc);
       } else {
@@ -516,6 +565,8 @@ __global__ __launch_bounds__(256) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T>
       const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
       store_tile_t(sHt, L::LK, 16 * mi, 16 * ni, hs[t]);
     }
+    if (n + 1 < dm.NT) commit();
+    __syncthreads();
   }
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
