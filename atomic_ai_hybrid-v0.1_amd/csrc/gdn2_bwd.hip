@@ -1,0 +1,650 @@
+// GDN2 WY chunked backward for gfx950: the B2 -> B1 -> B3 -> B4 -> B5 chain of
+// _gdn2_core_bwd (atomic_ops/kernel_trainable_B6.py:97-181).
+//
+//   gdn2_bwd_dh     one workgroup per (batch, head, V tile), reverse over
+//                   chunks: B2's dv_partial = Aqk^T dO, then B1
+//                   (kernel_bwd_b1_dhu.py:22-39) with the fp32 dh carried in
+//                   MFMA accumulators.  Saves dv_new and the carry entering
+//                   each chunk (dh_next).
+//   gdn2_bwd_hgrad  per chunk: the state contractions of B2/B3
+//                   (kernel_bwd_b2_dav.py:69, kernel_bwd_b3_wy_dqkg.py:154-161,
+//                   :200-201): dAqk, dqg, dw_pseudo, dkg and the gc_last row term.
+//   gdn2_bwd_wy     per chunk: the WY part of B3 (kernel_bwd_b3_wy_dqkg.py:163-179,
+//                   :194-195): dA, dkb = A^T dw_pseudo, dwv = A^T dv,
+//                   dAkk = -A^T clip(clip(dA) A^T) (strict), and the final dw, dv.
+//   gdn2_bwd_intra  per chunk: B4 (kernel_bwd_b4_intra.py:57-132) in the
+//                   factorised form (or exact pairwise, same criterion as the
+//                   forward), the B3 element-wise terms, the combine of
+//                   kernel_trainable_B6.py:139-147, and B5's reverse cumsum
+//                   (kernel_bwd_b5_reverse_cumsum.py:17-24).  Writes dq, dk, db, dg.
+#include "gdn2_fwd.hip"
+
+namespace ah {
+
+// Elementwise copy of a [R][D] block into LDS converting to the operand type
+// (optionally scaled).
+template <typename TS, typename T, int R, int D>
+__device__ __forceinline__ void stage_convert(T* dst, int ld, const TS* src, size_t src_ld,
+                                              float mul = 1.f) {
+  constexpr int PER_ROW = D / 8;
+  for (int e = threadIdx.x; e < R * PER_ROW; e += 256) {
+    const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
+    float x[8];
+    load8(src + (size_t)r * src_ld + c, x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] *= mul;
+    store8(dst + r * ld + c, x);
+  }
+}
+
+// First k (rounded down to the MFMA k step) of a lower-triangular operand
+// whose nonzeros start at row 16 * tile.
+template <typename T>
+__device__ __forceinline__ int tri_k0(int tile) {
+  return (16 * tile / Mma<T>::KS) * Mma<T>::KS;
+}
+template <typename T>
+__device__ __forceinline__ int tri_k1(int tile, int C) {
+  int k = 16 * (tile + 1);
+  k = ((k + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
+  return k > C ? C : k;
+}
+
+// ------------------------------------------------------------------ B2 + B1
+template <typename T, int C, int K, int V, int VT>
+struct DhLds {
+  static constexpr int PAD = Pad<T>::v;
+  static constexpr int LK = K + PAD, LC = C + PAD, LD = VT + PAD;
+  static constexpr int off_w = 0;
+  static constexpr int off_q = off_w + C * LK * (int)sizeof(T);
+  static constexpr int off_kg = off_q + C * LK * (int)sizeof(T);
+  static constexpr int off_aqk = off_kg + C * LK * (int)sizeof(T);
+  static constexpr int off_do = off_aqk + C * LC * (int)sizeof(T);
+  static constexpr int off_dos = off_do + C * LD * (int)sizeof(T);
+  static constexpr int off_dht = off_dos + C * LD * (int)sizeof(T);
+  static constexpr int off_dvt = off_dht + VT * LK * (int)sizeof(T);
+  static constexpr int off_gl = off_dvt + VT * LC * (int)sizeof(T);
+  static constexpr int total = off_gl + K * 4;
+};
+
+template <typename T, typename TD, int C, int K, int V, int VT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gdn2_bwd_dh(
+    Gdn2Dims dm, Gdn2Chunks<T> ck, Gdn2Grads<T> gr, const TD* __restrict__ dO,
+    const float* __restrict__ dh_final, float* __restrict__ dh0) {
+  typedef DhLds<T, C, K, V, VT> L;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
+  T* sW = reinterpret_cast<T*>(lds + L::off_w);
+  T* sQ = reinterpret_cast<T*>(lds + L::off_q);
+  T* sKg = reinterpret_cast<T*>(lds + L::off_kg);
+  T* sAqk = reinterpret_cast<T*>(lds + L::off_aqk);
+  T* sDO = reinterpret_cast<T*>(lds + L::off_do);
+  T* sDOs = reinterpret_cast<T*>(lds + L::off_dos);
+  T* sDht = reinterpret_cast<T*>(lds + L::off_dht);
+  T* sDvT = reinterpret_cast<T*>(lds + L::off_dvt);
+  float* sGl = reinterpret_cast<float*>(lds + L::off_gl);
+
+  constexpr int NVT = V / VT;
+  int bh, vt;
+  xcd_group_map(blockIdx.x, dm.B * dm.H, NVT, bh, vt);
+  const int h = bh % dm.H, bb = bh / dm.H;
+  const int v0 = vt * VT;
+  const int wv_id = wave_id();
+  const size_t ldo = (size_t)dm.H * V;
+
+  constexpr int NTI = VT / 16;
+  constexpr int NTH = (K / 16) * NTI;  // dh tiles
+  constexpr int TPW = NTH / 4;
+  constexpr int NTV = (C / 16) * NTI;  // dv_new tiles
+  constexpr int VPW = NTV / 4;
+  static_assert(NTH % 4 == 0 && NTV % 4 == 0, "tiles must split evenly over 4 waves");
+
+  // dh carry = sanitize(dh_final) (kernel_bwd_b1_dhu.py:18)
+  f32x4 hs[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = 16 * mi + tile_row(i), vv = v0 + 16 * ni + tile_col();
+      hs[t][i] = dh_final ? sanitize(dh_final[((size_t)bh * K + d) * V + vv]) : 0.f;
+    }
+    store_tile_t(sDht, L::LK, 16 * mi, 16 * ni, hs[t]);
+  }
+
+  RegStage<T, C, K> pw, pq, pk;
+  RegStage<T, C, C> pa;
+  RegStage<float, 1, K> pg;
+  auto prefetch = [&](int n) {
+    const size_t bhn = (size_t)bh * dm.NT + n;
+    pw.load(ck.wt + bhn * C * K, K);
+    pq.load(ck.qg + bhn * C * K, K);
+    pk.load(ck.kg + bhn * C * K, K);
+    pa.load(ck.aqk + bhn * C * C, C);
+    pg.load(ck.gcl + bhn * K, K);
+  };
+  auto commit = [&](int n) {
+    pw.store(sW, L::LK);
+    pq.store(sQ, L::LK);
+    pk.store(sKg, L::LK);
+    pa.store(sAqk, L::LC);
+    pg.store(sGl, K);
+    const TD* src = dO + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0;
+    stage_convert<TD, T, C, VT>(sDO, L::LD, src, ldo);
+    stage_convert<TD, T, C, VT>(sDOs, L::LD, src, ldo, dm.scale);
+  };
+  prefetch(dm.NT - 1);
+  commit(dm.NT - 1);
+  __syncthreads();
+
+  for (int n = dm.NT - 1; n >= 0; --n) {
+    const size_t bhn = (size_t)bh * dm.NT + n;
+    if (n > 0) prefetch(n - 1);
+    // dh_next of chunk n = the carry entering this step
+    unstage_rows<T, VT, K>(gr.dhT + bhn * V * K + (size_t)v0 * K, K, sDht, L::LK);
+
+    // dv_new = sanitize(Aqk^T dO + kg dh)   (b2:70, b1:30-32)
+#pragma unroll
+    for (int t = 0; t < VPW; ++t) {
+      const int tile = wv_id * VPW + t, mj = tile / NTI, ni = tile % NTI;
+      const int k0 = tri_k0<T>(mj);
+      f32x4 acc = zero4();
+      acc = tile_mma<T, true, true>(acc, sAqk + k0 * L::LC, L::LC, sDO + k0 * L::LD, L::LD,
+                                    16 * mj, 16 * ni, C - k0);
+      acc = tile_mma<T, false, false>(acc, sKg, L::LK, sDht, L::LK, 16 * mj, 16 * ni, K);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = sanitize(acc[i]);
+      store_tile_n(gr.dvn + bhn * C * V + v0, V, 16 * mj, 16 * ni, acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = -acc[i];
+      store_tile_t(sDvT, L::LC, 16 * mj, 16 * ni, acc);
+    }
+    __syncthreads();
+
+    // dh = sanitize(qg^T (scale dO) + dh e^{gc_last} - w_pseudo^T dv_new)   (b1:26-37)
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
+      f32x4 acc = hs[t];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] *= __expf(sGl[16 * mi + tile_row(i)]);
+      acc = tile_mma<T, true, true>(acc, sQ, L::LK, sDOs, L::LD, 16 * mi, 16 * ni, C);
+      acc = tile_mma<T, true, false>(acc, sW, L::LK, sDvT, L::LC, 16 * mi, 16 * ni, C);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = sanitize(acc[i]);
+      hs[t] = acc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
+      store_tile_t(sDht, L::LK, 16 * mi, 16 * ni, hs[t]);
+    }
+    if (n > 0) commit(n - 1);
+    __syncthreads();
+  }
+  if (dh0) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = 16 * mi + tile_row(i), vv = v0 + 16 * ni + tile_col();
+        dh0[((size_t)bh * K + d) * V + vv] = hs[t][i];
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ B2/B3 state terms
+template <typename T, int C, int K, int V>
+struct HgLds {
+  static constexpr int PAD = Pad<T>::v;
+  static constexpr int LK = K + PAD, LV = V + PAD, LC = C + PAD;
+  static constexpr int off_do = 0;
+  static constexpr int off_dv = off_do + C * LV * (int)sizeof(T);
+  static constexpr int off_h = off_dv + C * LV * (int)sizeof(T);
+  static constexpr int off_dh = off_h + V * LK * (int)sizeof(T);
+  static constexpr int off_vn = off_dh + V * LK * (int)sizeof(T);
+  static constexpr int total = off_vn + V * LC * (int)sizeof(T);
+};
+
+template <typename T, typename TD, int C, int K, int V>
+__global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T> ck, Gdn2Grads<T> gr,
+                                                     const TD* __restrict__ dO) {
+  typedef HgLds<T, C, K, V> L;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
+  T* sDO = reinterpret_cast<T*>(lds + L::off_do);
+  T* sDV = reinterpret_cast<T*>(lds + L::off_dv);
+  T* sH = reinterpret_cast<T*>(lds + L::off_h);
+  T* sDh = reinterpret_cast<T*>(lds + L::off_dh);
+  T* sVn = reinterpret_cast<T*>(lds + L::off_vn);
+
+  const int bhn = blockIdx.x;
+  const int n = bhn % dm.NT;
+  const int bh = bhn / dm.NT;
+  const int h = bh % dm.H, bb = bh / dm.H;
+  const int wv_id = wave_id();
+  const size_t blk = (size_t)bhn;
+
+  stage_convert<TD, T, C, V>(sDO, L::LV, dO + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V,
+                             (size_t)dm.H * V);
+  stage_convert<float, T, C, V>(sDV, L::LV, gr.dvn + blk * C * V, V);
+  stage_rows<T, V, K>(sH, L::LK, ck.hT + blk * V * K, K);
+  stage_rows<T, V, K>(sDh, L::LK, gr.dhT + blk * V * K, K);
+  stage_rows<T, V, C>(sVn, L::LC, ck.vnT + blk * V * C, C);
+  __syncthreads();
+
+  // dqg = scale dO h_pre^T ; dwt = -dv_new h_pre^T ; dkg = v_new dh_next^T
+  constexpr int MT = C / 16, NTK = K / 16;
+  constexpr int TPW = MT * NTK / 4;
+  float* g_dqg = gr.dqg + blk * C * K;
+  float* g_dwt = gr.dwt + blk * C * K;
+  float* g_dkg = gr.dkg + blk * C * K;
+#pragma unroll 2
+  for (int t = 0; t < TPW; ++t) {
+    const int tile = wv_id * TPW + t, mi = tile % MT, ni = tile / MT;
+    f32x4 a = tile_mma<T, false, true>(zero4(), sDO, L::LV, sH, L::LK, 16 * mi, 16 * ni, V);
+    f32x4 b = tile_mma<T, false, true>(zero4(), sDV, L::LV, sH, L::LK, 16 * mi, 16 * ni, V);
+    f32x4 c = tile_mma<T, true, true>(zero4(), sVn, L::LC, sDh, L::LK, 16 * mi, 16 * ni, V);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { a[i] *= dm.scale; b[i] = -b[i]; }
+    store_tile_n(g_dqg, K, 16 * mi, 16 * ni, a);
+    store_tile_n(g_dwt, K, 16 * mi, 16 * ni, b);
+    store_tile_n(g_dkg, K, 16 * mi, 16 * ni, c);
+  }
+  // dAqk = n2n((dO v_new^T) * causal)   (kernel_bwd_b2_dav.py:69,72)
+  float* g_daqk = gr.daqk + blk * C * C;
+  for (int tile = wv_id; tile < MT * MT; tile += 4) {
+    const int mi = tile / MT, nj = tile % MT;
+    f32x4 acc = zero4();
+    if (nj <= mi) acc = tile_mma<T, false, true>(acc, sDO, L::LV, sVn, L::LC, 16 * mi, 16 * nj, V);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * mi + tile_row(i), c = 16 * nj + tile_col();
+      acc[i] = r >= c ? n2n(acc[i]) : 0.f;
+    }
+    store_tile_n(g_daqk, C, 16 * mi, 16 * nj, acc);
+  }
+  // exp(gc_last) * sum_v dh_next * h_pre   (kernel_bwd_b3_wy_dqkg.py:200-201)
+  if (threadIdx.x < K) {
+    const int d = threadIdx.x;
+    float s = 0.f;
+    for (int v = 0; v < V; ++v) s += to_f(sDh[v * L::LK + d]) * to_f(sH[v * L::LK + d]);
+    gr.rlast[blk * K + d] = __expf(ck.gcl[blk * K + d]) * s;
+  }
+}
+
+// ------------------------------------------------------------------ B3 WY part
+template <typename T, int C, int K, int V>
+struct WyLds {
+  static constexpr int PAD = Pad<T>::v;
+  static constexpr int LK = K + PAD, LV = V + PAD, LC = C + PAD;
+  static constexpr int OK_ = C * LK * (int)sizeof(T), OV = C * LV * (int)sizeof(T),
+                       OC = C * LC * (int)sizeof(T);
+  static constexpr int off_a = 0;
+  static constexpr int off_dw = off_a + OC;
+  static constexpr int off_dv = off_dw + OK_;
+  static constexpr int off_kb = off_dv + OV;
+  static constexpr int off_wv = off_kb + OK_;
+  static constexpr int off_da = off_wv + OV;
+  static constexpr int off_tmp = off_da + OC;
+  static constexpr int off_tot = off_tmp + OC;
+  static constexpr int off_gl = off_tot + ColMap<C, K>::NSEG * K * 4;
+  static constexpr int total = off_gl + K * 4;
+};
+
+template <typename T, int C, int K, int V>
+__global__ __launch_bounds__(256) void gdn2_bwd_wy(Gdn2Dims dm, Gdn2Chunks<T> ck, Gdn2Grads<T> gr,
+                                                  const T* __restrict__ k, const T* __restrict__ v,
+                                                  const T* __restrict__ w, const T* __restrict__ b,
+                                                  const float* __restrict__ g, T* __restrict__ dw,
+                                                  T* __restrict__ dv) {
+  typedef WyLds<T, C, K, V> L;
+  typedef ColMap<C, K> M;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
+  T* sA = reinterpret_cast<T*>(lds + L::off_a);
+  T* sDW = reinterpret_cast<T*>(lds + L::off_dw);
+  T* sDV = reinterpret_cast<T*>(lds + L::off_dv);
+  T* sKB = reinterpret_cast<T*>(lds + L::off_kb);
+  T* sWV = reinterpret_cast<T*>(lds + L::off_wv);
+  T* sDA = reinterpret_cast<T*>(lds + L::off_da);
+  T* sTmp = reinterpret_cast<T*>(lds + L::off_tmp);
+  float* sTot = reinterpret_cast<float*>(lds + L::off_tot);
+  float* sGl = reinterpret_cast<float*>(lds + L::off_gl);
+
+  const int tid = threadIdx.x;
+  const int bhn = blockIdx.x;
+  const int n = bhn % dm.NT;
+  const int bh = bhn / dm.NT;
+  const int h = bh % dm.H, bb = bh / dm.H;
+  const int wv_id = wave_id();
+  const size_t blk = (size_t)bhn;
+  const size_t rsK = (size_t)dm.H * K, rsV = (size_t)dm.H * V;
+  const size_t t0 = (size_t)bb * dm.T + (size_t)n * C;
+
+  // kb = b k e^{gc}, wv = w v (rounded to the input dtype), raw v and w
+  float gcr[M::RS][8];
+  chunk_cumsum<C, K>(g + (t0 * dm.H + h) * K, rsK, gcr, sTot, sGl);
+  {
+    const int cg = tid % M::NCG, seg = tid / M::NCG;
+#pragma unroll
+    for (int rr = 0; rr < M::RS; ++rr) {
+      const int r = seg * M::RS + rr;
+      float kv[8], bv[8], kb[8];
+      load8(k + ((t0 + r) * dm.H + h) * K + cg * 8, kv);
+      load8(b + ((t0 + r) * dm.H + h) * K + cg * 8, bv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) kb[j] = (bv[j] * kv[j]) * __expf(gcr[rr][j]);
+      store8(sKB + r * L::LK + cg * 8, kb);
+    }
+  }
+  {
+    typedef ColMap<C, V> MV;
+    const int cg = tid % MV::NCG, seg = tid / MV::NCG;
+#pragma unroll
+    for (int rr = 0; rr < MV::RS; ++rr) {
+      const int r = seg * MV::RS + rr;
+      float vv[8], ww[8], wv[8];
+      load8(v + ((t0 + r) * dm.H + h) * V + cg * 8, vv);
+      load8(w + ((t0 + r) * dm.H + h) * V + cg * 8, ww);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) wv[j] = to_f(from_f<T>(ww[j] * vv[j]));
+      store8(sWV + r * L::LV + cg * 8, wv);
+    }
+  }
+  stage_rows<T, C, C>(sA, L::LC, ck.ainv + blk * C * C, C);
+  stage_convert<float, T, C, K>(sDW, L::LK, gr.dwt + blk * C * K, K);
+  stage_convert<float, T, C, V>(sDV, L::LV, gr.dvn + blk * C * V, V);
+  __syncthreads();
+
+  constexpr int MT = C / 16;
+  // dA = clip(dw_pseudo kb^T + dv wv^T)   (b3:163-172)
+  for (int tile = wv_id; tile < MT * MT; tile += 4) {
+    const int mi = tile / MT, nj = tile % MT;
+    f32x4 acc = tile_mma<T, false, false>(zero4(), sDW, L::LK, sKB, L::LK, 16 * mi, 16 * nj, K);
+    acc = tile_mma<T, false, false>(acc, sDV, L::LV, sWV, L::LV, 16 * mi, 16 * nj, V);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = sanitize(acc[i]);
+    store_tile_n(sDA, L::LC, 16 * mi, 16 * nj, acc);
+  }
+  // dkb = A^T dw_pseudo (A lower triangular, so rows i >= j only)   (b3:164)
+  {
+    constexpr int NTK = K / 16, TPW = MT * NTK / 4;
+    float* g_dkb = gr.dwt + blk * C * K;
+#pragma unroll 2
+    for (int t = 0; t < TPW; ++t) {
+      const int tile = wv_id * TPW + t, mj = tile % MT, ni = tile / MT;
+      const int k0 = tri_k0<T>(mj);
+      f32x4 acc = tile_mma<T, true, true>(zero4(), sA + k0 * L::LC, L::LC, sDW + k0 * L::LK, L::LK,
+                                          16 * mj, 16 * ni, C - k0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = n2n(acc[i]);
+      store_tile_n(g_dkb, K, 16 * mj, 16 * ni, acc);
+    }
+  }
+  // dwv = A^T dv ; dw = dwv * v, dv = dwv * w   (b3:167,194-195) + final sanitize / cast
+  {
+    constexpr int NTV = V / 16, TPW = MT * NTV / 4;
+    T* dwc = dw + (t0 * dm.H + h) * V;
+    T* dvc = dv + (t0 * dm.H + h) * V;
+    const T* vc = v + (t0 * dm.H + h) * V;
+    const T* wc = w + (t0 * dm.H + h) * V;
+#pragma unroll 2
+    for (int t = 0; t < TPW; ++t) {
+      const int tile = wv_id * TPW + t, mj = tile % MT, ni = tile / MT;
+      const int k0 = tri_k0<T>(mj);
+      f32x4 acc = tile_mma<T, true, true>(zero4(), sA + k0 * L::LC, L::LC, sDV + k0 * L::LV, L::LV,
+                                          16 * mj, 16 * ni, C - k0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * mj + tile_row(i), c = 16 * ni + tile_col();
+        const float gw = sanitize(n2n(acc[i] * to_f(vc[(size_t)r * rsV + c])));
+        const float gv = sanitize(n2n(acc[i] * to_f(wc[(size_t)r * rsV + c])));
+        dwc[(size_t)r * rsV + c] = from_f<T>(gw);
+        dvc[(size_t)r * rsV + c] = from_f<T>(gv);
+      }
+    }
+  }
+  __syncthreads();
+  // tmp = clip(dA A^T)   (b3:177-178); A[j][l] = 0 for l > j
+  for (int tile = wv_id; tile < MT * MT; tile += 4) {
+    const int mi = tile / MT, nj = tile % MT;
+    f32x4 acc = tile_mma<T, false, false>(zero4(), sDA, L::LC, sA, L::LC, 16 * mi, 16 * nj,
+                                          tri_k1<T>(nj, C));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = sanitize(acc[i]);
+    store_tile_n(sTmp, L::LC, 16 * mi, 16 * nj, acc);
+  }
+  __syncthreads();
+  // dAkk = n2n(-(A^T tmp) * strict)   (b3:179-180,212)
+  float* g_dakk = gr.dakk + blk * C * C;
+  for (int tile = wv_id; tile < MT * MT; tile += 4) {
+    const int mj = tile / MT, nl = tile % MT;
+    f32x4 acc = zero4();
+    if (nl <= mj) {
+      const int k0 = tri_k0<T>(mj);
+      acc = tile_mma<T, true, true>(acc, sA + k0 * L::LC, L::LC, sTmp + k0 * L::LC, L::LC, 16 * mj,
+                                    16 * nl, C - k0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * mj + tile_row(i), c = 16 * nl + tile_col();
+      acc[i] = r > c ? n2n(-acc[i]) : 0.f;
+    }
+    store_tile_n(g_dakk, C, 16 * mj, 16 * nl, acc);
+  }
+}
+
+// ------------------------------------------------------------------ B4 + combine + B5
+template <typename T, int C, int K>
+struct InLds {
+  static constexpr int PAD = Pad<T>::v;
+  static constexpr int LK = K + PAD, LC = C + PAD, LG = K + 4;
+  static constexpr int OK_ = C * LK * (int)sizeof(T), OC = C * LC * (int)sizeof(T);
+  static constexpr int off_q = 0;            // q e^{gc}  (then raw q)
+  static constexpr int off_kt = off_q + OK_; // k e^{-gc} (then raw k)
+  static constexpr int off_kb = off_kt + OK_;// b k e^{gc} (then raw b)
+  static constexpr int off_daqk = off_kb + OK_;
+  static constexpr int off_dakk = off_daqk + OC;
+  static constexpr int off_gc = off_dakk + OC;   // fp32 gc, then fp32 dgc
+  static constexpr int off_tot = off_gc + C * LG * 4;
+  static constexpr int off_gl = off_tot + ColMap<C, K>::NSEG * K * 4;
+  static constexpr int off_part = off_gl + K * 4;  // [4][K] column partial sums
+  static constexpr int total = off_part + 4 * K * 4;
+};
+
+template <typename T, int C, int K, int V>
+__global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> gr,
+                                                     const T* __restrict__ q, const T* __restrict__ k,
+                                                     const T* __restrict__ b, const float* __restrict__ g,
+                                                     T* __restrict__ dq, T* __restrict__ dk,
+                                                     T* __restrict__ db, float* __restrict__ dg) {
+  typedef InLds<T, C, K> L;
+  typedef ColMap<C, K> M;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
+  T* sQ = reinterpret_cast<T*>(lds + L::off_q);
+  T* sKt = reinterpret_cast<T*>(lds + L::off_kt);
+  T* sKB = reinterpret_cast<T*>(lds + L::off_kb);
+  T* sDAqk = reinterpret_cast<T*>(lds + L::off_daqk);
+  T* sDAkk = reinterpret_cast<T*>(lds + L::off_dakk);
+  float* sGc = reinterpret_cast<float*>(lds + L::off_gc);
+  float* sTot = reinterpret_cast<float*>(lds + L::off_tot);
+  float* sGl = reinterpret_cast<float*>(lds + L::off_gl);
+  float* sPart = reinterpret_cast<float*>(lds + L::off_part);
+
+  const int tid = threadIdx.x;
+  const int bhn = blockIdx.x;
+  const int n = bhn % dm.NT;
+  const int bh = bhn / dm.NT;
+  const int h = bh % dm.H, bb = bh / dm.H;
+  const int wv_id = wave_id();
+  const size_t blk = (size_t)bhn;
+  const size_t rsK = (size_t)dm.H * K;
+  const size_t t0 = (size_t)bb * dm.T + (size_t)n * C;
+  const size_t base = (t0 * dm.H + h) * K;
+
+  float gcr[M::RS][8];
+  const bool exact = chunk_cumsum<C, K>(g + base, rsK, gcr, sTot, sGl);
+  const int cg = tid % M::NCG, seg = tid / M::NCG;
+#pragma unroll
+  for (int rr = 0; rr < M::RS; ++rr) {
+    const int r = seg * M::RS + rr;
+    float qv[8], kv[8], bv[8], o1[8], o2[8], o3[8];
+    load8(q + base + (size_t)r * rsK + cg * 8, qv);
+    load8(k + base + (size_t)r * rsK + cg * 8, kv);
+    load8(b + base + (size_t)r * rsK + cg * 8, bv);
+    if (!exact) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float e = __expf(gcr[rr][j]);
+        o1[j] = qv[j] * e;
+        o2[j] = kv[j] * __expf(-gcr[rr][j]);
+        o3[j] = (bv[j] * kv[j]) * e;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { o1[j] = qv[j]; o2[j] = kv[j]; o3[j] = bv[j]; }
+    }
+    store8(sQ + r * L::LK + cg * 8, o1);
+    store8(sKt + r * L::LK + cg * 8, o2);
+    store8(sKB + r * L::LK + cg * 8, o3);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sGc[r * L::LG + cg * 8 + j] = gcr[rr][j];
+  }
+  // scale folded into the dAqk operand: Aqk = scale Q~ K~^T
+  stage_convert<float, T, C, C>(sDAqk, L::LC, gr.daqk + blk * C * C, C, dm.scale);
+  stage_convert<float, T, C, C>(sDAkk, L::LC, gr.dakk + blk * C * C, C);
+  __syncthreads();
+
+  // Tiles of [C][K], column-major over tiles so each wave owns whole columns.
+  constexpr int MT = C / 16, NTK = K / 16;
+  constexpr int TPW = MT * NTK / 4;
+  static_assert((MT * NTK) % 4 == 0 && TPW % MT == 0, "each wave must own whole tile columns");
+  f32x4 dQt[TPW], dKt[TPW], dKB[TPW];
+  if (!exact) {
+    // dQ~ = (scale dAqk) K~ ; dK~ = (scale dAqk)^T Q~ + dAkk^T KB ; dKB = dAkk K~
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int tile = wv_id * TPW + t, mi = tile % MT, ni = tile / MT;
+      const int k1 = tri_k1<T>(mi, C);   // dA* lower triangular: j <= i
+      const int k0 = tri_k0<T>(mi);      // transposed use: i >= j
+      dQt[t] = tile_mma<T, false, true>(zero4(), sDAqk, L::LC, sKt, L::LK, 16 * mi, 16 * ni, k1);
+      dKB[t] = tile_mma<T, false, true>(zero4(), sDAkk, L::LC, sKt, L::LK, 16 * mi, 16 * ni, k1);
+      f32x4 a = tile_mma<T, true, true>(zero4(), sDAqk + k0 * L::LC, L::LC, sQ + k0 * L::LK, L::LK,
+                                        16 * mi, 16 * ni, C - k0);
+      dKt[t] = tile_mma<T, true, true>(a, sDAkk + k0 * L::LC, L::LC, sKB + k0 * L::LK, L::LK,
+                                       16 * mi, 16 * ni, C - k0);
+    }
+  }
+  __syncthreads();
+  // raw q, k, b for the element-wise stage (fp32 exact multipliers)
+  stage_rows<T, C, K>(sQ, L::LK, q + base, rsK);
+  stage_rows<T, C, K>(sKt, L::LK, k + base, rsK);
+  stage_rows<T, C, K>(sKB, L::LK, b + base, rsK);
+  __syncthreads();
+
+  const float* g_dqg = gr.dqg + blk * C * K;
+  const float* g_dkb = gr.dwt + blk * C * K;
+  const float* g_dkg = gr.dkg + blk * C * K;
+  float colsum[TPW / MT];
+  f32x4 dgcr[TPW];  // written to LDS only after every lane has read gc
+#pragma unroll
+  for (int c = 0; c < TPW / MT; ++c) colsum[c] = 0.f;
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int tile = wv_id * TPW + t, mi = tile % MT, ni = tile / MT;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * mi + tile_row(i), d = 16 * ni + tile_col();
+      const float gcv = sGc[r * L::LG + d];
+      const float e = __expf(gcv), ei = __expf(-gcv), eg = __expf(sGl[d] - gcv);
+      const float qv = to_f(sQ[r * L::LK + d]), kv = to_f(sKt[r * L::LK + d]),
+                  bv = to_f(sKB[r * L::LK + d]);
+      // B4 (kernel_bwd_b4_intra.py:101-132)
+      float dq4, dk4, db4, dgc4;
+      if (!exact) {
+        dq4 = dQt[t][i] * e;
+        dk4 = dKt[t][i] * ei + dKB[t][i] * bv * e;
+        db4 = dKB[t][i] * kv * e;
+        dgc4 = dQt[t][i] * (qv * e) - dKt[t][i] * (kv * ei) + dKB[t][i] * (bv * kv * e);
+      } else {
+        // pairwise with exp(clip(gc_i - gc_j, -20, 20)) and the clip mask
+        float sq = 0.f, sb = 0.f, sk = 0.f, sgi = 0.f, sgj = 0.f;
+        for (int j = 0; j <= r; ++j) {
+          const float dd = gcv - sGc[j * L::LG + d];
+          const float E = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
+          const float msk = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
+          const float kj = to_f(sKt[j * L::LK + d]);
+          const float aq = to_f(sDAqk[r * L::LC + j]);  // holds scale * dAqk
+          const float ak = (j < r) ? to_f(sDAkk[r * L::LC + j]) : 0.f;
+          sq += aq * E * kj;
+          sb += ak * E * kj;
+          sgi += (aq * qv + ak * bv * kv) * E * kj * msk;
+        }
+        for (int i2 = r; i2 < C; ++i2) {
+          const float dd = sGc[i2 * L::LG + d] - gcv;
+          const float E = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
+          const float msk = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
+          const float aq = to_f(sDAqk[i2 * L::LC + r]);
+          const float ak = (i2 > r) ? to_f(sDAkk[i2 * L::LC + r]) : 0.f;
+          const float li = aq * to_f(sQ[i2 * L::LK + d]) +
+                           ak * to_f(sKB[i2 * L::LK + d]) * to_f(sKt[i2 * L::LK + d]);
+          sk += li * E;
+          sgj += li * E * kv * msk;
+        }
+        dq4 = sq;
+        dk4 = sk + sb * bv;
+        db4 = sb * kv;
+        dgc4 = sgi - sgj;
+      }
+      dq4 = sanitize(dq4); dk4 = sanitize(dk4); db4 = sanitize(db4); dgc4 = sanitize(dgc4);
+      // B3 element-wise terms (kernel_bwd_b3_wy_dqkg.py:182-198)
+      const size_t o = (size_t)r * K + d;
+      const float dqg = g_dqg[o], dkb = g_dkb[o], dkg = g_dkg[o];
+      const float kgv = kv * eg;
+      const float dq3 = n2n(dqg * e);
+      const float dk3 = n2n(dkb * e * bv + dkg * eg);
+      const float db3 = n2n(dkb * e * kv);
+      const float dx = dkg * kgv;
+      const float dgc3 = dkb * (bv * kv * e) + dqg * (qv * e) - dx;
+      colsum[t / MT] += dx;
+      const size_t go = base + (size_t)r * rsK + d;
+      dq[go] = from_f<T>(sanitize(dq3 + dq4));
+      dk[go] = from_f<T>(sanitize(dk3 + dk4));
+      db[go] = from_f<T>(sanitize(db3 + db4));
+      dgcr[t][i] = dgc3 + dgc4;
+    }
+  }
+  __syncthreads();  // the exact path reads gc of other rows: finish all reads first
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int tile = wv_id * TPW + t, mi = tile % MT, ni = tile / MT;
+    store_tile_n(sGc, L::LG, 16 * mi, 16 * ni, dgcr[t]);
+  }
+  // gc_last row terms: sum_i dkg * kg + exp(gc_last) sum_v dh_next h_pre   (b3:189,200-205)
+#pragma unroll
+  for (int c = 0; c < TPW / MT; ++c) {
+    const int ni = (wv_id * TPW) / MT + c;
+    sPart[(lane_id() >> 4) * K + 16 * ni + tile_col()] = colsum[c];
+  }
+  __syncthreads();
+  if (tid < K) {
+    const float extra = sPart[tid] + sPart[K + tid] + sPart[2 * K + tid] + sPart[3 * K + tid] +
+                        gr.rlast[blk * K + tid];
+    // dgc3 gets the row term before its n2n in the reference; dgc4 is already
+    // sanitized, so the sum below matches dgc3 + dgc4 in unclipped regimes.
+    sGc[(C - 1) * L::LG + tid] += extra;
+  }
+  __syncthreads();
+  // B5: dg = sanitize(reverse cumsum over the chunk)   (kernel_bwd_b5_reverse_cumsum.py:17-24)
+  if (tid < K) {
+    const int d = tid;
+    float s = 0.f;
+    for (int r = C - 1; r >= 0; --r) {
+      s += sGc[r * L::LG + d];
+      dg[base + (size_t)r * rsK + d] = sanitize(s);
+    }
+  }
+}
+
+}  // namespace ah

@@ -26,6 +26,61 @@ namespace ah {
 
 constexpr float kFactorLimit = 64.f;
 
+// ------------------------------------------------------------------ cumsum
+// Thread map for [C][K] fp32 element-wise passes: column group cg (8
+// columns), segment seg (RS consecutive rows).
+template <int C, int K>
+struct ColMap {
+  static constexpr int NCG = K / 8, NSEG = 256 / NCG, RS = C / NSEG;
+  static_assert(RS >= 1, "chunk too small for the thread mapping");
+};
+
+// gc = cumsum(g) over one chunk (gdn2_wy_reference.py:63) for this thread's
+// RS rows x 8 columns.  Writes gc_last to sGl[K] (sTot: NSEG*K floats of
+// scratch).  Returns, uniformly over the workgroup, whether the factorised
+// pairwise decay is unsafe for this chunk: some g > 0, or gc_last below
+// -kFactorLimit in some column.
+template <int C, int K>
+__device__ __forceinline__ bool chunk_cumsum(const float* __restrict__ g, size_t rs,
+                                             float (&gcr)[ColMap<C, K>::RS][8], float* sTot,
+                                             float* sGl) {
+  typedef ColMap<C, K> M;
+  const int tid = threadIdx.x, cg = tid % M::NCG, seg = tid / M::NCG;
+  bool positive = false;
+#pragma unroll
+  for (int rr = 0; rr < M::RS; ++rr) {
+    load8(g + (size_t)(seg * M::RS + rr) * rs + cg * 8, gcr[rr]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) positive |= gcr[rr][j] > 0.f;
+  }
+#pragma unroll
+  for (int rr = 1; rr < M::RS; ++rr)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) gcr[rr][j] += gcr[rr - 1][j];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sTot[seg * K + cg * 8 + j] = gcr[M::RS - 1][j];
+  __syncthreads();
+  float off[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) off[j] = 0.f;
+  for (int s = 0; s < seg; ++s)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) off[j] += sTot[s * K + cg * 8 + j];
+#pragma unroll
+  for (int rr = 0; rr < M::RS; ++rr)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) gcr[rr][j] += off[j];
+  bool too_deep = false;
+  if (seg == M::NSEG - 1) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      sGl[cg * 8 + j] = gcr[M::RS - 1][j];
+      too_deep |= gcr[M::RS - 1][j] < -kFactorLimit;
+    }
+  }
+  return __syncthreads_or(positive || too_deep);
+}
+
 // ------------------------------------------------------------------ layout
 template <typename T, int C, int K, int V>
 struct IntraLds {
@@ -118,41 +173,7 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
   // ---- phase 0: gc = cumsum(g) over the chunk (gdn2_wy_reference.py:63)
   const int cg = tid % L::NCG, seg = tid / L::NCG;
   float gcr[L::RS][8];
-  bool positive = false;
-#pragma unroll
-  for (int rr = 0; rr < L::RS; ++rr) {
-    load8(gc_in + (size_t)(seg * L::RS + rr) * rsK + cg * 8, gcr[rr]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) positive |= gcr[rr][j] > 0.f;
-  }
-#pragma unroll
-  for (int rr = 1; rr < L::RS; ++rr)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) gcr[rr][j] += gcr[rr - 1][j];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) sTot[seg * K + cg * 8 + j] = gcr[L::RS - 1][j];
-  __syncthreads();
-  {
-    float off[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) off[j] = 0.f;
-    for (int s = 0; s < seg; ++s)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) off[j] += sTot[s * K + cg * 8 + j];
-#pragma unroll
-    for (int rr = 0; rr < L::RS; ++rr)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) gcr[rr][j] += off[j];
-  }
-  bool too_deep = false;
-  if (seg == L::NSEG - 1) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      sGl[cg * 8 + j] = gcr[L::RS - 1][j];
-      too_deep |= gcr[L::RS - 1][j] < -kFactorLimit;
-    }
-  }
-  const bool exact = __syncthreads_or(positive || too_deep);
+  const bool exact = chunk_cumsum<C, K>(gc_in, rsK, gcr, sTot, sGl);
   if (tid < K) ck.gcl[(size_t)bhn * K + tid] = sGl[tid];
 
   // ---- phase 1: elementwise operands (gdn2_wy_reference.py:92-100)
@@ -529,7 +550,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     if (save) unstage_rows<T, VT, C>(ck.vnT + bhn * V * C + (size_t)v0 * C, C, sVn, L::LC);
 
     // o = scale qg h + Aqk v_new   (rows of the qg half)
-    float* og = o + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0;
+    float* og = o ? o + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0 : nullptr;
 #pragma unroll
     for (int t = 0; t < XPW; ++t) {
       const int tile = wv_id * XPW + t, mi = tile / NTI, ni = tile % NTI;
@@ -539,10 +560,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         kr = ((kr + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
         if (kr > C) kr = C;
         f32x4 acc = tile_mma<T, false, false>(xo[t], sAqk, L::LC, sVn, L::LC, 16 * mo, 16 * ni, kr);
+        if (og) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 16 * mo + tile_row(i), c = 16 * ni + tile_col();
-          og[(size_t)r * dm.H * V + c] = n2n(acc[i]);
+          for (int i = 0; i < 4; ++i) {
+            const int r = 16 * mo + tile_row(i), c = 16 * ni + tile_col();
+            og[(size_t)r * dm.H * V + c] = n2n(acc[i]);
+          }
         }
       }
     }
@@ -568,13 +591,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     if (n + 1 < dm.NT) commit();
     __syncthreads();
   }
+  if (h_final) {
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
+    for (int t = 0; t < TPW; ++t) {
+      const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = 16 * mi + tile_row(i), vv = v0 + 16 * ni + tile_col();
-      h_final[((size_t)bh * K + d) * V + vv] = hs[t][i];
+      for (int i = 0; i < 4; ++i) {
+        const int d = 16 * mi + tile_row(i), vv = v0 + 16 * ni + tile_col();
+        h_final[((size_t)bh * K + d) * V + vv] = hs[t][i];
+      }
     }
   }
 }

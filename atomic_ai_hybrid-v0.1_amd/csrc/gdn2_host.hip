@@ -1,7 +1,7 @@
 // Host side of the GDN2 chunk pipeline: argument checks, workspace layout,
 // template dispatch and the extern "C" entry points of include/atomic_hybrid.h.
 #include "../../include/atomic_hybrid.h"
-#include "gdn2_fwd.hip"
+#include "gdn2_bwd.hip"
 
 namespace ah {
 
@@ -14,7 +14,7 @@ struct Gdn2Plan {
   // forward intermediates
   size_t o_qg, o_kg, o_wt, o_u, o_aqk, o_ainv, o_gcl, o_ht, o_vnt, fwd_end;
   // backward scratch
-  size_t o_dvn, o_dht, o_dqg, o_dwt, o_dkg, o_daqk, o_rlast, total;
+  size_t o_dvn, o_dht, o_dqg, o_dwt, o_dkg, o_daqk, o_dakk, o_rlast, total;
 };
 
 static int gdn2_plan(const atomic_gdn2_args* a, Gdn2Plan* p) {
@@ -51,6 +51,7 @@ static int gdn2_plan(const atomic_gdn2_args* a, Gdn2Plan* p) {
   p->o_dwt = take(N * C * K * 4);
   p->o_dkg = take(N * C * K * 4);
   p->o_daqk = take(N * C * C * 4);
+  p->o_dakk = take(N * C * C * 4);
   p->o_rlast = take(N * K * 4);
   p->total = off;
   return ATOMIC_OK;
@@ -86,6 +87,73 @@ static int gdn2_forward_impl(const Gdn2Plan& p, const void* q, const void* k, co
                      h_final, save);
   if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
   return ATOMIC_OK;
+}
+
+template <typename T>
+static Gdn2Grads<T> gdn2_grads(const Gdn2Plan& p, void* ws) {
+  char* base = static_cast<char*>(ws);
+  Gdn2Grads<T> g;
+  g.dvn = reinterpret_cast<float*>(base + p.o_dvn);
+  g.dhT = reinterpret_cast<T*>(base + p.o_dht);
+  g.dqg = reinterpret_cast<float*>(base + p.o_dqg);
+  g.dwt = reinterpret_cast<float*>(base + p.o_dwt);
+  g.dkg = reinterpret_cast<float*>(base + p.o_dkg);
+  g.daqk = reinterpret_cast<float*>(base + p.o_daqk);
+  g.dakk = reinterpret_cast<float*>(base + p.o_dakk);
+  g.rlast = reinterpret_cast<float*>(base + p.o_rlast);
+  return g;
+}
+
+template <typename T, typename TD, int K>
+static int gdn2_backward_impl(const Gdn2Plan& p, const void* q, const void* k, const void* v,
+                              const void* w, const void* b, const float* g, const float* h0,
+                              const void* dO, const float* dh_final, void* dq, void* dk, void* dv,
+                              void* dw, void* db, float* dg, float* dh0, void* ws, bool reuse,
+                              hipStream_t st) {
+  constexpr int C = 64, V = K, VT = 32;
+  Gdn2Chunks<T> ck = gdn2_chunks<T>(p, ws);
+  Gdn2Grads<T> gr = gdn2_grads<T>(p, ws);
+  if (!reuse) {
+    // recompute the forward intermediates (the reference's residuals are the
+    // inputs only, kernel_trainable_B6.py:91-94,104-111)
+    const int rc = gdn2_forward_impl<T, K>(p, q, k, v, w, b, g, h0, nullptr, nullptr, ws, 1, st);
+    if (rc != ATOMIC_OK) return rc;
+  }
+  const unsigned nseq = (unsigned)(p.dm.B * p.dm.H * (V / VT));
+  const unsigned nblk = (unsigned)p.bhn;
+  hipLaunchKernelGGL((gdn2_bwd_dh<T, TD, C, K, V, VT>), dim3(nseq), dim3(256), 0, st, p.dm, ck, gr,
+                     (const TD*)dO, dh_final, dh0);
+  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
+  hipLaunchKernelGGL((gdn2_bwd_hgrad<T, TD, C, K, V>), dim3(nblk), dim3(256), 0, st, p.dm, ck, gr,
+                     (const TD*)dO);
+  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
+  hipLaunchKernelGGL((gdn2_bwd_wy<T, C, K, V>), dim3(nblk), dim3(256), 0, st, p.dm, ck, gr,
+                     (const T*)k, (const T*)v, (const T*)w, (const T*)b, g, (T*)dw, (T*)dv);
+  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
+  hipLaunchKernelGGL((gdn2_bwd_intra<T, C, K, V>), dim3(nblk), dim3(256), 0, st, p.dm, gr,
+                     (const T*)q, (const T*)k, (const T*)b, g, (T*)dq, (T*)dk, (T*)db, dg);
+  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
+  return ATOMIC_OK;
+}
+
+int gdn2_backward(const Gdn2Plan& p, int dtype, int do_dtype, const void* q, const void* k,
+                  const void* v, const void* w, const void* b, const float* g, const float* h0,
+                  const void* dO, const float* dh_final, void* dq, void* dk, void* dv, void* dw,
+                  void* db, float* dg, float* dh0, void* ws, bool reuse, hipStream_t st) {
+#define AH_GDN2_BWD(T, TD, KK) \
+  return gdn2_backward_impl<T, TD, KK>(p, q, k, v, w, b, g, h0, dO, dh_final, dq, dk, dv, dw, db, dg, dh0, ws, reuse, st)
+  if (dtype == ATOMIC_BF16) {
+    if (p.dm.K == 128) {
+      if (do_dtype == ATOMIC_BF16) AH_GDN2_BWD(bf16, bf16, 128);
+      AH_GDN2_BWD(bf16, float, 128);
+    }
+    if (do_dtype == ATOMIC_BF16) AH_GDN2_BWD(bf16, bf16, 64);
+    AH_GDN2_BWD(bf16, float, 64);
+  }
+  if (p.dm.K != 64) return ATOMIC_ERR_SHAPE;  // fp32 backward: the per-chunk tiles fit LDS for K = 64
+  if (do_dtype == ATOMIC_BF16) AH_GDN2_BWD(float, bf16, 64);
+  AH_GDN2_BWD(float, float, 64);
+#undef AH_GDN2_BWD
 }
 
 int gdn2_forward(const Gdn2Plan& p, int dtype, const void* q, const void* k, const void* v,
@@ -131,4 +199,21 @@ extern "C" int atomic_gdn2_fwd(const atomic_gdn2_args* a, const void* q, const v
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
   return gdn2_forward(p, a->dtype, q, k, v, w, b, g, h0, o, h_final, workspace,
                       (a->flags & ATOMIC_GDN2_SAVE) ? 1 : 0, (hipStream_t)stream);
+}
+
+extern "C" int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
+                               const void* w, const void* b, const float* g, const float* h0,
+                               const void* dO, const float* dh_final, void* dq, void* dk, void* dv,
+                               void* dw, void* db, float* dg, float* dh0, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  Gdn2Plan p;
+  const int rc = gdn2_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (a->dtype == ATOMIC_F32 && a->dk != 64) return ATOMIC_ERR_SHAPE;
+  if (!q || !k || !v || !w || !b || !g || !dO || !dq || !dk || !dv || !dw || !db || !dg)
+    return ATOMIC_ERR_NULL;
+  if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
+  return gdn2_backward(p, a->dtype, a->do_dtype, q, k, v, w, b, g, h0, dO, dh_final, dq, dk, dv, dw,
+                       db, dg, dh0, workspace, (a->flags & ATOMIC_GDN2_REUSE) != 0,
+                       (hipStream_t)stream);
 }
