@@ -1,0 +1,52 @@
+"""Drop-in trainable GDN2 op (mirror of reference atomic_ops/kernel_trainable_B6.py).
+
+``gdn2_pallas_forward_trainable(q, k, v, w, b, g, scale, h0=None)`` keeps the
+reference signature and argument order (kernel_trainable_B6.py:187-194) and
+returns ``(o, h_final)``; its backward returns ``(dq, dk, dv, dw, db, dg, dh0)``
+cast to the primals' dtypes after the final clip(+-1e4) / nan_to_num
+(kernel_trainable_B6.py:173-181).  ``scale`` is not differentiable
+(kernel_trainable_B6.py:86).  Forward and backward run in libatomic_hybrid.so;
+the forward keeps its per-chunk intermediates for the backward instead of
+recomputing them (the reference recomputes; both give the same gradient).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import gdn2 as _g
+
+
+class _Gdn2Core(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, w, b, g, scale, h0):
+        need = any(ctx.needs_input_grad)
+        o, h_final, ws = _g.forward(q, k, v, w, b, g, scale, h0, save=need)
+        if need:
+            ctx.save_for_backward(q, k, v, w, b, g, h0)
+            ctx.ws = ws
+            ctx.scale = scale
+        return o, h_final
+
+    @staticmethod
+    def backward(ctx, do, dh_final):
+        q, k, v, w, b, g, h0 = ctx.saved_tensors
+        grads = _g.backward(q, k, v, w, b, g, ctx.scale, do, dh_final=dh_final, h0=h0,
+                            workspace=ctx.ws, reuse=True)
+        ctx.ws = None
+        dq, dk, dv, dw, db, dg, dh0 = grads
+        return dq, dk, dv, dw, db, dg, None, dh0.to(h0.dtype)
+
+
+def gdn2_pallas_forward_trainable(q, k, v, w, b, g, scale, h0=None):
+    """q, k, b, g: [B, T, H, K]; v, w: [B, T, H, V]; h0: [B, H, K, V] fp32
+    (zeros when None).  Returns o [B, T, H, V] fp32 and h_final [B, H, K, V]."""
+    B, T, H, K = q.shape
+    if h0 is None:
+        h0 = torch.zeros(B, H, K, v.shape[-1], dtype=torch.float32, device=q.device)
+    return _Gdn2Core.apply(q, k, v, w, b, g, scale, h0)
+
+
+def gdn2_pallas_forward(q, k, v, w, b, g, scale, h0=None):
+    """Forward only (reference kernel_d_pipeline.py:161-196)."""
+    o, h_final, _ = _g.forward(q, k, v, w, b, g, scale, h0)
+    return o, h_final

@@ -21,22 +21,6 @@
 
 namespace ah {
 
-// Elementwise copy of a [R][D] block into LDS converting to the operand type
-// (optionally scaled).
-template <typename TS, typename T, int R, int D>
-__device__ __forceinline__ void stage_convert(T* dst, int ld, const TS* src, size_t src_ld,
-                                              float mul = 1.f) {
-  constexpr int PER_ROW = D / 8;
-  for (int e = threadIdx.x; e < R * PER_ROW; e += 256) {
-    const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
-    float x[8];
-    load8(src + (size_t)r * src_ld + c, x);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] *= mul;
-    store8(dst + r * ld + c, x);
-  }
-}
-
 // First k (rounded down to the MFMA k step) of a lower-triangular operand
 // whose nonzeros start at row 16 * tile.
 template <typename T>

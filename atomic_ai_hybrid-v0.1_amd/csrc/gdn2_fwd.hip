@@ -387,69 +387,6 @@ struct StateLds {
   static constexpr int total = off_gl + K * 4;
 };
 
-// A [R][D] block moved global -> registers -> LDS in 16-byte pieces, so the
-// next chunk's loads can be in flight while the current chunk computes.
-template <typename T, int R, int D>
-struct RegStage {
-  static constexpr int VEC = 16 / (int)sizeof(T);
-  static constexpr int PER_ROW = D / VEC;
-  static constexpr int N = R * PER_ROW;
-  static constexpr int PT = (N + 255) / 256;
-  uint4 r[PT];
-  __device__ __forceinline__ void load(const T* src, size_t ld) {
-#pragma unroll
-    for (int i = 0; i < PT; ++i) {
-      const int e = threadIdx.x + 256 * i;
-      if (N % 256 == 0 || e < N)
-        r[i] = *reinterpret_cast<const uint4*>(src + (size_t)(e / PER_ROW) * ld + (e % PER_ROW) * VEC);
-    }
-  }
-  __device__ __forceinline__ void store(T* dst, int ld) const {
-#pragma unroll
-    for (int i = 0; i < PT; ++i) {
-      const int e = threadIdx.x + 256 * i;
-      if (N % 256 == 0 || e < N)
-        *reinterpret_cast<uint4*>(dst + (e / PER_ROW) * ld + (e % PER_ROW) * VEC) = r[i];
-    }
-  }
-};
-
-// Copy a [R][D] block (row stride `src_ld`) into LDS rows of length `dst_ld`.
-template <typename T, int R, int D>
-__device__ __forceinline__ void stage_rows(T* dst, int dst_ld, const T* src, size_t src_ld) {
-  constexpr int VEC = 16 / sizeof(T);
-  constexpr int PER_ROW = D / VEC;
-  for (int e = threadIdx.x; e < R * PER_ROW; e += 256) {
-    const int r = e / PER_ROW, c = (e % PER_ROW) * VEC;
-    *reinterpret_cast<uint4*>(dst + r * dst_ld + c) =
-        *reinterpret_cast<const uint4*>(src + r * src_ld + c);
-  }
-}
-template <typename T, int R, int D>
-__device__ __forceinline__ void unstage_rows(T* dst, size_t dst_ld, const T* src, int src_ld) {
-  constexpr int VEC = 16 / sizeof(T);
-  constexpr int PER_ROW = D / VEC;
-  for (int e = threadIdx.x; e < R * PER_ROW; e += 256) {
-    const int r = e / PER_ROW, c = (e % PER_ROW) * VEC;
-    *reinterpret_cast<uint4*>(dst + r * dst_ld + c) =
-        *reinterpret_cast<const uint4*>(src + r * src_ld + c);
-  }
-}
-
-// Workgroup -> (bh, vt) so that the V tiles of one head share an XCD (and
-// its L2): consecutive workgroup ids are dealt round-robin over 8 XCDs.
-__device__ __forceinline__ void xcd_group_map(int x, int groups, int per_group, int& grp, int& mem) {
-  const int total = groups * per_group;
-  if (per_group > 1 && total % (8 * per_group) == 0) {
-    const int xcd = x % 8, slot = x / 8;
-    grp = xcd * (total / (8 * per_group)) + slot / per_group;
-    mem = slot % per_group;
-  } else {
-    grp = x / per_group;
-    mem = x % per_group;
-  }
-}
-
 template <typename T, int C, int K, int V, int VT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T> ck,
                                                      const float* __restrict__ h0, float* __restrict__ o,

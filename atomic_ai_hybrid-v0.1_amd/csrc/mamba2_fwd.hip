@@ -1,0 +1,309 @@
+// Mamba2 SSD chunk-scan forward for gfx950.
+//
+// mamba2_cb    one workgroup per (batch, chunk): CB = sanitize(C B^T), the
+//              [C][C] score shared by every head (mamba2_ssd_reference.py:122-123;
+//              the reference's M3 broadcasts B/C to every head instead,
+//              kernel_mamba2_b_intra.py:136-142).
+// mamba2_scan  one workgroup per (batch, head, PT channels), sequential over
+//              chunks; the fp32 [PT][N] state stays in MFMA accumulators.  Per
+//              chunk it follows _chunk_ssd (mamba2_ssd_reference.py:70-149):
+//                cum    = sanitize(cumsum(sanitize(dt A, 20)), 1e4)
+//                y_diag = sum_{j<=i} exp(clip(cum_i - cum_j, +-20)) CB_ij dBx_j
+//                state_end = sum_j B_j (dBx_j exp(clip(cum_last - cum_j, +-20)))
+//                y_off  = (C state_prev) exp(clip(cum, -20, 0))
+//                state  = sanitize(state exp(clip(cum_last, -20, 0)) + state_end)
+//              y_diag is split into 16-row blocks.  For a source block J below
+//              the output block I the decay factorises as
+//              exp(cum_i - cum_r) exp(cum_r - cum_j) with r the first row of I;
+//              both factors are <= 1 whenever dt A <= 0 (the model's A < 0,
+//              dt > 0), so the off-diagonal part is one bf16 MFMA GEMM per block
+//              with no overflow.  Pairs there whose decay is below -20 carry
+//              their true weight instead of the reference's exp(-20) floor
+//              (a difference below 2e-9 |CB dBx|).  Diagonal 16x16 blocks are
+//              evaluated pairwise exactly as the reference does.  A chunk with
+//              any dt A > 0 evaluates every pair that way.
+#include "mamba2.hpp"
+
+namespace ah {
+
+template <typename T, int C, int N>
+__global__ __launch_bounds__(256) void mamba2_cb(Mamba2Dims dm, const T* __restrict__ Bm,
+                                                const T* __restrict__ Cm, Mamba2Chunks<T> ck) {
+  constexpr int PAD = Pad<T>::v, LN = N + PAD;
+  __shared__ __attribute__((aligned(16))) T sB[C * LN];
+  __shared__ __attribute__((aligned(16))) T sC[C * LN];
+  const int bn = blockIdx.x;  // b * NT + n
+  const size_t row0 = (size_t)bn * C;  // rows of [B*T][N]
+  constexpr int VEC = 16 / sizeof(T), PER_ROW = N / VEC;
+  for (int e = threadIdx.x; e < C * PER_ROW; e += 256) {
+    const int r = e / PER_ROW, c = (e % PER_ROW) * VEC;
+    *reinterpret_cast<uint4*>(sB + r * LN + c) = *reinterpret_cast<const uint4*>(Bm + (row0 + r) * N + c);
+    *reinterpret_cast<uint4*>(sC + r * LN + c) = *reinterpret_cast<const uint4*>(Cm + (row0 + r) * N + c);
+  }
+  __syncthreads();
+  constexpr int MT = C / 16;
+  T* out = ck.cb + (size_t)bn * C * C;
+  for (int tile = wave_id(); tile < MT * MT; tile += 4) {
+    const int mi = tile / MT, nj = tile % MT;
+    f32x4 acc = tile_mma<T, false, false>(zero4(), sC, LN, sB, LN, 16 * mi, 16 * nj, N);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = sanitize(acc[i]);
+    store_tile_n(out, C, 16 * mi, 16 * nj, acc);
+  }
+}
+
+// Rows of the block-I operand Z^(I) (source rows j < 16 I, padded to the MFMA k step).
+template <typename T>
+__host__ __device__ constexpr int zrows(int I) {
+  return ((16 * I + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
+}
+template <typename T>
+__host__ __device__ constexpr int zrows_before(int I) {
+  int s = 0;
+  for (int i = 1; i < I; ++i) s += zrows<T>(i);
+  return s;
+}
+
+template <typename T, int C, int N, int PT>
+struct ScanLds {
+  static constexpr int PAD = Pad<T>::v;
+  static constexpr int LN = N + PAD, LCB = C + PAD, LPT = PT + PAD;
+  static constexpr int NB = C / 16;
+  static constexpr int ZROWS = zrows_before<T>(NB);
+  static constexpr int NSEG = 256 / PT, RS = C / NSEG;
+  static constexpr int off_b = 0;
+  static constexpr int off_cb = off_b + C * LN * (int)sizeof(T);
+  static constexpr int off_z = off_cb + C * LCB * (int)sizeof(T);
+  static constexpr int off_w = off_z + ZROWS * LPT * (int)sizeof(T);
+  static constexpr int off_st = off_w + C * LPT * (int)sizeof(T);
+  static constexpr int off_cum = off_st + N * LPT * (int)sizeof(T);
+  static constexpr int off_dbx = off_cum + C * PT * 4;
+  static constexpr int off_tot = off_dbx + C * PT * 4;
+  static constexpr int total = off_tot + NSEG * PT * 4;
+  static_assert(RS >= 1 && C % NSEG == 0, "scan mapping");
+};
+
+// Inclusive column scan of sCum ([C][PT] fp32, holding sanitize(dt A, 20) on
+// entry) into sanitize(cumsum, 1e4).  Thread map: column tid % PT, RS rows.
+template <int C, int PT>
+__device__ __forceinline__ void column_cumsum(float* sCum, float* sTot) {
+  constexpr int NSEG = 256 / PT, RS = C / NSEG;
+  const int p = threadIdx.x % PT, seg = threadIdx.x / PT;
+  float v[RS];
+#pragma unroll
+  for (int r = 0; r < RS; ++r) v[r] = sCum[(seg * RS + r) * PT + p];
+#pragma unroll
+  for (int r = 1; r < RS; ++r) v[r] += v[r - 1];
+  sTot[seg * PT + p] = v[RS - 1];
+  __syncthreads();
+  float off = 0.f;
+  for (int s = 0; s < seg; ++s) off += sTot[s * PT + p];
+#pragma unroll
+  for (int r = 0; r < RS; ++r) sCum[(seg * RS + r) * PT + p] = sanitize(v[r] + off, kClipAcc);
+}
+
+template <typename T, int C, int P, int N, int PT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void mamba2_scan(
+    Mamba2Dims dm, const T* __restrict__ dt, const T* __restrict__ x, const float* __restrict__ A,
+    const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ state0,
+    Mamba2Chunks<T> ck, float* __restrict__ y, float* __restrict__ state_final, int save) {
+  typedef ScanLds<T, C, N, PT> L;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
+  T* sB = reinterpret_cast<T*>(lds + L::off_b);
+  T* sCB = reinterpret_cast<T*>(lds + L::off_cb);
+  T* sZ = reinterpret_cast<T*>(lds + L::off_z);
+  T* sW = reinterpret_cast<T*>(lds + L::off_w);
+  T* sSt = reinterpret_cast<T*>(lds + L::off_st);
+  float* sCum = reinterpret_cast<float*>(lds + L::off_cum);
+  float* sDbx = reinterpret_cast<float*>(lds + L::off_dbx);
+  float* sTot = reinterpret_cast<float*>(lds + L::off_tot);
+
+  constexpr int NPT = P / PT;
+  const int x_id = blockIdx.x;
+  const int pt = x_id % NPT;
+  const int bh = x_id / NPT;
+  const int h = bh % dm.H, bb = bh / dm.H;
+  const int p0 = pt * PT;
+  const int wv_id = wave_id();
+  const float Ah = A[h];
+  const size_t rsx = (size_t)dm.H * P;  // row stride of dt / x / y
+
+  // state tiles [PT][N]: (PT/16) x (N/16)
+  constexpr int SNI = N / 16;
+  constexpr int NTS = (PT / 16) * SNI;
+  constexpr int SPW = NTS / 4;
+  // y tiles [C][PT]: (C/16) x (PT/16)
+  constexpr int YNI = PT / 16;
+  constexpr int NTY = (C / 16) * YNI;
+  constexpr int YPW = NTY / 4;
+  static_assert(NTS % 4 == 0 && NTY % 4 == 0, "tiles must split evenly over 4 waves");
+  constexpr int KN = N / Mma<T>::KS;
+
+  f32x4 st[SPW];
+#pragma unroll
+  for (int t = 0; t < SPW; ++t) {
+    const int tile = wv_id * SPW + t, mi = tile / SNI, ni = tile % SNI;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = 16 * mi + tile_row(i), s = 16 * ni + tile_col();
+      st[t][i] = state0 ? state0[((size_t)bh * P + p0 + p) * N + s] : 0.f;
+    }
+    store_tile_t(sSt, L::LPT, 16 * mi, 16 * ni, st[t]);
+  }
+
+  // prefetch: B, CB to registers; dt / x tile; the C fragments of this wave's y tiles
+  RegStage<T, C, N> pB;
+  RegStage<T, C, C> pCB;
+  RegStage<T, C, PT> pdt, px;
+  typename Mma<T>::frag fC[YPW][KN], fCn[YPW][KN];  // this chunk's / the next chunk's
+  auto prefetch = [&](int n) {
+    const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
+    pB.load(Bm + row0 * N, N);
+    pCB.load(ck.cb + ((size_t)bb * dm.NT + n) * C * C, C);
+    pdt.load(dt + (row0 * dm.H + h) * P + p0, rsx);
+    px.load(x + (row0 * dm.H + h) * P + p0, rsx);
+    const T* cg = Cm + row0 * N;
+#pragma unroll
+    for (int t = 0; t < YPW; ++t) {
+      const int mi = (wv_id * YPW + t) / YNI;
+#pragma unroll
+      for (int kk = 0; kk < KN; ++kk) fCn[t][kk] = Mma<T>::ld_c(cg, N, 16 * mi, kk * Mma<T>::KS);
+    }
+  };
+  auto rotate = [&]() {
+#pragma unroll
+    for (int t = 0; t < YPW; ++t)
+#pragma unroll
+      for (int kk = 0; kk < KN; ++kk) fC[t][kk] = fCn[t][kk];
+  };
+  // raw dt / x -> sCum = sanitize(dt A, 20), sDbx = sanitize(dt x)
+  auto commit = [&]() {
+    pB.store(sB, L::LN);
+    pCB.store(sCB, L::LCB);
+    constexpr int VEC = 16 / (int)sizeof(T), PER_ROW = PT / VEC;
+#pragma unroll
+    for (int i = 0; i < RegStage<T, C, PT>::PT; ++i) {
+      const int e = threadIdx.x + 256 * i;
+      if (e < C * PER_ROW) {
+        const int r = e / PER_ROW, c = (e % PER_ROW) * VEC;
+        const T* dv = reinterpret_cast<const T*>(&pdt.r[i]);
+        const T* xv = reinterpret_cast<const T*>(&px.r[i]);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          const float d = to_f(dv[j]);
+          sCum[r * PT + c + j] = sanitize(d * Ah, kClipDecay);
+          sDbx[r * PT + c + j] = sanitize(d * to_f(xv[j]));
+        }
+      }
+    }
+  };
+  prefetch(0);
+  commit();
+  rotate();
+  __syncthreads();
+
+  for (int n = 0; n < dm.NT; ++n) {
+    const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
+    // a chunk with a positive step exponent breaks the monotone decay the
+    // factorisation relies on
+    int pos = 0;
+    for (int e = threadIdx.x; e < C * PT; e += 256) pos |= sCum[e] > 0.f;
+    const bool exact = __syncthreads_or(pos);
+    column_cumsum<C, PT>(sCum, sTot);
+    if (n + 1 < dm.NT) prefetch(n + 1);
+    if (save) {
+      T* sp = ck.state_pre + (((size_t)bh * dm.NT + n) * P + p0) * N;
+#pragma unroll
+      for (int t = 0; t < SPW; ++t) {
+        const int tile = wv_id * SPW + t, mi = tile / SNI, ni = tile % SNI;
+        store_tile_n(sp, N, 16 * mi, 16 * ni, st[t]);
+      }
+    }
+    __syncthreads();
+
+    // Z^(I)[j][p] = exp(cum_{16I} - cum_j) dBx_j  (j < 16 I; zero padding rows)
+    if (!exact) {
+#pragma unroll
+      for (int I = 1; I < L::NB; ++I) {
+        T* z = sZ + zrows_before<T>(I) * L::LPT;
+        for (int e = threadIdx.x; e < zrows<T>(I) * PT; e += 256) {
+          const int j = e / PT, p = e % PT;
+          float val = 0.f;
+          if (j < 16 * I) val = __expf(sCum[16 * I * PT + p] - sCum[j * PT + p]) * sDbx[j * PT + p];
+          z[j * L::LPT + p] = from_f<T>(val);
+        }
+      }
+    }
+    // write = dBx * sanitize(exp(clip(cum_last - cum, +-20)), 1e6)   (:133-135)
+    for (int e = threadIdx.x; e < C * PT; e += 256) {
+      const int j = e / PT, p = e % PT;
+      const float dte = sanitize(__expf(fminf(fmaxf(sCum[(C - 1) * PT + p] - sCum[j * PT + p],
+                                                    -kClipDecay), kClipDecay)), 1e6f);
+      sW[j * L::LPT + p] = from_f<T>(sDbx[j * PT + p] * dte);
+    }
+    __syncthreads();
+
+    // y = sanitize(y_diag + y_off)
+    float* yg = y + (row0 * dm.H + h) * P + p0;
+#pragma unroll
+    for (int t = 0; t < YPW; ++t) {
+      const int tile = wv_id * YPW + t, mi = tile / YNI, ni = tile % YNI;
+      f32x4 yo = zero4();
+#pragma unroll
+      for (int kk = 0; kk < KN; ++kk)
+        yo = Mma<T>::mma(fC[t][kk], Mma<T>::ld_t(sSt, L::LPT, 16 * ni, kk * Mma<T>::KS), yo);
+      f32x4 yd = zero4();
+      if (!exact && mi > 0)
+        yd = tile_mma<T, false, true>(yd, sCB, L::LCB, sZ + zrows_before<T>(mi) * L::LPT, L::LPT,
+                                      16 * mi, 16 * ni, zrows<T>(mi));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * mi + tile_row(i), p = 16 * ni + tile_col();
+        const float ci = sCum[r * PT + p];
+        const int j0 = exact ? 0 : 16 * mi;
+        float diag = 0.f;
+        for (int j = j0; j <= r; ++j) {
+          const float dd = fminf(fmaxf(ci - sCum[j * PT + p], -kClipDecay), kClipDecay);
+          diag += __expf(dd) * to_f(sCB[r * L::LCB + j]) * sDbx[j * PT + p];
+        }
+        const float off = (!exact && mi > 0) ? yd[i] * __expf(ci - sCum[16 * mi * PT + p]) : 0.f;
+        const float ydiag = sanitize(off + diag);
+        const float yoff = sanitize(yo[i] * __expf(fminf(fmaxf(ci, -kClipDecay), 0.f)));
+        yg[(size_t)r * rsx + p] = sanitize(ydiag + yoff);
+      }
+    }
+    if (n + 1 < dm.NT) rotate();
+
+    // state = sanitize(state exp(clip(cum_last, -20, 0)) + sanitize(B^T write))
+#pragma unroll
+    for (int t = 0; t < SPW; ++t) {
+      const int tile = wv_id * SPW + t, mi = tile / SNI, ni = tile % SNI;
+      f32x4 se = tile_mma<T, true, true>(zero4(), sW, L::LPT, sB, L::LN, 16 * mi, 16 * ni, C);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = 16 * mi + tile_row(i);
+        const float dce = __expf(fminf(fmaxf(sCum[(C - 1) * PT + p], -kClipDecay), 0.f));
+        st[t][i] = sanitize(st[t][i] * dce + sanitize(se[i]));
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < SPW; ++t) {
+      const int tile = wv_id * SPW + t, mi = tile / SNI, ni = tile % SNI;
+      store_tile_t(sSt, L::LPT, 16 * mi, 16 * ni, st[t]);
+    }
+    if (n + 1 < dm.NT) commit();
+    __syncthreads();
+  }
+#pragma unroll
+  for (int t = 0; t < SPW; ++t) {
+    const int tile = wv_id * SPW + t, mi = tile / SNI, ni = tile % SNI;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = 16 * mi + tile_row(i), s = 16 * ni + tile_col();
+      state_final[((size_t)bh * P + p0 + p) * N + s] = st[t][i];
+    }
+  }
+}
+
+}  // namespace ah

@@ -1,0 +1,112 @@
+// Host side of the Mamba2 SSD chunk scan: argument checks, workspace layout,
+// template dispatch and the extern "C" entry points of include/atomic_hybrid.h.
+#include "../../include/atomic_hybrid.h"
+#include "mamba2_bwd.hip"
+
+namespace ah {
+
+static size_t m2_align(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct Mamba2Plan {
+  Mamba2Dims dm;
+  size_t o_cb, o_state, fwd_end;
+  size_t o_dstate, o_lasta, o_part, o_dap, total;
+  int G;  // head groups of the cross-head reduction
+};
+
+static int mamba2_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
+  if (!a) return ATOMIC_ERR_NULL;
+  if (a->dtype != ATOMIC_BF16) return ATOMIC_ERR_DTYPE;
+  if (a->dy_dtype != ATOMIC_F32 && a->dy_dtype != ATOMIC_BF16) return ATOMIC_ERR_DTYPE;
+  if (a->batch <= 0 || a->heads <= 0 || a->seqlen <= 0) return ATOMIC_ERR_SHAPE;
+  if (a->chunk != 64 && a->chunk != 128) return ATOMIC_ERR_SHAPE;
+  if (a->seqlen % a->chunk != 0) return ATOMIC_ERR_SHAPE;
+  if (a->headdim != 64 && a->headdim != 128) return ATOMIC_ERR_SHAPE;
+  if (a->dstate != 64 && a->dstate != 128) return ATOMIC_ERR_SHAPE;
+  Mamba2Dims d;
+  d.B = a->batch; d.T = a->seqlen; d.H = a->heads; d.P = a->headdim; d.N = a->dstate;
+  d.C = a->chunk; d.NT = a->seqlen / a->chunk;
+  p->dm = d;
+  const size_t es = 2, B = d.B, H = d.H, NT = d.NT, C = d.C, P = d.P, N = d.N;
+  p->G = (int)(H < 4 ? H : 4);
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off += m2_align(bytes); return o; };
+  p->o_cb = take(B * NT * C * C * es);
+  p->o_state = take(B * H * NT * P * N * es);
+  p->fwd_end = off;
+  p->o_dstate = take(B * H * NT * P * N * es);       // dstate entering each chunk (reverse)
+  p->o_lasta = take(B * H * NT * P * 4);             // d cum_last from decay_chunk_end
+  p->o_part = take(B * NT * (size_t)p->G * (C * C + 2 * C * N) * 4);  // cross-head partials
+  p->o_dap = take(B * NT * H * 4);                   // per-chunk dA
+  p->total = off;
+  return ATOMIC_OK;
+}
+
+template <typename T>
+static Mamba2Chunks<T> mamba2_chunks(const Mamba2Plan& p, void* ws) {
+  char* base = static_cast<char*>(ws);
+  Mamba2Chunks<T> c;
+  c.cb = reinterpret_cast<T*>(base + p.o_cb);
+  c.state_pre = reinterpret_cast<T*>(base + p.o_state);
+  return c;
+}
+
+template <int C, int P, int N>
+static int mamba2_forward_impl(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm,
+                               const void* Cm, const float* A, const float* state0, float* y,
+                               float* state_final, void* ws, int save, hipStream_t st) {
+  typedef bf16 T;
+  constexpr int PT = 16;
+  Mamba2Chunks<T> ck = mamba2_chunks<T>(p, ws);
+  hipLaunchKernelGGL((mamba2_cb<T, C, N>), dim3((unsigned)(p.dm.B * p.dm.NT)), dim3(256), 0, st,
+                     p.dm, (const T*)Bm, (const T*)Cm, ck);
+  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
+  hipLaunchKernelGGL((mamba2_scan<T, C, P, N, PT>), dim3((unsigned)(p.dm.B * p.dm.H * (P / PT))),
+                     dim3(256), 0, st, p.dm, (const T*)dt, (const T*)x, A, (const T*)Bm,
+                     (const T*)Cm, state0, ck, y, state_final, save);
+  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
+  return ATOMIC_OK;
+}
+
+#define AH_M2_DISPATCH(FN, ...)                                                         \
+  do {                                                                                  \
+    const int c_ = p.dm.C, p_ = p.dm.P, n_ = p.dm.N;                                    \
+    if (c_ == 128 && p_ == 64 && n_ == 128) return FN<128, 64, 128>(__VA_ARGS__);       \
+    if (c_ == 128 && p_ == 128 && n_ == 128) return FN<128, 128, 128>(__VA_ARGS__);     \
+    if (c_ == 64 && p_ == 64 && n_ == 128) return FN<64, 64, 128>(__VA_ARGS__);         \
+    if (c_ == 64 && p_ == 128 && n_ == 128) return FN<64, 128, 128>(__VA_ARGS__);       \
+    if (c_ == 128 && p_ == 64 && n_ == 64) return FN<128, 64, 64>(__VA_ARGS__);         \
+    if (c_ == 128 && p_ == 128 && n_ == 64) return FN<128, 128, 64>(__VA_ARGS__);       \
+    if (c_ == 64 && p_ == 64 && n_ == 64) return FN<64, 64, 64>(__VA_ARGS__);           \
+    if (c_ == 64 && p_ == 128 && n_ == 64) return FN<64, 128, 64>(__VA_ARGS__);         \
+    return ATOMIC_ERR_SHAPE;                                                            \
+  } while (0)
+
+int mamba2_forward(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm, const void* Cm,
+                   const float* A, const float* state0, float* y, float* state_final, void* ws,
+                   int save, hipStream_t st) {
+  AH_M2_DISPATCH(mamba2_forward_impl, p, dt, x, Bm, Cm, A, state0, y, state_final, ws, save, st);
+}
+
+}  // namespace ah
+
+using namespace ah;
+
+extern "C" size_t atomic_mamba2_workspace_size(const atomic_mamba2_args* a) {
+  Mamba2Plan p;
+  if (mamba2_plan(a, &p) != ATOMIC_OK) return 0;
+  return p.total;
+}
+
+extern "C" int atomic_mamba2_fwd(const atomic_mamba2_args* a, const void* dt, const void* x,
+                                 const void* B, const void* C, const float* A, const float* state0,
+                                 float* y, float* state_final, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  Mamba2Plan p;
+  const int rc = mamba2_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!dt || !x || !B || !C || !A || !y || !state_final) return ATOMIC_ERR_NULL;
+  if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
+  return mamba2_forward(p, dt, x, B, C, A, state0, y, state_final, workspace,
+                        (a->flags & ATOMIC_MAMBA2_SAVE) ? 1 : 0, (hipStream_t)stream);
+}

@@ -109,6 +109,64 @@ int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const void* k, con
                     void* dw, void* db, float* dg, float* dh0, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------- Mamba2 */
+
+enum {
+  /* forward: keep the state entering each chunk in the workspace for a
+     following atomic_mamba2_bwd on the same inputs and workspace */
+  ATOMIC_MAMBA2_SAVE = 1,
+  /* backward: the workspace holds the intermediates of an
+     atomic_mamba2_fwd(..., ATOMIC_MAMBA2_SAVE) call on identical inputs */
+  ATOMIC_MAMBA2_REUSE = 2
+};
+
+typedef struct atomic_mamba2_args {
+  int32_t batch;     /* B                                                  */
+  int32_t seqlen;    /* T, a multiple of chunk                             */
+  int32_t heads;     /* H                                                  */
+  int32_t headdim;   /* P: 64 or 128                                       */
+  int32_t dstate;    /* N: 64 or 128 (ngroups = 1: B and C shared by heads) */
+  int32_t chunk;     /* C: 64 or 128                                       */
+  int32_t dtype;     /* dt, x, B, C and their gradients: ATOMIC_BF16       */
+  int32_t dy_dtype;  /* upstream gradient dy: ATOMIC_F32 / ATOMIC_BF16     */
+  int32_t flags;     /* ATOMIC_MAMBA2_*                                    */
+} atomic_mamba2_args;
+
+/* Bytes of workspace atomic_mamba2_fwd / atomic_mamba2_bwd need. */
+size_t atomic_mamba2_workspace_size(const atomic_mamba2_args* a);
+
+/*
+ * Mamba2 SSD chunk-scan forward.  Replaces mamba2_pallas_forward / the forward
+ * of mamba2_pallas_forward_trainable_B6(dt, x, B, C, A, chunk_size, state0)
+ * (reference atomic_ops/kernel_mamba2_trainable_B6.py:137-155,
+ *  atomic_ops/kernel_mamba2_c_interchunk.py:90-100); numerics follow
+ * mamba2_ssd_reference (atomic_ops/mamba2_ssd_reference.py:152-179).
+ *   dt, x  : [B, T, H, P]  dtype       B, C : [B, T, N]  dtype
+ *   A      : [H]           fp32 (negative log-decay rate per unit dt)
+ *   state0 : [B, H, P, N]  fp32, NULL means zeros
+ *   y      : [B, T, H, P]  fp32 (the reference returns fp32, :148,178)
+ *   state_final : [B, H, P, N] fp32
+ * There is no D * x skip term (the reference has none, :152).
+ */
+int atomic_mamba2_fwd(const atomic_mamba2_args* a, const void* dt, const void* x, const void* B,
+                      const void* C, const float* A, const float* state0, float* y,
+                      float* state_final, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Mamba2 SSD chunk-scan backward with the semantics of the hand-derived MB0
+ * backward chunk_ssd_bwd_scan (reference atomic_ops/mamba2_bwd_reference.py:55-266):
+ * straight-through clip masks, per-chunk sanitising, dA summed over batch,
+ * chunks, time and channels; then the final clip(+-1e4) / nan_to_num and
+ * cast of kernel_mamba2_trainable_B6.py:108-129.
+ *   dy : [B, T, H, P] dy_dtype          dstate_final : [B, H, P, N] fp32 or NULL
+ *   ddt, dx : [B, T, H, P] dtype        dB, dC : [B, T, N] dtype
+ *   dA : [H] fp32                       dstate0 : [B, H, P, N] fp32 (may be NULL)
+ */
+int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, const void* x, const void* B,
+                      const void* C, const float* A, const float* state0, const void* dy,
+                      const float* dstate_final, void* ddt, void* dx, void* dB, void* dC, float* dA,
+                      float* dstate0, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
