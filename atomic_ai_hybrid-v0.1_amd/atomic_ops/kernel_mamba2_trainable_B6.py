@@ -1,0 +1,53 @@
+"""Drop-in trainable Mamba2 SSD op (mirror of reference
+atomic_ops/kernel_mamba2_trainable_B6.py).
+
+``mamba2_pallas_forward_trainable_B6(dt, x, B, C, A, chunk_size, state0=None)``
+keeps the reference signature (kernel_mamba2_trainable_B6.py:137-155) and
+returns ``(y, state_final)``; its backward returns ``(ddt, dx, dB, dC, dA,
+dstate0)`` cast to the primals' dtypes after the final clip(+-1e4) /
+nan_to_num (kernel_mamba2_trainable_B6.py:108-131).  ``chunk_size`` is not
+differentiable (:72).  The forward keeps the per-chunk states for the
+backward instead of re-running the forward scan.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import mamba2 as _m
+
+
+class _Mamba2Core(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, dt, x, B, C, A, chunk_size, state0):
+        need = any(ctx.needs_input_grad)
+        y, state_final, ws = _m.forward(dt, x, B, C, A, chunk_size, state0, save=need)
+        if need:
+            ctx.save_for_backward(dt, x, B, C, A, state0)
+            ctx.ws = ws
+            ctx.chunk_size = chunk_size
+        return y, state_final
+
+    @staticmethod
+    def backward(ctx, dy, dstate_final):
+        dt, x, B, C, A, state0 = ctx.saved_tensors
+        ddt, dx, dB, dC, dA, dstate0 = _m.backward(dt, x, B, C, A, ctx.chunk_size, dy,
+                                                   dstate_final=dstate_final, state0=state0,
+                                                   workspace=ctx.ws, reuse=True)
+        ctx.ws = None
+        return ddt, dx, dB, dC, dA.to(A.dtype), None, dstate0.to(state0.dtype)
+
+
+def mamba2_pallas_forward_trainable_B6(dt, x, B, C, A, chunk_size, state0=None):
+    """dt, x: [b, l, h, p]; B, C: [b, l, n]; A: [h] float32; state0: [b, h, p, n]
+    float32 (zeros when None).  Returns y [b, l, h, p] float32 and
+    state_final [b, h, p, n] float32."""
+    b, l, h, p = dt.shape
+    if state0 is None:
+        state0 = torch.zeros(b, h, p, B.shape[-1], dtype=torch.float32, device=dt.device)
+    return _Mamba2Core.apply(dt, x, B, C, A, chunk_size, state0)
+
+
+def mamba2_pallas_forward(dt, x, B, C, A, chunk_size, state0=None):
+    """Forward only (reference kernel_mamba2_c_interchunk.py:90-100)."""
+    y, state_final, _ = _m.forward(dt, x, B, C, A, chunk_size, state0)
+    return y, state_final

@@ -244,7 +244,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     __syncthreads();
 
     // y = sanitize(y_diag + y_off)
-    float* yg = y + (row0 * dm.H + h) * P + p0;
+    float* yg = y ? y + (row0 * dm.H + h) * P + p0 : nullptr;
 #pragma unroll
     for (int t = 0; t < YPW; ++t) {
       const int tile = wv_id * YPW + t, mi = tile / YNI, ni = tile % YNI;
@@ -269,7 +269,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const float off = (!exact && mi > 0) ? yd[i] * __expf(ci - sCum[16 * mi * PT + p]) : 0.f;
         const float ydiag = sanitize(off + diag);
         const float yoff = sanitize(yo[i] * __expf(fminf(fmaxf(ci, -kClipDecay), 0.f)));
-        yg[(size_t)r * rsx + p] = sanitize(ydiag + yoff);
+        if (y) yg[(size_t)r * rsx + p] = sanitize(ydiag + yoff);
       }
     }
     if (n + 1 < dm.NT) rotate();
@@ -295,13 +295,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     if (n + 1 < dm.NT) commit();
     __syncthreads();
   }
+  if (state_final) {
 #pragma unroll
-  for (int t = 0; t < SPW; ++t) {
-    const int tile = wv_id * SPW + t, mi = tile / SNI, ni = tile % SNI;
+    for (int t = 0; t < SPW; ++t) {
+      const int tile = wv_id * SPW + t, mi = tile / SNI, ni = tile % SNI;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = 16 * mi + tile_row(i), s = 16 * ni + tile_col();
-      state_final[((size_t)bh * P + p0 + p) * N + s] = st[t][i];
+      for (int i = 0; i < 4; ++i) {
+        const int p = 16 * mi + tile_row(i), s = 16 * ni + tile_col();
+        state_final[((size_t)bh * P + p0 + p) * N + s] = st[t][i];
+      }
     }
   }
 }

@@ -28,7 +28,9 @@ static int mamba2_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
   d.C = a->chunk; d.NT = a->seqlen / a->chunk;
   p->dm = d;
   const size_t es = 2, B = d.B, H = d.H, NT = d.NT, C = d.C, P = d.P, N = d.N;
-  p->G = (int)(H < 4 ? H : 4);
+  int G = 1;
+  while ((size_t)G * B * NT < 256 && (size_t)(2 * G) <= H && H % (size_t)(2 * G) == 0) G *= 2;
+  p->G = G;
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += m2_align(bytes); return o; };
   p->o_cb = take(B * NT * C * C * es);
@@ -68,6 +70,23 @@ static int mamba2_forward_impl(const Mamba2Plan& p, const void* dt, const void* 
   return ATOMIC_OK;
 }
 
+template <typename T>
+static Mamba2Grads<T> mamba2_grads(const Mamba2Plan& p, void* ws) {
+  char* base = static_cast<char*>(ws);
+  Mamba2Grads<T> g;
+  g.dstate = reinterpret_cast<T*>(base + p.o_dstate);
+  g.lasta = reinterpret_cast<float*>(base + p.o_lasta);
+  g.part = reinterpret_cast<float*>(base + p.o_part);
+  g.dap = reinterpret_cast<float*>(base + p.o_dap);
+  return g;
+}
+
+template <int C, int P, int N, typename TD>
+static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm,
+                             const void* Cm, const float* A, const float* state0, const void* dy,
+                             const float* dstate_final, void* ddt, void* dx, void* dB, void* dC,
+                             float* dA, float* dstate0, void* ws, bool reuse, hipStream_t st);
+
 #define AH_M2_DISPATCH(FN, ...)                                                         \
   do {                                                                                  \
     const int c_ = p.dm.C, p_ = p.dm.P, n_ = p.dm.N;                                    \
@@ -86,6 +105,58 @@ int mamba2_forward(const Mamba2Plan& p, const void* dt, const void* x, const voi
                    const float* A, const float* state0, float* y, float* state_final, void* ws,
                    int save, hipStream_t st) {
   AH_M2_DISPATCH(mamba2_forward_impl, p, dt, x, Bm, Cm, A, state0, y, state_final, ws, save, st);
+}
+
+template <int C, int P, int N, typename TD>
+static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm,
+                             const void* Cm, const float* A, const float* state0, const void* dy,
+                             const float* dstate_final, void* ddt, void* dx, void* dB, void* dC,
+                             float* dA, float* dstate0, void* ws, bool reuse, hipStream_t st) {
+  typedef bf16 T;
+  if (!reuse) {
+    // recompute the forward's per-chunk states (the reference re-runs the
+    // forward scan, mamba2_bwd_reference.py:229-234)
+    const int rc = mamba2_forward_impl<C, P, N>(p, dt, x, Bm, Cm, A, state0, nullptr, nullptr, ws, 1, st);
+    if (rc != ATOMIC_OK) return rc;
+  }
+  Mamba2Chunks<T> ck = mamba2_chunks<T>(p, ws);
+  Mamba2Grads<T> gr = mamba2_grads<T>(p, ws);
+  constexpr int PT = 16;
+  hipLaunchKernelGGL((mamba2_bwd_dstate<T, TD, C, P, N, PT>), dim3((unsigned)(p.dm.B * p.dm.H * (P / PT))),
+                     dim3(256), 0, st, p.dm, (const T*)dt, A, (const T*)Cm, (const TD*)dy, dstate_final,
+                     ck, gr, dstate0);
+  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
+  hipLaunchKernelGGL((mamba2_bwd_chunk<T, TD, C, P, N>), dim3((unsigned)(p.dm.B * p.dm.NT * p.G)), dim3(256),
+                     0, st, p.dm, p.G, (const T*)dt, (const T*)x, A, (const T*)Bm, (const T*)Cm,
+                     (const TD*)dy, ck, gr, (T*)ddt, (T*)dx);
+  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
+  hipLaunchKernelGGL((mamba2_bwd_bc<T, C, N>), dim3((unsigned)(p.dm.B * p.dm.NT)), dim3(256), 0, st, p.dm,
+                     p.G, (const T*)Bm, (const T*)Cm, gr, (T*)dB, (T*)dC);
+  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
+  hipLaunchKernelGGL(mamba2_bwd_da, dim3(1), dim3(256), 0, st, p.dm, (const float*)gr.dap, dA);
+  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
+  return ATOMIC_OK;
+}
+
+template <int C, int P, int N>
+static int mamba2_backward_impl(const Mamba2Plan& p, int dy_dtype, const void* dt, const void* x,
+                                const void* Bm, const void* Cm, const float* A, const float* state0,
+                                const void* dy, const float* dstate_final, void* ddt, void* dx,
+                                void* dB, void* dC, float* dA, float* dstate0, void* ws, bool reuse,
+                                hipStream_t st) {
+  if (dy_dtype == ATOMIC_BF16)
+    return mamba2_backward_t<C, P, N, bf16>(p, dt, x, Bm, Cm, A, state0, dy, dstate_final, ddt, dx, dB,
+                                            dC, dA, dstate0, ws, reuse, st);
+  return mamba2_backward_t<C, P, N, float>(p, dt, x, Bm, Cm, A, state0, dy, dstate_final, ddt, dx, dB,
+                                           dC, dA, dstate0, ws, reuse, st);
+}
+
+int mamba2_backward(const Mamba2Plan& p, int dy_dtype, const void* dt, const void* x, const void* Bm,
+                    const void* Cm, const float* A, const float* state0, const void* dy,
+                    const float* dstate_final, void* ddt, void* dx, void* dB, void* dC, float* dA,
+                    float* dstate0, void* ws, bool reuse, hipStream_t st) {
+  AH_M2_DISPATCH(mamba2_backward_impl, p, dy_dtype, dt, x, Bm, Cm, A, state0, dy, dstate_final, ddt, dx,
+                 dB, dC, dA, dstate0, ws, reuse, st);
 }
 
 }  // namespace ah
@@ -109,4 +180,18 @@ extern "C" int atomic_mamba2_fwd(const atomic_mamba2_args* a, const void* dt, co
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
   return mamba2_forward(p, dt, x, B, C, A, state0, y, state_final, workspace,
                         (a->flags & ATOMIC_MAMBA2_SAVE) ? 1 : 0, (hipStream_t)stream);
+}
+
+extern "C" int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, const void* x,
+                                 const void* B, const void* C, const float* A, const float* state0,
+                                 const void* dy, const float* dstate_final, void* ddt, void* dx,
+                                 void* dB, void* dC, float* dA, float* dstate0, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  Mamba2Plan p;
+  const int rc = mamba2_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!dt || !x || !B || !C || !A || !dy || !ddt || !dx || !dB || !dC || !dA) return ATOMIC_ERR_NULL;
+  if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
+  return mamba2_backward(p, a->dy_dtype, dt, x, B, C, A, state0, dy, dstate_final, ddt, dx, dB, dC, dA,
+                         dstate0, workspace, (a->flags & ATOMIC_MAMBA2_REUSE) != 0, (hipStream_t)stream);
 }

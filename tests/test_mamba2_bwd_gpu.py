@@ -1,0 +1,86 @@
+"""Mamba2 SSD backward on the GPU (through the C ABI) against the MB0 oracle
+(oracle/mamba2.py chunk_ssd_bwd_scan, float64; itself pinned against
+autodiff and finite differences)."""
+import pytest
+import torch
+
+from _util import banner, rel_err, tol_for
+from atomic_ops import inputs
+from atomic_ops import mamba2 as M
+from oracle import mamba2 as om
+
+pytestmark = pytest.mark.gpu
+
+BF16, F32 = torch.bfloat16, torch.float32
+NAMES = ("ddt", "dx", "dB", "dC", "dA", "dstate0")
+
+
+def _case(B, T, H, P, N, C, seed, state=False, dy_dtype=BF16, mutate=None):
+    inp = inputs.mamba2_inputs(B, T, H, P, N, seed=seed, dO=True)
+    if mutate:
+        mutate(inp)
+    dt, x, Bm, Cm, A, dy = (inp[n] for n in ("dt", "x", "Bm", "Cm", "A", "dy"))
+    dy = dy.to(dy_dtype)
+    gen = torch.Generator().manual_seed(seed + 3)
+    s0 = 0.3 * torch.randn(B, H, P, N, generator=gen) if state else None
+    ds = torch.randn(B, H, P, N, generator=gen) if state else None
+    ref = om.chunk_ssd_bwd_scan(dt, A, Bm, Cm, x, C, dy, ds, state0=s0)
+    ddt, dB, dC, dx, dA, ds0 = ref
+    return (dt, x, Bm, Cm, A, dy, s0, ds), (ddt, dx, dB, dC, dA, ds0)
+
+
+def _gpu(args, C, reuse):
+    dt, x, Bm, Cm, A, dy, s0, ds = (t.cuda() if t is not None else None for t in args)
+    ws = None
+    if reuse:
+        _, _, ws = M.forward(dt, x, Bm, Cm, A, C, state0=s0, save=True)
+    out = M.backward(dt, x, Bm, Cm, A, C, dy, dstate_final=ds, state0=s0, workspace=ws, reuse=reuse)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("B,T,H,P,N,C,state,reuse", [
+    (1, 256, 2, 64, 128, 128, False, False),    # config 1 head shape
+    (2, 256, 4, 64, 128, 128, True, True),
+    (1, 256, 2, 128, 128, 128, True, False),    # headline P = 128
+    (1, 256, 2, 64, 128, 64, True, True),       # chunk 64
+    (1, 128, 2, 64, 64, 128, False, True),      # N = 64
+])
+def test_backward_matches_mb0(B, T, H, P, N, C, state, reuse):
+    banner(f"mamba2 bwd B{B} T{T} H{H} P{P} N{N} C{C} state={state} reuse={reuse}")
+    args, ref = _case(B, T, H, P, N, C, seed=T + H + C, state=state)
+    out = _gpu(args, C, reuse)
+    errs = {}
+    for name, got, want in zip(NAMES, out, ref):
+        if name == "dstate0" and not state:
+            want = torch.zeros_like(got.cpu(), dtype=torch.float64) if want is None else want
+        assert torch.isfinite(got).all(), name
+        errs[name] = rel_err(got, want) if want.abs().max() > 0 else got.abs().max().item()
+    print("  rel_err " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+    for name, e in errs.items():
+        assert e < tol_for(BF16), (name, e)
+
+
+def test_backward_fp32_upstream_gradient():
+    banner("mamba2 bwd fp32 dy")
+    args, ref = _case(1, 256, 2, 64, 128, 128, seed=9, state=True, dy_dtype=F32)
+    out = _gpu(args, 128, reuse=False)
+    for name, got, want in zip(NAMES, out, ref):
+        e = rel_err(got, want)
+        assert e < tol_for(BF16), (name, e)
+
+
+def test_trainable_wrapper_autograd():
+    """mamba2_pallas_forward_trainable_B6 through torch.autograd matches the
+    direct forward / backward calls."""
+    from atomic_ops.kernel_mamba2_trainable_B6 import mamba2_pallas_forward_trainable_B6
+    banner("mamba2 trainable wrapper")
+    inp = inputs.mamba2_inputs(1, 256, 2, 64, 128, seed=4, device="cuda", dO=True)
+    dt, x, Bm, Cm, A, dy = (inp[n] for n in ("dt", "x", "Bm", "Cm", "A", "dy"))
+    leaves = [t.clone().requires_grad_(True) for t in (dt, x, Bm, Cm, A)]
+    y, s = mamba2_pallas_forward_trainable_B6(*leaves[:4], leaves[4], 128)
+    (y * dy.float()).sum().backward()
+    direct = M.backward(dt, x, Bm, Cm, A, 128, dy.float())
+    for leaf, ref in zip(leaves, direct[:5]):
+        assert leaf.grad.dtype == leaf.dtype
+        assert torch.equal(leaf.grad, ref) or rel_err(leaf.grad, ref) < 1e-6
