@@ -29,7 +29,7 @@ class Gdn2Args(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int32), ("seqlen", ctypes.c_int32), ("heads", ctypes.c_int32),
                 ("dk", ctypes.c_int32), ("dv", ctypes.c_int32), ("chunk", ctypes.c_int32),
                 ("dtype", ctypes.c_int32), ("do_dtype", ctypes.c_int32), ("scale", ctypes.c_float),
-                ("flags", ctypes.c_int32)]
+                ("flags", ctypes.c_int32), ("profile", ctypes.c_void_p)]
 
 
 class Gdn2Layout(ctypes.Structure):
@@ -40,7 +40,49 @@ class Gdn2Layout(ctypes.Structure):
 class Mamba2Args(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int32), ("seqlen", ctypes.c_int32), ("heads", ctypes.c_int32),
                 ("headdim", ctypes.c_int32), ("dstate", ctypes.c_int32), ("chunk", ctypes.c_int32),
-                ("dtype", ctypes.c_int32), ("dy_dtype", ctypes.c_int32), ("flags", ctypes.c_int32)]
+                ("dtype", ctypes.c_int32), ("dy_dtype", ctypes.c_int32), ("flags", ctypes.c_int32),
+                ("profile", ctypes.c_void_p)]
+
+
+PROFILE_MAX = 16
+
+
+class AtomicProfile(ctypes.Structure):
+    _fields_ = [("start", ctypes.c_void_p * PROFILE_MAX), ("stop", ctypes.c_void_p * PROFILE_MAX),
+                ("capacity", ctypes.c_int32), ("count", ctypes.c_int32),
+                ("names", ctypes.c_char_p * PROFILE_MAX)]
+
+
+class KernelTimer:
+    """Caller-owned event pairs that the library records around each kernel
+    it launches (on the launch stream).  ``durations()`` returns
+    ``[(kernel_name, ms), ...]`` of the last call, after synchronising."""
+
+    def __init__(self, device=None):
+        import torch
+        self._torch = torch
+        self.start = [torch.cuda.Event(enable_timing=True) for _ in range(PROFILE_MAX)]
+        self.stop = [torch.cuda.Event(enable_timing=True) for _ in range(PROFILE_MAX)]
+        stream = torch.cuda.current_stream(device)
+        for e in self.start + self.stop:   # create the underlying hipEvent_t
+            e.record(stream)
+        torch.cuda.synchronize(device)
+        self.struct = AtomicProfile()
+        for i in range(PROFILE_MAX):
+            self.struct.start[i] = self.start[i].cuda_event
+            self.struct.stop[i] = self.stop[i].cuda_event
+        self.struct.capacity = PROFILE_MAX
+
+    def arm(self):
+        """Pointer for the ``profile`` field of an args struct."""
+        self.struct.count = 0
+        return ctypes.cast(ctypes.pointer(self.struct), ctypes.c_void_p)
+
+    def durations(self):
+        self._torch.cuda.synchronize()
+        n = min(self.struct.count, PROFILE_MAX)
+        return [(self.struct.names[i].decode(), self.start[i].elapsed_time(self.stop[i]))
+                for i in range(n)]
 
 
 class AtomicError(RuntimeError):

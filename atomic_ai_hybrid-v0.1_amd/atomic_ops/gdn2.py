@@ -71,7 +71,7 @@ def workspace_layout(args):
     return lay
 
 
-def forward(q, k, v, w, b, g, scale, h0=None, *, save=False, workspace=None, chunk=CHUNK):
+def forward(q, k, v, w, b, g, scale, h0=None, *, save=False, workspace=None, chunk=CHUNK, timer=None):
     """Returns ``(o, h_final, workspace)``.  With ``save`` the workspace keeps
     the per-chunk intermediates for :func:`backward`."""
     _check_inputs(q, k, v, w, b, g)
@@ -80,6 +80,8 @@ def forward(q, k, v, w, b, g, scale, h0=None, *, save=False, workspace=None, chu
     B, T, H, K = q.shape
     V = v.shape[-1]
     args = make_args(q, v, scale, flags=_lib.GDN2_SAVE if save else 0, chunk=chunk)
+    if timer is not None:
+        args.profile = timer.arm()
     if workspace is None:
         workspace = new_workspace(args, q.device)
     if h0 is not None:
@@ -94,7 +96,7 @@ def forward(q, k, v, w, b, g, scale, h0=None, *, save=False, workspace=None, chu
 
 
 def backward(q, k, v, w, b, g, scale, dO, dh_final=None, h0=None, *, workspace=None, reuse=False,
-             chunk=CHUNK):
+             chunk=CHUNK, timer=None):
     """Gradients ``(dq, dk, dv, dw, db, dg, dh0)`` in the primals' dtypes
     (dg and dh0 float32).  ``reuse`` declares that ``workspace`` holds the
     intermediates of a ``forward(..., save=True)`` on the same inputs."""
@@ -105,6 +107,8 @@ def backward(q, k, v, w, b, g, scale, dO, dh_final=None, h0=None, *, workspace=N
     if dO.dtype not in _DT:
         dO = dO.to(torch.float32)
     args = make_args(q, v, scale, do_dtype=dO.dtype, flags=_lib.GDN2_REUSE if reuse else 0, chunk=chunk)
+    if timer is not None:
+        args.profile = timer.arm()
     if workspace is None:
         workspace = new_workspace(args, q.device)
     if h0 is not None:

@@ -54,7 +54,7 @@ def workspace_bytes(args):
     return n
 
 
-def forward(dt, x, Bm, Cm, A, chunk_size, state0=None, *, save=False, workspace=None):
+def forward(dt, x, Bm, Cm, A, chunk_size, state0=None, *, save=False, workspace=None, timer=None):
     """Returns ``(y, state_final, workspace)``."""
     _check(dt, x, Bm, Cm, A)
     lib = _lib.load()
@@ -62,6 +62,8 @@ def forward(dt, x, Bm, Cm, A, chunk_size, state0=None, *, save=False, workspace=
     b, l, h, p = dt.shape
     n = Bm.shape[-1]
     args = make_args(dt, Bm, chunk_size, flags=M2_SAVE if save else 0)
+    if timer is not None:
+        args.profile = timer.arm()
     if workspace is None:
         workspace = torch.empty(workspace_bytes(args), dtype=torch.uint8, device=dt.device)
     if state0 is not None:
@@ -76,7 +78,7 @@ def forward(dt, x, Bm, Cm, A, chunk_size, state0=None, *, save=False, workspace=
 
 
 def backward(dt, x, Bm, Cm, A, chunk_size, dy, dstate_final=None, state0=None, *, workspace=None,
-             reuse=False):
+             reuse=False, timer=None):
     """Gradients ``(ddt, dx, dB, dC, dA, dstate0)`` (MB0 semantics) in the
     primals' dtypes (dA, dstate0 float32)."""
     _check(dt, x, Bm, Cm, A)
@@ -86,6 +88,8 @@ def backward(dt, x, Bm, Cm, A, chunk_size, dy, dstate_final=None, state0=None, *
     if dy.dtype not in _DT:
         dy = dy.to(torch.float32)
     args = make_args(dt, Bm, chunk_size, dy_dtype=dy.dtype, flags=M2_REUSE if reuse else 0)
+    if timer is not None:
+        args.profile = timer.arm()
     if workspace is None:
         workspace = torch.empty(workspace_bytes(args), dtype=torch.uint8, device=dt.device)
     if state0 is not None:

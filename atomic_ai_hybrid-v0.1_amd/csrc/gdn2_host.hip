@@ -2,6 +2,7 @@
 // template dispatch and the extern "C" entry points of include/atomic_hybrid.h.
 #include "../../include/atomic_hybrid.h"
 #include "gdn2_bwd.hip"
+#include "launch.hpp"
 
 namespace ah {
 
@@ -76,17 +77,20 @@ static Gdn2Chunks<T> gdn2_chunks(const Gdn2Plan& p, void* ws) {
 template <typename T, int K>
 static int gdn2_forward_impl(const Gdn2Plan& p, const void* q, const void* k, const void* v,
                              const void* w, const void* b, const float* g, const float* h0,
-                             float* o, float* h_final, void* ws, int save, hipStream_t st) {
+                             float* o, float* h_final, void* ws, int save, Launch& L) {
   constexpr int C = 64, V = K, VT = 32;
   Gdn2Chunks<T> ck = gdn2_chunks<T>(p, ws);
-  hipLaunchKernelGGL((gdn2_fwd_intra<T, C, K, V>), dim3((unsigned)p.bhn), dim3(256), 0, st, p.dm,
-                     (const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b, g, ck);
-  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
+  hipStream_t st = L.st;
+  int rc = L("gdn2_fwd_intra", [&] {
+    hipLaunchKernelGGL((gdn2_fwd_intra<T, C, K, V>), dim3((unsigned)p.bhn), dim3(256), 0, st, p.dm,
+                       (const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b, g, ck);
+  });
+  if (rc) return rc;
   const unsigned nwg = (unsigned)(p.dm.B * p.dm.H * (V / VT));
-  hipLaunchKernelGGL((gdn2_fwd_state<T, C, K, V, VT>), dim3(nwg), dim3(256), 0, st, p.dm, ck, h0, o,
-                     h_final, save);
-  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
-  return ATOMIC_OK;
+  return L("gdn2_fwd_state", [&] {
+    hipLaunchKernelGGL((gdn2_fwd_state<T, C, K, V, VT>), dim3(nwg), dim3(256), 0, st, p.dm, ck, h0, o,
+                       h_final, save);
+  });
 }
 
 template <typename T>
@@ -109,39 +113,47 @@ static int gdn2_backward_impl(const Gdn2Plan& p, const void* q, const void* k, c
                               const void* w, const void* b, const float* g, const float* h0,
                               const void* dO, const float* dh_final, void* dq, void* dk, void* dv,
                               void* dw, void* db, float* dg, float* dh0, void* ws, bool reuse,
-                              hipStream_t st) {
+                              Launch& L) {
   constexpr int C = 64, V = K, VT = 32;
   Gdn2Chunks<T> ck = gdn2_chunks<T>(p, ws);
   Gdn2Grads<T> gr = gdn2_grads<T>(p, ws);
+  int rc;
   if (!reuse) {
     // recompute the forward intermediates (the reference's residuals are the
     // inputs only, kernel_trainable_B6.py:91-94,104-111)
-    const int rc = gdn2_forward_impl<T, K>(p, q, k, v, w, b, g, h0, nullptr, nullptr, ws, 1, st);
-    if (rc != ATOMIC_OK) return rc;
+    rc = gdn2_forward_impl<T, K>(p, q, k, v, w, b, g, h0, nullptr, nullptr, ws, 1, L);
+    if (rc) return rc;
   }
+  hipStream_t st = L.st;
   const unsigned nseq = (unsigned)(p.dm.B * p.dm.H * (V / VT));
   const unsigned nblk = (unsigned)p.bhn;
-  hipLaunchKernelGGL((gdn2_bwd_dh<T, TD, C, K, V, VT>), dim3(nseq), dim3(256), 0, st, p.dm, ck, gr,
-                     (const TD*)dO, dh_final, dh0);
-  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
-  hipLaunchKernelGGL((gdn2_bwd_hgrad<T, TD, C, K, V>), dim3(nblk), dim3(256), 0, st, p.dm, ck, gr,
-                     (const TD*)dO);
-  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
-  hipLaunchKernelGGL((gdn2_bwd_wy<T, C, K, V>), dim3(nblk), dim3(256), 0, st, p.dm, ck, gr,
-                     (const T*)k, (const T*)v, (const T*)w, (const T*)b, g, (T*)dw, (T*)dv);
-  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
-  hipLaunchKernelGGL((gdn2_bwd_intra<T, C, K, V>), dim3(nblk), dim3(256), 0, st, p.dm, gr,
-                     (const T*)q, (const T*)k, (const T*)b, g, (T*)dq, (T*)dk, (T*)db, dg);
-  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
-  return ATOMIC_OK;
+  rc = L("gdn2_bwd_dh", [&] {
+    hipLaunchKernelGGL((gdn2_bwd_dh<T, TD, C, K, V, VT>), dim3(nseq), dim3(256), 0, st, p.dm, ck, gr,
+                       (const TD*)dO, dh_final, dh0);
+  });
+  if (rc) return rc;
+  rc = L("gdn2_bwd_hgrad", [&] {
+    hipLaunchKernelGGL((gdn2_bwd_hgrad<T, TD, C, K, V>), dim3(nblk), dim3(256), 0, st, p.dm, ck, gr,
+                       (const TD*)dO);
+  });
+  if (rc) return rc;
+  rc = L("gdn2_bwd_wy", [&] {
+    hipLaunchKernelGGL((gdn2_bwd_wy<T, C, K, V>), dim3(nblk), dim3(256), 0, st, p.dm, ck, gr,
+                       (const T*)k, (const T*)v, (const T*)w, (const T*)b, g, (T*)dw, (T*)dv);
+  });
+  if (rc) return rc;
+  return L("gdn2_bwd_intra", [&] {
+    hipLaunchKernelGGL((gdn2_bwd_intra<T, C, K, V>), dim3(nblk), dim3(256), 0, st, p.dm, gr,
+                       (const T*)q, (const T*)k, (const T*)b, g, (T*)dq, (T*)dk, (T*)db, dg);
+  });
 }
 
 int gdn2_backward(const Gdn2Plan& p, int dtype, int do_dtype, const void* q, const void* k,
                   const void* v, const void* w, const void* b, const float* g, const float* h0,
                   const void* dO, const float* dh_final, void* dq, void* dk, void* dv, void* dw,
-                  void* db, float* dg, float* dh0, void* ws, bool reuse, hipStream_t st) {
+                  void* db, float* dg, float* dh0, void* ws, bool reuse, Launch& L) {
 #define AH_GDN2_BWD(T, TD, KK) \
-  return gdn2_backward_impl<T, TD, KK>(p, q, k, v, w, b, g, h0, dO, dh_final, dq, dk, dv, dw, db, dg, dh0, ws, reuse, st)
+  return gdn2_backward_impl<T, TD, KK>(p, q, k, v, w, b, g, h0, dO, dh_final, dq, dk, dv, dw, db, dg, dh0, ws, reuse, L)
   if (dtype == ATOMIC_BF16) {
     if (p.dm.K == 128) {
       if (do_dtype == ATOMIC_BF16) AH_GDN2_BWD(bf16, bf16, 128);
@@ -158,13 +170,13 @@ int gdn2_backward(const Gdn2Plan& p, int dtype, int do_dtype, const void* q, con
 
 int gdn2_forward(const Gdn2Plan& p, int dtype, const void* q, const void* k, const void* v,
                  const void* w, const void* b, const float* g, const float* h0, float* o,
-                 float* h_final, void* ws, int save, hipStream_t st) {
+                 float* h_final, void* ws, int save, Launch& L) {
   if (dtype == ATOMIC_BF16) {
-    if (p.dm.K == 128) return gdn2_forward_impl<bf16, 128>(p, q, k, v, w, b, g, h0, o, h_final, ws, save, st);
-    return gdn2_forward_impl<bf16, 64>(p, q, k, v, w, b, g, h0, o, h_final, ws, save, st);
+    if (p.dm.K == 128) return gdn2_forward_impl<bf16, 128>(p, q, k, v, w, b, g, h0, o, h_final, ws, save, L);
+    return gdn2_forward_impl<bf16, 64>(p, q, k, v, w, b, g, h0, o, h_final, ws, save, L);
   }
-  if (p.dm.K == 128) return gdn2_forward_impl<float, 128>(p, q, k, v, w, b, g, h0, o, h_final, ws, save, st);
-  return gdn2_forward_impl<float, 64>(p, q, k, v, w, b, g, h0, o, h_final, ws, save, st);
+  if (p.dm.K == 128) return gdn2_forward_impl<float, 128>(p, q, k, v, w, b, g, h0, o, h_final, ws, save, L);
+  return gdn2_forward_impl<float, 64>(p, q, k, v, w, b, g, h0, o, h_final, ws, save, L);
 }
 
 }  // namespace ah
@@ -197,8 +209,9 @@ extern "C" int atomic_gdn2_fwd(const atomic_gdn2_args* a, const void* q, const v
   if (rc != ATOMIC_OK) return rc;
   if (!q || !k || !v || !w || !b || !g || !o || !h_final) return ATOMIC_ERR_NULL;
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
+  Launch L{a->profile, (hipStream_t)stream};
   return gdn2_forward(p, a->dtype, q, k, v, w, b, g, h0, o, h_final, workspace,
-                      (a->flags & ATOMIC_GDN2_SAVE) ? 1 : 0, (hipStream_t)stream);
+                      (a->flags & ATOMIC_GDN2_SAVE) ? 1 : 0, L);
 }
 
 extern "C" int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
@@ -213,7 +226,7 @@ extern "C" int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const v
   if (!q || !k || !v || !w || !b || !g || !dO || !dq || !dk || !dv || !dw || !db || !dg)
     return ATOMIC_ERR_NULL;
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
+  Launch L{a->profile, (hipStream_t)stream};
   return gdn2_backward(p, a->dtype, a->do_dtype, q, k, v, w, b, g, h0, dO, dh_final, dq, dk, dv, dw,
-                       db, dg, dh0, workspace, (a->flags & ATOMIC_GDN2_REUSE) != 0,
-                       (hipStream_t)stream);
+                       db, dg, dh0, workspace, (a->flags & ATOMIC_GDN2_REUSE) != 0, L);
 }

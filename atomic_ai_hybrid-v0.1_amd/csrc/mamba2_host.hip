@@ -2,6 +2,7 @@
 // template dispatch and the extern "C" entry points of include/atomic_hybrid.h.
 #include "../../include/atomic_hybrid.h"
 #include "mamba2_bwd.hip"
+#include "launch.hpp"
 
 namespace ah {
 
@@ -56,18 +57,21 @@ static Mamba2Chunks<T> mamba2_chunks(const Mamba2Plan& p, void* ws) {
 template <int C, int P, int N>
 static int mamba2_forward_impl(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm,
                                const void* Cm, const float* A, const float* state0, float* y,
-                               float* state_final, void* ws, int save, hipStream_t st) {
+                               float* state_final, void* ws, int save, Launch& L) {
   typedef bf16 T;
   constexpr int PT = 16;
   Mamba2Chunks<T> ck = mamba2_chunks<T>(p, ws);
-  hipLaunchKernelGGL((mamba2_cb<T, C, N>), dim3((unsigned)(p.dm.B * p.dm.NT)), dim3(256), 0, st,
-                     p.dm, (const T*)Bm, (const T*)Cm, ck);
-  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
-  hipLaunchKernelGGL((mamba2_scan<T, C, P, N, PT>), dim3((unsigned)(p.dm.B * p.dm.H * (P / PT))),
-                     dim3(256), 0, st, p.dm, (const T*)dt, (const T*)x, A, (const T*)Bm,
-                     (const T*)Cm, state0, ck, y, state_final, save);
-  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
-  return ATOMIC_OK;
+  hipStream_t st = L.st;
+  int rc = L("mamba2_cb", [&] {
+    hipLaunchKernelGGL((mamba2_cb<T, C, N>), dim3((unsigned)(p.dm.B * p.dm.NT)), dim3(256), 0, st,
+                       p.dm, (const T*)Bm, (const T*)Cm, ck);
+  });
+  if (rc) return rc;
+  return L("mamba2_scan", [&] {
+    hipLaunchKernelGGL((mamba2_scan<T, C, P, N, PT>), dim3((unsigned)(p.dm.B * p.dm.H * (P / PT))),
+                       dim3(256), 0, st, p.dm, (const T*)dt, (const T*)x, A, (const T*)Bm,
+                       (const T*)Cm, state0, ck, y, state_final, save);
+  });
 }
 
 template <typename T>
@@ -85,7 +89,7 @@ template <int C, int P, int N, typename TD>
 static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm,
                              const void* Cm, const float* A, const float* state0, const void* dy,
                              const float* dstate_final, void* ddt, void* dx, void* dB, void* dC,
-                             float* dA, float* dstate0, void* ws, bool reuse, hipStream_t st);
+                             float* dA, float* dstate0, void* ws, bool reuse, Launch& L);
 
 #define AH_M2_DISPATCH(FN, ...)                                                         \
   do {                                                                                  \
@@ -103,39 +107,47 @@ static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x,
 
 int mamba2_forward(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm, const void* Cm,
                    const float* A, const float* state0, float* y, float* state_final, void* ws,
-                   int save, hipStream_t st) {
-  AH_M2_DISPATCH(mamba2_forward_impl, p, dt, x, Bm, Cm, A, state0, y, state_final, ws, save, st);
+                   int save, Launch& L) {
+  AH_M2_DISPATCH(mamba2_forward_impl, p, dt, x, Bm, Cm, A, state0, y, state_final, ws, save, L);
 }
 
 template <int C, int P, int N, typename TD>
 static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm,
                              const void* Cm, const float* A, const float* state0, const void* dy,
                              const float* dstate_final, void* ddt, void* dx, void* dB, void* dC,
-                             float* dA, float* dstate0, void* ws, bool reuse, hipStream_t st) {
+                             float* dA, float* dstate0, void* ws, bool reuse, Launch& L) {
   typedef bf16 T;
+  int rc;
   if (!reuse) {
     // recompute the forward's per-chunk states (the reference re-runs the
     // forward scan, mamba2_bwd_reference.py:229-234)
-    const int rc = mamba2_forward_impl<C, P, N>(p, dt, x, Bm, Cm, A, state0, nullptr, nullptr, ws, 1, st);
-    if (rc != ATOMIC_OK) return rc;
+    rc = mamba2_forward_impl<C, P, N>(p, dt, x, Bm, Cm, A, state0, nullptr, nullptr, ws, 1, L);
+    if (rc) return rc;
   }
   Mamba2Chunks<T> ck = mamba2_chunks<T>(p, ws);
   Mamba2Grads<T> gr = mamba2_grads<T>(p, ws);
   constexpr int PT = 16;
-  hipLaunchKernelGGL((mamba2_bwd_dstate<T, TD, C, P, N, PT>), dim3((unsigned)(p.dm.B * p.dm.H * (P / PT))),
-                     dim3(256), 0, st, p.dm, (const T*)dt, A, (const T*)Cm, (const TD*)dy, dstate_final,
-                     ck, gr, dstate0);
-  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
-  hipLaunchKernelGGL((mamba2_bwd_chunk<T, TD, C, P, N>), dim3((unsigned)(p.dm.B * p.dm.NT * p.G)), dim3(256),
-                     0, st, p.dm, p.G, (const T*)dt, (const T*)x, A, (const T*)Bm, (const T*)Cm,
-                     (const TD*)dy, ck, gr, (T*)ddt, (T*)dx);
-  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
-  hipLaunchKernelGGL((mamba2_bwd_bc<T, C, N>), dim3((unsigned)(p.dm.B * p.dm.NT)), dim3(256), 0, st, p.dm,
-                     p.G, (const T*)Bm, (const T*)Cm, gr, (T*)dB, (T*)dC);
-  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
-  hipLaunchKernelGGL(mamba2_bwd_da, dim3(1), dim3(256), 0, st, p.dm, (const float*)gr.dap, dA);
-  if (hipGetLastError() != hipSuccess) return ATOMIC_ERR_LAUNCH;
-  return ATOMIC_OK;
+  hipStream_t st = L.st;
+  rc = L("mamba2_bwd_dstate", [&] {
+    hipLaunchKernelGGL((mamba2_bwd_dstate<T, TD, C, P, N, PT>), dim3((unsigned)(p.dm.B * p.dm.H * (P / PT))),
+                       dim3(256), 0, st, p.dm, (const T*)dt, A, (const T*)Cm, (const TD*)dy, dstate_final,
+                       ck, gr, dstate0);
+  });
+  if (rc) return rc;
+  rc = L("mamba2_bwd_chunk", [&] {
+    hipLaunchKernelGGL((mamba2_bwd_chunk<T, TD, C, P, N>), dim3((unsigned)(p.dm.B * p.dm.NT * p.G)),
+                       dim3(256), 0, st, p.dm, p.G, (const T*)dt, (const T*)x, A, (const T*)Bm,
+                       (const T*)Cm, (const TD*)dy, ck, gr, (T*)ddt, (T*)dx);
+  });
+  if (rc) return rc;
+  rc = L("mamba2_bwd_bc", [&] {
+    hipLaunchKernelGGL((mamba2_bwd_bc<T, C, N>), dim3((unsigned)(p.dm.B * p.dm.NT)), dim3(256), 0, st,
+                       p.dm, p.G, (const T*)Bm, (const T*)Cm, gr, (T*)dB, (T*)dC);
+  });
+  if (rc) return rc;
+  return L("mamba2_bwd_da", [&] {
+    hipLaunchKernelGGL(mamba2_bwd_da, dim3(1), dim3(256), 0, st, p.dm, (const float*)gr.dap, dA);
+  });
 }
 
 template <int C, int P, int N>
@@ -143,20 +155,20 @@ static int mamba2_backward_impl(const Mamba2Plan& p, int dy_dtype, const void* d
                                 const void* Bm, const void* Cm, const float* A, const float* state0,
                                 const void* dy, const float* dstate_final, void* ddt, void* dx,
                                 void* dB, void* dC, float* dA, float* dstate0, void* ws, bool reuse,
-                                hipStream_t st) {
+                                Launch& L) {
   if (dy_dtype == ATOMIC_BF16)
     return mamba2_backward_t<C, P, N, bf16>(p, dt, x, Bm, Cm, A, state0, dy, dstate_final, ddt, dx, dB,
-                                            dC, dA, dstate0, ws, reuse, st);
+                                            dC, dA, dstate0, ws, reuse, L);
   return mamba2_backward_t<C, P, N, float>(p, dt, x, Bm, Cm, A, state0, dy, dstate_final, ddt, dx, dB,
-                                           dC, dA, dstate0, ws, reuse, st);
+                                           dC, dA, dstate0, ws, reuse, L);
 }
 
 int mamba2_backward(const Mamba2Plan& p, int dy_dtype, const void* dt, const void* x, const void* Bm,
                     const void* Cm, const float* A, const float* state0, const void* dy,
                     const float* dstate_final, void* ddt, void* dx, void* dB, void* dC, float* dA,
-                    float* dstate0, void* ws, bool reuse, hipStream_t st) {
+                    float* dstate0, void* ws, bool reuse, Launch& L) {
   AH_M2_DISPATCH(mamba2_backward_impl, p, dy_dtype, dt, x, Bm, Cm, A, state0, dy, dstate_final, ddt, dx,
-                 dB, dC, dA, dstate0, ws, reuse, st);
+                 dB, dC, dA, dstate0, ws, reuse, L);
 }
 
 }  // namespace ah
@@ -178,8 +190,9 @@ extern "C" int atomic_mamba2_fwd(const atomic_mamba2_args* a, const void* dt, co
   if (rc != ATOMIC_OK) return rc;
   if (!dt || !x || !B || !C || !A || !y || !state_final) return ATOMIC_ERR_NULL;
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
+  Launch L{a->profile, (hipStream_t)stream};
   return mamba2_forward(p, dt, x, B, C, A, state0, y, state_final, workspace,
-                        (a->flags & ATOMIC_MAMBA2_SAVE) ? 1 : 0, (hipStream_t)stream);
+                        (a->flags & ATOMIC_MAMBA2_SAVE) ? 1 : 0, L);
 }
 
 extern "C" int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, const void* x,
@@ -192,6 +205,7 @@ extern "C" int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, co
   if (rc != ATOMIC_OK) return rc;
   if (!dt || !x || !B || !C || !A || !dy || !ddt || !dx || !dB || !dC || !dA) return ATOMIC_ERR_NULL;
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
+  Launch L{a->profile, (hipStream_t)stream};
   return mamba2_backward(p, a->dy_dtype, dt, x, B, C, A, state0, dy, dstate_final, ddt, dx, dB, dC, dA,
-                         dstate0, workspace, (a->flags & ATOMIC_MAMBA2_REUSE) != 0, (hipStream_t)stream);
+                         dstate0, workspace, (a->flags & ATOMIC_MAMBA2_REUSE) != 0, L);
 }

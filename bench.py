@@ -1,0 +1,267 @@
+"""Benchmark of the GDN2 + Mamba2 SSD chunked forward+backward on one MI355X.
+
+One step = the two paths' training step over one batch of synthetic inputs
+already resident in HBM:
+  GDN2   forward (saving the per-chunk intermediates) + backward   B4 T8192 H16 K=V=128 C64
+  Mamba2 forward (saving the per-chunk states) + backward          B4 T8192 H16 P128 N128 C128
+The value is tokens/s = B*T / step time.  Per-kernel durations come from HIP
+events that the library records around each of its launches, on the launch
+stream, over the timed steps; the dominant kernel's roofline fraction is its
+algorithmic bytes (or flops) per launch over that average duration.
+
+The CPU baseline times this repository's float32 restatement of the
+reference algorithm (the test oracle) on a bounded sample of the same
+workload, on the host's cores, at N=1 only.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "atomic_ai_hybrid-v0.1_amd")]
+
+METRIC = "tokens/sec GDN2+SSD chunked fwd+bwd at T=8192 on 1 MI355X; % MFMA/HBM peak"
+HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
+MFMA_BF16_PEAK = 2.5e15    # flop/s, dense bf16
+RIDGE = MFMA_BF16_PEAK / HBM_PEAK
+
+GDN2 = dict(B=4, T=8192, H=16, K=128, V=128, C=64)
+MAMBA2 = dict(B=4, T=8192, H=16, P=128, N=128, C=128)
+CPU_SAMPLE_T = 2048        # tokens of the bounded CPU sample (batch 1, same heads)
+CPU_THREADS_MAX = 16
+
+
+# --------------------------------------------------------------------------- models
+def gdn2_kernel_model(B, T, H, K, V, C, es=2, save=True):
+    """Algorithmic (flops, HBM bytes) per launch of each GDN2 kernel: every
+    operand the kernel must read and every result it must write, once.  U
+    counts (batch, head, chunk) units; operands are bf16 (es bytes), g and
+    the backward's per-chunk gradients float32, o float32."""
+    U = B * H * (T // C)
+    CK, CV, CC, KV = C * K, C * V, C * C, K * V
+    return {
+        "gdn2_fwd_intra": (U * (6 * CC * K + 2 * CC * V + C ** 3 / 3),
+                           U * (3 * CK * es + CK * 4 + 2 * CV * es          # q k b g v w
+                                + 3 * CK * es + CV * es + 2 * CC * es + K * 4)),  # qg kg wt u aqk ainv gcl
+        "gdn2_fwd_state": (U * (6 * C * KV + 2 * CC * V),
+                           U * (3 * CK * es + CV * es + CC * es + K * 4     # qg kg wt u aqk gcl
+                                + CV * 4                                     # o
+                                + (KV * es + CV * es if save else 0))),      # h_pre, v_new
+        "gdn2_bwd_dh": (U * (2 * CC * V + 6 * C * KV),
+                        U * (CV * es + CC * es + 3 * CK * es + K * 4        # dO aqk qg kg wt gcl
+                             + CV * 4 + KV * es) + B * H * KV * 4),          # dv_new, dh_next; dh0
+        "gdn2_bwd_hgrad": (U * (2 * CC * V + 6 * C * KV),
+                           U * (CV * es + CV * 4 + 2 * KV * es + CV * es + K * 4   # dO dvn h dh vn gcl
+                                + CC * 4 + 3 * CK * 4 + K * 4)),             # daqk dqg dwt dkg rlast
+        "gdn2_bwd_wy": (U * (4 * CC * K + 4 * CC * V + 4 * C ** 3),
+                        U * (CC * es + CV * 4 + CK * 4 + 2 * CK * es + 2 * CV * es + CK * 4  # ainv dvn dwt k b v w g
+                             + CC * 4 + CK * 4 + 2 * CV * es)),              # dakk dkb dw dv
+        "gdn2_bwd_intra": (U * 8 * CC * K,
+                           U * (3 * CK * es + CK * 4 + 2 * CC * 4 + 3 * CK * 4 + K * 4  # q k b g daqk dakk dkg dqg dkb rlast
+                                + 3 * CK * es + CK * 4)),                    # dq dk db dg
+    }
+
+
+def mamba2_groups(B, T, H, C):
+    NT = T // C
+    G = 1
+    while G * B * NT < 256 and 2 * G <= H and H % (2 * G) == 0:
+        G *= 2
+    return G
+
+
+def mamba2_kernel_model(B, T, H, P, N, C, es=2, save=True):
+    """Algorithmic (flops, HBM bytes) per launch of each Mamba2 kernel.  Uh
+    counts (batch, head, chunk) units, Ub (batch, chunk) units (B, C and the
+    C·Bᵀ scores are shared by every head); y is float32."""
+    NT = T // C
+    Uh, Ub = B * H * NT, B * NT
+    G = mamba2_groups(B, T, H, C)
+    CP, CN, CC, PN = C * P, C * N, C * C, P * N
+    part = G * (CC + 2 * CN) * 4
+    return {
+        "mamba2_cb": (Ub * 2 * CC * N, Ub * (2 * CN * es + CC * es)),
+        "mamba2_scan": (Uh * (2 * CC * P + 4 * C * PN),
+                        Uh * (2 * CP * es + CP * 4 + (PN * es if save else 0))
+                        + Ub * (2 * CN * es + CC * es)),
+        "mamba2_bwd_dstate": (Uh * 2 * C * PN,
+                              Uh * (2 * CP * es + 2 * PN * es + P * 4) + Ub * CN * es
+                              + B * H * PN * 4),
+        "mamba2_bwd_chunk": (Uh * (4 * CC * P + 6 * C * PN),
+                             Uh * (3 * CP * es + 2 * PN * es + P * 4 + 2 * CP * es + 4)
+                             + Ub * (2 * CN * es + CC * es + part)),
+        "mamba2_bwd_bc": (Ub * 4 * CC * N, Ub * (2 * CN * es + part + 2 * CN * es)),
+        "mamba2_bwd_da": (0.0, B * NT * H * 4 + H * 4),
+    }
+
+
+def roofline(flops, nbytes, seconds):
+    ai = flops / nbytes if nbytes else float("inf")
+    if ai < RIDGE:
+        achieved = nbytes / seconds / 1e9
+        return dict(bound="hbm", achieved=achieved, peak=HBM_PEAK / 1e9, unit="GB/s",
+                    frac=achieved / (HBM_PEAK / 1e9))
+    achieved = flops / seconds / 1e12
+    return dict(bound="mfma", achieved=achieved, peak=MFMA_BF16_PEAK / 1e12, unit="TFLOP/s",
+                frac=achieved / (MFMA_BF16_PEAK / 1e12))
+
+
+# --------------------------------------------------------------------------- CPU baseline
+def cpu_baseline(sample_t=CPU_SAMPLE_T):
+    """Times the float32 restatement (oracle/) of the reference's GDN2 WY
+    forward + B1..B5 backward and Mamba2 SSD forward + MB0 backward on
+    batch 1, ``sample_t`` tokens, the benchmark's head shapes."""
+    import torch
+    from atomic_ops import inputs
+    from oracle import gdn2 as og, mamba2 as om
+    threads = max(1, min(os.cpu_count() or 1, CPU_THREADS_MAX))
+    torch.set_num_threads(threads)
+    f = torch.float32
+    g, m = GDN2, MAMBA2
+
+    def run(T):
+        d = inputs.gdn2_inputs(1, T, g["H"], g["K"], g["V"], seed=11, dO=True)
+        q, k, v, w, b, do = (d[n].to(f) for n in ("q", "k", "v", "w", "b", "do"))
+        og.gdn2_chunked_wy_reference(q, k, v, d["g"], b, w, 1.0, g["C"], dtype=f)
+        og.gdn2_backward_chain(q, k, v, w, b, d["g"], 1.0, g["C"], do, dtype=f)
+        e = inputs.mamba2_inputs(1, T, m["H"], m["P"], m["N"], seed=12, dO=True)
+        dt, x, Bm, Cm, A, dy = (e[n].to(f) for n in ("dt", "x", "Bm", "Cm", "A", "dy"))
+        om.mamba2_ssd_reference(dt, A, Bm, Cm, x, m["C"], dtype=f)
+        om.chunk_ssd_bwd_scan(dt, A, Bm, Cm, x, m["C"], dy, dtype=f)
+
+    run(m["C"])                       # warm-up: one chunk of each path
+    t0 = time.perf_counter()
+    run(sample_t)
+    sec = time.perf_counter() - t0
+    return {"value": sample_t / sec, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle/ float32 restatement, GDN2 fwd + B1..B5 bwd and Mamba2 fwd + MB0 "
+                       f"bwd at batch 1, T={sample_t}, the benchmark's head shapes; "
+                       f"{sec:.1f} s on {threads} threads (work is linear in B*T)")}
+
+
+# --------------------------------------------------------------------------- GPU step
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(every (batch, head) unit is independent; sharding is described in the "
+              "design notes, not implemented). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from atomic_ops import _lib, inputs
+    from atomic_ops import gdn2 as G2
+    from atomic_ops import mamba2 as M2
+    _lib.load()   # raises if the HIP library is not built: there is no fallback
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    g, m = GDN2, MAMBA2
+    gi = inputs.gdn2_inputs(g["B"], g["T"], g["H"], g["K"], g["V"], seed=2, device=dev, dO=True)
+    mi = inputs.mamba2_inputs(m["B"], m["T"], m["H"], m["P"], m["N"], seed=3, device=dev, dO=True)
+    q, k, v, w, b, gg, do = (gi[n] for n in ("q", "k", "v", "w", "b", "g", "do"))
+    dt, x, Bm, Cm, A, dy = (mi[n] for n in ("dt", "x", "Bm", "Cm", "A", "dy"))
+    scale = 1.0
+    g_args = G2.make_args(q, v, scale, flags=_lib.GDN2_SAVE)
+    g_ws = G2.new_workspace(g_args, dev)
+    m_ws = torch.empty(M2.workspace_bytes(M2.make_args(dt, Bm, m["C"])), dtype=torch.uint8, device=dev)
+
+    # one set of event pairs per timed step, so the timed region has no host sync
+    timers = [[_lib.KernelTimer(dev) for _ in range(4)] for _ in range(args.steps)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+
+    def step(i=None):
+        t = timers[i] if i is not None else [None] * 4
+        if i is not None:
+            ev[i][0].record()
+        G2.forward(q, k, v, w, b, gg, scale, save=True, workspace=g_ws, timer=t[0])
+        G2.backward(q, k, v, w, b, gg, scale, do, workspace=g_ws, reuse=True, timer=t[1])
+        if i is not None:
+            ev[i][1].record()
+        M2.forward(dt, x, Bm, Cm, A, m["C"], save=True, workspace=m_ws, timer=t[2])
+        M2.backward(dt, x, Bm, Cm, A, m["C"], dy, workspace=m_ws, reuse=True, timer=t[3])
+        if i is not None:
+            ev[i][2].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Timed region: exactly K steps, no host synchronisation inside.
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    kern_ms = {}
+    path_ms = {"gdn2": [], "mamba2": []}
+    for i in range(args.steps):
+        for tm in timers[i]:
+            for name, ms in tm.durations():
+                kern_ms.setdefault(name, []).append(ms)
+        path_ms["gdn2"].append(ev[i][0].elapsed_time(ev[i][1]))
+        path_ms["mamba2"].append(ev[i][1].elapsed_time(ev[i][2]))
+
+    step_dev_ms = [a + b_ for a, b_ in zip(path_ms["gdn2"], path_ms["mamba2"])]
+    ms_per_step = wall * 1e3 / args.steps
+    tokens = g["B"] * g["T"]
+    value = tokens / (ms_per_step / 1e3)
+
+    models = {}
+    models.update(gdn2_kernel_model(**g))
+    models.update(mamba2_kernel_model(**m))
+    kernels = {}
+    for name, ms in kern_ms.items():
+        per_step = sum(ms) / args.steps        # kernel time per step
+        launches = len(ms) / args.steps
+        avg = sum(ms) / len(ms)
+        fl, by = models[name]
+        rf = roofline(fl, by, avg / 1e3)
+        kernels[name] = dict(ms_per_launch=round(avg, 4), launches_per_step=launches,
+                             ms_per_step=round(per_step, 4), bytes=int(by), flops=fl,
+                             gbps=round(by / (avg / 1e3) / 1e9, 1),
+                             tflops=round(fl / (avg / 1e3) / 1e12, 2),
+                             bound=rf["bound"], frac=round(rf["frac"], 4))
+    dom = max(kernels, key=lambda n: kernels[n]["ms_per_step"])
+    fl, by = models[dom]
+    rf = roofline(fl, by, kernels[dom]["ms_per_launch"] / 1e3)
+    rf = {k_: (round(v_, 4) if isinstance(v_, float) else v_) for k_, v_ in rf.items()}
+    rf["kernel"] = dom
+    rf["traffic"] = None
+
+    cpu = None if args.no_cpu else cpu_baseline()
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded, the benchmark configurations' distributions)",
+        "config": {"workload": "GDN2 WY + Mamba2 SSD chunked fwd+bwd",
+                   "gdn2": "B4 T8192 H16 K=V=128 C64 bf16 (g f32), scale 1",
+                   "mamba2": "B4 T8192 H16 P128 N128 C128 bf16 (A f32)",
+                   "tokens_per_step": tokens},
+        "roofline": rf,
+        "cpu_baseline": cpu,
+        "paths_ms_median": {k_: round(statistics.median(v_), 4) for k_, v_ in path_ms.items()},
+        "device_ms_per_step_median": round(statistics.median(step_dev_ms), 4),
+        "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

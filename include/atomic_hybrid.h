@@ -37,6 +37,20 @@ enum {
 
 enum { ATOMIC_F32 = 0, ATOMIC_BF16 = 1 };
 
+/* Optional per-kernel timing: when an args struct's `profile` is non-NULL the
+   call records start[k] / stop[k] (hipEvent_t created by the caller) on its
+   stream around the k-th kernel it launches, for k < capacity, and reports
+   how many kernels it launched in `count` with their names in `names`.  No
+   host synchronisation; the caller reads the events after the stream. */
+#define ATOMIC_PROFILE_MAX 16
+typedef struct atomic_profile {
+  void* start[ATOMIC_PROFILE_MAX];
+  void* stop[ATOMIC_PROFILE_MAX];
+  int32_t capacity;
+  int32_t count;
+  const char* names[ATOMIC_PROFILE_MAX];
+} atomic_profile;
+
 /* ------------------------------------------------------------------ GDN2 */
 
 /* Flags for atomic_gdn2_args.flags */
@@ -61,6 +75,7 @@ typedef struct atomic_gdn2_args {
   int32_t do_dtype;  /* upstream gradient dO: ATOMIC_F32 / ATOMIC_BF16          */
   float scale;       /* query scale (the model passes 1.0, model.py:631)        */
   int32_t flags;     /* ATOMIC_GDN2_*                                           */
+  atomic_profile* profile;  /* optional per-kernel event timing, or NULL      */
 } atomic_gdn2_args;
 
 /* Bytes of workspace atomic_gdn2_fwd / atomic_gdn2_bwd need for these args. */
@@ -130,6 +145,7 @@ typedef struct atomic_mamba2_args {
   int32_t dtype;     /* dt, x, B, C and their gradients: ATOMIC_BF16       */
   int32_t dy_dtype;  /* upstream gradient dy: ATOMIC_F32 / ATOMIC_BF16     */
   int32_t flags;     /* ATOMIC_MAMBA2_*                                    */
+  atomic_profile* profile;  /* optional per-kernel event timing, or NULL */
 } atomic_mamba2_args;
 
 /* Bytes of workspace atomic_mamba2_fwd / atomic_mamba2_bwd need. */
