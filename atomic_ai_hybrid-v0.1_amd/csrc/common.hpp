@@ -144,6 +144,14 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// A zero the compiler cannot see through: offsets built from it are recomputed
+// where they are used instead of being hoisted out of enclosing loops.
+__device__ __forceinline__ int opaque_zero() {
+  int z = 0;
+  asm volatile("" : "+s"(z));
+  return z;
+}
+
 __device__ __forceinline__ f32x4 zero4() { f32x4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
 
 // Tile element coordinates held by this lane: rows m0 + 4g + i, column n0 + r.
@@ -161,6 +169,26 @@ __device__ __forceinline__ void store_tile_n(T* dst, int ld, int m0, int n0, f32
 #pragma unroll
   for (int i = 0; i < 4; ++i) dst[(m0 + tile_row(i)) * ld + n0 + tile_col()] = from_f<T>(v[i]);
 }
+
+// Eight consecutive elements held raw (loads stay in flight until first use).
+template <typename T> struct Raw8;
+template <> struct Raw8<bf16> {
+  uint4 v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ float operator[](int j) const {
+    return (float)reinterpret_cast<const bf16*>(&v)[j];
+  }
+};
+template <> struct Raw8<float> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const float4*>(p);
+    b = *reinterpret_cast<const float4*>(p + 4);
+  }
+  __device__ __forceinline__ float operator[](int j) const {
+    return j < 4 ? (&a.x)[j] : (&b.x)[j - 4];
+  }
+};
 
 // Row padding (elements) that keeps rows 16-byte aligned.
 template <typename T> struct Pad { static constexpr int v = 16 / sizeof(T); };

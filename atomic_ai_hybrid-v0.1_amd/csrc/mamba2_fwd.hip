@@ -1,27 +1,40 @@
 // Mamba2 SSD chunk-scan forward for gfx950.
 //
-// mamba2_cb    one workgroup per (batch, chunk): CB = sanitize(C B^T), the
-//              [C][C] score shared by every head (mamba2_ssd_reference.py:122-123;
-//              the reference's M3 broadcasts B/C to every head instead,
-//              kernel_mamba2_b_intra.py:136-142).
-// mamba2_scan  one workgroup per (batch, head, PT channels), sequential over
-//              chunks; the fp32 [PT][N] state stays in MFMA accumulators.  Per
-//              chunk it follows _chunk_ssd (mamba2_ssd_reference.py:70-149):
-//                cum    = sanitize(cumsum(sanitize(dt A, 20)), 1e4)
-//                y_diag = sum_{j<=i} exp(clip(cum_i - cum_j, +-20)) CB_ij dBx_j
-//                state_end = sum_j B_j (dBx_j exp(clip(cum_last - cum_j, +-20)))
-//                y_off  = (C state_prev) exp(clip(cum, -20, 0))
-//                state  = sanitize(state exp(clip(cum_last, -20, 0)) + state_end)
-//              y_diag is split into 16-row blocks.  For a source block J below
-//              the output block I the decay factorises as
-//              exp(cum_i - cum_r) exp(cum_r - cum_j) with r the first row of I;
-//              both factors are <= 1 whenever dt A <= 0 (the model's A < 0,
-//              dt > 0), so the off-diagonal part is one bf16 MFMA GEMM per block
-//              with no overflow.  Pairs there whose decay is below -20 carry
-//              their true weight instead of the reference's exp(-20) floor
-//              (a difference below 2e-9 |CB dBx|).  Diagonal 16x16 blocks are
-//              evaluated pairwise exactly as the reference does.  A chunk with
-//              any dt A > 0 evaluates every pair that way.
+// The state transition of a chunk is diagonal (state[p][s] decays by
+// exp(cum_last[p]) independently of s), so the only sequential part of the
+// scan is an elementwise recurrence; everything with a contraction runs
+// chunk-parallel.  Per chunk the arithmetic follows _chunk_ssd
+// (mamba2_ssd_reference.py:70-149):
+//   a      = sanitize(dt A, 20)                 cum = sanitize(cumsum(a), 1e4)
+//   y_diag = sum_{j<=i} min(exp(clip(cum_i - cum_j, +-20)), 1e6) CB_ij dBx_j
+//   s_end  = sanitize(B^T (dBx sanitize(exp(clip(cum_last - cum, +-20)), 1e6)))
+//   y_off  = sanitize((C state^T) exp(clip(cum, -20, 0)))
+//   state  = sanitize(state exp(clip(cum_last, -20, 0)) + s_end)
+//
+// mamba2_cb           one workgroup per (batch, chunk): CB = sanitize(C B^T),
+//                     shared by every head (the reference's M3 broadcasts B/C
+//                     to every head instead, kernel_mamba2_b_intra.py:136-142).
+// mamba2_chunk_outer  one workgroup per (batch, chunk, head, channel slice):
+//                     the chunk's cum and s_end = W^T B (forward), or the
+//                     backward's (dy decay_h)^T C, Ydh and W (BWD = true).
+// mamba2_state_pass   one workgroup per (batch, head, 8 or 16 channels),
+//                     sequential over chunks, elementwise: the state entering
+//                     every chunk (forward) or the dstate carry and the
+//                     decay_chunk_end term (backward).
+// mamba2_chunk_y      one workgroup per (batch, chunk, head, 32 channels):
+//                     y = y_diag + y_off.
+//
+// y_diag off the diagonal 16-row blocks: for output block I and source block
+// J < I the decay factorises as
+//   exp(cum_i - cum_j) = exp(cum_i - cum_{16I}) exp(cum_{16I} - cum_{16J+15})
+//                        exp(cum_{16J+15} - cum_j),
+// each factor <= 1 whenever dt A <= 0 (the model's A < 0, dt > 0), so the
+// pair (I, J) is one MFMA on V_j = exp(cum_{16J+15} - cum_j) dBx_j with a
+// per-channel scale, and nothing overflows.  Pairs there whose decay is below
+// -20 carry their true weight instead of the reference's exp(-20) floor (a
+// difference below 2e-9 |CB dBx|).  Diagonal 16x16 blocks are evaluated
+// pairwise exactly as the reference does, and a slice with any dt A > 0
+// evaluates every pair that way.
 #include "mamba2.hpp"
 
 namespace ah {
@@ -34,12 +47,8 @@ __global__ __launch_bounds__(256) void mamba2_cb(Mamba2Dims dm, const T* __restr
   __shared__ __attribute__((aligned(16))) T sC[C * LN];
   const int bn = blockIdx.x;  // b * NT + n
   const size_t row0 = (size_t)bn * C;  // rows of [B*T][N]
-  constexpr int VEC = 16 / sizeof(T), PER_ROW = N / VEC;
-  for (int e = threadIdx.x; e < C * PER_ROW; e += 256) {
-    const int r = e / PER_ROW, c = (e % PER_ROW) * VEC;
-    *reinterpret_cast<uint4*>(sB + r * LN + c) = *reinterpret_cast<const uint4*>(Bm + (row0 + r) * N + c);
-    *reinterpret_cast<uint4*>(sC + r * LN + c) = *reinterpret_cast<const uint4*>(Cm + (row0 + r) * N + c);
-  }
+  stage_rows<T, C, N>(sB, LN, Bm + row0 * N, N);
+  stage_rows<T, C, N>(sC, LN, Cm + row0 * N, N);
   __syncthreads();
   constexpr int MT = C / 16;
   T* out = ck.cb + (size_t)bn * C * C;
@@ -52,46 +61,16 @@ __global__ __launch_bounds__(256) void mamba2_cb(Mamba2Dims dm, const T* __restr
   }
 }
 
-// Rows of the block-I operand Z^(I) (source rows j < 16 I, padded to the MFMA k step).
-template <typename T>
-__host__ __device__ constexpr int zrows(int I) {
-  return ((16 * I + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
-}
-template <typename T>
-__host__ __device__ constexpr int zrows_before(int I) {
-  int s = 0;
-  for (int i = 1; i < I; ++i) s += zrows<T>(i);
-  return s;
-}
-
-template <typename T, int C, int N, int PT>
-struct ScanLds {
-  static constexpr int PAD = Pad<T>::v;
-  static constexpr int LN = N + PAD, LCB = C + PAD, LPT = PT + PAD;
-  static constexpr int NB = C / 16;
-  static constexpr int ZROWS = zrows_before<T>(NB);
-  static constexpr int NSEG = 256 / PT, RS = C / NSEG;
-  static constexpr int off_b = 0;
-  static constexpr int off_cb = off_b + C * LN * (int)sizeof(T);
-  static constexpr int off_z = off_cb + C * LCB * (int)sizeof(T);
-  static constexpr int off_w = off_z + ZROWS * LPT * (int)sizeof(T);
-  static constexpr int off_st = off_w + C * LPT * (int)sizeof(T);
-  static constexpr int off_cum = off_st + N * LPT * (int)sizeof(T);
-  static constexpr int off_dbx = off_cum + C * PT * 4;
-  static constexpr int off_tot = off_dbx + C * PT * 4;
-  static constexpr int total = off_tot + NSEG * PT * 4;
-  static_assert(RS >= 1 && C % NSEG == 0, "scan mapping");
-};
-
-// Inclusive column scan of sCum ([C][PT] fp32, holding sanitize(dt A, 20) on
-// entry) into sanitize(cumsum, 1e4).  Thread map: column tid % PT, RS rows.
-template <int C, int PT>
+// Inclusive column scan of sCum ([C][PT] fp32 with row stride LD, holding
+// sanitize(dt A, 20) on entry) into sanitize(cumsum, 1e4).  Thread map:
+// column tid % PT, RS rows.
+template <int C, int PT, int LD = PT>
 __device__ __forceinline__ void column_cumsum(float* sCum, float* sTot) {
   constexpr int NSEG = 256 / PT, RS = C / NSEG;
   const int p = threadIdx.x % PT, seg = threadIdx.x / PT;
   float v[RS];
 #pragma unroll
-  for (int r = 0; r < RS; ++r) v[r] = sCum[(seg * RS + r) * PT + p];
+  for (int r = 0; r < RS; ++r) v[r] = sCum[(seg * RS + r) * LD + p];
 #pragma unroll
   for (int r = 1; r < RS; ++r) v[r] += v[r - 1];
   sTot[seg * PT + p] = v[RS - 1];
@@ -99,210 +78,335 @@ __device__ __forceinline__ void column_cumsum(float* sCum, float* sTot) {
   float off = 0.f;
   for (int s = 0; s < seg; ++s) off += sTot[s * PT + p];
 #pragma unroll
-  for (int r = 0; r < RS; ++r) sCum[(seg * RS + r) * PT + p] = sanitize(v[r] + off, kClipAcc);
+  for (int r = 0; r < RS; ++r) sCum[(seg * RS + r) * LD + p] = sanitize(v[r] + off, kClipAcc);
+}
+
+// ------------------------------------------------------------------ chunk outer products
+template <typename T, int C, int N, int PT>
+struct OuterLds {
+  static constexpr int PAD = Pad<T>::v;
+  static constexpr int LS = PT + PAD, LN = N + PAD;
+  static constexpr int NSEG = 256 / PT;
+  static constexpr int off_cum = 0;  // fp32 cum [C][PT]; then the bf16 operand S [C][LS]
+  static constexpr int off_tot = off_cum + C * PT * 4;
+  static constexpr int off_r = off_tot + NSEG * PT * 4;
+  static constexpr int total = off_r + C * LN * (int)sizeof(T);
+  static_assert(C * LS * (int)sizeof(T) <= C * PT * 4, "S must fit in the cum buffer");
+};
+
+// out[p][s] = sum_i S[i][p] R[i][s] for one (batch, chunk, head, PT channels):
+//   forward  (BWD = false): S = dBx dte (the chunk's write, :133-135), R = B,
+//            out = sanitize(.) = state_end (:136-137); also the chunk's cum_last.
+//   backward (BWD = true):  S = Ydh = dy decay_h (:123 of mamba2_bwd_reference.py),
+//            R = C, out = (dy decay_h)^T C (:128); also writes Ydh and
+//            W = sanitize(dBx dte) (:135), the operands of dC_1 and dB_1.
+template <typename T, typename TD, int C, int P, int N, int PT, bool BWD>
+__global__ __launch_bounds__(256) void mamba2_chunk_outer(
+    Mamba2Dims dm, const T* __restrict__ dt, const T* __restrict__ x, const float* __restrict__ A,
+    const T* __restrict__ R, const TD* __restrict__ dy, Mamba2Chunks<T> ck, T* __restrict__ ydh,
+    T* __restrict__ wr) {
+  typedef OuterLds<T, C, N, PT> L;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
+  float* sCum = reinterpret_cast<float*>(lds + L::off_cum);
+  T* sS = reinterpret_cast<T*>(lds + L::off_cum);
+  float* sTot = reinterpret_cast<float*>(lds + L::off_tot);
+  T* sR = reinterpret_cast<T*>(lds + L::off_r);
+
+  constexpr int NPT = P / PT;
+  int bn, m;
+  xcd_group_map(blockIdx.x, dm.B * dm.NT, dm.H * NPT, bn, m);
+  const int h = m / NPT, p0 = (m % NPT) * PT;
+  const int bb = bn / dm.NT, n = bn % dm.NT;
+  const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
+  const size_t rsx = (size_t)dm.H * P;
+  const size_t base = (row0 * dm.H + h) * P + p0;  // element (r, c) at base + r * rsx + c
+  const float Ah = A[h];
+
+  constexpr int PER_ROW = PT / 8, NE = C * PER_ROW, EPT = NE / 256;
+  static_assert(NE % 256 == 0, "slice must split evenly over the workgroup");
+  Raw8<T> rdt[EPT], rx[EPT];
+  Raw8<TD> rdy[BWD ? EPT : 1];
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
+    rdt[i].load(dt + base + r * rsx + c);
+    rx[i].load(x + base + r * rsx + c);
+    if constexpr (BWD) rdy[i].load(dy + base + r * rsx + c);
+  }
+  stage_rows<T, C, N>(sR, L::LN, R + row0 * N, N);
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sCum[r * PT + c + j] = sanitize(rdt[i][j] * Ah, kClipDecay);
+  }
+  __syncthreads();
+  column_cumsum<C, PT>(sCum, sTot);
+  __syncthreads();
+
+  float sv[EPT][8];
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
+    float wv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float ci = sCum[r * PT + c + j];
+      const float cl = sCum[(C - 1) * PT + c + j];
+      const float dbx = sanitize(rdt[i][j] * rx[i][j]);
+      const float dte = sanitize(__expf(fminf(fmaxf(cl - ci, -kClipDecay), kClipDecay)), 1e6f);
+      if constexpr (BWD) {
+        sv[i][j] = rdy[i][j] * __expf(fminf(fmaxf(ci, -kClipDecay), 0.f));
+        wv[j] = sanitize(dbx * dte);
+      } else {
+        sv[i][j] = dbx * dte;
+      }
+    }
+    if constexpr (BWD) {
+      store8(ydh + base + r * rsx + c, sv[i]);
+      store8(wr + base + r * rsx + c, wv);
+    }
+  }
+  const size_t bnh = (size_t)bn * dm.H + h;
+  if (!BWD && threadIdx.x < PT) ck.cl[bnh * P + p0 + threadIdx.x] = sCum[(C - 1) * PT + threadIdx.x];
+  __syncthreads();  // every cum read is done: S overwrites the cum buffer
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
+    store8(sS + r * L::LS + c, sv[i]);
+  }
+  __syncthreads();
+
+  constexpr int NI = N / 16, TILES = (PT / 16) * NI, TPW = TILES / 4;
+  static_assert(TILES % 4 == 0, "tiles must split evenly over 4 waves");
+  float* out = ck.src + (bnh * P + p0) * N;
+  const int wv_id = wave_id();
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int tile = wv_id * TPW + t, mi = tile / NI, ni = tile % NI;
+    f32x4 acc = tile_mma<T, true, true>(zero4(), sS, L::LS, sR, L::LN, 16 * mi, 16 * ni, C);
+    if constexpr (!BWD) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[k] = sanitize(acc[k]);
+    }
+    store_tile_n(out, N, 16 * mi, 16 * ni, acc);
+  }
+}
+
+// ------------------------------------------------------------------ sequential pass
+// Forward: state entering chunk n -> state_pre (bf16), then
+//   state = sanitize(state exp(clip(cum_last, -20, 0)) + s_end)      (:144-146)
+// Backward (MB0, mamba2_bwd_reference.py:236-247), reverse over chunks:
+//   dstate carry entering chunk n's backward -> dstate (bf16);
+//   d_cum_last_a = sum_s dstate state_prev * decay_chunk_end * mask  (:116,120)
+//   dstate = sanitize(dstate decay_chunk_end + (dy decay_h)^T C)      (:115,128,195)
+// Thread map: one float4 of one channel row; RP channel rows per workgroup.
+template <typename T, int P, int N, bool BWD>
+__global__ __launch_bounds__(256) void mamba2_state_pass(Mamba2Dims dm, Mamba2Chunks<T> ck,
+                                                        T* __restrict__ dstate, float* __restrict__ lasta,
+                                                        const float* __restrict__ init,
+                                                        float* __restrict__ fin) {
+  constexpr int TPR = N / 4, RP = 256 / TPR, NRP = P / RP;
+  const int bh = blockIdx.x / NRP, rp = blockIdx.x % NRP;
+  const int bb = bh / dm.H, h = bh % dm.H;
+  const int r = threadIdx.x / TPR, c4 = threadIdx.x % TPR;
+  const int p = rp * RP + r, s0 = 4 * c4;
+  const int NT = dm.NT;
+  auto rowi = [&](int n) { return (((size_t)bb * NT + n) * dm.H + h) * P + p; };
+
+  float4 st = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (init) st = *reinterpret_cast<const float4*>(init + ((size_t)bh * P + p) * N + s0);
+
+  constexpr int D = 4;  // chunks in flight
+  float4 src[D];
+  float cl[D];
+  uint2 sp[D];
+  auto load = [&](int k, int it) {
+    const int n = BWD ? NT - 1 - it : it;
+    const size_t ri = rowi(n);
+    src[k] = *reinterpret_cast<const float4*>(ck.src + ri * N + s0);
+    cl[k] = ck.cl[ri];
+    if (BWD) sp[k] = *reinterpret_cast<const uint2*>(ck.state_pre + ri * N + s0);
+  };
+#pragma unroll
+  for (int k = 0; k < D; ++k)
+    if (k < NT) load(k, k);
+  for (int it0 = 0; it0 < NT; it0 += D) {
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      const int it = it0 + k;
+      if (it < NT) {
+        const int n = BWD ? NT - 1 - it : it;
+        const size_t ri = rowi(n);
+        const float c = cl[k];
+        const float dce = __expf(fminf(fmaxf(c, -kClipDecay), 0.f));
+        f32x4 sv = {st.x, st.y, st.z, st.w};
+        store4((BWD ? dstate : ck.state_pre) + ri * N + s0, sv);
+        if (BWD) {
+          const bf16* spv = reinterpret_cast<const bf16*>(&sp[k]);
+          float part = st.x * (float)spv[0] + st.y * (float)spv[1] + st.z * (float)spv[2] +
+                       st.w * (float)spv[3];
+#pragma unroll
+          for (int o = 1; o < TPR; o <<= 1) part += __shfl_xor(part, o);
+          const float msk = (c >= -kClipDecay && c <= 0.f) ? 1.f : 0.f;
+          if (c4 == 0) lasta[ri] = part * dce * msk;
+        }
+        st.x = sanitize(st.x * dce + src[k].x);
+        st.y = sanitize(st.y * dce + src[k].y);
+        st.z = sanitize(st.z * dce + src[k].z);
+        st.w = sanitize(st.w * dce + src[k].w);
+        if (it + D < NT) load(k, it + D);
+      }
+    }
+  }
+  if (fin) {
+    if (BWD) {  // :264 and the final clip
+      st.x = sanitize(st.x); st.y = sanitize(st.y); st.z = sanitize(st.z); st.w = sanitize(st.w);
+    }
+    *reinterpret_cast<float4*>(fin + ((size_t)bh * P + p) * N + s0) = st;
+  }
+}
+
+// ------------------------------------------------------------------ outputs
+template <typename T, int C, int N, int PT>
+struct YLds {
+  static constexpr int PAD = Pad<T>::v;
+  static constexpr int LPT = PT + PAD, LN = N + PAD, LD = 16 + PAD;
+  static constexpr int NSEG = 256 / PT;
+  static constexpr int off_cum = 0;
+  static constexpr int off_dbx = off_cum + C * PT * 4;
+  static constexpr int off_v = off_dbx + C * PT * 4;
+  static constexpr int off_st = off_v + C * LPT * (int)sizeof(T);
+  static constexpr int off_cbd = off_st + PT * LN * (int)sizeof(T);
+  static constexpr int off_tot = off_cbd + C * LD * (int)sizeof(T);
+  static constexpr int total = off_tot + NSEG * PT * 4;
+};
+
+// Output block of wave w's b-th assignment: blocks {w, NB-1-w} balance the
+// number of off-diagonal source blocks over the four waves.
+template <int NB>
+__device__ __forceinline__ int y_block(int w, int b) {
+  return b == 0 ? w : NB - 1 - w;
 }
 
 template <typename T, int C, int P, int N, int PT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void mamba2_scan(
-    Mamba2Dims dm, const T* __restrict__ dt, const T* __restrict__ x, const float* __restrict__ A,
-    const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ state0,
-    Mamba2Chunks<T> ck, float* __restrict__ y, float* __restrict__ state_final, int save) {
-  typedef ScanLds<T, C, N, PT> L;
+__global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __restrict__ dt,
+                                                     const T* __restrict__ x, const float* __restrict__ A,
+                                                     const T* __restrict__ Cm, Mamba2Chunks<T> ck,
+                                                     float* __restrict__ y) {
+  typedef YLds<T, C, N, PT> L;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
-  T* sB = reinterpret_cast<T*>(lds + L::off_b);
-  T* sCB = reinterpret_cast<T*>(lds + L::off_cb);
-  T* sZ = reinterpret_cast<T*>(lds + L::off_z);
-  T* sW = reinterpret_cast<T*>(lds + L::off_w);
-  T* sSt = reinterpret_cast<T*>(lds + L::off_st);
   float* sCum = reinterpret_cast<float*>(lds + L::off_cum);
   float* sDbx = reinterpret_cast<float*>(lds + L::off_dbx);
+  T* sV = reinterpret_cast<T*>(lds + L::off_v);
+  T* sSt = reinterpret_cast<T*>(lds + L::off_st);
+  T* sCbd = reinterpret_cast<T*>(lds + L::off_cbd);
   float* sTot = reinterpret_cast<float*>(lds + L::off_tot);
 
   constexpr int NPT = P / PT;
-  const int x_id = blockIdx.x;
-  const int pt = x_id % NPT;
-  const int bh = x_id / NPT;
-  const int h = bh % dm.H, bb = bh / dm.H;
-  const int p0 = pt * PT;
-  const int wv_id = wave_id();
+  int bn, m;
+  xcd_group_map(blockIdx.x, dm.B * dm.NT, dm.H * NPT, bn, m);
+  const int h = m / NPT, p0 = (m % NPT) * PT;
+  const int bb = bn / dm.NT, n = bn % dm.NT;
+  const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
+  const size_t rsx = (size_t)dm.H * P;
+  const size_t base = (row0 * dm.H + h) * P + p0;
   const float Ah = A[h];
-  const size_t rsx = (size_t)dm.H * P;  // row stride of dt / x / y
+  const T* cbg = ck.cb + (size_t)bn * C * C;
+  const T* cg = Cm + row0 * N;
+  const int wv_id = wave_id();
 
-  // state tiles [PT][N]: (PT/16) x (N/16)
-  constexpr int SNI = N / 16;
-  constexpr int NTS = (PT / 16) * SNI;
-  constexpr int SPW = NTS / 4;
-  // y tiles [C][PT]: (C/16) x (PT/16)
-  constexpr int YNI = PT / 16;
-  constexpr int NTY = (C / 16) * YNI;
-  constexpr int YPW = NTY / 4;
-  static_assert(NTS % 4 == 0 && NTY % 4 == 0, "tiles must split evenly over 4 waves");
-  constexpr int KN = N / Mma<T>::KS;
-
-  f32x4 st[SPW];
+  constexpr int PER_ROW = PT / 8, NE = C * PER_ROW, EPT = NE / 256;
+  static_assert(NE % 256 == 0, "slice must split evenly over the workgroup");
+  Raw8<T> rdt[EPT], rx[EPT];
 #pragma unroll
-  for (int t = 0; t < SPW; ++t) {
-    const int tile = wv_id * SPW + t, mi = tile / SNI, ni = tile % SNI;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = 16 * mi + tile_row(i), s = 16 * ni + tile_col();
-      st[t][i] = state0 ? state0[((size_t)bh * P + p0 + p) * N + s] : 0.f;
-    }
-    store_tile_t(sSt, L::LPT, 16 * mi, 16 * ni, st[t]);
+  for (int i = 0; i < EPT; ++i) {
+    const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
+    rdt[i].load(dt + base + r * rsx + c);
+    rx[i].load(x + base + r * rsx + c);
   }
-
-  // prefetch: B, CB to registers; dt / x tile; the C fragments of this wave's y tiles
-  RegStage<T, C, N> pB;
-  RegStage<T, C, C> pCB;
-  RegStage<T, C, PT> pdt, px;
-  typename Mma<T>::frag fC[YPW][KN], fCn[YPW][KN];  // this chunk's / the next chunk's
-  auto prefetch = [&](int n) {
-    const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
-    pB.load(Bm + row0 * N, N);
-    pCB.load(ck.cb + ((size_t)bb * dm.NT + n) * C * C, C);
-    pdt.load(dt + (row0 * dm.H + h) * P + p0, rsx);
-    px.load(x + (row0 * dm.H + h) * P + p0, rsx);
-    const T* cg = Cm + row0 * N;
+  stage_rows<T, PT, N>(sSt, L::LN, ck.state_pre + (((size_t)bn * dm.H + h) * P + p0) * N, N);
+  // diagonal 16x16 blocks of CB: row i, columns 16 (i / 16) .. + 15
+  for (int e = threadIdx.x; e < 2 * C; e += 256) {
+    const int i = e >> 1, half = e & 1;
+    *reinterpret_cast<uint4*>(sCbd + i * L::LD + 8 * half) =
+        *reinterpret_cast<const uint4*>(cbg + (size_t)i * C + 16 * (i >> 4) + 8 * half);
+  }
+  int pos = 0;
 #pragma unroll
-    for (int t = 0; t < YPW; ++t) {
-      const int mi = (wv_id * YPW + t) / YNI;
+  for (int i = 0; i < EPT; ++i) {
+    const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
 #pragma unroll
-      for (int kk = 0; kk < KN; ++kk) fCn[t][kk] = Mma<T>::ld_c(cg, N, 16 * mi, kk * Mma<T>::KS);
+    for (int j = 0; j < 8; ++j) {
+      const float a = rdt[i][j] * Ah;
+      pos |= a > 0.f;
+      sCum[r * PT + c + j] = sanitize(a, kClipDecay);
+      sDbx[r * PT + c + j] = sanitize(rdt[i][j] * rx[i][j]);
     }
-  };
-  auto rotate = [&]() {
-#pragma unroll
-    for (int t = 0; t < YPW; ++t)
-#pragma unroll
-      for (int kk = 0; kk < KN; ++kk) fC[t][kk] = fCn[t][kk];
-  };
-  // raw dt / x -> sCum = sanitize(dt A, 20), sDbx = sanitize(dt x)
-  auto commit = [&]() {
-    pB.store(sB, L::LN);
-    pCB.store(sCB, L::LCB);
-    constexpr int VEC = 16 / (int)sizeof(T), PER_ROW = PT / VEC;
-#pragma unroll
-    for (int i = 0; i < RegStage<T, C, PT>::PT; ++i) {
-      const int e = threadIdx.x + 256 * i;
-      if (e < C * PER_ROW) {
-        const int r = e / PER_ROW, c = (e % PER_ROW) * VEC;
-        const T* dv = reinterpret_cast<const T*>(&pdt.r[i]);
-        const T* xv = reinterpret_cast<const T*>(&px.r[i]);
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) {
-          const float d = to_f(dv[j]);
-          sCum[r * PT + c + j] = sanitize(d * Ah, kClipDecay);
-          sDbx[r * PT + c + j] = sanitize(d * to_f(xv[j]));
-        }
-      }
-    }
-  };
-  prefetch(0);
-  commit();
-  rotate();
+  }
+  // a slice with a positive step exponent breaks the monotone decay the
+  // factorisation relies on
+  const bool exact = __syncthreads_or(pos);
+  column_cumsum<C, PT>(sCum, sTot);
   __syncthreads();
-
-  for (int n = 0; n < dm.NT; ++n) {
-    const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
-    // a chunk with a positive step exponent breaks the monotone decay the
-    // factorisation relies on
-    int pos = 0;
-    for (int e = threadIdx.x; e < C * PT; e += 256) pos |= sCum[e] > 0.f;
-    const bool exact = __syncthreads_or(pos);
-    column_cumsum<C, PT>(sCum, sTot);
-    if (n + 1 < dm.NT) prefetch(n + 1);
-    if (save) {
-      T* sp = ck.state_pre + (((size_t)bh * dm.NT + n) * P + p0) * N;
-#pragma unroll
-      for (int t = 0; t < SPW; ++t) {
-        const int tile = wv_id * SPW + t, mi = tile / SNI, ni = tile % SNI;
-        store_tile_n(sp, N, 16 * mi, 16 * ni, st[t]);
-      }
-    }
-    __syncthreads();
-
-    // Z^(I)[j][p] = exp(cum_{16I} - cum_j) dBx_j  (j < 16 I; zero padding rows)
-    if (!exact) {
-#pragma unroll
-      for (int I = 1; I < L::NB; ++I) {
-        T* z = sZ + zrows_before<T>(I) * L::LPT;
-        for (int e = threadIdx.x; e < zrows<T>(I) * PT; e += 256) {
-          const int j = e / PT, p = e % PT;
-          float val = 0.f;
-          if (j < 16 * I) val = __expf(sCum[16 * I * PT + p] - sCum[j * PT + p]) * sDbx[j * PT + p];
-          z[j * L::LPT + p] = from_f<T>(val);
-        }
-      }
-    }
-    // write = dBx * sanitize(exp(clip(cum_last - cum, +-20)), 1e6)   (:133-135)
+  if (!exact) {
     for (int e = threadIdx.x; e < C * PT; e += 256) {
       const int j = e / PT, p = e % PT;
-      const float dte = sanitize(__expf(fminf(fmaxf(sCum[(C - 1) * PT + p] - sCum[j * PT + p],
-                                                    -kClipDecay), kClipDecay)), 1e6f);
-      sW[j * L::LPT + p] = from_f<T>(sDbx[j * PT + p] * dte);
+      sV[j * L::LPT + p] = from_f<T>(__expf(sCum[(j | 15) * PT + p] - sCum[j * PT + p]) * sDbx[j * PT + p]);
     }
-    __syncthreads();
-
-    // y = sanitize(y_diag + y_off)
-    float* yg = y ? y + (row0 * dm.H + h) * P + p0 : nullptr;
-#pragma unroll
-    for (int t = 0; t < YPW; ++t) {
-      const int tile = wv_id * YPW + t, mi = tile / YNI, ni = tile % YNI;
-      f32x4 yo = zero4();
-#pragma unroll
-      for (int kk = 0; kk < KN; ++kk)
-        yo = Mma<T>::mma(fC[t][kk], Mma<T>::ld_t(sSt, L::LPT, 16 * ni, kk * Mma<T>::KS), yo);
-      f32x4 yd = zero4();
-      if (!exact && mi > 0)
-        yd = tile_mma<T, false, true>(yd, sCB, L::LCB, sZ + zrows_before<T>(mi) * L::LPT, L::LPT,
-                                      16 * mi, 16 * ni, zrows<T>(mi));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 16 * mi + tile_row(i), p = 16 * ni + tile_col();
-        const float ci = sCum[r * PT + p];
-        const int j0 = exact ? 0 : 16 * mi;
-        float diag = 0.f;
-        for (int j = j0; j <= r; ++j) {
-          const float dd = fminf(fmaxf(ci - sCum[j * PT + p], -kClipDecay), kClipDecay);
-          diag += __expf(dd) * to_f(sCB[r * L::LCB + j]) * sDbx[j * PT + p];
-        }
-        const float off = (!exact && mi > 0) ? yd[i] * __expf(ci - sCum[16 * mi * PT + p]) : 0.f;
-        const float ydiag = sanitize(off + diag);
-        const float yoff = sanitize(yo[i] * __expf(fminf(fmaxf(ci, -kClipDecay), 0.f)));
-        if (y) yg[(size_t)r * rsx + p] = sanitize(ydiag + yoff);
-      }
-    }
-    if (n + 1 < dm.NT) rotate();
-
-    // state = sanitize(state exp(clip(cum_last, -20, 0)) + sanitize(B^T write))
-#pragma unroll
-    for (int t = 0; t < SPW; ++t) {
-      const int tile = wv_id * SPW + t, mi = tile / SNI, ni = tile % SNI;
-      f32x4 se = tile_mma<T, true, true>(zero4(), sW, L::LPT, sB, L::LN, 16 * mi, 16 * ni, C);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int p = 16 * mi + tile_row(i);
-        const float dce = __expf(fminf(fmaxf(sCum[(C - 1) * PT + p], -kClipDecay), 0.f));
-        st[t][i] = sanitize(st[t][i] * dce + sanitize(se[i]));
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int t = 0; t < SPW; ++t) {
-      const int tile = wv_id * SPW + t, mi = tile / SNI, ni = tile % SNI;
-      store_tile_t(sSt, L::LPT, 16 * mi, 16 * ni, st[t]);
-    }
-    if (n + 1 < dm.NT) commit();
-    __syncthreads();
   }
-  if (state_final) {
+  __syncthreads();
+
+  constexpr int NB = C / 16, BPW = NB / 4, YNI = PT / 16, KN = N / Mma<T>::KS;
+  static_assert(NB % 4 == 0, "row blocks must split evenly over 4 waves");
 #pragma unroll
-    for (int t = 0; t < SPW; ++t) {
-      const int tile = wv_id * SPW + t, mi = tile / SNI, ni = tile % SNI;
+  for (int bi = 0; bi < BPW; ++bi) {
+    const int I = y_block<NB>(wv_id, bi);
+    f32x4 off[YNI], yo[YNI];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int p = 16 * mi + tile_row(i), s = 16 * ni + tile_col();
-        state_final[((size_t)bh * P + p0 + p) * N + s] = st[t][i];
+    for (int ni = 0; ni < YNI; ++ni) { off[ni] = zero4(); yo[ni] = zero4(); }
+    if (!exact) {
+      for (int J = 0; J < I; ++J) {
+        // A = CB[16I.., 16J..16J+15]; k = 16..31 (the lanes of groups 2, 3) zeroed
+        typename Mma<T>::frag a = Mma<T>::ld_c(cbg, C, 16 * I, 16 * J);
+        if (lane_id() >= 32) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) a[k] = (T)0.f;
+        }
+#pragma unroll
+        for (int ni = 0; ni < YNI; ++ni) {
+          const f32x4 q = Mma<T>::mma(a, Mma<T>::ld_t(sV, L::LPT, 16 * ni, 16 * J), zero4());
+          const int pc = 16 * ni + tile_col();
+          const float mf = __expf(sCum[16 * I * PT + pc] - sCum[(16 * J + 15) * PT + pc]);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) off[ni][k] += mf * q[k];
+        }
+      }
+    }
+#pragma unroll
+    for (int kk = 0; kk < KN; ++kk) {
+      const typename Mma<T>::frag a = Mma<T>::ld_c(cg, N, 16 * I, kk * Mma<T>::KS);
+#pragma unroll
+      for (int ni = 0; ni < YNI; ++ni)
+        yo[ni] = Mma<T>::mma(a, Mma<T>::ld_c(sSt, L::LN, 16 * ni, kk * Mma<T>::KS), yo[ni]);
+    }
+#pragma unroll
+    for (int ni = 0; ni < YNI; ++ni) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = 16 * I + tile_row(k), p = 16 * ni + tile_col();
+        const float ci = sCum[i * PT + p];
+        const float offv = exact ? 0.f : off[ni][k] * __expf(ci - sCum[16 * I * PT + p]);
+        float diag = 0.f;
+        const int j0 = exact ? 0 : 16 * I;
+        for (int j = j0; j <= i; ++j) {
+          const float cbv = j >= 16 * I ? to_f(sCbd[i * L::LD + j - 16 * I]) : to_f(cbg[(size_t)i * C + j]);
+          const float dd = fminf(fmaxf(ci - sCum[j * PT + p], -kClipDecay), kClipDecay);
+          diag += fminf(__expf(dd), 1e6f) * cbv * sDbx[j * PT + p];
+        }
+        const float ydiag = sanitize(offv + diag);
+        const float yoff = sanitize(yo[ni][k] * __expf(fminf(fmaxf(ci, -kClipDecay), 0.f)));
+        y[base + (size_t)i * rsx + p] = sanitize(ydiag + yoff);
       }
     }
   }

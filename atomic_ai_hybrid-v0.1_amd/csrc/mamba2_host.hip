@@ -10,9 +10,9 @@ static size_t m2_align(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct Mamba2Plan {
   Mamba2Dims dm;
-  size_t o_cb, o_state, fwd_end;
-  size_t o_dstate, o_lasta, o_part, o_dap, total;
-  int G;  // head groups of the cross-head reduction
+  size_t o_cb, o_state, o_cl, o_src, fwd_end;
+  size_t o_dstate, o_lasta, o_ydh, o_wr, o_part, o_dap, total;
+  int G;  // head groups of the cross-head dCB reduction
 };
 
 static int mamba2_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
@@ -28,18 +28,23 @@ static int mamba2_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
   d.B = a->batch; d.T = a->seqlen; d.H = a->heads; d.P = a->headdim; d.N = a->dstate;
   d.C = a->chunk; d.NT = a->seqlen / a->chunk;
   p->dm = d;
-  const size_t es = 2, B = d.B, H = d.H, NT = d.NT, C = d.C, P = d.P, N = d.N;
+  const size_t es = 2, B = d.B, H = d.H, NT = d.NT, C = d.C, P = d.P, N = d.N, T = d.T;
+  // enough (batch, chunk, head group) workgroups to fill the chip
   int G = 1;
-  while ((size_t)G * B * NT < 256 && (size_t)(2 * G) <= H && H % (size_t)(2 * G) == 0) G *= 2;
+  while ((size_t)G * B * NT < 1024 && (size_t)(2 * G) <= H && H % (size_t)(2 * G) == 0) G *= 2;
   p->G = G;
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += m2_align(bytes); return o; };
   p->o_cb = take(B * NT * C * C * es);
-  p->o_state = take(B * H * NT * P * N * es);
+  p->o_state = take(B * NT * H * P * N * es);        // state entering each chunk
+  p->o_cl = take(B * NT * H * P * 4);                // cum at each chunk's last row
+  p->o_src = take(B * NT * H * P * N * 4);           // state_end; then the backward's dstate source
   p->fwd_end = off;
-  p->o_dstate = take(B * H * NT * P * N * es);       // dstate entering each chunk (reverse)
-  p->o_lasta = take(B * H * NT * P * 4);             // d cum_last from decay_chunk_end
-  p->o_part = take(B * NT * (size_t)p->G * (C * C + 2 * C * N) * 4);  // cross-head partials
+  p->o_dstate = take(B * NT * H * P * N * es);       // dstate entering each chunk's backward
+  p->o_lasta = take(B * NT * H * P * 4);             // d cum_last from decay_chunk_end
+  p->o_ydh = take(B * T * H * P * es);               // dy decay_h
+  p->o_wr = take(B * T * H * P * es);                // sanitize(dBx decay_to_end)
+  p->o_part = take(B * NT * (size_t)p->G * C * C * 4);  // dCB per head group
   p->o_dap = take(B * NT * H * 4);                   // per-chunk dA
   p->total = off;
   return ATOMIC_OK;
@@ -51,27 +56,9 @@ static Mamba2Chunks<T> mamba2_chunks(const Mamba2Plan& p, void* ws) {
   Mamba2Chunks<T> c;
   c.cb = reinterpret_cast<T*>(base + p.o_cb);
   c.state_pre = reinterpret_cast<T*>(base + p.o_state);
+  c.cl = reinterpret_cast<float*>(base + p.o_cl);
+  c.src = reinterpret_cast<float*>(base + p.o_src);
   return c;
-}
-
-template <int C, int P, int N>
-static int mamba2_forward_impl(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm,
-                               const void* Cm, const float* A, const float* state0, float* y,
-                               float* state_final, void* ws, int save, Launch& L) {
-  typedef bf16 T;
-  constexpr int PT = 16;
-  Mamba2Chunks<T> ck = mamba2_chunks<T>(p, ws);
-  hipStream_t st = L.st;
-  int rc = L("mamba2_cb", [&] {
-    hipLaunchKernelGGL((mamba2_cb<T, C, N>), dim3((unsigned)(p.dm.B * p.dm.NT)), dim3(256), 0, st,
-                       p.dm, (const T*)Bm, (const T*)Cm, ck);
-  });
-  if (rc) return rc;
-  return L("mamba2_scan", [&] {
-    hipLaunchKernelGGL((mamba2_scan<T, C, P, N, PT>), dim3((unsigned)(p.dm.B * p.dm.H * (P / PT))),
-                       dim3(256), 0, st, p.dm, (const T*)dt, (const T*)x, A, (const T*)Bm,
-                       (const T*)Cm, state0, ck, y, state_final, save);
-  });
 }
 
 template <typename T>
@@ -80,9 +67,53 @@ static Mamba2Grads<T> mamba2_grads(const Mamba2Plan& p, void* ws) {
   Mamba2Grads<T> g;
   g.dstate = reinterpret_cast<T*>(base + p.o_dstate);
   g.lasta = reinterpret_cast<float*>(base + p.o_lasta);
+  g.ydh = reinterpret_cast<T*>(base + p.o_ydh);
+  g.wr = reinterpret_cast<T*>(base + p.o_wr);
   g.part = reinterpret_cast<float*>(base + p.o_part);
   g.dap = reinterpret_cast<float*>(base + p.o_dap);
   return g;
+}
+
+// channels per workgroup of the chunk-parallel kernels
+constexpr int kOuterPT = 64, kYPT = 32;
+
+template <int P, int N>
+static unsigned pass_grid(const Mamba2Dims& d) {
+  constexpr int RP = 256 / (N / 4);
+  return (unsigned)(d.B * d.H * (P / RP));
+}
+
+// Forward: CB, per-chunk state_end, the state pass and (when y is wanted) the
+// outputs.  The state entering every chunk always lands in the workspace.
+template <int C, int P, int N>
+static int mamba2_forward_impl(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm,
+                               const void* Cm, const float* A, const float* state0, float* y,
+                               float* state_final, void* ws, Launch& L) {
+  typedef bf16 T;
+  const Mamba2Dims& d = p.dm;
+  Mamba2Chunks<T> ck = mamba2_chunks<T>(p, ws);
+  hipStream_t st = L.st;
+  int rc = L("mamba2_cb", [&] {
+    hipLaunchKernelGGL((mamba2_cb<T, C, N>), dim3((unsigned)(d.B * d.NT)), dim3(256), 0, st, d,
+                       (const T*)Bm, (const T*)Cm, ck);
+  });
+  if (rc) return rc;
+  rc = L("mamba2_chunk_state", [&] {
+    hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false>),
+                       dim3((unsigned)(d.B * d.NT * d.H * (P / kOuterPT))), dim3(256), 0, st, d,
+                       (const T*)dt, (const T*)x, A, (const T*)Bm, (const T*)nullptr, ck, (T*)nullptr,
+                       (T*)nullptr);
+  });
+  if (rc) return rc;
+  rc = L("mamba2_state_pass", [&] {
+    hipLaunchKernelGGL((mamba2_state_pass<T, P, N, false>), dim3(pass_grid<P, N>(d)), dim3(256), 0, st,
+                       d, ck, (T*)nullptr, (float*)nullptr, state0, state_final);
+  });
+  if (rc || !y) return rc;
+  return L("mamba2_chunk_y", [&] {
+    hipLaunchKernelGGL((mamba2_chunk_y<T, C, P, N, kYPT>), dim3((unsigned)(d.B * d.NT * d.H * (P / kYPT))),
+                       dim3(256), 0, st, d, (const T*)dt, (const T*)x, A, (const T*)Cm, ck, y);
+  });
 }
 
 template <int C, int P, int N, typename TD>
@@ -107,8 +138,8 @@ static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x,
 
 int mamba2_forward(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm, const void* Cm,
                    const float* A, const float* state0, float* y, float* state_final, void* ws,
-                   int save, Launch& L) {
-  AH_M2_DISPATCH(mamba2_forward_impl, p, dt, x, Bm, Cm, A, state0, y, state_final, ws, save, L);
+                   Launch& L) {
+  AH_M2_DISPATCH(mamba2_forward_impl, p, dt, x, Bm, Cm, A, state0, y, state_final, ws, L);
 }
 
 template <int C, int P, int N, typename TD>
@@ -117,36 +148,41 @@ static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x,
                              const float* dstate_final, void* ddt, void* dx, void* dB, void* dC,
                              float* dA, float* dstate0, void* ws, bool reuse, Launch& L) {
   typedef bf16 T;
+  const Mamba2Dims& d = p.dm;
   int rc;
   if (!reuse) {
     // recompute the forward's per-chunk states (the reference re-runs the
     // forward scan, mamba2_bwd_reference.py:229-234)
-    rc = mamba2_forward_impl<C, P, N>(p, dt, x, Bm, Cm, A, state0, nullptr, nullptr, ws, 1, L);
+    rc = mamba2_forward_impl<C, P, N>(p, dt, x, Bm, Cm, A, state0, nullptr, nullptr, ws, L);
     if (rc) return rc;
   }
   Mamba2Chunks<T> ck = mamba2_chunks<T>(p, ws);
   Mamba2Grads<T> gr = mamba2_grads<T>(p, ws);
-  constexpr int PT = 16;
   hipStream_t st = L.st;
-  rc = L("mamba2_bwd_dstate", [&] {
-    hipLaunchKernelGGL((mamba2_bwd_dstate<T, TD, C, P, N, PT>), dim3((unsigned)(p.dm.B * p.dm.H * (P / PT))),
-                       dim3(256), 0, st, p.dm, (const T*)dt, A, (const T*)Cm, (const TD*)dy, dstate_final,
-                       ck, gr, dstate0);
+  rc = L("mamba2_bwd_source", [&] {
+    hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true>),
+                       dim3((unsigned)(d.B * d.NT * d.H * (P / kOuterPT))), dim3(256), 0, st, d,
+                       (const T*)dt, (const T*)x, A, (const T*)Cm, (const TD*)dy, ck, gr.ydh, gr.wr);
+  });
+  if (rc) return rc;
+  rc = L("mamba2_bwd_state_pass", [&] {
+    hipLaunchKernelGGL((mamba2_state_pass<T, P, N, true>), dim3(pass_grid<P, N>(d)), dim3(256), 0, st,
+                       d, ck, gr.dstate, gr.lasta, dstate_final, dstate0);
   });
   if (rc) return rc;
   rc = L("mamba2_bwd_chunk", [&] {
-    hipLaunchKernelGGL((mamba2_bwd_chunk<T, TD, C, P, N>), dim3((unsigned)(p.dm.B * p.dm.NT * p.G)),
-                       dim3(256), 0, st, p.dm, p.G, (const T*)dt, (const T*)x, A, (const T*)Bm,
+    hipLaunchKernelGGL((mamba2_bwd_chunk<T, TD, C, P, N>), dim3((unsigned)(d.B * d.NT * p.G)),
+                       dim3(256), 0, st, d, p.G, (const T*)dt, (const T*)x, A, (const T*)Bm,
                        (const T*)Cm, (const TD*)dy, ck, gr, (T*)ddt, (T*)dx);
   });
   if (rc) return rc;
   rc = L("mamba2_bwd_bc", [&] {
-    hipLaunchKernelGGL((mamba2_bwd_bc<T, C, N>), dim3((unsigned)(p.dm.B * p.dm.NT)), dim3(256), 0, st,
-                       p.dm, p.G, (const T*)Bm, (const T*)Cm, gr, (T*)dB, (T*)dC);
+    hipLaunchKernelGGL((mamba2_bwd_bc<T, C, P, N>), dim3((unsigned)(d.B * d.NT * (N / 32))), dim3(256),
+                       0, st, d, p.G, (const T*)Bm, (const T*)Cm, ck, gr, (T*)dB, (T*)dC);
   });
   if (rc) return rc;
   return L("mamba2_bwd_da", [&] {
-    hipLaunchKernelGGL(mamba2_bwd_da, dim3(1), dim3(256), 0, st, p.dm, (const float*)gr.dap, dA);
+    hipLaunchKernelGGL(mamba2_bwd_da, dim3(1), dim3(256), 0, st, d, (const float*)gr.dap, dA);
   });
 }
 
@@ -191,8 +227,7 @@ extern "C" int atomic_mamba2_fwd(const atomic_mamba2_args* a, const void* dt, co
   if (!dt || !x || !B || !C || !A || !y || !state_final) return ATOMIC_ERR_NULL;
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
   Launch L{a->profile, (hipStream_t)stream};
-  return mamba2_forward(p, dt, x, B, C, A, state0, y, state_final, workspace,
-                        (a->flags & ATOMIC_MAMBA2_SAVE) ? 1 : 0, L);
+  return mamba2_forward(p, dt, x, B, C, A, state0, y, state_final, workspace, L);
 }
 
 extern "C" int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, const void* x,

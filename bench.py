@@ -72,32 +72,42 @@ def gdn2_kernel_model(B, T, H, K, V, C, es=2, save=True):
 def mamba2_groups(B, T, H, C):
     NT = T // C
     G = 1
-    while G * B * NT < 256 and 2 * G <= H and H % (2 * G) == 0:
+    while G * B * NT < 1024 and 2 * G <= H and H % (2 * G) == 0:
         G *= 2
     return G
 
 
-def mamba2_kernel_model(B, T, H, P, N, C, es=2, save=True):
+def mamba2_kernel_model(B, T, H, P, N, C, es=2):
     """Algorithmic (flops, HBM bytes) per launch of each Mamba2 kernel.  Uh
-    counts (batch, head, chunk) units, Ub (batch, chunk) units (B, C and the
-    C·Bᵀ scores are shared by every head); y is float32."""
+    counts (batch, chunk, head) units, Ub (batch, chunk) units (B, C and the
+    C.B^T scores are shared by every head); y, state_end and the dstate
+    source are float32, the saved states bf16."""
     NT = T // C
     Uh, Ub = B * H * NT, B * NT
     G = mamba2_groups(B, T, H, C)
     CP, CN, CC, PN = C * P, C * N, C * C, P * N
-    part = G * (CC + 2 * CN) * 4
     return {
         "mamba2_cb": (Ub * 2 * CC * N, Ub * (2 * CN * es + CC * es)),
-        "mamba2_scan": (Uh * (2 * CC * P + 4 * C * PN),
-                        Uh * (2 * CP * es + CP * 4 + (PN * es if save else 0))
-                        + Ub * (2 * CN * es + CC * es)),
-        "mamba2_bwd_dstate": (Uh * 2 * C * PN,
-                              Uh * (2 * CP * es + 2 * PN * es + P * 4) + Ub * CN * es
-                              + B * H * PN * 4),
-        "mamba2_bwd_chunk": (Uh * (4 * CC * P + 6 * C * PN),
+        # state_end = B^T (dBx dte): dt, x in; state_end (f32) and cum_last out
+        "mamba2_chunk_state": (Uh * 2 * C * PN, Uh * (2 * CP * es + PN * 4 + P * 4) + Ub * CN * es),
+        # elementwise recurrence: state_end, cum_last in; state entering each chunk out
+        "mamba2_state_pass": (Uh * 2 * PN, Uh * (PN * 4 + P * 4 + PN * es) + 2 * B * H * PN * 4),
+        # y = y_diag + y_off: dt, x, state_prev in (C, CB shared); y (f32) out
+        "mamba2_chunk_y": (Uh * (CC * P + 2 * C * PN),
+                           Uh * (2 * CP * es + CP * 4 + PN * es) + Ub * (CN * es + CC * es)),
+        # (dy decay_h)^T C; dt, x, dy in; source (f32), Ydh, W out
+        "mamba2_bwd_source": (Uh * 2 * C * PN,
+                              Uh * (3 * CP * es + PN * 4 + 2 * CP * es) + Ub * CN * es),
+        "mamba2_bwd_state_pass": (Uh * 2 * PN,
+                                  Uh * (PN * 4 + P * 4 + 2 * PN * es + P * 4) + 2 * B * H * PN * 4),
+        # y_off / dwrite recompute, the pairwise-decay products and dCB; dt, x, dy,
+        # state_prev, dstate, last-row term in; ddt, dx, dCB partials out
+        "mamba2_bwd_chunk": (Uh * (4 * C * PN + 3 * CC * P),
                              Uh * (3 * CP * es + 2 * PN * es + P * 4 + 2 * CP * es + 4)
-                             + Ub * (2 * CN * es + CC * es + part)),
-        "mamba2_bwd_bc": (Ub * 4 * CC * N, Ub * (2 * CN * es + part + 2 * CN * es)),
+                             + Ub * (2 * CN * es + CC * es + G * CC * 4)),
+        # dC_1 + dB_1 over (head, channel), dCB B and dCB^T C
+        "mamba2_bwd_bc": (Uh * 4 * C * PN + Ub * 4 * CC * N,
+                          Uh * (2 * CP * es + 2 * PN * es) + Ub * (G * CC * 4 + 4 * CN * es)),
         "mamba2_bwd_da": (0.0, B * NT * H * 4 + H * 4),
     }
 

@@ -84,3 +84,27 @@ def test_trainable_wrapper_autograd():
     for leaf, ref in zip(leaves, direct[:5]):
         assert leaf.grad.dtype == leaf.dtype
         assert torch.equal(leaf.grad, ref) or rel_err(leaf.grad, ref) < 1e-6
+
+
+def test_backward_positive_step_exponent_takes_exact_path():
+    """dt A > 0 for one head: that head's slices are evaluated pairwise with
+    the reference's clip masks (no factorised decay).  The positive head's dA
+    is ill-conditioned (a sum of nearly cancelling pair terms): rounding only
+    the shared CB scores to bf16 moves the float64 oracle's value by 1.3 %,
+    so that one entry is held to 5 %; every other output meets the bf16
+    tolerance."""
+    banner("mamba2 bwd positive exponent")
+
+    def mutate(inp):
+        inp["A"][1] = 0.05
+    args, ref = _case(1, 256, 3, 64, 128, 128, seed=21, state=True, mutate=mutate)
+    out = _gpu(args, 128, reuse=False)
+    errs = {n: rel_err(g, w) for n, g, w in zip(NAMES, out, ref)}
+    print("  rel_err " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+    for name, e in errs.items():
+        if name != "dA":
+            assert e < tol_for(BF16), (name, e)
+    dA, dA_ref = out[4].cpu().double(), ref[4]
+    for h in (0, 2):
+        assert abs(dA[h] - dA_ref[h]) < tol_for(BF16) * dA_ref.abs().max(), h
+    assert abs(dA[1] - dA_ref[1]) < 0.05 * abs(dA_ref[1])

@@ -52,3 +52,29 @@ def test_positive_step_exponent_takes_exact_path():
     ey, es = rel_err(y, y_ref), rel_err(s, s_ref)
     print(f"  rel_err y={ey:.3e} state={es:.3e}")
     assert ey < tol_for(BF16) and es < tol_for(BF16)
+
+
+def test_decay_weight_cap():
+    """A positive step exponent (A = +1) drives exp(clip(cum_i - cum_j, +-20))
+    past the reference's 1e6 cap on L (mamba2_ssd_reference.py:120) for the
+    far pairs of a chunk.  One chunk, so y is y_diag alone, which the exact
+    path evaluates pairwise in fp32.  The capped terms reach ~1e4, where the
+    bf16 rounding of the shared CB scores would dominate a sum with
+    cancellation, so x, B and C are made non-negative: every term is then
+    positive and the comparison isolates the cap.  x is scaled by 1e-3 so
+    that y stays below the 1e4 output clip; there the uncapped weights would
+    change y by about 2x its maximum."""
+    banner("mamba2 fwd L cap")
+
+    def mutate(inp):
+        inp["A"][0] = 1.0
+        for n in ("x", "Bm", "Cm"):
+            inp[n] = inp[n].abs()
+        inp["x"] = (inp["x"].float() * 1e-3).to(inp["x"].dtype)
+    (y, s), (y_ref, s_ref) = _run(1, 128, 2, 64, 128, 128, seed=6, mutate=mutate)
+    dt = inputs.mamba2_inputs(1, 128, 2, 64, 128, seed=6)["dt"].double()
+    cum = torch.cumsum(dt[0, :, 0], 0)
+    assert (cum[-1] - cum[0]).max() > 13.9, "the cap must be reached"
+    ey = rel_err(y, y_ref)
+    print(f"  rel_err y={ey:.3e}")
+    assert ey < tol_for(BF16)
