@@ -34,40 +34,72 @@ struct Mamba2Grads {
 };
 
 // ------------------------------------------------------------------ per-chunk gradients
-// Rows of the block-I operand Z^(I) (source rows j < 16 I, padded to the MFMA k step).
-template <typename T>
-__host__ __device__ constexpr int zrows(int I) {
-  return ((16 * I + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
-}
-// Y^(I) rows start at the MFMA k step at or below 16 (I + 1).
-template <typename T>
-__host__ __device__ constexpr int ybase(int I) {
-  return (16 * (I + 1) / Mma<T>::KS) * Mma<T>::KS;
-}
+// The pair sums of the chunk, for channel p and rows i, j of the chunk:
+//   R_i   = sum_{j<=i} CB_ij exp(cum_i - cum_j) dBx_j     (row side; d_cum_i, :162)
+//   S_j   = sum_{i>=j} CB_ij exp(cum_i - cum_j) dy_i      (column side; d_dBx_2, :148; d_cum_j, :163)
+//   dCB_ij += sum_p dy_i exp(cum_i - cum_j) dBx_j         (cross-head, :152)
+// On 16-row blocks I (rows 16I..16I+15) the decay factorises into
+//   U_i = exp(cum_i - cum_{16I}),  M_IJ = exp(cum_{16I} - cum_{16J+15}),
+//   V_j = exp(cum_{16J+15} - cum_j),
+// all <= 1 when dt A <= 0, and inside a diagonal block into U_i and
+// exp(cum_{16I} - cum_j) <= exp(range_I), range_I = cum_{16I} - cum_{16I+15}.
+// Every pair is then an MFMA on Yu = dy U or Vd = V dBx with per-channel
+// scales; the two copies of each pair term in d_cum (row and column side)
+// use Yu / Vd split into bf16 high + low parts so the reverse cumsum's
+// cancellation survives.  Masks |cum_i - cum_j| <= 20 and the exp(-20) floor
+// change only pairs whose weight is below exp(-20) (a relative 2e-9).
+// A slice with a positive step exponent or a block range above kMaxRange is
+// evaluated pairwise with the reference's clips and masks instead.
+constexpr float kMaxRange = 60.f;
 
 template <typename T, int C, int N, int PT>
 struct CkLds {
   static constexpr int PAD = Pad<T>::v;
-  static constexpr int LCB = C + PAD, LN = N + PAD, LPT = PT + PAD;
+  static constexpr int LN = N + PAD, LPT = PT + PAD;
   static constexpr int LC = PT + 1;  // fp32 [C][PT] rows, padded against bank conflicts
   static constexpr int NSEG = 256 / PT;
   static constexpr int OPT = C * LPT * (int)sizeof(T);
-  static constexpr int off_cb = 0;
-  static constexpr int off_st = off_cb + C * LCB * (int)sizeof(T);
+  static constexpr int OPR = (C + 16) * LPT * (int)sizeof(T);  // MFMA operand + 16 zero rows
+  static constexpr int off_st = 0;
   static constexpr int off_dst = off_st + PT * LN * (int)sizeof(T);
   static constexpr int off_dy = off_dst + PT * LN * (int)sizeof(T);
-  static constexpr int off_zlo = off_dy + OPT;   // then fp32 ddt_1 (with off_ylo)
-  static constexpr int off_ylo = off_zlo + OPT;
-  static constexpr int off_ydec = off_ylo + OPT;  // then fp32 d_cum (with off_z, off_y)
-  static constexpr int off_z = off_ydec + OPT;
-  static constexpr int off_y = off_z + OPT;
-  static constexpr int off_cum = off_y + OPT;
-  static constexpr int off_dbx = off_cum + C * LC * 4;
-  static constexpr int off_tot = off_dbx + C * LC * 4;
+  static constexpr int off_dt = off_dy + OPT;
+  static constexpr int off_x = off_dt + OPT;
+  static constexpr int off_yu = off_x + OPT;  // Yu hi, Yu lo, Vd hi, Vd lo
+  static constexpr int off_yul = off_yu + OPR;
+  static constexpr int off_vd = off_yul + OPR;
+  static constexpr int off_vdl = off_vd + OPR;
+  static constexpr int off_cum = off_vdl + OPR;
+  static constexpr int off_red = off_cum + C * LC * 4;    // fp32 d_cum
+  static constexpr int off_ddt1 = off_red + C * LC * 4;   // fp32 ddt_1
+  static constexpr int off_tot = off_ddt1 + C * LC * 4;
   static constexpr int off_misc = off_tot + NSEG * PT * 4;   // lasta[PT], lastb[4][PT], dA[8]
   static constexpr int total = off_misc + (PT + 4 * PT + 8) * 4;
-  static_assert(2 * OPT >= C * LC * 4 && 3 * OPT >= C * LC * 4, "fp32 aliases must fit");
 };
+
+// A fragment of a 16x16 (k = 16) block of a row-major [C][C] matrix in global
+// memory: lanes of groups 0, 1 hold k = 0..15; groups 2, 3 hold zeros (and
+// read nothing).  mask: 0 none, 1 keep k <= m (lower), 2 keep k >= m (upper).
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::frag cb_frag(const T* g, int ld, int m0, int k0, int mask) {
+  typename Mma<T>::frag a;
+  const int l = lane_id();
+  if (l < 32) {
+    a = Mma<T>::ld_c(g, ld, m0, k0);
+    if (mask) {
+      const int m = l & 15, kb = 8 * (l >> 4);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bool keep = mask == 1 ? (kb + e <= m) : (kb + e >= m);
+        if (!keep) a[e] = (T)0.f;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[e] = (T)0.f;
+  }
+  return a;
+}
 
 template <typename T, typename TD, int C, int P, int N>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void mamba2_bwd_chunk(
@@ -77,32 +109,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     T* __restrict__ dx) {
   constexpr int PT = 32;
   typedef CkLds<T, C, N, PT> L;
+  typedef typename Mma<T>::frag frag;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
   // LDS views; rebuilt from an opaque base at every (head, slice) iteration so
   // the compiler cannot hoist the hundreds of per-lane addresses of the
   // unrolled loop bodies out of the iteration loop (that hoisting spilled them).
-  T *sCB, *sSt, *sDst, *sDy, *sYdec, *sZ, *sY, *sZlo, *sYlo;
-  float *sCum, *sDbx, *sTot, *sLastA, *sLastB, *sDa, *sDdt1, *sRed;
+  T *sSt, *sDst, *sDy, *sDt, *sX, *sYu, *sYul, *sVd, *sVdl;
+  float *sCum, *sTot, *sLastA, *sLastB, *sDa, *sRed, *sDdt1;
   auto views = [&](int z) {
     unsigned char* lb = lds + z;
-    sCB = reinterpret_cast<T*>(lb + L::off_cb);
     sSt = reinterpret_cast<T*>(lb + L::off_st);
     sDst = reinterpret_cast<T*>(lb + L::off_dst);
     sDy = reinterpret_cast<T*>(lb + L::off_dy);
-    sYdec = reinterpret_cast<T*>(lb + L::off_ydec);
-    sZ = reinterpret_cast<T*>(lb + L::off_z);
-    sY = reinterpret_cast<T*>(lb + L::off_y);
+    sDt = reinterpret_cast<T*>(lb + L::off_dt);
+    sX = reinterpret_cast<T*>(lb + L::off_x);
+    sYu = reinterpret_cast<T*>(lb + L::off_yu);
+    sYul = reinterpret_cast<T*>(lb + L::off_yul);
+    sVd = reinterpret_cast<T*>(lb + L::off_vd);
+    sVdl = reinterpret_cast<T*>(lb + L::off_vdl);
     sCum = reinterpret_cast<float*>(lb + L::off_cum);
-    sDbx = reinterpret_cast<float*>(lb + L::off_dbx);
     sTot = reinterpret_cast<float*>(lb + L::off_tot);
     sLastA = reinterpret_cast<float*>(lb + L::off_misc);
     sLastB = sLastA + PT;
     sDa = sLastB + 4 * PT;
-    // low halves of the split Z / Y operands
-    sZlo = reinterpret_cast<T*>(lb + L::off_zlo);
-    sYlo = reinterpret_cast<T*>(lb + L::off_ylo);
-    sDdt1 = reinterpret_cast<float*>(lb + L::off_zlo);  // aliases Zlo + Ylo in the epilogue
-    sRed = reinterpret_cast<float*>(lb + L::off_ydec);  // aliases Ydec + Z + Y in the epilogue
+    sRed = reinterpret_cast<float*>(lb + L::off_red);
+    sDdt1 = reinterpret_cast<float*>(lb + L::off_ddt1);
   };
   views(0);
 
@@ -113,14 +144,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int HG = dm.H / G;
   const int wv_id = wave_id();
   const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
-  const size_t rsx = (size_t)dm.H * P;
   const T* Bg0 = Bm + row0 * N;
   const T* Cg0 = Cm + row0 * N;
+  const T* cb0 = ck.cb + (size_t)bn * C * C;
+  const T* cbt0 = ck.cbt + (size_t)bn * C * C;
   constexpr int NB = C / 16;
+  static_assert(NB % 4 == 0, "row blocks must split evenly over 4 waves");
 
-  stage_rows<T, C, C>(sCB, L::LCB, ck.cb + (size_t)bn * C * C, C);
-
-  // cross-head accumulator: dCB lower tiles (I >= J)
+  // cross-head accumulator: dCB lower tiles (I >= J), tile k of wave w = w + 4 s
   constexpr int NBC = NB * (NB + 1) / 2;
   constexpr int BCPW = (NBC + 3) / 4;
   f32x4 acc_bc[BCPW];
@@ -132,10 +163,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     J = k;
   };
 
-  // y-shaped tiles [C][PT]: wave w owns row blocks 2w, 2w+1 (NB = 8) or w (NB = 4)
-  constexpr int BPW = NB / 4;          // row blocks per wave
-  constexpr int YNI = PT / 16;         // column tiles
-  static_assert(NB % 4 == 0, "row blocks must split evenly over 4 waves");
+  // y-shaped tiles [C][PT]: wave w owns row blocks {w, NB-1-w} (NB = 8) or w (NB = 4)
+  constexpr int BPW = NB / 4;
+  constexpr int YNI = PT / 16;
+  auto my_block = [&](int bi) { return bi == 0 ? wv_id : NB - 1 - wv_id; };
 
   for (int hh = 0; hh < HG; ++hh) {
     const int h = g * HG + hh;
@@ -146,23 +177,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       views(z);
       const T* Bg = Bg0 + z;
       const T* Cg = Cg0 + z;
+      const T* cbg = cb0 + z;
+      const T* cbtg = cbt0 + z;
       const size_t bnh = (size_t)bn * dm.H + h;
-      // ---- A: slice inputs
-      int pos = 0;
+      // ---- A: slice inputs (dt, x, dy kept exactly as bf16), a = sanitize(dt A, 20)
+      int flag = 0;
       {
-        constexpr int VEC = 8, PER_ROW = PT / VEC;
+        constexpr int PER_ROW = PT / 8;
         for (int e = tid; e < C * PER_ROW; e += 256) {
-          const int r = e / PER_ROW, c = (e % PER_ROW) * VEC;
+          const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
           const size_t o = ((row0 + r) * dm.H + h) * P + p0 + c;
-          float dv[8], xv[8], yv[8];
-          load8(dt + o, dv);
-          load8(x + o, xv);
-          load8(dy + o, yv);
+          Raw8<T> rdt, rx;
+          Raw8<TD> rdy;
+          rdt.load(dt + o);
+          rx.load(x + o);
+          rdy.load(dy + o);
+          *reinterpret_cast<uint4*>(sDt + r * L::LPT + c) = rdt.v;
+          *reinterpret_cast<uint4*>(sX + r * L::LPT + c) = rx.v;
+          float yv[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            pos |= dv[j] * Ah > 0.f;
-            sCum[r * L::LC + c + j] = sanitize(dv[j] * Ah, kClipDecay);
-            sDbx[r * L::LC + c + j] = sanitize(dv[j] * xv[j]);
+            const float a = rdt[j] * Ah;
+            flag |= a > 0.f;
+            sCum[r * L::LC + c + j] = sanitize(a, kClipDecay);
+            yv[j] = rdy[j];
           }
           store8(sDy + r * L::LPT + c, yv);
         }
@@ -170,104 +208,74 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       stage_rows<T, PT, N>(sSt, L::LN, ck.state_pre + (bnh * P + p0) * N, N);
       stage_rows<T, PT, N>(sDst, L::LN, gr.dstate + (bnh * P + p0) * N, N);
       if (tid < PT) sLastA[tid] = gr.lasta[bnh * P + p0 + tid];
-      // a slice with a positive step exponent is evaluated pairwise everywhere
-      const bool exact = __syncthreads_or(pos);
+      __syncthreads();
       column_cumsum<C, PT, L::LC>(sCum, sTot);
       __syncthreads();
-      // ---- B: dy exp(cum - cum_{block start})
-      for (int e = tid; e < C * PT; e += 256) {
-        const int r = e / PT, p = e % PT;
-        const float cum = sCum[r * L::LC + p];
-        const float dyv = to_f(sDy[r * L::LPT + p]);
-        sYdec[r * L::LPT + p] = from_f<T>(dyv * __expf(cum - sCum[(r & ~15) * L::LC + p]));
+      for (int e = tid; e < NB * PT; e += 256) {
+        const int I = e / PT, p = e % PT;
+        flag |= sCum[16 * I * L::LC + p] - sCum[(16 * I + 15) * L::LC + p] > kMaxRange;
       }
-      __syncthreads();
-      f32x4 ydo[BPW][YNI], dd2[BPW][YNI];
-#pragma unroll
-      for (int bi = 0; bi < BPW; ++bi)
-#pragma unroll
-        for (int ni = 0; ni < YNI; ++ni) {
-          ydo[bi][ni] = zero4();
-          dd2[bi][ni] = zero4();
-        }
-      // ---- D: off-diagonal blocks, one output block I at a time.
-      // d_cum receives every pairwise term dy_i W_ij dBx_j twice, with opposite
-      // signs at i and at j (:159-163), and the reverse cumsum cancels the
-      // pairs that do not straddle a row.  Both sides therefore use Z / Y
-      // split into bf16 high + low parts (about 16 mantissa bits), so the two
-      // copies of each term agree and the cancellation survives.
-      for (int I = 0; I < (exact ? 0 : NB); ++I) {
-        const int zr = zrows<T>(I), yb = ybase<T>(I);
-        for (int e = tid; e < zr * PT; e += 256) {
+      // positive step exponent or too steep a block: pairwise evaluation
+      const bool exact = __syncthreads_or(flag);
+
+      // ---- B: operands Yu = dy U, Vd = V dBx (bf16 high + low parts)
+      if (!exact) {
+        for (int e = tid; e < (C + 16) * PT; e += 256) {
           const int j = e / PT, p = e % PT;
-          float v = 0.f;
-          if (j < 16 * I) v = __expf(sCum[16 * I * L::LC + p] - sCum[j * L::LC + p]) * sDbx[j * L::LC + p];
-          const T hi = from_f<T>(v);
-          sZ[j * L::LPT + p] = hi;
-          sZlo[j * L::LPT + p] = from_f<T>(v - to_f(hi));
-        }
-        for (int e = tid; e < (C - yb) * PT; e += 256) {
-          const int i = yb + e / PT, p = e % PT;
-          float v = 0.f;
-          if (i >= 16 * (I + 1))
-            v = __expf(sCum[i * L::LC + p] - sCum[(16 * I + 15) * L::LC + p]) * to_f(sDy[i * L::LPT + p]);
-          const T hi = from_f<T>(v);
-          sY[(i - yb) * L::LPT + p] = hi;
-          sYlo[(i - yb) * L::LPT + p] = from_f<T>(v - to_f(hi));
+          float yu = 0.f, vd = 0.f;
+          if (j < C) {
+            const float cj = sCum[j * L::LC + p];
+            const float dbx = sanitize(to_f(sDt[j * L::LPT + p]) * to_f(sX[j * L::LPT + p]));
+            yu = to_f(sDy[j * L::LPT + p]) * __expf(cj - sCum[(j & ~15) * L::LC + p]);
+            vd = dbx * __expf(sCum[(j | 15) * L::LC + p] - cj);
+          }
+          const T yh = from_f<T>(yu), vh = from_f<T>(vd);
+          sYu[j * L::LPT + p] = yh;
+          sYul[j * L::LPT + p] = from_f<T>(yu - to_f(yh));
+          sVd[j * L::LPT + p] = vh;
+          sVdl[j * L::LPT + p] = from_f<T>(vd - to_f(vh));
         }
         __syncthreads();
-        if (I / BPW == wv_id) {
-          const int bi = I % BPW;
-#pragma unroll
-          for (int ni = 0; ni < YNI; ++ni) {
-            f32x4 r1 = zero4(), r2 = zero4();
-            if (I > 0) {
-              r1 = tile_mma<T, false, true>(r1, sCB, L::LCB, sZ, L::LPT, 16 * I, 16 * ni, zr);
-              r1 = tile_mma<T, false, true>(r1, sCB, L::LCB, sZlo, L::LPT, 16 * I, 16 * ni, zr);
-            }
-            if (yb < C) {
-              r2 = tile_mma<T, true, true>(r2, sCB + yb * L::LCB, L::LCB, sY, L::LPT, 16 * I, 16 * ni,
-                                           C - yb);
-              r2 = tile_mma<T, true, true>(r2, sCB + yb * L::LCB, L::LCB, sYlo, L::LPT, 16 * I,
-                                           16 * ni, C - yb);
-            }
-            // static register indices (a runtime index would put the arrays in scratch)
-#pragma unroll
-            for (int b2 = 0; b2 < BPW; ++b2)
-              if (b2 == bi) { ydo[b2][ni] = r1; dd2[b2][ni] = r2; }
-          }
-        }
-        // dCB tiles (I, J < I): sum_p Ydec_i Z_j
+      }
+
+      // ---- C: dCB tiles
+      if (!exact) {
+        // sum_p Yu_i M_IJ[p] Vd_j (M_II = exp(range_I)); the upper half of
+        // diagonal tiles is dropped when the partials are written
 #pragma unroll
         for (int s = 0; s < BCPW; ++s) {
           const int k = wv_id + 4 * s;
           if (k < NBC) {
             int TI, TJ;
             bc_tile(k, TI, TJ);
-            if (TI == I && TJ < I)
-              acc_bc[s] = tile_mma<T, false, false>(acc_bc[s], sYdec, L::LPT, sZ, L::LPT, 16 * TI,
-                                                    16 * TJ, PT);
+            frag a = Mma<T>::ld_c(sYu, L::LPT, 16 * TI, 0);
+            const int pb = 8 * (lane_id() >> 4);
+            const int rs = 16 * TI, re = 16 * TJ + 15;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float mf = __expf(sCum[rs * L::LC + pb + e] - sCum[re * L::LC + pb + e]);
+              a[e] = from_f<T>(to_f(a[e]) * mf);
+            }
+            acc_bc[s] = Mma<T>::mma(a, Mma<T>::ld_c(sVd, L::LPT, 16 * TJ, 0), acc_bc[s]);
           }
         }
-        __syncthreads();
-      }
-      // ---- E: diagonal blocks (every lower block on the exact path) pairwise
+      } else {
+        // exact path: pairwise with the reference's clips
 #pragma unroll
-      for (int s = 0; s < BCPW; ++s) {
-        const int k = wv_id + 4 * s;
-        if (k < NBC) {
-          int TI, TJ;
-          bc_tile(k, TI, TJ);
-          if (TI == TJ || exact) {
+        for (int s = 0; s < BCPW; ++s) {
+          const int k = wv_id + 4 * s;
+          if (k < NBC) {
+            int TI, TJ;
+            bc_tile(k, TI, TJ);
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
               const int i = 16 * TI + tile_row(ii), j = 16 * TJ + tile_col();
               if (j <= i) {
                 float sum = 0.f;
-#pragma unroll 4
                 for (int p = 0; p < PT; ++p) {
                   const float dd = fminf(fmaxf(sCum[i * L::LC + p] - sCum[j * L::LC + p], -kClipDecay), kClipDecay);
-                  sum += to_f(sDy[i * L::LPT + p]) * sDbx[j * L::LC + p] * fminf(__expf(dd), 1e6f);
+                  const float dbx = sanitize(to_f(sDt[j * L::LPT + p]) * to_f(sX[j * L::LPT + p]));
+                  sum += to_f(sDy[i * L::LPT + p]) * dbx * fminf(__expf(dd), 1e6f);
                 }
                 acc_bc[s][ii] += sum;
               }
@@ -275,16 +283,68 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           }
         }
       }
-      // ---- F: per-element terms (tile layout of this wave's row blocks)
+
+      // ---- D: per row block of this wave: R, S and the per-element terms
       float lastb[YNI][4];
 #pragma unroll
       for (int ni = 0; ni < YNI; ++ni)
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) lastb[ni][ii] = 0.f;
-      float dcum_v[BPW][YNI][4], ddt1_v[BPW][YNI][4];
-#pragma unroll
+#pragma unroll 1
       for (int bi = 0; bi < BPW; ++bi) {
-        const int I = wv_id * BPW + bi;
+        const int I = my_block(bi);
+        f32x4 Rv[YNI], Sv[YNI];
+        if (!exact) {
+          f32x4 ro[YNI], rd[YNI], so[YNI], sd[YNI];
+#pragma unroll
+          for (int ni = 0; ni < YNI; ++ni) { ro[ni] = zero4(); so[ni] = zero4(); }
+          for (int J = 0; J < I; ++J) {  // sources below the block
+            const frag a = cb_frag<T>(cbg, C, 16 * I, 16 * J, 0);
+#pragma unroll
+            for (int ni = 0; ni < YNI; ++ni) {
+              f32x4 q = Mma<T>::mma(a, Mma<T>::ld_t(sVd, L::LPT, 16 * ni, 16 * J), zero4());
+              q = Mma<T>::mma(a, Mma<T>::ld_t(sVdl, L::LPT, 16 * ni, 16 * J), q);
+              const int pc = 16 * ni + tile_col();
+              const float mf = __expf(sCum[16 * I * L::LC + pc] - sCum[(16 * J + 15) * L::LC + pc]);
+#pragma unroll
+              for (int k = 0; k < 4; ++k) ro[ni][k] += mf * q[k];
+            }
+          }
+          for (int I2 = I + 1; I2 < NB; ++I2) {  // targets above the block (column side)
+            const frag a = cb_frag<T>(cbtg, C, 16 * I, 16 * I2, 0);
+#pragma unroll
+            for (int ni = 0; ni < YNI; ++ni) {
+              f32x4 q = Mma<T>::mma(a, Mma<T>::ld_t(sYu, L::LPT, 16 * ni, 16 * I2), zero4());
+              q = Mma<T>::mma(a, Mma<T>::ld_t(sYul, L::LPT, 16 * ni, 16 * I2), q);
+              const int pc = 16 * ni + tile_col();
+              const float mf = __expf(sCum[16 * I2 * L::LC + pc] - sCum[(16 * I + 15) * L::LC + pc]);
+#pragma unroll
+              for (int k = 0; k < 4; ++k) so[ni][k] += mf * q[k];
+            }
+          }
+          {  // the diagonal block
+            const frag ar = cb_frag<T>(cbg, C, 16 * I, 16 * I, 1);
+            const frag as = cb_frag<T>(cbtg, C, 16 * I, 16 * I, 2);
+#pragma unroll
+            for (int ni = 0; ni < YNI; ++ni) {
+              rd[ni] = Mma<T>::mma(ar, Mma<T>::ld_t(sVd, L::LPT, 16 * ni, 16 * I), zero4());
+              rd[ni] = Mma<T>::mma(ar, Mma<T>::ld_t(sVdl, L::LPT, 16 * ni, 16 * I), rd[ni]);
+              sd[ni] = Mma<T>::mma(as, Mma<T>::ld_t(sYu, L::LPT, 16 * ni, 16 * I), zero4());
+              sd[ni] = Mma<T>::mma(as, Mma<T>::ld_t(sYul, L::LPT, 16 * ni, 16 * I), sd[ni]);
+            }
+          }
+#pragma unroll
+          for (int ni = 0; ni < YNI; ++ni) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const int i = 16 * I + tile_row(k), p = 16 * ni + tile_col();
+              const float ci = sCum[i * L::LC + p];
+              const float cs = sCum[16 * I * L::LC + p], ce = sCum[(16 * I + 15) * L::LC + p];
+              Rv[ni][k] = __expf(ci - cs) * ro[ni][k] + __expf(ci - ce) * rd[ni][k];
+              Sv[ni][k] = __expf(ce - ci) * so[ni][k] + __expf(cs - ci) * sd[ni][k];
+            }
+          }
+        }
 #pragma unroll
         for (int ni = 0; ni < YNI; ++ni) {
           // y_off_raw = C state^T and dwrite = B dstate^T for this tile (:126,134)
@@ -296,60 +356,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             const float ci = sCum[i * L::LC + p];
             const float cl = sCum[(C - 1) * L::LC + p];
             const float dyi = to_f(sDy[i * L::LPT + p]);
-            const float dbxi = sDbx[i * L::LC + p];
-            // pairwise part (the diagonal block, or every pair on the exact
-            // path): S1m (i as row), S2 / S2m (i as column)
-            float s1m = 0.f, s2 = 0.f, s2m = 0.f;
-            for (int j = exact ? 0 : 16 * I; j <= i; ++j) {
-              const float dd = ci - sCum[j * L::LC + p];
-              const float m = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
-              s1m += to_f(sCB[i * L::LCB + j]) *
-                     fminf(__expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay)), 1e6f) * sDbx[j * L::LC + p] * m;
+            const float dtv = to_f(sDt[i * L::LPT + p]), xv = to_f(sX[i * L::LPT + p]);
+            const float dbxi = sanitize(dtv * xv);
+            float rsum, ssum, ssum_m;
+            if (!exact) {
+              rsum = Rv[ni][ii];
+              ssum = ssum_m = Sv[ni][ii];
+            } else {
+              // every pair with the reference's clip, 1e6 cap and masks:
+              // R (i as row, masked), S / S_m (i as column)
+              rsum = 0.f; ssum = 0.f; ssum_m = 0.f;
+              for (int j = 0; j <= i; ++j) {
+                const float dd = ci - sCum[j * L::LC + p];
+                const float m = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
+                const float dbx = sanitize(to_f(sDt[j * L::LPT + p]) * to_f(sX[j * L::LPT + p]));
+                rsum += to_f(cbg[(size_t)i * C + j]) *
+                        fminf(__expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay)), 1e6f) * dbx * m;
+              }
+              for (int i2 = i; i2 < C; ++i2) {
+                const float dd = sCum[i2 * L::LC + p] - ci;
+                const float m = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
+                const float v = to_f(cbg[(size_t)i2 * C + i]) *
+                                fminf(__expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay)), 1e6f) *
+                                to_f(sDy[i2 * L::LPT + p]);
+                ssum += v;
+                ssum_m += v * m;
+              }
             }
-            for (int i2 = i; i2 < (exact ? C : 16 * I + 16); ++i2) {
-              const float dd = sCum[i2 * L::LC + p] - ci;
-              const float m = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
-              const float v = to_f(sCB[i2 * L::LCB + i]) *
-                              fminf(__expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay)), 1e6f) *
-                              to_f(sDy[i2 * L::LPT + p]);
-              s2 += v;
-              s2m += v * m;
-            }
-            const float ydo_f =
-                (!exact && I > 0) ? ydo[bi][ni][ii] * __expf(ci - sCum[16 * I * L::LC + p]) : 0.f;
-            const float dd2_f = (!exact && ybase<T>(I) < C)
-                                    ? dd2[bi][ni][ii] * __expf(sCum[(16 * I + 15) * L::LC + p] - ci)
-                                    : 0.f;
             const float dte_raw = cl - ci;
             const float dte = sanitize(__expf(fminf(fmaxf(dte_raw, -kClipDecay), kClipDecay)), 1e6f);
             const float m2 = (dte_raw >= -kClipDecay && dte_raw <= kClipDecay) ? 1.f : 0.f;
             const float dh = __expf(fminf(fmaxf(ci, -kClipDecay), 0.f));
             const float m1 = (ci >= -kClipDecay && ci <= 0.f) ? 1.f : 0.f;
             const float dw = dwr[ii];
-            const float ddbx = sanitize(dw * dte + dd2_f + s2);          // :138,148,166
+            const float ddbx = sanitize(dw * dte + ssum);                 // :138,148,166
             const size_t o = ((row0 + i) * dm.H + h) * P + p0 + p;
-            const float dtv = to_f(dt[o]), xv = to_f(x[o]);
-            ddt1_v[bi][ni][ii] = ddbx * xv;                               // :167
+            sDdt1[i * L::LC + p] = ddbx * xv;                             // :167
             dx[o] = from_f<T>(sanitize(ddbx * dtv));                     // :168,193 + final
             const float dte_term = dw * dbxi * dte * m2;                  // d_decay_to_end_diff :142
             lastb[ni][ii] += dte_term;
-            dcum_v[bi][ni][ii] = sanitize(dyi * (ydo_f + s1m) - dbxi * (dd2_f + s2m) +
-                                          dyi * yoff[ii] * dh * m1 - dte_term);  // :162-173
+            sRed[i * L::LC + p] = sanitize(dyi * rsum - dbxi * ssum_m +
+                                           dyi * yoff[ii] * dh * m1 - dte_term);  // :162-173
           }
         }
-      }
-      __syncthreads();  // Ydh / W / Ydec / Z / Y are dead: reuse as fp32 scratch
-#pragma unroll
-      for (int bi = 0; bi < BPW; ++bi) {
-        const int I = wv_id * BPW + bi;
-#pragma unroll
-        for (int ni = 0; ni < YNI; ++ni)
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const int i = 16 * I + tile_row(ii), p = 16 * ni + tile_col();
-            sRed[i * L::LC + p] = dcum_v[bi][ni][ii];
-            sDdt1[i * L::LC + p] = ddt1_v[bi][ni][ii];
-          }
       }
       // column sums of the decay_to_end term over this wave's rows
 #pragma unroll
@@ -387,7 +436,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         for (int r = 0; r < RS; ++r) {
           const int row = seg * RS + r;
           const size_t o = ((row0 + row) * dm.H + h) * P + p0 + p;
-          const float dtv = to_f(dt[o]);
+          const float dtv = to_f(sDt[row * L::LPT + p]);
           const float araw = dtv * Ah;
           const float dA = (araw >= -kClipDecay && araw <= kClipDecay) ? (v[r] + off) : 0.f;
           ddt[o] = from_f<T>(sanitize(sDdt1[row * L::LC + p] + dA * Ah));   // :187,190 + final
