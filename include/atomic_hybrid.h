@@ -127,8 +127,9 @@ int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const void* k, con
 /* ---------------------------------------------------------------- Mamba2 */
 
 enum {
-  /* forward: keep the state entering each chunk in the workspace for a
-     following atomic_mamba2_bwd on the same inputs and workspace */
+  /* forward: the per-chunk states a following atomic_mamba2_bwd on the same
+     inputs and workspace can reuse (the forward always leaves them in the
+     workspace; the flag is accepted for symmetry with GDN2) */
   ATOMIC_MAMBA2_SAVE = 1,
   /* backward: the workspace holds the intermediates of an
      atomic_mamba2_fwd(..., ATOMIC_MAMBA2_SAVE) call on identical inputs */
