@@ -50,7 +50,6 @@ struct Mamba2Grads {
 // change only pairs whose weight is below exp(-20) (a relative 2e-9).
 // A slice with a positive step exponent or a block range above kMaxRange is
 // evaluated pairwise with the reference's clips and masks instead.
-constexpr float kMaxRange = 60.f;
 
 template <typename T, int C, int N, int PT>
 struct CkLds {
@@ -76,30 +75,6 @@ struct CkLds {
   static constexpr int off_misc = off_tot + NSEG * PT * 4;   // lasta[PT], lastb[4][PT], dA[8]
   static constexpr int total = off_misc + (PT + 4 * PT + 8) * 4;
 };
-
-// A fragment of a 16x16 (k = 16) block of a row-major [C][C] matrix in global
-// memory: lanes of groups 0, 1 hold k = 0..15; groups 2, 3 hold zeros (and
-// read nothing).  mask: 0 none, 1 keep k <= m (lower), 2 keep k >= m (upper).
-template <typename T>
-__device__ __forceinline__ typename Mma<T>::frag cb_frag(const T* g, int ld, int m0, int k0, int mask) {
-  typename Mma<T>::frag a;
-  const int l = lane_id();
-  if (l < 32) {
-    a = Mma<T>::ld_c(g, ld, m0, k0);
-    if (mask) {
-      const int m = l & 15, kb = 8 * (l >> 4);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const bool keep = mask == 1 ? (kb + e <= m) : (kb + e >= m);
-        if (!keep) a[e] = (T)0.f;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) a[e] = (T)0.f;
-  }
-  return a;
-}
 
 template <typename T, typename TD, int C, int P, int N>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void mamba2_bwd_chunk(
@@ -577,18 +552,22 @@ __global__ __launch_bounds__(256) void mamba2_bwd_bc(Mamba2Dims dm, int G, const
     }
 }
 
-// dA[h] = sanitize(sum_n sanitize(sum_b dap[b][n][h]))
+// dA[h] = sanitize(sum_n sanitize(sum_b dap[b][n][h])); one workgroup per head.
 __global__ __launch_bounds__(256) void mamba2_bwd_da(Mamba2Dims dm, const float* __restrict__ dap,
                                                     float* __restrict__ dA) {
-  for (int h = threadIdx.x; h < dm.H; h += 256) {
-    float tot = 0.f;
-    for (int n = 0; n < dm.NT; ++n) {
-      float s = 0.f;
-      for (int b = 0; b < dm.B; ++b) s += dap[((size_t)b * dm.NT + n) * dm.H + h];
-      tot += sanitize(s);
-    }
-    dA[h] = sanitize(tot);
+  __shared__ float red[4];
+  const int h = blockIdx.x;
+  float tot = 0.f;
+  for (int n = threadIdx.x; n < dm.NT; n += 256) {
+    float s = 0.f;
+    for (int b = 0; b < dm.B; ++b) s += dap[((size_t)b * dm.NT + n) * dm.H + h];
+    tot += sanitize(s);
   }
+#pragma unroll
+  for (int sh = 1; sh < 64; sh <<= 1) tot += __shfl_xor(tot, sh);
+  if (lane_id() == 0) red[wave_id()] = tot;
+  __syncthreads();
+  if (threadIdx.x == 0) dA[h] = sanitize(red[0] + red[1] + red[2] + red[3]);
 }
 
 }  // namespace ah

@@ -24,17 +24,18 @@
 // mamba2_chunk_y      one workgroup per (batch, chunk, head, 32 channels):
 //                     y = y_diag + y_off.
 //
-// y_diag off the diagonal 16-row blocks: for output block I and source block
-// J < I the decay factorises as
+// y_diag on 16-row blocks: for output block I and source block J < I the
+// decay factorises as
 //   exp(cum_i - cum_j) = exp(cum_i - cum_{16I}) exp(cum_{16I} - cum_{16J+15})
 //                        exp(cum_{16J+15} - cum_j),
 // each factor <= 1 whenever dt A <= 0 (the model's A < 0, dt > 0), so the
 // pair (I, J) is one MFMA on V_j = exp(cum_{16J+15} - cum_j) dBx_j with a
-// per-channel scale, and nothing overflows.  Pairs there whose decay is below
-// -20 carry their true weight instead of the reference's exp(-20) floor (a
-// difference below 2e-9 |CB dBx|).  Diagonal 16x16 blocks are evaluated
-// pairwise exactly as the reference does, and a slice with any dt A > 0
-// evaluates every pair that way.
+// per-channel scale, and nothing overflows.  Inside the diagonal block the
+// same V_j carries a factor exp(cum_i - cum_{16I+15}) <= exp(range_I), used
+// while every block's range stays below kMaxRange.  Pairs whose decay is
+// below -20 carry their true weight instead of the reference's exp(-20)
+// floor (a difference below 2e-9 |CB dBx|).  A slice with any dt A > 0, or a
+// steeper block, evaluates every pair with the reference's clip and cap.
 #include "mamba2.hpp"
 
 namespace ah {
@@ -270,17 +271,45 @@ __global__ __launch_bounds__(256) void mamba2_state_pass(Mamba2Dims dm, Mamba2Ch
 }
 
 // ------------------------------------------------------------------ outputs
+// Blocks whose decay range cum_{16I} - cum_{16I+15} exceeds this are not
+// factorised (the factor exp(cum_{16I} - cum_j) >= 1 must stay finite).
+constexpr float kMaxRange = 60.f;
+
+// A fragment of a 16x16 (k = 16) block of a row-major [C][C] matrix in global
+// memory: lanes of groups 0, 1 hold k = 0..15; groups 2, 3 hold zeros (and
+// read nothing).  mask: 0 none, 1 keep k <= m (lower), 2 keep k >= m (upper).
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::frag cb_frag(const T* g, int ld, int m0, int k0, int mask) {
+  typename Mma<T>::frag a;
+  const int l = lane_id();
+  if (l < 32) {
+    a = Mma<T>::ld_c(g, ld, m0, k0);
+    if (mask) {
+      const int m = l & 15, kb = 8 * (l >> 4);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bool keep = mask == 1 ? (kb + e <= m) : (kb + e >= m);
+        if (!keep) a[e] = (T)0.f;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[e] = (T)0.f;
+  }
+  return a;
+}
+
 template <typename T, int C, int N, int PT>
 struct YLds {
   static constexpr int PAD = Pad<T>::v;
-  static constexpr int LPT = PT + PAD, LN = N + PAD, LD = 16 + PAD;
+  static constexpr int LPT = PT + PAD, LN = N + PAD;
+  static constexpr int LC = PT + 1;  // fp32 rows, padded against bank conflicts
   static constexpr int NSEG = 256 / PT;
   static constexpr int off_cum = 0;
-  static constexpr int off_dbx = off_cum + C * PT * 4;
-  static constexpr int off_v = off_dbx + C * PT * 4;
-  static constexpr int off_st = off_v + C * LPT * (int)sizeof(T);
-  static constexpr int off_cbd = off_st + PT * LN * (int)sizeof(T);
-  static constexpr int off_tot = off_cbd + C * LD * (int)sizeof(T);
+  static constexpr int off_dbx = off_cum + C * LC * 4;
+  static constexpr int off_v = off_dbx + C * LC * 4;                 // V dBx, + 16 zero rows
+  static constexpr int off_st = off_v + (C + 16) * LPT * (int)sizeof(T);
+  static constexpr int off_tot = off_st + PT * LN * (int)sizeof(T);
   static constexpr int total = off_tot + NSEG * PT * 4;
 };
 
@@ -291,6 +320,10 @@ __device__ __forceinline__ int y_block(int w, int b) {
   return b == 0 ? w : NB - 1 - w;
 }
 
+// y_diag on 16-row blocks, Vd_j = exp(cum_{16J+15} - cum_j) dBx_j:
+//   off the diagonal  U_i sum_{J<I} M_IJ (CB_IJ Vd_J)_i
+//   diagonal block    exp(cum_i - cum_{16I+15}) (tril(CB_II) Vd_I)_i
+// with U_i = exp(cum_i - cum_{16I}), M_IJ = exp(cum_{16I} - cum_{16J+15}).
 template <typename T, int C, int P, int N, int PT>
 __global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __restrict__ dt,
                                                      const T* __restrict__ x, const float* __restrict__ A,
@@ -302,7 +335,6 @@ __global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __
   float* sDbx = reinterpret_cast<float*>(lds + L::off_dbx);
   T* sV = reinterpret_cast<T*>(lds + L::off_v);
   T* sSt = reinterpret_cast<T*>(lds + L::off_st);
-  T* sCbd = reinterpret_cast<T*>(lds + L::off_cbd);
   float* sTot = reinterpret_cast<float*>(lds + L::off_tot);
 
   constexpr int NPT = P / PT;
@@ -317,6 +349,8 @@ __global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __
   const T* cbg = ck.cb + (size_t)bn * C * C;
   const T* cg = Cm + row0 * N;
   const int wv_id = wave_id();
+  constexpr int NB = C / 16, BPW = NB / 4, YNI = PT / 16, KN = N / Mma<T>::KS;
+  static_assert(NB % 4 == 0, "row blocks must split evenly over 4 waves");
 
   constexpr int PER_ROW = PT / 8, NE = C * PER_ROW, EPT = NE / 256;
   static_assert(NE % 256 == 0, "slice must split evenly over the workgroup");
@@ -328,62 +362,58 @@ __global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __
     rx[i].load(x + base + r * rsx + c);
   }
   stage_rows<T, PT, N>(sSt, L::LN, ck.state_pre + (((size_t)bn * dm.H + h) * P + p0) * N, N);
-  // diagonal 16x16 blocks of CB: row i, columns 16 (i / 16) .. + 15
-  for (int e = threadIdx.x; e < 2 * C; e += 256) {
-    const int i = e >> 1, half = e & 1;
-    *reinterpret_cast<uint4*>(sCbd + i * L::LD + 8 * half) =
-        *reinterpret_cast<const uint4*>(cbg + (size_t)i * C + 16 * (i >> 4) + 8 * half);
-  }
-  int pos = 0;
+  int flag = 0;
 #pragma unroll
   for (int i = 0; i < EPT; ++i) {
     const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float a = rdt[i][j] * Ah;
-      pos |= a > 0.f;
-      sCum[r * PT + c + j] = sanitize(a, kClipDecay);
-      sDbx[r * PT + c + j] = sanitize(rdt[i][j] * rx[i][j]);
+      flag |= a > 0.f;
+      sCum[r * L::LC + c + j] = sanitize(a, kClipDecay);
+      sDbx[r * L::LC + c + j] = sanitize(rdt[i][j] * rx[i][j]);
     }
   }
-  // a slice with a positive step exponent breaks the monotone decay the
-  // factorisation relies on
-  const bool exact = __syncthreads_or(pos);
-  column_cumsum<C, PT>(sCum, sTot);
   __syncthreads();
+  column_cumsum<C, PT, L::LC>(sCum, sTot);
+  __syncthreads();
+  for (int e = threadIdx.x; e < NB * PT; e += 256) {
+    const int I = e / PT, p = e % PT;
+    flag |= sCum[16 * I * L::LC + p] - sCum[(16 * I + 15) * L::LC + p] > kMaxRange;
+  }
+  // a positive step exponent (or too steep a block) is evaluated pairwise
+  const bool exact = __syncthreads_or(flag);
   if (!exact) {
-    for (int e = threadIdx.x; e < C * PT; e += 256) {
+    for (int e = threadIdx.x; e < (C + 16) * PT; e += 256) {
       const int j = e / PT, p = e % PT;
-      sV[j * L::LPT + p] = from_f<T>(__expf(sCum[(j | 15) * PT + p] - sCum[j * PT + p]) * sDbx[j * PT + p]);
+      const float v = j < C ? __expf(sCum[(j | 15) * L::LC + p] - sCum[j * L::LC + p]) * sDbx[j * L::LC + p] : 0.f;
+      sV[j * L::LPT + p] = from_f<T>(v);
     }
   }
   __syncthreads();
 
-  constexpr int NB = C / 16, BPW = NB / 4, YNI = PT / 16, KN = N / Mma<T>::KS;
-  static_assert(NB % 4 == 0, "row blocks must split evenly over 4 waves");
 #pragma unroll
   for (int bi = 0; bi < BPW; ++bi) {
     const int I = y_block<NB>(wv_id, bi);
-    f32x4 off[YNI], yo[YNI];
+    f32x4 off[YNI], dg[YNI], yo[YNI];
 #pragma unroll
-    for (int ni = 0; ni < YNI; ++ni) { off[ni] = zero4(); yo[ni] = zero4(); }
+    for (int ni = 0; ni < YNI; ++ni) { off[ni] = zero4(); dg[ni] = zero4(); yo[ni] = zero4(); }
     if (!exact) {
       for (int J = 0; J < I; ++J) {
-        // A = CB[16I.., 16J..16J+15]; k = 16..31 (the lanes of groups 2, 3) zeroed
-        typename Mma<T>::frag a = Mma<T>::ld_c(cbg, C, 16 * I, 16 * J);
-        if (lane_id() >= 32) {
-#pragma unroll
-          for (int k = 0; k < 8; ++k) a[k] = (T)0.f;
-        }
+        const typename Mma<T>::frag a = cb_frag<T>(cbg, C, 16 * I, 16 * J, 0);
 #pragma unroll
         for (int ni = 0; ni < YNI; ++ni) {
           const f32x4 q = Mma<T>::mma(a, Mma<T>::ld_t(sV, L::LPT, 16 * ni, 16 * J), zero4());
           const int pc = 16 * ni + tile_col();
-          const float mf = __expf(sCum[16 * I * PT + pc] - sCum[(16 * J + 15) * PT + pc]);
+          const float mf = __expf(sCum[16 * I * L::LC + pc] - sCum[(16 * J + 15) * L::LC + pc]);
 #pragma unroll
           for (int k = 0; k < 4; ++k) off[ni][k] += mf * q[k];
         }
       }
+      const typename Mma<T>::frag ad = cb_frag<T>(cbg, C, 16 * I, 16 * I, 1);
+#pragma unroll
+      for (int ni = 0; ni < YNI; ++ni)
+        dg[ni] = Mma<T>::mma(ad, Mma<T>::ld_t(sV, L::LPT, 16 * ni, 16 * I), zero4());
     }
 #pragma unroll
     for (int kk = 0; kk < KN; ++kk) {
@@ -397,18 +427,20 @@ __global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int i = 16 * I + tile_row(k), p = 16 * ni + tile_col();
-        const float ci = sCum[i * PT + p];
-        const float offv = exact ? 0.f : off[ni][k] * __expf(ci - sCum[16 * I * PT + p]);
-        float diag = 0.f;
-        const int j0 = exact ? 0 : 16 * I;
-        for (int j = j0; j <= i; ++j) {
-          const float cbv = j >= 16 * I ? to_f(sCbd[i * L::LD + j - 16 * I]) : to_f(cbg[(size_t)i * C + j]);
-          const float dd = fminf(fmaxf(ci - sCum[j * PT + p], -kClipDecay), kClipDecay);
-          diag += fminf(__expf(dd), 1e6f) * cbv * sDbx[j * PT + p];
+        const float ci = sCum[i * L::LC + p];
+        float ydiag;
+        if (!exact) {
+          ydiag = off[ni][k] * __expf(ci - sCum[16 * I * L::LC + p]) +
+                  dg[ni][k] * __expf(ci - sCum[(16 * I + 15) * L::LC + p]);
+        } else {
+          ydiag = 0.f;
+          for (int j = 0; j <= i; ++j) {
+            const float dd = fminf(fmaxf(ci - sCum[j * L::LC + p], -kClipDecay), kClipDecay);
+            ydiag += fminf(__expf(dd), 1e6f) * to_f(cbg[(size_t)i * C + j]) * sDbx[j * L::LC + p];
+          }
         }
-        const float ydiag = sanitize(offv + diag);
         const float yoff = sanitize(yo[ni][k] * __expf(fminf(fmaxf(ci, -kClipDecay), 0.f)));
-        y[base + (size_t)i * rsx + p] = sanitize(ydiag + yoff);
+        y[base + (size_t)i * rsx + p] = sanitize(sanitize(ydiag) + yoff);
       }
     }
   }

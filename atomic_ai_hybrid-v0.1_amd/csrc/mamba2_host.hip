@@ -184,7 +184,7 @@ static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x,
   });
   if (rc) return rc;
   return L("mamba2_bwd_da", [&] {
-    hipLaunchKernelGGL(mamba2_bwd_da, dim3(1), dim3(256), 0, st, d, (const float*)gr.dap, dA);
+    hipLaunchKernelGGL(mamba2_bwd_da, dim3((unsigned)d.H), dim3(256), 0, st, d, (const float*)gr.dap, dA);
   });
 }
 
