@@ -212,7 +212,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
 
   stage_convert<TD, T, C, V>(sDO, L::LV, dO + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V,
                              (size_t)dm.H * V);
-  stage_convert<float, T, C, V>(sDV, L::LV, gr.dvn + blk * C * V, V);
+  stage_rows<T, C, V>(sDV, L::LV, gr.dvn + blk * C * V, V);
   stage_rows<T, V, K>(sH, L::LK, ck.hT + blk * V * K, K);
   stage_rows<T, V, K>(sDh, L::LK, gr.dhT + blk * V * K, K);
   stage_rows<T, V, C>(sVn, L::LC, ck.vnT + blk * V * C, C);
@@ -222,7 +222,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
   constexpr int MT = C / 16, NTK = K / 16;
   constexpr int TPW = MT * NTK / 4;
   float* g_dqg = gr.dqg + blk * C * K;
-  float* g_dwt = gr.dwt + blk * C * K;
+  T* g_dwt = gr.dwt + blk * C * K;
   float* g_dkg = gr.dkg + blk * C * K;
 #pragma unroll 2
   for (int t = 0; t < TPW; ++t) {
@@ -237,7 +237,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
     store_tile_n(g_dkg, K, 16 * mi, 16 * ni, c);
   }
   // dAqk = n2n((dO v_new^T) * causal)   (kernel_bwd_b2_dav.py:69,72)
-  float* g_daqk = gr.daqk + blk * C * C;
+  T* g_daqk = gr.daqk + blk * C * C;
   for (int tile = wv_id; tile < MT * MT; tile += 4) {
     const int mi = tile / MT, nj = tile % MT;
     f32x4 acc = zero4();
@@ -245,16 +245,31 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * mi + tile_row(i), c = 16 * nj + tile_col();
-      acc[i] = r >= c ? n2n(acc[i]) : 0.f;
+      acc[i] = r >= c ? n2n(acc[i]) * dm.scale : 0.f;  // the scale of Aqk folded in
     }
     store_tile_n(g_daqk, C, 16 * mi, 16 * nj, acc);
   }
-  // exp(gc_last) * sum_v dh_next * h_pre   (kernel_bwd_b3_wy_dqkg.py:200-201)
-  if (threadIdx.x < K) {
-    const int d = threadIdx.x;
-    float s = 0.f;
-    for (int v = 0; v < V; ++v) s += to_f(sDh[v * L::LK + d]) * to_f(sH[v * L::LK + d]);
-    gr.rlast[blk * K + d] = __expf(ck.gcl[blk * K + d]) * s;
+  // exp(gc_last) * sum_v dh_next * h_pre   (kernel_bwd_b3_wy_dqkg.py:200-201):
+  // 256 / K threads per column, each over a V / (256 / K) slice
+  {
+    constexpr int SPL = 256 / K, VS = V / SPL;
+    const int d = threadIdx.x % K, sp = threadIdx.x / K;
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll 8
+    for (int v = sp * VS; v < sp * VS + VS; v += 2) {
+      s0 += to_f(sDh[v * L::LK + d]) * to_f(sH[v * L::LK + d]);
+      s1 += to_f(sDh[(v + 1) * L::LK + d]) * to_f(sH[(v + 1) * L::LK + d]);
+    }
+    __syncthreads();  // the dAqk tiles are done with sDO: reuse it as scratch
+    float* red = reinterpret_cast<float*>(sDO);
+    red[threadIdx.x] = s0 + s1;
+    __syncthreads();
+    if (threadIdx.x < K) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < SPL; ++j) s += red[j * K + d];
+      gr.rlast[blk * K + d] = __expf(ck.gcl[blk * K + d]) * s;
+    }
   }
 }
 
@@ -337,8 +352,8 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy(Gdn2Dims dm, Gdn2Chunks<T> ck
     }
   }
   stage_rows<T, C, C>(sA, L::LC, ck.ainv + blk * C * C, C);
-  stage_convert<float, T, C, K>(sDW, L::LK, gr.dwt + blk * C * K, K);
-  stage_convert<float, T, C, V>(sDV, L::LV, gr.dvn + blk * C * V, V);
+  stage_rows<T, C, K>(sDW, L::LK, gr.dwt + blk * C * K, K);
+  stage_rows<T, C, V>(sDV, L::LV, gr.dvn + blk * C * V, V);
   __syncthreads();
 
   constexpr int MT = C / 16;
@@ -354,7 +369,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy(Gdn2Dims dm, Gdn2Chunks<T> ck
   // dkb = A^T dw_pseudo (A lower triangular, so rows i >= j only)   (b3:164)
   {
     constexpr int NTK = K / 16, TPW = MT * NTK / 4;
-    float* g_dkb = gr.dwt + blk * C * K;
+    float* g_dkb = gr.dkb + blk * C * K;
 #pragma unroll 2
     for (int t = 0; t < TPW; ++t) {
       const int tile = wv_id * TPW + t, mj = tile % MT, ni = tile / MT;
@@ -401,7 +416,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy(Gdn2Dims dm, Gdn2Chunks<T> ck
   }
   __syncthreads();
   // dAkk = n2n(-(A^T tmp) * strict)   (b3:179-180,212)
-  float* g_dakk = gr.dakk + blk * C * C;
+  T* g_dakk = gr.dakk + blk * C * C;
   for (int tile = wv_id; tile < MT * MT; tile += 4) {
     const int mj = tile / MT, nl = tile % MT;
     f32x4 acc = zero4();
@@ -496,8 +511,8 @@ __global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> 
     for (int j = 0; j < 8; ++j) sGc[r * L::LG + cg * 8 + j] = gcr[rr][j];
   }
   // scale folded into the dAqk operand: Aqk = scale Q~ K~^T
-  stage_convert<float, T, C, C>(sDAqk, L::LC, gr.daqk + blk * C * C, C, dm.scale);
-  stage_convert<float, T, C, C>(sDAkk, L::LC, gr.dakk + blk * C * C, C);
+  stage_rows<T, C, C>(sDAqk, L::LC, gr.daqk + blk * C * C, C);
+  stage_rows<T, C, C>(sDAkk, L::LC, gr.dakk + blk * C * C, C);
   __syncthreads();
 
   // Tiles of [C][K], column-major over tiles so each wave owns whole columns.
@@ -528,7 +543,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> 
   __syncthreads();
 
   const float* g_dqg = gr.dqg + blk * C * K;
-  const float* g_dkb = gr.dwt + blk * C * K;
+  const float* g_dkb = gr.dkb + blk * C * K;
   const float* g_dkg = gr.dkg + blk * C * K;
   float colsum[TPW / MT];
   f32x4 dgcr[TPW];  // written to LDS only after every lane has read gc
@@ -621,12 +636,33 @@ __global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> 
   }
   __syncthreads();
   // B5: dg = sanitize(reverse cumsum over the chunk)   (kernel_bwd_b5_reverse_cumsum.py:17-24)
-  if (tid < K) {
-    const int d = tid;
-    float s = 0.f;
-    for (int r = C - 1; r >= 0; --r) {
-      s += sGc[r * L::LG + d];
-      dg[base + (size_t)r * rsK + d] = sanitize(s);
+  // thread (column group, row segment): suffix sums within the segment, then
+  // the totals of the later segments
+  {
+    const int cg = tid % M::NCG, seg = tid / M::NCG;
+    float v[M::RS][8];
+#pragma unroll
+    for (int rr = M::RS - 1; rr >= 0; --rr) {
+      const int r = seg * M::RS + rr;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[rr][j] = sGc[r * L::LG + cg * 8 + j] + (rr + 1 < M::RS ? v[rr + 1][j] : 0.f);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sTot[seg * K + cg * 8 + j] = v[0][j];
+    __syncthreads();
+    float off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) off[j] = 0.f;
+    for (int s2 = seg + 1; s2 < M::NSEG; ++s2)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) off[j] += sTot[s2 * K + cg * 8 + j];
+#pragma unroll
+    for (int rr = 0; rr < M::RS; ++rr) {
+      const int r = seg * M::RS + rr;
+      float o8[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o8[j] = sanitize(v[rr][j] + off[j]);
+      store8(dg + base + (size_t)r * rsK + cg * 8, o8);
     }
   }
 }

@@ -15,7 +15,7 @@ struct Gdn2Plan {
   // forward intermediates
   size_t o_qg, o_kg, o_wt, o_u, o_aqk, o_ainv, o_gcl, o_ht, o_vnt, fwd_end;
   // backward scratch
-  size_t o_dvn, o_dht, o_dqg, o_dwt, o_dkg, o_daqk, o_dakk, o_rlast, total;
+  size_t o_dvn, o_dht, o_dqg, o_dwt, o_dkb, o_dkg, o_daqk, o_dakk, o_rlast, total;
 };
 
 static int gdn2_plan(const atomic_gdn2_args* a, Gdn2Plan* p) {
@@ -46,13 +46,14 @@ static int gdn2_plan(const atomic_gdn2_args* a, Gdn2Plan* p) {
   p->o_ht = take(N * V * K * es);
   p->o_vnt = take(N * V * C * es);
   p->fwd_end = off;
-  p->o_dvn = take(N * C * V * 4);
+  p->o_dvn = take(N * C * V * es);
   p->o_dht = take(N * V * K * es);
   p->o_dqg = take(N * C * K * 4);
-  p->o_dwt = take(N * C * K * 4);
+  p->o_dwt = take(N * C * K * es);
+  p->o_dkb = take(N * C * K * 4);
   p->o_dkg = take(N * C * K * 4);
-  p->o_daqk = take(N * C * C * 4);
-  p->o_dakk = take(N * C * C * 4);
+  p->o_daqk = take(N * C * C * es);
+  p->o_dakk = take(N * C * C * es);
   p->o_rlast = take(N * K * 4);
   p->total = off;
   return ATOMIC_OK;
@@ -97,13 +98,14 @@ template <typename T>
 static Gdn2Grads<T> gdn2_grads(const Gdn2Plan& p, void* ws) {
   char* base = static_cast<char*>(ws);
   Gdn2Grads<T> g;
-  g.dvn = reinterpret_cast<float*>(base + p.o_dvn);
+  g.dvn = reinterpret_cast<T*>(base + p.o_dvn);
   g.dhT = reinterpret_cast<T*>(base + p.o_dht);
   g.dqg = reinterpret_cast<float*>(base + p.o_dqg);
-  g.dwt = reinterpret_cast<float*>(base + p.o_dwt);
+  g.dwt = reinterpret_cast<T*>(base + p.o_dwt);
+  g.dkb = reinterpret_cast<float*>(base + p.o_dkb);
   g.dkg = reinterpret_cast<float*>(base + p.o_dkg);
-  g.daqk = reinterpret_cast<float*>(base + p.o_daqk);
-  g.dakk = reinterpret_cast<float*>(base + p.o_dakk);
+  g.daqk = reinterpret_cast<T*>(base + p.o_daqk);
+  g.dakk = reinterpret_cast<T*>(base + p.o_dakk);
   g.rlast = reinterpret_cast<float*>(base + p.o_rlast);
   return g;
 }
