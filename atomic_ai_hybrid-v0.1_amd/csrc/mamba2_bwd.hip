@@ -113,8 +113,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   views(0);
 
   const int tid = threadIdx.x;
-  const int g = blockIdx.x % G;
-  const int bn = blockIdx.x / G;
+  // the G head groups of one (batch, chunk) share an XCD (and its L2) for CB, B, C
+  int bn, g;
+  xcd_group_map(blockIdx.x, dm.B * dm.NT, G, bn, g);
   const int bb = bn / dm.NT, n = bn % dm.NT;
   const int HG = dm.H / G;
   const int wv_id = wave_id();
