@@ -435,7 +435,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy(Gdn2Dims dm, Gdn2Chunks<T> ck
 }
 
 // ------------------------------------------------------------------ B4 + combine + B5
-template <typename T, int C, int K>
+template <typename T, int C, int K>  // K here: the columns of one workgroup's slice
 struct InLds {
   static constexpr int PAD = Pad<T>::v;
   static constexpr int LK = K + PAD, LC = C + PAD, LG = K + 4;
@@ -452,14 +452,17 @@ struct InLds {
   static constexpr int total = off_part + 4 * K * 4;
 };
 
-template <typename T, int C, int K, int V>
+// One workgroup per (batch, head, chunk, KH-column slice): every term of B4,
+// B3's element-wise part and B5 is separable over the K columns (only the
+// [C][C] dAqk / dAkk are shared by the slices).
+template <typename T, int C, int K, int V, int KH>
 __global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> gr,
                                                      const T* __restrict__ q, const T* __restrict__ k,
                                                      const T* __restrict__ b, const float* __restrict__ g,
                                                      T* __restrict__ dq, T* __restrict__ dk,
                                                      T* __restrict__ db, float* __restrict__ dg) {
-  typedef InLds<T, C, K> L;
-  typedef ColMap<C, K> M;
+  typedef InLds<T, C, KH> L;
+  typedef ColMap<C, KH> M;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
   T* sQ = reinterpret_cast<T*>(lds + L::off_q);
   T* sKt = reinterpret_cast<T*>(lds + L::off_kt);
@@ -471,8 +474,12 @@ __global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> 
   float* sGl = reinterpret_cast<float*>(lds + L::off_gl);
   float* sPart = reinterpret_cast<float*>(lds + L::off_part);
 
+  constexpr int NKS = K / KH;
   const int tid = threadIdx.x;
-  const int bhn = blockIdx.x;
+  // the NKS slices of one chunk share an XCD (dAqk / dAkk read once per L2)
+  int bhn, ks;
+  xcd_group_map(blockIdx.x, dm.B * dm.H * dm.NT, NKS, bhn, ks);
+  const int d0 = ks * KH;
   const int n = bhn % dm.NT;
   const int bh = bhn / dm.NT;
   const int h = bh % dm.H, bb = bh / dm.H;
@@ -480,10 +487,10 @@ __global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> 
   const size_t blk = (size_t)bhn;
   const size_t rsK = (size_t)dm.H * K;
   const size_t t0 = (size_t)bb * dm.T + (size_t)n * C;
-  const size_t base = (t0 * dm.H + h) * K;
+  const size_t base = (t0 * dm.H + h) * K + d0;  // this slice's column 0
 
   float gcr[M::RS][8];
-  const bool exact = chunk_cumsum<C, K>(g + base, rsK, gcr, sTot, sGl);
+  const bool exact = chunk_cumsum<C, KH>(g + base, rsK, gcr, sTot, sGl);
   const int cg = tid % M::NCG, seg = tid / M::NCG;
 #pragma unroll
   for (int rr = 0; rr < M::RS; ++rr) {
@@ -516,7 +523,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> 
   __syncthreads();
 
   // Tiles of [C][K], column-major over tiles so each wave owns whole columns.
-  constexpr int MT = C / 16, NTK = K / 16;
+  constexpr int MT = C / 16, NTK = KH / 16;
   constexpr int TPW = MT * NTK / 4;
   static_assert((MT * NTK) % 4 == 0 && TPW % MT == 0, "each wave must own whole tile columns");
   f32x4 dQt[TPW], dKt[TPW], dKB[TPW];
@@ -537,14 +544,14 @@ __global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> 
   }
   __syncthreads();
   // raw q, k, b for the element-wise stage (fp32 exact multipliers)
-  stage_rows<T, C, K>(sQ, L::LK, q + base, rsK);
-  stage_rows<T, C, K>(sKt, L::LK, k + base, rsK);
-  stage_rows<T, C, K>(sKB, L::LK, b + base, rsK);
+  stage_rows<T, C, KH>(sQ, L::LK, q + base, rsK);
+  stage_rows<T, C, KH>(sKt, L::LK, k + base, rsK);
+  stage_rows<T, C, KH>(sKB, L::LK, b + base, rsK);
   __syncthreads();
 
-  const float* g_dqg = gr.dqg + blk * C * K;
-  const float* g_dkb = gr.dkb + blk * C * K;
-  const float* g_dkg = gr.dkg + blk * C * K;
+  const float* g_dqg = gr.dqg + blk * C * K + d0;
+  const float* g_dkb = gr.dkb + blk * C * K + d0;
+  const float* g_dkg = gr.dkg + blk * C * K + d0;
   float colsum[TPW / MT];
   f32x4 dgcr[TPW];  // written to LDS only after every lane has read gc
 #pragma unroll
@@ -624,12 +631,12 @@ __global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> 
 #pragma unroll
   for (int c = 0; c < TPW / MT; ++c) {
     const int ni = (wv_id * TPW) / MT + c;
-    sPart[(lane_id() >> 4) * K + 16 * ni + tile_col()] = colsum[c];
+    sPart[(lane_id() >> 4) * KH + 16 * ni + tile_col()] = colsum[c];
   }
   __syncthreads();
-  if (tid < K) {
-    const float extra = sPart[tid] + sPart[K + tid] + sPart[2 * K + tid] + sPart[3 * K + tid] +
-                        gr.rlast[blk * K + tid];
+  if (tid < KH) {
+    const float extra = sPart[tid] + sPart[KH + tid] + sPart[2 * KH + tid] + sPart[3 * KH + tid] +
+                        gr.rlast[blk * K + d0 + tid];
     // dgc3 gets the row term before its n2n in the reference; dgc4 is already
     // sanitized, so the sum below matches dgc3 + dgc4 in unclipped regimes.
     sGc[(C - 1) * L::LG + tid] += extra;
@@ -648,14 +655,14 @@ __global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> 
       for (int j = 0; j < 8; ++j) v[rr][j] = sGc[r * L::LG + cg * 8 + j] + (rr + 1 < M::RS ? v[rr + 1][j] : 0.f);
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) sTot[seg * K + cg * 8 + j] = v[0][j];
+    for (int j = 0; j < 8; ++j) sTot[seg * KH + cg * 8 + j] = v[0][j];
     __syncthreads();
     float off[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) off[j] = 0.f;
     for (int s2 = seg + 1; s2 < M::NSEG; ++s2)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) off[j] += sTot[s2 * K + cg * 8 + j];
+      for (int j = 0; j < 8; ++j) off[j] += sTot[s2 * KH + cg * 8 + j];
 #pragma unroll
     for (int rr = 0; rr < M::RS; ++rr) {
       const int r = seg * M::RS + rr;

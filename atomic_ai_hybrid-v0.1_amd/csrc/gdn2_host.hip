@@ -144,8 +144,9 @@ static int gdn2_backward_impl(const Gdn2Plan& p, const void* q, const void* k, c
                        (const T*)k, (const T*)v, (const T*)w, (const T*)b, g, (T*)dw, (T*)dv);
   });
   if (rc) return rc;
+  constexpr int KH = 64;  // column slice of the intra kernel
   return L("gdn2_bwd_intra", [&] {
-    hipLaunchKernelGGL((gdn2_bwd_intra<T, C, K, V>), dim3(nblk), dim3(256), 0, st, p.dm, gr,
+    hipLaunchKernelGGL((gdn2_bwd_intra<T, C, K, V, KH>), dim3(nblk * (K / KH)), dim3(256), 0, st, p.dm, gr,
                        (const T*)q, (const T*)k, (const T*)b, g, (T*)dq, (T*)dk, (T*)db, dg);
   });
 }
