@@ -9,9 +9,10 @@
 //   gdn2_bwd_hgrad  per chunk: the state contractions of B2/B3
 //                   (kernel_bwd_b2_dav.py:69, kernel_bwd_b3_wy_dqkg.py:154-161,
 //                   :200-201): dAqk, dqg, dw_pseudo, dkg and the gc_last row term.
-//   gdn2_bwd_wy     per chunk: the WY part of B3 (kernel_bwd_b3_wy_dqkg.py:163-179,
-//                   :194-195): dA, dkb = A^T dw_pseudo, dwv = A^T dv,
-//                   dAkk = -A^T clip(clip(dA) A^T) (strict), and the final dw, dv.
+//   gdn2_bwd_wy_a   per chunk: the WY part of B3 (kernel_bwd_b3_wy_dqkg.py:163-180):
+//                   dA and dAkk = -A^T clip(clip(dA) A^T) (strict).
+//   gdn2_bwd_wy_b   per (chunk, 64 columns): dkb = A^T dw_pseudo, dwv = A^T dv
+//                   and the final dw, dv (:164,167,194-195).
 //   gdn2_bwd_intra  per chunk: B4 (kernel_bwd_b4_intra.py:57-132) in the
 //                   factorised form (or exact pairwise, same criterion as the
 //                   forward), the B3 element-wise terms, the combine of
@@ -274,32 +275,37 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
 }
 
 // ------------------------------------------------------------------ B3 WY part
-template <typename T, int C, int K, int V>
-struct WyLds {
+// gdn2_bwd_wy_a  per chunk: dA = clip(dw_pseudo kb^T + dv_new wv^T) with the
+//                K / V contraction staged in 64-column halves, then
+//                dAkk = n2n(-(A^T clip(dA A^T)) * strict)   (b3:163-180,212)
+// gdn2_bwd_wy_b  per (chunk, 64-column slice): dkb = A^T dw_pseudo and
+//                dwv = A^T dv_new; dw = dwv v, dv = dwv w   (b3:164,167,194-195)
+template <typename T, int C, int KH>
+struct WyALds {
   static constexpr int PAD = Pad<T>::v;
-  static constexpr int LK = K + PAD, LV = V + PAD, LC = C + PAD;
-  static constexpr int OK_ = C * LK * (int)sizeof(T), OV = C * LV * (int)sizeof(T),
-                       OC = C * LC * (int)sizeof(T);
+  static constexpr int LH = KH + PAD, LC = C + PAD;
+  static constexpr int OH = C * LH * (int)sizeof(T), OC = C * LC * (int)sizeof(T);
   static constexpr int off_a = 0;
   static constexpr int off_dw = off_a + OC;
-  static constexpr int off_dv = off_dw + OK_;
-  static constexpr int off_kb = off_dv + OV;
-  static constexpr int off_wv = off_kb + OK_;
-  static constexpr int off_da = off_wv + OV;
-  static constexpr int off_tmp = off_da + OC;
-  static constexpr int off_tot = off_tmp + OC;
-  static constexpr int off_gl = off_tot + ColMap<C, K>::NSEG * K * 4;
-  static constexpr int total = off_gl + K * 4;
+  static constexpr int off_dv = off_dw + OH;
+  static constexpr int off_kb = off_dv + OH;  // then clip(dA A^T)
+  static constexpr int off_wv = off_kb + OH;
+  static constexpr int off_da = off_wv + OH;
+  static constexpr int off_tot = off_da + OC;
+  static constexpr int off_gl = off_tot + ColMap<C, KH>::NSEG * KH * 4;
+  static constexpr int total = off_gl + KH * 4;
+  static_assert(OC <= OH * 2, "dA A^T must fit in the kb / wv region");
 };
 
 template <typename T, int C, int K, int V>
-__global__ __launch_bounds__(256) void gdn2_bwd_wy(Gdn2Dims dm, Gdn2Chunks<T> ck, Gdn2Grads<T> gr,
-                                                  const T* __restrict__ k, const T* __restrict__ v,
-                                                  const T* __restrict__ w, const T* __restrict__ b,
-                                                  const float* __restrict__ g, T* __restrict__ dw,
-                                                  T* __restrict__ dv) {
-  typedef WyLds<T, C, K, V> L;
-  typedef ColMap<C, K> M;
+__global__ __launch_bounds__(256) void gdn2_bwd_wy_a(Gdn2Dims dm, Gdn2Chunks<T> ck, Gdn2Grads<T> gr,
+                                                    const T* __restrict__ k, const T* __restrict__ v,
+                                                    const T* __restrict__ w, const T* __restrict__ b,
+                                                    const float* __restrict__ g) {
+  constexpr int KH = 64;
+  static_assert(K == V && K % KH == 0, "K and V are staged in the same 64-column halves");
+  typedef WyALds<T, C, KH> L;
+  typedef ColMap<C, KH> M;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
   T* sA = reinterpret_cast<T*>(lds + L::off_a);
   T* sDW = reinterpret_cast<T*>(lds + L::off_dw);
@@ -307,7 +313,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy(Gdn2Dims dm, Gdn2Chunks<T> ck
   T* sKB = reinterpret_cast<T*>(lds + L::off_kb);
   T* sWV = reinterpret_cast<T*>(lds + L::off_wv);
   T* sDA = reinterpret_cast<T*>(lds + L::off_da);
-  T* sTmp = reinterpret_cast<T*>(lds + L::off_tmp);
+  T* sTmp = reinterpret_cast<T*>(lds + L::off_kb);
   float* sTot = reinterpret_cast<float*>(lds + L::off_tot);
   float* sGl = reinterpret_cast<float*>(lds + L::off_gl);
 
@@ -321,88 +327,51 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy(Gdn2Dims dm, Gdn2Chunks<T> ck
   const size_t rsK = (size_t)dm.H * K, rsV = (size_t)dm.H * V;
   const size_t t0 = (size_t)bb * dm.T + (size_t)n * C;
 
-  // kb = b k e^{gc}, wv = w v (rounded to the input dtype), raw v and w
-  float gcr[M::RS][8];
-  chunk_cumsum<C, K>(g + (t0 * dm.H + h) * K, rsK, gcr, sTot, sGl);
-  {
-    const int cg = tid % M::NCG, seg = tid / M::NCG;
+  stage_rows<T, C, C>(sA, L::LC, ck.ainv + blk * C * C, C);
+  constexpr int MT = C / 16;
+  constexpr int TPW = MT * MT / 4;
+  f32x4 da[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) da[t] = zero4();
+  const int cg = tid % M::NCG, seg = tid / M::NCG;
+  for (int c0 = 0; c0 < K; c0 += KH) {
+    // kb = b k e^{gc} and wv = w v (rounded to the input dtype) for these columns
+    float gcr[M::RS][8];
+    chunk_cumsum<C, KH>(g + (t0 * dm.H + h) * K + c0, rsK, gcr, sTot, sGl);
 #pragma unroll
     for (int rr = 0; rr < M::RS; ++rr) {
       const int r = seg * M::RS + rr;
-      float kv[8], bv[8], kb[8];
-      load8(k + ((t0 + r) * dm.H + h) * K + cg * 8, kv);
-      load8(b + ((t0 + r) * dm.H + h) * K + cg * 8, bv);
+      float kv[8], bv[8], kb[8], vv[8], ww[8], wv[8];
+      load8(k + ((t0 + r) * dm.H + h) * K + c0 + cg * 8, kv);
+      load8(b + ((t0 + r) * dm.H + h) * K + c0 + cg * 8, bv);
+      load8(v + ((t0 + r) * dm.H + h) * V + c0 + cg * 8, vv);
+      load8(w + ((t0 + r) * dm.H + h) * V + c0 + cg * 8, ww);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) kb[j] = (bv[j] * kv[j]) * __expf(gcr[rr][j]);
-      store8(sKB + r * L::LK + cg * 8, kb);
+      for (int j = 0; j < 8; ++j) {
+        kb[j] = (bv[j] * kv[j]) * __expf(gcr[rr][j]);
+        wv[j] = to_f(from_f<T>(ww[j] * vv[j]));
+      }
+      store8(sKB + r * L::LH + cg * 8, kb);
+      store8(sWV + r * L::LH + cg * 8, wv);
     }
-  }
-  {
-    typedef ColMap<C, V> MV;
-    const int cg = tid % MV::NCG, seg = tid / MV::NCG;
+    stage_rows<T, C, KH>(sDW, L::LH, gr.dwt + blk * C * K + c0, K);
+    stage_rows<T, C, KH>(sDV, L::LH, gr.dvn + blk * C * V + c0, V);
+    __syncthreads();
 #pragma unroll
-    for (int rr = 0; rr < MV::RS; ++rr) {
-      const int r = seg * MV::RS + rr;
-      float vv[8], ww[8], wv[8];
-      load8(v + ((t0 + r) * dm.H + h) * V + cg * 8, vv);
-      load8(w + ((t0 + r) * dm.H + h) * V + cg * 8, ww);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) wv[j] = to_f(from_f<T>(ww[j] * vv[j]));
-      store8(sWV + r * L::LV + cg * 8, wv);
+    for (int t = 0; t < TPW; ++t) {
+      const int tile = wv_id * TPW + t, mi = tile / MT, nj = tile % MT;
+      da[t] = tile_mma<T, false, false>(da[t], sDW, L::LH, sKB, L::LH, 16 * mi, 16 * nj, KH);
+      da[t] = tile_mma<T, false, false>(da[t], sDV, L::LH, sWV, L::LH, 16 * mi, 16 * nj, KH);
     }
+    __syncthreads();  // before the next half overwrites the operands
   }
-  stage_rows<T, C, C>(sA, L::LC, ck.ainv + blk * C * C, C);
-  stage_rows<T, C, K>(sDW, L::LK, gr.dwt + blk * C * K, K);
-  stage_rows<T, C, V>(sDV, L::LV, gr.dvn + blk * C * V, V);
-  __syncthreads();
-
-  constexpr int MT = C / 16;
-  // dA = clip(dw_pseudo kb^T + dv wv^T)   (b3:163-172)
-  for (int tile = wv_id; tile < MT * MT; tile += 4) {
-    const int mi = tile / MT, nj = tile % MT;
-    f32x4 acc = tile_mma<T, false, false>(zero4(), sDW, L::LK, sKB, L::LK, 16 * mi, 16 * nj, K);
-    acc = tile_mma<T, false, false>(acc, sDV, L::LV, sWV, L::LV, 16 * mi, 16 * nj, V);
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int tile = wv_id * TPW + t, mi = tile / MT, nj = tile % MT;
+    f32x4 acc = da[t];
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = sanitize(acc[i]);
     store_tile_n(sDA, L::LC, 16 * mi, 16 * nj, acc);
-  }
-  // dkb = A^T dw_pseudo (A lower triangular, so rows i >= j only)   (b3:164)
-  {
-    constexpr int NTK = K / 16, TPW = MT * NTK / 4;
-    float* g_dkb = gr.dkb + blk * C * K;
-#pragma unroll 2
-    for (int t = 0; t < TPW; ++t) {
-      const int tile = wv_id * TPW + t, mj = tile % MT, ni = tile / MT;
-      const int k0 = tri_k0<T>(mj);
-      f32x4 acc = tile_mma<T, true, true>(zero4(), sA + k0 * L::LC, L::LC, sDW + k0 * L::LK, L::LK,
-                                          16 * mj, 16 * ni, C - k0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = n2n(acc[i]);
-      store_tile_n(g_dkb, K, 16 * mj, 16 * ni, acc);
-    }
-  }
-  // dwv = A^T dv ; dw = dwv * v, dv = dwv * w   (b3:167,194-195) + final sanitize / cast
-  {
-    constexpr int NTV = V / 16, TPW = MT * NTV / 4;
-    T* dwc = dw + (t0 * dm.H + h) * V;
-    T* dvc = dv + (t0 * dm.H + h) * V;
-    const T* vc = v + (t0 * dm.H + h) * V;
-    const T* wc = w + (t0 * dm.H + h) * V;
-#pragma unroll 2
-    for (int t = 0; t < TPW; ++t) {
-      const int tile = wv_id * TPW + t, mj = tile % MT, ni = tile / MT;
-      const int k0 = tri_k0<T>(mj);
-      f32x4 acc = tile_mma<T, true, true>(zero4(), sA + k0 * L::LC, L::LC, sDV + k0 * L::LV, L::LV,
-                                          16 * mj, 16 * ni, C - k0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 16 * mj + tile_row(i), c = 16 * ni + tile_col();
-        const float gw = sanitize(n2n(acc[i] * to_f(vc[(size_t)r * rsV + c])));
-        const float gv = sanitize(n2n(acc[i] * to_f(wc[(size_t)r * rsV + c])));
-        dwc[(size_t)r * rsV + c] = from_f<T>(gw);
-        dvc[(size_t)r * rsV + c] = from_f<T>(gv);
-      }
-    }
   }
   __syncthreads();
   // tmp = clip(dA A^T)   (b3:177-178); A[j][l] = 0 for l > j
@@ -431,6 +400,77 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy(Gdn2Dims dm, Gdn2Chunks<T> ck
       acc[i] = r > c ? n2n(-acc[i]) : 0.f;
     }
     store_tile_n(g_dakk, C, 16 * mj, 16 * nl, acc);
+  }
+}
+
+template <typename T, int C, int KH>
+struct WyBLds {
+  static constexpr int PAD = Pad<T>::v;
+  static constexpr int LH = KH + PAD, LC = C + PAD;
+  static constexpr int OH = C * LH * (int)sizeof(T), OC = C * LC * (int)sizeof(T);
+  static constexpr int off_a = 0;
+  static constexpr int off_dw = off_a + OC;
+  static constexpr int off_dv = off_dw + OH;
+  static constexpr int off_v = off_dv + OH;
+  static constexpr int off_w = off_v + OH;
+  static constexpr int total = off_w + OH;
+};
+
+template <typename T, int C, int K, int V>
+__global__ __launch_bounds__(256) void gdn2_bwd_wy_b(Gdn2Dims dm, Gdn2Chunks<T> ck, Gdn2Grads<T> gr,
+                                                    const T* __restrict__ v, const T* __restrict__ w,
+                                                    T* __restrict__ dw, T* __restrict__ dv) {
+  constexpr int KH = 64;
+  static_assert(K == V && K % KH == 0, "K and V are sliced alike");
+  typedef WyBLds<T, C, KH> L;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
+  T* sA = reinterpret_cast<T*>(lds + L::off_a);
+  T* sDW = reinterpret_cast<T*>(lds + L::off_dw);
+  T* sDV = reinterpret_cast<T*>(lds + L::off_dv);
+  T* sV = reinterpret_cast<T*>(lds + L::off_v);
+  T* sW = reinterpret_cast<T*>(lds + L::off_w);
+
+  constexpr int NKS = K / KH;
+  int bhn, ks;
+  xcd_group_map(blockIdx.x, dm.B * dm.H * dm.NT, NKS, bhn, ks);
+  const int c0 = ks * KH;
+  const int n = bhn % dm.NT;
+  const int bh = bhn / dm.NT;
+  const int h = bh % dm.H, bb = bh / dm.H;
+  const int wv_id = wave_id();
+  const size_t blk = (size_t)bhn;
+  const size_t rsV = (size_t)dm.H * V;
+  const size_t t0 = (size_t)bb * dm.T + (size_t)n * C;
+  const size_t vb = (t0 * dm.H + h) * V + c0;
+
+  stage_rows<T, C, C>(sA, L::LC, ck.ainv + blk * C * C, C);
+  stage_rows<T, C, KH>(sDW, L::LH, gr.dwt + blk * C * K + c0, K);
+  stage_rows<T, C, KH>(sDV, L::LH, gr.dvn + blk * C * V + c0, V);
+  stage_rows<T, C, KH>(sV, L::LH, v + vb, rsV);
+  stage_rows<T, C, KH>(sW, L::LH, w + vb, rsV);
+  __syncthreads();
+
+  constexpr int MT = C / 16, NT2 = KH / 16, TPW = MT * NT2 / 4;
+  float* g_dkb = gr.dkb + blk * C * K + c0;
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int tile = wv_id * TPW + t, mj = tile % MT, ni = tile / MT;
+    const int k0 = tri_k0<T>(mj);  // A lower triangular: rows i >= j only
+    f32x4 a = tile_mma<T, true, true>(zero4(), sA + k0 * L::LC, L::LC, sDW + k0 * L::LH, L::LH,
+                                      16 * mj, 16 * ni, C - k0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = n2n(a[i]);
+    store_tile_n(g_dkb, K, 16 * mj, 16 * ni, a);
+    const f32x4 d = tile_mma<T, true, true>(zero4(), sA + k0 * L::LC, L::LC, sDV + k0 * L::LH, L::LH,
+                                            16 * mj, 16 * ni, C - k0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * mj + tile_row(i), c = 16 * ni + tile_col();
+      const float gw = sanitize(n2n(d[i] * to_f(sV[r * L::LH + c])));
+      const float gv = sanitize(n2n(d[i] * to_f(sW[r * L::LH + c])));
+      dw[vb + (size_t)r * rsV + c] = from_f<T>(gw);
+      dv[vb + (size_t)r * rsV + c] = from_f<T>(gv);
+    }
   }
 }
 
