@@ -202,13 +202,17 @@ struct RegStage {
   static constexpr int PER_ROW = D / VEC;
   static constexpr int N = R * PER_ROW;
   static constexpr int PT = (N + 255) / 256;
-  uint4 r[PT];
+  // one SSA vector (not an array) so the staging stays in registers
+  typedef uint32_t vec_t __attribute__((ext_vector_type(4 * PT)));
+  vec_t r;
   __device__ __forceinline__ void load(const T* src, size_t ld) {
 #pragma unroll
     for (int i = 0; i < PT; ++i) {
       const int e = threadIdx.x + 256 * i;
-      if (N % 256 == 0 || e < N)
-        r[i] = *reinterpret_cast<const uint4*>(src + (size_t)(e / PER_ROW) * ld + (e % PER_ROW) * VEC);
+      if (N % 256 == 0 || e < N) {
+        const uint4 x = *reinterpret_cast<const uint4*>(src + (size_t)(e / PER_ROW) * ld + (e % PER_ROW) * VEC);
+        r[4 * i] = x.x; r[4 * i + 1] = x.y; r[4 * i + 2] = x.z; r[4 * i + 3] = x.w;
+      }
     }
   }
   __device__ __forceinline__ void store(T* dst, int ld) const {
@@ -216,8 +220,13 @@ struct RegStage {
     for (int i = 0; i < PT; ++i) {
       const int e = threadIdx.x + 256 * i;
       if (N % 256 == 0 || e < N)
-        *reinterpret_cast<uint4*>(dst + (e / PER_ROW) * ld + (e % PER_ROW) * VEC) = r[i];
+        *reinterpret_cast<uint4*>(dst + (e / PER_ROW) * ld + (e % PER_ROW) * VEC) =
+            make_uint4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
     }
+  }
+  // the i-th 16-byte piece, as loaded
+  __device__ __forceinline__ uint4 piece(int i) const {
+    return make_uint4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
   }
 };
 

@@ -53,7 +53,7 @@ struct DhLds {
 };
 
 template <typename T, typename TD, int C, int K, int V, int VT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gdn2_bwd_dh(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn2_bwd_dh(
     Gdn2Dims dm, Gdn2Chunks<T> ck, Gdn2Grads<T> gr, const TD* __restrict__ dO,
     const float* __restrict__ dh_final, float* __restrict__ dh0) {
   typedef DhLds<T, C, K, V, VT> L;

@@ -388,7 +388,7 @@ struct StateLds {
 };
 
 template <typename T, int C, int K, int V, int VT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T> ck,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T> ck,
                                                      const float* __restrict__ h0, float* __restrict__ o,
                                                      float* __restrict__ h_final, int save) {
   typedef StateLds<T, C, K, V, VT> L;

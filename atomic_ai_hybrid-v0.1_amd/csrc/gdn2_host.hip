@@ -79,7 +79,7 @@ template <typename T, int K>
 static int gdn2_forward_impl(const Gdn2Plan& p, const void* q, const void* k, const void* v,
                              const void* w, const void* b, const float* g, const float* h0,
                              float* o, float* h_final, void* ws, int save, Launch& L) {
-  constexpr int C = 64, V = K, VT = 32;
+  constexpr int C = 64, V = K, VT = 16;
   Gdn2Chunks<T> ck = gdn2_chunks<T>(p, ws);
   hipStream_t st = L.st;
   int rc = L("gdn2_fwd_intra", [&] {
@@ -116,7 +116,7 @@ static int gdn2_backward_impl(const Gdn2Plan& p, const void* q, const void* k, c
                               const void* dO, const float* dh_final, void* dq, void* dk, void* dv,
                               void* dw, void* db, float* dg, float* dh0, void* ws, bool reuse,
                               Launch& L) {
-  constexpr int C = 64, V = K, VT = 32;
+  constexpr int C = 64, V = K, VT = 16;
   Gdn2Chunks<T> ck = gdn2_chunks<T>(p, ws);
   Gdn2Grads<T> gr = gdn2_grads<T>(p, ws);
   int rc;
