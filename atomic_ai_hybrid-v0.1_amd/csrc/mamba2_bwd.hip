@@ -274,33 +274,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           f32x4 ro[YNI], rd[YNI], so[YNI], sd[YNI];
 #pragma unroll
           for (int ni = 0; ni < YNI; ++ni) { ro[ni] = zero4(); so[ni] = zero4(); }
-          for (int J = 0; J < I; ++J) {  // sources below the block
-            const frag a = cb_frag<T>(cbg, C, 16 * I, 16 * J, 0);
+          // every CB fragment of the block row, issued together: CB(I, J) for
+          // J < I (row side), CB^T(I, J) for J > I (column side), the diagonal
+          frag fa[NB];
 #pragma unroll
-            for (int ni = 0; ni < YNI; ++ni) {
-              f32x4 q = Mma<T>::mma(a, Mma<T>::ld_t(sVd, L::LPT, 16 * ni, 16 * J), zero4());
-              q = Mma<T>::mma(a, Mma<T>::ld_t(sVdl, L::LPT, 16 * ni, 16 * J), q);
-              const int pc = 16 * ni + tile_col();
-              const float mf = __expf(sCum[16 * I * L::LC + pc] - sCum[(16 * J + 15) * L::LC + pc]);
+          for (int J = 0; J < NB; ++J)
+            if (J != I) fa[J] = cb_frag<T>(J < I ? cbg : cbtg, C, 16 * I, 16 * J, 0);
+          const frag ar = cb_frag<T>(cbg, C, 16 * I, 16 * I, 1);
+          const frag as = cb_frag<T>(cbtg, C, 16 * I, 16 * I, 2);
 #pragma unroll
-              for (int k = 0; k < 4; ++k) ro[ni][k] += mf * q[k];
-            }
-          }
-          for (int I2 = I + 1; I2 < NB; ++I2) {  // targets above the block (column side)
-            const frag a = cb_frag<T>(cbtg, C, 16 * I, 16 * I2, 0);
+          for (int J = 0; J < NB; ++J) {
+            if (J < I) {  // sources below the block
 #pragma unroll
-            for (int ni = 0; ni < YNI; ++ni) {
-              f32x4 q = Mma<T>::mma(a, Mma<T>::ld_t(sYu, L::LPT, 16 * ni, 16 * I2), zero4());
-              q = Mma<T>::mma(a, Mma<T>::ld_t(sYul, L::LPT, 16 * ni, 16 * I2), q);
-              const int pc = 16 * ni + tile_col();
-              const float mf = __expf(sCum[16 * I2 * L::LC + pc] - sCum[(16 * I + 15) * L::LC + pc]);
+              for (int ni = 0; ni < YNI; ++ni) {
+                f32x4 q = Mma<T>::mma(fa[J], Mma<T>::ld_t(sVd, L::LPT, 16 * ni, 16 * J), zero4());
+                q = Mma<T>::mma(fa[J], Mma<T>::ld_t(sVdl, L::LPT, 16 * ni, 16 * J), q);
+                const int pc = 16 * ni + tile_col();
+                const float mf = __expf(sCum[16 * I * L::LC + pc] - sCum[(16 * J + 15) * L::LC + pc]);
 #pragma unroll
-              for (int k = 0; k < 4; ++k) so[ni][k] += mf * q[k];
+                for (int k = 0; k < 4; ++k) ro[ni][k] += mf * q[k];
+              }
+            } else if (J > I) {  // targets above the block (column side)
+#pragma unroll
+              for (int ni = 0; ni < YNI; ++ni) {
+                f32x4 q = Mma<T>::mma(fa[J], Mma<T>::ld_t(sYu, L::LPT, 16 * ni, 16 * J), zero4());
+                q = Mma<T>::mma(fa[J], Mma<T>::ld_t(sYul, L::LPT, 16 * ni, 16 * J), q);
+                const int pc = 16 * ni + tile_col();
+                const float mf = __expf(sCum[16 * J * L::LC + pc] - sCum[(16 * I + 15) * L::LC + pc]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) so[ni][k] += mf * q[k];
+              }
             }
           }
           {  // the diagonal block
-            const frag ar = cb_frag<T>(cbg, C, 16 * I, 16 * I, 1);
-            const frag as = cb_frag<T>(cbtg, C, 16 * I, 16 * I, 2);
 #pragma unroll
             for (int ni = 0; ni < YNI; ++ni) {
               rd[ni] = Mma<T>::mma(ar, Mma<T>::ld_t(sVd, L::LPT, 16 * ni, 16 * I), zero4());

@@ -399,18 +399,25 @@ __global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __
 #pragma unroll
     for (int ni = 0; ni < YNI; ++ni) { off[ni] = zero4(); dg[ni] = zero4(); yo[ni] = zero4(); }
     if (!exact) {
-      for (int J = 0; J < I; ++J) {
-        const typename Mma<T>::frag a = cb_frag<T>(cbg, C, 16 * I, 16 * J, 0);
+      // the CB fragments of the block row, issued together
+      typename Mma<T>::frag fa[NB];
 #pragma unroll
-        for (int ni = 0; ni < YNI; ++ni) {
-          const f32x4 q = Mma<T>::mma(a, Mma<T>::ld_t(sV, L::LPT, 16 * ni, 16 * J), zero4());
-          const int pc = 16 * ni + tile_col();
-          const float mf = __expf(sCum[16 * I * L::LC + pc] - sCum[(16 * J + 15) * L::LC + pc]);
+      for (int J = 0; J < NB; ++J)
+        if (J < I) fa[J] = cb_frag<T>(cbg, C, 16 * I, 16 * J, 0);
+      const typename Mma<T>::frag ad = cb_frag<T>(cbg, C, 16 * I, 16 * I, 1);
 #pragma unroll
-          for (int k = 0; k < 4; ++k) off[ni][k] += mf * q[k];
+      for (int J = 0; J < NB; ++J) {
+        if (J < I) {
+#pragma unroll
+          for (int ni = 0; ni < YNI; ++ni) {
+            const f32x4 q = Mma<T>::mma(fa[J], Mma<T>::ld_t(sV, L::LPT, 16 * ni, 16 * J), zero4());
+            const int pc = 16 * ni + tile_col();
+            const float mf = __expf(sCum[16 * I * L::LC + pc] - sCum[(16 * J + 15) * L::LC + pc]);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) off[ni][k] += mf * q[k];
+          }
         }
       }
-      const typename Mma<T>::frag ad = cb_frag<T>(cbg, C, 16 * I, 16 * I, 1);
 #pragma unroll
       for (int ni = 0; ni < YNI; ++ni)
         dg[ni] = Mma<T>::mma(ad, Mma<T>::ld_t(sV, L::LPT, 16 * ni, 16 * I), zero4());
