@@ -181,28 +181,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // ------------------------------------------------------------------ B2/B3 state terms
-template <typename T, int C, int K, int V>
+// One workgroup per (batch, head, chunk).  dO, dv_new and v_new stay in LDS;
+// h_pre and dh_next pass through in KQ-column quarters (the next quarter is
+// loaded into registers while the current one computes), which keeps the LDS
+// at two workgroups per CU.
+template <typename T, int C, int KQ, int V>
 struct HgLds {
   static constexpr int PAD = Pad<T>::v;
-  static constexpr int LK = K + PAD, LV = V + PAD, LC = C + PAD;
+  static constexpr int LK = KQ + PAD, LV = V + PAD, LC = C + PAD;
   static constexpr int off_do = 0;
   static constexpr int off_dv = off_do + C * LV * (int)sizeof(T);
-  static constexpr int off_h = off_dv + C * LV * (int)sizeof(T);
+  static constexpr int off_vn = off_dv + C * LV * (int)sizeof(T);
+  static constexpr int off_h = off_vn + V * LC * (int)sizeof(T);
   static constexpr int off_dh = off_h + V * LK * (int)sizeof(T);
-  static constexpr int off_vn = off_dh + V * LK * (int)sizeof(T);
-  static constexpr int total = off_vn + V * LC * (int)sizeof(T);
+  static constexpr int off_red = off_dh + V * LK * (int)sizeof(T);
+  static constexpr int total = off_red + 256 * 4;
 };
 
 template <typename T, typename TD, int C, int K, int V>
 __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T> ck, Gdn2Grads<T> gr,
                                                      const TD* __restrict__ dO) {
-  typedef HgLds<T, C, K, V> L;
+  constexpr int KQ = 32;
+  typedef HgLds<T, C, KQ, V> L;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
   T* sDO = reinterpret_cast<T*>(lds + L::off_do);
   T* sDV = reinterpret_cast<T*>(lds + L::off_dv);
+  T* sVn = reinterpret_cast<T*>(lds + L::off_vn);
   T* sH = reinterpret_cast<T*>(lds + L::off_h);
   T* sDh = reinterpret_cast<T*>(lds + L::off_dh);
-  T* sVn = reinterpret_cast<T*>(lds + L::off_vn);
+  float* red = reinterpret_cast<float*>(lds + L::off_red);
 
   const int bhn = blockIdx.x;
   const int n = bhn % dm.NT;
@@ -210,33 +217,21 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
   const int h = bh % dm.H, bb = bh / dm.H;
   const int wv_id = wave_id();
   const size_t blk = (size_t)bhn;
+  const T* hg = ck.hT + blk * V * K;
+  const T* dhg = gr.dhT + blk * V * K;
 
+  RegStage<T, V, KQ> ph, pdh;
+  ph.load(hg, K);
+  pdh.load(dhg, K);
   stage_convert<TD, T, C, V>(sDO, L::LV, dO + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V,
                              (size_t)dm.H * V);
   stage_rows<T, C, V>(sDV, L::LV, gr.dvn + blk * C * V, V);
-  stage_rows<T, V, K>(sH, L::LK, ck.hT + blk * V * K, K);
-  stage_rows<T, V, K>(sDh, L::LK, gr.dhT + blk * V * K, K);
   stage_rows<T, V, C>(sVn, L::LC, ck.vnT + blk * V * C, C);
+  ph.store(sH, L::LK);
+  pdh.store(sDh, L::LK);
   __syncthreads();
 
-  // dqg = scale dO h_pre^T ; dwt = -dv_new h_pre^T ; dkg = v_new dh_next^T
-  constexpr int MT = C / 16, NTK = K / 16;
-  constexpr int TPW = MT * NTK / 4;
-  float* g_dqg = gr.dqg + blk * C * K;
-  T* g_dwt = gr.dwt + blk * C * K;
-  float* g_dkg = gr.dkg + blk * C * K;
-#pragma unroll 2
-  for (int t = 0; t < TPW; ++t) {
-    const int tile = wv_id * TPW + t, mi = tile % MT, ni = tile / MT;
-    f32x4 a = tile_mma<T, false, true>(zero4(), sDO, L::LV, sH, L::LK, 16 * mi, 16 * ni, V);
-    f32x4 b = tile_mma<T, false, true>(zero4(), sDV, L::LV, sH, L::LK, 16 * mi, 16 * ni, V);
-    f32x4 c = tile_mma<T, true, true>(zero4(), sVn, L::LC, sDh, L::LK, 16 * mi, 16 * ni, V);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { a[i] *= dm.scale; b[i] = -b[i]; }
-    store_tile_n(g_dqg, K, 16 * mi, 16 * ni, a);
-    store_tile_n(g_dwt, K, 16 * mi, 16 * ni, b);
-    store_tile_n(g_dkg, K, 16 * mi, 16 * ni, c);
-  }
+  constexpr int MT = C / 16;
   // dAqk = n2n((dO v_new^T) * causal)   (kernel_bwd_b2_dav.py:69,72)
   T* g_daqk = gr.daqk + blk * C * C;
   for (int tile = wv_id; tile < MT * MT; tile += 4) {
@@ -250,27 +245,56 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
     }
     store_tile_n(g_daqk, C, 16 * mi, 16 * nj, acc);
   }
-  // exp(gc_last) * sum_v dh_next * h_pre   (kernel_bwd_b3_wy_dqkg.py:200-201):
-  // 256 / K threads per column, each over a V / (256 / K) slice
-  {
-    constexpr int SPL = 256 / K, VS = V / SPL;
-    const int d = threadIdx.x % K, sp = threadIdx.x / K;
-    float s0 = 0.f, s1 = 0.f;
-#pragma unroll 8
-    for (int v = sp * VS; v < sp * VS + VS; v += 2) {
-      s0 += to_f(sDh[v * L::LK + d]) * to_f(sH[v * L::LK + d]);
-      s1 += to_f(sDh[(v + 1) * L::LK + d]) * to_f(sH[(v + 1) * L::LK + d]);
+
+  // dqg = scale dO h_pre^T ; dwt = -dv_new h_pre^T ; dkg = v_new dh_next^T, per quarter
+  constexpr int NTQ = KQ / 16, TPW = MT * NTQ / 4;
+  static_assert((MT * NTQ) % 4 == 0, "tiles must split evenly over 4 waves");
+  constexpr int SPL = 256 / KQ, VS = V / SPL;  // gc_last row term: threads per column, rows each
+  static_assert(VS % 2 == 0, "pairs of rows per thread");
+  for (int c0 = 0; c0 < K; c0 += KQ) {
+    if (c0 + KQ < K) {
+      ph.load(hg + c0 + KQ, K);
+      pdh.load(dhg + c0 + KQ, K);
     }
-    __syncthreads();  // the dAqk tiles are done with sDO: reuse it as scratch
-    float* red = reinterpret_cast<float*>(sDO);
-    red[threadIdx.x] = s0 + s1;
-    __syncthreads();
-    if (threadIdx.x < K) {
+    float* g_dqg = gr.dqg + blk * C * K + c0;
+    T* g_dwt = gr.dwt + blk * C * K + c0;
+    float* g_dkg = gr.dkg + blk * C * K + c0;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int tile = wv_id * TPW + t, mi = tile % MT, ni = tile / MT;
+      f32x4 a = tile_mma<T, false, true>(zero4(), sDO, L::LV, sH, L::LK, 16 * mi, 16 * ni, V);
+      f32x4 b = tile_mma<T, false, true>(zero4(), sDV, L::LV, sH, L::LK, 16 * mi, 16 * ni, V);
+      f32x4 c = tile_mma<T, true, true>(zero4(), sVn, L::LC, sDh, L::LK, 16 * mi, 16 * ni, V);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { a[i] *= dm.scale; b[i] = -b[i]; }
+      store_tile_n(g_dqg, K, 16 * mi, 16 * ni, a);
+      store_tile_n(g_dwt, K, 16 * mi, 16 * ni, b);
+      store_tile_n(g_dkg, K, 16 * mi, 16 * ni, c);
+    }
+    // exp(gc_last) * sum_v dh_next * h_pre   (kernel_bwd_b3_wy_dqkg.py:200-201)
+    {
+      const int d = threadIdx.x % KQ, sp = threadIdx.x / KQ;
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int v = sp * VS; v < sp * VS + VS; v += 2) {
+        s0 += to_f(sDh[v * L::LK + d]) * to_f(sH[v * L::LK + d]);
+        s1 += to_f(sDh[(v + 1) * L::LK + d]) * to_f(sH[(v + 1) * L::LK + d]);
+      }
+      red[threadIdx.x] = s0 + s1;
+    }
+    __syncthreads();  // quarter done: its h / dh and the partial sums are read
+    if (threadIdx.x < KQ) {
+      const int d = threadIdx.x;
       float s = 0.f;
 #pragma unroll
-      for (int j = 0; j < SPL; ++j) s += red[j * K + d];
-      gr.rlast[blk * K + d] = __expf(ck.gcl[blk * K + d]) * s;
+      for (int j = 0; j < SPL; ++j) s += red[j * KQ + d];
+      gr.rlast[blk * K + c0 + d] = __expf(ck.gcl[blk * K + c0 + d]) * s;
     }
+    if (c0 + KQ < K) {
+      ph.store(sH, L::LK);
+      pdh.store(sDh, L::LK);
+    }
+    __syncthreads();
   }
 }
 
