@@ -31,10 +31,10 @@ template <typename T>
 struct Gdn2Grads {
   T* dvn;       // [C][V]  dv_new (B1 output; an MFMA operand downstream)
   T* dhT;       // [V][K]  dh carried into the chunk from the next one, transposed
-  float* dqg;   // [C][K]  scale dO h_pre^T
+  T* dqg;       // [C][K]  scale dO h_pre^T
   T* dwt;       // [C][K]  -dv_new h_pre^T (an MFMA operand of the WY step)
-  float* dkb;   // [C][K]  A^T dwt
-  float* dkg;   // [C][K]  v_new dh_next^T
+  T* dkb;       // [C][K]  A^T dwt
+  T* dkg;       // [C][K]  v_new dh_next^T
   T* daqk;      // [C][C]  scale (dO v_new^T) * causal
   T* dakk;      // [C][C]  -A^T (dA A^T) * strict
   float* rlast; // [K]     exp(gc_last) * sum_v dh_next * h_pre

@@ -256,9 +256,9 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
       ph.load(hg + c0 + KQ, K);
       pdh.load(dhg + c0 + KQ, K);
     }
-    float* g_dqg = gr.dqg + blk * C * K + c0;
+    T* g_dqg = gr.dqg + blk * C * K + c0;
     T* g_dwt = gr.dwt + blk * C * K + c0;
-    float* g_dkg = gr.dkg + blk * C * K + c0;
+    T* g_dkg = gr.dkg + blk * C * K + c0;
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       const int tile = wv_id * TPW + t, mi = tile % MT, ni = tile / MT;
@@ -475,7 +475,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy_b(Gdn2Dims dm, Gdn2Chunks<T> 
   __syncthreads();
 
   constexpr int MT = C / 16, NT2 = KH / 16, TPW = MT * NT2 / 4;
-  float* g_dkb = gr.dkb + blk * C * K + c0;
+  T* g_dkb = gr.dkb + blk * C * K + c0;
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
     const int tile = wv_id * TPW + t, mj = tile % MT, ni = tile / MT;
@@ -613,9 +613,9 @@ __global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> 
   stage_rows<T, C, KH>(sKB, L::LK, b + base, rsK);
   __syncthreads();
 
-  const float* g_dqg = gr.dqg + blk * C * K + d0;
-  const float* g_dkb = gr.dkb + blk * C * K + d0;
-  const float* g_dkg = gr.dkg + blk * C * K + d0;
+  const T* g_dqg = gr.dqg + blk * C * K + d0;
+  const T* g_dkb = gr.dkb + blk * C * K + d0;
+  const T* g_dkg = gr.dkg + blk * C * K + d0;
   float colsum[TPW / MT];
   f32x4 dgcr[TPW];  // written to LDS only after every lane has read gc
 #pragma unroll
@@ -670,7 +670,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> 
       dq4 = sanitize(dq4); dk4 = sanitize(dk4); db4 = sanitize(db4); dgc4 = sanitize(dgc4);
       // B3 element-wise terms (kernel_bwd_b3_wy_dqkg.py:182-198)
       const size_t o = (size_t)r * K + d;
-      const float dqg = g_dqg[o], dkb = g_dkb[o], dkg = g_dkg[o];
+      const float dqg = to_f(g_dqg[o]), dkb = to_f(g_dkb[o]), dkg = to_f(g_dkg[o]);
       const float kgv = kv * eg;
       const float dq3 = n2n(dqg * e);
       const float dk3 = n2n(dkb * e * bv + dkg * eg);

@@ -48,10 +48,10 @@ static int gdn2_plan(const atomic_gdn2_args* a, Gdn2Plan* p) {
   p->fwd_end = off;
   p->o_dvn = take(N * C * V * es);
   p->o_dht = take(N * V * K * es);
-  p->o_dqg = take(N * C * K * 4);
+  p->o_dqg = take(N * C * K * es);
   p->o_dwt = take(N * C * K * es);
-  p->o_dkb = take(N * C * K * 4);
-  p->o_dkg = take(N * C * K * 4);
+  p->o_dkb = take(N * C * K * es);
+  p->o_dkg = take(N * C * K * es);
   p->o_daqk = take(N * C * C * es);
   p->o_dakk = take(N * C * C * es);
   p->o_rlast = take(N * K * 4);
@@ -100,10 +100,10 @@ static Gdn2Grads<T> gdn2_grads(const Gdn2Plan& p, void* ws) {
   Gdn2Grads<T> g;
   g.dvn = reinterpret_cast<T*>(base + p.o_dvn);
   g.dhT = reinterpret_cast<T*>(base + p.o_dht);
-  g.dqg = reinterpret_cast<float*>(base + p.o_dqg);
+  g.dqg = reinterpret_cast<T*>(base + p.o_dqg);
   g.dwt = reinterpret_cast<T*>(base + p.o_dwt);
-  g.dkb = reinterpret_cast<float*>(base + p.o_dkb);
-  g.dkg = reinterpret_cast<float*>(base + p.o_dkg);
+  g.dkb = reinterpret_cast<T*>(base + p.o_dkb);
+  g.dkg = reinterpret_cast<T*>(base + p.o_dkg);
   g.daqk = reinterpret_cast<T*>(base + p.o_daqk);
   g.dakk = reinterpret_cast<T*>(base + p.o_dakk);
   g.rlast = reinterpret_cast<float*>(base + p.o_rlast);
