@@ -504,23 +504,26 @@ struct InLds {
   static constexpr int PAD = Pad<T>::v;
   static constexpr int LK = K + PAD, LC = C + PAD, LG = K + 4;
   static constexpr int OK_ = C * LK * (int)sizeof(T), OC = C * LC * (int)sizeof(T);
-  static constexpr int off_q = 0;            // q e^{gc}  (then raw q)
-  static constexpr int off_kt = off_q + OK_; // k e^{-gc} (then raw k)
-  static constexpr int off_kb = off_kt + OK_;// b k e^{gc} (then raw b)
+  static constexpr int off_gc = 0;           // fp32 gc, then fp32 dgc
+  static constexpr int off_q = off_gc + C * LG * 4;  // q e^{gc}  (exact path: then raw q)
+  static constexpr int off_kt = off_q + OK_; // k e^{-gc} (exact path: then raw k)
+  static constexpr int off_kb = off_kt + OK_;// b k e^{gc} (exact path: then raw b)
   static constexpr int off_daqk = off_kb + OK_;
   static constexpr int off_dakk = off_daqk + OC;
-  static constexpr int off_gc = off_dakk + OC;   // fp32 gc, then fp32 dgc
-  static constexpr int off_tot = off_gc + C * LG * 4;
+  static constexpr int off_tot = off_dakk + OC;
   static constexpr int off_gl = off_tot + ColMap<C, K>::NSEG * K * 4;
   static constexpr int off_part = off_gl + K * 4;  // [4][K] column partial sums
   static constexpr int total = off_part + 4 * K * 4;
+  // factorised path, after the MFMAs: dQ~, dK~, dKB as fp32 [C][LG] from off_q
+  static constexpr int off_res = off_q;
+  static_assert(off_res + 3 * C * LG * 4 <= off_gl, "the MFMA results must fit before gc_last");
 };
 
 // One workgroup per (batch, head, chunk, KH-column slice): every term of B4,
 // B3's element-wise part and B5 is separable over the K columns (only the
 // [C][C] dAqk / dAkk are shared by the slices).
 template <typename T, int C, int K, int V, int KH>
-__global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> gr,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> gr,
                                                      const T* __restrict__ q, const T* __restrict__ k,
                                                      const T* __restrict__ b, const float* __restrict__ g,
                                                      T* __restrict__ dq, T* __restrict__ dk,
@@ -607,105 +610,167 @@ __global__ __launch_bounds__(256) void gdn2_bwd_intra(Gdn2Dims dm, Gdn2Grads<T> 
     }
   }
   __syncthreads();
-  // raw q, k, b for the element-wise stage (fp32 exact multipliers)
-  stage_rows<T, C, KH>(sQ, L::LK, q + base, rsK);
-  stage_rows<T, C, KH>(sKt, L::LK, k + base, rsK);
-  stage_rows<T, C, KH>(sKB, L::LK, b + base, rsK);
-  __syncthreads();
-
   const T* g_dqg = gr.dqg + blk * C * K + d0;
   const T* g_dkb = gr.dkb + blk * C * K + d0;
   const T* g_dkg = gr.dkg + blk * C * K + d0;
-  float colsum[TPW / MT];
-  f32x4 dgcr[TPW];  // written to LDS only after every lane has read gc
+  if (!exact) {
+    // ---- factorised path: the MFMA results go through LDS so the
+    // element-wise stage runs in the row-contiguous layout (16-byte I/O)
+    float* sRes = reinterpret_cast<float*>(lds + L::off_res);
+    constexpr int RS3 = C * L::LG;
 #pragma unroll
-  for (int c = 0; c < TPW / MT; ++c) colsum[c] = 0.f;
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    const int tile = wv_id * TPW + t, mi = tile % MT, ni = tile / MT;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 16 * mi + tile_row(i), d = 16 * ni + tile_col();
-      const float gcv = sGc[r * L::LG + d];
-      const float e = __expf(gcv), ei = __expf(-gcv), eg = __expf(sGl[d] - gcv);
-      const float qv = to_f(sQ[r * L::LK + d]), kv = to_f(sKt[r * L::LK + d]),
-                  bv = to_f(sKB[r * L::LK + d]);
-      // B4 (kernel_bwd_b4_intra.py:101-132)
-      float dq4, dk4, db4, dgc4;
-      if (!exact) {
-        dq4 = dQt[t][i] * e;
-        dk4 = dKt[t][i] * ei + dKB[t][i] * bv * e;
-        db4 = dKB[t][i] * kv * e;
-        dgc4 = dQt[t][i] * (qv * e) - dKt[t][i] * (kv * ei) + dKB[t][i] * (bv * kv * e);
-      } else {
-        // pairwise with exp(clip(gc_i - gc_j, -20, 20)) and the clip mask
-        float sq = 0.f, sb = 0.f, sk = 0.f, sgi = 0.f, sgj = 0.f;
-        for (int j = 0; j <= r; ++j) {
-          const float dd = gcv - sGc[j * L::LG + d];
-          const float E = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
-          const float msk = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
-          const float kj = to_f(sKt[j * L::LK + d]);
-          const float aq = to_f(sDAqk[r * L::LC + j]);  // holds scale * dAqk
-          const float ak = (j < r) ? to_f(sDAkk[r * L::LC + j]) : 0.f;
-          sq += aq * E * kj;
-          sb += ak * E * kj;
-          sgi += (aq * qv + ak * bv * kv) * E * kj * msk;
-        }
-        for (int i2 = r; i2 < C; ++i2) {
-          const float dd = sGc[i2 * L::LG + d] - gcv;
-          const float E = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
-          const float msk = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
-          const float aq = to_f(sDAqk[i2 * L::LC + r]);
-          const float ak = (i2 > r) ? to_f(sDAkk[i2 * L::LC + r]) : 0.f;
-          const float li = aq * to_f(sQ[i2 * L::LK + d]) +
-                           ak * to_f(sKB[i2 * L::LK + d]) * to_f(sKt[i2 * L::LK + d]);
-          sk += li * E;
-          sgj += li * E * kv * msk;
-        }
-        dq4 = sq;
-        dk4 = sk + sb * bv;
-        db4 = sb * kv;
-        dgc4 = sgi - sgj;
-      }
-      dq4 = sanitize(dq4); dk4 = sanitize(dk4); db4 = sanitize(db4); dgc4 = sanitize(dgc4);
-      // B3 element-wise terms (kernel_bwd_b3_wy_dqkg.py:182-198)
-      const size_t o = (size_t)r * K + d;
-      const float dqg = to_f(g_dqg[o]), dkb = to_f(g_dkb[o]), dkg = to_f(g_dkg[o]);
-      const float kgv = kv * eg;
-      const float dq3 = n2n(dqg * e);
-      const float dk3 = n2n(dkb * e * bv + dkg * eg);
-      const float db3 = n2n(dkb * e * kv);
-      const float dx = dkg * kgv;
-      const float dgc3 = dkb * (bv * kv * e) + dqg * (qv * e) - dx;
-      colsum[t / MT] += dx;
-      const size_t go = base + (size_t)r * rsK + d;
-      dq[go] = from_f<T>(sanitize(dq3 + dq4));
-      dk[go] = from_f<T>(sanitize(dk3 + dk4));
-      db[go] = from_f<T>(sanitize(db3 + db4));
-      dgcr[t][i] = dgc3 + dgc4;
+    for (int t = 0; t < TPW; ++t) {
+      const int tile = wv_id * TPW + t, mi = tile % MT, ni = tile / MT;
+      store_tile_n(sRes, L::LG, 16 * mi, 16 * ni, dQt[t]);
+      store_tile_n(sRes + RS3, L::LG, 16 * mi, 16 * ni, dKt[t]);
+      store_tile_n(sRes + 2 * RS3, L::LG, 16 * mi, 16 * ni, dKB[t]);
     }
-  }
-  __syncthreads();  // the exact path reads gc of other rows: finish all reads first
+    __syncthreads();
+    float csum[8];
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    const int tile = wv_id * TPW + t, mi = tile % MT, ni = tile / MT;
-    store_tile_n(sGc, L::LG, 16 * mi, 16 * ni, dgcr[t]);
-  }
-  // gc_last row terms: sum_i dkg * kg + exp(gc_last) sum_v dh_next h_pre   (b3:189,200-205)
+    for (int j = 0; j < 8; ++j) csum[j] = 0.f;
+#pragma unroll 1
+    for (int rr = 0; rr < M::RS; ++rr) {
+      const int r = seg * M::RS + rr;
+      const int c8 = cg * 8;
+      float qv[8], kv[8], bv[8], dqg[8], dkb[8], dkg[8], oq[8], ok[8], ob[8];
+      load8(q + base + (size_t)r * rsK + c8, qv);
+      load8(k + base + (size_t)r * rsK + c8, kv);
+      load8(b + base + (size_t)r * rsK + c8, bv);
+      load8(g_dqg + (size_t)r * K + c8, dqg);
+      load8(g_dkb + (size_t)r * K + c8, dkb);
+      load8(g_dkg + (size_t)r * K + c8, dkg);
 #pragma unroll
-  for (int c = 0; c < TPW / MT; ++c) {
-    const int ni = (wv_id * TPW) / MT + c;
-    sPart[(lane_id() >> 4) * KH + 16 * ni + tile_col()] = colsum[c];
+      for (int j = 0; j < 8; ++j) {
+        const int d = c8 + j;
+        const float gcv = sGc[r * L::LG + d];
+        const float e = __expf(gcv), ei = __expf(-gcv), eg = __expf(sGl[d] - gcv);
+        const float tq = sRes[r * L::LG + d], tk = sRes[RS3 + r * L::LG + d],
+                    tb = sRes[2 * RS3 + r * L::LG + d];
+        // B4 (kernel_bwd_b4_intra.py:101-132)
+        const float dq4 = sanitize(tq * e);
+        const float dk4 = sanitize(tk * ei + tb * bv[j] * e);
+        const float db4 = sanitize(tb * kv[j] * e);
+        const float dgc4 = sanitize(tq * (qv[j] * e) - tk * (kv[j] * ei) + tb * (bv[j] * kv[j] * e));
+        // B3 element-wise terms (kernel_bwd_b3_wy_dqkg.py:182-198)
+        const float kgv = kv[j] * eg;
+        const float dq3 = n2n(dqg[j] * e);
+        const float dk3 = n2n(dkb[j] * e * bv[j] + dkg[j] * eg);
+        const float db3 = n2n(dkb[j] * e * kv[j]);
+        const float dx = dkg[j] * kgv;
+        const float dgc3 = dkb[j] * (bv[j] * kv[j] * e) + dqg[j] * (qv[j] * e) - dx;
+        csum[j] += dx;
+        oq[j] = sanitize(dq3 + dq4);
+        ok[j] = sanitize(dk3 + dk4);
+        ob[j] = sanitize(db3 + db4);
+        sGc[r * L::LG + d] = dgc3 + dgc4;  // each element read (as gc) and written by this thread only
+      }
+      const size_t go = base + (size_t)r * rsK + c8;
+      store8(dq + go, oq);
+      store8(dk + go, ok);
+      store8(db + go, ob);
+    }
+    __syncthreads();  // the MFMA results are dead: column partial sums go to their space
+    float* sCol = sRes;  // [NSEG][KH]
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sCol[seg * KH + cg * 8 + j] = csum[j];
+    __syncthreads();
+    if (tid < KH) {
+      float extra = gr.rlast[blk * K + d0 + tid];
+      for (int sg = 0; sg < M::NSEG; ++sg) extra += sCol[sg * KH + tid];
+      sGc[(C - 1) * L::LG + tid] += extra;
+    }
+    __syncthreads();
+  } else {
+    // ---- exact path: raw q, k, b for the element-wise stage (fp32 exact multipliers)
+    stage_rows<T, C, KH>(sQ, L::LK, q + base, rsK);
+    stage_rows<T, C, KH>(sKt, L::LK, k + base, rsK);
+    stage_rows<T, C, KH>(sKB, L::LK, b + base, rsK);
+    __syncthreads();
+    // dgc is parked in this slice's dg rows (written by B5 below) until every
+    // lane has read gc; the loop is kept rolled, this path is the rare one
+    float* dgp = dg + base;
+    float colsum = 0.f;
+  #pragma unroll 1
+    for (int t = 0; t < TPW; ++t) {
+      const int tile = wv_id * TPW + t, mi = tile % MT, ni = tile / MT;
+  #pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * mi + tile_row(i), d = 16 * ni + tile_col();
+        const float gcv = sGc[r * L::LG + d];
+        const float e = __expf(gcv), ei = __expf(-gcv), eg = __expf(sGl[d] - gcv);
+        const float qv = to_f(sQ[r * L::LK + d]), kv = to_f(sKt[r * L::LK + d]),
+                    bv = to_f(sKB[r * L::LK + d]);
+        // B4 (kernel_bwd_b4_intra.py:101-132)
+        float dq4, dk4, db4, dgc4;
+        {
+          // pairwise with exp(clip(gc_i - gc_j, -20, 20)) and the clip mask
+          float sq = 0.f, sb = 0.f, sk = 0.f, sgi = 0.f, sgj = 0.f;
+          for (int j = 0; j <= r; ++j) {
+            const float dd = gcv - sGc[j * L::LG + d];
+            const float E = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
+            const float msk = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
+            const float kj = to_f(sKt[j * L::LK + d]);
+            const float aq = to_f(sDAqk[r * L::LC + j]);  // holds scale * dAqk
+            const float ak = (j < r) ? to_f(sDAkk[r * L::LC + j]) : 0.f;
+            sq += aq * E * kj;
+            sb += ak * E * kj;
+            sgi += (aq * qv + ak * bv * kv) * E * kj * msk;
+          }
+          for (int i2 = r; i2 < C; ++i2) {
+            const float dd = sGc[i2 * L::LG + d] - gcv;
+            const float E = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
+            const float msk = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
+            const float aq = to_f(sDAqk[i2 * L::LC + r]);
+            const float ak = (i2 > r) ? to_f(sDAkk[i2 * L::LC + r]) : 0.f;
+            const float li = aq * to_f(sQ[i2 * L::LK + d]) +
+                             ak * to_f(sKB[i2 * L::LK + d]) * to_f(sKt[i2 * L::LK + d]);
+            sk += li * E;
+            sgj += li * E * kv * msk;
+          }
+          dq4 = sq;
+          dk4 = sk + sb * bv;
+          db4 = sb * kv;
+          dgc4 = sgi - sgj;
+        }
+        dq4 = sanitize(dq4); dk4 = sanitize(dk4); db4 = sanitize(db4); dgc4 = sanitize(dgc4);
+        // B3 element-wise terms (kernel_bwd_b3_wy_dqkg.py:182-198)
+        const size_t o = (size_t)r * K + d;
+        const float dqg = to_f(g_dqg[o]), dkb = to_f(g_dkb[o]), dkg = to_f(g_dkg[o]);
+        const float kgv = kv * eg;
+        const float dq3 = n2n(dqg * e);
+        const float dk3 = n2n(dkb * e * bv + dkg * eg);
+        const float db3 = n2n(dkb * e * kv);
+        const float dx = dkg * kgv;
+        const float dgc3 = dkb * (bv * kv * e) + dqg * (qv * e) - dx;
+        colsum += dx;
+        const size_t go = base + (size_t)r * rsK + d;
+        dq[go] = from_f<T>(sanitize(dq3 + dq4));
+        dk[go] = from_f<T>(sanitize(dk3 + dk4));
+        db[go] = from_f<T>(sanitize(db3 + db4));
+        dgp[(size_t)r * rsK + d] = dgc3 + dgc4;
+      }
+      if ((t + 1) % MT == 0) {  // a tile column is complete: its partial sums go out
+        const int ni = tile / MT;
+        sPart[(lane_id() >> 4) * KH + 16 * ni + tile_col()] = colsum;
+        colsum = 0.f;
+      }
+    }
+    __syncthreads();  // every lane has read gc: the parked dgc replaces it
+    for (int e = tid; e < C * KH; e += 256) {
+      const int r = e / KH, d = e % KH;
+      sGc[r * L::LG + d] = dgp[(size_t)r * rsK + d];
+    }
+    __syncthreads();
+    if (tid < KH) {
+      const float extra = sPart[tid] + sPart[KH + tid] + sPart[2 * KH + tid] + sPart[3 * KH + tid] +
+                          gr.rlast[blk * K + d0 + tid];
+      // dgc3 gets the row term before its n2n in the reference; dgc4 is already
+      // sanitized, so the sum below matches dgc3 + dgc4 in unclipped regimes.
+      sGc[(C - 1) * L::LG + tid] += extra;
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  if (tid < KH) {
-    const float extra = sPart[tid] + sPart[KH + tid] + sPart[2 * KH + tid] + sPart[3 * KH + tid] +
-                        gr.rlast[blk * K + d0 + tid];
-    // dgc3 gets the row term before its n2n in the reference; dgc4 is already
-    // sanitized, so the sum below matches dgc3 + dgc4 in unclipped regimes.
-    sGc[(C - 1) * L::LG + tid] += extra;
-  }
-  __syncthreads();
   // B5: dg = sanitize(reverse cumsum over the chunk)   (kernel_bwd_b5_reverse_cumsum.py:17-24)
   // thread (column group, row segment): suffix sums within the segment, then
   // the totals of the later segments
