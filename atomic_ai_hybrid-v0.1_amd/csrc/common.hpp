@@ -152,6 +152,14 @@ __device__ __forceinline__ int opaque_zero() {
   return z;
 }
 
+// The same pointer, opaque to the compiler: per-lane addresses built from it
+// stay inside the loop that calls this instead of being hoisted (and kept live).
+template <typename P>
+__device__ __forceinline__ P* opaque_ptr(P* p) {
+  asm volatile("" : "+s"(p));
+  return p;
+}
+
 __device__ __forceinline__ f32x4 zero4() { f32x4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
 
 // Tile element coordinates held by this lane: rows m0 + 4g + i, column n0 + r.
@@ -230,12 +238,13 @@ struct RegStage {
   }
 };
 
-// Copy a [R][D] block (row stride `src_ld`) into LDS rows of length `dst_ld`.
-template <typename T, int R, int D>
+// Copy a [R][D] block (row stride `src_ld`) into LDS rows of length `dst_ld`
+// (NTH threads in the workgroup).
+template <typename T, int R, int D, int NTH = 256>
 __device__ __forceinline__ void stage_rows(T* dst, int dst_ld, const T* src, size_t src_ld) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int PER_ROW = D / VEC;
-  for (int e = threadIdx.x; e < R * PER_ROW; e += 256) {
+  for (int e = threadIdx.x; e < R * PER_ROW; e += NTH) {
     const int r = e / PER_ROW, c = (e % PER_ROW) * VEC;
     *reinterpret_cast<uint4*>(dst + r * dst_ld + c) =
         *reinterpret_cast<const uint4*>(src + r * src_ld + c);

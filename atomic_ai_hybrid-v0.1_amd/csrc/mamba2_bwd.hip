@@ -51,12 +51,13 @@ struct Mamba2Grads {
 // A slice with a positive step exponent or a block range above kMaxRange is
 // evaluated pairwise with the reference's clips and masks instead.
 
-template <typename T, int C, int N, int PT>
+template <typename T, int C, int N, int PT, int NTH>
 struct CkLds {
   static constexpr int PAD = Pad<T>::v;
   static constexpr int LN = N + PAD, LPT = PT + PAD;
   static constexpr int LC = PT + 1;  // fp32 [C][PT] rows, padded against bank conflicts
-  static constexpr int NSEG = 256 / PT;
+  static constexpr int NW = NTH / 64;
+  static constexpr int NSEG = NTH / PT;
   static constexpr int OPT = C * LPT * (int)sizeof(T);
   static constexpr int OPR = (C + 16) * LPT * (int)sizeof(T);  // MFMA operand + 16 zero rows
   static constexpr int off_st = 0;
@@ -72,18 +73,20 @@ struct CkLds {
   static constexpr int off_red = off_cum + C * LC * 4;    // fp32 d_cum
   static constexpr int off_ddt1 = off_red + C * LC * 4;   // fp32 ddt_1
   static constexpr int off_tot = off_ddt1 + C * LC * 4;
-  static constexpr int off_misc = off_tot + NSEG * PT * 4;   // lasta[PT], lastb[4][PT], dA[8]
-  static constexpr int total = off_misc + (PT + 4 * PT + 8) * 4;
+  static constexpr int off_misc = off_tot + NSEG * PT * 4;   // lasta[PT], lastb[NW][PT], dA[1 + NW]
+  static constexpr int total = off_misc + (PT + NW * PT + 1 + NW) * 4;
 };
 
+// 512 threads: eight waves, two per SIMD, so one wave's LDS / global / MFMA
+// latency overlaps the other's work; wave w owns one 16-row block.
 template <typename T, typename TD, int C, int P, int N>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void mamba2_bwd_chunk(
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void mamba2_bwd_chunk(
     Mamba2Dims dm, int G, const T* __restrict__ dt, const T* __restrict__ x,
     const float* __restrict__ A, const T* __restrict__ Bm, const T* __restrict__ Cm,
     const TD* __restrict__ dy, Mamba2Chunks<T> ck, Mamba2Grads<T> gr, T* __restrict__ ddt,
     T* __restrict__ dx) {
-  constexpr int PT = 32;
-  typedef CkLds<T, C, N, PT> L;
+  constexpr int PT = 32, NTH = 512, NW = NTH / 64;
+  typedef CkLds<T, C, N, PT, NTH> L;
   typedef typename Mma<T>::frag frag;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
   // LDS views; rebuilt from an opaque base at every (head, slice) iteration so
@@ -106,7 +109,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     sTot = reinterpret_cast<float*>(lb + L::off_tot);
     sLastA = reinterpret_cast<float*>(lb + L::off_misc);
     sLastB = sLastA + PT;
-    sDa = sLastB + 4 * PT;
+    sDa = sLastB + NW * PT;
     sRed = reinterpret_cast<float*>(lb + L::off_red);
     sDdt1 = reinterpret_cast<float*>(lb + L::off_ddt1);
   };
@@ -125,11 +128,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const T* cb0 = ck.cb + (size_t)bn * C * C;
   const T* cbt0 = ck.cbt + (size_t)bn * C * C;
   constexpr int NB = C / 16;
-  static_assert(NB % 4 == 0, "row blocks must split evenly over 4 waves");
 
-  // cross-head accumulator: dCB lower tiles (I >= J), tile k of wave w = w + 4 s
+  // cross-head accumulator: dCB lower tiles (I >= J), tile k of wave w = w + NW s
   constexpr int NBC = NB * (NB + 1) / 2;
-  constexpr int BCPW = (NBC + 3) / 4;
+  constexpr int BCPW = (NBC + NW - 1) / NW;
   f32x4 acc_bc[BCPW];
 #pragma unroll
   for (int i = 0; i < BCPW; ++i) acc_bc[i] = zero4();
@@ -139,10 +141,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     J = k;
   };
 
-  // y-shaped tiles [C][PT]: wave w owns row blocks {w, NB-1-w} (NB = 8) or w (NB = 4)
-  constexpr int BPW = NB / 4;
+  // y-shaped tiles [C][PT] as (row block I, column tile ni) units: wave w owns
+  // NIW consecutive units, all in one row block
   constexpr int YNI = PT / 16;
-  auto my_block = [&](int bi) { return bi == 0 ? wv_id : NB - 1 - wv_id; };
+  constexpr int NIW = NB * YNI / NW;
+  static_assert(NIW >= 1 && (NB * YNI) % NW == 0 && YNI % NIW == 0, "units must split evenly over the waves");
+  const int I0 = (wv_id * NIW) / YNI, ni00 = (wv_id * NIW) % YNI;
 
   for (int hh = 0; hh < HG; ++hh) {
     const int h = g * HG + hh;
@@ -151,18 +155,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int p0 = 0; p0 < P; p0 += PT) {
       const int z = opaque_zero();
       views(z);
-      const T* Bg = Bg0 + z;
-      const T* Cg = Cg0 + z;
-      const T* cbg = cb0 + z;
-      const T* cbtg = cbt0 + z;
+      const T* Bg = opaque_ptr(Bg0);
+      const T* Cg = opaque_ptr(Cg0);
+      const T* cbg = opaque_ptr(cb0);
+      const T* cbtg = opaque_ptr(cbt0);
+      // this wave's block, also rebuilt per iteration (its addresses stay in the loop)
+      const int I = I0 + z, ni0 = ni00 + z;
+      const size_t rowz = row0 + z;
       const size_t bnh = (size_t)bn * dm.H + h;
       // ---- A: slice inputs (dt, x, dy kept exactly as bf16), a = sanitize(dt A, 20)
       int flag = 0;
       {
         constexpr int PER_ROW = PT / 8;
-        for (int e = tid; e < C * PER_ROW; e += 256) {
+        for (int e = tid; e < C * PER_ROW; e += NTH) {
           const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
-          const size_t o = ((row0 + r) * dm.H + h) * P + p0 + c;
+          const size_t o = ((rowz + r) * dm.H + h) * P + p0 + c;
           Raw8<T> rdt, rx;
           Raw8<TD> rdy;
           rdt.load(dt + o);
@@ -181,13 +188,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           store8(sDy + r * L::LPT + c, yv);
         }
       }
-      stage_rows<T, PT, N>(sSt, L::LN, ck.state_pre + (bnh * P + p0) * N, N);
-      stage_rows<T, PT, N>(sDst, L::LN, gr.dstate + (bnh * P + p0) * N, N);
+      stage_rows<T, PT, N, NTH>(sSt, L::LN, ck.state_pre + (bnh * P + p0) * N, N);
+      stage_rows<T, PT, N, NTH>(sDst, L::LN, gr.dstate + (bnh * P + p0) * N, N);
       if (tid < PT) sLastA[tid] = gr.lasta[bnh * P + p0 + tid];
       __syncthreads();
-      column_cumsum<C, PT, L::LC>(sCum, sTot);
+      column_cumsum<C, PT, L::LC, NTH>(sCum, sTot);
       __syncthreads();
-      for (int e = tid; e < NB * PT; e += 256) {
+      for (int e = tid; e < NB * PT; e += NTH) {
         const int I = e / PT, p = e % PT;
         flag |= sCum[16 * I * L::LC + p] - sCum[(16 * I + 15) * L::LC + p] > kMaxRange;
       }
@@ -196,7 +203,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
       // ---- B: operands Yu = dy U, Vd = V dBx (bf16 high + low parts)
       if (!exact) {
-        for (int e = tid; e < (C + 16) * PT; e += 256) {
+        for (int e = tid; e < (C + 16) * PT; e += NTH) {
           const int j = e / PT, p = e % PT;
           float yu = 0.f, vd = 0.f;
           if (j < C) {
@@ -220,7 +227,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // diagonal tiles is dropped when the partials are written
 #pragma unroll
         for (int s = 0; s < BCPW; ++s) {
-          const int k = wv_id + 4 * s;
+          const int k = wv_id + NW * s;
           if (k < NBC) {
             int TI, TJ;
             bc_tile(k, TI, TJ);
@@ -239,7 +246,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // exact path: pairwise with the reference's clips
 #pragma unroll
         for (int s = 0; s < BCPW; ++s) {
-          const int k = wv_id + 4 * s;
+          const int k = wv_id + NW * s;
           if (k < NBC) {
             int TI, TJ;
             bc_tile(k, TI, TJ);
@@ -261,19 +268,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       }
 
       // ---- D: per row block of this wave: R, S and the per-element terms
-      float lastb[YNI][4];
+      float lastb[NIW][4];
 #pragma unroll
-      for (int ni = 0; ni < YNI; ++ni)
+      for (int q = 0; q < NIW; ++q)
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) lastb[ni][ii] = 0.f;
-#pragma unroll 1
-      for (int bi = 0; bi < BPW; ++bi) {
-        const int I = my_block(bi);
-        f32x4 Rv[YNI], Sv[YNI];
+        for (int ii = 0; ii < 4; ++ii) lastb[q][ii] = 0.f;
+      {
+        f32x4 Rv[NIW], Sv[NIW];
         if (!exact) {
-          f32x4 ro[YNI], rd[YNI], so[YNI], sd[YNI];
+          f32x4 ro[NIW], rd[NIW], so[NIW], sd[NIW];
 #pragma unroll
-          for (int ni = 0; ni < YNI; ++ni) { ro[ni] = zero4(); so[ni] = zero4(); }
+          for (int q = 0; q < NIW; ++q) { ro[q] = zero4(); so[q] = zero4(); }
           // every CB fragment of the block row, issued together: CB(I, J) for
           // J < I (row side), CB^T(I, J) for J > I (column side), the diagonal
           frag fa[NB];
@@ -286,49 +291,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           for (int J = 0; J < NB; ++J) {
             if (J < I) {  // sources below the block
 #pragma unroll
-              for (int ni = 0; ni < YNI; ++ni) {
-                f32x4 q = Mma<T>::mma(fa[J], Mma<T>::ld_t(sVd, L::LPT, 16 * ni, 16 * J), zero4());
-                q = Mma<T>::mma(fa[J], Mma<T>::ld_t(sVdl, L::LPT, 16 * ni, 16 * J), q);
+              for (int q = 0; q < NIW; ++q) {
+                const int ni = ni0 + q;
+                f32x4 m = Mma<T>::mma(fa[J], Mma<T>::ld_t(sVd, L::LPT, 16 * ni, 16 * J), zero4());
+                m = Mma<T>::mma(fa[J], Mma<T>::ld_t(sVdl, L::LPT, 16 * ni, 16 * J), m);
                 const int pc = 16 * ni + tile_col();
                 const float mf = __expf(sCum[16 * I * L::LC + pc] - sCum[(16 * J + 15) * L::LC + pc]);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) ro[ni][k] += mf * q[k];
+                for (int k = 0; k < 4; ++k) ro[q][k] += mf * m[k];
               }
             } else if (J > I) {  // targets above the block (column side)
 #pragma unroll
-              for (int ni = 0; ni < YNI; ++ni) {
-                f32x4 q = Mma<T>::mma(fa[J], Mma<T>::ld_t(sYu, L::LPT, 16 * ni, 16 * J), zero4());
-                q = Mma<T>::mma(fa[J], Mma<T>::ld_t(sYul, L::LPT, 16 * ni, 16 * J), q);
+              for (int q = 0; q < NIW; ++q) {
+                const int ni = ni0 + q;
+                f32x4 m = Mma<T>::mma(fa[J], Mma<T>::ld_t(sYu, L::LPT, 16 * ni, 16 * J), zero4());
+                m = Mma<T>::mma(fa[J], Mma<T>::ld_t(sYul, L::LPT, 16 * ni, 16 * J), m);
                 const int pc = 16 * ni + tile_col();
                 const float mf = __expf(sCum[16 * J * L::LC + pc] - sCum[(16 * I + 15) * L::LC + pc]);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) so[ni][k] += mf * q[k];
+                for (int k = 0; k < 4; ++k) so[q][k] += mf * m[k];
               }
             }
+            __builtin_amdgcn_sched_barrier(0);  // keep the operand reads of one J together
           }
           {  // the diagonal block
 #pragma unroll
-            for (int ni = 0; ni < YNI; ++ni) {
-              rd[ni] = Mma<T>::mma(ar, Mma<T>::ld_t(sVd, L::LPT, 16 * ni, 16 * I), zero4());
-              rd[ni] = Mma<T>::mma(ar, Mma<T>::ld_t(sVdl, L::LPT, 16 * ni, 16 * I), rd[ni]);
-              sd[ni] = Mma<T>::mma(as, Mma<T>::ld_t(sYu, L::LPT, 16 * ni, 16 * I), zero4());
-              sd[ni] = Mma<T>::mma(as, Mma<T>::ld_t(sYul, L::LPT, 16 * ni, 16 * I), sd[ni]);
+            for (int q = 0; q < NIW; ++q) {
+              const int ni = ni0 + q;
+              rd[q] = Mma<T>::mma(ar, Mma<T>::ld_t(sVd, L::LPT, 16 * ni, 16 * I), zero4());
+              rd[q] = Mma<T>::mma(ar, Mma<T>::ld_t(sVdl, L::LPT, 16 * ni, 16 * I), rd[q]);
+              sd[q] = Mma<T>::mma(as, Mma<T>::ld_t(sYu, L::LPT, 16 * ni, 16 * I), zero4());
+              sd[q] = Mma<T>::mma(as, Mma<T>::ld_t(sYul, L::LPT, 16 * ni, 16 * I), sd[q]);
             }
           }
 #pragma unroll
-          for (int ni = 0; ni < YNI; ++ni) {
+          for (int q = 0; q < NIW; ++q) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-              const int i = 16 * I + tile_row(k), p = 16 * ni + tile_col();
+              const int i = 16 * I + tile_row(k), p = 16 * (ni0 + q) + tile_col();
               const float ci = sCum[i * L::LC + p];
               const float cs = sCum[16 * I * L::LC + p], ce = sCum[(16 * I + 15) * L::LC + p];
-              Rv[ni][k] = __expf(ci - cs) * ro[ni][k] + __expf(ci - ce) * rd[ni][k];
-              Sv[ni][k] = __expf(ce - ci) * so[ni][k] + __expf(cs - ci) * sd[ni][k];
+              Rv[q][k] = __expf(ci - cs) * ro[q][k] + __expf(ci - ce) * rd[q][k];
+              Sv[q][k] = __expf(ce - ci) * so[q][k] + __expf(cs - ci) * sd[q][k];
             }
           }
         }
 #pragma unroll
-        for (int ni = 0; ni < YNI; ++ni) {
+        for (int q = 0; q < NIW; ++q) {
+          const int ni = ni0 + q;
           // y_off_raw = C state^T and dwrite = B dstate^T for this tile (:126,134)
           const f32x4 yoff = tile_mma<T, false, false>(zero4(), Cg, N, sSt, L::LN, 16 * I, 16 * ni, N);
           const f32x4 dwr = tile_mma<T, false, false>(zero4(), Bg, N, sDst, L::LN, 16 * I, 16 * ni, N);
@@ -342,8 +352,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             const float dbxi = sanitize(dtv * xv);
             float rsum, ssum, ssum_m;
             if (!exact) {
-              rsum = Rv[ni][ii];
-              ssum = ssum_m = Sv[ni][ii];
+              rsum = Rv[q][ii];
+              ssum = ssum_m = Sv[q][ii];
             } else {
               // every pair with the reference's clip, 1e6 cap and masks:
               // R (i as row, masked), S / S_m (i as column)
@@ -372,11 +382,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             const float m1 = (ci >= -kClipDecay && ci <= 0.f) ? 1.f : 0.f;
             const float dw = dwr[ii];
             const float ddbx = sanitize(dw * dte + ssum);                 // :138,148,166
-            const size_t o = ((row0 + i) * dm.H + h) * P + p0 + p;
+            const size_t o = ((rowz + i) * dm.H + h) * P + p0 + p;
             sDdt1[i * L::LC + p] = ddbx * xv;                             // :167
             dx[o] = from_f<T>(sanitize(ddbx * dtv));                     // :168,193 + final
             const float dte_term = dw * dbxi * dte * m2;                  // d_decay_to_end_diff :142
-            lastb[ni][ii] += dte_term;
+            lastb[q][ii] += dte_term;
             sRed[i * L::LC + p] = sanitize(dyi * rsum - dbxi * ssum_m +
                                            dyi * yoff[ii] * dh * m1 - dte_term);  // :162-173
           }
@@ -384,21 +394,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       }
       // column sums of the decay_to_end term over this wave's rows
 #pragma unroll
-      for (int ni = 0; ni < YNI; ++ni) {
-        float v = lastb[ni][0] + lastb[ni][1] + lastb[ni][2] + lastb[ni][3];
+      for (int ni = 0; ni < YNI; ++ni) {  // columns outside this wave's units get 0
+        float v = 0.f;
+#pragma unroll
+        for (int q = 0; q < NIW; ++q)
+          if (ni == ni0 + q) v = lastb[q][0] + lastb[q][1] + lastb[q][2] + lastb[q][3];
         v += __shfl_xor(v, 16);
         v += __shfl_xor(v, 32);
         if (lane_id() < 16) sLastB[wv_id * PT + 16 * ni + lane_id()] = v;
       }
       __syncthreads();
       if (tid < PT) {  // row C-1 extra terms (:176-177)
-        const float lb = sLastB[tid] + sLastB[PT + tid] + sLastB[2 * PT + tid] + sLastB[3 * PT + tid];
+        float lb = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) lb += sLastB[w * PT + tid];
         sRed[(C - 1) * L::LC + tid] += sLastA[tid] + lb;
       }
       __syncthreads();
       // ---- reverse cumsum over the chunk with the clip masks (:181-189)
       {
-        constexpr int NSEG = 256 / PT, RS = C / NSEG;
+        constexpr int NSEG = NTH / PT, RS = C / NSEG;
         const int p = tid % PT, seg = tid / PT;
         float v[RS];
 #pragma unroll
@@ -417,7 +432,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int r = 0; r < RS; ++r) {
           const int row = seg * RS + r;
-          const size_t o = ((row0 + row) * dm.H + h) * P + p0 + p;
+          const size_t o = ((rowz + row) * dm.H + h) * P + p0 + p;
           const float dtv = to_f(sDt[row * L::LPT + p]);
           const float araw = dtv * Ah;
           const float dA = (araw >= -kClipDecay && araw <= kClipDecay) ? (v[r] + off) : 0.f;
@@ -430,7 +445,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         __syncthreads();
         if (lane_id() == 0) sDa[1 + wv_id] = da;
         __syncthreads();
-        if (tid == 0) sDa[0] += sDa[1] + sDa[2] + sDa[3] + sDa[4];
+        if (tid == 0) {
+          float t = 0.f;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) t += sDa[1 + w];
+          sDa[0] += t;
+        }
       }
       __syncthreads();
     }
@@ -441,7 +461,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   float* part = gr.part + ((size_t)bn * G + g) * C * C;
 #pragma unroll
   for (int s = 0; s < BCPW; ++s) {
-    const int k = wv_id + 4 * s;
+    const int k = wv_id + NW * s;
     if (k < NBC) {
       int TI, TJ;
       bc_tile(k, TI, TJ);

@@ -66,10 +66,10 @@ __global__ __launch_bounds__(256) void mamba2_cb(Mamba2Dims dm, const T* __restr
 
 // Inclusive column scan of sCum ([C][PT] fp32 with row stride LD, holding
 // sanitize(dt A, 20) on entry) into sanitize(cumsum, 1e4).  Thread map:
-// column tid % PT, RS rows.
-template <int C, int PT, int LD = PT>
+// column tid % PT, RS rows (NTH threads in the workgroup).
+template <int C, int PT, int LD = PT, int NTH = 256>
 __device__ __forceinline__ void column_cumsum(float* sCum, float* sTot) {
-  constexpr int NSEG = 256 / PT, RS = C / NSEG;
+  constexpr int NSEG = NTH / PT, RS = C / NSEG;
   const int p = threadIdx.x % PT, seg = threadIdx.x / PT;
   float v[RS];
 #pragma unroll

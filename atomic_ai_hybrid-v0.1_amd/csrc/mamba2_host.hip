@@ -174,7 +174,7 @@ static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x,
   if (rc) return rc;
   rc = L("mamba2_bwd_chunk", [&] {
     hipLaunchKernelGGL((mamba2_bwd_chunk<T, TD, C, P, N>), dim3((unsigned)(d.B * d.NT * p.G)),
-                       dim3(256), 0, st, d, p.G, (const T*)dt, (const T*)x, A, (const T*)Bm,
+                       dim3(512), 0, st, d, p.G, (const T*)dt, (const T*)x, A, (const T*)Bm,
                        (const T*)Cm, (const TD*)dy, ck, gr, (T*)ddt, (T*)dx);
   });
   if (rc) return rc;
