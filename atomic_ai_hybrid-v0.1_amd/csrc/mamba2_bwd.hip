@@ -148,6 +148,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   static_assert(NIW >= 1 && (NB * YNI) % NW == 0 && YNI % NIW == 0, "units must split evenly over the waves");
   const int I0 = (wv_id * NIW) / YNI, ni00 = (wv_id * NIW) % YNI;
 
+  // rows C..C+15 of the MFMA operands stay zero (the K = 32 steps of 16-row blocks read them)
+  for (int e = tid; e < 16 * L::LPT; e += NTH) {
+    const int r = C + e / L::LPT, c = e % L::LPT;
+    sYu[r * L::LPT + c] = from_f<T>(0.f);
+    sYul[r * L::LPT + c] = from_f<T>(0.f);
+    sVd[r * L::LPT + c] = from_f<T>(0.f);
+    sVdl[r * L::LPT + c] = from_f<T>(0.f);
+  }
   for (int hh = 0; hh < HG; ++hh) {
     const int h = g * HG + hh;
     const float Ah = A[h];
@@ -163,27 +171,30 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const int I = I0 + z, ni0 = ni00 + z;
       const size_t rowz = row0 + z;
       const size_t bnh = (size_t)bn * dm.H + h;
-      // ---- A: slice inputs (dt, x, dy kept exactly as bf16), a = sanitize(dt A, 20)
+      // ---- A: slice inputs (dt, x, dy kept exactly as bf16), a = sanitize(dt A, 20);
+      // thread item = 8 channels of one row, kept in registers for B
       int flag = 0;
-      {
-        constexpr int PER_ROW = PT / 8;
-        for (int e = tid; e < C * PER_ROW; e += NTH) {
+      constexpr int PER_ROW = PT / 8, NE = C * PER_ROW, EPT = (NE + NTH - 1) / NTH;
+      Raw8<T> rdt[EPT], rx[EPT];
+      Raw8<TD> rdy[EPT];
+#pragma unroll
+      for (int it = 0; it < EPT; ++it) {
+        const int e = tid + NTH * it;
+        if (NE % NTH == 0 || e < NE) {
           const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
           const size_t o = ((rowz + r) * dm.H + h) * P + p0 + c;
-          Raw8<T> rdt, rx;
-          Raw8<TD> rdy;
-          rdt.load(dt + o);
-          rx.load(x + o);
-          rdy.load(dy + o);
-          *reinterpret_cast<uint4*>(sDt + r * L::LPT + c) = rdt.v;
-          *reinterpret_cast<uint4*>(sX + r * L::LPT + c) = rx.v;
+          rdt[it].load(dt + o);
+          rx[it].load(x + o);
+          rdy[it].load(dy + o);
+          *reinterpret_cast<uint4*>(sDt + r * L::LPT + c) = rdt[it].v;
+          *reinterpret_cast<uint4*>(sX + r * L::LPT + c) = rx[it].v;
           float yv[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            const float a = rdt[j] * Ah;
+            const float a = rdt[it][j] * Ah;
             flag |= a > 0.f;
             sCum[r * L::LC + c + j] = sanitize(a, kClipDecay);
-            yv[j] = rdy[j];
+            yv[j] = rdy[it][j];
           }
           store8(sDy + r * L::LPT + c, yv);
         }
@@ -201,22 +212,34 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // positive step exponent or too steep a block: pairwise evaluation
       const bool exact = __syncthreads_or(flag);
 
-      // ---- B: operands Yu = dy U, Vd = V dBx (bf16 high + low parts)
+      // ---- B: operands Yu = dy U, Vd = V dBx (bf16 high + low parts), from the
+      // registers of A; the 16 zero rows below the chunk are written once
       if (!exact) {
-        for (int e = tid; e < (C + 16) * PT; e += NTH) {
-          const int j = e / PT, p = e % PT;
-          float yu = 0.f, vd = 0.f;
-          if (j < C) {
-            const float cj = sCum[j * L::LC + p];
-            const float dbx = sanitize(to_f(sDt[j * L::LPT + p]) * to_f(sX[j * L::LPT + p]));
-            yu = to_f(sDy[j * L::LPT + p]) * __expf(cj - sCum[(j & ~15) * L::LC + p]);
-            vd = dbx * __expf(sCum[(j | 15) * L::LC + p] - cj);
+#pragma unroll
+        for (int it = 0; it < EPT; ++it) {
+          const int e = tid + NTH * it;
+          if (NE % NTH == 0 || e < NE) {
+            const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
+            const float* cr = sCum + r * L::LC + c;
+            const float* cs = sCum + (r & ~15) * L::LC + c;
+            const float* ce = sCum + (r | 15) * L::LC + c;
+            float yh[8], yl[8], vh[8], vl[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const float cj = cr[j];
+              const float dbx = sanitize(rdt[it][j] * rx[it][j]);
+              const float yu = rdy[it][j] * __expf(cj - cs[j]);
+              const float vd = dbx * __expf(ce[j] - cj);
+              yh[j] = to_f(from_f<T>(yu));
+              yl[j] = yu - yh[j];
+              vh[j] = to_f(from_f<T>(vd));
+              vl[j] = vd - vh[j];
+            }
+            store8(sYu + r * L::LPT + c, yh);
+            store8(sYul + r * L::LPT + c, yl);
+            store8(sVd + r * L::LPT + c, vh);
+            store8(sVdl + r * L::LPT + c, vl);
           }
-          const T yh = from_f<T>(yu), vh = from_f<T>(vd);
-          sYu[j * L::LPT + p] = yh;
-          sYul[j * L::LPT + p] = from_f<T>(yu - to_f(yh));
-          sVd[j * L::LPT + p] = vh;
-          sVdl[j * L::LPT + p] = from_f<T>(vd - to_f(vh));
         }
         __syncthreads();
       }
