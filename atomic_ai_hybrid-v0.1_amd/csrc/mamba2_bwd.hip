@@ -70,9 +70,8 @@ struct CkLds {
   static constexpr int off_vd = off_yul + OPR;
   static constexpr int off_vdl = off_vd + OPR;
   static constexpr int off_cum = off_vdl + OPR;
-  static constexpr int off_red = off_cum + C * LC * 4;    // fp32 d_cum
-  static constexpr int off_ddt1 = off_red + C * LC * 4;   // fp32 ddt_1
-  static constexpr int off_tot = off_ddt1 + C * LC * 4;
+  static constexpr int off_tot = off_cum + C * LC * 4;  // column / block totals
+  static_assert(NSEG >= C / 16, "the block totals reuse the column-scan totals");
   static constexpr int off_misc = off_tot + NSEG * PT * 4;   // lasta[PT], lastb[NW][PT], dA[1 + NW]
   static constexpr int total = off_misc + (PT + NW * PT + 1 + NW) * 4;
 };
@@ -93,7 +92,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // the compiler cannot hoist the hundreds of per-lane addresses of the
   // unrolled loop bodies out of the iteration loop (that hoisting spilled them).
   T *sSt, *sDst, *sDy, *sDt, *sX, *sYu, *sYul, *sVd, *sVdl;
-  float *sCum, *sTot, *sLastA, *sLastB, *sDa, *sRed, *sDdt1;
+  float *sCum, *sTot, *sLastA, *sLastB, *sDa;
   auto views = [&](int z) {
     unsigned char* lb = lds + z;
     sSt = reinterpret_cast<T*>(lb + L::off_st);
@@ -110,8 +109,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     sLastA = reinterpret_cast<float*>(lb + L::off_misc);
     sLastB = sLastA + PT;
     sDa = sLastB + NW * PT;
-    sRed = reinterpret_cast<float*>(lb + L::off_red);
-    sDdt1 = reinterpret_cast<float*>(lb + L::off_ddt1);
   };
   views(0);
 
@@ -291,7 +288,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
 
       // ---- D: per row block of this wave: R, S and the per-element terms
-      float lastb[NIW][4];
+      float lastb[NIW][4], redv[NIW][4], ddt1v[NIW][4];
 #pragma unroll
       for (int q = 0; q < NIW; ++q)
 #pragma unroll
@@ -406,14 +403,30 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const float dw = dwr[ii];
             const float ddbx = sanitize(dw * dte + ssum);                 // :138,148,166
             const size_t o = ((rowz + i) * dm.H + h) * P + p0 + p;
-            sDdt1[i * L::LC + p] = ddbx * xv;                             // :167
+            ddt1v[q][ii] = ddbx * xv;                                     // :167
             dx[o] = from_f<T>(sanitize(ddbx * dtv));                     // :168,193 + final
             const float dte_term = dw * dbxi * dte * m2;                  // d_decay_to_end_diff :142
             lastb[q][ii] += dte_term;
-            sRed[i * L::LC + p] = sanitize(dyi * rsum - dbxi * ssum_m +
-                                           dyi * yoff[ii] * dh * m1 - dte_term);  // :162-173
+            // d_cum of this element (:162-173), masked for the reverse cumsum (:181-186)
+            redv[q][ii] = (fabsf(ci) < kClipAcc)
+                              ? sanitize(dyi * rsum - dbxi * ssum_m + dyi * yoff[ii] * dh * m1 - dte_term)
+                              : 0.f;
           }
         }
+      }
+      // ---- reverse cumsum over the chunk with the clip masks (:181-189), in the
+      // tile layout: the lane's 4 rows, the lane groups below it in the block,
+      // then the blocks below (block totals through LDS), then the row C-1 terms
+      const int g4 = lane_id() >> 4;
+      float gsuf[NIW];
+#pragma unroll
+      for (int q = 0; q < NIW; ++q) {
+#pragma unroll
+        for (int ii = 2; ii >= 0; --ii) redv[q][ii] += redv[q][ii + 1];
+        const float tg = redv[q][0];
+        const float t1 = __shfl_down(tg, 16), t2 = __shfl_down(tg, 32), t3 = __shfl_down(tg, 48);
+        gsuf[q] = (g4 < 3 ? t1 : 0.f) + (g4 < 2 ? t2 : 0.f) + (g4 < 1 ? t3 : 0.f);
+        if (g4 == 0) sTot[I * PT + 16 * (ni0 + q) + tile_col()] = tg + gsuf[q];
       }
       // column sums of the decay_to_end term over this wave's rows
 #pragma unroll
@@ -427,55 +440,40 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (lane_id() < 16) sLastB[wv_id * PT + 16 * ni + lane_id()] = v;
       }
       __syncthreads();
-      if (tid < PT) {  // row C-1 extra terms (:176-177)
-        float lb = 0.f;
+      float da = 0.f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) lb += sLastB[w * PT + tid];
-        sRed[(C - 1) * L::LC + tid] += sLastA[tid] + lb;
-      }
-      __syncthreads();
-      // ---- reverse cumsum over the chunk with the clip masks (:181-189)
-      {
-        constexpr int NSEG = NTH / PT, RS = C / NSEG;
-        const int p = tid % PT, seg = tid / PT;
-        float v[RS];
+      for (int q = 0; q < NIW; ++q) {
+        const int p = 16 * (ni0 + q) + tile_col();
+        float off = gsuf[q];
+        for (int J = I + 1; J < NB; ++J) off += sTot[J * PT + p];
+        // row C-1 extra terms (:176-177), under row C-1's clip mask
+        float extra = sLastA[p];
 #pragma unroll
-        for (int r = 0; r < RS; ++r) {
-          const int row = seg * RS + r;
-          const float cum = sCum[row * L::LC + p];
-          v[r] = (fabsf(cum) < kClipAcc) ? sRed[row * L::LC + p] : 0.f;
-        }
+        for (int w = 0; w < NW; ++w) extra += sLastB[w * PT + p];
+        if (fabsf(sCum[(C - 1) * L::LC + p]) < kClipAcc) off += extra;
 #pragma unroll
-        for (int r = RS - 2; r >= 0; --r) v[r] += v[r + 1];
-        sTot[seg * PT + p] = v[0];
-        __syncthreads();
-        float off = 0.f;
-        for (int s = seg + 1; s < NSEG; ++s) off += sTot[s * PT + p];
-        float da = 0.f;
-#pragma unroll
-        for (int r = 0; r < RS; ++r) {
-          const int row = seg * RS + r;
-          const size_t o = ((rowz + row) * dm.H + h) * P + p0 + p;
-          const float dtv = to_f(sDt[row * L::LPT + p]);
+        for (int ii = 0; ii < 4; ++ii) {
+          const int i = 16 * I + tile_row(ii);
+          const float dtv = to_f(sDt[i * L::LPT + p]);
           const float araw = dtv * Ah;
-          const float dA = (araw >= -kClipDecay && araw <= kClipDecay) ? (v[r] + off) : 0.f;
-          ddt[o] = from_f<T>(sanitize(sDdt1[row * L::LC + p] + dA * Ah));   // :187,190 + final
+          const float dA = (araw >= -kClipDecay && araw <= kClipDecay) ? (redv[q][ii] + off) : 0.f;
+          const size_t o = ((rowz + i) * dm.H + h) * P + p0 + p;
+          ddt[o] = from_f<T>(sanitize(ddt1v[q][ii] + dA * Ah));   // :187,190 + final
           da += dA * dtv;
         }
-        // workgroup sum of this slice's dA contribution
-#pragma unroll
-        for (int sh = 1; sh < 64; sh <<= 1) da += __shfl_xor(da, sh);
-        __syncthreads();
-        if (lane_id() == 0) sDa[1 + wv_id] = da;
-        __syncthreads();
-        if (tid == 0) {
-          float t = 0.f;
-#pragma unroll
-          for (int w = 0; w < NW; ++w) t += sDa[1 + w];
-          sDa[0] += t;
-        }
       }
+      // workgroup sum of this slice's dA contribution
+#pragma unroll
+      for (int sh = 1; sh < 64; sh <<= 1) da += __shfl_xor(da, sh);
+      if (lane_id() == 0) sDa[1 + wv_id] = da;
+      // every read of this slice's LDS is done when the barrier below is passed
       __syncthreads();
+      if (tid == 0) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) t += sDa[1 + w];
+        sDa[0] += t;
+      }
     }
     if (tid == 0) gr.dap[(size_t)bn * dm.H + h] = sDa[0];
     __syncthreads();
