@@ -73,7 +73,9 @@ struct CkLds {
   static constexpr int off_tot = off_cum + C * LC * 4;  // column / block totals
   static_assert(NSEG >= C / 16, "the block totals reuse the column-scan totals");
   static constexpr int off_misc = off_tot + NSEG * PT * 4;   // lasta[PT], lastb[NW][PT], dA[1 + NW]
-  static constexpr int total = off_misc + (PT + NW * PT + 1 + NW) * 4;
+  static constexpr int off_m = off_misc + (PT + NW * PT + 1 + NW) * 4;
+  // M_IJ[p] = exp(cum_{16I} - cum_{16J+15}) for the 16-row block pairs I >= J
+  static constexpr int total = off_m + (C / 16) * (C / 16 + 1) / 2 * PT * 4;
 };
 
 // 512 threads: eight waves, two per SIMD, so one wave's LDS / global / MFMA
@@ -92,7 +94,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // the compiler cannot hoist the hundreds of per-lane addresses of the
   // unrolled loop bodies out of the iteration loop (that hoisting spilled them).
   T *sSt, *sDst, *sDy, *sDt, *sX, *sYu, *sYul, *sVd, *sVdl;
-  float *sCum, *sTot, *sLastA, *sLastB, *sDa;
+  float *sCum, *sTot, *sLastA, *sLastB, *sDa, *sM;
   auto views = [&](int z) {
     unsigned char* lb = lds + z;
     sSt = reinterpret_cast<T*>(lb + L::off_st);
@@ -109,6 +111,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     sLastA = reinterpret_cast<float*>(lb + L::off_misc);
     sLastB = sLastA + PT;
     sDa = sLastB + NW * PT;
+    sM = reinterpret_cast<float*>(lb + L::off_m);
   };
   views(0);
 
@@ -202,9 +205,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       __syncthreads();
       column_cumsum<C, PT, L::LC, NTH>(sCum, sTot);
       __syncthreads();
-      for (int e = tid; e < NB * PT; e += NTH) {
-        const int I = e / PT, p = e % PT;
-        flag |= sCum[16 * I * L::LC + p] - sCum[(16 * I + 15) * L::LC + p] > kMaxRange;
+      // block-pair decays (one exp per pair and channel, shared by phases C and D)
+      // and the range check on the diagonal pairs
+      for (int e = tid; e < NBC * PT; e += NTH) {
+        const int k = e / PT, p = e % PT;
+        int TI, TJ;
+        bc_tile(k, TI, TJ);
+        const float d = sCum[16 * TI * L::LC + p] - sCum[(16 * TJ + 15) * L::LC + p];
+        sM[e] = __expf(d);
+        if (TI == TJ) flag |= d > kMaxRange;
       }
       // positive step exponent or too steep a block: pairwise evaluation
       const bool exact = __syncthreads_or(flag);
@@ -252,13 +261,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             int TI, TJ;
             bc_tile(k, TI, TJ);
             frag a = Mma<T>::ld_c(sYu, L::LPT, 16 * TI, 0);
-            const int pb = 8 * (lane_id() >> 4);
-            const int rs = 16 * TI, re = 16 * TJ + 15;
+            const float* mk = sM + k * PT + 8 * (lane_id() >> 4);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float mf = __expf(sCum[rs * L::LC + pb + e] - sCum[re * L::LC + pb + e]);
-              a[e] = from_f<T>(to_f(a[e]) * mf);
-            }
+            for (int e = 0; e < 8; ++e) a[e] = from_f<T>(to_f(a[e]) * mk[e]);
             acc_bc[s] = Mma<T>::mma(a, Mma<T>::ld_c(sVd, L::LPT, 16 * TJ, 0), acc_bc[s]);
           }
         }
@@ -316,7 +321,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 f32x4 m = Mma<T>::mma(fa[J], Mma<T>::ld_t(sVd, L::LPT, 16 * ni, 16 * J), zero4());
                 m = Mma<T>::mma(fa[J], Mma<T>::ld_t(sVdl, L::LPT, 16 * ni, 16 * J), m);
                 const int pc = 16 * ni + tile_col();
-                const float mf = __expf(sCum[16 * I * L::LC + pc] - sCum[(16 * J + 15) * L::LC + pc]);
+                const float mf = sM[(I * (I + 1) / 2 + J) * PT + pc];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) ro[q][k] += mf * m[k];
               }
@@ -327,7 +332,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 f32x4 m = Mma<T>::mma(fa[J], Mma<T>::ld_t(sYu, L::LPT, 16 * ni, 16 * J), zero4());
                 m = Mma<T>::mma(fa[J], Mma<T>::ld_t(sYul, L::LPT, 16 * ni, 16 * J), m);
                 const int pc = 16 * ni + tile_col();
-                const float mf = __expf(sCum[16 * J * L::LC + pc] - sCum[(16 * I + 15) * L::LC + pc]);
+                const float mf = sM[(J * (J + 1) / 2 + I) * PT + pc];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) so[q][k] += mf * m[k];
               }
