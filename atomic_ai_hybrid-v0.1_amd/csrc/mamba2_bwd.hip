@@ -156,6 +156,40 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     sVd[r * L::LPT + c] = from_f<T>(0.f);
     sVdl[r * L::LPT + c] = from_f<T>(0.f);
   }
+  // slice inputs of the next (head, slice), loaded while the current one computes:
+  // thread item = 8 channels of one row of dt / x / dy, one 16-byte piece of
+  // each of the state_pre / dstate rows, one lasta value
+  constexpr int PER_ROW = PT / 8, NE = C * PER_ROW, EPT = (NE + NTH - 1) / NTH;
+  constexpr int SPR = N * (int)sizeof(T) / 16, NS = PT * SPR, SPT = (NS + NTH - 1) / NTH;
+  Raw8<T> ndt[EPT], nx[EPT];
+  Raw8<TD> ndy[EPT];
+  uint4 nst[SPT], ndst[SPT];
+  float nla = 0.f;
+  auto load_slice = [&](int hn, int pn, size_t rowb) {
+    const size_t bnhn = (size_t)bn * dm.H + hn;
+#pragma unroll
+    for (int it = 0; it < EPT; ++it) {
+      const int e = tid + NTH * it;
+      if (NE % NTH == 0 || e < NE) {
+        const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
+        const size_t o = ((rowb + r) * dm.H + hn) * P + pn + c;
+        ndt[it].load(dt + o);
+        nx[it].load(x + o);
+        ndy[it].load(dy + o);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < SPT; ++it) {
+      const int e = tid + NTH * it;
+      if (NS % NTH == 0 || e < NS) {
+        const size_t o = (bnhn * P + pn + e / SPR) * N + (e % SPR) * (16 / sizeof(T));
+        nst[it] = *reinterpret_cast<const uint4*>(ck.state_pre + o);
+        ndst[it] = *reinterpret_cast<const uint4*>(gr.dstate + o);
+      }
+    }
+    if (tid < PT) nla = gr.lasta[bnhn * P + pn + tid];
+  };
+  load_slice(g * HG, 0, row0);
   for (int hh = 0; hh < HG; ++hh) {
     const int h = g * HG + hh;
     const float Ah = A[h];
@@ -170,22 +204,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // this wave's block, also rebuilt per iteration (its addresses stay in the loop)
       const int I = I0 + z, ni0 = ni00 + z;
       const size_t rowz = row0 + z;
-      const size_t bnh = (size_t)bn * dm.H + h;
       // ---- A: slice inputs (dt, x, dy kept exactly as bf16), a = sanitize(dt A, 20);
       // thread item = 8 channels of one row, kept in registers for B
       int flag = 0;
-      constexpr int PER_ROW = PT / 8, NE = C * PER_ROW, EPT = (NE + NTH - 1) / NTH;
       Raw8<T> rdt[EPT], rx[EPT];
       Raw8<TD> rdy[EPT];
+#pragma unroll
+      for (int it = 0; it < EPT; ++it) {
+        rdt[it] = ndt[it];
+        rx[it] = nx[it];
+        rdy[it] = ndy[it];
+      }
+#pragma unroll
+      for (int it = 0; it < SPT; ++it) {
+        const int e = tid + NTH * it;
+        if (NS % NTH == 0 || e < NS) {
+          const int r = e / SPR, c = (e % SPR) * (16 / (int)sizeof(T));
+          *reinterpret_cast<uint4*>(sSt + r * L::LN + c) = nst[it];
+          *reinterpret_cast<uint4*>(sDst + r * L::LN + c) = ndst[it];
+        }
+      }
+      if (tid < PT) sLastA[tid] = nla;
 #pragma unroll
       for (int it = 0; it < EPT; ++it) {
         const int e = tid + NTH * it;
         if (NE % NTH == 0 || e < NE) {
           const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
-          const size_t o = ((rowz + r) * dm.H + h) * P + p0 + c;
-          rdt[it].load(dt + o);
-          rx[it].load(x + o);
-          rdy[it].load(dy + o);
           *reinterpret_cast<uint4*>(sDt + r * L::LPT + c) = rdt[it].v;
           *reinterpret_cast<uint4*>(sX + r * L::LPT + c) = rx[it].v;
           float yv[8];
@@ -199,9 +243,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           store8(sDy + r * L::LPT + c, yv);
         }
       }
-      stage_rows<T, PT, N, NTH>(sSt, L::LN, ck.state_pre + (bnh * P + p0) * N, N);
-      stage_rows<T, PT, N, NTH>(sDst, L::LN, gr.dstate + (bnh * P + p0) * N, N);
-      if (tid < PT) sLastA[tid] = gr.lasta[bnh * P + p0 + tid];
       __syncthreads();
       column_cumsum<C, PT, L::LC, NTH>(sCum, sTot);
       __syncthreads();
@@ -248,6 +289,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           }
         }
         __syncthreads();
+      }
+
+      // the next slice's loads (the registers of A are free again)
+      {
+        const bool last_p = p0 + PT >= P;
+        if (!(last_p && hh + 1 == HG)) load_slice(last_p ? h + 1 : h, last_p ? 0 : p0 + PT, rowz);
       }
 
       // ---- C: dCB tiles
