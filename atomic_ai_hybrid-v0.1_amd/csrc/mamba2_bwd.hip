@@ -55,7 +55,9 @@ template <typename T, int C, int N, int PT, int NTH>
 struct CkLds {
   static constexpr int PAD = Pad<T>::v;
   static constexpr int LN = N + PAD, LPT = PT + PAD;
-  static constexpr int LC = PT + 1;  // fp32 [C][PT] rows, padded against bank conflicts
+  // fp32 [C][PT] rows: 16-byte aligned, and rows 4 apart land 16 banks apart
+  // (the MFMA tile layout reads 4 row groups x 16 columns)
+  static constexpr int LC = PT + 4;
   static constexpr int NW = NTH / 64;
   static constexpr int NSEG = NTH / PT;
   static constexpr int OPT = C * LPT * (int)sizeof(T);
@@ -232,14 +234,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
           *reinterpret_cast<uint4*>(sDt + r * L::LPT + c) = rdt[it].v;
           *reinterpret_cast<uint4*>(sX + r * L::LPT + c) = rx[it].v;
-          float yv[8];
+          float yv[8], av[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             const float a = rdt[it][j] * Ah;
             flag |= a > 0.f;
-            sCum[r * L::LC + c + j] = sanitize(a, kClipDecay);
+            av[j] = sanitize(a, kClipDecay);
             yv[j] = rdy[it][j];
           }
+          store8(sCum + r * L::LC + c, av);
           store8(sDy + r * L::LPT + c, yv);
         }
       }
@@ -267,9 +270,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           const int e = tid + NTH * it;
           if (NE % NTH == 0 || e < NE) {
             const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
-            const float* cr = sCum + r * L::LC + c;
-            const float* cs = sCum + (r & ~15) * L::LC + c;
-            const float* ce = sCum + (r | 15) * L::LC + c;
+            float cr[8], cs[8], ce[8];
+            load8(sCum + r * L::LC + c, cr);
+            load8(sCum + (r & ~15) * L::LC + c, cs);
+            load8(sCum + (r | 15) * L::LC + c, ce);
             float yh[8], yl[8], vh[8], vl[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
