@@ -51,6 +51,30 @@ struct Mamba2Grads {
 // A slice with a positive step exponent or a block range above kMaxRange is
 // evaluated pairwise with the reference's clips and masks instead.
 
+// The pair sums take one K = 32 MFMA per 16-row block: the A fragment holds
+// the 16 x 16 CB block twice along K, the B fragment the block's 16 rows of
+// the high part and then of the low part, so hi and lo are summed in the MFMA.
+// mask 1 keeps columns <= row (lower triangle), mask 2 columns >= row.
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::frag cb_frag_dup(const T* g, int ld, int m0, int k0, int mask) {
+  typedef typename Mma<T>::frag frag;
+  const int l = lane_id(), m = l & 15, kb = 8 * ((l >> 4) & 1);
+  frag a = *reinterpret_cast<const frag*>(g + (m0 + m) * ld + k0 + kb);
+  if (mask) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool keep = mask == 1 ? (kb + e <= m) : (kb + e >= m);
+      if (!keep) a[e] = (T)0.f;
+    }
+  }
+  return a;
+}
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::frag ld_t_hilo(const T* hi, const T* lo, int ld, int i0, int k0) {
+  const int g2 = lane_id() >> 5;  // lanes 32..63 hold K rows 16..31
+  return Mma<T>::ld_t(g2 ? lo : hi, ld, i0, k0 - 16 * g2);
+}
+
 template <typename T, int C, int N, int PT, int NTH>
 struct CkLds {
   static constexpr int PAD = Pad<T>::v;
@@ -61,7 +85,7 @@ struct CkLds {
   static constexpr int NW = NTH / 64;
   static constexpr int NSEG = NTH / PT;
   static constexpr int OPT = C * LPT * (int)sizeof(T);
-  static constexpr int OPR = (C + 16) * LPT * (int)sizeof(T);  // MFMA operand + 16 zero rows
+  static constexpr int OPR = C * LPT * (int)sizeof(T);  // MFMA operand
   static constexpr int off_st = 0;
   static constexpr int off_dst = off_st + PT * LN * (int)sizeof(T);
   static constexpr int off_dy = off_dst + PT * LN * (int)sizeof(T);
@@ -150,14 +174,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   static_assert(NIW >= 1 && (NB * YNI) % NW == 0 && YNI % NIW == 0, "units must split evenly over the waves");
   const int I0 = (wv_id * NIW) / YNI, ni00 = (wv_id * NIW) % YNI;
 
-  // rows C..C+15 of the MFMA operands stay zero (the K = 32 steps of 16-row blocks read them)
-  for (int e = tid; e < 16 * L::LPT; e += NTH) {
-    const int r = C + e / L::LPT, c = e % L::LPT;
-    sYu[r * L::LPT + c] = from_f<T>(0.f);
-    sYul[r * L::LPT + c] = from_f<T>(0.f);
-    sVd[r * L::LPT + c] = from_f<T>(0.f);
-    sVdl[r * L::LPT + c] = from_f<T>(0.f);
-  }
   // slice inputs of the next (head, slice), loaded while the current one computes:
   // thread item = 8 channels of one row of dt / x / dy, one 16-byte piece of
   // each of the state_pre / dstate rows, one lasta value
@@ -263,7 +279,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const bool exact = __syncthreads_or(flag);
 
       // ---- B: operands Yu = dy U, Vd = V dBx (bf16 high + low parts), from the
-      // registers of A; the 16 zero rows below the chunk are written once
+      // registers of A
       if (!exact) {
 #pragma unroll
         for (int it = 0; it < EPT; ++it) {
@@ -360,17 +376,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           frag fa[NB];
 #pragma unroll
           for (int J = 0; J < NB; ++J)
-            if (J != I) fa[J] = cb_frag<T>(J < I ? cbg : cbtg, C, 16 * I, 16 * J, 0);
-          const frag ar = cb_frag<T>(cbg, C, 16 * I, 16 * I, 1);
-          const frag as = cb_frag<T>(cbtg, C, 16 * I, 16 * I, 2);
+            if (J != I) fa[J] = cb_frag_dup<T>(J < I ? cbg : cbtg, C, 16 * I, 16 * J, 0);
+          const frag ar = cb_frag_dup<T>(cbg, C, 16 * I, 16 * I, 1);
+          const frag as = cb_frag_dup<T>(cbtg, C, 16 * I, 16 * I, 2);
 #pragma unroll
           for (int J = 0; J < NB; ++J) {
             if (J < I) {  // sources below the block
 #pragma unroll
               for (int q = 0; q < NIW; ++q) {
                 const int ni = ni0 + q;
-                f32x4 m = Mma<T>::mma(fa[J], Mma<T>::ld_t(sVd, L::LPT, 16 * ni, 16 * J), zero4());
-                m = Mma<T>::mma(fa[J], Mma<T>::ld_t(sVdl, L::LPT, 16 * ni, 16 * J), m);
+                const f32x4 m = Mma<T>::mma(fa[J], ld_t_hilo<T>(sVd, sVdl, L::LPT, 16 * ni, 16 * J), zero4());
                 const int pc = 16 * ni + tile_col();
                 const float mf = sM[(I * (I + 1) / 2 + J) * PT + pc];
 #pragma unroll
@@ -380,8 +395,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
               for (int q = 0; q < NIW; ++q) {
                 const int ni = ni0 + q;
-                f32x4 m = Mma<T>::mma(fa[J], Mma<T>::ld_t(sYu, L::LPT, 16 * ni, 16 * J), zero4());
-                m = Mma<T>::mma(fa[J], Mma<T>::ld_t(sYul, L::LPT, 16 * ni, 16 * J), m);
+                const f32x4 m = Mma<T>::mma(fa[J], ld_t_hilo<T>(sYu, sYul, L::LPT, 16 * ni, 16 * J), zero4());
                 const int pc = 16 * ni + tile_col();
                 const float mf = sM[(J * (J + 1) / 2 + I) * PT + pc];
 #pragma unroll
@@ -394,10 +408,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int q = 0; q < NIW; ++q) {
               const int ni = ni0 + q;
-              rd[q] = Mma<T>::mma(ar, Mma<T>::ld_t(sVd, L::LPT, 16 * ni, 16 * I), zero4());
-              rd[q] = Mma<T>::mma(ar, Mma<T>::ld_t(sVdl, L::LPT, 16 * ni, 16 * I), rd[q]);
-              sd[q] = Mma<T>::mma(as, Mma<T>::ld_t(sYu, L::LPT, 16 * ni, 16 * I), zero4());
-              sd[q] = Mma<T>::mma(as, Mma<T>::ld_t(sYul, L::LPT, 16 * ni, 16 * I), sd[q]);
+              rd[q] = Mma<T>::mma(ar, ld_t_hilo<T>(sVd, sVdl, L::LPT, 16 * ni, 16 * I), zero4());
+              sd[q] = Mma<T>::mma(as, ld_t_hilo<T>(sYu, sYul, L::LPT, 16 * ni, 16 * I), zero4());
             }
           }
 #pragma unroll
