@@ -203,21 +203,22 @@ template <typename T> struct Pad { static constexpr int v = 16 / sizeof(T); };
 
 // ------------------------------------------------------------- staging
 // A [R][D] block moved global -> registers -> LDS in 16-byte pieces, so the
-// next chunk's loads can be in flight while the current chunk computes.
-template <typename T, int R, int D>
+// next chunk's loads can be in flight while the current chunk computes
+// (NTH threads in the workgroup).
+template <typename T, int R, int D, int NTH = 256>
 struct RegStage {
   static constexpr int VEC = 16 / (int)sizeof(T);
   static constexpr int PER_ROW = D / VEC;
   static constexpr int N = R * PER_ROW;
-  static constexpr int PT = (N + 255) / 256;
+  static constexpr int PT = (N + NTH - 1) / NTH;
   // one SSA vector (not an array) so the staging stays in registers
   typedef uint32_t vec_t __attribute__((ext_vector_type(4 * PT)));
   vec_t r;
   __device__ __forceinline__ void load(const T* src, size_t ld) {
 #pragma unroll
     for (int i = 0; i < PT; ++i) {
-      const int e = threadIdx.x + 256 * i;
-      if (N % 256 == 0 || e < N) {
+      const int e = threadIdx.x + NTH * i;
+      if (N % NTH == 0 || e < N) {
         const uint4 x = *reinterpret_cast<const uint4*>(src + (size_t)(e / PER_ROW) * ld + (e % PER_ROW) * VEC);
         r[4 * i] = x.x; r[4 * i + 1] = x.y; r[4 * i + 2] = x.z; r[4 * i + 3] = x.w;
       }
@@ -226,8 +227,8 @@ struct RegStage {
   __device__ __forceinline__ void store(T* dst, int ld) const {
 #pragma unroll
     for (int i = 0; i < PT; ++i) {
-      const int e = threadIdx.x + 256 * i;
-      if (N % 256 == 0 || e < N)
+      const int e = threadIdx.x + NTH * i;
+      if (N % NTH == 0 || e < N)
         *reinterpret_cast<uint4*>(dst + (e / PER_ROW) * ld + (e % PER_ROW) * VEC) =
             make_uint4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
     }
@@ -250,11 +251,11 @@ __device__ __forceinline__ void stage_rows(T* dst, int dst_ld, const T* src, siz
         *reinterpret_cast<const uint4*>(src + r * src_ld + c);
   }
 }
-template <typename T, int R, int D>
+template <typename T, int R, int D, int NTH = 256>
 __device__ __forceinline__ void unstage_rows(T* dst, size_t dst_ld, const T* src, int src_ld) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int PER_ROW = D / VEC;
-  for (int e = threadIdx.x; e < R * PER_ROW; e += 256) {
+  for (int e = threadIdx.x; e < R * PER_ROW; e += NTH) {
     const int r = e / PER_ROW, c = (e % PER_ROW) * VEC;
     *reinterpret_cast<uint4*>(dst + r * dst_ld + c) =
         *reinterpret_cast<const uint4*>(src + r * src_ld + c);
@@ -277,11 +278,11 @@ __device__ __forceinline__ void xcd_group_map(int x, int groups, int per_group, 
 
 // Elementwise copy of a [R][D] block into LDS converting to the operand type
 // (optionally scaled).
-template <typename TS, typename T, int R, int D>
+template <typename TS, typename T, int R, int D, int NTH = 256>
 __device__ __forceinline__ void stage_convert(T* dst, int ld, const TS* src, size_t src_ld,
                                               float mul = 1.f) {
   constexpr int PER_ROW = D / 8;
-  for (int e = threadIdx.x; e < R * PER_ROW; e += 256) {
+  for (int e = threadIdx.x; e < R * PER_ROW; e += NTH) {
     const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
     float x[8];
     load8(src + (size_t)r * src_ld + c, x);

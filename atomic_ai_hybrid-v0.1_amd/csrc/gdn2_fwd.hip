@@ -387,8 +387,10 @@ struct StateLds {
   static constexpr int total = off_gl + K * 4;
 };
 
+// Eight waves (two per SIMD): the state tiles and the [w; q] h tiles of one
+// V tile split over them by row blocks.
 template <typename T, int C, int K, int V, int VT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T> ck,
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T> ck,
                                                      const float* __restrict__ h0, float* __restrict__ o,
                                                      float* __restrict__ h_final, int save) {
   typedef StateLds<T, C, K, V, VT> L;
@@ -410,10 +412,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int wv_id = wave_id();
 
   // state tiles h[d][v]: (K/16) x (VT/16), TPW per wave
+  constexpr int NW = 8, NTHR = 64 * NW;
   constexpr int NTI = VT / 16;
   constexpr int NTH = (K / 16) * NTI;
-  constexpr int TPW = NTH / 4;
-  static_assert(NTH % 4 == 0, "state tiles must split evenly over 4 waves");
+  constexpr int TPW = NTH / NW;
+  static_assert(NTH % NW == 0 && TPW >= 1, "state tiles must split evenly over the waves");
   f32x4 hs[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
@@ -428,13 +431,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   // X tiles: rows [0, C) = w_pseudo h, rows [C, 2C) = qg h; (2C/16) x NTI tiles
   constexpr int NTX = (2 * C / 16) * NTI;
-  constexpr int XPW = NTX / 4;
-  static_assert(NTX % 4 == 0, "output tiles must split evenly over 4 waves");
+  constexpr int XPW = NTX / NW;
+  static_assert(NTX % NW == 0 && XPW >= 1, "output tiles must split evenly over the waves");
 
-  RegStage<T, C, K> pw, pq, pk;
-  RegStage<T, C, C> pa;
-  RegStage<T, C, VT> pu;
-  RegStage<float, 1, K> pg;
+  RegStage<T, C, K, NTHR> pw, pq, pk;
+  RegStage<T, C, C, NTHR> pa;
+  RegStage<T, C, VT, NTHR> pu;
+  RegStage<float, 1, K, NTHR> pg;
   auto prefetch = [&](int n) {
     const size_t bhn = (size_t)bh * dm.NT + n;
     pw.load(ck.wt + bhn * C * K, K);
@@ -459,7 +462,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   for (int n = 0; n < dm.NT; ++n) {
     const size_t bhn = (size_t)bh * dm.NT + n;
     if (n + 1 < dm.NT) prefetch(n + 1);
-    if (save) unstage_rows<T, VT, K>(ck.hT + bhn * V * K + (size_t)v0 * K, K, sHt, L::LK);
+    if (save) unstage_rows<T, VT, K, NTHR>(ck.hT + bhn * V * K + (size_t)v0 * K, K, sHt, L::LK);
 
     // v_new = u - w_pseudo h ; qh = qg h
     f32x4 xo[XPW];
@@ -484,7 +487,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       xo[t] = acc;
     }
     __syncthreads();
-    if (save) unstage_rows<T, VT, C>(ck.vnT + bhn * V * C + (size_t)v0 * C, C, sVn, L::LC);
+    if (save) unstage_rows<T, VT, C, NTHR>(ck.vnT + bhn * V * C + (size_t)v0 * C, C, sVn, L::LC);
 
     // o = scale qg h + Aqk v_new   (rows of the qg half)
     float* og = o ? o + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0 : nullptr;

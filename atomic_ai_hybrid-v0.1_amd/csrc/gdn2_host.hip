@@ -79,7 +79,7 @@ template <typename T, int K>
 static int gdn2_forward_impl(const Gdn2Plan& p, const void* q, const void* k, const void* v,
                              const void* w, const void* b, const float* g, const float* h0,
                              float* o, float* h_final, void* ws, int save, Launch& L) {
-  constexpr int C = 64, V = K, VT = 16;
+  constexpr int C = 64, V = K, VT = 32;
   Gdn2Chunks<T> ck = gdn2_chunks<T>(p, ws);
   hipStream_t st = L.st;
   int rc = L("gdn2_fwd_intra", [&] {
@@ -89,7 +89,7 @@ static int gdn2_forward_impl(const Gdn2Plan& p, const void* q, const void* k, co
   if (rc) return rc;
   const unsigned nwg = (unsigned)(p.dm.B * p.dm.H * (V / VT));
   return L("gdn2_fwd_state", [&] {
-    hipLaunchKernelGGL((gdn2_fwd_state<T, C, K, V, VT>), dim3(nwg), dim3(256), 0, st, p.dm, ck, h0, o,
+    hipLaunchKernelGGL((gdn2_fwd_state<T, C, K, V, VT>), dim3(nwg), dim3(512), 0, st, p.dm, ck, h0, o,
                        h_final, save);
   });
 }
