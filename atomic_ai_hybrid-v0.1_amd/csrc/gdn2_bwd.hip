@@ -52,8 +52,10 @@ struct DhLds {
   static constexpr int total = off_gl + K * 4;
 };
 
+// Eight waves (two per SIMD): the dh tiles and the dv_new tiles of one V
+// tile split over them by row blocks.
 template <typename T, typename TD, int C, int K, int V, int VT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn2_bwd_dh(
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn2_bwd_dh(
     Gdn2Dims dm, Gdn2Chunks<T> ck, Gdn2Grads<T> gr, const TD* __restrict__ dO,
     const float* __restrict__ dh_final, float* __restrict__ dh0) {
   typedef DhLds<T, C, K, V, VT> L;
@@ -76,12 +78,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int wv_id = wave_id();
   const size_t ldo = (size_t)dm.H * V;
 
+  constexpr int NW = 8, NTHR = 64 * NW;
   constexpr int NTI = VT / 16;
   constexpr int NTH = (K / 16) * NTI;  // dh tiles
-  constexpr int TPW = NTH / 4;
+  constexpr int TPW = NTH / NW;
   constexpr int NTV = (C / 16) * NTI;  // dv_new tiles
-  constexpr int VPW = NTV / 4;
-  static_assert(NTH % 4 == 0 && NTV % 4 == 0, "tiles must split evenly over 4 waves");
+  constexpr int VPW = NTV / NW;
+  static_assert(NTH % NW == 0 && NTV % NW == 0 && TPW >= 1 && VPW >= 1,
+                "tiles must split evenly over the waves");
 
   // dh carry = sanitize(dh_final) (kernel_bwd_b1_dhu.py:18)
   f32x4 hs[TPW];
@@ -96,9 +100,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     store_tile_t(sDht, L::LK, 16 * mi, 16 * ni, hs[t]);
   }
 
-  RegStage<T, C, K> pw, pq, pk;
-  RegStage<T, C, C> pa;
-  RegStage<float, 1, K> pg;
+  RegStage<T, C, K, NTHR> pw, pq, pk;
+  RegStage<T, C, C, NTHR> pa;
+  RegStage<float, 1, K, NTHR> pg;
   auto prefetch = [&](int n) {
     const size_t bhn = (size_t)bh * dm.NT + n;
     pw.load(ck.wt + bhn * C * K, K);
@@ -114,8 +118,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     pa.store(sAqk, L::LC);
     pg.store(sGl, K);
     const TD* src = dO + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0;
-    stage_convert<TD, T, C, VT>(sDO, L::LD, src, ldo);
-    stage_convert<TD, T, C, VT>(sDOs, L::LD, src, ldo, dm.scale);
+    stage_convert<TD, T, C, VT, NTHR>(sDO, L::LD, src, ldo);
+    stage_convert<TD, T, C, VT, NTHR>(sDOs, L::LD, src, ldo, dm.scale);
   };
   prefetch(dm.NT - 1);
   commit(dm.NT - 1);
@@ -125,7 +129,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const size_t bhn = (size_t)bh * dm.NT + n;
     if (n > 0) prefetch(n - 1);
     // dh_next of chunk n = the carry entering this step
-    unstage_rows<T, VT, K>(gr.dhT + bhn * V * K + (size_t)v0 * K, K, sDht, L::LK);
+    unstage_rows<T, VT, K, NTHR>(gr.dhT + bhn * V * K + (size_t)v0 * K, K, sDht, L::LK);
 
     // dv_new = sanitize(Aqk^T dO + kg dh)   (b2:70, b1:30-32)
 #pragma unroll

@@ -116,7 +116,7 @@ static int gdn2_backward_impl(const Gdn2Plan& p, const void* q, const void* k, c
                               const void* dO, const float* dh_final, void* dq, void* dk, void* dv,
                               void* dw, void* db, float* dg, float* dh0, void* ws, bool reuse,
                               Launch& L) {
-  constexpr int C = 64, V = K, VT = 16;
+  constexpr int C = 64, V = K, VT = 32;
   Gdn2Chunks<T> ck = gdn2_chunks<T>(p, ws);
   Gdn2Grads<T> gr = gdn2_grads<T>(p, ws);
   int rc;
@@ -130,7 +130,7 @@ static int gdn2_backward_impl(const Gdn2Plan& p, const void* q, const void* k, c
   const unsigned nseq = (unsigned)(p.dm.B * p.dm.H * (V / VT));
   const unsigned nblk = (unsigned)p.bhn;
   rc = L("gdn2_bwd_dh", [&] {
-    hipLaunchKernelGGL((gdn2_bwd_dh<T, TD, C, K, V, VT>), dim3(nseq), dim3(256), 0, st, p.dm, ck, gr,
+    hipLaunchKernelGGL((gdn2_bwd_dh<T, TD, C, K, V, VT>), dim3(nseq), dim3(512), 0, st, p.dm, ck, gr,
                        (const TD*)dO, dh_final, dh0);
   });
   if (rc) return rc;
