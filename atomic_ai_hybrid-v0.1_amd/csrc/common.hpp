@@ -136,6 +136,23 @@ __device__ __forceinline__ f32x4 tile_mma(f32x4 acc, const T* A, int lda, const 
   return acc;
 }
 
+// NT adjacent column tiles (n0, n0 + 16, ...) of one row block: each A
+// fragment is read once for all of them.
+template <typename T, bool A_T, bool B_T, int NT>
+__device__ __forceinline__ void tile_mma_row(f32x4 (&acc)[NT], const T* A, int lda, const T* B, int ldb,
+                                             int m0, int n0, int K) {
+#pragma unroll 4
+  for (int k0 = 0; k0 < K; k0 += Mma<T>::KS) {
+    typename Mma<T>::frag a = A_T ? Mma<T>::ld_t(A, lda, m0, k0) : Mma<T>::ld_c(A, lda, m0, k0);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      typename Mma<T>::frag b =
+          B_T ? Mma<T>::ld_t(B, ldb, n0 + 16 * t, k0) : Mma<T>::ld_c(B, ldb, n0 + 16 * t, k0);
+      acc[t] = Mma<T>::mma(a, b, acc[t]);
+    }
+  }
+}
+
 // Make this wave's LDS writes visible to its own later LDS reads (no
 // workgroup barrier: only valid for data private to one wave).
 __device__ __forceinline__ void wave_lds_sync() {

@@ -86,6 +86,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int VPW = NTV / NW;
   static_assert(NTH % NW == 0 && NTV % NW == 0 && TPW >= 1 && VPW >= 1,
                 "tiles must split evenly over the waves");
+  // tiles of one row block computed together (sharing their A fragments)
+  constexpr int GV = VPW < NTI ? VPW : NTI, GT = TPW < NTI ? TPW : NTI;
+  static_assert(VPW % GV == 0 && NTI % GV == 0 && TPW % GT == 0 && NTI % GT == 0, "tile groups");
 
   // dh carry = sanitize(dh_final) (kernel_bwd_b1_dhu.py:18)
   f32x4 hs[TPW];
@@ -133,34 +136,47 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     // dv_new = sanitize(Aqk^T dO + kg dh)   (b2:70, b1:30-32)
 #pragma unroll
-    for (int t = 0; t < VPW; ++t) {
-      const int tile = wv_id * VPW + t, mj = tile / NTI, ni = tile % NTI;
+    for (int gi = 0; gi < VPW / GV; ++gi) {
+      const int tile0 = wv_id * VPW + gi * GV, mj = tile0 / NTI, ni0 = tile0 % NTI;
       const int k0 = tri_k0<T>(mj);
-      f32x4 acc = zero4();
-      acc = tile_mma<T, true, true>(acc, sAqk + k0 * L::LC, L::LC, sDO + k0 * L::LD, L::LD,
-                                    16 * mj, 16 * ni, C - k0);
-      acc = tile_mma<T, false, false>(acc, sKg, L::LK, sDht, L::LK, 16 * mj, 16 * ni, K);
+      f32x4 acc[GV];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = sanitize(acc[i]);
-      store_tile_n(gr.dvn + bhn * C * V + v0, V, 16 * mj, 16 * ni, acc);
+      for (int u = 0; u < GV; ++u) acc[u] = zero4();
+      tile_mma_row<T, true, true, GV>(acc, sAqk + k0 * L::LC, L::LC, sDO + k0 * L::LD, L::LD,
+                                      16 * mj, 16 * ni0, C - k0);
+      tile_mma_row<T, false, false, GV>(acc, sKg, L::LK, sDht, L::LK, 16 * mj, 16 * ni0, K);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = -acc[i];
-      store_tile_t(sDvT, L::LC, 16 * mj, 16 * ni, acc);
+      for (int u = 0; u < GV; ++u) {
+        const int ni = ni0 + u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[u][i] = sanitize(acc[u][i]);
+        store_tile_n(gr.dvn + bhn * C * V + v0, V, 16 * mj, 16 * ni, acc[u]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[u][i] = -acc[u][i];
+        store_tile_t(sDvT, L::LC, 16 * mj, 16 * ni, acc[u]);
+      }
     }
     __syncthreads();
 
     // dh = sanitize(qg^T (scale dO) + dh e^{gc_last} - w_pseudo^T dv_new)   (b1:26-37)
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-      const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
-      f32x4 acc = hs[t];
+    for (int gi = 0; gi < TPW / GT; ++gi) {
+      const int tile0 = wv_id * TPW + gi * GT, mi = tile0 / NTI, ni0 = tile0 % NTI;
+      f32x4 acc[GT];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] *= __expf(sGl[16 * mi + tile_row(i)]);
-      acc = tile_mma<T, true, true>(acc, sQ, L::LK, sDOs, L::LD, 16 * mi, 16 * ni, C);
-      acc = tile_mma<T, true, false>(acc, sW, L::LK, sDvT, L::LC, 16 * mi, 16 * ni, C);
+      for (int u = 0; u < GT; ++u) {
+        acc[u] = hs[gi * GT + u];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = sanitize(acc[i]);
-      hs[t] = acc;
+        for (int i = 0; i < 4; ++i) acc[u][i] *= __expf(sGl[16 * mi + tile_row(i)]);
+      }
+      tile_mma_row<T, true, true, GT>(acc, sQ, L::LK, sDOs, L::LD, 16 * mi, 16 * ni0, C);
+      tile_mma_row<T, true, false, GT>(acc, sW, L::LK, sDvT, L::LC, 16 * mi, 16 * ni0, C);
+#pragma unroll
+      for (int u = 0; u < GT; ++u) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[u][i] = sanitize(acc[u][i]);
+        hs[gi * GT + u] = acc[u];
+      }
     }
     __syncthreads();
 #pragma unroll

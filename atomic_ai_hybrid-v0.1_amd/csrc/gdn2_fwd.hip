@@ -433,6 +433,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int NTX = (2 * C / 16) * NTI;
   constexpr int XPW = NTX / NW;
   static_assert(NTX % NW == 0 && XPW >= 1, "output tiles must split evenly over the waves");
+  // tiles of one row block computed together (sharing their A fragments)
+  constexpr int GX = XPW < NTI ? XPW : NTI, GT = TPW < NTI ? TPW : NTI;
+  static_assert(XPW % GX == 0 && NTI % GX == 0 && TPW % GT == 0 && NTI % GT == 0, "tile groups");
 
   RegStage<T, C, K, NTHR> pw, pq, pk;
   RegStage<T, C, C, NTHR> pa;
@@ -464,27 +467,33 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (n + 1 < dm.NT) prefetch(n + 1);
     if (save) unstage_rows<T, VT, K, NTHR>(ck.hT + bhn * V * K + (size_t)v0 * K, K, sHt, L::LK);
 
-    // v_new = u - w_pseudo h ; qh = qg h
+    // v_new = u - w_pseudo h ; qh = qg h   (GX tiles of one row block share the A reads)
     f32x4 xo[XPW];
 #pragma unroll
-    for (int t = 0; t < XPW; ++t) {
-      const int tile = wv_id * XPW + t, mi = tile / NTI, ni = tile % NTI;
+    for (int gi = 0; gi < XPW / GX; ++gi) {
+      const int tile0 = wv_id * XPW + gi * GX, mi = tile0 / NTI, ni0 = tile0 % NTI;
       const bool is_w = mi < C / 16;
-      f32x4 acc = zero4();
-      acc = tile_mma<T, false, false>(acc, is_w ? sW : sQ, L::LK, sHt, L::LK,
-                                      16 * (is_w ? mi : mi - C / 16), 16 * ni, K);
-      if (is_w) {
+      f32x4 acc[GX];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int j = 16 * mi + tile_row(i), vv = 16 * ni + tile_col();
-          acc[i] = to_f(sU[j * L::LU + vv]) - acc[i];
+      for (int u = 0; u < GX; ++u) acc[u] = zero4();
+      tile_mma_row<T, false, false, GX>(acc, is_w ? sW : sQ, L::LK, sHt, L::LK,
+                                        16 * (is_w ? mi : mi - C / 16), 16 * ni0, K);
+#pragma unroll
+      for (int u = 0; u < GX; ++u) {
+        const int ni = ni0 + u;
+        if (is_w) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = 16 * mi + tile_row(i), vv = 16 * ni + tile_col();
+            acc[u][i] = to_f(sU[j * L::LU + vv]) - acc[u][i];
+          }
+          store_tile_t(sVn, L::LC, 16 * mi, 16 * ni, acc[u]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[u][i] *= dm.scale;
         }
-        store_tile_t(sVn, L::LC, 16 * mi, 16 * ni, acc);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] *= dm.scale;
+        xo[gi * GX + u] = acc[u];
       }
-      xo[t] = acc;
     }
     __syncthreads();
     if (save) unstage_rows<T, VT, C, NTHR>(ck.vnT + bhn * V * C + (size_t)v0 * C, C, sVn, L::LC);
@@ -492,35 +501,47 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // o = scale qg h + Aqk v_new   (rows of the qg half)
     float* og = o ? o + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0 : nullptr;
 #pragma unroll
-    for (int t = 0; t < XPW; ++t) {
-      const int tile = wv_id * XPW + t, mi = tile / NTI, ni = tile % NTI;
+    for (int gi = 0; gi < XPW / GX; ++gi) {
+      const int tile0 = wv_id * XPW + gi * GX, mi = tile0 / NTI, ni0 = tile0 % NTI;
       if (mi >= C / 16) {
         const int mo = mi - C / 16;
         int kr = 16 * (mo + 1);
         kr = ((kr + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
         if (kr > C) kr = C;
-        f32x4 acc = tile_mma<T, false, false>(xo[t], sAqk, L::LC, sVn, L::LC, 16 * mo, 16 * ni, kr);
+        f32x4 acc[GX];
+#pragma unroll
+        for (int u = 0; u < GX; ++u) acc[u] = xo[gi * GX + u];
+        tile_mma_row<T, false, false, GX>(acc, sAqk, L::LC, sVn, L::LC, 16 * mo, 16 * ni0, kr);
         if (og) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = 16 * mo + tile_row(i), c = 16 * ni + tile_col();
-            og[(size_t)r * dm.H * V + c] = n2n(acc[i]);
-          }
+          for (int u = 0; u < GX; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int r = 16 * mo + tile_row(i), c = 16 * (ni0 + u) + tile_col();
+              og[(size_t)r * dm.H * V + c] = n2n(acc[u][i]);
+            }
         }
       }
     }
 
     // h = sanitize(h e^{gc_last} + kg^T v_new)
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-      const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
-      f32x4 acc = hs[t];
+    for (int gi = 0; gi < TPW / GT; ++gi) {
+      const int tile0 = wv_id * TPW + gi * GT, mi = tile0 / NTI, ni0 = tile0 % NTI;
+      f32x4 acc[GT];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] *= __expf(sGl[16 * mi + tile_row(i)]);
-      acc = tile_mma<T, true, false>(acc, sKg, L::LK, sVn, L::LC, 16 * mi, 16 * ni, C);
+      for (int u = 0; u < GT; ++u) {
+        acc[u] = hs[gi * GT + u];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = sanitize(acc[i]);
-      hs[t] = acc;
+        for (int i = 0; i < 4; ++i) acc[u][i] *= __expf(sGl[16 * mi + tile_row(i)]);
+      }
+      tile_mma_row<T, true, false, GT>(acc, sKg, L::LK, sVn, L::LC, 16 * mi, 16 * ni0, C);
+#pragma unroll
+      for (int u = 0; u < GT; ++u) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[u][i] = sanitize(acc[u][i]);
+        hs[gi * GT + u] = acc[u];
+      }
     }
     __syncthreads();  // all reads of sHt / sVn / staged chunk done
 #pragma unroll
