@@ -178,6 +178,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // thread item = 8 channels of one row of dt / x / dy, one 16-byte piece of
   // each of the state_pre / dstate rows, one lasta value
   constexpr int PER_ROW = PT / 8, NE = C * PER_ROW, EPT = (NE + NTH - 1) / NTH;
+  // item e -> (row, 8 channels): 16 consecutive items take 16 consecutive rows
+  // at the same columns, so a 16-lane group's 16-byte LDS accesses start 16
+  // rows apart in the bank map instead of four lanes sharing each row
+  auto item_row = [](int e) { return (e % 16) + 16 * (e / (16 * PER_ROW)); };
+  auto item_col = [](int e) { return ((e / 16) % PER_ROW) * 8; };
   constexpr int SPR = N * (int)sizeof(T) / 16, NS = PT * SPR, SPT = (NS + NTH - 1) / NTH;
   Raw8<T> ndt[EPT], nx[EPT];
   Raw8<TD> ndy[EPT];
@@ -189,7 +194,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int it = 0; it < EPT; ++it) {
       const int e = tid + NTH * it;
       if (NE % NTH == 0 || e < NE) {
-        const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
+        const int r = item_row(e), c = item_col(e);
         const size_t o = ((rowb + r) * dm.H + hn) * P + pn + c;
         ndt[it].load(dt + o);
         nx[it].load(x + o);
@@ -247,7 +252,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int it = 0; it < EPT; ++it) {
         const int e = tid + NTH * it;
         if (NE % NTH == 0 || e < NE) {
-          const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
+          const int r = item_row(e), c = item_col(e);
           *reinterpret_cast<uint4*>(sDt + r * L::LPT + c) = rdt[it].v;
           *reinterpret_cast<uint4*>(sX + r * L::LPT + c) = rx[it].v;
           float yv[8], av[8];
@@ -285,7 +290,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int it = 0; it < EPT; ++it) {
           const int e = tid + NTH * it;
           if (NE % NTH == 0 || e < NE) {
-            const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
+            const int r = item_row(e), c = item_col(e);
             float cr[8], cs[8], ce[8];
             load8(sCum + r * L::LC + c, cr);
             load8(sCum + (r & ~15) * L::LC + c, cs);
