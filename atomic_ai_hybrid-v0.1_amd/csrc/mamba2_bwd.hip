@@ -630,29 +630,51 @@ __global__ __launch_bounds__(256) void mamba2_bwd_bc(Mamba2Dims dm, int G, const
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) { accC[rt][ct] = zero4(); accB[rt][ct] = zero4(); }
 
+  // the state_prev / dstate block of the next kb staged in registers, and the
+  // Ydh / W fragments of the next kb (global, this wave's rows) in registers
+  constexpr int KK = KB / Mma<T>::KS;
+  typedef typename Mma<T>::frag frag;
   RegStage<T, KB, NTL> ps, pd;
+  frag ayn[RT][KK], awn[RT][KK];
+  auto load_a = [&](int kb) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int q = 0; q < KK; ++q) {
+        const int m0 = 16 * (RT * wv_id + rt);
+        ayn[rt][q] = Mma<T>::ld_c(yg, HP, m0, kb + q * Mma<T>::KS);
+        awn[rt][q] = Mma<T>::ld_c(wg, HP, m0, kb + q * Mma<T>::KS);
+      }
+  };
   ps.load(sg, N);
   pd.load(dg, N);
+  load_a(0);
   for (int kb = 0; kb < HP; kb += KB) {
+    frag ay[RT][KK], aw[RT][KK];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int q = 0; q < KK; ++q) { ay[rt][q] = ayn[rt][q]; aw[rt][q] = awn[rt][q]; }
     __syncthreads();  // previous block's reads done
     ps.store(sS, L::LK);
     pd.store(sD, L::LK);
     if (kb + KB < HP) {
       ps.load(sg + (size_t)(kb + KB) * N, N);
       pd.load(dg + (size_t)(kb + KB) * N, N);
+      load_a(kb + KB);
     }
     __syncthreads();
 #pragma unroll
-    for (int kk = 0; kk < KB; kk += Mma<T>::KS) {
+    for (int q = 0; q < KK; ++q) {
+      const int kk = q * Mma<T>::KS;
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const int m0 = 16 * (RT * wv_id + rt);
-        const typename Mma<T>::frag ay = Mma<T>::ld_c(yg, HP, m0, kb + kk);
-        const typename Mma<T>::frag aw = Mma<T>::ld_c(wg, HP, m0, kb + kk);
+      for (int ct = 0; ct < CT; ++ct) {
+        const frag bs = Mma<T>::ld_t(sS, L::LK, 16 * ct, kk);
+        const frag bd = Mma<T>::ld_t(sD, L::LK, 16 * ct, kk);
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-          accC[rt][ct] = Mma<T>::mma(ay, Mma<T>::ld_t(sS, L::LK, 16 * ct, kk), accC[rt][ct]);
-          accB[rt][ct] = Mma<T>::mma(aw, Mma<T>::ld_t(sD, L::LK, 16 * ct, kk), accB[rt][ct]);
+        for (int rt = 0; rt < RT; ++rt) {
+          accC[rt][ct] = Mma<T>::mma(ay[rt][q], bs, accC[rt][ct]);
+          accB[rt][ct] = Mma<T>::mma(aw[rt][q], bd, accB[rt][ct]);
         }
       }
     }
