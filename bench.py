@@ -42,8 +42,8 @@ CPU_THREADS_MAX = 16
 def gdn2_kernel_model(B, T, H, K, V, C, es=2, save=True):
     """Algorithmic (flops, HBM bytes) per launch of each GDN2 kernel: every
     operand the kernel must read and every result it must write, once.  U
-    counts (batch, head, chunk) units; operands are bf16 (es bytes), g and
-    the backward's per-chunk gradients float32, o float32."""
+    counts (batch, head, chunk) units; operands and the backward's per-chunk
+    intermediates are bf16 (es bytes), g, gc_last and o float32."""
     U = B * H * (T // C)
     CK, CV, CC, KV = C * K, C * V, C * C, K * V
     return {
@@ -59,15 +59,15 @@ def gdn2_kernel_model(B, T, H, K, V, C, es=2, save=True):
                              + CV * es + KV * es) + B * H * KV * 4),         # dv_new, dh_next; dh0
         "gdn2_bwd_hgrad": (U * (2 * CC * V + 6 * C * KV),
                            U * (CV * es + CV * es + 2 * KV * es + CV * es + K * 4  # dO dvn h dh vn gcl
-                                + CC * es + CK * 4 + CK * es + CK * 4 + K * 4)),   # daqk dqg dwt dkg rlast
+                                + CC * es + 3 * CK * es + K * 4)),           # daqk dqg dwt dkg rlast
         "gdn2_bwd_wy_a": (U * (2 * CC * K + 2 * CC * V + 4 * C ** 3),
                           U * (CC * es + CK * es + CV * es + 2 * CK * es + 2 * CV * es + CK * 4  # ainv dwt dvn k b v w g
                                + CC * es)),                                  # dakk
         "gdn2_bwd_wy_b": (U * (2 * CC * K + 2 * CC * V),
                           U * (CC * es + CK * es + CV * es + 2 * CV * es     # ainv dwt dvn v w
-                               + CK * 4 + 2 * CV * es)),                     # dkb dw dv
+                               + CK * es + 2 * CV * es)),                    # dkb dw dv
         "gdn2_bwd_intra": (U * 8 * CC * K,
-                           U * (3 * CK * es + CK * 4 + 2 * CC * es + 3 * CK * 4 + K * 4  # q k b g daqk dakk dqg dkb dkg rlast
+                           U * (3 * CK * es + CK * 4 + 2 * CC * es + 3 * CK * es + K * 4  # q k b g daqk dakk dqg dkb dkg rlast
                                 + 3 * CK * es + CK * 4)),                    # dq dk db dg
     }
 
