@@ -303,7 +303,8 @@ template <typename T, int C, int N, int PT>
 struct YLds {
   static constexpr int PAD = Pad<T>::v;
   static constexpr int LPT = PT + PAD, LN = N + PAD;
-  static constexpr int LC = PT + 1;  // fp32 rows, padded against bank conflicts
+  // fp32 rows: 16-byte aligned, rows 4 apart 16 banks apart (tile-layout reads)
+  static constexpr int LC = PT + 4;
   static constexpr int NSEG = 256 / PT;
   static constexpr int off_cum = 0;
   static constexpr int off_dbx = off_cum + C * LC * 4;
@@ -352,27 +353,40 @@ __global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __
   constexpr int NB = C / 16, BPW = NB / 4, YNI = PT / 16, KN = N / Mma<T>::KS;
   static_assert(NB % 4 == 0, "row blocks must split evenly over 4 waves");
 
+  // thread item = 8 channels of one row; 16 consecutive items take 16
+  // consecutive rows (conflict-free 16-byte LDS accesses)
   constexpr int PER_ROW = PT / 8, NE = C * PER_ROW, EPT = NE / 256;
   static_assert(NE % 256 == 0, "slice must split evenly over the workgroup");
+  auto item_row = [](int e) { return (e % 16) + 16 * (e / (16 * PER_ROW)); };
+  auto item_col = [](int e) { return ((e / 16) % PER_ROW) * 8; };
   Raw8<T> rdt[EPT], rx[EPT];
 #pragma unroll
   for (int i = 0; i < EPT; ++i) {
-    const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
+    const int e = threadIdx.x + 256 * i, r = item_row(e), c = item_col(e);
     rdt[i].load(dt + base + r * rsx + c);
     rx[i].load(x + base + r * rsx + c);
   }
   stage_rows<T, PT, N>(sSt, L::LN, ck.state_pre + (((size_t)bn * dm.H + h) * P + p0) * N, N);
   int flag = 0;
+  float dbx[EPT][8];
 #pragma unroll
   for (int i = 0; i < EPT; ++i) {
-    const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
+    const int e = threadIdx.x + 256 * i, r = item_row(e), c = item_col(e);
+    float av[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float a = rdt[i][j] * Ah;
       flag |= a > 0.f;
-      sCum[r * L::LC + c + j] = sanitize(a, kClipDecay);
-      sDbx[r * L::LC + c + j] = sanitize(rdt[i][j] * rx[i][j]);
+      av[j] = sanitize(a, kClipDecay);
+      dbx[i][j] = sanitize(rdt[i][j] * rx[i][j]);
     }
+    store8(sCum + r * L::LC + c, av);
+    store8(sDbx + r * L::LC + c, dbx[i]);
+  }
+  // the 16 zero rows below the chunk (read by the K = 32 steps of the last block)
+  if (threadIdx.x < 16 * PER_ROW) {
+    const int r = C + threadIdx.x / PER_ROW, c = (threadIdx.x % PER_ROW) * 8;
+    *reinterpret_cast<uint4*>(sV + r * L::LPT + c) = make_uint4(0u, 0u, 0u, 0u);
   }
   __syncthreads();
   column_cumsum<C, PT, L::LC>(sCum, sTot);
@@ -384,10 +398,15 @@ __global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __
   // a positive step exponent (or too steep a block) is evaluated pairwise
   const bool exact = __syncthreads_or(flag);
   if (!exact) {
-    for (int e = threadIdx.x; e < (C + 16) * PT; e += 256) {
-      const int j = e / PT, p = e % PT;
-      const float v = j < C ? __expf(sCum[(j | 15) * L::LC + p] - sCum[j * L::LC + p]) * sDbx[j * L::LC + p] : 0.f;
-      sV[j * L::LPT + p] = from_f<T>(v);
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int e = threadIdx.x + 256 * i, r = item_row(e), c = item_col(e);
+      float cr[8], ce[8], v[8];
+      load8(sCum + r * L::LC + c, cr);
+      load8(sCum + (r | 15) * L::LC + c, ce);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = __expf(ce[j] - cr[j]) * dbx[i][j];
+      store8(sV + r * L::LPT + c, v);
     }
   }
   __syncthreads();
