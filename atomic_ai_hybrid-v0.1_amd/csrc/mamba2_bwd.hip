@@ -162,9 +162,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
   for (int i = 0; i < BCPW; ++i) acc_bc[i] = zero4();
   auto bc_tile = [](int k, int& I, int& J) {  // k-th lower tile in row order
-    I = 0;
-    while (k > I) { k -= I + 1; ++I; }
-    J = k;
+    int i = 0;
+#pragma unroll
+    for (int t = 1; t < NB; ++t) i += k >= t * (t + 1) / 2;
+    I = i;
+    J = k - i * (i + 1) / 2;
   };
 
   // y-shaped tiles [C][PT] as (row block I, column tile ni) units: wave w owns
