@@ -104,6 +104,14 @@ struct IntraLds {
   static constexpr int off_gl = off_tot + (TOT > 4 * 16 * 17 * 4 ? TOT : 4 * 16 * 17 * 4);
   static constexpr int off_flag = off_gl + K * 4;
   static constexpr int total = off_flag + 16;
+  // phase 4 (operand-type path): per-wave [16][LS] staging of one row block of
+  // w_pseudo / u, placed over the operands that are dead by then (q, k, the
+  // fp32 Akk / inverse), after the operand-type inverse
+  static constexpr int LS = (K > V ? K : V) + PAD;
+  static constexpr int off_stage =
+      alias_a ? ((off_af + C * (C + PAD) * (int)sizeof(T) + 15) / 16) * 16 : 0;
+  static constexpr int stage_end = off_stage + 4 * 16 * LS * (int)sizeof(T);
+  static constexpr bool stage_fits = stage_end <= off_b && (alias_a || stage_end <= off_af);
   static_assert(RS >= 1 && RSV >= 1, "chunk too small for the thread mapping");
   static_assert(2 * OPK >= C * K * 4, "gc scratch of the exact path must fit in sQ+sK");
 };
@@ -351,22 +359,57 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
   // ---- phase 4: w_pseudo = A kb, u = A wv (gdn2_wy_reference.py:92-96)
   T* g_wt = ck.wt + (size_t)bhn * C * K;
   T* g_u = ck.u + (size_t)bhn * C * V;
-  constexpr int TW = NB * (K / 16), TU = NB * (V / 16);
-  for (int job = wv_id; job < TW + TU; job += 4) {
-    const bool isu = job >= TW;
-    const int jj = isu ? job - TW : job;
-    const int nbk = isu ? V / 16 : K / 16;
-    const int mi = jj / nbk, ni = jj % nbk;
-    int kr = 16 * (mi + 1);
-    kr = ((kr + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
-    if (kr > C) kr = C;
-    f32x4 acc = zero4();
-    if (isu) acc = tile_mma<T, false, true>(acc, opA, ldA, sW, L::LV, 16 * mi, 16 * ni, kr);
-    else acc = tile_mma<T, false, true>(acc, opA, ldA, sB, L::LK, 16 * mi, 16 * ni, kr);
+  if constexpr (sizeof(T) == 2 && L::stage_fits) {
+    // one row block per wave: its column tiles share the A reads, go through
+    // the wave's LDS staging rows and leave as 16-byte row pieces
+    T* stg = reinterpret_cast<T*>(lds + L::off_stage) + wv_id * 16 * L::LS;
+    auto row_block = [&](int mi, int kr, const T* Bop, int ldb, auto ncol, T* gout) {
+      constexpr int NC = decltype(ncol)::value;
+      f32x4 acc[NC / 16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = n2n(acc[i]);
-    if (isu) store_tile_n(g_u, V, 16 * mi, 16 * ni, acc);
-    else store_tile_n(g_wt, K, 16 * mi, 16 * ni, acc);
+      for (int t = 0; t < NC / 16; ++t) acc[t] = zero4();
+      tile_mma_row<T, false, true, NC / 16>(acc, opA, ldA, Bop, ldb, 16 * mi, 0, kr);
+#pragma unroll
+      for (int t = 0; t < NC / 16; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] = n2n(acc[t][i]);
+        store_tile_n(stg, L::LS, 0, 16 * t, acc[t]);
+      }
+      wave_lds_sync();
+      constexpr int PR = NC / 8;  // 16-byte pieces per row
+#pragma unroll
+      for (int e = lane_id(); e < 16 * PR; e += 64) {
+        const int r = e / PR, c = (e % PR) * 8;
+        *reinterpret_cast<uint4*>(gout + (size_t)(16 * mi + r) * NC + c) =
+            *reinterpret_cast<const uint4*>(stg + r * L::LS + c);
+      }
+      wave_lds_sync();  // the staging rows are rewritten next
+    };
+    for (int mi = wv_id; mi < NB; mi += 4) {
+      int kr = 16 * (mi + 1);
+      kr = ((kr + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
+      if (kr > C) kr = C;
+      row_block(mi, kr, sB, L::LK, std::integral_constant<int, K>(), g_wt);
+      row_block(mi, kr, sW, L::LV, std::integral_constant<int, V>(), g_u);
+    }
+  } else {
+    constexpr int TW = NB * (K / 16), TU = NB * (V / 16);
+    for (int job = wv_id; job < TW + TU; job += 4) {
+      const bool isu = job >= TW;
+      const int jj = isu ? job - TW : job;
+      const int nbk = isu ? V / 16 : K / 16;
+      const int mi = jj / nbk, ni = jj % nbk;
+      int kr = 16 * (mi + 1);
+      kr = ((kr + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
+      if (kr > C) kr = C;
+      f32x4 acc = zero4();
+      if (isu) acc = tile_mma<T, false, true>(acc, opA, ldA, sW, L::LV, 16 * mi, 16 * ni, kr);
+      else acc = tile_mma<T, false, true>(acc, opA, ldA, sB, L::LK, 16 * mi, 16 * ni, kr);
+  #pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = n2n(acc[i]);
+      if (isu) store_tile_n(g_u, V, 16 * mi, 16 * ni, acc);
+      else store_tile_n(g_wt, K, 16 * mi, 16 * ni, acc);
+    }
   }
 }
 
