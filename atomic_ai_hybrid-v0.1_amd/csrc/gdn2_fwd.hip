@@ -336,11 +336,14 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
   int ldA;
   if constexpr (sizeof(T) == 2) {
     T* sAb = reinterpret_cast<T*>(lds + L::off_af);  // Akk is dead
-    for (int e = tid; e < C * C; e += 256) {
-      const int i = e / C, j = e % C;
-      const float x = n2n(sX[i * L::LA + j]);
-      sAb[i * (C + Pad<T>::v) + j] = from_f<T>(x);
-      g_ainv[i * C + j] = from_f<T>(x);
+    for (int e = tid; e < C * C / 8; e += 256) {  // 8 consecutive columns per item
+      const int i = e / (C / 8), j = (e % (C / 8)) * 8;
+      float x[8];
+      load8(sX + i * L::LA + j, x);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) x[t] = n2n(x[t]);
+      store8(sAb + i * (C + Pad<T>::v) + j, x);
+      store8(g_ainv + i * C + j, x);
     }
     opA = sAb;
     ldA = C + Pad<T>::v;
