@@ -803,15 +803,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[rr][j] = sGc[r * L::LG + cg * 8 + j] + (rr + 1 < M::RS ? v[rr + 1][j] : 0.f);
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sTot[seg * KH + cg * 8 + j] = v[0][j];
-    __syncthreads();
     float off[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) off[j] = 0.f;
-    for (int s2 = seg + 1; s2 < M::NSEG; ++s2)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) off[j] += sTot[s2 * KH + cg * 8 + j];
+    seg_scan8<M::NCG, true>(v[0], off, sTot);
 #pragma unroll
     for (int rr = 0; rr < M::RS; ++rr) {
       const int r = seg * M::RS + rr;

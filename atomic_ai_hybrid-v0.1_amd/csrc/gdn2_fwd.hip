@@ -35,6 +35,41 @@ struct ColMap {
   static_assert(RS >= 1, "chunk too small for the thread mapping");
 };
 
+// Exclusive scan over the row segments of a ColMap pass: t holds this
+// thread's segment total for its 8 columns; out gets the sum over the lower
+// segments (REV = false) or the higher ones (REV = true).  Within a wave by
+// lane shuffles, across the 4 waves through sW (4 * K floats).
+template <int NCG, bool REV>
+__device__ __forceinline__ void seg_scan8(const float (&t)[8], float (&out)[8], float* sW) {
+  constexpr int SPW = 64 / NCG;  // segments per wave
+  static_assert(SPW * NCG == 64, "column groups must tile a wave");
+  const int lane = lane_id(), w = wave_id(), sl = lane / NCG, cg = lane % NCG;
+  float x[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) x[j] = t[j];
+#pragma unroll
+  for (int d = 1; d < SPW; d <<= 1) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float y = REV ? __shfl_down(x[j], d * NCG) : __shfl_up(x[j], d * NCG);
+      if (REV ? (sl + d < SPW) : (sl >= d)) x[j] += y;
+    }
+  }
+  if (sl == (REV ? 0 : SPW - 1)) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sW[w * NCG * 8 + cg * 8 + j] = x[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 8; ++j) out[j] = x[j] - t[j];
+#pragma unroll
+  for (int w2 = 0; w2 < 4; ++w2)
+    if (REV ? w2 > w : w2 < w) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) out[j] += sW[w2 * NCG * 8 + cg * 8 + j];
+    }
+}
+
 // gc = cumsum(g) over one chunk (gdn2_wy_reference.py:63) for this thread's
 // RS rows x 8 columns.  Writes gc_last to sGl[K] (sTot: NSEG*K floats of
 // scratch).  Returns, uniformly over the workgroup, whether the factorised
@@ -57,15 +92,8 @@ __device__ __forceinline__ bool chunk_cumsum(const float* __restrict__ g, size_t
   for (int rr = 1; rr < M::RS; ++rr)
 #pragma unroll
     for (int j = 0; j < 8; ++j) gcr[rr][j] += gcr[rr - 1][j];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) sTot[seg * K + cg * 8 + j] = gcr[M::RS - 1][j];
-  __syncthreads();
   float off[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) off[j] = 0.f;
-  for (int s = 0; s < seg; ++s)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) off[j] += sTot[s * K + cg * 8 + j];
+  seg_scan8<M::NCG, false>(gcr[M::RS - 1], off, sTot);
 #pragma unroll
   for (int rr = 0; rr < M::RS; ++rr)
 #pragma unroll
