@@ -36,6 +36,7 @@ GDN2 = dict(B=4, T=8192, H=16, K=128, V=128, C=64)
 MAMBA2 = dict(B=4, T=8192, H=16, P=128, N=128, C=128)
 CPU_SAMPLE_T = 2048        # tokens of the bounded CPU sample (batch 1, same heads)
 CPU_THREADS_MAX = 16
+CALIB_BYTES = 256 << 20    # the --calib-copy copy: 256 MiB read + 256 MiB written
 
 
 # --------------------------------------------------------------------------- models
@@ -126,6 +127,21 @@ def roofline(flops, nbytes, seconds):
                 frac=achieved / (MFMA_BF16_PEAK / 1e12))
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary
+    (two rocprofv3 --pmc runs, FETCH_SIZE then WRITE_SIZE, each scaled by the
+    same counter's reading for a plain copy of CALIB_BYTES), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("kernel") != kernel:
+        return None
+    return int(t["bytes_per_launch"])
+
+
 # --------------------------------------------------------------------------- CPU baseline
 def cpu_baseline(sample_t=CPU_SAMPLE_T):
     """Times the float32 restatement (oracle/) of the reference's GDN2 WY
@@ -166,6 +182,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="run one plain device copy of CALIB_BYTES before the steps (the reference "
+                         "dispatch for scaling FETCH_SIZE / WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -208,6 +227,13 @@ def main():
         M2.backward(dt, x, Bm, Cm, A, m["C"], dy, workspace=m_ws, reuse=True, timer=t[3])
         if i is not None:
             ev[i][2].record()
+
+    if args.calib_copy:
+        src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     for _ in range(args.warmup):
         step()
@@ -254,7 +280,7 @@ def main():
     rf = roofline(fl, by, kernels[dom]["ms_per_launch"] / 1e3)
     rf = {k_: (round(v_, 4) if isinstance(v_, float) else v_) for k_, v_ in rf.items()}
     rf["kernel"] = dom
-    rf["traffic"] = None
+    rf["traffic"] = measured_traffic(dom)
 
     cpu = None if args.no_cpu else cpu_baseline()
 
