@@ -511,120 +511,132 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int GX = XPW < NTI ? XPW : NTI, GT = TPW < NTI ? TPW : NTI;
   static_assert(XPW % GX == 0 && NTI % GX == 0 && TPW % GT == 0 && NTI % GT == 0, "tile groups");
 
-  RegStage<T, C, K, NTHR> pw, pq, pk;
-  RegStage<T, C, C, NTHR> pa;
-  RegStage<T, C, VT, NTHR> pu;
-  RegStage<float, 1, K, NTHR> pg;
-  auto prefetch = [&](int n) {
+  // the chunk operands move global -> registers -> LDS; two register sets
+  // keep the loads of chunk n + 2 in flight while chunk n computes
+  struct Stage {
+    RegStage<T, C, K, NTHR> w, q, k;
+    RegStage<T, C, C, NTHR> a;
+    RegStage<T, C, VT, NTHR> u;
+    RegStage<float, 1, K, NTHR> g;
+  };
+  auto prefetch = [&](Stage& S, int n) {
     const size_t bhn = (size_t)bh * dm.NT + n;
-    pw.load(ck.wt + bhn * C * K, K);
-    pq.load(ck.qg + bhn * C * K, K);
-    pk.load(ck.kg + bhn * C * K, K);
-    pa.load(ck.aqk + bhn * C * C, C);
-    pu.load(ck.u + bhn * C * V + v0, V);
-    pg.load(ck.gcl + bhn * K, K);
+    S.w.load(ck.wt + bhn * C * K, K);
+    S.q.load(ck.qg + bhn * C * K, K);
+    S.k.load(ck.kg + bhn * C * K, K);
+    S.a.load(ck.aqk + bhn * C * C, C);
+    S.u.load(ck.u + bhn * C * V + v0, V);
+    S.g.load(ck.gcl + bhn * K, K);
   };
-  auto commit = [&]() {
-    pw.store(sW, L::LK);
-    pq.store(sQ, L::LK);
-    pk.store(sKg, L::LK);
-    pa.store(sAqk, L::LC);
-    pu.store(sU, L::LU);
-    pg.store(sGl, K);
+  auto commit = [&](const Stage& S) {
+    S.w.store(sW, L::LK);
+    S.q.store(sQ, L::LK);
+    S.k.store(sKg, L::LK);
+    S.a.store(sAqk, L::LC);
+    S.u.store(sU, L::LU);
+    S.g.store(sGl, K);
   };
-  prefetch(0);
-  commit();
+  Stage s0, s1;
+  prefetch(s0, 0);
+  commit(s0);
   __syncthreads();
+  if (dm.NT > 1) prefetch(s0, 1);
+  if (dm.NT > 2) prefetch(s1, 2);
 
-  for (int n = 0; n < dm.NT; ++n) {
+  // one chunk step; S holds chunk n + 1 on entry and is refilled with chunk n + 3
+  auto chunk_step = [&](int n, Stage& S) {
     const size_t bhn = (size_t)bh * dm.NT + n;
-    if (n + 1 < dm.NT) prefetch(n + 1);
-    if (save) unstage_rows<T, VT, K, NTHR>(ck.hT + bhn * V * K + (size_t)v0 * K, K, sHt, L::LK);
+      if (save) unstage_rows<T, VT, K, NTHR>(ck.hT + bhn * V * K + (size_t)v0 * K, K, sHt, L::LK);
 
-    // v_new = u - w_pseudo h ; qh = qg h   (GX tiles of one row block share the A reads)
-    f32x4 xo[XPW];
-#pragma unroll
-    for (int gi = 0; gi < XPW / GX; ++gi) {
-      const int tile0 = wv_id * XPW + gi * GX, mi = tile0 / NTI, ni0 = tile0 % NTI;
-      const bool is_w = mi < C / 16;
-      f32x4 acc[GX];
-#pragma unroll
-      for (int u = 0; u < GX; ++u) acc[u] = zero4();
-      tile_mma_row<T, false, false, GX>(acc, is_w ? sW : sQ, L::LK, sHt, L::LK,
-                                        16 * (is_w ? mi : mi - C / 16), 16 * ni0, K);
-#pragma unroll
-      for (int u = 0; u < GX; ++u) {
-        const int ni = ni0 + u;
-        if (is_w) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int j = 16 * mi + tile_row(i), vv = 16 * ni + tile_col();
-            acc[u][i] = to_f(sU[j * L::LU + vv]) - acc[u][i];
-          }
-          store_tile_t(sVn, L::LC, 16 * mi, 16 * ni, acc[u]);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[u][i] *= dm.scale;
-        }
-        xo[gi * GX + u] = acc[u];
-      }
-    }
-    __syncthreads();
-    if (save) unstage_rows<T, VT, C, NTHR>(ck.vnT + bhn * V * C + (size_t)v0 * C, C, sVn, L::LC);
-
-    // o = scale qg h + Aqk v_new   (rows of the qg half)
-    float* og = o ? o + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0 : nullptr;
-#pragma unroll
-    for (int gi = 0; gi < XPW / GX; ++gi) {
-      const int tile0 = wv_id * XPW + gi * GX, mi = tile0 / NTI, ni0 = tile0 % NTI;
-      if (mi >= C / 16) {
-        const int mo = mi - C / 16;
-        int kr = 16 * (mo + 1);
-        kr = ((kr + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
-        if (kr > C) kr = C;
+      // v_new = u - w_pseudo h ; qh = qg h   (GX tiles of one row block share the A reads)
+      f32x4 xo[XPW];
+  #pragma unroll
+      for (int gi = 0; gi < XPW / GX; ++gi) {
+        const int tile0 = wv_id * XPW + gi * GX, mi = tile0 / NTI, ni0 = tile0 % NTI;
+        const bool is_w = mi < C / 16;
         f32x4 acc[GX];
-#pragma unroll
-        for (int u = 0; u < GX; ++u) acc[u] = xo[gi * GX + u];
-        tile_mma_row<T, false, false, GX>(acc, sAqk, L::LC, sVn, L::LC, 16 * mo, 16 * ni0, kr);
-        if (og) {
-#pragma unroll
-          for (int u = 0; u < GX; ++u)
-#pragma unroll
+  #pragma unroll
+        for (int u = 0; u < GX; ++u) acc[u] = zero4();
+        tile_mma_row<T, false, false, GX>(acc, is_w ? sW : sQ, L::LK, sHt, L::LK,
+                                          16 * (is_w ? mi : mi - C / 16), 16 * ni0, K);
+  #pragma unroll
+        for (int u = 0; u < GX; ++u) {
+          const int ni = ni0 + u;
+          if (is_w) {
+  #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const int r = 16 * mo + tile_row(i), c = 16 * (ni0 + u) + tile_col();
-              og[(size_t)r * dm.H * V + c] = n2n(acc[u][i]);
+              const int j = 16 * mi + tile_row(i), vv = 16 * ni + tile_col();
+              acc[u][i] = to_f(sU[j * L::LU + vv]) - acc[u][i];
             }
+            store_tile_t(sVn, L::LC, 16 * mi, 16 * ni, acc[u]);
+          } else {
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) acc[u][i] *= dm.scale;
+          }
+          xo[gi * GX + u] = acc[u];
         }
       }
-    }
+      __syncthreads();
+      if (save) unstage_rows<T, VT, C, NTHR>(ck.vnT + bhn * V * C + (size_t)v0 * C, C, sVn, L::LC);
 
-    // h = sanitize(h e^{gc_last} + kg^T v_new)
-#pragma unroll
-    for (int gi = 0; gi < TPW / GT; ++gi) {
-      const int tile0 = wv_id * TPW + gi * GT, mi = tile0 / NTI, ni0 = tile0 % NTI;
-      f32x4 acc[GT];
-#pragma unroll
-      for (int u = 0; u < GT; ++u) {
-        acc[u] = hs[gi * GT + u];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[u][i] *= __expf(sGl[16 * mi + tile_row(i)]);
+      // o = scale qg h + Aqk v_new   (rows of the qg half)
+      float* og = o ? o + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0 : nullptr;
+  #pragma unroll
+      for (int gi = 0; gi < XPW / GX; ++gi) {
+        const int tile0 = wv_id * XPW + gi * GX, mi = tile0 / NTI, ni0 = tile0 % NTI;
+        if (mi >= C / 16) {
+          const int mo = mi - C / 16;
+          int kr = 16 * (mo + 1);
+          kr = ((kr + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
+          if (kr > C) kr = C;
+          f32x4 acc[GX];
+  #pragma unroll
+          for (int u = 0; u < GX; ++u) acc[u] = xo[gi * GX + u];
+          tile_mma_row<T, false, false, GX>(acc, sAqk, L::LC, sVn, L::LC, 16 * mo, 16 * ni0, kr);
+          if (og) {
+  #pragma unroll
+            for (int u = 0; u < GX; ++u)
+  #pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int r = 16 * mo + tile_row(i), c = 16 * (ni0 + u) + tile_col();
+                og[(size_t)r * dm.H * V + c] = n2n(acc[u][i]);
+              }
+          }
+        }
       }
-      tile_mma_row<T, true, false, GT>(acc, sKg, L::LK, sVn, L::LC, 16 * mi, 16 * ni0, C);
-#pragma unroll
-      for (int u = 0; u < GT; ++u) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[u][i] = sanitize(acc[u][i]);
-        hs[gi * GT + u] = acc[u];
+
+      // h = sanitize(h e^{gc_last} + kg^T v_new)
+  #pragma unroll
+      for (int gi = 0; gi < TPW / GT; ++gi) {
+        const int tile0 = wv_id * TPW + gi * GT, mi = tile0 / NTI, ni0 = tile0 % NTI;
+        f32x4 acc[GT];
+  #pragma unroll
+        for (int u = 0; u < GT; ++u) {
+          acc[u] = hs[gi * GT + u];
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) acc[u][i] *= __expf(sGl[16 * mi + tile_row(i)]);
+        }
+        tile_mma_row<T, true, false, GT>(acc, sKg, L::LK, sVn, L::LC, 16 * mi, 16 * ni0, C);
+  #pragma unroll
+        for (int u = 0; u < GT; ++u) {
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) acc[u][i] = sanitize(acc[u][i]);
+          hs[gi * GT + u] = acc[u];
+        }
       }
-    }
-    __syncthreads();  // all reads of sHt / sVn / staged chunk done
-#pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-      const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
-      store_tile_t(sHt, L::LK, 16 * mi, 16 * ni, hs[t]);
-    }
-    if (n + 1 < dm.NT) commit();
+      __syncthreads();  // all reads of sHt / sVn / staged chunk done
+  #pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
+        store_tile_t(sHt, L::LK, 16 * mi, 16 * ni, hs[t]);
+      }
+    if (n + 1 < dm.NT) commit(S);
+    if (n + 3 < dm.NT) prefetch(S, n + 3);
     __syncthreads();
+  };
+  for (int n = 0; n < dm.NT; n += 2) {
+    chunk_step(n, s0);
+    if (n + 1 < dm.NT) chunk_step(n + 1, s1);
   }
   if (h_final) {
 #pragma unroll
