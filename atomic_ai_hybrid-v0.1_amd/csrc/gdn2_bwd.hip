@@ -103,89 +103,117 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     store_tile_t(sDht, L::LK, 16 * mi, 16 * ni, hs[t]);
   }
 
-  RegStage<T, C, K, NTHR> pw, pq, pk;
-  RegStage<T, C, C, NTHR> pa;
-  RegStage<float, 1, K, NTHR> pg;
-  auto prefetch = [&](int n) {
+  // the chunk operands (and dO) move global -> registers -> LDS; two register
+  // sets keep the loads of chunk n - 2 in flight while chunk n computes
+  struct Stage {
+    RegStage<T, C, K, NTHR> w, q, k;
+    RegStage<T, C, C, NTHR> a;
+    RegStage<float, 1, K, NTHR> g;
+    RegStage<TD, C, VT, NTHR> o;
+  };
+  auto prefetch = [&](Stage& S, int n) {
     const size_t bhn = (size_t)bh * dm.NT + n;
-    pw.load(ck.wt + bhn * C * K, K);
-    pq.load(ck.qg + bhn * C * K, K);
-    pk.load(ck.kg + bhn * C * K, K);
-    pa.load(ck.aqk + bhn * C * C, C);
-    pg.load(ck.gcl + bhn * K, K);
+    S.w.load(ck.wt + bhn * C * K, K);
+    S.q.load(ck.qg + bhn * C * K, K);
+    S.k.load(ck.kg + bhn * C * K, K);
+    S.a.load(ck.aqk + bhn * C * C, C);
+    S.g.load(ck.gcl + bhn * K, K);
+    S.o.load(dO + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0, ldo);
   };
-  auto commit = [&](int n) {
-    pw.store(sW, L::LK);
-    pq.store(sQ, L::LK);
-    pk.store(sKg, L::LK);
-    pa.store(sAqk, L::LC);
-    pg.store(sGl, K);
-    const TD* src = dO + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0;
-    stage_convert<TD, T, C, VT, NTHR>(sDO, L::LD, src, ldo);
-    stage_convert<TD, T, C, VT, NTHR>(sDOs, L::LD, src, ldo, dm.scale);
+  auto commit = [&](const Stage& S) {
+    S.w.store(sW, L::LK);
+    S.q.store(sQ, L::LK);
+    S.k.store(sKg, L::LK);
+    S.a.store(sAqk, L::LC);
+    S.g.store(sGl, K);
+    // dO and scale dO in the operand dtype
+    typedef RegStage<TD, C, VT, NTHR> RO;
+#pragma unroll
+    for (int i = 0; i < RO::PT; ++i) {
+      const int e = threadIdx.x + NTHR * i;
+      if (RO::N % NTHR == 0 || e < RO::N) {
+        const int r = e / RO::PER_ROW, c = (e % RO::PER_ROW) * RO::VEC;
+        const uint4 raw = S.o.piece(i);
+        const TD* v = reinterpret_cast<const TD*>(&raw);
+#pragma unroll
+        for (int j = 0; j < RO::VEC; ++j) {
+          const float x = to_f(v[j]);
+          sDO[r * L::LD + c + j] = from_f<T>(x);
+          sDOs[r * L::LD + c + j] = from_f<T>(x * dm.scale);
+        }
+      }
+    }
   };
-  prefetch(dm.NT - 1);
-  commit(dm.NT - 1);
+  Stage s0, s1;
+  prefetch(s0, dm.NT - 1);
+  commit(s0);
   __syncthreads();
+  if (dm.NT > 1) prefetch(s0, dm.NT - 2);
+  if (dm.NT > 2) prefetch(s1, dm.NT - 3);
 
-  for (int n = dm.NT - 1; n >= 0; --n) {
+  // one chunk step (reverse); S holds chunk n - 1 on entry and is refilled with chunk n - 3
+  auto chunk_step = [&](int n, Stage& S) {
     const size_t bhn = (size_t)bh * dm.NT + n;
-    if (n > 0) prefetch(n - 1);
-    // dh_next of chunk n = the carry entering this step
-    unstage_rows<T, VT, K, NTHR>(gr.dhT + bhn * V * K + (size_t)v0 * K, K, sDht, L::LK);
+      // dh_next of chunk n = the carry entering this step
+      unstage_rows<T, VT, K, NTHR>(gr.dhT + bhn * V * K + (size_t)v0 * K, K, sDht, L::LK);
 
-    // dv_new = sanitize(Aqk^T dO + kg dh)   (b2:70, b1:30-32)
-#pragma unroll
-    for (int gi = 0; gi < VPW / GV; ++gi) {
-      const int tile0 = wv_id * VPW + gi * GV, mj = tile0 / NTI, ni0 = tile0 % NTI;
-      const int k0 = tri_k0<T>(mj);
-      f32x4 acc[GV];
-#pragma unroll
-      for (int u = 0; u < GV; ++u) acc[u] = zero4();
-      tile_mma_row<T, true, true, GV>(acc, sAqk + k0 * L::LC, L::LC, sDO + k0 * L::LD, L::LD,
-                                      16 * mj, 16 * ni0, C - k0);
-      tile_mma_row<T, false, false, GV>(acc, sKg, L::LK, sDht, L::LK, 16 * mj, 16 * ni0, K);
-#pragma unroll
-      for (int u = 0; u < GV; ++u) {
-        const int ni = ni0 + u;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[u][i] = sanitize(acc[u][i]);
-        store_tile_n(gr.dvn + bhn * C * V + v0, V, 16 * mj, 16 * ni, acc[u]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[u][i] = -acc[u][i];
-        store_tile_t(sDvT, L::LC, 16 * mj, 16 * ni, acc[u]);
+      // dv_new = sanitize(Aqk^T dO + kg dh)   (b2:70, b1:30-32)
+  #pragma unroll
+      for (int gi = 0; gi < VPW / GV; ++gi) {
+        const int tile0 = wv_id * VPW + gi * GV, mj = tile0 / NTI, ni0 = tile0 % NTI;
+        const int k0 = tri_k0<T>(mj);
+        f32x4 acc[GV];
+  #pragma unroll
+        for (int u = 0; u < GV; ++u) acc[u] = zero4();
+        tile_mma_row<T, true, true, GV>(acc, sAqk + k0 * L::LC, L::LC, sDO + k0 * L::LD, L::LD,
+                                        16 * mj, 16 * ni0, C - k0);
+        tile_mma_row<T, false, false, GV>(acc, sKg, L::LK, sDht, L::LK, 16 * mj, 16 * ni0, K);
+  #pragma unroll
+        for (int u = 0; u < GV; ++u) {
+          const int ni = ni0 + u;
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) acc[u][i] = sanitize(acc[u][i]);
+          store_tile_n(gr.dvn + bhn * C * V + v0, V, 16 * mj, 16 * ni, acc[u]);
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) acc[u][i] = -acc[u][i];
+          store_tile_t(sDvT, L::LC, 16 * mj, 16 * ni, acc[u]);
+        }
       }
-    }
-    __syncthreads();
+      __syncthreads();
 
-    // dh = sanitize(qg^T (scale dO) + dh e^{gc_last} - w_pseudo^T dv_new)   (b1:26-37)
-#pragma unroll
-    for (int gi = 0; gi < TPW / GT; ++gi) {
-      const int tile0 = wv_id * TPW + gi * GT, mi = tile0 / NTI, ni0 = tile0 % NTI;
-      f32x4 acc[GT];
-#pragma unroll
-      for (int u = 0; u < GT; ++u) {
-        acc[u] = hs[gi * GT + u];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[u][i] *= __expf(sGl[16 * mi + tile_row(i)]);
+      // dh = sanitize(qg^T (scale dO) + dh e^{gc_last} - w_pseudo^T dv_new)   (b1:26-37)
+  #pragma unroll
+      for (int gi = 0; gi < TPW / GT; ++gi) {
+        const int tile0 = wv_id * TPW + gi * GT, mi = tile0 / NTI, ni0 = tile0 % NTI;
+        f32x4 acc[GT];
+  #pragma unroll
+        for (int u = 0; u < GT; ++u) {
+          acc[u] = hs[gi * GT + u];
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) acc[u][i] *= __expf(sGl[16 * mi + tile_row(i)]);
+        }
+        tile_mma_row<T, true, true, GT>(acc, sQ, L::LK, sDOs, L::LD, 16 * mi, 16 * ni0, C);
+        tile_mma_row<T, true, false, GT>(acc, sW, L::LK, sDvT, L::LC, 16 * mi, 16 * ni0, C);
+  #pragma unroll
+        for (int u = 0; u < GT; ++u) {
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) acc[u][i] = sanitize(acc[u][i]);
+          hs[gi * GT + u] = acc[u];
+        }
       }
-      tile_mma_row<T, true, true, GT>(acc, sQ, L::LK, sDOs, L::LD, 16 * mi, 16 * ni0, C);
-      tile_mma_row<T, true, false, GT>(acc, sW, L::LK, sDvT, L::LC, 16 * mi, 16 * ni0, C);
-#pragma unroll
-      for (int u = 0; u < GT; ++u) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[u][i] = sanitize(acc[u][i]);
-        hs[gi * GT + u] = acc[u];
+      __syncthreads();
+  #pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
+        store_tile_t(sDht, L::LK, 16 * mi, 16 * ni, hs[t]);
       }
-    }
+    if (n > 0) commit(S);
+    if (n >= 3) prefetch(S, n - 3);
     __syncthreads();
-#pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-      const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
-      store_tile_t(sDht, L::LK, 16 * mi, 16 * ni, hs[t]);
-    }
-    if (n > 0) commit(n - 1);
-    __syncthreads();
+  };
+  for (int n = dm.NT - 1; n >= 0; n -= 2) {
+    chunk_step(n, s0);
+    if (n >= 1) chunk_step(n - 1, s1);
   }
   if (dh0) {
 #pragma unroll
