@@ -604,16 +604,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const size_t t0 = (size_t)bb * dm.T + (size_t)n * C;
   const size_t base = (t0 * dm.H + h) * K + d0;  // this slice's column 0
 
+  // q, k, b and dAqk / dAkk are requested before the cumsum of g, so their
+  // latency overlaps it
+  const int cg = tid % M::NCG, seg = tid / M::NCG;
+  Raw8<T> rq[M::RS], rk[M::RS], rb[M::RS];
+#pragma unroll
+  for (int rr = 0; rr < M::RS; ++rr) {
+    const size_t o = base + (size_t)(seg * M::RS + rr) * rsK + cg * 8;
+    rq[rr].load(q + o);
+    rk[rr].load(k + o);
+    rb[rr].load(b + o);
+  }
+  RegStage<T, C, C> pqk, pkk;
+  pqk.load(gr.daqk + blk * C * C, C);
+  pkk.load(gr.dakk + blk * C * C, C);
   float gcr[M::RS][8];
   const bool exact = chunk_cumsum<C, KH>(g + base, rsK, gcr, sTot, sGl);
-  const int cg = tid % M::NCG, seg = tid / M::NCG;
 #pragma unroll
   for (int rr = 0; rr < M::RS; ++rr) {
     const int r = seg * M::RS + rr;
     float qv[8], kv[8], bv[8], o1[8], o2[8], o3[8];
-    load8(q + base + (size_t)r * rsK + cg * 8, qv);
-    load8(k + base + (size_t)r * rsK + cg * 8, kv);
-    load8(b + base + (size_t)r * rsK + cg * 8, bv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { qv[j] = rq[rr][j]; kv[j] = rk[rr][j]; bv[j] = rb[rr][j]; }
     if (!exact) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -633,8 +645,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int j = 0; j < 8; ++j) sGc[r * L::LG + cg * 8 + j] = gcr[rr][j];
   }
   // scale folded into the dAqk operand: Aqk = scale Q~ K~^T
-  stage_rows<T, C, C>(sDAqk, L::LC, gr.daqk + blk * C * C, C);
-  stage_rows<T, C, C>(sDAkk, L::LC, gr.dakk + blk * C * C, C);
+  pqk.store(sDAqk, L::LC);
+  pkk.store(sDAkk, L::LC);
   __syncthreads();
 
   // Tiles of [C][K], column-major over tiles so each wave owns whole columns.
@@ -677,14 +689,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     float csum[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) csum[j] = 0.f;
-#pragma unroll 1
+#pragma unroll
     for (int rr = 0; rr < M::RS; ++rr) {
       const int r = seg * M::RS + rr;
       const int c8 = cg * 8;
       float qv[8], kv[8], bv[8], dqg[8], dkb[8], dkg[8], oq[8], ok[8], ob[8];
-      load8(q + base + (size_t)r * rsK + c8, qv);
-      load8(k + base + (size_t)r * rsK + c8, kv);
-      load8(b + base + (size_t)r * rsK + c8, bv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { qv[j] = rq[rr][j]; kv[j] = rk[rr][j]; bv[j] = rb[rr][j]; }
       load8(g_dqg + (size_t)r * K + c8, dqg);
       load8(g_dkb + (size_t)r * K + c8, dkb);
       load8(g_dkg + (size_t)r * K + c8, dkg);
