@@ -618,6 +618,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   RegStage<T, C, C> pqk, pkk;
   pqk.load(gr.daqk + blk * C * C, C);
   pkk.load(gr.dakk + blk * C * C, C);
+  // the B3 intermediates of the element-wise stage (same thread map), likewise
+  Raw8<T> rdqg[M::RS], rdkb[M::RS], rdkg[M::RS];
+#pragma unroll
+  for (int rr = 0; rr < M::RS; ++rr) {
+    const size_t o = blk * C * K + d0 + (size_t)(seg * M::RS + rr) * K + cg * 8;
+    rdqg[rr].load(gr.dqg + o);
+    rdkb[rr].load(gr.dkb + o);
+    rdkg[rr].load(gr.dkg + o);
+  }
   float gcr[M::RS][8];
   const bool exact = chunk_cumsum<C, KH>(g + base, rsK, gcr, sTot, sGl);
 #pragma unroll
@@ -696,9 +705,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       float qv[8], kv[8], bv[8], dqg[8], dkb[8], dkg[8], oq[8], ok[8], ob[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) { qv[j] = rq[rr][j]; kv[j] = rk[rr][j]; bv[j] = rb[rr][j]; }
-      load8(g_dqg + (size_t)r * K + c8, dqg);
-      load8(g_dkb + (size_t)r * K + c8, dkb);
-      load8(g_dkg + (size_t)r * K + c8, dkg);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { dqg[j] = rdqg[rr][j]; dkb[j] = rdkb[rr][j]; dkg[j] = rdkg[rr][j]; }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int d = c8 + j;
