@@ -206,8 +206,25 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
   const T* vc = v + (t0 * dm.H + h) * V;
   const T* wc = w + (t0 * dm.H + h) * V;
 
-  // ---- phase 0: gc = cumsum(g) over the chunk (gdn2_wy_reference.py:63)
+  // q, k, b, v, w are requested before the cumsum of g, so their latency overlaps it
   const int cg = tid % L::NCG, seg = tid / L::NCG;
+  const int cgv = tid % L::NCGV, segv = tid / L::NCGV;
+  Raw8<T> rq[L::RS], rk[L::RS], rb[L::RS], rv[L::RSV], rw[L::RSV];
+#pragma unroll
+  for (int rr = 0; rr < L::RS; ++rr) {
+    const size_t o = (size_t)(seg * L::RS + rr) * rsK + cg * 8;
+    rq[rr].load(qc + o);
+    rk[rr].load(kc + o);
+    rb[rr].load(bc + o);
+  }
+#pragma unroll
+  for (int rr = 0; rr < L::RSV; ++rr) {
+    const size_t o = (size_t)(segv * L::RSV + rr) * rsV + cgv * 8;
+    rv[rr].load(vc + o);
+    rw[rr].load(wc + o);
+  }
+
+  // ---- phase 0: gc = cumsum(g) over the chunk (gdn2_wy_reference.py:63)
   float gcr[L::RS][8];
   const bool exact = chunk_cumsum<C, K>(gc_in, rsK, gcr, sTot, sGl);
   if (tid < K) ck.gcl[(size_t)bhn * K + tid] = sGl[tid];
@@ -219,9 +236,8 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
   for (int rr = 0; rr < L::RS; ++rr) {
     const int r = seg * L::RS + rr;
     float qv[8], kv[8], bv[8], o_qg[8], o_kt[8], o_kb[8], o_kg[8];
-    load8(qc + (size_t)r * rsK + cg * 8, qv);
-    load8(kc + (size_t)r * rsK + cg * 8, kv);
-    load8(bc + (size_t)r * rsK + cg * 8, bv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { qv[j] = rq[rr][j]; kv[j] = rk[rr][j]; bv[j] = rb[rr][j]; }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float gcv = gcr[rr][j];
@@ -243,13 +259,12 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
     }
   }
   {
-    const int cgv = tid % L::NCGV, segv = tid / L::NCGV;
 #pragma unroll
     for (int rr = 0; rr < L::RSV; ++rr) {
       const int r = segv * L::RSV + rr;
       float vv[8], wv[8];
-      load8(vc + (size_t)r * rsV + cgv * 8, vv);
-      load8(wc + (size_t)r * rsV + cgv * 8, wv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { vv[j] = rv[rr][j]; wv[j] = rw[rr][j]; }
       // w * v is formed in the input dtype before the upcast (gdn2_wy_reference.py:94)
 #pragma unroll
       for (int j = 0; j < 8; ++j) wv[j] = to_f(from_f<T>(wv[j] * vv[j]));
