@@ -258,14 +258,25 @@ struct RegStage {
 
 // Copy a [R][D] block (row stride `src_ld`) into LDS rows of length `dst_ld`
 // (NTH threads in the workgroup).
+// All of a thread's loads are issued before its stores (the pieces are held in
+// registers), so the loads of one call are in flight together.
 template <typename T, int R, int D, int NTH = 256>
 __device__ __forceinline__ void stage_rows(T* dst, int dst_ld, const T* src, size_t src_ld) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int PER_ROW = D / VEC;
-  for (int e = threadIdx.x; e < R * PER_ROW; e += NTH) {
-    const int r = e / PER_ROW, c = (e % PER_ROW) * VEC;
-    *reinterpret_cast<uint4*>(dst + r * dst_ld + c) =
-        *reinterpret_cast<const uint4*>(src + r * src_ld + c);
+  constexpr int NP = R * PER_ROW, IT = (NP + NTH - 1) / NTH;
+  uint4 tmp[IT];
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int e = threadIdx.x + NTH * i;
+    if (NP % NTH == 0 || e < NP)
+      tmp[i] = *reinterpret_cast<const uint4*>(src + (size_t)(e / PER_ROW) * src_ld + (e % PER_ROW) * VEC);
+  }
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int e = threadIdx.x + NTH * i;
+    if (NP % NTH == 0 || e < NP)
+      *reinterpret_cast<uint4*>(dst + (e / PER_ROW) * dst_ld + (e % PER_ROW) * VEC) = tmp[i];
   }
 }
 template <typename T, int R, int D, int NTH = 256>
