@@ -283,10 +283,19 @@ template <typename T, int R, int D, int NTH = 256>
 __device__ __forceinline__ void unstage_rows(T* dst, size_t dst_ld, const T* src, int src_ld) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int PER_ROW = D / VEC;
-  for (int e = threadIdx.x; e < R * PER_ROW; e += NTH) {
-    const int r = e / PER_ROW, c = (e % PER_ROW) * VEC;
-    *reinterpret_cast<uint4*>(dst + r * dst_ld + c) =
-        *reinterpret_cast<const uint4*>(src + r * src_ld + c);
+  constexpr int NP = R * PER_ROW, IT = (NP + NTH - 1) / NTH;
+  uint4 tmp[IT];
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int e = threadIdx.x + NTH * i;
+    if (NP % NTH == 0 || e < NP)
+      tmp[i] = *reinterpret_cast<const uint4*>(src + (e / PER_ROW) * src_ld + (e % PER_ROW) * VEC);
+  }
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int e = threadIdx.x + NTH * i;
+    if (NP % NTH == 0 || e < NP)
+      *reinterpret_cast<uint4*>(dst + (size_t)(e / PER_ROW) * dst_ld + (e % PER_ROW) * VEC) = tmp[i];
   }
 }
 
@@ -310,13 +319,22 @@ template <typename TS, typename T, int R, int D, int NTH = 256>
 __device__ __forceinline__ void stage_convert(T* dst, int ld, const TS* src, size_t src_ld,
                                               float mul = 1.f) {
   constexpr int PER_ROW = D / 8;
-  for (int e = threadIdx.x; e < R * PER_ROW; e += NTH) {
-    const int r = e / PER_ROW, c = (e % PER_ROW) * 8;
-    float x[8];
-    load8(src + (size_t)r * src_ld + c, x);
+  constexpr int NP = R * PER_ROW, IT = (NP + NTH - 1) / NTH;
+  Raw8<TS> tmp[IT];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] *= mul;
-    store8(dst + r * ld + c, x);
+  for (int i = 0; i < IT; ++i) {
+    const int e = threadIdx.x + NTH * i;
+    if (NP % NTH == 0 || e < NP) tmp[i].load(src + (size_t)(e / PER_ROW) * src_ld + (e % PER_ROW) * 8);
+  }
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int e = threadIdx.x + NTH * i;
+    if (NP % NTH == 0 || e < NP) {
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = tmp[i][j] * mul;
+      store8(dst + (e / PER_ROW) * ld + (e % PER_ROW) * 8, x);
+    }
   }
 }
 

@@ -407,27 +407,36 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy_a(Gdn2Dims dm, Gdn2Chunks<T> 
   for (int t = 0; t < TPW; ++t) da[t] = zero4();
   const int cg = tid % M::NCG, seg = tid / M::NCG;
   for (int c0 = 0; c0 < K; c0 += KH) {
-    // kb = b k e^{gc} and wv = w v (rounded to the input dtype) for these columns
+    // kb = b k e^{gc} and wv = w v (rounded to the input dtype) for these
+    // columns; k, b, v, w, dw~, dv_new are requested before the cumsum of g
+    Raw8<T> rk[M::RS], rb[M::RS], rv[M::RS], rw[M::RS];
+#pragma unroll
+    for (int rr = 0; rr < M::RS; ++rr) {
+      const size_t r = (size_t)(seg * M::RS + rr);
+      rk[rr].load(k + ((t0 + r) * dm.H + h) * K + c0 + cg * 8);
+      rb[rr].load(b + ((t0 + r) * dm.H + h) * K + c0 + cg * 8);
+      rv[rr].load(v + ((t0 + r) * dm.H + h) * V + c0 + cg * 8);
+      rw[rr].load(w + ((t0 + r) * dm.H + h) * V + c0 + cg * 8);
+    }
+    RegStage<T, C, KH> pdw, pdv;
+    pdw.load(gr.dwt + blk * C * K + c0, K);
+    pdv.load(gr.dvn + blk * C * V + c0, V);
     float gcr[M::RS][8];
     chunk_cumsum<C, KH>(g + (t0 * dm.H + h) * K + c0, rsK, gcr, sTot, sGl);
 #pragma unroll
     for (int rr = 0; rr < M::RS; ++rr) {
       const int r = seg * M::RS + rr;
-      float kv[8], bv[8], kb[8], vv[8], ww[8], wv[8];
-      load8(k + ((t0 + r) * dm.H + h) * K + c0 + cg * 8, kv);
-      load8(b + ((t0 + r) * dm.H + h) * K + c0 + cg * 8, bv);
-      load8(v + ((t0 + r) * dm.H + h) * V + c0 + cg * 8, vv);
-      load8(w + ((t0 + r) * dm.H + h) * V + c0 + cg * 8, ww);
+      float kb[8], wv[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        kb[j] = (bv[j] * kv[j]) * __expf(gcr[rr][j]);
-        wv[j] = to_f(from_f<T>(ww[j] * vv[j]));
+        kb[j] = (rb[rr][j] * rk[rr][j]) * __expf(gcr[rr][j]);
+        wv[j] = to_f(from_f<T>(rw[rr][j] * rv[rr][j]));
       }
       store8(sKB + r * L::LH + cg * 8, kb);
       store8(sWV + r * L::LH + cg * 8, wv);
     }
-    stage_rows<T, C, KH>(sDW, L::LH, gr.dwt + blk * C * K + c0, K);
-    stage_rows<T, C, KH>(sDV, L::LH, gr.dvn + blk * C * V + c0, V);
+    pdw.store(sDW, L::LH);
+    pdv.store(sDV, L::LH);
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
