@@ -615,13 +615,20 @@ __global__ __launch_bounds__(256) void mamba2_bwd_bc(Mamba2Dims dm, int G, const
 
   stage_rows<T, C, NTL>(sB, L::LK, Bm + row0 * N + n0, N);
   stage_rows<T, C, NTL>(sC, L::LK, Cm + row0 * N + n0, N);
+  // dCB = the sum of the head-group partials (lower triangle), 4 columns per item
   const float* part = gr.part + (size_t)bn * G * C * C;
-  for (int e = threadIdx.x; e < C * C; e += 256) {
-    const int i = e / C, j = e % C;
-    float s = 0.f;
+#pragma unroll 4
+  for (int e4 = threadIdx.x; e4 < C * C / 4; e4 += 256) {
+    const int i = (4 * e4) / C, j = (4 * e4) % C;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     if (j <= i)
-      for (int gg = 0; gg < G; ++gg) s += part[(size_t)gg * C * C + e];
-    sCB[i * L::LCB + j] = from_f<T>(s);
+      for (int gg = 0; gg < G; ++gg) {
+        const float4 v = *reinterpret_cast<const float4*>(part + (size_t)gg * C * C + 4 * e4);
+        s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+      }
+    const f32x4 sv = {j <= i ? s.x : 0.f, j + 1 <= i ? s.y : 0.f, j + 2 <= i ? s.z : 0.f,
+                      j + 3 <= i ? s.w : 0.f};
+    store4(sCB + i * L::LCB + j, sv);
   }
 
   constexpr int RT = C / 64, CT = NTL / 16;  // row tiles per wave, column tiles

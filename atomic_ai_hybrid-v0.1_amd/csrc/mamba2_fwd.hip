@@ -89,12 +89,13 @@ template <typename T, int C, int N, int PT>
 struct OuterLds {
   static constexpr int PAD = Pad<T>::v;
   static constexpr int LS = PT + PAD, LN = N + PAD;
+  static constexpr int LC = PT + 4;  // fp32 cum rows: 16-byte aligned, 4 banks apart
   static constexpr int NSEG = 256 / PT;
-  static constexpr int off_cum = 0;  // fp32 cum [C][PT]; then the bf16 operand S [C][LS]
-  static constexpr int off_tot = off_cum + C * PT * 4;
+  static constexpr int off_cum = 0;  // fp32 cum [C][LC]; then the bf16 operand S [C][LS]
+  static constexpr int off_tot = off_cum + C * LC * 4;
   static constexpr int off_r = off_tot + NSEG * PT * 4;
   static constexpr int total = off_r + C * LN * (int)sizeof(T);
-  static_assert(C * LS * (int)sizeof(T) <= C * PT * 4, "S must fit in the cum buffer");
+  static_assert(C * LS * (int)sizeof(T) <= C * LC * 4, "S must fit in the cum buffer");
 };
 
 // out[p][s] = sum_i S[i][p] R[i][s] for one (batch, chunk, head, PT channels):
@@ -140,22 +141,26 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
 #pragma unroll
   for (int i = 0; i < EPT; ++i) {
     const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
+    float av[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) sCum[r * PT + c + j] = sanitize(rdt[i][j] * Ah, kClipDecay);
+    for (int j = 0; j < 8; ++j) av[j] = sanitize(rdt[i][j] * Ah, kClipDecay);
+    store8(sCum + r * L::LC + c, av);
   }
   __syncthreads();
-  column_cumsum<C, PT>(sCum, sTot);
+  column_cumsum<C, PT, L::LC>(sCum, sTot);
   __syncthreads();
 
   float sv[EPT][8];
 #pragma unroll
   for (int i = 0; i < EPT; ++i) {
     const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
-    float wv[8];
+    float wv[8], cr[8], clr[8];
+    load8(sCum + r * L::LC + c, cr);
+    load8(sCum + (C - 1) * L::LC + c, clr);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float ci = sCum[r * PT + c + j];
-      const float cl = sCum[(C - 1) * PT + c + j];
+      const float ci = cr[j];
+      const float cl = clr[j];
       const float dbx = sanitize(rdt[i][j] * rx[i][j]);
       const float dte = sanitize(__expf(fminf(fmaxf(cl - ci, -kClipDecay), kClipDecay)), 1e6f);
       if constexpr (BWD) {
@@ -171,7 +176,7 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
     }
   }
   const size_t bnh = (size_t)bn * dm.H + h;
-  if (!BWD && threadIdx.x < PT) ck.cl[bnh * P + p0 + threadIdx.x] = sCum[(C - 1) * PT + threadIdx.x];
+  if (!BWD && threadIdx.x < PT) ck.cl[bnh * P + p0 + threadIdx.x] = sCum[(C - 1) * L::LC + threadIdx.x];
   __syncthreads();  // every cum read is done: S overwrites the cum buffer
 #pragma unroll
   for (int i = 0; i < EPT; ++i) {
