@@ -372,6 +372,20 @@ __global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __
     rx[i].load(x + base + r * rsx + c);
   }
   stage_rows<T, PT, N>(sSt, L::LN, ck.state_pre + (((size_t)bn * dm.H + h) * P + p0) * N, N);
+  // the global operands of the output blocks (CB fragments, C rows), requested
+  // now so their latency overlaps the cumsum
+  typedef typename Mma<T>::frag frag;
+  frag fa[BPW][NB], fd[BPW], fc[BPW][KN];
+#pragma unroll
+  for (int bi = 0; bi < BPW; ++bi) {
+    const int I = y_block<NB>(wv_id, bi);
+#pragma unroll
+    for (int J = 0; J < NB; ++J)
+      if (J < I) fa[bi][J] = cb_frag<T>(cbg, C, 16 * I, 16 * J, 0);
+    fd[bi] = cb_frag<T>(cbg, C, 16 * I, 16 * I, 1);
+#pragma unroll
+    for (int kk = 0; kk < KN; ++kk) fc[bi][kk] = Mma<T>::ld_c(cg, N, 16 * I, kk * Mma<T>::KS);
+  }
   int flag = 0;
   float dbx[EPT][8];
 #pragma unroll
@@ -423,18 +437,12 @@ __global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __
 #pragma unroll
     for (int ni = 0; ni < YNI; ++ni) { off[ni] = zero4(); dg[ni] = zero4(); yo[ni] = zero4(); }
     if (!exact) {
-      // the CB fragments of the block row, issued together
-      typename Mma<T>::frag fa[NB];
-#pragma unroll
-      for (int J = 0; J < NB; ++J)
-        if (J < I) fa[J] = cb_frag<T>(cbg, C, 16 * I, 16 * J, 0);
-      const typename Mma<T>::frag ad = cb_frag<T>(cbg, C, 16 * I, 16 * I, 1);
 #pragma unroll
       for (int J = 0; J < NB; ++J) {
         if (J < I) {
 #pragma unroll
           for (int ni = 0; ni < YNI; ++ni) {
-            const f32x4 q = Mma<T>::mma(fa[J], Mma<T>::ld_t(sV, L::LPT, 16 * ni, 16 * J), zero4());
+            const f32x4 q = Mma<T>::mma(fa[bi][J], Mma<T>::ld_t(sV, L::LPT, 16 * ni, 16 * J), zero4());
             const int pc = 16 * ni + tile_col();
             const float mf = __expf(sCum[16 * I * L::LC + pc] - sCum[(16 * J + 15) * L::LC + pc]);
 #pragma unroll
@@ -444,14 +452,13 @@ __global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __
       }
 #pragma unroll
       for (int ni = 0; ni < YNI; ++ni)
-        dg[ni] = Mma<T>::mma(ad, Mma<T>::ld_t(sV, L::LPT, 16 * ni, 16 * I), zero4());
+        dg[ni] = Mma<T>::mma(fd[bi], Mma<T>::ld_t(sV, L::LPT, 16 * ni, 16 * I), zero4());
     }
 #pragma unroll
     for (int kk = 0; kk < KN; ++kk) {
-      const typename Mma<T>::frag a = Mma<T>::ld_c(cg, N, 16 * I, kk * Mma<T>::KS);
 #pragma unroll
       for (int ni = 0; ni < YNI; ++ni)
-        yo[ni] = Mma<T>::mma(a, Mma<T>::ld_c(sSt, L::LN, 16 * ni, kk * Mma<T>::KS), yo[ni]);
+        yo[ni] = Mma<T>::mma(fc[bi][kk], Mma<T>::ld_c(sSt, L::LN, 16 * ni, kk * Mma<T>::KS), yo[ni]);
     }
 #pragma unroll
     for (int ni = 0; ni < YNI; ++ni) {
