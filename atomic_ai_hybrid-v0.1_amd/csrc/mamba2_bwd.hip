@@ -69,6 +69,25 @@ __device__ __forceinline__ typename Mma<T>::frag cb_frag_dup(const T* g, int ld,
   }
   return a;
 }
+// The same duplicated A fragments from the chunk's CB staged in LDS (row
+// pitch ld): CB(m0.., k0..) for the row side, CB^T(m0.., k0..) by a
+// transposed read for the column side.
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::frag cb_lds_dup(const T* s, int ld, int m0, int k0, int mask,
+                                                            bool transposed) {
+  typedef typename Mma<T>::frag frag;
+  const int l = lane_id(), m = l & 15, g2 = l >> 5, kb = 8 * ((l >> 4) & 1);
+  frag a = transposed ? Mma<T>::ld_t(s, ld, m0, k0 - 16 * g2)
+                      : *reinterpret_cast<const frag*>(s + (m0 + m) * ld + k0 + kb);
+  if (mask) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool keep = mask == 1 ? (kb + e <= m) : (kb + e >= m);
+      if (!keep) a[e] = (T)0.f;
+    }
+  }
+  return a;
+}
 template <typename T>
 __device__ __forceinline__ typename Mma<T>::frag ld_t_hilo(const T* hi, const T* lo, int ld, int i0, int k0) {
   const int g2 = lane_id() >> 5;  // lanes 32..63 hold K rows 16..31
@@ -99,7 +118,10 @@ struct CkLds {
   static constexpr int off_tot = off_cum + C * LC * 4;  // column / block totals
   static_assert(NSEG >= C / 16, "the block totals reuse the column-scan totals");
   static constexpr int off_misc = off_tot + NSEG * PT * 4;   // lasta[PT], lastb[NW][PT], dA[1 + NW]
-  static constexpr int off_m = off_misc + (PT + NW * PT + 1 + NW) * 4;
+  static constexpr int LCB = C + PAD;
+  static constexpr int off_cb = (off_misc + (PT + NW * PT + 1 + NW) * 4 + 15) / 16 * 16;  // CB [C][LCB]
+  static constexpr int off_m = off_cb + C * LCB * (int)sizeof(T);
+  static_assert(off_cb % 16 == 0 && off_m % 16 == 0, "16-byte LDS accesses");
   // M_IJ[p] = exp(cum_{16I} - cum_{16J+15}) for the 16-row block pairs I >= J
   static constexpr int total = off_m + (C / 16) * (C / 16 + 1) / 2 * PT * 4;
 };
@@ -121,6 +143,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // unrolled loop bodies out of the iteration loop (that hoisting spilled them).
   T *sSt, *sDst, *sDy, *sDt, *sX, *sYu, *sYul, *sVd, *sVdl;
   float *sCum, *sTot, *sLastA, *sLastB, *sDa, *sM;
+  T* sCB;
   auto views = [&](int z) {
     unsigned char* lb = lds + z;
     sSt = reinterpret_cast<T*>(lb + L::off_st);
@@ -138,6 +161,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     sLastB = sLastA + PT;
     sDa = sLastB + NW * PT;
     sM = reinterpret_cast<float*>(lb + L::off_m);
+    sCB = reinterpret_cast<T*>(lb + L::off_cb);
   };
   views(0);
 
@@ -152,7 +176,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const T* Bg0 = Bm + row0 * N;
   const T* Cg0 = Cm + row0 * N;
   const T* cb0 = ck.cb + (size_t)bn * C * C;
-  const T* cbt0 = ck.cbt + (size_t)bn * C * C;
   constexpr int NB = C / 16;
 
   // cross-head accumulator: dCB lower tiles (I >= J), tile k of wave w = w + NW s
@@ -215,6 +238,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (tid < PT) nla = gr.lasta[bnhn * P + pn + tid];
   };
   load_slice(g * HG, 0, row0);
+  // the chunk's CB, shared by every head and slice of this workgroup
+  stage_rows<T, C, C, NTH>(sCB, L::LCB, cb0, C);
   for (int hh = 0; hh < HG; ++hh) {
     const int h = g * HG + hh;
     const float Ah = A[h];
@@ -225,7 +250,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const T* Bg = opaque_ptr(Bg0);
       const T* Cg = opaque_ptr(Cg0);
       const T* cbg = opaque_ptr(cb0);
-      const T* cbtg = opaque_ptr(cbt0);
       // this wave's block, also rebuilt per iteration (its addresses stay in the loop)
       const int I = I0 + z, ni0 = ni00 + z;
       const size_t rowz = row0 + z;
@@ -378,38 +402,35 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           f32x4 ro[NIW], rd[NIW], so[NIW], sd[NIW];
 #pragma unroll
           for (int q = 0; q < NIW; ++q) { ro[q] = zero4(); so[q] = zero4(); }
-          // every CB fragment of the block row, issued together: CB(I, J) for
-          // J < I (row side), CB^T(I, J) for J > I (column side), the diagonal
-          frag fa[NB];
-#pragma unroll
-          for (int J = 0; J < NB; ++J)
-            if (J != I) fa[J] = cb_frag_dup<T>(J < I ? cbg : cbtg, C, 16 * I, 16 * J, 0);
-          const frag ar = cb_frag_dup<T>(cbg, C, 16 * I, 16 * I, 1);
-          const frag as = cb_frag_dup<T>(cbtg, C, 16 * I, 16 * I, 2);
+          // CB(I, J) for J < I (row side), CB^T(I, J) for J > I (column side)
+          // and the diagonal, read from the chunk's CB in LDS where used
+          const frag ar = cb_lds_dup<T>(sCB, L::LCB, 16 * I, 16 * I, 1, false);
+          const frag as = cb_lds_dup<T>(sCB, L::LCB, 16 * I, 16 * I, 2, true);
 #pragma unroll
           for (int J = 0; J < NB; ++J) {
             if (J < I) {  // sources below the block
+              const frag fa = cb_lds_dup<T>(sCB, L::LCB, 16 * I, 16 * J, 0, false);
 #pragma unroll
               for (int q = 0; q < NIW; ++q) {
                 const int ni = ni0 + q;
-                const f32x4 m = Mma<T>::mma(fa[J], ld_t_hilo<T>(sVd, sVdl, L::LPT, 16 * ni, 16 * J), zero4());
+                const f32x4 m = Mma<T>::mma(fa, ld_t_hilo<T>(sVd, sVdl, L::LPT, 16 * ni, 16 * J), zero4());
                 const int pc = 16 * ni + tile_col();
                 const float mf = sM[(I * (I + 1) / 2 + J) * PT + pc];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) ro[q][k] += mf * m[k];
               }
             } else if (J > I) {  // targets above the block (column side)
+              const frag fa = cb_lds_dup<T>(sCB, L::LCB, 16 * I, 16 * J, 0, true);
 #pragma unroll
               for (int q = 0; q < NIW; ++q) {
                 const int ni = ni0 + q;
-                const f32x4 m = Mma<T>::mma(fa[J], ld_t_hilo<T>(sYu, sYul, L::LPT, 16 * ni, 16 * J), zero4());
+                const f32x4 m = Mma<T>::mma(fa, ld_t_hilo<T>(sYu, sYul, L::LPT, 16 * ni, 16 * J), zero4());
                 const int pc = 16 * ni + tile_col();
                 const float mf = sM[(J * (J + 1) / 2 + I) * PT + pc];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) so[q][k] += mf * m[k];
               }
             }
-            __builtin_amdgcn_sched_barrier(0);  // keep the operand reads of one J together
           }
           {  // the diagonal block
 #pragma unroll
