@@ -12,7 +12,6 @@ struct Mamba2Dims {
 template <typename T>
 struct Mamba2Chunks {
   T* cb;         // [B][NT][C][C]      sanitize(C_i . B_j), shared by every head
-  T* cbt;        // [B][NT][C][C]      its transpose
   T* state_pre;  // [B][NT][H][P][N]   state entering each chunk
   float* cl;     // [B][NT][H][P]      cumulative log decay at the chunk's last row
   float* src;    // [B][NT][H][P][N]   forward: sanitize(state_end) of each chunk;

@@ -54,24 +54,10 @@ struct Mamba2Grads {
 // The pair sums take one K = 32 MFMA per 16-row block: the A fragment holds
 // the 16 x 16 CB block twice along K, the B fragment the block's 16 rows of
 // the high part and then of the low part, so hi and lo are summed in the MFMA.
-// mask 1 keeps columns <= row (lower triangle), mask 2 columns >= row.
-template <typename T>
-__device__ __forceinline__ typename Mma<T>::frag cb_frag_dup(const T* g, int ld, int m0, int k0, int mask) {
-  typedef typename Mma<T>::frag frag;
-  const int l = lane_id(), m = l & 15, kb = 8 * ((l >> 4) & 1);
-  frag a = *reinterpret_cast<const frag*>(g + (m0 + m) * ld + k0 + kb);
-  if (mask) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const bool keep = mask == 1 ? (kb + e <= m) : (kb + e >= m);
-      if (!keep) a[e] = (T)0.f;
-    }
-  }
-  return a;
-}
-// The same duplicated A fragments from the chunk's CB staged in LDS (row
-// pitch ld): CB(m0.., k0..) for the row side, CB^T(m0.., k0..) by a
-// transposed read for the column side.
+// The A fragments come from the chunk's CB staged in LDS (row pitch ld):
+// CB(m0.., k0..) for the row side, CB^T(m0.., k0..) by a transposed read for
+// the column side.  mask 1 keeps columns <= row (lower triangle), mask 2
+// columns >= row.
 template <typename T>
 __device__ __forceinline__ typename Mma<T>::frag cb_lds_dup(const T* s, int ld, int m0, int k0, int mask,
                                                             bool transposed) {

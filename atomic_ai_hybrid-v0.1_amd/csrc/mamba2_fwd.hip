@@ -11,8 +11,8 @@
 //   y_off  = sanitize((C state^T) exp(clip(cum, -20, 0)))
 //   state  = sanitize(state exp(clip(cum_last, -20, 0)) + s_end)
 //
-// mamba2_cb           one workgroup per (batch, chunk): CB = sanitize(C B^T)
-//                     and its transpose, shared by every head (the reference's M3 broadcasts B/C
+// mamba2_cb           one workgroup per (batch, chunk): CB = sanitize(C B^T),
+//                     shared by every head (the reference's M3 broadcasts B/C
 //                     to every head instead, kernel_mamba2_b_intra.py:136-142).
 // mamba2_chunk_outer  one workgroup per (batch, chunk, head, channel slice):
 //                     the chunk's cum and s_end = W^T B (forward), or the
@@ -53,14 +53,12 @@ __global__ __launch_bounds__(256) void mamba2_cb(Mamba2Dims dm, const T* __restr
   __syncthreads();
   constexpr int MT = C / 16;
   T* out = ck.cb + (size_t)bn * C * C;
-  T* outt = ck.cbt + (size_t)bn * C * C;
   for (int tile = wave_id(); tile < MT * MT; tile += 4) {
     const int mi = tile / MT, nj = tile % MT;
     f32x4 acc = tile_mma<T, false, false>(zero4(), sC, LN, sB, LN, 16 * mi, 16 * nj, N);
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = sanitize(acc[i]);
     store_tile_n(out, C, 16 * mi, 16 * nj, acc);
-    store_tile_t(outt, C, 16 * mi, 16 * nj, acc);
   }
 }
 

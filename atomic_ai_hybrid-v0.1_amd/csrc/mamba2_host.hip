@@ -10,7 +10,7 @@ static size_t m2_align(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct Mamba2Plan {
   Mamba2Dims dm;
-  size_t o_cb, o_cbt, o_state, o_cl, o_src, fwd_end;
+  size_t o_cb, o_state, o_cl, o_src, fwd_end;
   size_t o_dstate, o_lasta, o_ydh, o_wr, o_part, o_dap, total;
   int G;  // head groups of the cross-head dCB reduction
 };
@@ -36,7 +36,6 @@ static int mamba2_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += m2_align(bytes); return o; };
   p->o_cb = take(B * NT * C * C * es);
-  p->o_cbt = take(B * NT * C * C * es);
   p->o_state = take(B * NT * H * P * N * es);        // state entering each chunk
   p->o_cl = take(B * NT * H * P * 4);                // cum at each chunk's last row
   p->o_src = take(B * NT * H * P * N * 4);           // state_end; then the backward's dstate source
@@ -56,7 +55,6 @@ static Mamba2Chunks<T> mamba2_chunks(const Mamba2Plan& p, void* ws) {
   char* base = static_cast<char*>(ws);
   Mamba2Chunks<T> c;
   c.cb = reinterpret_cast<T*>(base + p.o_cb);
-  c.cbt = reinterpret_cast<T*>(base + p.o_cbt);
   c.state_pre = reinterpret_cast<T*>(base + p.o_state);
   c.cl = reinterpret_cast<float*>(base + p.o_cl);
   c.src = reinterpret_cast<float*>(base + p.o_src);
