@@ -239,6 +239,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // this wave's block, also rebuilt per iteration (its addresses stay in the loop)
       const int I = I0 + z, ni0 = ni00 + z;
       const size_t rowz = row0 + z;
+      // the C / B rows of this wave's block for y_off / dwrite, requested now
+      frag cfr[N / 32], bfr[N / 32];
+#pragma unroll
+      for (int kk = 0; kk < N / 32; ++kk) {
+        cfr[kk] = Mma<T>::ld_c(Cg, N, 16 * I, 32 * kk);
+        bfr[kk] = Mma<T>::ld_c(Bg, N, 16 * I, 32 * kk);
+      }
       // ---- A: slice inputs (dt, x, dy kept exactly as bf16), a = sanitize(dt A, 20);
       // thread item = 8 channels of one row, kept in registers for B
       int flag = 0;
@@ -442,8 +449,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int q = 0; q < NIW; ++q) {
           const int ni = ni0 + q;
           // y_off_raw = C state^T and dwrite = B dstate^T for this tile (:126,134)
-          const f32x4 yoff = tile_mma<T, false, false>(zero4(), Cg, N, sSt, L::LN, 16 * I, 16 * ni, N);
-          const f32x4 dwr = tile_mma<T, false, false>(zero4(), Bg, N, sDst, L::LN, 16 * I, 16 * ni, N);
+          f32x4 yoff = zero4(), dwr = zero4();
+#pragma unroll
+          for (int kk = 0; kk < N / 32; ++kk) {
+            yoff = Mma<T>::mma(cfr[kk], Mma<T>::ld_c(sSt, L::LN, 16 * ni, 32 * kk), yoff);
+            dwr = Mma<T>::mma(bfr[kk], Mma<T>::ld_c(sDst, L::LN, 16 * ni, 32 * kk), dwr);
+          }
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) {
             const int i = 16 * I + tile_row(ii), p = 16 * ni + tile_col();
