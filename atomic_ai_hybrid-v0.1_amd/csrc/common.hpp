@@ -256,6 +256,24 @@ struct RegStage {
   }
 };
 
+// Store a RegStage block of source type TS into LDS as type T (times mul).
+template <typename T, typename TS, int R, int D, int NTH>
+__device__ __forceinline__ void store_convert(const RegStage<TS, R, D, NTH>& S, T* dst, int ld,
+                                              float mul = 1.f) {
+  typedef RegStage<TS, R, D, NTH> RS;
+#pragma unroll
+  for (int i = 0; i < RS::PT; ++i) {
+    const int e = threadIdx.x + NTH * i;
+    if (RS::N % NTH == 0 || e < RS::N) {
+      const int r = e / RS::PER_ROW, c = (e % RS::PER_ROW) * RS::VEC;
+      const uint4 raw = S.piece(i);
+      const TS* v = reinterpret_cast<const TS*>(&raw);
+#pragma unroll
+      for (int j = 0; j < RS::VEC; ++j) dst[r * ld + c + j] = from_f<T>(to_f(v[j]) * mul);
+    }
+  }
+}
+
 // Copy a [R][D] block (row stride `src_ld`) into LDS rows of length `dst_ld`
 // (NTH threads in the workgroup).
 // All of a thread's loads are issued before its stores (the pieces are held in

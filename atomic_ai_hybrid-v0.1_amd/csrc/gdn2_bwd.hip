@@ -268,13 +268,19 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
   const T* hg = ck.hT + blk * V * K;
   const T* dhg = gr.dhT + blk * V * K;
 
+  // every operand is requested before the first LDS store
   RegStage<T, V, KQ> ph, pdh;
+  RegStage<TD, C, V> pdo;
+  RegStage<T, C, V> pdv;
+  RegStage<T, V, C> pvn;
   ph.load(hg, K);
   pdh.load(dhg, K);
-  stage_convert<TD, T, C, V>(sDO, L::LV, dO + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V,
-                             (size_t)dm.H * V);
-  stage_rows<T, C, V>(sDV, L::LV, gr.dvn + blk * C * V, V);
-  stage_rows<T, V, C>(sVn, L::LC, ck.vnT + blk * V * C, C);
+  pdo.load(dO + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V, (size_t)dm.H * V);
+  pdv.load(gr.dvn + blk * C * V, V);
+  pvn.load(ck.vnT + blk * V * C, C);
+  store_convert(pdo, sDO, L::LV);
+  pdv.store(sDV, L::LV);
+  pvn.store(sVn, L::LC);
   ph.store(sH, L::LK);
   pdh.store(sDh, L::LK);
   __syncthreads();
