@@ -328,8 +328,10 @@ __device__ __forceinline__ int y_block(int w, int b) {
 //   off the diagonal  U_i sum_{J<I} M_IJ (CB_IJ Vd_J)_i
 //   diagonal block    exp(cum_i - cum_{16I+15}) (tril(CB_II) Vd_I)_i
 // with U_i = exp(cum_i - cum_{16I}), M_IJ = exp(cum_{16I} - cum_{16J+15}).
-template <typename T, int C, int P, int N, int PT>
-__global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __restrict__ dt,
+// SL channel slices of one head per workgroup (the CB / C fragments are
+// loaded once for them).
+template <typename T, int C, int P, int N, int PT, int SL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void mamba2_chunk_y(Mamba2Dims dm, const T* __restrict__ dt,
                                                      const T* __restrict__ x, const float* __restrict__ A,
                                                      const T* __restrict__ Cm, Mamba2Chunks<T> ck,
                                                      float* __restrict__ y) {
@@ -342,20 +344,37 @@ __global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __
   float* sTot = reinterpret_cast<float*>(lds + L::off_tot);
 
   constexpr int NPT = P / PT;
-  int bn, m;
-  xcd_group_map(blockIdx.x, dm.B * dm.NT, dm.H * NPT, bn, m);
-  const int h = m / NPT, p0 = (m % NPT) * PT;
+  static_assert(NPT % SL == 0, "slices per workgroup must divide the channel slices");
+  int bn, m2;
+  xcd_group_map(blockIdx.x, dm.B * dm.NT, dm.H * NPT / SL, bn, m2);
   const int bb = bn / dm.NT, n = bn % dm.NT;
   const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
   const size_t rsx = (size_t)dm.H * P;
-  const size_t base = (row0 * dm.H + h) * P + p0;
-  const float Ah = A[h];
   const T* cbg = ck.cb + (size_t)bn * C * C;
   const T* cg = Cm + row0 * N;
   const int wv_id = wave_id();
   constexpr int NB = C / 16, BPW = NB / 4, YNI = PT / 16, KN = N / Mma<T>::KS;
   static_assert(NB % 4 == 0, "row blocks must split evenly over 4 waves");
 
+  // the global operands of the output blocks (CB fragments, C rows), shared by
+  // the workgroup's slices, requested before the first slice's cumsum
+  typedef typename Mma<T>::frag frag;
+  frag fa[BPW][NB], fd[BPW], fc[BPW][KN];
+#pragma unroll
+  for (int bi = 0; bi < BPW; ++bi) {
+    const int I = y_block<NB>(wv_id, bi);
+#pragma unroll
+    for (int J = 0; J < NB; ++J)
+      if (J < I) fa[bi][J] = cb_frag<T>(cbg, C, 16 * I, 16 * J, 0);
+    fd[bi] = cb_frag<T>(cbg, C, 16 * I, 16 * I, 1);
+#pragma unroll
+    for (int kk = 0; kk < KN; ++kk) fc[bi][kk] = Mma<T>::ld_c(cg, N, 16 * I, kk * Mma<T>::KS);
+  }
+  for (int sl = 0; sl < SL; ++sl) {
+  const int m = m2 * SL + sl;
+  const int h = m / NPT, p0 = (m % NPT) * PT;
+  const size_t base = (row0 * dm.H + h) * P + p0;
+  const float Ah = A[h];
   // thread item = 8 channels of one row; 16 consecutive items take 16
   // consecutive rows (conflict-free 16-byte LDS accesses)
   constexpr int PER_ROW = PT / 8, NE = C * PER_ROW, EPT = NE / 256;
@@ -370,20 +389,6 @@ __global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __
     rx[i].load(x + base + r * rsx + c);
   }
   stage_rows<T, PT, N>(sSt, L::LN, ck.state_pre + (((size_t)bn * dm.H + h) * P + p0) * N, N);
-  // the global operands of the output blocks (CB fragments, C rows), requested
-  // now so their latency overlaps the cumsum
-  typedef typename Mma<T>::frag frag;
-  frag fa[BPW][NB], fd[BPW], fc[BPW][KN];
-#pragma unroll
-  for (int bi = 0; bi < BPW; ++bi) {
-    const int I = y_block<NB>(wv_id, bi);
-#pragma unroll
-    for (int J = 0; J < NB; ++J)
-      if (J < I) fa[bi][J] = cb_frag<T>(cbg, C, 16 * I, 16 * J, 0);
-    fd[bi] = cb_frag<T>(cbg, C, 16 * I, 16 * I, 1);
-#pragma unroll
-    for (int kk = 0; kk < KN; ++kk) fc[bi][kk] = Mma<T>::ld_c(cg, N, 16 * I, kk * Mma<T>::KS);
-  }
   int flag = 0;
   float dbx[EPT][8];
 #pragma unroll
@@ -479,6 +484,8 @@ __global__ __launch_bounds__(256) void mamba2_chunk_y(Mamba2Dims dm, const T* __
         y[base + (size_t)i * rsx + p] = sanitize(sanitize(ydiag) + yoff);
       }
     }
+  }
+  __syncthreads();  // the next slice rewrites the LDS
   }
 }
 

@@ -75,7 +75,7 @@ static Mamba2Grads<T> mamba2_grads(const Mamba2Plan& p, void* ws) {
 }
 
 // channels per workgroup of the chunk-parallel kernels
-constexpr int kOuterPT = 64, kYPT = 32;
+constexpr int kOuterPT = 64, kYPT = 32, kYSL = 2;
 
 template <int P, int N>
 static unsigned pass_grid(const Mamba2Dims& d) {
@@ -111,7 +111,7 @@ static int mamba2_forward_impl(const Mamba2Plan& p, const void* dt, const void* 
   });
   if (rc || !y) return rc;
   return L("mamba2_chunk_y", [&] {
-    hipLaunchKernelGGL((mamba2_chunk_y<T, C, P, N, kYPT>), dim3((unsigned)(d.B * d.NT * d.H * (P / kYPT))),
+    hipLaunchKernelGGL((mamba2_chunk_y<T, C, P, N, kYPT, kYSL>), dim3((unsigned)(d.B * d.NT * d.H * (P / kYPT) / kYSL)),
                        dim3(256), 0, st, d, (const T*)dt, (const T*)x, A, (const T*)Cm, ck, y);
   });
 }
