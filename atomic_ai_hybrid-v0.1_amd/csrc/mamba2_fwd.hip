@@ -328,8 +328,8 @@ __device__ __forceinline__ int y_block(int w, int b) {
 //   off the diagonal  U_i sum_{J<I} M_IJ (CB_IJ Vd_J)_i
 //   diagonal block    exp(cum_i - cum_{16I+15}) (tril(CB_II) Vd_I)_i
 // with U_i = exp(cum_i - cum_{16I}), M_IJ = exp(cum_{16I} - cum_{16J+15}).
-// SL channel slices of one head per workgroup (the CB / C fragments are
-// loaded once for them).
+// SL consecutive (head, channel slice) pairs of one chunk per workgroup (the
+// CB / C fragments are loaded once for them); (dm.H * P / PT) % SL == 0.
 template <typename T, int C, int P, int N, int PT, int SL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void mamba2_chunk_y(Mamba2Dims dm, const T* __restrict__ dt,
                                                      const T* __restrict__ x, const float* __restrict__ A,
@@ -344,7 +344,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float* sTot = reinterpret_cast<float*>(lds + L::off_tot);
 
   constexpr int NPT = P / PT;
-  static_assert(NPT % SL == 0, "slices per workgroup must divide the channel slices");
   int bn, m2;
   xcd_group_map(blockIdx.x, dm.B * dm.NT, dm.H * NPT / SL, bn, m2);
   const int bb = bn / dm.NT, n = bn % dm.NT;

@@ -75,7 +75,7 @@ static Mamba2Grads<T> mamba2_grads(const Mamba2Plan& p, void* ws) {
 }
 
 // channels per workgroup of the chunk-parallel kernels
-constexpr int kOuterPT = 64, kYPT = 32, kYSL = 2;
+constexpr int kOuterPT = 64, kYPT = 32;
 
 template <int P, int N>
 static unsigned pass_grid(const Mamba2Dims& d) {
@@ -110,9 +110,17 @@ static int mamba2_forward_impl(const Mamba2Plan& p, const void* dt, const void* 
                        d, ck, (T*)nullptr, (float*)nullptr, state0, state_final);
   });
   if (rc || !y) return rc;
+  // chunk_y workgroups take SL (head, channel slice) pairs of one chunk: 16
+  // when they divide the pairs, else the channel slices of one head
+  constexpr int NPT = P / kYPT;
+  const size_t pairs = (size_t)d.H * NPT;
   return L("mamba2_chunk_y", [&] {
-    hipLaunchKernelGGL((mamba2_chunk_y<T, C, P, N, kYPT, kYSL>), dim3((unsigned)(d.B * d.NT * d.H * (P / kYPT) / kYSL)),
-                       dim3(256), 0, st, d, (const T*)dt, (const T*)x, A, (const T*)Cm, ck, y);
+    if (pairs % 16 == 0)
+      hipLaunchKernelGGL((mamba2_chunk_y<T, C, P, N, kYPT, 16>), dim3((unsigned)(d.B * d.NT * pairs / 16)),
+                         dim3(256), 0, st, d, (const T*)dt, (const T*)x, A, (const T*)Cm, ck, y);
+    else
+      hipLaunchKernelGGL((mamba2_chunk_y<T, C, P, N, kYPT, NPT>), dim3((unsigned)(d.B * d.NT * d.H)),
+                         dim3(256), 0, st, d, (const T*)dt, (const T*)x, A, (const T*)Cm, ck, y);
   });
 }
 
