@@ -96,13 +96,14 @@ struct OuterLds {
   static_assert(C * LS * (int)sizeof(T) <= C * LC * 4, "S must fit in the cum buffer");
 };
 
-// out[p][s] = sum_i S[i][p] R[i][s] for one (batch, chunk, head, PT channels):
+// out[p][s] = sum_i S[i][p] R[i][s] for (batch, chunk, head, PT channels), SL
+// consecutive (head, slice) pairs per workgroup sharing R; (dm.H * P / PT) % SL == 0:
 //   forward  (BWD = false): S = dBx dte (the chunk's write, :133-135), R = B,
 //            out = sanitize(.) = state_end (:136-137); also the chunk's cum_last.
 //   backward (BWD = true):  S = Ydh = dy decay_h (:123 of mamba2_bwd_reference.py),
 //            R = C, out = (dy decay_h)^T C (:128); also writes Ydh and
 //            W = sanitize(dBx dte) (:135), the operands of dC_1 and dB_1.
-template <typename T, typename TD, int C, int P, int N, int PT, bool BWD>
+template <typename T, typename TD, int C, int P, int N, int PT, bool BWD, int SL>
 __global__ __launch_bounds__(256) void mamba2_chunk_outer(
     Mamba2Dims dm, const T* __restrict__ dt, const T* __restrict__ x, const float* __restrict__ A,
     const T* __restrict__ R, const TD* __restrict__ dy, Mamba2Chunks<T> ck, T* __restrict__ ydh,
@@ -115,12 +116,16 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
   T* sR = reinterpret_cast<T*>(lds + L::off_r);
 
   constexpr int NPT = P / PT;
-  int bn, m;
-  xcd_group_map(blockIdx.x, dm.B * dm.NT, dm.H * NPT, bn, m);
-  const int h = m / NPT, p0 = (m % NPT) * PT;
+  int bn, m2;
+  xcd_group_map(blockIdx.x, dm.B * dm.NT, dm.H * NPT / SL, bn, m2);
   const int bb = bn / dm.NT, n = bn % dm.NT;
   const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
   const size_t rsx = (size_t)dm.H * P;
+  // R (B or C of the chunk) is shared by the workgroup's SL (head, slice) pairs
+  stage_rows<T, C, N>(sR, L::LN, R + row0 * N, N);
+  for (int sl = 0; sl < SL; ++sl) {
+  const int m = m2 * SL + sl;
+  const int h = m / NPT, p0 = (m % NPT) * PT;
   const size_t base = (row0 * dm.H + h) * P + p0;  // element (r, c) at base + r * rsx + c
   const float Ah = A[h];
 
@@ -135,7 +140,6 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
     rx[i].load(x + base + r * rsx + c);
     if constexpr (BWD) rdy[i].load(dy + base + r * rsx + c);
   }
-  stage_rows<T, C, N>(sR, L::LN, R + row0 * N, N);
 #pragma unroll
   for (int i = 0; i < EPT; ++i) {
     const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
@@ -196,6 +200,8 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
       for (int k = 0; k < 4; ++k) acc[k] = sanitize(acc[k]);
     }
     store_tile_n(out, N, 16 * mi, 16 * ni, acc);
+  }
+  __syncthreads();  // the next pair rewrites the cum / S buffer
   }
 }
 

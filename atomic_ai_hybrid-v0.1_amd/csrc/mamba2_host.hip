@@ -99,10 +99,16 @@ static int mamba2_forward_impl(const Mamba2Plan& p, const void* dt, const void* 
   });
   if (rc) return rc;
   rc = L("mamba2_chunk_state", [&] {
-    hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false>),
-                       dim3((unsigned)(d.B * d.NT * d.H * (P / kOuterPT))), dim3(256), 0, st, d,
-                       (const T*)dt, (const T*)x, A, (const T*)Bm, (const T*)nullptr, ck, (T*)nullptr,
-                       (T*)nullptr);
+    constexpr int NPO = P / kOuterPT;
+    const size_t pairs = (size_t)d.H * NPO;
+    if (pairs % 8 == 0)
+      hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, 8>),
+                         dim3((unsigned)(d.B * d.NT * pairs / 8)), dim3(256), 0, st, d, (const T*)dt,
+                         (const T*)x, A, (const T*)Bm, (const T*)nullptr, ck, (T*)nullptr, (T*)nullptr);
+    else
+      hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, NPO>),
+                         dim3((unsigned)(d.B * d.NT * d.H)), dim3(256), 0, st, d, (const T*)dt,
+                         (const T*)x, A, (const T*)Bm, (const T*)nullptr, ck, (T*)nullptr, (T*)nullptr);
   });
   if (rc) return rc;
   rc = L("mamba2_state_pass", [&] {
@@ -168,9 +174,16 @@ static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x,
   Mamba2Grads<T> gr = mamba2_grads<T>(p, ws);
   hipStream_t st = L.st;
   rc = L("mamba2_bwd_source", [&] {
-    hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true>),
-                       dim3((unsigned)(d.B * d.NT * d.H * (P / kOuterPT))), dim3(256), 0, st, d,
-                       (const T*)dt, (const T*)x, A, (const T*)Cm, (const TD*)dy, ck, gr.ydh, gr.wr);
+    constexpr int NPO = P / kOuterPT;
+    const size_t pairs = (size_t)d.H * NPO;
+    if (pairs % 8 == 0)
+      hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true, 8>),
+                         dim3((unsigned)(d.B * d.NT * pairs / 8)), dim3(256), 0, st, d, (const T*)dt,
+                         (const T*)x, A, (const T*)Cm, (const TD*)dy, ck, gr.ydh, gr.wr);
+    else
+      hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true, NPO>),
+                         dim3((unsigned)(d.B * d.NT * d.H)), dim3(256), 0, st, d, (const T*)dt,
+                         (const T*)x, A, (const T*)Cm, (const TD*)dy, ck, gr.ydh, gr.wr);
   });
   if (rc) return rc;
   rc = L("mamba2_bwd_state_pass", [&] {
