@@ -463,17 +463,22 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
 template <typename T, int C, int K, int V, int VT>
 struct StateLds {
   static constexpr int PAD = Pad<T>::v;
-  static constexpr int LK = K + PAD, LC = C + PAD;
-  static constexpr int off_w = 0;
-  static constexpr int off_q = off_w + C * LK * (int)sizeof(T);
-  static constexpr int off_kg = off_q + C * LK * (int)sizeof(T);
-  static constexpr int off_aqk = off_kg + C * LK * (int)sizeof(T);
-  static constexpr int off_ht = off_aqk + C * LC * (int)sizeof(T);
+  static constexpr int LK = K + PAD, LC = C + PAD, LU = VT + PAD;
+  // one chunk's staged operands (offsets within a stage buffer)
+  static constexpr int s_w = 0;
+  static constexpr int s_q = s_w + C * LK * (int)sizeof(T);
+  static constexpr int s_kg = s_q + C * LK * (int)sizeof(T);
+  static constexpr int s_aqk = s_kg + C * LK * (int)sizeof(T);
+  static constexpr int s_u = s_aqk + C * LC * (int)sizeof(T);
+  static constexpr int s_gl = s_u + C * LU * (int)sizeof(T);
+  static constexpr int SB = (s_gl + K * 4 + 15) / 16 * 16;
+  static constexpr int REST = VT * LK * (int)sizeof(T) + VT * LC * (int)sizeof(T);
+  // two stage buffers when they fit: chunk n + 1 is written while chunk n
+  // computes, which also saves a barrier per chunk
+  static constexpr int NBUF = 2 * SB + REST <= 160 * 1024 ? 2 : 1;
+  static constexpr int off_ht = NBUF * SB;
   static constexpr int off_vn = off_ht + VT * LK * (int)sizeof(T);
-  static constexpr int LU = VT + PAD;
-  static constexpr int off_u = off_vn + VT * LC * (int)sizeof(T);
-  static constexpr int off_gl = off_u + C * LU * (int)sizeof(T);
-  static constexpr int total = off_gl + K * 4;
+  static constexpr int total = off_vn + VT * LC * (int)sizeof(T);
 };
 
 // Eight waves (two per SIMD): the state tiles and the [w; q] h tiles of one
@@ -484,14 +489,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                                      float* __restrict__ h_final, int save) {
   typedef StateLds<T, C, K, V, VT> L;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
-  T* sW = reinterpret_cast<T*>(lds + L::off_w);
-  T* sQ = reinterpret_cast<T*>(lds + L::off_q);
-  T* sKg = reinterpret_cast<T*>(lds + L::off_kg);
-  T* sAqk = reinterpret_cast<T*>(lds + L::off_aqk);
   T* sHt = reinterpret_cast<T*>(lds + L::off_ht);
   T* sVn = reinterpret_cast<T*>(lds + L::off_vn);
-  T* sU = reinterpret_cast<T*>(lds + L::off_u);
-  float* sGl = reinterpret_cast<float*>(lds + L::off_gl);
+  // the stage buffer the current chunk reads
+  T *sW, *sQ, *sKg, *sAqk, *sU;
+  float* sGl;
+  auto use_buf = [&](int bsel) {
+    unsigned char* bp = lds + bsel * L::SB;
+    sW = reinterpret_cast<T*>(bp + L::s_w);
+    sQ = reinterpret_cast<T*>(bp + L::s_q);
+    sKg = reinterpret_cast<T*>(bp + L::s_kg);
+    sAqk = reinterpret_cast<T*>(bp + L::s_aqk);
+    sU = reinterpret_cast<T*>(bp + L::s_u);
+    sGl = reinterpret_cast<float*>(bp + L::s_gl);
+  };
+  use_buf(0);
 
   constexpr int NVT = V / VT;
   int bh, vt;
@@ -543,24 +555,33 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     S.u.load(ck.u + bhn * C * V + v0, V);
     S.g.load(ck.gcl + bhn * K, K);
   };
-  auto commit = [&](const Stage& S) {
-    S.w.store(sW, L::LK);
-    S.q.store(sQ, L::LK);
-    S.k.store(sKg, L::LK);
-    S.a.store(sAqk, L::LC);
-    S.u.store(sU, L::LU);
-    S.g.store(sGl, K);
+  auto commit = [&](const Stage& S, int bsel) {
+    unsigned char* bp = lds + bsel * L::SB;
+    S.w.store(reinterpret_cast<T*>(bp + L::s_w), L::LK);
+    S.q.store(reinterpret_cast<T*>(bp + L::s_q), L::LK);
+    S.k.store(reinterpret_cast<T*>(bp + L::s_kg), L::LK);
+    S.a.store(reinterpret_cast<T*>(bp + L::s_aqk), L::LC);
+    S.u.store(reinterpret_cast<T*>(bp + L::s_u), L::LU);
+    S.g.store(reinterpret_cast<float*>(bp + L::s_gl), K);
   };
   Stage s0, s1;
   prefetch(s0, 0);
-  commit(s0);
+  commit(s0, 0);
   __syncthreads();
   if (dm.NT > 1) prefetch(s0, 1);
   if (dm.NT > 2) prefetch(s1, 2);
 
-  // one chunk step; S holds chunk n + 1 on entry and is refilled with chunk n + 3
+  // One chunk step; S holds chunk n + 1 on entry and is refilled with chunk n + 3.
+  // Two stage buffers: chunk n + 1 goes into the other buffer at the start (its
+  // last readers finished before the previous step's final barrier), and only
+  // two barriers are left per step (after v_new, after the new h).
   auto chunk_step = [&](int n, Stage& S) {
     const size_t bhn = (size_t)bh * dm.NT + n;
+    use_buf(L::NBUF == 2 ? (n & 1) : 0);
+    if constexpr (L::NBUF == 2) {
+      if (n + 1 < dm.NT) commit(S, (n + 1) & 1);
+      if (n + 3 < dm.NT) prefetch(S, n + 3);
+    }
       if (save) unstage_rows<T, VT, K, NTHR>(ck.hT + bhn * V * K + (size_t)v0 * K, K, sHt, L::LK);
 
       // v_new = u - w_pseudo h ; qh = qg h   (GX tiles of one row block share the A reads)
@@ -639,14 +660,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           hs[gi * GT + u] = acc[u];
         }
       }
-      __syncthreads();  // all reads of sHt / sVn / staged chunk done
+      // sHt was last read by this step's [w; q] h, before the v_new barrier;
+      // with one stage buffer, the staged chunk is still being read here
+      if constexpr (L::NBUF == 1) __syncthreads();
   #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
         store_tile_t(sHt, L::LK, 16 * mi, 16 * ni, hs[t]);
       }
-    if (n + 1 < dm.NT) commit(S);
-    if (n + 3 < dm.NT) prefetch(S, n + 3);
+    if constexpr (L::NBUF == 1) {
+      if (n + 1 < dm.NT) commit(S, 0);
+      if (n + 3 < dm.NT) prefetch(S, n + 3);
+    }
     __syncthreads();
   };
   for (int n = 0; n < dm.NT; n += 2) {
