@@ -7,18 +7,19 @@
 //                    (dy decay_h)^T C, and the operands Ydh, W of dC_1, dB_1.
 // mamba2_state_pass<BWD>   (mamba2_fwd.hip) reverse elementwise dstate carry
 //                    and the decay_chunk_end row term d_cum_last_a.
-// mamba2_bwd_chunk   one workgroup per (batch, chunk, head group): every
-//                    per-head term of :123-190 for each head and 32-channel
-//                    slice, with the cross-head sum dCB (:147-152) accumulated
-//                    in registers.  The pairwise decay of the off-diagonal
-//                    16-row blocks is factorised as in the forward; diagonal
-//                    blocks are evaluated pairwise with the reference's clip
-//                    masks.
+// mamba2_bwd_chunk   one workgroup (8 waves) per (batch, chunk, head group):
+//                    every per-head term of :123-190 for each head and
+//                    32-channel slice, with the cross-head sum dCB (:147-152)
+//                    accumulated in registers.  The pairwise decay is
+//                    factorised on 16-row blocks (below); slices outside the
+//                    factorisation's bounds are evaluated pairwise with the
+//                    reference's clip masks.
 // mamba2_bwd_bc      one workgroup per (batch, chunk, 32 state columns):
 //                    dC = dC_1 + dCB B and dB = dB_1 + dCB^T C (:127,135,
 //                    :154-156,191-192) with dC_1 = Ydh . state_prev and
 //                    dB_1 = W . dstate contracted over (head, channel).
-// mamba2_bwd_da      dA = sum over chunks of sanitize(sum over batch) (:188,194,263).
+//                    Its first H workgroups also reduce dA = sum over chunks
+//                    of sanitize(sum over batch) (:188,194,263).
 #include "mamba2_fwd.hip"
 
 namespace ah {
@@ -590,6 +591,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
+// dA[h] = sanitize(sum_n sanitize(sum_b dap[b][n][h])) (:188,194,263), by the
+// whole workgroup; red holds 4 floats of LDS.
+__device__ __forceinline__ void mamba2_da_head(const Mamba2Dims& dm, const float* __restrict__ dap,
+                                               float* __restrict__ dA, int h, float* red) {
+  float tot = 0.f;
+  for (int n = threadIdx.x; n < dm.NT; n += 256) {
+    float s = 0.f;
+    for (int b = 0; b < dm.B; ++b) s += dap[((size_t)b * dm.NT + n) * dm.H + h];
+    tot += sanitize(s);
+  }
+#pragma unroll
+  for (int sh = 1; sh < 64; sh <<= 1) tot += __shfl_xor(tot, sh);
+  if (lane_id() == 0) red[wave_id()] = tot;
+  __syncthreads();
+  if (threadIdx.x == 0) dA[h] = sanitize(red[0] + red[1] + red[2] + red[3]);
+  __syncthreads();
+}
+
 // ------------------------------------------------------------------ dB, dC
 template <typename T, int C, int NTL, int KB>
 struct BcLds {
@@ -607,11 +626,13 @@ struct BcLds {
 //   dC = sanitize(Ydh . state_prev + dCB B)     dB = sanitize(W . dstate + dCB^T C)
 // the first terms contracted over k = (head, channel): Ydh / W rows are the
 // [B][T][H][P] rows of the chunk, state_prev / dstate the [NT][H][P][N] block.
+// The first H workgroups also reduce dA (the dA partials of the chunk
+// backward are complete when this kernel starts).
 template <typename T, int C, int P, int N>
 __global__ __launch_bounds__(256) void mamba2_bwd_bc(Mamba2Dims dm, int G, const T* __restrict__ Bm,
                                                     const T* __restrict__ Cm, Mamba2Chunks<T> ck,
                                                     Mamba2Grads<T> gr, T* __restrict__ dB,
-                                                    T* __restrict__ dC) {
+                                                    T* __restrict__ dC, float* __restrict__ dA) {
   constexpr int NTL = 32, KB = 64, NNT = N / NTL;
   typedef BcLds<T, C, NTL, KB> L;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
@@ -621,6 +642,10 @@ __global__ __launch_bounds__(256) void mamba2_bwd_bc(Mamba2Dims dm, int G, const
   T* sB = reinterpret_cast<T*>(lds + L::off_b);
   T* sC = reinterpret_cast<T*>(lds + L::off_c);
 
+  {
+    __shared__ float red[4];
+    for (int hh = blockIdx.x; hh < dm.H; hh += gridDim.x) mamba2_da_head(dm, gr.dap, dA, hh, red);
+  }
   int bn, nt;
   xcd_group_map(blockIdx.x, dm.B * dm.NT, NNT, bn, nt);
   const int n0 = nt * NTL;
@@ -720,24 +745,6 @@ __global__ __launch_bounds__(256) void mamba2_bwd_bc(Mamba2Dims dm, int G, const
       store_tile_n(dCo, N, m0, 16 * ct, c);
       store_tile_n(dBo, N, m0, 16 * ct, b);
     }
-}
-
-// dA[h] = sanitize(sum_n sanitize(sum_b dap[b][n][h])); one workgroup per head.
-__global__ __launch_bounds__(256) void mamba2_bwd_da(Mamba2Dims dm, const float* __restrict__ dap,
-                                                    float* __restrict__ dA) {
-  __shared__ float red[4];
-  const int h = blockIdx.x;
-  float tot = 0.f;
-  for (int n = threadIdx.x; n < dm.NT; n += 256) {
-    float s = 0.f;
-    for (int b = 0; b < dm.B; ++b) s += dap[((size_t)b * dm.NT + n) * dm.H + h];
-    tot += sanitize(s);
-  }
-#pragma unroll
-  for (int sh = 1; sh < 64; sh <<= 1) tot += __shfl_xor(tot, sh);
-  if (lane_id() == 0) red[wave_id()] = tot;
-  __syncthreads();
-  if (threadIdx.x == 0) dA[h] = sanitize(red[0] + red[1] + red[2] + red[3]);
 }
 
 }  // namespace ah

@@ -199,12 +199,9 @@ static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x,
   if (rc) return rc;
   rc = L("mamba2_bwd_bc", [&] {
     hipLaunchKernelGGL((mamba2_bwd_bc<T, C, P, N>), dim3((unsigned)(d.B * d.NT * (N / 32))), dim3(256),
-                       0, st, d, p.G, (const T*)Bm, (const T*)Cm, ck, gr, (T*)dB, (T*)dC);
+                       0, st, d, p.G, (const T*)Bm, (const T*)Cm, ck, gr, (T*)dB, (T*)dC, dA);
   });
-  if (rc) return rc;
-  return L("mamba2_bwd_da", [&] {
-    hipLaunchKernelGGL(mamba2_bwd_da, dim3((unsigned)d.H), dim3(256), 0, st, d, (const float*)gr.dap, dA);
-  });
+  return rc;
 }
 
 template <int C, int P, int N>

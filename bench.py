@@ -111,9 +111,10 @@ def mamba2_kernel_model(B, T, H, P, N, C, es=2):
                              Uh * (3 * CP * es + 2 * PN * es + P * 4 + 2 * CP * es + 4)
                              + Ub * (2 * CN * es + CC * es + G * CC * 4)),
         # dC_1 + dB_1 over (head, channel), dCB B and dCB^T C
+        # (its first H workgroups also reduce dA from the per-chunk partials)
         "mamba2_bwd_bc": (Uh * 4 * C * PN + Ub * 4 * CC * N,
-                          Uh * (2 * CP * es + 2 * PN * es) + Ub * (G * CC * 4 + 4 * CN * es)),
-        "mamba2_bwd_da": (0.0, B * NT * H * 4 + H * 4),
+                          Uh * (2 * CP * es + 2 * PN * es) + Ub * (G * CC * 4 + 4 * CN * es)
+                          + B * NT * H * 4 + H * 4),
     }
 
 
