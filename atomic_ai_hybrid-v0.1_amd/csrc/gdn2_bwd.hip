@@ -9,10 +9,9 @@
 //   gdn2_bwd_hgrad  per chunk: the state contractions of B2/B3
 //                   (kernel_bwd_b2_dav.py:69, kernel_bwd_b3_wy_dqkg.py:154-161,
 //                   :200-201): dAqk, dqg, dw_pseudo, dkg and the gc_last row term.
-//   gdn2_bwd_wy_a   per chunk: the WY part of B3 (kernel_bwd_b3_wy_dqkg.py:163-180):
-//                   dA and dAkk = -A^T clip(clip(dA) A^T) (strict).
-//   gdn2_bwd_wy_b   per (chunk, 64 columns): dkb = A^T dw_pseudo, dwv = A^T dv
-//                   and the final dw, dv (:164,167,194-195).
+//   gdn2_bwd_wy     per chunk: the WY part of B3 (kernel_bwd_b3_wy_dqkg.py:163-180):
+//                   dA, dAkk = -A^T clip(clip(dA) A^T) (strict), dkb = A^T dw_pseudo,
+//                   dwv = A^T dv and the final dw, dv (:164,167,194-195).
 //   gdn2_bwd_intra  per chunk: B4 (kernel_bwd_b4_intra.py:57-132) in the
 //                   factorised form (or exact pairwise, same criterion as the
 //                   forward), the B3 element-wise terms, the combine of
@@ -353,36 +352,40 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
 }
 
 // ------------------------------------------------------------------ B3 WY part
-// gdn2_bwd_wy_a  per chunk: dA = clip(dw_pseudo kb^T + dv_new wv^T) with the
-//                K / V contraction staged in 64-column halves, then
-//                dAkk = n2n(-(A^T clip(dA A^T)) * strict)   (b3:163-180,212)
-// gdn2_bwd_wy_b  per (chunk, 64-column slice): dkb = A^T dw_pseudo and
-//                dwv = A^T dv_new; dw = dwv v, dv = dwv w   (b3:164,167,194-195)
+// gdn2_bwd_wy  per chunk, in 64-column halves of K / V:
+//   dA = clip(dw_pseudo kb^T + dv_new wv^T)                     (b3:163-176)
+//   dkb = n2n(A^T dw_pseudo), dwv = A^T dv_new,
+//   dw = clip(n2n(dwv v)), dv = clip(n2n(dwv w))                (b3:164,167,194-195)
+// and after the last half dAkk = n2n(-(A^T clip(dA A^T)) * strict) (b3:177-180,212).
+// Each half's k, b, v, w, dw_pseudo and dv_new are read once for both parts.
 template <typename T, int C, int KH>
-struct WyALds {
+struct WyLds {
   static constexpr int PAD = Pad<T>::v;
   static constexpr int LH = KH + PAD, LC = C + PAD;
+  static constexpr int LW = KH + 4;  // fp32 dwv rows, 16-byte aligned
   static constexpr int OH = C * LH * (int)sizeof(T), OC = C * LC * (int)sizeof(T);
   static constexpr int off_a = 0;
   static constexpr int off_dw = off_a + OC;
   static constexpr int off_dv = off_dw + OH;
   static constexpr int off_kb = off_dv + OH;  // then clip(dA A^T)
   static constexpr int off_wv = off_kb + OH;
-  static constexpr int off_da = off_wv + OH;
+  static constexpr int off_da = off_wv + OH;  // during the halves: fp32 dwv over da and tot
   static constexpr int off_tot = off_da + OC;
   static constexpr int off_gl = off_tot + ColMap<C, KH>::NSEG * KH * 4;
   static constexpr int total = off_gl + KH * 4;
   static_assert(OC <= OH * 2, "dA A^T must fit in the kb / wv region");
+  static_assert(C * LW * 4 <= off_gl - off_da, "fp32 dwv must fit in the da / tot region");
 };
 
 template <typename T, int C, int K, int V>
-__global__ __launch_bounds__(256) void gdn2_bwd_wy_a(Gdn2Dims dm, Gdn2Chunks<T> ck, Gdn2Grads<T> gr,
-                                                    const T* __restrict__ k, const T* __restrict__ v,
-                                                    const T* __restrict__ w, const T* __restrict__ b,
-                                                    const float* __restrict__ g) {
+__global__ __launch_bounds__(256) void gdn2_bwd_wy(Gdn2Dims dm, Gdn2Chunks<T> ck, Gdn2Grads<T> gr,
+                                                  const T* __restrict__ k, const T* __restrict__ v,
+                                                  const T* __restrict__ w, const T* __restrict__ b,
+                                                  const float* __restrict__ g, T* __restrict__ dw,
+                                                  T* __restrict__ dv) {
   constexpr int KH = 64;
   static_assert(K == V && K % KH == 0, "K and V are staged in the same 64-column halves");
-  typedef WyALds<T, C, KH> L;
+  typedef WyLds<T, C, KH> L;
   typedef ColMap<C, KH> M;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
   T* sA = reinterpret_cast<T*>(lds + L::off_a);
@@ -391,6 +394,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy_a(Gdn2Dims dm, Gdn2Chunks<T> 
   T* sKB = reinterpret_cast<T*>(lds + L::off_kb);
   T* sWV = reinterpret_cast<T*>(lds + L::off_wv);
   T* sDA = reinterpret_cast<T*>(lds + L::off_da);
+  float* sDwv = reinterpret_cast<float*>(lds + L::off_da);
   T* sTmp = reinterpret_cast<T*>(lds + L::off_kb);
   float* sTot = reinterpret_cast<float*>(lds + L::off_tot);
   float* sGl = reinterpret_cast<float*>(lds + L::off_gl);
@@ -402,12 +406,13 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy_a(Gdn2Dims dm, Gdn2Chunks<T> 
   const int h = bh % dm.H, bb = bh / dm.H;
   const int wv_id = wave_id();
   const size_t blk = (size_t)bhn;
-  const size_t rsK = (size_t)dm.H * K, rsV = (size_t)dm.H * V;
+  const size_t rsK = (size_t)dm.H * K;
   const size_t t0 = (size_t)bb * dm.T + (size_t)n * C;
 
   stage_rows<T, C, C>(sA, L::LC, ck.ainv + blk * C * C, C);
   constexpr int MT = C / 16;
-  constexpr int TPW = MT * MT / 4;
+  constexpr int TPW = MT * MT / 4;       // dA tiles per wave
+  constexpr int TPH = MT * (KH / 16) / 4;  // dkb / dwv tiles per wave and half
   f32x4 da[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) da[t] = zero4();
@@ -450,6 +455,38 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy_a(Gdn2Dims dm, Gdn2Chunks<T> 
       da[t] = tile_mma<T, false, false>(da[t], sDW, L::LH, sKB, L::LH, 16 * mi, 16 * nj, KH);
       da[t] = tile_mma<T, false, false>(da[t], sDV, L::LH, sWV, L::LH, 16 * mi, 16 * nj, KH);
     }
+    // dkb straight to memory; dwv (fp32) to LDS for the element-wise products
+    T* g_dkb = gr.dkb + blk * C * K + c0;
+#pragma unroll
+    for (int t = 0; t < TPH; ++t) {
+      const int tile = wv_id * TPH + t, mj = tile % MT, ni = tile / MT;
+      const int k0 = tri_k0<T>(mj);  // A lower triangular: rows i >= j only
+      f32x4 a = tile_mma<T, true, true>(zero4(), sA + k0 * L::LC, L::LC, sDW + k0 * L::LH, L::LH,
+                                        16 * mj, 16 * ni, C - k0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = n2n(a[i]);
+      store_tile_n(g_dkb, K, 16 * mj, 16 * ni, a);
+      const f32x4 d = tile_mma<T, true, true>(zero4(), sA + k0 * L::LC, L::LC, sDV + k0 * L::LH, L::LH,
+                                              16 * mj, 16 * ni, C - k0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sDwv[(16 * mj + tile_row(i)) * L::LW + 16 * ni + tile_col()] = d[i];
+    }
+    __syncthreads();
+    // dw = dwv v, dv = dwv w with this thread's v / w rows still in registers
+#pragma unroll
+    for (int rr = 0; rr < M::RS; ++rr) {
+      const int r = seg * M::RS + rr;
+      float d8[8], gw[8], gv[8];
+      load8(sDwv + r * L::LW + cg * 8, d8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        gw[j] = sanitize(n2n(d8[j] * rv[rr][j]));
+        gv[j] = sanitize(n2n(d8[j] * rw[rr][j]));
+      }
+      const size_t o = ((t0 + r) * dm.H + h) * V + c0 + cg * 8;
+      store8(dw + o, gw);
+      store8(dv + o, gv);
+    }
     __syncthreads();  // before the next half overwrites the operands
   }
 #pragma unroll
@@ -487,77 +524,6 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy_a(Gdn2Dims dm, Gdn2Chunks<T> 
       acc[i] = r > c ? n2n(-acc[i]) : 0.f;
     }
     store_tile_n(g_dakk, C, 16 * mj, 16 * nl, acc);
-  }
-}
-
-template <typename T, int C, int KH>
-struct WyBLds {
-  static constexpr int PAD = Pad<T>::v;
-  static constexpr int LH = KH + PAD, LC = C + PAD;
-  static constexpr int OH = C * LH * (int)sizeof(T), OC = C * LC * (int)sizeof(T);
-  static constexpr int off_a = 0;
-  static constexpr int off_dw = off_a + OC;
-  static constexpr int off_dv = off_dw + OH;
-  static constexpr int off_v = off_dv + OH;
-  static constexpr int off_w = off_v + OH;
-  static constexpr int total = off_w + OH;
-};
-
-template <typename T, int C, int K, int V>
-__global__ __launch_bounds__(256) void gdn2_bwd_wy_b(Gdn2Dims dm, Gdn2Chunks<T> ck, Gdn2Grads<T> gr,
-                                                    const T* __restrict__ v, const T* __restrict__ w,
-                                                    T* __restrict__ dw, T* __restrict__ dv) {
-  constexpr int KH = 64;
-  static_assert(K == V && K % KH == 0, "K and V are sliced alike");
-  typedef WyBLds<T, C, KH> L;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
-  T* sA = reinterpret_cast<T*>(lds + L::off_a);
-  T* sDW = reinterpret_cast<T*>(lds + L::off_dw);
-  T* sDV = reinterpret_cast<T*>(lds + L::off_dv);
-  T* sV = reinterpret_cast<T*>(lds + L::off_v);
-  T* sW = reinterpret_cast<T*>(lds + L::off_w);
-
-  constexpr int NKS = K / KH;
-  int bhn, ks;
-  xcd_group_map(blockIdx.x, dm.B * dm.H * dm.NT, NKS, bhn, ks);
-  const int c0 = ks * KH;
-  const int n = bhn % dm.NT;
-  const int bh = bhn / dm.NT;
-  const int h = bh % dm.H, bb = bh / dm.H;
-  const int wv_id = wave_id();
-  const size_t blk = (size_t)bhn;
-  const size_t rsV = (size_t)dm.H * V;
-  const size_t t0 = (size_t)bb * dm.T + (size_t)n * C;
-  const size_t vb = (t0 * dm.H + h) * V + c0;
-
-  stage_rows<T, C, C>(sA, L::LC, ck.ainv + blk * C * C, C);
-  stage_rows<T, C, KH>(sDW, L::LH, gr.dwt + blk * C * K + c0, K);
-  stage_rows<T, C, KH>(sDV, L::LH, gr.dvn + blk * C * V + c0, V);
-  stage_rows<T, C, KH>(sV, L::LH, v + vb, rsV);
-  stage_rows<T, C, KH>(sW, L::LH, w + vb, rsV);
-  __syncthreads();
-
-  constexpr int MT = C / 16, NT2 = KH / 16, TPW = MT * NT2 / 4;
-  T* g_dkb = gr.dkb + blk * C * K + c0;
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    const int tile = wv_id * TPW + t, mj = tile % MT, ni = tile / MT;
-    const int k0 = tri_k0<T>(mj);  // A lower triangular: rows i >= j only
-    f32x4 a = tile_mma<T, true, true>(zero4(), sA + k0 * L::LC, L::LC, sDW + k0 * L::LH, L::LH,
-                                      16 * mj, 16 * ni, C - k0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = n2n(a[i]);
-    store_tile_n(g_dkb, K, 16 * mj, 16 * ni, a);
-    const f32x4 d = tile_mma<T, true, true>(zero4(), sA + k0 * L::LC, L::LC, sDV + k0 * L::LH, L::LH,
-                                            16 * mj, 16 * ni, C - k0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 16 * mj + tile_row(i), c = 16 * ni + tile_col();
-      const float gw = sanitize(n2n(d[i] * to_f(sV[r * L::LH + c])));
-      const float gv = sanitize(n2n(d[i] * to_f(sW[r * L::LH + c])));
-      dw[vb + (size_t)r * rsV + c] = from_f<T>(gw);
-      dv[vb + (size_t)r * rsV + c] = from_f<T>(gv);
-    }
   }
 }
 

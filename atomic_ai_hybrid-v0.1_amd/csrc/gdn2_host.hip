@@ -139,14 +139,9 @@ static int gdn2_backward_impl(const Gdn2Plan& p, const void* q, const void* k, c
                        (const TD*)dO);
   });
   if (rc) return rc;
-  rc = L("gdn2_bwd_wy_a", [&] {
-    hipLaunchKernelGGL((gdn2_bwd_wy_a<T, C, K, V>), dim3(nblk), dim3(256), 0, st, p.dm, ck, gr,
-                       (const T*)k, (const T*)v, (const T*)w, (const T*)b, g);
-  });
-  if (rc) return rc;
-  rc = L("gdn2_bwd_wy_b", [&] {
-    hipLaunchKernelGGL((gdn2_bwd_wy_b<T, C, K, V>), dim3(nblk * (K / 64)), dim3(256), 0, st, p.dm, ck,
-                       gr, (const T*)v, (const T*)w, (T*)dw, (T*)dv);
+  rc = L("gdn2_bwd_wy", [&] {
+    hipLaunchKernelGGL((gdn2_bwd_wy<T, C, K, V>), dim3(nblk), dim3(256), 0, st, p.dm, ck, gr,
+                       (const T*)k, (const T*)v, (const T*)w, (const T*)b, g, (T*)dw, (T*)dv);
   });
   if (rc) return rc;
   constexpr int KH = 64;  // column slice of the intra kernel

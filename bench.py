@@ -62,12 +62,9 @@ def gdn2_kernel_model(B, T, H, K, V, C, es=2, save=True):
         "gdn2_bwd_hgrad": (U * (2 * CC * V + 6 * C * KV),
                            U * (CV * es + CV * es + 2 * KV * es + CV * es + K * 4  # dO dvn h dh vn gcl
                                 + CC * es + 3 * CK * es + K * 4)),           # daqk dqg dwt dkg rlast
-        "gdn2_bwd_wy_a": (U * (2 * CC * K + 2 * CC * V + 4 * C ** 3),
-                          U * (CC * es + CK * es + CV * es + 2 * CK * es + 2 * CV * es + CK * 4  # ainv dwt dvn k b v w g
-                               + CC * es)),                                  # dakk
-        "gdn2_bwd_wy_b": (U * (2 * CC * K + 2 * CC * V),
-                          U * (CC * es + CK * es + CV * es + 2 * CV * es     # ainv dwt dvn v w
-                               + CK * es + 2 * CV * es)),                    # dkb dw dv
+        "gdn2_bwd_wy": (U * (4 * CC * K + 4 * CC * V + 4 * C ** 3),
+                        U * (CC * es + CK * es + CV * es + 2 * CK * es + 2 * CV * es + CK * 4  # ainv dwt dvn k b v w g
+                             + CC * es + CK * es + 2 * CV * es)),            # dakk dkb dw dv
         "gdn2_bwd_intra": (U * 8 * CC * K,
                            U * (3 * CK * es + CK * 4 + 2 * CC * es + 3 * CK * es + K * 4  # q k b g daqk dakk dqg dkb dkg rlast
                                 + 3 * CK * es + CK * 4)),                    # dq dk db dg
