@@ -177,6 +177,19 @@ __device__ __forceinline__ P* opaque_ptr(P* p) {
   return p;
 }
 
+// f(IntC<i>{}) for a runtime i in [0, N): the body is compiled once per value
+// with i a constant (for wave-uniform i, a chain of scalar compares).
+template <int V> struct IntC { static constexpr int value = V; };
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_switch(int i, F&& f) {
+  if constexpr (I + 1 >= N) {
+    f(IntC<I>{});
+  } else {
+    if (i == I) f(IntC<I>{});
+    else static_switch<N, I + 1>(i, f);
+  }
+}
+
 __device__ __forceinline__ f32x4 zero4() { f32x4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
 
 // Tile element coordinates held by this lane: rows m0 + 4g + i, column n0 + r.

@@ -158,7 +158,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   xcd_group_map(blockIdx.x, dm.B * dm.NT, G, bn, g);
   const int bb = bn / dm.NT, n = bn % dm.NT;
   const int HG = dm.H / G;
-  const int wv_id = wave_id();
+  const int wv_id = __builtin_amdgcn_readfirstlane(wave_id());  // wave-uniform: scalar branches
   const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
   const T* Bg0 = Bm + row0 * N;
   const T* Cg0 = Cm + row0 * N;
@@ -240,6 +240,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // this wave's block, also rebuilt per iteration (its addresses stay in the loop)
       const int I = I0 + z, ni0 = ni00 + z;
       const size_t rowz = row0 + z;
+      // dx / ddt of this lane (rows 16 I + tile_row(ii), channels p0 + 16 (ni0 + q) + tile_col())
+      // as a uniform base and 32-bit lane offsets
+      const unsigned HP = (unsigned)(dm.H * P);
+      const unsigned olane = (unsigned)tile_row(0) * HP + (unsigned)(16 * ni0 + tile_col());
       // the C / B rows of this wave's block for y_off / dwrite, requested now
       frag cfr[N / 32], bfr[N / 32];
 #pragma unroll
@@ -292,6 +296,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       __syncthreads();
       // block-pair decays (one exp per pair and channel, shared by phases C and D)
       // and the range check on the diagonal pairs
+#pragma unroll
       for (int e = tid; e < NBC * PT; e += NTH) {
         const int k = e / PT, p = e % PT;
         int TI, TJ;
@@ -301,7 +306,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (TI == TJ) flag |= d > kMaxRange;
       }
       // positive step exponent or too steep a block: pairwise evaluation
-      const bool exact = __syncthreads_or(flag);
+      const bool exact = __builtin_amdgcn_readfirstlane(__syncthreads_or(flag)) != 0;
 
       // ---- B: operands Yu = dy U, Vd = V dBx (bf16 high + low parts), from the
       // registers of A
@@ -393,56 +398,51 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       {
         f32x4 Rv[NIW], Sv[NIW];
         if (!exact) {
-          f32x4 ro[NIW], rd[NIW], so[NIW], sd[NIW];
+          // ra = sum_{J <= I} M_IJ (CB_IJ Vd_J) and sa = sum_{J >= I} M_JI (CB_JI^T Yu_J),
+          // the diagonal block masked to its lower / upper triangle.  With
+          // M_II = exp(cum_{16I} - cum_{16I+15}) the row scales U_i, V_i below turn
+          // the diagonal terms into exp(ci - ce) (CB_II Vd_I) and exp(cs - ci) (CB_II^T Yu_I).
+          // Compiled per block index, so every operand read is issued up front.
+          f32x4 ra[NIW], sa[NIW];
 #pragma unroll
-          for (int q = 0; q < NIW; ++q) { ro[q] = zero4(); so[q] = zero4(); }
-          // CB(I, J) for J < I (row side), CB^T(I, J) for J > I (column side)
-          // and the diagonal, read from the chunk's CB in LDS where used
-          const frag ar = cb_lds_dup<T>(sCB, L::LCB, 16 * I, 16 * I, 1, false);
-          const frag as = cb_lds_dup<T>(sCB, L::LCB, 16 * I, 16 * I, 2, true);
+          for (int q = 0; q < NIW; ++q) { ra[q] = zero4(); sa[q] = zero4(); }
+          static_switch<NB>(I - z, [&](auto Ic) {
+            constexpr int IS = decltype(Ic)::value;
 #pragma unroll
-          for (int J = 0; J < NB; ++J) {
-            if (J < I) {  // sources below the block
-              const frag fa = cb_lds_dup<T>(sCB, L::LCB, 16 * I, 16 * J, 0, false);
+            for (int J = 0; J <= IS; ++J) {  // sources at or below the block (row side)
+              const frag fa = cb_lds_dup<T>(sCB, L::LCB, 16 * IS, 16 * J, J == IS ? 1 : 0, false);
+              const float* mr = sM + (IS * (IS + 1) / 2 + J) * PT;
 #pragma unroll
               for (int q = 0; q < NIW; ++q) {
                 const int ni = ni0 + q;
                 const f32x4 m = Mma<T>::mma(fa, ld_t_hilo<T>(sVd, sVdl, L::LPT, 16 * ni, 16 * J), zero4());
-                const int pc = 16 * ni + tile_col();
-                const float mf = sM[(I * (I + 1) / 2 + J) * PT + pc];
+                const float mf = mr[16 * ni + tile_col()];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) ro[q][k] += mf * m[k];
+                for (int k = 0; k < 4; ++k) ra[q][k] += mf * m[k];
               }
-            } else if (J > I) {  // targets above the block (column side)
-              const frag fa = cb_lds_dup<T>(sCB, L::LCB, 16 * I, 16 * J, 0, true);
+            }
+#pragma unroll
+            for (int J = IS; J < NB; ++J) {  // targets at or above the block (column side)
+              const frag fa = cb_lds_dup<T>(sCB, L::LCB, 16 * IS, 16 * J, J == IS ? 2 : 0, true);
+              const float* mc = sM + (J * (J + 1) / 2 + IS) * PT;
 #pragma unroll
               for (int q = 0; q < NIW; ++q) {
                 const int ni = ni0 + q;
                 const f32x4 m = Mma<T>::mma(fa, ld_t_hilo<T>(sYu, sYul, L::LPT, 16 * ni, 16 * J), zero4());
-                const int pc = 16 * ni + tile_col();
-                const float mf = sM[(J * (J + 1) / 2 + I) * PT + pc];
+                const float mf = mc[16 * ni + tile_col()];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) so[q][k] += mf * m[k];
+                for (int k = 0; k < 4; ++k) sa[q][k] += mf * m[k];
               }
             }
-          }
-          {  // the diagonal block
-#pragma unroll
-            for (int q = 0; q < NIW; ++q) {
-              const int ni = ni0 + q;
-              rd[q] = Mma<T>::mma(ar, ld_t_hilo<T>(sVd, sVdl, L::LPT, 16 * ni, 16 * I), zero4());
-              sd[q] = Mma<T>::mma(as, ld_t_hilo<T>(sYu, sYul, L::LPT, 16 * ni, 16 * I), zero4());
-            }
-          }
+          });
 #pragma unroll
           for (int q = 0; q < NIW; ++q) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
               const int i = 16 * I + tile_row(k), p = 16 * (ni0 + q) + tile_col();
               const float ci = sCum[i * L::LC + p];
-              const float cs = sCum[16 * I * L::LC + p], ce = sCum[(16 * I + 15) * L::LC + p];
-              Rv[q][k] = __expf(ci - cs) * ro[q][k] + __expf(ci - ce) * rd[q][k];
-              Sv[q][k] = __expf(ce - ci) * so[q][k] + __expf(cs - ci) * sd[q][k];
+              Rv[q][k] = __expf(ci - sCum[16 * I * L::LC + p]) * ra[q][k];
+              Sv[q][k] = __expf(sCum[(16 * I + 15) * L::LC + p] - ci) * sa[q][k];
             }
           }
         }
@@ -496,9 +496,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const float m1 = (ci >= -kClipDecay && ci <= 0.f) ? 1.f : 0.f;
             const float dw = dwr[ii];
             const float ddbx = sanitize(dw * dte + ssum);                 // :138,148,166
-            const size_t o = ((rowz + i) * dm.H + h) * P + p0 + p;
             ddt1v[q][ii] = ddbx * xv;                                     // :167
-            dx[o] = from_f<T>(sanitize(ddbx * dtv));                     // :168,193 + final
+            dx[((rowz + 16 * I) * dm.H + h) * P + p0 + (olane + ii * HP + 16 * q)] =
+                from_f<T>(sanitize(ddbx * dtv));                          // :168,193 + final
             const float dte_term = dw * dbxi * dte * m2;                  // d_decay_to_end_diff :142
             lastb[q][ii] += dte_term;
             // d_cum of this element (:162-173), masked for the reverse cumsum (:181-186)
@@ -539,7 +539,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int q = 0; q < NIW; ++q) {
         const int p = 16 * (ni0 + q) + tile_col();
         float off = gsuf[q];
-        for (int J = I + 1; J < NB; ++J) off += sTot[J * PT + p];
+#pragma unroll
+        for (int J = 1; J < NB; ++J) off += J > I ? sTot[J * PT + p] : 0.f;
         // row C-1 extra terms (:176-177), under row C-1's clip mask
         float extra = sLastA[p];
 #pragma unroll
@@ -551,8 +552,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           const float dtv = to_f(sDt[i * L::LPT + p]);
           const float araw = dtv * Ah;
           const float dA = (araw >= -kClipDecay && araw <= kClipDecay) ? (redv[q][ii] + off) : 0.f;
-          const size_t o = ((rowz + i) * dm.H + h) * P + p0 + p;
-          ddt[o] = from_f<T>(sanitize(ddt1v[q][ii] + dA * Ah));   // :187,190 + final
+          ddt[((rowz + 16 * I) * dm.H + h) * P + p0 + (olane + ii * HP + 16 * q)] =
+              from_f<T>(sanitize(ddt1v[q][ii] + dA * Ah));                // :187,190 + final
           da += dA * dtv;
         }
       }

@@ -76,8 +76,9 @@ __device__ __forceinline__ void column_cumsum(float* sCum, float* sTot) {
   for (int r = 1; r < RS; ++r) v[r] += v[r - 1];
   sTot[seg * PT + p] = v[RS - 1];
   __syncthreads();
-  float off = 0.f;
-  for (int s = 0; s < seg; ++s) off += sTot[s * PT + p];
+  float off = 0.f;  // all lower segment totals requested at once
+#pragma unroll
+  for (int s = 0; s < NSEG - 1; ++s) off += s < seg ? sTot[s * PT + p] : 0.f;
 #pragma unroll
   for (int r = 0; r < RS; ++r) sCum[(seg * RS + r) * LD + p] = sanitize(v[r] + off, kClipAcc);
 }
