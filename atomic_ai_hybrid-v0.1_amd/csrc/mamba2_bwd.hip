@@ -593,11 +593,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // dA[h] = sanitize(sum_n sanitize(sum_b dap[b][n][h])) (:188,194,263), by the
-// whole workgroup; red holds 4 floats of LDS.
+// whole workgroup of NTH threads; red holds NTH / 64 floats of LDS.
+template <int NTH>
 __device__ __forceinline__ void mamba2_da_head(const Mamba2Dims& dm, const float* __restrict__ dap,
                                                float* __restrict__ dA, int h, float* red) {
   float tot = 0.f;
-  for (int n = threadIdx.x; n < dm.NT; n += 256) {
+  for (int n = threadIdx.x; n < dm.NT; n += NTH) {
     float s = 0.f;
     for (int b = 0; b < dm.B; ++b) s += dap[((size_t)b * dm.NT + n) * dm.H + h];
     tot += sanitize(s);
@@ -606,7 +607,12 @@ __device__ __forceinline__ void mamba2_da_head(const Mamba2Dims& dm, const float
   for (int sh = 1; sh < 64; sh <<= 1) tot += __shfl_xor(tot, sh);
   if (lane_id() == 0) red[wave_id()] = tot;
   __syncthreads();
-  if (threadIdx.x == 0) dA[h] = sanitize(red[0] + red[1] + red[2] + red[3]);
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < NTH / 64; ++w) t += red[w];
+    dA[h] = sanitize(t);
+  }
   __syncthreads();
 }
 
@@ -628,13 +634,15 @@ struct BcLds {
 // the first terms contracted over k = (head, channel): Ydh / W rows are the
 // [B][T][H][P] rows of the chunk, state_prev / dstate the [NT][H][P][N] block.
 // The first H workgroups also reduce dA (the dA partials of the chunk
-// backward are complete when this kernel starts).
+// backward are complete when this kernel starts).  Eight waves, four per SIMD
+// with two workgroups on a CU, so many k blocks' loads are in flight at once.
 template <typename T, int C, int P, int N>
-__global__ __launch_bounds__(256) void mamba2_bwd_bc(Mamba2Dims dm, int G, const T* __restrict__ Bm,
-                                                    const T* __restrict__ Cm, Mamba2Chunks<T> ck,
-                                                    Mamba2Grads<T> gr, T* __restrict__ dB,
-                                                    T* __restrict__ dC, float* __restrict__ dA) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void mamba2_bwd_bc(
+    Mamba2Dims dm, int G, const T* __restrict__ Bm, const T* __restrict__ Cm, Mamba2Chunks<T> ck,
+    Mamba2Grads<T> gr, T* __restrict__ dB, T* __restrict__ dC, float* __restrict__ dA) {
+  constexpr int NTH = 512, NW = NTH / 64;
   constexpr int NTL = 32, KB = 64, NNT = N / NTL;
+  static_assert(P % KB == 0, "whole k blocks per head");
   typedef BcLds<T, C, NTL, KB> L;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
   T* sS = reinterpret_cast<T*>(lds + L::off_s);
@@ -644,8 +652,8 @@ __global__ __launch_bounds__(256) void mamba2_bwd_bc(Mamba2Dims dm, int G, const
   T* sC = reinterpret_cast<T*>(lds + L::off_c);
 
   {
-    __shared__ float red[4];
-    for (int hh = blockIdx.x; hh < dm.H; hh += gridDim.x) mamba2_da_head(dm, gr.dap, dA, hh, red);
+    __shared__ float red[NW];
+    for (int hh = blockIdx.x; hh < dm.H; hh += gridDim.x) mamba2_da_head<NTH>(dm, gr.dap, dA, hh, red);
   }
   int bn, nt;
   xcd_group_map(blockIdx.x, dm.B * dm.NT, NNT, bn, nt);
@@ -657,95 +665,100 @@ __global__ __launch_bounds__(256) void mamba2_bwd_bc(Mamba2Dims dm, int G, const
   const T* sg = ck.state_pre + (size_t)bn * HP * N + n0;
   const T* dg = gr.dstate + (size_t)bn * HP * N + n0;
 
-  stage_rows<T, C, NTL>(sB, L::LK, Bm + row0 * N + n0, N);
-  stage_rows<T, C, NTL>(sC, L::LK, Cm + row0 * N + n0, N);
-  // dCB = the sum of the head-group partials (lower triangle), 4 columns per item
-  const float* part = gr.part + (size_t)bn * G * C * C;
-#pragma unroll 4
-  for (int e4 = threadIdx.x; e4 < C * C / 4; e4 += 256) {
-    const int i = (4 * e4) / C, j = (4 * e4) % C;
-    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (j <= i)
-      for (int gg = 0; gg < G; ++gg) {
-        const float4 v = *reinterpret_cast<const float4*>(part + (size_t)gg * C * C + 4 * e4);
-        s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
-      }
-    const f32x4 sv = {j <= i ? s.x : 0.f, j + 1 <= i ? s.y : 0.f, j + 2 <= i ? s.z : 0.f,
-                      j + 3 <= i ? s.w : 0.f};
-    store4(sCB + i * L::LCB + j, sv);
-  }
-
-  constexpr int RT = C / 64, CT = NTL / 16;  // row tiles per wave, column tiles
-  const int wv_id = wave_id();
-  f32x4 accC[RT][CT], accB[RT][CT];
+  // output tiles [C / 16][NTL / 16]: wave w owns TPW consecutive column tiles of one row tile
+  constexpr int CT = NTL / 16, NTILE = (C / 16) * CT, TPW = NTILE / NW;
+  static_assert(TPW >= 1 && NTILE % NW == 0 && CT % TPW == 0, "a wave's tiles share one row tile");
+  const int wv_id = __builtin_amdgcn_readfirstlane(wave_id());
+  const int m0 = 16 * ((wv_id * TPW) / CT), ct0 = (wv_id * TPW) % CT;
+  f32x4 accC[TPW], accB[TPW];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) { accC[rt][ct] = zero4(); accB[rt][ct] = zero4(); }
+  for (int u = 0; u < TPW; ++u) { accC[u] = zero4(); accB[u] = zero4(); }
 
-  // the state_prev / dstate block of the next kb staged in registers, and the
-  // Ydh / W fragments of the next kb (global, this wave's rows) in registers
+  // k blocks in flight two ahead: the state_prev / dstate block staged in
+  // registers and the Ydh / W fragments of this wave's rows
   constexpr int KK = KB / Mma<T>::KS;
   typedef typename Mma<T>::frag frag;
-  RegStage<T, KB, NTL> ps, pd;
-  frag ayn[RT][KK], awn[RT][KK];
-  auto load_a = [&](int kb) {
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-      for (int q = 0; q < KK; ++q) {
-        const int m0 = 16 * (RT * wv_id + rt);
-        ayn[rt][q] = Mma<T>::ld_c(yg, HP, m0, kb + q * Mma<T>::KS);
-        awn[rt][q] = Mma<T>::ld_c(wg, HP, m0, kb + q * Mma<T>::KS);
-      }
+  struct Stage {
+    RegStage<T, KB, NTL, NTH> ps, pd;
+    frag ay[KK], aw[KK];
   };
-  ps.load(sg, N);
-  pd.load(dg, N);
-  load_a(0);
-  for (int kb = 0; kb < HP; kb += KB) {
-    frag ay[RT][KK], aw[RT][KK];
+  auto load = [&](Stage& st, int kb) {
+    st.ps.load(sg + (size_t)kb * N, N);
+    st.pd.load(dg + (size_t)kb * N, N);
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-      for (int q = 0; q < KK; ++q) { ay[rt][q] = ayn[rt][q]; aw[rt][q] = awn[rt][q]; }
-    __syncthreads();  // previous block's reads done
-    ps.store(sS, L::LK);
-    pd.store(sD, L::LK);
-    if (kb + KB < HP) {
-      ps.load(sg + (size_t)(kb + KB) * N, N);
-      pd.load(dg + (size_t)(kb + KB) * N, N);
-      load_a(kb + KB);
+    for (int q = 0; q < KK; ++q) {
+      st.ay[q] = Mma<T>::ld_c(yg, HP, m0, kb + q * Mma<T>::KS);
+      st.aw[q] = Mma<T>::ld_c(wg, HP, m0, kb + q * Mma<T>::KS);
     }
+  };
+  Stage s0, s1;
+  load(s0, 0);
+  // dCB = the sum of the head-group partials (lower triangle), 4 columns per
+  // item; one group's loads of all this thread's items are in flight together
+  const float* part = gr.part + (size_t)bn * G * C * C;
+  constexpr int E4 = C * C / 4 / NTH;
+  static_assert(E4 * NTH * 4 == C * C, "whole items per thread");
+  f32x4 cbs[E4];
+#pragma unroll
+  for (int t = 0; t < E4; ++t) cbs[t] = zero4();
+  for (int gg = 0; gg < G; ++gg) {
+    f32x4 v[E4];
+#pragma unroll
+    for (int t = 0; t < E4; ++t)
+      v[t] = *reinterpret_cast<const f32x4*>(part + (size_t)gg * C * C + 4 * (threadIdx.x + NTH * t));
+#pragma unroll
+    for (int t = 0; t < E4; ++t) cbs[t] += v[t];
+  }
+#pragma unroll
+  for (int t = 0; t < E4; ++t) {
+    const int e4 = threadIdx.x + NTH * t, i = (4 * e4) / C, j = (4 * e4) % C;
+    f32x4 sv;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) sv[c] = j + c <= i ? cbs[t][c] : 0.f;
+    store4(sCB + i * L::LCB + j, sv);
+  }
+  if (KB < HP) load(s1, KB);
+  stage_rows<T, C, NTL, NTH>(sB, L::LK, Bm + row0 * N + n0, N);
+  stage_rows<T, C, NTL, NTH>(sC, L::LK, Cm + row0 * N + n0, N);
+
+  // one k block: its staged rows to LDS, the stage refilled two blocks ahead,
+  // then the MFMAs on the fragments kept from the stage
+  auto step = [&](Stage& st, int kb) {
+    frag ay[KK], aw[KK];
+#pragma unroll
+    for (int q = 0; q < KK; ++q) { ay[q] = st.ay[q]; aw[q] = st.aw[q]; }
+    __syncthreads();  // previous block's reads done
+    st.ps.store(sS, L::LK);
+    st.pd.store(sD, L::LK);
+    if (kb + 2 * KB < HP) load(st, kb + 2 * KB);
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < KK; ++q) {
       const int kk = q * Mma<T>::KS;
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        const frag bs = Mma<T>::ld_t(sS, L::LK, 16 * ct, kk);
-        const frag bd = Mma<T>::ld_t(sD, L::LK, 16 * ct, kk);
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          accC[rt][ct] = Mma<T>::mma(ay[rt][q], bs, accC[rt][ct]);
-          accB[rt][ct] = Mma<T>::mma(aw[rt][q], bd, accB[rt][ct]);
-        }
+      for (int u = 0; u < TPW; ++u) {
+        const int ct = ct0 + u;
+        accC[u] = Mma<T>::mma(ay[q], Mma<T>::ld_t(sS, L::LK, 16 * ct, kk), accC[u]);
+        accB[u] = Mma<T>::mma(aw[q], Mma<T>::ld_t(sD, L::LK, 16 * ct, kk), accB[u]);
       }
     }
+  };
+  for (int kb = 0; kb < HP; kb += 2 * KB) {
+    step(s0, kb);
+    if (kb + KB < HP) step(s1, kb + KB);
   }
   T* dCo = dC + row0 * N + n0;
   T* dBo = dB + row0 * N + n0;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
+  for (int u = 0; u < TPW; ++u) {
+    const int ct = ct0 + u;
+    f32x4 c = tile_mma<T, false, true>(accC[u], sCB, L::LCB, sB, L::LK, m0, 16 * ct, C);
+    f32x4 b = tile_mma<T, true, true>(accB[u], sCB, L::LCB, sC, L::LK, m0, 16 * ct, C);
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      const int m0 = 16 * (RT * wv_id + rt);
-      f32x4 c = tile_mma<T, false, true>(accC[rt][ct], sCB, L::LCB, sB, L::LK, m0, 16 * ct, C);
-      f32x4 b = tile_mma<T, true, true>(accB[rt][ct], sCB, L::LCB, sC, L::LK, m0, 16 * ct, C);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) { c[k] = sanitize(c[k]); b[k] = sanitize(b[k]); }
-      store_tile_n(dCo, N, m0, 16 * ct, c);
-      store_tile_n(dBo, N, m0, 16 * ct, b);
-    }
+    for (int k = 0; k < 4; ++k) { c[k] = sanitize(c[k]); b[k] = sanitize(b[k]); }
+    store_tile_n(dCo, N, m0, 16 * ct, c);
+    store_tile_n(dBo, N, m0, 16 * ct, b);
+  }
 }
 
 }  // namespace ah
