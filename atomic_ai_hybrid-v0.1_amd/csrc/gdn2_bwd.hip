@@ -539,13 +539,13 @@ struct InLds {
   static constexpr int off_kb = off_kt + OK_;// b k e^{gc} (exact path: then raw b)
   static constexpr int off_daqk = off_kb + OK_;
   static constexpr int off_dakk = off_daqk + OC;
-  static constexpr int off_tot = off_dakk + OC;
-  static constexpr int off_gl = off_tot + ColMap<C, K>::NSEG * K * 4;
-  static constexpr int off_part = off_gl + K * 4;  // [4][K] column partial sums
-  static constexpr int total = off_part + 4 * K * 4;
+  static constexpr int off_tot = off_dakk + OC;  // the cross-wave segment totals: 4 K floats
   // factorised path, after the MFMAs: dQ~, dK~, dKB as fp32 [C][LG] from off_q
   static constexpr int off_res = off_q;
-  static_assert(off_res + 3 * C * LG * 4 <= off_gl, "the MFMA results must fit before gc_last");
+  static constexpr int end_res = off_res + 3 * C * LG * 4;
+  static constexpr int off_gl = end_res > off_tot + 4 * K * 4 ? end_res : off_tot + 4 * K * 4;
+  static constexpr int off_part = off_gl + K * 4;  // [4 C / 16][K] column partial sums
+  static constexpr int total = off_part + 4 * (C / 16) * K * 4;
 };
 
 // One workgroup per (batch, head, chunk, KH-column slice): every term of B4,
@@ -642,7 +642,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // Tiles of [C][K], column-major over tiles so each wave owns whole columns.
   constexpr int MT = C / 16, NTK = KH / 16;
   constexpr int TPW = MT * NTK / 4;
-  static_assert((MT * NTK) % 4 == 0 && TPW % MT == 0, "each wave must own whole tile columns");
+  static_assert((MT * NTK) % 4 == 0 && (TPW % MT == 0 || MT % TPW == 0),
+                "a wave's tiles must be whole tile columns or part of one");
+  // waves sharing a tile column (exact path partial sums)
+  constexpr int WPC = TPW < MT ? MT / TPW : 1;
   f32x4 dQt[TPW], dKt[TPW], dKB[TPW];
   if (!exact) {
     // dQ~ = (scale dAqk) K~ ; dK~ = (scale dAqk)^T Q~ + dAkk^T KB ; dKB = dAkk K~
@@ -798,9 +801,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         db[go] = from_f<T>(sanitize(db3 + db4));
         dgp[(size_t)r * rsK + d] = dgc3 + dgc4;
       }
-      if ((t + 1) % MT == 0) {  // a tile column is complete: its partial sums go out
-        const int ni = tile / MT;
-        sPart[(lane_id() >> 4) * KH + 16 * ni + tile_col()] = colsum;
+      if ((t + 1) % MT == 0 || t + 1 == TPW) {  // this wave's part of a tile column is done
+        const int ni = tile / MT, pi = WPC > 1 ? (wv_id * TPW % MT) / TPW : 0;
+        sPart[(4 * pi + (lane_id() >> 4)) * KH + 16 * ni + tile_col()] = colsum;
         colsum = 0.f;
       }
     }
@@ -811,8 +814,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     __syncthreads();
     if (tid < KH) {
-      const float extra = sPart[tid] + sPart[KH + tid] + sPart[2 * KH + tid] + sPart[3 * KH + tid] +
-                          gr.rlast[blk * K + d0 + tid];
+      float extra = 0.f;
+#pragma unroll
+      for (int sl = 0; sl < 4 * WPC; ++sl) extra += sPart[sl * KH + tid];
+      extra += gr.rlast[blk * K + d0 + tid];
       // dgc3 gets the row term before its n2n in the reference; dgc4 is already
       // sanitized, so the sum below matches dgc3 + dgc4 in unclipped regimes.
       sGc[(C - 1) * L::LG + tid] += extra;
