@@ -22,6 +22,7 @@ typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kClipAcc = 1e4f;
 constexpr float kClipDecay = 20.0f;
@@ -190,6 +191,15 @@ __device__ __forceinline__ void static_switch(int i, F&& f) {
   }
 }
 
+// f(IntC<0>{}), ..., f(IntC<N - 1>{}): a loop whose index is a constant in the body.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(IntC<I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
 __device__ __forceinline__ f32x4 zero4() { f32x4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
 
 // Tile element coordinates held by this lane: rows m0 + 4g + i, column n0 + r.
@@ -296,18 +306,18 @@ __device__ __forceinline__ void stage_rows(T* dst, int dst_ld, const T* src, siz
   constexpr int VEC = 16 / sizeof(T);
   constexpr int PER_ROW = D / VEC;
   constexpr int NP = R * PER_ROW, IT = (NP + NTH - 1) / NTH;
-  uint4 tmp[IT];
+  u32x4 tmp[IT];  // native vectors: the array stays in registers
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int e = threadIdx.x + NTH * i;
     if (NP % NTH == 0 || e < NP)
-      tmp[i] = *reinterpret_cast<const uint4*>(src + (size_t)(e / PER_ROW) * src_ld + (e % PER_ROW) * VEC);
+      tmp[i] = *reinterpret_cast<const u32x4*>(src + (size_t)(e / PER_ROW) * src_ld + (e % PER_ROW) * VEC);
   }
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int e = threadIdx.x + NTH * i;
     if (NP % NTH == 0 || e < NP)
-      *reinterpret_cast<uint4*>(dst + (e / PER_ROW) * dst_ld + (e % PER_ROW) * VEC) = tmp[i];
+      *reinterpret_cast<u32x4*>(dst + (e / PER_ROW) * dst_ld + (e % PER_ROW) * VEC) = tmp[i];
   }
 }
 template <typename T, int R, int D, int NTH = 256>
@@ -315,18 +325,18 @@ __device__ __forceinline__ void unstage_rows(T* dst, size_t dst_ld, const T* src
   constexpr int VEC = 16 / sizeof(T);
   constexpr int PER_ROW = D / VEC;
   constexpr int NP = R * PER_ROW, IT = (NP + NTH - 1) / NTH;
-  uint4 tmp[IT];
+  u32x4 tmp[IT];  // native vectors: the array stays in registers
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int e = threadIdx.x + NTH * i;
     if (NP % NTH == 0 || e < NP)
-      tmp[i] = *reinterpret_cast<const uint4*>(src + (e / PER_ROW) * src_ld + (e % PER_ROW) * VEC);
+      tmp[i] = *reinterpret_cast<const u32x4*>(src + (e / PER_ROW) * src_ld + (e % PER_ROW) * VEC);
   }
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int e = threadIdx.x + NTH * i;
     if (NP % NTH == 0 || e < NP)
-      *reinterpret_cast<uint4*>(dst + (size_t)(e / PER_ROW) * dst_ld + (e % PER_ROW) * VEC) = tmp[i];
+      *reinterpret_cast<u32x4*>(dst + (size_t)(e / PER_ROW) * dst_ld + (e % PER_ROW) * VEC) = tmp[i];
   }
 }
 

@@ -317,8 +317,9 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
     float eqk[PER], ekk[PER];
     intra_scores_exact<T, C, K>(sGcExact, qc, kc, bc, rsK, dm.scale, eqk, ekk);
     __syncthreads();
-    for (int e = tid, s = 0; e < C * C; e += 256, ++s) {
-      const int i = e / C, j = e % C;
+#pragma unroll
+    for (int s = 0; s < PER; ++s) {
+      const int e = tid + 256 * s, i = e / C, j = e % C;
       g_aqk[i * C + j] = from_f<T>(eqk[s]);
       sAf[i * L::LA + j] = ekk[s];
     }
@@ -345,7 +346,8 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
       for (int i = 0; i < 16; ++i) {
         float s = (i == lane) ? 1.f : 0.f;
 #pragma unroll
-        for (int j = 0; j < i; ++j) s -= sAf[(o + i) * L::LA + o + j] * x[j];
+        for (int j = 0; j < 15; ++j)  // constant trip count: x stays in registers
+          if (j < i) s -= sAf[(o + i) * L::LA + o + j] * x[j];
         x[i] = s;
       }
 #pragma unroll

@@ -327,7 +327,7 @@ struct YLds {
 // Output block of wave w's b-th assignment: blocks {w, NB-1-w} balance the
 // number of off-diagonal source blocks over the four waves.
 template <int NB>
-__device__ __forceinline__ int y_block(int w, int b) {
+__device__ __forceinline__ constexpr int y_block(int w, int b) {
   return b == 0 ? w : NB - 1 - w;
 }
 
@@ -358,24 +358,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const size_t rsx = (size_t)dm.H * P;
   const T* cbg = ck.cb + (size_t)bn * C * C;
   const T* cg = Cm + row0 * N;
-  const int wv_id = wave_id();
   constexpr int NB = C / 16, BPW = NB / 4, YNI = PT / 16, KN = N / Mma<T>::KS;
   static_assert(NB % 4 == 0, "row blocks must split evenly over 4 waves");
+  // compiled per wave (its output blocks are constants): the fragment arrays
+  // hold exactly the blocks used and no branch depends on the block index
+  static_switch<4>(__builtin_amdgcn_readfirstlane(wave_id()), [&, dm, ck](auto Wc) {
+  constexpr int W = decltype(Wc)::value;
 
   // the global operands of the output blocks (CB fragments, C rows), shared by
   // the workgroup's slices, requested before the first slice's cumsum
   typedef typename Mma<T>::frag frag;
   frag fa[BPW][NB], fd[BPW], fc[BPW][KN];
+  static_for<BPW>([&](auto Bc) {
+    constexpr int bi = decltype(Bc)::value, I = y_block<NB>(W, bi);
 #pragma unroll
-  for (int bi = 0; bi < BPW; ++bi) {
-    const int I = y_block<NB>(wv_id, bi);
-#pragma unroll
-    for (int J = 0; J < NB; ++J)
-      if (J < I) fa[bi][J] = cb_frag<T>(cbg, C, 16 * I, 16 * J, 0);
+    for (int J = 0; J < I; ++J) fa[bi][J] = cb_frag<T>(cbg, C, 16 * I, 16 * J, 0);
     fd[bi] = cb_frag<T>(cbg, C, 16 * I, 16 * I, 1);
 #pragma unroll
     for (int kk = 0; kk < KN; ++kk) fc[bi][kk] = Mma<T>::ld_c(cg, N, 16 * I, kk * Mma<T>::KS);
-  }
+  });
   for (int sl = 0; sl < SL; ++sl) {
   const int m = m2 * SL + sl;
   const int h = m / NPT, p0 = (m % NPT) * PT;
@@ -396,20 +397,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   stage_rows<T, PT, N>(sSt, L::LN, ck.state_pre + (((size_t)bn * dm.H + h) * P + p0) * N, N);
   int flag = 0;
-  float dbx[EPT][8];
 #pragma unroll
   for (int i = 0; i < EPT; ++i) {
     const int e = threadIdx.x + 256 * i, r = item_row(e), c = item_col(e);
-    float av[8];
+    float av[8], dbx[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float a = rdt[i][j] * Ah;
       flag |= a > 0.f;
       av[j] = sanitize(a, kClipDecay);
-      dbx[i][j] = sanitize(rdt[i][j] * rx[i][j]);
+      dbx[j] = sanitize(rdt[i][j] * rx[i][j]);
     }
     store8(sCum + r * L::LC + c, av);
-    store8(sDbx + r * L::LC + c, dbx[i]);
+    store8(sDbx + r * L::LC + c, dbx);
   }
   // the 16 zero rows below the chunk (read by the K = 32 steps of the last block)
   if (threadIdx.x < 16 * PER_ROW) {
@@ -424,7 +424,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     flag |= sCum[16 * I * L::LC + p] - sCum[(16 * I + 15) * L::LC + p] > kMaxRange;
   }
   // a positive step exponent (or too steep a block) is evaluated pairwise
-  const bool exact = __syncthreads_or(flag);
+  const bool exact = __builtin_amdgcn_readfirstlane(__syncthreads_or(flag)) != 0;
   if (!exact) {
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
@@ -433,35 +433,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       load8(sCum + r * L::LC + c, cr);
       load8(sCum + (r | 15) * L::LC + c, ce);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = __expf(ce[j] - cr[j]) * dbx[i][j];
+      for (int j = 0; j < 8; ++j) v[j] = __expf(ce[j] - cr[j]) * sanitize(rdt[i][j] * rx[i][j]);
       store8(sV + r * L::LPT + c, v);
     }
   }
   __syncthreads();
 
+  // this lane's y elements: a uniform base and 32-bit lane offsets
+  float* const yb = y + base;
+  const unsigned ylane = (unsigned)tile_row(0) * (unsigned)rsx + (unsigned)tile_col();
+  static_for<BPW>([&](auto Bc) {
+    constexpr int bi = decltype(Bc)::value, I = y_block<NB>(W, bi);
+    f32x4 off[YNI], yo[YNI];
 #pragma unroll
-  for (int bi = 0; bi < BPW; ++bi) {
-    const int I = y_block<NB>(wv_id, bi);
-    f32x4 off[YNI], dg[YNI], yo[YNI];
-#pragma unroll
-    for (int ni = 0; ni < YNI; ++ni) { off[ni] = zero4(); dg[ni] = zero4(); yo[ni] = zero4(); }
+    for (int ni = 0; ni < YNI; ++ni) { off[ni] = zero4(); yo[ni] = zero4(); }
     if (!exact) {
+      // off = sum_{J < I} M_IJ (CB_IJ Vd_J) + M_II (tril(CB_II) Vd_I): with the row
+      // scale U_i below, the diagonal term becomes exp(cum_i - cum_{16I+15}) (.)
+      static_for<I + 1>([&](auto Jc) {
+        constexpr int J = decltype(Jc)::value;
+        frag a;
+        if constexpr (J < I) a = fa[bi][J];
+        else a = fd[bi];
 #pragma unroll
-      for (int J = 0; J < NB; ++J) {
-        if (J < I) {
+        for (int ni = 0; ni < YNI; ++ni) {
+          const f32x4 q = Mma<T>::mma(a, Mma<T>::ld_t(sV, L::LPT, 16 * ni, 16 * J), zero4());
+          const int pc = 16 * ni + tile_col();
+          const float mf = __expf(sCum[16 * I * L::LC + pc] - sCum[(16 * J + 15) * L::LC + pc]);
 #pragma unroll
-          for (int ni = 0; ni < YNI; ++ni) {
-            const f32x4 q = Mma<T>::mma(fa[bi][J], Mma<T>::ld_t(sV, L::LPT, 16 * ni, 16 * J), zero4());
-            const int pc = 16 * ni + tile_col();
-            const float mf = __expf(sCum[16 * I * L::LC + pc] - sCum[(16 * J + 15) * L::LC + pc]);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) off[ni][k] += mf * q[k];
-          }
+          for (int k = 0; k < 4; ++k) off[ni][k] += mf * q[k];
         }
-      }
-#pragma unroll
-      for (int ni = 0; ni < YNI; ++ni)
-        dg[ni] = Mma<T>::mma(fd[bi], Mma<T>::ld_t(sV, L::LPT, 16 * ni, 16 * I), zero4());
+      });
     }
 #pragma unroll
     for (int kk = 0; kk < KN; ++kk) {
@@ -477,8 +479,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const float ci = sCum[i * L::LC + p];
         float ydiag;
         if (!exact) {
-          ydiag = off[ni][k] * __expf(ci - sCum[16 * I * L::LC + p]) +
-                  dg[ni][k] * __expf(ci - sCum[(16 * I + 15) * L::LC + p]);
+          ydiag = off[ni][k] * __expf(ci - sCum[16 * I * L::LC + p]);
         } else {
           ydiag = 0.f;
           for (int j = 0; j <= i; ++j) {
@@ -487,12 +488,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           }
         }
         const float yoff = sanitize(yo[ni][k] * __expf(fminf(fmaxf(ci, -kClipDecay), 0.f)));
-        y[base + (size_t)i * rsx + p] = sanitize(sanitize(ydiag) + yoff);
+        yb[ylane + (unsigned)(16 * I + k) * (unsigned)rsx + 16 * ni] = sanitize(sanitize(ydiag) + yoff);
       }
     }
-  }
+  });
   __syncthreads();  // the next slice rewrites the LDS
   }
+  });
 }
 
 }  // namespace ah
