@@ -28,7 +28,9 @@ constexpr float kClipAcc = 1e4f;
 constexpr float kClipDecay = 20.0f;
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
-__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+// wave index of a 1-D workgroup, as a wave-uniform (scalar) value so that
+// branches and addresses derived from it stay scalar
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 __device__ __forceinline__ float to_f(float x) { return x; }
 __device__ __forceinline__ float to_f(bf16 x) { return (float)x; }

@@ -158,7 +158,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   xcd_group_map(blockIdx.x, dm.B * dm.NT, G, bn, g);
   const int bb = bn / dm.NT, n = bn % dm.NT;
   const int HG = dm.H / G;
-  const int wv_id = __builtin_amdgcn_readfirstlane(wave_id());  // wave-uniform: scalar branches
+  const int wv_id = wave_id();
   const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
   const T* Bg0 = Bm + row0 * N;
   const T* Cg0 = Cm + row0 * N;
@@ -668,7 +668,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   // output tiles [C / 16][NTL / 16]: wave w owns TPW consecutive column tiles of one row tile
   constexpr int CT = NTL / 16, NTILE = (C / 16) * CT, TPW = NTILE / NW;
   static_assert(TPW >= 1 && NTILE % NW == 0 && CT % TPW == 0, "a wave's tiles share one row tile");
-  const int wv_id = __builtin_amdgcn_readfirstlane(wave_id());
+  const int wv_id = wave_id();
   const int m0 = 16 * ((wv_id * TPW) / CT), ct0 = (wv_id * TPW) % CT;
   f32x4 accC[TPW], accB[TPW];
 #pragma unroll

@@ -362,7 +362,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   static_assert(NB % 4 == 0, "row blocks must split evenly over 4 waves");
   // compiled per wave (its output blocks are constants): the fragment arrays
   // hold exactly the blocks used and no branch depends on the block index
-  static_switch<4>(__builtin_amdgcn_readfirstlane(wave_id()), [&, dm, ck](auto Wc) {
+  static_switch<4>(wave_id(), [&](auto Wc) {
   constexpr int W = decltype(Wc)::value;
 
   // the global operands of the output blocks (CB fragments, C rows), shared by
