@@ -44,6 +44,13 @@ class Mamba2Args(ctypes.Structure):
                 ("profile", ctypes.c_void_p)]
 
 
+class NormGateArgs(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_int32), ("dim", ctypes.c_int32), ("variant", ctypes.c_int32),
+                ("eps", ctypes.c_float), ("profile", ctypes.c_void_p)]
+
+
+NORM_GATE_GDN2, NORM_GATE_MAMBA2 = 0, 1
+
 PROFILE_MAX = 16
 
 
@@ -98,6 +105,9 @@ _SIGS = {
     "atomic_mamba2_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(Mamba2Args)]),
     "atomic_mamba2_fwd": (ctypes.c_int, [ctypes.POINTER(Mamba2Args)] + [_P] * 8 + [_P, ctypes.c_size_t, _P]),
     "atomic_mamba2_bwd": (ctypes.c_int, [ctypes.POINTER(Mamba2Args)] + [_P] * 14 + [_P, ctypes.c_size_t, _P]),
+    "atomic_norm_gate_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(NormGateArgs)]),
+    "atomic_norm_gate_fwd": (ctypes.c_int, [ctypes.POINTER(NormGateArgs)] + [_P] * 4 + [_P]),
+    "atomic_norm_gate_bwd": (ctypes.c_int, [ctypes.POINTER(NormGateArgs)] + [_P] * 7 + [_P, ctypes.c_size_t, _P]),
 }
 
 _lib = None

@@ -18,6 +18,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import statistics
@@ -68,6 +69,17 @@ def gdn2_kernel_model(B, T, H, K, V, C, es=2, save=True):
         "gdn2_bwd_intra": (U * 8 * CC * K,
                            U * (3 * CK * es + CK * 4 + 2 * CC * es + 3 * CK * es + K * 4  # q k b g daqk dakk dqg dkb dkg rlast
                                 + 3 * CK * es + CK * 4)),                    # dq dk db dg
+    }
+
+
+def norm_gate_model(rows, d, nparts):
+    """Algorithmic (flops, HBM bytes) per launch of the fused output-epilogue
+    kernels: x fp32, gate / out / dout / dgate bf16, dx fp32, one fp32
+    weight-gradient partial row per backward workgroup."""
+    return {
+        "norm_gate_fwd": (rows * d * 12, rows * d * (4 + 2 + 2) + d * 4),
+        "norm_gate_bwd": (rows * d * 30, rows * d * (4 + 2 + 2 + 4 + 2) + nparts * d * 4 + d * 4),
+        "norm_gate_dweight": (nparts * d, nparts * d * 4 + d * 4),
     }
 
 
@@ -175,6 +187,51 @@ def cpu_baseline(sample_t=CPU_SAMPLE_T):
 
 
 # --------------------------------------------------------------------------- GPU step
+def measure_epilogue(args, dev, g, m, q, k, v, w, b, gg, dt, x, Bm, Cm, A, scale, g_ws, m_ws):
+    """The fused output epilogue (RMSNorm + SiLU gate, forward and backward) on
+    the path's own outputs at the benchmark shapes, timed per kernel with HIP
+    events.  Outside the timed region: not part of the headline metric."""
+    import torch
+    from atomic_ops import _lib
+    from atomic_ops import gdn2 as G2
+    from atomic_ops import mamba2 as M2
+    from atomic_ops import norm_gate as NG
+    o, _, _ = G2.forward(q, k, v, w, b, gg, scale, workspace=g_ws)
+    y, _, _ = M2.forward(dt, x, Bm, Cm, A, m["C"], workspace=m_ws)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    res = {}
+    for name, var, xin in (("gdn2", NG.GDN2, o), ("mamba2", NG.MAMBA2, y)):
+        rows, d = xin.shape[0] * xin.shape[1], xin.shape[2] * xin.shape[3]
+        gate = torch.randn(rows, d, generator=gen, device=dev).to(torch.bfloat16)
+        wt = 1.0 + 0.1 * torch.randn(d, generator=gen, device=dev)
+        dout = torch.randn(rows, d, generator=gen, device=dev).to(torch.bfloat16)
+        args_ = NG.make_args(rows, d, var, 1e-6)
+        nparts = _lib.load().atomic_norm_gate_workspace_size(ctypes.byref(args_)) // (d * 4)
+        ws = torch.empty(nparts * d * 4, dtype=torch.uint8, device=dev)
+        model = norm_gate_model(rows, d, nparts)
+        n_it = max(PROF_STEPS, 5)
+        tms = [(_lib.KernelTimer(dev), _lib.KernelTimer(dev)) for _ in range(n_it + 2)]
+        for i in range(n_it + 2):      # two warm-up iterations
+            NG.forward(xin, gate, wt, var, timer=tms[i][0])
+            NG.backward(xin, gate, wt, dout, var, workspace=ws, timer=tms[i][1])
+        torch.cuda.synchronize()
+        per = {}
+        for i in range(2, n_it + 2):
+            for tm in tms[i]:
+                for kn, ms in tm.durations():
+                    per.setdefault(kn, []).append(ms)
+        ks = {}
+        for kn, v_ in per.items():
+            avg = sum(v_) / len(v_)
+            fl, by = model[kn]
+            rf = roofline(fl, by, avg / 1e3)
+            ks[kn] = dict(ms_per_launch=round(avg, 4), bytes=int(by), gbps=round(by / (avg / 1e3) / 1e9, 1),
+                          bound=rf["bound"], frac=round(rf["frac"], 4))
+        res[name] = dict(rows=rows, dim=d, kernels=ks,
+                         ms_fwd_bwd=round(sum(kv["ms_per_launch"] for kv in ks.values()), 4))
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -288,6 +345,8 @@ def main():
     rf["kernel"] = dom
     rf["traffic"] = measured_traffic(dom)
 
+    epilogue = measure_epilogue(args, dev, g, m, q, k, v, w, b, gg, dt, x, Bm, Cm, A, scale, g_ws, m_ws)
+
     cpu = None if args.no_cpu else cpu_baseline()
 
     line = {
@@ -304,6 +363,7 @@ def main():
         "paths_ms_median": {k_: round(statistics.median(v_), 4) for k_, v_ in path_ms.items()},
         "device_ms_per_step_median": round(statistics.median(step_dev_ms), 4),
         "kernels": kernels,
+        "epilogue": epilogue,
     }
     print(json.dumps(line), flush=True)
 

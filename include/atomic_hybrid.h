@@ -184,6 +184,50 @@ int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, const void* x
                       const float* dstate_final, void* ddt, void* dx, void* dB, void* dC, float* dA,
                       float* dstate0, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------- output epilogue (downstream) */
+
+/* The two mixer blocks' output epilogue: RMSNorm over the model dimension
+   and the SiLU gate, fused.
+     ATOMIC_NORM_GATE_GDN2:   out = bf16(bf16(RMSNorm(x)) * silu(clip(gate, +-1e2)))
+                              (reference model.py:612-613,650-653; x is the
+                              GDN2 output o, gate the out_gate projection)
+     ATOMIC_NORM_GATE_MAMBA2: out = clip(bf16(bf16(RMSNorm(bf16(x))) * silu(gate)), +-3e2)
+                              (reference model.py:516-525; x is the SSD
+                              output y, gate the `res` half of in_proj)
+   RMSNorm(x) = x * rsqrt(mean(x^2) + eps) * weight, statistics in fp32 (flax
+   linen RMSNorm).  The result feeds the block's out_proj GEMM. */
+enum { ATOMIC_NORM_GATE_GDN2 = 0, ATOMIC_NORM_GATE_MAMBA2 = 1 };
+
+typedef struct atomic_norm_gate_args {
+  int32_t rows;      /* B * T                                                   */
+  int32_t dim;       /* d (H * V, or H * P): a multiple of 512, at most 8192    */
+  int32_t variant;   /* ATOMIC_NORM_GATE_*                                      */
+  float eps;         /* 1e-6 in both blocks                                     */
+  atomic_profile* profile;  /* optional per-kernel event timing, or NULL      */
+} atomic_norm_gate_args;
+
+/* Bytes of workspace atomic_norm_gate_bwd needs (0 for unsupported args). */
+size_t atomic_norm_gate_workspace_size(const atomic_norm_gate_args* a);
+
+/*
+ * Forward.  Replaces the inline epilogue of GatedDeltaNet2J.__call__
+ * (model.py:650-653) / the Mamba2 block (model.py:516-525).
+ *   x      : [rows, dim] fp32 (o / y as the path returns them, [B, T, H, V])
+ *   gate   : [rows, dim] bf16 (out_gate, or res)
+ *   weight : [dim]       fp32 RMSNorm scale
+ *   out    : [rows, dim] bf16
+ */
+int atomic_norm_gate_fwd(const atomic_norm_gate_args* a, const float* x, const void* gate,
+                         const float* weight, void* out, void* stream);
+
+/*
+ * Backward of the same function for dout = d loss / d out (bf16):
+ *   dx : [rows, dim] fp32    dgate : [rows, dim] bf16    dweight : [dim] fp32
+ */
+int atomic_norm_gate_bwd(const atomic_norm_gate_args* a, const float* x, const void* gate,
+                         const float* weight, const void* dout, float* dx, void* dgate,
+                         float* dweight, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
