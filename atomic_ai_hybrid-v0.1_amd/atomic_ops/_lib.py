@@ -51,6 +51,12 @@ class NormGateArgs(ctypes.Structure):
 
 NORM_GATE_GDN2, NORM_GATE_MAMBA2 = 0, 1
 
+
+class PrologueArgs(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_int32), ("seqlen", ctypes.c_int32), ("heads", ctypes.c_int32),
+                ("dhead", ctypes.c_int32), ("dconv", ctypes.c_int32), ("eps", ctypes.c_float),
+                ("profile", ctypes.c_void_p)]
+
 PROFILE_MAX = 16
 
 
@@ -108,6 +114,9 @@ _SIGS = {
     "atomic_norm_gate_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(NormGateArgs)]),
     "atomic_norm_gate_fwd": (ctypes.c_int, [ctypes.POINTER(NormGateArgs)] + [_P] * 4 + [_P]),
     "atomic_norm_gate_bwd": (ctypes.c_int, [ctypes.POINTER(NormGateArgs)] + [_P] * 7 + [_P, ctypes.c_size_t, _P]),
+    "atomic_gdn2_prologue_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(PrologueArgs)]),
+    "atomic_gdn2_prologue_fwd": (ctypes.c_int, [ctypes.POINTER(PrologueArgs)] + [_P] * 15 + [_P]),
+    "atomic_gdn2_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(PrologueArgs)] + [_P] * 24 + [_P, ctypes.c_size_t, _P]),
 }
 
 _lib = None

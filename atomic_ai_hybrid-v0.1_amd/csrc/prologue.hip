@@ -1,0 +1,558 @@
+// Fused prologue of the GDN2 block (the path's upstream caller), forward and
+// backward, for gfx950.  From the projection outputs (bf16 [B, L, d],
+// d = H dh) it produces the path's inputs q, k, v, w, b (bf16) and g (fp32)
+// in the [B, L, H, dh] layout the chunk pipeline reads, with the semantics of
+// GatedDeltaNet2J.__call__ (reference model.py:574-619):
+//   q, k: normalize(silu(conv(lin) + bias)) per head    v: clip(silu(conv + bias), +-50)
+//   b, w: sigmoid(pre)     g: nan_to_num(-exp(clip(a, +-20)) softplus(f))
+//   every output: nan_to_num(clip(., +-1e3))
+// conv is the causal depthwise convolution (d_conv = 4 taps) with the fp32
+// parameters cast to bf16; normalize(t) = t rsqrt(sum_head t^2 + eps^2).
+// bf16 roundings follow the reference's dtypes: each bf16 elementwise op
+// rounds once, the conv taps and the head's sum of squares accumulate in
+// fp32 and round once.
+//
+// Mapping: one wave per (batch, token tile, 512 channels); lane l holds the
+// 8 consecutive channels 8 l .. 8 l + 7 of the block, so a head's channels
+// sit in dh / 8 consecutive lanes (its sum of squares is a lane-group
+// reduction) and every access is a 16-byte vector.  The convolution slides a
+// register window over the tile's tokens (the forward walks time upwards
+// with the three previous inputs, the backward walks it downwards with the
+// three following cotangents, recomputed past the tile's end).  Parameter
+// gradients: each workgroup (four consecutive tiles) combines its waves'
+// sums through LDS into one partial row; a final kernel sums the rows.
+#include "../../include/atomic_hybrid.h"
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace ah {
+
+constexpr int kDc = 4;         // d_conv of the model config
+constexpr int kTileF = 16;     // tokens per wave, forward
+constexpr int kTileB = 32;     // tokens per wave, backward
+
+struct PlDims {
+  int B, L, H, dh, d;
+  float eps;
+};
+
+__device__ __forceinline__ float bfr(float x) { return (float)(bf16)x; }
+__device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
+// jax.nn.softplus(x) = logaddexp(x, 0)
+__device__ __forceinline__ float softplus_(float x) { return fmaxf(x, 0.f) + log1pf(__expf(-fabsf(x))); }
+// cotangent factor of clip(v, -c, c) = min(max(v, -c), c): ties split evenly
+__device__ __forceinline__ float clip_g(float v, float c) {
+  const float a = fabsf(v);
+  return a < c ? 1.f : (a == c ? 0.5f : 0.f);
+}
+// nan_to_num(clip(x, -c, c)) (model.py:615-617)
+__device__ __forceinline__ float sanit(float x, float c) {
+  if (__builtin_isnan(x)) return 0.f;
+  return fminf(fmaxf(x, -c), c);
+}
+
+// sum over the lanes of one head (G = dh / 8 consecutive lanes)
+template <int G>
+__device__ __forceinline__ float head_sum(float v) {
+#pragma unroll
+  for (int sh = 1; sh < G; sh <<= 1) v += __shfl_xor(v, sh);
+  return v;
+}
+
+// the lane's conv weights (bf16-rounded, [tap][8 channels]) and biases
+struct ConvW {
+  float w[kDc][8], b[8];
+  __device__ __forceinline__ void load(const float* __restrict__ cw, const float* __restrict__ cb, int c) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float4 t = *reinterpret_cast<const float4*>(cw + (size_t)(c + j) * kDc);
+      w[0][j] = bfr(t.x); w[1][j] = bfr(t.y); w[2][j] = bfr(t.z); w[3][j] = bfr(t.w);
+      b[j] = bfr(cb[c + j]);
+    }
+  }
+};
+
+// silu(conv + bias) at one token from the window u[t-3..t] (tap order)
+__device__ __forceinline__ void conv_silu(const ConvW& W, const float (&win)[kDc][8], float (&pre)[8],
+                                          float (&s)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float acc = 0.f;
+#pragma unroll
+    for (int tp = 0; tp < kDc; ++tp) acc += win[tp][j] * W.w[tp][j];
+    pre[j] = bfr(bfr(acc) + W.b[j]);
+    s[j] = bfr(pre[j] * sigm(pre[j]));
+  }
+}
+
+// ---------------------------------------------------------------- forward
+// WHICH: 0 q, 1 k (normalised), 2 v (clipped to +-50)
+template <int WHICH, int DH>
+__global__ __launch_bounds__(256) void prologue_conv_fwd(PlDims dm, const bf16* __restrict__ lin,
+                                                         const float* __restrict__ conv_w,
+                                                         const float* __restrict__ conv_b,
+                                                         bf16* __restrict__ out) {
+  constexpr int G = DH / 8;
+  const int lane = lane_id();
+  const int nblk = dm.d / 512, ntile = dm.L / kTileF;
+  const int wv = blockIdx.x * 4 + wave_id();
+  if (wv >= dm.B * ntile * nblk) return;  // wave-uniform
+  const int cb = wv % nblk, tile = (wv / nblk) % ntile, b = wv / (nblk * ntile);
+  const int c = cb * 512 + 8 * lane, t0 = tile * kTileF;
+  ConvW W;
+  W.load(conv_w + (size_t)WHICH * dm.d * kDc, conv_b + (size_t)WHICH * dm.d, c);
+  const bf16* u = lin + (size_t)b * dm.L * dm.d + c;
+  bf16* o = out + (size_t)b * dm.L * dm.d + c;
+  float win[kDc][8];
+#pragma unroll
+  for (int tp = 0; tp < kDc - 1; ++tp) {
+    const int t = t0 - (kDc - 1) + tp;
+    if (t >= 0) load8(u + (size_t)t * dm.d, win[tp]);
+    else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) win[tp][j] = 0.f;
+    }
+  }
+#pragma unroll 2
+  for (int t = t0; t < t0 + kTileF; ++t) {
+    load8(u + (size_t)t * dm.d, win[kDc - 1]);
+    float pre[8], s[8], y[8];
+    conv_silu(W, win, pre, s);
+    if (WHICH == 2) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = sanit(fminf(fmaxf(s[j], -50.f), 50.f), 1e3f);
+    } else {
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += bfr(s[j] * s[j]);
+      ss = bfr(head_sum<G>(ss));
+      const float r = bfr(rsqrtf(bfr(ss + dm.eps * dm.eps)));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = sanit(bfr(s[j] * r), 1e3f);
+    }
+    store8(o + (size_t)t * dm.d, y);
+#pragma unroll
+    for (int tp = 0; tp < kDc - 1; ++tp)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) win[tp][j] = win[tp + 1][j];
+  }
+}
+
+// b, w = sigmoid(pre); g = nan_to_num(-exp(clip(a)) softplus(f)); 8 channels per thread
+template <int DH>
+__global__ __launch_bounds__(256) void prologue_gates_fwd(PlDims dm, const bf16* __restrict__ b_pre,
+                                                          const bf16* __restrict__ w_pre,
+                                                          const bf16* __restrict__ f_pre,
+                                                          const float* __restrict__ a_param,
+                                                          bf16* __restrict__ bo, bf16* __restrict__ wo,
+                                                          float* __restrict__ go) {
+  const size_t e = ((size_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e >= (size_t)dm.B * dm.L * dm.d) return;
+  const int h = (int)((e % dm.d) / DH);
+  const float ea = __expf(fminf(fmaxf(a_param[h], -20.f), 20.f));
+  float bv[8], wv[8], fv[8], gv[8];
+  load8(b_pre + e, bv);
+  load8(w_pre + e, wv);
+  load8(f_pre + e, fv);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    bv[j] = sanit(bfr(sigm(bv[j])), 1e3f);
+    wv[j] = sanit(bfr(sigm(wv[j])), 1e3f);
+    float g = -ea * softplus_(fv[j]);
+    if (__builtin_isnan(g)) g = 0.f;
+    else if (__builtin_isinf(g)) g = g > 0.f ? 0.f : -20.f;
+    gv[j] = sanit(g, 1e3f);
+  }
+  store8(bo + e, bv);
+  store8(wo + e, wv);
+  store8(go + e, gv);
+}
+
+// ---------------------------------------------------------------- backward
+// Per token of the reverse sweep: the cotangent of the conv accumulator
+// (e = d(conv + bias)), from the output cotangent dy and the forward values.
+template <int WHICH, int G>
+__device__ __forceinline__ void conv_out_vjp(const ConvW& W, const float (&win)[kDc][8], const float (&dy)[8],
+                                             float eps, float (&e)[8]) {
+  float pre[8], s[8], ds[8];
+  conv_silu(W, win, pre, s);
+  if (WHICH == 2) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = fminf(fmaxf(s[j], -50.f), 50.f);
+      ds[j] = bfr(dy[j] * clip_g(v, 1e3f) * clip_g(s[j], 50.f));
+    }
+  } else {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += bfr(s[j] * s[j]);
+    ss = bfr(head_sum<G>(ss));
+    const float r = bfr(rsqrtf(bfr(ss + eps * eps)));
+    // output clip (|y| <= 1 passes), then the gradient sanitiser (model.py:206-214)
+    float gy[8], dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float y = bfr(s[j] * r);
+      float g = dy[j] * clip_g(y, 1e3f);
+      g = __builtin_isnan(g) ? 0.f : fminf(fmaxf(g, -1e3f), 1e3f);
+      gy[j] = g;
+      dot += g * s[j];
+    }
+    dot = head_sum<G>(dot);
+    const float r3 = r * r * r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ds[j] = bfr(gy[j] * r - s[j] * r3 * dot);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float sg = sigm(pre[j]);
+    e[j] = bfr(ds[j] * (sg * (1.f + pre[j] * (1.f - sg))));
+  }
+}
+
+// Partial sums of one workgroup (4 waves) combined through LDS and written
+// as one row of NV floats per channel: the row is [d][NV] at `dst`.
+template <int NV>
+__device__ __forceinline__ void combine_partials(float (&v)[NV][8], float* __restrict__ dst, int c) {
+  __shared__ __attribute__((aligned(16))) float red[4][512];
+  const int w = wave_id(), lane = lane_id();
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    store8(&red[w][8 * lane], v[k]);
+    __syncthreads();
+    if (w == 0) {
+      float a[8], t[8];
+      load8(&red[0][8 * lane], a);
+#pragma unroll
+      for (int u = 1; u < 4; ++u) {
+        load8(&red[u][8 * lane], t);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] += t[j];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dst[(size_t)(c + j) * NV + k] = a[j];
+    }
+    __syncthreads();
+  }
+}
+
+// The four waves of a workgroup take four consecutive tiles of one
+// (batch, channel block); partial row index = (batch, tile group).
+template <int WHICH, int DH>
+__global__ __launch_bounds__(256) void prologue_conv_bwd(PlDims dm, const bf16* __restrict__ lin,
+                                                         const float* __restrict__ conv_w,
+                                                         const float* __restrict__ conv_b,
+                                                         const bf16* __restrict__ dout,
+                                                         bf16* __restrict__ dlin, float* __restrict__ part) {
+  constexpr int G = DH / 8, NV = kDc + 1;  // partials: the 4 taps, then the bias
+  const int lane = lane_id();
+  const int nblk = dm.d / 512, ngrp = dm.L / (4 * kTileB);
+  const int cb = blockIdx.x % nblk, grp = (blockIdx.x / nblk) % ngrp, b = blockIdx.x / (nblk * ngrp);
+  const int tile = grp * 4 + wave_id();
+  const int c = cb * 512 + 8 * lane, t0 = tile * kTileB;
+  ConvW W;
+  W.load(conv_w + (size_t)WHICH * dm.d * kDc, conv_b + (size_t)WHICH * dm.d, c);
+  const bf16* u = lin + (size_t)b * dm.L * dm.d + c;
+  const bf16* dy = dout + (size_t)b * dm.L * dm.d + c;
+  bf16* du = dlin + (size_t)b * dm.L * dm.d + c;
+  float acc[NV][8];
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[k][j] = 0.f;
+  // reverse sweep from the last halo token: window u[t-3..t] and the conv
+  // cotangents e[t+1..t+3] of the tokens above
+  const int t_hi = min(t0 + kTileB + kDc - 2, dm.L - 1);
+  float win[kDc][8], en[kDc - 1][8];
+#pragma unroll
+  for (int tp = 0; tp < kDc; ++tp) {
+    const int t = t_hi - (kDc - 1) + tp;
+    if (t >= 0) load8(u + (size_t)t * dm.d, win[tp]);
+    else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) win[tp][j] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kDc - 1; ++k)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) en[k][j] = 0.f;
+  for (int t = t_hi; t >= t0; --t) {
+    float g8[8], e[8];
+    load8(dy + (size_t)t * dm.d, g8);
+    conv_out_vjp<WHICH, G>(W, win, g8, dm.eps, e);
+    if (t < t0 + kTileB) {
+      // d lin[t] = sum_s e[t + s] w[3 - s]; the parameter sums
+      float o8[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float v = e[j] * W.w[kDc - 1][j];
+#pragma unroll
+        for (int s = 1; s < kDc; ++s) v += en[s - 1][j] * W.w[kDc - 1 - s][j];
+        o8[j] = v;
+#pragma unroll
+        for (int tp = 0; tp < kDc; ++tp) acc[tp][j] += e[j] * win[tp][j];
+        acc[kDc][j] += e[j];
+      }
+      store8(du + (size_t)t * dm.d, o8);
+    }
+    // slide: e[t] becomes the nearest token above; the window moves down
+#pragma unroll
+    for (int k = kDc - 2; k >= 1; --k)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) en[k][j] = en[k - 1][j];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) en[0][j] = e[j];
+#pragma unroll
+    for (int tp = kDc - 1; tp >= 1; --tp)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) win[tp][j] = win[tp - 1][j];
+    const int tn = t - kDc;
+    if (tn >= 0) load8(u + (size_t)tn * dm.d, win[0]);
+    else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) win[0][j] = 0.f;
+    }
+  }
+  combine_partials<NV>(acc, part + ((size_t)WHICH * dm.B * ngrp + (size_t)b * ngrp + grp) * dm.d * NV, c);
+}
+
+// b, w, g gradients; per-head partial sums of da
+template <int DH>
+__global__ __launch_bounds__(256) void prologue_gates_bwd(PlDims dm, const bf16* __restrict__ b_pre,
+                                                          const bf16* __restrict__ w_pre,
+                                                          const bf16* __restrict__ f_pre,
+                                                          const float* __restrict__ a_param,
+                                                          const bf16* __restrict__ db, const bf16* __restrict__ dw,
+                                                          const float* __restrict__ dg, bf16* __restrict__ dbp,
+                                                          bf16* __restrict__ dwp, bf16* __restrict__ dfp,
+                                                          float* __restrict__ part_a) {
+  constexpr int G = DH / 8;
+  const int lane = lane_id();
+  const int nblk = dm.d / 512, ntile = dm.L / kTileB;
+  const int wv = blockIdx.x * 4 + wave_id();
+  if (wv >= dm.B * ntile * nblk) return;  // wave-uniform
+  const int cb = wv % nblk, tile = (wv / nblk) % ntile, b = wv / (nblk * ntile);
+  const int c = cb * 512 + 8 * lane, h = c / DH;
+  const float araw = a_param[h];
+  const float ea = __expf(fminf(fmaxf(araw, -20.f), 20.f)), ga = clip_g(araw, 20.f);
+  float da = 0.f;
+  for (int t = tile * kTileB; t < (tile + 1) * kTileB; ++t) {
+    const size_t e = ((size_t)b * dm.L + t) * dm.d + c;
+    float bv[8], wv8[8], fv[8], gb[8], gw[8], gg[8], o1[8], o2[8], o3[8];
+    load8(b_pre + e, bv);
+    load8(w_pre + e, wv8);
+    load8(f_pre + e, fv);
+    load8(db + e, gb);
+    load8(dw + e, gw);
+    load8(dg + e, gg);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float sb = bfr(sigm(bv[j])), sw = bfr(sigm(wv8[j]));
+      o1[j] = bfr(gb[j] * clip_g(sb, 1e3f) * sb * (1.f - sb));
+      o2[j] = bfr(gw[j] * clip_g(sw, 1e3f) * sw * (1.f - sw));
+      const float sp = softplus_(fv[j]);
+      const float g = -ea * sp;
+      // nan_to_num passes the cotangent of finite values; then the +-1e3 clip
+      const float dgi = (__builtin_isfinite(g) ? gg[j] : 0.f) * clip_g(g, 1e3f);
+      o3[j] = bfr(dgi * (-ea) * sigm(fv[j]));
+      da += dgi * g * ga;
+    }
+    store8(dbp + e, o1);
+    store8(dwp + e, o2);
+    store8(dfp + e, o3);
+  }
+  da = head_sum<G>(da);
+  // one partial per (wave, head of the block): lane 0 of each head group writes
+  if ((lane % G) == 0) part_a[(size_t)wv * (512 / DH) + lane / G] = da;
+}
+
+// Column sums of the partial rows: out[c] = sum_r part[r][c] for c < ncol
+// (64 columns per workgroup of 16 waves, eight loads in flight per lane).
+__global__ __launch_bounds__(1024) void prologue_colsum(int ncol, int nrows, const float* __restrict__ part,
+                                                        float* __restrict__ out) {
+  constexpr int NWV = 16, U = 8;
+  __shared__ float red[NWV][64];
+  const int c = blockIdx.x * 64 + lane_id(), w = wave_id();
+  const bool ok = c < ncol;
+  float acc[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) acc[u] = 0.f;
+  int k = w;
+  if (ok) {
+    for (; k + (U - 1) * NWV < nrows; k += U * NWV) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc[u] += part[(size_t)(k + u * NWV) * ncol + c];
+    }
+    for (; k < nrows; k += NWV) acc[0] += part[(size_t)k * ncol + c];
+  }
+  float t = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) t += acc[u];
+  red[w][lane_id()] = t;
+  __syncthreads();
+  if (w == 0 && ok) {
+    float s = 0.f;
+#pragma unroll
+    for (int u = 0; u < NWV; ++u) s += red[u][lane_id()];
+    out[c] = s;
+  }
+}
+
+// conv weight / bias gradients from the summed [3][d][5] block, bf16-rounded
+// like the reference's bf16 conv-parameter cotangents
+__global__ __launch_bounds__(256) void prologue_param_split(int d, const float* __restrict__ sums,
+                                                            float* __restrict__ dconv_w,
+                                                            float* __restrict__ dconv_b) {
+  const int i = blockIdx.x * 256 + threadIdx.x;  // (which, channel)
+  if (i >= 3 * d) return;
+#pragma unroll
+  for (int tp = 0; tp < kDc; ++tp) dconv_w[(size_t)i * kDc + tp] = bfr(sums[(size_t)i * (kDc + 1) + tp]);
+  dconv_b[i] = bfr(sums[(size_t)i * (kDc + 1) + kDc]);
+}
+
+// ------------------------------------------------------------------ host
+static int pl_check(const atomic_gdn2_prologue_args* a) {
+  if (!a) return ATOMIC_ERR_NULL;
+  if (a->batch <= 0 || a->seqlen <= 0 || a->heads <= 0) return ATOMIC_ERR_SHAPE;
+  if (a->dhead != 64 && a->dhead != 128) return ATOMIC_ERR_SHAPE;
+  if (a->dconv != kDc) return ATOMIC_ERR_SHAPE;
+  if ((a->heads * a->dhead) % 512 != 0) return ATOMIC_ERR_SHAPE;
+  if (a->seqlen % (4 * kTileB) != 0) return ATOMIC_ERR_SHAPE;
+  if (!(a->eps >= 0.f)) return ATOMIC_ERR_SHAPE;
+  return ATOMIC_OK;
+}
+
+static PlDims pl_dims(const atomic_gdn2_prologue_args* a) {
+  return PlDims{a->batch, a->seqlen, a->heads, a->dhead, a->heads * a->dhead, a->eps};
+}
+
+// workspace: conv partial rows [3][B][L / 128][d][5], then the da partials
+// [B][L / 32][d / 512][512 / dh], then the summed [3][d][5] block
+struct PlWs {
+  size_t conv, da, sums, total;
+  int conv_rows, da_rows;
+};
+static PlWs pl_ws(const PlDims& d) {
+  PlWs w;
+  const size_t ngrp = (size_t)d.L / (4 * kTileB);
+  w.conv_rows = (int)(3 * d.B * ngrp);
+  w.da_rows = (int)((size_t)d.B * (d.L / kTileB) * (d.d / 512));
+  auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
+  w.conv = 0;
+  w.da = al((size_t)w.conv_rows * d.d * (kDc + 1) * 4);
+  w.sums = w.da + al((size_t)w.da_rows * (512 / d.dh) * 4);
+  w.total = w.sums + al((size_t)3 * d.d * (kDc + 1) * 4);
+  return w;
+}
+
+}  // namespace ah
+
+using namespace ah;
+
+extern "C" size_t atomic_gdn2_prologue_workspace_size(const atomic_gdn2_prologue_args* a) {
+  if (pl_check(a) != ATOMIC_OK) return 0;
+  return pl_ws(pl_dims(a)).total;
+}
+
+extern "C" int atomic_gdn2_prologue_fwd(const atomic_gdn2_prologue_args* a, const void* q_lin,
+                                        const void* k_lin, const void* v_lin, const float* conv_w,
+                                        const float* conv_b, const void* b_pre, const void* w_pre,
+                                        const void* f_pre, const float* a_param, void* q, void* k,
+                                        void* v, void* w, void* b, float* g, void* stream) {
+  int rc = pl_check(a);
+  if (rc) return rc;
+  if (!q_lin || !k_lin || !v_lin || !conv_w || !conv_b || !b_pre || !w_pre || !f_pre || !a_param || !q ||
+      !k || !v || !w || !b || !g)
+    return ATOMIC_ERR_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  const PlDims dm = pl_dims(a);
+  Launch L{a->profile, st};
+  const unsigned nconv = (unsigned)(((size_t)dm.B * (dm.L / kTileF) * (dm.d / 512) + 3) / 4);
+  const unsigned ngate = (unsigned)(((size_t)dm.B * dm.L * dm.d / 8 + 255) / 256);
+  const bf16* lins[3] = {(const bf16*)q_lin, (const bf16*)k_lin, (const bf16*)v_lin};
+  bf16* outs[3] = {(bf16*)q, (bf16*)k, (bf16*)v};
+  auto run = [&](auto Dc) {
+    constexpr int DH = decltype(Dc)::value;
+    int r = L("prologue_conv_fwd", [&] {
+      hipLaunchKernelGGL((prologue_conv_fwd<0, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[0], conv_w, conv_b,
+                         outs[0]);
+      hipLaunchKernelGGL((prologue_conv_fwd<1, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[1], conv_w, conv_b,
+                         outs[1]);
+      hipLaunchKernelGGL((prologue_conv_fwd<2, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[2], conv_w, conv_b,
+                         outs[2]);
+    });
+    if (r) return r;
+    return L("prologue_gates_fwd", [&] {
+      hipLaunchKernelGGL((prologue_gates_fwd<DH>), dim3(ngate), dim3(256), 0, st, dm, (const bf16*)b_pre,
+                         (const bf16*)w_pre, (const bf16*)f_pre, a_param, (bf16*)b, (bf16*)w, g);
+    });
+  };
+  return dm.dh == 64 ? run(IntC<64>{}) : run(IntC<128>{});
+}
+
+extern "C" int atomic_gdn2_prologue_bwd(const atomic_gdn2_prologue_args* a, const void* q_lin,
+                                        const void* k_lin, const void* v_lin, const float* conv_w,
+                                        const float* conv_b, const void* b_pre, const void* w_pre,
+                                        const void* f_pre, const float* a_param, const void* dq,
+                                        const void* dk, const void* dv, const void* dw, const void* db,
+                                        const float* dg, void* dq_lin, void* dk_lin, void* dv_lin,
+                                        float* dconv_w, float* dconv_b, void* db_pre, void* dw_pre,
+                                        void* df_pre, float* da_param, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  int rc = pl_check(a);
+  if (rc) return rc;
+  if (!q_lin || !k_lin || !v_lin || !conv_w || !conv_b || !b_pre || !w_pre || !f_pre || !a_param || !dq ||
+      !dk || !dv || !dw || !db || !dg || !dq_lin || !dk_lin || !dv_lin || !dconv_w || !dconv_b || !db_pre ||
+      !dw_pre || !df_pre || !da_param)
+    return ATOMIC_ERR_NULL;
+  const PlDims dm = pl_dims(a);
+  const PlWs ws = pl_ws(dm);
+  if (!workspace || workspace_bytes < ws.total) return ATOMIC_ERR_WORKSPACE;
+  unsigned char* wsb = (unsigned char*)workspace;
+  float* pconv = (float*)(wsb + ws.conv);
+  float* pda = (float*)(wsb + ws.da);
+  float* sums = (float*)(wsb + ws.sums);
+  hipStream_t st = (hipStream_t)stream;
+  Launch L{a->profile, st};
+  const int ngrp = dm.L / (4 * kTileB);
+  const unsigned nconv = (unsigned)((size_t)dm.B * ngrp * (dm.d / 512));
+  const unsigned ngate = (unsigned)(((size_t)dm.B * (dm.L / kTileB) * (dm.d / 512) + 3) / 4);
+  const bf16* lins[3] = {(const bf16*)q_lin, (const bf16*)k_lin, (const bf16*)v_lin};
+  const bf16* dys[3] = {(const bf16*)dq, (const bf16*)dk, (const bf16*)dv};
+  bf16* dls[3] = {(bf16*)dq_lin, (bf16*)dk_lin, (bf16*)dv_lin};
+  auto run = [&](auto Dc) {
+    constexpr int DH = decltype(Dc)::value;
+    int r = L("prologue_conv_bwd", [&] {
+      hipLaunchKernelGGL((prologue_conv_bwd<0, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[0], conv_w, conv_b,
+                         dys[0], dls[0], pconv);
+      hipLaunchKernelGGL((prologue_conv_bwd<1, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[1], conv_w, conv_b,
+                         dys[1], dls[1], pconv);
+      hipLaunchKernelGGL((prologue_conv_bwd<2, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[2], conv_w, conv_b,
+                         dys[2], dls[2], pconv);
+    });
+    if (r) return r;
+    return L("prologue_gates_bwd", [&] {
+      hipLaunchKernelGGL((prologue_gates_bwd<DH>), dim3(ngate), dim3(256), 0, st, dm, (const bf16*)b_pre,
+                         (const bf16*)w_pre, (const bf16*)f_pre, a_param, (const bf16*)db, (const bf16*)dw, dg,
+                         (bf16*)db_pre, (bf16*)dw_pre, (bf16*)df_pre, pda);
+    });
+  };
+  rc = dm.dh == 64 ? run(IntC<64>{}) : run(IntC<128>{});
+  if (rc) return rc;
+  // parameter gradients: conv partial rows per `which`, then the da partials
+  rc = L("prologue_colsum", [&] {
+    const int ncol = dm.d * (kDc + 1), rows = dm.B * ngrp;
+    for (int wch = 0; wch < 3; ++wch)
+      hipLaunchKernelGGL(prologue_colsum, dim3((unsigned)((ncol + 63) / 64)), dim3(1024), 0, st, ncol, rows,
+                         pconv + (size_t)wch * rows * ncol, sums + (size_t)wch * ncol);
+    // da: the partial rows are [B][L / 32] x [d / 512][heads per block] = [rows][H]
+    hipLaunchKernelGGL(prologue_colsum, dim3((unsigned)((dm.H + 63) / 64)), dim3(1024), 0, st, dm.H,
+                       dm.B * (dm.L / kTileB), pda, da_param);
+  });
+  if (rc) return rc;
+  return L("prologue_param_split", [&] {
+    hipLaunchKernelGGL(prologue_param_split, dim3((unsigned)((3 * dm.d + 255) / 256)), dim3(256), 0, st, dm.d,
+                       sums, dconv_w, dconv_b);
+  });
+}

@@ -83,6 +83,22 @@ def norm_gate_model(rows, d, nparts):
     }
 
 
+def prologue_model(B, L, d):
+    """Algorithmic (flops, HBM bytes) per call of the GDN2 prologue kernels
+    (each conv entry covers its three q / k / v launches): projections and
+    cotangents bf16, g and dg fp32, conv-parameter partial rows fp32."""
+    n = B * L * d
+    parts = 3 * B * (L // 128) * d * 5 * 4
+    return {
+        "prologue_conv_fwd": (3 * n * 14, 3 * n * (2 + 2)),
+        "prologue_gates_fwd": (n * 12, n * (3 * 2 + 2 * 2 + 4)),
+        "prologue_conv_bwd": (3 * n * 30, 3 * n * (2 + 2 + 2) + parts),
+        "prologue_gates_bwd": (n * 16, n * (3 * 2 + 2 * 2 + 4 + 3 * 2)),
+        "prologue_colsum": (parts // 4, parts),
+        "prologue_param_split": (0, 3 * d * 5 * 4 * 2),
+    }
+
+
 def mamba2_groups(B, T, H, C):
     NT = T // C
     G = 1
@@ -232,6 +248,45 @@ def measure_epilogue(args, dev, g, m, q, k, v, w, b, gg, dt, x, Bm, Cm, A, scale
     return res
 
 
+def measure_prologue(dev, g):
+    """The fused GDN2 prologue (forward and backward) at the benchmark's GDN2
+    shape (d = H K), on synthetic projection outputs, timed per kernel with
+    HIP events.  Outside the timed region: not part of the headline metric."""
+    import torch
+    from atomic_ops import _lib
+    from atomic_ops import prologue as PL
+    B, L, H, dh = g["B"], g["T"], g["H"], g["K"]
+    d = H * dh
+    gen = torch.Generator(device=dev).manual_seed(6)
+    r = lambda *s_: torch.randn(*s_, generator=gen, device=dev)
+    ins = [r(B, L, d).to(torch.bfloat16) for _ in range(3)] + [0.5 * r(3, d, 4), 0.1 * r(3, d)]
+    ins += [r(B, L, d).to(torch.bfloat16) for _ in range(3)] + [r(H)]
+    cots = [r(B, L, H, dh).to(torch.bfloat16) for _ in range(5)] + [r(B, L, H, dh)]
+    model = prologue_model(B, L, d)
+    ws = torch.empty(_lib.load().atomic_gdn2_prologue_workspace_size(
+        ctypes.byref(PL.make_args(B, L, H, dh))), dtype=torch.uint8, device=dev)
+    n_it = max(PROF_STEPS, 5)
+    tms = [(_lib.KernelTimer(dev), _lib.KernelTimer(dev)) for _ in range(n_it + 2)]
+    for i in range(n_it + 2):      # two warm-up iterations
+        PL.forward(*ins, H, timer=tms[i][0])
+        PL.backward(*ins, H, *cots, workspace=ws, timer=tms[i][1])
+    torch.cuda.synchronize()
+    per = {}
+    for i in range(2, n_it + 2):
+        for tm in tms[i]:
+            for kn, ms in tm.durations():
+                per.setdefault(kn, []).append(ms)
+    ks = {}
+    for kn, v_ in per.items():
+        avg = sum(v_) / len(v_)
+        fl, by = model[kn]
+        rf = roofline(fl, by, avg / 1e3)
+        ks[kn] = dict(ms_per_launch=round(avg, 4), bytes=int(by), gbps=round(by / (avg / 1e3) / 1e9, 1),
+                      bound=rf["bound"], frac=round(rf["frac"], 4))
+    return dict(shape=f"B{B} L{L} H{H} dh{dh} (d {d}), d_conv 4", kernels=ks,
+                ms_fwd_bwd=round(sum(kv["ms_per_launch"] for kv in ks.values()), 4))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -346,6 +401,7 @@ def main():
     rf["traffic"] = measured_traffic(dom)
 
     epilogue = measure_epilogue(args, dev, g, m, q, k, v, w, b, gg, dt, x, Bm, Cm, A, scale, g_ws, m_ws)
+    prologue = measure_prologue(dev, g)
 
     cpu = None if args.no_cpu else cpu_baseline()
 
@@ -364,6 +420,7 @@ def main():
         "device_ms_per_step_median": round(statistics.median(step_dev_ms), 4),
         "kernels": kernels,
         "epilogue": epilogue,
+        "prologue": prologue,
     }
     print(json.dumps(line), flush=True)
 

@@ -228,6 +228,61 @@ int atomic_norm_gate_bwd(const atomic_norm_gate_args* a, const float* x, const v
                          const float* weight, const void* dout, float* dx, void* dgate,
                          float* dweight, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------- GDN2 prologue (upstream) */
+
+/* The GDN2 block's prologue, fused: from the projection outputs to the
+   chunk pipeline's inputs (reference model.py:574-619):
+     q, k = normalize(silu(conv(q_lin / k_lin) + bias))   per head of dh channels
+     v    = clip(silu(conv(v_lin) + bias), +-50)
+     b, w = sigmoid(b_pre / w_pre)
+     g    = nan_to_num(-exp(clip(a, +-20))[h] softplus(f_pre), nan 0, +inf 0, -inf -20)
+     each = nan_to_num(clip(., +-1e3))
+   conv is the causal depthwise convolution of short_causal_conv (d_conv taps,
+   padding d_conv - 1 on the left) with the fp32 parameters cast to bf16;
+   normalize(t) = t * rsqrt(sum t^2 + eps^2). */
+typedef struct atomic_gdn2_prologue_args {
+  int32_t batch;     /* B                                                     */
+  int32_t seqlen;    /* L: a multiple of 128                                  */
+  int32_t heads;     /* H                                                     */
+  int32_t dhead;     /* dh: 64 or 128; d = H * dh a multiple of 512           */
+  int32_t dconv;     /* d_conv: 4 (the model's)                               */
+  float eps;         /* 1e-6 (the normalisation adds eps^2)                   */
+  atomic_profile* profile;  /* optional per-kernel event timing, or NULL    */
+} atomic_gdn2_prologue_args;
+
+/* Bytes of workspace atomic_gdn2_prologue_bwd needs (0 for unsupported args). */
+size_t atomic_gdn2_prologue_workspace_size(const atomic_gdn2_prologue_args* a);
+
+/*
+ * Forward.  Replaces GatedDeltaNet2J.__call__ between the projections and
+ * the gdn2_pallas_forward_trainable call (model.py:574-619).
+ *   q_lin, k_lin, v_lin, b_pre, w_pre, f_pre : [B, L, d] bf16 (projection outputs)
+ *   conv_w : [3][d][dconv] fp32 (q, k, v)     conv_b : [3][d] fp32     a_param : [H] fp32
+ *   q, k, v, w, b : [B, L, H, dh] bf16        g : [B, L, H, dh] fp32
+ */
+int atomic_gdn2_prologue_fwd(const atomic_gdn2_prologue_args* a, const void* q_lin, const void* k_lin,
+                             const void* v_lin, const float* conv_w, const float* conv_b,
+                             const void* b_pre, const void* w_pre, const void* f_pre,
+                             const float* a_param, void* q, void* k, void* v, void* w, void* b,
+                             float* g, void* stream);
+
+/*
+ * Backward for the cotangents dq, dk, dv, dw, db (bf16) and dg (fp32) of the
+ * forward's outputs (the gradients atomic_gdn2_bwd returns):
+ *   dq_lin, dk_lin, dv_lin, db_pre, dw_pre, df_pre : [B, L, d] bf16
+ *   dconv_w : [3][d][dconv] fp32   dconv_b : [3][d] fp32   da_param : [H] fp32
+ * q and k's cotangents pass the gradient sanitiser of model.py:192-217
+ * (nan_to_num(clip(., +-1e3))) before the normalisation's VJP.
+ */
+int atomic_gdn2_prologue_bwd(const atomic_gdn2_prologue_args* a, const void* q_lin, const void* k_lin,
+                             const void* v_lin, const float* conv_w, const float* conv_b,
+                             const void* b_pre, const void* w_pre, const void* f_pre,
+                             const float* a_param, const void* dq, const void* dk, const void* dv,
+                             const void* dw, const void* db, const float* dg, void* dq_lin,
+                             void* dk_lin, void* dv_lin, float* dconv_w, float* dconv_b,
+                             void* db_pre, void* dw_pre, void* df_pre, float* da_param,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
