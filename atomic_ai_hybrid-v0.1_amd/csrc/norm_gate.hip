@@ -31,11 +31,24 @@ struct NgDims {
 };
 
 __device__ __forceinline__ float bf16r(float x) { return (float)(bf16)x; }
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
+// logistic with the hardware reciprocal (about 1 ulp; every use rounds to bf16)
+__device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Sum over the wave, every lane getting the total: DPP steps inside each
+// 16-lane row (swap neighbours, swap pairs, mirror halves, mirror the row),
+// then the four rows through two lane exchanges.  Each step adds a lane
+// pair's values in both lanes, so every lane holds the identical sum.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int sh = 32; sh >= 1; sh >>= 1) v += __shfl_xor(v, sh);
+  v = dpp_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  v = dpp_add<0x140>(v);  // row_mirror
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
   return v;
 }
 

@@ -37,9 +37,27 @@ struct PlDims {
 };
 
 __device__ __forceinline__ float bfr(float x) { return (float)(bf16)x; }
-__device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
-// jax.nn.softplus(x) = logaddexp(x, 0)
-__device__ __forceinline__ float softplus_(float x) { return fmaxf(x, 0.f) + log1pf(__expf(-fabsf(x))); }
+// logistic with the hardware reciprocal (about 1 ulp; every use rounds to bf16)
+__device__ __forceinline__ float sigm(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+// jax.nn.softplus(x) = logaddexp(x, 0) = max(x, 0) + log(1 + e^{-|x|}); the
+// fast log of 1 + e (in [1, 2]) drops only terms below 1e-7 of max(x, 0)
+__device__ __forceinline__ float softplus_(float x) { return fmaxf(x, 0.f) + __logf(1.f + __expf(-fabsf(x))); }
+
+// 8 bf16 of a row as floats, from a raw 16-byte piece
+__device__ __forceinline__ void unpack8(const u32x4& r, float (&o)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = __uint_as_float(r[i] << 16);
+    o[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+  }
+}
+// the row piece of token t, or zeros for t < 0 (the conv's left padding); the
+// load itself is unconditional (clamped row) so loads can be issued early
+__device__ __forceinline__ u32x4 row_or_zero(const bf16* p, int t, int ld) {
+  const u32x4 v = *reinterpret_cast<const u32x4*>(p + (size_t)(t < 0 ? 0 : t) * ld);
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  return t < 0 ? z : v;
+}
 // cotangent factor of clip(v, -c, c) = min(max(v, -c), c): ties split evenly
 __device__ __forceinline__ float clip_g(float v, float c) {
   const float a = fabsf(v);
@@ -51,11 +69,23 @@ __device__ __forceinline__ float sanit(float x, float c) {
   return fminf(fmaxf(x, -c), c);
 }
 
-// sum over the lanes of one head (G = dh / 8 consecutive lanes)
+// v + v of the lane that the DPP control CTRL selects (within a 16-lane row)
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Sum over the lanes of one head (G = dh / 8 consecutive lanes, 8 or 16),
+// every lane getting the total, by DPP steps inside a 16-lane row: swap
+// neighbours, swap pairs (quad_perm 1032, 2301), mirror the 8-lane halves,
+// mirror the row.  Each step adds a lane pair's values in both lanes (the
+// same sum), so the lanes of a head end with identical totals.
 template <int G>
 __device__ __forceinline__ float head_sum(float v) {
-#pragma unroll
-  for (int sh = 1; sh < G; sh <<= 1) v += __shfl_xor(v, sh);
+  static_assert(G == 8 || G == 16, "heads of 64 or 128 channels");
+  v = dpp_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  if (G == 16) v = dpp_add<0x140>(v);  // row_mirror
   return v;
 }
 
@@ -103,19 +133,17 @@ __global__ __launch_bounds__(256) void prologue_conv_fwd(PlDims dm, const bf16* 
   W.load(conv_w + (size_t)WHICH * dm.d * kDc, conv_b + (size_t)WHICH * dm.d, c);
   const bf16* u = lin + (size_t)b * dm.L * dm.d + c;
   bf16* o = out + (size_t)b * dm.L * dm.d + c;
+  // every input row of the tile (three before it) requested at once
+  u32x4 rows[kTileF + kDc - 1];
+#pragma unroll
+  for (int r = 0; r < kTileF + kDc - 1; ++r) rows[r] = row_or_zero(u, t0 - (kDc - 1) + r, dm.d);
   float win[kDc][8];
 #pragma unroll
-  for (int tp = 0; tp < kDc - 1; ++tp) {
-    const int t = t0 - (kDc - 1) + tp;
-    if (t >= 0) load8(u + (size_t)t * dm.d, win[tp]);
-    else {
+  for (int tp = 0; tp < kDc - 1; ++tp) unpack8(rows[tp], win[tp]);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) win[tp][j] = 0.f;
-    }
-  }
-#pragma unroll 2
-  for (int t = t0; t < t0 + kTileF; ++t) {
-    load8(u + (size_t)t * dm.d, win[kDc - 1]);
+  for (int i = 0; i < kTileF; ++i) {
+    const int t = t0 + i;
+    unpack8(rows[i + kDc - 1], win[kDc - 1]);
     float pre[8], s[8], y[8];
     conv_silu(W, win, pre, s);
     if (WHICH == 2) {
@@ -277,9 +305,12 @@ __global__ __launch_bounds__(256) void prologue_conv_bwd(PlDims dm, const bf16* 
   for (int k = 0; k < kDc - 1; ++k)
 #pragma unroll
     for (int j = 0; j < 8; ++j) en[k][j] = 0.f;
+#pragma unroll 4
   for (int t = t_hi; t >= t0; --t) {
     float g8[8], e[8];
-    load8(dy + (size_t)t * dm.d, g8);
+    const u32x4 rdy = *reinterpret_cast<const u32x4*>(dy + (size_t)t * dm.d);
+    const u32x4 rnext = row_or_zero(u, t - kDc, dm.d);
+    unpack8(rdy, g8);
     conv_out_vjp<WHICH, G>(W, win, g8, dm.eps, e);
     if (t < t0 + kTileB) {
       // d lin[t] = sum_s e[t + s] w[3 - s]; the parameter sums
@@ -307,12 +338,7 @@ __global__ __launch_bounds__(256) void prologue_conv_bwd(PlDims dm, const bf16* 
     for (int tp = kDc - 1; tp >= 1; --tp)
 #pragma unroll
       for (int j = 0; j < 8; ++j) win[tp][j] = win[tp - 1][j];
-    const int tn = t - kDc;
-    if (tn >= 0) load8(u + (size_t)tn * dm.d, win[0]);
-    else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) win[0][j] = 0.f;
-    }
+    unpack8(rnext, win[0]);
   }
   combine_partials<NV>(acc, part + ((size_t)WHICH * dm.B * ngrp + (size_t)b * ngrp + grp) * dm.d * NV, c);
 }
@@ -337,6 +363,7 @@ __global__ __launch_bounds__(256) void prologue_gates_bwd(PlDims dm, const bf16*
   const float araw = a_param[h];
   const float ea = __expf(fminf(fmaxf(araw, -20.f), 20.f)), ga = clip_g(araw, 20.f);
   float da = 0.f;
+#pragma unroll 4
   for (int t = tile * kTileB; t < (tile + 1) * kTileB; ++t) {
     const size_t e = ((size_t)b * dm.L + t) * dm.d + c;
     float bv[8], wv8[8], fv[8], gb[8], gw[8], gg[8], o1[8], o2[8], o3[8];
