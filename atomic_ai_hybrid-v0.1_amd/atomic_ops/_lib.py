@@ -52,6 +52,12 @@ class NormGateArgs(ctypes.Structure):
 NORM_GATE_GDN2, NORM_GATE_MAMBA2 = 0, 1
 
 
+class Mamba2PrologueArgs(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_int32), ("seqlen", ctypes.c_int32), ("heads", ctypes.c_int32),
+                ("headdim", ctypes.c_int32), ("dstate", ctypes.c_int32), ("dconv", ctypes.c_int32),
+                ("profile", ctypes.c_void_p)]
+
+
 class PrologueArgs(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int32), ("seqlen", ctypes.c_int32), ("heads", ctypes.c_int32),
                 ("dhead", ctypes.c_int32), ("dconv", ctypes.c_int32), ("eps", ctypes.c_float),
@@ -117,6 +123,9 @@ _SIGS = {
     "atomic_gdn2_prologue_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(PrologueArgs)]),
     "atomic_gdn2_prologue_fwd": (ctypes.c_int, [ctypes.POINTER(PrologueArgs)] + [_P] * 15 + [_P]),
     "atomic_gdn2_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(PrologueArgs)] + [_P] * 24 + [_P, ctypes.c_size_t, _P]),
+    "atomic_mamba2_prologue_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(Mamba2PrologueArgs)]),
+    "atomic_mamba2_prologue_fwd": (ctypes.c_int, [ctypes.POINTER(Mamba2PrologueArgs)] + [_P] * 12 + [_P]),
+    "atomic_mamba2_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(Mamba2PrologueArgs)] + [_P] * 19 + [_P, ctypes.c_size_t, _P]),
 }
 
 _lib = None

@@ -122,3 +122,81 @@ class GDN2Prologue(torch.autograd.Function):
                          zero(dv, torch.bfloat16), zero(dw, torch.bfloat16), zero(db, torch.bfloat16),
                          zero(dg, torch.float32), ctx.eps)
         return (*grads, None, None)
+
+
+# ------------------------------------------------------------------ Mamba2
+def mamba2_make_args(b, l, heads, headdim, dstate):
+    return _lib.Mamba2PrologueArgs(b, l, heads, headdim, dstate, DCONV)
+
+
+def _m2_check(x_bc, conv_w, conv_b, dt_pre, b_pre, c_pre, a_log, heads):
+    if not x_bc.is_cuda:
+        raise ValueError("prologue inputs must be HIP device tensors")
+    b, l, d = x_bc.shape
+    if x_bc.dtype != torch.bfloat16 or dt_pre.shape != x_bc.shape or dt_pre.dtype != torch.bfloat16:
+        raise TypeError("x_bc and dt_pre must be bfloat16 [B, L, d_inner]")
+    if b_pre.shape[:2] != (b, l) or c_pre.shape != b_pre.shape or b_pre.dtype != torch.bfloat16 \
+            or c_pre.dtype != torch.bfloat16:
+        raise TypeError("B / C projections must be bfloat16 [B, L, N]")
+    if conv_w.shape != (d, DCONV) or conv_b.shape != (d,) or conv_w.dtype != torch.float32 \
+            or conv_b.dtype != torch.float32:
+        raise TypeError("conv_w / conv_b must be float32 [d_inner, 4] / [d_inner]")
+    if a_log.shape != (heads,) or a_log.dtype != torch.float32 or d % heads:
+        raise TypeError("A_log must be float32 [H] with d_inner divisible by H")
+    return b, l, d, b_pre.shape[-1]
+
+
+def mamba2_forward(x_bc, conv_w, conv_b, dt_pre, b_pre, c_pre, a_log, heads, *, timer=None):
+    """``(x, dt, B, C, A)``: x, dt [B, L, H, P] bf16, B, C [B, L, N] bf16, A float32 [H]."""
+    ins = [t.contiguous() for t in (x_bc, dt_pre, b_pre, c_pre)]
+    b, l, d, n = _m2_check(ins[0], conv_w, conv_b, ins[1], ins[2], ins[3], a_log, heads)
+    lib = _lib.load()
+    args = mamba2_make_args(b, l, heads, d // heads, n)
+    if timer is not None:
+        args.profile = timer.arm()
+    dev = x_bc.device
+    shp = (b, l, heads, d // heads)
+    x = torch.empty(shp, dtype=torch.bfloat16, device=dev)
+    dt = torch.empty(shp, dtype=torch.bfloat16, device=dev)
+    B = torch.empty(b, l, n, dtype=torch.bfloat16, device=dev)
+    C = torch.empty(b, l, n, dtype=torch.bfloat16, device=dev)
+    A = torch.empty(heads, dtype=torch.float32, device=dev)
+    rc = lib.atomic_mamba2_prologue_fwd(ctypes.byref(args), _ptr(ins[0]), _ptr(conv_w.contiguous()),
+                                        _ptr(conv_b.contiguous()), _ptr(ins[1]), _ptr(ins[2]), _ptr(ins[3]),
+                                        _ptr(a_log.contiguous()), _ptr(x), _ptr(dt), _ptr(B), _ptr(C), _ptr(A),
+                                        _stream(dev))
+    _lib.check(rc, "atomic_mamba2_prologue_fwd")
+    return x, dt, B, C, A
+
+
+def mamba2_backward(x_bc, conv_w, conv_b, dt_pre, b_pre, c_pre, a_log, heads, dx, ddt, dB, dC, dA, *,
+                    workspace=None, timer=None):
+    """``(dx_bc, dconv_w, dconv_b, ddt_pre, db_pre, dc_pre, da_log)`` (dx_bc: the
+    convolution path's part of x_bc's gradient)."""
+    ins = [t.contiguous() for t in (x_bc, dt_pre, b_pre, c_pre)]
+    b, l, d, n = _m2_check(ins[0], conv_w, conv_b, ins[1], ins[2], ins[3], a_log, heads)
+    lib = _lib.load()
+    args = mamba2_make_args(b, l, heads, d // heads, n)
+    if timer is not None:
+        args.profile = timer.arm()
+    nbytes = lib.atomic_mamba2_prologue_workspace_size(ctypes.byref(args))
+    if nbytes == 0:
+        raise _lib.AtomicError("atomic_mamba2_prologue_workspace_size: unsupported shape")
+    dev = x_bc.device
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    cots = [t.to(torch.bfloat16).contiguous() for t in (dx, ddt, dB, dC)] + [dA.to(torch.float32).contiguous()]
+    dxb = torch.empty(b, l, d, dtype=torch.bfloat16, device=dev)
+    dcw = torch.empty(d, DCONV, dtype=torch.float32, device=dev)
+    dcb = torch.empty(d, dtype=torch.float32, device=dev)
+    ddtp = torch.empty(b, l, d, dtype=torch.bfloat16, device=dev)
+    dbp = torch.empty(b, l, n, dtype=torch.bfloat16, device=dev)
+    dcp = torch.empty(b, l, n, dtype=torch.bfloat16, device=dev)
+    dal = torch.empty(heads, dtype=torch.float32, device=dev)
+    rc = lib.atomic_mamba2_prologue_bwd(
+        ctypes.byref(args), _ptr(ins[0]), _ptr(conv_w.contiguous()), _ptr(conv_b.contiguous()), _ptr(ins[1]),
+        _ptr(ins[2]), _ptr(ins[3]), _ptr(a_log.contiguous()), *(_ptr(c) for c in cots), _ptr(dxb), _ptr(dcw),
+        _ptr(dcb), _ptr(ddtp), _ptr(dbp), _ptr(dcp), _ptr(dal), _ptr(workspace), ctypes.c_size_t(workspace.numel()),
+        _stream(dev))
+    _lib.check(rc, "atomic_mamba2_prologue_bwd")
+    return dxb, dcw, dcb, ddtp, dbp, dcp, dal

@@ -116,8 +116,11 @@ __device__ __forceinline__ void conv_silu(const ConvW& W, const float (&win)[kDc
 }
 
 // ---------------------------------------------------------------- forward
-// WHICH: 0 q, 1 k (normalised), 2 v (clipped to +-50)
-template <int WHICH, int DH>
+// Output of a conv path (MODE): kNorm (GDN2 q, k: per-head normalisation),
+// kClip50 (GDN2 v: clip +-50), kPlain (Mamba2 x); every one is sanitised +-1e3.
+enum { kNorm = 0, kClip50 = 1, kPlain = 2 };
+
+template <int MODE, int DH>
 __global__ __launch_bounds__(256) void prologue_conv_fwd(PlDims dm, const bf16* __restrict__ lin,
                                                          const float* __restrict__ conv_w,
                                                          const float* __restrict__ conv_b,
@@ -130,7 +133,7 @@ __global__ __launch_bounds__(256) void prologue_conv_fwd(PlDims dm, const bf16* 
   const int cb = wv % nblk, tile = (wv / nblk) % ntile, b = wv / (nblk * ntile);
   const int c = cb * 512 + 8 * lane, t0 = tile * kTileF;
   ConvW W;
-  W.load(conv_w + (size_t)WHICH * dm.d * kDc, conv_b + (size_t)WHICH * dm.d, c);
+  W.load(conv_w, conv_b, c);
   const bf16* u = lin + (size_t)b * dm.L * dm.d + c;
   bf16* o = out + (size_t)b * dm.L * dm.d + c;
   // every input row of the tile (three before it) requested at once
@@ -146,9 +149,12 @@ __global__ __launch_bounds__(256) void prologue_conv_fwd(PlDims dm, const bf16* 
     unpack8(rows[i + kDc - 1], win[kDc - 1]);
     float pre[8], s[8], y[8];
     conv_silu(W, win, pre, s);
-    if (WHICH == 2) {
+    if (MODE == kClip50) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) y[j] = sanit(fminf(fmaxf(s[j], -50.f), 50.f), 1e3f);
+    } else if (MODE == kPlain) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = sanit(s[j], 1e3f);
     } else {
       float ss = 0.f;
 #pragma unroll
@@ -199,17 +205,20 @@ __global__ __launch_bounds__(256) void prologue_gates_fwd(PlDims dm, const bf16*
 // ---------------------------------------------------------------- backward
 // Per token of the reverse sweep: the cotangent of the conv accumulator
 // (e = d(conv + bias)), from the output cotangent dy and the forward values.
-template <int WHICH, int G>
+template <int MODE, int G>
 __device__ __forceinline__ void conv_out_vjp(const ConvW& W, const float (&win)[kDc][8], const float (&dy)[8],
                                              float eps, float (&e)[8]) {
   float pre[8], s[8], ds[8];
   conv_silu(W, win, pre, s);
-  if (WHICH == 2) {
+  if (MODE == kClip50) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float v = fminf(fmaxf(s[j], -50.f), 50.f);
       ds[j] = bfr(dy[j] * clip_g(v, 1e3f) * clip_g(s[j], 50.f));
     }
+  } else if (MODE == kPlain) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ds[j] = bfr(dy[j] * clip_g(s[j], 1e3f));
   } else {
     float ss = 0.f;
 #pragma unroll
@@ -266,7 +275,7 @@ __device__ __forceinline__ void combine_partials(float (&v)[NV][8], float* __res
 
 // The four waves of a workgroup take four consecutive tiles of one
 // (batch, channel block); partial row index = (batch, tile group).
-template <int WHICH, int DH>
+template <int MODE, int DH>
 __global__ __launch_bounds__(256) void prologue_conv_bwd(PlDims dm, const bf16* __restrict__ lin,
                                                          const float* __restrict__ conv_w,
                                                          const float* __restrict__ conv_b,
@@ -279,7 +288,7 @@ __global__ __launch_bounds__(256) void prologue_conv_bwd(PlDims dm, const bf16* 
   const int tile = grp * 4 + wave_id();
   const int c = cb * 512 + 8 * lane, t0 = tile * kTileB;
   ConvW W;
-  W.load(conv_w + (size_t)WHICH * dm.d * kDc, conv_b + (size_t)WHICH * dm.d, c);
+  W.load(conv_w, conv_b, c);
   const bf16* u = lin + (size_t)b * dm.L * dm.d + c;
   const bf16* dy = dout + (size_t)b * dm.L * dm.d + c;
   bf16* du = dlin + (size_t)b * dm.L * dm.d + c;
@@ -311,7 +320,7 @@ __global__ __launch_bounds__(256) void prologue_conv_bwd(PlDims dm, const bf16* 
     const u32x4 rdy = *reinterpret_cast<const u32x4*>(dy + (size_t)t * dm.d);
     const u32x4 rnext = row_or_zero(u, t - kDc, dm.d);
     unpack8(rdy, g8);
-    conv_out_vjp<WHICH, G>(W, win, g8, dm.eps, e);
+    conv_out_vjp<MODE, G>(W, win, g8, dm.eps, e);
     if (t < t0 + kTileB) {
       // d lin[t] = sum_s e[t + s] w[3 - s]; the parameter sums
       float o8[8];
@@ -340,7 +349,7 @@ __global__ __launch_bounds__(256) void prologue_conv_bwd(PlDims dm, const bf16* 
       for (int j = 0; j < 8; ++j) win[tp][j] = win[tp - 1][j];
     unpack8(rnext, win[0]);
   }
-  combine_partials<NV>(acc, part + ((size_t)WHICH * dm.B * ngrp + (size_t)b * ngrp + grp) * dm.d * NV, c);
+  combine_partials<NV>(acc, part + ((size_t)b * ngrp + grp) * dm.d * NV, c);
 }
 
 // b, w, g gradients; per-head partial sums of da
@@ -438,6 +447,99 @@ __global__ __launch_bounds__(256) void prologue_param_split(int d, const float* 
   dconv_b[i] = bfr(sums[(size_t)i * (kDc + 1) + kDc]);
 }
 
+// ---------------------------------------------------------- Mamba2 prologue
+// dt = clip(softplus(dt_pre), bf16(1e-2), 1) and B, C, x, dt sanitised
+// (reference model.py:426-433): the element-wise part; x's convolution is
+// prologue_conv_* in kPlain mode.  A = -exp(clip(A_log, +-20)) (:420-422).
+__device__ __forceinline__ float dt_lo() { return bfr(1e-2f); }
+
+__global__ __launch_bounds__(256) void m2_prologue_elem_fwd(size_t n_dt, size_t n_bc, int H,
+                                                            const bf16* __restrict__ dt_pre,
+                                                            const bf16* __restrict__ b_pre,
+                                                            const bf16* __restrict__ c_pre,
+                                                            const float* __restrict__ a_log,
+                                                            bf16* __restrict__ dt, bf16* __restrict__ bo,
+                                                            bf16* __restrict__ co, float* __restrict__ a_out) {
+  const size_t e = ((size_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e < n_dt) {
+    float v[8];
+    load8(dt_pre + e, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = sanit(fminf(fmaxf(bfr(softplus_(v[j])), dt_lo()), 1.f), 1e3f);
+    store8(dt + e, v);
+  }
+  if (e < n_bc) {
+    float b8[8], c8[8];
+    load8(b_pre + e, b8);
+    load8(c_pre + e, c8);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { b8[j] = sanit(b8[j], 1e3f); c8[j] = sanit(c8[j], 1e3f); }
+    store8(bo + e, b8);
+    store8(co + e, c8);
+  }
+  if (blockIdx.x == 0)
+    for (int h = threadIdx.x; h < H; h += 256) a_out[h] = -__expf(fminf(fmaxf(a_log[h], -20.f), 20.f));
+}
+
+// cotangent factor of clip(x, lo, hi) = min(max(x, lo), hi)
+__device__ __forceinline__ float clip_range_g(float x, float lo, float hi) {
+  const float a = x > lo ? 1.f : (x == lo ? 0.5f : 0.f);
+  const float b = x < hi ? 1.f : (x == hi ? 0.5f : 0.f);
+  return a * b;
+}
+
+__global__ __launch_bounds__(256) void m2_prologue_elem_bwd(size_t n_dt, size_t n_bc, int H,
+                                                            const bf16* __restrict__ dt_pre,
+                                                            const bf16* __restrict__ b_pre,
+                                                            const bf16* __restrict__ c_pre,
+                                                            const float* __restrict__ a_log,
+                                                            const bf16* __restrict__ ddt, const bf16* __restrict__ dbo,
+                                                            const bf16* __restrict__ dco, const float* __restrict__ da,
+                                                            bf16* __restrict__ ddt_pre, bf16* __restrict__ db_pre,
+                                                            bf16* __restrict__ dc_pre, float* __restrict__ da_log) {
+  const size_t e = ((size_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e < n_dt) {
+    float v[8], g[8], o[8];
+    load8(dt_pre + e, v);
+    load8(ddt + e, g);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float sp = bfr(softplus_(v[j]));
+      const float c = fminf(fmaxf(sp, dt_lo()), 1.f);
+      const float dsp = bfr(g[j] * clip_g(c, 1e3f) * clip_range_g(sp, dt_lo(), 1.f));
+      o[j] = bfr(dsp * sigm(v[j]));   // softplus' = logistic
+    }
+    store8(ddt_pre + e, o);
+  }
+  if (e < n_bc) {
+    float b8[8], c8[8], gb[8], gc[8];
+    load8(b_pre + e, b8);
+    load8(c_pre + e, c8);
+    load8(dbo + e, gb);
+    load8(dco + e, gc);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { gb[j] = bfr(gb[j] * clip_g(b8[j], 1e3f)); gc[j] = bfr(gc[j] * clip_g(c8[j], 1e3f)); }
+    store8(db_pre + e, gb);
+    store8(dc_pre + e, gc);
+  }
+  if (blockIdx.x == 0)
+    for (int h = threadIdx.x; h < H; h += 256) {
+      const float al = a_log[h];
+      da_log[h] = da[h] * (-__expf(fminf(fmaxf(al, -20.f), 20.f))) * clip_g(al, 20.f);
+    }
+}
+
+// one conv's weight / bias gradients from its summed [d][5] block
+__global__ __launch_bounds__(256) void prologue_param_split1(int d, const float* __restrict__ sums,
+                                                             float* __restrict__ dconv_w,
+                                                             float* __restrict__ dconv_b) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= d) return;
+#pragma unroll
+  for (int tp = 0; tp < kDc; ++tp) dconv_w[(size_t)i * kDc + tp] = bfr(sums[(size_t)i * (kDc + 1) + tp]);
+  dconv_b[i] = bfr(sums[(size_t)i * (kDc + 1) + kDc]);
+}
+
 // ------------------------------------------------------------------ host
 static int pl_check(const atomic_gdn2_prologue_args* a) {
   if (!a) return ATOMIC_ERR_NULL;
@@ -502,12 +604,13 @@ extern "C" int atomic_gdn2_prologue_fwd(const atomic_gdn2_prologue_args* a, cons
   auto run = [&](auto Dc) {
     constexpr int DH = decltype(Dc)::value;
     int r = L("prologue_conv_fwd", [&] {
-      hipLaunchKernelGGL((prologue_conv_fwd<0, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[0], conv_w, conv_b,
-                         outs[0]);
-      hipLaunchKernelGGL((prologue_conv_fwd<1, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[1], conv_w, conv_b,
-                         outs[1]);
-      hipLaunchKernelGGL((prologue_conv_fwd<2, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[2], conv_w, conv_b,
-                         outs[2]);
+      const size_t ow = (size_t)dm.d * kDc, ob = (size_t)dm.d;
+      hipLaunchKernelGGL((prologue_conv_fwd<kNorm, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[0], conv_w,
+                         conv_b, outs[0]);
+      hipLaunchKernelGGL((prologue_conv_fwd<kNorm, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[1],
+                         conv_w + ow, conv_b + ob, outs[1]);
+      hipLaunchKernelGGL((prologue_conv_fwd<kClip50, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[2],
+                         conv_w + 2 * ow, conv_b + 2 * ob, outs[2]);
     });
     if (r) return r;
     return L("prologue_gates_fwd", [&] {
@@ -551,12 +654,14 @@ extern "C" int atomic_gdn2_prologue_bwd(const atomic_gdn2_prologue_args* a, cons
   auto run = [&](auto Dc) {
     constexpr int DH = decltype(Dc)::value;
     int r = L("prologue_conv_bwd", [&] {
-      hipLaunchKernelGGL((prologue_conv_bwd<0, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[0], conv_w, conv_b,
-                         dys[0], dls[0], pconv);
-      hipLaunchKernelGGL((prologue_conv_bwd<1, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[1], conv_w, conv_b,
-                         dys[1], dls[1], pconv);
-      hipLaunchKernelGGL((prologue_conv_bwd<2, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[2], conv_w, conv_b,
-                         dys[2], dls[2], pconv);
+      const size_t ow = (size_t)dm.d * kDc, ob = (size_t)dm.d;
+      const size_t op = (size_t)dm.B * ngrp * dm.d * (kDc + 1);  // one conv's partial rows
+      hipLaunchKernelGGL((prologue_conv_bwd<kNorm, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[0], conv_w,
+                         conv_b, dys[0], dls[0], pconv);
+      hipLaunchKernelGGL((prologue_conv_bwd<kNorm, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[1],
+                         conv_w + ow, conv_b + ob, dys[1], dls[1], pconv + op);
+      hipLaunchKernelGGL((prologue_conv_bwd<kClip50, DH>), dim3(nconv), dim3(256), 0, st, dm, lins[2],
+                         conv_w + 2 * ow, conv_b + 2 * ob, dys[2], dls[2], pconv + 2 * op);
     });
     if (r) return r;
     return L("prologue_gates_bwd", [&] {
@@ -581,5 +686,104 @@ extern "C" int atomic_gdn2_prologue_bwd(const atomic_gdn2_prologue_args* a, cons
   return L("prologue_param_split", [&] {
     hipLaunchKernelGGL(prologue_param_split, dim3((unsigned)((3 * dm.d + 255) / 256)), dim3(256), 0, st, dm.d,
                        sums, dconv_w, dconv_b);
+  });
+}
+
+// ------------------------------------------------------------ Mamba2 entry points
+static int m2p_check(const atomic_mamba2_prologue_args* a) {
+  if (!a) return ATOMIC_ERR_NULL;
+  if (a->batch <= 0 || a->seqlen <= 0 || a->heads <= 0 || a->headdim <= 0 || a->dstate <= 0)
+    return ATOMIC_ERR_SHAPE;
+  if (a->dconv != kDc || (a->heads * a->headdim) % 512 != 0 || a->seqlen % (4 * kTileB) != 0 ||
+      a->dstate % 8 != 0)
+    return ATOMIC_ERR_SHAPE;
+  return ATOMIC_OK;
+}
+static PlDims m2p_dims(const atomic_mamba2_prologue_args* a) {
+  return PlDims{a->batch, a->seqlen, a->heads, 128, a->heads * a->headdim, 0.f};
+}
+// workspace: x's conv partial rows [B][L / 128][d][5], then the summed [d][5]
+static size_t m2p_ws(const PlDims& d, size_t* sums_off) {
+  auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
+  const size_t rows = (size_t)d.B * (d.L / (4 * kTileB));
+  *sums_off = al(rows * d.d * (kDc + 1) * 4);
+  return *sums_off + al((size_t)d.d * (kDc + 1) * 4);
+}
+
+extern "C" size_t atomic_mamba2_prologue_workspace_size(const atomic_mamba2_prologue_args* a) {
+  if (m2p_check(a) != ATOMIC_OK) return 0;
+  size_t so;
+  return m2p_ws(m2p_dims(a), &so);
+}
+
+extern "C" int atomic_mamba2_prologue_fwd(const atomic_mamba2_prologue_args* a, const void* x_bc,
+                                          const float* conv_w, const float* conv_b, const void* dt_pre,
+                                          const void* b_pre, const void* c_pre, const float* a_log, void* x,
+                                          void* dt, void* B, void* C, float* A, void* stream) {
+  int rc = m2p_check(a);
+  if (rc) return rc;
+  if (!x_bc || !conv_w || !conv_b || !dt_pre || !b_pre || !c_pre || !a_log || !x || !dt || !B || !C || !A)
+    return ATOMIC_ERR_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  const PlDims dm = m2p_dims(a);
+  Launch L{a->profile, st};
+  const unsigned nconv = (unsigned)(((size_t)dm.B * (dm.L / kTileF) * (dm.d / 512) + 3) / 4);
+  rc = L("prologue_conv_fwd", [&] {
+    hipLaunchKernelGGL((prologue_conv_fwd<kPlain, 128>), dim3(nconv), dim3(256), 0, st, dm, (const bf16*)x_bc,
+                       conv_w, conv_b, (bf16*)x);
+  });
+  if (rc) return rc;
+  const size_t n_dt = (size_t)dm.B * dm.L * dm.d, n_bc = (size_t)dm.B * dm.L * a->dstate;
+  const size_t n = n_dt > n_bc ? n_dt : n_bc;
+  return L("m2_prologue_elem_fwd", [&] {
+    hipLaunchKernelGGL(m2_prologue_elem_fwd, dim3((unsigned)((n / 8 + 255) / 256)), dim3(256), 0, st, n_dt, n_bc,
+                       dm.H, (const bf16*)dt_pre, (const bf16*)b_pre, (const bf16*)c_pre, a_log, (bf16*)dt,
+                       (bf16*)B, (bf16*)C, A);
+  });
+}
+
+extern "C" int atomic_mamba2_prologue_bwd(const atomic_mamba2_prologue_args* a, const void* x_bc,
+                                          const float* conv_w, const float* conv_b, const void* dt_pre,
+                                          const void* b_pre, const void* c_pre, const float* a_log,
+                                          const void* dx, const void* ddt, const void* dB, const void* dC,
+                                          const float* dA, void* dx_bc, float* dconv_w, float* dconv_b,
+                                          void* ddt_pre, void* db_pre, void* dc_pre, float* da_log,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = m2p_check(a);
+  if (rc) return rc;
+  if (!x_bc || !conv_w || !conv_b || !dt_pre || !b_pre || !c_pre || !a_log || !dx || !ddt || !dB || !dC || !dA ||
+      !dx_bc || !dconv_w || !dconv_b || !ddt_pre || !db_pre || !dc_pre || !da_log)
+    return ATOMIC_ERR_NULL;
+  const PlDims dm = m2p_dims(a);
+  size_t so;
+  if (!workspace || workspace_bytes < m2p_ws(dm, &so)) return ATOMIC_ERR_WORKSPACE;
+  float* part = (float*)workspace;
+  float* sums = (float*)((unsigned char*)workspace + so);
+  hipStream_t st = (hipStream_t)stream;
+  Launch L{a->profile, st};
+  const int ngrp = dm.L / (4 * kTileB);
+  rc = L("prologue_conv_bwd", [&] {
+    hipLaunchKernelGGL((prologue_conv_bwd<kPlain, 128>), dim3((unsigned)((size_t)dm.B * ngrp * (dm.d / 512))),
+                       dim3(256), 0, st, dm, (const bf16*)x_bc, conv_w, conv_b, (const bf16*)dx, (bf16*)dx_bc, part);
+  });
+  if (rc) return rc;
+  const size_t n_dt = (size_t)dm.B * dm.L * dm.d, n_bc = (size_t)dm.B * dm.L * a->dstate;
+  const size_t n = n_dt > n_bc ? n_dt : n_bc;
+  rc = L("m2_prologue_elem_bwd", [&] {
+    hipLaunchKernelGGL(m2_prologue_elem_bwd, dim3((unsigned)((n / 8 + 255) / 256)), dim3(256), 0, st, n_dt, n_bc,
+                       dm.H, (const bf16*)dt_pre, (const bf16*)b_pre, (const bf16*)c_pre, a_log, (const bf16*)ddt,
+                       (const bf16*)dB, (const bf16*)dC, dA, (bf16*)ddt_pre, (bf16*)db_pre, (bf16*)dc_pre, da_log);
+  });
+  if (rc) return rc;
+  rc = L("prologue_colsum", [&] {
+    const int ncol = dm.d * (kDc + 1);
+    hipLaunchKernelGGL(prologue_colsum, dim3((unsigned)((ncol + 63) / 64)), dim3(1024), 0, st, ncol,
+                       dm.B * ngrp, part, sums);
+  });
+  if (rc) return rc;
+  return L("prologue_param_split", [&] {
+    // one conv: the split kernel's (which, channel) range is just the channels
+    hipLaunchKernelGGL(prologue_param_split1, dim3((unsigned)((dm.d + 255) / 256)), dim3(256), 0, st, dm.d, sums,
+                       dconv_w, dconv_b);
   });
 }

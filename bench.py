@@ -99,6 +99,20 @@ def prologue_model(B, L, d):
     }
 
 
+def mamba2_prologue_model(B, L, d, N):
+    """Algorithmic (flops, HBM bytes) per call of the Mamba2 prologue kernels."""
+    n, nb = B * L * d, B * L * N
+    parts = B * (L // 128) * d * 5 * 4
+    return {
+        "prologue_conv_fwd": (n * 14, n * (2 + 2)),
+        "m2_prologue_elem_fwd": (n * 8, n * (2 + 2) + nb * (2 + 2) * 2),
+        "prologue_conv_bwd": (n * 30, n * (2 + 2 + 2) + parts),
+        "m2_prologue_elem_bwd": (n * 10, n * (2 + 2 + 2) + nb * (2 + 2 + 2) * 2),
+        "prologue_colsum": (parts // 4, parts),
+        "prologue_param_split": (0, d * 5 * 4 * 2),
+    }
+
+
 def mamba2_groups(B, T, H, C):
     NT = T // C
     G = 1
@@ -287,6 +301,46 @@ def measure_prologue(dev, g):
                 ms_fwd_bwd=round(sum(kv["ms_per_launch"] for kv in ks.values()), 4))
 
 
+def measure_mamba2_prologue(dev, m):
+    """The fused Mamba2 prologue (forward and backward) at the benchmark's
+    Mamba2 shape, on synthetic projection outputs; per-kernel HIP events.
+    Outside the timed region: not part of the headline metric."""
+    import torch
+    from atomic_ops import _lib
+    from atomic_ops import prologue as PL
+    B, L, H, P, N = m["B"], m["T"], m["H"], m["P"], m["N"]
+    d = H * P
+    gen = torch.Generator(device=dev).manual_seed(8)
+    r = lambda *s_: torch.randn(*s_, generator=gen, device=dev)
+    ins = [r(B, L, d).to(torch.bfloat16), 0.5 * r(d, 4), 0.1 * r(d), (r(B, L, d) - 1.0).to(torch.bfloat16),
+           r(B, L, N).to(torch.bfloat16), r(B, L, N).to(torch.bfloat16), r(H)]
+    cots = [r(B, L, H, P).to(torch.bfloat16), r(B, L, H, P).to(torch.bfloat16), r(B, L, N).to(torch.bfloat16),
+            r(B, L, N).to(torch.bfloat16), r(H)]
+    model = mamba2_prologue_model(B, L, d, N)
+    ws = torch.empty(_lib.load().atomic_mamba2_prologue_workspace_size(
+        ctypes.byref(PL.mamba2_make_args(B, L, H, P, N))), dtype=torch.uint8, device=dev)
+    n_it = max(PROF_STEPS, 5)
+    tms = [(_lib.KernelTimer(dev), _lib.KernelTimer(dev)) for _ in range(n_it + 2)]
+    for i in range(n_it + 2):      # two warm-up iterations
+        PL.mamba2_forward(*ins, H, timer=tms[i][0])
+        PL.mamba2_backward(*ins, H, *cots, workspace=ws, timer=tms[i][1])
+    torch.cuda.synchronize()
+    per = {}
+    for i in range(2, n_it + 2):
+        for tm in tms[i]:
+            for kn, ms in tm.durations():
+                per.setdefault(kn, []).append(ms)
+    ks = {}
+    for kn, v_ in per.items():
+        avg = sum(v_) / len(v_)
+        fl, by = model[kn]
+        rf = roofline(fl, by, avg / 1e3)
+        ks[kn] = dict(ms_per_launch=round(avg, 4), bytes=int(by), gbps=round(by / (avg / 1e3) / 1e9, 1),
+                      bound=rf["bound"], frac=round(rf["frac"], 4))
+    return dict(shape=f"B{B} L{L} H{H} P{P} N{N} (d_inner {d}), d_conv 4", kernels=ks,
+                ms_fwd_bwd=round(sum(kv["ms_per_launch"] for kv in ks.values()), 4))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -402,6 +456,7 @@ def main():
 
     epilogue = measure_epilogue(args, dev, g, m, q, k, v, w, b, gg, dt, x, Bm, Cm, A, scale, g_ws, m_ws)
     prologue = measure_prologue(dev, g)
+    prologue_m2 = measure_mamba2_prologue(dev, m)
 
     cpu = None if args.no_cpu else cpu_baseline()
 
@@ -421,6 +476,7 @@ def main():
         "kernels": kernels,
         "epilogue": epilogue,
         "prologue": prologue,
+        "prologue_mamba2": prologue_m2,
     }
     print(json.dumps(line), flush=True)
 

@@ -283,6 +283,56 @@ int atomic_gdn2_prologue_bwd(const atomic_gdn2_prologue_args* a, const void* q_l
                              void* db_pre, void* dw_pre, void* df_pre, float* da_param,
                              void* workspace, size_t workspace_bytes, void* stream);
 
+/* ----------------------------------------- Mamba2 prologue (upstream) */
+
+/* The Mamba2 block's element-wise prologue, fused (reference model.py:405-433),
+   between in_proj / B_proj / C_proj / dt_proj (GEMMs, in the model) and the
+   SSD call:
+     x  = silu(conv(x_bc) + bias)                  (causal depthwise, dconv taps)
+     dt = clip(softplus(dt_pre), bf16(1e-2), 1)
+     x, dt, B, C = nan_to_num(clip(., +-1e3))
+     A  = -exp(clip(A_log, +-20))                  (per head, fp32) */
+typedef struct atomic_mamba2_prologue_args {
+  int32_t batch;     /* B                                                   */
+  int32_t seqlen;    /* L: a multiple of 128                                */
+  int32_t heads;     /* H                                                   */
+  int32_t headdim;   /* P; d_inner = H * P a multiple of 512                */
+  int32_t dstate;    /* N: a multiple of 8                                  */
+  int32_t dconv;     /* 4 (the model's)                                     */
+  atomic_profile* profile;  /* optional per-kernel event timing, or NULL  */
+} atomic_mamba2_prologue_args;
+
+/* Bytes of workspace atomic_mamba2_prologue_bwd needs (0 for unsupported args). */
+size_t atomic_mamba2_prologue_workspace_size(const atomic_mamba2_prologue_args* a);
+
+/*
+ * Forward.
+ *   x_bc, dt_pre : [B, L, d_inner] bf16 (the in_proj half, the dt_proj output)
+ *   conv_w : [d_inner][dconv] fp32   conv_b : [d_inner] fp32   a_log : [H] fp32
+ *   b_pre, c_pre : [B, L, N] bf16 (B_proj, C_proj outputs)
+ *   x, dt : [B, L, H, P] bf16   B, C : [B, L, N] bf16   A : [H] fp32
+ */
+int atomic_mamba2_prologue_fwd(const atomic_mamba2_prologue_args* a, const void* x_bc,
+                               const float* conv_w, const float* conv_b, const void* dt_pre,
+                               const void* b_pre, const void* c_pre, const float* a_log, void* x,
+                               void* dt, void* B, void* C, float* A, void* stream);
+
+/*
+ * Backward for the cotangents dx, ddt (bf16), dB, dC (bf16) and dA (fp32) of
+ * the forward's outputs (the gradients atomic_mamba2_bwd returns).  dx_bc is
+ * the convolution path's part of x_bc's gradient (the B / C / dt projections'
+ * parts come from their GEMMs in the model).
+ *   dx_bc, ddt_pre : [B, L, d_inner] bf16   db_pre, dc_pre : [B, L, N] bf16
+ *   dconv_w : [d_inner][dconv] fp32   dconv_b : [d_inner] fp32   da_log : [H] fp32
+ */
+int atomic_mamba2_prologue_bwd(const atomic_mamba2_prologue_args* a, const void* x_bc,
+                               const float* conv_w, const float* conv_b, const void* dt_pre,
+                               const void* b_pre, const void* c_pre, const float* a_log,
+                               const void* dx, const void* ddt, const void* dB, const void* dC,
+                               const float* dA, void* dx_bc, float* dconv_w, float* dconv_b,
+                               void* ddt_pre, void* db_pre, void* dc_pre, float* da_log,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -133,3 +133,46 @@ def gdn2_prologue_grads(inputs, cotangents, heads, eps=1e-6, exact=False):
     outs = gdn2_prologue(*leaves, heads, eps=eps, exact=exact)
     torch.autograd.backward(outs, [c.to(o.dtype) for c, o in zip(cotangents, outs)])
     return tuple(t.grad for t in leaves)
+
+
+class _ClipRange(torch.autograd.Function):
+    """clip(x, lo, hi) = min(max(x, lo), hi) with JAX's max / min VJP."""
+
+    @staticmethod
+    def forward(ctx, x, lo, hi):
+        ctx.save_for_backward(x)
+        ctx.lo, ctx.hi = lo, hi
+        return x.clamp(lo, hi)
+
+    @staticmethod
+    def backward(ctx, g):
+        (x,) = ctx.saved_tensors
+        a = torch.where(x > ctx.lo, 1.0, torch.where(x == ctx.lo, 0.5, 0.0))
+        b = torch.where(x < ctx.hi, 1.0, torch.where(x == ctx.hi, 0.5, 0.0))
+        return g * (a * b).to(g.dtype), None, None
+
+
+def mamba2_prologue(x_bc, conv_w, conv_b, dt_pre, b_pre, c_pre, a_log, heads, exact=False):
+    """The Mamba2 block's element-wise prologue (model.py:405-433) after the
+    in_proj / B_proj / C_proj / dt_proj GEMMs: (x, dt, B, C, A) with x, dt as
+    [B, L, H, P] in the activation dtype, B, C [B, L, N], A float32 [H].
+    conv_w: [d_inner, dc] float32; conv_b: [d_inner] float32; a_log: [H] float32."""
+    x = torch.nn.functional.silu(causal_conv(x_bc, conv_w, conv_b, exact))      # :409-417
+    a = _Clip.apply(a_log.to(torch.float64 if exact else torch.float32), 20.0)
+    A = -torch.exp(a)                                                            # :420-422
+    dt = torch.logaddexp(dt_pre, torch.zeros_like(dt_pre))                       # softplus (:425)
+    lo = 1e-2 if exact else float(torch.tensor(1e-2, dtype=torch.bfloat16))    # jnp.array(1e-2, bf16)
+    dt = _ClipRange.apply(dt, lo, 1.0)                                           # (:426)
+    dt, B, C, x = (_sanitize(t) for t in (dt, b_pre, c_pre, x))                  # (:428-432)
+    b_, l, d = x.shape
+    shp = (b_, l, heads, d // heads)
+    return x.reshape(shp), dt.reshape(shp), B, C, A
+
+
+def mamba2_prologue_grads(inputs, cotangents, heads, exact=False):
+    """Gradients of ``mamba2_prologue`` w.r.t. (x_bc, conv_w, conv_b, dt_pre,
+    b_pre, c_pre, a_log) for cotangents (dx, ddt, dB, dC, dA)."""
+    leaves = [t.detach().clone().requires_grad_(True) for t in inputs]
+    outs = mamba2_prologue(*leaves, heads, exact=exact)
+    torch.autograd.backward(outs, [c.to(o.dtype) for c, o in zip(cotangents, outs)])
+    return tuple(t.grad for t in leaves)

@@ -24,7 +24,8 @@ def test_every_header_function_has_a_ctypes_signature():
 
 STRUCTS = [(_lib.Gdn2Args, "atomic_gdn2_args"), (_lib.Mamba2Args, "atomic_mamba2_args"),
            (_lib.Gdn2Layout, "atomic_gdn2_layout"), (_lib.AtomicProfile, "atomic_profile"),
-           (_lib.NormGateArgs, "atomic_norm_gate_args"), (_lib.PrologueArgs, "atomic_gdn2_prologue_args")]
+           (_lib.NormGateArgs, "atomic_norm_gate_args"), (_lib.PrologueArgs, "atomic_gdn2_prologue_args"),
+           (_lib.Mamba2PrologueArgs, "atomic_mamba2_prologue_args")]
 
 
 def _header_fields(cname):

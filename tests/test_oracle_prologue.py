@@ -97,3 +97,54 @@ def test_bf16_flow_stays_near_exact():
     bf = op.gdn2_prologue(*ins, H)
     for a, b in zip(bf, ex):
         assert rel_err(a, b) < 2e-2
+
+
+def _m2_inputs(B, L, H, P, N, seed, dtype=F64):
+    g = torch.Generator().manual_seed(seed)
+    d = H * P
+    r = lambda *s: torch.randn(*s, generator=g, dtype=F64)
+    ins = [r(B, L, d), 0.5 * r(d, 4), 0.1 * r(d), r(B, L, d) - 1.0, r(B, L, N), r(B, L, N), r(H)]
+    return [t.to(dtype) if i in (0, 3, 4, 5) else t for i, t in enumerate(ins)]
+
+
+def test_mamba2_prologue_autograd_matches_finite_differences():
+    B, L, H, P, N = 1, 5, 2, 2, 3
+    ins = _m2_inputs(B, L, H, P, N, 5)
+    g = torch.Generator().manual_seed(6)
+    cots = [torch.randn(B, L, H, P, generator=g, dtype=F64), torch.randn(B, L, H, P, generator=g, dtype=F64),
+            torch.randn(B, L, N, generator=g, dtype=F64), torch.randn(B, L, N, generator=g, dtype=F64),
+            torch.randn(H, generator=g, dtype=F64)]
+    grads = op.mamba2_prologue_grads(ins, cots, H, exact=True)
+
+    def loss(args):
+        return sum((o * c).sum() for o, c in zip(op.mamba2_prologue(*args, H, exact=True), cots))
+
+    h = 1e-6
+    for i, t in enumerate(ins):
+        fd = torch.zeros_like(t)
+        for idx in range(t.numel()):
+            e = torch.zeros(t.numel(), dtype=F64)
+            e[idx] = h
+            e = e.view(t.shape)
+            p = list(ins); p[i] = t + e
+            m = list(ins); m[i] = t - e
+            fd.view(-1)[idx] = (loss(p) - loss(m)) / (2 * h)
+        assert rel_err(grads[i], fd) < 1e-6, i
+
+
+def test_mamba2_prologue_closed_forms():
+    B, L, H, P, N = 1, 8, 2, 4, 4
+    ins = _m2_inputs(B, L, H, P, N, 7)
+    ins[6] = torch.tensor([0.0, 30.0], dtype=F64)
+    ins[3] = torch.tensor([-50.0, 0.0, 50.0, 2.0], dtype=F64).repeat(B, L, H * P // 4)
+    x, dt, Bo, Co, A = op.mamba2_prologue(*ins, H, exact=True)
+    assert rel_err(A, torch.tensor([-1.0, -torch.exp(torch.tensor(20.0, dtype=F64))], dtype=F64)) < 1e-12
+    sp = torch.log1p(torch.exp(ins[3])).clamp(1e-2, 1.0).view(B, L, H, P)
+    assert rel_err(dt, sp) < 1e-12              # softplus(-50) floors at 1e-2, softplus(50) caps at 1
+    assert torch.equal(Bo, ins[4]) and torch.equal(Co, ins[5])
+    # identity taps: x = silu(x_bc)
+    ident = list(ins)
+    cw = torch.zeros_like(ins[1]); cw[:, 3] = 1.0
+    ident[1], ident[2] = cw, torch.zeros_like(ins[2])
+    assert rel_err(op.mamba2_prologue(*ident, H, exact=True)[0],
+                   torch.nn.functional.silu(ins[0]).view(B, L, H, P)) < 1e-12

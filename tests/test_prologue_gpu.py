@@ -69,3 +69,37 @@ def test_unsupported_shape_is_rejected_before_launch():
     ins, _ = _inputs(1, 96, 4, 128, 3)      # L not a multiple of 128
     with pytest.raises(_lib.AtomicError, match="SHAPE"):
         PL.forward(*(t.cuda() for t in ins), 4)
+
+
+M2_OUT = ("x", "dt", "B", "C", "A")
+M2_GRADS = ("dx_bc", "dconv_w", "dconv_b", "ddt_pre", "db_pre", "dc_pre", "da_log")
+
+
+def _m2_inputs(B, L, H, P, N, seed):
+    g = torch.Generator().manual_seed(seed)
+    d = H * P
+    r = lambda *s: torch.randn(*s, generator=g)
+    ins = [r(B, L, d).to(BF16), 0.5 * r(d, 4), 0.1 * r(d), (2.0 * r(B, L, d) - 1.0).to(BF16),
+           r(B, L, N).to(BF16), r(B, L, N).to(BF16), r(H)]
+    cots = [r(B, L, H, P).to(BF16), r(B, L, H, P).to(BF16), r(B, L, N).to(BF16), r(B, L, N).to(BF16), r(H)]
+    return ins, cots
+
+
+@pytest.mark.parametrize("B,L,H,P,N", [
+    (2, 128, 4, 128, 64),     # two sequences, d_inner 512
+    (1, 256, 16, 128, 128),   # the benchmark's Mamba2 head shape (d_inner 2048)
+])
+def test_mamba2_prologue_matches_oracle(B, L, H, P, N):
+    banner(f"mamba2 prologue B={B} L={L} H={H} P={P} N={N}")
+    ins, cots = _m2_inputs(B, L, H, P, N, B + L + H + N)
+    ref_out = op.mamba2_prologue(*ins, H)
+    ref_grads = op.mamba2_prologue_grads(ins, cots, H)
+    gi = [t.cuda() for t in ins]
+    outs = PL.mamba2_forward(*gi, H)
+    grads = PL.mamba2_backward(*gi, H, *(c.cuda() for c in cots))
+    torch.cuda.synchronize()
+    for name, a, b in list(zip(M2_OUT, outs, ref_out)) + list(zip(M2_GRADS, grads, ref_grads)):
+        assert a.dtype == b.dtype and a.shape == b.shape, name
+        e = rel_err(a, b)
+        print(f"  {name}: rel_err {e:.2e}")
+        assert e < TOL_BF16, name
