@@ -81,20 +81,22 @@ __device__ __forceinline__ float dpp_add(float v) {
 // same sum), so the lanes of a head end with identical totals.
 template <int G>
 __device__ __forceinline__ float head_sum(float v) {
-  static_assert(G == 8 || G == 16, "heads of 64 or 128 channels");
+  static_assert(G == 8 || G == 16 || G == 32, "8, 16 or 32 lanes per head");
   v = dpp_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
   v = dpp_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
   v = dpp_add<0x141>(v);  // row_half_mirror
-  if (G == 16) v = dpp_add<0x140>(v);  // row_mirror
+  if (G >= 16) v = dpp_add<0x140>(v);  // row_mirror
+  if (G == 32) v += __shfl_xor(v, 16);  // the neighbouring row
   return v;
 }
 
-// the lane's conv weights (bf16-rounded, [tap][8 channels]) and biases
+// the lane's conv weights (bf16-rounded, [tap][CPL channels]) and biases
+template <int CPL = 8>
 struct ConvW {
-  float w[kDc][8], b[8];
+  float w[kDc][CPL], b[CPL];
   __device__ __forceinline__ void load(const float* __restrict__ cw, const float* __restrict__ cb, int c) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < CPL; ++j) {
       const float4 t = *reinterpret_cast<const float4*>(cw + (size_t)(c + j) * kDc);
       w[0][j] = bfr(t.x); w[1][j] = bfr(t.y); w[2][j] = bfr(t.z); w[3][j] = bfr(t.w);
       b[j] = bfr(cb[c + j]);
@@ -103,10 +105,11 @@ struct ConvW {
 };
 
 // silu(conv + bias) at one token from the window u[t-3..t] (tap order)
-__device__ __forceinline__ void conv_silu(const ConvW& W, const float (&win)[kDc][8], float (&pre)[8],
-                                          float (&s)[8]) {
+template <int CPL>
+__device__ __forceinline__ void conv_silu(const ConvW<CPL>& W, const float (&win)[kDc][CPL], float (&pre)[CPL],
+                                          float (&s)[CPL]) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < CPL; ++j) {
     float acc = 0.f;
 #pragma unroll
     for (int tp = 0; tp < kDc; ++tp) acc += win[tp][j] * W.w[tp][j];
@@ -132,7 +135,7 @@ __global__ __launch_bounds__(256) void prologue_conv_fwd(PlDims dm, const bf16* 
   if (wv >= dm.B * ntile * nblk) return;  // wave-uniform
   const int cb = wv % nblk, tile = (wv / nblk) % ntile, b = wv / (nblk * ntile);
   const int c = cb * 512 + 8 * lane, t0 = tile * kTileF;
-  ConvW W;
+  ConvW<8> W;
   W.load(conv_w, conv_b, c);
   const bf16* u = lin + (size_t)b * dm.L * dm.d + c;
   bf16* o = out + (size_t)b * dm.L * dm.d + c;
@@ -205,30 +208,30 @@ __global__ __launch_bounds__(256) void prologue_gates_fwd(PlDims dm, const bf16*
 // ---------------------------------------------------------------- backward
 // Per token of the reverse sweep: the cotangent of the conv accumulator
 // (e = d(conv + bias)), from the output cotangent dy and the forward values.
-template <int MODE, int G>
-__device__ __forceinline__ void conv_out_vjp(const ConvW& W, const float (&win)[kDc][8], const float (&dy)[8],
-                                             float eps, float (&e)[8]) {
-  float pre[8], s[8], ds[8];
+template <int MODE, int G, int CPL>
+__device__ __forceinline__ void conv_out_vjp(const ConvW<CPL>& W, const float (&win)[kDc][CPL],
+                                             const float (&dy)[CPL], float eps, float (&e)[CPL]) {
+  float pre[CPL], s[CPL], ds[CPL];
   conv_silu(W, win, pre, s);
   if (MODE == kClip50) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < CPL; ++j) {
       const float v = fminf(fmaxf(s[j], -50.f), 50.f);
       ds[j] = bfr(dy[j] * clip_g(v, 1e3f) * clip_g(s[j], 50.f));
     }
   } else if (MODE == kPlain) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ds[j] = bfr(dy[j] * clip_g(s[j], 1e3f));
+    for (int j = 0; j < CPL; ++j) ds[j] = bfr(dy[j] * clip_g(s[j], 1e3f));
   } else {
     float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ss += bfr(s[j] * s[j]);
+    for (int j = 0; j < CPL; ++j) ss += bfr(s[j] * s[j]);
     ss = bfr(head_sum<G>(ss));
     const float r = bfr(rsqrtf(bfr(ss + eps * eps)));
     // output clip (|y| <= 1 passes), then the gradient sanitiser (model.py:206-214)
-    float gy[8], dot = 0.f;
+    float gy[CPL], dot = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < CPL; ++j) {
       const float y = bfr(s[j] * r);
       float g = dy[j] * clip_g(y, 1e3f);
       g = __builtin_isnan(g) ? 0.f : fminf(fmaxf(g, -1e3f), 1e3f);
@@ -238,118 +241,128 @@ __device__ __forceinline__ void conv_out_vjp(const ConvW& W, const float (&win)[
     dot = head_sum<G>(dot);
     const float r3 = r * r * r;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ds[j] = bfr(gy[j] * r - s[j] * r3 * dot);
+    for (int j = 0; j < CPL; ++j) ds[j] = bfr(gy[j] * r - s[j] * r3 * dot);
   }
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < CPL; ++j) {
     const float sg = sigm(pre[j]);
     e[j] = bfr(ds[j] * (sg * (1.f + pre[j] * (1.f - sg))));
   }
 }
 
-// Partial sums of one workgroup (4 waves) combined through LDS and written
-// as one row of NV floats per channel: the row is [d][NV] at `dst`.
-template <int NV>
-__device__ __forceinline__ void combine_partials(float (&v)[NV][8], float* __restrict__ dst, int c) {
-  __shared__ __attribute__((aligned(16))) float red[4][512];
+// 4 bf16 of a row as floats, from a raw 8-byte piece
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void unpack4(const u32x2& r, float (&o)[4]) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    o[2 * i] = __uint_as_float(r[i] << 16);
+    o[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ u32x2 row4_or_zero(const bf16* p, int t, int ld) {
+  const u32x2 v = *reinterpret_cast<const u32x2*>(p + (size_t)(t < 0 ? 0 : t) * ld);
+  const u32x2 z = {0u, 0u};
+  return t < 0 ? z : v;
+}
+__device__ __forceinline__ void store4f(bf16* p, const float (&v)[4]) {
+  bf16x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = (bf16)v[i];
+  *reinterpret_cast<bf16x4*>(p) = o;
+}
+
+// Partial sums of one workgroup (4 waves, 64 CPL channels each) combined
+// through LDS and written as one row of NV floats per channel ([d][NV] at dst).
+template <int NV, int CPL>
+__device__ __forceinline__ void combine_partials(float (&v)[NV][CPL], float* __restrict__ dst, int c) {
+  __shared__ __attribute__((aligned(16))) float red[4][64 * CPL];
   const int w = wave_id(), lane = lane_id();
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
-    store8(&red[w][8 * lane], v[k]);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) red[w][CPL * lane + j] = v[k][j];
     __syncthreads();
     if (w == 0) {
-      float a[8], t[8];
-      load8(&red[0][8 * lane], a);
 #pragma unroll
-      for (int u = 1; u < 4; ++u) {
-        load8(&red[u][8 * lane], t);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) a[j] += t[j];
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) dst[(size_t)(c + j) * NV + k] = a[j];
+      for (int j = 0; j < CPL; ++j)
+        dst[(size_t)(c + j) * NV + k] = red[0][CPL * lane + j] + red[1][CPL * lane + j] +
+                                        red[2][CPL * lane + j] + red[3][CPL * lane + j];
     }
     __syncthreads();
   }
 }
 
-// The four waves of a workgroup take four consecutive tiles of one
-// (batch, channel block); partial row index = (batch, tile group).
+// Four channels per lane (a wave covers 256 channels): half the registers of
+// the 8-channel mapping, so four waves fit per SIMD.  The four waves of a
+// workgroup take four consecutive tiles of one (batch, 256-channel block);
+// partial row index = (batch, tile group).
+constexpr int kCplB = 4;
 template <int MODE, int DH>
-__global__ __launch_bounds__(256) void prologue_conv_bwd(PlDims dm, const bf16* __restrict__ lin,
-                                                         const float* __restrict__ conv_w,
-                                                         const float* __restrict__ conv_b,
-                                                         const bf16* __restrict__ dout,
-                                                         bf16* __restrict__ dlin, float* __restrict__ part) {
-  constexpr int G = DH / 8, NV = kDc + 1;  // partials: the 4 taps, then the bias
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void prologue_conv_bwd(
+    PlDims dm, const bf16* __restrict__ lin, const float* __restrict__ conv_w, const float* __restrict__ conv_b,
+    const bf16* __restrict__ dout, bf16* __restrict__ dlin, float* __restrict__ part) {
+  constexpr int CPL = kCplB, G = DH / CPL, NV = kDc + 1;  // partials: the 4 taps, then the bias
   const int lane = lane_id();
-  const int nblk = dm.d / 512, ngrp = dm.L / (4 * kTileB);
+  const int nblk = dm.d / (64 * CPL), ngrp = dm.L / (4 * kTileB);
   const int cb = blockIdx.x % nblk, grp = (blockIdx.x / nblk) % ngrp, b = blockIdx.x / (nblk * ngrp);
   const int tile = grp * 4 + wave_id();
-  const int c = cb * 512 + 8 * lane, t0 = tile * kTileB;
-  ConvW W;
+  const int c = cb * 64 * CPL + CPL * lane, t0 = tile * kTileB;
+  ConvW<CPL> W;
   W.load(conv_w, conv_b, c);
   const bf16* u = lin + (size_t)b * dm.L * dm.d + c;
   const bf16* dy = dout + (size_t)b * dm.L * dm.d + c;
   bf16* du = dlin + (size_t)b * dm.L * dm.d + c;
-  float acc[NV][8];
+  float acc[NV][CPL];
 #pragma unroll
   for (int k = 0; k < NV; ++k)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[k][j] = 0.f;
+    for (int j = 0; j < CPL; ++j) acc[k][j] = 0.f;
   // reverse sweep from the last halo token: window u[t-3..t] and the conv
   // cotangents e[t+1..t+3] of the tokens above
   const int t_hi = min(t0 + kTileB + kDc - 2, dm.L - 1);
-  float win[kDc][8], en[kDc - 1][8];
+  float win[kDc][CPL], en[kDc - 1][CPL];
 #pragma unroll
-  for (int tp = 0; tp < kDc; ++tp) {
-    const int t = t_hi - (kDc - 1) + tp;
-    if (t >= 0) load8(u + (size_t)t * dm.d, win[tp]);
-    else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) win[tp][j] = 0.f;
-    }
-  }
+  for (int tp = 0; tp < kDc; ++tp) unpack4(row4_or_zero(u, t_hi - (kDc - 1) + tp, dm.d), win[tp]);
 #pragma unroll
   for (int k = 0; k < kDc - 1; ++k)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) en[k][j] = 0.f;
+    for (int j = 0; j < CPL; ++j) en[k][j] = 0.f;
 #pragma unroll 4
   for (int t = t_hi; t >= t0; --t) {
-    float g8[8], e[8];
-    const u32x4 rdy = *reinterpret_cast<const u32x4*>(dy + (size_t)t * dm.d);
-    const u32x4 rnext = row_or_zero(u, t - kDc, dm.d);
-    unpack8(rdy, g8);
-    conv_out_vjp<MODE, G>(W, win, g8, dm.eps, e);
+    float g4[CPL], e[CPL];
+    const u32x2 rdy = *reinterpret_cast<const u32x2*>(dy + (size_t)t * dm.d);
+    const u32x2 rnext = row4_or_zero(u, t - kDc, dm.d);
+    unpack4(rdy, g4);
+    conv_out_vjp<MODE, G, CPL>(W, win, g4, dm.eps, e);
     if (t < t0 + kTileB) {
       // d lin[t] = sum_s e[t + s] w[3 - s]; the parameter sums
-      float o8[8];
+      float o4[CPL];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < CPL; ++j) {
         float v = e[j] * W.w[kDc - 1][j];
 #pragma unroll
-        for (int s = 1; s < kDc; ++s) v += en[s - 1][j] * W.w[kDc - 1 - s][j];
-        o8[j] = v;
+        for (int s2 = 1; s2 < kDc; ++s2) v += en[s2 - 1][j] * W.w[kDc - 1 - s2][j];
+        o4[j] = v;
 #pragma unroll
         for (int tp = 0; tp < kDc; ++tp) acc[tp][j] += e[j] * win[tp][j];
         acc[kDc][j] += e[j];
       }
-      store8(du + (size_t)t * dm.d, o8);
+      store4f(du + (size_t)t * dm.d, o4);
     }
     // slide: e[t] becomes the nearest token above; the window moves down
 #pragma unroll
     for (int k = kDc - 2; k >= 1; --k)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) en[k][j] = en[k - 1][j];
+      for (int j = 0; j < CPL; ++j) en[k][j] = en[k - 1][j];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) en[0][j] = e[j];
+    for (int j = 0; j < CPL; ++j) en[0][j] = e[j];
 #pragma unroll
     for (int tp = kDc - 1; tp >= 1; --tp)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) win[tp][j] = win[tp - 1][j];
-    unpack8(rnext, win[0]);
+      for (int j = 0; j < CPL; ++j) win[tp][j] = win[tp - 1][j];
+    unpack4(rnext, win[0]);
   }
-  combine_partials<NV>(acc, part + ((size_t)b * ngrp + grp) * dm.d * NV, c);
+  combine_partials<NV, CPL>(acc, part + ((size_t)b * ngrp + grp) * dm.d * NV, c);
 }
 
 // b, w, g gradients; per-head partial sums of da
@@ -646,7 +659,7 @@ extern "C" int atomic_gdn2_prologue_bwd(const atomic_gdn2_prologue_args* a, cons
   hipStream_t st = (hipStream_t)stream;
   Launch L{a->profile, st};
   const int ngrp = dm.L / (4 * kTileB);
-  const unsigned nconv = (unsigned)((size_t)dm.B * ngrp * (dm.d / 512));
+  const unsigned nconv = (unsigned)((size_t)dm.B * ngrp * (dm.d / (64 * kCplB)));
   const unsigned ngate = (unsigned)(((size_t)dm.B * (dm.L / kTileB) * (dm.d / 512) + 3) / 4);
   const bf16* lins[3] = {(const bf16*)q_lin, (const bf16*)k_lin, (const bf16*)v_lin};
   const bf16* dys[3] = {(const bf16*)dq, (const bf16*)dk, (const bf16*)dv};
@@ -763,7 +776,7 @@ extern "C" int atomic_mamba2_prologue_bwd(const atomic_mamba2_prologue_args* a, 
   Launch L{a->profile, st};
   const int ngrp = dm.L / (4 * kTileB);
   rc = L("prologue_conv_bwd", [&] {
-    hipLaunchKernelGGL((prologue_conv_bwd<kPlain, 128>), dim3((unsigned)((size_t)dm.B * ngrp * (dm.d / 512))),
+    hipLaunchKernelGGL((prologue_conv_bwd<kPlain, 128>), dim3((unsigned)((size_t)dm.B * ngrp * (dm.d / (64 * kCplB)))),
                        dim3(256), 0, st, dm, (const bf16*)x_bc, conv_w, conv_b, (const bf16*)dx, (bf16*)dx_bc, part);
   });
   if (rc) return rc;
