@@ -143,12 +143,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
   };
+  // Every prefetch is issued on every path (before chunk 0 it re-reads chunk
+  // 0, whose registers are never committed): the wait counter before a
+  // commit then always has the other set's loads behind it, so the commit
+  // waits for its own set only and the two-deep prefetch holds.
   Stage s0, s1;
   prefetch(s0, dm.NT - 1);
   commit(s0);
   __syncthreads();
-  if (dm.NT > 1) prefetch(s0, dm.NT - 2);
-  if (dm.NT > 2) prefetch(s1, dm.NT - 3);
+  prefetch(s0, max(dm.NT - 2, 0));
+  prefetch(s1, max(dm.NT - 3, 0));
 
   // one chunk step (reverse); S holds chunk n - 1 on entry and is refilled with chunk n - 3
   auto chunk_step = [&](int n, Stage& S) {
@@ -207,13 +211,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         store_tile_t(sDht, L::LK, 16 * mi, 16 * ni, hs[t]);
       }
     if (n > 0) commit(S);
-    if (n >= 3) prefetch(S, n - 3);
+    prefetch(S, max(n - 3, 0));
     __syncthreads();
   };
-  for (int n = dm.NT - 1; n >= 0; n -= 2) {
+  // both steps of a pair run on every trip (no path skips the second set's
+  // loads); an odd first chunk runs after the loop
+  int n = dm.NT - 1;
+  for (; n >= 1; n -= 2) {
     chunk_step(n, s0);
-    if (n >= 1) chunk_step(n - 1, s1);
+    chunk_step(n - 1, s1);
   }
+  if (n == 0) chunk_step(0, s0);
   if (dh0) {
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {

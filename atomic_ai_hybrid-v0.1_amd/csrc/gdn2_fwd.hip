@@ -566,12 +566,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     S.u.store(reinterpret_cast<T*>(bp + L::s_u), L::LU);
     S.g.store(reinterpret_cast<float*>(bp + L::s_gl), K);
   };
+  // Every prefetch is issued on every path (past the last chunk it re-reads
+  // chunk NT - 1, whose registers are never committed): the wait counter
+  // before a commit then always has the other set's loads behind it, so the
+  // commit waits for its own set only and the two-deep prefetch holds.
+  const int last = dm.NT - 1;
   Stage s0, s1;
   prefetch(s0, 0);
   commit(s0, 0);
   __syncthreads();
-  if (dm.NT > 1) prefetch(s0, 1);
-  if (dm.NT > 2) prefetch(s1, 2);
+  prefetch(s0, min(1, last));
+  prefetch(s1, min(2, last));
 
   // One chunk step; S holds chunk n + 1 on entry and is refilled with chunk n + 3.
   // Two stage buffers: chunk n + 1 goes into the other buffer at the start (its
@@ -582,7 +587,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     use_buf(L::NBUF == 2 ? (n & 1) : 0);
     if constexpr (L::NBUF == 2) {
       if (n + 1 < dm.NT) commit(S, (n + 1) & 1);
-      if (n + 3 < dm.NT) prefetch(S, n + 3);
+      prefetch(S, min(n + 3, last));
     }
       if (save) unstage_rows<T, VT, K, NTHR>(ck.hT + bhn * V * K + (size_t)v0 * K, K, sHt, L::LK);
 
@@ -672,14 +677,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     if constexpr (L::NBUF == 1) {
       if (n + 1 < dm.NT) commit(S, 0);
-      if (n + 3 < dm.NT) prefetch(S, n + 3);
+      prefetch(S, min(n + 3, last));
     }
     __syncthreads();
   };
-  for (int n = 0; n < dm.NT; n += 2) {
+  // both steps of a pair run on every trip (no path skips the second set's
+  // loads); an odd last chunk runs after the loop
+  int n = 0;
+  for (; n + 1 < dm.NT; n += 2) {
     chunk_step(n, s0);
-    if (n + 1 < dm.NT) chunk_step(n + 1, s1);
+    chunk_step(n + 1, s1);
   }
+  if (n < dm.NT) chunk_step(n, s0);
   if (h_final) {
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {

@@ -341,6 +341,78 @@ def measure_mamba2_prologue(dev, m):
                 ms_fwd_bwd=round(sum(kv["ms_per_launch"] for kv in ks.values()), 4))
 
 
+def measure_configs(dev):
+    """The benchmark's configurations 1-4 at their own shapes (median of 5
+    timed calls each, torch events on the launch stream, inputs resident):
+    tokens/s of what each configuration exercises.  Configuration 0 is the
+    CPU-runnable float32 case (a parity-test case, not timed here).  Runs
+    after, and outside, the timed region of the headline metric."""
+    import statistics as st
+    import torch
+    from atomic_ops import _lib, inputs
+    from atomic_ops import gdn2 as G2
+    from atomic_ops import mamba2 as M2
+
+    def timed(fn, n=5, warm=2):
+        for _ in range(warm):
+            fn()
+        ts = []
+        for _ in range(n):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        return st.median(ts)
+
+    out = {}
+    # configuration 1: Mamba2 forward, B2 T4096 H32 P64 N128 C128
+    mi = inputs.mamba2_inputs(2, 4096, 32, 64, 128, seed=11, device=dev)
+    ma = [mi[n] for n in ("dt", "x", "Bm", "Cm", "A")]
+    mws = torch.empty(M2.workspace_bytes(M2.make_args(ma[0], ma[2], 128)), dtype=torch.uint8, device=dev)
+    ms = timed(lambda: M2.forward(*ma, 128, workspace=mws))
+    out["cfg1_mamba2_fwd"] = dict(shape="B2 T4096 H32 P64 N128 C128 bf16", ms=round(ms, 4),
+                                  tokens_per_s=round(2 * 4096 / (ms / 1e3), 1))
+    del mi, ma, mws
+    # configurations 2 and 3: the headline GDN2 shape, forward and backward separately
+    gi = inputs.gdn2_inputs(4, 8192, 16, 128, 128, seed=12, device=dev, dO=True)
+    ga = [gi[n] for n in ("q", "k", "v", "w", "b", "g")]
+    gws = G2.new_workspace(G2.make_args(ga[0], ga[2], 1.0, flags=_lib.GDN2_SAVE), dev)
+    ms_f = timed(lambda: G2.forward(*ga, 1.0, save=True, workspace=gws))
+    ms_b = timed(lambda: G2.backward(*ga, 1.0, gi["do"], workspace=gws, reuse=True))
+    out["cfg2_gdn2_fwd"] = dict(shape="B4 T8192 H16 K=V=128 C64 bf16", ms=round(ms_f, 4),
+                                tokens_per_s=round(4 * 8192 / (ms_f / 1e3), 1))
+    out["cfg3_gdn2_bwd"] = dict(shape="as cfg2, dO bf16, forward intermediates reused", ms=round(ms_b, 4),
+                                tokens_per_s=round(4 * 8192 / (ms_b / 1e3), 1))
+    del gi, ga, gws
+    # configuration 4: B1 T32768, both paths forward + backward
+    gi = inputs.gdn2_inputs(1, 32768, 16, 128, 128, seed=13, device=dev, dO=True)
+    ga = [gi[n] for n in ("q", "k", "v", "w", "b", "g")]
+    gws = G2.new_workspace(G2.make_args(ga[0], ga[2], 1.0, flags=_lib.GDN2_SAVE), dev)
+    mi = inputs.mamba2_inputs(1, 32768, 64, 64, 128, seed=14, device=dev, dO=True)
+    ma = [mi[n] for n in ("dt", "x", "Bm", "Cm", "A")]
+    mws = torch.empty(M2.workspace_bytes(M2.make_args(ma[0], ma[2], 128)), dtype=torch.uint8, device=dev)
+
+    def gdn2_fb():
+        G2.forward(*ga, 1.0, save=True, workspace=gws)
+        G2.backward(*ga, 1.0, gi["do"], workspace=gws, reuse=True)
+
+    def mamba2_fb():
+        M2.forward(*ma, 128, save=True, workspace=mws)
+        M2.backward(*ma, 128, mi["dy"], workspace=mws, reuse=True)
+
+    def cfg4():
+        gdn2_fb()
+        mamba2_fb()
+    ms4 = timed(cfg4, n=3, warm=1)
+    out["cfg4_hybrid_fwd_bwd"] = dict(shape="B1 T32768; GDN2 H16 K=V=128 C64; Mamba2 H64 P64 N128 C128; bf16",
+                                      ms=round(ms4, 4), tokens_per_s=round(32768 / (ms4 / 1e3), 1),
+                                      gdn2_ms=round(timed(gdn2_fb, n=3, warm=1), 4),
+                                      mamba2_ms=round(timed(mamba2_fb, n=3, warm=1), 4))
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -457,6 +529,7 @@ def main():
     epilogue = measure_epilogue(args, dev, g, m, q, k, v, w, b, gg, dt, x, Bm, Cm, A, scale, g_ws, m_ws)
     prologue = measure_prologue(dev, g)
     prologue_m2 = measure_mamba2_prologue(dev, m)
+    configs = measure_configs(dev)
 
     cpu = None if args.no_cpu else cpu_baseline()
 
@@ -477,6 +550,7 @@ def main():
         "epilogue": epilogue,
         "prologue": prologue,
         "prologue_mamba2": prologue_m2,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
 
