@@ -639,8 +639,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     store8(sQ + r * L::LK + cg * 8, o1);
     store8(sKt + r * L::LK + cg * 8, o2);
     store8(sKB + r * L::LK + cg * 8, o3);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sGc[r * L::LG + cg * 8 + j] = gcr[rr][j];
+    // 16-byte row pieces: the eight threads of a row would put scalar
+    // accesses of a wave on a handful of banks
+    store8(sGc + r * L::LG + cg * 8, gcr[rr]);
   }
   // scale folded into the dAqk operand: Aqk = scale Q~ K~^T
   pqk.store(sDAqk, L::LC);
@@ -699,13 +700,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int j = 0; j < 8; ++j) { qv[j] = rq[rr][j]; kv[j] = rk[rr][j]; bv[j] = rb[rr][j]; }
 #pragma unroll
       for (int j = 0; j < 8; ++j) { dqg[j] = rdqg[rr][j]; dkb[j] = rdkb[rr][j]; dkg[j] = rdkg[rr][j]; }
+      // the row piece's gc, MFMA results and gc_last as 16-byte LDS reads
+      float gc8[8], tq8[8], tk8[8], tb8[8], gl8[8], dgc8[8];
+      load8(sGc + r * L::LG + c8, gc8);
+      load8(sRes + r * L::LG + c8, tq8);
+      load8(sRes + RS3 + r * L::LG + c8, tk8);
+      load8(sRes + 2 * RS3 + r * L::LG + c8, tb8);
+      load8(sGl + c8, gl8);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int d = c8 + j;
-        const float gcv = sGc[r * L::LG + d];
-        const float e = __expf(gcv), ei = __expf(-gcv), eg = __expf(sGl[d] - gcv);
-        const float tq = sRes[r * L::LG + d], tk = sRes[RS3 + r * L::LG + d],
-                    tb = sRes[2 * RS3 + r * L::LG + d];
+        const float gcv = gc8[j];
+        const float e = __expf(gcv), ei = __expf(-gcv), eg = __expf(gl8[j] - gcv);
+        const float tq = tq8[j], tk = tk8[j], tb = tb8[j];
         // B4 (kernel_bwd_b4_intra.py:101-132)
         const float dq4 = sanitize(tq * e);
         const float dk4 = sanitize(tk * ei + tb * bv[j] * e);
@@ -722,8 +728,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         oq[j] = sanitize(dq3 + dq4);
         ok[j] = sanitize(dk3 + dk4);
         ob[j] = sanitize(db3 + db4);
-        sGc[r * L::LG + d] = dgc3 + dgc4;  // each element read (as gc) and written by this thread only
+        dgc8[j] = dgc3 + dgc4;
       }
+      store8(sGc + r * L::LG + c8, dgc8);  // each element read (as gc) and written by this thread only
       const size_t go = base + (size_t)r * rsK + c8;
       store8(dq + go, oq);
       store8(dk + go, ok);
@@ -731,8 +738,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     __syncthreads();  // the MFMA results are dead: column partial sums go to their space
     float* sCol = sRes;  // [NSEG][KH]
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sCol[seg * KH + cg * 8 + j] = csum[j];
+    store8(sCol + seg * KH + cg * 8, csum);
     __syncthreads();
     if (tid < KH) {
       float extra = gr.rlast[blk * K + d0 + tid];
