@@ -250,7 +250,7 @@ struct HgLds {
   static constexpr int off_h = off_vn + V * LC * (int)sizeof(T);
   static constexpr int off_dh = off_h + V * LK * (int)sizeof(T);
   static constexpr int off_red = off_dh + V * LK * (int)sizeof(T);
-  static constexpr int total = off_red + 256 * 4;
+  static constexpr int total = off_red + 512 * 4;  // row-term partials [16][KQ]
 };
 
 template <typename T, typename TD, int C, int K, int V>
@@ -310,8 +310,10 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
   // dqg = scale dO h_pre^T ; dwt = -dv_new h_pre^T ; dkg = v_new dh_next^T, per quarter
   constexpr int NTQ = KQ / 16, TPW = MT * NTQ / 4;
   static_assert((MT * NTQ) % 4 == 0, "tiles must split evenly over 4 waves");
-  constexpr int SPL = 256 / KQ, VS = V / SPL;  // gc_last row term: threads per column, rows each
-  static_assert(VS % 2 == 0, "pairs of rows per thread");
+  // gc_last row term: a thread takes a column pair and every SPL-th row, so
+  // a wave's 4-byte reads cover consecutive rows
+  constexpr int CPQ = KQ / 2, SPL = 256 / CPQ, VS = V / SPL;
+  static_assert(SPL * KQ <= 512 && V % SPL == 0, "row-term partials fit their LDS");
   for (int c0 = 0; c0 < K; c0 += KQ) {
     if (c0 + KQ < K) {
       ph.load(hg + c0 + KQ, K);
@@ -334,14 +336,19 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
     }
     // exp(gc_last) * sum_v dh_next * h_pre   (kernel_bwd_b3_wy_dqkg.py:200-201)
     {
-      const int d = threadIdx.x % KQ, sp = threadIdx.x / KQ;
+      typedef T T2 __attribute__((ext_vector_type(2)));
+      const int sp = threadIdx.x % SPL, d = 2 * (threadIdx.x / SPL);
       float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-      for (int v = sp * VS; v < sp * VS + VS; v += 2) {
-        s0 += to_f(sDh[v * L::LK + d]) * to_f(sH[v * L::LK + d]);
-        s1 += to_f(sDh[(v + 1) * L::LK + d]) * to_f(sH[(v + 1) * L::LK + d]);
+      for (int t = 0; t < VS; ++t) {
+        const int v = sp + SPL * t;
+        const T2 a = *reinterpret_cast<const T2*>(sDh + v * L::LK + d);
+        const T2 c = *reinterpret_cast<const T2*>(sH + v * L::LK + d);
+        s0 += to_f(a[0]) * to_f(c[0]);
+        s1 += to_f(a[1]) * to_f(c[1]);
       }
-      red[threadIdx.x] = s0 + s1;
+      red[sp * KQ + d] = s0;
+      red[sp * KQ + d + 1] = s1;
     }
     __syncthreads();  // quarter done: its h / dh and the partial sums are read
     if (threadIdx.x < KQ) {
