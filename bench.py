@@ -419,6 +419,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the widened rows' and configurations 1-4 timings (counter runs that "
+                         "should hold the headline dispatches only)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run one plain device copy of CALIB_BYTES before the steps (the reference "
                          "dispatch for scaling FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -526,10 +529,12 @@ def main():
     rf["kernel"] = dom
     rf["traffic"] = measured_traffic(dom)
 
-    epilogue = measure_epilogue(args, dev, g, m, q, k, v, w, b, gg, dt, x, Bm, Cm, A, scale, g_ws, m_ws)
-    prologue = measure_prologue(dev, g)
-    prologue_m2 = measure_mamba2_prologue(dev, m)
-    configs = measure_configs(dev)
+    epilogue = prologue = prologue_m2 = configs = None
+    if not args.no_extras:
+        epilogue = measure_epilogue(args, dev, g, m, q, k, v, w, b, gg, dt, x, Bm, Cm, A, scale, g_ws, m_ws)
+        prologue = measure_prologue(dev, g)
+        prologue_m2 = measure_mamba2_prologue(dev, m)
+        configs = measure_configs(dev)
 
     cpu = None if args.no_cpu else cpu_baseline()
 
