@@ -87,7 +87,21 @@ static int gdn2_forward_impl(const Gdn2Plan& p, const void* q, const void* k, co
                        (const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b, g, ck);
   });
   if (rc) return rc;
-  const unsigned nwg = (unsigned)(p.dm.B * p.dm.H * (V / VT));
+  const int bh = p.dm.B * p.dm.H;
+  if constexpr (sizeof(T) == 2 && K == 128) {
+    // Few (batch, head) pairs (long sequences at batch 1): 16-column V tiles
+    // while they still fit one workgroup per CU (256 CUs).  The chunk step is
+    // shorter and twice the workgroups walk the chunks; every tile re-reads
+    // the chunk's w, q, kg, which its XCD's L2 serves.
+    constexpr int VT16 = 16;
+    if (bh * (V / VT16) <= 256) {
+      return L("gdn2_fwd_state", [&] {
+        hipLaunchKernelGGL((gdn2_fwd_state<T, C, K, V, VT16>), dim3((unsigned)(bh * (V / VT16))), dim3(512), 0,
+                           st, p.dm, ck, h0, o, h_final, save);
+      });
+    }
+  }
+  const unsigned nwg = (unsigned)(bh * (V / VT));
   return L("gdn2_fwd_state", [&] {
     hipLaunchKernelGGL((gdn2_fwd_state<T, C, K, V, VT>), dim3(nwg), dim3(512), 0, st, p.dm, ck, h0, o,
                        h_final, save);

@@ -59,6 +59,7 @@ def _check(out, ref, dtype, primal_dtypes):
     (2, 128, 2, 128, BF16, 128 ** -0.5, True, False),
     (1, 128, 2, 64, BF16, 1.0, True, True),
     (1, 64, 2, 128, BF16, 1.0, True, True),           # one chunk: only the state loop's tail step
+    (1, 128, 48, 128, BF16, 1.0, True, True),         # 48 heads: 32-column V tiles in the forward
 ])
 def test_backward_matches_autodiff(B, T, H, K, dtype, scale, with_state, reuse):
     banner(f"gdn2 bwd B{B} T{T} H{H} K{K} {dtype} scale={scale} state={with_state} reuse={reuse}")

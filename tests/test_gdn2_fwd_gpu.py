@@ -35,6 +35,7 @@ def _run(B, T, H, K, dtype, seed, scale=1.0, g_mean=3.0, h0=False, mutate=None):
     (1, 128, 2, 128, F32, 1.0, False),
     (2, 128, 2, 64, BF16, 1.0, False),
     (1, 64, 2, 128, BF16, 1.0, True),        # one chunk: only the state loop's tail step
+    (1, 128, 48, 128, BF16, 1.0, True),      # 48 heads: 32-column V tiles (fewer heads take 16)
 ])
 def test_forward_matches_oracle(B, T, H, K, dtype, scale, h0):
     banner(f"gdn2 fwd B{B} T{T} H{H} K{K} {dtype} scale={scale} h0={h0}")
