@@ -82,8 +82,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int NTH = (K / 16) * NTI;  // dh tiles
   constexpr int TPW = NTH / NW;
   constexpr int NTV = (C / 16) * NTI;  // dv_new tiles
-  constexpr int VPW = NTV / NW;
-  static_assert(NTH % NW == 0 && NTV % NW == 0 && TPW >= 1 && VPW >= 1,
+  // with fewer dv_new tiles than waves (16-column V tiles) the first NTV waves take one each
+  constexpr int VPW = NTV >= NW ? NTV / NW : 1;
+  static_assert(NTH % NW == 0 && (NTV % NW == 0 || NW % NTV == 0) && TPW >= 1,
                 "tiles must split evenly over the waves");
   // tiles of one row block computed together (sharing their A fragments)
   constexpr int GV = VPW < NTI ? VPW : NTI, GT = TPW < NTI ? TPW : NTI;
@@ -162,7 +163,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
       // dv_new = sanitize(Aqk^T dO + kg dh)   (b2:70, b1:30-32)
   #pragma unroll
-      for (int gi = 0; gi < VPW / GV; ++gi) {
+      for (int gi = 0; gi < ((NTV >= NW || wv_id < NTV) ? VPW / GV : 0); ++gi) {
         const int tile0 = wv_id * VPW + gi * GV, mj = tile0 / NTI, ni0 = tile0 % NTI;
         const int k0 = tri_k0<T>(mj);
         f32x4 acc[GV];

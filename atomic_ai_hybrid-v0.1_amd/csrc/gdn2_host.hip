@@ -141,12 +141,24 @@ static int gdn2_backward_impl(const Gdn2Plan& p, const void* q, const void* k, c
     if (rc) return rc;
   }
   hipStream_t st = L.st;
-  const unsigned nseq = (unsigned)(p.dm.B * p.dm.H * (V / VT));
+  const int bh = p.dm.B * p.dm.H;
   const unsigned nblk = (unsigned)p.bhn;
-  rc = L("gdn2_bwd_dh", [&] {
-    hipLaunchKernelGGL((gdn2_bwd_dh<T, TD, C, K, V, VT>), dim3(nseq), dim3(512), 0, st, p.dm, ck, gr,
-                       (const TD*)dO, dh_final, dh0);
-  });
+  // 16-column V tiles under the same condition as the forward state loop
+  bool dh16 = false;
+  if constexpr (sizeof(T) == 2 && K == 128) dh16 = bh * (V / 16) <= 256;
+  if (dh16) {
+    if constexpr (sizeof(T) == 2 && K == 128) {
+      rc = L("gdn2_bwd_dh", [&] {
+        hipLaunchKernelGGL((gdn2_bwd_dh<T, TD, C, K, V, 16>), dim3((unsigned)(bh * (V / 16))), dim3(512), 0, st,
+                           p.dm, ck, gr, (const TD*)dO, dh_final, dh0);
+      });
+    }
+  } else {
+    rc = L("gdn2_bwd_dh", [&] {
+      hipLaunchKernelGGL((gdn2_bwd_dh<T, TD, C, K, V, VT>), dim3((unsigned)(bh * (V / VT))), dim3(512), 0, st,
+                         p.dm, ck, gr, (const TD*)dO, dh_final, dh0);
+    });
+  }
   if (rc) return rc;
   rc = L("gdn2_bwd_hgrad", [&] {
     hipLaunchKernelGGL((gdn2_bwd_hgrad<T, TD, C, K, V>), dim3(nblk), dim3(256), 0, st, p.dm, ck, gr,
