@@ -241,37 +241,42 @@ __global__ __launch_bounds__(256) void mamba2_state_pass(Mamba2Dims dm, Mamba2Ch
     cl[k] = ck.cl[ri];
     if (BWD) sp[k] = *reinterpret_cast<const uint2*>(ck.state_pre + ri * N + s0);
   };
+  // Every load is issued on every path (past the last chunk it re-reads that
+  // chunk, whose registers are never used), and the loop body runs whole
+  // groups of D chunks: the wait before a chunk's use then leaves the other
+  // D - 1 chunks' loads in flight.
+  auto step = [&](int k, int it) {
+    const int n = BWD ? NT - 1 - it : it;
+    const size_t ri = rowi(n);
+    const float c = cl[k];
+    const float dce = __expf(fminf(fmaxf(c, -kClipDecay), 0.f));
+    f32x4 sv = {st.x, st.y, st.z, st.w};
+    store4((BWD ? dstate : ck.state_pre) + ri * N + s0, sv);
+    if (BWD) {
+      const bf16* spv = reinterpret_cast<const bf16*>(&sp[k]);
+      float part = st.x * (float)spv[0] + st.y * (float)spv[1] + st.z * (float)spv[2] +
+                   st.w * (float)spv[3];
+#pragma unroll
+      for (int o = 1; o < TPR; o <<= 1) part += __shfl_xor(part, o);
+      const float msk = (c >= -kClipDecay && c <= 0.f) ? 1.f : 0.f;
+      if (c4 == 0) lasta[ri] = part * dce * msk;
+    }
+    st.x = sanitize(st.x * dce + src[k].x);
+    st.y = sanitize(st.y * dce + src[k].y);
+    st.z = sanitize(st.z * dce + src[k].z);
+    st.w = sanitize(st.w * dce + src[k].w);
+    load(k, min(it + D, NT - 1));
+  };
+#pragma unroll
+  for (int k = 0; k < D; ++k) load(k, min(k, NT - 1));
+  int it0 = 0;
+  for (; it0 + D <= NT; it0 += D) {
+#pragma unroll
+    for (int k = 0; k < D; ++k) step(k, it0 + k);
+  }
 #pragma unroll
   for (int k = 0; k < D; ++k)
-    if (k < NT) load(k, k);
-  for (int it0 = 0; it0 < NT; it0 += D) {
-#pragma unroll
-    for (int k = 0; k < D; ++k) {
-      const int it = it0 + k;
-      if (it < NT) {
-        const int n = BWD ? NT - 1 - it : it;
-        const size_t ri = rowi(n);
-        const float c = cl[k];
-        const float dce = __expf(fminf(fmaxf(c, -kClipDecay), 0.f));
-        f32x4 sv = {st.x, st.y, st.z, st.w};
-        store4((BWD ? dstate : ck.state_pre) + ri * N + s0, sv);
-        if (BWD) {
-          const bf16* spv = reinterpret_cast<const bf16*>(&sp[k]);
-          float part = st.x * (float)spv[0] + st.y * (float)spv[1] + st.z * (float)spv[2] +
-                       st.w * (float)spv[3];
-#pragma unroll
-          for (int o = 1; o < TPR; o <<= 1) part += __shfl_xor(part, o);
-          const float msk = (c >= -kClipDecay && c <= 0.f) ? 1.f : 0.f;
-          if (c4 == 0) lasta[ri] = part * dce * msk;
-        }
-        st.x = sanitize(st.x * dce + src[k].x);
-        st.y = sanitize(st.y * dce + src[k].y);
-        st.z = sanitize(st.z * dce + src[k].z);
-        st.w = sanitize(st.w * dce + src[k].w);
-        if (it + D < NT) load(k, it + D);
-      }
-    }
-  }
+    if (it0 + k < NT) step(k, it0 + k);
   if (fin) {
     if (BWD) {  // :264 and the final clip
       st.x = sanitize(st.x); st.y = sanitize(st.y); st.z = sanitize(st.z); st.w = sanitize(st.w);
