@@ -30,10 +30,12 @@ class _Mamba2Core(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy, dstate_final):
         dt, x, B, C, A, state0 = ctx.saved_tensors
+        # The first backward reuses the forward's per-chunk states and releases
+        # them; a further backward (retain_graph) recomputes them.
+        ws, ctx.ws = ctx.ws, None
         ddt, dx, dB, dC, dA, dstate0 = _m.backward(dt, x, B, C, A, ctx.chunk_size, dy,
                                                    dstate_final=dstate_final, state0=state0,
-                                                   workspace=ctx.ws, reuse=True)
-        ctx.ws = None
+                                                   workspace=ws, reuse=ws is not None)
         return ddt, dx, dB, dC, dA.to(A.dtype), None, dstate0.to(state0.dtype)
 
 

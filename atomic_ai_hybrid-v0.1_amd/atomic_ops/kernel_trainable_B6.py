@@ -30,9 +30,12 @@ class _Gdn2Core(torch.autograd.Function):
     @staticmethod
     def backward(ctx, do, dh_final):
         q, k, v, w, b, g, h0 = ctx.saved_tensors
+        # The first backward reuses the forward's intermediates and releases
+        # them; a further backward (retain_graph) recomputes the forward into
+        # a fresh workspace instead of reading one that holds nothing.
+        ws, ctx.ws = ctx.ws, None
         grads = _g.backward(q, k, v, w, b, g, ctx.scale, do, dh_final=dh_final, h0=h0,
-                            workspace=ctx.ws, reuse=True)
-        ctx.ws = None
+                            workspace=ws, reuse=ws is not None)
         dq, dk, dv, dw, db, dg, dh0 = grads
         return dq, dk, dv, dw, db, dg, None, dh0.to(h0.dtype)
 

@@ -262,6 +262,11 @@ static int ng_check(const atomic_norm_gate_args* a) {
   if (!a) return ATOMIC_ERR_NULL;
   if (a->variant != ATOMIC_NORM_GATE_GDN2 && a->variant != ATOMIC_NORM_GATE_MAMBA2) return ATOMIC_ERR_SHAPE;
   if (a->rows <= 0 || a->dim <= 0 || a->dim % 512 != 0 || a->dim > 8192) return ATOMIC_ERR_SHAPE;
+  // the instantiated row widths (ng_dispatch): 512 x {1, 2, 3, 4, 6, 8, 12, 16}
+  switch (a->dim / 512) {
+    case 1: case 2: case 3: case 4: case 6: case 8: case 12: case 16: break;
+    default: return ATOMIC_ERR_SHAPE;
+  }
   if (!(a->eps >= 0.f)) return ATOMIC_ERR_SHAPE;
   return ATOMIC_OK;
 }

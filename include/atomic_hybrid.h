@@ -200,7 +200,7 @@ enum { ATOMIC_NORM_GATE_GDN2 = 0, ATOMIC_NORM_GATE_MAMBA2 = 1 };
 
 typedef struct atomic_norm_gate_args {
   int32_t rows;      /* B * T                                                   */
-  int32_t dim;       /* d (H * V, or H * P): a multiple of 512, at most 8192    */
+  int32_t dim;       /* d (H * V, or H * P): 512 x {1,2,3,4,6,8,12,16}          */
   int32_t variant;   /* ATOMIC_NORM_GATE_*                                      */
   float eps;         /* 1e-6 in both blocks                                     */
   atomic_profile* profile;  /* optional per-kernel event timing, or NULL      */

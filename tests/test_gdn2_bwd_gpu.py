@@ -76,13 +76,70 @@ def test_backward_fp32_upstream_gradient():
     _check(out, ref, BF16, (BF16,) * 5 + (F32, F32))
 
 
-def test_backward_exact_pairwise_path():
+@pytest.mark.parametrize("case,dtype,K", [
+    ("deep_decay", F32, 64), ("deep_decay", BF16, 128), ("deep_decay_upper_columns", BF16, 128),
+    ("positive_gate", BF16, 128),
+])
+def test_backward_exact_pairwise_path(case, dtype, K):
     """A chunk whose decay exceeds the factorisation bound takes the exact
-    pairwise intra backward (with the reference's clip masks)."""
-    banner("gdn2 bwd exact path")
+    pairwise intra backward (with the reference's clip masks).  The intra
+    backward decides per 64-column slice: in the upper-columns case chunk 1
+    mixes a factorised slice (columns 0..63) with an exact one (64..127)."""
+    banner(f"gdn2 bwd exact path {case} {dtype} K{K}")
 
     def mutate(inp):
-        inp["g"][:, 64:128] *= 40.0
-    args, ref = _case(1, 192, 2, 64, F32, seed=21, mutate=mutate)
+        g = inp["g"]
+        if case == "deep_decay":
+            g[:, 64:128] *= 40.0
+        elif case == "positive_gate":
+            g[:, 70:74] = 0.4
+        else:
+            g[:, 64:128, :, 64:] *= 40.0
+    args, ref = _case(1, 192, 2, K, dtype, seed=21, mutate=mutate)
     out = _gpu(args, 1.0, reuse=False)
-    _check(out, ref, F32, (F32,) * 5 + (F32, F32))
+    _check(out, ref, dtype, (dtype,) * 5 + (F32, F32))
+
+
+@pytest.mark.parametrize("h0_given,use_h_final", [(False, False), (True, True)])
+def test_trainable_wrapper_autograd(h0_given, use_h_final):
+    """gdn2_pallas_forward_trainable (kernel_trainable_B6.py:187-194) through
+    torch.autograd: primal dtypes kept on every gradient, equal to the direct
+    forward / backward calls, within tolerance of the oracle; a second
+    backward through the retained graph (which recomputes the forward's
+    intermediates) gives the same gradients."""
+    from atomic_ops.kernel_trainable_B6 import gdn2_pallas_forward_trainable
+    B, T, H, K = 1, 192, 2, 128
+    banner(f"gdn2 trainable wrapper h0={h0_given} h_final used={use_h_final}")
+    inp = inputs.gdn2_inputs(B, T, H, K, K, seed=31, dtype=BF16, dO=True)
+    gen = torch.Generator().manual_seed(32)
+    h0 = 0.3 * torch.randn(B, H, K, K, generator=gen) if h0_given else None
+    dh = torch.randn(B, H, K, K, generator=gen) if use_h_final else None
+    names = ("q", "k", "v", "w", "b", "g")
+    dev = {n: inp[n].cuda() for n in names + ("do",)}
+    leaves = [dev[n].clone().requires_grad_(True) for n in names]
+    h0l = h0.cuda().requires_grad_(True) if h0_given else None
+    o, hf = gdn2_pallas_forward_trainable(*leaves, 1.0, h0l)
+    assert o.dtype == torch.float32 and hf.dtype == torch.float32
+    loss = (o * dev["do"].float()).sum()
+    if use_h_final:
+        loss = loss + (hf * dh.cuda()).sum()
+    loss.backward(retain_graph=True)
+    wrt = leaves + ([h0l] if h0_given else [])
+    first = [t.grad.clone() for t in wrt]
+    for t in wrt:
+        assert t.grad.dtype == t.dtype
+    direct = G.backward(*(dev[n] for n in names), 1.0, dev["do"].float(),
+                        dh_final=dh.cuda() if use_h_final else None,
+                        h0=h0.cuda() if h0_given else None)
+    for got, want in zip(first, direct[:6] + (direct[6],) if h0_given else direct[:6]):
+        assert torch.equal(got, want) or rel_err(got, want) < 1e-6
+    ref = og.gdn2_backward_autodiff(*(inp[n] for n in names), 1.0, 64, inp["do"], dh, h0=h0)
+    errs = {n: rel_err(g_, r) for n, g_, r in zip(NAMES, first, ref)}
+    print("  rel_err " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+    for n, e in errs.items():
+        assert e < tol_for(BF16), (n, e)
+    for t in wrt:
+        t.grad = None
+    loss.backward()
+    for t, want in zip(wrt, first):
+        assert torch.equal(t.grad, want) or rel_err(t.grad, want) < 1e-6

@@ -71,23 +71,30 @@ def test_chunk_intermediates_match_oracle(dtype, K):
         assert e < tol, (n, "v_new", e)
 
 
-@pytest.mark.parametrize("case", ["positive_gate", "deep_decay"])
-def test_exact_pairwise_path(case):
+@pytest.mark.parametrize("case,dtype,K", [
+    ("positive_gate", F32, 64), ("deep_decay", F32, 64),
+    ("positive_gate", BF16, 128), ("deep_decay", BF16, 128),
+    ("deep_decay_upper_columns", BF16, 128),
+])
+def test_exact_pairwise_path(case, dtype, K):
     """Chunks where the factorised scores could overflow (or a gate is
     positive) take the exact pairwise path; results still match the oracle,
-    including the reference's +-20 clip on the pairwise decay."""
-    banner(f"gdn2 exact path {case}")
+    including the reference's +-20 clip on the pairwise decay.  In the last
+    case only columns 64..127 of chunk 1 decay past the bound."""
+    banner(f"gdn2 exact path {case} {dtype} K{K}")
 
     def mutate(inp):
         g = inp["g"]
         if case == "positive_gate":
             g[:, 5:9] = 0.4           # breaks monotone decay in chunk 0
-        else:
+        elif case == "deep_decay":
             g[:, 64:128] *= 40.0      # ~-2 per step: chunk 1 decays past -64
-    _, (o, hf, _), (o_ref, h_ref) = _run(1, 192, 2, 64, F32, seed=11, mutate=mutate)
+        else:
+            g[:, 64:128, :, 64:] *= 40.0
+    _, (o, hf, _), (o_ref, h_ref) = _run(1, 192, 2, K, dtype, seed=11, mutate=mutate)
     eo, eh = rel_err(o, o_ref), rel_err(hf, h_ref)
     print(f"  rel_err o={eo:.3e} h_final={eh:.3e}")
-    assert eo < 1e-4 and eh < 1e-4
+    assert eo < tol_for(dtype) and eh < tol_for(dtype)
 
 
 def test_rejects_bad_shapes():

@@ -108,3 +108,24 @@ def test_backward_positive_step_exponent_takes_exact_path():
     for h in (0, 2):
         assert abs(dA[h] - dA_ref[h]) < tol_for(BF16) * dA_ref.abs().max(), h
     assert abs(dA[1] - dA_ref[1]) < 0.05 * abs(dA_ref[1])
+
+
+def test_trainable_wrapper_second_backward_recomputes():
+    """A second backward through a retained graph no longer holds the
+    forward's saved states; it recomputes them and gives the same
+    gradients (state0 given and differentiated)."""
+    from atomic_ops.kernel_mamba2_trainable_B6 import mamba2_pallas_forward_trainable_B6
+    banner("mamba2 trainable wrapper, backward twice")
+    inp = inputs.mamba2_inputs(1, 256, 2, 64, 128, seed=6, device="cuda", dO=True)
+    leaves = [inp[n].clone().requires_grad_(True) for n in ("dt", "x", "Bm", "Cm", "A")]
+    s0 = (0.3 * torch.randn(1, 2, 64, 128, device="cuda")).requires_grad_(True)
+    y, s = mamba2_pallas_forward_trainable_B6(*leaves, 128, s0)
+    loss = (y * inp["dy"].float()).sum() + s.square().sum()
+    loss.backward(retain_graph=True)
+    first = [t.grad.clone() for t in leaves + [s0]]
+    for t in leaves + [s0]:
+        t.grad = None
+    loss.backward()
+    for t, want in zip(leaves + [s0], first):
+        assert t.grad.dtype == t.dtype
+        assert torch.equal(t.grad, want) or rel_err(t.grad, want) < 1e-6
