@@ -20,6 +20,8 @@ ERRORS = {
     -3: "ATOMIC_ERR_WORKSPACE: workspace missing or too small",
     -4: "ATOMIC_ERR_LAUNCH: kernel launch failed",
     -5: "ATOMIC_ERR_NULL: required pointer is NULL",
+    -6: "ATOMIC_ERR_SCRATCH: does not fit the no-allocation entry point's fixed scratch "
+        "(or asks it to keep intermediates)",
 }
 ATOMIC_F32, ATOMIC_BF16 = 0, 1
 GDN2_SAVE, GDN2_REUSE = 1, 2
@@ -114,6 +116,7 @@ _SIGS = {
     "atomic_gdn2_workspace_layout": (ctypes.c_int, [ctypes.POINTER(Gdn2Args), ctypes.POINTER(Gdn2Layout)]),
     "atomic_gdn2_fwd": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 9 + [_P, ctypes.c_size_t, _P]),
     "atomic_gdn2_bwd": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 16 + [_P, ctypes.c_size_t, _P]),
+    "atomic_gdn2_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 9 + [_P]),
     "atomic_mamba2_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(Mamba2Args)]),
     "atomic_mamba2_fwd": (ctypes.c_int, [ctypes.POINTER(Mamba2Args)] + [_P] * 8 + [_P, ctypes.c_size_t, _P]),
     "atomic_mamba2_bwd": (ctypes.c_int, [ctypes.POINTER(Mamba2Args)] + [_P] * 14 + [_P, ctypes.c_size_t, _P]),

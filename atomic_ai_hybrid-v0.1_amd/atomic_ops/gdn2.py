@@ -95,6 +95,31 @@ def forward(q, k, v, w, b, g, scale, h0=None, *, save=False, workspace=None, chu
     return o, h_final, workspace
 
 
+def forward_noalloc(q, k, v, w, b, g, scale, h0=None, *, o=None, h_final=None, chunk=CHUNK,
+                    timer=None):
+    """The forward through ``atomic_gdn2_fwd_noalloc``: no workspace, the
+    library's fixed device scratch instead.  ``o`` / ``h_final`` may be
+    given (preallocated outputs).  Returns ``(o, h_final)``."""
+    _check_inputs(q, k, v, w, b, g)
+    lib = _lib.load()
+    q, k, v, w, b, g = (t.contiguous() for t in (q, k, v, w, b, g))
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    args = make_args(q, v, scale, chunk=chunk)
+    if timer is not None:
+        args.profile = timer.arm()
+    if h0 is not None:
+        h0 = h0.to(torch.float32).contiguous()
+    if o is None:
+        o = torch.empty(B, T, H, V, dtype=torch.float32, device=q.device)
+    if h_final is None:
+        h_final = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
+    rc = lib.atomic_gdn2_fwd_noalloc(ctypes.byref(args), _ptr(q), _ptr(k), _ptr(v), _ptr(w), _ptr(b),
+                                     _ptr(g), _ptr(h0), _ptr(o), _ptr(h_final), _stream(q.device))
+    _lib.check(rc, "atomic_gdn2_fwd_noalloc")
+    return o, h_final
+
+
 def backward(q, k, v, w, b, g, scale, dO, dh_final=None, h0=None, *, workspace=None, reuse=False,
              chunk=CHUNK, timer=None):
     """Gradients ``(dq, dk, dv, dw, db, dg, dh0)`` in the primals' dtypes

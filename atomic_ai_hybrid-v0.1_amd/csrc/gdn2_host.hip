@@ -1,5 +1,7 @@
 // Host side of the GDN2 chunk pipeline: argument checks, workspace layout,
 // template dispatch and the extern "C" entry points of include/atomic_hybrid.h.
+#include <mutex>
+
 #include "../../include/atomic_hybrid.h"
 #include "gdn2_bwd.hip"
 #include "launch.hpp"
@@ -208,6 +210,108 @@ int gdn2_forward(const Gdn2Plan& p, int dtype, const void* q, const void* k, con
   return gdn2_forward_impl<float, 64>(p, q, k, v, w, b, g, h0, o, h_final, ws, save, L);
 }
 
+// ------------------------------------------------ no-allocation forward
+// atomic_gdn2_fwd_noalloc runs the forward kernels out of a file-scope device
+// array instead of a caller workspace.  Each device the library runs on holds
+// its own copy of the array (64 MiB) from module load until the process ends.
+// In host code the array's name is only a host-side stand-in: its device
+// address is looked up once per device (hipGetSymbolAddress, with that device
+// current) and only that address reaches the kernels.
+constexpr size_t kNoallocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+constexpr int kNoallocMaxDevices = 64;
+static std::mutex g_noalloc_mu;
+static void* g_noalloc_ptr[kNoallocMaxDevices];
+
+// Device address of `scratch` on the current device (looked up on the first
+// call on that device).
+static int noalloc_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNoallocMaxDevices) return ATOMIC_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr)
+      return ATOMIC_ERR_LAUNCH;
+    g_noalloc_ptr[dev] = ptr;
+  }
+  *out = g_noalloc_ptr[dev];
+  return ATOMIC_OK;
+}
+
+// Plan of one window: batch 1, `nw` chunks, the call's heads and head dims.
+static int gdn2_window_plan(const atomic_gdn2_args* a, int nw, Gdn2Plan* p) {
+  atomic_gdn2_args w = *a;
+  w.batch = 1;
+  w.seqlen = nw * a->chunk;
+  w.flags = 0;
+  return gdn2_plan(&w, p);
+}
+
+// The forward processes one batch row and a window of chunks at a time: the
+// window's per-chunk intermediates fill the scratch after two fp32 state
+// slots [H][K][V]; the state leaving a window goes to a slot (alternating,
+// so a launch never reads the slot it writes) and enters the next window as
+// its h0.  The last window of each batch row writes h_final.  Nothing in the
+// scratch is read before the same call writes it.
+static int gdn2_forward_noalloc(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
+                                const void* w, const void* b, const float* g, const float* h0, float* o,
+                                float* h_final, hipStream_t st) {
+  const int NT = a->seqlen / a->chunk, H = a->heads, K = a->dk, V = a->dv;
+  const size_t es = a->dtype == ATOMIC_BF16 ? 2 : 4;
+  const size_t state_elems = (size_t)H * K * V;
+  const size_t slot = align256(state_elems * 4);
+  if (2 * slot >= kNoallocScratchBytes) return ATOMIC_ERR_SCRATCH;
+  const size_t room = kNoallocScratchBytes - 2 * slot;
+  // largest window whose intermediates (the blocks before the saved-state
+  // ones, which a forward without ATOMIC_GDN2_SAVE never touches) fit
+  Gdn2Plan p1;
+  int rc = gdn2_window_plan(a, 1, &p1);
+  if (rc) return rc;
+  if (p1.o_ht > room) return ATOMIC_ERR_SCRATCH;
+  int W = (int)(room / p1.o_ht);
+  if (W > NT) W = NT;
+  Gdn2Plan pfull, ptail;  // full windows, and the shorter last window of a row
+  for (;; --W) {
+    rc = gdn2_window_plan(a, W, &pfull);
+    if (rc) return rc;
+    if (pfull.o_ht <= room) break;
+  }
+  const int tail = NT % W;
+  if (tail) {
+    rc = gdn2_window_plan(a, tail, &ptail);
+    if (rc) return rc;
+  }
+  void* base = nullptr;
+  rc = noalloc_scratch(&base);
+  if (rc) return rc;
+  float* slots[2] = {reinterpret_cast<float*>(base),
+                     reinterpret_cast<float*>(static_cast<char*>(base) + slot)};
+  void* ws = static_cast<char*>(base) + 2 * slot;
+  Launch L{a->profile, st};
+  const size_t T = (size_t)a->seqlen, rowK = (size_t)H * K, rowV = (size_t)H * V;
+  for (int bb = 0; bb < a->batch; ++bb) {
+    const float* hin = h0 ? h0 + (size_t)bb * state_elems : nullptr;
+    int wi = 0;
+    for (int n0 = 0; n0 < NT; n0 += W, ++wi) {
+      const int nw = NT - n0 < W ? NT - n0 : W;
+      const Gdn2Plan& pw = nw == W ? pfull : ptail;
+      const size_t t0 = (size_t)bb * T + (size_t)n0 * a->chunk;  // first row of the window
+      const char* qp = static_cast<const char*>(q) + t0 * rowK * es;
+      const char* kp = static_cast<const char*>(k) + t0 * rowK * es;
+      const char* bp = static_cast<const char*>(b) + t0 * rowK * es;
+      const char* vp = static_cast<const char*>(v) + t0 * rowV * es;
+      const char* wp = static_cast<const char*>(w) + t0 * rowV * es;
+      float* hout = n0 + nw == NT ? h_final + (size_t)bb * state_elems : slots[wi & 1];
+      rc = gdn2_forward(pw, a->dtype, qp, kp, vp, wp, bp, g + t0 * rowK, hin, o + t0 * rowV, hout, ws, 0, L);
+      if (rc) return rc;
+      hin = hout;
+    }
+  }
+  return ATOMIC_OK;
+}
+
 }  // namespace ah
 
 using namespace ah;
@@ -258,4 +362,16 @@ extern "C" int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const v
   Launch L{a->profile, (hipStream_t)stream};
   return gdn2_backward(p, a->dtype, a->do_dtype, q, k, v, w, b, g, h0, dO, dh_final, dq, dk, dv, dw,
                        db, dg, dh0, workspace, (a->flags & ATOMIC_GDN2_REUSE) != 0, L);
+}
+
+extern "C" int atomic_gdn2_fwd_noalloc(const atomic_gdn2_args* a, const void* q, const void* k,
+                                       const void* v, const void* w, const void* b, const float* g,
+                                       const float* h0, float* o, float* h_final, void* stream) {
+  Gdn2Plan p;
+  const int rc = gdn2_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  // the shared scratch cannot keep intermediates for a later backward
+  if (a->flags & (ATOMIC_GDN2_SAVE | ATOMIC_GDN2_REUSE)) return ATOMIC_ERR_SCRATCH;
+  if (!q || !k || !v || !w || !b || !g || !o || !h_final) return ATOMIC_ERR_NULL;
+  return gdn2_forward_noalloc(a, q, k, v, w, b, g, h0, o, h_final, (hipStream_t)stream);
 }

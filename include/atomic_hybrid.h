@@ -32,7 +32,10 @@ enum {
   ATOMIC_ERR_DTYPE = -2,      /* unsupported dtype code                       */
   ATOMIC_ERR_WORKSPACE = -3,  /* workspace NULL or smaller than required      */
   ATOMIC_ERR_LAUNCH = -4,     /* a kernel launch failed                       */
-  ATOMIC_ERR_NULL = -5        /* a required pointer is NULL                   */
+  ATOMIC_ERR_NULL = -5,       /* a required pointer is NULL                   */
+  ATOMIC_ERR_SCRATCH = -6     /* a no-allocation entry point: the shape does not
+                                 fit its fixed scratch, or the flags ask for
+                                 intermediates to outlive the call            */
 };
 
 enum { ATOMIC_F32 = 0, ATOMIC_BF16 = 1 };
@@ -123,6 +126,27 @@ int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const void* k, con
                     const void* dO, const float* dh_final, void* dq, void* dk, void* dv,
                     void* dw, void* db, float* dg, float* dh0, void* workspace,
                     size_t workspace_bytes, void* stream);
+
+/*
+ * GDN2 forward that allocates nothing and takes no workspace.  It has no
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Arguments and results are those of
+ * atomic_gdn2_fwd without the workspace; `a->flags` must be 0.
+ * Scratch: a 64 MiB device array inside the library, one per device, held
+ * from the library's first use on that device until the process ends.  The
+ * call runs one batch row and a window of chunks at a time out of it, so any
+ * batch and sequence length fit; it returns ATOMIC_ERR_SCRATCH when a single
+ * chunk of all heads, with two fp32 states of all heads, does not fit (about
+ * 310 heads at K = V = 128 in bf16).
+ * Every call on a device shares that device's array: calls that overlap on
+ * one device (concurrent streams or host threads) race and must be
+ * serialised by the caller.  Nothing in it needs clearing: each call writes
+ * what it reads.  The current device must be the one `stream` belongs to.
+ */
+int atomic_gdn2_fwd_noalloc(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
+                            const void* w, const void* b, const float* g, const float* h0, float* o,
+                            float* h_final, void* stream);
 
 /* ---------------------------------------------------------------- Mamba2 */
 
