@@ -31,7 +31,7 @@ class Gdn2Args(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int32), ("seqlen", ctypes.c_int32), ("heads", ctypes.c_int32),
                 ("dk", ctypes.c_int32), ("dv", ctypes.c_int32), ("chunk", ctypes.c_int32),
                 ("dtype", ctypes.c_int32), ("do_dtype", ctypes.c_int32), ("scale", ctypes.c_float),
-                ("flags", ctypes.c_int32), ("profile", ctypes.c_void_p)]
+                ("flags", ctypes.c_int32), ("profile", ctypes.c_void_p), ("diag", ctypes.c_void_p)]
 
 
 class Gdn2Layout(ctypes.Structure):
@@ -43,7 +43,7 @@ class Mamba2Args(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int32), ("seqlen", ctypes.c_int32), ("heads", ctypes.c_int32),
                 ("headdim", ctypes.c_int32), ("dstate", ctypes.c_int32), ("chunk", ctypes.c_int32),
                 ("dtype", ctypes.c_int32), ("dy_dtype", ctypes.c_int32), ("flags", ctypes.c_int32),
-                ("profile", ctypes.c_void_p)]
+                ("profile", ctypes.c_void_p), ("diag", ctypes.c_void_p)]
 
 
 class NormGateArgs(ctypes.Structure):
@@ -108,6 +108,56 @@ class KernelTimer:
 
 class AtomicError(RuntimeError):
     pass
+
+
+# Stage names of the args structs' `diag` reports, in the header's order
+# (ATOMIC_GDN2_DIAG_* / ATOMIC_MAMBA2_DIAG_*), with the reference's tags for
+# the GDN2 forward stages (kernel_d_pipeline.py:177-187,121-123).
+GDN2_DIAG_STAGES = ("kernel_A_Aqk", "kernel_A_Akk", "kernel_B_wy_inverse_A", "kernel_C_w_pseudo",
+                    "kernel_C_u", "kernel_C_kg", "kernel_C_qg", "kernel_D_o", "kernel_D_h_final",
+                    "bwd_dv_new", "bwd_dh", "bwd_dAqk", "bwd_dAkk", "dq", "dk", "dv", "dw", "db", "dg",
+                    "dh0")
+GDN2_DIAG_FWD = 9
+MAMBA2_DIAG_STAGES = ("cb", "chunk_states", "ssm_out", "state_final", "bwd_dstates", "ddt", "dx", "dB",
+                      "dC", "dA", "dstate0")
+MAMBA2_DIAG_FWD = 4
+DIAG_LARGE = 1e6   # the reference's "suspiciously large but still finite" level
+
+
+class StageReports:
+    """Device buffer of ``atomic_stage_report`` entries (uint32 n_nonfinite,
+    float max_abs) for an args struct's ``diag`` field."""
+
+    def __init__(self, stages, device):
+        import torch
+        self.stages = stages
+        self.buf = torch.zeros(len(stages), 2, dtype=torch.int32, device=device)
+
+    @property
+    def ptr(self):
+        return ctypes.c_void_p(self.buf.data_ptr())
+
+    def read(self, first=0, count=None):
+        """``{stage: (n_nonfinite, max_abs)}`` for stages [first, first+count)
+        (synchronises with the device)."""
+        import torch
+        host = self.buf.cpu()
+        n = host[:, 0].tolist()
+        mx = host[:, 1].view(torch.float32).tolist()
+        end = len(self.stages) if count is None else first + count
+        return {self.stages[i]: (n[i], mx[i]) for i in range(first, end)}
+
+    def messages(self, tag, first=0, count=None):
+        """The reference's report lines: a stage with non-finite entries, or
+        finite but above 1e6 (kernel_d_pipeline.py:58-91)."""
+        out = []
+        for name, (bad, mx) in self.read(first, count).items():
+            if bad:
+                out.append(f"[GDN2-FWD-DIAG] non-finite at {tag}:{name}: n_nonfinite={bad} "
+                           f"max_abs(finite part)={mx:.3e}")
+            elif mx > DIAG_LARGE:
+                out.append(f"[GDN2-FWD-DIAG] suspiciously large at {tag}:{name}: max_abs={mx:.3e}")
+        return out
 
 
 _P = ctypes.c_void_p

@@ -71,9 +71,12 @@ def workspace_layout(args):
     return lay
 
 
-def forward(q, k, v, w, b, g, scale, h0=None, *, save=False, workspace=None, chunk=CHUNK, timer=None):
+def forward(q, k, v, w, b, g, scale, h0=None, *, save=False, workspace=None, chunk=CHUNK, timer=None,
+            diag=None):
     """Returns ``(o, h_final, workspace)``.  With ``save`` the workspace keeps
-    the per-chunk intermediates for :func:`backward`."""
+    the per-chunk intermediates for :func:`backward`.  ``diag`` (an
+    ``_lib.StageReports`` over ``_lib.GDN2_DIAG_STAGES``) receives the
+    forward's per-stage reports."""
     _check_inputs(q, k, v, w, b, g)
     lib = _lib.load()
     q, k, v, w, b, g = (t.contiguous() for t in (q, k, v, w, b, g))
@@ -82,6 +85,8 @@ def forward(q, k, v, w, b, g, scale, h0=None, *, save=False, workspace=None, chu
     args = make_args(q, v, scale, flags=_lib.GDN2_SAVE if save else 0, chunk=chunk)
     if timer is not None:
         args.profile = timer.arm()
+    if diag is not None:
+        args.diag = diag.ptr
     if workspace is None:
         workspace = new_workspace(args, q.device)
     if h0 is not None:
@@ -96,7 +101,7 @@ def forward(q, k, v, w, b, g, scale, h0=None, *, save=False, workspace=None, chu
 
 
 def forward_noalloc(q, k, v, w, b, g, scale, h0=None, *, o=None, h_final=None, chunk=CHUNK,
-                    timer=None):
+                    timer=None, diag=None):
     """The forward through ``atomic_gdn2_fwd_noalloc``: no workspace, the
     library's fixed device scratch instead.  ``o`` / ``h_final`` may be
     given (preallocated outputs).  Returns ``(o, h_final)``."""
@@ -108,6 +113,8 @@ def forward_noalloc(q, k, v, w, b, g, scale, h0=None, *, o=None, h_final=None, c
     args = make_args(q, v, scale, chunk=chunk)
     if timer is not None:
         args.profile = timer.arm()
+    if diag is not None:
+        args.diag = diag.ptr
     if h0 is not None:
         h0 = h0.to(torch.float32).contiguous()
     if o is None:
@@ -121,7 +128,7 @@ def forward_noalloc(q, k, v, w, b, g, scale, h0=None, *, o=None, h_final=None, c
 
 
 def backward(q, k, v, w, b, g, scale, dO, dh_final=None, h0=None, *, workspace=None, reuse=False,
-             chunk=CHUNK, timer=None):
+             chunk=CHUNK, timer=None, diag=None):
     """Gradients ``(dq, dk, dv, dw, db, dg, dh0)`` in the primals' dtypes
     (dg and dh0 float32).  ``reuse`` declares that ``workspace`` holds the
     intermediates of a ``forward(..., save=True)`` on the same inputs."""
@@ -134,6 +141,8 @@ def backward(q, k, v, w, b, g, scale, dO, dh_final=None, h0=None, *, workspace=N
     args = make_args(q, v, scale, do_dtype=dO.dtype, flags=_lib.GDN2_REUSE if reuse else 0, chunk=chunk)
     if timer is not None:
         args.profile = timer.arm()
+    if diag is not None:
+        args.diag = diag.ptr
     if workspace is None:
         workspace = new_workspace(args, q.device)
     if h0 is not None:

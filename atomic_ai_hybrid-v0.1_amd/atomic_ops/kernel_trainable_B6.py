@@ -11,16 +11,37 @@ recomputing them (the reference recomputes; both give the same gradient).
 """
 from __future__ import annotations
 
+import os
+import sys
+
 import torch
 
+from . import _lib
 from . import gdn2 as _g
+
+# The reference's opt-in stage check (GDN2_FWD_DIAG=1, read at import,
+# kernel_d_pipeline.py:48-91): every forward then also reduces each stage of
+# the pipeline to its non-finite count and max |x| (extra launches; nothing
+# extra runs when it is off) and prints the stages that are non-finite or
+# above 1e6.
+_GDN2_FWD_DIAG = os.environ.get("GDN2_FWD_DIAG", "0") == "1"
+
+
+def _forward(q, k, v, w, b, g, scale, h0, save, debug_tag=""):
+    if not _GDN2_FWD_DIAG:
+        return _g.forward(q, k, v, w, b, g, scale, h0, save=save)
+    rep = _lib.StageReports(_lib.GDN2_DIAG_STAGES, q.device)
+    out = _g.forward(q, k, v, w, b, g, scale, h0, save=save, diag=rep)
+    for line in rep.messages(debug_tag, 0, _lib.GDN2_DIAG_FWD):
+        print(line, file=sys.stderr, flush=True)
+    return out
 
 
 class _Gdn2Core(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, w, b, g, scale, h0):
         need = any(ctx.needs_input_grad)
-        o, h_final, ws = _g.forward(q, k, v, w, b, g, scale, h0, save=need)
+        o, h_final, ws = _forward(q, k, v, w, b, g, scale, h0, need)
         if need:
             ctx.save_for_backward(q, k, v, w, b, g, h0)
             ctx.ws = ws
@@ -49,7 +70,8 @@ def gdn2_pallas_forward_trainable(q, k, v, w, b, g, scale, h0=None):
     return _Gdn2Core.apply(q, k, v, w, b, g, scale, h0)
 
 
-def gdn2_pallas_forward(q, k, v, w, b, g, scale, h0=None):
-    """Forward only (reference kernel_d_pipeline.py:161-196)."""
-    o, h_final, _ = _g.forward(q, k, v, w, b, g, scale, h0)
+def gdn2_pallas_forward(q, k, v, w, b, g, scale, h0=None, debug_tag=""):
+    """Forward only (reference kernel_d_pipeline.py:161-196); ``debug_tag``
+    prefixes the stage reports when GDN2_FWD_DIAG=1."""
+    o, h_final, _ = _forward(q, k, v, w, b, g, scale, h0, False, debug_tag)
     return o, h_final

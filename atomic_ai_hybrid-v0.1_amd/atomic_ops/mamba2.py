@@ -54,8 +54,11 @@ def workspace_bytes(args):
     return n
 
 
-def forward(dt, x, Bm, Cm, A, chunk_size, state0=None, *, save=False, workspace=None, timer=None):
-    """Returns ``(y, state_final, workspace)``."""
+def forward(dt, x, Bm, Cm, A, chunk_size, state0=None, *, save=False, workspace=None, timer=None,
+            diag=None):
+    """Returns ``(y, state_final, workspace)``.  ``diag`` (an
+    ``_lib.StageReports`` over ``_lib.MAMBA2_DIAG_STAGES``) receives the
+    forward's per-stage reports."""
     _check(dt, x, Bm, Cm, A)
     lib = _lib.load()
     dt, x, Bm, Cm, A = (t.contiguous() for t in (dt, x, Bm, Cm, A))
@@ -64,6 +67,8 @@ def forward(dt, x, Bm, Cm, A, chunk_size, state0=None, *, save=False, workspace=
     args = make_args(dt, Bm, chunk_size, flags=M2_SAVE if save else 0)
     if timer is not None:
         args.profile = timer.arm()
+    if diag is not None:
+        args.diag = diag.ptr
     if workspace is None:
         workspace = torch.empty(workspace_bytes(args), dtype=torch.uint8, device=dt.device)
     if state0 is not None:
@@ -78,7 +83,7 @@ def forward(dt, x, Bm, Cm, A, chunk_size, state0=None, *, save=False, workspace=
 
 
 def backward(dt, x, Bm, Cm, A, chunk_size, dy, dstate_final=None, state0=None, *, workspace=None,
-             reuse=False, timer=None):
+             reuse=False, timer=None, diag=None):
     """Gradients ``(ddt, dx, dB, dC, dA, dstate0)`` (MB0 semantics) in the
     primals' dtypes (dA, dstate0 float32)."""
     _check(dt, x, Bm, Cm, A)
@@ -90,6 +95,8 @@ def backward(dt, x, Bm, Cm, A, chunk_size, dy, dstate_final=None, state0=None, *
     args = make_args(dt, Bm, chunk_size, dy_dtype=dy.dtype, flags=M2_REUSE if reuse else 0)
     if timer is not None:
         args.profile = timer.arm()
+    if diag is not None:
+        args.diag = diag.ptr
     if workspace is None:
         workspace = torch.empty(workspace_bytes(args), dtype=torch.uint8, device=dt.device)
     if state0 is not None:

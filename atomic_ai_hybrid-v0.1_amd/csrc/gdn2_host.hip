@@ -3,6 +3,7 @@
 #include <mutex>
 
 #include "../../include/atomic_hybrid.h"
+#include "diag.hpp"
 #include "gdn2_bwd.hip"
 #include "launch.hpp"
 
@@ -210,6 +211,106 @@ int gdn2_forward(const Gdn2Plan& p, int dtype, const void* q, const void* k, con
   return gdn2_forward_impl<float, 64>(p, q, k, v, w, b, g, h0, o, h_final, ws, save, L);
 }
 
+// ------------------------------------------------ stage reports
+// Akk of one chunk (kernel A's second output, gdn2_wy_reference.py:80-81,87),
+// recomputed pairwise from the inputs for its stage report: the fused intra
+// kernel keeps it in LDS only.
+//   Akk[i,j] = n2n(sum_d (b k)[i,d] k[j,d] exp(clip(gc[i,d] - gc[j,d], +-20))), i > j
+template <typename T, int C, int K>
+__global__ __launch_bounds__(256) void gdn2_diag_akk(Gdn2Dims dm, const T* __restrict__ k,
+                                                     const T* __restrict__ b, const float* __restrict__ g,
+                                                     atomic_stage_report* r) {
+  constexpr int LD = K + 1;
+  __shared__ float sgc[C * LD], sk[C * LD], sbk[C * LD];
+  const int tid = threadIdx.x, bhn = blockIdx.x;
+  const int n = bhn % dm.NT, bh = bhn / dm.NT, h = bh % dm.H, bb = bh / dm.H;
+  const size_t t0 = (size_t)bb * dm.T + (size_t)n * C;
+  const size_t rs = (size_t)dm.H * K;
+  for (int e = tid; e < C * K; e += 256) {
+    const int i = e / K, d = e % K;
+    const size_t off = (t0 + i) * rs + (size_t)h * K + d;
+    const float kv = to_f(k[off]);
+    sgc[i * LD + d] = g[off];
+    sk[i * LD + d] = kv;
+    sbk[i * LD + d] = to_f(b[off]) * kv;
+  }
+  __syncthreads();
+  for (int d = tid; d < K; d += 256)
+    for (int i = 1; i < C; ++i) sgc[i * LD + d] += sgc[(i - 1) * LD + d];
+  __syncthreads();
+  uint32_t bad = 0;
+  float mx = 0.f;
+  for (int e = tid; e < C * C; e += 256) {
+    const int i = e / C, j = e % C;
+    if (i <= j) continue;
+    float acc = 0.f;
+    for (int d = 0; d < K; ++d) {
+      const float dd = fminf(fmaxf(sgc[i * LD + d] - sgc[j * LD + d], -kClipDecay), kClipDecay);
+      acc += sbk[i * LD + d] * sk[j * LD + d] * __expf(dd);
+    }
+    acc = n2n(acc);
+    if (__builtin_isfinite(acc)) mx = fmaxf(mx, fabsf(acc));
+    else ++bad;
+  }
+  stage_report_fold(bad, mx, r);
+}
+
+// Forward stage reports from the workspace of plan p (one window, for the
+// no-allocation forward) and the outputs o / h_final (either may be NULL).
+template <typename T, int K>
+static int gdn2_forward_diag_t(const Gdn2Plan& p, StageDiag& D, const void* k, const void* b,
+                               const float* g, const float* o, const float* h_final, void* ws) {
+  constexpr int C = 64, V = K;
+  const Gdn2Chunks<T> ck = gdn2_chunks<T>(p, ws);
+  const size_t N = p.bhn;
+  int rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_AQK, ck.aqk, N * C * C))) return rc;
+  rc = D.L("gdn2_diag_akk", [&] {
+    hipLaunchKernelGGL((gdn2_diag_akk<T, C, K>), dim3((unsigned)N), dim3(256), 0, D.L.st, p.dm, (const T*)k,
+                       (const T*)b, g, D.r + ATOMIC_GDN2_DIAG_AKK);
+  });
+  if (rc) return rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_AINV, ck.ainv, N * C * C))) return rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_W_PSEUDO, ck.wt, N * C * K))) return rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_U, ck.u, N * C * V))) return rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_KG, ck.kg, N * C * K))) return rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_QG, ck.qg, N * C * K))) return rc;
+  const size_t rows = (size_t)p.dm.B * p.dm.T * p.dm.H;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_O, o, rows * V))) return rc;
+  return D.reduce(ATOMIC_GDN2_DIAG_H_FINAL, h_final, (size_t)p.dm.B * p.dm.H * K * V);
+}
+
+static int gdn2_forward_diag(const Gdn2Plan& p, int dtype, StageDiag& D, const void* k, const void* b,
+                             const float* g, const float* o, const float* h_final, void* ws) {
+  if (dtype == ATOMIC_BF16) {
+    if (p.dm.K == 128) return gdn2_forward_diag_t<bf16, 128>(p, D, k, b, g, o, h_final, ws);
+    return gdn2_forward_diag_t<bf16, 64>(p, D, k, b, g, o, h_final, ws);
+  }
+  if (p.dm.K == 128) return gdn2_forward_diag_t<float, 128>(p, D, k, b, g, o, h_final, ws);
+  return gdn2_forward_diag_t<float, 64>(p, D, k, b, g, o, h_final, ws);
+}
+
+template <typename T>
+static int gdn2_backward_diag_t(const Gdn2Plan& p, StageDiag& D, const void* dq, const void* dk,
+                                const void* dv, const void* dw, const void* db, const float* dg,
+                                const float* dh0, void* ws) {
+  const Gdn2Grads<T> gr = gdn2_grads<T>(p, ws);
+  const size_t N = p.bhn, C = p.dm.C, K = p.dm.K, V = p.dm.V;
+  const size_t rows = (size_t)p.dm.B * p.dm.T * p.dm.H;
+  int rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_DV_NEW, gr.dvn, N * C * V))) return rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_DH, gr.dhT, N * V * K))) return rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_DAQK, gr.daqk, N * C * C))) return rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_DAKK, gr.dakk, N * C * C))) return rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_DQ, (const T*)dq, rows * K))) return rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_DK, (const T*)dk, rows * K))) return rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_DV, (const T*)dv, rows * V))) return rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_DW, (const T*)dw, rows * V))) return rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_DB, (const T*)db, rows * K))) return rc;
+  if ((rc = D.reduce(ATOMIC_GDN2_DIAG_DG, dg, rows * K))) return rc;
+  return D.reduce(ATOMIC_GDN2_DIAG_DH0, dh0, (size_t)p.dm.B * p.dm.H * K * V);
+}
+
 // ------------------------------------------------ no-allocation forward
 // atomic_gdn2_fwd_noalloc runs the forward kernels out of a file-scope device
 // array instead of a caller workspace.  Each device the library runs on holds
@@ -290,6 +391,8 @@ static int gdn2_forward_noalloc(const atomic_gdn2_args* a, const void* q, const 
                      reinterpret_cast<float*>(static_cast<char*>(base) + slot)};
   void* ws = static_cast<char*>(base) + 2 * slot;
   Launch L{a->profile, st};
+  StageDiag D{a->diag, L};
+  if (D && (rc = D.clear(0, ATOMIC_GDN2_DIAG_DV_NEW))) return rc;
   const size_t T = (size_t)a->seqlen, rowK = (size_t)H * K, rowV = (size_t)H * V;
   for (int bb = 0; bb < a->batch; ++bb) {
     const float* hin = h0 ? h0 + (size_t)bb * state_elems : nullptr;
@@ -306,6 +409,11 @@ static int gdn2_forward_noalloc(const atomic_gdn2_args* a, const void* q, const 
       float* hout = n0 + nw == NT ? h_final + (size_t)bb * state_elems : slots[wi & 1];
       rc = gdn2_forward(pw, a->dtype, qp, kp, vp, wp, bp, g + t0 * rowK, hin, o + t0 * rowV, hout, ws, 0, L);
       if (rc) return rc;
+      if (D) {  // the reports accumulate over the windows
+        rc = gdn2_forward_diag(pw, a->dtype, D, kp, bp, g + t0 * rowK, o + t0 * rowV,
+                               n0 + nw == NT ? hout : nullptr, ws);
+        if (rc) return rc;
+      }
       hin = hout;
     }
   }
@@ -343,8 +451,12 @@ extern "C" int atomic_gdn2_fwd(const atomic_gdn2_args* a, const void* q, const v
   if (!q || !k || !v || !w || !b || !g || !o || !h_final) return ATOMIC_ERR_NULL;
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
   Launch L{a->profile, (hipStream_t)stream};
-  return gdn2_forward(p, a->dtype, q, k, v, w, b, g, h0, o, h_final, workspace,
-                      (a->flags & ATOMIC_GDN2_SAVE) ? 1 : 0, L);
+  int r2 = gdn2_forward(p, a->dtype, q, k, v, w, b, g, h0, o, h_final, workspace,
+                        (a->flags & ATOMIC_GDN2_SAVE) ? 1 : 0, L);
+  if (r2 || !a->diag) return r2;
+  StageDiag D{a->diag, L};
+  if ((r2 = D.clear(0, ATOMIC_GDN2_DIAG_DV_NEW))) return r2;
+  return gdn2_forward_diag(p, a->dtype, D, k, b, g, o, h_final, workspace);
 }
 
 extern "C" int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
@@ -360,8 +472,14 @@ extern "C" int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const v
     return ATOMIC_ERR_NULL;
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
   Launch L{a->profile, (hipStream_t)stream};
-  return gdn2_backward(p, a->dtype, a->do_dtype, q, k, v, w, b, g, h0, dO, dh_final, dq, dk, dv, dw,
-                       db, dg, dh0, workspace, (a->flags & ATOMIC_GDN2_REUSE) != 0, L);
+  int r2 = gdn2_backward(p, a->dtype, a->do_dtype, q, k, v, w, b, g, h0, dO, dh_final, dq, dk, dv, dw,
+                         db, dg, dh0, workspace, (a->flags & ATOMIC_GDN2_REUSE) != 0, L);
+  if (r2 || !a->diag) return r2;
+  StageDiag D{a->diag, L};
+  if ((r2 = D.clear(ATOMIC_GDN2_DIAG_DV_NEW, ATOMIC_GDN2_DIAG_COUNT - ATOMIC_GDN2_DIAG_DV_NEW))) return r2;
+  if (a->dtype == ATOMIC_BF16)
+    return gdn2_backward_diag_t<bf16>(p, D, dq, dk, dv, dw, db, dg, dh0, workspace);
+  return gdn2_backward_diag_t<float>(p, D, dq, dk, dv, dw, db, dg, dh0, workspace);
 }
 
 extern "C" int atomic_gdn2_fwd_noalloc(const atomic_gdn2_args* a, const void* q, const void* k,

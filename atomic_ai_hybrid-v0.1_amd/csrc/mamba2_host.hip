@@ -1,6 +1,7 @@
 // Host side of the Mamba2 SSD chunk scan: argument checks, workspace layout,
 // template dispatch and the extern "C" entry points of include/atomic_hybrid.h.
 #include "../../include/atomic_hybrid.h"
+#include "diag.hpp"
 #include "mamba2_bwd.hip"
 #include "launch.hpp"
 
@@ -225,6 +226,40 @@ int mamba2_backward(const Mamba2Plan& p, int dy_dtype, const void* dt, const voi
                  dB, dC, dA, dstate0, ws, reuse, L);
 }
 
+// Stage reports of the forward (CB, the states entering each chunk, y,
+// state_final) and of the backward (the dstate entering each chunk's
+// backward, then every gradient).
+static int mamba2_forward_diag(const Mamba2Plan& p, StageDiag& D, const float* y, const float* state_final,
+                               void* ws) {
+  const Mamba2Dims& d = p.dm;
+  const Mamba2Chunks<bf16> ck = mamba2_chunks<bf16>(p, ws);
+  const size_t B = d.B, NT = d.NT, H = d.H, P = d.P, N = d.N, C = d.C, T = d.T;
+  int rc;
+  if ((rc = D.clear(0, ATOMIC_MAMBA2_DIAG_DSTATES))) return rc;
+  if ((rc = D.reduce(ATOMIC_MAMBA2_DIAG_CB, ck.cb, B * NT * C * C))) return rc;
+  if ((rc = D.reduce(ATOMIC_MAMBA2_DIAG_STATES, ck.state_pre, B * NT * H * P * N))) return rc;
+  if ((rc = D.reduce(ATOMIC_MAMBA2_DIAG_Y, y, B * T * H * P))) return rc;
+  return D.reduce(ATOMIC_MAMBA2_DIAG_STATE_FINAL, state_final, B * H * P * N);
+}
+
+static int mamba2_backward_diag(const Mamba2Plan& p, StageDiag& D, const void* ddt, const void* dx,
+                                const void* dB, const void* dC, const float* dA, const float* dstate0,
+                                void* ws) {
+  const Mamba2Dims& d = p.dm;
+  const Mamba2Grads<bf16> gr = mamba2_grads<bf16>(p, ws);
+  const size_t B = d.B, NT = d.NT, H = d.H, P = d.P, N = d.N, T = d.T;
+  int rc;
+  if ((rc = D.clear(ATOMIC_MAMBA2_DIAG_DSTATES, ATOMIC_MAMBA2_DIAG_COUNT - ATOMIC_MAMBA2_DIAG_DSTATES)))
+    return rc;
+  if ((rc = D.reduce(ATOMIC_MAMBA2_DIAG_DSTATES, gr.dstate, B * NT * H * P * N))) return rc;
+  if ((rc = D.reduce(ATOMIC_MAMBA2_DIAG_DDT, (const bf16*)ddt, B * T * H * P))) return rc;
+  if ((rc = D.reduce(ATOMIC_MAMBA2_DIAG_DX, (const bf16*)dx, B * T * H * P))) return rc;
+  if ((rc = D.reduce(ATOMIC_MAMBA2_DIAG_DB, (const bf16*)dB, B * T * N))) return rc;
+  if ((rc = D.reduce(ATOMIC_MAMBA2_DIAG_DC, (const bf16*)dC, B * T * N))) return rc;
+  if ((rc = D.reduce(ATOMIC_MAMBA2_DIAG_DA, dA, H))) return rc;
+  return D.reduce(ATOMIC_MAMBA2_DIAG_DSTATE0, dstate0, B * H * P * N);
+}
+
 }  // namespace ah
 
 using namespace ah;
@@ -245,7 +280,10 @@ extern "C" int atomic_mamba2_fwd(const atomic_mamba2_args* a, const void* dt, co
   if (!dt || !x || !B || !C || !A || !y || !state_final) return ATOMIC_ERR_NULL;
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
   Launch L{a->profile, (hipStream_t)stream};
-  return mamba2_forward(p, dt, x, B, C, A, state0, y, state_final, workspace, L);
+  int r2 = mamba2_forward(p, dt, x, B, C, A, state0, y, state_final, workspace, L);
+  if (r2 || !a->diag) return r2;
+  StageDiag D{a->diag, L};
+  return mamba2_forward_diag(p, D, y, state_final, workspace);
 }
 
 extern "C" int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, const void* x,
@@ -259,6 +297,9 @@ extern "C" int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, co
   if (!dt || !x || !B || !C || !A || !dy || !ddt || !dx || !dB || !dC || !dA) return ATOMIC_ERR_NULL;
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
   Launch L{a->profile, (hipStream_t)stream};
-  return mamba2_backward(p, a->dy_dtype, dt, x, B, C, A, state0, dy, dstate_final, ddt, dx, dB, dC, dA,
-                         dstate0, workspace, (a->flags & ATOMIC_MAMBA2_REUSE) != 0, L);
+  int r2 = mamba2_backward(p, a->dy_dtype, dt, x, B, C, A, state0, dy, dstate_final, ddt, dx, dB, dC, dA,
+                           dstate0, workspace, (a->flags & ATOMIC_MAMBA2_REUSE) != 0, L);
+  if (r2 || !a->diag) return r2;
+  StageDiag D{a->diag, L};
+  return mamba2_backward_diag(p, D, ddt, dx, dB, dC, dA, dstate0, workspace);
 }

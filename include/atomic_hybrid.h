@@ -54,7 +54,50 @@ typedef struct atomic_profile {
   const char* names[ATOMIC_PROFILE_MAX];
 } atomic_profile;
 
+/* Optional per-stage report, the counterpart of the reference's opt-in
+   GDN2_FWD_DIAG stage check (atomic_ops/kernel_d_pipeline.py:50-91, applied
+   to each kernel's output at :177-187,121-123; model.py:107-124 for the
+   Mamba2 output): for every stage a call covers, the number of non-finite
+   entries of the stage's output and the largest |x| over its finite entries.
+   When an args struct's `diag` is a device pointer to ATOMIC_*_DIAG_COUNT
+   reports, the call clears the entries of the stages it covers and fills
+   them with extra reductions launched on its stream after the path's own
+   kernels (reading each stage's buffer; Akk, which no kernel stores, is
+   recomputed from the inputs).  With `diag` NULL nothing extra runs.  The
+   reference prints when a stage is non-finite or above 1e6; the caller reads
+   the reports after the stream and decides. */
+typedef struct atomic_stage_report {
+  uint32_t n_nonfinite;  /* entries that are NaN or +-inf                     */
+  float max_abs;         /* max |x| over the finite entries (0 if none)       */
+} atomic_stage_report;
+
 /* ------------------------------------------------------------------ GDN2 */
+
+/* Stages of atomic_gdn2_args.diag: the forward fills [AQK, H_FINAL] (o and
+   h_final when passed), the backward fills [DV_NEW, DH0]. */
+enum {
+  ATOMIC_GDN2_DIAG_AQK = 0,       /* kernel A: scale q k^T under the decay    */
+  ATOMIC_GDN2_DIAG_AKK = 1,       /* kernel A: (b k) k^T under the decay      */
+  ATOMIC_GDN2_DIAG_AINV = 2,      /* kernel B: (I + Akk)^-1                   */
+  ATOMIC_GDN2_DIAG_W_PSEUDO = 3,  /* kernel C                                 */
+  ATOMIC_GDN2_DIAG_U = 4,
+  ATOMIC_GDN2_DIAG_KG = 5,
+  ATOMIC_GDN2_DIAG_QG = 6,
+  ATOMIC_GDN2_DIAG_O = 7,         /* kernel D                                 */
+  ATOMIC_GDN2_DIAG_H_FINAL = 8,
+  ATOMIC_GDN2_DIAG_DV_NEW = 9,    /* B2 + B1: dv_new per chunk                */
+  ATOMIC_GDN2_DIAG_DH = 10,       /* B1: dh entering each chunk               */
+  ATOMIC_GDN2_DIAG_DAQK = 11,     /* B2 dAqk times the query scale            */
+  ATOMIC_GDN2_DIAG_DAKK = 12,     /* B3                                       */
+  ATOMIC_GDN2_DIAG_DQ = 13,
+  ATOMIC_GDN2_DIAG_DK = 14,
+  ATOMIC_GDN2_DIAG_DV = 15,
+  ATOMIC_GDN2_DIAG_DW = 16,
+  ATOMIC_GDN2_DIAG_DB = 17,
+  ATOMIC_GDN2_DIAG_DG = 18,
+  ATOMIC_GDN2_DIAG_DH0 = 19,
+  ATOMIC_GDN2_DIAG_COUNT = 20
+};
 
 /* Flags for atomic_gdn2_args.flags */
 enum {
@@ -79,6 +122,8 @@ typedef struct atomic_gdn2_args {
   float scale;       /* query scale (the model passes 1.0, model.py:631)        */
   int32_t flags;     /* ATOMIC_GDN2_*                                           */
   atomic_profile* profile;  /* optional per-kernel event timing, or NULL      */
+  atomic_stage_report* diag;  /* optional stage reports (device memory,
+                                 ATOMIC_GDN2_DIAG_COUNT entries), or NULL    */
 } atomic_gdn2_args;
 
 /* Bytes of workspace atomic_gdn2_fwd / atomic_gdn2_bwd need for these args. */
@@ -160,6 +205,23 @@ enum {
   ATOMIC_MAMBA2_REUSE = 2
 };
 
+/* Stages of atomic_mamba2_args.diag: the forward fills [CB, STATE_FINAL],
+   the backward fills [DSTATES, DSTATE0]. */
+enum {
+  ATOMIC_MAMBA2_DIAG_CB = 0,           /* C B^T per chunk (shared by heads)   */
+  ATOMIC_MAMBA2_DIAG_STATES = 1,       /* state entering each chunk           */
+  ATOMIC_MAMBA2_DIAG_Y = 2,            /* the SSD output (model.py:519)       */
+  ATOMIC_MAMBA2_DIAG_STATE_FINAL = 3,
+  ATOMIC_MAMBA2_DIAG_DSTATES = 4,      /* dstate entering each chunk's bwd    */
+  ATOMIC_MAMBA2_DIAG_DDT = 5,
+  ATOMIC_MAMBA2_DIAG_DX = 6,
+  ATOMIC_MAMBA2_DIAG_DB = 7,
+  ATOMIC_MAMBA2_DIAG_DC = 8,
+  ATOMIC_MAMBA2_DIAG_DA = 9,
+  ATOMIC_MAMBA2_DIAG_DSTATE0 = 10,
+  ATOMIC_MAMBA2_DIAG_COUNT = 11
+};
+
 typedef struct atomic_mamba2_args {
   int32_t batch;     /* B                                                  */
   int32_t seqlen;    /* T, a multiple of chunk                             */
@@ -171,6 +233,8 @@ typedef struct atomic_mamba2_args {
   int32_t dy_dtype;  /* upstream gradient dy: ATOMIC_F32 / ATOMIC_BF16     */
   int32_t flags;     /* ATOMIC_MAMBA2_*                                    */
   atomic_profile* profile;  /* optional per-kernel event timing, or NULL */
+  atomic_stage_report* diag;  /* optional stage reports (device memory,
+                                 ATOMIC_MAMBA2_DIAG_COUNT entries), or NULL */
 } atomic_mamba2_args;
 
 /* Bytes of workspace atomic_mamba2_fwd / atomic_mamba2_bwd need. */

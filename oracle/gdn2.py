@@ -224,6 +224,7 @@ def gdn2_backward_chain(q, k, v, w, b, g, scale, chunk_size, do, dh_final=None,
     dh0 = dh
 
     outs = {k_: [] for k_ in ("dq", "dk", "db", "dw", "dv", "dg")}
+    dAkk_all = []
     for n in range(NT):
         s = st[n]
         qf, kf, bf_, wf, vf = (t[n].to(f) for t in (qc, kc, bc, wc, vc))
@@ -250,6 +251,7 @@ def gdn2_backward_chain(q, k, v, w, b, g, scale, chunk_size, do, dh_final=None,
         dA_total = sanitize(dA_total)
         tmp = sanitize(dA_total @ A.transpose(-1, -2))
         dAkk = n2n(-(A.transpose(-1, -2) @ tmp) * strict)
+        dAkk_all.append(dAkk)
         dk3 = dkb * egc * bf_ + dkg * torch.exp(gcl[..., None, :] - gc)
         db3 = dkb * egc * kf
         dx = dkg * kg
@@ -290,6 +292,7 @@ def gdn2_backward_chain(q, k, v, w, b, g, scale, chunk_size, do, dh_final=None,
         outs["dv"].append(dv3)
         outs["dg"].append(dg)
     res = {k_: final_sanitize(_from_chunks(torch.stack(vv, 0))) for k_, vv in outs.items()}
-    inter = dict(dAqk=dAqk, dv_partial=dv_partial, dh_next=dh_next, dv_new=dv_all, stages=st)
+    inter = dict(dAqk=dAqk, dAkk=dAkk_all, dv_partial=dv_partial, dh_next=dh_next, dv_new=dv_all,
+                 stages=st)
     return (res["dq"], res["dk"], res["dv"], res["dw"], res["db"], res["dg"],
             final_sanitize(dh0)), inter
