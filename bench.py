@@ -35,8 +35,8 @@ RIDGE = MFMA_BF16_PEAK / HBM_PEAK
 
 GDN2 = dict(B=4, T=8192, H=16, K=128, V=128, C=64)
 MAMBA2 = dict(B=4, T=8192, H=16, P=128, N=128, C=128)
-CPU_SAMPLE_T = 2048        # tokens of the bounded CPU sample (batch 1, same heads)
-CPU_THREADS_MAX = 16
+CPU_SAMPLE_T = 1024        # tokens of the bounded CPU sample (batch 1, same heads)
+CPU_REPEATS = 3            # the CPU baseline is the median of this many runs
 CALIB_BYTES = 256 << 20    # the --calib-copy copy: 256 MiB read + 256 MiB written
 PROF_STEPS = 10            # steps of the instrumented (per-kernel timing) pass
 
@@ -157,6 +157,65 @@ def mamba2_kernel_model(B, T, H, P, N, C, es=2):
     }
 
 
+# ------------------------------------------------- path-level bytes and flops
+def survey_path_model(g, m):
+    """Algorithmic HBM bytes and flops per step of each path, from the
+    per-token-head (bytes) and per-chunk-head (GDN2 flops) figures the
+    benchmark's measurement plan fixes: every path-level input read once and
+    every output written once; recompute and intermediates excluded.
+      GDN2 fwd bytes  q, k, b (bf16 K), v, w (bf16 V), g (f32 K), o (f32 V)
+      GDN2 bwd bytes  the inputs + dO (bf16 V) in; dq, dk, db, dv, dw (bf16), dg (f32) out
+      GDN2 flops      fwd 6C^2K + 4C^2V + 6CKV + C^3/3, bwd 12C^2K + 8C^2V + 12CKV + 4C^3
+      Mamba2 bytes    fwd 2P (x) + 2P (dt) + 4P (y) + 4N/H (B, C);
+                      bwd 6P + 4N/H in (x, dt, dy, B, C), 4P + 4N/H out
+      Mamba2 flops    fwd 2CN/H + 2CP + 4NP, bwd 8NP + 4CP + 4CN/H
+    Returns {path: {"fwd": (flops, bytes), "bwd": (flops, bytes)}}."""
+    B, T, H, K, V, C = g["B"], g["T"], g["H"], g["K"], g["V"], g["C"]
+    th = B * T * H
+    ch = B * H * (T // C)
+    gf = 6 * C * C * K + 4 * C * C * V + 6 * C * K * V + C ** 3 / 3
+    gb = 12 * C * C * K + 8 * C * C * V + 12 * C * K * V + 4 * C ** 3
+    g_in = 3 * 2 * K + 2 * 2 * V + 4 * K
+    gdn2 = {"fwd": (ch * gf, th * (g_in + 4 * V)),
+            "bwd": (ch * gb, th * (g_in + 2 * V + 3 * 2 * K + 2 * 2 * V + 4 * K))}
+    B, T, H, P, N, C = m["B"], m["T"], m["H"], m["P"], m["N"], m["C"]
+    th = B * T * H
+    mf = 2 * C * N / H + 2 * C * P + 4 * N * P
+    mb = 8 * N * P + 4 * C * P + 4 * C * N / H
+    mamba2 = {"fwd": (th * mf, th * (2 * P + 2 * P + 4 * P + 4 * N / H)),
+              "bwd": (th * mb, th * (6 * P + 4 * N / H + 4 * P + 4 * N / H))}
+    return {"gdn2": gdn2, "mamba2": mamba2}
+
+
+def survey_kernel_share(g, m):
+    """Each kernel's share of the path-level bytes above: the path inputs it
+    reads and the path outputs it writes (a tensor two kernels read counts
+    in both shares; intermediates count in none).  Per launch, by kernel."""
+    B, T, H, K, V = g["B"], g["T"], g["H"], g["K"], g["V"]
+    th = B * T * H
+    share = {
+        "gdn2_fwd_intra": th * (3 * 2 * K + 4 * K + 2 * 2 * V),   # q k b g v w
+        "gdn2_fwd_state": th * 4 * V,                              # o
+        "gdn2_bwd_dh": th * 2 * V,                                 # dO
+        "gdn2_bwd_hgrad": th * 2 * V,                              # dO
+        "gdn2_bwd_wy": th * (2 * 2 * K + 4 * K + 2 * 2 * V + 2 * 2 * V),   # k b g v w in; dw dv out
+        "gdn2_bwd_intra": th * (3 * 2 * K + 4 * K + 3 * 2 * K + 4 * K),    # q k b g in; dq dk db dg out
+    }
+    B, T, H, P, N = m["B"], m["T"], m["H"], m["P"], m["N"]
+    th, bt = B * T * H, B * T
+    share.update({
+        "mamba2_cb": bt * 2 * 2 * N,                               # B C
+        "mamba2_chunk_state": th * 4 * P + bt * 2 * N,             # dt x B
+        "mamba2_state_pass": B * H * P * N * 4,                    # state_final
+        "mamba2_chunk_y": th * (4 * P + 4 * P) + bt * 2 * N,       # dt x C in; y out
+        "mamba2_bwd_source": th * 6 * P + bt * 2 * N,              # dt x dy C
+        "mamba2_bwd_state_pass": B * H * P * N * 4,                # dstate0
+        "mamba2_bwd_chunk": th * (6 * P + 4 * P) + bt * 4 * N,     # dt x dy B C in; ddt dx out
+        "mamba2_bwd_bc": bt * 4 * N * 2 + H * 4,                   # B C in; dB dC dA out
+    })
+    return share
+
+
 def roofline(flops, nbytes, seconds):
     ai = flops / nbytes if nbytes else float("inf")
     if ai < RIDGE:
@@ -184,14 +243,37 @@ def measured_traffic(kernel):
 
 
 # --------------------------------------------------------------------------- CPU baseline
-def cpu_baseline(sample_t=CPU_SAMPLE_T):
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads():
+    """Threads for the CPU baseline: every core this process may run on,
+    capped by OMP_NUM_THREADS when the environment sets it (a GPU box's CPU
+    share; os.cpu_count() there counts the whole host)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_baseline(sample_t=CPU_SAMPLE_T, repeats=CPU_REPEATS):
     """Times the float32 restatement (oracle/) of the reference's GDN2 WY
     forward + B1..B5 backward and Mamba2 SSD forward + MB0 backward on
-    batch 1, ``sample_t`` tokens, the benchmark's head shapes."""
+    batch 1, ``sample_t`` tokens, the benchmark's head shapes: the median of
+    ``repeats`` runs."""
     import torch
     from atomic_ops import inputs
     from oracle import gdn2 as og, mamba2 as om
-    threads = max(1, min(os.cpu_count() or 1, CPU_THREADS_MAX))
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     f = torch.float32
     g, m = GDN2, MAMBA2
@@ -207,13 +289,18 @@ def cpu_baseline(sample_t=CPU_SAMPLE_T):
         om.chunk_ssd_bwd_scan(dt, A, Bm, Cm, x, m["C"], dy, dtype=f)
 
     run(m["C"])                       # warm-up: one chunk of each path
-    t0 = time.perf_counter()
-    run(sample_t)
-    sec = time.perf_counter() - t0
+    secs = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        run(sample_t)
+        secs.append(time.perf_counter() - t0)
+    sec = statistics.median(secs)
     return {"value": sample_t / sec, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "host_cpu_count": os.cpu_count(), "cpu_model": _cpu_model(),
+            "runs_s": [round(x, 2) for x in secs],
             "sample": (f"oracle/ float32 restatement, GDN2 fwd + B1..B5 bwd and Mamba2 fwd + MB0 "
-                       f"bwd at batch 1, T={sample_t}, the benchmark's head shapes; "
-                       f"{sec:.1f} s on {threads} threads (work is linear in B*T)")}
+                       f"bwd at batch 1, T={sample_t}, the benchmark's head shapes; median of "
+                       f"{repeats} runs ({sec:.1f} s) on {threads} threads (work is linear in B*T)")}
 
 
 # --------------------------------------------------------------------------- GPU step
@@ -510,6 +597,7 @@ def main():
     models = {}
     models.update(gdn2_kernel_model(**g))
     models.update(mamba2_kernel_model(**m))
+    shares = survey_kernel_share(g, m)
     kernels = {}
     for name, ms in kern_ms.items():
         per_step = sum(ms) / nprof             # kernel time per step
@@ -517,17 +605,43 @@ def main():
         avg = sum(ms) / len(ms)
         fl, by = models[name]
         rf = roofline(fl, by, avg / 1e3)
+        sh = shares[name]
         kernels[name] = dict(ms_per_launch=round(avg, 4), launches_per_step=launches,
-                             ms_per_step=round(per_step, 4), bytes=int(by), flops=fl,
+                             ms_per_step=round(per_step, 4),
+                             share_bytes=int(sh), share_frac=round(sh / (avg / 1e3) / HBM_PEAK, 4),
+                             bytes=int(by), flops=fl,
                              gbps=round(by / (avg / 1e3) / 1e9, 1),
                              tflops=round(fl / (avg / 1e3) / 1e12, 2),
                              bound=rf["bound"], frac=round(rf["frac"], 4))
     dom = max(kernels, key=lambda n: kernels[n]["ms_per_step"])
+    # the dominant kernel against HBM on its share of the path-level bytes;
+    # the intermediate-inclusive model (every buffer it must touch once)
+    # stays beside it
     fl, by = models[dom]
-    rf = roofline(fl, by, kernels[dom]["ms_per_launch"] / 1e3)
-    rf = {k_: (round(v_, 4) if isinstance(v_, float) else v_) for k_, v_ in rf.items()}
-    rf["kernel"] = dom
-    rf["traffic"] = measured_traffic(dom)
+    sh = shares[dom]
+    sec = kernels[dom]["ms_per_launch"] / 1e3
+    rf = dict(bound="hbm", achieved=round(sh / sec / 1e9, 1), peak=HBM_PEAK / 1e9, unit="GB/s",
+              frac=round(sh / sec / HBM_PEAK, 4), kernel=dom, traffic=measured_traffic(dom),
+              algorithmic_bytes=int(sh),
+              with_intermediates=dict(bytes=int(by), achieved=round(by / sec / 1e9, 1),
+                                      frac=round(by / sec / HBM_PEAK, 4)))
+    # whole step and each path against the same path-level figures
+    pm = survey_path_model(g, m)
+    med = {k_: statistics.median(v_) / 1e3 for k_, v_ in path_ms.items()}
+
+    def _pr(flops, nbytes, secs):
+        return dict(ms=round(secs * 1e3, 4), bytes=int(nbytes), flops=round(flops),
+                    gbps=round(nbytes / secs / 1e9, 1), hbm_frac=round(nbytes / secs / HBM_PEAK, 4),
+                    mfma_frac=round(flops / secs / MFMA_BF16_PEAK, 4),
+                    bound_ms=round(max(nbytes / HBM_PEAK, flops / MFMA_BF16_PEAK) * 1e3, 4))
+    path_rf = {}
+    for pth in ("gdn2", "mamba2"):
+        fl_ = pm[pth]["fwd"][0] + pm[pth]["bwd"][0]
+        by_ = pm[pth]["fwd"][1] + pm[pth]["bwd"][1]
+        path_rf[pth] = _pr(fl_, by_, med[pth])
+    fl_all = sum(pm[p_][d_][0] for p_ in pm for d_ in ("fwd", "bwd"))
+    by_all = sum(pm[p_][d_][1] for p_ in pm for d_ in ("fwd", "bwd"))
+    path_rf["step"] = _pr(fl_all, by_all, ms_per_step / 1e3)
 
     epilogue = prologue = prologue_m2 = configs = None
     if not args.no_extras:
@@ -548,6 +662,7 @@ def main():
                    "mamba2": "B4 T8192 H16 P128 N128 C128 bf16 (A f32)",
                    "tokens_per_step": tokens},
         "roofline": rf,
+        "path_roofline": path_rf,
         "cpu_baseline": cpu,
         "paths_ms_median": {k_: round(statistics.median(v_), 4) for k_, v_ in path_ms.items()},
         "device_ms_per_step_median": round(statistics.median(step_dev_ms), 4),

@@ -67,3 +67,37 @@ def test_measured_traffic_reads_the_committed_summary():
         t = json.load(f)
     assert b.measured_traffic(t["kernel"]) == int(t["bytes_per_launch"])
     assert b.measured_traffic("not_a_kernel") is None
+
+
+def test_path_model_reproduces_the_measurement_plan_figures():
+    """The path-level model gives the figures the measurement plan states:
+    GDN2 at configurations 2 / 3 fwd 95.2 GFLOP / 1.21 GB and bwd 197.6 GFLOP /
+    2.01 GB; Mamba2 forward at configuration 1 13.2 GFLOP / 138 MB; the
+    headline Mamba2 forward 100.4 kFLOP and 1056 B per token-head."""
+    b = _bench()
+    pm = b.survey_path_model(b.GDN2, dict(B=2, T=4096, H=32, P=64, N=128, C=128))
+    assert pm["gdn2"]["fwd"][0] == pytest.approx(95.2e9, rel=2e-3)
+    assert pm["gdn2"]["fwd"][1] == pytest.approx(1.21e9, rel=5e-3)
+    assert pm["gdn2"]["bwd"][0] == pytest.approx(197.6e9, rel=2e-3)
+    assert pm["gdn2"]["bwd"][1] == pytest.approx(2.01e9, rel=5e-3)
+    assert pm["mamba2"]["fwd"][0] == pytest.approx(13.2e9, rel=5e-3)
+    assert pm["mamba2"]["fwd"][1] == pytest.approx(138e6, rel=5e-3)
+    head = b.survey_path_model(b.GDN2, b.MAMBA2)["mamba2"]["fwd"]
+    th = b.MAMBA2["B"] * b.MAMBA2["T"] * b.MAMBA2["H"]
+    assert head[0] / th == pytest.approx(100.4e3, rel=2e-3)
+    assert head[1] / th == pytest.approx(1056)
+
+
+def test_kernel_shares_cover_the_path_bytes():
+    """Every path-level byte lands in some kernel's share: the GDN2 forward
+    shares add up to the forward's bytes exactly (o and the inputs are each
+    touched by one forward kernel), and every backward output is in a share."""
+    b = _bench()
+    g, m = b.GDN2, b.MAMBA2
+    sh = b.survey_kernel_share(g, m)
+    pm = b.survey_path_model(g, m)
+    assert sh["gdn2_fwd_intra"] + sh["gdn2_fwd_state"] == pm["gdn2"]["fwd"][1]
+    th = g["B"] * g["T"] * g["H"]
+    outs = th * (3 * 2 * g["K"] + 2 * 2 * g["V"] + 4 * g["K"])
+    assert sh["gdn2_bwd_wy"] + sh["gdn2_bwd_intra"] >= outs
+    assert set(sh) == set(b.gdn2_kernel_model(**g)) | set(b.mamba2_kernel_model(**m))
