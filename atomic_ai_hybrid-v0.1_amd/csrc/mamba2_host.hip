@@ -21,13 +21,21 @@ static int mamba2_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
   if (a->dtype != ATOMIC_BF16) return ATOMIC_ERR_DTYPE;
   if (a->dy_dtype != ATOMIC_F32 && a->dy_dtype != ATOMIC_BF16) return ATOMIC_ERR_DTYPE;
   if (a->batch <= 0 || a->heads <= 0 || a->seqlen <= 0) return ATOMIC_ERR_SHAPE;
-  if (a->chunk != 64 && a->chunk != 128) return ATOMIC_ERR_SHAPE;
+  if (a->chunk != 64 && a->chunk != 128 && a->chunk != 256) return ATOMIC_ERR_SHAPE;
   if (a->seqlen % a->chunk != 0) return ATOMIC_ERR_SHAPE;
-  if (a->headdim != 64 && a->headdim != 128) return ATOMIC_ERR_SHAPE;
+  if (a->headdim != 64 && a->headdim != 128 && a->headdim != 192) return ATOMIC_ERR_SHAPE;
   if (a->dstate != 64 && a->dstate != 128) return ATOMIC_ERR_SHAPE;
+  if (a->headdim == 192 && a->dstate != 128) return ATOMIC_ERR_SHAPE;
   Mamba2Dims d;
   d.B = a->batch; d.T = a->seqlen; d.H = a->heads; d.P = a->headdim; d.N = a->dstate;
-  d.C = a->chunk; d.NT = a->seqlen / a->chunk;
+  // Chunk 256 (the model's chunk_size = min(256, L), model.py:436) runs as
+  // 128-row chunks.  With every step exponent dt A <= 0 (the model's A < 0,
+  // dt > 0) the two differ only in the reference's exp(-20) floors on pairs
+  // 128..255 rows apart and on the old state's decay, below 1e-7 of y; with a
+  // positive exponent the reference's per-chunk caps (1e6 on the pair weight,
+  // exp(20) on the decay to the chunk end) apply over 256 rows instead.
+  d.C = a->chunk == 256 ? 128 : a->chunk;
+  d.NT = a->seqlen / d.C;
   p->dm = d;
   const size_t es = 2, B = d.B, H = d.H, NT = d.NT, C = d.C, P = d.P, N = d.N, T = d.T;
   // enough (batch, chunk, head group) workgroups to fill the chip
@@ -148,6 +156,8 @@ static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x,
     if (c_ == 128 && p_ == 128 && n_ == 64) return FN<128, 128, 64>(__VA_ARGS__);       \
     if (c_ == 64 && p_ == 64 && n_ == 64) return FN<64, 64, 64>(__VA_ARGS__);           \
     if (c_ == 64 && p_ == 128 && n_ == 64) return FN<64, 128, 64>(__VA_ARGS__);         \
+    if (c_ == 128 && p_ == 192 && n_ == 128) return FN<128, 192, 128>(__VA_ARGS__);     \
+    if (c_ == 64 && p_ == 192 && n_ == 128) return FN<64, 192, 128>(__VA_ARGS__);       \
     return ATOMIC_ERR_SHAPE;                                                            \
   } while (0)
 

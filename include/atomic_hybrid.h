@@ -226,9 +226,10 @@ typedef struct atomic_mamba2_args {
   int32_t batch;     /* B                                                  */
   int32_t seqlen;    /* T, a multiple of chunk                             */
   int32_t heads;     /* H                                                  */
-  int32_t headdim;   /* P: 64 or 128                                       */
+  int32_t headdim;   /* P: 64, 128, or 192 (the model's d_inner / heads) with N = 128 */
   int32_t dstate;    /* N: 64 or 128 (ngroups = 1: B and C shared by heads) */
-  int32_t chunk;     /* C: 64 or 128                                       */
+  int32_t chunk;     /* C: 64, 128 or 256 (256 runs as 128-row chunks: equal
+                        while every dt A <= 0, up to exp(-20) floor terms)   */
   int32_t dtype;     /* dt, x, B, C and their gradients: ATOMIC_BF16       */
   int32_t dy_dtype;  /* upstream gradient dy: ATOMIC_F32 / ATOMIC_BF16     */
   int32_t flags;     /* ATOMIC_MAMBA2_*                                    */

@@ -45,6 +45,8 @@ def _gpu(args, C, reuse):
     (1, 256, 2, 128, 128, 128, True, False),    # headline P = 128
     (1, 256, 2, 64, 128, 64, True, True),       # chunk 64
     (1, 128, 2, 64, 64, 128, False, True),      # N = 64
+    (1, 512, 2, 192, 128, 256, True, True),     # the model's call site: headdim 192, chunk_size 256
+    (1, 256, 3, 192, 128, 128, False, False),   # headdim 192, chunk 128
 ])
 def test_backward_matches_mb0(B, T, H, P, N, C, state, reuse):
     banner(f"mamba2 bwd B{B} T{T} H{H} P{P} N{N} C{C} state={state} reuse={reuse}")
@@ -129,3 +131,25 @@ def test_trainable_wrapper_second_backward_recomputes():
     for t, want in zip(leaves + [s0], first):
         assert t.grad.dtype == t.dtype
         assert torch.equal(t.grad, want) or rel_err(t.grad, want) < 1e-6
+
+
+def test_trainable_wrapper_at_the_model_call_site():
+    """mamba2_pallas_forward_trainable_B6 as model.py:494-497 calls it:
+    headdim 192 (d_inner 1536 over 8 heads), d_state 128, chunk_size
+    min(256, L) = 256; y and every gradient against the MB0 oracle at chunk 256."""
+    from atomic_ops.kernel_mamba2_trainable_B6 import mamba2_pallas_forward_trainable_B6
+    banner("mamba2 trainable wrapper, P192 N128 chunk 256")
+    cpu = inputs.mamba2_inputs(1, 512, 2, 192, 128, seed=8, dO=True)
+    dev = {n: t.cuda() for n, t in cpu.items()}
+    leaves = [dev[n].clone().requires_grad_(True) for n in ("dt", "x", "Bm", "Cm", "A")]
+    y, s = mamba2_pallas_forward_trainable_B6(*leaves, 256)
+    (y * dev["dy"].float()).sum().backward()
+    dt, x, Bm, Cm, A, dy = (cpu[n] for n in ("dt", "x", "Bm", "Cm", "A", "dy"))
+    y_ref, _ = om.mamba2_ssd_reference(dt, A, Bm, Cm, x, 256)
+    ddt, dB, dC, dx, dA, _ = om.chunk_ssd_bwd_scan(dt, A, Bm, Cm, x, 256, dy)
+    errs = {"y": rel_err(y, y_ref)}
+    errs.update({n: rel_err(t.grad, r) for n, t, r in zip(("ddt", "dx", "dB", "dC", "dA"), leaves,
+                                                          (ddt, dx, dB, dC, dA))})
+    print("  rel_err " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+    for n, e in errs.items():
+        assert e < tol_for(BF16), (n, e)

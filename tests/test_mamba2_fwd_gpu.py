@@ -31,6 +31,8 @@ def _run(B, T, H, P, N, C, seed, state=False, mutate=None, **kw):
     (1, 256, 2, 128, 128, 128, True),     # headline P=128
     (2, 256, 2, 64, 128, 64, False),      # chunk 64
     (1, 256, 2, 64, 64, 128, True),       # N = 64
+    (1, 512, 2, 192, 128, 256, True),     # the model's call site: headdim 192, chunk_size 256
+    (2, 256, 3, 192, 128, 128, False),    # headdim 192, chunk 128
 ])
 def test_forward_matches_oracle(B, T, H, P, N, C, state):
     banner(f"mamba2 fwd B{B} T{T} H{H} P{P} N{N} C{C} state={state}")
