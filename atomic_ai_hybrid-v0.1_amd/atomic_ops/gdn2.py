@@ -13,7 +13,8 @@ import torch
 
 from . import _lib
 
-CHUNK = 64
+CHUNK = 64       # the default chunk_size; 128 and 256 are accepted too
+RUN_CHUNK = 64   # the chunk length the kernels (and the workspace layout) use
 
 _DT = {torch.float32: _lib.ATOMIC_F32, torch.bfloat16: _lib.ATOMIC_BF16}
 
@@ -166,7 +167,7 @@ def chunk_views(workspace, args):
     """Per-chunk intermediates inside ``workspace`` as tensors
     ``[B, H, NT, rows, cols]`` (for stage-level tests)."""
     lay = workspace_layout(args)
-    B, H, C, K, V = args.batch, args.heads, args.chunk, args.dk, args.dv
+    B, H, C, K, V = args.batch, args.heads, RUN_CHUNK, args.dk, args.dv
     NT = args.seqlen // C
     dt = torch.bfloat16 if args.dtype == _lib.ATOMIC_BF16 else torch.float32
     es = 2 if dt == torch.bfloat16 else 4

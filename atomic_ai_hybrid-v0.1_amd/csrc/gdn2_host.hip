@@ -11,6 +11,9 @@ namespace ah {
 
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// The chunk length every GDN2 kernel runs at.
+constexpr int kGdn2RunChunk = 64;
+
 struct Gdn2Plan {
   Gdn2Dims dm;
   int es;        // operand element size
@@ -26,12 +29,19 @@ static int gdn2_plan(const atomic_gdn2_args* a, Gdn2Plan* p) {
   if (a->dtype != ATOMIC_F32 && a->dtype != ATOMIC_BF16) return ATOMIC_ERR_DTYPE;
   if (a->do_dtype != ATOMIC_F32 && a->do_dtype != ATOMIC_BF16) return ATOMIC_ERR_DTYPE;
   if (a->batch <= 0 || a->heads <= 0 || a->seqlen <= 0) return ATOMIC_ERR_SHAPE;
-  if (a->chunk != 64) return ATOMIC_ERR_SHAPE;
+  if (a->chunk != 64 && a->chunk != 128 && a->chunk != 256) return ATOMIC_ERR_SHAPE;
   if (a->seqlen % a->chunk != 0) return ATOMIC_ERR_SHAPE;
   if (!((a->dk == 64 || a->dk == 128) && a->dv == a->dk)) return ATOMIC_ERR_SHAPE;
   Gdn2Dims d;
-  d.B = a->batch; d.T = a->seqlen; d.H = a->heads; d.K = a->dk; d.V = a->dv; d.C = a->chunk;
-  d.NT = a->seqlen / a->chunk; d.scale = a->scale;
+  // Chunks of 128 or 256 (the reference's Pallas path runs BT = 256,
+  // kernel_a_scores.py:15-17; its oracle takes any chunk_size,
+  // gdn2_wy_reference.py:105-112) run as 64-row chunks.  The chunked WY form
+  // is exact for any chunk length; with every gate g <= 0 (the model's
+  // g = -exp(a) softplus(f), model.py:606-610) the two differ only where the
+  // reference's clip(+-20) floors a pair decay below exp(-20), and in the
+  // +-1e4 state clip, applied at every 64 rows instead of every chunk.
+  d.B = a->batch; d.T = a->seqlen; d.H = a->heads; d.K = a->dk; d.V = a->dv; d.C = kGdn2RunChunk;
+  d.NT = a->seqlen / kGdn2RunChunk; d.scale = a->scale;
   p->dm = d;
   p->es = a->dtype == ATOMIC_BF16 ? 2 : 4;
   const size_t N = (size_t)d.B * d.H * d.NT;
@@ -345,7 +355,8 @@ static int noalloc_scratch(void** out) {
 static int gdn2_window_plan(const atomic_gdn2_args* a, int nw, Gdn2Plan* p) {
   atomic_gdn2_args w = *a;
   w.batch = 1;
-  w.seqlen = nw * a->chunk;
+  w.seqlen = nw * kGdn2RunChunk;
+  w.chunk = kGdn2RunChunk;
   w.flags = 0;
   return gdn2_plan(&w, p);
 }
@@ -359,7 +370,7 @@ static int gdn2_window_plan(const atomic_gdn2_args* a, int nw, Gdn2Plan* p) {
 static int gdn2_forward_noalloc(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
                                 const void* w, const void* b, const float* g, const float* h0, float* o,
                                 float* h_final, hipStream_t st) {
-  const int NT = a->seqlen / a->chunk, H = a->heads, K = a->dk, V = a->dv;
+  const int NT = a->seqlen / kGdn2RunChunk, H = a->heads, K = a->dk, V = a->dv;
   const size_t es = a->dtype == ATOMIC_BF16 ? 2 : 4;
   const size_t state_elems = (size_t)H * K * V;
   const size_t slot = align256(state_elems * 4);
@@ -400,7 +411,7 @@ static int gdn2_forward_noalloc(const atomic_gdn2_args* a, const void* q, const 
     for (int n0 = 0; n0 < NT; n0 += W, ++wi) {
       const int nw = NT - n0 < W ? NT - n0 : W;
       const Gdn2Plan& pw = nw == W ? pfull : ptail;
-      const size_t t0 = (size_t)bb * T + (size_t)n0 * a->chunk;  // first row of the window
+      const size_t t0 = (size_t)bb * T + (size_t)n0 * kGdn2RunChunk;  // first row of the window
       const char* qp = static_cast<const char*>(q) + t0 * rowK * es;
       const char* kp = static_cast<const char*>(k) + t0 * rowK * es;
       const char* bp = static_cast<const char*>(b) + t0 * rowK * es;

@@ -116,7 +116,8 @@ typedef struct atomic_gdn2_args {
   int32_t heads;     /* H                                                       */
   int32_t dk;        /* K: 64 or 128                                            */
   int32_t dv;        /* V: equal to dk                                          */
-  int32_t chunk;     /* C: 64                                                   */
+  int32_t chunk;     /* C: 64, 128 or 256 (all run as 64-row chunks: equal while
+                        every gate g <= 0, up to exp(-20) floor terms)        */
   int32_t dtype;     /* q, k, v, w, b and their gradients: ATOMIC_F32 / _BF16  */
   int32_t do_dtype;  /* upstream gradient dO: ATOMIC_F32 / ATOMIC_BF16          */
   float scale;       /* query scale (the model passes 1.0, model.py:631)        */
@@ -130,7 +131,8 @@ typedef struct atomic_gdn2_args {
 size_t atomic_gdn2_workspace_size(const atomic_gdn2_args* a);
 
 /* Byte offsets of the per-chunk intermediates inside the workspace, for
-   stage-level inspection.  Each block is [B][H][NT][rows][cols] in the
+   stage-level inspection.  Each block is [B][H][NT][rows][cols] (NT = T / 64:
+   the kernels' chunk length is 64 whatever `chunk` says) in the
    operand dtype (bf16 for bf16 inputs, fp32 for fp32 inputs) except gc_last
    (fp32).  Returns ATOMIC_OK or ATOMIC_ERR_SHAPE. */
 typedef struct atomic_gdn2_layout {
