@@ -227,6 +227,105 @@ __global__ __launch_bounds__(256) void norm_gate_bwd(NgDims dm, const float* __r
   }
 }
 
+// The same gradients for wide rows (d >= 4096): one row at a time per
+// workgroup, wave w holding pieces [w NPW, (w + 1) NPW) of it (channel
+// 8 (lane + 64 s)), so a lane keeps NPL / 4 pieces of each array instead of
+// NPL.  The row's two sums (x^2 and d_n w x) cross the four waves through
+// LDS, alternating buffers, one barrier each; every wave's weight-gradient
+// partial sums cover its own channels, so the workgroup's partial row needs
+// no combine.
+template <int VAR, int NPL>
+__global__ __launch_bounds__(256) void norm_gate_bwd_wide(NgDims dm, const float* __restrict__ x,
+                                                          const bf16* __restrict__ gate,
+                                                          const float* __restrict__ weight,
+                                                          const bf16* __restrict__ dout,
+                                                          float* __restrict__ dx, bf16* __restrict__ dgate,
+                                                          float* __restrict__ part) {
+  constexpr int NPW = NPL / 4;
+  static_assert(NPL % 4 == 0, "whole pieces per wave");
+  __shared__ float red[2][4];
+  const int lane = lane_id(), wv = wave_id();
+  float dw[NPW][8];
+#pragma unroll
+  for (int s = 0; s < NPW; ++s)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dw[s][j] = 0.f;
+  for (int row = blockIdx.x; row < dm.rows; row += gridDim.x) {
+    const size_t ro = (size_t)row * dm.d;
+    float xr[NPW][8], gr[NPW][8], du[NPW][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int s = 0; s < NPW; ++s) {
+      const int c = 8 * (lane + 64 * (wv * NPW + s));
+      load8(x + ro + c, xr[s]);
+      load8(gate + ro + c, gr[s]);
+      load8(dout + ro + c, du[s]);
+    }
+#pragma unroll
+    for (int s = 0; s < NPW; ++s)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (VAR == kNgMamba2) xr[s][j] = bf16r(xr[s][j]);
+        ss += xr[s][j] * xr[s][j];
+      }
+    ss = wave_sum(ss);
+    if (lane == 0) red[0][wv] = ss;
+    __syncthreads();
+    const float inv = rsqrtf((red[0][0] + red[0][1] + red[0][2] + red[0][3]) / (float)dm.d + dm.eps);
+    float dn[NPW][8];
+    float dot = 0.f;
+#pragma unroll
+    for (int s = 0; s < NPW; ++s) {
+      const int c = 8 * (lane + 64 * (wv * NPW + s));
+      float w8[8], dg8[8];
+      load8(weight + c, w8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float mul = inv * w8[j];
+        const float nb = bf16r(xr[s][j] * mul);
+        const float g = gr[s][j];
+        const float gc = gate_in<VAR>(g);
+        const float sg = sigmoidf_(gc);
+        const float sl = bf16r(gc * sg);
+        float u = du[s][j];
+        if (VAR == kNgMamba2) {  // clip(+-3e2) of the product (model.py:524)
+          const float pr = bf16r(nb * sl);
+          u *= clip_grad(pr, 3e2f);
+        }
+        const float d_nb = bf16r(u * sl);
+        const float d_sl = bf16r(u * nb);
+        float d_g = bf16r(d_sl * (sg * (1.f + gc * (1.f - sg))));
+        if (VAR == kNgGdn2) d_g *= clip_grad(g, 1e2f);  // clip(+-1e2) (model.py:613)
+        dg8[j] = d_g;
+        dn[s][j] = d_nb;
+        dot += d_nb * w8[j] * xr[s][j];
+        dw[s][j] += d_nb * xr[s][j] * inv;
+      }
+      store8(dgate + ro + c, dg8);
+    }
+    dot = wave_sum(dot);
+    if (lane == 0) red[1][wv] = dot;
+    __syncthreads();
+    const float dsum = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    const float k3 = inv * inv * inv * dsum / (float)dm.d;
+#pragma unroll
+    for (int s = 0; s < NPW; ++s) {
+      const int c = 8 * (lane + 64 * (wv * NPW + s));
+      float w8[8], o8[8];
+      load8(weight + c, w8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        o8[j] = dn[s][j] * w8[j] * inv - xr[s][j] * k3;
+        if (VAR == kNgMamba2) o8[j] = bf16r(o8[j]);
+      }
+      store8(dx + ro + c, o8);
+    }
+  }
+  float* pw = part + (size_t)blockIdx.x * dm.d;
+#pragma unroll
+  for (int s = 0; s < NPW; ++s) store8(pw + 8 * (lane + 64 * (wv * NPW + s)), dw[s]);
+}
+
 // dweight[c] = sum over the partial rows: 64 columns per workgroup of 16
 // waves; wave w takes the rows w, w + 16, ... with eight loads in flight,
 // then LDS combines the 16 sums.
@@ -340,12 +439,23 @@ extern "C" int atomic_norm_gate_bwd(const atomic_norm_gate_args* a, const float*
   rc = ng_dispatch(a->dim, [&](auto Nc) {
     constexpr int NPL = decltype(Nc)::value;
     return L("norm_gate_bwd", [&] {
-      if (a->variant == ATOMIC_NORM_GATE_GDN2)
-        hipLaunchKernelGGL((norm_gate_bwd<kNgGdn2, NPL>), dim3((unsigned)nparts), dim3(256), 0, st,
-                           dm, x, (const bf16*)gate, weight, (const bf16*)dout, dx, (bf16*)dgate, part);
-      else
-        hipLaunchKernelGGL((norm_gate_bwd<kNgMamba2, NPL>), dim3((unsigned)nparts), dim3(256), 0, st,
-                           dm, x, (const bf16*)gate, weight, (const bf16*)dout, dx, (bf16*)dgate, part);
+      // rows of d >= 4096 take a workgroup each (the per-lane arrays of one
+      // wave per row would not fit the registers)
+      if constexpr (NPL >= 8) {
+        if (a->variant == ATOMIC_NORM_GATE_GDN2)
+          hipLaunchKernelGGL((norm_gate_bwd_wide<kNgGdn2, NPL>), dim3((unsigned)nparts), dim3(256), 0, st,
+                             dm, x, (const bf16*)gate, weight, (const bf16*)dout, dx, (bf16*)dgate, part);
+        else
+          hipLaunchKernelGGL((norm_gate_bwd_wide<kNgMamba2, NPL>), dim3((unsigned)nparts), dim3(256), 0, st,
+                             dm, x, (const bf16*)gate, weight, (const bf16*)dout, dx, (bf16*)dgate, part);
+      } else {
+        if (a->variant == ATOMIC_NORM_GATE_GDN2)
+          hipLaunchKernelGGL((norm_gate_bwd<kNgGdn2, NPL>), dim3((unsigned)nparts), dim3(256), 0, st,
+                             dm, x, (const bf16*)gate, weight, (const bf16*)dout, dx, (bf16*)dgate, part);
+        else
+          hipLaunchKernelGGL((norm_gate_bwd<kNgMamba2, NPL>), dim3((unsigned)nparts), dim3(256), 0, st,
+                             dm, x, (const bf16*)gate, weight, (const bf16*)dout, dx, (bf16*)dgate, part);
+      }
     });
   });
   if (rc) return rc;

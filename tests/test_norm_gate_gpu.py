@@ -28,7 +28,9 @@ def _inputs(rows, d, seed, gate_scale):
     (37, 512, 3.0),      # ragged row count (last workgroup partly idle)
     (256, 2048, 3.0),    # the benchmark's model dimension (H 16 x 128)
     (64, 1536, 60.0),    # three pieces per lane; gates beyond the +-1e2 clip
-    (9, 8192, 3.0),      # the largest supported dimension
+    (9, 8192, 3.0),      # the largest supported dimension (a workgroup per row in the backward)
+    (1100, 4096, 3.0),   # the smallest workgroup-per-row width; rows beyond the 512 partial rows
+    (13, 6144, 60.0),    # twelve pieces per row: three per wave
 ])
 def test_epilogue_matches_oracle(variant, ovar, rows, d, gate_scale):
     banner(f"norm_gate {ovar} rows={rows} d={d} gate_scale={gate_scale}")
