@@ -60,6 +60,12 @@ class Mamba2PrologueArgs(ctypes.Structure):
                 ("profile", ctypes.c_void_p)]
 
 
+class Mamba2ProjArgs(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_int32), ("seqlen", ctypes.c_int32), ("heads", ctypes.c_int32),
+                ("headdim", ctypes.c_int32), ("dstate", ctypes.c_int32), ("dconv", ctypes.c_int32),
+                ("in_stride", ctypes.c_int64), ("profile", ctypes.c_void_p)]
+
+
 class PrologueArgs(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int32), ("seqlen", ctypes.c_int32), ("heads", ctypes.c_int32),
                 ("dhead", ctypes.c_int32), ("dconv", ctypes.c_int32), ("eps", ctypes.c_float),
@@ -179,6 +185,9 @@ _SIGS = {
     "atomic_mamba2_prologue_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(Mamba2PrologueArgs)]),
     "atomic_mamba2_prologue_fwd": (ctypes.c_int, [ctypes.POINTER(Mamba2PrologueArgs)] + [_P] * 12 + [_P]),
     "atomic_mamba2_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(Mamba2PrologueArgs)] + [_P] * 19 + [_P, ctypes.c_size_t, _P]),
+    "atomic_mamba2_proj_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(Mamba2ProjArgs), ctypes.c_int]),
+    "atomic_mamba2_proj_fwd": (ctypes.c_int, [ctypes.POINTER(Mamba2ProjArgs)] + [_P] * 16 + [_P, ctypes.c_size_t, _P]),
+    "atomic_mamba2_proj_bwd": (ctypes.c_int, [ctypes.POINTER(Mamba2ProjArgs)] + [_P] * 24 + [_P, ctypes.c_size_t, _P]),
 }
 
 _lib = None

@@ -24,6 +24,7 @@
 #include "../../include/atomic_hybrid.h"
 #include "common.hpp"
 #include "launch.hpp"
+#include "proj_gemm.hpp"
 
 namespace ah {
 
@@ -34,6 +35,7 @@ constexpr int kTileB = 32;     // tokens per wave, backward
 struct PlDims {
   int B, L, H, dh, d;
   float eps;
+  int ldi;  // elements between consecutive tokens of the convolutions' input (>= d)
 };
 
 __device__ __forceinline__ float bfr(float x) { return (float)(bf16)x; }
@@ -137,12 +139,12 @@ __global__ __launch_bounds__(256) void prologue_conv_fwd(PlDims dm, const bf16* 
   const int c = cb * 512 + 8 * lane, t0 = tile * kTileF;
   ConvW<8> W;
   W.load(conv_w, conv_b, c);
-  const bf16* u = lin + (size_t)b * dm.L * dm.d + c;
+  const bf16* u = lin + (size_t)b * dm.L * dm.ldi + c;
   bf16* o = out + (size_t)b * dm.L * dm.d + c;
   // every input row of the tile (three before it) requested at once
   u32x4 rows[kTileF + kDc - 1];
 #pragma unroll
-  for (int r = 0; r < kTileF + kDc - 1; ++r) rows[r] = row_or_zero(u, t0 - (kDc - 1) + r, dm.d);
+  for (int r = 0; r < kTileF + kDc - 1; ++r) rows[r] = row_or_zero(u, t0 - (kDc - 1) + r, dm.ldi);
   float win[kDc][8];
 #pragma unroll
   for (int tp = 0; tp < kDc - 1; ++tp) unpack8(rows[tp], win[tp]);
@@ -309,7 +311,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   const int c = cb * 64 * CPL + CPL * lane, t0 = tile * kTileB;
   ConvW<CPL> W;
   W.load(conv_w, conv_b, c);
-  const bf16* u = lin + (size_t)b * dm.L * dm.d + c;
+  const bf16* u = lin + (size_t)b * dm.L * dm.ldi + c;
   const bf16* dy = dout + (size_t)b * dm.L * dm.d + c;
   bf16* du = dlin + (size_t)b * dm.L * dm.d + c;
   float acc[NV][CPL];
@@ -322,7 +324,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   const int t_hi = min(t0 + kTileB + kDc - 2, dm.L - 1);
   float win[kDc][CPL], en[kDc - 1][CPL];
 #pragma unroll
-  for (int tp = 0; tp < kDc; ++tp) unpack4(row4_or_zero(u, t_hi - (kDc - 1) + tp, dm.d), win[tp]);
+  for (int tp = 0; tp < kDc; ++tp) unpack4(row4_or_zero(u, t_hi - (kDc - 1) + tp, dm.ldi), win[tp]);
 #pragma unroll
   for (int k = 0; k < kDc - 1; ++k)
 #pragma unroll
@@ -331,7 +333,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   for (int t = t_hi; t >= t0; --t) {
     float g4[CPL], e[CPL];
     const u32x2 rdy = *reinterpret_cast<const u32x2*>(dy + (size_t)t * dm.d);
-    const u32x2 rnext = row4_or_zero(u, t - kDc, dm.d);
+    const u32x2 rnext = row4_or_zero(u, t - kDc, dm.ldi);
     unpack4(rdy, g4);
     conv_out_vjp<MODE, G, CPL>(W, win, g4, dm.eps, e);
     if (t < t0 + kTileB) {
@@ -566,7 +568,7 @@ static int pl_check(const atomic_gdn2_prologue_args* a) {
 }
 
 static PlDims pl_dims(const atomic_gdn2_prologue_args* a) {
-  return PlDims{a->batch, a->seqlen, a->heads, a->dhead, a->heads * a->dhead, a->eps};
+  return PlDims{a->batch, a->seqlen, a->heads, a->dhead, a->heads * a->dhead, a->eps, a->heads * a->dhead};
 }
 
 // workspace: conv partial rows [3][B][L / 128][d][5], then the da partials
@@ -713,7 +715,7 @@ static int m2p_check(const atomic_mamba2_prologue_args* a) {
   return ATOMIC_OK;
 }
 static PlDims m2p_dims(const atomic_mamba2_prologue_args* a) {
-  return PlDims{a->batch, a->seqlen, a->heads, 128, a->heads * a->headdim, 0.f};
+  return PlDims{a->batch, a->seqlen, a->heads, 128, a->heads * a->headdim, 0.f, a->heads * a->headdim};
 }
 // workspace: x's conv partial rows [B][L / 128][d][5], then the summed [d][5]
 static size_t m2p_ws(const PlDims& d, size_t* sums_off) {
@@ -798,5 +800,179 @@ extern "C" int atomic_mamba2_prologue_bwd(const atomic_mamba2_prologue_args* a, 
     // one conv: the split kernel's (which, channel) range is just the channels
     hipLaunchKernelGGL(prologue_param_split1, dim3((unsigned)((dm.d + 255) / 256)), dim3(256), 0, st, dm.d, sums,
                        dconv_w, dconv_b);
+  });
+}
+
+// ------------------------------------------------- Mamba2 prologue with its projections
+static int m2x_check(const atomic_mamba2_proj_args* a) {
+  if (!a) return ATOMIC_ERR_NULL;
+  if (a->batch <= 0 || a->seqlen <= 0 || a->heads <= 0 || a->headdim <= 0 || a->dstate <= 0)
+    return ATOMIC_ERR_SHAPE;
+  const long long d = (long long)a->heads * a->headdim;
+  if (a->dconv != kDc || d % 512 != 0 || a->seqlen % (4 * kTileB) != 0 || a->dstate % 64 != 0)
+    return ATOMIC_ERR_SHAPE;
+  if (a->in_stride < d || a->in_stride % 8 != 0 || a->in_stride > (1LL << 30)) return ATOMIC_ERR_SHAPE;
+  return ATOMIC_OK;
+}
+
+// Workspace: the packed bf16 weights [W_dt | W_B | W_C] (either layout); for
+// the backward also dPre [M][d + 2n] bf16, the convolution path's dx [M][d]
+// bf16, the weight-gradient partials [splits][d][d + 2n] fp32, the b_dt
+// partials [M / 32][d] and sums [d] fp32, and the convolution's partial rows.
+struct M2xPlan {
+  PlDims dm;
+  int M, d, n, nt, splits;
+  size_t o_w, o_dpre, o_dxc, o_dw, o_dbp, o_dbs, o_conv, o_convsum, total;
+};
+static M2xPlan m2x_plan(const atomic_mamba2_proj_args* a, bool bwd) {
+  M2xPlan p;
+  p.d = a->heads * a->headdim;
+  p.n = a->dstate;
+  p.nt = p.d + 2 * p.n;
+  p.M = a->batch * a->seqlen;
+  p.dm = PlDims{a->batch, a->seqlen, a->heads, 128, p.d, 0.f, (int)a->in_stride};
+  // row splits of the weight-gradient GEMM: enough workgroups to fill the chip,
+  // each split a multiple of 64 rows
+  const int tiles = (p.d / kGT) * (p.nt / kGT);
+  int s = 1;
+  while (s * tiles < 1024 && p.M % (2 * s * kGK) == 0) s *= 2;
+  p.splits = s;
+  auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
+  size_t off = 0;
+  auto take = [&](size_t bytes) { const size_t o = off; off += al(bytes); return o; };
+  const size_t M = p.M, d = p.d, nt = p.nt;
+  p.o_w = take(d * nt * 2);
+  p.o_dpre = p.o_dxc = p.o_dw = p.o_dbp = p.o_dbs = p.o_conv = p.o_convsum = 0;
+  if (bwd) {
+    p.o_dpre = take(M * nt * 2);
+    p.o_dxc = take(M * d * 2);
+    p.o_dw = take((size_t)p.splits * d * nt * 4);
+    p.o_dbp = take((M / 32) * d * 4);
+    p.o_dbs = take(d * 4);
+    size_t so;
+    const size_t cb = m2p_ws(p.dm, &so);
+    p.o_conv = take(cb);
+    p.o_convsum = p.o_conv + so;
+  }
+  p.total = off;
+  return p;
+}
+
+extern "C" size_t atomic_mamba2_proj_workspace_size(const atomic_mamba2_proj_args* a, int backward) {
+  if (m2x_check(a) != ATOMIC_OK) return 0;
+  return m2x_plan(a, backward != 0).total;
+}
+
+extern "C" int atomic_mamba2_proj_fwd(const atomic_mamba2_proj_args* a, const void* x_bc, const float* conv_w,
+                                      const float* conv_b, const float* w_dt, const float* b_dt,
+                                      const float* w_b, const float* w_c, const float* a_log, void* x,
+                                      void* dt, void* B, void* C, float* A, void* dt_pre, void* b_pre,
+                                      void* c_pre, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = m2x_check(a);
+  if (rc) return rc;
+  if (!x_bc || !conv_w || !conv_b || !w_dt || !b_dt || !w_b || !w_c || !a_log || !x || !dt || !B || !C || !A)
+    return ATOMIC_ERR_NULL;
+  const M2xPlan p = m2x_plan(a, false);
+  if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
+  bf16* wt = reinterpret_cast<bf16*>(static_cast<unsigned char*>(workspace) + p.o_w);
+  hipStream_t st = (hipStream_t)stream;
+  Launch L{a->profile, st};
+  rc = L("m2p_pack_t", [&] {
+    hipLaunchKernelGGL(m2p_pack_t, dim3((unsigned)((p.nt / 64) * (p.d / 64))), dim3(256), 0, st, p.d, p.n, w_dt,
+                       w_b, w_c, wt);
+  });
+  if (rc) return rc;
+  rc = L("prologue_conv_fwd", [&] {
+    const unsigned nconv = (unsigned)(((size_t)p.dm.B * (p.dm.L / kTileF) * (p.d / 512) + 3) / 4);
+    hipLaunchKernelGGL((prologue_conv_fwd<kPlain, 128>), dim3(nconv), dim3(256), 0, st, p.dm, (const bf16*)x_bc,
+                       conv_w, conv_b, (bf16*)x);
+  });
+  if (rc) return rc;
+  rc = L("m2p_proj_gemm", [&] {
+    const GemmNT g{(const bf16*)x_bc, (long long)a->in_stride, wt, (long long)p.d, p.M, p.nt, p.d};
+    const M2ProjEpi e{p.d, p.n, b_dt, (bf16*)dt, (bf16*)B, (bf16*)C, (bf16*)dt_pre, (bf16*)b_pre, (bf16*)c_pre};
+    hipLaunchKernelGGL((gemm_nt<M2ProjEpi>), dim3((unsigned)((p.M / kGT) * (p.nt / kGT))), dim3(256), 0, st, g, e);
+  });
+  if (rc) return rc;
+  return L("m2_prologue_elem_fwd", [&] {  // A only (no element ranges)
+    hipLaunchKernelGGL(m2_prologue_elem_fwd, dim3(1), dim3(256), 0, st, (size_t)0, (size_t)0, a->heads,
+                       (const bf16*)nullptr, (const bf16*)nullptr, (const bf16*)nullptr, a_log, (bf16*)nullptr,
+                       (bf16*)nullptr, (bf16*)nullptr, A);
+  });
+}
+
+extern "C" int atomic_mamba2_proj_bwd(const atomic_mamba2_proj_args* a, const void* x_bc, const float* conv_w,
+                                      const float* conv_b, const float* w_dt, const float* b_dt,
+                                      const float* w_b, const float* w_c, const float* a_log,
+                                      const void* dt_pre, const void* b_pre, const void* c_pre, const void* dx,
+                                      const void* ddt, const void* dB, const void* dC, const float* dA,
+                                      void* dx_bc, float* dconv_w, float* dconv_b, float* dw_dt, float* db_dt,
+                                      float* dw_b, float* dw_c, float* da_log, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  int rc = m2x_check(a);
+  if (rc) return rc;
+  if (!x_bc || !conv_w || !conv_b || !w_dt || !b_dt || !w_b || !w_c || !a_log || !dt_pre || !b_pre || !c_pre ||
+      !dx || !ddt || !dB || !dC || !dA || !dx_bc || !dconv_w || !dconv_b || !dw_dt || !db_dt || !dw_b || !dw_c ||
+      !da_log)
+    return ATOMIC_ERR_NULL;
+  const M2xPlan p = m2x_plan(a, true);
+  if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
+  unsigned char* wsb = static_cast<unsigned char*>(workspace);
+  bf16* w = reinterpret_cast<bf16*>(wsb + p.o_w);
+  bf16* dpre = reinterpret_cast<bf16*>(wsb + p.o_dpre);
+  bf16* dxc = reinterpret_cast<bf16*>(wsb + p.o_dxc);
+  float* dwp = reinterpret_cast<float*>(wsb + p.o_dw);
+  float* dbp = reinterpret_cast<float*>(wsb + p.o_dbp);
+  float* dbs = reinterpret_cast<float*>(wsb + p.o_dbs);
+  float* cpart = reinterpret_cast<float*>(wsb + p.o_conv);
+  float* csum = reinterpret_cast<float*>(wsb + p.o_convsum);
+  hipStream_t st = (hipStream_t)stream;
+  Launch L{a->profile, st};
+  const PlDims& dm = p.dm;
+  rc = L("m2p_pack", [&] {
+    hipLaunchKernelGGL(m2p_pack, dim3((unsigned)(((size_t)p.d * p.nt + 255) / 256)), dim3(256), 0, st, p.d, p.n,
+                       w_dt, w_b, w_c, w);
+  });
+  if (rc) return rc;
+  rc = L("m2p_vjp", [&] {
+    const size_t nth = (size_t)(p.M / 32) * (p.nt / 8);
+    hipLaunchKernelGGL(m2p_vjp, dim3((unsigned)((nth + 255) / 256)), dim3(256), 0, st, p.M, p.d, p.n, a->heads,
+                       (const bf16*)dt_pre, (const bf16*)b_pre, (const bf16*)c_pre, a_log, (const bf16*)ddt,
+                       (const bf16*)dB, (const bf16*)dC, dA, dpre, dbp, da_log);
+  });
+  if (rc) return rc;
+  const int ngrp = dm.L / (4 * kTileB);
+  rc = L("prologue_conv_bwd", [&] {
+    hipLaunchKernelGGL((prologue_conv_bwd<kPlain, 128>), dim3((unsigned)((size_t)dm.B * ngrp * (dm.d / (64 * kCplB)))),
+                       dim3(256), 0, st, dm, (const bf16*)x_bc, conv_w, conv_b, (const bf16*)dx, dxc, cpart);
+  });
+  if (rc) return rc;
+  rc = L("m2p_dx_gemm", [&] {
+    const GemmNT g{dpre, (long long)p.nt, w, (long long)p.nt, p.M, p.d, p.nt};
+    const M2DxEpi e{dxc, p.d, (bf16*)dx_bc, (long long)a->in_stride};
+    hipLaunchKernelGGL((gemm_nt<M2DxEpi>), dim3((unsigned)((p.M / kGT) * (p.d / kGT))), dim3(256), 0, st, g, e);
+  });
+  if (rc) return rc;
+  rc = L("m2p_dw_gemm", [&] {
+    const GemmTN g{(const bf16*)x_bc, (long long)a->in_stride, dpre, (long long)p.nt, p.d, p.nt, p.M / p.splits, dwp};
+    hipLaunchKernelGGL(gemm_tn, dim3((unsigned)(p.splits * (p.d / kGT) * (p.nt / kGT))), dim3(256), 0, st, g);
+  });
+  if (rc) return rc;
+  rc = L("prologue_colsum", [&] {
+    const int ncol = dm.d * (kDc + 1);
+    hipLaunchKernelGGL(prologue_colsum, dim3((unsigned)((ncol + 63) / 64)), dim3(1024), 0, st, ncol, dm.B * ngrp,
+                       cpart, csum);
+    hipLaunchKernelGGL(prologue_colsum, dim3((unsigned)((p.d + 63) / 64)), dim3(1024), 0, st, p.d, p.M / 32, dbp,
+                       dbs);
+  });
+  if (rc) return rc;
+  rc = L("prologue_param_split", [&] {
+    hipLaunchKernelGGL(prologue_param_split1, dim3((unsigned)((dm.d + 255) / 256)), dim3(256), 0, st, dm.d, csum,
+                       dconv_w, dconv_b);
+  });
+  if (rc) return rc;
+  return L("m2p_dw_finish", [&] {
+    hipLaunchKernelGGL(m2p_dw_finish, dim3((unsigned)(((size_t)p.d * p.nt + 255) / 256)), dim3(256), 0, st, p.d,
+                       p.n, p.splits, dwp, dbs, dw_dt, dw_b, dw_c, db_dt);
   });
 }

@@ -424,6 +424,68 @@ int atomic_mamba2_prologue_bwd(const atomic_mamba2_prologue_args* a, const void*
                                void* ddt_pre, void* db_pre, void* dc_pre, float* da_log,
                                void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Mamba2 prologue with its projections (Mamba2J.__call__, reference
+ * model.py:405-433): from the in_proj output, read in place (its x_bc half,
+ * the first d_inner columns of each [2 d_inner] row after jnp.split, :405-406)
+ *   dt_pre = bf16(x_bc W_dt) + bf16(b_dt)      (dt_proj, :427)
+ *   b_pre  = bf16(x_bc W_B)   c_pre = bf16(x_bc W_C)   (B_proj / C_proj, :425-426)
+ * (bf16 products accumulated in fp32, as Dense(dtype=bfloat16)), then the
+ * element-wise prologue of atomic_mamba2_prologue_fwd.  The three
+ * projections are one MFMA GEMM of x_bc against [W_dt | W_B | W_C] whose
+ * epilogue applies softplus / clip / sanitise; x_bc is read with its row
+ * stride (no copy of the split).  Weights are the model's fp32 parameters in
+ * the Dense layout ([in][out]): W_dt [d_inner][d_inner], b_dt [d_inner],
+ * W_B and W_C [d_inner][N].  This pair has no single-function counterpart in
+ * the reference (the block is inline in Mamba2J.__call__).
+ */
+typedef struct atomic_mamba2_proj_args {
+  int32_t batch;      /* B                                                  */
+  int32_t seqlen;     /* L: a multiple of 128                               */
+  int32_t heads;      /* H                                                  */
+  int32_t headdim;    /* P; d_inner = H * P a multiple of 512               */
+  int32_t dstate;     /* N: a multiple of 64                                */
+  int32_t dconv;      /* 4 (the model's)                                    */
+  int64_t in_stride;  /* elements between consecutive tokens of x_bc and of
+                         dx_bc (2 d_inner for the in_proj output); >= d_inner,
+                         a multiple of 8                                    */
+  atomic_profile* profile;  /* optional per-kernel event timing, or NULL  */
+} atomic_mamba2_proj_args;
+
+/* Bytes of workspace the forward (backward = 0) or backward (1) needs; 0 for
+ * unsupported args. */
+size_t atomic_mamba2_proj_workspace_size(const atomic_mamba2_proj_args* a, int backward);
+
+/*
+ * Forward.
+ *   x_bc : [B * L] rows of in_stride bf16 (d_inner used)
+ *   x, dt : [B, L, H, P] bf16   B, C : [B, L, N] bf16   A : [H] fp32
+ *   dt_pre : [B, L, d_inner] bf16, b_pre / c_pre : [B, L, N] bf16 -- the
+ *   projection outputs, written when non-NULL (the backward takes them)
+ */
+int atomic_mamba2_proj_fwd(const atomic_mamba2_proj_args* a, const void* x_bc, const float* conv_w,
+                           const float* conv_b, const float* w_dt, const float* b_dt, const float* w_b,
+                           const float* w_c, const float* a_log, void* x, void* dt, void* B, void* C,
+                           float* A, void* dt_pre, void* b_pre, void* c_pre, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/*
+ * Backward for the cotangents dx, ddt, dB, dC (bf16) and dA (fp32) of the
+ * forward's outputs.  dx_bc (rows of in_stride, d_inner columns written) is
+ * x_bc's whole gradient: the convolution path's plus the three projections'.
+ * Parameter gradients in fp32: dconv_w [d_inner][dconv], dconv_b [d_inner],
+ * dw_dt [d_inner][d_inner], db_dt [d_inner], dw_b / dw_c [d_inner][N],
+ * da_log [H]; the projection gradients are bf16-rounded like the reference's
+ * bf16 dot / bias VJPs before the cast to the fp32 parameters.
+ */
+int atomic_mamba2_proj_bwd(const atomic_mamba2_proj_args* a, const void* x_bc, const float* conv_w,
+                           const float* conv_b, const float* w_dt, const float* b_dt, const float* w_b,
+                           const float* w_c, const float* a_log, const void* dt_pre, const void* b_pre,
+                           const void* c_pre, const void* dx, const void* ddt, const void* dB, const void* dC,
+                           const float* dA, void* dx_bc, float* dconv_w, float* dconv_b, float* dw_dt,
+                           float* db_dt, float* dw_b, float* dw_c, float* da_log, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

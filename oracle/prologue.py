@@ -176,3 +176,56 @@ def mamba2_prologue_grads(inputs, cotangents, heads, exact=False):
     outs = mamba2_prologue(*leaves, heads, exact=exact)
     torch.autograd.backward(outs, [c.to(o.dtype) for c, o in zip(cotangents, outs)])
     return tuple(t.grad for t in leaves)
+
+
+class _DotBf16(torch.autograd.Function):
+    """The product of flax ``Dense(dtype=bfloat16)`` (model.py:425-427): x @ W
+    with float32 accumulation rounded once to the operand dtype (float64
+    throughout in exact mode), and the same for both VJP products."""
+
+    @staticmethod
+    def forward(ctx, x, w):
+        ctx.save_for_backward(x, w)
+        acc = torch.float64 if x.dtype == torch.float64 else torch.float32
+        return (x.to(acc) @ w.to(acc)).to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, w = ctx.saved_tensors
+        acc = torch.float64 if x.dtype == torch.float64 else torch.float32
+        gx = (g.to(acc) @ w.to(acc).t()).to(x.dtype)
+        gw = (x.to(acc).reshape(-1, x.shape[-1]).t() @ g.to(acc).reshape(-1, g.shape[-1])).to(w.dtype)
+        return gx, gw
+
+
+def dense(x, w, b=None, exact=False):
+    """``nn.Dense(out, use_bias=b is not None, dtype=bfloat16)(x)``: the float32
+    kernel [in, out] and bias cast to bf16 (autograd casts their cotangents
+    back to float32), the product rounded once, the bias added in bf16."""
+    dt = torch.float64 if exact else torch.bfloat16
+    y = _DotBf16.apply(x, w.to(dt))
+    if b is not None:
+        y = y + b.to(dt)
+    return y
+
+
+def mamba2_projections(x_bc, w_dt, b_dt, w_b, w_c, exact=False):
+    """dt_proj, B_proj, C_proj of Mamba2J (model.py:425-427) on x_bc, the first
+    half of the in_proj output (:405-406): (dt_pre, b_pre, c_pre)."""
+    return dense(x_bc, w_dt, b_dt, exact), dense(x_bc, w_b, None, exact), dense(x_bc, w_c, None, exact)
+
+
+def mamba2_proj_prologue(x_bc, conv_w, conv_b, w_dt, b_dt, w_b, w_c, a_log, heads, exact=False):
+    """Mamba2J's input preparation with its projections (model.py:405-433):
+    (x, dt, B, C, A) as ``mamba2_prologue`` of the projection outputs."""
+    dt_pre, b_pre, c_pre = mamba2_projections(x_bc, w_dt, b_dt, w_b, w_c, exact)
+    return mamba2_prologue(x_bc, conv_w, conv_b, dt_pre, b_pre, c_pre, a_log, heads, exact)
+
+
+def mamba2_proj_prologue_grads(inputs, cotangents, heads, exact=False):
+    """Gradients of ``mamba2_proj_prologue`` w.r.t. (x_bc, conv_w, conv_b, w_dt,
+    b_dt, w_b, w_c, a_log) for cotangents (dx, ddt, dB, dC, dA)."""
+    leaves = [t.detach().clone().requires_grad_(True) for t in inputs]
+    outs = mamba2_proj_prologue(*leaves, heads, exact=exact)
+    torch.autograd.backward(outs, [c.to(o.dtype) for c, o in zip(cotangents, outs)])
+    return tuple(t.grad for t in leaves)

@@ -25,7 +25,8 @@ def test_every_header_function_has_a_ctypes_signature():
 STRUCTS = [(_lib.Gdn2Args, "atomic_gdn2_args"), (_lib.Mamba2Args, "atomic_mamba2_args"),
            (_lib.Gdn2Layout, "atomic_gdn2_layout"), (_lib.AtomicProfile, "atomic_profile"),
            (_lib.NormGateArgs, "atomic_norm_gate_args"), (_lib.PrologueArgs, "atomic_gdn2_prologue_args"),
-           (_lib.Mamba2PrologueArgs, "atomic_mamba2_prologue_args")]
+           (_lib.Mamba2PrologueArgs, "atomic_mamba2_prologue_args"),
+           (_lib.Mamba2ProjArgs, "atomic_mamba2_proj_args")]
 
 
 def _header_fields(cname):
@@ -83,3 +84,13 @@ def test_workspace_size_rejects_bad_shapes_without_a_gpu():
     assert lib.atomic_mamba2_workspace_size(ctypes.byref(m_ok)) > 0
     m_bad = _lib.Mamba2Args(1, 256, 2, 64, 128, 128, _lib.ATOMIC_F32, _lib.ATOMIC_BF16, 0, None)
     assert lib.atomic_mamba2_workspace_size(ctypes.byref(m_bad)) == 0
+
+    p_ok = _lib.Mamba2ProjArgs(1, 128, 4, 128, 64, 4, 1024, None)
+    assert lib.atomic_mamba2_proj_workspace_size(ctypes.byref(p_ok), 0) > 0
+    assert lib.atomic_mamba2_proj_workspace_size(ctypes.byref(p_ok), 1) > \
+        lib.atomic_mamba2_proj_workspace_size(ctypes.byref(p_ok), 0)
+    for bad in (_lib.Mamba2ProjArgs(1, 128, 4, 128, 32, 4, 1024, None),    # N not a multiple of 64
+                _lib.Mamba2ProjArgs(1, 128, 4, 128, 64, 4, 500, None),     # stride below d_inner
+                _lib.Mamba2ProjArgs(1, 128, 4, 128, 64, 4, 1026, None),    # stride not a multiple of 8
+                _lib.Mamba2ProjArgs(1, 96, 4, 128, 64, 4, 1024, None)):    # L not a multiple of 128
+        assert lib.atomic_mamba2_proj_workspace_size(ctypes.byref(bad), 1) == 0

@@ -148,3 +148,67 @@ def test_mamba2_prologue_closed_forms():
     ident[1], ident[2] = cw, torch.zeros_like(ins[2])
     assert rel_err(op.mamba2_prologue(*ident, H, exact=True)[0],
                    torch.nn.functional.silu(ins[0]).view(B, L, H, P)) < 1e-12
+
+
+def _m2x_inputs(B, L, H, P, N, seed, dtype=F64):
+    g = torch.Generator().manual_seed(seed)
+    d = H * P
+    r = lambda *s: torch.randn(*s, generator=g, dtype=F64)
+    x_bc = r(B, L, d).to(dtype)
+    pd = F64 if dtype == F64 else torch.float32   # the model's parameters are float32
+    ps = [0.5 * r(d, 4), 0.1 * r(d), r(d, d) / d ** 0.5, r(d) - 1.0, r(d, N) / d ** 0.5, r(d, N) / d ** 0.5, r(H)]
+    return [x_bc] + [t.to(pd) for t in ps]
+
+
+def test_mamba2_proj_prologue_autograd_matches_finite_differences():
+    """The projections composed with the element-wise prologue: every input's
+    gradient (x_bc through four paths, the Dense kernels and bias) against
+    central differences in float64."""
+    B, L, H, P, N = 1, 5, 2, 2, 3
+    ins = _m2x_inputs(B, L, H, P, N, 21)
+    g = torch.Generator().manual_seed(22)
+    cots = [torch.randn(B, L, H, P, generator=g, dtype=F64), torch.randn(B, L, H, P, generator=g, dtype=F64),
+            torch.randn(B, L, N, generator=g, dtype=F64), torch.randn(B, L, N, generator=g, dtype=F64),
+            torch.randn(H, generator=g, dtype=F64)]
+    grads = op.mamba2_proj_prologue_grads(ins, cots, H, exact=True)
+
+    def loss(args):
+        return sum((o * c).sum() for o, c in zip(op.mamba2_proj_prologue(*args, H, exact=True), cots))
+
+    h = 1e-6
+    for i, t in enumerate(ins):
+        fd = torch.zeros_like(t)
+        for idx in range(t.numel()):
+            e = torch.zeros(t.numel(), dtype=F64)
+            e[idx] = h
+            e = e.view(t.shape)
+            p = list(ins); p[i] = t + e
+            m = list(ins); m[i] = t - e
+            fd.view(-1)[idx] = (loss(p) - loss(m)) / (2 * h)
+        assert rel_err(grads[i], fd) < 1e-6, i
+
+
+def test_mamba2_projections_match_linear_in_bf16():
+    """bf16 dtype flow of the Dense layers: one rounding of the float32-accumulated
+    product (torch.nn.functional.linear in float64, rounded), the bias added in
+    bf16; the weight gradient is one rounding of x^T g, the bias gradient one
+    rounding of the column sums, both returned as float32."""
+    B, L, H, P, N = 2, 16, 2, 8, 8
+    ins = _m2x_inputs(B, L, H, P, N, 23, dtype=torch.bfloat16)
+    x, w_dt, b_dt, w_b = ins[0], ins[3], ins[4], ins[5]
+    dt_pre, b_pre, _ = op.mamba2_projections(x, w_dt, b_dt, w_b, ins[6])
+    lin = lambda w: torch.nn.functional.linear(x.double(), w.to(torch.bfloat16).double().t())
+    assert torch.equal(b_pre, lin(w_b).to(torch.bfloat16))
+    assert torch.equal(dt_pre, (lin(w_dt).to(torch.bfloat16) + b_dt.to(torch.bfloat16)))
+    # gradients of the dt projection alone
+    xl = x.clone().requires_grad_(True)
+    wl = w_dt.clone().requires_grad_(True)
+    bl = b_dt.clone().requires_grad_(True)
+    gy = torch.randn(B, L, H * P, generator=torch.Generator().manual_seed(24)).to(torch.bfloat16)
+    torch.autograd.backward(op.dense(xl, wl, bl), gy)
+    assert wl.grad.dtype == torch.float32 and bl.grad.dtype == torch.float32
+    x2 = x.double().reshape(-1, H * P)
+    g2 = gy.double().reshape(-1, H * P)
+    assert torch.equal(wl.grad, (x2.t() @ g2).to(torch.bfloat16).float())
+    assert rel_err(bl.grad.double(), g2.sum(0)) < 1e-2      # bf16 sum of the cotangent rows
+    assert torch.equal(xl.grad, (g2 @ w_dt.to(torch.bfloat16).double().t()).to(torch.bfloat16).reshape(x.shape))
