@@ -428,6 +428,78 @@ def measure_mamba2_prologue(dev, m):
                 ms_fwd_bwd=round(sum(kv["ms_per_launch"] for kv in ks.values()), 4))
 
 
+def mamba2_proj_model(B, L, d, N, splits):
+    """Algorithmic (flops, HBM bytes) per call of the kernels of the Mamba2
+    prologue with its projections (forward saving the projection outputs)."""
+    M, nt = B * L, d + 2 * N
+    n = M * d
+    parts = B * (L // 128) * d * 5 * 4
+    return {
+        "m2p_pack_t": (0, d * nt * (4 + 2)),
+        "prologue_conv_fwd": (n * 14, n * (2 + 2)),
+        "m2p_proj_gemm": (2 * M * d * nt, M * d * 2 + nt * d * 2 + 2 * M * nt * 2 + d * 4),
+        "m2_prologue_elem_fwd": (0, 0),
+        "m2p_pack": (0, d * nt * (4 + 2)),
+        "m2p_vjp": (M * nt * 10, M * nt * (2 + 2 + 2) + (M // 32) * d * 4),
+        "prologue_conv_bwd": (n * 30, n * (2 + 2 + 2) + parts),
+        "m2p_dx_gemm": (2 * M * nt * d, M * nt * 2 + d * nt * 2 + M * d * (2 + 2)),
+        "m2p_dw_gemm": (2 * M * d * nt, M * d * 2 + M * nt * 2 + splits * d * nt * 4),
+        "prologue_colsum": (parts // 4 + (M // 32) * d, parts + (M // 32) * d * 4),
+        "prologue_param_split": (0, d * 5 * 4 * 2),
+        "m2p_dw_finish": (splits * d * nt, splits * d * nt * 4 + d * nt * 4),
+    }
+
+
+def measure_mamba2_proj_prologue(dev, m):
+    """The Mamba2 prologue with its projections (in_proj output read in place,
+    the dt / B / C projection GEMM with its activation epilogue; backward dX /
+    dW GEMMs) at the benchmark's Mamba2 shape, per-kernel HIP events.  Outside
+    the timed region: not part of the headline metric."""
+    import torch
+    from atomic_ops import _lib
+    from atomic_ops import prologue as PL
+    B, L, H, P, N = m["B"], m["T"], m["H"], m["P"], m["N"]
+    d = H * P
+    gen = torch.Generator(device=dev).manual_seed(9)
+    r = lambda *s_: torch.randn(*s_, generator=gen, device=dev)
+    in_proj = r(B, L, 2 * d).to(torch.bfloat16)
+    params = [0.5 * r(d, 4), 0.1 * r(d), r(d, d) / d ** 0.5, r(d) - 2.0, r(d, N) / d ** 0.5, r(d, N) / d ** 0.5, r(H)]
+    cots = [r(B, L, H, P).to(torch.bfloat16), r(B, L, H, P).to(torch.bfloat16), r(B, L, N).to(torch.bfloat16),
+            r(B, L, N).to(torch.bfloat16), r(H)]
+    lib = _lib.load()
+    args_ = PL.mamba2_proj_make_args(B, L, H, P, N, 2 * d)
+    ws_f = torch.empty(lib.atomic_mamba2_proj_workspace_size(ctypes.byref(args_), 0), dtype=torch.uint8, device=dev)
+    ws_b = torch.empty(lib.atomic_mamba2_proj_workspace_size(ctypes.byref(args_), 1), dtype=torch.uint8, device=dev)
+    d_in = torch.empty_like(in_proj)
+    tiles = (d // 128) * ((d + 2 * N) // 128)
+    splits = 1
+    while splits * tiles < 1024 and (B * L) % (2 * splits * 64) == 0:
+        splits *= 2
+    model = mamba2_proj_model(B, L, d, N, splits)
+    n_it = max(PROF_STEPS, 5)
+    tms = [(_lib.KernelTimer(dev), _lib.KernelTimer(dev)) for _ in range(n_it + 2)]
+    for i in range(n_it + 2):      # two warm-up iterations
+        _, pres = PL.mamba2_proj_forward(in_proj[..., :d], *params, H, save=True, workspace=ws_f, timer=tms[i][0])
+        PL.mamba2_proj_backward(in_proj[..., :d], *params, H, pres, *cots, dx_bc=d_in, workspace=ws_b,
+                                timer=tms[i][1])
+    torch.cuda.synchronize()
+    per = {}
+    for i in range(2, n_it + 2):
+        for tm in tms[i]:
+            for kn, ms in tm.durations():
+                per.setdefault(kn, []).append(ms)
+    ks = {}
+    for kn, v_ in per.items():
+        avg = sum(v_) / len(v_)
+        fl, by = model[kn]
+        rf = roofline(fl, by, avg / 1e3)
+        ks[kn] = dict(ms_per_launch=round(avg, 4), flops=int(fl), bytes=int(by),
+                      tflops=round(fl / (avg / 1e3) / 1e12, 1), gbps=round(by / (avg / 1e3) / 1e9, 1),
+                      bound=rf["bound"], frac=round(rf["frac"], 4))
+    return dict(shape=f"B{B} L{L} H{H} P{P} N{N} (d_inner {d}), in_proj row stride {2 * d}, d_conv 4",
+                kernels=ks, ms_fwd_bwd=round(sum(kv["ms_per_launch"] for kv in ks.values()), 4))
+
+
 def measure_configs(dev):
     """The benchmark's configurations 1-4 at their own shapes (median of 5
     timed calls each, torch events on the launch stream, inputs resident):
@@ -643,11 +715,12 @@ def main():
     by_all = sum(pm[p_][d_][1] for p_ in pm for d_ in ("fwd", "bwd"))
     path_rf["step"] = _pr(fl_all, by_all, ms_per_step / 1e3)
 
-    epilogue = prologue = prologue_m2 = configs = None
+    epilogue = prologue = prologue_m2 = prologue_m2x = configs = None
     if not args.no_extras:
         epilogue = measure_epilogue(args, dev, g, m, q, k, v, w, b, gg, dt, x, Bm, Cm, A, scale, g_ws, m_ws)
         prologue = measure_prologue(dev, g)
         prologue_m2 = measure_mamba2_prologue(dev, m)
+        prologue_m2x = measure_mamba2_proj_prologue(dev, m)
         configs = measure_configs(dev)
 
     cpu = None if args.no_cpu else cpu_baseline()
@@ -670,6 +743,7 @@ def main():
         "epilogue": epilogue,
         "prologue": prologue,
         "prologue_mamba2": prologue_m2,
+        "prologue_mamba2_proj": prologue_m2x,
         "configs": configs,
     }
     print(json.dumps(line), flush=True)
