@@ -8,17 +8,17 @@
 //   gemm_tn   P[s][K][N] = sum over the rows m of split s of X[m][K] D[m][N]
 //             (the weight gradient X^T D over the tokens), fp32 partials.
 //
-// Tiles: one 128 x 128 block of C per workgroup of four waves (2 x 2, each
-// 64 x 64 as 4 x 4 v_mfma_f32_16x16x32_bf16 tiles); the reduction dimension
-// in steps of 64 through double-buffered LDS: every thread moves four
-// 16-byte pieces of each operand per step, loading the next step's pieces
-// while the current step's MFMAs run.
+// Tiles: one 128 x BN block of C per workgroup of four waves (2 x 2, each
+// 64 x BN/2 as v_mfma_f32_16x16x32_bf16 tiles; BN = 256 where N allows, else
+// 128); the reduction dimension in steps of 64 through one LDS stage: the
+// next step's 16-byte pieces are loaded into registers while the current
+// step's MFMAs run, and stored after a barrier.
 #pragma once
 #include "common.hpp"
 
 namespace ah {
 
-constexpr int kGT = 128;       // C tile edge
+constexpr int kGT = 128;       // C tile rows (M)
 constexpr int kGK = 64;        // reduction step
 constexpr int kGP = kGK + 8;   // NT staging row pitch (elements): 16 rows of a fragment read hit distinct banks
 constexpr int kTP = kGT + 16;  // TN staging row pitch: four rows of a transposed read hit distinct banks
@@ -70,68 +70,81 @@ struct GemmNT {
   long long lda;
   const bf16* Bt;  // [N][K], row stride ldb
   long long ldb;
-  int M, N, K;     // multiples of 128, 128, 64
+  int M, N, K;     // multiples of 128, BN, 64
 };
 
-// The epilogue gets each wave's 64 x 64 block (rows m0.., columns n0..) as
-// acc[i][j]: the 16 x 16 tile at rows m0 + 16 i, columns n0 + 16 j.
-template <typename Epi>
-__global__ __launch_bounds__(256) void gemm_nt(GemmNT g, Epi epi) {
-  __shared__ __attribute__((aligned(16))) bf16 sA[2][kGT * kGP];
-  __shared__ __attribute__((aligned(16))) bf16 sB[2][kGT * kGP];
+// One 128 x BN tile of C per workgroup: waves in a 2 x 2 grid, each 64 x BN/2
+// as 4 x (BN / 32) MFMA tiles.  One LDS stage: the next step's pieces are
+// loaded into registers while the current step's MFMAs read the stage, then
+// stored after a barrier.  The epilogue gets each wave's block (rows m0..,
+// columns n0..) as acc[i][j], the 16 x 16 tile at rows m0 + 16 i, columns n0 + 16 j.
+template <int BN, typename Epi>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_nt(GemmNT g, Epi epi) {
+  constexpr int NJ = BN / 32, PB = BN / 32;  // tiles per wave along N; Bt pieces per thread
+  __shared__ __attribute__((aligned(16))) bf16 sA[kGT * kGP];
+  __shared__ __attribute__((aligned(16))) bf16 sB[BN * kGP];
   typedef Mma<bf16>::frag frag;
   const int tid = threadIdx.x, w = wave_id();
-  const int ntn = g.N / kGT;
+  const int ntn = g.N / BN;
   const int tm = blockIdx.x / ntn, tn = blockIdx.x % ntn;  // consecutive workgroups share the A rows
   const bf16* Ag = g.A + (size_t)tm * kGT * g.lda;
-  const bf16* Bg = g.Bt + (size_t)tn * kGT * g.ldb;
-  u32x4 ra[4], rb[4];
+  const bf16* Bg = g.Bt + (size_t)tn * BN * g.ldb;
+  u32x4 ra[4], rb[PB];
   auto gload = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = tid + 256 * i, r = e >> 3, c = (e & 7) * 8;
       ra[i] = *reinterpret_cast<const u32x4*>(Ag + (size_t)r * g.lda + k0 + c);
+    }
+#pragma unroll
+    for (int i = 0; i < PB; ++i) {
+      const int e = tid + 256 * i, r = e >> 3, c = (e & 7) * 8;
       rb[i] = *reinterpret_cast<const u32x4*>(Bg + (size_t)r * g.ldb + k0 + c);
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&]() {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = tid + 256 * i, r = e >> 3, c = (e & 7) * 8;
-      *reinterpret_cast<u32x4*>(&sA[buf][r * kGP + c]) = ra[i];
-      *reinterpret_cast<u32x4*>(&sB[buf][r * kGP + c]) = rb[i];
+      *reinterpret_cast<u32x4*>(&sA[r * kGP + c]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < PB; ++i) {
+      const int e = tid + 256 * i, r = e >> 3, c = (e & 7) * 8;
+      *reinterpret_cast<u32x4*>(&sB[r * kGP + c]) = rb[i];
     }
   };
-  f32x4 acc[4][4];
+  f32x4 acc[4][NJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = zero4();
-  const int wm = (w >> 1) * 64, wn = (w & 1) * 64;
+    for (int j = 0; j < NJ; ++j) acc[i][j] = zero4();
+  const int wm = (w >> 1) * 64, wn = (w & 1) * (BN / 2);
   const int nk = g.K / kGK;
   gload(0);
-  lstore(0);
+  lstore();
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
     if (kt + 1 < nk) gload((kt + 1) * kGK);
 #pragma unroll
     for (int ks = 0; ks < kGK; ks += 32) {
-      frag af[4], bfr[4];
+      frag af[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = Mma<bf16>::ld_c(sA[buf], kGP, wm + 16 * i, ks);
+      for (int i = 0; i < 4; ++i) af[i] = Mma<bf16>::ld_c(sA, kGP, wm + 16 * i, ks);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bfr[j] = Mma<bf16>::ld_c(sB[buf], kGP, wn + 16 * j, ks);
+      for (int j = 0; j < NJ; ++j) {
+        const frag bfr = Mma<bf16>::ld_c(sB, kGP, wn + 16 * j, ks);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = Mma<bf16>::mma(af[i], bfr[j], acc[i][j]);
+        for (int i = 0; i < 4; ++i) acc[i][j] = Mma<bf16>::mma(af[i], bfr, acc[i][j]);
+      }
     }
-    // the other buffer was last read before the previous barrier
-    if (kt + 1 < nk) lstore(buf ^ 1);
-    __syncthreads();
+    if (kt + 1 < nk) {
+      __syncthreads();  // every wave is done reading the stage
+      lstore();
+      __syncthreads();
+    }
   }
-  epi(tm * kGT + wm, tn * kGT + wn, acc);
+  epi(tm * kGT + wm, tn * BN + wn, acc);
 }
 
 // ---------------------------------------------------------------- TN GEMM
@@ -140,66 +153,80 @@ struct GemmTN {
   long long ldx;
   const bf16* D;  // [M][N], row stride ldd
   long long ldd;
-  int Kd, N;      // multiples of 128
+  int Kd, N;      // multiples of 128 and BN
   int rows;       // rows per split (a multiple of 64); split s covers rows [s rows, (s + 1) rows)
   float* part;    // [splits][Kd][N]
 };
 
-__global__ __launch_bounds__(256) void gemm_tn(GemmTN g) {
-  __shared__ __attribute__((aligned(16))) bf16 sX[2][kGK * kTP];
-  __shared__ __attribute__((aligned(16))) bf16 sD[2][kGK * kTP];
+// P[s] tile (128 x BN) = X^T D over the split's rows, both operands staged as
+// 64-row tiles and read transposed (ds_read_b64_tr_b16) as the MFMA fragments.
+template <int BN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_tn(GemmTN g) {
+  constexpr int NJ = BN / 32, PD = BN / 32, LD = BN + 16;
+  __shared__ __attribute__((aligned(16))) bf16 sX[kGK * kTP];
+  __shared__ __attribute__((aligned(16))) bf16 sD[kGK * LD];
   typedef Mma<bf16>::frag frag;
   const int tid = threadIdx.x, w = wave_id();
-  const int ntn = g.N / kGT, ntk = g.Kd / kGT;
+  const int ntn = g.N / BN, ntk = g.Kd / kGT;
   const int s = blockIdx.x / (ntk * ntn), t = blockIdx.x % (ntk * ntn);
   const int tk = t / ntn, tn = t % ntn;
   const bf16* Xg = g.X + (size_t)s * g.rows * g.ldx + tk * kGT;
-  const bf16* Dg = g.D + (size_t)s * g.rows * g.ldd + tn * kGT;
-  u32x4 ra[4], rb[4];
-  auto gload = [&](int m0) {  // 64 rows x 128 columns of each operand
+  const bf16* Dg = g.D + (size_t)s * g.rows * g.ldd + tn * BN;
+  u32x4 ra[4], rb[PD];
+  auto gload = [&](int m0) {  // 64 rows x 128 columns of X, 64 x BN of D
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = tid + 256 * i, r = e >> 4, c = (e & 15) * 8;
       ra[i] = *reinterpret_cast<const u32x4*>(Xg + (size_t)(m0 + r) * g.ldx + c);
+    }
+#pragma unroll
+    for (int i = 0; i < PD; ++i) {
+      const int e = tid + 256 * i, r = e / (BN / 8), c = (e % (BN / 8)) * 8;
       rb[i] = *reinterpret_cast<const u32x4*>(Dg + (size_t)(m0 + r) * g.ldd + c);
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&]() {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = tid + 256 * i, r = e >> 4, c = (e & 15) * 8;
-      *reinterpret_cast<u32x4*>(&sX[buf][r * kTP + c]) = ra[i];
-      *reinterpret_cast<u32x4*>(&sD[buf][r * kTP + c]) = rb[i];
+      *reinterpret_cast<u32x4*>(&sX[r * kTP + c]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < PD; ++i) {
+      const int e = tid + 256 * i, r = e / (BN / 8), c = (e % (BN / 8)) * 8;
+      *reinterpret_cast<u32x4*>(&sD[r * LD + c]) = rb[i];
     }
   };
-  f32x4 acc[4][4];
+  f32x4 acc[4][NJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = zero4();
-  const int wm = (w >> 1) * 64, wn = (w & 1) * 64;
+    for (int j = 0; j < NJ; ++j) acc[i][j] = zero4();
+  const int wm = (w >> 1) * 64, wn = (w & 1) * (BN / 2);
   const int nk = g.rows / kGK;
   gload(0);
-  lstore(0);
+  lstore();
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
     if (kt + 1 < nk) gload((kt + 1) * kGK);
 #pragma unroll
     for (int ks = 0; ks < kGK; ks += 32) {
       // A(k, m) = X[m][k] and B(m, n) = D[m][n]: both read transposed from the row tiles
-      frag af[4], bfr[4];
+      frag af[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = Mma<bf16>::ld_t(sX[buf], kTP, wm + 16 * i, ks);
+      for (int i = 0; i < 4; ++i) af[i] = Mma<bf16>::ld_t(sX, kTP, wm + 16 * i, ks);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bfr[j] = Mma<bf16>::ld_t(sD[buf], kTP, wn + 16 * j, ks);
+      for (int j = 0; j < NJ; ++j) {
+        const frag bfr = Mma<bf16>::ld_t(sD, LD, wn + 16 * j, ks);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = Mma<bf16>::mma(af[i], bfr[j], acc[i][j]);
+        for (int i = 0; i < 4; ++i) acc[i][j] = Mma<bf16>::mma(af[i], bfr, acc[i][j]);
+      }
     }
-    if (kt + 1 < nk) lstore(buf ^ 1);
-    __syncthreads();
+    if (kt + 1 < nk) {
+      __syncthreads();
+      lstore();
+      __syncthreads();
+    }
   }
   // partial tile, stored as 4-column vectors after a quad transpose
   float* P = g.part + (size_t)s * g.Kd * g.N;
@@ -207,11 +234,11 @@ __global__ __launch_bounds__(256) void gemm_tn(GemmTN g) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
       quad_transpose(v);
       const int row = tk * kGT + wm + 16 * i + tile_row(0) + (c & 3);
-      const int col = tn * kGT + wn + 16 * j + (c & ~3);
+      const int col = tn * BN + wn + 16 * j + (c & ~3);
       *reinterpret_cast<float4*>(P + (size_t)row * g.N + col) = make_float4(v[0], v[1], v[2], v[3]);
     }
 }
@@ -235,10 +262,11 @@ struct M2ProjEpi {
   const float* b_dt;               // [d]
   bf16 *dt, *B, *C;                // [M][d], [M][n], [M][n]
   bf16 *dt_pre, *b_pre, *c_pre;    // the same shapes, or NULL
-  __device__ __forceinline__ void operator()(int m0, int n0, f32x4 (&acc)[4][4]) const {
+  template <int NJ>
+  __device__ __forceinline__ void operator()(int m0, int n0, f32x4 (&acc)[4][NJ]) const {
     const int c = tile_col();
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int col = n0 + 16 * j + (c & ~3);  // this lane's four columns after the transpose
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -282,10 +310,11 @@ struct M2DxEpi {
   int d;
   bf16* out;        // [M] rows of stride ldo
   long long ldo;
-  __device__ __forceinline__ void operator()(int m0, int n0, f32x4 (&acc)[4][4]) const {
+  template <int NJ>
+  __device__ __forceinline__ void operator()(int m0, int n0, f32x4 (&acc)[4][NJ]) const {
     const int c = tile_col();
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int col = n0 + 16 * j + (c & ~3);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {

@@ -833,7 +833,7 @@ static M2xPlan m2x_plan(const atomic_mamba2_proj_args* a, bool bwd) {
   p.dm = PlDims{a->batch, a->seqlen, a->heads, 128, p.d, 0.f, (int)a->in_stride};
   // row splits of the weight-gradient GEMM: enough workgroups to fill the chip,
   // each split a multiple of 64 rows
-  const int tiles = (p.d / kGT) * (p.nt / kGT);
+  const int tiles = (p.d / kGT) * (p.nt / (p.nt % 256 == 0 ? 256 : 128));
   int s = 1;
   while (s * tiles < 1024 && p.M % (2 * s * kGK) == 0) s *= 2;
   p.splits = s;
@@ -891,7 +891,12 @@ extern "C" int atomic_mamba2_proj_fwd(const atomic_mamba2_proj_args* a, const vo
   rc = L("m2p_proj_gemm", [&] {
     const GemmNT g{(const bf16*)x_bc, (long long)a->in_stride, wt, (long long)p.d, p.M, p.nt, p.d};
     const M2ProjEpi e{p.d, p.n, b_dt, (bf16*)dt, (bf16*)B, (bf16*)C, (bf16*)dt_pre, (bf16*)b_pre, (bf16*)c_pre};
-    hipLaunchKernelGGL((gemm_nt<M2ProjEpi>), dim3((unsigned)((p.M / kGT) * (p.nt / kGT))), dim3(256), 0, st, g, e);
+    if (p.nt % 256 == 0)
+      hipLaunchKernelGGL((gemm_nt<256, M2ProjEpi>), dim3((unsigned)((p.M / kGT) * (p.nt / 256))), dim3(256), 0, st, g,
+                         e);
+    else
+      hipLaunchKernelGGL((gemm_nt<128, M2ProjEpi>), dim3((unsigned)((p.M / kGT) * (p.nt / 128))), dim3(256), 0, st, g,
+                         e);
   });
   if (rc) return rc;
   return L("m2_prologue_elem_fwd", [&] {  // A only (no element ranges)
@@ -950,12 +955,15 @@ extern "C" int atomic_mamba2_proj_bwd(const atomic_mamba2_proj_args* a, const vo
   rc = L("m2p_dx_gemm", [&] {
     const GemmNT g{dpre, (long long)p.nt, w, (long long)p.nt, p.M, p.d, p.nt};
     const M2DxEpi e{dxc, p.d, (bf16*)dx_bc, (long long)a->in_stride};
-    hipLaunchKernelGGL((gemm_nt<M2DxEpi>), dim3((unsigned)((p.M / kGT) * (p.d / kGT))), dim3(256), 0, st, g, e);
+    hipLaunchKernelGGL((gemm_nt<256, M2DxEpi>), dim3((unsigned)((p.M / kGT) * (p.d / 256))), dim3(256), 0, st, g, e);
   });
   if (rc) return rc;
   rc = L("m2p_dw_gemm", [&] {
     const GemmTN g{(const bf16*)x_bc, (long long)a->in_stride, dpre, (long long)p.nt, p.d, p.nt, p.M / p.splits, dwp};
-    hipLaunchKernelGGL(gemm_tn, dim3((unsigned)(p.splits * (p.d / kGT) * (p.nt / kGT))), dim3(256), 0, st, g);
+    if (p.nt % 256 == 0)
+      hipLaunchKernelGGL(gemm_tn<256>, dim3((unsigned)(p.splits * (p.d / kGT) * (p.nt / 256))), dim3(256), 0, st, g);
+    else
+      hipLaunchKernelGGL(gemm_tn<128>, dim3((unsigned)(p.splits * (p.d / kGT) * (p.nt / 128))), dim3(256), 0, st, g);
   });
   if (rc) return rc;
   rc = L("prologue_colsum", [&] {

@@ -471,7 +471,8 @@ def measure_mamba2_proj_prologue(dev, m):
     ws_f = torch.empty(lib.atomic_mamba2_proj_workspace_size(ctypes.byref(args_), 0), dtype=torch.uint8, device=dev)
     ws_b = torch.empty(lib.atomic_mamba2_proj_workspace_size(ctypes.byref(args_), 1), dtype=torch.uint8, device=dev)
     d_in = torch.empty_like(in_proj)
-    tiles = (d // 128) * ((d + 2 * N) // 128)
+    nt = d + 2 * N
+    tiles = (d // 128) * (nt // (256 if nt % 256 == 0 else 128))
     splits = 1
     while splits * tiles < 1024 and (B * L) % (2 * splits * 64) == 0:
         splits *= 2
