@@ -22,6 +22,7 @@ ERRORS = {
     -5: "ATOMIC_ERR_NULL: required pointer is NULL",
     -6: "ATOMIC_ERR_SCRATCH: does not fit the no-allocation entry point's fixed scratch "
         "(or asks it to keep intermediates)",
+    -7: "ATOMIC_ERR_REUSE: the workspace does not hold the matching forward (REUSE)",
 }
 ATOMIC_F32, ATOMIC_BF16 = 0, 1
 GDN2_SAVE, GDN2_REUSE = 1, 2

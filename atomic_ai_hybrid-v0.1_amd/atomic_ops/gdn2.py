@@ -132,9 +132,15 @@ def backward(q, k, v, w, b, g, scale, dO, dh_final=None, h0=None, *, workspace=N
              chunk=CHUNK, timer=None, diag=None):
     """Gradients ``(dq, dk, dv, dw, db, dg, dh0)`` in the primals' dtypes
     (dg and dh0 float32).  ``reuse`` declares that ``workspace`` holds the
-    intermediates of a ``forward(..., save=True)`` on the same inputs."""
+    intermediates of a ``forward(..., save=True)`` on the same inputs; the
+    library checks that by the input addresses, so an input that has to be
+    copied here (not contiguous, or h0 not float32) turns reuse into a
+    recompute."""
     _check_inputs(q, k, v, w, b, g)
     lib = _lib.load()
+    if reuse and not all(t.is_contiguous() for t in (q, k, v, w, b, g)) or \
+            (h0 is not None and (h0.dtype != torch.float32 or not h0.is_contiguous())):
+        reuse = False
     q, k, v, w, b, g = (t.contiguous() for t in (q, k, v, w, b, g))
     dO = dO.contiguous()
     if dO.dtype not in _DT:

@@ -20,6 +20,12 @@ class _Mamba2Core(torch.autograd.Function):
     @staticmethod
     def forward(ctx, dt, x, B, C, A, chunk_size, state0):
         need = any(ctx.needs_input_grad)
+        ctx.A_dtype, ctx.state0_dtype = A.dtype, state0.dtype
+        # the tensors the library sees, kept for the backward: its reuse of
+        # the forward's workspace is checked against these addresses
+        dt, x, B, C = (t.contiguous() for t in (dt, x, B, C))
+        A = A.to(torch.float32).contiguous()
+        state0 = state0.to(torch.float32).contiguous()
         y, state_final, ws = _m.forward(dt, x, B, C, A, chunk_size, state0, save=need)
         if need:
             ctx.save_for_backward(dt, x, B, C, A, state0)
@@ -36,7 +42,7 @@ class _Mamba2Core(torch.autograd.Function):
         ddt, dx, dB, dC, dA, dstate0 = _m.backward(dt, x, B, C, A, ctx.chunk_size, dy,
                                                    dstate_final=dstate_final, state0=state0,
                                                    workspace=ws, reuse=ws is not None)
-        return ddt, dx, dB, dC, dA.to(A.dtype), None, dstate0.to(state0.dtype)
+        return ddt, dx, dB, dC, dA.to(ctx.A_dtype), None, dstate0.to(ctx.state0_dtype)
 
 
 def mamba2_pallas_forward_trainable_B6(dt, x, B, C, A, chunk_size, state0=None):

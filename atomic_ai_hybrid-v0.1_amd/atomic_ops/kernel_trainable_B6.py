@@ -41,11 +41,17 @@ class _Gdn2Core(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, w, b, g, scale, h0):
         need = any(ctx.needs_input_grad)
+        h0_dtype = h0.dtype
+        # the tensors the library sees, kept for the backward: its reuse of
+        # the forward's workspace is checked against these addresses
+        q, k, v, w, b, g = (t.contiguous() for t in (q, k, v, w, b, g))
+        h0 = h0.to(torch.float32).contiguous()
         o, h_final, ws = _forward(q, k, v, w, b, g, scale, h0, need)
         if need:
             ctx.save_for_backward(q, k, v, w, b, g, h0)
             ctx.ws = ws
             ctx.scale = scale
+            ctx.h0_dtype = h0_dtype
         return o, h_final
 
     @staticmethod
@@ -58,7 +64,7 @@ class _Gdn2Core(torch.autograd.Function):
         grads = _g.backward(q, k, v, w, b, g, ctx.scale, do, dh_final=dh_final, h0=h0,
                             workspace=ws, reuse=ws is not None)
         dq, dk, dv, dw, db, dg, dh0 = grads
-        return dq, dk, dv, dw, db, dg, None, dh0.to(h0.dtype)
+        return dq, dk, dv, dw, db, dg, None, dh0.to(ctx.h0_dtype)
 
 
 def gdn2_pallas_forward_trainable(q, k, v, w, b, g, scale, h0=None):

@@ -85,9 +85,15 @@ def forward(dt, x, Bm, Cm, A, chunk_size, state0=None, *, save=False, workspace=
 def backward(dt, x, Bm, Cm, A, chunk_size, dy, dstate_final=None, state0=None, *, workspace=None,
              reuse=False, timer=None, diag=None):
     """Gradients ``(ddt, dx, dB, dC, dA, dstate0)`` (MB0 semantics) in the
-    primals' dtypes (dA, dstate0 float32)."""
+    primals' dtypes (dA, dstate0 float32).  ``reuse`` declares that
+    ``workspace`` holds the forward of the same inputs; the library checks
+    that by the input addresses, so an input that has to be copied here (not
+    contiguous, or state0 not float32) turns reuse into a recompute."""
     _check(dt, x, Bm, Cm, A)
     lib = _lib.load()
+    if reuse and not all(t.is_contiguous() for t in (dt, x, Bm, Cm, A)) or \
+            (state0 is not None and (state0.dtype != torch.float32 or not state0.is_contiguous())):
+        reuse = False
     dt, x, Bm, Cm, A = (t.contiguous() for t in (dt, x, Bm, Cm, A))
     dy = dy.contiguous()
     if dy.dtype not in _DT:

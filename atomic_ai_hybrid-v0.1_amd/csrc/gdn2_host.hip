@@ -1,15 +1,71 @@
 // Host side of the GDN2 chunk pipeline: argument checks, workspace layout,
 // template dispatch and the extern "C" entry points of include/atomic_hybrid.h.
 #include <mutex>
+#include <vector>
 
 #include "../../include/atomic_hybrid.h"
 #include "diag.hpp"
 #include "gdn2_bwd.hip"
 #include "launch.hpp"
+#include "ws_tag.hpp"
 
 namespace ah {
 
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// ------------------------------------------------ workspace records (ws_tag.hpp)
+namespace {
+struct WsEntry {
+  const char *lo, *hi;
+  WsTag t;
+};
+std::mutex g_ws_mu;
+std::vector<WsEntry> g_ws_tags;
+bool ws_same(const WsTag& a, const WsTag& b) {
+  if (a.kind != b.kind) return false;
+  for (int i = 0; i < 8; ++i)
+    if (a.dims[i] != b.dims[i] || a.ptrs[i] != b.ptrs[i]) return false;
+  return true;
+}
+void ws_erase_overlap(const char* lo, const char* hi) {
+  size_t j = 0;
+  for (size_t i = 0; i < g_ws_tags.size(); ++i)
+    if (g_ws_tags[i].hi <= lo || g_ws_tags[i].lo >= hi) g_ws_tags[j++] = g_ws_tags[i];
+  g_ws_tags.resize(j);
+}
+}  // namespace
+
+void ws_tag_clobber(const void* ws, size_t bytes) {
+  if (!ws) return;
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  const char* lo = static_cast<const char*>(ws);
+  ws_erase_overlap(lo, lo + bytes);
+}
+void ws_tag_set(const void* ws, size_t bytes, const WsTag& t) {
+  if (!ws) return;
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  const char* lo = static_cast<const char*>(ws);
+  ws_erase_overlap(lo, lo + bytes);
+  if (g_ws_tags.size() >= 1024) g_ws_tags.erase(g_ws_tags.begin());  // oldest record
+  g_ws_tags.push_back(WsEntry{lo, lo + bytes, t});
+}
+bool ws_tag_matches(const void* ws, const WsTag& t) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  for (const WsEntry& e : g_ws_tags)
+    if (e.lo == static_cast<const char*>(ws)) return ws_same(e.t, t);
+  return false;
+}
+
+// the forward a GDN2 workspace holds: shapes, dtype and the input pointers
+static WsTag gdn2_tag(const atomic_gdn2_args* a, const void* q, const void* k, const void* v, const void* w,
+                      const void* b, const void* g, const void* h0) {
+  WsTag t{};
+  t.kind = 1;
+  const int32_t d[8] = {a->batch, a->seqlen, a->heads, a->dk, a->dv, a->chunk, a->dtype, 0};
+  const void* ptr[8] = {q, k, v, w, b, g, h0, nullptr};
+  for (int i = 0; i < 8; ++i) { t.dims[i] = d[i]; t.ptrs[i] = ptr[i]; }
+  return t;
+}
 
 // The chunk length every GDN2 kernel runs at.
 constexpr int kGdn2RunChunk = 64;
@@ -462,8 +518,10 @@ extern "C" int atomic_gdn2_fwd(const atomic_gdn2_args* a, const void* q, const v
   if (!q || !k || !v || !w || !b || !g || !o || !h_final) return ATOMIC_ERR_NULL;
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
   Launch L{a->profile, (hipStream_t)stream};
-  int r2 = gdn2_forward(p, a->dtype, q, k, v, w, b, g, h0, o, h_final, workspace,
-                        (a->flags & ATOMIC_GDN2_SAVE) ? 1 : 0, L);
+  const bool save = (a->flags & ATOMIC_GDN2_SAVE) != 0;
+  ws_tag_clobber(workspace, p.total);
+  int r2 = gdn2_forward(p, a->dtype, q, k, v, w, b, g, h0, o, h_final, workspace, save ? 1 : 0, L);
+  if (r2 == ATOMIC_OK && save) ws_tag_set(workspace, p.total, gdn2_tag(a, q, k, v, w, b, g, h0));
   if (r2 || !a->diag) return r2;
   StageDiag D{a->diag, L};
   if ((r2 = D.clear(0, ATOMIC_GDN2_DIAG_DV_NEW))) return r2;
@@ -482,9 +540,15 @@ extern "C" int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const v
   if (!q || !k || !v || !w || !b || !g || !dO || !dq || !dk || !dv || !dw || !db || !dg)
     return ATOMIC_ERR_NULL;
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
+  const bool reuse = (a->flags & ATOMIC_GDN2_REUSE) != 0;
+  const WsTag tag = gdn2_tag(a, q, k, v, w, b, g, h0);
+  if (reuse && !ws_tag_matches(workspace, tag)) return ATOMIC_ERR_REUSE;
   Launch L{a->profile, (hipStream_t)stream};
   int r2 = gdn2_backward(p, a->dtype, a->do_dtype, q, k, v, w, b, g, h0, dO, dh_final, dq, dk, dv, dw,
-                         db, dg, dh0, workspace, (a->flags & ATOMIC_GDN2_REUSE) != 0, L);
+                         db, dg, dh0, workspace, reuse, L);
+  // the workspace now holds this forward (recomputed, or kept) and nothing else
+  if (r2 == ATOMIC_OK) ws_tag_set(workspace, p.total, tag);
+  else ws_tag_clobber(workspace, p.total);
   if (r2 || !a->diag) return r2;
   StageDiag D{a->diag, L};
   if ((r2 = D.clear(ATOMIC_GDN2_DIAG_DV_NEW, ATOMIC_GDN2_DIAG_COUNT - ATOMIC_GDN2_DIAG_DV_NEW))) return r2;

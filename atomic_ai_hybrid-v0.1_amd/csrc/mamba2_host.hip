@@ -4,6 +4,7 @@
 #include "diag.hpp"
 #include "mamba2_bwd.hip"
 #include "launch.hpp"
+#include "ws_tag.hpp"
 
 namespace ah {
 
@@ -280,6 +281,17 @@ extern "C" size_t atomic_mamba2_workspace_size(const atomic_mamba2_args* a) {
   return p.total;
 }
 
+// the forward a Mamba2 workspace holds: shapes, dtype and the input pointers
+static WsTag mamba2_tag(const atomic_mamba2_args* a, const void* dt, const void* x, const void* B, const void* C,
+                        const void* A, const void* state0) {
+  WsTag t{};
+  t.kind = 2;
+  const int32_t d[8] = {a->batch, a->seqlen, a->heads, a->headdim, a->dstate, a->chunk, a->dtype, 0};
+  const void* ptr[8] = {dt, x, B, C, A, state0, nullptr, nullptr};
+  for (int i = 0; i < 8; ++i) { t.dims[i] = d[i]; t.ptrs[i] = ptr[i]; }
+  return t;
+}
+
 extern "C" int atomic_mamba2_fwd(const atomic_mamba2_args* a, const void* dt, const void* x,
                                  const void* B, const void* C, const float* A, const float* state0,
                                  float* y, float* state_final, void* workspace,
@@ -291,6 +303,9 @@ extern "C" int atomic_mamba2_fwd(const atomic_mamba2_args* a, const void* dt, co
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
   Launch L{a->profile, (hipStream_t)stream};
   int r2 = mamba2_forward(p, dt, x, B, C, A, state0, y, state_final, workspace, L);
+  // the forward always leaves its per-chunk states in the workspace
+  if (r2 == ATOMIC_OK) ws_tag_set(workspace, p.total, mamba2_tag(a, dt, x, B, C, A, state0));
+  else ws_tag_clobber(workspace, p.total);
   if (r2 || !a->diag) return r2;
   StageDiag D{a->diag, L};
   return mamba2_forward_diag(p, D, y, state_final, workspace);
@@ -306,9 +321,15 @@ extern "C" int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, co
   if (rc != ATOMIC_OK) return rc;
   if (!dt || !x || !B || !C || !A || !dy || !ddt || !dx || !dB || !dC || !dA) return ATOMIC_ERR_NULL;
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
+  const bool reuse = (a->flags & ATOMIC_MAMBA2_REUSE) != 0;
+  const WsTag tag = mamba2_tag(a, dt, x, B, C, A, state0);
+  if (reuse && !ws_tag_matches(workspace, tag)) return ATOMIC_ERR_REUSE;
   Launch L{a->profile, (hipStream_t)stream};
   int r2 = mamba2_backward(p, a->dy_dtype, dt, x, B, C, A, state0, dy, dstate_final, ddt, dx, dB, dC, dA,
-                           dstate0, workspace, (a->flags & ATOMIC_MAMBA2_REUSE) != 0, L);
+                           dstate0, workspace, reuse, L);
+  // the per-chunk states (kept or recomputed) outlive the backward's own scratch
+  if (r2 == ATOMIC_OK) ws_tag_set(workspace, p.total, tag);
+  else ws_tag_clobber(workspace, p.total);
   if (r2 || !a->diag) return r2;
   StageDiag D{a->diag, L};
   return mamba2_backward_diag(p, D, ddt, dx, dB, dC, dA, dstate0, workspace);

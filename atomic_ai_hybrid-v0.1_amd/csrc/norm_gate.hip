@@ -20,6 +20,7 @@
 #include "../../include/atomic_hybrid.h"
 #include "common.hpp"
 #include "launch.hpp"
+#include "ws_tag.hpp"
 
 namespace ah {
 
@@ -431,6 +432,7 @@ extern "C" int atomic_norm_gate_bwd(const atomic_norm_gate_args* a, const float*
   if (rc) return rc;
   if (!x || !gate || !weight || !dout || !dx || !dgate || !dweight) return ATOMIC_ERR_NULL;
   if (!workspace || workspace_bytes < atomic_norm_gate_workspace_size(a)) return ATOMIC_ERR_WORKSPACE;
+  ws_tag_clobber(workspace, atomic_norm_gate_workspace_size(a));
   hipStream_t st = (hipStream_t)stream;
   const NgDims dm{a->rows, a->dim, a->eps};
   const int nparts = ng_parts(a);

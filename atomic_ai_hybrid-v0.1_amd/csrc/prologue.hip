@@ -24,6 +24,7 @@
 #include "../../include/atomic_hybrid.h"
 #include "common.hpp"
 #include "launch.hpp"
+#include "ws_tag.hpp"
 #include "proj_gemm.hpp"
 
 namespace ah {
@@ -654,6 +655,7 @@ extern "C" int atomic_gdn2_prologue_bwd(const atomic_gdn2_prologue_args* a, cons
   const PlDims dm = pl_dims(a);
   const PlWs ws = pl_ws(dm);
   if (!workspace || workspace_bytes < ws.total) return ATOMIC_ERR_WORKSPACE;
+  ws_tag_clobber(workspace, ws.total);
   unsigned char* wsb = (unsigned char*)workspace;
   float* pconv = (float*)(wsb + ws.conv);
   float* pda = (float*)(wsb + ws.da);
@@ -772,6 +774,7 @@ extern "C" int atomic_mamba2_prologue_bwd(const atomic_mamba2_prologue_args* a, 
   const PlDims dm = m2p_dims(a);
   size_t so;
   if (!workspace || workspace_bytes < m2p_ws(dm, &so)) return ATOMIC_ERR_WORKSPACE;
+  ws_tag_clobber(workspace, m2p_ws(dm, &so));
   float* part = (float*)workspace;
   float* sums = (float*)((unsigned char*)workspace + so);
   hipStream_t st = (hipStream_t)stream;
@@ -874,6 +877,7 @@ extern "C" int atomic_mamba2_proj_fwd(const atomic_mamba2_proj_args* a, const vo
     return ATOMIC_ERR_NULL;
   const M2xPlan p = m2x_plan(a, false);
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
+  ws_tag_clobber(workspace, p.total);
   bf16* wt = reinterpret_cast<bf16*>(static_cast<unsigned char*>(workspace) + p.o_w);
   hipStream_t st = (hipStream_t)stream;
   Launch L{a->profile, st};
@@ -922,6 +926,7 @@ extern "C" int atomic_mamba2_proj_bwd(const atomic_mamba2_proj_args* a, const vo
     return ATOMIC_ERR_NULL;
   const M2xPlan p = m2x_plan(a, true);
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
+  ws_tag_clobber(workspace, p.total);
   unsigned char* wsb = static_cast<unsigned char*>(workspace);
   bf16* w = reinterpret_cast<bf16*>(wsb + p.o_w);
   bf16* dpre = reinterpret_cast<bf16*>(wsb + p.o_dpre);

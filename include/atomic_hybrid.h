@@ -33,9 +33,14 @@ enum {
   ATOMIC_ERR_WORKSPACE = -3,  /* workspace NULL or smaller than required      */
   ATOMIC_ERR_LAUNCH = -4,     /* a kernel launch failed                       */
   ATOMIC_ERR_NULL = -5,       /* a required pointer is NULL                   */
-  ATOMIC_ERR_SCRATCH = -6     /* a no-allocation entry point: the shape does not
+  ATOMIC_ERR_SCRATCH = -6,    /* a no-allocation entry point: the shape does not
                                  fit its fixed scratch, or the flags ask for
                                  intermediates to outlive the call            */
+  ATOMIC_ERR_REUSE = -7       /* a backward with the REUSE flag on a workspace
+                                 that does not hold the matching forward (no
+                                 saving forward on it, a forward of other
+                                 shapes or input pointers, or written since by
+                                 another call of this library)                */
 };
 
 enum { ATOMIC_F32 = 0, ATOMIC_BF16 = 1 };
@@ -106,7 +111,11 @@ enum {
      inputs and workspace can skip the forward recompute */
   ATOMIC_GDN2_SAVE = 1,
   /* backward: the workspace holds the intermediates of an
-     atomic_gdn2_fwd(..., ATOMIC_GDN2_SAVE) call on identical inputs */
+     atomic_gdn2_fwd(..., ATOMIC_GDN2_SAVE) call on identical inputs.  The
+     library records (host side) which forward each workspace holds and
+     returns ATOMIC_ERR_REUSE before launching anything when it is not this
+     call's (same shapes, dtype and input pointers); contents rewritten in
+     place between the calls are not detected */
   ATOMIC_GDN2_REUSE = 2
 };
 
@@ -203,7 +212,8 @@ enum {
      workspace; the flag is accepted for symmetry with GDN2) */
   ATOMIC_MAMBA2_SAVE = 1,
   /* backward: the workspace holds the intermediates of an
-     atomic_mamba2_fwd(..., ATOMIC_MAMBA2_SAVE) call on identical inputs */
+     atomic_mamba2_fwd call on identical inputs (checked as for
+     ATOMIC_GDN2_REUSE: ATOMIC_ERR_REUSE otherwise) */
   ATOMIC_MAMBA2_REUSE = 2
 };
 

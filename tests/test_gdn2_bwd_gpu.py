@@ -169,3 +169,38 @@ def test_longer_chunks_match_the_oracle_at_that_chunk(chunk, dtype, K, g_mean):
     print(f"  rel_err o={eo:.2e} h_final={eh:.2e}")
     assert eo < tol_for(dtype) and eh < tol_for(dtype)
     _check(out, ref, dtype, (dtype,) * 5 + (F32, F32))
+
+
+def test_reuse_requires_the_matching_forward():
+    """REUSE on a workspace that holds another forward is refused before any
+    launch: other input tensors (same shapes), and the workspace overwritten by
+    another call of the library since; the matching forward reuses as before,
+    and a non-contiguous input turns reuse into a recompute (same gradients)."""
+    from atomic_ops import _lib
+    from atomic_ops import norm_gate as NG
+    banner("gdn2 reuse tag")
+    args, _ = _case(1, 128, 2, 64, BF16, 41)
+    q, k, v, w, b, g, dO, _, _ = (t.cuda() if t is not None else None for t in args)
+    _, _, ws = G.forward(q, k, v, w, b, g, 1.0, save=True)
+    with pytest.raises(_lib.AtomicError, match="REUSE"):
+        G.backward(q.clone(), k, v, w, b, g, 1.0, dO, workspace=ws, reuse=True)
+    ref = G.backward(q, k, v, w, b, g, 1.0, dO, workspace=ws, reuse=True)
+    again = G.backward(q, k, v, w, b, g, 1.0, dO, workspace=ws, reuse=True)   # the forward is still there
+    for a, r in zip(again, ref):
+        assert torch.equal(a, r)
+    # another entry point writes the workspace: its record is gone
+    rows, d = 64, 512
+    x = torch.randn(rows, d, device="cuda")
+    gate = torch.randn(rows, d, device="cuda").to(BF16)
+    NG.backward(x, gate, torch.ones(d, device="cuda"), torch.randn(rows, d, device="cuda").to(BF16), NG.GDN2,
+                workspace=ws)
+    with pytest.raises(_lib.AtomicError, match="REUSE"):
+        G.backward(q, k, v, w, b, g, 1.0, dO, workspace=ws, reuse=True)
+    # a transposed-and-back (non-contiguous) input is copied, so the call recomputes
+    _, _, ws = G.forward(q, k, v, w, b, g, 1.0, save=True)
+    qn = q.transpose(1, 2).contiguous().transpose(1, 2)
+    assert not qn.is_contiguous()
+    got = G.backward(qn, k, v, w, b, g, 1.0, dO, workspace=ws, reuse=True)
+    torch.cuda.synchronize()
+    for a, r in zip(got, ref):
+        assert torch.equal(a, r)

@@ -153,3 +153,24 @@ def test_trainable_wrapper_at_the_model_call_site():
     print("  rel_err " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
     for n, e in errs.items():
         assert e < tol_for(BF16), (n, e)
+
+
+def test_reuse_requires_the_matching_forward():
+    """REUSE on a workspace that holds another forward is refused before any
+    launch; the matching forward's workspace is reused (twice), and gives the
+    recompute's gradients."""
+    from atomic_ops import _lib
+    banner("mamba2 reuse tag")
+    d = inputs.mamba2_inputs(1, 256, 2, 64, 128, seed=43, device=torch.device("cuda"), dO=True)
+    dt, x, Bm, Cm, A, dy = (d[n] for n in ("dt", "x", "Bm", "Cm", "A", "dy"))
+    _, _, ws = M.forward(dt, x, Bm, Cm, A, 128, save=True)
+    with pytest.raises(_lib.AtomicError, match="REUSE"):
+        M.backward(dt, x.clone(), Bm, Cm, A, 128, dy, workspace=ws, reuse=True)
+    r1 = M.backward(dt, x, Bm, Cm, A, 128, dy, workspace=ws, reuse=True)
+    r2 = M.backward(dt, x, Bm, Cm, A, 128, dy, workspace=ws, reuse=True)
+    rc = M.backward(dt, x, Bm, Cm, A, 128, dy)
+    torch.cuda.synchronize()
+    for a, b_, c in zip(r1, r2, rc):
+        if a is None:
+            continue
+        assert torch.equal(a, b_) and torch.equal(a, c)
