@@ -116,7 +116,7 @@ def mamba2_prologue_model(B, L, d, N):
 def mamba2_groups(B, T, H, C):
     NT = T // C
     G = 1
-    while G * B * NT < 1024 and 2 * G <= H and H % (2 * G) == 0:
+    while G * B * NT < 512 and 2 * G <= H and H % (2 * G) == 0:
         G *= 2
     return G
 
