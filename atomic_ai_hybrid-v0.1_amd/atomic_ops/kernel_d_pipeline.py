@@ -1,0 +1,77 @@
+"""Stage-level GDN2 forward (mirror of reference atomic_ops/kernel_d_pipeline.py).
+
+``gdn2_inter_chunk_combine(Aqk, w_pseudo, u, kg, qg, gc_last, scale, h0=None,
+debug_tag="")`` keeps the reference signature (kernel_d_pipeline.py:94) and
+returns ``(o, h_final)`` with o per chunk, ``[B, H, NT, BT, V]`` float32;
+``build_chunk_wy(q, k, v, w, b, g, scale)`` runs the reference's kernels
+A + B + C (build_chunk_scores_pallas, wy_solve_pallas, recompute_wy_pallas:
+kernel_a_scores.py:69, kernel_b_solve.py:151, kernel_c_recompute.py:91) as one
+pass and returns ``(Aqk, A, w_pseudo, u, kg, qg, gc_last)``.  Both run at
+64-row chunks (BT = 64, the whole-path chunk of this library); the arrays are
+float32 for float32 inputs and bfloat16 for bfloat16 ones (gc_last float32).
+Every computation runs in libatomic_hybrid.so; there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from . import gdn2 as _g
+from .kernel_trainable_B6 import gdn2_pallas_forward  # noqa: F401  (the whole staged forward)
+
+BT = 64
+
+
+def build_chunk_wy(q, k, v, w, b, g, scale):
+    """Per-chunk ``(Aqk, A, w_pseudo, u, kg, qg, gc_last)`` of q, k, b, g
+    [B, T, H, K], v, w [B, T, H, V]: Aqk, A [B, H, NT, 64, 64], w_pseudo, kg,
+    qg [B, H, NT, 64, K], u [B, H, NT, 64, V], gc_last [B, H, NT, K]."""
+    _g._check_inputs(q, k, v, w, b, g)
+    q, k, v, w, b, g = (t.contiguous() for t in (q, k, v, w, b, g))
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    NT = T // BT
+    args = _g.make_args(q, v, scale, chunk=BT)
+    dt, dev = q.dtype, q.device
+    Aqk = torch.empty(B, H, NT, BT, BT, dtype=dt, device=dev)
+    A = torch.empty(B, H, NT, BT, BT, dtype=dt, device=dev)
+    wp, kg, qg = (torch.empty(B, H, NT, BT, K, dtype=dt, device=dev) for _ in range(3))
+    u = torch.empty(B, H, NT, BT, V, dtype=dt, device=dev)
+    gl = torch.empty(B, H, NT, K, dtype=torch.float32, device=dev)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    rc = _lib.load().atomic_gdn2_chunk_wy(ctypes.byref(args), p(q), p(k), p(v), p(w), p(b), p(g), p(Aqk), p(A),
+                                          p(wp), p(u), p(kg), p(qg), p(gl), _g._stream(dev))
+    _lib.check(rc, "atomic_gdn2_chunk_wy")
+    return Aqk, A, wp, u, kg, qg, gl
+
+
+def gdn2_inter_chunk_combine(Aqk, w_pseudo, u, kg, qg, gc_last, scale, h0=None, debug_tag=""):
+    """Kernel D over per-chunk arrays (see ``build_chunk_wy``); h0 [B, H, K, V]
+    (sanitised like the reference's ``_sanitize_h0``) or None.  Returns o
+    [B, H, NT, BT, V] float32 and h_final [B, H, K, V] float32."""
+    B, H, NT, C, K = w_pseudo.shape
+    V = u.shape[-1]
+    if C != BT:
+        raise _lib.AtomicError(f"gdn2_inter_chunk_combine: chunks of {C} rows (this library runs {BT})")
+    dt = w_pseudo.dtype
+    for t in (Aqk, w_pseudo, u, kg, qg):
+        if t.dtype != dt or not t.is_cuda:
+            raise TypeError("per-chunk arrays must share one dtype and live on the device")
+    if Aqk.shape != (B, H, NT, C, C) or u.shape[:4] != (B, H, NT, C) or kg.shape != w_pseudo.shape \
+            or qg.shape != w_pseudo.shape or gc_last.shape != (B, H, NT, K):
+        raise ValueError("inconsistent per-chunk array shapes")
+    Aqk, w_pseudo, u, kg, qg = (t.contiguous() for t in (Aqk, w_pseudo, u, kg, qg))
+    gc_last = gc_last.to(torch.float32).contiguous()
+    dev = w_pseudo.device
+    args = _lib.Gdn2Args(B, NT * C, H, K, V, C, _g._DT[dt], _g._DT[dt], float(scale), 0, None, None)
+    if h0 is not None:
+        h0 = h0.to(torch.float32).contiguous()
+    o = torch.empty(B, H, NT, C, V, dtype=torch.float32, device=dev)
+    h_final = torch.empty(B, H, K, V, dtype=torch.float32, device=dev)
+    p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+    rc = _lib.load().atomic_gdn2_inter_chunk_combine(ctypes.byref(args), p(Aqk), p(w_pseudo), p(u), p(kg), p(qg),
+                                                     p(gc_last), p(h0), p(o), p(h_final), _g._stream(dev))
+    _lib.check(rc, "atomic_gdn2_inter_chunk_combine")
+    return o, h_final

@@ -483,12 +483,19 @@ struct StateLds {
   static constexpr int total = off_vn + VT * LC * (int)sizeof(T);
 };
 
+// gdn2_fwd_state mode bits: keep the per-chunk states and v_new for the
+// backward; write o per chunk ([B][H][NT][C][V], the layout of
+// gdn2_inter_chunk_combine's result, kernel_d_pipeline.py:94-124) instead of
+// [B][T][H][V]; sanitise h0 (nan_to_num(clip(h0, +-1e4)), its _sanitize_h0).
+enum { kStateSave = 1, kStateChunkO = 2, kStateSanitizeH0 = 4 };
+
 // Eight waves (two per SIMD): the state tiles and the [w; q] h tiles of one
 // V tile split over them by row blocks.
 template <typename T, int C, int K, int V, int VT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T> ck,
                                                      const float* __restrict__ h0, float* __restrict__ o,
-                                                     float* __restrict__ h_final, int save) {
+                                                     float* __restrict__ h_final, int mode) {
+  const int save = mode & kStateSave;
   typedef StateLds<T, C, K, V, VT> L;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
   T* sHt = reinterpret_cast<T*>(lds + L::off_ht);
@@ -527,7 +534,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int d = 16 * mi + tile_row(i), vv = v0 + 16 * ni + tile_col();
-      hs[t][i] = h0 ? h0[((size_t)bh * K + d) * V + vv] : 0.f;
+      const float hv = h0 ? h0[((size_t)bh * K + d) * V + vv] : 0.f;
+      hs[t][i] = (mode & kStateSanitizeH0) ? sanitize(hv) : hv;
     }
     store_tile_t(sHt, L::LK, 16 * mi, 16 * ni, hs[t]);
   }
@@ -623,7 +631,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (save) unstage_rows<T, VT, C, NTHR>(ck.vnT + bhn * V * C + (size_t)v0 * C, C, sVn, L::LC);
 
       // o = scale qg h + Aqk v_new   (rows of the qg half)
-      float* og = o ? o + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0 : nullptr;
+      const bool chunk_o = (mode & kStateChunkO) != 0;
+      float* og = !o ? nullptr
+                     : chunk_o ? o + (size_t)bhn * C * V + v0
+                               : o + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0;
+      const size_t ors = chunk_o ? (size_t)V : (size_t)dm.H * V;  // o's row stride
   #pragma unroll
       for (int gi = 0; gi < XPW / GX; ++gi) {
         const int tile0 = wv_id * XPW + gi * GX, mi = tile0 / NTI, ni0 = tile0 % NTI;
@@ -642,7 +654,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   #pragma unroll
               for (int i = 0; i < 4; ++i) {
                 const int r = 16 * mo + tile_row(i), c = 16 * (ni0 + u) + tile_col();
-                og[(size_t)r * dm.H * V + c] = n2n(acc[u][i]);
+                og[(size_t)r * ors + c] = n2n(acc[u][i]);
               }
           }
         }

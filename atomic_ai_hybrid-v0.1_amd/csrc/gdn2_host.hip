@@ -144,18 +144,24 @@ static Gdn2Chunks<T> gdn2_chunks(const Gdn2Plan& p, void* ws) {
   return c;
 }
 
+// Kernels A + B + C (gdn2_fwd_intra): the per-chunk intermediates into ck.
 template <typename T, int K>
-static int gdn2_forward_impl(const Gdn2Plan& p, const void* q, const void* k, const void* v,
-                             const void* w, const void* b, const float* g, const float* h0,
-                             float* o, float* h_final, void* ws, int save, Launch& L) {
-  constexpr int C = 64, V = K, VT = 32;
-  Gdn2Chunks<T> ck = gdn2_chunks<T>(p, ws);
+static int gdn2_intra_launch(const Gdn2Plan& p, const void* q, const void* k, const void* v, const void* w,
+                             const void* b, const float* g, const Gdn2Chunks<T>& ck, Launch& L) {
+  constexpr int C = 64, V = K;
   hipStream_t st = L.st;
-  int rc = L("gdn2_fwd_intra", [&] {
+  return L("gdn2_fwd_intra", [&] {
     hipLaunchKernelGGL((gdn2_fwd_intra<T, C, K, V>), dim3((unsigned)p.bhn), dim3(256), 0, st, p.dm,
                        (const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b, g, ck);
   });
-  if (rc) return rc;
+}
+
+// Kernel D (gdn2_fwd_state) over the intermediates in ck; mode: kState* bits.
+template <typename T, int K>
+static int gdn2_state_launch(const Gdn2Plan& p, const Gdn2Chunks<T>& ck, const float* h0, float* o,
+                             float* h_final, int mode, Launch& L) {
+  constexpr int C = 64, V = K, VT = 32;
+  hipStream_t st = L.st;
   const int bh = p.dm.B * p.dm.H;
   if constexpr (sizeof(T) == 2 && K == 128) {
     // Few (batch, head) pairs (long sequences at batch 1): 16-column V tiles
@@ -166,15 +172,25 @@ static int gdn2_forward_impl(const Gdn2Plan& p, const void* q, const void* k, co
     if (bh * (V / VT16) <= 256) {
       return L("gdn2_fwd_state", [&] {
         hipLaunchKernelGGL((gdn2_fwd_state<T, C, K, V, VT16>), dim3((unsigned)(bh * (V / VT16))), dim3(512), 0,
-                           st, p.dm, ck, h0, o, h_final, save);
+                           st, p.dm, ck, h0, o, h_final, mode);
       });
     }
   }
   const unsigned nwg = (unsigned)(bh * (V / VT));
   return L("gdn2_fwd_state", [&] {
     hipLaunchKernelGGL((gdn2_fwd_state<T, C, K, V, VT>), dim3(nwg), dim3(512), 0, st, p.dm, ck, h0, o,
-                       h_final, save);
+                       h_final, mode);
   });
+}
+
+template <typename T, int K>
+static int gdn2_forward_impl(const Gdn2Plan& p, const void* q, const void* k, const void* v,
+                             const void* w, const void* b, const float* g, const float* h0,
+                             float* o, float* h_final, void* ws, int save, Launch& L) {
+  Gdn2Chunks<T> ck = gdn2_chunks<T>(p, ws);
+  int rc = gdn2_intra_launch<T, K>(p, q, k, v, w, b, g, ck, L);
+  if (rc) return rc;
+  return gdn2_state_launch<T, K>(p, ck, h0, o, h_final, save ? kStateSave : 0, L);
 }
 
 template <typename T>
@@ -555,6 +571,77 @@ extern "C" int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const v
   if (a->dtype == ATOMIC_BF16)
     return gdn2_backward_diag_t<bf16>(p, D, dq, dk, dv, dw, db, dg, dh0, workspace);
   return gdn2_backward_diag_t<float>(p, D, dq, dk, dv, dw, db, dg, dh0, workspace);
+}
+
+// ------------------------------------------------ stage-level forward
+// The two halves of the forward over caller-owned per-chunk arrays in the
+// reference's layout ([B][H][NT][64][D], gc_last [B][H][NT][K]), in
+// args.dtype (gc_last and the outputs fp32): kernels A + B + C in one pass,
+// then kernel D.  64-row chunks only (the arrays are per chunk).
+static int gdn2_stage_plan(const atomic_gdn2_args* a, Gdn2Plan* p) {
+  const int rc = gdn2_plan(a, p);
+  if (rc != ATOMIC_OK) return rc;
+  return a->chunk == kGdn2RunChunk ? ATOMIC_OK : ATOMIC_ERR_SHAPE;
+}
+
+template <typename T>
+static Gdn2Chunks<T> gdn2_stage_chunks(void* aqk, void* ainv, void* wt, void* u, void* kg, void* qg, float* gcl) {
+  Gdn2Chunks<T> c;
+  c.qg = (T*)qg;
+  c.kg = (T*)kg;
+  c.wt = (T*)wt;
+  c.u = (T*)u;
+  c.aqk = (T*)aqk;
+  c.ainv = (T*)ainv;
+  c.gcl = gcl;
+  c.hT = nullptr;
+  c.vnT = nullptr;
+  return c;
+}
+
+extern "C" int atomic_gdn2_chunk_wy(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
+                                    const void* w, const void* b, const float* g, void* Aqk, void* A,
+                                    void* w_pseudo, void* u, void* kg, void* qg, float* gc_last, void* stream) {
+  Gdn2Plan p;
+  const int rc = gdn2_stage_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!q || !k || !v || !w || !b || !g || !Aqk || !A || !w_pseudo || !u || !kg || !qg || !gc_last)
+    return ATOMIC_ERR_NULL;
+  Launch L{a->profile, (hipStream_t)stream};
+  if (a->dtype == ATOMIC_BF16) {
+    const Gdn2Chunks<bf16> ck = gdn2_stage_chunks<bf16>(Aqk, A, w_pseudo, u, kg, qg, gc_last);
+    return p.dm.K == 128 ? gdn2_intra_launch<bf16, 128>(p, q, k, v, w, b, g, ck, L)
+                         : gdn2_intra_launch<bf16, 64>(p, q, k, v, w, b, g, ck, L);
+  }
+  const Gdn2Chunks<float> ck = gdn2_stage_chunks<float>(Aqk, A, w_pseudo, u, kg, qg, gc_last);
+  return p.dm.K == 128 ? gdn2_intra_launch<float, 128>(p, q, k, v, w, b, g, ck, L)
+                       : gdn2_intra_launch<float, 64>(p, q, k, v, w, b, g, ck, L);
+}
+
+extern "C" int atomic_gdn2_inter_chunk_combine(const atomic_gdn2_args* a, const void* Aqk, const void* w_pseudo,
+                                               const void* u, const void* kg, const void* qg,
+                                               const float* gc_last, const float* h0, float* o, float* h_final,
+                                               void* stream) {
+  Gdn2Plan p;
+  const int rc = gdn2_stage_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!Aqk || !w_pseudo || !u || !kg || !qg || !gc_last || !o || !h_final) return ATOMIC_ERR_NULL;
+  Launch L{a->profile, (hipStream_t)stream};
+  const int mode = kStateChunkO | kStateSanitizeH0;
+  void* aq = const_cast<void*>(Aqk);
+  void* wt = const_cast<void*>(w_pseudo);
+  void* uu = const_cast<void*>(u);
+  void* kk = const_cast<void*>(kg);
+  void* qq = const_cast<void*>(qg);
+  float* gl = const_cast<float*>(gc_last);
+  if (a->dtype == ATOMIC_BF16) {
+    const Gdn2Chunks<bf16> ck = gdn2_stage_chunks<bf16>(aq, nullptr, wt, uu, kk, qq, gl);
+    return p.dm.K == 128 ? gdn2_state_launch<bf16, 128>(p, ck, h0, o, h_final, mode, L)
+                         : gdn2_state_launch<bf16, 64>(p, ck, h0, o, h_final, mode, L);
+  }
+  const Gdn2Chunks<float> ck = gdn2_stage_chunks<float>(aq, nullptr, wt, uu, kk, qq, gl);
+  return p.dm.K == 128 ? gdn2_state_launch<float, 128>(p, ck, h0, o, h_final, mode, L)
+                       : gdn2_state_launch<float, 64>(p, ck, h0, o, h_final, mode, L);
 }
 
 extern "C" int atomic_gdn2_fwd_noalloc(const atomic_gdn2_args* a, const void* q, const void* k,

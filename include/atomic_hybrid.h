@@ -204,6 +204,30 @@ int atomic_gdn2_fwd_noalloc(const atomic_gdn2_args* a, const void* q, const void
                             const void* w, const void* b, const float* g, const float* h0, float* o,
                             float* h_final, void* stream);
 
+/* ------------------------------------------------------------------------
+ * GDN2 stage-level forward: the staged pipeline's two halves over caller-owned
+ * per-chunk arrays in the reference's layout, 64-row chunks (args.chunk = 64;
+ * the arrays are per chunk).  Operands in args.dtype; gc_last, o, h_final fp32.
+ *   Aqk, A : [B][H][NT][64][64]   w_pseudo, kg, qg : [B][H][NT][64][K]
+ *   u : [B][H][NT][64][V]         gc_last : [B][H][NT][K]
+ *
+ * Kernels A + B + C in one pass: build_chunk_scores_pallas (Aqk, scaled;
+ * kernel_a_scores.py:69), wy_solve_pallas (A = (I + Akk)^-1;
+ * kernel_b_solve.py:151) and recompute_wy_pallas (w_pseudo, u, kg, qg,
+ * gc_last; kernel_c_recompute.py:91).  Akk itself stays on chip.
+ */
+int atomic_gdn2_chunk_wy(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
+                         const void* w, const void* b, const float* g, void* Aqk, void* A, void* w_pseudo,
+                         void* u, void* kg, void* qg, float* gc_last, void* stream);
+
+/* Kernel D: gdn2_inter_chunk_combine (kernel_d_pipeline.py:94-124), the
+ * sequential state loop over those arrays.  h0 [B][H][K][V] (NULL: zeros) is
+ * sanitised first like the reference's _sanitize_h0 (:54-55); o is written per
+ * chunk, [B][H][NT][64][V] fp32, and h_final [B][H][K][V] fp32. */
+int atomic_gdn2_inter_chunk_combine(const atomic_gdn2_args* a, const void* Aqk, const void* w_pseudo,
+                                    const void* u, const void* kg, const void* qg, const float* gc_last,
+                                    const float* h0, float* o, float* h_final, void* stream);
+
 /* ---------------------------------------------------------------- Mamba2 */
 
 enum {

@@ -132,6 +132,27 @@ def gdn2_chunked_wy_reference(q, k, v, g, b, w, scale, chunk_size, h0=None,
     return o, h
 
 
+def gdn2_inter_chunk_combine(Aqk, w_pseudo, u, kg, qg, gc_last, scale, h0=None, dtype=torch.float64):
+    """Kernel D of the staged forward, ``gdn2_inter_chunk_combine``
+    (kernel_d_pipeline.py:94-124), over per-chunk arrays in its layout:
+    Aqk [B, H, NT, C, C]; w_pseudo, kg, qg [B, H, NT, C, K]; u [B, H, NT, C, V];
+    gc_last [B, H, NT, K].  Returns o [B, H, NT, C, V] and h_final.  Unlike the
+    chunked reference it sanitises h0 first (``_sanitize_h0``, :54-55,101)."""
+    f = dtype
+    Aqk, w_pseudo, u, kg, qg, gc_last = (t.to(f) for t in (Aqk, w_pseudo, u, kg, qg, gc_last))
+    B, H, NT, C, K = w_pseudo.shape
+    V = u.shape[-1]
+    h = torch.zeros(B, H, K, V, dtype=f) if h0 is None else sanitize(h0.to(f))   # :98-101
+    outs = []
+    for n in range(NT):                                                        # :105-123
+        h_pre = h
+        v_new = u[:, :, n] - w_pseudo[:, :, n] @ h_pre
+        o_c = scale * (qg[:, :, n] @ h_pre) + Aqk[:, :, n] @ v_new
+        h = sanitize(h_pre * torch.exp(gc_last[:, :, n])[..., None] + kg[:, :, n].transpose(-1, -2) @ v_new)
+        outs.append(n2n(o_c))
+    return torch.stack(outs, 2), h
+
+
 def gdn2_token_serial_reference(q, k, v, g, b, w, scale, h0=None, dtype=torch.float64):
     """Token-serial recurrence (gdn2_wy_reference.py:33-56), an independent
     oracle for the chunked form.  Returns o in ``dtype`` (the reference casts

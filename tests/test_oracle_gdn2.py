@@ -198,3 +198,30 @@ def test_planted_mistakes_are_caught(monkeypatch):
     monkeypatch.setattr(og, "build_chunk_wy", diag_kept)
     o_bad, _ = og.gdn2_chunked_wy_reference(q, k, v, g, b, w, 1.0, 8)
     assert _rel(o_bad, o_s) > 1e-6
+
+
+def test_inter_chunk_combine_reproduces_the_chunked_reference():
+    """Kernel D's restatement fed with the chunked reference's own per-chunk
+    stages gives its o and h_final (the combine is the reference's scan step
+    over those stages); a NaN / +-inf / beyond-1e4 h0 is sanitised first."""
+    B, T, H, K, C = 1, 192, 2, 8, 64
+    gen = torch.Generator().manual_seed(17)
+    r = lambda *s: torch.randn(*s, generator=gen, dtype=torch.float64)
+    q, k = torch.nn.functional.normalize(r(B, T, H, K), dim=-1), torch.nn.functional.normalize(r(B, T, H, K), dim=-1)
+    v, w = r(B, T, H, K), torch.sigmoid(r(B, T, H, K))
+    b, g = torch.sigmoid(r(B, T, H, K)), torch.nn.functional.logsigmoid(r(B, T, H, K) + 3.0)
+    h0 = 0.5 * r(B, H, K, K)
+    o, h, st = og.gdn2_chunked_wy_reference(q, k, v, g, b, w, 0.7, C, h0=h0, return_stages=True)
+    stack = lambda name: torch.stack([s[name] for s in st], 2)
+    o_c, h_c = og.gdn2_inter_chunk_combine(stack("Aqk"), stack("w_pseudo"), stack("u"), stack("kg"), stack("qg"),
+                                           stack("gc_last"), 0.7, h0=h0)
+    o_c = o_c.permute(0, 2, 3, 1, 4).reshape(B, T, H, K)
+    assert torch.allclose(o_c, o, rtol=0, atol=1e-12) and torch.allclose(h_c, h, rtol=0, atol=1e-12)
+    bad = h0.clone()
+    bad[0, 0, 0, 0], bad[0, 0, 1, 1], bad[0, 1, 2, 2], bad[0, 1, 3, 3] = float("nan"), float("inf"), 5e4, -float("inf")
+    o_b, h_b = og.gdn2_inter_chunk_combine(stack("Aqk"), stack("w_pseudo"), stack("u"), stack("kg"), stack("qg"),
+                                           stack("gc_last"), 0.7, h0=bad)
+    clean = torch.nan_to_num(bad.clamp(-1e4, 1e4), nan=0.0, posinf=1e4, neginf=-1e4)
+    o_r, h_r = og.gdn2_inter_chunk_combine(stack("Aqk"), stack("w_pseudo"), stack("u"), stack("kg"), stack("qg"),
+                                           stack("gc_last"), 0.7, h0=clean)
+    assert torch.equal(o_b, o_r) and torch.equal(h_b, h_r) and torch.isfinite(o_b).all()
