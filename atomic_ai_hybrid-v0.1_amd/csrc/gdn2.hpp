@@ -21,6 +21,7 @@ struct Gdn2Chunks {
   T* u;       // [C][V]  A (w v)
   T* aqk;     // [C][C]  scale * sum_d q k exp(gc_i - gc_j), causal
   T* ainv;    // [C][C]  A = (I + Akk)^-1
+  T* akk;     // [C][C]  strict Akk (written or read by the stage-level kernels A / B only)
   float* gcl; // [K]     gc of the chunk's last row
   T* hT;      // [V][K]  state entering the chunk, transposed (saved for backward)
   T* vnT;     // [V][C]  v_new = u - w_pseudo h, transposed (saved for backward)

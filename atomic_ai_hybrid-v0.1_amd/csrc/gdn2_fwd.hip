@@ -173,7 +173,16 @@ __device__ void intra_scores_exact(const float* sgc, const T* q, const T* k, con
   }
 }
 
-template <typename T, int C, int K, int V>
+// What one gdn2_fwd_intra launch builds: the whole per-chunk build (kernels
+// A + B + C in one pass), or one of the reference's three kernels over
+// caller-owned per-chunk arrays:
+//   kIntraScores    A: Aqk and the strict Akk (kernel_a_scores.py:21-66)
+//   kIntraSolve     B: A = (I + Akk)^-1 from a given Akk (kernel_b_solve.py)
+//   kIntraRecompute C: w_pseudo = A kb, u = A (w v), kg, qg, gc_last from a
+//                   given A, all clipped to +-1e4 (kernel_c_recompute.py:46-88)
+enum { kIntraAll = 0, kIntraScores = 1, kIntraSolve = 2, kIntraRecompute = 3 };
+
+template <typename T, int C, int K, int V, int ST = kIntraAll>
 __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __restrict__ q,
                                                      const T* __restrict__ k, const T* __restrict__ v,
                                                      const T* __restrict__ w, const T* __restrict__ b,
@@ -209,25 +218,36 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
   // q, k, b, v, w are requested before the cumsum of g, so their latency overlaps it
   const int cg = tid % L::NCG, seg = tid / L::NCG;
   const int cgv = tid % L::NCGV, segv = tid / L::NCGV;
+  constexpr bool kRows = ST != kIntraSolve;                          // reads q, k, b, g
+  constexpr bool kVals = ST == kIntraAll || ST == kIntraRecompute;   // reads v, w; writes qg, kg
+  constexpr bool kScores = ST == kIntraAll || ST == kIntraScores;
+  // the stage-level kernel C clips every output to +-1e4 (kernel_c_recompute.py:74-82)
+  auto fin = [](float x) { return ST == kIntraRecompute ? sanitize(x) : n2n(x); };
   Raw8<T> rq[L::RS], rk[L::RS], rb[L::RS], rv[L::RSV], rw[L::RSV];
+  if constexpr (kRows) {
 #pragma unroll
-  for (int rr = 0; rr < L::RS; ++rr) {
-    const size_t o = (size_t)(seg * L::RS + rr) * rsK + cg * 8;
-    rq[rr].load(qc + o);
-    rk[rr].load(kc + o);
-    rb[rr].load(bc + o);
+    for (int rr = 0; rr < L::RS; ++rr) {
+      const size_t o = (size_t)(seg * L::RS + rr) * rsK + cg * 8;
+      rq[rr].load(qc + o);
+      rk[rr].load(kc + o);
+      rb[rr].load(bc + o);
+    }
   }
+  if constexpr (kVals) {
 #pragma unroll
-  for (int rr = 0; rr < L::RSV; ++rr) {
-    const size_t o = (size_t)(segv * L::RSV + rr) * rsV + cgv * 8;
-    rv[rr].load(vc + o);
-    rw[rr].load(wc + o);
+    for (int rr = 0; rr < L::RSV; ++rr) {
+      const size_t o = (size_t)(segv * L::RSV + rr) * rsV + cgv * 8;
+      rv[rr].load(vc + o);
+      rw[rr].load(wc + o);
+    }
   }
 
+  bool exact = false;
+  if constexpr (kRows) {
   // ---- phase 0: gc = cumsum(g) over the chunk (gdn2_wy_reference.py:63)
   float gcr[L::RS][8];
-  const bool exact = chunk_cumsum<C, K>(gc_in, rsK, gcr, sTot, sGl);
-  if (tid < K) ck.gcl[(size_t)bhn * K + tid] = sGl[tid];
+  exact = chunk_cumsum<C, K>(gc_in, rsK, gcr, sTot, sGl);
+  if (kVals && tid < K) ck.gcl[(size_t)bhn * K + tid] = fin(sGl[tid]);
 
   // ---- phase 1: elementwise operands (gdn2_wy_reference.py:92-100)
   T* g_qg = ck.qg + (size_t)bhn * C * K;
@@ -247,18 +267,26 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
       o_kb[j] = (bv[j] * kv[j]) * e;
       o_kg[j] = kv[j] * __expf(sGl[cg * 8 + j] - gcv);
     }
-    store8(g_qg + r * K + cg * 8, o_qg);
-    store8(g_kg + r * K + cg * 8, o_kg);
     store8(sB + r * L::LK + cg * 8, o_kb);
-    if (!exact) {
-      store8(sQ + r * L::LK + cg * 8, o_qg);
-      store8(sK + r * L::LK + cg * 8, o_kt);
-    } else {
+    if constexpr (kScores) {
+      if (!exact) {
+        store8(sQ + r * L::LK + cg * 8, o_qg);
+        store8(sK + r * L::LK + cg * 8, o_kt);
+      } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) sGcExact[r * K + cg * 8 + j] = gcr[rr][j];
+        for (int j = 0; j < 8; ++j) sGcExact[r * K + cg * 8 + j] = gcr[rr][j];
+      }
+    }
+    if constexpr (kVals) {
+      if constexpr (ST == kIntraRecompute) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) { o_qg[j] = fin(o_qg[j]); o_kg[j] = fin(o_kg[j]); }
+      }
+      store8(g_qg + r * K + cg * 8, o_qg);
+      store8(g_kg + r * K + cg * 8, o_kg);
     }
   }
-  {
+  if constexpr (kVals) {
 #pragma unroll
     for (int rr = 0; rr < L::RSV; ++rr) {
       const int r = segv * L::RSV + rr;
@@ -272,12 +300,15 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
     }
   }
   __syncthreads();
+  }  // kRows
 
   // ---- phase 2: Aqk (causal, scaled) and Akk (strict) (gdn2_wy_reference.py:79-87)
   constexpr int NB = C / 16;
   constexpr int NTRI = NB * (NB + 1) / 2;
   T* g_aqk = ck.aqk + (size_t)bhn * C * C;
+  T* g_akk = ck.akk + (size_t)bhn * C * C;  // kernel A alone: Akk leaves in the operand type
   const int wv_id = wave_id();
+  if constexpr (kScores) {
   if (!exact) {
     constexpr int JPW = (2 * NTRI + 3) / 4;
     f32x4 res[JPW];
@@ -310,6 +341,7 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
       while (t > mi) { t -= mi + 1; ++mi; }
       const int ni = t;
       if (which == 0) store_tile_n(g_aqk, C, 16 * mi, 16 * ni, res[cnt]);
+      else if constexpr (ST == kIntraScores) store_tile_n(g_akk, C, 16 * mi, 16 * ni, res[cnt]);
       else store_tile_n(sAf, L::LA, 16 * mi, 16 * ni, res[cnt]);
     }
   } else {
@@ -321,7 +353,8 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
     for (int s = 0; s < PER; ++s) {
       const int e = tid + 256 * s, i = e / C, j = e % C;
       g_aqk[i * C + j] = from_f<T>(eqk[s]);
-      sAf[i * L::LA + j] = ekk[s];
+      if constexpr (ST == kIntraScores) g_akk[i * C + j] = from_f<T>(ekk[s]);
+      else sAf[i * L::LA + j] = ekk[s];
     }
   }
   // upper tiles of Aqk / Akk are zero
@@ -329,13 +362,29 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
     const int i = e / C, j = e % C;
     if ((j >> 4) > (i >> 4)) {
       if (!exact) g_aqk[i * C + j] = from_f<T>(0.f);
-      sAf[i * L::LA + j] = 0.f;
+      if constexpr (ST == kIntraScores) g_akk[i * C + j] = from_f<T>(0.f);
+      else sAf[i * L::LA + j] = 0.f;
     }
-    sX[i * L::LA + j] = 0.f;
+    if constexpr (ST == kIntraAll) sX[i * L::LA + j] = 0.f;
   }
+  if constexpr (ST == kIntraScores) return;
   __syncthreads();
+  }  // kScores
+  if constexpr (ST == kIntraSolve) {
+    // Akk from the caller (only its strictly lower blocks are read below)
+    for (int e = tid; e < C * C; e += 256) {
+      const int i = e / C, j = e % C;
+      sAf[i * L::LA + j] = to_f(g_akk[i * C + j]);
+      sX[i * L::LA + j] = 0.f;
+    }
+    __syncthreads();
+  }
 
   // ---- phase 3: A = (I + Akk)^-1 (gdn2_wy_reference.py:16-30,89-90)
+  T* g_ainv = ck.ainv + (size_t)bhn * C * C;
+  const T* opA;
+  int ldA;
+  if constexpr (ST != kIntraRecompute) {
   // Diagonal 16x16 blocks by forward substitution (wave w, lane = column).
   {
     const int lane = lane_id();
@@ -376,9 +425,6 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
   }
   __syncthreads();
   // n2n, operand-type copy, global A
-  T* g_ainv = ck.ainv + (size_t)bhn * C * C;
-  const T* opA;
-  int ldA;
   if constexpr (sizeof(T) == 2) {
     T* sAb = reinterpret_cast<T*>(lds + L::off_af);  // Akk is dead
     for (int e = tid; e < C * C / 8; e += 256) {  // 8 consecutive columns per item
@@ -402,6 +448,27 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
     opA = reinterpret_cast<const T*>(sX);
     ldA = L::LA;
   }
+  if constexpr (ST == kIntraSolve) return;
+  } else {
+    // A from the caller, into the operand-type rows phase 4 reads
+    if constexpr (sizeof(T) == 2) {
+      T* sAb = reinterpret_cast<T*>(lds + L::off_af);
+      for (int e = tid; e < C * C / 8; e += 256) {
+        const int i = e / (C / 8), j = (e % (C / 8)) * 8;
+        *reinterpret_cast<uint4*>(sAb + i * (C + Pad<T>::v) + j) =
+            *reinterpret_cast<const uint4*>(g_ainv + i * C + j);
+      }
+      opA = sAb;
+      ldA = C + Pad<T>::v;
+    } else {
+      for (int e = tid; e < C * C; e += 256) {
+        const int i = e / C, j = e % C;
+        sX[i * L::LA + j] = g_ainv[i * C + j];
+      }
+      opA = reinterpret_cast<const T*>(sX);
+      ldA = L::LA;
+    }
+  }
   __syncthreads();
 
   // ---- phase 4: w_pseudo = A kb, u = A wv (gdn2_wy_reference.py:92-96)
@@ -420,7 +487,7 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
 #pragma unroll
       for (int t = 0; t < NC / 16; ++t) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[t][i] = n2n(acc[t][i]);
+        for (int i = 0; i < 4; ++i) acc[t][i] = fin(acc[t][i]);
         store_tile_n(stg, L::LS, 0, 16 * t, acc[t]);
       }
       wave_lds_sync();
@@ -434,7 +501,8 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
       wave_lds_sync();  // the staging rows are rewritten next
     };
     for (int mi = wv_id; mi < NB; mi += 4) {
-      int kr = 16 * (mi + 1);
+      // A is block lower triangular; a caller's A (kernel C alone) is read whole
+      int kr = ST == kIntraRecompute ? C : 16 * (mi + 1);
       kr = ((kr + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
       if (kr > C) kr = C;
       row_block(mi, kr, sB, L::LK, std::integral_constant<int, K>(), g_wt);
@@ -447,14 +515,14 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
       const int jj = isu ? job - TW : job;
       const int nbk = isu ? V / 16 : K / 16;
       const int mi = jj / nbk, ni = jj % nbk;
-      int kr = 16 * (mi + 1);
+      int kr = ST == kIntraRecompute ? C : 16 * (mi + 1);
       kr = ((kr + Mma<T>::KS - 1) / Mma<T>::KS) * Mma<T>::KS;
       if (kr > C) kr = C;
       f32x4 acc = zero4();
       if (isu) acc = tile_mma<T, false, true>(acc, opA, ldA, sW, L::LV, 16 * mi, 16 * ni, kr);
       else acc = tile_mma<T, false, true>(acc, opA, ldA, sB, L::LK, 16 * mi, 16 * ni, kr);
   #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = n2n(acc[i]);
+      for (int i = 0; i < 4; ++i) acc[i] = fin(acc[i]);
       if (isu) store_tile_n(g_u, V, 16 * mi, 16 * ni, acc);
       else store_tile_n(g_wt, K, 16 * mi, 16 * ni, acc);
     }

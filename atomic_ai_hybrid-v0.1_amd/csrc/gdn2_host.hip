@@ -138,6 +138,7 @@ static Gdn2Chunks<T> gdn2_chunks(const Gdn2Plan& p, void* ws) {
   c.u = reinterpret_cast<T*>(base + p.o_u);
   c.aqk = reinterpret_cast<T*>(base + p.o_aqk);
   c.ainv = reinterpret_cast<T*>(base + p.o_ainv);
+  c.akk = nullptr;
   c.gcl = reinterpret_cast<float*>(base + p.o_gcl);
   c.hT = reinterpret_cast<T*>(base + p.o_ht);
   c.vnT = reinterpret_cast<T*>(base + p.o_vnt);
@@ -145,13 +146,14 @@ static Gdn2Chunks<T> gdn2_chunks(const Gdn2Plan& p, void* ws) {
 }
 
 // Kernels A + B + C (gdn2_fwd_intra): the per-chunk intermediates into ck.
-template <typename T, int K>
+template <typename T, int K, int ST = kIntraAll>
 static int gdn2_intra_launch(const Gdn2Plan& p, const void* q, const void* k, const void* v, const void* w,
                              const void* b, const float* g, const Gdn2Chunks<T>& ck, Launch& L) {
   constexpr int C = 64, V = K;
   hipStream_t st = L.st;
-  return L("gdn2_fwd_intra", [&] {
-    hipLaunchKernelGGL((gdn2_fwd_intra<T, C, K, V>), dim3((unsigned)p.bhn), dim3(256), 0, st, p.dm,
+  static const char* const names[] = {"gdn2_fwd_intra", "gdn2_chunk_scores", "gdn2_wy_solve", "gdn2_recompute_wy"};
+  return L(names[ST], [&] {
+    hipLaunchKernelGGL((gdn2_fwd_intra<T, C, K, V, ST>), dim3((unsigned)p.bhn), dim3(256), 0, st, p.dm,
                        (const T*)q, (const T*)k, (const T*)v, (const T*)w, (const T*)b, g, ck);
   });
 }
@@ -574,10 +576,10 @@ extern "C" int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const v
 }
 
 // ------------------------------------------------ stage-level forward
-// The two halves of the forward over caller-owned per-chunk arrays in the
-// reference's layout ([B][H][NT][64][D], gc_last [B][H][NT][K]), in
-// args.dtype (gc_last and the outputs fp32): kernels A + B + C in one pass,
-// then kernel D.  64-row chunks only (the arrays are per chunk).
+// The forward's stages over caller-owned per-chunk arrays in the reference's
+// layout ([B][H][NT][64][D], gc_last [B][H][NT][K]), in args.dtype (gc_last
+// and the outputs fp32): kernels A, B and C alone or in one pass, then
+// kernel D.  64-row chunks only (the arrays are per chunk).
 static int gdn2_stage_plan(const atomic_gdn2_args* a, Gdn2Plan* p) {
   const int rc = gdn2_plan(a, p);
   if (rc != ATOMIC_OK) return rc;
@@ -585,8 +587,10 @@ static int gdn2_stage_plan(const atomic_gdn2_args* a, Gdn2Plan* p) {
 }
 
 template <typename T>
-static Gdn2Chunks<T> gdn2_stage_chunks(void* aqk, void* ainv, void* wt, void* u, void* kg, void* qg, float* gcl) {
+static Gdn2Chunks<T> gdn2_stage_chunks(void* aqk, void* ainv, void* wt, void* u, void* kg, void* qg, float* gcl,
+                                       void* akk = nullptr) {
   Gdn2Chunks<T> c;
+  c.akk = (T*)akk;
   c.qg = (T*)qg;
   c.kg = (T*)kg;
   c.wt = (T*)wt;
@@ -616,6 +620,53 @@ extern "C" int atomic_gdn2_chunk_wy(const atomic_gdn2_args* a, const void* q, co
   const Gdn2Chunks<float> ck = gdn2_stage_chunks<float>(Aqk, A, w_pseudo, u, kg, qg, gc_last);
   return p.dm.K == 128 ? gdn2_intra_launch<float, 128>(p, q, k, v, w, b, g, ck, L)
                        : gdn2_intra_launch<float, 64>(p, q, k, v, w, b, g, ck, L);
+}
+
+// One of kernels A, B, C alone (ST), bf16 or fp32, K = 64 or 128.
+template <int ST>
+static int gdn2_stage_launch(const atomic_gdn2_args* a, const Gdn2Plan& p, const void* q, const void* k,
+                             const void* v, const void* w, const void* b, const float* g, void* aqk, void* akk,
+                             void* ainv, void* wt, void* u, void* kg, void* qg, float* gcl, void* stream) {
+  Launch L{a->profile, (hipStream_t)stream};
+  if (a->dtype == ATOMIC_BF16) {
+    const Gdn2Chunks<bf16> ck = gdn2_stage_chunks<bf16>(aqk, ainv, wt, u, kg, qg, gcl, akk);
+    return p.dm.K == 128 ? gdn2_intra_launch<bf16, 128, ST>(p, q, k, v, w, b, g, ck, L)
+                         : gdn2_intra_launch<bf16, 64, ST>(p, q, k, v, w, b, g, ck, L);
+  }
+  const Gdn2Chunks<float> ck = gdn2_stage_chunks<float>(aqk, ainv, wt, u, kg, qg, gcl, akk);
+  return p.dm.K == 128 ? gdn2_intra_launch<float, 128, ST>(p, q, k, v, w, b, g, ck, L)
+                       : gdn2_intra_launch<float, 64, ST>(p, q, k, v, w, b, g, ck, L);
+}
+
+extern "C" int atomic_gdn2_chunk_scores(const atomic_gdn2_args* a, const void* q, const void* k, const void* b,
+                                        const float* g, void* Aqk, void* Akk, void* stream) {
+  Gdn2Plan p;
+  const int rc = gdn2_stage_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!q || !k || !b || !g || !Aqk || !Akk) return ATOMIC_ERR_NULL;
+  return gdn2_stage_launch<kIntraScores>(a, p, q, k, nullptr, nullptr, b, g, Aqk, Akk, nullptr, nullptr, nullptr,
+                                         nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int atomic_gdn2_wy_solve(const atomic_gdn2_args* a, const void* Akk, void* A, void* stream) {
+  Gdn2Plan p;
+  const int rc = gdn2_stage_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!Akk || !A) return ATOMIC_ERR_NULL;
+  return gdn2_stage_launch<kIntraSolve>(a, p, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                        const_cast<void*>(Akk), A, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                        stream);
+}
+
+extern "C" int atomic_gdn2_recompute_wy(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
+                                        const void* w, const void* b, const float* g, const void* A,
+                                        void* w_pseudo, void* u, void* kg, void* qg, float* gc_last, void* stream) {
+  Gdn2Plan p;
+  const int rc = gdn2_stage_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!q || !k || !v || !w || !b || !g || !A || !w_pseudo || !u || !kg || !qg || !gc_last) return ATOMIC_ERR_NULL;
+  return gdn2_stage_launch<kIntraRecompute>(a, p, q, k, v, w, b, g, nullptr, nullptr, const_cast<void*>(A),
+                                            w_pseudo, u, kg, qg, gc_last, stream);
 }
 
 extern "C" int atomic_gdn2_inter_chunk_combine(const atomic_gdn2_args* a, const void* Aqk, const void* w_pseudo,

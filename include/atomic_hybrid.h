@@ -205,9 +205,12 @@ int atomic_gdn2_fwd_noalloc(const atomic_gdn2_args* a, const void* q, const void
                             float* h_final, void* stream);
 
 /* ------------------------------------------------------------------------
- * GDN2 stage-level forward: the staged pipeline's two halves over caller-owned
- * per-chunk arrays in the reference's layout, 64-row chunks (args.chunk = 64;
- * the arrays are per chunk).  Operands in args.dtype; gc_last, o, h_final fp32.
+ * GDN2 stage-level forward: the staged pipeline's kernels A, B, C, D over
+ * caller-owned per-chunk arrays in the reference's layout.  The chunk is 64
+ * rows (args.chunk = 64, the chunk of this library's kernels; the reference's
+ * Pallas kernels fix 256, kernel_a_scores.py:15, and its oracle takes any).
+ * The arrays are in args.dtype (the reference's are fp32); gc_last, o,
+ * h_final fp32.
  *   Aqk, A : [B][H][NT][64][64]   w_pseudo, kg, qg : [B][H][NT][64][K]
  *   u : [B][H][NT][64][V]         gc_last : [B][H][NT][K]
  *
@@ -219,6 +222,25 @@ int atomic_gdn2_fwd_noalloc(const atomic_gdn2_args* a, const void* q, const void
 int atomic_gdn2_chunk_wy(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
                          const void* w, const void* b, const float* g, void* Aqk, void* A, void* w_pseudo,
                          void* u, void* kg, void* qg, float* gc_last, void* stream);
+
+/* Kernel A alone: build_chunk_scores_pallas(q, k, b, g, scale)
+ * (kernel_a_scores.py:69-99): Aqk (causal, scaled) and the strict Akk,
+ * [B][H][NT][64][64] in args.dtype, nan_to_num'd (kernel_a_scores.py:65-66). */
+int atomic_gdn2_chunk_scores(const atomic_gdn2_args* a, const void* q, const void* k, const void* b,
+                             const float* g, void* Aqk, void* Akk, void* stream);
+
+/* Kernel B alone: wy_solve_pallas(Akk) (kernel_b_solve.py:151-169),
+ * A = (I + Akk)^-1 by 16-row block forward substitution; like the
+ * reference, only the strictly lower blocks of Akk are read. */
+int atomic_gdn2_wy_solve(const atomic_gdn2_args* a, const void* Akk, void* A, void* stream);
+
+/* Kernel C alone: recompute_wy_pallas(q, k, v, w, b, g, A)
+ * (kernel_c_recompute.py:91-123): w_pseudo = A (b k e^gc), u = A (w v),
+ * kg, qg, gc_last, each clipped to +-1e4 (kernel_c_recompute.py:74-82);
+ * the whole A is read. */
+int atomic_gdn2_recompute_wy(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
+                             const void* w, const void* b, const float* g, const void* A, void* w_pseudo,
+                             void* u, void* kg, void* qg, float* gc_last, void* stream);
 
 /* Kernel D: gdn2_inter_chunk_combine (kernel_d_pipeline.py:94-124), the
  * sequential state loop over those arrays.  h0 [B][H][K][V] (NULL: zeros) is

@@ -1,14 +1,20 @@
-"""Stage-level GDN2 forward through the C ABI: kernels A + B + C
-(``build_chunk_wy``) and kernel D (``gdn2_inter_chunk_combine``,
-kernel_d_pipeline.py:94-124) over per-chunk arrays in the reference's layout.
-Against the oracle's stages and its restatement of the combine, and the two
-stages chained against the whole-path forward."""
+"""Stage-level GDN2 forward through the C ABI: kernels A, B and C alone
+(``build_chunk_scores_pallas``, ``wy_solve_pallas``, ``recompute_wy_pallas``,
+kernel_a_scores.py:69, kernel_b_solve.py:151, kernel_c_recompute.py:91) and
+in one pass (``build_chunk_wy``), and kernel D (``gdn2_inter_chunk_combine``,
+kernel_d_pipeline.py:94-124), over per-chunk arrays in the reference's
+layout.  Against the oracle's stages and its restatement of the combine, the
+stages chained against the whole-path forward, and the solve against the
+identity (I + Akk) A = I."""
 import pytest
 import torch
 
 from _util import banner, rel_err, tol_for
 from atomic_ops import _lib, inputs
 from atomic_ops import gdn2 as G
+from atomic_ops import kernel_a_scores as KA
+from atomic_ops import kernel_b_solve as KB
+from atomic_ops import kernel_c_recompute as KC
 from atomic_ops import kernel_d_pipeline as KD
 from oracle import gdn2 as og
 
@@ -64,9 +70,76 @@ def test_chained_stages_equal_the_whole_forward(dtype):
     assert torch.equal(o_c, o_w) and torch.equal(h_c, h_w)
 
 
+def _oracle_stages(q, k, v, w, b, g, scale):
+    _, _, st = og.gdn2_chunked_wy_reference(q, k, v, g, b, w, scale, 64, return_stages=True)
+    return {n: torch.stack([s[n] for s in st], 2) for n in STAGES + ("Akk",)}
+
+
+@pytest.mark.parametrize("dtype,K", [(F32, 64), (F32, 128), (BF16, 64), (BF16, 128)])
+def test_kernels_a_b_c_alone_match_the_oracle(dtype, K):
+    """Each kernel on the oracle's inputs to that kernel, against the oracle's
+    outputs of it: A on q, k, b, g; B on the oracle's Akk (in the operand
+    type, against the oracle's inverse of that same Akk); C on the oracle's A."""
+    B, T, H = 2, 192, 2
+    banner(f"gdn2 kernels A, B, C alone {dtype} K{K}")
+    q, k, v, w, b, g = _inputs(B, T, H, K, dtype, 71 + K)
+    ref = _oracle_stages(q, k, v, w, b, g, 0.7)
+    dq, dk, dv, dw, db, dg = (t.cuda() for t in (q, k, v, w, b, g))
+    tol = tol_for(dtype)
+    Aqk, Akk = KA.build_chunk_scores_pallas(dq, dk, db, dg, 0.7)
+    akk_in = ref["Akk"].to(dtype)
+    A = KB.wy_solve_pallas(akk_in.cuda())
+    A_ref = og.n2n(og.wy_inverse(akk_in.double()))
+    outs = KC.recompute_wy_pallas(dq, dk, dv, dw, db, dg, ref["A"].to(dtype).cuda())
+    torch.cuda.synchronize()
+    checks = [("Aqk", Aqk, ref["Aqk"]), ("Akk", Akk, ref["Akk"]), ("A", A, A_ref)]
+    checks += [(n, t, ref[n]) for n, t in zip(STAGES[2:], outs)]
+    for name, t, r in checks:
+        e = rel_err(t, r)
+        print(f"  {name}: rel_err {e:.2e}")
+        assert t.shape == r.shape and t.dtype == (F32 if name == "gc_last" else dtype) and e < tol, name
+    # the strictly upper part of the scores is zero, the diagonal of Akk too
+    assert torch.count_nonzero(torch.triu(Aqk.float(), 1)).item() == 0
+    assert torch.count_nonzero(torch.triu(Akk.float(), 0)).item() == 0
+    # (I + Akk) A = I for the solve's own input
+    eye = torch.eye(64, dtype=torch.float64)
+    resid = (eye + akk_in.double()) @ A.cpu().double() - eye
+    print(f"  max |(I + Akk) A - I| = {resid.abs().max().item():.2e}")
+    assert resid.abs().max().item() < (1e-5 if dtype == F32 else 5e-3)
+
+
+def test_kernels_a_b_c_chained_equal_the_one_pass_build_in_fp32():
+    """fp32: Akk leaves kernel A in fp32, so A -> B -> C gives the one-pass
+    build's arrays bit for bit (kernel C's wider product only adds zeros)."""
+    B, T, H, K = 2, 256, 2, 128
+    banner("gdn2 kernels A -> B -> C vs the one-pass build (fp32)")
+    q, k, v, w, b, g = (t.cuda() for t in _inputs(B, T, H, K, F32, 81))
+    one = KD.build_chunk_wy(q, k, v, w, b, g, 0.9)
+    Aqk, Akk = KA.build_chunk_scores_pallas(q, k, b, g, 0.9)
+    A = KB.wy_solve_pallas(Akk)
+    wp, u, kg, qg, gl = KC.recompute_wy_pallas(q, k, v, w, b, g, A)
+    torch.cuda.synchronize()
+    for name, x, y in zip(STAGES, (Aqk, A, wp, u, kg, qg, gl), one):
+        assert torch.equal(x, y), name
+
+
+def test_kernel_c_clips_like_the_reference():
+    """Kernel C alone clips w_pseudo and u to +-1e4 (kernel_c_recompute.py:74-78):
+    a large A drives them past it."""
+    B, T, H, K = 1, 64, 1, 64
+    banner("gdn2 kernel C clip")
+    q, k, v, w, b, g = (t.cuda() for t in _inputs(B, T, H, K, F32, 91))
+    A = torch.full((B, H, 1, 64, 64), 1e6, device="cuda")
+    wp, u, kg, qg, gl = KC.recompute_wy_pallas(q, k, v, 10 * torch.ones_like(w), b, g, A)
+    torch.cuda.synchronize()
+    assert wp.abs().max().item() <= 1e4 and u.abs().max().item() == 1e4
+
+
 def test_stage_entries_reject_other_chunks():
     banner("gdn2 stage chunk check")
     q, k, v, w, b, g = (t.cuda() for t in _inputs(1, 256, 2, 64, F32, 3))
     with pytest.raises(_lib.AtomicError):
         KD.gdn2_inter_chunk_combine(*(torch.zeros(1, 2, 2, 128, n, device="cuda") for n in (128, 64, 64, 64, 64)),
                                     torch.zeros(1, 2, 2, 64, device="cuda"), 1.0)
+    with pytest.raises(ValueError):
+        KB.wy_solve_pallas(torch.zeros(1, 2, 2, 128, 128, device="cuda"))
