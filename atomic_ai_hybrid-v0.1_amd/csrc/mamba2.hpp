@@ -16,6 +16,10 @@ struct Mamba2Chunks {
   float* cl;     // [B][NT][H][P]      cumulative log decay at the chunk's last row
   float* src;    // [B][NT][H][P][N]   forward: sanitize(state_end) of each chunk;
                  //                    backward: (dy decay_h)^T C of each chunk
+                 //                    (stage-level entries: [B][H][NT][P][N])
+  // stage-level entries only (NULL on the whole path):
+  const float* cum;    // [B][H][NT][C][P]  the caller's cumdecay
+  const float* ydiag;  // [B][T][H][P]      the caller's y_diag (the combine)
 };
 
 }  // namespace ah

@@ -23,6 +23,15 @@
 //                     decay_chunk_end term (backward).
 // mamba2_chunk_y      one workgroup per (batch, chunk, head, 32 channels):
 //                     y = y_diag + y_off.
+// mamba2_cumdecay     one workgroup per (batch, chunk, head, 64 channels):
+//                     the stage-level kernel M2 alone (cumdecay to HBM).
+//
+// The stage-level entries (the reference's M2, M3 and M4 over caller-owned
+// arrays) run the same kernels in a stage mode: the cum comes from the
+// caller's cumdecay, the per-chunk arrays are in the reference's [B][H][NT]
+// order, and the arithmetic is that of the stage kernels, which drop the
+// 1e6 caps (kernel_mamba2_b_intra.py:96-112) and sanitise the chunk's write
+// and the initial state (kernel_mamba2_c_interchunk.py:58).
 //
 // y_diag on 16-row blocks: for output block I and source block J < I the
 // decay factorises as
@@ -83,6 +92,58 @@ __device__ __forceinline__ void column_cumsum(float* sCum, float* sTot) {
   for (int r = 0; r < RS; ++r) sCum[(seg * RS + r) * LD + p] = sanitize(v[r] + off, kClipAcc);
 }
 
+// ------------------------------------------------------------------ cumdecay (M2 alone)
+// build_chunk_cumdecay_pallas (kernel_mamba2_a_decay.py:53-66):
+// sanitize(cumsum(sanitize(dt A, 20)), 1e4), out[B][H][NT][C][P] fp32 (the
+// same cum the chunk kernels build in LDS).
+template <typename T, int C, int P, int PT>
+__global__ __launch_bounds__(256) void mamba2_cumdecay(Mamba2Dims dm, const T* __restrict__ dt,
+                                                      const float* __restrict__ A, float* __restrict__ out) {
+  constexpr int LC = PT + 4, NSEG = 256 / PT, NPT = P / PT;
+  __shared__ __attribute__((aligned(16))) float sCum[C * LC];
+  __shared__ __attribute__((aligned(16))) float sTot[NSEG * PT];
+  const int m = blockIdx.x % (dm.H * NPT), bn = blockIdx.x / (dm.H * NPT);
+  const int h = m / NPT, p0 = (m % NPT) * PT;
+  const int bb = bn / dm.NT, n = bn % dm.NT;
+  const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
+  const size_t rsx = (size_t)dm.H * P;
+  const size_t base = (row0 * dm.H + h) * P + p0;
+  const float Ah = A[h];
+  constexpr int PER_ROW = PT / 8, NE = C * PER_ROW, EPT = NE / 256;
+  static_assert(NE % 256 == 0, "slice must split evenly over the workgroup");
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
+    Raw8<T> rdt;
+    rdt.load(dt + base + r * rsx + c);
+    float av[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) av[j] = sanitize(rdt[j] * Ah, kClipDecay);
+    store8(sCum + r * LC + c, av);
+  }
+  __syncthreads();
+  column_cumsum<C, PT, LC>(sCum, sTot);
+  __syncthreads();
+  float* o = out + (((size_t)bb * dm.H + h) * dm.NT + n) * C * P + p0;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
+    *reinterpret_cast<float4*>(o + (size_t)r * P + c) = *reinterpret_cast<const float4*>(sCum + r * LC + c);
+    *reinterpret_cast<float4*>(o + (size_t)r * P + c + 4) =
+        *reinterpret_cast<const float4*>(sCum + r * LC + c + 4);
+  }
+}
+
+// Rows [0, C) of one (batch, head, chunk)'s cumdecay slice into sCum.
+template <int C, int PT, int LC>
+__device__ __forceinline__ void load_cum_rows(float* sCum, const float* __restrict__ g, int P) {
+  constexpr int PER_ROW = PT / 4;  // float4 pieces per row
+  for (int e = threadIdx.x; e < C * PER_ROW; e += 256) {
+    const int r = e / PER_ROW, c = (e % PER_ROW) * 4;
+    *reinterpret_cast<float4*>(sCum + r * LC + c) = *reinterpret_cast<const float4*>(g + (size_t)r * P + c);
+  }
+}
+
 // ------------------------------------------------------------------ chunk outer products
 template <typename T, int C, int N, int PT>
 struct OuterLds {
@@ -104,7 +165,10 @@ struct OuterLds {
 //   backward (BWD = true):  S = Ydh = dy decay_h (:123 of mamba2_bwd_reference.py),
 //            R = C, out = (dy decay_h)^T C (:128); also writes Ydh and
 //            W = sanitize(dBx dte) (:135), the operands of dC_1 and dB_1.
-template <typename T, typename TD, int C, int P, int N, int PT, bool BWD, int SL>
+//   stage M3 (STG = true, forward): cum from ck.cum, S = sanitize(dBx
+//            exp(clip(cum_last - cum, +-20))) and out = state_end in
+//            [B][H][NT][P][N] (kernel_mamba2_b_intra.py:110-116).
+template <typename T, typename TD, int C, int P, int N, int PT, bool BWD, int SL, bool STG = false>
 __global__ __launch_bounds__(256) void mamba2_chunk_outer(
     Mamba2Dims dm, const T* __restrict__ dt, const T* __restrict__ x, const float* __restrict__ A,
     const T* __restrict__ R, const TD* __restrict__ dy, Mamba2Chunks<T> ck, T* __restrict__ ydh,
@@ -128,7 +192,7 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
   const int m = m2 * SL + sl;
   const int h = m / NPT, p0 = (m % NPT) * PT;
   const size_t base = (row0 * dm.H + h) * P + p0;  // element (r, c) at base + r * rsx + c
-  const float Ah = A[h];
+  const size_t bhn_ref = ((size_t)bb * dm.H + h) * dm.NT + n;  // [B][H][NT] order (stage mode)
 
   constexpr int PER_ROW = PT / 8, NE = C * PER_ROW, EPT = NE / 256;
   static_assert(NE % 256 == 0, "slice must split evenly over the workgroup");
@@ -141,17 +205,23 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
     rx[i].load(x + base + r * rsx + c);
     if constexpr (BWD) rdy[i].load(dy + base + r * rsx + c);
   }
+  if constexpr (STG) {
+    load_cum_rows<C, PT, L::LC>(sCum, ck.cum + bhn_ref * C * P + p0, P);
+    __syncthreads();
+  } else {
+    const float Ah = A[h];
 #pragma unroll
-  for (int i = 0; i < EPT; ++i) {
-    const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
-    float av[8];
+    for (int i = 0; i < EPT; ++i) {
+      const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
+      float av[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) av[j] = sanitize(rdt[i][j] * Ah, kClipDecay);
-    store8(sCum + r * L::LC + c, av);
+      for (int j = 0; j < 8; ++j) av[j] = sanitize(rdt[i][j] * Ah, kClipDecay);
+      store8(sCum + r * L::LC + c, av);
+    }
+    __syncthreads();
+    column_cumsum<C, PT, L::LC>(sCum, sTot);
+    __syncthreads();
   }
-  __syncthreads();
-  column_cumsum<C, PT, L::LC>(sCum, sTot);
-  __syncthreads();
 
   float sv[EPT][8];
 #pragma unroll
@@ -165,10 +235,13 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
       const float ci = cr[j];
       const float cl = clr[j];
       const float dbx = sanitize(rdt[i][j] * rx[i][j]);
-      const float dte = sanitize(__expf(fminf(fmaxf(cl - ci, -kClipDecay), kClipDecay)), 1e6f);
+      const float ed = __expf(fminf(fmaxf(cl - ci, -kClipDecay), kClipDecay));
+      const float dte = sanitize(ed, 1e6f);
       if constexpr (BWD) {
         sv[i][j] = rdy[i][j] * __expf(fminf(fmaxf(ci, -kClipDecay), 0.f));
         wv[j] = sanitize(dbx * dte);
+      } else if constexpr (STG) {
+        sv[i][j] = sanitize(dbx * ed);
       } else {
         sv[i][j] = dbx * dte;
       }
@@ -179,7 +252,7 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
     }
   }
   const size_t bnh = (size_t)bn * dm.H + h;
-  if (!BWD && threadIdx.x < PT) ck.cl[bnh * P + p0 + threadIdx.x] = sCum[(C - 1) * L::LC + threadIdx.x];
+  if (!BWD && !STG && threadIdx.x < PT) ck.cl[bnh * P + p0 + threadIdx.x] = sCum[(C - 1) * L::LC + threadIdx.x];
   __syncthreads();  // every cum read is done: S overwrites the cum buffer
 #pragma unroll
   for (int i = 0; i < EPT; ++i) {
@@ -190,7 +263,7 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
 
   constexpr int NI = N / 16, TILES = (PT / 16) * NI, TPW = TILES / 4;
   static_assert(TILES % 4 == 0, "tiles must split evenly over 4 waves");
-  float* out = ck.src + (bnh * P + p0) * N;
+  float* out = ck.src + ((STG ? bhn_ref : bnh) * P + p0) * N;
   const int wv_id = wave_id();
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
@@ -214,7 +287,10 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
 //   d_cum_last_a = sum_s dstate state_prev * decay_chunk_end * mask  (:116,120)
 //   dstate = sanitize(dstate decay_chunk_end + (dy decay_h)^T C)      (:115,128,195)
 // Thread map: one float4 of one channel row; RP channel rows per workgroup.
-template <typename T, int P, int N, bool BWD>
+// Stage M4 (STG = true, forward): src = the caller's state_end in
+// [B][H][NT][P][N], cum_last from the caller's cumdecay, and the initial
+// state sanitised (kernel_mamba2_c_interchunk.py:58,68-78).
+template <typename T, int P, int N, bool BWD, bool STG = false>
 __global__ __launch_bounds__(256) void mamba2_state_pass(Mamba2Dims dm, Mamba2Chunks<T> ck,
                                                         T* __restrict__ dstate, float* __restrict__ lasta,
                                                         const float* __restrict__ init,
@@ -226,9 +302,18 @@ __global__ __launch_bounds__(256) void mamba2_state_pass(Mamba2Dims dm, Mamba2Ch
   const int p = rp * RP + r, s0 = 4 * c4;
   const int NT = dm.NT;
   auto rowi = [&](int n) { return (((size_t)bb * NT + n) * dm.H + h) * P + p; };
+  // src and cum_last rows: the workspace's [B][NT][H] order, or the caller's
+  // [B][H][NT] arrays in stage mode
+  auto rows = [&](int n) { return STG ? ((size_t)bh * NT + n) * P + p : rowi(n); };
+  auto cl_at = [&](int n) {
+    return STG ? ck.cum[(((size_t)bh * NT + n) * dm.C + dm.C - 1) * P + p] : ck.cl[rowi(n)];
+  };
 
   float4 st = make_float4(0.f, 0.f, 0.f, 0.f);
   if (init) st = *reinterpret_cast<const float4*>(init + ((size_t)bh * P + p) * N + s0);
+  if constexpr (STG) {
+    st.x = sanitize(st.x); st.y = sanitize(st.y); st.z = sanitize(st.z); st.w = sanitize(st.w);
+  }
 
   constexpr int D = 4;  // chunks in flight
   float4 src[D];
@@ -237,8 +322,8 @@ __global__ __launch_bounds__(256) void mamba2_state_pass(Mamba2Dims dm, Mamba2Ch
   auto load = [&](int k, int it) {
     const int n = BWD ? NT - 1 - it : it;
     const size_t ri = rowi(n);
-    src[k] = *reinterpret_cast<const float4*>(ck.src + ri * N + s0);
-    cl[k] = ck.cl[ri];
+    src[k] = *reinterpret_cast<const float4*>(ck.src + rows(n) * N + s0);
+    cl[k] = cl_at(n);
     if (BWD) sp[k] = *reinterpret_cast<const uint2*>(ck.state_pre + ri * N + s0);
   };
   // Every load is issued on every path (past the last chunk it re-reads that
@@ -342,7 +427,11 @@ __device__ __forceinline__ constexpr int y_block(int w, int b) {
 // with U_i = exp(cum_i - cum_{16I}), M_IJ = exp(cum_{16I} - cum_{16J+15}).
 // SL consecutive (head, channel slice) pairs of one chunk per workgroup (the
 // CB / C fragments are loaded once for them); (dm.H * P / PT) % SL == 0.
-template <typename T, int C, int P, int N, int PT, int SL>
+// YM: 0 the whole path's y; 1 stage M3's y_diag alone, cum from ck.cum and
+// no 1e6 cap on the pair weight (kernel_mamba2_b_intra.py:96-108); 2 stage
+// M4's combine, y = sanitize(y_diag + y_off) with y_diag from ck.ydiag and
+// cum from ck.cum (kernel_mamba2_c_interchunk.py:68-78).
+template <typename T, int C, int P, int N, int PT, int SL, int YM = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void mamba2_chunk_y(Mamba2Dims dm, const T* __restrict__ dt,
                                                      const T* __restrict__ x, const float* __restrict__ A,
                                                      const T* __restrict__ Cm, Mamba2Chunks<T> ck,
@@ -376,17 +465,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   frag fa[BPW][NB], fd[BPW], fc[BPW][KN];
   static_for<BPW>([&](auto Bc) {
     constexpr int bi = decltype(Bc)::value, I = y_block<NB>(W, bi);
+    if constexpr (YM != 2) {
 #pragma unroll
-    for (int J = 0; J < I; ++J) fa[bi][J] = cb_frag<T>(cbg, C, 16 * I, 16 * J, 0);
-    fd[bi] = cb_frag<T>(cbg, C, 16 * I, 16 * I, 1);
+      for (int J = 0; J < I; ++J) fa[bi][J] = cb_frag<T>(cbg, C, 16 * I, 16 * J, 0);
+      fd[bi] = cb_frag<T>(cbg, C, 16 * I, 16 * I, 1);
+    }
+    if constexpr (YM != 1) {
 #pragma unroll
-    for (int kk = 0; kk < KN; ++kk) fc[bi][kk] = Mma<T>::ld_c(cg, N, 16 * I, kk * Mma<T>::KS);
+      for (int kk = 0; kk < KN; ++kk) fc[bi][kk] = Mma<T>::ld_c(cg, N, 16 * I, kk * Mma<T>::KS);
+    }
   });
   for (int sl = 0; sl < SL; ++sl) {
   const int m = m2 * SL + sl;
   const int h = m / NPT, p0 = (m % NPT) * PT;
   const size_t base = (row0 * dm.H + h) * P + p0;
-  const float Ah = A[h];
+  const float Ah = YM == 0 ? A[h] : 0.f;
   // thread item = 8 channels of one row; 16 consecutive items take 16
   // consecutive rows (conflict-free 16-byte LDS accesses)
   constexpr int PER_ROW = PT / 8, NE = C * PER_ROW, EPT = NE / 256;
@@ -394,42 +487,60 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   auto item_row = [](int e) { return (e % 16) + 16 * (e / (16 * PER_ROW)); };
   auto item_col = [](int e) { return ((e / 16) % PER_ROW) * 8; };
   Raw8<T> rdt[EPT], rx[EPT];
+  if constexpr (YM != 2) {
 #pragma unroll
-  for (int i = 0; i < EPT; ++i) {
-    const int e = threadIdx.x + 256 * i, r = item_row(e), c = item_col(e);
-    rdt[i].load(dt + base + r * rsx + c);
-    rx[i].load(x + base + r * rsx + c);
-  }
-  stage_rows<T, PT, N>(sSt, L::LN, ck.state_pre + (((size_t)bn * dm.H + h) * P + p0) * N, N);
-  int flag = 0;
-#pragma unroll
-  for (int i = 0; i < EPT; ++i) {
-    const int e = threadIdx.x + 256 * i, r = item_row(e), c = item_col(e);
-    float av[8], dbx[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float a = rdt[i][j] * Ah;
-      flag |= a > 0.f;
-      av[j] = sanitize(a, kClipDecay);
-      dbx[j] = sanitize(rdt[i][j] * rx[i][j]);
+    for (int i = 0; i < EPT; ++i) {
+      const int e = threadIdx.x + 256 * i, r = item_row(e), c = item_col(e);
+      rdt[i].load(dt + base + r * rsx + c);
+      rx[i].load(x + base + r * rsx + c);
     }
-    store8(sCum + r * L::LC + c, av);
-    store8(sDbx + r * L::LC + c, dbx);
   }
-  // the 16 zero rows below the chunk (read by the K = 32 steps of the last block)
-  if (threadIdx.x < 16 * PER_ROW) {
-    const int r = C + threadIdx.x / PER_ROW, c = (threadIdx.x % PER_ROW) * 8;
-    *reinterpret_cast<uint4*>(sV + r * L::LPT + c) = make_uint4(0u, 0u, 0u, 0u);
+  if constexpr (YM != 1)
+    stage_rows<T, PT, N>(sSt, L::LN, ck.state_pre + (((size_t)bn * dm.H + h) * P + p0) * N, N);
+  if constexpr (YM != 0)
+    load_cum_rows<C, PT, L::LC>(sCum, ck.cum + (((size_t)bb * dm.H + h) * dm.NT + n) * C * P + p0, P);
+  int flag = 0;
+  if constexpr (YM != 2) {
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int e = threadIdx.x + 256 * i, r = item_row(e), c = item_col(e);
+      float av[8], dbx[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float a = rdt[i][j] * Ah;
+        flag |= YM == 0 && a > 0.f;
+        av[j] = sanitize(a, kClipDecay);
+        dbx[j] = sanitize(rdt[i][j] * rx[i][j]);
+      }
+      if constexpr (YM == 0) store8(sCum + r * L::LC + c, av);
+      store8(sDbx + r * L::LC + c, dbx);
+    }
+    // the 16 zero rows below the chunk (read by the K = 32 steps of the last block)
+    if (threadIdx.x < 16 * PER_ROW) {
+      const int r = C + threadIdx.x / PER_ROW, c = (threadIdx.x % PER_ROW) * 8;
+      *reinterpret_cast<uint4*>(sV + r * L::LPT + c) = make_uint4(0u, 0u, 0u, 0u);
+    }
   }
   __syncthreads();
-  column_cumsum<C, PT, L::LC>(sCum, sTot);
-  __syncthreads();
+  if constexpr (YM == 0) {
+    column_cumsum<C, PT, L::LC>(sCum, sTot);
+    __syncthreads();
+  }
+  bool exact = false;
+  if constexpr (YM != 2) {
   for (int e = threadIdx.x; e < NB * PT; e += 256) {
     const int I = e / PT, p = e % PT;
     flag |= sCum[16 * I * L::LC + p] - sCum[(16 * I + 15) * L::LC + p] > kMaxRange;
   }
+  if constexpr (YM == 1) {
+    // the caller's cum: a rise between consecutive rows is a positive step
+    for (int e = threadIdx.x; e < (C - 1) * PT; e += 256) {
+      const int r = 1 + e / PT, p = e % PT;
+      flag |= sCum[r * L::LC + p] > sCum[(r - 1) * L::LC + p];
+    }
+  }
   // a positive step exponent (or too steep a block) is evaluated pairwise
-  const bool exact = __builtin_amdgcn_readfirstlane(__syncthreads_or(flag)) != 0;
+  exact = __builtin_amdgcn_readfirstlane(__syncthreads_or(flag)) != 0;
   if (!exact) {
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
@@ -442,6 +553,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       store8(sV + r * L::LPT + c, v);
     }
   }
+  }  // YM != 2
   __syncthreads();
 
   // this lane's y elements: a uniform base and 32-bit lane offsets
@@ -452,7 +564,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     f32x4 off[YNI], yo[YNI];
 #pragma unroll
     for (int ni = 0; ni < YNI; ++ni) { off[ni] = zero4(); yo[ni] = zero4(); }
-    if (!exact) {
+    if (YM != 2 && !exact) {
       // off = sum_{J < I} M_IJ (CB_IJ Vd_J) + M_II (tril(CB_II) Vd_I): with the row
       // scale U_i below, the diagonal term becomes exp(cum_i - cum_{16I+15}) (.)
       static_for<I + 1>([&](auto Jc) {
@@ -470,11 +582,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       });
     }
+    if constexpr (YM != 1) {
 #pragma unroll
-    for (int kk = 0; kk < KN; ++kk) {
+      for (int kk = 0; kk < KN; ++kk) {
 #pragma unroll
-      for (int ni = 0; ni < YNI; ++ni)
-        yo[ni] = Mma<T>::mma(fc[bi][kk], Mma<T>::ld_c(sSt, L::LN, 16 * ni, kk * Mma<T>::KS), yo[ni]);
+        for (int ni = 0; ni < YNI; ++ni)
+          yo[ni] = Mma<T>::mma(fc[bi][kk], Mma<T>::ld_c(sSt, L::LN, 16 * ni, kk * Mma<T>::KS), yo[ni]);
+      }
     }
 #pragma unroll
     for (int ni = 0; ni < YNI; ++ni) {
@@ -482,18 +596,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int k = 0; k < 4; ++k) {
         const int i = 16 * I + tile_row(k), p = 16 * ni + tile_col();
         const float ci = sCum[i * L::LC + p];
-        float ydiag;
-        if (!exact) {
-          ydiag = off[ni][k] * __expf(ci - sCum[16 * I * L::LC + p]);
-        } else {
-          ydiag = 0.f;
-          for (int j = 0; j <= i; ++j) {
-            const float dd = fminf(fmaxf(ci - sCum[j * L::LC + p], -kClipDecay), kClipDecay);
-            ydiag += fminf(__expf(dd), 1e6f) * to_f(cbg[(size_t)i * C + j]) * sDbx[j * L::LC + p];
+        const unsigned yi = ylane + (unsigned)(16 * I + k) * (unsigned)rsx + 16 * ni;
+        float ydiag = 0.f;
+        if constexpr (YM != 2) {
+          if (!exact) {
+            ydiag = off[ni][k] * __expf(ci - sCum[16 * I * L::LC + p]);
+          } else {
+            for (int j = 0; j <= i; ++j) {
+              const float dd = fminf(fmaxf(ci - sCum[j * L::LC + p], -kClipDecay), kClipDecay);
+              const float wgt = YM == 1 ? __expf(dd) : fminf(__expf(dd), 1e6f);
+              ydiag += wgt * to_f(cbg[(size_t)i * C + j]) * sDbx[j * L::LC + p];
+            }
           }
         }
-        const float yoff = sanitize(yo[ni][k] * __expf(fminf(fmaxf(ci, -kClipDecay), 0.f)));
-        yb[ylane + (unsigned)(16 * I + k) * (unsigned)rsx + 16 * ni] = sanitize(sanitize(ydiag) + yoff);
+        const float yoff = YM == 1 ? 0.f : sanitize(yo[ni][k] * __expf(fminf(fmaxf(ci, -kClipDecay), 0.f)));
+        float yv;
+        if constexpr (YM == 0) yv = sanitize(sanitize(ydiag) + yoff);
+        else if constexpr (YM == 1) yv = sanitize(ydiag);
+        else yv = sanitize(ck.ydiag[base + yi] + yoff);
+        yb[yi] = yv;
       }
     }
   });

@@ -70,6 +70,8 @@ static Mamba2Chunks<T> mamba2_chunks(const Mamba2Plan& p, void* ws) {
   c.state_pre = reinterpret_cast<T*>(base + p.o_state);
   c.cl = reinterpret_cast<float*>(base + p.o_cl);
   c.src = reinterpret_cast<float*>(base + p.o_src);
+  c.cum = nullptr;
+  c.ydiag = nullptr;
   return c;
 }
 
@@ -273,6 +275,128 @@ static int mamba2_backward_diag(const Mamba2Plan& p, StageDiag& D, const void* d
   return D.reduce(ATOMIC_MAMBA2_DIAG_DSTATE0, dstate0, B * H * P * N);
 }
 
+// ------------------------------------------------ stage-level forward
+// The reference's M2, M3 and M4 (kernel_mamba2_a_decay.py:71,
+// kernel_mamba2_b_intra.py:119, kernel_mamba2_c_interchunk.py:38) over
+// caller-owned arrays in its layout: cumdecay [B][H][NT][C][P] fp32,
+// state_end [B][H][NT][P][N] fp32, y_diag and y [B][T][H][P] fp32.  The
+// arrays are per chunk, so chunk 256 (which the whole path runs as 128-row
+// chunks) is not taken.
+static int mamba2_stage_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
+  const int rc = mamba2_plan(a, p);
+  if (rc != ATOMIC_OK) return rc;
+  return a->chunk == p->dm.C ? ATOMIC_OK : ATOMIC_ERR_SHAPE;
+}
+
+// M3 keeps CB ([B][NT][C][C] bf16) and M4 the states entering each chunk
+// ([B][NT][H][P][N] bf16) in the caller's workspace.
+static size_t mamba2_stage_ws(const Mamba2Plan& p) {
+  const Mamba2Dims& d = p.dm;
+  const size_t cb = (size_t)d.B * d.NT * d.C * d.C * 2;
+  const size_t st = (size_t)d.B * d.NT * d.H * d.P * d.N * 2;
+  return m2_align(cb > st ? cb : st);
+}
+
+template <int C, int P, int N>
+static int mamba2_cumdecay_impl(const Mamba2Plan& p, const void* dt, const float* A, float* cum, Launch& L) {
+  const Mamba2Dims& d = p.dm;
+  hipStream_t st = L.st;
+  return L("mamba2_cumdecay", [&] {
+    hipLaunchKernelGGL((mamba2_cumdecay<bf16, C, P, kOuterPT>), dim3((unsigned)(d.B * d.NT * d.H * (P / kOuterPT))),
+                       dim3(256), 0, st, d, (const bf16*)dt, A, cum);
+  });
+}
+
+template <int C, int P, int N>
+static int mamba2_intra_stage_impl(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm,
+                                   const void* Cm, const float* cum, float* y_diag, float* state_end, void* ws,
+                                   Launch& L) {
+  typedef bf16 T;
+  const Mamba2Dims& d = p.dm;
+  Mamba2Chunks<T> ck{};
+  ck.cb = static_cast<T*>(ws);
+  ck.src = state_end;
+  ck.cum = cum;
+  hipStream_t st = L.st;
+  int rc = L("mamba2_cb", [&] {
+    hipLaunchKernelGGL((mamba2_cb<T, C, N>), dim3((unsigned)(d.B * d.NT)), dim3(256), 0, st, d,
+                       (const T*)Bm, (const T*)Cm, ck);
+  });
+  if (rc) return rc;
+  rc = L("mamba2_chunk_state", [&] {
+    constexpr int NPO = P / kOuterPT;
+    const size_t pairs = (size_t)d.H * NPO;
+    if (pairs % 8 == 0)
+      hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, 8, true>),
+                         dim3((unsigned)(d.B * d.NT * pairs / 8)), dim3(256), 0, st, d, (const T*)dt,
+                         (const T*)x, (const float*)nullptr, (const T*)Bm, (const T*)nullptr, ck, (T*)nullptr,
+                         (T*)nullptr);
+    else
+      hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, NPO, true>),
+                         dim3((unsigned)(d.B * d.NT * d.H)), dim3(256), 0, st, d, (const T*)dt, (const T*)x,
+                         (const float*)nullptr, (const T*)Bm, (const T*)nullptr, ck, (T*)nullptr, (T*)nullptr);
+  });
+  if (rc) return rc;
+  constexpr int NPT = P / kYPT;
+  const size_t pairs = (size_t)d.H * NPT;
+  return L("mamba2_chunk_y_diag", [&] {
+    if (pairs % 16 == 0)
+      hipLaunchKernelGGL((mamba2_chunk_y<T, C, P, N, kYPT, 16, 1>), dim3((unsigned)(d.B * d.NT * pairs / 16)),
+                         dim3(256), 0, st, d, (const T*)dt, (const T*)x, (const float*)nullptr, (const T*)Cm,
+                         ck, y_diag);
+    else
+      hipLaunchKernelGGL((mamba2_chunk_y<T, C, P, N, kYPT, NPT, 1>), dim3((unsigned)(d.B * d.NT * d.H)),
+                         dim3(256), 0, st, d, (const T*)dt, (const T*)x, (const float*)nullptr, (const T*)Cm,
+                         ck, y_diag);
+  });
+}
+
+template <int C, int P, int N>
+static int mamba2_combine_stage_impl(const Mamba2Plan& p, const float* y_diag, const float* state_end,
+                                     const float* cum, const void* Cm, const float* state0, float* y,
+                                     float* state_final, void* ws, Launch& L) {
+  typedef bf16 T;
+  const Mamba2Dims& d = p.dm;
+  Mamba2Chunks<T> ck{};
+  ck.state_pre = static_cast<T*>(ws);
+  ck.src = const_cast<float*>(state_end);
+  ck.cum = cum;
+  ck.ydiag = y_diag;
+  hipStream_t st = L.st;
+  int rc = L("mamba2_state_pass", [&] {
+    hipLaunchKernelGGL((mamba2_state_pass<T, P, N, false, true>), dim3(pass_grid<P, N>(d)), dim3(256), 0, st,
+                       d, ck, (T*)nullptr, (float*)nullptr, state0, state_final);
+  });
+  if (rc) return rc;
+  constexpr int NPT = P / kYPT;
+  const size_t pairs = (size_t)d.H * NPT;
+  return L("mamba2_chunk_y_combine", [&] {
+    if (pairs % 16 == 0)
+      hipLaunchKernelGGL((mamba2_chunk_y<T, C, P, N, kYPT, 16, 2>), dim3((unsigned)(d.B * d.NT * pairs / 16)),
+                         dim3(256), 0, st, d, (const T*)nullptr, (const T*)nullptr, (const float*)nullptr,
+                         (const T*)Cm, ck, y);
+    else
+      hipLaunchKernelGGL((mamba2_chunk_y<T, C, P, N, kYPT, NPT, 2>), dim3((unsigned)(d.B * d.NT * d.H)),
+                         dim3(256), 0, st, d, (const T*)nullptr, (const T*)nullptr, (const float*)nullptr,
+                         (const T*)Cm, ck, y);
+  });
+}
+
+static int mamba2_cumdecay_stage(const Mamba2Plan& p, const void* dt, const float* A, float* cum, Launch& L) {
+  AH_M2_DISPATCH(mamba2_cumdecay_impl, p, dt, A, cum, L);
+}
+
+static int mamba2_intra_stage(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm, const void* Cm,
+                              const float* cum, float* y_diag, float* state_end, void* ws, Launch& L) {
+  AH_M2_DISPATCH(mamba2_intra_stage_impl, p, dt, x, Bm, Cm, cum, y_diag, state_end, ws, L);
+}
+
+static int mamba2_combine_stage(const Mamba2Plan& p, const float* y_diag, const float* state_end, const float* cum,
+                                const void* Cm, const float* state0, float* y, float* state_final, void* ws,
+                                Launch& L) {
+  AH_M2_DISPATCH(mamba2_combine_stage_impl, p, y_diag, state_end, cum, Cm, state0, y, state_final, ws, L);
+}
+
 }  // namespace ah
 
 using namespace ah;
@@ -335,4 +459,48 @@ extern "C" int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, co
   if (r2 || !a->diag) return r2;
   StageDiag D{a->diag, L};
   return mamba2_backward_diag(p, D, ddt, dx, dB, dC, dA, dstate0, workspace);
+}
+
+extern "C" size_t atomic_mamba2_stage_workspace_size(const atomic_mamba2_args* a) {
+  Mamba2Plan p;
+  if (mamba2_stage_plan(a, &p) != ATOMIC_OK) return 0;
+  return mamba2_stage_ws(p);
+}
+
+extern "C" int atomic_mamba2_chunk_cumdecay(const atomic_mamba2_args* a, const void* dt, const float* A,
+                                            float* cumdecay, void* stream) {
+  Mamba2Plan p;
+  const int rc = mamba2_stage_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!dt || !A || !cumdecay) return ATOMIC_ERR_NULL;
+  Launch L{a->profile, (hipStream_t)stream};
+  return mamba2_cumdecay_stage(p, dt, A, cumdecay, L);
+}
+
+extern "C" int atomic_mamba2_intra_chunk_ssd(const atomic_mamba2_args* a, const void* dt, const void* x,
+                                             const void* B, const void* C, const float* cumdecay, float* y_diag,
+                                             float* state_end, void* workspace, size_t workspace_bytes,
+                                             void* stream) {
+  Mamba2Plan p;
+  const int rc = mamba2_stage_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!dt || !x || !B || !C || !cumdecay || !y_diag || !state_end) return ATOMIC_ERR_NULL;
+  if (!workspace || workspace_bytes < mamba2_stage_ws(p)) return ATOMIC_ERR_WORKSPACE;
+  ws_tag_clobber(workspace, workspace_bytes);
+  Launch L{a->profile, (hipStream_t)stream};
+  return mamba2_intra_stage(p, dt, x, B, C, cumdecay, y_diag, state_end, workspace, L);
+}
+
+extern "C" int atomic_mamba2_inter_chunk_combine(const atomic_mamba2_args* a, const float* y_diag,
+                                                 const float* state_end, const float* cumdecay, const void* C,
+                                                 const float* state0, float* y, float* state_final,
+                                                 void* workspace, size_t workspace_bytes, void* stream) {
+  Mamba2Plan p;
+  const int rc = mamba2_stage_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!y_diag || !state_end || !cumdecay || !C || !y || !state_final) return ATOMIC_ERR_NULL;
+  if (!workspace || workspace_bytes < mamba2_stage_ws(p)) return ATOMIC_ERR_WORKSPACE;
+  ws_tag_clobber(workspace, workspace_bytes);
+  Launch L{a->profile, (hipStream_t)stream};
+  return mamba2_combine_stage(p, y_diag, state_end, cumdecay, C, state0, y, state_final, workspace, L);
 }

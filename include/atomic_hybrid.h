@@ -331,6 +331,42 @@ int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, const void* x
                       const float* dstate_final, void* ddt, void* dx, void* dB, void* dC, float* dA,
                       float* dstate0, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Mamba2 stage-level forward: the reference's staged pipeline M2 -> M3 -> M4
+ * (mamba2_pallas_forward, kernel_mamba2_c_interchunk.py:90-100) over
+ * caller-owned arrays in its layout.  args.chunk is 64 or 128 (the arrays
+ * are per chunk; 256 is refused).  dt, x, B, C bf16; the arrays fp32:
+ *   cumdecay : [B][H][NT][C][P]     state_end : [B][H][NT][P][N]
+ *   y_diag, y : [B][T][H][P]        state0, state_final : [B][H][P][N]
+ * The arithmetic is that of the stage kernels, which differ from the whole
+ * path only where a step exponent dt A is positive: no 1e6 caps on the pair
+ * weight and the decay to the chunk end (kernel_mamba2_b_intra.py:96-112).
+ */
+
+/* bytes of workspace atomic_mamba2_intra_chunk_ssd and
+   atomic_mamba2_inter_chunk_combine need (0 for unsupported args) */
+size_t atomic_mamba2_stage_workspace_size(const atomic_mamba2_args* a);
+
+/* M2: build_chunk_cumdecay_pallas(dt, A, chunk_size)
+ * (kernel_mamba2_a_decay.py:71-105): sanitize(cumsum(sanitize(dt A, 20)), 1e4). */
+int atomic_mamba2_chunk_cumdecay(const atomic_mamba2_args* a, const void* dt, const float* A, float* cumdecay,
+                                 void* stream);
+
+/* M3: intra_chunk_ssd_pallas(dt, x, B, C, cumdecay, chunk_size)
+ * (kernel_mamba2_b_intra.py:119-163): y_diag and each chunk's state_end
+ * from the given cumdecay. */
+int atomic_mamba2_intra_chunk_ssd(const atomic_mamba2_args* a, const void* dt, const void* x, const void* B,
+                                  const void* C, const float* cumdecay, float* y_diag, float* state_end,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* M4: mamba2_inter_chunk_combine(y_diag, state_end, cumdecay, C, chunk_size,
+ * state0) (kernel_mamba2_c_interchunk.py:38-87): the sequential state pass
+ * (state0 sanitised, NULL = zeros) and y = sanitize(y_diag + y_off). */
+int atomic_mamba2_inter_chunk_combine(const atomic_mamba2_args* a, const float* y_diag, const float* state_end,
+                                      const float* cumdecay, const void* C, const float* state0, float* y,
+                                      float* state_final, void* workspace, size_t workspace_bytes,
+                                      void* stream);
+
 /* ------------------------------------------- output epilogue (downstream) */
 
 /* The two mixer blocks' output epilogue: RMSNorm over the model dimension

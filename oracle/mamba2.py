@@ -115,6 +115,125 @@ def mamba2_token_serial(dt, A, Bm, Cm, x, state0=None, dtype=torch.float64):
     return torch.stack(ys, 1), s
 
 
+# ---------------------------------------------------------------- stages
+# The staged forward the reference's trainable wrapper runs
+# (mamba2_pallas_forward, kernel_mamba2_c_interchunk.py:90-100): M2 -> M3 ->
+# M4 over per-chunk arrays [b, h, NT, C, p] (cumdecay) and [b, h, NT, p, n]
+# (state_end).  Same mathematics as mamba2_ssd_reference; the stage kernels
+# drop the 1e6 caps on the pair weight and the decay to the chunk end,
+# sanitise the chunk's write, accumulate y_diag per 128-row sub-block
+# (sanitising between them) and sanitise state0.
+
+def _stage_chunks(t, C):
+    """[b, l, h, d] -> [b, h, NT, C, d]."""
+    b, l, h, d = t.shape
+    return t.reshape(b, l // C, C, h, d).permute(0, 3, 1, 2, 4)
+
+
+def _stage_unchunk(t):
+    """[b, h, NT, C, d] -> [b, l, h, d]."""
+    b, h, nt, C, d = t.shape
+    return t.permute(0, 2, 3, 1, 4).reshape(b, nt * C, h, d)
+
+
+def build_chunk_cumdecay(dt, A, chunk_size, dtype=torch.float64):
+    """M2 (kernel_mamba2_a_decay.py:53-66): per chunk,
+    sanitize(tril @ sanitize(dt A, 20), 1e4) -> [b, h, NT, C, p]."""
+    f = dtype
+    dA = sanitize(dt.to(f) * A.to(f)[None, None, :, None], CLIP_STEP)              # :59-60
+    cum = torch.cumsum(_stage_chunks(dA, chunk_size), dim=3)                     # :62-64 (tril @ dA)
+    return sanitize(cum, CLIP_ACC)                                              # :66
+
+
+def intra_chunk_ssd(dt, x, Bm, Cm, cumdecay, chunk_size, dtype=torch.float64):
+    """M3 (kernel_mamba2_b_intra.py:69-116): (y_diag [b, l, h, p],
+    state_end [b, h, NT, p, n])."""
+    f = dtype
+    C = chunk_size
+    bc = min(128, C)                                                            # :61-62,71
+    dtc, xc = (_stage_chunks(t.to(f), C) for t in (dt, x))                      # [b, h, nt, C, p]
+    b, h, nt = dtc.shape[:3]
+    Bc = Bm.to(f).reshape(b, nt, C, -1)[:, None]                                # broadcast over heads (:137-142)
+    Cc = Cm.to(f).reshape(b, nt, C, -1)[:, None]
+    cum = cumdecay.to(f)
+    dBx = sanitize(dtc * xc)                                                    # :81
+    BC_inner = sanitize(Cc @ Bc.transpose(-1, -2))                              # :83-84
+    y_diag = torch.zeros_like(dtc)                                              # :86
+    idx = torch.arange(bc)
+    causal = (idx[:, None] >= idx[None, :]).to(f)
+    for si in range(C // bc):                                                   # :88-108
+        for sj in range(si + 1):
+            i0, j0 = si * bc, sj * bc
+            dd = cum[..., i0:i0 + bc, None, :] - cum[..., None, j0:j0 + bc, :]
+            w = torch.exp(torch.clamp(dd, -CLIP_STEP, CLIP_STEP)) * BC_inner[..., i0:i0 + bc, j0:j0 + bc, None]
+            if si == sj:
+                w = w * causal[:, :, None]
+            y_blk = torch.einsum("...ijd,...jd->...id", w, dBx[..., j0:j0 + bc, :])
+            y_diag[..., i0:i0 + bc, :] = sanitize(y_diag[..., i0:i0 + bc, :] + y_blk)
+    dte = torch.exp(torch.clamp(cum[..., -1:, :] - cum, -CLIP_STEP, CLIP_STEP))  # :111-112
+    write = sanitize(dBx * dte)                                                 # :113
+    state_end = sanitize(torch.einsum("...jd,...js->...ds", write, Bc.expand(-1, h, -1, -1, -1)))  # :115-116
+    return _stage_unchunk(y_diag), state_end
+
+
+def mamba2_inter_chunk_combine(y_diag, state_end, cumdecay, Cm, chunk_size, state0=None, dtype=torch.float64):
+    """M4 (kernel_mamba2_c_interchunk.py:38-87): (y [b, l, h, p],
+    state_final [b, h, p, n])."""
+    f = dtype
+    C = chunk_size
+    b, l, h, p = y_diag.shape
+    n = Cm.shape[-1]
+    nt = l // C
+    ydc = _stage_chunks(y_diag.to(f), C)
+    Cc = Cm.to(f).reshape(b, nt, C, n)
+    state = torch.zeros(b, h, p, n, dtype=f) if state0 is None else state0.to(f)
+    state = sanitize(state)                                                     # :58
+    ys = []
+    for c in range(nt):                                                         # :68-80
+        cum = cumdecay[:, :, c].to(f)                                           # [b, h, C, p]
+        dfs = torch.exp(torch.clamp(cum, -CLIP_STEP, 0.0))
+        y_off = sanitize(torch.einsum("bis,bhds->bhid", Cc[:, c], state) * dfs)
+        dce = torch.exp(torch.clamp(cum[:, :, -1, :], -CLIP_STEP, 0.0))
+        state = sanitize(state * dce[..., None] + state_end[:, :, c].to(f))
+        ys.append(sanitize(ydc[:, :, c] + y_off))
+    return _stage_unchunk(torch.stack(ys, 2)), state
+
+
+def intra_chunk_ssd_loops(dt, x, Bm, Cm, cumdecay, chunk_size):
+    """M3 element by element in Python floats (tiny inputs only): the
+    independent restatement the vectorised one is checked against."""
+    import math
+    b, l, h, p = dt.shape
+    n = Bm.shape[-1]
+    C = chunk_size
+    bc = min(128, C)
+    cl = lambda v, c: 0.0 if math.isnan(v) else min(max(v, -c), c)
+    y = torch.zeros(b, l, h, p, dtype=torch.float64)
+    se = torch.zeros(b, h, l // C, p, n, dtype=torch.float64)
+    for bb in range(b):
+        for c in range(l // C):
+            t0 = c * C
+            cb = [[cl(sum(float(Cm[bb, t0 + i, s]) * float(Bm[bb, t0 + j, s]) for s in range(n)), CLIP_ACC)
+                   for j in range(C)] for i in range(C)]
+            for hh in range(h):
+                for d in range(p):
+                    cum = [float(cumdecay[bb, hh, c, i, d]) for i in range(C)]
+                    dbx = [cl(float(dt[bb, t0 + j, hh, d]) * float(x[bb, t0 + j, hh, d]), CLIP_ACC) for j in range(C)]
+                    for i in range(C):
+                        acc = 0.0
+                        for sj in range(i // bc + 1):
+                            blk = 0.0
+                            for j in range(sj * bc, min((sj + 1) * bc, i + 1)):
+                                blk += math.exp(cl(cum[i] - cum[j], CLIP_STEP)) * cb[i][j] * dbx[j]
+                            acc = cl(acc + blk, CLIP_ACC)
+                        y[bb, t0 + i, hh, d] = acc
+                    for s in range(n):
+                        v = sum(cl(dbx[j] * math.exp(cl(cum[-1] - cum[j], CLIP_STEP)), CLIP_ACC) * float(Bm[bb, t0 + j, s])
+                                for j in range(C))
+                        se[bb, hh, c, d, s] = cl(v, CLIP_ACC)
+    return y, se
+
+
 def chunk_ssd_bwd(dt_c, A, B_c, C_c, x_c, state_prev, dy_c, dstate_new, dtype=torch.float64):
     """Hand-derived backward of one chunk: MB0 ``_chunk_ssd_bwd``
     (mamba2_bwd_reference.py:55-197).  Returns

@@ -162,3 +162,65 @@ def test_planted_mistakes_are_caught(monkeypatch):
     bad = om.chunk_ssd_bwd_scan(dt, A, Bm, Cm, x, C, dy, ds, state0=s0)
     assert _rel(bad[0], ad[0]) > 1e-6
     assert _rel(bad[4], ad[1]) > 1e-6
+
+
+# ---------------------------------------------------------------- stages M2 -> M3 -> M4
+@pytest.mark.parametrize("C", [16, 32, 256])
+def test_stages_compose_to_the_chunked_reference(C):
+    """With every step exponent negative and a moderate state0 the stage
+    kernels' clips never bind, so M2 -> M3 -> M4 equals the chunked reference
+    (chunk 256: two 128-row sub-blocks inside M3)."""
+    l = 512 if C == 256 else 64
+    dt, A, Bm, Cm, x = _inputs(2, l, 3, 5, 7, seed=41)
+    s0 = 0.3 * torch.randn(2, 3, 5, 7, generator=torch.Generator().manual_seed(42), dtype=F64)
+    cum = om.build_chunk_cumdecay(dt, A, C)
+    y_diag, state_end = om.intra_chunk_ssd(dt, x, Bm, Cm, cum, C)
+    y, sf = om.mamba2_inter_chunk_combine(y_diag, state_end, cum, Cm, C, state0=s0)
+    y_r, s_r, parts = om.mamba2_ssd_reference(dt, A, Bm, Cm, x, C, state0=s0, return_parts=True)
+    assert _rel(y, y_r) < 1e-12 and _rel(sf, s_r) < 1e-12
+    # the per-chunk stage arrays are the reference's own intermediates
+    assert _rel(cum[:, :, 1], parts[1]["cumdecay"].permute(0, 2, 1, 3)) < 1e-12
+    assert _rel(state_end[:, :, 1], parts[1]["state_end"]) < 1e-12
+
+
+def test_single_chunk_y_diag_is_the_whole_output():
+    """One chunk from a zero state: y_diag is y and state_end is the final
+    state (the identity the reference's M3 docstring cross-checks)."""
+    dt, A, Bm, Cm, x = _inputs(1, 32, 2, 4, 6, seed=43, a_max=2.0)   # no -20 clip fires
+    cum = om.build_chunk_cumdecay(dt, A, 32)
+    y_diag, state_end = om.intra_chunk_ssd(dt, x, Bm, Cm, cum, 32)
+    y, s = om.mamba2_token_serial(dt, A, Bm, Cm, x)
+    assert _rel(y_diag, y) < 1e-12 and _rel(state_end[:, :, 0], s) < 1e-12
+
+
+@pytest.mark.parametrize("C", [8, 16])
+def test_stage_m3_matches_element_loops_with_positive_exponents(C):
+    """A positive step exponent (A > 0 for one head) drives the pair weights
+    to exp(20) and the chunk's write past 1e4, where the stage kernel's clips
+    (no 1e6 cap, a sanitised write) decide the result: the vectorised M3
+    against the element-by-element restatement, and unlike the whole-path
+    oracle's capped y_diag."""
+    dt, A, Bm, Cm, x = _inputs(1, 2 * C, 2, 3, 4, seed=44)
+    A[0] = 6.0
+    dt = dt * 8.0
+    cum = om.build_chunk_cumdecay(dt, A, C)
+    y_diag, state_end = om.intra_chunk_ssd(dt, x, Bm, Cm, cum, C)
+    y_l, se_l = om.intra_chunk_ssd_loops(dt, x, Bm, Cm, cum, C)
+    assert _rel(y_diag, y_l) < 1e-12 and _rel(state_end, se_l) < 1e-12
+    _, _, parts = om.mamba2_ssd_reference(dt, A, Bm, Cm, x, C, return_parts=True)
+    whole = torch.cat([q["y_diag"] for q in parts], 1)
+    assert (y_diag - whole).abs().max().item() > 1.0
+
+
+def test_stage_m4_sanitises_state0():
+    """M4 clips state0 to +-1e4 and zeroes its NaNs (kernel_mamba2_c_interchunk.py:58)."""
+    dt, A, Bm, Cm, x = _inputs(1, 32, 1, 2, 3, seed=45)
+    cum = om.build_chunk_cumdecay(dt, A, 16)
+    y_diag, state_end = om.intra_chunk_ssd(dt, x, Bm, Cm, cum, 16)
+    s0 = torch.zeros(1, 1, 2, 3, dtype=F64)
+    s0[0, 0, 0, 0], s0[0, 0, 1, 2] = float("nan"), 5e4
+    y, sf = om.mamba2_inter_chunk_combine(y_diag, state_end, cum, Cm, 16, state0=s0)
+    clean = s0.clone()
+    clean[0, 0, 0, 0], clean[0, 0, 1, 2] = 0.0, 1e4
+    y2, sf2 = om.mamba2_inter_chunk_combine(y_diag, state_end, cum, Cm, 16, state0=clean)
+    assert torch.equal(y, y2) and torch.equal(sf, sf2) and torch.isfinite(y).all()
