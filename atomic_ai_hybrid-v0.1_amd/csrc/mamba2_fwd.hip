@@ -475,26 +475,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int kk = 0; kk < KN; ++kk) fc[bi][kk] = Mma<T>::ld_c(cg, N, 16 * I, kk * Mma<T>::KS);
     }
   });
-  for (int sl = 0; sl < SL; ++sl) {
-  const int m = m2 * SL + sl;
-  const int h = m / NPT, p0 = (m % NPT) * PT;
-  const size_t base = (row0 * dm.H + h) * P + p0;
-  const float Ah = YM == 0 ? A[h] : 0.f;
   // thread item = 8 channels of one row; 16 consecutive items take 16
   // consecutive rows (conflict-free 16-byte LDS accesses)
   constexpr int PER_ROW = PT / 8, NE = C * PER_ROW, EPT = NE / 256;
   static_assert(NE % 256 == 0, "slice must split evenly over the workgroup");
   auto item_row = [](int e) { return (e % 16) + 16 * (e / (16 * PER_ROW)); };
   auto item_col = [](int e) { return ((e / 16) % PER_ROW) * 8; };
+  auto slice_base = [&](int sl) {
+    const int m = m2 * SL + sl;
+    return (row0 * dm.H + m / NPT) * P + (m % NPT) * PT;
+  };
+  // dt, x of a slice: the next slice's are requested once the current one's
+  // registers are free, so their latency overlaps its MFMA phase
   Raw8<T> rdt[EPT], rx[EPT];
-  if constexpr (YM != 2) {
+  auto load_dtx = [&](int sl) {
+    const size_t b = slice_base(sl);
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
       const int e = threadIdx.x + 256 * i, r = item_row(e), c = item_col(e);
-      rdt[i].load(dt + base + r * rsx + c);
-      rx[i].load(x + base + r * rsx + c);
+      rdt[i].load(dt + b + r * rsx + c);
+      rx[i].load(x + b + r * rsx + c);
     }
-  }
+  };
+  if constexpr (YM != 2) load_dtx(0);
+  for (int sl = 0; sl < SL; ++sl) {
+  const int m = m2 * SL + sl;
+  const int h = m / NPT, p0 = (m % NPT) * PT;
+  const size_t base = slice_base(sl);
+  const float Ah = YM == 0 ? A[h] : 0.f;
   if constexpr (YM != 1)
     stage_rows<T, PT, N>(sSt, L::LN, ck.state_pre + (((size_t)bn * dm.H + h) * P + p0) * N, N);
   if constexpr (YM != 0)
@@ -553,6 +561,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       store8(sV + r * L::LPT + c, v);
     }
   }
+  if (sl + 1 < SL) load_dtx(sl + 1);
   }  // YM != 2
   __syncthreads();
 
