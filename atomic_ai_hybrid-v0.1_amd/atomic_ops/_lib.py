@@ -32,7 +32,8 @@ class Gdn2Args(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int32), ("seqlen", ctypes.c_int32), ("heads", ctypes.c_int32),
                 ("dk", ctypes.c_int32), ("dv", ctypes.c_int32), ("chunk", ctypes.c_int32),
                 ("dtype", ctypes.c_int32), ("do_dtype", ctypes.c_int32), ("scale", ctypes.c_float),
-                ("flags", ctypes.c_int32), ("profile", ctypes.c_void_p), ("diag", ctypes.c_void_p)]
+                ("flags", ctypes.c_int32), ("profile", ctypes.c_void_p), ("diag", ctypes.c_void_p),
+                ("row_stride", ctypes.c_int64 * 7)]
 
 
 class Gdn2Layout(ctypes.Structure):

@@ -27,6 +27,32 @@ def _stream(device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+def rows(t):
+    """``(tensor, row_stride)`` for a [B, T, H, D] input as the library reads
+    it: a view whose tokens are evenly spaced rows (a slice of a wider
+    [B, T, F] tensor: strides (T s, s, D, 1), s a multiple of 8, 16-byte
+    aligned) is passed as it is with its row stride s; a dense tensor with
+    stride 0; anything else as a dense copy."""
+    if t.is_contiguous():
+        return t, 0
+    B, T, H, D = t.shape
+    sb, st, sh, sd = t.stride()
+    if sd == 1 and (H == 1 or sh == D) and (B == 1 or sb == T * st) and st >= H * D and st % 8 == 0 \
+            and t.data_ptr() % 16 == 0:
+        return t, st
+    return t.contiguous(), 0
+
+
+def _rows_of(args, tensors, first=0):
+    """rows() of each tensor, their strides into args.row_stride[first:]."""
+    out = []
+    for i, t in enumerate(tensors):
+        t2, s = rows(t)
+        args.row_stride[first + i] = s
+        out.append(t2)
+    return out
+
+
 def _check_inputs(q, k, v, w, b, g):
     if not q.is_cuda:
         raise ValueError("GDN2 inputs must be HIP device tensors")
@@ -80,10 +106,10 @@ def forward(q, k, v, w, b, g, scale, h0=None, *, save=False, workspace=None, chu
     forward's per-stage reports."""
     _check_inputs(q, k, v, w, b, g)
     lib = _lib.load()
-    q, k, v, w, b, g = (t.contiguous() for t in (q, k, v, w, b, g))
     B, T, H, K = q.shape
     V = v.shape[-1]
     args = make_args(q, v, scale, flags=_lib.GDN2_SAVE if save else 0, chunk=chunk)
+    q, k, v, w, b, g = _rows_of(args, (q, k, v, w, b, g))
     if timer is not None:
         args.profile = timer.arm()
     if diag is not None:
@@ -108,10 +134,10 @@ def forward_noalloc(q, k, v, w, b, g, scale, h0=None, *, o=None, h_final=None, c
     given (preallocated outputs).  Returns ``(o, h_final)``."""
     _check_inputs(q, k, v, w, b, g)
     lib = _lib.load()
-    q, k, v, w, b, g = (t.contiguous() for t in (q, k, v, w, b, g))
     B, T, H, K = q.shape
     V = v.shape[-1]
     args = make_args(q, v, scale, chunk=chunk)
+    q, k, v, w, b, g = _rows_of(args, (q, k, v, w, b, g))
     if timer is not None:
         args.profile = timer.arm()
     if diag is not None:
@@ -133,19 +159,20 @@ def backward(q, k, v, w, b, g, scale, dO, dh_final=None, h0=None, *, workspace=N
     """Gradients ``(dq, dk, dv, dw, db, dg, dh0)`` in the primals' dtypes
     (dg and dh0 float32).  ``reuse`` declares that ``workspace`` holds the
     intermediates of a ``forward(..., save=True)`` on the same inputs; the
-    library checks that by the input addresses, so an input that has to be
-    copied here (not contiguous, or h0 not float32) turns reuse into a
-    recompute."""
+    library checks that by the input addresses and row strides, so an input
+    that has to be copied here (see ``rows``, or h0 not float32) turns reuse
+    into a recompute."""
     _check_inputs(q, k, v, w, b, g)
     lib = _lib.load()
-    if reuse and not all(t.is_contiguous() for t in (q, k, v, w, b, g)) or \
-            (h0 is not None and (h0.dtype != torch.float32 or not h0.is_contiguous())):
-        reuse = False
-    q, k, v, w, b, g = (t.contiguous() for t in (q, k, v, w, b, g))
-    dO = dO.contiguous()
     if dO.dtype not in _DT:
         dO = dO.to(torch.float32)
-    args = make_args(q, v, scale, do_dtype=dO.dtype, flags=_lib.GDN2_REUSE if reuse else 0, chunk=chunk)
+    args = make_args(q, v, scale, do_dtype=dO.dtype, chunk=chunk)
+    seen = (q, k, v, w, b, g)
+    q, k, v, w, b, g, dO = _rows_of(args, seen + (dO,))
+    if any(x is not y for x, y in zip((q, k, v, w, b, g), seen)) or \
+            (h0 is not None and (h0.dtype != torch.float32 or not h0.is_contiguous())):
+        reuse = False
+    args.flags = _lib.GDN2_REUSE if reuse else 0
     if timer is not None:
         args.profile = timer.arm()
     if diag is not None:
@@ -157,9 +184,10 @@ def backward(q, k, v, w, b, g, scale, dO, dh_final=None, h0=None, *, workspace=N
     if dh_final is not None:
         dh_final = dh_final.to(torch.float32).contiguous()
     B, T, H, K = q.shape
-    dq, dk, db = (torch.empty_like(q) for _ in range(3))
-    dv, dw = torch.empty_like(v), torch.empty_like(w)
-    dg = torch.empty_like(g)
+    # the gradients are dense
+    dq, dk, db = (torch.empty(q.shape, dtype=q.dtype, device=q.device) for _ in range(3))
+    dv, dw = (torch.empty(v.shape, dtype=v.dtype, device=v.device) for _ in range(2))
+    dg = torch.empty(g.shape, dtype=g.dtype, device=g.device)
     dh0 = torch.empty(B, H, K, v.shape[-1], dtype=torch.float32, device=q.device)
     rc = lib.atomic_gdn2_bwd(ctypes.byref(args), _ptr(q), _ptr(k), _ptr(v), _ptr(w), _ptr(b), _ptr(g),
                              _ptr(h0), _ptr(dO), _ptr(dh_final), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dw),

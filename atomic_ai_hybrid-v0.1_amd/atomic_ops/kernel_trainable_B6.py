@@ -42,9 +42,10 @@ class _Gdn2Core(torch.autograd.Function):
     def forward(ctx, q, k, v, w, b, g, scale, h0):
         need = any(ctx.needs_input_grad)
         h0_dtype = h0.dtype
-        # the tensors the library sees, kept for the backward: its reuse of
-        # the forward's workspace is checked against these addresses
-        q, k, v, w, b, g = (t.contiguous() for t in (q, k, v, w, b, g))
+        # the tensors the library sees (row-strided views as they are, other
+        # layouts as dense copies), kept for the backward: its reuse of the
+        # forward's workspace is checked against these addresses and strides
+        q, k, v, w, b, g = (_g.rows(t)[0] for t in (q, k, v, w, b, g))
         h0 = h0.to(torch.float32).contiguous()
         o, h_final, ws = _forward(q, k, v, w, b, g, scale, h0, need)
         if need:

@@ -8,6 +8,9 @@ namespace ah {
 struct Gdn2Dims {
   int B, T, H, K, V, C, NT;
   float scale;
+  // row strides of the [B, T, H, D] inputs in elements (token t of batch b
+  // starts at (b T + t) * stride): q, k, v, w, b, g, dO
+  long long rq, rk, rv, rw, rb, rg, rdo;
 };
 
 // Per-(batch, head, chunk) intermediates, each a contiguous block indexed by

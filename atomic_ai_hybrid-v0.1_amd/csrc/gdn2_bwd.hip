@@ -75,7 +75,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int h = bh % dm.H, bb = bh / dm.H;
   const int v0 = vt * VT;
   const int wv_id = wave_id();
-  const size_t ldo = (size_t)dm.H * V;
+  const size_t ldo = (size_t)dm.rdo;
 
   constexpr int NW = 8, NTHR = 64 * NW;
   constexpr int NTI = VT / 16;
@@ -118,7 +118,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     S.k.load(ck.kg + bhn * C * K, K);
     S.a.load(ck.aqk + bhn * C * C, C);
     S.g.load(ck.gcl + bhn * K, K);
-    S.o.load(dO + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0, ldo);
+    S.o.load(dO + ((size_t)bb * dm.T + (size_t)n * C) * ldo + (size_t)h * V + v0, ldo);
   };
   auto commit = [&](const Stage& S) {
     S.w.store(sW, L::LK);
@@ -283,7 +283,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
   RegStage<T, V, C> pvn;
   ph.load(hg, K);
   pdh.load(dhg, K);
-  pdo.load(dO + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V, (size_t)dm.H * V);
+  pdo.load(dO + ((size_t)bb * dm.T + (size_t)n * C) * dm.rdo + (size_t)h * V, (size_t)dm.rdo);
   pdv.load(gr.dvn + blk * C * V, V);
   pvn.load(ck.vnT + blk * V * C, C);
   store_convert(pdo, sDO, L::LV);
@@ -422,7 +422,6 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy(Gdn2Dims dm, Gdn2Chunks<T> ck
   const int h = bh % dm.H, bb = bh / dm.H;
   const int wv_id = wave_id();
   const size_t blk = (size_t)bhn;
-  const size_t rsK = (size_t)dm.H * K;
   const size_t t0 = (size_t)bb * dm.T + (size_t)n * C;
 
   stage_rows<T, C, C>(sA, L::LC, ck.ainv + blk * C * C, C);
@@ -440,16 +439,16 @@ __global__ __launch_bounds__(256) void gdn2_bwd_wy(Gdn2Dims dm, Gdn2Chunks<T> ck
 #pragma unroll
     for (int rr = 0; rr < M::RS; ++rr) {
       const size_t r = (size_t)(seg * M::RS + rr);
-      rk[rr].load(k + ((t0 + r) * dm.H + h) * K + c0 + cg * 8);
-      rb[rr].load(b + ((t0 + r) * dm.H + h) * K + c0 + cg * 8);
-      rv[rr].load(v + ((t0 + r) * dm.H + h) * V + c0 + cg * 8);
-      rw[rr].load(w + ((t0 + r) * dm.H + h) * V + c0 + cg * 8);
+      rk[rr].load(k + (t0 + r) * dm.rk + (size_t)h * K + c0 + cg * 8);
+      rb[rr].load(b + (t0 + r) * dm.rb + (size_t)h * K + c0 + cg * 8);
+      rv[rr].load(v + (t0 + r) * dm.rv + (size_t)h * V + c0 + cg * 8);
+      rw[rr].load(w + (t0 + r) * dm.rw + (size_t)h * V + c0 + cg * 8);
     }
     RegStage<T, C, KH> pdw, pdv;
     pdw.load(gr.dwt + blk * C * K + c0, K);
     pdv.load(gr.dvn + blk * C * V + c0, V);
     float gcr[M::RS][8];
-    chunk_cumsum<C, KH>(g + (t0 * dm.H + h) * K + c0, rsK, gcr, sTot, sGl);
+    chunk_cumsum<C, KH>(g + t0 * dm.rg + (size_t)h * K + c0, (size_t)dm.rg, gcr, sTot, sGl);
 #pragma unroll
     for (int rr = 0; rr < M::RS; ++rr) {
       const int r = seg * M::RS + rr;
@@ -597,9 +596,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int h = bh % dm.H, bb = bh / dm.H;
   const int wv_id = wave_id();
   const size_t blk = (size_t)bhn;
-  const size_t rsK = (size_t)dm.H * K;
+  const size_t rsK = (size_t)dm.H * K;  // the gradients' (dense) row stride
   const size_t t0 = (size_t)bb * dm.T + (size_t)n * C;
-  const size_t base = (t0 * dm.H + h) * K + d0;  // this slice's column 0
+  const size_t base = (t0 * dm.H + h) * K + d0;  // this slice's column 0 in the gradients
+  const size_t hk = (size_t)h * K + d0;           // ... and within an input row
 
   // q, k, b and dAqk / dAkk are requested before the cumsum of g, so their
   // latency overlaps it
@@ -607,10 +607,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   Raw8<T> rq[M::RS], rk[M::RS], rb[M::RS];
 #pragma unroll
   for (int rr = 0; rr < M::RS; ++rr) {
-    const size_t o = base + (size_t)(seg * M::RS + rr) * rsK + cg * 8;
-    rq[rr].load(q + o);
-    rk[rr].load(k + o);
-    rb[rr].load(b + o);
+    const size_t r = t0 + (size_t)(seg * M::RS + rr);
+    rq[rr].load(q + r * dm.rq + hk + cg * 8);
+    rk[rr].load(k + r * dm.rk + hk + cg * 8);
+    rb[rr].load(b + r * dm.rb + hk + cg * 8);
   }
   RegStage<T, C, C> pqk, pkk;
   pqk.load(gr.daqk + blk * C * C, C);
@@ -625,7 +625,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     rdkg[rr].load(gr.dkg + o);
   }
   float gcr[M::RS][8];
-  const bool exact = chunk_cumsum<C, KH>(g + base, rsK, gcr, sTot, sGl);
+  const bool exact = chunk_cumsum<C, KH>(g + t0 * dm.rg + hk, (size_t)dm.rg, gcr, sTot, sGl);
 #pragma unroll
   for (int rr = 0; rr < M::RS; ++rr) {
     const int r = seg * M::RS + rr;
@@ -756,9 +756,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __syncthreads();
   } else {
     // ---- exact path: raw q, k, b for the element-wise stage (fp32 exact multipliers)
-    stage_rows<T, C, KH>(sQ, L::LK, q + base, rsK);
-    stage_rows<T, C, KH>(sKt, L::LK, k + base, rsK);
-    stage_rows<T, C, KH>(sKB, L::LK, b + base, rsK);
+    stage_rows<T, C, KH>(sQ, L::LK, q + t0 * dm.rq + hk, (size_t)dm.rq);
+    stage_rows<T, C, KH>(sKt, L::LK, k + t0 * dm.rk + hk, (size_t)dm.rk);
+    stage_rows<T, C, KH>(sKB, L::LK, b + t0 * dm.rb + hk, (size_t)dm.rb);
     __syncthreads();
     // dgc is parked in this slice's dg rows (written by B5 below) until every
     // lane has read gc; the loop is kept rolled, this path is the rare one

@@ -147,17 +147,17 @@ struct IntraLds {
 // Exact pairwise scores for one chunk (reference form, used when the
 // factorised form could overflow or a positive gate breaks monotonicity).
 template <typename T, int C, int K>
-__device__ void intra_scores_exact(const float* sgc, const T* q, const T* k, const T* b,
-                                   size_t row_stride, float scale, float* out_qk, float* out_kk) {
+__device__ void intra_scores_exact(const float* sgc, const T* q, const T* k, const T* b, size_t sq,
+                                   size_t sk, size_t sb, float scale, float* out_qk, float* out_kk) {
   // thread t computes entries e = t, t + 256, ... of the C x C matrices
   for (int e = threadIdx.x, s = 0; e < C * C; e += 256, ++s) {
     const int i = e / C, j = e % C;
     float aqk = 0.f, akk = 0.f;
     if (j <= i) {
-      const T* qi = q + i * row_stride;
-      const T* ki = k + i * row_stride;
-      const T* bi = b + i * row_stride;
-      const T* kj = k + j * row_stride;
+      const T* qi = q + i * sq;
+      const T* ki = k + i * sk;
+      const T* bi = b + i * sb;
+      const T* kj = k + j * sk;
       for (int d = 0; d < K; ++d) {
         const float dd = sgc[i * K + d] - sgc[j * K + d];
         const float ed = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
@@ -205,15 +205,13 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
   const int bh = bhn / dm.NT;
   const int h = bh % dm.H;
   const int bb = bh / dm.H;
-  const size_t rsK = (size_t)dm.H * K;  // row stride of [B,T,H,K]
-  const size_t rsV = (size_t)dm.H * V;
   const size_t t0 = (size_t)bb * dm.T + (size_t)n * C;
-  const T* qc = q + (t0 * dm.H + h) * K;
-  const T* kc = k + (t0 * dm.H + h) * K;
-  const T* bc = b + (t0 * dm.H + h) * K;
-  const float* gc_in = g + (t0 * dm.H + h) * K;
-  const T* vc = v + (t0 * dm.H + h) * V;
-  const T* wc = w + (t0 * dm.H + h) * V;
+  const T* qc = q + t0 * dm.rq + (size_t)h * K;
+  const T* kc = k + t0 * dm.rk + (size_t)h * K;
+  const T* bc = b + t0 * dm.rb + (size_t)h * K;
+  const float* gc_in = g + t0 * dm.rg + (size_t)h * K;
+  const T* vc = v + t0 * dm.rv + (size_t)h * V;
+  const T* wc = w + t0 * dm.rw + (size_t)h * V;
 
   // q, k, b, v, w are requested before the cumsum of g, so their latency overlaps it
   const int cg = tid % L::NCG, seg = tid / L::NCG;
@@ -227,18 +225,18 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
   if constexpr (kRows) {
 #pragma unroll
     for (int rr = 0; rr < L::RS; ++rr) {
-      const size_t o = (size_t)(seg * L::RS + rr) * rsK + cg * 8;
-      rq[rr].load(qc + o);
-      rk[rr].load(kc + o);
-      rb[rr].load(bc + o);
+      const size_t r = (size_t)(seg * L::RS + rr);
+      rq[rr].load(qc + r * dm.rq + cg * 8);
+      rk[rr].load(kc + r * dm.rk + cg * 8);
+      rb[rr].load(bc + r * dm.rb + cg * 8);
     }
   }
   if constexpr (kVals) {
 #pragma unroll
     for (int rr = 0; rr < L::RSV; ++rr) {
-      const size_t o = (size_t)(segv * L::RSV + rr) * rsV + cgv * 8;
-      rv[rr].load(vc + o);
-      rw[rr].load(wc + o);
+      const size_t r = (size_t)(segv * L::RSV + rr);
+      rv[rr].load(vc + r * dm.rv + cgv * 8);
+      rw[rr].load(wc + r * dm.rw + cgv * 8);
     }
   }
 
@@ -246,7 +244,7 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
   if constexpr (kRows) {
   // ---- phase 0: gc = cumsum(g) over the chunk (gdn2_wy_reference.py:63)
   float gcr[L::RS][8];
-  exact = chunk_cumsum<C, K>(gc_in, rsK, gcr, sTot, sGl);
+  exact = chunk_cumsum<C, K>(gc_in, (size_t)dm.rg, gcr, sTot, sGl);
   if (kVals && tid < K) ck.gcl[(size_t)bhn * K + tid] = fin(sGl[tid]);
 
   // ---- phase 1: elementwise operands (gdn2_wy_reference.py:92-100)
@@ -347,7 +345,7 @@ __global__ __launch_bounds__(256) void gdn2_fwd_intra(Gdn2Dims dm, const T* __re
   } else {
     constexpr int PER = C * C / 256;
     float eqk[PER], ekk[PER];
-    intra_scores_exact<T, C, K>(sGcExact, qc, kc, bc, rsK, dm.scale, eqk, ekk);
+    intra_scores_exact<T, C, K>(sGcExact, qc, kc, bc, dm.rq, dm.rk, dm.rb, dm.scale, eqk, ekk);
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < PER; ++s) {

@@ -24,7 +24,7 @@ std::vector<WsEntry> g_ws_tags;
 bool ws_same(const WsTag& a, const WsTag& b) {
   if (a.kind != b.kind) return false;
   for (int i = 0; i < 8; ++i)
-    if (a.dims[i] != b.dims[i] || a.ptrs[i] != b.ptrs[i]) return false;
+    if (a.dims[i] != b.dims[i] || a.ptrs[i] != b.ptrs[i] || a.strides[i] != b.strides[i]) return false;
   return true;
 }
 void ws_erase_overlap(const char* lo, const char* hi) {
@@ -64,6 +64,9 @@ static WsTag gdn2_tag(const atomic_gdn2_args* a, const void* q, const void* k, c
   const int32_t d[8] = {a->batch, a->seqlen, a->heads, a->dk, a->dv, a->chunk, a->dtype, 0};
   const void* ptr[8] = {q, k, v, w, b, g, h0, nullptr};
   for (int i = 0; i < 8; ++i) { t.dims[i] = d[i]; t.ptrs[i] = ptr[i]; }
+  const int64_t dK = (int64_t)a->heads * a->dk, dV = (int64_t)a->heads * a->dv;
+  const int64_t dense[6] = {dK, dK, dV, dV, dK, dK};
+  for (int i = 0; i < 6; ++i) t.strides[i] = a->row_stride[i] ? a->row_stride[i] : dense[i];  // the forward's inputs
   return t;
 }
 
@@ -98,6 +101,16 @@ static int gdn2_plan(const atomic_gdn2_args* a, Gdn2Plan* p) {
   // +-1e4 state clip, applied at every 64 rows instead of every chunk.
   d.B = a->batch; d.T = a->seqlen; d.H = a->heads; d.K = a->dk; d.V = a->dv; d.C = kGdn2RunChunk;
   d.NT = a->seqlen / kGdn2RunChunk; d.scale = a->scale;
+  {
+    const long long dK = (long long)a->heads * a->dk, dV = (long long)a->heads * a->dv;
+    const long long dense[7] = {dK, dK, dV, dV, dK, dK, dV};
+    long long* out[7] = {&d.rq, &d.rk, &d.rv, &d.rw, &d.rb, &d.rg, &d.rdo};
+    for (int i = 0; i < 7; ++i) {
+      const long long s = a->row_stride[i];
+      if (s != 0 && (s < dense[i] || s % 8 != 0)) return ATOMIC_ERR_SHAPE;
+      *out[i] = s ? s : dense[i];
+    }
+  }
   p->dm = d;
   p->es = a->dtype == ATOMIC_BF16 ? 2 : 4;
   const size_t N = (size_t)d.B * d.H * d.NT;
@@ -309,14 +322,13 @@ __global__ __launch_bounds__(256) void gdn2_diag_akk(Gdn2Dims dm, const T* __res
   const int tid = threadIdx.x, bhn = blockIdx.x;
   const int n = bhn % dm.NT, bh = bhn / dm.NT, h = bh % dm.H, bb = bh / dm.H;
   const size_t t0 = (size_t)bb * dm.T + (size_t)n * C;
-  const size_t rs = (size_t)dm.H * K;
   for (int e = tid; e < C * K; e += 256) {
     const int i = e / K, d = e % K;
-    const size_t off = (t0 + i) * rs + (size_t)h * K + d;
-    const float kv = to_f(k[off]);
-    sgc[i * LD + d] = g[off];
+    const size_t hd = (size_t)h * K + d;
+    const float kv = to_f(k[(t0 + i) * dm.rk + hd]);
+    sgc[i * LD + d] = g[(t0 + i) * dm.rg + hd];
     sk[i * LD + d] = kv;
-    sbk[i * LD + d] = to_f(b[off]) * kv;
+    sbk[i * LD + d] = to_f(b[(t0 + i) * dm.rb + hd]) * kv;
   }
   __syncthreads();
   for (int d = tid; d < K; d += 256)
@@ -478,7 +490,8 @@ static int gdn2_forward_noalloc(const atomic_gdn2_args* a, const void* q, const 
   Launch L{a->profile, st};
   StageDiag D{a->diag, L};
   if (D && (rc = D.clear(0, ATOMIC_GDN2_DIAG_DV_NEW))) return rc;
-  const size_t T = (size_t)a->seqlen, rowK = (size_t)H * K, rowV = (size_t)H * V;
+  const size_t T = (size_t)a->seqlen, rowV = (size_t)H * V;
+  const Gdn2Dims& sd = p1.dm;  // the inputs' row strides
   for (int bb = 0; bb < a->batch; ++bb) {
     const float* hin = h0 ? h0 + (size_t)bb * state_elems : nullptr;
     int wi = 0;
@@ -486,16 +499,17 @@ static int gdn2_forward_noalloc(const atomic_gdn2_args* a, const void* q, const 
       const int nw = NT - n0 < W ? NT - n0 : W;
       const Gdn2Plan& pw = nw == W ? pfull : ptail;
       const size_t t0 = (size_t)bb * T + (size_t)n0 * kGdn2RunChunk;  // first row of the window
-      const char* qp = static_cast<const char*>(q) + t0 * rowK * es;
-      const char* kp = static_cast<const char*>(k) + t0 * rowK * es;
-      const char* bp = static_cast<const char*>(b) + t0 * rowK * es;
-      const char* vp = static_cast<const char*>(v) + t0 * rowV * es;
-      const char* wp = static_cast<const char*>(w) + t0 * rowV * es;
+      const char* qp = static_cast<const char*>(q) + t0 * sd.rq * es;
+      const char* kp = static_cast<const char*>(k) + t0 * sd.rk * es;
+      const char* bp = static_cast<const char*>(b) + t0 * sd.rb * es;
+      const char* vp = static_cast<const char*>(v) + t0 * sd.rv * es;
+      const char* wp = static_cast<const char*>(w) + t0 * sd.rw * es;
+      const float* gp = g + t0 * sd.rg;
       float* hout = n0 + nw == NT ? h_final + (size_t)bb * state_elems : slots[wi & 1];
-      rc = gdn2_forward(pw, a->dtype, qp, kp, vp, wp, bp, g + t0 * rowK, hin, o + t0 * rowV, hout, ws, 0, L);
+      rc = gdn2_forward(pw, a->dtype, qp, kp, vp, wp, bp, gp, hin, o + t0 * rowV, hout, ws, 0, L);
       if (rc) return rc;
       if (D) {  // the reports accumulate over the windows
-        rc = gdn2_forward_diag(pw, a->dtype, D, kp, bp, g + t0 * rowK, o + t0 * rowV,
+        rc = gdn2_forward_diag(pw, a->dtype, D, kp, bp, gp, o + t0 * rowV,
                                n0 + nw == NT ? hout : nullptr, ws);
         if (rc) return rc;
       }

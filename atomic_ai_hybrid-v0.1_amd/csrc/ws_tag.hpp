@@ -15,6 +15,7 @@ struct WsTag {
   int kind;              // which forward wrote the workspace
   int32_t dims[8];       // its shape / dtype arguments
   const void* ptrs[8];   // its input pointers
+  int64_t strides[8];    // its inputs' row strides (0 where dense)
 };
 
 // Forget every record overlapping [ws, ws + bytes): the caller's call writes there.

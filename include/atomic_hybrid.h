@@ -134,6 +134,12 @@ typedef struct atomic_gdn2_args {
   atomic_profile* profile;  /* optional per-kernel event timing, or NULL      */
   atomic_stage_report* diag;  /* optional stage reports (device memory,
                                  ATOMIC_GDN2_DIAG_COUNT entries), or NULL    */
+  /* Row strides of the [B, T, H, D] inputs q, k, v, w, b, g, dO, in elements:
+     token t of batch row b starts at (b T + t) * row_stride[i] (a slice of a
+     wider [B, T, F] tensor, e.g. one part of a fused projection).  0 = dense
+     (H K or H V).  Otherwise at least the dense value and a multiple of 8;
+     every input pointer 16-byte aligned.  Outputs and gradients are dense. */
+  int64_t row_stride[7];
 } atomic_gdn2_args;
 
 /* Bytes of workspace atomic_gdn2_fwd / atomic_gdn2_bwd need for these args. */

@@ -80,6 +80,13 @@ def test_workspace_size_rejects_bad_shapes_without_a_gpu():
     assert lib.atomic_gdn2_workspace_size(ctypes.byref(ok)) > 0
     bad = _lib.Gdn2Args(1, 100, 2, 128, 128, 64, _lib.ATOMIC_BF16, _lib.ATOMIC_BF16, 1.0, 0, None)
     assert lib.atomic_gdn2_workspace_size(ctypes.byref(bad)) == 0
+    # row strides: 0 (dense), or at least the dense row and a multiple of 8
+    ok.row_stride[0] = 200
+    assert lib.atomic_gdn2_workspace_size(ctypes.byref(ok)) == 0
+    ok.row_stride[0] = 260
+    assert lib.atomic_gdn2_workspace_size(ctypes.byref(ok)) == 0
+    ok.row_stride[0] = 264
+    assert lib.atomic_gdn2_workspace_size(ctypes.byref(ok)) > 0
     m_ok = _lib.Mamba2Args(1, 256, 2, 64, 128, 128, _lib.ATOMIC_BF16, _lib.ATOMIC_BF16, 0, None)
     assert lib.atomic_mamba2_workspace_size(ctypes.byref(m_ok)) > 0
     m_bad = _lib.Mamba2Args(1, 256, 2, 64, 128, 128, _lib.ATOMIC_F32, _lib.ATOMIC_BF16, 0, None)
