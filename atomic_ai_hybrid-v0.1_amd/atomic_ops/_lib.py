@@ -36,6 +36,27 @@ class Gdn2Args(ctypes.Structure):
                 ("row_stride", ctypes.c_int64 * 7)]
 
 
+def row_view(t):
+    """``(tensor, row_stride)`` for a [B, T, ...] input as the library reads
+    it: a view whose tokens are evenly spaced rows with the trailing dims
+    dense inside a row (a slice of a wider [B, T, F] tensor; row stride s a
+    multiple of 8, 16-byte aligned, batch stride T s) is passed as it is with
+    its row stride s; a contiguous tensor with 0; anything else as a
+    contiguous copy."""
+    if t.is_contiguous():
+        return t, 0
+    shape, st = t.shape, t.stride()
+    B, T = shape[0], shape[1]
+    inner, ok = 1, True
+    for d in range(len(shape) - 1, 1, -1):   # the trailing dims dense within a row
+        ok &= shape[d] == 1 or st[d] == inner
+        inner *= shape[d]
+    s = st[1]
+    if ok and (B == 1 or st[0] == T * s) and s >= inner and s % 8 == 0 and t.data_ptr() % 16 == 0:
+        return t, s
+    return t.contiguous(), 0
+
+
 class Gdn2Layout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_size_t) for n in
                 ("qg", "kg", "w_pseudo", "u", "aqk", "ainv", "gc_last", "h_pre_t", "v_new_t", "total")]
@@ -45,7 +66,7 @@ class Mamba2Args(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int32), ("seqlen", ctypes.c_int32), ("heads", ctypes.c_int32),
                 ("headdim", ctypes.c_int32), ("dstate", ctypes.c_int32), ("chunk", ctypes.c_int32),
                 ("dtype", ctypes.c_int32), ("dy_dtype", ctypes.c_int32), ("flags", ctypes.c_int32),
-                ("profile", ctypes.c_void_p), ("diag", ctypes.c_void_p)]
+                ("profile", ctypes.c_void_p), ("diag", ctypes.c_void_p), ("row_stride", ctypes.c_int64 * 5)]
 
 
 class NormGateArgs(ctypes.Structure):

@@ -28,19 +28,9 @@ def _stream(device):
 
 
 def rows(t):
-    """``(tensor, row_stride)`` for a [B, T, H, D] input as the library reads
-    it: a view whose tokens are evenly spaced rows (a slice of a wider
-    [B, T, F] tensor: strides (T s, s, D, 1), s a multiple of 8, 16-byte
-    aligned) is passed as it is with its row stride s; a dense tensor with
-    stride 0; anything else as a dense copy."""
-    if t.is_contiguous():
-        return t, 0
-    B, T, H, D = t.shape
-    sb, st, sh, sd = t.stride()
-    if sd == 1 and (H == 1 or sh == D) and (B == 1 or sb == T * st) and st >= H * D and st % 8 == 0 \
-            and t.data_ptr() % 16 == 0:
-        return t, st
-    return t.contiguous(), 0
+    """``(tensor, row_stride)`` of a [B, T, H, D] input as the library reads
+    it (``_lib.row_view``)."""
+    return _lib.row_view(t)
 
 
 def _rows_of(args, tensors, first=0):

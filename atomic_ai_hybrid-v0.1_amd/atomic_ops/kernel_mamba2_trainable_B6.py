@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import torch
 
+from . import _lib
 from . import mamba2 as _m
 
 
@@ -21,9 +22,10 @@ class _Mamba2Core(torch.autograd.Function):
     def forward(ctx, dt, x, B, C, A, chunk_size, state0):
         need = any(ctx.needs_input_grad)
         ctx.A_dtype, ctx.state0_dtype = A.dtype, state0.dtype
-        # the tensors the library sees, kept for the backward: its reuse of
-        # the forward's workspace is checked against these addresses
-        dt, x, B, C = (t.contiguous() for t in (dt, x, B, C))
+        # the tensors the library sees (row-strided views as they are, other
+        # layouts as dense copies), kept for the backward: its reuse of the
+        # forward's workspace is checked against these addresses and strides
+        dt, x, B, C = (_lib.row_view(t)[0] for t in (dt, x, B, C))
         A = A.to(torch.float32).contiguous()
         state0 = state0.to(torch.float32).contiguous()
         y, state_final, ws = _m.forward(dt, x, B, C, A, chunk_size, state0, save=need)

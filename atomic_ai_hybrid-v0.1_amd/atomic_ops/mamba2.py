@@ -39,6 +39,16 @@ def _check(dt, x, Bm, Cm, A):
         raise ValueError("A must be float32 [H]")
 
 
+def _rows_of(args, tensors):
+    """_lib.row_view of dt, x, B, C (and dy), their strides into args.row_stride."""
+    out = []
+    for i, t in enumerate(tensors):
+        t2, s = _lib.row_view(t)
+        args.row_stride[i] = s
+        out.append(t2)
+    return out
+
+
 def make_args(dt, Bm, chunk_size, *, dy_dtype=None, flags=0):
     b, l, h, p = dt.shape
     if l % chunk_size != 0:
@@ -61,10 +71,11 @@ def forward(dt, x, Bm, Cm, A, chunk_size, state0=None, *, save=False, workspace=
     forward's per-stage reports."""
     _check(dt, x, Bm, Cm, A)
     lib = _lib.load()
-    dt, x, Bm, Cm, A = (t.contiguous() for t in (dt, x, Bm, Cm, A))
     b, l, h, p = dt.shape
     n = Bm.shape[-1]
     args = make_args(dt, Bm, chunk_size, flags=M2_SAVE if save else 0)
+    dt, x, Bm, Cm = _rows_of(args, (dt, x, Bm, Cm))
+    A = A.contiguous()
     if timer is not None:
         args.profile = timer.arm()
     if diag is not None:
@@ -88,17 +99,20 @@ def backward(dt, x, Bm, Cm, A, chunk_size, dy, dstate_final=None, state0=None, *
     primals' dtypes (dA, dstate0 float32).  ``reuse`` declares that
     ``workspace`` holds the forward of the same inputs; the library checks
     that by the input addresses, so an input that has to be copied here (not
-    contiguous, or state0 not float32) turns reuse into a recompute."""
+    contiguous and not row-strided, or state0 not float32) turns reuse into a
+    recompute."""
     _check(dt, x, Bm, Cm, A)
     lib = _lib.load()
-    if reuse and not all(t.is_contiguous() for t in (dt, x, Bm, Cm, A)) or \
-            (state0 is not None and (state0.dtype != torch.float32 or not state0.is_contiguous())):
-        reuse = False
-    dt, x, Bm, Cm, A = (t.contiguous() for t in (dt, x, Bm, Cm, A))
-    dy = dy.contiguous()
     if dy.dtype not in _DT:
         dy = dy.to(torch.float32)
-    args = make_args(dt, Bm, chunk_size, dy_dtype=dy.dtype, flags=M2_REUSE if reuse else 0)
+    args = make_args(dt, Bm, chunk_size, dy_dtype=dy.dtype)
+    seen = (dt, x, Bm, Cm)
+    dt, x, Bm, Cm, dy = _rows_of(args, seen + (dy,))
+    if any(a is not b_ for a, b_ in zip((dt, x, Bm, Cm), seen)) or not A.is_contiguous() or \
+            (state0 is not None and (state0.dtype != torch.float32 or not state0.is_contiguous())):
+        reuse = False
+    A = A.contiguous()
+    args.flags = M2_REUSE if reuse else 0
     if timer is not None:
         args.profile = timer.arm()
     if diag is not None:
@@ -111,8 +125,9 @@ def backward(dt, x, Bm, Cm, A, chunk_size, dy, dstate_final=None, state0=None, *
         dstate_final = dstate_final.to(torch.float32).contiguous()
     b, l, h, p = dt.shape
     n = Bm.shape[-1]
-    ddt, dx = torch.empty_like(dt), torch.empty_like(x)
-    dB, dC = torch.empty_like(Bm), torch.empty_like(Cm)
+    # the gradients are dense
+    ddt, dx = (torch.empty(dt.shape, dtype=dt.dtype, device=dt.device) for _ in range(2))
+    dB, dC = (torch.empty(Bm.shape, dtype=Bm.dtype, device=Bm.device) for _ in range(2))
     dA = torch.empty(h, dtype=torch.float32, device=dt.device)
     dstate0 = torch.empty(b, h, p, n, dtype=torch.float32, device=dt.device)
     rc = lib.atomic_mamba2_bwd(ctypes.byref(args), _ptr(dt), _ptr(x), _ptr(Bm), _ptr(Cm), _ptr(A),

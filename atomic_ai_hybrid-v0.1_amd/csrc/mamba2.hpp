@@ -7,6 +7,9 @@ namespace ah {
 
 struct Mamba2Dims {
   int B, T, H, P, N, C, NT;
+  // row strides of the inputs in elements (token t of batch b starts at
+  // (b T + t) * stride): dt, x, B, C, dy
+  long long rdt, rx, rB, rC, rdy;
 };
 
 template <typename T>

@@ -160,8 +160,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int HG = dm.H / G;
   const int wv_id = wave_id();
   const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
-  const T* Bg0 = Bm + row0 * N;
-  const T* Cg0 = Cm + row0 * N;
+  const T* Bg0 = Bm + row0 * dm.rB;
+  const T* Cg0 = Cm + row0 * dm.rC;
+  const int ldb = (int)dm.rB, ldc = (int)dm.rC;
   const T* cb0 = ck.cb + (size_t)bn * C * C;
   constexpr int NB = C / 16;
 
@@ -207,10 +208,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const int e = tid + NTH * it;
       if (NE % NTH == 0 || e < NE) {
         const int r = item_row(e), c = item_col(e);
-        const size_t o = ((rowb + r) * dm.H + hn) * P + pn + c;
-        ndt[it].load(dt + o);
-        nx[it].load(x + o);
-        ndy[it].load(dy + o);
+        const size_t hp = (size_t)hn * P + pn + c;
+        ndt[it].load(dt + (rowb + r) * dm.rdt + hp);
+        nx[it].load(x + (rowb + r) * dm.rx + hp);
+        ndy[it].load(dy + (rowb + r) * dm.rdy + hp);
       }
     }
 #pragma unroll
@@ -248,8 +249,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       frag cfr[N / 32], bfr[N / 32];
 #pragma unroll
       for (int kk = 0; kk < N / 32; ++kk) {
-        cfr[kk] = Mma<T>::ld_c(Cg, N, 16 * I, 32 * kk);
-        bfr[kk] = Mma<T>::ld_c(Bg, N, 16 * I, 32 * kk);
+        cfr[kk] = Mma<T>::ld_c(Cg, ldc, 16 * I, 32 * kk);
+        bfr[kk] = Mma<T>::ld_c(Bg, ldb, 16 * I, 32 * kk);
       }
       // ---- A: slice inputs (dt, x, dy kept exactly as bf16), a = sanitize(dt A, 20);
       // thread item = 8 channels of one row, kept in registers for B
@@ -718,8 +719,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     store4(sCB + i * L::LCB + j, sv);
   }
   if (KB < HP) load(s1, KB);
-  stage_rows<T, C, NTL, NTH>(sB, L::LK, Bm + row0 * N + n0, N);
-  stage_rows<T, C, NTL, NTH>(sC, L::LK, Cm + row0 * N + n0, N);
+  stage_rows<T, C, NTL, NTH>(sB, L::LK, Bm + row0 * dm.rB + n0, dm.rB);
+  stage_rows<T, C, NTL, NTH>(sC, L::LK, Cm + row0 * dm.rC + n0, dm.rC);
 
   // one k block: its staged rows to LDS, the stage refilled two blocks ahead,
   // then the MFMAs on the fragments kept from the stage

@@ -57,8 +57,8 @@ __global__ __launch_bounds__(256) void mamba2_cb(Mamba2Dims dm, const T* __restr
   __shared__ __attribute__((aligned(16))) T sC[C * LN];
   const int bn = blockIdx.x;  // b * NT + n
   const size_t row0 = (size_t)bn * C;  // rows of [B*T][N]
-  stage_rows<T, C, N>(sB, LN, Bm + row0 * N, N);
-  stage_rows<T, C, N>(sC, LN, Cm + row0 * N, N);
+  stage_rows<T, C, N>(sB, LN, Bm + row0 * dm.rB, dm.rB);
+  stage_rows<T, C, N>(sC, LN, Cm + row0 * dm.rC, dm.rC);
   __syncthreads();
   constexpr int MT = C / 16;
   T* out = ck.cb + (size_t)bn * C * C;
@@ -106,8 +106,7 @@ __global__ __launch_bounds__(256) void mamba2_cumdecay(Mamba2Dims dm, const T* _
   const int h = m / NPT, p0 = (m % NPT) * PT;
   const int bb = bn / dm.NT, n = bn % dm.NT;
   const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
-  const size_t rsx = (size_t)dm.H * P;
-  const size_t base = (row0 * dm.H + h) * P + p0;
+  const size_t hp = (size_t)h * P + p0;
   const float Ah = A[h];
   constexpr int PER_ROW = PT / 8, NE = C * PER_ROW, EPT = NE / 256;
   static_assert(NE % 256 == 0, "slice must split evenly over the workgroup");
@@ -115,7 +114,7 @@ __global__ __launch_bounds__(256) void mamba2_cumdecay(Mamba2Dims dm, const T* _
   for (int i = 0; i < EPT; ++i) {
     const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
     Raw8<T> rdt;
-    rdt.load(dt + base + r * rsx + c);
+    rdt.load(dt + (row0 + r) * dm.rdt + hp + c);
     float av[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) av[j] = sanitize(rdt[j] * Ah, kClipDecay);
@@ -185,9 +184,10 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
   xcd_group_map(blockIdx.x, dm.B * dm.NT, dm.H * NPT / SL, bn, m2);
   const int bb = bn / dm.NT, n = bn % dm.NT;
   const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
-  const size_t rsx = (size_t)dm.H * P;
+  const size_t rsx = (size_t)dm.H * P;  // the workspace rows (Ydh, W)
   // R (B or C of the chunk) is shared by the workgroup's SL (head, slice) pairs
-  stage_rows<T, C, N>(sR, L::LN, R + row0 * N, N);
+  const size_t rR = BWD ? (size_t)dm.rC : (size_t)dm.rB;
+  stage_rows<T, C, N>(sR, L::LN, R + row0 * rR, rR);
   for (int sl = 0; sl < SL; ++sl) {
   const int m = m2 * SL + sl;
   const int h = m / NPT, p0 = (m % NPT) * PT;
@@ -201,9 +201,10 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
 #pragma unroll
   for (int i = 0; i < EPT; ++i) {
     const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
-    rdt[i].load(dt + base + r * rsx + c);
-    rx[i].load(x + base + r * rsx + c);
-    if constexpr (BWD) rdy[i].load(dy + base + r * rsx + c);
+    const size_t hp = (size_t)h * P + p0 + c, rr = row0 + r;
+    rdt[i].load(dt + rr * dm.rdt + hp);
+    rx[i].load(x + rr * dm.rx + hp);
+    if constexpr (BWD) rdy[i].load(dy + rr * dm.rdy + hp);
   }
   if constexpr (STG) {
     load_cum_rows<C, PT, L::LC>(sCum, ck.cum + bhn_ref * C * P + p0, P);
@@ -451,7 +452,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
   const size_t rsx = (size_t)dm.H * P;
   const T* cbg = ck.cb + (size_t)bn * C * C;
-  const T* cg = Cm + row0 * N;
+  const T* cg = Cm + row0 * dm.rC;
+  const int ldc = (int)dm.rC;
   constexpr int NB = C / 16, BPW = NB / 4, YNI = PT / 16, KN = N / Mma<T>::KS;
   static_assert(NB % 4 == 0, "row blocks must split evenly over 4 waves");
   // compiled per wave (its output blocks are constants): the fragment arrays
@@ -472,7 +474,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     if constexpr (YM != 1) {
 #pragma unroll
-      for (int kk = 0; kk < KN; ++kk) fc[bi][kk] = Mma<T>::ld_c(cg, N, 16 * I, kk * Mma<T>::KS);
+      for (int kk = 0; kk < KN; ++kk) fc[bi][kk] = Mma<T>::ld_c(cg, ldc, 16 * I, kk * Mma<T>::KS);
     }
   });
   // thread item = 8 channels of one row; 16 consecutive items take 16
@@ -485,16 +487,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int m = m2 * SL + sl;
     return (row0 * dm.H + m / NPT) * P + (m % NPT) * PT;
   };
+  auto slice_hp = [&](int sl) {  // the slice's column within an input row
+    const int m = m2 * SL + sl;
+    return (size_t)(m / NPT) * P + (m % NPT) * PT;
+  };
   // dt, x of a slice: the next slice's are requested once the current one's
   // registers are free, so their latency overlaps its MFMA phase
   Raw8<T> rdt[EPT], rx[EPT];
   auto load_dtx = [&](int sl) {
-    const size_t b = slice_base(sl);
+    const size_t hp = slice_hp(sl);
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
       const int e = threadIdx.x + 256 * i, r = item_row(e), c = item_col(e);
-      rdt[i].load(dt + b + r * rsx + c);
-      rx[i].load(x + b + r * rsx + c);
+      rdt[i].load(dt + (row0 + r) * dm.rdt + hp + c);
+      rx[i].load(x + (row0 + r) * dm.rx + hp + c);
     }
   };
   if constexpr (YM != 2) load_dtx(0);

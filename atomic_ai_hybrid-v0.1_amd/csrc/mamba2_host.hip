@@ -37,6 +37,16 @@ static int mamba2_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
   // exp(20) on the decay to the chunk end) apply over 256 rows instead.
   d.C = a->chunk == 256 ? 128 : a->chunk;
   d.NT = a->seqlen / d.C;
+  {
+    const long long dP = (long long)a->heads * a->headdim, dN = a->dstate;
+    const long long dense[5] = {dP, dP, dN, dN, dP};
+    long long* out[5] = {&d.rdt, &d.rx, &d.rB, &d.rC, &d.rdy};
+    for (int i = 0; i < 5; ++i) {
+      const long long s = a->row_stride[i];
+      if (s != 0 && (s < dense[i] || s % 8 != 0)) return ATOMIC_ERR_SHAPE;
+      *out[i] = s ? s : dense[i];
+    }
+  }
   p->dm = d;
   const size_t es = 2, B = d.B, H = d.H, NT = d.NT, C = d.C, P = d.P, N = d.N, T = d.T;
   // enough (batch, chunk, head group) workgroups for two rounds of the chip's
@@ -415,6 +425,9 @@ static WsTag mamba2_tag(const atomic_mamba2_args* a, const void* dt, const void*
   const int32_t d[8] = {a->batch, a->seqlen, a->heads, a->headdim, a->dstate, a->chunk, a->dtype, 0};
   const void* ptr[8] = {dt, x, B, C, A, state0, nullptr, nullptr};
   for (int i = 0; i < 8; ++i) { t.dims[i] = d[i]; t.ptrs[i] = ptr[i]; }
+  const int64_t dP = (int64_t)a->heads * a->headdim, dN = a->dstate;
+  const int64_t dense[4] = {dP, dP, dN, dN};
+  for (int i = 0; i < 4; ++i) t.strides[i] = a->row_stride[i] ? a->row_stride[i] : dense[i];  // dt, x, B, C
   return t;
 }
 

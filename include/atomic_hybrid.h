@@ -300,6 +300,12 @@ typedef struct atomic_mamba2_args {
   atomic_profile* profile;  /* optional per-kernel event timing, or NULL */
   atomic_stage_report* diag;  /* optional stage reports (device memory,
                                  ATOMIC_MAMBA2_DIAG_COUNT entries), or NULL */
+  /* Row strides of the inputs dt, x ([B, T, H, P]), B, C ([B, T, N]) and dy,
+     in elements: token t of batch row b starts at (b T + t) * row_stride[i].
+     0 = dense (H P, or N).  Otherwise at least the dense value and a multiple
+     of 8; every input pointer 16-byte aligned.  Outputs and gradients are
+     dense, and so are the stage entries' per-chunk arrays. */
+  int64_t row_stride[5];
 } atomic_mamba2_args;
 
 /* Bytes of workspace atomic_mamba2_fwd / atomic_mamba2_bwd need. */

@@ -85,3 +85,46 @@ def test_gdn2_strided_noalloc_and_wrapper():
     for i in range(5):
         assert torch.equal(big.grad[..., i * HK:(i + 1) * HK].reshape(B, T, H, K), leaves[i].grad), i
     assert torch.equal(gbig.grad[..., :HK].reshape(B, T, H, K), leaves[5].grad)
+
+
+def test_mamba2_strided_inputs_equal_dense():
+    """dt, x as slices of one [B, T, 2 H P + 8] tensor and B, C of one
+    [B, T, 2 N + 8] tensor (the in_proj / projection outputs of a fused
+    layer), dy a slice too: outputs and gradients bit-identical to dense."""
+    from atomic_ops import mamba2 as M
+    from atomic_ops import kernel_mamba2_trainable_B6 as KM
+    B, T, H, P, N, C = 2, 256, 4, 64, 128, 128
+    banner("mamba2 row-strided inputs")
+    d = inputs.mamba2_inputs(B, T, H, P, N, seed=31, dO=True)
+    dt, x = _slices([d["dt"], d["x"]], 8)
+    Bm, Cm = (t.view(B, T, N) for t in _slices([d["Bm"].view(B, T, 1, N), d["Cm"].view(B, T, 1, N)], 8))
+    (dy,) = _slices([d["dy"]], 8)
+    A = d["A"].cuda()
+    views = [dt, x, Bm, Cm]
+    for t in views + [dy]:
+        assert not t.is_contiguous() and _lib.row_view(t)[1] == t.stride(1)
+    dense = [t.contiguous() for t in views]
+    s0 = 0.2 * torch.randn(B, H, P, N, device="cuda")
+    y_s, f_s, ws_s = M.forward(*views, A, C, s0, save=True)
+    y_d, f_d, ws_d = M.forward(*dense, A, C, s0, save=True)
+    torch.cuda.synchronize()
+    assert torch.equal(y_s, y_d) and torch.equal(f_s, f_d)
+    g_s = M.backward(*views, A, C, dy, state0=s0, workspace=ws_s, reuse=True)
+    g_d = M.backward(*dense, A, C, dy.contiguous(), state0=s0, workspace=ws_d, reuse=True)
+    g_r = M.backward(*views, A, C, dy, state0=s0)
+    torch.cuda.synchronize()
+    for name, a, b_, c in zip(("ddt", "dx", "dB", "dC", "dA", "dstate0"), g_s, g_d, g_r):
+        assert torch.equal(a, b_) and torch.equal(c, b_), name
+    # the trainable wrapper on views of a parent that requires grad
+    big = dt._base.detach().clone().requires_grad_(True)
+    HP = H * P
+    src = [big[..., :HP].view(B, T, H, P), big[..., HP:2 * HP].view(B, T, H, P), Bm, Cm]
+    y1, _ = KM.mamba2_pallas_forward_trainable_B6(*src, A, C)
+    leaves = [t.detach().clone().requires_grad_(True) for t in dense[:2]]
+    y2, _ = KM.mamba2_pallas_forward_trainable_B6(leaves[0], leaves[1], dense[2], dense[3], A, C)
+    torch.autograd.backward(y1, dy.float())
+    torch.autograd.backward(y2, dy.float())
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert torch.equal(big.grad[..., :HP].reshape(B, T, H, P), leaves[0].grad)
+    assert torch.equal(big.grad[..., HP:2 * HP].reshape(B, T, H, P), leaves[1].grad)
