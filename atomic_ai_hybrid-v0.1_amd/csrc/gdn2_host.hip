@@ -291,7 +291,12 @@ int gdn2_backward(const Gdn2Plan& p, int dtype, int do_dtype, const void* q, con
     if (do_dtype == ATOMIC_BF16) AH_GDN2_BWD(bf16, bf16, 64);
     AH_GDN2_BWD(bf16, float, 64);
   }
-  if (p.dm.K != 64) return ATOMIC_ERR_SHAPE;  // fp32 backward: the per-chunk tiles fit LDS for K = 64
+  // fp32 operands: at K = 128 every backward kernel fits the LDS at one
+  // workgroup per CU (gdn2_bwd_dh 160 KB, gdn2_bwd_hgrad 138 KB)
+  if (p.dm.K == 128) {
+    if (do_dtype == ATOMIC_BF16) AH_GDN2_BWD(float, bf16, 128);
+    AH_GDN2_BWD(float, float, 128);
+  }
   if (do_dtype == ATOMIC_BF16) AH_GDN2_BWD(float, bf16, 64);
   AH_GDN2_BWD(float, float, 64);
 #undef AH_GDN2_BWD
@@ -568,7 +573,6 @@ extern "C" int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const v
   Gdn2Plan p;
   const int rc = gdn2_plan(a, &p);
   if (rc != ATOMIC_OK) return rc;
-  if (a->dtype == ATOMIC_F32 && a->dk != 64) return ATOMIC_ERR_SHAPE;
   if (!q || !k || !v || !w || !b || !g || !dO || !dq || !dk || !dv || !dw || !db || !dg)
     return ATOMIC_ERR_NULL;
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;

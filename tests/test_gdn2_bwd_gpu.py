@@ -60,6 +60,8 @@ def _check(out, ref, dtype, primal_dtypes):
     (1, 128, 2, 64, BF16, 1.0, True, True),
     (1, 64, 2, 128, BF16, 1.0, True, True),           # one chunk: only the state loop's tail step
     (1, 128, 48, 128, BF16, 1.0, True, True),         # 48 heads: 32-column V tiles in the forward
+    (1, 192, 2, 128, F32, 128 ** -0.5, True, True),   # fp32 operands at K = 128 (fp32 tolerance)
+    (2, 128, 3, 128, F32, 1.0, False, False),
 ])
 def test_backward_matches_autodiff(B, T, H, K, dtype, scale, with_state, reuse):
     banner(f"gdn2 bwd B{B} T{T} H{H} K{K} {dtype} scale={scale} state={with_state} reuse={reuse}")
@@ -78,7 +80,7 @@ def test_backward_fp32_upstream_gradient():
 
 @pytest.mark.parametrize("case,dtype,K", [
     ("deep_decay", F32, 64), ("deep_decay", BF16, 128), ("deep_decay_upper_columns", BF16, 128),
-    ("positive_gate", BF16, 128),
+    ("positive_gate", BF16, 128), ("deep_decay_upper_columns", F32, 128),
 ])
 def test_backward_exact_pairwise_path(case, dtype, K):
     """A chunk whose decay exceeds the factorisation bound takes the exact
