@@ -214,6 +214,7 @@ _SIGS = {
     "atomic_mamba2_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(Mamba2PrologueArgs)] + [_P] * 19 + [_P, ctypes.c_size_t, _P]),
     "atomic_gdn2_chunk_wy": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 13 + [_P]),
     "atomic_gdn2_inter_chunk_combine": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 9 + [_P]),
+    "atomic_gdn2_inter_chunk_combine_with_state": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 11 + [_P]),
     "atomic_gdn2_chunk_scores": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 6 + [_P]),
     "atomic_gdn2_wy_solve": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 2 + [_P]),
     "atomic_gdn2_recompute_wy": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 12 + [_P]),

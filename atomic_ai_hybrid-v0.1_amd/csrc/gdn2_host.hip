@@ -713,6 +713,38 @@ extern "C" int atomic_gdn2_inter_chunk_combine(const atomic_gdn2_args* a, const 
                        : gdn2_state_launch<float, 64>(p, ck, h0, o, h_final, mode, L);
 }
 
+extern "C" int atomic_gdn2_inter_chunk_combine_with_state(const atomic_gdn2_args* a, const void* Aqk,
+                                                          const void* w_pseudo, const void* u, const void* kg,
+                                                          const void* qg, const float* gc_last, const float* h0,
+                                                          float* o, float* h_final, void* h_pre_t, void* v_new_t,
+                                                          void* stream) {
+  Gdn2Plan p;
+  const int rc = gdn2_stage_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!Aqk || !w_pseudo || !u || !kg || !qg || !gc_last || !o || !h_final || !h_pre_t || !v_new_t)
+    return ATOMIC_ERR_NULL;
+  Launch L{a->profile, (hipStream_t)stream};
+  const int mode = kStateSave | kStateChunkO | kStateSanitizeH0;
+  void* aq = const_cast<void*>(Aqk);
+  void* wt = const_cast<void*>(w_pseudo);
+  void* uu = const_cast<void*>(u);
+  void* kk = const_cast<void*>(kg);
+  void* qq = const_cast<void*>(qg);
+  float* gl = const_cast<float*>(gc_last);
+  if (a->dtype == ATOMIC_BF16) {
+    Gdn2Chunks<bf16> ck = gdn2_stage_chunks<bf16>(aq, nullptr, wt, uu, kk, qq, gl);
+    ck.hT = static_cast<bf16*>(h_pre_t);
+    ck.vnT = static_cast<bf16*>(v_new_t);
+    return p.dm.K == 128 ? gdn2_state_launch<bf16, 128>(p, ck, h0, o, h_final, mode, L)
+                         : gdn2_state_launch<bf16, 64>(p, ck, h0, o, h_final, mode, L);
+  }
+  Gdn2Chunks<float> ck = gdn2_stage_chunks<float>(aq, nullptr, wt, uu, kk, qq, gl);
+  ck.hT = static_cast<float*>(h_pre_t);
+  ck.vnT = static_cast<float*>(v_new_t);
+  return p.dm.K == 128 ? gdn2_state_launch<float, 128>(p, ck, h0, o, h_final, mode, L)
+                       : gdn2_state_launch<float, 64>(p, ck, h0, o, h_final, mode, L);
+}
+
 extern "C" int atomic_gdn2_fwd_noalloc(const atomic_gdn2_args* a, const void* q, const void* k,
                                        const void* v, const void* w, const void* b, const float* g,
                                        const float* h0, float* o, float* h_final, void* stream) {

@@ -256,6 +256,16 @@ int atomic_gdn2_inter_chunk_combine(const atomic_gdn2_args* a, const void* Aqk, 
                                     const void* u, const void* kg, const void* qg, const float* gc_last,
                                     const float* h0, float* o, float* h_final, void* stream);
 
+/* Kernel D keeping its per-chunk states: gdn2_inter_chunk_combine_with_state
+ * (kernel_d_pipeline.py:127-158), the residuals of the reference's backward.
+ * Besides o and h_final it writes, in args.dtype and transposed (the layout
+ * this library's backward reads), the state entering each chunk
+ * h_pre_t [B][H][NT][V][K] and v_new_t [B][H][NT][V][64]. */
+int atomic_gdn2_inter_chunk_combine_with_state(const atomic_gdn2_args* a, const void* Aqk, const void* w_pseudo,
+                                               const void* u, const void* kg, const void* qg,
+                                               const float* gc_last, const float* h0, float* o, float* h_final,
+                                               void* h_pre_t, void* v_new_t, void* stream);
+
 /* ---------------------------------------------------------------- Mamba2 */
 
 enum {

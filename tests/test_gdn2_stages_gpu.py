@@ -143,3 +143,33 @@ def test_stage_entries_reject_other_chunks():
                                     torch.zeros(1, 2, 2, 64, device="cuda"), 1.0)
     with pytest.raises(ValueError):
         KB.wy_solve_pallas(torch.zeros(1, 2, 2, 128, 128, device="cuda"))
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+def test_combine_with_state_and_residuals(dtype):
+    """gdn2_inter_chunk_combine_with_state / gdn2_pallas_forward_with_residuals
+    (kernel_d_pipeline.py:127,199): o, h_final equal to the plain combine and
+    the whole forward; h_pre_all and v_new_all against the oracle's scan of
+    the same stages, in the reference's [NT, B, H, ., .] order."""
+    B, T, H, K = 2, 192, 2, 128
+    banner(f"gdn2 combine with state {dtype}")
+    q, k, v, w, b, g = _inputs(B, T, H, K, dtype, 95)
+    h0 = 0.4 * torch.randn(B, H, K, K, generator=torch.Generator().manual_seed(96))
+    dq, dk, dv, dw, db, dg = (t.cuda() for t in (q, k, v, w, b, g))
+    o, hf, res = KD.gdn2_pallas_forward_with_residuals(dq, dk, dv, dw, db, dg, 0.6, h0=h0.cuda())
+    o_w, h_w, _ = G.forward(dq, dk, dv, dw, db, dg, 0.6, h0=h0.cuda())
+    torch.cuda.synchronize()
+    tol = tol_for(dtype)
+    assert rel_err(o, o_w) < tol and rel_err(hf, h_w) < tol
+    # the states of the scan against the oracle on the device's own stages
+    st = [res[n].float().cpu() for n in ("Aqk", "w_pseudo", "u", "kg", "qg", "gc_last")]
+    h = h0.double()
+    NT = T // 64
+    for n in range(NT):
+        Aqk_c, wp_c, u_c, kg_c, qg_c, gl_c = (t[:, :, n].double() for t in st)
+        v_new = u_c - wp_c @ h
+        e_h, e_v = rel_err(res["h_pre_all"][n], h), rel_err(res["v_new_all"][n], v_new)
+        print(f"  chunk {n}: h_pre {e_h:.2e} v_new {e_v:.2e}")
+        assert res["h_pre_all"].shape == (NT, B, H, K, K) and e_h < tol and e_v < tol
+        h = og.sanitize(h * torch.exp(gl_c)[..., None] + kg_c.transpose(-1, -2) @ v_new)
+    assert set(res) == {"Aqk", "Akk", "A", "h_pre_all", "v_new_all", "w_pseudo", "u", "kg", "qg", "gc_last"}
