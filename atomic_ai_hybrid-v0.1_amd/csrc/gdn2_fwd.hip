@@ -555,10 +555,12 @@ struct StateLds {
 // [B][T][H][V]; sanitise h0 (nan_to_num(clip(h0, +-1e4)), its _sanitize_h0).
 enum { kStateSave = 1, kStateChunkO = 2, kStateSanitizeH0 = 4 };
 
-// Eight waves (two per SIMD): the state tiles and the [w; q] h tiles of one
-// V tile split over them by row blocks.
-template <typename T, int C, int K, int V, int VT>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T> ck,
+// NW waves (NW / 4 per SIMD): the state tiles and the [w; q] h tiles of one
+// V tile split over them by row blocks.  PD register sets of chunk operands
+// are in flight (two at eight waves; one at sixteen, where the other waves
+// hide the load latency and the VGPR budget is 128).
+template <typename T, int C, int K, int V, int VT, int NW = 8, int PD = 2>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4))) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T> ck,
                                                      const float* __restrict__ h0, float* __restrict__ o,
                                                      float* __restrict__ h_final, int mode) {
   const int save = mode & kStateSave;
@@ -588,7 +590,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int wv_id = wave_id();
 
   // state tiles h[d][v]: (K/16) x (VT/16), TPW per wave
-  constexpr int NW = 8, NTHR = 64 * NW;
+  constexpr int NTHR = 64 * NW;
   constexpr int NTI = VT / 16;
   constexpr int NTH = (K / 16) * NTI;
   constexpr int TPW = NTH / NW;
@@ -650,7 +652,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   commit(s0, 0);
   __syncthreads();
   prefetch(s0, min(1, last));
-  prefetch(s1, min(2, last));
+  if constexpr (PD == 2) prefetch(s1, min(2, last));
 
   // One chunk step; S holds chunk n + 1 on entry and is refilled with chunk n + 3.
   // Two stage buffers: chunk n + 1 goes into the other buffer at the start (its
@@ -661,7 +663,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     use_buf(L::NBUF == 2 ? (n & 1) : 0);
     if constexpr (L::NBUF == 2) {
       if (n + 1 < dm.NT) commit(S, (n + 1) & 1);
-      prefetch(S, min(n + 3, last));
+      prefetch(S, min(n + 1 + PD, last));
     }
       if (save) unstage_rows<T, VT, K, NTHR>(ck.hT + bhn * V * K + (size_t)v0 * K, K, sHt, L::LK);
 
@@ -755,18 +757,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     if constexpr (L::NBUF == 1) {
       if (n + 1 < dm.NT) commit(S, 0);
-      prefetch(S, min(n + 3, last));
+      prefetch(S, min(n + 1 + PD, last));
     }
     __syncthreads();
   };
   // both steps of a pair run on every trip (no path skips the second set's
   // loads); an odd last chunk runs after the loop
   int n = 0;
-  for (; n + 1 < dm.NT; n += 2) {
-    chunk_step(n, s0);
-    chunk_step(n + 1, s1);
+  if constexpr (PD == 2) {
+    for (; n + 1 < dm.NT; n += 2) {
+      chunk_step(n, s0);
+      chunk_step(n + 1, s1);
+    }
+    if (n < dm.NT) chunk_step(n, s0);
+  } else {
+    for (; n < dm.NT; ++n) chunk_step(n, s0);
   }
-  if (n < dm.NT) chunk_step(n, s0);
   if (h_final) {
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {

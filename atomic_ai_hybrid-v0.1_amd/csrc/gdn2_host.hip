@@ -192,6 +192,14 @@ static int gdn2_state_launch(const Gdn2Plan& p, const Gdn2Chunks<T>& ck, const f
     }
   }
   const unsigned nwg = (unsigned)(bh * (V / VT));
+  // bf16 at K = 128: sixteen waves with one prefetch set (measured 3-5 %
+  // faster than eight waves with two; the same tiles, so the same bits)
+  if constexpr (sizeof(T) == 2 && K == 128) {
+    return L("gdn2_fwd_state", [&] {
+      hipLaunchKernelGGL((gdn2_fwd_state<T, C, K, V, VT, 16, 1>), dim3(nwg), dim3(1024), 0, st, p.dm, ck, h0, o,
+                         h_final, mode);
+    });
+  }
   return L("gdn2_fwd_state", [&] {
     hipLaunchKernelGGL((gdn2_fwd_state<T, C, K, V, VT>), dim3(nwg), dim3(512), 0, st, p.dm, ck, h0, o,
                        h_final, mode);
