@@ -14,7 +14,7 @@
 //                    factorised on 16-row blocks (below); slices outside the
 //                    factorisation's bounds are evaluated pairwise with the
 //                    reference's clip masks.
-// mamba2_bwd_bc      one workgroup per (batch, chunk, 32 state columns):
+// mamba2_bwd_bc      one workgroup per (batch, chunk, 64 state columns):
 //                    dC = dC_1 + dCB B and dB = dB_1 + dCB^T C (:127,135,
 //                    :154-156,191-192) with dC_1 = Ydh . state_prev and
 //                    dB_1 = W . dstate contracted over (head, channel).
@@ -622,12 +622,15 @@ template <typename T, int C, int NTL, int KB>
 struct BcLds {
   static constexpr int PAD = Pad<T>::v;
   static constexpr int LCB = C + PAD, LK = NTL + PAD;
+  // the k loop's blocks, then (the same bytes) the epilogue's operands
   static constexpr int off_s = 0;                                   // state_prev rows [KB][NTL]
   static constexpr int off_d = off_s + KB * LK * (int)sizeof(T);    // dstate rows [KB][NTL]
-  static constexpr int off_cb = off_d + KB * LK * (int)sizeof(T);   // dCB [C][C]
+  static constexpr int end_loop = off_d + KB * LK * (int)sizeof(T);
+  static constexpr int off_cb = 0;                                  // dCB [C][C]
   static constexpr int off_b = off_cb + C * LCB * (int)sizeof(T);   // B [C][NTL]
   static constexpr int off_c = off_b + C * LK * (int)sizeof(T);     // C [C][NTL]
-  static constexpr int total = off_c + C * LK * (int)sizeof(T);
+  static constexpr int end_epi = off_c + C * LK * (int)sizeof(T);
+  static constexpr int total = end_loop > end_epi ? end_loop : end_epi;
 };
 
 // One workgroup per (batch, chunk, NTL state columns):
@@ -636,14 +639,19 @@ struct BcLds {
 // [B][T][H][P] rows of the chunk, state_prev / dstate the [NT][H][P][N] block.
 // The first H workgroups also reduce dA (the dA partials of the chunk
 // backward are complete when this kernel starts).  Eight waves, four per SIMD
-// with two workgroups on a CU, so many k blocks' loads are in flight at once.
-template <typename T, int C, int P, int N>
+// with two workgroups on a CU, so many k blocks' loads are in flight at once;
+// PD k blocks are staged ahead in registers.  The dCB / B / C operands of the
+// epilogue are staged after the k loop into the same LDS bytes, which keeps
+// two 64-column workgroups per CU (64 columns read each chunk's Ydh / W rows
+// half as often as 32).
+template <typename T, int C, int P, int N, int NTL = 64, int PD = 1>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void mamba2_bwd_bc(
     Mamba2Dims dm, int G, const T* __restrict__ Bm, const T* __restrict__ Cm, Mamba2Chunks<T> ck,
     Mamba2Grads<T> gr, T* __restrict__ dB, T* __restrict__ dC, float* __restrict__ dA) {
   constexpr int NTH = 512, NW = NTH / 64;
-  constexpr int NTL = 32, KB = 64, NNT = N / NTL;
+  constexpr int KB = 64, NNT = N / NTL;
   static_assert(P % KB == 0, "whole k blocks per head");
+  static_assert(N % NTL == 0, "whole column blocks");
   typedef BcLds<T, C, NTL, KB> L;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
   T* sS = reinterpret_cast<T*>(lds + L::off_s);
@@ -694,8 +702,42 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   };
   Stage s0, s1;
   load(s0, 0);
+  if (PD == 2 && KB < HP) load(s1, KB);
+
+  // one k block: its staged rows to LDS, the stage refilled two blocks ahead,
+  // then the MFMAs on the fragments kept from the stage
+  auto step = [&](Stage& st, int kb) {
+    frag ay[KK], aw[KK];
+#pragma unroll
+    for (int q = 0; q < KK; ++q) { ay[q] = st.ay[q]; aw[q] = st.aw[q]; }
+    __syncthreads();  // previous block's reads done
+    st.ps.store(sS, L::LK);
+    st.pd.store(sD, L::LK);
+    if (kb + PD * KB < HP) load(st, kb + PD * KB);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < KK; ++q) {
+      const int kk = q * Mma<T>::KS;
+#pragma unroll
+      for (int u = 0; u < TPW; ++u) {
+        const int ct = ct0 + u;
+        accC[u] = Mma<T>::mma(ay[q], Mma<T>::ld_t(sS, L::LK, 16 * ct, kk), accC[u]);
+        accB[u] = Mma<T>::mma(aw[q], Mma<T>::ld_t(sD, L::LK, 16 * ct, kk), accB[u]);
+      }
+    }
+  };
+  if constexpr (PD == 2) {
+    for (int kb = 0; kb < HP; kb += 2 * KB) {
+      step(s0, kb);
+      if (kb + KB < HP) step(s1, kb + KB);
+    }
+  } else {
+    for (int kb = 0; kb < HP; kb += KB) step(s0, kb);
+  }
+
+  // the epilogue's operands, into the bytes of the k loop's blocks:
   // dCB = the sum of the head-group partials (lower triangle), 4 columns per
-  // item; one group's loads of all this thread's items are in flight together
+  // item (requested before the barrier), and the chunk's B / C rows
   const float* part = gr.part + (size_t)bn * G * C * C;
   constexpr int E4 = C * C / 4 / NTH;
   static_assert(E4 * NTH * 4 == C * C, "whole items per thread");
@@ -710,6 +752,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 #pragma unroll
     for (int t = 0; t < E4; ++t) cbs[t] += v[t];
   }
+  __syncthreads();  // the last k block's reads are done
 #pragma unroll
   for (int t = 0; t < E4; ++t) {
     const int e4 = threadIdx.x + NTH * t, i = (4 * e4) / C, j = (4 * e4) % C;
@@ -718,36 +761,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     for (int c = 0; c < 4; ++c) sv[c] = j + c <= i ? cbs[t][c] : 0.f;
     store4(sCB + i * L::LCB + j, sv);
   }
-  if (KB < HP) load(s1, KB);
   stage_rows<T, C, NTL, NTH>(sB, L::LK, Bm + row0 * dm.rB + n0, dm.rB);
   stage_rows<T, C, NTL, NTH>(sC, L::LK, Cm + row0 * dm.rC + n0, dm.rC);
-
-  // one k block: its staged rows to LDS, the stage refilled two blocks ahead,
-  // then the MFMAs on the fragments kept from the stage
-  auto step = [&](Stage& st, int kb) {
-    frag ay[KK], aw[KK];
-#pragma unroll
-    for (int q = 0; q < KK; ++q) { ay[q] = st.ay[q]; aw[q] = st.aw[q]; }
-    __syncthreads();  // previous block's reads done
-    st.ps.store(sS, L::LK);
-    st.pd.store(sD, L::LK);
-    if (kb + 2 * KB < HP) load(st, kb + 2 * KB);
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < KK; ++q) {
-      const int kk = q * Mma<T>::KS;
-#pragma unroll
-      for (int u = 0; u < TPW; ++u) {
-        const int ct = ct0 + u;
-        accC[u] = Mma<T>::mma(ay[q], Mma<T>::ld_t(sS, L::LK, 16 * ct, kk), accC[u]);
-        accB[u] = Mma<T>::mma(aw[q], Mma<T>::ld_t(sD, L::LK, 16 * ct, kk), accB[u]);
-      }
-    }
-  };
-  for (int kb = 0; kb < HP; kb += 2 * KB) {
-    step(s0, kb);
-    if (kb + KB < HP) step(s1, kb + KB);
-  }
+  __syncthreads();
   T* dCo = dC + row0 * N + n0;
   T* dBo = dB + row0 * N + n0;
 #pragma unroll

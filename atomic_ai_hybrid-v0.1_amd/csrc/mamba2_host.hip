@@ -224,7 +224,8 @@ static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x,
   });
   if (rc) return rc;
   rc = L("mamba2_bwd_bc", [&] {
-    hipLaunchKernelGGL((mamba2_bwd_bc<T, C, P, N>), dim3((unsigned)(d.B * d.NT * (N / 32))), dim3(512),
+    constexpr int NTL = 64;  // state columns per workgroup
+    hipLaunchKernelGGL((mamba2_bwd_bc<T, C, P, N, NTL>), dim3((unsigned)(d.B * d.NT * (N / NTL))), dim3(512),
                        0, st, d, p.G, (const T*)Bm, (const T*)Cm, ck, gr, (T*)dB, (T*)dC, dA);
   });
   return rc;
