@@ -39,16 +39,22 @@ template <typename T, int C, int K, int V, int VT>
 struct DhLds {
   static constexpr int PAD = Pad<T>::v;
   static constexpr int LK = K + PAD, LC = C + PAD, LD = VT + PAD;
-  static constexpr int off_w = 0;
-  static constexpr int off_q = off_w + C * LK * (int)sizeof(T);
-  static constexpr int off_kg = off_q + C * LK * (int)sizeof(T);
-  static constexpr int off_aqk = off_kg + C * LK * (int)sizeof(T);
-  static constexpr int off_do = off_aqk + C * LC * (int)sizeof(T);
-  static constexpr int off_dos = off_do + C * LD * (int)sizeof(T);
-  static constexpr int off_dht = off_dos + C * LD * (int)sizeof(T);
+  // one chunk's staged operands (offsets within a stage buffer)
+  static constexpr int s_w = 0;
+  static constexpr int s_q = s_w + C * LK * (int)sizeof(T);
+  static constexpr int s_kg = s_q + C * LK * (int)sizeof(T);
+  static constexpr int s_aqk = s_kg + C * LK * (int)sizeof(T);
+  static constexpr int s_do = s_aqk + C * LC * (int)sizeof(T);
+  static constexpr int s_dos = s_do + C * LD * (int)sizeof(T);
+  static constexpr int s_gl = s_dos + C * LD * (int)sizeof(T);
+  static constexpr int SB = (s_gl + K * 4 + 15) / 16 * 16;
+  static constexpr int REST = VT * LK * (int)sizeof(T) + VT * LC * (int)sizeof(T);
+  // two stage buffers when they fit: chunk n - 1 is written while chunk n
+  // computes, which also saves a barrier per chunk
+  static constexpr int NBUF = 2 * SB + REST <= 160 * 1024 ? 2 : 1;
+  static constexpr int off_dht = NBUF * SB;
   static constexpr int off_dvt = off_dht + VT * LK * (int)sizeof(T);
-  static constexpr int off_gl = off_dvt + VT * LC * (int)sizeof(T);
-  static constexpr int total = off_gl + K * 4;
+  static constexpr int total = off_dvt + VT * LC * (int)sizeof(T);
 };
 
 // Eight waves (two per SIMD): the dh tiles and the dv_new tiles of one V
@@ -59,15 +65,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const float* __restrict__ dh_final, float* __restrict__ dh0) {
   typedef DhLds<T, C, K, V, VT> L;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
-  T* sW = reinterpret_cast<T*>(lds + L::off_w);
-  T* sQ = reinterpret_cast<T*>(lds + L::off_q);
-  T* sKg = reinterpret_cast<T*>(lds + L::off_kg);
-  T* sAqk = reinterpret_cast<T*>(lds + L::off_aqk);
-  T* sDO = reinterpret_cast<T*>(lds + L::off_do);
-  T* sDOs = reinterpret_cast<T*>(lds + L::off_dos);
   T* sDht = reinterpret_cast<T*>(lds + L::off_dht);
   T* sDvT = reinterpret_cast<T*>(lds + L::off_dvt);
-  float* sGl = reinterpret_cast<float*>(lds + L::off_gl);
+  // the stage buffer the current chunk reads
+  T *sW, *sQ, *sKg, *sAqk, *sDO, *sDOs;
+  float* sGl;
+  auto use_buf = [&](int bsel) {
+    unsigned char* bp = lds + bsel * L::SB;
+    sW = reinterpret_cast<T*>(bp + L::s_w);
+    sQ = reinterpret_cast<T*>(bp + L::s_q);
+    sKg = reinterpret_cast<T*>(bp + L::s_kg);
+    sAqk = reinterpret_cast<T*>(bp + L::s_aqk);
+    sDO = reinterpret_cast<T*>(bp + L::s_do);
+    sDOs = reinterpret_cast<T*>(bp + L::s_dos);
+    sGl = reinterpret_cast<float*>(bp + L::s_gl);
+  };
 
   constexpr int NVT = V / VT;
   int bh, vt;
@@ -120,12 +132,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     S.g.load(ck.gcl + bhn * K, K);
     S.o.load(dO + ((size_t)bb * dm.T + (size_t)n * C) * ldo + (size_t)h * V + v0, ldo);
   };
-  auto commit = [&](const Stage& S) {
-    S.w.store(sW, L::LK);
-    S.q.store(sQ, L::LK);
-    S.k.store(sKg, L::LK);
-    S.a.store(sAqk, L::LC);
-    S.g.store(sGl, K);
+  auto commit = [&](const Stage& S, int bsel) {
+    unsigned char* bp = lds + bsel * L::SB;
+    T* dW = reinterpret_cast<T*>(bp + L::s_w);
+    T* dDO = reinterpret_cast<T*>(bp + L::s_do);
+    T* dDOs = reinterpret_cast<T*>(bp + L::s_dos);
+    S.w.store(dW, L::LK);
+    S.q.store(reinterpret_cast<T*>(bp + L::s_q), L::LK);
+    S.k.store(reinterpret_cast<T*>(bp + L::s_kg), L::LK);
+    S.a.store(reinterpret_cast<T*>(bp + L::s_aqk), L::LC);
+    S.g.store(reinterpret_cast<float*>(bp + L::s_gl), K);
     // dO and scale dO in the operand dtype
     typedef RegStage<TD, C, VT, NTHR> RO;
 #pragma unroll
@@ -138,8 +154,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int j = 0; j < RO::VEC; ++j) {
           const float x = to_f(v[j]);
-          sDO[r * L::LD + c + j] = from_f<T>(x);
-          sDOs[r * L::LD + c + j] = from_f<T>(x * dm.scale);
+          dDO[r * L::LD + c + j] = from_f<T>(x);
+          dDOs[r * L::LD + c + j] = from_f<T>(x * dm.scale);
         }
       }
     }
@@ -148,16 +164,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // 0, whose registers are never committed): the wait counter before a
   // commit then always has the other set's loads behind it, so the commit
   // waits for its own set only and the two-deep prefetch holds.
+  auto buf_of = [](int n) { return L::NBUF == 2 ? (n & 1) : 0; };
   Stage s0, s1;
   prefetch(s0, dm.NT - 1);
-  commit(s0);
+  commit(s0, buf_of(dm.NT - 1));
   __syncthreads();
   prefetch(s0, max(dm.NT - 2, 0));
   prefetch(s1, max(dm.NT - 3, 0));
 
-  // one chunk step (reverse); S holds chunk n - 1 on entry and is refilled with chunk n - 3
+  // one chunk step (reverse); S holds chunk n - 1 on entry and is refilled with chunk n - 3.
+  // Two stage buffers: chunk n - 1 goes into the other buffer at the start (its
+  // last readers finished before the previous step's final barrier), and two
+  // barriers are left per step (after dv_new, after the new dh).
   auto chunk_step = [&](int n, Stage& S) {
     const size_t bhn = (size_t)bh * dm.NT + n;
+    use_buf(buf_of(n));
+    if constexpr (L::NBUF == 2) {
+      if (n > 0) commit(S, buf_of(n - 1));
+      prefetch(S, max(n - 3, 0));
+    }
       // dh_next of chunk n = the carry entering this step
       unstage_rows<T, VT, K, NTHR>(gr.dhT + bhn * V * K + (size_t)v0 * K, K, sDht, L::LK);
 
@@ -205,14 +230,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           hs[gi * GT + u] = acc[u];
         }
       }
-      __syncthreads();
+      // sDht was last read by this step's dv_new, before the dv_new barrier;
+      // with one stage buffer the commit below overwrites what dh just read
+      if constexpr (L::NBUF == 1) __syncthreads();
   #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int tile = wv_id * TPW + t, mi = tile / NTI, ni = tile % NTI;
         store_tile_t(sDht, L::LK, 16 * mi, 16 * ni, hs[t]);
       }
-    if (n > 0) commit(S);
-    prefetch(S, max(n - 3, 0));
+    if constexpr (L::NBUF == 1) {
+      if (n > 0) commit(S, 0);
+      prefetch(S, max(n - 3, 0));
+    }
     __syncthreads();
   };
   // both steps of a pair run on every trip (no path skips the second set's
