@@ -157,7 +157,7 @@ def mamba2_kernel_model(B, T, H, P, N, C, es=2):
     }
 
 
-# ------------------------------------------------- path-level bytes and flops
+# ------------------------------------------------- path-level algorithmic bytes and flops
 def survey_path_model(g, m):
     """Algorithmic HBM bytes and flops per step of each path, from the
     per-token-head (bytes) and per-chunk-head (GDN2 flops) figures the

@@ -1,8 +1,8 @@
 """Per-stage reports (the args structs' `diag`; the reference's opt-in
 GDN2_FWD_DIAG stage check, kernel_d_pipeline.py:50-91) on the GPU, and the
-clip / nan_to_num placement on inputs that make it fire (SURVEY's failure
-handling: NaN, +-inf and beyond-1e4 inputs return the reference's
-sanitised values).
+clip / nan_to_num placement on inputs that make it fire (the reference's
+failure handling: NaN, +-inf and beyond-1e4 inputs return its sanitised
+values).
 
 Each report must equal the non-finite count and max |x| of the same stage
 in the float64 oracle: the GDN2 stages of gdn2_wy_reference.py:59-152 and the
