@@ -125,12 +125,19 @@ static int mamba2_forward_impl(const Mamba2Plan& p, const void* dt, const void* 
                        (const T*)Bm, (const T*)Cm, ck);
   });
   if (rc) return rc;
+  // chunk_outer workgroups take 8 (head, channel slice) pairs of one chunk,
+  // 4 when 8 would leave fewer than two workgroups per CU (0.045 -> 0.039 ms
+  // at B2 T4096 H32 P64), else one head's slices; the backward likewise
   rc = L("mamba2_chunk_state", [&] {
     constexpr int NPO = P / kOuterPT;
     const size_t pairs = (size_t)d.H * NPO;
     if (pairs % 8 == 0 && d.B * d.NT * pairs / 8 >= kFullGrid)
       hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, 8>),
                          dim3((unsigned)(d.B * d.NT * pairs / 8)), dim3(256), 0, st, d, (const T*)dt,
+                         (const T*)x, A, (const T*)Bm, (const T*)nullptr, ck, (T*)nullptr, (T*)nullptr);
+    else if (pairs % 4 == 0 && d.B * d.NT * pairs / 4 >= kFullGrid)
+      hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, 4>),
+                         dim3((unsigned)(d.B * d.NT * pairs / 4)), dim3(256), 0, st, d, (const T*)dt,
                          (const T*)x, A, (const T*)Bm, (const T*)nullptr, ck, (T*)nullptr, (T*)nullptr);
     else
       hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, NPO>),
@@ -145,13 +152,16 @@ static int mamba2_forward_impl(const Mamba2Plan& p, const void* dt, const void* 
   if (rc || !y) return rc;
   // chunk_y workgroups take SL (head, channel slice) pairs of one chunk: 16
   // when they divide the pairs and the grid still holds two workgroups per
-  // CU, else 4 (small batches: 0.093 -> 0.070 ms at B2 T4096 H32 P64), else
-  // the channel slices of one head
+  // CU, else 8 under the same condition, else 4 (small batches: 0.093 ->
+  // 0.066 ms at B2 T4096 H32 P64), else the channel slices of one head
   constexpr int NPT = P / kYPT;
   const size_t pairs = (size_t)d.H * NPT;
   return L("mamba2_chunk_y", [&] {
     if (pairs % 16 == 0 && d.B * d.NT * pairs / 16 >= kFullGrid)
       hipLaunchKernelGGL((mamba2_chunk_y<T, C, P, N, kYPT, 16>), dim3((unsigned)(d.B * d.NT * pairs / 16)),
+                         dim3(256), 0, st, d, (const T*)dt, (const T*)x, A, (const T*)Cm, ck, y);
+    else if (pairs % 8 == 0 && d.B * d.NT * pairs / 8 >= kFullGrid)
+      hipLaunchKernelGGL((mamba2_chunk_y<T, C, P, N, kYPT, 8>), dim3((unsigned)(d.B * d.NT * pairs / 8)),
                          dim3(256), 0, st, d, (const T*)dt, (const T*)x, A, (const T*)Cm, ck, y);
     else if (pairs % 4 == 0)
       hipLaunchKernelGGL((mamba2_chunk_y<T, C, P, N, kYPT, 4>), dim3((unsigned)(d.B * d.NT * pairs / 4)),
@@ -213,6 +223,10 @@ static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x,
     if (pairs % 8 == 0 && d.B * d.NT * pairs / 8 >= kFullGrid)
       hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true, 8>),
                          dim3((unsigned)(d.B * d.NT * pairs / 8)), dim3(256), 0, st, d, (const T*)dt,
+                         (const T*)x, A, (const T*)Cm, (const TD*)dy, ck, gr.ydh, gr.wr);
+    else if (pairs % 4 == 0 && d.B * d.NT * pairs / 4 >= kFullGrid)
+      hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true, 4>),
+                         dim3((unsigned)(d.B * d.NT * pairs / 4)), dim3(256), 0, st, d, (const T*)dt,
                          (const T*)x, A, (const T*)Cm, (const TD*)dy, ck, gr.ydh, gr.wr);
     else
       hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true, NPO>),
@@ -344,6 +358,9 @@ static int mamba2_intra_stage_impl(const Mamba2Plan& p, const void* dt, const vo
                        (const T*)Bm, (const T*)Cm, ck);
   });
   if (rc) return rc;
+  // chunk_outer workgroups take 8 (head, channel slice) pairs of one chunk,
+  // 4 when 8 would leave fewer than two workgroups per CU (0.045 -> 0.039 ms
+  // at B2 T4096 H32 P64), else one head's slices; the backward likewise
   rc = L("mamba2_chunk_state", [&] {
     constexpr int NPO = P / kOuterPT;
     const size_t pairs = (size_t)d.H * NPO;
