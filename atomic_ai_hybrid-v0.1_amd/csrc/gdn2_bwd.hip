@@ -58,8 +58,10 @@ struct DhLds {
 };
 
 // Eight waves (two per SIMD): the dh tiles and the dv_new tiles of one V
-// tile split over them by row blocks.
-template <typename T, typename TD, int C, int K, int V, int VT>
+// tile split over them by row blocks.  With DD, each step's dv_new tiles stay
+// in registers and are written by the next step between its commit and its
+// prefetch (faster with 16-column tiles).
+template <typename T, typename TD, int C, int K, int V, int VT, bool DD = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn2_bwd_dh(
     Gdn2Dims dm, Gdn2Chunks<T> ck, Gdn2Grads<T> gr, const TD* __restrict__ dO,
     const float* __restrict__ dh_final, float* __restrict__ dh0) {
@@ -165,6 +167,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // commit then always has the other set's loads behind it, so the commit
   // waits for its own set only and the two-deep prefetch holds.
   auto buf_of = [](int n) { return L::NBUF == 2 ? (n & 1) : 0; };
+  static_assert(!DD || L::NBUF == 2, "deferred dv_new stores follow the step-start commit");
+  f32x4 pdv[VPW];
+  T* pdvn = nullptr;
+  auto store_dv = [&](T* dvb) {
+  #pragma unroll
+    for (int gi = 0; gi < ((NTV >= NW || wv_id < NTV) ? VPW / GV : 0); ++gi) {
+      const int tile0 = wv_id * VPW + gi * GV, mj = tile0 / NTI, ni0 = tile0 % NTI;
+  #pragma unroll
+      for (int u = 0; u < GV; ++u) store_tile_n(dvb, V, 16 * mj, 16 * (ni0 + u), pdv[gi * GV + u]);
+    }
+  };
   Stage s0, s1;
   prefetch(s0, dm.NT - 1);
   commit(s0, buf_of(dm.NT - 1));
@@ -181,6 +194,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     use_buf(buf_of(n));
     if constexpr (L::NBUF == 2) {
       if (n > 0) commit(S, buf_of(n - 1));
+      if constexpr (DD) {
+        if (pdvn) store_dv(pdvn);
+        pdvn = nullptr;
+      }
       prefetch(S, max(n - 3, 0));
     }
       // dh_next of chunk n = the carry entering this step
@@ -202,12 +219,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           const int ni = ni0 + u;
   #pragma unroll
           for (int i = 0; i < 4; ++i) acc[u][i] = sanitize(acc[u][i]);
-          store_tile_n(gr.dvn + bhn * C * V + v0, V, 16 * mj, 16 * ni, acc[u]);
+          if constexpr (DD) pdv[gi * GV + u] = acc[u];
+          else store_tile_n(gr.dvn + bhn * C * V + v0, V, 16 * mj, 16 * ni, acc[u]);
   #pragma unroll
           for (int i = 0; i < 4; ++i) acc[u][i] = -acc[u][i];
           store_tile_t(sDvT, L::LC, 16 * mj, 16 * ni, acc[u]);
         }
       }
+      if constexpr (DD) pdvn = gr.dvn + bhn * C * V + v0;
       __syncthreads();
 
       // dh = sanitize(qg^T (scale dO) + dh e^{gc_last} - w_pseudo^T dv_new)   (b1:26-37)
@@ -252,6 +271,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     chunk_step(n - 1, s1);
   }
   if (n == 0) chunk_step(0, s0);
+  if constexpr (DD) {
+    if (pdvn) store_dv(pdvn);
+  }
   if (dh0) {
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {

@@ -556,10 +556,12 @@ struct StateLds {
 enum { kStateSave = 1, kStateChunkO = 2, kStateSanitizeH0 = 4 };
 
 // NW waves (NW / 4 per SIMD): the state tiles and the [w; q] h tiles of one
-// V tile split over them by row blocks.  PD register sets of chunk operands
+// V tile split over them by row blocks.  With DO, each step's o tiles stay in
+// registers and are written by the next step between its commit and its
+// prefetch (faster with 16-column tiles, slower with 32).  PD register sets of chunk operands
 // are in flight (two at eight waves; one at sixteen, where the other waves
 // hide the load latency and the VGPR budget is 128).
-template <typename T, int C, int K, int V, int VT, int NW = 8, int PD = 2>
+template <typename T, int C, int K, int V, int VT, int NW = 8, int PD = 2, bool DO = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4))) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T> ck,
                                                      const float* __restrict__ h0, float* __restrict__ o,
                                                      float* __restrict__ h_final, int mode) {
@@ -654,6 +656,28 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4,
   prefetch(s0, min(1, last));
   if constexpr (PD == 2) prefetch(s1, min(2, last));
 
+  const bool chunk_o = (mode & kStateChunkO) != 0;
+  const size_t ors = chunk_o ? (size_t)V : (size_t)dm.H * V;  // o's row stride
+  f32x4 po[XPW];
+  float* pog = nullptr;
+  // this wave's o tiles (rows of the qg half) at o's row base og
+  auto store_o = [&](float* og, const f32x4 (&ov)[XPW]) {
+#pragma unroll
+    for (int gi = 0; gi < XPW / GX; ++gi) {
+      const int tile0 = wv_id * XPW + gi * GX, mi = tile0 / NTI, ni0 = tile0 % NTI;
+      if (mi >= C / 16) {
+        const int mo = mi - C / 16;
+#pragma unroll
+        for (int u = 0; u < GX; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 16 * mo + tile_row(i), c = 16 * (ni0 + u) + tile_col();
+            og[(size_t)r * ors + c] = n2n(ov[gi * GX + u][i]);
+          }
+      }
+    }
+  };
+
   // One chunk step; S holds chunk n + 1 on entry and is refilled with chunk n + 3.
   // Two stage buffers: chunk n + 1 goes into the other buffer at the start (its
   // last readers finished before the previous step's final barrier), and only
@@ -663,6 +687,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4,
     use_buf(L::NBUF == 2 ? (n & 1) : 0);
     if constexpr (L::NBUF == 2) {
       if (n + 1 < dm.NT) commit(S, (n + 1) & 1);
+      if constexpr (DO) {
+        if (pog) store_o(pog, po);
+        pog = nullptr;
+      }
       prefetch(S, min(n + 1 + PD, last));
     }
       if (save) unstage_rows<T, VT, K, NTHR>(ck.hT + bhn * V * K + (size_t)v0 * K, K, sHt, L::LK);
@@ -699,11 +727,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4,
       if (save) unstage_rows<T, VT, C, NTHR>(ck.vnT + bhn * V * C + (size_t)v0 * C, C, sVn, L::LC);
 
       // o = scale qg h + Aqk v_new   (rows of the qg half)
-      const bool chunk_o = (mode & kStateChunkO) != 0;
       float* og = !o ? nullptr
                      : chunk_o ? o + (size_t)bhn * C * V + v0
                                : o + (((size_t)bb * dm.T + (size_t)n * C) * dm.H + h) * V + v0;
-      const size_t ors = chunk_o ? (size_t)V : (size_t)dm.H * V;  // o's row stride
   #pragma unroll
       for (int gi = 0; gi < XPW / GX; ++gi) {
         const int tile0 = wv_id * XPW + gi * GX, mi = tile0 / NTI, ni0 = tile0 % NTI;
@@ -716,7 +742,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4,
   #pragma unroll
           for (int u = 0; u < GX; ++u) acc[u] = xo[gi * GX + u];
           tile_mma_row<T, false, false, GX>(acc, sAqk, L::LC, sVn, L::LC, 16 * mo, 16 * ni0, kr);
-          if (og) {
+          if constexpr (DO) {
+  #pragma unroll
+            for (int u = 0; u < GX; ++u) po[gi * GX + u] = acc[u];
+          } else if (og) {
   #pragma unroll
             for (int u = 0; u < GX; ++u)
   #pragma unroll
@@ -727,6 +756,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4,
           }
         }
       }
+      if constexpr (DO) pog = og;
 
       // h = sanitize(h e^{gc_last} + kg^T v_new)
   #pragma unroll
@@ -772,6 +802,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4,
     if (n < dm.NT) chunk_step(n, s0);
   } else {
     for (; n < dm.NT; ++n) chunk_step(n, s0);
+  }
+  if constexpr (DO) {
+    if (pog) store_o(pog, po);
   }
   if (h_final) {
 #pragma unroll

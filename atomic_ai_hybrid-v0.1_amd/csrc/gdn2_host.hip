@@ -186,7 +186,7 @@ static int gdn2_state_launch(const Gdn2Plan& p, const Gdn2Chunks<T>& ck, const f
     constexpr int VT16 = 16;
     if (bh * (V / VT16) <= 256) {
       return L("gdn2_fwd_state", [&] {
-        hipLaunchKernelGGL((gdn2_fwd_state<T, C, K, V, VT16>), dim3((unsigned)(bh * (V / VT16))), dim3(512), 0,
+        hipLaunchKernelGGL((gdn2_fwd_state<T, C, K, V, VT16, 8, 2, true>), dim3((unsigned)(bh * (V / VT16))), dim3(512), 0,
                            st, p.dm, ck, h0, o, h_final, mode);
       });
     }
@@ -257,7 +257,7 @@ static int gdn2_backward_impl(const Gdn2Plan& p, const void* q, const void* k, c
   if (dh16) {
     if constexpr (sizeof(T) == 2 && K == 128) {
       rc = L("gdn2_bwd_dh", [&] {
-        hipLaunchKernelGGL((gdn2_bwd_dh<T, TD, C, K, V, 16>), dim3((unsigned)(bh * (V / 16))), dim3(512), 0, st,
+        hipLaunchKernelGGL((gdn2_bwd_dh<T, TD, C, K, V, 16, true>), dim3((unsigned)(bh * (V / 16))), dim3(512), 0, st,
                            p.dm, ck, gr, (const TD*)dO, dh_final, dh0);
       });
     }
