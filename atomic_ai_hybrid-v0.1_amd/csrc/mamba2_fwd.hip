@@ -49,21 +49,24 @@
 
 namespace ah {
 
-template <typename T, int C, int N>
+// One workgroup per (batch, chunk, RB-row block of CB): with RB < C a small
+// batch still spreads over the CUs.
+template <typename T, int C, int N, int RB = C>
 __global__ __launch_bounds__(256) void mamba2_cb(Mamba2Dims dm, const T* __restrict__ Bm,
                                                 const T* __restrict__ Cm, Mamba2Chunks<T> ck) {
-  constexpr int PAD = Pad<T>::v, LN = N + PAD;
+  constexpr int PAD = Pad<T>::v, LN = N + PAD, NRB = C / RB;
+  static_assert(C % RB == 0, "whole row blocks");
   __shared__ __attribute__((aligned(16))) T sB[C * LN];
-  __shared__ __attribute__((aligned(16))) T sC[C * LN];
-  const int bn = blockIdx.x;  // b * NT + n
+  __shared__ __attribute__((aligned(16))) T sC[RB * LN];
+  const int bn = blockIdx.x / NRB, rb = blockIdx.x % NRB;  // b * NT + n, row block
   const size_t row0 = (size_t)bn * C;  // rows of [B*T][N]
   stage_rows<T, C, N>(sB, LN, Bm + row0 * dm.rB, dm.rB);
-  stage_rows<T, C, N>(sC, LN, Cm + row0 * dm.rC, dm.rC);
+  stage_rows<T, RB, N>(sC, LN, Cm + (row0 + (size_t)rb * RB) * dm.rC, dm.rC);
   __syncthreads();
-  constexpr int MT = C / 16;
-  T* out = ck.cb + (size_t)bn * C * C;
-  for (int tile = wave_id(); tile < MT * MT; tile += 4) {
-    const int mi = tile / MT, nj = tile % MT;
+  constexpr int MT = RB / 16, NTT = C / 16;
+  T* out = ck.cb + (size_t)bn * C * C + (size_t)rb * RB * C;
+  for (int tile = wave_id(); tile < MT * NTT; tile += 4) {
+    const int mi = tile / NTT, nj = tile % NTT;
     f32x4 acc = tile_mma<T, false, false>(zero4(), sC, LN, sB, LN, 16 * mi, 16 * nj, N);
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = sanitize(acc[i]);

@@ -121,8 +121,14 @@ static int mamba2_forward_impl(const Mamba2Plan& p, const void* dt, const void* 
   Mamba2Chunks<T> ck = mamba2_chunks<T>(p, ws);
   hipStream_t st = L.st;
   int rc = L("mamba2_cb", [&] {
-    hipLaunchKernelGGL((mamba2_cb<T, C, N>), dim3((unsigned)(d.B * d.NT)), dim3(256), 0, st, d,
-                       (const T*)Bm, (const T*)Cm, ck);
+    // one workgroup per chunk, or per 32-row block when the chunks are fewer
+    // than the CUs (B2 T4096: 0.011 -> 0.007 ms)
+    if (d.B * d.NT >= 256)
+      hipLaunchKernelGGL((mamba2_cb<T, C, N>), dim3((unsigned)(d.B * d.NT)), dim3(256), 0, st, d,
+                         (const T*)Bm, (const T*)Cm, ck);
+    else
+      hipLaunchKernelGGL((mamba2_cb<T, C, N, 32>), dim3((unsigned)(d.B * d.NT * (C / 32))), dim3(256), 0, st,
+                         d, (const T*)Bm, (const T*)Cm, ck);
   });
   if (rc) return rc;
   // chunk_outer workgroups take 8 (head, channel slice) pairs of one chunk,
@@ -354,8 +360,14 @@ static int mamba2_intra_stage_impl(const Mamba2Plan& p, const void* dt, const vo
   ck.cum = cum;
   hipStream_t st = L.st;
   int rc = L("mamba2_cb", [&] {
-    hipLaunchKernelGGL((mamba2_cb<T, C, N>), dim3((unsigned)(d.B * d.NT)), dim3(256), 0, st, d,
-                       (const T*)Bm, (const T*)Cm, ck);
+    // one workgroup per chunk, or per 32-row block when the chunks are fewer
+    // than the CUs (B2 T4096: 0.011 -> 0.007 ms)
+    if (d.B * d.NT >= 256)
+      hipLaunchKernelGGL((mamba2_cb<T, C, N>), dim3((unsigned)(d.B * d.NT)), dim3(256), 0, st, d,
+                         (const T*)Bm, (const T*)Cm, ck);
+    else
+      hipLaunchKernelGGL((mamba2_cb<T, C, N, 32>), dim3((unsigned)(d.B * d.NT * (C / 32))), dim3(256), 0, st,
+                         d, (const T*)Bm, (const T*)Cm, ck);
   });
   if (rc) return rc;
   // chunk_outer workgroups take 8 (head, channel slice) pairs of one chunk,
