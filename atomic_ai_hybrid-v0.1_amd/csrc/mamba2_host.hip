@@ -370,9 +370,7 @@ static int mamba2_intra_stage_impl(const Mamba2Plan& p, const void* dt, const vo
                          d, (const T*)Bm, (const T*)Cm, ck);
   });
   if (rc) return rc;
-  // chunk_outer workgroups take 8 (head, channel slice) pairs of one chunk,
-  // 4 when 8 would leave fewer than two workgroups per CU (0.045 -> 0.039 ms
-  // at B2 T4096 H32 P64), else one head's slices; the backward likewise
+  // 8 pairs per workgroup, or one head's slices on grids under two per CU
   rc = L("mamba2_chunk_state", [&] {
     constexpr int NPO = P / kOuterPT;
     const size_t pairs = (size_t)d.H * NPO;
