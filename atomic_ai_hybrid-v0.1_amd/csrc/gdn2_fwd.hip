@@ -556,11 +556,11 @@ struct StateLds {
 enum { kStateSave = 1, kStateChunkO = 2, kStateSanitizeH0 = 4 };
 
 // NW waves (NW / 4 per SIMD): the state tiles and the [w; q] h tiles of one
-// V tile split over them by row blocks.  With DO, each step's o tiles stay in
-// registers and are written by the next step between its commit and its
-// prefetch (faster with 16-column tiles, slower with 32).  PD register sets of chunk operands
+// V tile split over them by row blocks.  PD register sets of chunk operands
 // are in flight (two at eight waves; one at sixteen, where the other waves
-// hide the load latency and the VGPR budget is 128).
+// hide the load latency and the VGPR budget is 128).  With DO, each step's o
+// tiles stay in registers and are written by the next step between its
+// commit and its prefetch (faster with 16-column tiles, slower with 32).
 template <typename T, int C, int K, int V, int VT, int NW = 8, int PD = 2, bool DO = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4))) void gdn2_fwd_state(Gdn2Dims dm, Gdn2Chunks<T> ck,
                                                      const float* __restrict__ h0, float* __restrict__ o,
@@ -658,6 +658,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4,
 
   const bool chunk_o = (mode & kStateChunkO) != 0;
   const size_t ors = chunk_o ? (size_t)V : (size_t)dm.H * V;  // o's row stride
+  static_assert(!DO || L::NBUF == 2, "deferred o stores follow the step-start commit");
   f32x4 po[XPW];
   float* pog = nullptr;
   // this wave's o tiles (rows of the qg half) at o's row base og
