@@ -263,7 +263,8 @@ static int gdn2_backward_impl(const Gdn2Plan& p, const void* q, const void* k, c
     }
   } else {
     rc = L("gdn2_bwd_dh", [&] {
-      hipLaunchKernelGGL((gdn2_bwd_dh<T, TD, C, K, V, VT>), dim3((unsigned)(bh * (V / VT))), dim3(512), 0, st,
+      hipLaunchKernelGGL((gdn2_bwd_dh<T, TD, C, K, V, VT, sizeof(T) == 2>), dim3((unsigned)(bh * (V / VT))),
+                         dim3(512), 0, st,
                          p.dm, ck, gr, (const TD*)dO, dh_final, dh0);
     });
   }
