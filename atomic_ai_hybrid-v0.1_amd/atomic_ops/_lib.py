@@ -25,7 +25,8 @@ ERRORS = {
     -7: "ATOMIC_ERR_REUSE: the workspace does not hold the matching forward (REUSE)",
 }
 ATOMIC_F32, ATOMIC_BF16 = 0, 1
-GDN2_SAVE, GDN2_REUSE = 1, 2
+GDN2_SAVE, GDN2_REUSE, GDN2_SANITIZE_H0 = 1, 2, 4
+ATOMIC_ERR_REUSE = -7
 
 
 class Gdn2Args(ctypes.Structure):
@@ -136,7 +137,12 @@ class KernelTimer:
 
 
 class AtomicError(RuntimeError):
-    pass
+    """A negative status of the C ABI; ``code`` holds it (None for errors
+    raised by the Python layer itself)."""
+
+    def __init__(self, msg, code=None):
+        super().__init__(msg)
+        self.code = code
 
 
 # Stage names of the args structs' `diag` reports, in the header's order
@@ -255,4 +261,4 @@ def load():
 
 def check(rc, what):
     if rc != ATOMIC_OK:
-        raise AtomicError(f"{what}: {ERRORS.get(rc, rc)}")
+        raise AtomicError(f"{what}: {ERRORS.get(rc, rc)}", rc)

@@ -89,16 +89,19 @@ def workspace_layout(args):
 
 
 def forward(q, k, v, w, b, g, scale, h0=None, *, save=False, workspace=None, chunk=CHUNK, timer=None,
-            diag=None):
+            diag=None, sanitize_h0=False):
     """Returns ``(o, h_final, workspace)``.  With ``save`` the workspace keeps
     the per-chunk intermediates for :func:`backward`.  ``diag`` (an
     ``_lib.StageReports`` over ``_lib.GDN2_DIAG_STAGES``) receives the
-    forward's per-stage reports."""
+    forward's per-stage reports.  ``sanitize_h0`` clips h0 to +-1e4 and
+    nan_to_nums it first, as the reference's staged forward does
+    (kernel_d_pipeline.py:54-55,101)."""
     _check_inputs(q, k, v, w, b, g)
     lib = _lib.load()
     B, T, H, K = q.shape
     V = v.shape[-1]
-    args = make_args(q, v, scale, flags=_lib.GDN2_SAVE if save else 0, chunk=chunk)
+    flags = (_lib.GDN2_SAVE if save else 0) | (_lib.GDN2_SANITIZE_H0 if sanitize_h0 else 0)
+    args = make_args(q, v, scale, flags=flags, chunk=chunk)
     q, k, v, w, b, g = _rows_of(args, (q, k, v, w, b, g))
     if timer is not None:
         args.profile = timer.arm()
@@ -145,13 +148,13 @@ def forward_noalloc(q, k, v, w, b, g, scale, h0=None, *, o=None, h_final=None, c
 
 
 def backward(q, k, v, w, b, g, scale, dO, dh_final=None, h0=None, *, workspace=None, reuse=False,
-             chunk=CHUNK, timer=None, diag=None):
+             chunk=CHUNK, timer=None, diag=None, sanitize_h0=False):
     """Gradients ``(dq, dk, dv, dw, db, dg, dh0)`` in the primals' dtypes
     (dg and dh0 float32).  ``reuse`` declares that ``workspace`` holds the
     intermediates of a ``forward(..., save=True)`` on the same inputs; the
     library checks that by the input addresses and row strides, so an input
     that has to be copied here (see ``rows``, or h0 not float32) turns reuse
-    into a recompute."""
+    into a recompute.  ``sanitize_h0`` must match the forward's."""
     _check_inputs(q, k, v, w, b, g)
     lib = _lib.load()
     if dO.dtype not in _DT:
@@ -162,7 +165,7 @@ def backward(q, k, v, w, b, g, scale, dO, dh_final=None, h0=None, *, workspace=N
     if any(x is not y for x, y in zip((q, k, v, w, b, g), seen)) or \
             (h0 is not None and (h0.dtype != torch.float32 or not h0.is_contiguous())):
         reuse = False
-    args.flags = _lib.GDN2_REUSE if reuse else 0
+    args.flags = (_lib.GDN2_REUSE if reuse else 0) | (_lib.GDN2_SANITIZE_H0 if sanitize_h0 else 0)
     if timer is not None:
         args.profile = timer.arm()
     if diag is not None:

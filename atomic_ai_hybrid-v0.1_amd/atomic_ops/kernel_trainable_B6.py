@@ -5,7 +5,9 @@ reference signature and argument order (kernel_trainable_B6.py:187-194) and
 returns ``(o, h_final)``; its backward returns ``(dq, dk, dv, dw, db, dg, dh0)``
 cast to the primals' dtypes after the final clip(+-1e4) / nan_to_num
 (kernel_trainable_B6.py:173-181).  ``scale`` is not differentiable
-(kernel_trainable_B6.py:86).  Forward and backward run in libatomic_hybrid.so;
+(kernel_trainable_B6.py:86).  h0 is clipped to +-1e4 and nan_to_num'd before
+the first chunk, as in the reference's forward (kernel_d_pipeline.py:54-55);
+dh0 is the gradient at the sanitised h0.  Forward and backward run in libatomic_hybrid.so;
 the forward keeps its per-chunk intermediates for the backward instead of
 recomputing them (the reference recomputes; both give the same gradient).
 """
@@ -28,10 +30,12 @@ _GDN2_FWD_DIAG = os.environ.get("GDN2_FWD_DIAG", "0") == "1"
 
 
 def _forward(q, k, v, w, b, g, scale, h0, save, debug_tag=""):
+    # h0 is sanitised first, as the reference's staged forward does
+    # (gdn2_pallas_forward -> gdn2_inter_chunk_combine, kernel_d_pipeline.py:54-55,101)
     if not _GDN2_FWD_DIAG:
-        return _g.forward(q, k, v, w, b, g, scale, h0, save=save)
+        return _g.forward(q, k, v, w, b, g, scale, h0, save=save, sanitize_h0=True)
     rep = _lib.StageReports(_lib.GDN2_DIAG_STAGES, q.device)
-    out = _g.forward(q, k, v, w, b, g, scale, h0, save=save, diag=rep)
+    out = _g.forward(q, k, v, w, b, g, scale, h0, save=save, diag=rep, sanitize_h0=True)
     for line in rep.messages(debug_tag, 0, _lib.GDN2_DIAG_FWD):
         print(line, file=sys.stderr, flush=True)
     return out
@@ -62,8 +66,17 @@ class _Gdn2Core(torch.autograd.Function):
         # them; a further backward (retain_graph) recomputes the forward into
         # a fresh workspace instead of reading one that holds nothing.
         ws, ctx.ws = ctx.ws, None
-        grads = _g.backward(q, k, v, w, b, g, ctx.scale, do, dh_final=dh_final, h0=h0,
-                            workspace=ws, reuse=ws is not None)
+        try:
+            grads = _g.backward(q, k, v, w, b, g, ctx.scale, do, dh_final=dh_final, h0=h0,
+                                workspace=ws, reuse=ws is not None, sanitize_h0=True)
+        except _lib.AtomicError as e:
+            if e.code != _lib.ATOMIC_ERR_REUSE:
+                raise
+            # the library no longer holds the record of the saving forward
+            # (e.g. evicted): recompute it into the same workspace instead,
+            # which gives the same gradients
+            grads = _g.backward(q, k, v, w, b, g, ctx.scale, do, dh_final=dh_final, h0=h0,
+                                workspace=ws, reuse=False, sanitize_h0=True)
         dq, dk, dv, dw, db, dg, dh0 = grads
         return dq, dk, dv, dw, db, dg, None, dh0.to(ctx.h0_dtype)
 

@@ -14,7 +14,7 @@ import torch
 from . import _lib
 
 _DT = {torch.float32: _lib.ATOMIC_F32, torch.bfloat16: _lib.ATOMIC_BF16}
-M2_SAVE, M2_REUSE = 1, 2
+M2_SAVE, M2_REUSE, M2_SANITIZE_STATE0 = 1, 2, 4
 
 
 def _ptr(t):
@@ -65,15 +65,18 @@ def workspace_bytes(args):
 
 
 def forward(dt, x, Bm, Cm, A, chunk_size, state0=None, *, save=False, workspace=None, timer=None,
-            diag=None):
+            diag=None, sanitize_state0=False):
     """Returns ``(y, state_final, workspace)``.  ``diag`` (an
     ``_lib.StageReports`` over ``_lib.MAMBA2_DIAG_STAGES``) receives the
-    forward's per-stage reports."""
+    forward's per-stage reports.  ``sanitize_state0`` clips state0 to +-1e4
+    and nan_to_nums it first, as the reference's staged combine does
+    (kernel_mamba2_c_interchunk.py:56-58)."""
     _check(dt, x, Bm, Cm, A)
     lib = _lib.load()
     b, l, h, p = dt.shape
     n = Bm.shape[-1]
-    args = make_args(dt, Bm, chunk_size, flags=M2_SAVE if save else 0)
+    flags = (M2_SAVE if save else 0) | (M2_SANITIZE_STATE0 if sanitize_state0 else 0)
+    args = make_args(dt, Bm, chunk_size, flags=flags)
     dt, x, Bm, Cm = _rows_of(args, (dt, x, Bm, Cm))
     A = A.contiguous()
     if timer is not None:
@@ -94,13 +97,13 @@ def forward(dt, x, Bm, Cm, A, chunk_size, state0=None, *, save=False, workspace=
 
 
 def backward(dt, x, Bm, Cm, A, chunk_size, dy, dstate_final=None, state0=None, *, workspace=None,
-             reuse=False, timer=None, diag=None):
+             reuse=False, timer=None, diag=None, sanitize_state0=False):
     """Gradients ``(ddt, dx, dB, dC, dA, dstate0)`` (MB0 semantics) in the
     primals' dtypes (dA, dstate0 float32).  ``reuse`` declares that
     ``workspace`` holds the forward of the same inputs; the library checks
     that by the input addresses, so an input that has to be copied here (not
     contiguous and not row-strided, or state0 not float32) turns reuse into a
-    recompute."""
+    recompute.  ``sanitize_state0`` must match the forward's."""
     _check(dt, x, Bm, Cm, A)
     lib = _lib.load()
     if dy.dtype not in _DT:
@@ -112,7 +115,7 @@ def backward(dt, x, Bm, Cm, A, chunk_size, dy, dstate_final=None, state0=None, *
             (state0 is not None and (state0.dtype != torch.float32 or not state0.is_contiguous())):
         reuse = False
     A = A.contiguous()
-    args.flags = M2_REUSE if reuse else 0
+    args.flags = (M2_REUSE if reuse else 0) | (M2_SANITIZE_STATE0 if sanitize_state0 else 0)
     if timer is not None:
         args.profile = timer.arm()
     if diag is not None:

@@ -1,5 +1,6 @@
 // Host side of the GDN2 chunk pipeline: argument checks, workspace layout,
 // template dispatch and the extern "C" entry points of include/atomic_hybrid.h.
+#include <cstring>
 #include <mutex>
 #include <vector>
 
@@ -56,12 +57,16 @@ bool ws_tag_matches(const void* ws, const WsTag& t) {
   return false;
 }
 
-// the forward a GDN2 workspace holds: shapes, dtype and the input pointers
+// the forward a GDN2 workspace holds: shapes, dtype, query scale (folded into
+// the saved Aqk), whether h0 was sanitised, and the input pointers
 static WsTag gdn2_tag(const atomic_gdn2_args* a, const void* q, const void* k, const void* v, const void* w,
                       const void* b, const void* g, const void* h0) {
   WsTag t{};
-  t.kind = 1;
-  const int32_t d[8] = {a->batch, a->seqlen, a->heads, a->dk, a->dv, a->chunk, a->dtype, 0};
+  t.kind = (a->flags & ATOMIC_GDN2_SANITIZE_H0) ? 0x101 : 1;
+  int32_t scale_bits;
+  static_assert(sizeof(scale_bits) == sizeof(a->scale), "scale is a 32-bit float");
+  memcpy(&scale_bits, &a->scale, sizeof(scale_bits));
+  const int32_t d[8] = {a->batch, a->seqlen, a->heads, a->dk, a->dv, a->chunk, a->dtype, scale_bits};
   const void* ptr[8] = {q, k, v, w, b, g, h0, nullptr};
   for (int i = 0; i < 8; ++i) { t.dims[i] = d[i]; t.ptrs[i] = ptr[i]; }
   const int64_t dK = (int64_t)a->heads * a->dk, dV = (int64_t)a->heads * a->dv;
@@ -76,6 +81,7 @@ constexpr int kGdn2RunChunk = 64;
 struct Gdn2Plan {
   Gdn2Dims dm;
   int es;        // operand element size
+  bool sanitize_h0;  // ATOMIC_GDN2_SANITIZE_H0: the state loop clips / nan_to_nums h0 first
   size_t bhn;    // B * H * NT
   // forward intermediates
   size_t o_qg, o_kg, o_wt, o_u, o_aqk, o_ainv, o_gcl, o_ht, o_vnt, fwd_end;
@@ -113,6 +119,7 @@ static int gdn2_plan(const atomic_gdn2_args* a, Gdn2Plan* p) {
   }
   p->dm = d;
   p->es = a->dtype == ATOMIC_BF16 ? 2 : 4;
+  p->sanitize_h0 = (a->flags & ATOMIC_GDN2_SANITIZE_H0) != 0;
   const size_t N = (size_t)d.B * d.H * d.NT;
   p->bhn = N;
   const size_t es = p->es, C = d.C, K = d.K, V = d.V;
@@ -213,7 +220,8 @@ static int gdn2_forward_impl(const Gdn2Plan& p, const void* q, const void* k, co
   Gdn2Chunks<T> ck = gdn2_chunks<T>(p, ws);
   int rc = gdn2_intra_launch<T, K>(p, q, k, v, w, b, g, ck, L);
   if (rc) return rc;
-  return gdn2_state_launch<T, K>(p, ck, h0, o, h_final, save ? kStateSave : 0, L);
+  const int mode = (save ? kStateSave : 0) | (p.sanitize_h0 ? kStateSanitizeH0 : 0);
+  return gdn2_state_launch<T, K>(p, ck, h0, o, h_final, mode, L);
 }
 
 template <typename T>
@@ -457,7 +465,9 @@ static int gdn2_window_plan(const atomic_gdn2_args* a, int nw, Gdn2Plan* p) {
   w.batch = 1;
   w.seqlen = nw * kGdn2RunChunk;
   w.chunk = kGdn2RunChunk;
-  w.flags = 0;
+  // every window but a batch row's first starts from a state the loop has
+  // already clipped, so sanitising it again changes nothing
+  w.flags = a->flags & ATOMIC_GDN2_SANITIZE_H0;
   return gdn2_plan(&w, p);
 }
 

@@ -10,6 +10,10 @@ struct Mamba2Dims {
   // row strides of the inputs in elements (token t of batch b starts at
   // (b T + t) * stride): dt, x, B, C, dy
   long long rdt, rx, rB, rC, rdy;
+  // the forward state pass sanitises state0 (clip +-1e4, nan_to_num) before
+  // its first chunk, as the reference's staged combine does
+  // (kernel_mamba2_c_interchunk.py:58)
+  int sanitize_state0;
 };
 
 template <typename T>

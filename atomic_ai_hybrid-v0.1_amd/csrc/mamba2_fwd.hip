@@ -293,7 +293,8 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
 // Thread map: one float4 of one channel row; RP channel rows per workgroup.
 // Stage M4 (STG = true, forward): src = the caller's state_end in
 // [B][H][NT][P][N], cum_last from the caller's cumdecay, and the initial
-// state sanitised (kernel_mamba2_c_interchunk.py:58,68-78).
+// state sanitised (kernel_mamba2_c_interchunk.py:58,68-78).  The whole-path
+// forward sanitises it too when dm.sanitize_state0 is set.
 template <typename T, int P, int N, bool BWD, bool STG = false>
 __global__ __launch_bounds__(256) void mamba2_state_pass(Mamba2Dims dm, Mamba2Chunks<T> ck,
                                                         T* __restrict__ dstate, float* __restrict__ lasta,
@@ -315,7 +316,7 @@ __global__ __launch_bounds__(256) void mamba2_state_pass(Mamba2Dims dm, Mamba2Ch
 
   float4 st = make_float4(0.f, 0.f, 0.f, 0.f);
   if (init) st = *reinterpret_cast<const float4*>(init + ((size_t)bh * P + p) * N + s0);
-  if constexpr (STG) {
+  if (STG || (!BWD && dm.sanitize_state0)) {
     st.x = sanitize(st.x); st.y = sanitize(st.y); st.z = sanitize(st.z); st.w = sanitize(st.w);
   }
 

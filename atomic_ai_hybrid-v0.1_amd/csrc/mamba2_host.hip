@@ -29,6 +29,7 @@ static int mamba2_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
   if (a->headdim == 192 && a->dstate != 128) return ATOMIC_ERR_SHAPE;
   Mamba2Dims d;
   d.B = a->batch; d.T = a->seqlen; d.H = a->heads; d.P = a->headdim; d.N = a->dstate;
+  d.sanitize_state0 = (a->flags & ATOMIC_MAMBA2_SANITIZE_STATE0) != 0;
   // Chunk 256 (the model's chunk_size = min(256, L), model.py:436) runs as
   // 128-row chunks.  With every step exponent dt A <= 0 (the model's A < 0,
   // dt > 0) the two differ only in the reference's exp(-20) floors on pairs
@@ -459,7 +460,7 @@ extern "C" size_t atomic_mamba2_workspace_size(const atomic_mamba2_args* a) {
 static WsTag mamba2_tag(const atomic_mamba2_args* a, const void* dt, const void* x, const void* B, const void* C,
                         const void* A, const void* state0) {
   WsTag t{};
-  t.kind = 2;
+  t.kind = (a->flags & ATOMIC_MAMBA2_SANITIZE_STATE0) ? 0x102 : 2;  // the saved states depend on it
   const int32_t d[8] = {a->batch, a->seqlen, a->heads, a->headdim, a->dstate, a->chunk, a->dtype, 0};
   const void* ptr[8] = {dt, x, B, C, A, state0, nullptr, nullptr};
   for (int i = 0; i < 8; ++i) { t.dims[i] = d[i]; t.ptrs[i] = ptr[i]; }

@@ -4,10 +4,23 @@
  *
  * Plain pointers and sizes only.  Every tensor is a device pointer to a dense
  * row-major array; every call is stream-ordered on `stream` (a hipStream_t,
- * or NULL for the default stream), allocates nothing, never synchronises the
- * host, and keeps no global mutable state (reentrant).  Scratch memory is a
- * caller-owned `workspace` of at least the size the matching *_workspace_size
- * call returns.
+ * or NULL for the default stream), allocates nothing and never synchronises
+ * the host.  Scratch memory is a caller-owned `workspace` of at least the
+ * size the matching *_workspace_size call returns.
+ *
+ * Host state: the library keeps one piece of mutable host state, the REUSE
+ * table (a mutex-guarded list of at most 1024 records of which saving
+ * forward each workspace address range holds; see ATOMIC_GDN2_REUSE).  The
+ * entry points may be called from several host threads at once; the table's
+ * only effect is the ATOMIC_ERR_REUSE refusal.  The no-allocation forward
+ * also keeps a per-device scratch address (atomic_gdn2_fwd_noalloc).
+ *
+ * REUSE is safe only while the caller owns the workspace between the saving
+ * forward and the reusing backward: the table is keyed by addresses, so a
+ * workspace freed, reallocated at the same address and rewritten by other
+ * code (not this library), or an input rewritten in place, passes the check
+ * with stale intermediates.  A caller that cannot guarantee that passes no
+ * REUSE flag (the backward then recomputes the forward).
  *
  * Return value: ATOMIC_OK (0) or a negative ATOMIC_ERR_* code.  The reference
  * raises shape errors at trace time and has no runtime error channel
@@ -116,7 +129,15 @@ enum {
      returns ATOMIC_ERR_REUSE before launching anything when it is not this
      call's (same shapes, dtype and input pointers); contents rewritten in
      place between the calls are not detected */
-  ATOMIC_GDN2_REUSE = 2
+  ATOMIC_GDN2_REUSE = 2,
+  /* forward, and the backward's recompute of it: clip h0 to +-1e4 and
+     nan_to_num it before the first chunk, as the reference's staged forward
+     does (_sanitize_h0, kernel_d_pipeline.py:54-55,101), which the trainable
+     op runs (kernel_trainable_B6.py:87-88).  Without the flag h0 enters as
+     given, as in gdn2_chunked_wy_reference (gdn2_wy_reference.py:122-123).
+     dh0 is the gradient at the sanitised h0, unmasked, as B1 returns it
+     (kernel_bwd_b1_dhu.py:14-44).  The REUSE record includes the flag. */
+  ATOMIC_GDN2_SANITIZE_H0 = 4
 };
 
 typedef struct atomic_gdn2_args {
@@ -276,7 +297,13 @@ enum {
   /* backward: the workspace holds the intermediates of an
      atomic_mamba2_fwd call on identical inputs (checked as for
      ATOMIC_GDN2_REUSE: ATOMIC_ERR_REUSE otherwise) */
-  ATOMIC_MAMBA2_REUSE = 2
+  ATOMIC_MAMBA2_REUSE = 2,
+  /* forward, and the backward's recompute of it: clip state0 to +-1e4 and
+     nan_to_num it first, as the reference's staged combine does
+     (kernel_mamba2_c_interchunk.py:56-58), which the trainable op runs
+     (kernel_mamba2_trainable_B6.py:72-80).  Without the flag state0 enters
+     as given, as in mamba2_ssd_reference.  dstate0 is unmasked. */
+  ATOMIC_MAMBA2_SANITIZE_STATE0 = 4
 };
 
 /* Stages of atomic_mamba2_args.diag: the forward fills [CB, STATE_FINAL],
