@@ -8,9 +8,10 @@ A + B + C (build_chunk_scores_pallas, wy_solve_pallas, recompute_wy_pallas:
 kernel_a_scores.py:69, kernel_b_solve.py:151, kernel_c_recompute.py:91) as one
 pass and returns ``(Aqk, A, w_pseudo, u, kg, qg, gc_last)``;
 ``gdn2_inter_chunk_combine_with_state`` and ``gdn2_pallas_forward_with_residuals``
-(kernel_d_pipeline.py:127,199) also return the scan's per-chunk states.  All run at
-64-row chunks (BT = 64, the whole-path chunk of this library); the arrays are
-float32 for float32 inputs and bfloat16 for bfloat16 ones (gc_last float32).
+(kernel_d_pipeline.py:127,199) also return the scan's per-chunk states.  The
+combine runs at the block of its arrays: the reference's 256 rows (float32
+arrays, the kernels A, B, C mirrors' default) or this library's 64 (arrays
+in the inputs' dtype, as ``build_chunk_wy`` returns them; gc_last float32).
 Every computation runs in libatomic_hybrid.so; there is no fallback.
 """
 from __future__ import annotations
@@ -21,9 +22,10 @@ import torch
 
 from . import _lib
 from . import gdn2 as _g
+from .kernel_a_scores import BT as REF_BLOCK, check_block
 from .kernel_trainable_B6 import gdn2_pallas_forward  # noqa: F401  (the whole staged forward)
 
-BT = 64
+BT = 64   # the block of build_chunk_wy
 
 
 def build_chunk_wy(q, k, v, w, b, g, scale):
@@ -52,9 +54,11 @@ def build_chunk_wy(q, k, v, w, b, g, scale):
 def _combine_args(Aqk, w_pseudo, u, kg, qg, gc_last, scale, h0):
     B, H, NT, C, K = w_pseudo.shape
     V = u.shape[-1]
-    if C != BT:
-        raise _lib.AtomicError(f"gdn2_inter_chunk_combine: chunks of {C} rows (this library runs {BT})")
+    if C not in (BT, REF_BLOCK):
+        raise _lib.AtomicError(f"gdn2_inter_chunk_combine: blocks of {C} rows (takes {REF_BLOCK} or {BT})")
     dt = w_pseudo.dtype
+    if C == REF_BLOCK and dt != torch.float32:
+        raise TypeError("the 256-row combine takes the float32 arrays of kernels A and C")
     for t in (Aqk, w_pseudo, u, kg, qg):
         if t.dtype != dt or not t.is_cuda:
             raise TypeError("per-chunk arrays must share one dtype and live on the device")
@@ -90,35 +94,43 @@ def gdn2_inter_chunk_combine_with_state(Aqk, w_pseudo, u, kg, qg, gc_last, scale
     """Kernel D that also returns the states of the scan
     (kernel_d_pipeline.py:127-158): ``(o, h_final, h_pre_all, v_new_all)``
     with h_pre_all [NT, B, H, K, V] (the state entering each chunk) and
-    v_new_all [NT, B, H, BT, V] in the reference's scan order, float32.  The
-    library keeps them in the arrays' dtype, transposed; they are laid out
-    here."""
+    v_new_all [NT, B, H, BT, V] in the reference's scan order, float32.  At
+    256-row blocks the library writes them in float32 as [B, H, NT, ...]; at
+    64-row chunks in the arrays' dtype, transposed.  They are laid out here."""
     args, arrays, h0, o, h_final = _combine_args(Aqk, w_pseudo, u, kg, qg, gc_last, scale, h0)
     B, H, NT, C, K = w_pseudo.shape
     V = u.shape[-1]
     dt, dev = w_pseudo.dtype, w_pseudo.device
-    h_pre_t = torch.empty(B, H, NT, V, K, dtype=dt, device=dev)
-    v_new_t = torch.empty(B, H, NT, V, C, dtype=dt, device=dev)
+    if C == REF_BLOCK:
+        h_pre = torch.empty(B, H, NT, K, V, dtype=dt, device=dev)
+        v_new = torch.empty(B, H, NT, C, V, dtype=dt, device=dev)
+    else:
+        h_pre = torch.empty(B, H, NT, V, K, dtype=dt, device=dev)
+        v_new = torch.empty(B, H, NT, V, C, dtype=dt, device=dev)
     rc = _lib.load().atomic_gdn2_inter_chunk_combine_with_state(
-        ctypes.byref(args), *map(_p, arrays), _p(h0), _p(o), _p(h_final), _p(h_pre_t), _p(v_new_t),
+        ctypes.byref(args), *map(_p, arrays), _p(h0), _p(o), _p(h_final), _p(h_pre), _p(v_new),
         _g._stream(dev))
     _lib.check(rc, "atomic_gdn2_inter_chunk_combine_with_state")
-    h_pre_all = h_pre_t.transpose(-1, -2).permute(2, 0, 1, 3, 4).to(torch.float32)
-    v_new_all = v_new_t.transpose(-1, -2).permute(2, 0, 1, 3, 4).to(torch.float32)
+    if C != REF_BLOCK:
+        h_pre, v_new = h_pre.transpose(-1, -2), v_new.transpose(-1, -2)
+    h_pre_all = h_pre.permute(2, 0, 1, 3, 4).to(torch.float32)
+    v_new_all = v_new.permute(2, 0, 1, 3, 4).to(torch.float32)
     return o, h_final, h_pre_all, v_new_all
 
 
-def gdn2_pallas_forward_with_residuals(q, k, v, w, b, g, scale, h0=None, debug_tag=""):
+def gdn2_pallas_forward_with_residuals(q, k, v, w, b, g, scale, h0=None, debug_tag="", *, block=REF_BLOCK):
     """The staged forward keeping the backward's residuals
     (kernel_d_pipeline.py:199-228): ``(o [B, T, H, V], h_final, residuals)``
     with residuals Aqk, Akk, A, h_pre_all, v_new_all, w_pseudo, u, kg, qg,
-    gc_last, from kernels A, B, C and D run one by one."""
+    gc_last, from kernels A, B, C and D run one by one at ``block`` rows (the
+    reference's 256, or this library's 64)."""
     from .kernel_a_scores import build_chunk_scores_pallas
     from .kernel_b_solve import wy_solve_pallas
     from .kernel_c_recompute import recompute_wy_pallas
+    check_block(block)
     B, T, H, K = q.shape
     V = v.shape[-1]
-    Aqk, Akk = build_chunk_scores_pallas(q, k, b, g, scale)
+    Aqk, Akk = build_chunk_scores_pallas(q, k, b, g, scale, block=block)
     A = wy_solve_pallas(Akk)
     w_pseudo, u, kg, qg, gc_last = recompute_wy_pallas(q, k, v, w, b, g, A)
     o_chunks, h_final, h_pre_all, v_new_all = gdn2_inter_chunk_combine_with_state(

@@ -3,8 +3,7 @@
 ``build_chunk_cumdecay_pallas(dt, A, chunk_size, interpret=False)`` keeps the
 reference signature (kernel_mamba2_a_decay.py:71) and returns cumdecay
 ``[B, H, NT, C, P]`` float32: per chunk, sanitize(cumsum(sanitize(dt A, 20)),
-1e4).  chunk_size is 64 or 128 (the stage arrays are per chunk; the whole
-path runs 256 as 128-row chunks, which a per-chunk array cannot).
+1e4).  chunk_size is 64, 128 or 256 (the model's chunk, model.py:436).
 ``interpret`` is accepted and ignored (it selects the Pallas interpreter in
 the reference).  Every computation runs in libatomic_hybrid.so; there is no
 fallback.

@@ -6,7 +6,9 @@ keeps the reference signature (kernel_mamba2_b_intra.py:119) and returns
 given cumdecay: y_diag_i = sum_{j<=i} exp(clip(cum_i - cum_j, +-20))
 CB_ij dBx_j and state_end = B^T sanitize(dBx exp(clip(cum_last - cum,
 +-20))), with the reference stage kernel's clips (no 1e6 caps).  chunk_size
-is 64 or 128.  Every computation runs in libatomic_hybrid.so; there is no
+is 64, 128 or 256; at 256 the sum runs over the reference's two 128-row
+sub-blocks, each sub-block's part sanitised before the next is added
+(kernel_mamba2_b_intra.py:61-62,86-108).  Every computation runs in libatomic_hybrid.so; there is no
 fallback.
 """
 from __future__ import annotations

@@ -7,7 +7,7 @@ and returns ``(y [B, T, H, P], state_final [B, H, P, N])`` float32: the
 sequential state pass over the chunks (state0 sanitised) and y =
 sanitize(y_diag + y_off).  ``mamba2_pallas_forward(dt, x, B, C, A,
 chunk_size, state0=None, interpret=False)`` chains M2 -> M3 -> M4 like the
-reference (:90-100).  chunk_size is 64 or 128.  Every computation runs in
+reference (:90-100).  chunk_size is 64, 128 or 256.  Every computation runs in
 libatomic_hybrid.so; there is no fallback.
 """
 from __future__ import annotations

@@ -8,6 +8,7 @@
 #include "diag.hpp"
 #include "gdn2_bwd.hip"
 #include "launch.hpp"
+#include "stage256.hpp"
 #include "ws_tag.hpp"
 
 namespace ah {
@@ -614,13 +615,25 @@ extern "C" int atomic_gdn2_bwd(const atomic_gdn2_args* a, const void* q, const v
 
 // ------------------------------------------------ stage-level forward
 // The forward's stages over caller-owned per-chunk arrays in the reference's
-// layout ([B][H][NT][64][D], gc_last [B][H][NT][K]), in args.dtype (gc_last
-// and the outputs fp32): kernels A, B and C alone or in one pass, then
-// kernel D.  64-row chunks only (the arrays are per chunk).
+// layout ([B][H][NT][BT][D], gc_last [B][H][NT][K]): kernels A, B and C alone
+// or in one pass, then kernel D.  Two blocks BT (args.chunk):
+//   64   the chunk of this library's kernels, arrays in args.dtype (gc_last
+//        and the outputs fp32);
+//   256  the reference's Pallas block (kernel_a_scores.py:15-17), float32
+//        arrays, by the kernels of stage256.hip (the one-pass A + B + C entry
+//        takes 64 only).
 static int gdn2_stage_plan(const atomic_gdn2_args* a, Gdn2Plan* p) {
   const int rc = gdn2_plan(a, p);
   if (rc != ATOMIC_OK) return rc;
-  return a->chunk == kGdn2RunChunk ? ATOMIC_OK : ATOMIC_ERR_SHAPE;
+  return a->chunk == kGdn2RunChunk || a->chunk == kStageBlock ? ATOMIC_OK : ATOMIC_ERR_SHAPE;
+}
+
+// The plan's dims over blocks of kStageBlock rows.
+static Gdn2Dims gdn2_dims256(const Gdn2Plan& p) {
+  Gdn2Dims d = p.dm;
+  d.C = kStageBlock;
+  d.NT = d.T / kStageBlock;
+  return d;
 }
 
 template <typename T>
@@ -648,6 +661,7 @@ extern "C" int atomic_gdn2_chunk_wy(const atomic_gdn2_args* a, const void* q, co
   if (rc != ATOMIC_OK) return rc;
   if (!q || !k || !v || !w || !b || !g || !Aqk || !A || !w_pseudo || !u || !kg || !qg || !gc_last)
     return ATOMIC_ERR_NULL;
+  if (a->chunk != kGdn2RunChunk) return ATOMIC_ERR_SHAPE;  // Akk would need caller memory at 256
   Launch L{a->profile, (hipStream_t)stream};
   if (a->dtype == ATOMIC_BF16) {
     const Gdn2Chunks<bf16> ck = gdn2_stage_chunks<bf16>(Aqk, A, w_pseudo, u, kg, qg, gc_last);
@@ -681,6 +695,10 @@ extern "C" int atomic_gdn2_chunk_scores(const atomic_gdn2_args* a, const void* q
   const int rc = gdn2_stage_plan(a, &p);
   if (rc != ATOMIC_OK) return rc;
   if (!q || !k || !b || !g || !Aqk || !Akk) return ATOMIC_ERR_NULL;
+  if (a->chunk == kStageBlock) {
+    Launch L{a->profile, (hipStream_t)stream};
+    return g256_scores(gdn2_dims256(p), a->dtype, q, k, b, g, (float*)Aqk, (float*)Akk, L);
+  }
   return gdn2_stage_launch<kIntraScores>(a, p, q, k, nullptr, nullptr, b, g, Aqk, Akk, nullptr, nullptr, nullptr,
                                          nullptr, nullptr, nullptr, stream);
 }
@@ -690,6 +708,10 @@ extern "C" int atomic_gdn2_wy_solve(const atomic_gdn2_args* a, const void* Akk, 
   const int rc = gdn2_stage_plan(a, &p);
   if (rc != ATOMIC_OK) return rc;
   if (!Akk || !A) return ATOMIC_ERR_NULL;
+  if (a->chunk == kStageBlock) {
+    Launch L{a->profile, (hipStream_t)stream};
+    return g256_solve(gdn2_dims256(p), (const float*)Akk, (float*)A, L);
+  }
   return gdn2_stage_launch<kIntraSolve>(a, p, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                                         const_cast<void*>(Akk), A, nullptr, nullptr, nullptr, nullptr, nullptr,
                                         stream);
@@ -702,6 +724,11 @@ extern "C" int atomic_gdn2_recompute_wy(const atomic_gdn2_args* a, const void* q
   const int rc = gdn2_stage_plan(a, &p);
   if (rc != ATOMIC_OK) return rc;
   if (!q || !k || !v || !w || !b || !g || !A || !w_pseudo || !u || !kg || !qg || !gc_last) return ATOMIC_ERR_NULL;
+  if (a->chunk == kStageBlock) {
+    Launch L{a->profile, (hipStream_t)stream};
+    return g256_recompute(gdn2_dims256(p), a->dtype, q, k, v, w, b, g, (const float*)A, (float*)w_pseudo,
+                          (float*)u, (float*)kg, (float*)qg, gc_last, L);
+  }
   return gdn2_stage_launch<kIntraRecompute>(a, p, q, k, v, w, b, g, nullptr, nullptr, const_cast<void*>(A),
                                             w_pseudo, u, kg, qg, gc_last, stream);
 }
@@ -715,6 +742,9 @@ extern "C" int atomic_gdn2_inter_chunk_combine(const atomic_gdn2_args* a, const 
   if (rc != ATOMIC_OK) return rc;
   if (!Aqk || !w_pseudo || !u || !kg || !qg || !gc_last || !o || !h_final) return ATOMIC_ERR_NULL;
   Launch L{a->profile, (hipStream_t)stream};
+  if (a->chunk == kStageBlock)
+    return g256_combine(gdn2_dims256(p), (const float*)Aqk, (const float*)w_pseudo, (const float*)u,
+                        (const float*)kg, (const float*)qg, gc_last, h0, o, h_final, nullptr, nullptr, L);
   const int mode = kStateChunkO | kStateSanitizeH0;
   void* aq = const_cast<void*>(Aqk);
   void* wt = const_cast<void*>(w_pseudo);
@@ -743,6 +773,10 @@ extern "C" int atomic_gdn2_inter_chunk_combine_with_state(const atomic_gdn2_args
   if (!Aqk || !w_pseudo || !u || !kg || !qg || !gc_last || !o || !h_final || !h_pre_t || !v_new_t)
     return ATOMIC_ERR_NULL;
   Launch L{a->profile, (hipStream_t)stream};
+  if (a->chunk == kStageBlock)  // fp32, not transposed: h_pre [B][H][NT][K][V], v_new [B][H][NT][256][V]
+    return g256_combine(gdn2_dims256(p), (const float*)Aqk, (const float*)w_pseudo, (const float*)u,
+                        (const float*)kg, (const float*)qg, gc_last, h0, o, h_final, (float*)h_pre_t,
+                        (float*)v_new_t, L);
   const int mode = kStateSave | kStateChunkO | kStateSanitizeH0;
   void* aq = const_cast<void*>(Aqk);
   void* wt = const_cast<void*>(w_pseudo);

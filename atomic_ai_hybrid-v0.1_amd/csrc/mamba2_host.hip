@@ -4,6 +4,7 @@
 #include "diag.hpp"
 #include "mamba2_bwd.hip"
 #include "launch.hpp"
+#include "stage256.hpp"
 #include "ws_tag.hpp"
 
 namespace ah {
@@ -322,18 +323,25 @@ static int mamba2_backward_diag(const Mamba2Plan& p, StageDiag& D, const void* d
 // kernel_mamba2_b_intra.py:119, kernel_mamba2_c_interchunk.py:38) over
 // caller-owned arrays in its layout: cumdecay [B][H][NT][C][P] fp32,
 // state_end [B][H][NT][P][N] fp32, y_diag and y [B][T][H][P] fp32.  The
-// arrays are per chunk, so chunk 256 (which the whole path runs as 128-row
-// chunks) is not taken.
+// arrays are per chunk of the requested size: chunks of 64 and 128 run the
+// whole path's kernels in their stage modes; chunk 256 (which the whole path
+// runs as 128-row chunks) runs the kernels of stage256.hip, with M3's two
+// 128-row sub-blocks (kernel_mamba2_b_intra.py:61-62,86-108).
 static int mamba2_stage_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
   const int rc = mamba2_plan(a, p);
   if (rc != ATOMIC_OK) return rc;
-  return a->chunk == p->dm.C ? ATOMIC_OK : ATOMIC_ERR_SHAPE;
+  if (a->chunk == kStageBlock) {
+    p->dm.C = kStageBlock;
+    p->dm.NT = a->seqlen / kStageBlock;
+  }
+  return ATOMIC_OK;
 }
 
 // M3 keeps CB ([B][NT][C][C] bf16) and M4 the states entering each chunk
 // ([B][NT][H][P][N] bf16) in the caller's workspace.
 static size_t mamba2_stage_ws(const Mamba2Plan& p) {
   const Mamba2Dims& d = p.dm;
+  if (d.C == kStageBlock) return m2_align(m256_combine_ws(d));   // fp32 states entering each chunk
   const size_t cb = (size_t)d.B * d.NT * d.C * d.C * 2;
   const size_t st = (size_t)d.B * d.NT * d.H * d.P * d.N * 2;
   return m2_align(cb > st ? cb : st);
@@ -432,17 +440,25 @@ static int mamba2_combine_stage_impl(const Mamba2Plan& p, const float* y_diag, c
 }
 
 static int mamba2_cumdecay_stage(const Mamba2Plan& p, const void* dt, const float* A, float* cum, Launch& L) {
+  if (p.dm.C == kStageBlock) {   // the cumsum kernel over 256 rows (N does not enter)
+    if (p.dm.P == 64) return mamba2_cumdecay_impl<kStageBlock, 64, 128>(p, dt, A, cum, L);
+    if (p.dm.P == 128) return mamba2_cumdecay_impl<kStageBlock, 128, 128>(p, dt, A, cum, L);
+    return mamba2_cumdecay_impl<kStageBlock, 192, 128>(p, dt, A, cum, L);
+  }
   AH_M2_DISPATCH(mamba2_cumdecay_impl, p, dt, A, cum, L);
 }
 
 static int mamba2_intra_stage(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm, const void* Cm,
                               const float* cum, float* y_diag, float* state_end, void* ws, Launch& L) {
+  if (p.dm.C == kStageBlock) return m256_intra(p.dm, dt, x, Bm, Cm, cum, y_diag, state_end, L);
   AH_M2_DISPATCH(mamba2_intra_stage_impl, p, dt, x, Bm, Cm, cum, y_diag, state_end, ws, L);
 }
 
 static int mamba2_combine_stage(const Mamba2Plan& p, const float* y_diag, const float* state_end, const float* cum,
                                 const void* Cm, const float* state0, float* y, float* state_final, void* ws,
                                 Launch& L) {
+  if (p.dm.C == kStageBlock)
+    return m256_combine(p.dm, y_diag, state_end, cum, Cm, state0, y, state_final, static_cast<float*>(ws), L);
   AH_M2_DISPATCH(mamba2_combine_stage_impl, p, y_diag, state_end, cum, Cm, state0, y, state_final, ws, L);
 }
 

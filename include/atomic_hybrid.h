@@ -233,32 +233,42 @@ int atomic_gdn2_fwd_noalloc(const atomic_gdn2_args* a, const void* q, const void
 
 /* ------------------------------------------------------------------------
  * GDN2 stage-level forward: the staged pipeline's kernels A, B, C, D over
- * caller-owned per-chunk arrays in the reference's layout.  The chunk is 64
- * rows (args.chunk = 64, the chunk of this library's kernels; the reference's
- * Pallas kernels fix 256, kernel_a_scores.py:15, and its oracle takes any).
- * The arrays are in args.dtype (the reference's are fp32); gc_last, o,
- * h_final fp32.
- *   Aqk, A : [B][H][NT][64][64]   w_pseudo, kg, qg : [B][H][NT][64][K]
- *   u : [B][H][NT][64][V]         gc_last : [B][H][NT][K]
+ * caller-owned per-block arrays in the reference's layout.  args.chunk picks
+ * the block BT:
+ *   256  the reference's Pallas block (kernel_a_scores.py:15-17): every
+ *        array is float32 whatever args.dtype (the inputs' type), as the
+ *        reference's are; the kernels follow kernel A's 128-row sub-blocks
+ *        with pairwise exp(clip(gc_i - gc_j, +-20)), kernel B's 16-row block
+ *        recursion over two 128-row halves and its A10 = -A11 T10 A00 step
+ *        with a sanitise at every block product (kernel_b_solve.py:66-148),
+ *        kernel C's float32 w v (kernel_c_recompute.py:49-82);
+ *   64   this library's own chunk: the arrays are in args.dtype (gc_last,
+ *        o, h_final fp32), from the whole path's kernels.
+ * NT = T / BT.
+ *   Aqk, A : [B][H][NT][BT][BT]   w_pseudo, kg, qg : [B][H][NT][BT][K]
+ *   u : [B][H][NT][BT][V]         gc_last : [B][H][NT][K]
  *
  * Kernels A + B + C in one pass: build_chunk_scores_pallas (Aqk, scaled;
  * kernel_a_scores.py:69), wy_solve_pallas (A = (I + Akk)^-1;
  * kernel_b_solve.py:151) and recompute_wy_pallas (w_pseudo, u, kg, qg,
  * gc_last; kernel_c_recompute.py:91).  Akk itself stays on chip.
  */
+/* (64-row chunks only: at 256 it returns ATOMIC_ERR_SHAPE, since Akk would
+ * need caller memory; chain the three entries below instead.) */
 int atomic_gdn2_chunk_wy(const atomic_gdn2_args* a, const void* q, const void* k, const void* v,
                          const void* w, const void* b, const float* g, void* Aqk, void* A, void* w_pseudo,
                          void* u, void* kg, void* qg, float* gc_last, void* stream);
 
 /* Kernel A alone: build_chunk_scores_pallas(q, k, b, g, scale)
  * (kernel_a_scores.py:69-99): Aqk (causal, scaled) and the strict Akk,
- * [B][H][NT][64][64] in args.dtype, nan_to_num'd (kernel_a_scores.py:65-66). */
+ * [B][H][NT][BT][BT], nan_to_num'd (kernel_a_scores.py:65-66). */
 int atomic_gdn2_chunk_scores(const atomic_gdn2_args* a, const void* q, const void* k, const void* b,
                              const float* g, void* Aqk, void* Akk, void* stream);
 
 /* Kernel B alone: wy_solve_pallas(Akk) (kernel_b_solve.py:151-169),
  * A = (I + Akk)^-1 by 16-row block forward substitution; like the
- * reference, only the strictly lower blocks of Akk are read. */
+ * reference, only the strictly lower part of Akk is read.  At BT = 256 Akk
+ * and A are float32 and args.dtype is not read. */
 int atomic_gdn2_wy_solve(const atomic_gdn2_args* a, const void* Akk, void* A, void* stream);
 
 /* Kernel C alone: recompute_wy_pallas(q, k, v, w, b, g, A)
@@ -272,16 +282,17 @@ int atomic_gdn2_recompute_wy(const atomic_gdn2_args* a, const void* q, const voi
 /* Kernel D: gdn2_inter_chunk_combine (kernel_d_pipeline.py:94-124), the
  * sequential state loop over those arrays.  h0 [B][H][K][V] (NULL: zeros) is
  * sanitised first like the reference's _sanitize_h0 (:54-55); o is written per
- * chunk, [B][H][NT][64][V] fp32, and h_final [B][H][K][V] fp32. */
+ * block, [B][H][NT][BT][V] fp32, and h_final [B][H][K][V] fp32. */
 int atomic_gdn2_inter_chunk_combine(const atomic_gdn2_args* a, const void* Aqk, const void* w_pseudo,
                                     const void* u, const void* kg, const void* qg, const float* gc_last,
                                     const float* h0, float* o, float* h_final, void* stream);
 
 /* Kernel D keeping its per-chunk states: gdn2_inter_chunk_combine_with_state
  * (kernel_d_pipeline.py:127-158), the residuals of the reference's backward.
- * Besides o and h_final it writes, in args.dtype and transposed (the layout
- * this library's backward reads), the state entering each chunk
- * h_pre_t [B][H][NT][V][K] and v_new_t [B][H][NT][V][64]. */
+ * Besides o and h_final it writes the state entering each block and v_new:
+ * at BT = 64 in args.dtype and transposed (the layout this library's
+ * backward reads), h_pre_t [B][H][NT][V][K] and v_new_t [B][H][NT][V][64];
+ * at BT = 256 in float32, h_pre [B][H][NT][K][V] and v_new [B][H][NT][256][V]. */
 int atomic_gdn2_inter_chunk_combine_with_state(const atomic_gdn2_args* a, const void* Aqk, const void* w_pseudo,
                                                const void* u, const void* kg, const void* qg,
                                                const float* gc_last, const float* h0, float* o, float* h_final,
@@ -383,8 +394,12 @@ int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, const void* x
 /* ------------------------------------------------------------------------
  * Mamba2 stage-level forward: the reference's staged pipeline M2 -> M3 -> M4
  * (mamba2_pallas_forward, kernel_mamba2_c_interchunk.py:90-100) over
- * caller-owned arrays in its layout.  args.chunk is 64 or 128 (the arrays
- * are per chunk; 256 is refused).  dt, x, B, C bf16; the arrays fp32:
+ * caller-owned arrays in its layout.  args.chunk is 64, 128 or 256 (the
+ * model's chunk, model.py:436), the arrays per chunk of that size; at 256,
+ * M3 sums over the reference's two 128-row sub-blocks, sanitising each
+ * sub-block's part before the next is added (kernel_mamba2_b_intra.py:61-62,
+ * 86-108), and M4 keeps the states entering each chunk in float32.  dt, x,
+ * B, C bf16; the arrays fp32:
  *   cumdecay : [B][H][NT][C][P]     state_end : [B][H][NT][P][N]
  *   y_diag, y : [B][T][H][P]        state0, state_final : [B][H][P][N]
  * The arithmetic is that of the stage kernels, which differ from the whole

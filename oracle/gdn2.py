@@ -153,6 +153,116 @@ def gdn2_inter_chunk_combine(Aqk, w_pseudo, u, kg, qg, gc_last, scale, h0=None, 
     return torch.stack(outs, 2), h
 
 
+def _blocks(t, BT):
+    """[B, T, H, D] -> [B, H, NT, BT, D] (reshape_in, kernel_a_scores.py:75-77)."""
+    B, T, H, D = t.shape
+    return t.reshape(B, T // BT, BT, H, D).permute(0, 3, 1, 2, 4)
+
+
+def chunk_scores(q, k, b, g, scale, block=256, sub=128, dtype=torch.float64):
+    """Kernel A, ``build_chunk_scores_pallas`` (kernel_a_scores.py:26-98):
+    per block of ``block`` rows, gc = tril @ g (:32-34), and for each pair of
+    ``sub``-row sub-blocks (si >= sj) the pairwise-decay scores with the
+    causal / strict masks on diagonal sub-blocks and nan_to_num (:39-66).
+    Returns (Aqk, Akk) [B, H, NT, block, block] in ``dtype``."""
+    f = dtype
+    q_, k_, b_, g_ = (_blocks(t.to(f), block) for t in (q, k, b, g))
+    gc = torch.cumsum(g_, dim=-2)                                              # :32-34
+    Aqk = torch.zeros(q_.shape[:-1] + (block,), dtype=f)
+    Akk = torch.zeros_like(Aqk)
+    idx = torch.arange(sub)
+    causal = (idx[:, None] >= idx[None, :]).to(f)
+    strict = (idx[:, None] > idx[None, :]).to(f)
+    for si in range(block // sub):                                             # :39-40
+        for sj in range(si + 1):
+            i0, j0 = si * sub, sj * sub
+            dd = gc[..., i0:i0 + sub, None, :] - gc[..., None, j0:j0 + sub, :]  # :51
+            e = torch.exp(torch.clamp(dd, -CLIP_DECAY, CLIP_DECAY))             # :52
+            qi, ki, bi, kj = (t[..., r0:r0 + sub, :] for t, r0 in ((q_, i0), (k_, i0), (b_, i0), (k_, j0)))
+            aqk = scale * torch.einsum("...id,...ijd,...jd->...ij", qi, e, kj)  # :54
+            akk = torch.einsum("...id,...ijd,...jd->...ij", bi * ki, e, kj)     # :55-56
+            if si == sj:                                                      # :58-63
+                aqk = aqk * causal
+                akk = akk * strict
+            Aqk[..., i0:i0 + sub, j0:j0 + sub] = n2n(aqk)                     # :65
+            Akk[..., i0:i0 + sub, j0:j0 + sub] = n2n(akk)                     # :66
+    return Aqk, Akk
+
+
+def _micro_forward_substitution(T):
+    """One MB x MB block (kernel_b_solve.py:66-87): row i of A is
+    sanitize(e_i - T[i, :] @ A) with the rows >= i of A still zero."""
+    MB = T.shape[-1]
+    eye = torch.eye(MB, dtype=T.dtype)
+    A = torch.zeros_like(T)
+    for i in range(MB):
+        contrib = torch.einsum("...j,...jc->...c", T[..., i, :], A)           # :78-79
+        A = A.clone()
+        A[..., i, :] = sanitize(eye[i] - contrib)                             # :80-83
+    return A
+
+
+def _block_solve(T, mb=16):
+    """(I + T)^-1 of one strictly lower [.., BC, BC] block by the MB = 16
+    block recursion (kernel_b_solve.py:90-127), sanitising every block
+    product and accumulation."""
+    BC = T.shape[-1]
+    nm = BC // mb
+    sl = lambda i: slice(i * mb, (i + 1) * mb)
+    blocks = {}
+    for m in range(nm):
+        A_mm = sanitize(_micro_forward_substitution(T[..., sl(m), sl(m)]))    # :104
+        blocks[m, m] = A_mm
+        for n in range(m - 1, -1, -1):                                        # :107
+            acc = torch.zeros_like(A_mm)
+            for kk in range(n, m):                                            # :108-113
+                acc = sanitize(acc + T[..., sl(m), sl(kk)] @ blocks[kk, n])
+            blocks[m, n] = sanitize(-(A_mm @ acc))                            # :114-116
+    A = torch.zeros_like(T)
+    for (m, n), blk in blocks.items():                                        # :118-127
+        A[..., sl(m), sl(n)] = blk
+    return A
+
+
+def wy_solve_blocked(Akk, sub=128):
+    """Kernel B, ``wy_solve_pallas`` (kernel_b_solve.py:130-171): the two
+    ``sub``-row halves by ``_block_solve``, then A10 = sanitize(-A11
+    sanitize(T10 A00)).  Akk [..., 2 sub, 2 sub]; the upper-right block of
+    the result is zero."""
+    T00 = Akk[..., :sub, :sub]
+    T11 = Akk[..., sub:, sub:]
+    T10 = Akk[..., sub:, :sub]
+    A00 = _block_solve(T00)                                                   # :137
+    A11 = _block_solve(T11)                                                   # :138
+    tmp = sanitize(T10 @ A00)                                                 # :140-141
+    A10 = sanitize(-(A11 @ tmp))                                              # :142-143
+    A = torch.zeros_like(Akk)
+    A[..., :sub, :sub] = A00                                                  # :145-148
+    A[..., sub:, :sub] = A10
+    A[..., sub:, sub:] = A11
+    return A
+
+
+def recompute_wy(q, k, v, w, b, g, A, dtype=torch.float64):
+    """Kernel C, ``recompute_wy_pallas`` (kernel_c_recompute.py:48-82) at the
+    block of A ([B, H, NT, BT, BT]): w_pseudo = A (b k e^gc), u = A (w v)
+    with w v formed after the upcast (:49-56,64), kg = k e^(gc_last - gc),
+    qg = q e^gc, gc_last, each sanitised to +-1e4.  Returns
+    (w_pseudo, u, kg, qg, gc_last)."""
+    f = dtype
+    BT = A.shape[-1]
+    q_, k_, v_, w_, b_, g_ = (_blocks(t.to(f), BT) for t in (q, k, v, w, b, g))
+    gc = torch.cumsum(g_, dim=-2)                                              # :58-60
+    kb_decayed = b_ * k_ * torch.exp(gc)                                       # :62
+    A = A.to(f)
+    w_pseudo = sanitize(A @ kb_decayed)                                        # :63,68
+    u = sanitize(A @ (w_ * v_))                                                # :64,69
+    gl = gc[..., -1, :]                                                        # :71
+    kg = sanitize(k_ * torch.exp(gl[..., None, :] - gc))                       # :72,80
+    qg = sanitize(q_ * torch.exp(gc))                                          # :73,81
+    return w_pseudo, u, kg, qg, sanitize(gl)                                   # :82
+
+
 def gdn2_token_serial_reference(q, k, v, g, b, w, scale, h0=None, dtype=torch.float64):
     """Token-serial recurrence (gdn2_wy_reference.py:33-56), an independent
     oracle for the chunked form.  Returns o in ``dtype`` (the reference casts

@@ -86,7 +86,7 @@ def test_kernels_a_b_c_alone_match_the_oracle(dtype, K):
     ref = _oracle_stages(q, k, v, w, b, g, 0.7)
     dq, dk, dv, dw, db, dg = (t.cuda() for t in (q, k, v, w, b, g))
     tol = tol_for(dtype)
-    Aqk, Akk = KA.build_chunk_scores_pallas(dq, dk, db, dg, 0.7)
+    Aqk, Akk = KA.build_chunk_scores_pallas(dq, dk, db, dg, 0.7, block=64)
     akk_in = ref["Akk"].to(dtype)
     A = KB.wy_solve_pallas(akk_in.cuda())
     A_ref = og.n2n(og.wy_inverse(akk_in.double()))
@@ -115,7 +115,7 @@ def test_kernels_a_b_c_chained_equal_the_one_pass_build_in_fp32():
     banner("gdn2 kernels A -> B -> C vs the one-pass build (fp32)")
     q, k, v, w, b, g = (t.cuda() for t in _inputs(B, T, H, K, F32, 81))
     one = KD.build_chunk_wy(q, k, v, w, b, g, 0.9)
-    Aqk, Akk = KA.build_chunk_scores_pallas(q, k, b, g, 0.9)
+    Aqk, Akk = KA.build_chunk_scores_pallas(q, k, b, g, 0.9, block=64)
     A = KB.wy_solve_pallas(Akk)
     wp, u, kg, qg, gl = KC.recompute_wy_pallas(q, k, v, w, b, g, A)
     torch.cuda.synchronize()
@@ -156,7 +156,7 @@ def test_combine_with_state_and_residuals(dtype):
     q, k, v, w, b, g = _inputs(B, T, H, K, dtype, 95)
     h0 = 0.4 * torch.randn(B, H, K, K, generator=torch.Generator().manual_seed(96))
     dq, dk, dv, dw, db, dg = (t.cuda() for t in (q, k, v, w, b, g))
-    o, hf, res = KD.gdn2_pallas_forward_with_residuals(dq, dk, dv, dw, db, dg, 0.6, h0=h0.cuda())
+    o, hf, res = KD.gdn2_pallas_forward_with_residuals(dq, dk, dv, dw, db, dg, 0.6, h0=h0.cuda(), block=64)
     o_w, h_w, _ = G.forward(dq, dk, dv, dw, db, dg, 0.6, h0=h0.cuda())
     torch.cuda.synchronize()
     tol = tol_for(dtype)

@@ -106,10 +106,3 @@ def test_positive_exponent_follows_the_stage_kernels():
     torch.cuda.synchronize()
     _check("y", y, y_ref, TOL_BF16)
     _check("state_final", sf, sf_ref, TOL_BF16)
-
-
-def test_chunk_256_is_refused():
-    banner("mamba2 stage chunk 256")
-    g = [t.cuda() for t in _inp(1, 256, 2, 64, 64, seed=3)]
-    with pytest.raises(_lib.AtomicError, match="SHAPE"):
-        MA.build_chunk_cumdecay_pallas(g[0], g[4], 256)

@@ -225,3 +225,80 @@ def test_inter_chunk_combine_reproduces_the_chunked_reference():
     o_r, h_r = og.gdn2_inter_chunk_combine(stack("Aqk"), stack("w_pseudo"), stack("u"), stack("kg"), stack("qg"),
                                            stack("gc_last"), 0.7, h0=clean)
     assert torch.equal(o_b, o_r) and torch.equal(h_b, h_r) and torch.isfinite(o_b).all()
+
+
+# ------------------------------------------------------------------ the 256-row stage kernels
+def _stage_blocks(t, BT):
+    B, T, H, D = t.shape
+    return t.reshape(B, T // BT, BT, H, D).permute(0, 3, 1, 2, 4)
+
+
+def test_block_stages_compose_to_the_chunked_reference_at_256():
+    """Kernels A (128-row sub-blocks), B (16-row block recursion, 128-row
+    halves, A10 step), C and D at the reference's 256-row block, composed,
+    equal the chunked reference at chunk 256; A's scores and C's arrays
+    equal that reference's own per-chunk intermediates, and B's inverse its
+    row-wise forward substitution."""
+    q, k, v, g, b, w = _inputs(1, 512, 2, 16, 12, seed=21)
+    scale = 0.7
+    o_ref, h_ref, st = og.gdn2_chunked_wy_reference(q, k, v, g, b, w, scale, 256, return_stages=True)
+    Aqk, Akk = og.chunk_scores(q, k, b, g, scale)
+    assert Aqk.shape == (1, 2, 2, 256, 256)
+    for n in range(2):
+        assert _rel(Aqk[:, :, n], st[n]["Aqk"]) < 1e-12 and _rel(Akk[:, :, n], st[n]["Akk"]) < 1e-12
+    A = og.wy_solve_blocked(Akk)
+    assert _rel(A, og.wy_inverse(Akk)) < 1e-11
+    eye = torch.eye(256, dtype=F64)
+    assert ((eye + Akk) @ A - eye).abs().max().item() < 1e-10
+    wp, u, kg, qg, gl = og.recompute_wy(q, k, v, w, b, g, A)
+    for n in range(2):
+        for name, x in (("w_pseudo", wp), ("u", u), ("kg", kg), ("qg", qg)):
+            assert _rel(x[:, :, n], st[n][name]) < 1e-11, name
+        assert _rel(gl[:, :, n], st[n]["gc_last"]) < 1e-12
+    o, hf = og.gdn2_inter_chunk_combine(Aqk, wp, u, kg, qg, gl, scale)
+    o = o.permute(0, 2, 3, 1, 4).reshape(o_ref.shape)
+    assert _rel(o, o_ref) < 1e-11 and _rel(hf, h_ref) < 1e-11
+
+
+def test_block_scores_sub_block_split_and_masks():
+    """Kernel A's 128-row sub-blocks cover the block: the same scores at
+    sub = 256 (one sub-block) and sub = 64; the strictly upper triangle of
+    both and the diagonal of Akk are zero."""
+    q, k, v, g, b, w = _inputs(1, 256, 1, 8, 8, seed=22)
+    a128 = og.chunk_scores(q, k, b, g, 1.0)
+    for sub in (256, 64):
+        other = og.chunk_scores(q, k, b, g, 1.0, sub=sub)
+        assert _rel(other[0], a128[0]) < 1e-13 and _rel(other[1], a128[1]) < 1e-13
+    assert torch.count_nonzero(torch.triu(a128[0], 1)) == 0
+    assert torch.count_nonzero(torch.triu(a128[1], 0)) == 0
+
+
+def test_block_solve_sanitises_like_the_reference():
+    """With a near-singular Akk the blocked solve's entries stay within
+    +-1e4 and finite (every block product is sanitised), while the plain
+    inverse of the same Akk overflows that range."""
+    gen = torch.Generator().manual_seed(23)
+    Akk = torch.tril(torch.randn(1, 256, 256, generator=gen, dtype=F64) * 3.0, -1)
+    A = og.wy_solve_blocked(Akk)
+    assert torch.isfinite(A).all() and A.abs().max().item() <= 1e4
+    assert og.wy_inverse(Akk).abs().max().item() > 1e4
+    # below the clip the two agree
+    small = Akk * 0.01
+    assert _rel(og.wy_solve_blocked(small), og.wy_inverse(small)) < 1e-12
+
+
+def test_block_recompute_forms_w_v_in_float32():
+    """Kernel C multiplies w and v after the upcast (kernel_c_recompute.py:53,
+    64), the chunked reference before it (gdn2_wy_reference.py:94): with
+    bf16 inputs the two u differ by the bf16 rounding of w v; with float64
+    inputs they agree."""
+    q, k, v, g, b, w = _inputs(1, 256, 1, 8, 8, seed=24)
+    bf = [t.to(torch.bfloat16) for t in (q, k, v, b, w)]
+    qb, kb, vb, bb, wb = bf
+    _, _, st = og.gdn2_chunked_wy_reference(qb, kb, vb, g, bb, wb, 1.0, 256, return_stages=True)
+    A = st[0]["A"][:, :, None]
+    u_c = og.recompute_wy(qb, kb, vb, wb, bb, g, A)[1][:, :, 0]
+    u_ref = st[0]["u"]
+    wv32 = _stage_blocks(wb.double() * vb.double(), 256)[:, :, 0]
+    assert _rel(u_c, og.sanitize(st[0]["A"] @ wv32)) < 1e-12
+    assert 1e-5 < _rel(u_c, u_ref) < 2e-2
