@@ -4,9 +4,11 @@
 // sanitising of :166-195 is kept.
 //
 // mamba2_chunk_outer<BWD>  (mamba2_fwd.hip) per (batch, chunk, head, slice):
-//                    (dy decay_h)^T C, and the operands Ydh, W of dC_1, dB_1.
-// mamba2_state_pass<BWD>   (mamba2_fwd.hip) reverse elementwise dstate carry
-//                    and the decay_chunk_end row term d_cum_last_a.
+//                    Ydh = dy decay_h and W, the operands of the carry's
+//                    (dy decay_h)^T C and of dC_1, dB_1.
+// mamba2_state_chain<BWD>  (mamba2_seq.hpp) the reverse dstate carry, its
+//                    (dy decay_h)^T C on MFMA, and the decay_chunk_end row
+//                    term d_cum_last_a.
 // mamba2_bwd_chunk   one workgroup (8 waves) per (batch, chunk, head group):
 //                    every per-head term of :123-190 for each head and
 //                    32-channel slice, with the cross-head sum dCB (:147-152)

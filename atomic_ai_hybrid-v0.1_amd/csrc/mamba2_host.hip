@@ -13,8 +13,8 @@ static size_t m2_align(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct Mamba2Plan {
   Mamba2Dims dm;
-  size_t o_cb, o_state, o_cl, o_src, fwd_end;
-  size_t o_dstate, o_lasta, o_ydh, o_wr, o_part, o_dap, total;
+  size_t o_cb, o_state, o_cl, o_rows;
+  size_t o_dstate, o_lasta, o_wr, o_part, o_dap, total;
   int G;  // head groups of the cross-head dCB reduction
 };
 
@@ -62,11 +62,11 @@ static int mamba2_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
   p->o_cb = take(B * NT * C * C * es);
   p->o_state = take(B * NT * H * P * N * es);        // state entering each chunk
   p->o_cl = take(B * NT * H * P * 4);                // cum at each chunk's last row
-  p->o_src = take(B * NT * H * P * N * 4);           // state_end; then the backward's dstate source
-  p->fwd_end = off;
+  // S rows of the state loops: the forward's dBx dte, then the backward's
+  // Ydh = dy decay_h (a REUSE backward needs only the states and cum_last)
+  p->o_rows = take(B * T * H * P * es);
   p->o_dstate = take(B * NT * H * P * N * es);       // dstate entering each chunk's backward
   p->o_lasta = take(B * NT * H * P * 4);             // d cum_last from decay_chunk_end
-  p->o_ydh = take(B * T * H * P * es);               // dy decay_h
   p->o_wr = take(B * T * H * P * es);                // sanitize(dBx decay_to_end)
   p->o_part = take(B * NT * (size_t)p->G * C * C * 4);  // dCB per head group
   p->o_dap = take(B * NT * H * 4);                   // per-chunk dA
@@ -81,7 +81,7 @@ static Mamba2Chunks<T> mamba2_chunks(const Mamba2Plan& p, void* ws) {
   c.cb = reinterpret_cast<T*>(base + p.o_cb);
   c.state_pre = reinterpret_cast<T*>(base + p.o_state);
   c.cl = reinterpret_cast<float*>(base + p.o_cl);
-  c.src = reinterpret_cast<float*>(base + p.o_src);
+  c.src = nullptr;
   c.cum = nullptr;
   c.ydiag = nullptr;
   return c;
@@ -93,7 +93,7 @@ static Mamba2Grads<T> mamba2_grads(const Mamba2Plan& p, void* ws) {
   Mamba2Grads<T> g;
   g.dstate = reinterpret_cast<T*>(base + p.o_dstate);
   g.lasta = reinterpret_cast<float*>(base + p.o_lasta);
-  g.ydh = reinterpret_cast<T*>(base + p.o_ydh);
+  g.ydh = reinterpret_cast<T*>(base + p.o_rows);
   g.wr = reinterpret_cast<T*>(base + p.o_wr);
   g.part = reinterpret_cast<float*>(base + p.o_part);
   g.dap = reinterpret_cast<float*>(base + p.o_dap);
@@ -112,8 +112,20 @@ static unsigned pass_grid(const Mamba2Dims& d) {
   return (unsigned)(d.B * d.H * (P / RP));
 }
 
-// Forward: CB, per-chunk state_end, the state pass and (when y is wanted) the
-// outputs.  The state entering every chunk always lands in the workspace.
+// The state loops: one workgroup per (batch, head, 32 channels), eight waves
+// (four at N = 64, whose 64 columns make four 16-column tiles).
+template <typename T, int C, int P, int N, bool BWD>
+static void launch_state_chain(const Mamba2Dims& d, hipStream_t st, const T* S, const T* R,
+                               const Mamba2Chunks<T>& ck, T* dstate, float* lasta, const float* init,
+                               float* fin) {
+  constexpr int NW = N == 128 ? 8 : 4;
+  hipLaunchKernelGGL((mamba2_state_chain<T, C, P, N, BWD, NW>), dim3((unsigned)(d.B * d.H * (P / 32))),
+                     dim3(64 * NW), 0, st, d, S, R, ck, dstate, lasta, init, fin);
+}
+
+// Forward: CB, the chunks' S rows and cum_last, the state loop and (when y
+// is wanted) the outputs.  The state entering every chunk always lands in
+// the workspace.
 template <int C, int P, int N>
 static int mamba2_forward_impl(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm,
                                const void* Cm, const float* A, const float* state0, float* y,
@@ -133,29 +145,20 @@ static int mamba2_forward_impl(const Mamba2Plan& p, const void* dt, const void* 
                          d, (const T*)Bm, (const T*)Cm, ck);
   });
   if (rc) return rc;
-  // chunk_outer workgroups take 8 (head, channel slice) pairs of one chunk,
-  // 4 when 8 would leave fewer than two workgroups per CU (0.045 -> 0.039 ms
-  // at B2 T4096 H32 P64), else one head's slices; the backward likewise
-  rc = L("mamba2_chunk_state", [&] {
+  // the chunk's S rows and cum_last, one workgroup per (batch, chunk, head,
+  // 64 channels) (eight pairs per workgroup: 0.094 against 0.086 ms at the
+  // benchmark shape), then the state loop with S^T B on chip
+  T* srows = reinterpret_cast<T*>(static_cast<char*>(ws) + p.o_rows);
+  rc = L("mamba2_chunk_rows", [&] {
     constexpr int NPO = P / kOuterPT;
-    const size_t pairs = (size_t)d.H * NPO;
-    if (pairs % 8 == 0 && d.B * d.NT * pairs / 8 >= kFullGrid)
-      hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, 8>),
-                         dim3((unsigned)(d.B * d.NT * pairs / 8)), dim3(256), 0, st, d, (const T*)dt,
-                         (const T*)x, A, (const T*)Bm, (const T*)nullptr, ck, (T*)nullptr, (T*)nullptr);
-    else if (pairs % 4 == 0 && d.B * d.NT * pairs / 4 >= kFullGrid)
-      hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, 4>),
-                         dim3((unsigned)(d.B * d.NT * pairs / 4)), dim3(256), 0, st, d, (const T*)dt,
-                         (const T*)x, A, (const T*)Bm, (const T*)nullptr, ck, (T*)nullptr, (T*)nullptr);
-    else
-      hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, NPO>),
-                         dim3((unsigned)(d.B * d.NT * d.H)), dim3(256), 0, st, d, (const T*)dt,
-                         (const T*)x, A, (const T*)Bm, (const T*)nullptr, ck, (T*)nullptr, (T*)nullptr);
+    hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, 1>),
+                       dim3((unsigned)(d.B * d.NT * d.H * NPO)), dim3(256), 0, st, d, (const T*)dt,
+                       (const T*)x, A, (const T*)nullptr, (const T*)nullptr, ck, srows, (T*)nullptr);
   });
   if (rc) return rc;
-  rc = L("mamba2_state_pass", [&] {
-    hipLaunchKernelGGL((mamba2_state_pass<T, P, N, false>), dim3(pass_grid<P, N>(d)), dim3(256), 0, st,
-                       d, ck, (T*)nullptr, (float*)nullptr, state0, state_final);
+  rc = L("mamba2_state_chain", [&] {
+    launch_state_chain<T, C, P, N, false>(d, st, srows, (const T*)Bm, ck, (T*)nullptr, (float*)nullptr,
+                                          state0, state_final);
   });
   if (rc || !y) return rc;
   // chunk_y workgroups take SL (head, channel slice) pairs of one chunk: 16
@@ -225,26 +228,16 @@ static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x,
   Mamba2Chunks<T> ck = mamba2_chunks<T>(p, ws);
   Mamba2Grads<T> gr = mamba2_grads<T>(p, ws);
   hipStream_t st = L.st;
-  rc = L("mamba2_bwd_source", [&] {
+  rc = L("mamba2_bwd_rows", [&] {
     constexpr int NPO = P / kOuterPT;
-    const size_t pairs = (size_t)d.H * NPO;
-    if (pairs % 8 == 0 && d.B * d.NT * pairs / 8 >= kFullGrid)
-      hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true, 8>),
-                         dim3((unsigned)(d.B * d.NT * pairs / 8)), dim3(256), 0, st, d, (const T*)dt,
-                         (const T*)x, A, (const T*)Cm, (const TD*)dy, ck, gr.ydh, gr.wr);
-    else if (pairs % 4 == 0 && d.B * d.NT * pairs / 4 >= kFullGrid)
-      hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true, 4>),
-                         dim3((unsigned)(d.B * d.NT * pairs / 4)), dim3(256), 0, st, d, (const T*)dt,
-                         (const T*)x, A, (const T*)Cm, (const TD*)dy, ck, gr.ydh, gr.wr);
-    else
-      hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true, NPO>),
-                         dim3((unsigned)(d.B * d.NT * d.H)), dim3(256), 0, st, d, (const T*)dt,
-                         (const T*)x, A, (const T*)Cm, (const TD*)dy, ck, gr.ydh, gr.wr);
+    hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true, 1>),
+                       dim3((unsigned)(d.B * d.NT * d.H * NPO)), dim3(256), 0, st, d, (const T*)dt,
+                       (const T*)x, A, (const T*)nullptr, (const TD*)dy, ck, gr.ydh, gr.wr);
   });
   if (rc) return rc;
-  rc = L("mamba2_bwd_state_pass", [&] {
-    hipLaunchKernelGGL((mamba2_state_pass<T, P, N, true>), dim3(pass_grid<P, N>(d)), dim3(256), 0, st,
-                       d, ck, gr.dstate, gr.lasta, dstate_final, dstate0);
+  rc = L("mamba2_bwd_state_chain", [&] {
+    launch_state_chain<T, C, P, N, true>(d, st, gr.ydh, (const T*)Cm, ck, gr.dstate, gr.lasta, dstate_final,
+                                         dstate0);
   });
   if (rc) return rc;
   rc = L("mamba2_bwd_chunk", [&] {
@@ -421,8 +414,8 @@ static int mamba2_combine_stage_impl(const Mamba2Plan& p, const float* y_diag, c
   ck.ydiag = y_diag;
   hipStream_t st = L.st;
   int rc = L("mamba2_state_pass", [&] {
-    hipLaunchKernelGGL((mamba2_state_pass<T, P, N, false, true>), dim3(pass_grid<P, N>(d)), dim3(256), 0, st,
-                       d, ck, (T*)nullptr, (float*)nullptr, state0, state_final);
+    hipLaunchKernelGGL((mamba2_state_pass<T, P, N>), dim3(pass_grid<P, N>(d)), dim3(256), 0, st, d, ck,
+                       state0, state_final);
   });
   if (rc) return rc;
   constexpr int NPT = P / kYPT;

@@ -132,18 +132,22 @@ def mamba2_kernel_model(B, T, H, P, N, C, es=2):
     CP, CN, CC, PN = C * P, C * N, C * C, P * N
     return {
         "mamba2_cb": (Ub * 2 * CC * N, Ub * (2 * CN * es + CC * es)),
-        # state_end = B^T (dBx dte): dt, x in; state_end (f32) and cum_last out
-        "mamba2_chunk_state": (Uh * 2 * C * PN, Uh * (2 * CP * es + PN * 4 + P * 4) + Ub * CN * es),
-        # elementwise recurrence: state_end, cum_last in; state entering each chunk out
-        "mamba2_state_pass": (Uh * 2 * PN, Uh * (PN * 4 + P * 4 + PN * es) + 2 * B * H * PN * 4),
+        # the chunk's cum and S = dBx dte: dt, x in; S rows and cum_last out
+        "mamba2_chunk_rows": (Uh * 6 * CP, Uh * (2 * CP * es + CP * es + P * 4)),
+        # state loop: state_end = S^T B on MFMA and the recurrence; S, B, cum_last
+        # in; state entering each chunk out
+        "mamba2_state_chain": (Uh * (2 * C * PN + 2 * PN),
+                               Uh * (CP * es + P * 4 + PN * es) + Ub * CN * es + 2 * B * H * PN * 4),
         # y = y_diag + y_off: dt, x, state_prev in (C, CB shared); y (f32) out
         "mamba2_chunk_y": (Uh * (CC * P + 2 * C * PN),
                            Uh * (2 * CP * es + CP * 4 + PN * es) + Ub * (CN * es + CC * es)),
-        # (dy decay_h)^T C; dt, x, dy in; source (f32), Ydh, W out
-        "mamba2_bwd_source": (Uh * 2 * C * PN,
-                              Uh * (3 * CP * es + PN * 4 + 2 * CP * es) + Ub * CN * es),
-        "mamba2_bwd_state_pass": (Uh * 2 * PN,
-                                  Uh * (PN * 4 + P * 4 + 2 * PN * es + P * 4) + 2 * B * H * PN * 4),
+        # the chunk's cum, Ydh = dy decay_h and W: dt, x, dy in; Ydh, W out
+        "mamba2_bwd_rows": (Uh * 8 * CP, Uh * (3 * CP * es + 2 * CP * es)),
+        # reverse state loop: (dy decay_h)^T C on MFMA, the carry and the row term;
+        # Ydh, C, cum_last, state_prev in; dstate and the row term out
+        "mamba2_bwd_state_chain": (Uh * (2 * C * PN + 4 * PN),
+                                   Uh * (CP * es + P * 4 + 2 * PN * es + P * 4) + Ub * CN * es
+                                   + 2 * B * H * PN * 4),
         # y_off / dwrite recompute, the pairwise-decay products and dCB; dt, x, dy,
         # state_prev, dstate, last-row term in; ddt, dx, dCB partials out
         "mamba2_bwd_chunk": (Uh * (4 * C * PN + 3 * CC * P),
@@ -205,11 +209,11 @@ def survey_kernel_share(g, m):
     th, bt = B * T * H, B * T
     share.update({
         "mamba2_cb": bt * 2 * 2 * N,                               # B C
-        "mamba2_chunk_state": th * 4 * P + bt * 2 * N,             # dt x B
-        "mamba2_state_pass": B * H * P * N * 4,                    # state_final
+        "mamba2_chunk_rows": th * 4 * P,                           # dt x
+        "mamba2_state_chain": bt * 2 * N + B * H * P * N * 4,      # B in; state_final out
         "mamba2_chunk_y": th * (4 * P + 4 * P) + bt * 2 * N,       # dt x C in; y out
-        "mamba2_bwd_source": th * 6 * P + bt * 2 * N,              # dt x dy C
-        "mamba2_bwd_state_pass": B * H * P * N * 4,                # dstate0
+        "mamba2_bwd_rows": th * 6 * P,                             # dt x dy
+        "mamba2_bwd_state_chain": bt * 2 * N + B * H * P * N * 4,  # C in; dstate0 out
         "mamba2_bwd_chunk": th * (6 * P + 4 * P) + bt * 4 * N,     # dt x dy B C in; ddt dx out
         "mamba2_bwd_bc": bt * 4 * N * 2 + H * 4,                   # B C in; dB dC dA out
     })

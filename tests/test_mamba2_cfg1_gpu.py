@@ -1,10 +1,10 @@
 """Configuration 1 (B2 T4096 H32 P64 N128 C128) on the GPU, fwd + bwd.
 
-At this shape the chunk-parallel Mamba2 kernels run their small-grid launch
-forms: `mamba2_chunk_y` with 8 (head, channel slice) pairs per workgroup and
-`mamba2_chunk_state` / `mamba2_bwd_source` with 4, so that each grid keeps
-two workgroups per CU (larger shapes take 16 and 8 pairs, the small test
-shapes one head's slices).  Checked three ways:
+At this shape `mamba2_chunk_y` runs its small-grid launch form, 8 (head,
+channel slice) pairs per workgroup, so that the grid keeps two workgroups per
+CU (larger shapes take 16 pairs, the small test shapes one head's slices);
+the state loops run 64-channel heads as two 32-channel workgroups.  Checked
+three ways:
   * two heads of the full-shape run against the fp64 oracle (forward: y and
     the final state; backward: ddt, dx, dA, dstate0), and the single-head
     runs' dB / dC against that head's oracle dB / dC;
