@@ -83,6 +83,17 @@ __device__ __forceinline__ typename Mma<T>::frag ld_t_hilo(const T* hi, const T*
   return Mma<T>::ld_t(g2 ? lo : hi, ld, i0, k0 - 16 * g2);
 }
 
+// Rows r0 + 4g .. r0 + 4g + 3 of column c0 + (lane % 16) of a row-major bf16
+// LDS array (row pitch ld), g = lane / 16: the MFMA result-tile layout's four
+// elements of a lane, in one transposed read (ds_read_b64_tr_b16: lane s of a
+// 16-lane group points at row r0 + 4g + s / 4, columns c0 + 4 (s % 4) ..;
+// lane j receives column c0 + j of the four rows).
+__device__ __forceinline__ bf16x4 tile_rows4(const bf16* p, int ld, int r0, int c0) {
+  const int l = lane_id(), s = l & 15, g = l >> 4;
+  typedef __attribute__((address_space(3))) bf16x4* lds_p;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_p)(p + (r0 + 4 * g + (s >> 2)) * ld + c0 + 4 * (s & 3)));
+}
+
 template <typename T, int C, int N, int PT, int NTH>
 struct CkLds {
   static constexpr int PAD = Pad<T>::v;
@@ -399,14 +410,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) lastb[q][ii] = 0.f;
       {
-        f32x4 Rv[NIW], Sv[NIW];
+        f32x4 ra[NIW], sa[NIW];
         if (!exact) {
           // ra = sum_{J <= I} M_IJ (CB_IJ Vd_J) and sa = sum_{J >= I} M_JI (CB_JI^T Yu_J),
           // the diagonal block masked to its lower / upper triangle.  With
           // M_II = exp(cum_{16I} - cum_{16I+15}) the row scales U_i, V_i below turn
           // the diagonal terms into exp(ci - ce) (CB_II Vd_I) and exp(cs - ci) (CB_II^T Yu_I).
           // Compiled per block index, so every operand read is issued up front.
-          f32x4 ra[NIW], sa[NIW];
 #pragma unroll
           for (int q = 0; q < NIW; ++q) { ra[q] = zero4(); sa[q] = zero4(); }
           static_switch<NB>(I - z, [&](auto Ic) {
@@ -438,20 +448,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
               }
             }
           });
-#pragma unroll
-          for (int q = 0; q < NIW; ++q) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              const int i = 16 * I + tile_row(k), p = 16 * (ni0 + q) + tile_col();
-              const float ci = sCum[i * L::LC + p];
-              Rv[q][k] = __expf(ci - sCum[16 * I * L::LC + p]) * ra[q][k];
-              Sv[q][k] = __expf(sCum[(16 * I + 15) * L::LC + p] - ci) * sa[q][k];
-            }
-          }
         }
+        // exp(-20): the floor of the decay to the chunk end
+        const float dte_floor = __expf(-kClipDecay);
 #pragma unroll
         for (int q = 0; q < NIW; ++q) {
           const int ni = ni0 + q;
+          const int pc = 16 * ni + tile_col();
+          // the lane's four rows of dy, dt, x (one transposed read each)
+          const bf16x4 dy4 = tile_rows4(sDy, L::LPT, 16 * I, 16 * ni);
+          const bf16x4 dt4 = tile_rows4(sDt, L::LPT, 16 * I, 16 * ni);
+          const bf16x4 x4 = tile_rows4(sX, L::LPT, 16 * I, 16 * ni);
+          const float cl = sCum[(C - 1) * L::LC + pc];
+          const float cs = sCum[16 * I * L::LC + pc], ce = sCum[(16 * I + 15) * L::LC + pc];
+          // factorised path: exp(cl - ci) = E V_i and exp(ci) = D U_i with the
+          // row scales U_i = exp(ci - cs), V_i = exp(ce - ci) of the pair sums
+          // and the block factors E = exp(cl - ce), D = exp(cs)
+          const float Eb = __expf(cl - ce), Db = __expf(cs);
           // y_off_raw = C state^T and dwrite = B dstate^T for this tile (:126,134)
           f32x4 yoff = zero4(), dwr = zero4();
 #pragma unroll
@@ -461,16 +474,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           }
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) {
-            const int i = 16 * I + tile_row(ii), p = 16 * ni + tile_col();
+            const int i = 16 * I + tile_row(ii), p = pc;
             const float ci = sCum[i * L::LC + p];
-            const float cl = sCum[(C - 1) * L::LC + p];
-            const float dyi = to_f(sDy[i * L::LPT + p]);
-            const float dtv = to_f(sDt[i * L::LPT + p]), xv = to_f(sX[i * L::LPT + p]);
+            const float dyi = (float)dy4[ii];
+            const float dtv = (float)dt4[ii], xv = (float)x4[ii];
             const float dbxi = sanitize(dtv * xv);
-            float rsum, ssum, ssum_m;
+            const float dte_raw = cl - ci;
+            float rsum, ssum, ssum_m, dte, dh;
             if (!exact) {
-              rsum = Rv[q][ii];
-              ssum = ssum_m = Sv[q][ii];
+              // every step exponent <= 0 here, so cl <= ci <= 0: the clip of
+              // the decay to the chunk end is its exp(-20) floor alone, and
+              // exp(ci) is only used where ci >= -20
+              const float U = __expf(ci - cs), V = __expf(ce - ci);
+              rsum = U * ra[q][ii];
+              ssum = ssum_m = V * sa[q][ii];
+              dte = fmaxf(Eb * V, dte_floor);
+              dh = Db * U;
             } else {
               // every pair with the reference's clip, 1e6 cap and masks:
               // R (i as row, masked), S / S_m (i as column)
@@ -491,11 +510,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 ssum += v;
                 ssum_m += v * m;
               }
+              dte = sanitize(__expf(fminf(fmaxf(dte_raw, -kClipDecay), kClipDecay)), 1e6f);
+              dh = __expf(fminf(fmaxf(ci, -kClipDecay), 0.f));
             }
-            const float dte_raw = cl - ci;
-            const float dte = sanitize(__expf(fminf(fmaxf(dte_raw, -kClipDecay), kClipDecay)), 1e6f);
             const float m2 = (dte_raw >= -kClipDecay && dte_raw <= kClipDecay) ? 1.f : 0.f;
-            const float dh = __expf(fminf(fmaxf(ci, -kClipDecay), 0.f));
             const float m1 = (ci >= -kClipDecay && ci <= 0.f) ? 1.f : 0.f;
             const float dw = dwr[ii];
             const float ddbx = sanitize(dw * dte + ssum);                 // :138,148,166
@@ -549,10 +567,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int w = 0; w < NW; ++w) extra += sLastB[w * PT + p];
         if (fabsf(sCum[(C - 1) * L::LC + p]) < kClipAcc) off += extra;
+        const bf16x4 dt4 = tile_rows4(sDt, L::LPT, 16 * I, 16 * (ni0 + q));
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) {
-          const int i = 16 * I + tile_row(ii);
-          const float dtv = to_f(sDt[i * L::LPT + p]);
+          const float dtv = (float)dt4[ii];
           const float araw = dtv * Ah;
           const float dA = (araw >= -kClipDecay && araw <= kClipDecay) ? (redv[q][ii] + off) : 0.f;
           ddt[((rowz + 16 * I) * dm.H + h) * P + p0 + (olane + ii * HP + 16 * q)] =
