@@ -21,8 +21,11 @@ struct Mamba2Chunks {
   T* cb;         // [B][NT][C][C]      sanitize(C_i . B_j), shared by every head
   T* state_pre;  // [B][NT][H][P][N]   state entering each chunk
   float* cl;     // [B][NT][H][P]      cumulative log decay at the chunk's last row
+  float* src;    // [B][NT][H][P][N]   the two-pass form's per-chunk state_end, then
+                 //                    the backward's (dy decay_h)^T C (NULL when the
+                 //                    state loops form them); stage-level entries:
+                 //                    the caller's state_end [B][H][NT][P][N]
   // stage-level entries only (NULL on the whole path):
-  float* src;    // [B][H][NT][P][N]   the caller's state_end
   const float* cum;    // [B][H][NT][C][P]  the caller's cumdecay
   const float* ydiag;  // [B][T][H][P]      the caller's y_diag (the combine)
 };

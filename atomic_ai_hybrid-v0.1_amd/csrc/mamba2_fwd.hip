@@ -17,14 +17,19 @@
 //                     to every head instead, kernel_mamba2_b_intra.py:136-142).
 // mamba2_chunk_outer  one workgroup per (batch, chunk, head, channel slice):
 //                     the chunk's cum and its S rows, dBx dte (forward) or
-//                     the backward's Ydh = dy decay_h and W (BWD = true).
+//                     the backward's Ydh = dy decay_h and W (BWD = true), and
+//                     in the two-pass form the per-chunk S^T B (S^T C).
 // mamba2_state_chain  (mamba2_seq.hpp) one workgroup per (batch, head, 32
 //                     channels), sequential over chunks: s_end = S^T B on
 //                     MFMA and the recurrence, the state entering every chunk
 //                     (forward), or the dstate carry and the decay_chunk_end
 //                     term (backward).
-// mamba2_state_pass   the stage-level kernel M4 alone: the recurrence over a
-//                     caller's state_end.
+// mamba2_state_pass   one workgroup per (batch, head, 8 or 16 channels),
+//                     sequential over chunks, elementwise: the two-pass form
+//                     of the state loop over the per-chunk state_end (or the
+//                     backward's (dy decay_h)^T C) that mamba2_chunk_outer
+//                     formed, for grids too small for mamba2_state_chain; and
+//                     the stage-level kernel M4.
 // mamba2_chunk_y      one workgroup per (batch, chunk, head, 32 channels):
 //                     y = y_diag + y_off.
 // mamba2_cumdecay     one workgroup per (batch, chunk, head, 64 channels):
@@ -165,25 +170,29 @@ struct OuterLds {
   static_assert(C * LS * (int)sizeof(T) <= C * LC * 4, "S must fit in the cum buffer");
 };
 
-// The chunk's S for (batch, chunk, head, PT channels), SL consecutive (head,
-// slice) pairs per workgroup; (dm.H * P / PT) % SL == 0:
-//   forward  (BWD = false): S = dBx dte (the chunk's write, :133-135) into
-//            srows ([B][T][H][P], bf16) and the chunk's cum_last; the state
-//            loop forms S^T B (:136-137) on chip (mamba2_seq.hpp).
+// The chunk's cum and S for (batch, chunk, head, PT channels), SL
+// consecutive (head, slice) pairs per workgroup; (dm.H * P / PT) % SL == 0:
+//   forward  (BWD = false): S = dBx dte (the chunk's write, :133-135) and
+//            cum_last; with PROD the chunk's state_end = sanitize(S^T B)
+//            (:136-137) into ck.src, without it S into srows ([B][T][H][P],
+//            bf16) for the state loop that forms S^T B on chip
+//            (mamba2_seq.hpp).
 //   backward (BWD = true):  S = Ydh = dy decay_h (:123 of mamba2_bwd_reference.py)
-//            into srows, and W = sanitize(dBx dte) (:135) into wr: the
-//            operands of the state loop's (dy decay_h)^T C (:128), of dC_1
-//            and of dB_1.
+//            into srows and W = sanitize(dBx dte) (:135) into wr, the
+//            operands of dC_1 and dB_1; with PROD also (dy decay_h)^T C
+//            (:128) into ck.src, else the state loop forms it.
 //   stage M3 (STG = true, forward): cum from ck.cum, S = sanitize(dBx
-//            exp(clip(cum_last - cum, +-20))) and out[p][s] = sum_i S[i][p]
-//            R[i][s] = state_end with R = B, in [B][H][NT][P][N]
-//            (kernel_mamba2_b_intra.py:110-116); the SL pairs share R.
-template <typename T, typename TD, int C, int P, int N, int PT, bool BWD, int SL, bool STG = false>
+//            exp(clip(cum_last - cum, +-20))) and state_end in
+//            [B][H][NT][P][N] (kernel_mamba2_b_intra.py:110-116).
+// With PROD the SL pairs share the staged rows R (B forward, C backward) and
+// out[p][s] = sum_i S[i][p] R[i][s] runs on MFMA.
+template <typename T, typename TD, int C, int P, int N, int PT, bool BWD, int SL, bool STG = false,
+          bool PROD = STG>
 __global__ __launch_bounds__(256) void mamba2_chunk_outer(
     Mamba2Dims dm, const T* __restrict__ dt, const T* __restrict__ x, const float* __restrict__ A,
     const T* __restrict__ R, const TD* __restrict__ dy, Mamba2Chunks<T> ck, T* __restrict__ srows,
     T* __restrict__ wr) {
-  typedef OuterLds<T, C, N, PT, STG> L;
+  typedef OuterLds<T, C, N, PT, PROD> L;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
   float* sCum = reinterpret_cast<float*>(lds + L::off_cum);
   T* sS = reinterpret_cast<T*>(lds + L::off_cum);
@@ -197,7 +206,9 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
   const size_t row0 = (size_t)bb * dm.T + (size_t)n * C;
   const size_t rsx = (size_t)dm.H * P;  // the workspace rows (Ydh, W)
   // R (B or C of the chunk) is shared by the workgroup's SL (head, slice) pairs
-  if constexpr (STG) stage_rows<T, C, N>(sR, L::LN, R + row0 * (size_t)dm.rB, (size_t)dm.rB);
+  // R (B or C of the chunk) is shared by the workgroup's SL (head, slice) pairs
+  const size_t rR = BWD ? (size_t)dm.rC : (size_t)dm.rB;
+  if constexpr (PROD) stage_rows<T, C, N>(sR, L::LN, R + row0 * rR, rR);
   for (int sl = 0; sl < SL; ++sl) {
   const int m = m2 * SL + sl;
   const int h = m / NPT, p0 = (m % NPT) * PT;
@@ -257,13 +268,13 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
         sv[i][j] = dbx * dte;
       }
     }
-    if constexpr (!STG) store8(srows + base + r * rsx + c, sv[i]);
+    if constexpr (BWD || !PROD) store8(srows + base + r * rsx + c, sv[i]);
     if constexpr (BWD) store8(wr + base + r * rsx + c, wv);
   }
   const size_t bnh = (size_t)bn * dm.H + h;
   if (!BWD && !STG && threadIdx.x < PT) ck.cl[bnh * P + p0 + threadIdx.x] = sCum[(C - 1) * L::LC + threadIdx.x];
   __syncthreads();  // every cum read is done: S overwrites the cum buffer
-  if constexpr (STG) {
+  if constexpr (PROD) {
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
       const int e = threadIdx.x + 256 * i, r = e / PER_ROW, c = (e % PER_ROW) * 8;
@@ -273,14 +284,16 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
 
     constexpr int NI = N / 16, TILES = (PT / 16) * NI, TPW = TILES / 4;
     static_assert(TILES % 4 == 0, "tiles must split evenly over 4 waves");
-    float* out = ck.src + (bhn_ref * P + p0) * N;
+    float* out = ck.src + ((STG ? bhn_ref : bnh) * P + p0) * N;
     const int wv_id = wave_id();
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       const int tile = wv_id * TPW + t, mi = tile / NI, ni = tile % NI;
       f32x4 acc = tile_mma<T, true, true>(zero4(), sS, L::LS, sR, L::LN, 16 * mi, 16 * ni, C);
+      if constexpr (!BWD) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) acc[k] = sanitize(acc[k]);
+        for (int k = 0; k < 4; ++k) acc[k] = sanitize(acc[k]);
+      }
       store_tile_n(out, N, 16 * mi, 16 * ni, acc);
     }
     __syncthreads();  // the next pair rewrites the cum / S buffer
@@ -288,15 +301,21 @@ __global__ __launch_bounds__(256) void mamba2_chunk_outer(
   }
 }
 
-// ------------------------------------------------------------------ stage M4 state pass
-// The recurrence of inter_chunk_combine_pallas over the caller's state_end
-// [B][H][NT][P][N] and cumdecay, with the initial state sanitised
-// (kernel_mamba2_c_interchunk.py:58,68-78): the state entering chunk n ->
-// state_pre (bf16, [B][NT][H][P][N]), then
-//   state = sanitize(state exp(clip(cum_last, -20, 0)) + state_end)
+// ------------------------------------------------------------------ sequential pass
+// Forward: state entering chunk n -> state_pre (bf16), then
+//   state = sanitize(state exp(clip(cum_last, -20, 0)) + s_end)      (:144-146)
+// Backward (MB0, mamba2_bwd_reference.py:236-247), reverse over chunks:
+//   dstate carry entering chunk n's backward -> dstate (bf16);
+//   d_cum_last_a = sum_s dstate state_prev * decay_chunk_end * mask  (:116,120)
+//   dstate = sanitize(dstate decay_chunk_end + (dy decay_h)^T C)      (:115,128,195)
 // Thread map: one float4 of one channel row; RP channel rows per workgroup.
-template <typename T, int P, int N>
+// Stage M4 (STG = true, forward): src = the caller's state_end in
+// [B][H][NT][P][N], cum_last from the caller's cumdecay, and the initial
+// state sanitised (kernel_mamba2_c_interchunk.py:58,68-78).  The whole-path
+// forward sanitises it too when dm.sanitize_state0 is set.
+template <typename T, int P, int N, bool BWD, bool STG = false>
 __global__ __launch_bounds__(256) void mamba2_state_pass(Mamba2Dims dm, Mamba2Chunks<T> ck,
+                                                        T* __restrict__ dstate, float* __restrict__ lasta,
                                                         const float* __restrict__ init,
                                                         float* __restrict__ fin) {
   constexpr int TPR = N / 4, RP = 256 / TPR, NRP = P / RP;
@@ -305,46 +324,73 @@ __global__ __launch_bounds__(256) void mamba2_state_pass(Mamba2Dims dm, Mamba2Ch
   const int r = threadIdx.x / TPR, c4 = threadIdx.x % TPR;
   const int p = rp * RP + r, s0 = 4 * c4;
   const int NT = dm.NT;
-  auto rowi = [&](int n) { return (((size_t)bb * NT + n) * dm.H + h) * P + p; };   // [B][NT][H] order
-  auto rows = [&](int n) { return ((size_t)bh * NT + n) * P + p; };                 // [B][H][NT] order
-  auto cl_at = [&](int n) { return ck.cum[(((size_t)bh * NT + n) * dm.C + dm.C - 1) * P + p]; };
+  auto rowi = [&](int n) { return (((size_t)bb * NT + n) * dm.H + h) * P + p; };
+  // src and cum_last rows: the workspace's [B][NT][H] order, or the caller's
+  // [B][H][NT] arrays in stage mode
+  auto rows = [&](int n) { return STG ? ((size_t)bh * NT + n) * P + p : rowi(n); };
+  auto cl_at = [&](int n) {
+    return STG ? ck.cum[(((size_t)bh * NT + n) * dm.C + dm.C - 1) * P + p] : ck.cl[rowi(n)];
+  };
 
   float4 st = make_float4(0.f, 0.f, 0.f, 0.f);
   if (init) st = *reinterpret_cast<const float4*>(init + ((size_t)bh * P + p) * N + s0);
-  st.x = sanitize(st.x); st.y = sanitize(st.y); st.z = sanitize(st.z); st.w = sanitize(st.w);
+  if (STG || (!BWD && dm.sanitize_state0)) {
+    st.x = sanitize(st.x); st.y = sanitize(st.y); st.z = sanitize(st.z); st.w = sanitize(st.w);
+  }
 
   constexpr int D = 4;  // chunks in flight
   float4 src[D];
   float cl[D];
-  auto load = [&](int k, int n) {
+  uint2 sp[D];
+  auto load = [&](int k, int it) {
+    const int n = BWD ? NT - 1 - it : it;
+    const size_t ri = rowi(n);
     src[k] = *reinterpret_cast<const float4*>(ck.src + rows(n) * N + s0);
     cl[k] = cl_at(n);
+    if (BWD) sp[k] = *reinterpret_cast<const uint2*>(ck.state_pre + ri * N + s0);
   };
   // Every load is issued on every path (past the last chunk it re-reads that
   // chunk, whose registers are never used), and the loop body runs whole
   // groups of D chunks: the wait before a chunk's use then leaves the other
   // D - 1 chunks' loads in flight.
-  auto step = [&](int k, int n) {
-    const float dce = __expf(fminf(fmaxf(cl[k], -kClipDecay), 0.f));
+  auto step = [&](int k, int it) {
+    const int n = BWD ? NT - 1 - it : it;
+    const size_t ri = rowi(n);
+    const float c = cl[k];
+    const float dce = __expf(fminf(fmaxf(c, -kClipDecay), 0.f));
     f32x4 sv = {st.x, st.y, st.z, st.w};
-    store4(ck.state_pre + rowi(n) * N + s0, sv);
+    store4((BWD ? dstate : ck.state_pre) + ri * N + s0, sv);
+    if (BWD) {
+      const bf16* spv = reinterpret_cast<const bf16*>(&sp[k]);
+      float part = st.x * (float)spv[0] + st.y * (float)spv[1] + st.z * (float)spv[2] +
+                   st.w * (float)spv[3];
+#pragma unroll
+      for (int o = 1; o < TPR; o <<= 1) part += __shfl_xor(part, o);
+      const float msk = (c >= -kClipDecay && c <= 0.f) ? 1.f : 0.f;
+      if (c4 == 0) lasta[ri] = part * dce * msk;
+    }
     st.x = sanitize(st.x * dce + src[k].x);
     st.y = sanitize(st.y * dce + src[k].y);
     st.z = sanitize(st.z * dce + src[k].z);
     st.w = sanitize(st.w * dce + src[k].w);
-    load(k, min(n + D, NT - 1));
+    load(k, min(it + D, NT - 1));
   };
 #pragma unroll
   for (int k = 0; k < D; ++k) load(k, min(k, NT - 1));
-  int n0 = 0;
-  for (; n0 + D <= NT; n0 += D) {
+  int it0 = 0;
+  for (; it0 + D <= NT; it0 += D) {
 #pragma unroll
-    for (int k = 0; k < D; ++k) step(k, n0 + k);
+    for (int k = 0; k < D; ++k) step(k, it0 + k);
   }
 #pragma unroll
   for (int k = 0; k < D; ++k)
-    if (n0 + k < NT) step(k, n0 + k);
-  if (fin) *reinterpret_cast<float4*>(fin + ((size_t)bh * P + p) * N + s0) = st;
+    if (it0 + k < NT) step(k, it0 + k);
+  if (fin) {
+    if (BWD) {  // :264 and the final clip
+      st.x = sanitize(st.x); st.y = sanitize(st.y); st.z = sanitize(st.z); st.w = sanitize(st.w);
+    }
+    *reinterpret_cast<float4*>(fin + ((size_t)bh * P + p) * N + s0) = st;
+  }
 }
 
 // ------------------------------------------------------------------ outputs

@@ -13,9 +13,10 @@ static size_t m2_align(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct Mamba2Plan {
   Mamba2Dims dm;
-  size_t o_cb, o_state, o_cl, o_rows;
+  size_t o_cb, o_state, o_cl, o_rows, o_src;
   size_t o_dstate, o_lasta, o_wr, o_part, o_dap, total;
-  int G;  // head groups of the cross-head dCB reduction
+  int G;       // head groups of the cross-head dCB reduction
+  bool chain;  // state loops with the per-chunk product on chip (else two passes)
 };
 
 static int mamba2_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
@@ -57,14 +58,24 @@ static int mamba2_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
   int G = 1;
   while ((size_t)G * B * NT < 512 && (size_t)(2 * G) <= H && H % (size_t)(2 * G) == 0) G *= 2;
   p->G = G;
+  // The state loops walk the chunks with one 32-channel workgroup per
+  // (batch, head, slice) and form each chunk's product on chip; their step is
+  // latency-bound, so they pay only when the workgroups fill the 256 CUs.
+  // Smaller grids (long sequences over few heads) run the two-pass form: the
+  // chunk kernel writes each chunk's fp32 product and an element-wise pass
+  // with four chunks in flight carries the state (configuration 4, B1 H64
+  // P64 over 256 chunks: 3.15 against 3.37 ms for its Mamba2 fwd + bwd).
+  p->chain = B * H * (P / 32) >= 256;
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += m2_align(bytes); return o; };
   p->o_cb = take(B * NT * C * C * es);
   p->o_state = take(B * NT * H * P * N * es);        // state entering each chunk
   p->o_cl = take(B * NT * H * P * 4);                // cum at each chunk's last row
-  // S rows of the state loops: the forward's dBx dte, then the backward's
-  // Ydh = dy decay_h (a REUSE backward needs only the states and cum_last)
+  // S rows: the state loops' forward dBx dte, then the backward's Ydh =
+  // dy decay_h (a REUSE backward needs only the states and cum_last)
   p->o_rows = take(B * T * H * P * es);
+  // the two-pass form's per-chunk product (forward state_end, backward (dy decay_h)^T C)
+  p->o_src = p->chain ? 0 : take(B * NT * H * P * N * 4);
   p->o_dstate = take(B * NT * H * P * N * es);       // dstate entering each chunk's backward
   p->o_lasta = take(B * NT * H * P * 4);             // d cum_last from decay_chunk_end
   p->o_wr = take(B * T * H * P * es);                // sanitize(dBx decay_to_end)
@@ -81,7 +92,7 @@ static Mamba2Chunks<T> mamba2_chunks(const Mamba2Plan& p, void* ws) {
   c.cb = reinterpret_cast<T*>(base + p.o_cb);
   c.state_pre = reinterpret_cast<T*>(base + p.o_state);
   c.cl = reinterpret_cast<float*>(base + p.o_cl);
-  c.src = nullptr;
+  c.src = p.chain ? nullptr : reinterpret_cast<float*>(base + p.o_src);
   c.cum = nullptr;
   c.ydiag = nullptr;
   return c;
@@ -145,21 +156,47 @@ static int mamba2_forward_impl(const Mamba2Plan& p, const void* dt, const void* 
                          d, (const T*)Bm, (const T*)Cm, ck);
   });
   if (rc) return rc;
-  // the chunk's S rows and cum_last, one workgroup per (batch, chunk, head,
-  // 64 channels) (eight pairs per workgroup: 0.094 against 0.086 ms at the
-  // benchmark shape), then the state loop with S^T B on chip
-  T* srows = reinterpret_cast<T*>(static_cast<char*>(ws) + p.o_rows);
-  rc = L("mamba2_chunk_rows", [&] {
-    constexpr int NPO = P / kOuterPT;
-    hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, 1>),
-                       dim3((unsigned)(d.B * d.NT * d.H * NPO)), dim3(256), 0, st, d, (const T*)dt,
-                       (const T*)x, A, (const T*)nullptr, (const T*)nullptr, ck, srows, (T*)nullptr);
-  });
-  if (rc) return rc;
-  rc = L("mamba2_state_chain", [&] {
-    launch_state_chain<T, C, P, N, false>(d, st, srows, (const T*)Bm, ck, (T*)nullptr, (float*)nullptr,
-                                          state0, state_final);
-  });
+  constexpr int NPO = P / kOuterPT;
+  if (p.chain) {
+    // the chunk's S rows and cum_last, one workgroup per (batch, chunk, head,
+    // 64 channels) (eight pairs per workgroup: 0.094 against 0.086 ms at the
+    // benchmark shape), then the state loop with S^T B on chip
+    T* srows = reinterpret_cast<T*>(static_cast<char*>(ws) + p.o_rows);
+    rc = L("mamba2_chunk_rows", [&] {
+      hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, 1>),
+                         dim3((unsigned)(d.B * d.NT * d.H * NPO)), dim3(256), 0, st, d, (const T*)dt,
+                         (const T*)x, A, (const T*)nullptr, (const T*)nullptr, ck, srows, (T*)nullptr);
+    });
+    if (rc) return rc;
+    rc = L("mamba2_state_chain", [&] {
+      launch_state_chain<T, C, P, N, false>(d, st, srows, (const T*)Bm, ck, (T*)nullptr, (float*)nullptr,
+                                            state0, state_final);
+    });
+  } else {
+    // chunk_outer workgroups take 8 (head, channel slice) pairs of one chunk,
+    // 4 when 8 would leave fewer than two workgroups per CU (0.045 -> 0.039 ms
+    // at B2 T4096 H32 P64), else one head's slices; the backward likewise
+    rc = L("mamba2_chunk_state", [&] {
+      const size_t pairs = (size_t)d.H * NPO;
+      if (pairs % 8 == 0 && d.B * d.NT * pairs / 8 >= kFullGrid)
+        hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, 8, false, true>),
+                           dim3((unsigned)(d.B * d.NT * pairs / 8)), dim3(256), 0, st, d, (const T*)dt,
+                           (const T*)x, A, (const T*)Bm, (const T*)nullptr, ck, (T*)nullptr, (T*)nullptr);
+      else if (pairs % 4 == 0 && d.B * d.NT * pairs / 4 >= kFullGrid)
+        hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, 4, false, true>),
+                           dim3((unsigned)(d.B * d.NT * pairs / 4)), dim3(256), 0, st, d, (const T*)dt,
+                           (const T*)x, A, (const T*)Bm, (const T*)nullptr, ck, (T*)nullptr, (T*)nullptr);
+      else
+        hipLaunchKernelGGL((mamba2_chunk_outer<T, T, C, P, N, kOuterPT, false, NPO, false, true>),
+                           dim3((unsigned)(d.B * d.NT * d.H)), dim3(256), 0, st, d, (const T*)dt,
+                           (const T*)x, A, (const T*)Bm, (const T*)nullptr, ck, (T*)nullptr, (T*)nullptr);
+    });
+    if (rc) return rc;
+    rc = L("mamba2_state_pass", [&] {
+      hipLaunchKernelGGL((mamba2_state_pass<T, P, N, false>), dim3(pass_grid<P, N>(d)), dim3(256), 0, st,
+                         d, ck, (T*)nullptr, (float*)nullptr, state0, state_final);
+    });
+  }
   if (rc || !y) return rc;
   // chunk_y workgroups take SL (head, channel slice) pairs of one chunk: 16
   // when they divide the pairs and the grid still holds two workgroups per
@@ -228,17 +265,40 @@ static int mamba2_backward_t(const Mamba2Plan& p, const void* dt, const void* x,
   Mamba2Chunks<T> ck = mamba2_chunks<T>(p, ws);
   Mamba2Grads<T> gr = mamba2_grads<T>(p, ws);
   hipStream_t st = L.st;
-  rc = L("mamba2_bwd_rows", [&] {
-    constexpr int NPO = P / kOuterPT;
-    hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true, 1>),
-                       dim3((unsigned)(d.B * d.NT * d.H * NPO)), dim3(256), 0, st, d, (const T*)dt,
-                       (const T*)x, A, (const T*)nullptr, (const TD*)dy, ck, gr.ydh, gr.wr);
-  });
-  if (rc) return rc;
-  rc = L("mamba2_bwd_state_chain", [&] {
-    launch_state_chain<T, C, P, N, true>(d, st, gr.ydh, (const T*)Cm, ck, gr.dstate, gr.lasta, dstate_final,
-                                         dstate0);
-  });
+  constexpr int NPO = P / kOuterPT;
+  if (p.chain) {
+    rc = L("mamba2_bwd_rows", [&] {
+      hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true, 1>),
+                         dim3((unsigned)(d.B * d.NT * d.H * NPO)), dim3(256), 0, st, d, (const T*)dt,
+                         (const T*)x, A, (const T*)nullptr, (const TD*)dy, ck, gr.ydh, gr.wr);
+    });
+    if (rc) return rc;
+    rc = L("mamba2_bwd_state_chain", [&] {
+      launch_state_chain<T, C, P, N, true>(d, st, gr.ydh, (const T*)Cm, ck, gr.dstate, gr.lasta,
+                                           dstate_final, dstate0);
+    });
+  } else {
+    rc = L("mamba2_bwd_source", [&] {
+      const size_t pairs = (size_t)d.H * NPO;
+      if (pairs % 8 == 0 && d.B * d.NT * pairs / 8 >= kFullGrid)
+        hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true, 8, false, true>),
+                           dim3((unsigned)(d.B * d.NT * pairs / 8)), dim3(256), 0, st, d, (const T*)dt,
+                           (const T*)x, A, (const T*)Cm, (const TD*)dy, ck, gr.ydh, gr.wr);
+      else if (pairs % 4 == 0 && d.B * d.NT * pairs / 4 >= kFullGrid)
+        hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true, 4, false, true>),
+                           dim3((unsigned)(d.B * d.NT * pairs / 4)), dim3(256), 0, st, d, (const T*)dt,
+                           (const T*)x, A, (const T*)Cm, (const TD*)dy, ck, gr.ydh, gr.wr);
+      else
+        hipLaunchKernelGGL((mamba2_chunk_outer<T, TD, C, P, N, kOuterPT, true, NPO, false, true>),
+                           dim3((unsigned)(d.B * d.NT * d.H)), dim3(256), 0, st, d, (const T*)dt,
+                           (const T*)x, A, (const T*)Cm, (const TD*)dy, ck, gr.ydh, gr.wr);
+    });
+    if (rc) return rc;
+    rc = L("mamba2_bwd_state_pass", [&] {
+      hipLaunchKernelGGL((mamba2_state_pass<T, P, N, true>), dim3(pass_grid<P, N>(d)), dim3(256), 0, st,
+                         d, ck, gr.dstate, gr.lasta, dstate_final, dstate0);
+    });
+  }
   if (rc) return rc;
   rc = L("mamba2_bwd_chunk", [&] {
     hipLaunchKernelGGL((mamba2_bwd_chunk<T, TD, C, P, N>), dim3((unsigned)(d.B * d.NT * p.G)),
@@ -414,8 +474,8 @@ static int mamba2_combine_stage_impl(const Mamba2Plan& p, const float* y_diag, c
   ck.ydiag = y_diag;
   hipStream_t st = L.st;
   int rc = L("mamba2_state_pass", [&] {
-    hipLaunchKernelGGL((mamba2_state_pass<T, P, N>), dim3(pass_grid<P, N>(d)), dim3(256), 0, st, d, ck,
-                       state0, state_final);
+    hipLaunchKernelGGL((mamba2_state_pass<T, P, N, false, true>), dim3(pass_grid<P, N>(d)), dim3(256), 0, st,
+                       d, ck, (T*)nullptr, (float*)nullptr, state0, state_final);
   });
   if (rc) return rc;
   constexpr int NPT = P / kYPT;
