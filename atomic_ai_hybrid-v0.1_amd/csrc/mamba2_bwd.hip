@@ -97,7 +97,11 @@ __device__ __forceinline__ bf16x4 tile_rows4(const bf16* p, int ld, int r0, int 
 template <typename T, int C, int N, int PT, int NTH>
 struct CkLds {
   static constexpr int PAD = Pad<T>::v;
-  static constexpr int LN = N + PAD, LPT = PT + PAD;
+  // state_pre / dstate rows and the CB rows padded by 32 bytes: the y_off /
+  // dwrite and pair-sum fragment reads of 16 rows then spread over the banks
+  // (SQ_LDS_BANK_CONFLICT 3.07e7 -> 1.99e7 per launch against 16-byte pads;
+  // the [C][PT] operand rows keep 16 bytes, which the LDS budget needs)
+  static constexpr int LN = N + 2 * PAD, LPT = PT + PAD;
   // fp32 [C][PT] rows: 16-byte aligned, and rows 4 apart land 16 banks apart
   // (the MFMA tile layout reads 4 row groups x 16 columns)
   static constexpr int LC = PT + 4;
@@ -118,7 +122,7 @@ struct CkLds {
   static constexpr int off_tot = off_cum + C * LC * 4;  // column / block totals
   static_assert(NSEG >= C / 16, "the block totals reuse the column-scan totals");
   static constexpr int off_misc = off_tot + NSEG * PT * 4;   // lasta[PT], lastb[NW][PT], dA[1 + NW]
-  static constexpr int LCB = C + PAD;
+  static constexpr int LCB = C + 2 * PAD;
   static constexpr int off_cb = (off_misc + (PT + NW * PT + 1 + NW) * 4 + 15) / 16 * 16;  // CB [C][LCB]
   static constexpr int off_m = off_cb + C * LCB * (int)sizeof(T);
   static_assert(off_cb % 16 == 0 && off_m % 16 == 0, "16-byte LDS accesses");
