@@ -172,12 +172,18 @@ __device__ __forceinline__ int opaque_zero() {
   return z;
 }
 
-// The same pointer, opaque to the compiler: per-lane addresses built from it
-// stay inside the loop that calls this instead of being hoisted (and kept live).
+// The same global-memory pointer, opaque to the compiler: per-lane addresses
+// built from it stay inside the loop that calls this instead of being hoisted
+// (and kept live).  The barrier is placed on the address-space-1 form, so the
+// loads through the result stay global loads: through a generic pointer they
+// would be flat loads, which also count in lgkmcnt, and every later wait for an
+// LDS or scalar load would then wait for them as well.
 template <typename P>
 __device__ __forceinline__ P* opaque_ptr(P* p) {
-  asm volatile("" : "+s"(p));
-  return p;
+  typedef __attribute__((address_space(1))) P* GP;
+  GP q = (GP)p;
+  asm volatile("" : "+s"(q));
+  return (P*)q;
 }
 
 // f(IntC<i>{}) for a runtime i in [0, N): the body is compiled once per value
