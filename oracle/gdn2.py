@@ -132,24 +132,33 @@ def gdn2_chunked_wy_reference(q, k, v, g, b, w, scale, chunk_size, h0=None,
     return o, h
 
 
-def gdn2_inter_chunk_combine(Aqk, w_pseudo, u, kg, qg, gc_last, scale, h0=None, dtype=torch.float64):
+def gdn2_inter_chunk_combine(Aqk, w_pseudo, u, kg, qg, gc_last, scale, h0=None, dtype=torch.float64,
+                             return_state=False):
     """Kernel D of the staged forward, ``gdn2_inter_chunk_combine``
     (kernel_d_pipeline.py:94-124), over per-chunk arrays in its layout:
     Aqk [B, H, NT, C, C]; w_pseudo, kg, qg [B, H, NT, C, K]; u [B, H, NT, C, V];
     gc_last [B, H, NT, K].  Returns o [B, H, NT, C, V] and h_final.  Unlike the
-    chunked reference it sanitises h0 first (``_sanitize_h0``, :54-55,101)."""
+    chunked reference it sanitises h0 first (``_sanitize_h0``, :54-55,101).
+    With ``return_state`` it also returns the state entering each chunk and
+    v_new, [B, H, NT, K, V] and [B, H, NT, C, V]
+    (``gdn2_inter_chunk_combine_with_state``, :127-158)."""
     f = dtype
     Aqk, w_pseudo, u, kg, qg, gc_last = (t.to(f) for t in (Aqk, w_pseudo, u, kg, qg, gc_last))
     B, H, NT, C, K = w_pseudo.shape
     V = u.shape[-1]
     h = torch.zeros(B, H, K, V, dtype=f) if h0 is None else sanitize(h0.to(f))   # :98-101
-    outs = []
+    outs, pres, vnews = [], [], []
     for n in range(NT):                                                        # :105-123
         h_pre = h
         v_new = u[:, :, n] - w_pseudo[:, :, n] @ h_pre
         o_c = scale * (qg[:, :, n] @ h_pre) + Aqk[:, :, n] @ v_new
         h = sanitize(h_pre * torch.exp(gc_last[:, :, n])[..., None] + kg[:, :, n].transpose(-1, -2) @ v_new)
         outs.append(n2n(o_c))
+        if return_state:
+            pres.append(h_pre)
+            vnews.append(v_new)
+    if return_state:
+        return torch.stack(outs, 2), h, torch.stack(pres, 2), torch.stack(vnews, 2)
     return torch.stack(outs, 2), h
 
 
@@ -427,3 +436,181 @@ def gdn2_backward_chain(q, k, v, w, b, g, scale, chunk_size, do, dh_final=None,
                  stages=st)
     return (res["dq"], res["dk"], res["dv"], res["dw"], res["db"], res["dg"],
             final_sanitize(dh0)), inter
+
+
+# ---------------------------------------------------------------- backward stages
+# The staged backward of the reference's trainable op (kernel_trainable_B6.py:
+# 97-181) at its Pallas block: kernels B2, B1, B3, B4, B5 over per-block
+# arrays [B, H, NT, BT, *].  Each follows its reference kernel's clip /
+# nan_to_num placement; gdn2_backward_staged composes them as _gdn2_core_bwd.
+
+def dav_backward(Aqk, v_new, do, dtype=torch.float64):
+    """Kernel B2, ``dav_backward_pallas`` (kernel_bwd_b2_dav.py:17-51):
+    dAqk = nan_to_num((do v_new^T) * causal), dv_new = nan_to_num(Aqk^T do)."""
+    f = dtype
+    Aqk, v_new, do = (t.to(f) for t in (Aqk, v_new, do))
+    BT = Aqk.shape[-1]
+    causal = torch.tril(torch.ones(BT, BT, dtype=f))                           # :24
+    dAqk = n2n((do @ v_new.transpose(-1, -2)) * causal)                       # :26,29
+    dv_new = n2n(Aqk.transpose(-1, -2) @ do)                                  # :27,30
+    return dAqk, dv_new
+
+
+def dhu_backward(do, dv_partial, w_pseudo, qg, kg, gc_last, scale, dht=None, dtype=torch.float64):
+    """Kernel B1, ``gdn2_dhu_backward`` (kernel_bwd_b1_dhu.py:14-44): the
+    reverse scan over blocks.  Returns ``(dh_all, dh0, dv_all)``: dh_all[:, :, n]
+    is the carry after block n, i.e. the gradient of the state entering it."""
+    f = dtype
+    do, dvp, wp, qg, kg, gcl = (t.to(f) for t in (do, dv_partial, w_pseudo, qg, kg, gc_last))
+    B, H, NT, BT, K = qg.shape
+    V = do.shape[-1]
+    dh = torch.zeros(B, H, K, V, dtype=f) if dht is None else dht.to(f)        # :16-17
+    dh = sanitize(dh)                                                         # :18
+    dh_all, dv_all = [None] * NT, [None] * NT
+    for n in reversed(range(NT)):                                             # :42
+        decay = torch.exp(gcl[:, :, n])[..., None]                            # :24
+        from_out = qg[:, :, n].transpose(-1, -2) @ (scale * do[:, :, n])      # :26-27
+        from_state = dh * decay                                               # :28
+        dv_new = sanitize(dvp[:, :, n] + kg[:, :, n] @ dh)                    # :30-32
+        from_vnew = -(wp[:, :, n].transpose(-1, -2) @ dv_new)                 # :34
+        dh = sanitize(from_out + from_state + from_vnew)                      # :36-37
+        dh_all[n], dv_all[n] = dh, dv_new                                     # :39
+    return torch.stack(dh_all, 2), dh, torch.stack(dv_all, 2)
+
+
+def wy_dqkg_backward(q, k, b, w, v, gc, A, Akk, h_pre, v_new, do, dv, dh_next, scale,
+                     dtype=torch.float64):
+    """Kernel B3, ``wy_dqkg_backward_pallas`` (kernel_bwd_b3_wy_dqkg.py:33-148):
+    per block, the gradients through w_pseudo, u, kg, qg and the inverse
+    A = (I + Akk)^-1, with dA_total and tmp clipped before the two products
+    through A^T (:82-91).  Akk only fixes the shape.  Returns a dict of dq, dk,
+    db, dw, dv_raw, dgc (each nan_to_num'd) and dAkk."""
+    f = dtype
+    q, k, b, w, v, gc, A = (t.to(f) for t in (q, k, b, w, v, gc, A))
+    h_pre, v_new, do, dv, dh_next = (t.to(f) for t in (h_pre, v_new, do, dv, dh_next))
+    BT = A.shape[-1]
+    gcl = gc[..., BT - 1, :]                                                  # :53
+    egc = torch.exp(gc)
+    kb = b * k * egc                                                          # :55
+    ekg = torch.exp(gcl[..., None, :] - gc)
+    kg = k * ekg                                                              # :56
+    qg = q * egc                                                              # :57
+    wv = w * v                                                                # :58
+    dqg = (scale * do) @ h_pre.transpose(-1, -2)                              # :60-61
+    dw_pseudo = (-dv) @ h_pre.transpose(-1, -2)                               # :63-64
+    du = dv                                                                   # :65
+    dkg = v_new @ dh_next.transpose(-1, -2)                                   # :67
+    dA_from_w = dw_pseudo @ kb.transpose(-1, -2)                              # :69
+    dkb = A.transpose(-1, -2) @ dw_pseudo                                     # :70
+    dA_from_u = du @ wv.transpose(-1, -2)                                     # :72
+    dwv = A.transpose(-1, -2) @ du                                            # :73
+    dA_total = sanitize(dA_from_w + dA_from_u)                                # :75,78
+    strict = torch.tril(torch.ones(BT, BT, dtype=f), diagonal=-1)             # :80-81
+    tmp = sanitize(dA_total @ A.transpose(-1, -2))                            # :83-84
+    dAkk = -(A.transpose(-1, -2) @ tmp) * strict                              # :85-86
+    dk_from_kb = dkb * egc * b                                                # :88
+    db_ = dkb * egc * k                                                       # :89
+    dgc_from_kb = dkb * kb                                                    # :90
+    dx = dkg * kg                                                             # :92
+    dk_from_kg = dkg * ekg                                                    # :93
+    dgc_last_contrib = dx.sum(-2)                                             # :95
+    dq = dqg * egc                                                            # :97
+    dgc_from_qg = dqg * qg                                                    # :98
+    dw_ = dwv * v                                                             # :100
+    dv_raw = dwv * w                                                          # :101
+    dk = dk_from_kb + dk_from_kg                                              # :103
+    dgc = dgc_from_kb + dgc_from_qg - dx                                      # :94,104
+    dgc_last_from_decay = torch.exp(gcl) * (dh_next * h_pre).sum(-1)          # :106-107
+    dgc = dgc.clone()
+    dgc[..., BT - 1, :] = dgc[..., BT - 1, :] + dgc_last_contrib + dgc_last_from_decay   # :108-111
+    return dict(dq=n2n(dq), dk=n2n(dk), db=n2n(db_), dw=n2n(dw_), dv_raw=n2n(dv_raw),
+                dgc=n2n(dgc), dAkk=n2n(dAkk))                                 # :113-119
+
+
+def intra_backward(dAqk, dAkk, q, k, b, g, scale, sub=128, dtype=torch.float64):
+    """Kernel B4, ``intra_backward_pallas`` (kernel_bwd_b4_intra.py:57-165):
+    the backward of kernel A over its ``sub``-row sub-block pairs (si >= sj),
+    pairwise exp(clip(gc_i - gc_j, +-20)) with the clip mask on the dgc terms,
+    causal / strict masks on diagonal sub-blocks, and a clip to +-1e4 after
+    every accumulation (:113-121).  q, k, b, g [B, T, H, D]; dAqk, dAkk
+    [B, H, NT, BT, BT].  Returns dq, dk, db, dgc [B, H, NT, BT, D]."""
+    f = dtype
+    BT = dAqk.shape[-1]
+    q_, k_, b_, g_ = (_blocks(t.to(f), BT) for t in (q, k, b, g))
+    dAqk, dAkk = dAqk.to(f), dAkk.to(f)
+    gc = torch.cumsum(g_, dim=-2)                                              # :66-68
+    bk = b_ * k_                                                               # :70
+    dq = torch.zeros_like(q_)
+    dk = torch.zeros_like(q_)
+    dbk = torch.zeros_like(q_)
+    dgc = torch.zeros_like(q_)
+    idx = torch.arange(sub)
+    causal = (idx[:, None] >= idx[None, :]).to(f)
+    strict = (idx[:, None] > idx[None, :]).to(f)
+    for si in range(BT // sub):                                                # :77-78
+        for sj in range(si + 1):
+            i0, j0 = si * sub, sj * sub
+            I, J = slice(i0, i0 + sub), slice(j0, j0 + sub)
+            dd = gc[..., I, None, :] - gc[..., None, J, :]                      # :89
+            cm = ((dd >= -CLIP_DECAY) & (dd <= CLIP_DECAY)).to(f)               # :90
+            e = torch.exp(torch.clamp(dd, -CLIP_DECAY, CLIP_DECAY))             # :91
+            mqk, mkk = dAqk[..., I, J], dAkk[..., I, J]
+            if si == sj:                                                      # :95-99
+                mqk, mkk = mqk * causal, mkk * strict
+            Lqk, Rk, Lkk = scale * q_[..., I, :], k_[..., J, :], bk[..., I, :]
+            wq = mqk[..., None] * e                                           # dM * edecay
+            wk = mkk[..., None] * e
+            dL_qk = (wq * Rk[..., None, :, :]).sum(-2)                        # :38-41,103
+            dR_qk = (wq * Lqk[..., :, None, :]).sum(-3)                       # :44-47,104
+            gq = wq * Lqk[..., :, None, :] * Rk[..., None, :, :] * cm          # :50-54,105
+            dL_kk = (wk * Rk[..., None, :, :]).sum(-2)                        # :109
+            dR_kk = (wk * Lkk[..., :, None, :]).sum(-3)                       # :110
+            gk = wk * Lkk[..., :, None, :] * Rk[..., None, :, :] * cm          # :111
+            dq[..., I, :] = sanitize(dq[..., I, :] + dL_qk * scale)            # :117
+            dbk[..., I, :] = sanitize(dbk[..., I, :] + dL_kk)                 # :118
+            dk[..., J, :] = sanitize(dk[..., J, :] + dR_qk + dR_kk)           # :119
+            dgc[..., I, :] = sanitize(dgc[..., I, :] + gq.sum(-2) + gk.sum(-2))      # :120
+            dgc[..., J, :] = sanitize(dgc[..., J, :] - gq.sum(-3) - gk.sum(-3))      # :121
+    dk_f = dk + dbk * b_                                                       # :124
+    db_f = dbk * k_                                                            # :125
+    return sanitize(dq), sanitize(dk_f), sanitize(db_f), sanitize(dgc)         # :129-132
+
+
+def reverse_cumsum_bwd(dgc, chunk_size):
+    """Kernel B5, ``reverse_cumsum_bwd`` (kernel_bwd_b5_reverse_cumsum.py:17-24):
+    the suffix sum over each block's rows, clipped to +-1e4."""
+    return sanitize(torch.flip(torch.cumsum(torch.flip(dgc, [-2]), -2), [-2]))
+
+
+def _unblocks(t):
+    """[B, H, NT, BT, D] -> [B, T, H, D] (_reshape_out, kernel_trainable_B6.py)."""
+    B, H, NT, BT, D = t.shape
+    return t.permute(0, 2, 3, 1, 4).reshape(B, NT * BT, H, D)
+
+
+def gdn2_backward_staged(q, k, v, w, b, g, scale, do, dh_final=None, h0=None, block=256,
+                         dtype=torch.float64):
+    """``_gdn2_core_bwd`` (kernel_trainable_B6.py:97-181) from the stage
+    restatements: kernels A, B, C, D-with-state, then B2, B1, B3, B4, B5 and
+    the final sanitise.  Drop-in argument order; returns
+    ``(dq, dk, dv, dw, db, dg, dh0)``."""
+    f = dtype
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    Aqk, Akk = chunk_scores(q, k, b, g, scale, block=block, dtype=f)
+    A = wy_solve_blocked(Akk)
+    wp, u, kg, qg, gcl = recompute_wy(q, k, v, w, b, g, A, dtype=f)
+    _, _, h_pre, v_new = gdn2_inter_chunk_combine(Aqk, wp, u, kg, qg, gcl, scale, h0=h0, dtype=f,
+                                                  return_state=True)
+    gc = torch.cumsum(_blocks(g.to(f), block), dim=-2)                          # :116-118
+    q_r, k_r, b_r, w_r, v_r, do_r = (_blocks(t.to(f), block) for t in (q, k, b, w, v, do))
+    dAqk, dv_partial = dav_backward(Aqk, v_new, do_r, dtype=f)                  # :127
+    dht = torch.zeros(B, H, K, V, dtype=f) if dh_final is None else dh_final.to(f)
+    dh_all, dh0, dv_all = dhu_backward(do_r, dv_partial, wp, qg, kg, gcl, scale, dht=dht, dtype=f)
+    dh_next = torch.cat([dh_all[:, :, 1:], dht[:, :, None]], dim=2)             # :80-83,130
+    b3 = wy_dqkg_backward(q_r, k_r, b_r, w_r, v_r, gc, A, Akk, h_pre, v_new, do_r, dv_all, dh_next,
+                          scale, dtype=f)
+    dq4, dk4, db4, dgc4 = intra_backward(dAqk, b3["dAkk"], q, k, b, g, scale, dtype=f)
+    dg = reverse_cumsum_bwd(b3["dgc"] + dgc4, block)                            # :142-143
+    outs = (b3["dq"] + dq4, b3["dk"] + dk4, b3["dv_raw"], b3["dw"], b3["db"] + db4, dg)
+    return tuple(final_sanitize(_unblocks(t)) for t in outs) + (final_sanitize(dh0),)

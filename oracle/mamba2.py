@@ -344,3 +344,77 @@ def chunk_ssd_bwd_scan(dt, A, Bm, Cm, x, chunk_size, do, dstate_final=None, stat
 def final_sanitize(x):
     """``_final_sanitize`` at the custom_vjp boundary (kernel_mamba2_trainable_B6.py:67-69)."""
     return sanitize(x, CLIP_ACC)
+
+
+def intra_chunk_ssd_bwd(dt, x, Bm, Cm, cumdecay, dy, dstate_end_grad, chunk_size, dtype=torch.float64):
+    """MB2, ``intra_chunk_ssd_bwd_pallas`` (kernel_mamba2_bwd_b2_intra.py:32-180):
+    the backward of M3 (y_diag, state_end) per (batch, head, chunk), with the
+    state-end part as full-chunk products (:53-66), the y_diag part over
+    ``min(128, C)``-row sub-block pairs with a sanitise after every
+    accumulation (:74-113), and dB / dC summed over the heads after the
+    per-head sanitised values (:168-178).  dt, x, dy [b, l, h, p]; Bm, Cm
+    [b, l, n]; cumdecay [b, h, NT, C, p]; dstate_end_grad [b, h, NT, p, n].
+    Returns ``(ddt [b, l, h, p], dx [b, l, h, p], dB [b, l, n], dC [b, l, n],
+    dcum [b, h, NT, C, p])``."""
+    f = dtype
+    C = chunk_size
+    bc = min(128, C)                                                            # :20-21,35
+    dtc, xc, dyc = (_stage_chunks(t.to(f), C) for t in (dt, x, dy))            # [b, h, nt, C, p]
+    b, h, nt = dtc.shape[:3]
+    n = Bm.shape[-1]
+    Bc = Bm.to(f).reshape(b, nt, C, n)[:, None].expand(b, h, nt, C, n)          # :145-148
+    Cc = Cm.to(f).reshape(b, nt, C, n)[:, None].expand(b, h, nt, C, n)
+    cum = cumdecay.to(f)
+    dse = dstate_end_grad.to(f)                                                 # [b, h, nt, p, n]
+    dBx = sanitize(dtc * xc)                                                    # :47
+    BC_inner = sanitize(Cc @ Bc.transpose(-1, -2))                              # :48
+    cl = cum[..., C - 1:, :]                                                    # :50
+    dte_raw = cl - cum                                                          # :51
+    dte = torch.exp(torch.clamp(dte_raw, -CLIP_STEP, CLIP_STEP))                # :52
+    write = sanitize(dBx * dte)                                                 # :53
+    dwrite = sanitize(Bc @ dse.transpose(-1, -2))                               # :56  (C, p)
+    dB = sanitize(write @ dse)                                                  # :57  (C, n)
+    d_dBx_1 = sanitize(dwrite * dte)                                            # :59
+    d_dte = sanitize(dwrite * dBx)                                              # :60
+    d_dte_diff = sanitize(d_dte * dte * clip_mask(dte_raw, -CLIP_STEP, CLIP_STEP))   # :61-63
+    dcum_from_dte = -d_dte_diff                                                 # :64
+    dcum_last_b = d_dte_diff.sum(-2)                                            # :65
+    d_dBx_2 = torch.zeros_like(dtc)                                             # :68
+    dC = torch.zeros_like(Bc)                                                   # :70
+    dcum = torch.zeros_like(dtc)                                                # :71
+    idx = torch.arange(bc)
+    causal = (idx[:, None] >= idx[None, :]).to(f)
+    for si in range(C // bc):                                                   # :73-74
+        for sj in range(si + 1):
+            I, J = slice(si * bc, (si + 1) * bc), slice(sj * bc, (sj + 1) * bc)
+            dd = cum[..., I, None, :] - cum[..., None, J, :]                    # :80
+            e = torch.exp(torch.clamp(dd, -CLIP_STEP, CLIP_STEP))               # :81
+            blk = BC_inner[..., I, J]
+            if si == sj:                                                      # :84-87
+                blk = blk * causal
+            weight = e * blk[..., None]                                       # :89
+            dy_i, dbx_j = dyc[..., I, :], dBx[..., J, :]
+            dweight = dy_i[..., :, None, :] * dbx_j[..., None, :, :]           # :94
+            d_dBx_2_blk = torch.einsum("...ijd,...id->...jd", weight, dy_i)   # :95
+            dedecay = dweight * blk[..., None]                                # :97
+            dBC_blk = (dweight * e).sum(-1)                                   # :98
+            if si == sj:                                                      # :99-100
+                dBC_blk = dBC_blk * causal
+            dC_blk = dBC_blk @ Bc[..., J, :]                                  # :102
+            dB_blk = dBC_blk.transpose(-1, -2) @ Cc[..., I, :]                # :103
+            ddd = dedecay * e * clip_mask(dd, -CLIP_STEP, CLIP_STEP)          # :105
+            d_dBx_2[..., J, :] = sanitize(d_dBx_2[..., J, :] + d_dBx_2_blk)   # :109
+            dB[..., J, :] = sanitize(dB[..., J, :] + dB_blk)                  # :110
+            dC[..., I, :] = sanitize(dC[..., I, :] + dC_blk)                  # :111
+            dcum[..., I, :] = sanitize(dcum[..., I, :] + ddd.sum(-2))         # :106,112
+            dcum[..., J, :] = sanitize(dcum[..., J, :] - ddd.sum(-3))         # :107,113
+    d_dBx = sanitize(d_dBx_1 + d_dBx_2)                                         # :116
+    ddt = sanitize(d_dBx * xc)                                                  # :118,126
+    dx = sanitize(d_dBx * dtc)                                                  # :119,127
+    dcum = dcum + dcum_from_dte                                                 # :121
+    dcum = dcum.clone()
+    dcum[..., C - 1, :] = dcum[..., C - 1, :] + dcum_last_b                     # :122-123
+    dcum = sanitize(dcum)                                                       # :128
+    dB_out = dB.sum(1).reshape(b, nt * C, n)                                    # :176-178
+    dC_out = dC.sum(1).reshape(b, nt * C, n)
+    return _stage_unchunk(ddt), _stage_unchunk(dx), dB_out, dC_out, dcum
