@@ -224,6 +224,13 @@ _SIGS = {
     "atomic_gdn2_chunk_scores": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 6 + [_P]),
     "atomic_gdn2_wy_solve": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 2 + [_P]),
     "atomic_gdn2_recompute_wy": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 12 + [_P]),
+    "atomic_gdn2_dav_backward": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 5 + [_P]),
+    "atomic_gdn2_dhu_backward": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 10 + [_P]),
+    "atomic_gdn2_wy_dqkg_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(Gdn2Args)]),
+    "atomic_gdn2_wy_dqkg_backward": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 19
+                                     + [_P, ctypes.c_size_t, _P]),
+    "atomic_gdn2_intra_backward": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 10 + [_P]),
+    "atomic_gdn2_reverse_cumsum_bwd": (ctypes.c_int, [ctypes.POINTER(Gdn2Args)] + [_P] * 2 + [_P]),
     "atomic_mamba2_proj_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(Mamba2ProjArgs), ctypes.c_int]),
     "atomic_mamba2_proj_fwd": (ctypes.c_int, [ctypes.POINTER(Mamba2ProjArgs)] + [_P] * 16 + [_P, ctypes.c_size_t, _P]),
     "atomic_mamba2_proj_bwd": (ctypes.c_int, [ctypes.POINTER(Mamba2ProjArgs)] + [_P] * 24 + [_P, ctypes.c_size_t, _P]),

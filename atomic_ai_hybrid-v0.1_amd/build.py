@@ -19,7 +19,8 @@ LIB = os.path.join(OUT_DIR, "libatomic_hybrid.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 
 # translation units (each includes the kernel sources it launches)
-UNITS = ["gdn2_host.hip", "mamba2_host.hip", "norm_gate.hip", "prologue.hip", "stage256.hip"]
+UNITS = ["gdn2_host.hip", "mamba2_host.hip", "norm_gate.hip", "prologue.hip", "stage256.hip",
+         "stage256_bwd.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -809,3 +809,84 @@ extern "C" int atomic_gdn2_fwd_noalloc(const atomic_gdn2_args* a, const void* q,
   if (!q || !k || !v || !w || !b || !g || !o || !h_final) return ATOMIC_ERR_NULL;
   return gdn2_forward_noalloc(a, q, k, v, w, b, g, h0, o, h_final, (hipStream_t)stream);
 }
+
+// ------------------------------------------------------------------ backward stages (256-row blocks)
+// The staged backward of kernel_trainable_B6.py:97-181 at the reference's
+// block: chunk must be 256; every per-block array is float32.
+
+static int gdn2_bwd_stage_plan(const atomic_gdn2_args* a, Gdn2Plan* p) {
+  const int rc = gdn2_stage_plan(a, p);
+  if (rc != ATOMIC_OK) return rc;
+  return a->chunk == kStageBlock ? ATOMIC_OK : ATOMIC_ERR_SHAPE;
+}
+
+extern "C" int atomic_gdn2_dav_backward(const atomic_gdn2_args* a, const float* Aqk, const float* v_new,
+                                        const void* dO, float* dAqk, float* dv_new, void* stream) {
+  Gdn2Plan p;
+  const int rc = gdn2_bwd_stage_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!Aqk || !v_new || !dO || !dAqk || !dv_new) return ATOMIC_ERR_NULL;
+  Launch L{a->profile, (hipStream_t)stream};
+  return g256_dav_bwd(gdn2_dims256(p), a->do_dtype, Aqk, v_new, dO, dAqk, dv_new, L);
+}
+
+extern "C" int atomic_gdn2_dhu_backward(const atomic_gdn2_args* a, const void* dO, const float* dv_partial,
+                                        const float* w_pseudo, const float* qg, const float* kg,
+                                        const float* gc_last, const float* dht, float* dh_all, float* dh0,
+                                        float* dv_all, void* stream) {
+  Gdn2Plan p;
+  const int rc = gdn2_bwd_stage_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!dO || !dv_partial || !w_pseudo || !qg || !kg || !gc_last || !dh_all || !dh0 || !dv_all)
+    return ATOMIC_ERR_NULL;
+  Launch L{a->profile, (hipStream_t)stream};
+  return g256_dhu_bwd(gdn2_dims256(p), a->do_dtype, dO, dv_partial, w_pseudo, qg, kg, gc_last, dht, dh_all, dh0,
+                      dv_all, L);
+}
+
+extern "C" size_t atomic_gdn2_wy_dqkg_workspace_size(const atomic_gdn2_args* a) {
+  Gdn2Plan p;
+  if (gdn2_bwd_stage_plan(a, &p) != ATOMIC_OK) return 0;
+  return g256_b3_ws(gdn2_dims256(p));
+}
+
+extern "C" int atomic_gdn2_wy_dqkg_backward(const atomic_gdn2_args* a, const void* q, const void* k, const void* b,
+                                            const void* w, const void* v, const float* gc, const float* A,
+                                            const float* h_pre, const float* v_new, const void* dO,
+                                            const float* dv, const float* dh_next, float* dq, float* dk, float* db,
+                                            float* dw, float* dv_raw, float* dgc, float* dAkk, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+  Gdn2Plan p;
+  const int rc = gdn2_bwd_stage_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!q || !k || !b || !w || !v || !gc || !A || !h_pre || !v_new || !dO || !dv || !dh_next || !dq || !dk || !db ||
+      !dw || !dv_raw || !dgc || !dAkk)
+    return ATOMIC_ERR_NULL;
+  const Gdn2Dims d = gdn2_dims256(p);
+  if (!workspace || workspace_bytes < g256_b3_ws(d)) return ATOMIC_ERR_WORKSPACE;
+  Launch L{a->profile, (hipStream_t)stream};
+  return g256_b3_bwd(d, a->dtype, a->do_dtype, q, k, b, w, v, gc, A, h_pre, v_new, dO, dv, dh_next, dq, dk, db, dw,
+                     dv_raw, dgc, dAkk, static_cast<float*>(workspace), L);
+}
+
+extern "C" int atomic_gdn2_intra_backward(const atomic_gdn2_args* a, const float* dAqk, const float* dAkk,
+                                          const void* q, const void* k, const void* b, const float* g, float* dq,
+                                          float* dk, float* db, float* dgc, void* stream) {
+  Gdn2Plan p;
+  const int rc = gdn2_bwd_stage_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!dAqk || !dAkk || !q || !k || !b || !g || !dq || !dk || !db || !dgc) return ATOMIC_ERR_NULL;
+  Launch L{a->profile, (hipStream_t)stream};
+  return g256_intra_bwd(gdn2_dims256(p), a->dtype, dAqk, dAkk, q, k, b, g, dq, dk, db, dgc, L);
+}
+
+extern "C" int atomic_gdn2_reverse_cumsum_bwd(const atomic_gdn2_args* a, const float* dgc, float* dg,
+                                              void* stream) {
+  Gdn2Plan p;
+  const int rc = gdn2_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!dgc || !dg) return ATOMIC_ERR_NULL;
+  Launch L{a->profile, (hipStream_t)stream};
+  const long long blocks = (long long)a->batch * a->heads * (a->seqlen / a->chunk);
+  return rev_cumsum_bwd(dgc, dg, blocks, a->chunk, a->dk, L);
+}

@@ -34,4 +34,28 @@ int m256_combine(const Mamba2Dims& d, const float* y_diag, const float* state_en
                  const void* Cm, const float* state0, float* y, float* state_final, float* ws, Launch& L);
 size_t m256_combine_ws(const Mamba2Dims& d);
 
+// Backward stages (stage256_bwd.hip), GDN2 dims as above; dO is of type
+// do_dtype, q, k, b, w, v of type dtype, every other array fp32:
+//   B2  dAqk [B][H][NT][256][256], dv_new [B][H][NT][256][V]
+//   B1  dh_all [B][H][NT][K][V], dh0 [B][H][K][V], dv_all like dv_new
+//   B3  per-block q, k, b, w, v, gc, dO, dv [B][H][NT][256][D], A
+//       [B][H][NT][256][256], h_pre / dh_next [B][H][NT][K][V]; workspace
+//       g256_b3_ws bytes
+//   B4  q, k, b, g [B][T][H][K] (row strides of the dims), outputs per block
+//   B5  dg of a [blocks][rows][cols] array
+int g256_dav_bwd(const Gdn2Dims& d, int do_dtype, const float* aqk, const float* v_new, const void* dO,
+                 float* daqk, float* dvn, Launch& L);
+int g256_dhu_bwd(const Gdn2Dims& d, int do_dtype, const void* dO, const float* dvp, const float* wp,
+                 const float* qg, const float* kg, const float* gcl, const float* dht, float* dh_all, float* dh0,
+                 float* dv_all, Launch& L);
+size_t g256_b3_ws(const Gdn2Dims& d);
+int g256_b3_bwd(const Gdn2Dims& d, int dtype, int do_dtype, const void* q, const void* k, const void* b,
+                const void* w, const void* v, const float* gc, const float* A, const float* h_pre,
+                const float* v_new, const void* dO, const float* dv, const float* dh_next, float* dq, float* dk,
+                float* db, float* dw, float* dvr, float* dgc, float* dakk, float* ws, Launch& L);
+int g256_intra_bwd(const Gdn2Dims& d, int dtype, const float* daqk, const float* dakk, const void* q,
+                   const void* k, const void* b, const float* g, float* dq, float* dk, float* db, float* dgc,
+                   Launch& L);
+int rev_cumsum_bwd(const float* dgc, float* dg, long long blocks, int rows, int cols, Launch& L);
+
 }  // namespace ah

@@ -1,0 +1,550 @@
+// Stage-level backward kernels at the reference's 256-row Pallas block.
+//
+// The reference's trainable ops run their backward as separate staged
+// functions over per-block float32 arrays (kernel_trainable_B6.py:97-181):
+//   GDN2 B2  dav_backward_pallas           (kernel_bwd_b2_dav.py:17-51)
+//        B1  gdn2_dhu_backward             (kernel_bwd_b1_dhu.py:14-44)
+//        B3  wy_dqkg_backward_pallas       (kernel_bwd_b3_wy_dqkg.py:33-148)
+//        B4  intra_backward_pallas         (kernel_bwd_b4_intra.py:57-165)
+//        B5  reverse_cumsum_bwd            (kernel_bwd_b5_reverse_cumsum.py:17-24)
+//   Mamba2 MB2 intra_chunk_ssd_bwd_pallas  (kernel_mamba2_bwd_b2_intra.py:32-180)
+// The whole path fuses these into its own kernels at 64 / 128-row chunks;
+// the kernels here give each staged function with its own inputs, outputs
+// and clip / nan_to_num placement.  Every value is float32 (the reference
+// upcasts on entry).  They are the drop-in stage functions, not the
+// benchmark path: block products run on a float32 LDS-tiled GEMM, and the
+// pairwise-decay sums of B4 and MB2 are evaluated pair by pair on the vector
+// ALUs with exp(clip(., +-20)) as the reference does.
+#include "../../include/atomic_hybrid.h"
+#include "common.hpp"
+#include "stage256.hpp"
+
+namespace ah {
+
+namespace {
+
+// A read-only operand of either element type.
+struct In {
+  const void* p;
+  int bf;  // 1: bf16, 0: fp32
+};
+__device__ __forceinline__ float ld(const In& a, size_t i) {
+  return a.bf ? to_f(reinterpret_cast<const bf16*>(a.p)[i]) : reinterpret_cast<const float*>(a.p)[i];
+}
+
+// Offset of batch item z = (z2 * Z1 + z1) * Z0 + z0 in an operand.
+struct Bat {
+  long long s2, s1, s0;
+};
+__device__ __forceinline__ size_t bat_off(const Bat& s, int z, int Z1, int Z0) {
+  const int z0 = z % Z0, z1 = (z / Z0) % Z1, z2 = z / (Z0 * Z1);
+  return (size_t)((long long)z2 * s.s2 + (long long)z1 * s.s1 + (long long)z0 * s.s0);
+}
+
+__device__ __forceinline__ float n2n_acc(float x) { return n2n(x, 1e4f); }
+
+// ------------------------------------------------------------------ GEMM
+// C(m, n) [op]= alpha sum_k A(m, k) B(k, n) per batch item, float32
+// accumulation.  A(m, k) = ta ? A[k lda + m] : A[m lda + k]; likewise B.
+// Epilogue: accum adds the previous C, then mask (1: keep m >= n, 2: keep
+// m > n; masked entries are 0), then post (1: nan_to_num with +-1e4 for
+// +-inf, 2: clip to +-1e4 and nan_to_num).
+struct GemmOp {
+  int M, N, K, Z1, Z0;
+  In A;
+  long long lda;
+  Bat sa;
+  int ta;
+  In B;
+  long long ldb;
+  Bat sb;
+  int tb;
+  float* C;
+  long long ldc;
+  Bat sc;
+  float alpha;
+  int accum, mask, post;
+};
+
+constexpr int GT = 64, GK = 16;
+
+__global__ __launch_bounds__(256) void sb_gemm_k(GemmOp g) {
+  __shared__ __attribute__((aligned(16))) float sA[GK][GT + 4];
+  __shared__ __attribute__((aligned(16))) float sB[GK][GT + 4];
+  const int z = blockIdx.z;
+  const int m0 = blockIdx.y * GT, n0 = blockIdx.x * GT;
+  const int t = threadIdx.x, tx = t % 16, ty = t / 16;
+  const size_t oa = bat_off(g.sa, z, g.Z1, g.Z0), ob = bat_off(g.sb, z, g.Z1, g.Z0);
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+  for (int k0 = 0; k0 < g.K; k0 += GK) {
+#pragma unroll
+    for (int it = 0; it < GT * GK / 256; ++it) {
+      const int e = t + 256 * it;
+      const int mm = g.ta ? e % GT : e / GK, kk = g.ta ? e / GT : e % GK;
+      const int m = m0 + mm, k = k0 + kk;
+      sA[kk][mm] = (m < g.M && k < g.K)
+                       ? ld(g.A, oa + (g.ta ? (size_t)k * g.lda + m : (size_t)m * g.lda + k))
+                       : 0.f;
+      const int nn = g.tb ? e / GK : e % GT, kb = g.tb ? e % GK : e / GT;
+      const int n = n0 + nn, kq = k0 + kb;
+      sB[kb][nn] = (n < g.N && kq < g.K)
+                       ? ld(g.B, ob + (g.tb ? (size_t)n * g.ldb + kq : (size_t)kq * g.ldb + n))
+                       : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < GK; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = sA[kk][ty + 16 * i];
+      const float4 bv = *reinterpret_cast<const float4*>(&sB[kk][4 * tx]);
+      b[0] = bv.x; b[1] = bv.y; b[2] = bv.z; b[3] = bv.w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+  const size_t oc = bat_off(g.sc, z, g.Z1, g.Z0);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + ty + 16 * i;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + 4 * tx + j;
+      if (m >= g.M || n >= g.N) continue;
+      const size_t o = oc + (size_t)m * g.ldc + n;
+      float v = g.alpha * acc[i][j];
+      if (g.accum) v = g.C[o] + v;
+      if ((g.mask == 1 && n > m) || (g.mask == 2 && n >= m)) v = 0.f;
+      if (g.post == 1) v = n2n_acc(v);
+      else if (g.post == 2) v = sanitize(v);
+      g.C[o] = v;
+    }
+  }
+}
+
+int gemm(const GemmOp& g, int batch, const char* name, Launch& L) {
+  if (batch <= 0 || batch > 65535 || g.M <= 0 || g.N <= 0 || g.K <= 0) return ATOMIC_ERR_SHAPE;
+  const dim3 grid((g.N + GT - 1) / GT, (g.M + GT - 1) / GT, batch);
+  return L(name, [&] { hipLaunchKernelGGL(sb_gemm_k, grid, dim3(256), 0, L.st, g); });
+}
+
+// A dense [Z][rows][cols] operand: plain batch stride rows * cols.
+Bat dense(long long rows, long long cols) { return Bat{0, 0, rows * cols}; }
+
+GemmOp gemm_op(int M, int N, int K, int Z) {
+  GemmOp g{};
+  g.M = M; g.N = N; g.K = K; g.Z1 = 1; g.Z0 = Z;
+  g.alpha = 1.f;
+  return g;
+}
+
+// ------------------------------------------------------------------ GDN2 B1
+// Reverse scan per (batch, head, 32-column V tile): dh [K][32] in LDS; per
+// block the rows go in 32-row pieces: dv_new = sanitize(dv_partial + kg dh),
+// then from_out += qg^T (scale dO) and from_vnew += w_pseudo^T dv_new; at the
+// block's end dh = sanitize(from_out + dh e^{gc_last} - from_vnew)
+// (kernel_bwd_b1_dhu.py:22-39).
+template <int K>
+__global__ __launch_bounds__(256) void g256_dhu_k(Gdn2Dims d, In dO, const float* __restrict__ dvp,
+                                                  const float* __restrict__ wp, const float* __restrict__ qg,
+                                                  const float* __restrict__ kg, const float* __restrict__ gcl,
+                                                  const float* __restrict__ dht, float* __restrict__ dh_all,
+                                                  float* __restrict__ dh0, float* __restrict__ dv_all) {
+  constexpr int VT = 32, RB = 32, KR = K / 8, LKP = K + 1;
+  __shared__ float sDh[K][VT + 1];
+  __shared__ float sKg[RB][LKP], sQg[RB][LKP], sWp[RB][LKP];
+  __shared__ float sDo[RB][VT + 1], sDvn[RB][VT + 1];
+  const int t = threadIdx.x, c = t % VT, kr = t / VT;  // this thread: column c, rows kr + 8 i of dh
+  const int nvt = d.V / VT;
+  const int bh = blockIdx.x / nvt, v0 = (blockIdx.x % nvt) * VT;
+  const int V = d.V;
+  // dht sanitised (kernel_bwd_b1_dhu.py:16-18)
+  for (int i = 0; i < KR; ++i) {
+    const int k = kr + 8 * i;
+    sDh[k][c] = dht ? sanitize(dht[((size_t)bh * K + k) * V + v0 + c]) : 0.f;
+  }
+  __syncthreads();
+  for (int n = d.NT - 1; n >= 0; --n) {
+    const size_t blk = (size_t)bh * d.NT + n;
+    float fo[KR], fv[KR];
+    for (int i = 0; i < KR; ++i) { fo[i] = 0.f; fv[i] = 0.f; }
+    for (int r0 = 0; r0 < kStageBlock; r0 += RB) {
+      for (int e = t; e < RB * K; e += 256) {
+        const int r = e / K, k = e % K;
+        const size_t o = (blk * kStageBlock + r0 + r) * K + k;
+        sKg[r][k] = kg[o];
+        sQg[r][k] = qg[o];
+        sWp[r][k] = wp[o];
+      }
+      for (int e = t; e < RB * VT; e += 256) {
+        const int r = e / VT, cc = e % VT;
+        sDo[r][cc] = d.scale * ld(dO, (blk * kStageBlock + r0 + r) * V + v0 + cc);   // :26
+      }
+      __syncthreads();
+      for (int e = t; e < RB * VT; e += 256) {
+        const int r = e / VT, cc = e % VT;
+        float s = 0.f;
+        for (int k = 0; k < K; ++k) s = fmaf(sKg[r][k], sDh[k][cc], s);
+        const size_t o = (blk * kStageBlock + r0 + r) * V + v0 + cc;
+        const float dv = sanitize(dvp[o] + s);                                      // :30-32
+        sDvn[r][cc] = dv;
+        dv_all[o] = dv;
+      }
+      __syncthreads();
+      for (int r = 0; r < RB; ++r) {
+        const float dov = sDo[r][c], dvv = sDvn[r][c];
+        for (int i = 0; i < KR; ++i) {
+          const int k = kr + 8 * i;
+          fo[i] = fmaf(sQg[r][k], dov, fo[i]);                                      // :26-27
+          fv[i] = fmaf(sWp[r][k], dvv, fv[i]);                                      // :34
+        }
+      }
+      __syncthreads();
+    }
+    for (int i = 0; i < KR; ++i) {
+      const int k = kr + 8 * i;
+      const float decay = __expf(gcl[blk * K + k]);                                 // :24
+      const float h = sanitize(fo[i] + sDh[k][c] * decay + (-fv[i]));               // :36-37
+      sDh[k][c] = h;
+      dh_all[(blk * K + k) * V + v0 + c] = h;
+    }
+    __syncthreads();
+  }
+  for (int i = 0; i < KR; ++i) {
+    const int k = kr + 8 * i;
+    dh0[((size_t)bh * K + k) * V + v0 + c] = sDh[k][c];
+  }
+}
+
+// ------------------------------------------------------------------ GDN2 B3 element-wise parts
+// kb = b k e^gc, kg = k e^(gc_last - gc), qg = q e^gc, wv = w v
+// (kernel_bwd_b3_wy_dqkg.py:53-58), per block element.
+__global__ __launch_bounds__(256) void g256_b3_prep_k(Gdn2Dims d, In q, In k, In b, In w, In v,
+                                                      const float* __restrict__ gc, float* __restrict__ kb,
+                                                      float* __restrict__ kgo, float* __restrict__ qgo,
+                                                      float* __restrict__ wv) {
+  const int K = d.K;
+  const size_t total = (size_t)d.B * d.H * d.NT * kStageBlock * K;
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (size_t)gridDim.x * 256) {
+    const size_t blk = e / ((size_t)kStageBlock * K);
+    const int col = (int)(e % K);
+    const float g = gc[e], gl = gc[(blk * kStageBlock + kStageBlock - 1) * K + col];
+    const float kv = ld(k, e), eg = __expf(g);
+    kb[e] = ld(b, e) * kv * eg;
+    kgo[e] = kv * __expf(gl - g);
+    qgo[e] = ld(q, e) * eg;
+    wv[e] = ld(w, e) * ld(v, e);
+  }
+}
+
+// The gc_last row term per (block, column): sum over rows of dkg kg plus
+// e^(gc_last) sum_v dh_next h_pre (kernel_bwd_b3_wy_dqkg.py:92-107).
+__global__ __launch_bounds__(256) void g256_b3_row_k(Gdn2Dims d, const float* __restrict__ gc,
+                                                     const float* __restrict__ dkg, const float* __restrict__ kgo,
+                                                     const float* __restrict__ dh_next,
+                                                     const float* __restrict__ h_pre, float* __restrict__ row) {
+  const int K = d.K, V = d.V;
+  const size_t total = (size_t)d.B * d.H * d.NT * K;
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= total) return;
+  const size_t blk = e / K;
+  const int col = (int)(e % K);
+  float sx = 0.f;
+  for (int r = 0; r < kStageBlock; ++r) {
+    const size_t o = (blk * kStageBlock + r) * K + col;
+    sx += dkg[o] * kgo[o];
+  }
+  float sh = 0.f;
+  for (int j = 0; j < V; ++j) {
+    const size_t o = (blk * K + col) * V + j;
+    sh += dh_next[o] * h_pre[o];
+  }
+  const float gl = gc[(blk * kStageBlock + kStageBlock - 1) * K + col];
+  row[e] = sx + __expf(gl) * sh;
+}
+
+// dq, dk, db, dw, dv_raw, dgc (kernel_bwd_b3_wy_dqkg.py:88-119).
+__global__ __launch_bounds__(256) void g256_b3_final_k(Gdn2Dims d, In k, In b, In w, In v,
+                                                       const float* __restrict__ gc, const float* __restrict__ kb,
+                                                       const float* __restrict__ kgo, const float* __restrict__ qgo,
+                                                       const float* __restrict__ dqg, const float* __restrict__ dkg,
+                                                       const float* __restrict__ dkb, const float* __restrict__ dwv,
+                                                       const float* __restrict__ row, float* __restrict__ dq,
+                                                       float* __restrict__ dk, float* __restrict__ db,
+                                                       float* __restrict__ dw, float* __restrict__ dvr,
+                                                       float* __restrict__ dgc) {
+  const int K = d.K;
+  const size_t total = (size_t)d.B * d.H * d.NT * kStageBlock * K;
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (size_t)gridDim.x * 256) {
+    const size_t blk = e / ((size_t)kStageBlock * K);
+    const int r = (int)((e / K) % kStageBlock), col = (int)(e % K);
+    const float g = gc[e], gl = gc[(blk * kStageBlock + kStageBlock - 1) * K + col];
+    const float eg = __expf(g), ekg = __expf(gl - g);
+    const float vdkb = dkb[e], vdkg = dkg[e], vdqg = dqg[e];
+    const float dkfkb = vdkb * eg * ld(b, e);                     // :88
+    const float dbv = vdkb * eg * ld(k, e);                       // :89
+    const float dgkb = vdkb * kb[e];                              // :90
+    const float dx = vdkg * kgo[e];                               // :92
+    const float dkfkg = vdkg * ekg;                               // :93
+    const float dqv = vdqg * eg;                                  // :97
+    const float dgqg = vdqg * qgo[e];                             // :98
+    dq[e] = n2n_acc(dqv);
+    dk[e] = n2n_acc(dkfkb + dkfkg);                               // :103
+    db[e] = n2n_acc(dbv);
+    dw[e] = n2n_acc(dwv[e] * ld(v, e));                           // :100
+    dvr[e] = n2n_acc(dwv[e] * ld(w, e));                          // :101
+    float dg = dgkb + dgqg + (-dx);                               // :104
+    if (r == kStageBlock - 1) dg = dg + row[blk * K + col];       // :108-111
+    dgc[e] = n2n_acc(dg);
+  }
+}
+
+// ------------------------------------------------------------------ GDN2 B4
+// One workgroup per (batch, head, block, 16-column slice); thread (row
+// group, column): rows rg + 16 i.  Sub-blocks of 128 rows, pairs (si >= sj)
+// in the reference's order, with a clip after every accumulation
+// (kernel_bwd_b4_intra.py:77-121).
+constexpr int B4_SUB = 128, B4_DS = 16, B4_L = B4_DS + 1;
+
+__global__ __launch_bounds__(256) void g256_b4_k(Gdn2Dims d, const float* __restrict__ daqk,
+                                                 const float* __restrict__ dakk, In q, In k, In b,
+                                                 const float* __restrict__ g, float* __restrict__ dq,
+                                                 float* __restrict__ dk, float* __restrict__ db,
+                                                 float* __restrict__ dgc) {
+  constexpr int BT = kStageBlock;
+  __shared__ float sGc[BT][B4_L], sLq[BT][B4_L], sK[BT][B4_L], sBk[BT][B4_L];
+  const int K = d.K, nds = K / B4_DS;
+  const int blk = blockIdx.x / nds, d0 = (blockIdx.x % nds) * B4_DS;
+  const int n = blk % d.NT, bh = blk / d.NT, h = bh % d.H, bb = bh / d.H;
+  const int t = threadIdx.x, c = t % B4_DS, rg = t / B4_DS;
+  const size_t row0 = (size_t)bb * d.T + (size_t)n * BT;
+  const size_t hk = (size_t)h * K + d0 + c;
+  for (int i = 0; i < BT / 16; ++i) {
+    const int r = rg + 16 * i;
+    const size_t rr = row0 + r;
+    const float kv = ld(k, rr * d.rk + hk);
+    sLq[r][c] = d.scale * ld(q, rr * d.rq + hk);
+    sK[r][c] = kv;
+    sBk[r][c] = ld(b, rr * d.rb + hk) * kv;
+    sGc[r][c] = g[rr * d.rg + hk];
+  }
+  __syncthreads();
+  if (rg == 0) {  // gc = tril @ g over the block's rows (:66-68)
+    float s = 0.f;
+    for (int r = 0; r < BT; ++r) {
+      s += sGc[r][c];
+      sGc[r][c] = s;
+    }
+  }
+  __syncthreads();
+  const float* mq = daqk + (size_t)blk * BT * BT;
+  const float* mk = dakk + (size_t)blk * BT * BT;
+  const size_t ob = (size_t)blk * BT * K + d0 + c;
+  for (int i = 0; i < BT / 16; ++i) {
+    const int r = rg + 16 * i, rb = r / B4_SUB;
+    const float gr = sGc[r][c], lq = sLq[r][c], kr = sK[r][c], bkr = sBk[r][c];
+    float aq = 0.f, abk = 0.f, ak = 0.f, ag = 0.f;
+    for (int si = 0; si < BT / B4_SUB; ++si) {
+      for (int sj = 0; sj <= si; ++sj) {
+        if (si == rb) {  // r as a row i of the pair
+          float sq = 0.f, sk = 0.f, gq = 0.f, gk = 0.f;
+          for (int j = sj * B4_SUB; j < (sj + 1) * B4_SUB; ++j) {
+            const bool diag = si == sj;
+            const float mqv = (diag && j > r) ? 0.f : mq[(size_t)r * BT + j];   // causal (:95-99)
+            const float mkv = (diag && j >= r) ? 0.f : mk[(size_t)r * BT + j];  // strict
+            const float dd = gr - sGc[j][c];
+            const float e = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
+            const float cm = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
+            const float kj = sK[j][c];
+            sq += mqv * e * kj;                                   // _dL_pair_sum (:38-41)
+            sk += mkv * e * kj;
+            gq += mqv * lq * kj * e * cm;                         // _dgc_pair_sum (:50-54)
+            gk += mkv * bkr * kj * e * cm;
+          }
+          aq = sanitize(aq + sq * d.scale);                       // :117
+          abk = sanitize(abk + sk);                               // :118
+          ag = sanitize(ag + gq + gk);                            // :120
+        }
+        if (sj == rb) {  // r as a column j of the pair
+          float sq = 0.f, sk = 0.f, gq = 0.f, gk = 0.f;
+          for (int i2 = si * B4_SUB; i2 < (si + 1) * B4_SUB; ++i2) {
+            const bool diag = si == sj;
+            const float mqv = (diag && r > i2) ? 0.f : mq[(size_t)i2 * BT + r];
+            const float mkv = (diag && r >= i2) ? 0.f : mk[(size_t)i2 * BT + r];
+            const float dd = sGc[i2][c] - gr;
+            const float e = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
+            const float cm = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
+            const float li = sLq[i2][c], bki = sBk[i2][c];
+            sq += mqv * e * li;                                   // _dR_pair_sum (:44-47)
+            sk += mkv * e * bki;
+            gq += mqv * li * kr * e * cm;
+            gk += mkv * bki * kr * e * cm;
+          }
+          ak = sanitize(ak + sq + sk);                            // :119
+          ag = sanitize(ag + (-gq) + (-gk));                      // :121
+        }
+      }
+    }
+    const size_t o = ob + (size_t)r * K;
+    const float bv = ld(b, (row0 + r) * d.rb + hk);
+    dq[o] = sanitize(aq);                                         // :128-132
+    dk[o] = sanitize(ak + abk * bv);                              // :124
+    db[o] = sanitize(abk * kr);                                   // :125
+    dgc[o] = sanitize(ag);
+  }
+}
+
+// ------------------------------------------------------------------ B5
+// dg = sanitize(reverse cumsum over the block's rows) per (block, column)
+// (kernel_bwd_b5_reverse_cumsum.py:17-24).
+__global__ __launch_bounds__(256) void rev_cumsum_k(const float* __restrict__ x, float* __restrict__ y,
+                                                    long long blocks, int rows, int cols) {
+  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= blocks * cols) return;
+  const long long blk = e / cols;
+  const int col = (int)(e % cols);
+  const float* xp = x + (size_t)blk * rows * cols + col;
+  float* yp = y + (size_t)blk * rows * cols + col;
+  float s = 0.f;
+  for (int r = rows - 1; r >= 0; --r) {
+    s += xp[(size_t)r * cols];
+    yp[(size_t)r * cols] = sanitize(s);
+  }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ launchers
+int g256_dav_bwd(const Gdn2Dims& d, int do_dtype, const float* aqk, const float* v_new, const void* dO,
+                 float* daqk, float* dvn, Launch& L) {
+  constexpr int BT = kStageBlock;
+  const int Z = d.B * d.H * d.NT, V = d.V;
+  const int dob = do_dtype == ATOMIC_BF16;
+  // dAqk = nan_to_num((dO v_new^T) * causal)   (kernel_bwd_b2_dav.py:26,29)
+  GemmOp g = gemm_op(BT, BT, V, Z);
+  g.A = In{dO, dob}; g.lda = V; g.sa = dense(BT, V);
+  g.B = In{v_new, 0}; g.ldb = V; g.sb = dense(BT, V); g.tb = 1;
+  g.C = daqk; g.ldc = BT; g.sc = dense(BT, BT);
+  g.mask = 1; g.post = 1;
+  int rc = gemm(g, Z, "g256_dav_daqk", L);
+  if (rc != ATOMIC_OK) return rc;
+  // dv_new = nan_to_num(Aqk^T dO)   (:27,30)
+  GemmOp h = gemm_op(BT, V, BT, Z);
+  h.A = In{aqk, 0}; h.lda = BT; h.sa = dense(BT, BT); h.ta = 1;
+  h.B = In{dO, dob}; h.ldb = V; h.sb = dense(BT, V);
+  h.C = dvn; h.ldc = V; h.sc = dense(BT, V);
+  h.post = 1;
+  return gemm(h, Z, "g256_dav_dvnew", L);
+}
+
+int g256_dhu_bwd(const Gdn2Dims& d, int do_dtype, const void* dO, const float* dvp, const float* wp,
+                 const float* qg, const float* kg, const float* gcl, const float* dht, float* dh_all, float* dh0,
+                 float* dv_all, Launch& L) {
+  const In o{dO, do_dtype == ATOMIC_BF16};
+  const dim3 grid(d.B * d.H * (d.V / 32));
+  if (d.K == 128)
+    return L("g256_dhu", [&] {
+      hipLaunchKernelGGL((g256_dhu_k<128>), grid, dim3(256), 0, L.st, d, o, dvp, wp, qg, kg, gcl, dht, dh_all,
+                         dh0, dv_all);
+    });
+  return L("g256_dhu", [&] {
+    hipLaunchKernelGGL((g256_dhu_k<64>), grid, dim3(256), 0, L.st, d, o, dvp, wp, qg, kg, gcl, dht, dh_all, dh0,
+                       dv_all);
+  });
+}
+
+size_t g256_b3_ws(const Gdn2Dims& d) {
+  const size_t z = (size_t)d.B * d.H * d.NT, bk = (size_t)kStageBlock * d.K, bb = (size_t)kStageBlock * kStageBlock;
+  // kb, kg, qg, wv, dqg, dw_pseudo, dkg, dkb, dwv ([BT][K] each), dA, tmp ([BT][BT]), row ([K])
+  return (z * (9 * bk + 2 * bb + d.K)) * sizeof(float);
+}
+
+int g256_b3_bwd(const Gdn2Dims& d, int dtype, int do_dtype, const void* q, const void* k, const void* b,
+                const void* w, const void* v, const float* gc, const float* A, const float* h_pre,
+                const float* v_new, const void* dO, const float* dv, const float* dh_next, float* dq, float* dk,
+                float* db, float* dw, float* dvr, float* dgc, float* dakk, float* ws, Launch& L) {
+  constexpr int BT = kStageBlock;
+  const int Z = d.B * d.H * d.NT, K = d.K, V = d.V;
+  const int bf = dtype == ATOMIC_BF16;
+  const size_t zk = (size_t)Z * BT * K, zb = (size_t)Z * BT * BT;
+  float *kb = ws, *kgo = kb + zk, *qgo = kgo + zk, *wv = qgo + zk, *dqg = wv + zk, *dwp = dqg + zk,
+        *dkg = dwp + zk, *dkb = dkg + zk, *dwv = dkb + zk, *dA = dwv + zk, *tmp = dA + zb, *row = tmp + zb;
+  const In iq{q, bf}, ik{k, bf}, ib{b, bf}, iw{w, bf}, iv{v, bf}, ido{dO, do_dtype == ATOMIC_BF16};
+  const int eb = (int)((zk + 255) / 256 < 65536 ? (zk + 255) / 256 : 65536);
+  int rc = L("g256_b3_prep", [&] {
+    hipLaunchKernelGGL(g256_b3_prep_k, dim3(eb), dim3(256), 0, L.st, d, iq, ik, ib, iw, iv, gc, kb, kgo, qgo, wv);
+  });
+  if (rc != ATOMIC_OK) return rc;
+  auto mm = [&](int M, int N, int Kd, In a, long long lda, Bat sa, int ta, In bo, long long ldb, Bat sb, int tb,
+                float* c, long long ldc, Bat sc, float alpha, int accum, int mask, int post, const char* name) {
+    GemmOp g = gemm_op(M, N, Kd, Z);
+    g.A = a; g.lda = lda; g.sa = sa; g.ta = ta;
+    g.B = bo; g.ldb = ldb; g.sb = sb; g.tb = tb;
+    g.C = c; g.ldc = ldc; g.sc = sc;
+    g.alpha = alpha; g.accum = accum; g.mask = mask; g.post = post;
+    return gemm(g, Z, name, L);
+  };
+  const Bat sBK = dense(BT, K), sBV = dense(BT, V), sKV = dense(K, V), sBB = dense(BT, BT);
+  // dqg = (scale dO) h_pre^T; dw_pseudo = -dv h_pre^T; dkg = v_new dh_next^T   (:60-67)
+  if ((rc = mm(BT, K, V, ido, V, sBV, 0, In{h_pre, 0}, V, sKV, 1, dqg, K, sBK, d.scale, 0, 0, 0, "g256_b3_dqg")))
+    return rc;
+  if ((rc = mm(BT, K, V, In{dv, 0}, V, sBV, 0, In{h_pre, 0}, V, sKV, 1, dwp, K, sBK, -1.f, 0, 0, 0, "g256_b3_dwp")))
+    return rc;
+  if ((rc = mm(BT, K, V, In{v_new, 0}, V, sBV, 0, In{dh_next, 0}, V, sKV, 1, dkg, K, sBK, 1.f, 0, 0, 0,
+               "g256_b3_dkg")))
+    return rc;
+  // dA_total = sanitize(dw_pseudo kb^T + dv wv^T)   (:69,72,75,78)
+  if ((rc = mm(BT, BT, K, In{dwp, 0}, K, sBK, 0, In{kb, 0}, K, sBK, 1, dA, BT, sBB, 1.f, 0, 0, 0, "g256_b3_daw")))
+    return rc;
+  if ((rc = mm(BT, BT, V, In{dv, 0}, V, sBV, 0, In{wv, 0}, V, sBV, 1, dA, BT, sBB, 1.f, 1, 0, 2, "g256_b3_dau")))
+    return rc;
+  // dkb = A^T dw_pseudo; dwv = A^T dv   (:70,73)
+  if ((rc = mm(BT, K, BT, In{A, 0}, BT, sBB, 1, In{dwp, 0}, K, sBK, 0, dkb, K, sBK, 1.f, 0, 0, 0, "g256_b3_dkb")))
+    return rc;
+  if ((rc = mm(BT, V, BT, In{A, 0}, BT, sBB, 1, In{dv, 0}, V, sBV, 0, dwv, V, sBV, 1.f, 0, 0, 0, "g256_b3_dwv")))
+    return rc;
+  // tmp = sanitize(dA_total A^T); dAkk = nan_to_num(-(A^T tmp) * strict)   (:83-86,119)
+  if ((rc = mm(BT, BT, BT, In{dA, 0}, BT, sBB, 0, In{A, 0}, BT, sBB, 1, tmp, BT, sBB, 1.f, 0, 0, 2, "g256_b3_tmp")))
+    return rc;
+  if ((rc = mm(BT, BT, BT, In{A, 0}, BT, sBB, 1, In{tmp, 0}, BT, sBB, 0, dakk, BT, sBB, -1.f, 0, 2, 1,
+               "g256_b3_dakk")))
+    return rc;
+  const int rb = (int)(((size_t)Z * K + 255) / 256);
+  rc = L("g256_b3_row", [&] {
+    hipLaunchKernelGGL(g256_b3_row_k, dim3(rb), dim3(256), 0, L.st, d, gc, dkg, kgo, dh_next, h_pre, row);
+  });
+  if (rc != ATOMIC_OK) return rc;
+  return L("g256_b3_final", [&] {
+    hipLaunchKernelGGL(g256_b3_final_k, dim3(eb), dim3(256), 0, L.st, d, ik, ib, iw, iv, gc, kb, kgo, qgo, dqg,
+                       dkg, dkb, dwv, row, dq, dk, db, dw, dvr, dgc);
+  });
+}
+
+int g256_intra_bwd(const Gdn2Dims& d, int dtype, const float* daqk, const float* dakk, const void* q,
+                   const void* k, const void* b, const float* g, float* dq, float* dk, float* db, float* dgc,
+                   Launch& L) {
+  const int bf = dtype == ATOMIC_BF16;
+  const dim3 grid(d.B * d.H * d.NT * (d.K / B4_DS));
+  return L("g256_intra_bwd", [&] {
+    hipLaunchKernelGGL(g256_b4_k, grid, dim3(256), 0, L.st, d, daqk, dakk, In{q, bf}, In{k, bf}, In{b, bf}, g,
+                       dq, dk, db, dgc);
+  });
+}
+
+int rev_cumsum_bwd(const float* dgc, float* dg, long long blocks, int rows, int cols, Launch& L) {
+  const long long n = blocks * cols;
+  if (n <= 0) return ATOMIC_ERR_SHAPE;
+  return L("reverse_cumsum_bwd", [&] {
+    hipLaunchKernelGGL(rev_cumsum_k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, L.st, dgc, dg, blocks, rows,
+                       cols);
+  });
+}
+
+}  // namespace ah

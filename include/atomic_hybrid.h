@@ -298,6 +298,57 @@ int atomic_gdn2_inter_chunk_combine_with_state(const atomic_gdn2_args* a, const 
                                                const float* gc_last, const float* h0, float* o, float* h_final,
                                                void* h_pre_t, void* v_new_t, void* stream);
 
+/* ---- Backward stages at the reference's 256-row block
+ * The staged backward of the reference's trainable op
+ * (atomic_ops/kernel_trainable_B6.py:97-181): args.chunk must be 256
+ * (ATOMIC_ERR_SHAPE otherwise).  Every per-block array is float32, in the
+ * reference's layout: [B][H][NT][256][D] (D = K = V), scores [B][H][NT][256][256],
+ * states [B][H][NT][K][V].  dO is of args.do_dtype; q, k, b, w, v of
+ * args.dtype.  Block products accumulate in float32 in an order of their own;
+ * the clip / nan_to_num placement is the reference kernels'. */
+
+/* Kernel B2, dav_backward_pallas(Aqk, v_new, do) (kernel_bwd_b2_dav.py:17-51):
+ * dAqk = nan_to_num((do v_new^T) * causal), dv_new = nan_to_num(Aqk^T do);
+ * dO per block [B][H][NT][256][V]. */
+int atomic_gdn2_dav_backward(const atomic_gdn2_args* a, const float* Aqk, const float* v_new, const void* dO,
+                             float* dAqk, float* dv_new, void* stream);
+
+/* Kernel B1, gdn2_dhu_backward(do, dv_partial, w_pseudo, qg, kg, gc_last,
+ * scale, dht) (kernel_bwd_b1_dhu.py:14-44): the reverse scan.  dht
+ * [B][H][K][V] (NULL: zeros) is sanitised first; dh_all[n] is the carry after
+ * block n, dh0 the carry after block 0, dv_all the sanitised dv_new. */
+int atomic_gdn2_dhu_backward(const atomic_gdn2_args* a, const void* dO, const float* dv_partial,
+                             const float* w_pseudo, const float* qg, const float* kg, const float* gc_last,
+                             const float* dht, float* dh_all, float* dh0, float* dv_all, void* stream);
+
+/* Bytes of workspace atomic_gdn2_wy_dqkg_backward needs (0 for unsupported args). */
+size_t atomic_gdn2_wy_dqkg_workspace_size(const atomic_gdn2_args* a);
+
+/* Kernel B3, wy_dqkg_backward_pallas(q, k, b, w, v, gc, A, Akk, h_pre_all,
+ * v_new_all, do, dv, dh_next_all, scale) (kernel_bwd_b3_wy_dqkg.py:33-148):
+ * dq, dk, db, dw, dv_raw, dgc and dAkk, with dA_total and tmp clipped before
+ * the products through A^T (:75-86).  q, k, b, w, v, gc, dO, dv per block;
+ * Akk, which the reference reads for its shape only, is not an argument. */
+int atomic_gdn2_wy_dqkg_backward(const atomic_gdn2_args* a, const void* q, const void* k, const void* b,
+                                 const void* w, const void* v, const float* gc, const float* A, const float* h_pre,
+                                 const float* v_new, const void* dO, const float* dv, const float* dh_next,
+                                 float* dq, float* dk, float* db, float* dw, float* dv_raw, float* dgc,
+                                 float* dAkk, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Kernel B4, intra_backward_pallas(dAqk, dAkk, q, k, b, g, scale)
+ * (kernel_bwd_b4_intra.py:57-165): kernel A's backward over its 128-row
+ * sub-block pairs with a clip after every accumulation.  q, k, b, g are the
+ * [B][T][H][K] inputs (args.row_stride applies); dq, dk, db, dgc per block. */
+int atomic_gdn2_intra_backward(const atomic_gdn2_args* a, const float* dAqk, const float* dAkk, const void* q,
+                               const void* k, const void* b, const float* g, float* dq, float* dk, float* db,
+                               float* dgc, void* stream);
+
+/* Kernel B5, reverse_cumsum_bwd(dgc, chunk_size)
+ * (kernel_bwd_b5_reverse_cumsum.py:17-24): dg = sanitize(suffix sum over
+ * each block's rows) of a [B][H][T / chunk][chunk][K] float32 array, for any
+ * args.chunk. */
+int atomic_gdn2_reverse_cumsum_bwd(const atomic_gdn2_args* a, const float* dgc, float* dg, void* stream);
+
 /* ---------------------------------------------------------------- Mamba2 */
 
 enum {
