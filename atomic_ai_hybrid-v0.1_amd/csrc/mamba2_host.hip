@@ -625,3 +625,33 @@ extern "C" int atomic_mamba2_inter_chunk_combine(const atomic_mamba2_args* a, co
   Launch L{a->profile, (hipStream_t)stream};
   return mamba2_combine_stage(p, y_diag, state_end, cumdecay, C, state0, y, state_final, workspace, L);
 }
+
+// ------------------------------------------------------------------ MB2 stage entry
+extern "C" size_t atomic_mamba2_intra_chunk_ssd_bwd_workspace_size(const atomic_mamba2_args* a) {
+  Mamba2Plan p;
+  if (mamba2_plan(a, &p) != ATOMIC_OK) return 0;
+  Mamba2Dims d = p.dm;
+  d.C = a->chunk;
+  d.NT = a->seqlen / a->chunk;
+  return m2_align(m_intra_bwd_ws(d));
+}
+
+extern "C" int atomic_mamba2_intra_chunk_ssd_bwd(const atomic_mamba2_args* a, const void* dt, const void* x,
+                                                 const void* B, const void* C, const float* cumdecay,
+                                                 const void* dy, const float* dstate_end_grad, float* ddt,
+                                                 float* dx, float* dB, float* dC, float* dcum, void* workspace,
+                                                 size_t workspace_bytes, void* stream) {
+  Mamba2Plan p;
+  const int rc = mamba2_plan(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!dt || !x || !B || !C || !cumdecay || !dy || !dstate_end_grad || !ddt || !dx || !dB || !dC || !dcum)
+    return ATOMIC_ERR_NULL;
+  Mamba2Dims d = p.dm;  // the caller's chunk, whatever the whole path runs
+  d.C = a->chunk;
+  d.NT = a->seqlen / a->chunk;
+  if (!workspace || workspace_bytes < m_intra_bwd_ws(d)) return ATOMIC_ERR_WORKSPACE;
+  ws_tag_clobber(workspace, workspace_bytes);
+  Launch L{a->profile, (hipStream_t)stream};
+  return m_intra_bwd(d, a->dy_dtype, dt, x, B, C, cumdecay, dy, dstate_end_grad, ddt, dx, dB, dC, dcum,
+                     static_cast<float*>(workspace), L);
+}

@@ -58,4 +58,13 @@ int g256_intra_bwd(const Gdn2Dims& d, int dtype, const float* daqk, const float*
                    Launch& L);
 int rev_cumsum_bwd(const float* dgc, float* dg, long long blocks, int rows, int cols, Launch& L);
 
+// Mamba2 MB2 (chunk d.C of 64, 128 or 256): dt, x, B, C bf16, dy of
+// dy_dtype; cumdecay [B][H][NT][C][P] and dstate_end_grad [B][H][NT][P][N]
+// fp32.  ddt, dx [B][T][H][P], dB, dC [B][T][N] (summed over the heads),
+// dcum [B][H][NT][C][P], fp32; workspace m_intra_bwd_ws bytes.
+size_t m_intra_bwd_ws(const Mamba2Dims& d);
+int m_intra_bwd(const Mamba2Dims& d, int dy_dtype, const void* dt, const void* x, const void* Bm, const void* Cm,
+                const float* cum, const void* dy, const float* dse, float* ddt, float* dx, float* dB, float* dC,
+                float* dcum, float* ws, Launch& L);
+
 }  // namespace ah

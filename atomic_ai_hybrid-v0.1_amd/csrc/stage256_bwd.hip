@@ -419,6 +419,183 @@ __global__ __launch_bounds__(256) void rev_cumsum_k(const float* __restrict__ x,
   }
 }
 
+// ------------------------------------------------------------------ Mamba2 MB2
+// Per (batch, head, chunk) item z = (b H + h) NT + n, chunk rows C, sub-blocks
+// of bc = min(128, C) rows (kernel_mamba2_bwd_b2_intra.py:20-21,35), pairs
+// (si >= sj) in the reference's order.  Work arrays [Z][C][P] fp32 unless
+// noted.
+
+// dBx, the decay to the chunk end and its derived per-element terms
+// (kernel_mamba2_bwd_b2_intra.py:47-65): dbx = sanitize(dt x), write,
+// d_dBx_1, and d_dte_diff (its negation and column sums enter dcum).
+__global__ __launch_bounds__(256) void m2b_elem_k(Mamba2Dims d, In dt, In x, const float* __restrict__ cum,
+                                                  const float* __restrict__ dwrite, float* __restrict__ dbx,
+                                                  float* __restrict__ write, float* __restrict__ d1,
+                                                  float* __restrict__ ddd) {
+  const int C = d.C, P = d.P;
+  const size_t total = (size_t)d.B * d.H * d.NT * C * P;
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (size_t)gridDim.x * 256) {
+    const size_t z = e / ((size_t)C * P);
+    const int i = (int)((e / P) % C), p = (int)(e % P);
+    const int n = (int)(z % d.NT), h = (int)((z / d.NT) % d.H), b = (int)(z / ((size_t)d.NT * d.H));
+    const size_t row = (size_t)b * d.T + (size_t)n * C + i;
+    const float dtv = ld(dt, row * d.rdt + (size_t)h * P + p), xv = ld(x, row * d.rx + (size_t)h * P + p);
+    const float bx = sanitize(dtv * xv);                                              // :47
+    const float cl = cum[(z * C + C - 1) * P + p];
+    const float raw = cl - cum[e];                                                    // :51
+    const float dte = __expf(fminf(fmaxf(raw, -kClipDecay), kClipDecay));            // :52
+    const float dw = dwrite[e];
+    dbx[e] = bx;
+    write[e] = sanitize(bx * dte);                                                    // :53
+    d1[e] = sanitize(dw * dte);                                                       // :59
+    const float dd = sanitize(dw * bx);                                               // :60
+    const float m = (raw >= -kClipDecay && raw <= kClipDecay) ? 1.f : 0.f;
+    ddd[e] = sanitize(dd * dte * m);                                                  // :61-63
+  }
+}
+
+// dBC of each sub-block pair: sum_p dy_i dBx_j exp(clip(cum_i - cum_j)),
+// causal on diagonal pairs (:94,98-100); one 16 x 16 tile of (i, j) per
+// workgroup, lower pairs only.  dbc [Z][C][C].
+__global__ __launch_bounds__(256) void m2b_dbc_k(Mamba2Dims d, In dy, const float* __restrict__ cum,
+                                                 const float* __restrict__ dbx, float* __restrict__ dbc) {
+  __shared__ float sDy[16][17], sCi[16][17], sBx[16][17], sCj[16][17];
+  const int C = d.C, P = d.P, bc = C < 128 ? C : 128, nt16 = C / 16;
+  const int z = blockIdx.y, ti = blockIdx.x / nt16, tj = blockIdx.x % nt16;
+  const int i0 = 16 * ti, j0 = 16 * tj;
+  const int t = threadIdx.x, il = t / 16, jl = t % 16, i = i0 + il, j = j0 + jl;
+  const bool pair = i0 / bc >= j0 / bc;   // a lower sub-block pair (si >= sj)
+  const int n = z % d.NT, h = (z / d.NT) % d.H, b = z / (d.NT * d.H);
+  const size_t zr = (size_t)z * C;
+  float s = 0.f;
+  if (pair) {
+    for (int p0 = 0; p0 < P; p0 += 16) {
+      {
+        const int r = t / 16, c = t % 16;
+        const size_t row = (size_t)b * d.T + (size_t)n * C + i0 + r;
+        sDy[r][c] = ld(dy, row * d.rdy + (size_t)h * P + p0 + c);
+        sCi[r][c] = cum[(zr + i0 + r) * P + p0 + c];
+        sBx[r][c] = dbx[(zr + j0 + r) * P + p0 + c];
+        sCj[r][c] = cum[(zr + j0 + r) * P + p0 + c];
+      }
+      __syncthreads();
+#pragma unroll 4
+      for (int c = 0; c < 16; ++c) {
+        const float e = __expf(fminf(fmaxf(sCi[il][c] - sCj[jl][c], -kClipDecay), kClipDecay));
+        s += sDy[il][c] * sBx[jl][c] * e;
+      }
+      __syncthreads();
+    }
+    if (i / bc == j / bc && j > i) s = 0.f;   // causal on the diagonal pair
+  }
+  dbc[(zr + i) * C + j] = pair ? s : 0.f;
+}
+
+// d_dBx_2 and dcum over the sub-block pairs, then ddt, dx and dcum
+// (:74-128).  One workgroup per (item, 16-channel slice); thread (row group,
+// channel): rows rg + 16 m.
+__global__ __launch_bounds__(256) void m2b_pair_k(Mamba2Dims d, In dt, In x, In dy, const float* __restrict__ cum,
+                                                  const float* __restrict__ bcin, const float* __restrict__ dbx,
+                                                  const float* __restrict__ d1, const float* __restrict__ ddd,
+                                                  float* __restrict__ ddt, float* __restrict__ dx,
+                                                  float* __restrict__ dcum) {
+  constexpr int MAXC = 256;
+  __shared__ float sCum[MAXC][17], sDy[MAXC][17], sBx[MAXC][17];
+  __shared__ float sLast[16][17];
+  const int C = d.C, P = d.P, bc = C < 128 ? C : 128, nps = P / 16;
+  const int z = blockIdx.x / nps, p0 = (blockIdx.x % nps) * 16;
+  const int n = z % d.NT, h = z / d.NT % d.H, b = z / (d.NT * d.H);
+  const int t = threadIdx.x, c = t % 16, rg = t / 16;
+  const size_t zr = (size_t)z * C, row0 = (size_t)b * d.T + (size_t)n * C;
+  const float* bcz = bcin + ((size_t)b * d.NT + n) * C * C;   // sanitize(C B^T) of (b, n)
+  float lastp = 0.f;
+  for (int r = rg; r < C; r += 16) {
+    sCum[r][c] = cum[(zr + r) * P + p0 + c];
+    sDy[r][c] = ld(dy, (row0 + r) * d.rdy + (size_t)h * P + p0 + c);
+    sBx[r][c] = dbx[(zr + r) * P + p0 + c];
+    lastp += ddd[(zr + r) * P + p0 + c];
+  }
+  sLast[rg][c] = lastp;
+  __syncthreads();
+  for (int r = rg; r < C; r += 16) {
+    const int rb = r / bc;
+    const float cr = sCum[r][c], dyr = sDy[r][c], bxr = sBx[r][c];
+    float a2 = 0.f, ac = 0.f;
+    for (int si = 0; si < C / bc; ++si) {
+      for (int sj = 0; sj <= si; ++sj) {
+        const bool diag = si == sj;
+        if (sj == rb) {  // r as the column j: d_dBx_2 (:95,109)
+          float s2 = 0.f;
+          for (int i = si * bc; i < (si + 1) * bc; ++i) {
+            const float bl = (diag && i < r) ? 0.f : bcz[(size_t)i * C + r];
+            const float e = __expf(fminf(fmaxf(sCum[i][c] - cr, -kClipDecay), kClipDecay));
+            s2 += e * bl * sDy[i][c];
+          }
+          a2 = sanitize(a2 + s2);
+        }
+        if (si == rb) {  // r as the row i: dcum_i (:105-106,112)
+          float si_ = 0.f;
+          for (int j = sj * bc; j < (sj + 1) * bc; ++j) {
+            const float bl = (diag && j > r) ? 0.f : bcz[(size_t)r * C + j];
+            const float dd = cr - sCum[j][c];
+            const float e = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
+            const float m = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
+            si_ += dyr * sBx[j][c] * bl * e * m;
+          }
+          ac = sanitize(ac + si_);
+        }
+        if (sj == rb) {  // r as the column j: dcum_j (:107,113)
+          float sj_ = 0.f;
+          for (int i = si * bc; i < (si + 1) * bc; ++i) {
+            const float bl = (diag && i < r) ? 0.f : bcz[(size_t)i * C + r];
+            const float dd = sCum[i][c] - cr;
+            const float e = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
+            const float m = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
+            sj_ += sDy[i][c] * bxr * bl * e * m;
+          }
+          ac = sanitize(ac + (-sj_));
+        }
+      }
+    }
+    const size_t o = (zr + r) * P + p0 + c;
+    const float dtot = sanitize(d1[o] + a2);                                      // :116
+    const size_t io = (row0 + r) * (size_t)d.H * P + (size_t)h * P + p0 + c;
+    ddt[io] = sanitize(dtot * ld(x, (row0 + r) * d.rx + (size_t)h * P + p0 + c));  // :118,126
+    dx[io] = sanitize(dtot * ld(dt, (row0 + r) * d.rdt + (size_t)h * P + p0 + c)); // :119,127
+    float dc = ac + (-ddd[o]);                                                    // :64,121
+    if (r == C - 1) {                                                             // :65,122-123
+      float lb = 0.f;
+      for (int g2 = 0; g2 < 16; ++g2) lb += sLast[g2][c];
+      dc = dc + lb;
+    }
+    dcum[o] = sanitize(dc);                                                       // :128
+  }
+}
+
+// dB, dC summed over the heads (:176-178): [B][T][N] from [Z][C][N].
+__global__ __launch_bounds__(256) void m2b_headsum_k(Mamba2Dims d, const float* __restrict__ wb,
+                                                     const float* __restrict__ wc, float* __restrict__ dB,
+                                                     float* __restrict__ dC) {
+  const size_t total = (size_t)d.B * d.T * d.N;
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= total) return;
+  const int s = (int)(e % d.N);
+  const size_t tok = e / d.N;
+  const int b = (int)(tok / d.T), tt = (int)(tok % d.T), n = tt / d.C, i = tt % d.C;
+  float sb = 0.f, sc = 0.f;
+  for (int h = 0; h < d.H; ++h) {
+    const size_t o = ((((size_t)b * d.H + h) * d.NT + n) * d.C + i) * d.N + s;
+    sb += wb[o];
+    sc += wc[o];
+  }
+  dB[e] = sb;
+  dC[e] = sc;
+}
+
+__global__ __launch_bounds__(256) void fill0_k(float* __restrict__ p, size_t n) {
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (size_t)gridDim.x * 256) p[e] = 0.f;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ launchers
@@ -544,6 +721,100 @@ int rev_cumsum_bwd(const float* dgc, float* dg, long long blocks, int rows, int 
   return L("reverse_cumsum_bwd", [&] {
     hipLaunchKernelGGL(rev_cumsum_k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, L.st, dgc, dg, blocks, rows,
                        cols);
+  });
+}
+
+
+size_t m_intra_bwd_ws(const Mamba2Dims& d) {
+  const size_t Z = (size_t)d.B * d.H * d.NT, C = d.C;
+  // CB ([B][NT][C][C]), dwrite, dbx, write, d_dBx_1, d_dte_diff ([Z][C][P]),
+  // per-head dB, dC ([Z][C][N]), dBC ([Z][C][C])
+  return ((size_t)d.B * d.NT * C * C + 5 * Z * C * d.P + 2 * Z * C * d.N + Z * C * C) * sizeof(float);
+}
+
+int m_intra_bwd(const Mamba2Dims& d, int dy_dtype, const void* dt, const void* x, const void* Bm, const void* Cm,
+                const float* cum, const void* dy, const float* dse, float* ddt, float* dx, float* dB, float* dC,
+                float* dcum, float* ws, Launch& L) {
+  const int C = d.C, P = d.P, N = d.N, H = d.H, NT = d.NT, bc = C < 128 ? C : 128;
+  const int Z = d.B * H * NT;
+  const size_t zcp = (size_t)Z * C * P, zcn = (size_t)Z * C * N;
+  float *bcin = ws, *dwrite = bcin + (size_t)d.B * NT * C * C, *dbx = dwrite + zcp, *write = dbx + zcp,
+        *d1 = write + zcp, *ddd = d1 + zcp, *wB = ddd + zcp, *wC = wB + zcn, *dbc = wC + zcn;
+  const In idt{dt, 1}, ix{x, 1}, idy{dy, dy_dtype == ATOMIC_BF16};
+  const bf16* Bp = static_cast<const bf16*>(Bm);
+  const bf16* Cp = static_cast<const bf16*>(Cm);
+  // item z = (b H + h) NT + n: a dense per-item array of S elements, and the
+  // chunk rows of a [B][T][.] input (shared by the heads)
+  auto dense3 = [&](long long S) { return Bat{(long long)H * NT * S, (long long)NT * S, S}; };
+  auto rows3 = [&](long long r) { return Bat{(long long)d.T * r, 0, (long long)C * r}; };
+  // CB = sanitize(C B^T) per (batch, chunk)   (:48)
+  GemmOp g = gemm_op(C, C, N, d.B * NT);
+  g.Z1 = 1; g.Z0 = NT;
+  g.A = In{Cp, 1}; g.lda = d.rC; g.sa = Bat{(long long)d.T * d.rC, 0, (long long)C * d.rC};
+  g.B = In{Bp, 1}; g.ldb = d.rB; g.sb = Bat{(long long)d.T * d.rB, 0, (long long)C * d.rB}; g.tb = 1;
+  g.C = bcin; g.ldc = C; g.sc = Bat{(long long)NT * C * C, 0, (long long)C * C};
+  g.post = 2;
+  int rc = gemm(g, d.B * NT, "m2b_cb", L);
+  if (rc != ATOMIC_OK) return rc;
+  // dwrite = sanitize(B dstate_end^T)   (:56)
+  g = gemm_op(C, P, N, Z);
+  g.Z1 = H; g.Z0 = NT;
+  g.A = In{Bp, 1}; g.lda = d.rB; g.sa = rows3(d.rB);
+  g.B = In{dse, 0}; g.ldb = N; g.sb = dense3((long long)P * N); g.tb = 1;
+  g.C = dwrite; g.ldc = P; g.sc = dense3((long long)C * P);
+  g.post = 2;
+  if ((rc = gemm(g, Z, "m2b_dwrite", L))) return rc;
+  const int eb = (int)((zcp + 255) / 256 < 65536 ? (zcp + 255) / 256 : 65536);
+  rc = L("m2b_elem", [&] {
+    hipLaunchKernelGGL(m2b_elem_k, dim3(eb), dim3(256), 0, L.st, d, idt, ix, cum, dwrite, dbx, write, d1, ddd);
+  });
+  if (rc != ATOMIC_OK) return rc;
+  // per-head dB = sanitize(write dstate_end)   (:57), dC = 0   (:70)
+  g = gemm_op(C, N, P, Z);
+  g.Z1 = H; g.Z0 = NT;
+  g.A = In{write, 0}; g.lda = P; g.sa = dense3((long long)C * P);
+  g.B = In{dse, 0}; g.ldb = N; g.sb = dense3((long long)P * N);
+  g.C = wB; g.ldc = N; g.sc = dense3((long long)C * N);
+  g.post = 2;
+  if ((rc = gemm(g, Z, "m2b_db1", L))) return rc;
+  const int fb = (int)((zcn + 255) / 256 < 65536 ? (zcn + 255) / 256 : 65536);
+  rc = L("m2b_fill", [&] { hipLaunchKernelGGL(fill0_k, dim3(fb), dim3(256), 0, L.st, wC, zcn); });
+  if (rc != ATOMIC_OK) return rc;
+  const int nt16 = C / 16;
+  rc = L("m2b_dbc", [&] {
+    hipLaunchKernelGGL(m2b_dbc_k, dim3(nt16 * nt16, Z), dim3(256), 0, L.st, d, idy, cum, dbx, dbc);
+  });
+  if (rc != ATOMIC_OK) return rc;
+  // the sub-block pairs in order: dB[J] += dBC[I,J]^T C[I], dC[I] += dBC[I,J] B[J],
+  // each sanitised   (:102-103,110-111)
+  for (int si = 0; si < C / bc; ++si) {
+    for (int sj = 0; sj <= si; ++sj) {
+      const int i0 = si * bc, j0 = sj * bc;
+      g = gemm_op(bc, N, bc, Z);
+      g.Z1 = H; g.Z0 = NT;
+      g.A = In{dbc + (size_t)i0 * C + j0, 0};   // transposed: A(m = j, k = i) = dBC[i0 + i][j0 + j]
+      g.lda = C; g.sa = dense3((long long)C * C); g.ta = 1;
+      g.B = In{Cp + (size_t)i0 * d.rC, 1}; g.ldb = d.rC; g.sb = rows3(d.rC);
+      g.C = wB + (size_t)j0 * N; g.ldc = N; g.sc = dense3((long long)C * N);
+      g.accum = 1; g.post = 2;
+      if ((rc = gemm(g, Z, "m2b_db_pair", L))) return rc;
+      g = gemm_op(bc, N, bc, Z);
+      g.Z1 = H; g.Z0 = NT;
+      g.A = In{dbc + (size_t)i0 * C + j0, 0}; g.lda = C; g.sa = dense3((long long)C * C);
+      g.B = In{Bp + (size_t)j0 * d.rB, 1}; g.ldb = d.rB; g.sb = rows3(d.rB);
+      g.C = wC + (size_t)i0 * N; g.ldc = N; g.sc = dense3((long long)C * N);
+      g.accum = 1; g.post = 2;
+      if ((rc = gemm(g, Z, "m2b_dc_pair", L))) return rc;
+    }
+  }
+  rc = L("m2b_pair", [&] {
+    hipLaunchKernelGGL(m2b_pair_k, dim3(Z * (P / 16)), dim3(256), 0, L.st, d, idt, ix, idy, cum, bcin, dbx, d1,
+                       ddd, ddt, dx, dcum);
+  });
+  if (rc != ATOMIC_OK) return rc;
+  const size_t tn = (size_t)d.B * d.T * N;
+  return L("m2b_headsum", [&] {
+    hipLaunchKernelGGL(m2b_headsum_k, dim3((unsigned)((tn + 255) / 256)), dim3(256), 0, L.st, d, wB, wC, dB, dC);
   });
 }
 

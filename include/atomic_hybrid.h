@@ -482,6 +482,23 @@ int atomic_mamba2_inter_chunk_combine(const atomic_mamba2_args* a, const float* 
                                       float* state_final, void* workspace, size_t workspace_bytes,
                                       void* stream);
 
+/* Bytes of workspace atomic_mamba2_intra_chunk_ssd_bwd needs (0 for unsupported args). */
+size_t atomic_mamba2_intra_chunk_ssd_bwd_workspace_size(const atomic_mamba2_args* a);
+
+/* MB2: intra_chunk_ssd_bwd_pallas(dt, x, B, C, cumdecay, dy, dstate_end_grad,
+ * chunk_size) (kernel_mamba2_bwd_b2_intra.py:32-180): the backward of M3 at
+ * args.chunk (64, 128 or 256, run as that chunk): the state-end part as
+ * whole-chunk products, the y_diag part over min(128, chunk)-row sub-block
+ * pairs with a sanitise after every accumulation, in float32.  cumdecay
+ * [B][H][NT][C][P] and dstate_end_grad [B][H][NT][P][N] float32, dy of
+ * args.dy_dtype; outputs float32: ddt, dx [B][T][H][P], dB, dC [B][T][N]
+ * (the per-head values summed over the heads, :168-178) and dcum
+ * [B][H][NT][C][P]. */
+int atomic_mamba2_intra_chunk_ssd_bwd(const atomic_mamba2_args* a, const void* dt, const void* x, const void* B,
+                                      const void* C, const float* cumdecay, const void* dy,
+                                      const float* dstate_end_grad, float* ddt, float* dx, float* dB, float* dC,
+                                      float* dcum, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------- output epilogue (downstream) */
 
 /* The two mixer blocks' output epilogue: RMSNorm over the model dimension

@@ -202,3 +202,51 @@ def test_gdn2_backward_stage_chain_matches_the_staged_oracle(dtype):
     torch.cuda.synchronize()
     for n, x, r in zip(("dq", "dk", "dv", "dw", "db", "dg", "dh0"), got, ref):
         _check(f"chain {n}", x, r)
+
+
+# ---------------------------------------------------------------- Mamba2 MB2
+from atomic_ops import kernel_mamba2_bwd_b2_intra as MB2  # noqa: E402
+from oracle import mamba2 as om  # noqa: E402
+
+
+@pytest.mark.parametrize("C,P,N,dy_dtype", [(256, 64, 128, BF16), (256, 128, 64, F32), (128, 64, 64, F32),
+                                            (64, 128, 128, BF16)])
+def test_mamba2_intra_backward_matches_the_oracle(C, P, N, dy_dtype):
+    """MB2 (kernel_mamba2_bwd_b2_intra.py:32-180) against the oracle's
+    restatement (itself the vector-Jacobian product of M3) on the bf16
+    inputs, the oracle's cumdecay and random cotangents."""
+    b, l, h = 1, 512, 2
+    banner(f"mamba2 MB2 chunk {C} P{P} N{N} dy {dy_dtype}")
+    d = inputs.mamba2_inputs(b, l, h, P, N, seed=400 + C + P, device=torch.device("cpu"), dO=True)
+    dt, x, Bm, Cm, A = (d[n] for n in ("dt", "x", "Bm", "Cm", "A"))
+    gen = torch.Generator().manual_seed(401 + C)
+    dy = torch.randn(b, l, h, P, generator=gen).to(dy_dtype)
+    dse = 0.3 * torch.randn(b, h, l // C, P, N, generator=gen)
+    cum = om.build_chunk_cumdecay(dt, A, C).float()
+    ref = om.intra_chunk_ssd_bwd(dt, x, Bm, Cm, cum.double(), dy.double(), dse.double(), C)
+    got = MB2.intra_chunk_ssd_bwd_pallas(dt.cuda(), x.cuda(), Bm.cuda(), Cm.cuda(), cum.cuda(), dy.cuda(),
+                                         dse.cuda(), C)
+    torch.cuda.synchronize()
+    for n, g_, r in zip(("ddt", "dx", "dB", "dC", "dcum"), got, ref):
+        _check(f"MB2 {n}", g_, r)
+
+
+def test_mamba2_intra_backward_sanitises_every_sub_block():
+    """A cotangent large enough that single sub-block pair sums pass +-1e4:
+    every output finite, within +-1e4 and equal to the oracle's."""
+    b, l, h, P, N, C = 1, 256, 2, 64, 64, 256
+    banner("mamba2 MB2 sanitise points")
+    d = inputs.mamba2_inputs(b, l, h, P, N, seed=407, device=torch.device("cpu"), dO=True)
+    dt, x, Bm, Cm, A = (d[n] for n in ("dt", "x", "Bm", "Cm", "A"))
+    gen = torch.Generator().manual_seed(408)
+    dy = torch.randn(b, l, h, P, generator=gen)
+    dy[:, 128:] = 1e7 * dy[:, 128:].abs()
+    dse = torch.randn(b, h, 1, P, N, generator=gen)
+    cum = om.build_chunk_cumdecay(dt, A, C).float()
+    ref = om.intra_chunk_ssd_bwd(dt, x, Bm, Cm, cum.double(), dy.double(), dse.double(), C)
+    got = MB2.intra_chunk_ssd_bwd_pallas(dt.cuda(), x.cuda(), Bm.cuda(), Cm.cuda(), cum.cuda(), dy.cuda(),
+                                         dse.cuda(), C)
+    torch.cuda.synchronize()
+    for n, g_, r in zip(("ddt", "dx", "dB", "dC", "dcum"), got, ref):
+        assert torch.isfinite(g_).all(), n
+        _check(f"MB2 {n} (large dy)", g_, r)
