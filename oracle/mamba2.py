@@ -418,3 +418,91 @@ def intra_chunk_ssd_bwd(dt, x, Bm, Cm, cumdecay, dy, dstate_end_grad, chunk_size
     dB_out = dB.sum(1).reshape(b, nt * C, n)                                    # :176-178
     dC_out = dC.sum(1).reshape(b, nt * C, n)
     return _stage_unchunk(ddt), _stage_unchunk(dx), dB_out, dC_out, dcum
+
+
+def state_only_bwd(state_prev, C_c, cumdecay_c, dy_off, dstate_carry, dtype=torch.float64):
+    """MB1's per-chunk step, ``_state_only_bwd`` (mamba2_bwd_state_reference.py:87-137):
+    the adjoint of y_off = (C state_prev^T) e^{clip(cum, -20, 0)} and of the
+    carried state_prev e^{clip(cum_last, -20, 0)}.  state_prev [b, h, p, n],
+    C_c [b, C, n], cumdecay_c and dy_off [b, C, h, p], dstate_carry [b, h, p, n].
+    Returns ``(dC_c [b, C, n], dstate_prev, dcumdecay_state [b, C, h, p])``, each sanitised."""
+    f = dtype
+    state_prev, C_c, cum, dy_off, carry = (t.to(f) for t in (state_prev, C_c, cumdecay_c, dy_off, dstate_carry))
+    Cs = cum.shape[1]
+    decay_h_raw = torch.clamp(cum, -CLIP_STEP, 0.0)                                  # :103
+    decay_h = torch.exp(decay_h_raw)
+    y_off_raw = torch.einsum("bis,bhds->bihd", C_c, state_prev)                      # :105
+    dce = torch.exp(torch.clamp(cum[:, -1], -CLIP_STEP, 0.0))                         # :107-108
+    dstate_prev = carry * dce[..., None]                                             # :112
+    d_dce = (carry * state_prev).sum(-1)                                             # :113
+    d_last_a = d_dce * dce * clip_mask(cum[:, -1], -CLIP_STEP, 0.0)                  # :114
+    dy_off_raw = dy_off * decay_h                                                    # :117
+    d_decay_h = dy_off * y_off_raw                                                   # :118
+    dC_c = torch.einsum("bihd,bhds->bis", dy_off_raw, state_prev)                    # :119
+    dstate_prev = dstate_prev + torch.einsum("bihd,bis->bhds", dy_off_raw, C_c)      # :120
+    d_cum_yoff = d_decay_h * decay_h * clip_mask(decay_h_raw, -CLIP_STEP, 0.0)       # :123
+    row = (torch.arange(Cs) == Cs - 1).to(f)[None, :, None, None]                    # :126
+    dcum_state = d_cum_yoff + row * d_last_a[:, None]                                # :127
+    return sanitize(dC_c), sanitize(dstate_prev), sanitize(dcum_state)               # :129-131
+
+
+def mamba2_bwd_scan(dt, A, Bm, Cm, x, chunk_size, do, dstate_final=None, state0=None,
+                    dtype=torch.float64):
+    """MB1 + MB3, ``mamba2_bwd_scan`` (kernel_mamba2_bwd_b1_state.py:132-254):
+    M2's cumdecay, the forward re-run of the reference chunk for the state
+    entering each chunk, the state-only reverse scan (its carry, sanitised,
+    is MB2's dstate_end_grad), MB2, and the sanitised sums.  Returns
+    ``(ddt_partial, dB, dC, dx, dstate0, dcumdecay)``; ddt_partial is the
+    dBx = dt x part only, and dcumdecay [b, h, NT, C, p] is both halves'."""
+    f = dtype
+    b, l, h, p = dt.shape
+    n = Bm.shape[-1]
+    C = chunk_size
+    nc = l // C
+    state = torch.zeros(b, h, p, n, dtype=f) if state0 is None else state0.to(f)
+    state = sanitize(state)                                                          # :168-170
+    cum = build_chunk_cumdecay(dt, A, C, dtype=f)                                    # :184 [b, h, nc, C, p]
+    dtc, Bc, Cc, xc, doc = (_to_chunks(t, C) for t in (dt, Bm, Cm, x, do))
+    prevs = []
+    for c in range(nc):                                                              # :190-195
+        prevs.append(state)
+        _, state, _ = chunk_ssd(dtc[c], A, Bc[c], Cc[c], xc[c], state, dtype=f)
+    carry = torch.zeros(b, h, p, n, dtype=f) if dstate_final is None else dstate_final.to(f)
+    dC_state = [None] * nc
+    dcum_state = [None] * nc
+    used = [None] * nc
+    for c in reversed(range(nc)):                                                    # :205-218
+        carry = sanitize(carry)
+        cum_c = cum[:, :, c].permute(0, 2, 1, 3)                                     # [b, C, h, p]
+        dC_c, dprev, dcum_c = state_only_bwd(prevs[c], Cc[c], cum_c, doc[c], carry, dtype=f)
+        used[c] = carry
+        dC_state[c], dcum_state[c] = dC_c, dcum_c
+        carry = sanitize(dprev)
+    dstate0 = sanitize(carry)                                                        # :219
+    dC_s = torch.stack(dC_state, 1).reshape(b, l, n)                                 # :225
+    dse = sanitize(torch.stack(used, 2))                                             # :230-231 [b, h, nc, p, n]
+    dcum_s = torch.stack(dcum_state, 2).permute(0, 3, 2, 1, 4)                       # :235 [b, h, nc, C, p]
+    ddt_i, dx_i, dB_i, dC_i, dcum_i = intra_chunk_ssd_bwd(dt, x, Bm, Cm, cum, do, dse, C, dtype=f)   # :240-243
+    dC = sanitize(dC_s + dC_i)                                                       # :249
+    dcum = sanitize(dcum_s + dcum_i)                                                 # :250
+    return sanitize(ddt_i), sanitize(dB_i), dC, sanitize(dx_i), dstate0, dcum        # :252-256
+
+
+def mamba2_dA_backward(dt_pallas, A, dcumdecay, chunk_size, dtype=torch.float64):
+    """MB4, ``mamba2_dA_backward`` (mamba2_bwd_a_dA_reference.py:60-115): M2's
+    adjoint.  dt_pallas, dcumdecay [b, h, NT, C, p]; A [h].  The cumdecay
+    cotangent masked by cumdecay's own clip, reverse-cumsummed over the chunk,
+    masked by the step exponent's clip: ddt contribution (sanitised, the
+    pallas layout) and dA = sum over everything but the head (sanitised)."""
+    f = dtype
+    dt_f, A_f, dcum = dt_pallas.to(f), A.to(f), dcumdecay.to(f)
+    assert dt_f.shape[3] == chunk_size
+    raw = dt_f * A_f[None, :, None, None, None]                                      # :89
+    clipped = torch.clamp(raw, -CLIP_STEP, CLIP_STEP)                                # :90
+    cum_raw = torch.cumsum(clipped, dim=3)                                           # :92-94
+    d_cum_raw = dcum * clip_mask(cum_raw, -CLIP_ACC, CLIP_ACC)                       # :98
+    d_clipped = torch.flip(torch.cumsum(torch.flip(d_cum_raw, [3]), 3), [3])         # :101-103
+    d_raw = d_clipped * clip_mask(raw, -CLIP_STEP, CLIP_STEP)                        # :106
+    ddt2 = d_raw * A_f[None, :, None, None, None]                                    # :109
+    dA = (d_raw * dt_f).sum((0, 2, 3, 4))                                            # :110
+    return sanitize(ddt2), sanitize(dA)                                              # :112-113

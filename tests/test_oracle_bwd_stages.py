@@ -9,6 +9,10 @@
 * Mamba2 MB2 (kernel_mamba2_bwd_b2_intra.py:32-180) is the vector-Jacobian
   product of M3 (intra_chunk_ssd, pinned by the element-by-element loops):
   the same cotangents through torch autograd give the same five gradients.
+* Mamba2 MB1 + MB3 (mamba2_bwd_scan, kernel_mamba2_bwd_b1_state.py:132-254)
+  and MB4 (mamba2_dA_backward, mamba2_bwd_a_dA_reference.py:60-115), composed
+  as the trainable op composes them (kernel_mamba2_trainable_B6.py:83-131),
+  equal MB0's per-chunk backward (pinned against autograd).
 * Planted mistakes in a stage fail the composition.
 """
 import torch
@@ -125,3 +129,70 @@ def test_mamba2_intra_backward_mistake_is_caught(monkeypatch):
     monkeypatch.setattr(om, "clip_mask", lambda v, lo, hi: 1.0 - real(v, lo, hi))
     bad = om.intra_chunk_ssd_bwd(dt, x, Bm, Cm, cum, dy, dse, 256)
     assert _rel(bad[4], good[4]) > 1e-3
+
+
+def _mamba2_staged(dt, A, Bm, Cm, x, C, do, dsf, s0):
+    """_mamba2_core_bwd (kernel_mamba2_trainable_B6.py:83-131) from the stages."""
+    b, l, h, p = dt.shape
+    ddt_p, dB, dC, dx, ds0, dcum = om.mamba2_bwd_scan(dt, A, Bm, Cm, x, C, do, dsf, s0)
+    dtp = dt.reshape(b, l // C, C, h, p).permute(0, 3, 1, 2, 4)
+    ddt2, dA = om.mamba2_dA_backward(dtp, A, dcum, C)
+    ddt = ddt_p + ddt2.permute(0, 2, 3, 1, 4).reshape(b, l, h, p)
+    return tuple(om.final_sanitize(t) for t in (ddt, dB, dC, dx, dA, ds0))
+
+
+def _mamba2_full_case(seed=3, l=512, h=2, p=8, n=6):
+    gen = torch.Generator().manual_seed(seed)
+    dt = torch.nn.functional.softplus(torch.randn(1, l, h, p, generator=gen, dtype=F64) - 3)
+    x = torch.randn(1, l, h, p, generator=gen, dtype=F64)
+    Bm = torch.randn(1, l, n, generator=gen, dtype=F64) / n ** 0.5
+    Cm = torch.randn(1, l, n, generator=gen, dtype=F64) / n ** 0.5
+    A = -0.5 * torch.rand(h, generator=gen, dtype=F64)
+    do = torch.randn(1, l, h, p, generator=gen, dtype=F64)
+    dsf = 0.3 * torch.randn(1, h, p, n, generator=gen, dtype=F64)
+    s0 = 0.3 * torch.randn(1, h, p, n, generator=gen, dtype=F64)
+    return dt, A, Bm, Cm, x, do, dsf, s0
+
+
+def test_mamba2_backward_stages_compose_to_mb0():
+    """MB1 + MB2 + MB3 (mamba2_bwd_scan) and MB4 (mamba2_dA_backward), composed
+    as the trainable op does, equal MB0's per-chunk backward (itself pinned
+    against autograd and finite differences) at chunks 64, 128 and 256."""
+    dt, A, Bm, Cm, x, do, dsf, s0 = _mamba2_full_case()
+    for C in (64, 128, 256):
+        got = _mamba2_staged(dt, A, Bm, Cm, x, C, do, dsf, s0)
+        ref = om.chunk_ssd_bwd_scan(dt, A, Bm, Cm, x, C, do, dsf, s0)
+        ref = tuple(om.final_sanitize(t) for t in ref)
+        for name, a, c in zip(("ddt", "dB", "dC", "dx", "dA", "dstate0"), got, ref):
+            assert _rel(a, c) < 1e-11, (C, name)
+
+
+def test_mamba2_backward_stage_mistakes_are_caught(monkeypatch):
+    dt, A, Bm, Cm, x, do, dsf, s0 = _mamba2_full_case(seed=9)
+    ref = tuple(om.final_sanitize(t) for t in om.chunk_ssd_bwd_scan(dt, A, Bm, Cm, x, 128, do, dsf, s0))
+
+    def worst():
+        got = _mamba2_staged(dt, A, Bm, Cm, x, 128, do, dsf, s0)
+        return max(_rel(a, c) for a, c in zip(got, ref))
+
+    # (1) MB1 without the carried state's decay term on the last row
+    real = om.state_only_bwd
+
+    def no_last_row(state_prev, C_c, cum, dy_off, carry, dtype=F64):
+        dC, dp, dcum = real(state_prev, C_c, cum, dy_off, carry, dtype=dtype)
+        d0 = real(state_prev, C_c, cum, dy_off, torch.zeros_like(carry), dtype=dtype)[2]
+        dcum = dcum.clone()
+        dcum[:, -1] = d0[:, -1]
+        return dC, dp, dcum
+    monkeypatch.setattr(om, "state_only_bwd", no_last_row)
+    assert worst() > 1e-6
+    monkeypatch.undo()
+
+    # (2) MB4 with a forward instead of a reverse cumsum
+    def forward_cumsum(dt_p, A_, dcum, C, dtype=F64):
+        f = dtype
+        raw = dt_p.to(f) * A_.to(f)[None, :, None, None, None]
+        d = torch.cumsum(dcum.to(f), 3) * om.clip_mask(raw, -20.0, 20.0)
+        return om.sanitize(d * A_.to(f)[None, :, None, None, None]), om.sanitize((d * dt_p.to(f)).sum((0, 2, 3, 4)))
+    monkeypatch.setattr(om, "mamba2_dA_backward", forward_cumsum)
+    assert worst() > 1e-6
