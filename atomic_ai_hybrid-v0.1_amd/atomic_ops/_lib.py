@@ -212,6 +212,10 @@ _SIGS = {
     "atomic_mamba2_intra_chunk_ssd_bwd_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(Mamba2Args)]),
     "atomic_mamba2_intra_chunk_ssd_bwd": (ctypes.c_int, [ctypes.POINTER(Mamba2Args)] + [_P] * 12
                                           + [_P, ctypes.c_size_t, _P]),
+    "atomic_mamba2_bwd_scan_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(Mamba2Args)]),
+    "atomic_mamba2_bwd_scan": (ctypes.c_int, [ctypes.POINTER(Mamba2Args)] + [_P] * 14 + [_P, ctypes.c_size_t, _P]),
+    "atomic_mamba2_da_backward_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(Mamba2Args)]),
+    "atomic_mamba2_da_backward": (ctypes.c_int, [ctypes.POINTER(Mamba2Args)] + [_P] * 5 + [_P, ctypes.c_size_t, _P]),
     "atomic_norm_gate_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(NormGateArgs)]),
     "atomic_norm_gate_fwd": (ctypes.c_int, [ctypes.POINTER(NormGateArgs)] + [_P] * 4 + [_P]),
     "atomic_norm_gate_bwd": (ctypes.c_int, [ctypes.POINTER(NormGateArgs)] + [_P] * 7 + [_P, ctypes.c_size_t, _P]),

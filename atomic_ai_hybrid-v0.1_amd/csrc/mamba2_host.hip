@@ -655,3 +655,72 @@ extern "C" int atomic_mamba2_intra_chunk_ssd_bwd(const atomic_mamba2_args* a, co
   return m_intra_bwd(d, a->dy_dtype, dt, x, B, C, cumdecay, dy, dstate_end_grad, ddt, dx, dB, dC, dcum,
                      static_cast<float*>(workspace), L);
 }
+
+// ------------------------------------------------------------------ MB1 + MB3 and MB4 stage entries
+static int mamba2_bwd_stage_dims(const atomic_mamba2_args* a, Mamba2Plan* p) {
+  const int rc = mamba2_stage_plan(a, p);
+  if (rc != ATOMIC_OK) return rc;
+  return p->dm.P % 32 == 0 ? ATOMIC_OK : ATOMIC_ERR_SHAPE;
+}
+
+extern "C" size_t atomic_mamba2_bwd_scan_workspace_size(const atomic_mamba2_args* a) {
+  Mamba2Plan p;
+  if (mamba2_bwd_stage_dims(a, &p) != ATOMIC_OK) return 0;
+  return m2_align(m_bwd_scan_ws(p.dm));
+}
+
+extern "C" int atomic_mamba2_bwd_scan(const atomic_mamba2_args* a, const void* dt, const float* A, const void* B,
+                                      const void* C, const void* x, const void* dy, const float* dstate_final,
+                                      const float* state0, float* ddt, float* dB, float* dC, float* dx,
+                                      float* dstate0, float* dcumdecay, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+  Mamba2Plan p;
+  const int rc = mamba2_bwd_stage_dims(a, &p);
+  if (rc != ATOMIC_OK) return rc;
+  if (!dt || !A || !B || !C || !x || !dy || !ddt || !dB || !dC || !dx || !dstate0 || !dcumdecay)
+    return ATOMIC_ERR_NULL;
+  if (!workspace || workspace_bytes < m_bwd_scan_ws(p.dm)) return ATOMIC_ERR_WORKSPACE;
+  ws_tag_clobber(workspace, workspace_bytes);
+  Launch L{a->profile, (hipStream_t)stream};
+  // M2's cumdecay into the workspace's first array (kernel_mamba2_bwd_b1_state.py:184)
+  float* cum = static_cast<float*>(workspace);
+  const int r2 = mamba2_cumdecay_stage(p, dt, A, cum, L);
+  if (r2 != ATOMIC_OK) return r2;
+  return m_bwd_scan(p.dm, a->dy_dtype, dt, x, B, C, cum, dy, dstate_final, state0, ddt, dB, dC, dx, dstate0,
+                    dcumdecay, cum, L);
+}
+
+// MB4 takes dt in the per-chunk layout, bf16 or fp32 (args.dtype); dstate
+// does not enter.
+static int mamba2_da_dims(const atomic_mamba2_args* a, Mamba2Dims* d) {
+  if (!a) return ATOMIC_ERR_NULL;
+  if (a->dtype != ATOMIC_BF16 && a->dtype != ATOMIC_F32) return ATOMIC_ERR_DTYPE;
+  if (a->batch <= 0 || a->heads <= 0 || a->seqlen <= 0) return ATOMIC_ERR_SHAPE;
+  if (a->chunk != 64 && a->chunk != 128 && a->chunk != 256) return ATOMIC_ERR_SHAPE;
+  if (a->seqlen % a->chunk != 0) return ATOMIC_ERR_SHAPE;
+  if (a->headdim != 64 && a->headdim != 128 && a->headdim != 192) return ATOMIC_ERR_SHAPE;
+  Mamba2Dims m{};
+  m.B = a->batch; m.T = a->seqlen; m.H = a->heads; m.P = a->headdim; m.N = a->dstate;
+  m.C = a->chunk; m.NT = a->seqlen / a->chunk;
+  *d = m;
+  return ATOMIC_OK;
+}
+
+extern "C" size_t atomic_mamba2_da_backward_workspace_size(const atomic_mamba2_args* a) {
+  Mamba2Dims d;
+  if (mamba2_da_dims(a, &d) != ATOMIC_OK) return 0;
+  return m2_align(m_da_bwd_ws(d));
+}
+
+extern "C" int atomic_mamba2_da_backward(const atomic_mamba2_args* a, const void* dt_chunks, const float* A,
+                                         const float* dcumdecay, float* ddt_contrib, float* dA, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  Mamba2Dims d;
+  const int rc = mamba2_da_dims(a, &d);
+  if (rc != ATOMIC_OK) return rc;
+  if (!dt_chunks || !A || !dcumdecay || !ddt_contrib || !dA) return ATOMIC_ERR_NULL;
+  if (!workspace || workspace_bytes < m_da_bwd_ws(d)) return ATOMIC_ERR_WORKSPACE;
+  ws_tag_clobber(workspace, workspace_bytes);
+  Launch L{a->profile, (hipStream_t)stream};
+  return m_da_bwd(d, a->dtype, dt_chunks, A, dcumdecay, ddt_contrib, dA, static_cast<float*>(workspace), L);
+}

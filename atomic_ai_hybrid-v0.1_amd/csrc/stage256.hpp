@@ -67,4 +67,20 @@ int m_intra_bwd(const Mamba2Dims& d, int dy_dtype, const void* dt, const void* x
                 const float* cum, const void* dy, const float* dse, float* ddt, float* dx, float* dB, float* dC,
                 float* dcum, float* ws, Launch& L);
 
+// Mamba2 MB1 + MB3 (mamba2_bwd_scan): workspace m_bwd_scan_ws bytes, whose
+// first B H NT C P floats hold the cumdecay (M2's output, written by the
+// caller; ws doubles as cum).  Outputs fp32: ddt (the dBx part), dx [B][T][H][P],
+// dB, dC [B][T][N], dstate0 [B][H][P][N], dcum [B][H][NT][C][P].  P a
+// multiple of 32, N 64 or 128.
+size_t m_bwd_scan_ws(const Mamba2Dims& d);
+int m_bwd_scan(const Mamba2Dims& d, int dy_dtype, const void* dt, const void* x, const void* Bm, const void* Cm,
+               const float* cum, const void* dy, const float* dsf, const float* state0, float* ddt, float* dB,
+               float* dC, float* dx, float* ds0, float* dcum, float* ws, Launch& L);
+// Mamba2 MB4 (mamba2_dA_backward): dt per chunk [B][H][NT][C][P] of dt_dtype,
+// A [H], dcum [B][H][NT][C][P]; ddt2 like dt (fp32), dA [H]; workspace
+// m_da_bwd_ws bytes; C <= 256.
+size_t m_da_bwd_ws(const Mamba2Dims& d);
+int m_da_bwd(const Mamba2Dims& d, int dt_dtype, const void* dtp, const float* A, const float* dcum, float* ddt2,
+             float* dA, float* ws, Launch& L);
+
 }  // namespace ah

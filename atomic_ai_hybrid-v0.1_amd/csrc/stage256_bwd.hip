@@ -596,6 +596,228 @@ __global__ __launch_bounds__(256) void fill0_k(float* __restrict__ p, size_t n) 
   for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (size_t)gridDim.x * 256) p[e] = 0.f;
 }
 
+// ------------------------------------------------------------------ Mamba2 MB1 + MB3, MB4
+// The reference's trainable Mamba2 backward (kernel_mamba2_trainable_B6.py:
+// 83-131): mamba2_bwd_scan (kernel_mamba2_bwd_b1_state.py:132-254) re-runs
+// the reference chunk forward for the state entering each chunk, runs the
+// state-only reverse scan (mamba2_bwd_state_reference.py:87-137), MB2 with the
+// scan's carries, and sums the two halves; mamba2_dA_backward
+// (mamba2_bwd_a_dA_reference.py:60-115) is M2's adjoint.  The scans take one
+// workgroup per (batch, head, 32 channels); thread (channel dd, column group
+// sg) owns state columns sg + 8 k.
+constexpr int MS_PT = 32, MS_RB = 32;
+
+// The reference chunk's state recurrence (mamba2_ssd_reference.py:125-146):
+// state_end = sanitize(B^T (dBx sanitize(e^{clip(cl - cum, +-20)}, 1e6))),
+// state = sanitize(state e^{clip(cl, -20, 0)} + state_end); the state entering
+// each chunk goes to sprev [B][NT][H][P][N].
+template <int N>
+__global__ __launch_bounds__(256) void m2s_fwd_k(Mamba2Dims d, In dt, In x, In Bm, const float* __restrict__ cum,
+                                                 const float* __restrict__ state0, float* __restrict__ sprev) {
+  constexpr int NK = N / 8;
+  __shared__ float sW[MS_RB][MS_PT + 1];
+  __shared__ float sB[MS_RB][N + 1];
+  const int C = d.C, P = d.P, npt = P / MS_PT;
+  const int bh = blockIdx.x / npt, p0 = (blockIdx.x % npt) * MS_PT;
+  const int h = bh % d.H, b = bh / d.H;
+  const int t = threadIdx.x, dd = t % MS_PT, sg = t / MS_PT;
+  float st[NK];
+#pragma unroll
+  for (int k = 0; k < NK; ++k)
+    st[k] = state0 ? sanitize(state0[((size_t)bh * P + p0 + dd) * N + sg + 8 * k]) : 0.f;   // :168-170
+  for (int n = 0; n < d.NT; ++n) {
+    const float* cz = cum + ((size_t)bh * d.NT + n) * C * P;
+    float* sp = sprev + ((((size_t)b * d.NT + n) * d.H + h) * P + p0 + dd) * N;
+#pragma unroll
+    for (int k = 0; k < NK; ++k) sp[sg + 8 * k] = st[k];
+    float acc[NK];
+#pragma unroll
+    for (int k = 0; k < NK; ++k) acc[k] = 0.f;
+    for (int r0 = 0; r0 < C; r0 += MS_RB) {
+      for (int e = t; e < MS_RB * MS_PT; e += 256) {
+        const int r = e / MS_PT, c = e % MS_PT;
+        const size_t row = (size_t)b * d.T + (size_t)n * C + r0 + r, col = (size_t)h * P + p0 + c;
+        const float bx = sanitize(ld(dt, row * d.rdt + col) * ld(x, row * d.rx + col));          // :125-126
+        const float raw = cz[(size_t)(C - 1) * P + p0 + c] - cz[(size_t)(r0 + r) * P + p0 + c];
+        const float dte = sanitize(__expf(fminf(fmaxf(raw, -kClipDecay), kClipDecay)), 1e6f);  // :133-134
+        sW[r][c] = bx * dte;                                                                     // :135
+      }
+      for (int e = t; e < MS_RB * N; e += 256) {
+        const int r = e / N, s = e % N;
+        sB[r][s] = ld(Bm, ((size_t)b * d.T + (size_t)n * C + r0 + r) * d.rB + s);
+      }
+      __syncthreads();
+      for (int r = 0; r < MS_RB; ++r) {
+        const float w = sW[r][dd];
+#pragma unroll
+        for (int k = 0; k < NK; ++k) acc[k] = fmaf(w, sB[r][sg + 8 * k], acc[k]);
+      }
+      __syncthreads();
+    }
+    const float dce = __expf(fminf(fmaxf(cz[(size_t)(C - 1) * P + p0 + dd], -kClipDecay), 0.f));   // :144
+#pragma unroll
+    for (int k = 0; k < NK; ++k) st[k] = sanitize(st[k] * dce + sanitize(acc[k]));              // :136-137,145-146
+  }
+}
+
+// The state-only reverse scan (kernel_mamba2_bwd_b1_state.py:205-219 over
+// mamba2_bwd_state_reference.py:87-137): per chunk the sanitised carry (MB2's
+// dstate_end_grad, dse [B][H][NT][P][N]), dcum_state [B][H][NT][C][P],
+// dy_off_raw = dy e^{clip(cum, -20, 0)} ([B][T][H][P], for dC), and the next
+// carry sanitize(carry e^{clip(cl, -20, 0)} + dy_off_raw^T C).
+template <int N>
+__global__ __launch_bounds__(256) void m2s_bwd_k(Mamba2Dims d, In Cm, In dy, const float* __restrict__ cum,
+                                                 const float* __restrict__ sprev, const float* __restrict__ dsf,
+                                                 float* __restrict__ dyoff, float* __restrict__ dcum_s,
+                                                 float* __restrict__ dse, float* __restrict__ ds0) {
+  constexpr int NK = N / 8;
+  __shared__ float sCar[MS_PT][N + 1];
+  __shared__ float sSp[MS_PT][N + 1];
+  __shared__ float sC[MS_RB][N + 1];
+  __shared__ float sDo[MS_RB][MS_PT + 1];
+  __shared__ float sLa[MS_PT];
+  const int C = d.C, P = d.P, npt = P / MS_PT;
+  const int bh = blockIdx.x / npt, p0 = (blockIdx.x % npt) * MS_PT;
+  const int h = bh % d.H, b = bh / d.H;
+  const int t = threadIdx.x, dd = t % MS_PT, sg = t / MS_PT;
+#pragma unroll
+  for (int k = 0; k < NK; ++k)
+    sCar[dd][sg + 8 * k] = dsf ? dsf[((size_t)bh * P + p0 + dd) * N + sg + 8 * k] : 0.f;
+  for (int n = d.NT - 1; n >= 0; --n) {
+    const size_t z = (size_t)bh * d.NT + n;
+    const float* cz = cum + z * C * P;
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      const int s = sg + 8 * k;
+      const float c = sanitize(sCar[dd][s]);                                              // :208
+      sCar[dd][s] = c;
+      dse[(z * P + p0 + dd) * N + s] = c;                                                 // :216,230-231
+      sSp[dd][s] = sprev[((((size_t)b * d.NT + n) * d.H + h) * P + p0 + dd) * N + s];
+    }
+    __syncthreads();
+    if (t < MS_PT) {  // d_cumdecay_last_a (:113-114)
+      float a = 0.f;
+      for (int s = 0; s < N; ++s) a = fmaf(sCar[t][s], sSp[t][s], a);
+      const float cl = cz[(size_t)(C - 1) * P + p0 + t];
+      const float dce = __expf(fminf(fmaxf(cl, -kClipDecay), 0.f));
+      sLa[t] = a * dce * ((cl >= -kClipDecay && cl <= 0.f) ? 1.f : 0.f);
+    }
+    float acc[NK];
+#pragma unroll
+    for (int k = 0; k < NK; ++k) acc[k] = 0.f;
+    for (int r0 = 0; r0 < C; r0 += MS_RB) {
+      for (int e = t; e < MS_RB * N; e += 256) {
+        const int r = e / N, s = e % N;
+        sC[r][s] = ld(Cm, ((size_t)b * d.T + (size_t)n * C + r0 + r) * d.rC + s);
+      }
+      for (int e = t; e < MS_RB * MS_PT; e += 256) {
+        const int r = e / MS_PT, c = e % MS_PT;
+        const size_t row = (size_t)b * d.T + (size_t)n * C + r0 + r, col = (size_t)h * P + p0 + c;
+        const float dh = __expf(fminf(fmaxf(cz[(size_t)(r0 + r) * P + p0 + c], -kClipDecay), 0.f));   // :103-104
+        const float v = ld(dy, row * d.rdy + col) * dh;                                   // :117
+        sDo[r][c] = v;
+        dyoff[row * (size_t)d.H * P + col] = v;
+      }
+      __syncthreads();
+      for (int e = t; e < MS_RB * MS_PT; e += 256) {  // dcum_state of the piece (:118,123-127)
+        const int r = e / MS_PT, c = e % MS_PT;
+        float y = 0.f;
+        for (int s = 0; s < N; ++s) y = fmaf(sC[r][s], sSp[c][s], y);                     // y_off_raw (:105)
+        const size_t row = (size_t)b * d.T + (size_t)n * C + r0 + r, col = (size_t)h * P + p0 + c;
+        const float cv = cz[(size_t)(r0 + r) * P + p0 + c];
+        const float dh = __expf(fminf(fmaxf(cv, -kClipDecay), 0.f));
+        const float m = (cv >= -kClipDecay && cv <= 0.f) ? 1.f : 0.f;
+        float v = ld(dy, row * d.rdy + col) * y * dh * m;
+        if (r0 + r == C - 1) v = v + sLa[c];
+        dcum_s[(z * C + r0 + r) * P + p0 + c] = sanitize(v);                               // :131
+      }
+      for (int r = 0; r < MS_RB; ++r) {  // dy_off_raw^T C (:120)
+        const float v = sDo[r][dd];
+#pragma unroll
+        for (int k = 0; k < NK; ++k) acc[k] = fmaf(v, sC[r][sg + 8 * k], acc[k]);
+      }
+      __syncthreads();
+    }
+    const float dce = __expf(fminf(fmaxf(cz[(size_t)(C - 1) * P + p0 + dd], -kClipDecay), 0.f));
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      const int s = sg + 8 * k;
+      sCar[dd][s] = sanitize(sCar[dd][s] * dce + acc[k]);                                 // :112,120,130
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int k = 0; k < NK; ++k)
+    ds0[((size_t)bh * P + p0 + dd) * N + sg + 8 * k] = sanitize(sCar[dd][sg + 8 * k]);    // :219
+}
+
+// MB3's sums (kernel_mamba2_bwd_b1_state.py:249-256), in place on MB2's outputs.
+__global__ __launch_bounds__(256) void m2s_comb_k(size_t nhp, size_t nn, size_t ncum, float* __restrict__ ddt,
+                                                  float* __restrict__ dx, float* __restrict__ dB,
+                                                  float* __restrict__ dC, const float* __restrict__ dC_s,
+                                                  float* __restrict__ dcum, const float* __restrict__ dcum_s) {
+  const size_t top = nhp > ncum ? nhp : ncum;
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < top; e += (size_t)gridDim.x * 256) {
+    if (e < nhp) {
+      ddt[e] = sanitize(ddt[e]);
+      dx[e] = sanitize(dx[e]);
+    }
+    if (e < nn) {
+      dB[e] = sanitize(dB[e]);
+      dC[e] = sanitize(dC_s[e] + dC[e]);
+    }
+    if (e < ncum) dcum[e] = sanitize(dcum_s[e] + dcum[e]);
+  }
+}
+
+// MB4 per (batch, head, chunk, 64 channels), one lane per channel: the step
+// exponents' clipped cumsum (kept in LDS), then the masked cumdecay cotangent
+// reverse-cumsummed and masked by the step clip: ddt's second part and the
+// workgroup's part of dA (mamba2_bwd_a_dA_reference.py:89-113).
+__global__ __launch_bounds__(64) void m2s_da_k(Mamba2Dims d, In dtp, const float* __restrict__ A,
+                                               const float* __restrict__ dcum, float* __restrict__ ddt2,
+                                               float* __restrict__ part) {
+  __shared__ float sCr[256][65];
+  const int C = d.C, P = d.P, nps = (P + 63) / 64;
+  const size_t z = blockIdx.x / nps;
+  const int p0 = (blockIdx.x % nps) * 64, c = threadIdx.x, p = p0 + c;
+  const int h = (int)((z / d.NT) % d.H);
+  const float a = A[h];
+  float dsum = 0.f;
+  if (p < P) {
+    float s = 0.f;
+    for (int i = 0; i < C; ++i) {                                        // :89-94
+      s += fminf(fmaxf(ld(dtp, (z * C + i) * P + p) * a, -kClipDecay), kClipDecay);
+      sCr[i][c] = s;
+    }
+    float acc = 0.f;
+    for (int i = C - 1; i >= 0; --i) {
+      const size_t o = (z * C + i) * P + p;
+      const float cr = sCr[i][c];
+      acc += dcum[o] * ((cr >= -kClipAcc && cr <= kClipAcc) ? 1.f : 0.f);   // :98,101-103
+      const float dtv = ld(dtp, o), raw = dtv * a;
+      const float dr = acc * ((raw >= -kClipDecay && raw <= kClipDecay) ? 1.f : 0.f);   // :106
+      ddt2[o] = sanitize(dr * a);                                        // :109,112
+      dsum = fmaf(dr, dtv, dsum);                                        // :110
+    }
+  }
+#pragma unroll
+  for (int sh = 1; sh < 64; sh <<= 1) dsum += __shfl_xor(dsum, sh);
+  if (c == 0) part[blockIdx.x] = dsum;
+}
+
+// dA[h] = sanitize(sum of the head's workgroup parts), in a fixed order (:110,113).
+__global__ __launch_bounds__(256) void m2s_da_sum_k(Mamba2Dims d, int nps, const float* __restrict__ part,
+                                                    float* __restrict__ dA) {
+  const int h = blockIdx.x * 256 + threadIdx.x;
+  if (h >= d.H) return;
+  float s = 0.f;
+  for (int b = 0; b < d.B; ++b)
+    for (int n = 0; n < d.NT; ++n)
+      for (int q = 0; q < nps; ++q) s += part[(((size_t)b * d.H + h) * d.NT + n) * nps + q];
+  dA[h] = sanitize(s);
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ launchers
@@ -815,6 +1037,86 @@ int m_intra_bwd(const Mamba2Dims& d, int dy_dtype, const void* dt, const void* x
   const size_t tn = (size_t)d.B * d.T * N;
   return L("m2b_headsum", [&] {
     hipLaunchKernelGGL(m2b_headsum_k, dim3((unsigned)((tn + 255) / 256)), dim3(256), 0, L.st, d, wB, wC, dB, dC);
+  });
+}
+
+
+size_t m_bwd_scan_ws(const Mamba2Dims& d) {
+  const size_t Z = (size_t)d.B * d.H * d.NT, C = d.C;
+  const size_t own = Z * C * d.P            // cumdecay
+                     + (size_t)d.B * d.NT * d.H * d.P * d.N   // state entering each chunk
+                     + (size_t)d.B * d.T * d.H * d.P          // dy_off_raw
+                     + (size_t)d.B * d.T * d.N                // dC_state
+                     + Z * C * d.P                            // dcum_state
+                     + Z * d.P * d.N;                         // the carries (dstate_end_grad)
+  return own * sizeof(float) + m_intra_bwd_ws(d);
+}
+
+int m_bwd_scan(const Mamba2Dims& d, int dy_dtype, const void* dt, const void* x, const void* Bm, const void* Cm,
+               const float* cum, const void* dy, const float* dsf, const float* state0, float* ddt, float* dB,
+               float* dC, float* dx, float* ds0, float* dcum, float* ws, Launch& L) {
+  const int C = d.C, P = d.P, N = d.N;
+  const size_t Z = (size_t)d.B * d.H * d.NT;
+  if (P % MS_PT != 0 || (N != 64 && N != 128)) return ATOMIC_ERR_SHAPE;
+  float* sprev = ws + Z * C * P;   // ws starts with the cumdecay the caller wrote
+  float* dyoff = sprev + (size_t)d.B * d.NT * d.H * P * N;
+  float* dC_s = dyoff + (size_t)d.B * d.T * d.H * P;
+  float* dcum_s = dC_s + (size_t)d.B * d.T * N;
+  float* dse = dcum_s + Z * C * P;
+  float* wmb2 = dse + Z * P * N;
+  const In idt{dt, 1}, ix{x, 1}, iB{Bm, 1}, iC{Cm, 1}, idy{dy, dy_dtype == ATOMIC_BF16};
+  const dim3 grid((unsigned)(d.B * d.H * (P / MS_PT)));
+  int rc = L("m2s_fwd", [&] {
+    if (N == 128)
+      hipLaunchKernelGGL((m2s_fwd_k<128>), grid, dim3(256), 0, L.st, d, idt, ix, iB, cum, state0, sprev);
+    else
+      hipLaunchKernelGGL((m2s_fwd_k<64>), grid, dim3(256), 0, L.st, d, idt, ix, iB, cum, state0, sprev);
+  });
+  if (rc != ATOMIC_OK) return rc;
+  rc = L("m2s_bwd", [&] {
+    if (N == 128)
+      hipLaunchKernelGGL((m2s_bwd_k<128>), grid, dim3(256), 0, L.st, d, iC, idy, cum, sprev, dsf, dyoff, dcum_s,
+                         dse, ds0);
+    else
+      hipLaunchKernelGGL((m2s_bwd_k<64>), grid, dim3(256), 0, L.st, d, iC, idy, cum, sprev, dsf, dyoff, dcum_s, dse,
+                         ds0);
+  });
+  if (rc != ATOMIC_OK) return rc;
+  // dC_state = sanitize(dy_off_raw C-rows x state_prev over (head, channel)) per (batch, chunk)   (:119,129)
+  GemmOp g = gemm_op(C, N, d.H * P, d.B * d.NT);
+  g.Z1 = 1; g.Z0 = d.NT;
+  g.A = In{dyoff, 0}; g.lda = (long long)d.H * P;
+  g.sa = Bat{(long long)d.T * d.H * P, 0, (long long)C * d.H * P};
+  g.B = In{sprev, 0}; g.ldb = N; g.sb = Bat{(long long)d.NT * d.H * P * N, 0, (long long)d.H * P * N};
+  g.C = dC_s; g.ldc = N; g.sc = Bat{(long long)d.T * N, 0, (long long)C * N};
+  g.post = 2;
+  if ((rc = gemm(g, d.B * d.NT, "m2s_dc_state", L))) return rc;
+  // MB2 with the carries as dstate_end_grad (:240-243)
+  if ((rc = m_intra_bwd(d, dy_dtype, dt, x, Bm, Cm, cum, dy, dse, ddt, dx, dB, dC, dcum, wmb2, L))) return rc;
+  const size_t nhp = (size_t)d.B * d.T * d.H * P, nn = (size_t)d.B * d.T * N, ncum = Z * C * P;
+  const size_t top = nhp > ncum ? nhp : ncum;
+  const int eb = (int)((top + 255) / 256 < 65536 ? (top + 255) / 256 : 65536);
+  return L("m2s_comb", [&] {
+    hipLaunchKernelGGL(m2s_comb_k, dim3(eb), dim3(256), 0, L.st, nhp, nn, ncum, ddt, dx, dB, dC, dC_s, dcum, dcum_s);
+  });
+}
+
+size_t m_da_bwd_ws(const Mamba2Dims& d) {
+  return (size_t)d.B * d.H * d.NT * ((d.P + 63) / 64) * sizeof(float);
+}
+
+int m_da_bwd(const Mamba2Dims& d, int dt_dtype, const void* dtp, const float* A, const float* dcum, float* ddt2,
+             float* dA, float* ws, Launch& L) {
+  if (d.C > 256) return ATOMIC_ERR_SHAPE;
+  const int nps = (d.P + 63) / 64;
+  const unsigned nb = (unsigned)((size_t)d.B * d.H * d.NT * nps);
+  const In it{dtp, dt_dtype == ATOMIC_BF16};
+  int rc = L("m2s_da", [&] {
+    hipLaunchKernelGGL(m2s_da_k, dim3(nb), dim3(64), 0, L.st, d, it, A, dcum, ddt2, ws);
+  });
+  if (rc != ATOMIC_OK) return rc;
+  return L("m2s_da_sum", [&] {
+    hipLaunchKernelGGL(m2s_da_sum_k, dim3((unsigned)((d.H + 255) / 256)), dim3(256), 0, L.st, d, nps, ws, dA);
   });
 }
 

@@ -499,6 +499,35 @@ int atomic_mamba2_intra_chunk_ssd_bwd(const atomic_mamba2_args* a, const void* d
                                       const float* dstate_end_grad, float* ddt, float* dx, float* dB, float* dC,
                                       float* dcum, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of workspace atomic_mamba2_bwd_scan needs (0 for unsupported args). */
+size_t atomic_mamba2_bwd_scan_workspace_size(const atomic_mamba2_args* a);
+
+/* MB1 + MB3: mamba2_bwd_scan(dt, A, B, C, x, chunk_size, do, dstate_final,
+ * state0) (kernel_mamba2_bwd_b1_state.py:132-254) at args.chunk (64, 128 or
+ * 256; P a multiple of 32): M2's cumdecay, the reference chunk's forward
+ * re-run for the state entering each chunk (state0 sanitised, NULL = zeros),
+ * the state-only reverse scan (mamba2_bwd_state_reference.py:87-137) whose
+ * sanitised carries are MB2's dstate_end_grad, MB2, and the sanitised sums
+ * of the two halves.  dstate_final [B][H][P][N] or NULL.  Outputs float32:
+ * ddt (the dt x part only, as the reference's), dx [B][T][H][P], dB, dC
+ * [B][T][N], dstate0 [B][H][P][N] and dcumdecay [B][H][NT][C][P]. */
+int atomic_mamba2_bwd_scan(const atomic_mamba2_args* a, const void* dt, const float* A, const void* B, const void* C,
+                           const void* x, const void* dy, const float* dstate_final, const float* state0, float* ddt,
+                           float* dB, float* dC, float* dx, float* dstate0, float* dcumdecay, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace atomic_mamba2_da_backward needs (0 for unsupported args). */
+size_t atomic_mamba2_da_backward_workspace_size(const atomic_mamba2_args* a);
+
+/* MB4: mamba2_dA_backward(dt_pallas, A, dcumdecay_combined, chunk_size)
+ * (mamba2_bwd_a_dA_reference.py:60-115): M2's adjoint.  dt per chunk
+ * [B][H][NT][C][P] in args.dtype (bf16 or fp32), A [H], dcumdecay
+ * [B][H][NT][C][P] float32; ddt_contrib (float32, dt's layout) and dA [H],
+ * each sanitised.  args.dstate is not read. */
+int atomic_mamba2_da_backward(const atomic_mamba2_args* a, const void* dt_chunks, const float* A,
+                              const float* dcumdecay, float* ddt_contrib, float* dA, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------- output epilogue (downstream) */
 
 /* The two mixer blocks' output epilogue: RMSNorm over the model dimension

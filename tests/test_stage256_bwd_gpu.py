@@ -250,3 +250,50 @@ def test_mamba2_intra_backward_sanitises_every_sub_block():
     for n, g_, r in zip(("ddt", "dx", "dB", "dC", "dcum"), got, ref):
         assert torch.isfinite(g_).all(), n
         _check(f"MB2 {n} (large dy)", g_, r)
+
+
+# ---------------------------------------------------------------- Mamba2 MB1 + MB3, MB4
+from atomic_ops import kernel_mamba2_bwd_b1_state as MB1  # noqa: E402
+from atomic_ops import mamba2_bwd_a_dA_reference as MB4  # noqa: E402
+
+
+def _m2_full(b, l, h, P, N, seed, dy_dtype):
+    d = inputs.mamba2_inputs(b, l, h, P, N, seed=seed, device=torch.device("cpu"), dO=True)
+    dt, x, Bm, Cm, A = (d[n] for n in ("dt", "x", "Bm", "Cm", "A"))
+    gen = torch.Generator().manual_seed(seed + 1)
+    dy = torch.randn(b, l, h, P, generator=gen).to(dy_dtype)
+    dsf = 0.3 * torch.randn(b, h, P, N, generator=gen)
+    s0 = 0.3 * torch.randn(b, h, P, N, generator=gen)
+    return dt, x, Bm, Cm, A, dy, dsf, s0
+
+
+@pytest.mark.parametrize("C,P,N,dy_dtype", [(256, 64, 128, BF16), (128, 128, 64, F32), (64, 64, 128, F32)])
+def test_mamba2_bwd_scan_and_da_match_the_oracle(C, P, N, dy_dtype):
+    """MB1 + MB3 (kernel_mamba2_bwd_b1_state.py:132-254) and MB4
+    (mamba2_bwd_a_dA_reference.py:60-115) against the oracle's restatements
+    (composed, they equal MB0), then composed as the trainable op
+    (kernel_mamba2_trainable_B6.py:83-131) against MB0 itself."""
+    b, l, h = 1, 512, 2
+    banner(f"mamba2 MB1+MB3, MB4 chunk {C} P{P} N{N} dy {dy_dtype}")
+    dt, x, Bm, Cm, A, dy, dsf, s0 = _m2_full(b, l, h, P, N, 500 + C + P, dy_dtype)
+    ref = om.mamba2_bwd_scan(dt, A, Bm, Cm, x, C, dy.double(), dsf.double(), s0.double())
+    got = MB1.mamba2_bwd_scan(dt.cuda(), A.cuda(), Bm.cuda(), Cm.cuda(), x.cuda(), C, dy.cuda(), dsf.cuda(),
+                              state0=s0.cuda())
+    torch.cuda.synchronize()
+    for n, g_, r in zip(("ddt", "dB", "dC", "dx", "dstate0", "dcumdecay"), got, ref):
+        _check(f"MB1+MB3 {n}", g_, r)
+    dtp = MB4.reshape_dt_to_pallas(dt, C)
+    ref4 = om.mamba2_dA_backward(dtp, A, ref[5], C)
+    got4 = MB4.mamba2_dA_backward(dtp.cuda(), A.cuda(), ref[5].float().cuda(), C)
+    torch.cuda.synchronize()
+    _check("MB4 ddt_contrib2", got4[0], ref4[0])
+    _check("MB4 dA", got4[1], ref4[1])
+    # the trainable op's composition against MB0
+    ddt2, dA = MB4.mamba2_dA_backward(dtp.cuda(), A.cuda(), got[5], C)
+    fin = lambda t: torch.nan_to_num(torch.clamp(t, -1e4, 1e4), nan=0.0)
+    comp = (fin(got[0] + MB4.unreshape_dt_from_pallas(ddt2)), fin(got[1]), fin(got[2]), fin(got[3]), fin(dA),
+            fin(got[4]))
+    mb0 = om.chunk_ssd_bwd_scan(dt, A, Bm, Cm, x, C, dy.double(), dsf.double(), s0.double())
+    torch.cuda.synchronize()
+    for n, g_, r in zip(("ddt", "dB", "dC", "dx", "dA", "dstate0"), comp, mb0):
+        _check(f"composed vs MB0 {n}", g_, om.final_sanitize(r))
