@@ -24,12 +24,12 @@ def _ptr(t):
 
 def stage_args(dt, n_state, chunk_size):
     """Mamba2Args for the stage entries (B and C only size the state)."""
-    if not dt.is_cuda or dt.dtype != torch.bfloat16:
-        raise TypeError("the Mamba2 stage kernels take bfloat16 dt / x / B / C on the device")
+    if not dt.is_cuda or dt.dtype not in _m._DT:
+        raise TypeError("the Mamba2 stage kernels take bfloat16 or float32 dt / x / B / C on the device")
     b, l, h, p = dt.shape
     if l % chunk_size != 0:
         raise ValueError(f"seq_len={l} must be divisible by chunk_size={chunk_size}")
-    return _lib.Mamba2Args(b, l, h, p, n_state, chunk_size, _lib.ATOMIC_BF16, _lib.ATOMIC_BF16, 0)
+    return _lib.Mamba2Args(b, l, h, p, n_state, chunk_size, _m._DT[dt.dtype], _lib.ATOMIC_BF16, 0)
 
 
 def stage_workspace(args, device):

@@ -7,8 +7,8 @@ reference chunk's forward re-run for the state entering each chunk, the
 state-only reverse scan whose sanitised carries are MB2's dstate_end_grad,
 MB2 and the sanitised sums of the two halves (:168-256).  As in the reference,
 ddt is only the dt x part and dcumdecay [B, H, NT, C, P] is both halves' sum,
-for ``mamba2_dA_backward`` (MB4).  dt, x, B, C bfloat16 (the library's Mamba2
-operand type), do bf16 or float32, A, dstate_final, state0 float32; the
+for ``mamba2_dA_backward`` (MB4).  dt, x, B, C bfloat16 or float32
+(one dtype), do bf16 or float32, A, dstate_final, state0 float32; the
 results are float32.  Every computation runs in libatomic_hybrid.so; there is
 no fallback.
 """

@@ -7,7 +7,7 @@ the backward of M3 per (batch, head, chunk) with the state-end part as
 whole-chunk products (:53-66), the y_diag part over min(128, chunk_size)-row
 sub-block pairs with a sanitise after every accumulation (:73-113), and the
 per-head dB, dC summed over the heads (:168-178).  dt, x, B, C are bfloat16
-(the library's Mamba2 operand type), dy bf16 or float32, cumdecay
+or float32 (one dtype), dy bf16 or float32, cumdecay
 [B, H, NT, C, P] and dstate_end_grad [B, H, NT, P, N] float32.  Returns float32
 ddt, dx [B, T, H, P], dB, dC [B, T, N] and dcum [B, H, NT, C, P].  Every
 computation runs in libatomic_hybrid.so; there is no fallback.

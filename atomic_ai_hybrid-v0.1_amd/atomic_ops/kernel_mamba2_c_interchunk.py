@@ -29,9 +29,9 @@ def mamba2_inter_chunk_combine(y_diag, state_end, cumdecay, C, chunk_size, state
     if state_end.shape != (b, h, nt, p, n) or cumdecay.shape != (b, h, nt, chunk_size, p) \
             or C.shape != (b, l, n):
         raise ValueError("inconsistent stage array shapes")
-    if not C.is_cuda or C.dtype != torch.bfloat16:
-        raise TypeError("C must be a bfloat16 device tensor")
-    args = _lib.Mamba2Args(b, l, h, p, n, chunk_size, _lib.ATOMIC_BF16, _lib.ATOMIC_BF16, 0)
+    if not C.is_cuda or C.dtype not in _m._DT:
+        raise TypeError("C must be a bfloat16 or float32 device tensor")
+    args = _lib.Mamba2Args(b, l, h, p, n, chunk_size, _m._DT[C.dtype], _lib.ATOMIC_BF16, 0)
     y_diag, state_end, cumdecay = (t.to(torch.float32).contiguous() for t in (y_diag, state_end, cumdecay))
     C = C.contiguous()
     if state0 is not None:

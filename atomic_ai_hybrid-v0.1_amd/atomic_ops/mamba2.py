@@ -4,6 +4,9 @@ come from torch; every computation runs in libatomic_hybrid.so).
 Layouts follow the reference (``atomic_ops/kernel_mamba2_trainable_B6.py:137``):
 dt, x: [B, T, H, P]; Bm, Cm: [B, T, N] (shared by all heads); A: [H] float32;
 state0 / state_final: [B, H, P, N] float32; y: [B, T, H, P] float32.
+dt, x, Bm, Cm are bfloat16 or float32 (one dtype); float32 operands run the
+library's float32 staged chain at the given chunk (M2 -> M3 -> M4 forward,
+MB1 + MB3 -> MB4 backward), bfloat16 ones the fused whole-path kernels.
 """
 from __future__ import annotations
 
@@ -28,8 +31,8 @@ def _stream(device):
 def _check(dt, x, Bm, Cm, A):
     if not dt.is_cuda:
         raise ValueError("Mamba2 inputs must be HIP device tensors")
-    if dt.dtype != torch.bfloat16:
-        raise TypeError("the Mamba2 kernels take bfloat16 dt / x / B / C")
+    if dt.dtype not in _DT:
+        raise TypeError("the Mamba2 kernels take bfloat16 or float32 dt / x / B / C")
     if x.shape != dt.shape or x.dtype != dt.dtype:
         raise ValueError("x must match dt")
     b, l, h, p = dt.shape

@@ -17,11 +17,13 @@ struct Mamba2Plan {
   size_t o_dstate, o_lasta, o_wr, o_part, o_dap, total;
   int G;       // head groups of the cross-head dCB reduction
   bool chain;  // state loops with the per-chunk product on chip (else two passes)
+  bool f32;    // fp32 operands: the float32 staged kernels, at the caller's chunk (f32dm)
+  Mamba2Dims f32dm;
 };
 
 static int mamba2_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
   if (!a) return ATOMIC_ERR_NULL;
-  if (a->dtype != ATOMIC_BF16) return ATOMIC_ERR_DTYPE;
+  if (a->dtype != ATOMIC_BF16 && a->dtype != ATOMIC_F32) return ATOMIC_ERR_DTYPE;
   if (a->dy_dtype != ATOMIC_F32 && a->dy_dtype != ATOMIC_BF16) return ATOMIC_ERR_DTYPE;
   if (a->batch <= 0 || a->heads <= 0 || a->seqlen <= 0) return ATOMIC_ERR_SHAPE;
   if (a->chunk != 64 && a->chunk != 128 && a->chunk != 256) return ATOMIC_ERR_SHAPE;
@@ -51,6 +53,10 @@ static int mamba2_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
     }
   }
   p->dm = d;
+  p->f32 = a->dtype == ATOMIC_F32;
+  p->f32dm = d;
+  p->f32dm.C = a->chunk;
+  p->f32dm.NT = a->seqlen / a->chunk;
   const size_t es = 2, B = d.B, H = d.H, NT = d.NT, C = d.C, P = d.P, N = d.N, T = d.T;
   // enough (batch, chunk, head group) workgroups for two rounds of the chip's
   // 256 CUs (one 8-wave workgroup each); more groups (1024 workgroups) cost
@@ -503,7 +509,7 @@ static int mamba2_cumdecay_stage(const Mamba2Plan& p, const void* dt, const floa
 
 static int mamba2_intra_stage(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm, const void* Cm,
                               const float* cum, float* y_diag, float* state_end, void* ws, Launch& L) {
-  if (p.dm.C == kStageBlock) return m256_intra(p.dm, dt, x, Bm, Cm, cum, y_diag, state_end, L);
+  if (p.dm.C == kStageBlock) return m256_intra(p.dm, ATOMIC_BF16, dt, x, Bm, Cm, cum, y_diag, state_end, L);
   AH_M2_DISPATCH(mamba2_intra_stage_impl, p, dt, x, Bm, Cm, cum, y_diag, state_end, ws, L);
 }
 
@@ -511,7 +517,8 @@ static int mamba2_combine_stage(const Mamba2Plan& p, const float* y_diag, const 
                                 const void* Cm, const float* state0, float* y, float* state_final, void* ws,
                                 Launch& L) {
   if (p.dm.C == kStageBlock)
-    return m256_combine(p.dm, y_diag, state_end, cum, Cm, state0, y, state_final, static_cast<float*>(ws), L);
+    return m256_combine(p.dm, ATOMIC_BF16, y_diag, state_end, cum, Cm, state0, y, state_final,
+                        static_cast<float*>(ws), L);
   AH_M2_DISPATCH(mamba2_combine_stage_impl, p, y_diag, state_end, cum, Cm, state0, y, state_final, ws, L);
 }
 
@@ -519,10 +526,19 @@ static int mamba2_combine_stage(const Mamba2Plan& p, const float* y_diag, const 
 
 using namespace ah;
 
+// fp32 operands run the float32 staged chain (csrc/stage256_bwd.hip) at the
+// caller's chunk: the reference's trainable op composes the same stages
+// (kernel_mamba2_trainable_B6.py:72-131).  Its workspace holds the larger of
+// the forward's and the backward's arrays.
+static size_t mamba2_f32_ws(const Mamba2Plan& p) {
+  const size_t f = m_f32_fwd_ws(p.f32dm), b = m_f32_bwd_ws(p.f32dm);
+  return m2_align(f > b ? f : b);
+}
+
 extern "C" size_t atomic_mamba2_workspace_size(const atomic_mamba2_args* a) {
   Mamba2Plan p;
   if (mamba2_plan(a, &p) != ATOMIC_OK) return 0;
-  return p.total;
+  return p.f32 ? mamba2_f32_ws(p) : p.total;
 }
 
 // the forward a Mamba2 workspace holds: shapes, dtype and the input pointers
@@ -547,6 +563,13 @@ extern "C" int atomic_mamba2_fwd(const atomic_mamba2_args* a, const void* dt, co
   const int rc = mamba2_plan(a, &p);
   if (rc != ATOMIC_OK) return rc;
   if (!dt || !x || !B || !C || !A || !y || !state_final) return ATOMIC_ERR_NULL;
+  if (p.f32) {  // the float32 staged forward; no stage reports, nothing kept for a REUSE backward
+    if (a->diag) return ATOMIC_ERR_DTYPE;
+    if (!workspace || workspace_bytes < mamba2_f32_ws(p)) return ATOMIC_ERR_WORKSPACE;
+    ws_tag_clobber(workspace, workspace_bytes);
+    Launch L{a->profile, (hipStream_t)stream};
+    return m_f32_fwd(p.f32dm, dt, x, B, C, A, state0, y, state_final, static_cast<float*>(workspace), L);
+  }
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
   Launch L{a->profile, (hipStream_t)stream};
   int r2 = mamba2_forward(p, dt, x, B, C, A, state0, y, state_final, workspace, L);
@@ -567,6 +590,15 @@ extern "C" int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, co
   const int rc = mamba2_plan(a, &p);
   if (rc != ATOMIC_OK) return rc;
   if (!dt || !x || !B || !C || !A || !dy || !ddt || !dx || !dB || !dC || !dA) return ATOMIC_ERR_NULL;
+  if (p.f32) {  // the float32 staged backward, which always re-runs the forward (REUSE is not checked)
+    if (a->diag) return ATOMIC_ERR_DTYPE;
+    if (!dstate0) return ATOMIC_ERR_NULL;
+    if (!workspace || workspace_bytes < mamba2_f32_ws(p)) return ATOMIC_ERR_WORKSPACE;
+    ws_tag_clobber(workspace, workspace_bytes);
+    Launch L{a->profile, (hipStream_t)stream};
+    return m_f32_bwd(p.f32dm, a->dy_dtype, dt, x, B, C, A, state0, dy, dstate_final, (float*)ddt, (float*)dx,
+                     (float*)dB, (float*)dC, dA, dstate0, static_cast<float*>(workspace), L);
+  }
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
   const bool reuse = (a->flags & ATOMIC_MAMBA2_REUSE) != 0;
   const WsTag tag = mamba2_tag(a, dt, x, B, C, A, state0);
@@ -585,7 +617,7 @@ extern "C" int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, co
 extern "C" size_t atomic_mamba2_stage_workspace_size(const atomic_mamba2_args* a) {
   Mamba2Plan p;
   if (mamba2_stage_plan(a, &p) != ATOMIC_OK) return 0;
-  return mamba2_stage_ws(p);
+  return p.f32 ? m2_align(m256_combine_ws(p.f32dm)) : mamba2_stage_ws(p);
 }
 
 extern "C" int atomic_mamba2_chunk_cumdecay(const atomic_mamba2_args* a, const void* dt, const float* A,
@@ -595,6 +627,7 @@ extern "C" int atomic_mamba2_chunk_cumdecay(const atomic_mamba2_args* a, const v
   if (rc != ATOMIC_OK) return rc;
   if (!dt || !A || !cumdecay) return ATOMIC_ERR_NULL;
   Launch L{a->profile, (hipStream_t)stream};
+  if (p.f32) return m_cumdecay(p.f32dm, ATOMIC_F32, dt, A, cumdecay, L);
   return mamba2_cumdecay_stage(p, dt, A, cumdecay, L);
 }
 
@@ -606,6 +639,10 @@ extern "C" int atomic_mamba2_intra_chunk_ssd(const atomic_mamba2_args* a, const 
   const int rc = mamba2_stage_plan(a, &p);
   if (rc != ATOMIC_OK) return rc;
   if (!dt || !x || !B || !C || !cumdecay || !y_diag || !state_end) return ATOMIC_ERR_NULL;
+  if (p.f32) {
+    Launch L{a->profile, (hipStream_t)stream};
+    return m256_intra(p.f32dm, ATOMIC_F32, dt, x, B, C, cumdecay, y_diag, state_end, L);
+  }
   if (!workspace || workspace_bytes < mamba2_stage_ws(p)) return ATOMIC_ERR_WORKSPACE;
   ws_tag_clobber(workspace, workspace_bytes);
   Launch L{a->profile, (hipStream_t)stream};
@@ -620,6 +657,13 @@ extern "C" int atomic_mamba2_inter_chunk_combine(const atomic_mamba2_args* a, co
   const int rc = mamba2_stage_plan(a, &p);
   if (rc != ATOMIC_OK) return rc;
   if (!y_diag || !state_end || !cumdecay || !C || !y || !state_final) return ATOMIC_ERR_NULL;
+  if (p.f32) {
+    if (!workspace || workspace_bytes < m256_combine_ws(p.f32dm)) return ATOMIC_ERR_WORKSPACE;
+    ws_tag_clobber(workspace, workspace_bytes);
+    Launch L{a->profile, (hipStream_t)stream};
+    return m256_combine(p.f32dm, ATOMIC_F32, y_diag, state_end, cumdecay, C, state0, y, state_final,
+                        static_cast<float*>(workspace), L);
+  }
   if (!workspace || workspace_bytes < mamba2_stage_ws(p)) return ATOMIC_ERR_WORKSPACE;
   ws_tag_clobber(workspace, workspace_bytes);
   Launch L{a->profile, (hipStream_t)stream};
@@ -652,7 +696,7 @@ extern "C" int atomic_mamba2_intra_chunk_ssd_bwd(const atomic_mamba2_args* a, co
   if (!workspace || workspace_bytes < m_intra_bwd_ws(d)) return ATOMIC_ERR_WORKSPACE;
   ws_tag_clobber(workspace, workspace_bytes);
   Launch L{a->profile, (hipStream_t)stream};
-  return m_intra_bwd(d, a->dy_dtype, dt, x, B, C, cumdecay, dy, dstate_end_grad, ddt, dx, dB, dC, dcum,
+  return m_intra_bwd(d, a->dtype, a->dy_dtype, dt, x, B, C, cumdecay, dy, dstate_end_grad, ddt, dx, dB, dC, dcum,
                      static_cast<float*>(workspace), L);
 }
 
@@ -684,9 +728,9 @@ extern "C" int atomic_mamba2_bwd_scan(const atomic_mamba2_args* a, const void* d
   Launch L{a->profile, (hipStream_t)stream};
   // M2's cumdecay into the workspace's first array (kernel_mamba2_bwd_b1_state.py:184)
   float* cum = static_cast<float*>(workspace);
-  const int r2 = mamba2_cumdecay_stage(p, dt, A, cum, L);
+  const int r2 = p.f32 ? m_cumdecay(p.dm, ATOMIC_F32, dt, A, cum, L) : mamba2_cumdecay_stage(p, dt, A, cum, L);
   if (r2 != ATOMIC_OK) return r2;
-  return m_bwd_scan(p.dm, a->dy_dtype, dt, x, B, C, cum, dy, dstate_final, state0, ddt, dB, dC, dx, dstate0,
+  return m_bwd_scan(p.dm, a->dtype, a->dy_dtype, dt, x, B, C, cum, dy, dstate_final, state0, ddt, dB, dC, dx, dstate0,
                     dcumdecay, cum, L);
 }
 
@@ -722,5 +766,5 @@ extern "C" int atomic_mamba2_da_backward(const atomic_mamba2_args* a, const void
   if (!workspace || workspace_bytes < m_da_bwd_ws(d)) return ATOMIC_ERR_WORKSPACE;
   ws_tag_clobber(workspace, workspace_bytes);
   Launch L{a->profile, (hipStream_t)stream};
-  return m_da_bwd(d, a->dtype, dt_chunks, A, dcumdecay, ddt_contrib, dA, static_cast<float*>(workspace), L);
+  return m_da_bwd(d, a->dtype, 0, dt_chunks, A, dcumdecay, ddt_contrib, dA, static_cast<float*>(workspace), L);
 }

@@ -9,8 +9,11 @@
 //        kernel D  gdn2_inter_chunk_combine(_with_state) (kernel_d_pipeline.py:94-158)
 //   Mamba2 M3    intra_chunk_ssd_pallas       (kernel_mamba2_b_intra.py:69-168)
 //          M4    mamba2_inter_chunk_combine   (kernel_mamba2_c_interchunk.py:38-87)
-// Every value is computed in float32 (the reference upcasts its inputs on
-// entry); the clip / nan_to_num placement is the reference's.  These are the
+// The Mamba2 kernels take the chunk (64, 128 or 256) at run time and serve
+// every chunk for float32 operands, whose whole path is the staged chain;
+// bfloat16 operands use them at 256 only.  Operands are bfloat16 or float32
+// (StageIn).  Every value is computed in float32 (the reference upcasts its
+// inputs on entry); the clip / nan_to_num placement is the reference's.  These are the
 // drop-in stage functions, not the benchmark path: the decays are evaluated
 // pair by pair (exp(clip(gc_i - gc_j, +-20)), as the reference does) on the
 // vector ALUs, with the operands staged through LDS.
@@ -514,7 +517,7 @@ __global__ __launch_bounds__(256) void g256_combine_k(Gdn2Dims d, const float* _
 
 // ------------------------------------------------------------ Mamba2 M3
 // One workgroup per (batch, head, chunk, 64-row block I): y_diag of rows
-// [64 I, 64 I + 64) over the reference's 128-row sub-blocks,
+// [64 I, 64 I + 64) over the reference's min(128, C)-row sub-blocks,
 //   y_blk(si, sj)[i,p] = sum_j exp(clip(cum_i,p - cum_j,p, +-20)) CB_ij dBx_j,p  (j <= i)
 //   y_diag[si] = sanitize(y_diag[si] + y_blk(si, sj)) for sj = 0 .. si
 // (kernel_mamba2_b_intra.py:86-108), CB = sanitize(C B^T) (:83-84),
@@ -533,10 +536,8 @@ struct M3Lds {
 };
 
 template <int P, int N>
-__global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, const bf16* __restrict__ dt,
-                                                    const bf16* __restrict__ x, const bf16* __restrict__ Bm,
-                                                    const bf16* __restrict__ Cm, const float* __restrict__ cum,
-                                                    float* __restrict__ y_diag) {
+__global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, StageIn dt, StageIn x, StageIn Bm, StageIn Cm,
+                                                    const float* __restrict__ cum, float* __restrict__ y_diag) {
   typedef M3Lds<N> L;
   __shared__ float smem[L::floats];
   float* sCB = smem + L::off_cb;
@@ -544,15 +545,18 @@ __global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, const bf16* __
   float* sB = smem + L::off_b;
   float* sCum = smem + L::off_cum;
   float* sDbx = smem + L::off_dbx;
-  const int bhn = blockIdx.x / NRB, I = NRB - 1 - (int)(blockIdx.x % NRB);
+  const int C = d.C, nrb = C / RB;
+  const int bhn = blockIdx.x / nrb, I = nrb - 1 - (int)(blockIdx.x % nrb);
   const int bh = bhn / d.NT, n = bhn % d.NT, bb = bh / d.H, h = bh % d.H;
-  const size_t row0 = (size_t)bb * d.T + (size_t)n * BT;
+  const size_t row0 = (size_t)bb * d.T + (size_t)n * C;
   const int t = threadIdx.x;
-  const int jmax = I < 2 ? 128 : 256;   // source rows: this 128-row half and the ones before
+  // row blocks per sub-block, and block I's sub-block
+  const int srb = (C < 128 ? C : 128) / RB, si = I / srb;
+  const int jmax = (si + 1) * srb * RB;   // source rows: this sub-block and the ones before
   // CB rows of block I against source rows [0, jmax)
   for (int e = t; e < RB * N; e += 256) {
     const int rr = e / N, s = e % N;
-    sC[rr * L::LN + s] = (float)Cm[(row0 + RB * I + rr) * d.rC + s];
+    sC[rr * L::LN + s] = ld(Cm, (row0 + RB * I + rr) * d.rC + s);
   }
   {
     const int ti = t >> 4, tj = t & 15;   // rows ti + 16 a, columns tj + 16 c of a 64 x 64 tile
@@ -560,7 +564,7 @@ __global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, const bf16* __
       __syncthreads();
       for (int e = t; e < RB * N; e += 256) {
         const int rr = e / N, s = e % N;
-        sB[rr * L::LN + s] = (float)Bm[(row0 + RB * J + rr) * d.rB + s];
+        sB[rr * L::LN + s] = ld(Bm, (row0 + RB * J + rr) * d.rB + s);
       }
       __syncthreads();
       float acc[4][4];
@@ -589,7 +593,7 @@ __global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, const bf16* __
   const int p = t & 63, rg = 16 * (t >> 6);
   for (int p0 = 0; p0 < P; p0 += 64) {
     const size_t hp = (size_t)h * P + p0 + p;
-    const float* cb = cum + (size_t)bhn * BT * P + p0 + p;   // cum[b][h][n][row][p]
+    const float* cb = cum + (size_t)bhn * C * P + p0 + p;   // cum[b][h][n][row][p]
     float ci[16], acc0[16], acc1[16];
 #pragma unroll
     for (int a = 0; a < 16; ++a) {
@@ -601,14 +605,14 @@ __global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, const bf16* __
       for (int e = t; e < RB * 64; e += 256) {
         const int rr = e >> 6, pp = e & 63;
         const size_t row = row0 + RB * J + rr;
-        sCum[rr * L::LP + pp] = cum[((size_t)bhn * BT + RB * J + rr) * P + p0 + pp];
-        sDbx[rr * L::LP + pp] = sanitize((float)dt[row * d.rdt + (size_t)h * P + p0 + pp] *
-                                         (float)x[row * d.rx + (size_t)h * P + p0 + pp]);
+        sCum[rr * L::LP + pp] = cum[((size_t)bhn * C + RB * J + rr) * P + p0 + pp];
+        sDbx[rr * L::LP + pp] = sanitize(ld(dt, row * d.rdt + (size_t)h * P + p0 + pp) *
+                                         ld(x, row * d.rx + (size_t)h * P + p0 + pp));
       }
       __syncthreads();
-      // sources of the first 128-row half feed the second half's rows
-      // through their own sanitised sub-block sum (acc0)
-      const bool cross = I >= 2 && J < 2;
+      // sources of an earlier sub-block feed this sub-block's rows through
+      // their own sanitised sub-block sum (acc0); C <= 256 gives at most two
+      const bool cross = si > 0 && J / srb < si;
       for (int jj = 0; jj < RB; ++jj) {
         const int j = RB * J + jj;
         const float cj = sCum[jj * L::LP + p], xb = sDbx[jj * L::LP + p];
@@ -625,7 +629,7 @@ __global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, const bf16* __
     }
 #pragma unroll
     for (int a = 0; a < 16; ++a) {
-      const float y = I >= 2 ? sanitize(sanitize(acc0[a]) + acc1[a]) : sanitize(acc1[a]);
+      const float y = si > 0 ? sanitize(sanitize(acc0[a]) + acc1[a]) : sanitize(acc1[a]);
       y_diag[(row0 + RB * I + rg + a) * (size_t)d.H * P + hp] = y;
     }
   }
@@ -636,8 +640,7 @@ __global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, const bf16* __
 // workgroup per (batch, head, chunk, 32 channels); thread (s = t % N, channels
 // 32 N / 256 from (t / N) on).
 template <int P, int N>
-__global__ __launch_bounds__(256) void m256_state_end_k(Mamba2Dims d, const bf16* __restrict__ dt,
-                                                        const bf16* __restrict__ x, const bf16* __restrict__ Bm,
+__global__ __launch_bounds__(256) void m256_state_end_k(Mamba2Dims d, StageIn dt, StageIn x, StageIn Bm,
                                                         const float* __restrict__ cum,
                                                         float* __restrict__ state_end) {
   constexpr int PC = 32, LN = N + 1, LW = PC + 4, CPT = PC * N / 256;
@@ -645,24 +648,25 @@ __global__ __launch_bounds__(256) void m256_state_end_k(Mamba2Dims d, const bf16
   __shared__ __attribute__((aligned(16))) float sW[RB * LW];
   const int bhn = blockIdx.x / (P / PC), p0 = PC * (int)(blockIdx.x % (P / PC));
   const int bh = bhn / d.NT, n = bhn % d.NT, bb = bh / d.H, h = bh % d.H;
-  const size_t row0 = (size_t)bb * d.T + (size_t)n * BT;
-  const float* cb = cum + (size_t)bhn * BT * P + p0;
+  const int C = d.C;
+  const size_t row0 = (size_t)bb * d.T + (size_t)n * C;
+  const float* cb = cum + (size_t)bhn * C * P + p0;
   const int t = threadIdx.x, s = t % N, pc = CPT * (t / N);
   float acc[CPT];
 #pragma unroll
   for (int j = 0; j < CPT; ++j) acc[j] = 0.f;
-  for (int J = 0; J < NRB; ++J) {
+  for (int J = 0; J < C / RB; ++J) {
     __syncthreads();
     for (int e = t; e < RB * N; e += 256) {
       const int rr = e / N, ss = e % N;
-      sB[rr * LN + ss] = (float)Bm[(row0 + RB * J + rr) * d.rB + ss];
+      sB[rr * LN + ss] = ld(Bm, (row0 + RB * J + rr) * d.rB + ss);
     }
     for (int e = t; e < RB * PC; e += 256) {
       const int rr = e / PC, pp = e % PC;
       const size_t row = row0 + RB * J + rr;
-      const float dbx = sanitize((float)dt[row * d.rdt + (size_t)h * P + p0 + pp] *
-                                 (float)x[row * d.rx + (size_t)h * P + p0 + pp]);
-      const float dte = __expf(fminf(fmaxf(cb[(size_t)(BT - 1) * P + pp] - cb[(size_t)(RB * J + rr) * P + pp],
+      const float dbx = sanitize(ld(dt, row * d.rdt + (size_t)h * P + p0 + pp) *
+                                 ld(x, row * d.rx + (size_t)h * P + p0 + pp));
+      const float dte = __expf(fminf(fmaxf(cb[(size_t)(C - 1) * P + pp] - cb[(size_t)(RB * J + rr) * P + pp],
                                            -kClipDecay), kClipDecay));
       sW[rr * LW + pp] = sanitize(dbx * dte);
     }
@@ -695,7 +699,7 @@ __global__ __launch_bounds__(256) void m256_state_pass_k(Mamba2Dims d, const flo
   for (int n = 0; n < d.NT; ++n) {
     const size_t bhn = bh * d.NT + n;
     pre[((((size_t)bb * d.NT + n) * d.H + h) * P + p) * N + s] = st;
-    const float cl = cum[(bhn * BT + BT - 1) * P + p];
+    const float cl = cum[(bhn * d.C + d.C - 1) * P + p];
     st = sanitize(st * __expf(fminf(fmaxf(cl, -kClipDecay), 0.f)) + state_end[(bhn * P + p) * N + s]);
   }
   state_final[e] = st;
@@ -708,16 +712,17 @@ __global__ __launch_bounds__(256) void m256_state_pass_k(Mamba2Dims d, const flo
 template <int P, int N>
 __global__ __launch_bounds__(256) void m256_y_k(Mamba2Dims d, const float* __restrict__ y_diag,
                                                 const float* __restrict__ pre, const float* __restrict__ cum,
-                                                const bf16* __restrict__ Cm, float* __restrict__ y) {
+                                                StageIn Cm, float* __restrict__ y) {
   constexpr int LN = N + 1;
   __shared__ float sC[RB * LN], sS[64 * LN];
-  const int bhn = blockIdx.x / NRB, I = (int)(blockIdx.x % NRB);
+  const int C = d.C, nrb = C / RB;
+  const int bhn = blockIdx.x / nrb, I = (int)(blockIdx.x % nrb);
   const int bh = bhn / d.NT, n = bhn % d.NT, bb = bh / d.H, h = bh % d.H;
-  const size_t row0 = (size_t)bb * d.T + (size_t)n * BT + RB * I;
+  const size_t row0 = (size_t)bb * d.T + (size_t)n * C + RB * I;
   const int t = threadIdx.x, p = t & 63, rg = 16 * (t >> 6);
   for (int e = t; e < RB * N; e += 256) {
     const int rr = e / N, s = e % N;
-    sC[rr * LN + s] = (float)Cm[(row0 + rr) * d.rC + s];
+    sC[rr * LN + s] = ld(Cm, (row0 + rr) * d.rC + s);
   }
   const float* sp = pre + (((size_t)bb * d.NT + n) * d.H + h) * P * N;
   for (int p0 = 0; p0 < P; p0 += 64) {
@@ -738,7 +743,7 @@ __global__ __launch_bounds__(256) void m256_y_k(Mamba2Dims d, const float* __res
 #pragma unroll
     for (int a = 0; a < 16; ++a) {
       const int i = RB * I + rg + a;
-      const float dfs = __expf(fminf(fmaxf(cum[((size_t)bhn * BT + i) * P + p0 + p], -kClipDecay), 0.f));
+      const float dfs = __expf(fminf(fmaxf(cum[((size_t)bhn * C + i) * P + p0 + p], -kClipDecay), 0.f));
       const size_t o = (row0 + rg + a) * (size_t)d.H * P + (size_t)h * P + p0 + p;
       y[o] = sanitize(y_diag[o] + sanitize(acc[a] * dfs));
     }
@@ -815,26 +820,30 @@ int g256_combine(const Gdn2Dims& d, const float* aqk, const float* wt, const flo
 }
 
 template <int P, int N>
-static int m256_intra_t(const Mamba2Dims& d, const void* dt, const void* x, const void* Bm, const void* Cm,
-                        const float* cum, float* y_diag, float* state_end, Launch& L) {
+static int m256_intra_t(const Mamba2Dims& d, int dtype, const void* dt, const void* x, const void* Bm,
+                        const void* Cm, const float* cum, float* y_diag, float* state_end, Launch& L) {
   const size_t bhn = (size_t)d.B * d.H * d.NT;
   static_assert(M3Lds<N>::floats * sizeof(float) <= 160 * 1024, "M3 tiles fit the LDS");
+  if (d.C != 64 && d.C != 128 && d.C != 256) return ATOMIC_ERR_SHAPE;
+  const int bf = dtype == ATOMIC_BF16;
+  const StageIn idt{dt, bf}, ix{x, bf}, iB{Bm, bf}, iC{Cm, bf};
   int rc = L("mamba2_intra_bt256", [&] {
-    hipLaunchKernelGGL((m256_ydiag_k<P, N>), dim3((unsigned)(bhn * NRB)), dim3(256), 0, L.st, d,
-                       (const bf16*)dt, (const bf16*)x,
-                       (const bf16*)Bm, (const bf16*)Cm, cum, y_diag);
+    hipLaunchKernelGGL((m256_ydiag_k<P, N>), dim3((unsigned)(bhn * (d.C / RB))), dim3(256), 0, L.st, d, idt, ix,
+                       iB, iC, cum, y_diag);
   });
   if (rc) return rc;
   return L("mamba2_state_end_bt256", [&] {
-    hipLaunchKernelGGL((m256_state_end_k<P, N>), dim3((unsigned)(bhn * (P / 32))), dim3(256), 0, L.st, d,
-                       (const bf16*)dt, (const bf16*)x, (const bf16*)Bm, cum, state_end);
+    hipLaunchKernelGGL((m256_state_end_k<P, N>), dim3((unsigned)(bhn * (P / 32))), dim3(256), 0, L.st, d, idt,
+                       ix, iB, cum, state_end);
   });
 }
 
 template <int P, int N>
-static int m256_combine_t(const Mamba2Dims& d, const float* y_diag, const float* state_end, const float* cum,
-                          const void* Cm, const float* state0, float* y, float* state_final, float* ws,
-                          Launch& L) {
+static int m256_combine_t(const Mamba2Dims& d, int dtype, const float* y_diag, const float* state_end,
+                          const float* cum, const void* Cm, const float* state0, float* y, float* state_final,
+                          float* ws, Launch& L) {
+  if (d.C != 64 && d.C != 128 && d.C != 256) return ATOMIC_ERR_SHAPE;
+  const StageIn iC{Cm, dtype == ATOMIC_BF16};
   const size_t elems = (size_t)d.B * d.H * P * N;
   int rc = L("mamba2_state_pass_bt256", [&] {
     hipLaunchKernelGGL((m256_state_pass_k<P, N>), dim3((unsigned)(elems / 256)), dim3(256), 0, L.st, d,
@@ -842,8 +851,8 @@ static int m256_combine_t(const Mamba2Dims& d, const float* y_diag, const float*
   });
   if (rc) return rc;
   return L("mamba2_combine_y_bt256", [&] {
-    hipLaunchKernelGGL((m256_y_k<P, N>), dim3((unsigned)((size_t)d.B * d.H * d.NT * NRB)), dim3(256), 0, L.st,
-                       d, y_diag, ws, cum, (const bf16*)Cm, y);
+    hipLaunchKernelGGL((m256_y_k<P, N>), dim3((unsigned)((size_t)d.B * d.H * d.NT * (d.C / RB))), dim3(256), 0,
+                       L.st, d, y_diag, ws, cum, iC, y);
   });
 }
 
@@ -857,14 +866,14 @@ static int m256_combine_t(const Mamba2Dims& d, const float* y_diag, const float*
     return ATOMIC_ERR_SHAPE;                                                \
   } while (0)
 
-int m256_intra(const Mamba2Dims& d, const void* dt, const void* x, const void* Bm, const void* Cm,
+int m256_intra(const Mamba2Dims& d, int dtype, const void* dt, const void* x, const void* Bm, const void* Cm,
                const float* cum, float* y_diag, float* state_end, Launch& L) {
-  AH_M256_DISPATCH(m256_intra_t, d, dt, x, Bm, Cm, cum, y_diag, state_end, L);
+  AH_M256_DISPATCH(m256_intra_t, d, dtype, dt, x, Bm, Cm, cum, y_diag, state_end, L);
 }
 
-int m256_combine(const Mamba2Dims& d, const float* y_diag, const float* state_end, const float* cum,
+int m256_combine(const Mamba2Dims& d, int dtype, const float* y_diag, const float* state_end, const float* cum,
                  const void* Cm, const float* state0, float* y, float* state_final, float* ws, Launch& L) {
-  AH_M256_DISPATCH(m256_combine_t, d, y_diag, state_end, cum, Cm, state0, y, state_final, ws, L);
+  AH_M256_DISPATCH(m256_combine_t, d, dtype, y_diag, state_end, cum, Cm, state0, y, state_final, ws, L);
 }
 
 size_t m256_combine_ws(const Mamba2Dims& d) { return (size_t)d.B * d.NT * d.H * d.P * d.N * sizeof(float); }

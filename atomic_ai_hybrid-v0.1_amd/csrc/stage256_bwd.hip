@@ -23,14 +23,7 @@ namespace ah {
 
 namespace {
 
-// A read-only operand of either element type.
-struct In {
-  const void* p;
-  int bf;  // 1: bf16, 0: fp32
-};
-__device__ __forceinline__ float ld(const In& a, size_t i) {
-  return a.bf ? to_f(reinterpret_cast<const bf16*>(a.p)[i]) : reinterpret_cast<const float*>(a.p)[i];
-}
+using In = StageIn;  // a read-only bf16 or fp32 operand
 
 // Offset of batch item z = (z2 * Z1 + z1) * Z0 + z0 in an operand.
 struct Bat {
@@ -774,7 +767,9 @@ __global__ __launch_bounds__(256) void m2s_comb_k(size_t nhp, size_t nn, size_t 
 // exponents' clipped cumsum (kept in LDS), then the masked cumdecay cotangent
 // reverse-cumsummed and masked by the step clip: ddt's second part and the
 // workgroup's part of dA (mamba2_bwd_a_dA_reference.py:89-113).
-__global__ __launch_bounds__(64) void m2s_da_k(Mamba2Dims d, In dtp, const float* __restrict__ A,
+// tok: dt in the token layout [B][T][H][P] with row stride d.rdt instead of
+// the per-chunk one.
+__global__ __launch_bounds__(64) void m2s_da_k(Mamba2Dims d, In dtp, int tok, const float* __restrict__ A,
                                                const float* __restrict__ dcum, float* __restrict__ ddt2,
                                                float* __restrict__ part) {
   __shared__ float sCr[256][65];
@@ -782,12 +777,16 @@ __global__ __launch_bounds__(64) void m2s_da_k(Mamba2Dims d, In dtp, const float
   const size_t z = blockIdx.x / nps;
   const int p0 = (blockIdx.x % nps) * 64, c = threadIdx.x, p = p0 + c;
   const int h = (int)((z / d.NT) % d.H);
+  const size_t b_ = z / ((size_t)d.NT * d.H), n = z % d.NT;
+  auto dt_at = [&](int i) {
+    return tok ? ld(dtp, ((size_t)b_ * d.T + n * C + i) * d.rdt + (size_t)h * P + p) : ld(dtp, (z * C + i) * P + p);
+  };
   const float a = A[h];
   float dsum = 0.f;
   if (p < P) {
     float s = 0.f;
     for (int i = 0; i < C; ++i) {                                        // :89-94
-      s += fminf(fmaxf(ld(dtp, (z * C + i) * P + p) * a, -kClipDecay), kClipDecay);
+      s += fminf(fmaxf(dt_at(i) * a, -kClipDecay), kClipDecay);
       sCr[i][c] = s;
     }
     float acc = 0.f;
@@ -795,7 +794,7 @@ __global__ __launch_bounds__(64) void m2s_da_k(Mamba2Dims d, In dtp, const float
       const size_t o = (z * C + i) * P + p;
       const float cr = sCr[i][c];
       acc += dcum[o] * ((cr >= -kClipAcc && cr <= kClipAcc) ? 1.f : 0.f);   // :98,101-103
-      const float dtv = ld(dtp, o), raw = dtv * a;
+      const float dtv = dt_at(i), raw = dtv * a;
       const float dr = acc * ((raw >= -kClipDecay && raw <= kClipDecay) ? 1.f : 0.f);   // :106
       ddt2[o] = sanitize(dr * a);                                        // :109,112
       dsum = fmaf(dr, dtv, dsum);                                        // :110
@@ -816,6 +815,40 @@ __global__ __launch_bounds__(256) void m2s_da_sum_k(Mamba2Dims d, int nps, const
     for (int n = 0; n < d.NT; ++n)
       for (int q = 0; q < nps; ++q) s += part[(((size_t)b * d.H + h) * d.NT + n) * nps + q];
   dA[h] = sanitize(s);
+}
+
+// M2 for any chunk and operand type (kernel_mamba2_a_decay.py:53-66):
+// cum = sanitize(cumsum over the chunk of sanitize(dt A, 20), 1e4), one thread
+// per (batch, head, chunk, channel), the running sum kept unclipped.
+__global__ __launch_bounds__(256) void m2s_cum_k(Mamba2Dims d, In dt, const float* __restrict__ A,
+                                                 float* __restrict__ cum) {
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t total = (size_t)d.B * d.H * d.NT * d.P;
+  if (e >= total) return;
+  const int p = (int)(e % d.P);
+  const size_t z = e / d.P;
+  const int n = (int)(z % d.NT), h = (int)((z / d.NT) % d.H), b = (int)(z / ((size_t)d.NT * d.H));
+  const float a = A[h];
+  float s = 0.f;
+  for (int i = 0; i < d.C; ++i) {
+    const size_t row = (size_t)b * d.T + (size_t)n * d.C + i;
+    s += sanitize(ld(dt, row * d.rdt + (size_t)h * d.P + p) * a, kClipDecay);
+    cum[(z * d.C + i) * d.P + p] = sanitize(s);
+  }
+}
+
+// ddt = sanitize(the dt x part + the dt A part), the latter in the per-chunk
+// layout (kernel_mamba2_trainable_B6.py:100-106).
+__global__ __launch_bounds__(256) void m2s_ddt_k(Mamba2Dims d, const float* __restrict__ ddt_p,
+                                                 const float* __restrict__ ddt2, float* __restrict__ ddt) {
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t total = (size_t)d.B * d.T * d.H * d.P;
+  if (e >= total) return;
+  const int p = (int)(e % d.P), h = (int)((e / d.P) % d.H);
+  const size_t tok = e / ((size_t)d.H * d.P);
+  const int b = (int)(tok / d.T), t = (int)(tok % d.T), n = t / d.C, i = t % d.C;
+  const size_t o = ((((size_t)b * d.H + h) * d.NT + n) * d.C + i) * d.P + p;
+  ddt[e] = sanitize(ddt_p[e] + ddt2[o]);
 }
 
 }  // namespace
@@ -954,17 +987,18 @@ size_t m_intra_bwd_ws(const Mamba2Dims& d) {
   return ((size_t)d.B * d.NT * C * C + 5 * Z * C * d.P + 2 * Z * C * d.N + Z * C * C) * sizeof(float);
 }
 
-int m_intra_bwd(const Mamba2Dims& d, int dy_dtype, const void* dt, const void* x, const void* Bm, const void* Cm,
-                const float* cum, const void* dy, const float* dse, float* ddt, float* dx, float* dB, float* dC,
-                float* dcum, float* ws, Launch& L) {
+int m_intra_bwd(const Mamba2Dims& d, int dtype, int dy_dtype, const void* dt, const void* x, const void* Bm,
+                const void* Cm, const float* cum, const void* dy, const float* dse, float* ddt, float* dx, float* dB,
+                float* dC, float* dcum, float* ws, Launch& L) {
   const int C = d.C, P = d.P, N = d.N, H = d.H, NT = d.NT, bc = C < 128 ? C : 128;
   const int Z = d.B * H * NT;
   const size_t zcp = (size_t)Z * C * P, zcn = (size_t)Z * C * N;
   float *bcin = ws, *dwrite = bcin + (size_t)d.B * NT * C * C, *dbx = dwrite + zcp, *write = dbx + zcp,
         *d1 = write + zcp, *ddd = d1 + zcp, *wB = ddd + zcp, *wC = wB + zcn, *dbc = wC + zcn;
-  const In idt{dt, 1}, ix{x, 1}, idy{dy, dy_dtype == ATOMIC_BF16};
-  const bf16* Bp = static_cast<const bf16*>(Bm);
-  const bf16* Cp = static_cast<const bf16*>(Cm);
+  const int bf = dtype == ATOMIC_BF16, es = bf ? 2 : 4;
+  const In idt{dt, bf}, ix{x, bf}, idy{dy, dy_dtype == ATOMIC_BF16};
+  const char* Bp = static_cast<const char*>(Bm);   // byte pointers: the rows of a sub-block start at an offset
+  const char* Cp = static_cast<const char*>(Cm);
   // item z = (b H + h) NT + n: a dense per-item array of S elements, and the
   // chunk rows of a [B][T][.] input (shared by the heads)
   auto dense3 = [&](long long S) { return Bat{(long long)H * NT * S, (long long)NT * S, S}; };
@@ -972,8 +1006,8 @@ int m_intra_bwd(const Mamba2Dims& d, int dy_dtype, const void* dt, const void* x
   // CB = sanitize(C B^T) per (batch, chunk)   (:48)
   GemmOp g = gemm_op(C, C, N, d.B * NT);
   g.Z1 = 1; g.Z0 = NT;
-  g.A = In{Cp, 1}; g.lda = d.rC; g.sa = Bat{(long long)d.T * d.rC, 0, (long long)C * d.rC};
-  g.B = In{Bp, 1}; g.ldb = d.rB; g.sb = Bat{(long long)d.T * d.rB, 0, (long long)C * d.rB}; g.tb = 1;
+  g.A = In{Cp, bf}; g.lda = d.rC; g.sa = Bat{(long long)d.T * d.rC, 0, (long long)C * d.rC};
+  g.B = In{Bp, bf}; g.ldb = d.rB; g.sb = Bat{(long long)d.T * d.rB, 0, (long long)C * d.rB}; g.tb = 1;
   g.C = bcin; g.ldc = C; g.sc = Bat{(long long)NT * C * C, 0, (long long)C * C};
   g.post = 2;
   int rc = gemm(g, d.B * NT, "m2b_cb", L);
@@ -981,7 +1015,7 @@ int m_intra_bwd(const Mamba2Dims& d, int dy_dtype, const void* dt, const void* x
   // dwrite = sanitize(B dstate_end^T)   (:56)
   g = gemm_op(C, P, N, Z);
   g.Z1 = H; g.Z0 = NT;
-  g.A = In{Bp, 1}; g.lda = d.rB; g.sa = rows3(d.rB);
+  g.A = In{Bp, bf}; g.lda = d.rB; g.sa = rows3(d.rB);
   g.B = In{dse, 0}; g.ldb = N; g.sb = dense3((long long)P * N); g.tb = 1;
   g.C = dwrite; g.ldc = P; g.sc = dense3((long long)C * P);
   g.post = 2;
@@ -1016,14 +1050,14 @@ int m_intra_bwd(const Mamba2Dims& d, int dy_dtype, const void* dt, const void* x
       g.Z1 = H; g.Z0 = NT;
       g.A = In{dbc + (size_t)i0 * C + j0, 0};   // transposed: A(m = j, k = i) = dBC[i0 + i][j0 + j]
       g.lda = C; g.sa = dense3((long long)C * C); g.ta = 1;
-      g.B = In{Cp + (size_t)i0 * d.rC, 1}; g.ldb = d.rC; g.sb = rows3(d.rC);
+      g.B = In{Cp + (size_t)i0 * d.rC * es, bf}; g.ldb = d.rC; g.sb = rows3(d.rC);
       g.C = wB + (size_t)j0 * N; g.ldc = N; g.sc = dense3((long long)C * N);
       g.accum = 1; g.post = 2;
       if ((rc = gemm(g, Z, "m2b_db_pair", L))) return rc;
       g = gemm_op(bc, N, bc, Z);
       g.Z1 = H; g.Z0 = NT;
       g.A = In{dbc + (size_t)i0 * C + j0, 0}; g.lda = C; g.sa = dense3((long long)C * C);
-      g.B = In{Bp + (size_t)j0 * d.rB, 1}; g.ldb = d.rB; g.sb = rows3(d.rB);
+      g.B = In{Bp + (size_t)j0 * d.rB * es, bf}; g.ldb = d.rB; g.sb = rows3(d.rB);
       g.C = wC + (size_t)i0 * N; g.ldc = N; g.sc = dense3((long long)C * N);
       g.accum = 1; g.post = 2;
       if ((rc = gemm(g, Z, "m2b_dc_pair", L))) return rc;
@@ -1052,9 +1086,9 @@ size_t m_bwd_scan_ws(const Mamba2Dims& d) {
   return own * sizeof(float) + m_intra_bwd_ws(d);
 }
 
-int m_bwd_scan(const Mamba2Dims& d, int dy_dtype, const void* dt, const void* x, const void* Bm, const void* Cm,
-               const float* cum, const void* dy, const float* dsf, const float* state0, float* ddt, float* dB,
-               float* dC, float* dx, float* ds0, float* dcum, float* ws, Launch& L) {
+int m_bwd_scan(const Mamba2Dims& d, int dtype, int dy_dtype, const void* dt, const void* x, const void* Bm,
+               const void* Cm, const float* cum, const void* dy, const float* dsf, const float* state0, float* ddt,
+               float* dB, float* dC, float* dx, float* ds0, float* dcum, float* ws, Launch& L) {
   const int C = d.C, P = d.P, N = d.N;
   const size_t Z = (size_t)d.B * d.H * d.NT;
   if (P % MS_PT != 0 || (N != 64 && N != 128)) return ATOMIC_ERR_SHAPE;
@@ -1064,7 +1098,8 @@ int m_bwd_scan(const Mamba2Dims& d, int dy_dtype, const void* dt, const void* x,
   float* dcum_s = dC_s + (size_t)d.B * d.T * N;
   float* dse = dcum_s + Z * C * P;
   float* wmb2 = dse + Z * P * N;
-  const In idt{dt, 1}, ix{x, 1}, iB{Bm, 1}, iC{Cm, 1}, idy{dy, dy_dtype == ATOMIC_BF16};
+  const int bf = dtype == ATOMIC_BF16;
+  const In idt{dt, bf}, ix{x, bf}, iB{Bm, bf}, iC{Cm, bf}, idy{dy, dy_dtype == ATOMIC_BF16};
   const dim3 grid((unsigned)(d.B * d.H * (P / MS_PT)));
   int rc = L("m2s_fwd", [&] {
     if (N == 128)
@@ -1092,7 +1127,7 @@ int m_bwd_scan(const Mamba2Dims& d, int dy_dtype, const void* dt, const void* x,
   g.post = 2;
   if ((rc = gemm(g, d.B * d.NT, "m2s_dc_state", L))) return rc;
   // MB2 with the carries as dstate_end_grad (:240-243)
-  if ((rc = m_intra_bwd(d, dy_dtype, dt, x, Bm, Cm, cum, dy, dse, ddt, dx, dB, dC, dcum, wmb2, L))) return rc;
+  if ((rc = m_intra_bwd(d, dtype, dy_dtype, dt, x, Bm, Cm, cum, dy, dse, ddt, dx, dB, dC, dcum, wmb2, L))) return rc;
   const size_t nhp = (size_t)d.B * d.T * d.H * P, nn = (size_t)d.B * d.T * N, ncum = Z * C * P;
   const size_t top = nhp > ncum ? nhp : ncum;
   const int eb = (int)((top + 255) / 256 < 65536 ? (top + 255) / 256 : 65536);
@@ -1105,18 +1140,71 @@ size_t m_da_bwd_ws(const Mamba2Dims& d) {
   return (size_t)d.B * d.H * d.NT * ((d.P + 63) / 64) * sizeof(float);
 }
 
-int m_da_bwd(const Mamba2Dims& d, int dt_dtype, const void* dtp, const float* A, const float* dcum, float* ddt2,
-             float* dA, float* ws, Launch& L) {
+int m_da_bwd(const Mamba2Dims& d, int dt_dtype, int tok, const void* dtp, const float* A, const float* dcum,
+             float* ddt2, float* dA, float* ws, Launch& L) {
   if (d.C > 256) return ATOMIC_ERR_SHAPE;
   const int nps = (d.P + 63) / 64;
   const unsigned nb = (unsigned)((size_t)d.B * d.H * d.NT * nps);
   const In it{dtp, dt_dtype == ATOMIC_BF16};
   int rc = L("m2s_da", [&] {
-    hipLaunchKernelGGL(m2s_da_k, dim3(nb), dim3(64), 0, L.st, d, it, A, dcum, ddt2, ws);
+    hipLaunchKernelGGL(m2s_da_k, dim3(nb), dim3(64), 0, L.st, d, it, tok, A, dcum, ddt2, ws);
   });
   if (rc != ATOMIC_OK) return rc;
   return L("m2s_da_sum", [&] {
     hipLaunchKernelGGL(m2s_da_sum_k, dim3((unsigned)((d.H + 255) / 256)), dim3(256), 0, L.st, d, nps, ws, dA);
+  });
+}
+
+
+int m_cumdecay(const Mamba2Dims& d, int dtype, const void* dt, const float* A, float* cum, Launch& L) {
+  const size_t n = (size_t)d.B * d.H * d.NT * d.P;
+  const In idt{dt, dtype == ATOMIC_BF16};
+  return L("mamba2_cumdecay_f32", [&] {
+    hipLaunchKernelGGL(m2s_cum_k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, L.st, d, idt, A, cum);
+  });
+}
+
+size_t m_f32_fwd_ws(const Mamba2Dims& d) {
+  const size_t Z = (size_t)d.B * d.H * d.NT;
+  return (Z * d.C * d.P + (size_t)d.B * d.T * d.H * d.P + Z * d.P * d.N) * sizeof(float) + m256_combine_ws(d);
+}
+
+int m_f32_fwd(const Mamba2Dims& d, const void* dt, const void* x, const void* Bm, const void* Cm, const float* A,
+              const float* state0, float* y, float* state_final, float* ws, Launch& L) {
+  const size_t Z = (size_t)d.B * d.H * d.NT;
+  float* cum = ws;
+  float* y_diag = cum + Z * d.C * d.P;
+  float* state_end = y_diag + (size_t)d.B * d.T * d.H * d.P;
+  float* pre = state_end + Z * d.P * d.N;
+  int rc = m_cumdecay(d, ATOMIC_F32, dt, A, cum, L);
+  if (rc) return rc;
+  if ((rc = m256_intra(d, ATOMIC_F32, dt, x, Bm, Cm, cum, y_diag, state_end, L))) return rc;
+  return m256_combine(d, ATOMIC_F32, y_diag, state_end, cum, Cm, state0, y, state_final, pre, L);
+}
+
+size_t m_f32_bwd_ws(const Mamba2Dims& d) {
+  const size_t Z = (size_t)d.B * d.H * d.NT;
+  return m_bwd_scan_ws(d) + ((size_t)d.B * d.T * d.H * d.P + 2 * Z * d.C * d.P) * sizeof(float) + m_da_bwd_ws(d);
+}
+
+int m_f32_bwd(const Mamba2Dims& d, int dy_dtype, const void* dt, const void* x, const void* Bm, const void* Cm,
+              const float* A, const float* state0, const void* dy, const float* dsf, float* ddt, float* dx,
+              float* dB, float* dC, float* dA, float* ds0, float* ws, Launch& L) {
+  const size_t Z = (size_t)d.B * d.H * d.NT;
+  float* scan_ws = ws;                                  // cumdecay first
+  float* ddt_p = ws + m_bwd_scan_ws(d) / sizeof(float);
+  float* dcum = ddt_p + (size_t)d.B * d.T * d.H * d.P;
+  float* ddt2 = dcum + Z * d.C * d.P;
+  float* da_ws = ddt2 + Z * d.C * d.P;
+  int rc = m_cumdecay(d, ATOMIC_F32, dt, A, scan_ws, L);
+  if (rc) return rc;
+  if ((rc = m_bwd_scan(d, ATOMIC_F32, dy_dtype, dt, x, Bm, Cm, scan_ws, dy, dsf, state0, ddt_p, dB, dC, dx, ds0,
+                       dcum, scan_ws, L)))
+    return rc;
+  if ((rc = m_da_bwd(d, ATOMIC_F32, 1, dt, A, dcum, ddt2, dA, da_ws, L))) return rc;
+  const size_t n = (size_t)d.B * d.T * d.H * d.P;
+  return L("mamba2_ddt_f32", [&] {
+    hipLaunchKernelGGL(m2s_ddt_k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, L.st, d, ddt_p, ddt2, ddt);
   });
 }
 

@@ -393,7 +393,12 @@ typedef struct atomic_mamba2_args {
   int32_t dstate;    /* N: 64 or 128 (ngroups = 1: B and C shared by heads) */
   int32_t chunk;     /* C: 64, 128 or 256 (256 runs as 128-row chunks: equal
                         while every dt A <= 0, up to exp(-20) floor terms)   */
-  int32_t dtype;     /* dt, x, B, C and their gradients: ATOMIC_BF16       */
+  int32_t dtype;     /* dt, x, B, C and their gradients: ATOMIC_BF16, or
+                        ATOMIC_F32: then atomic_mamba2_fwd / _bwd run the
+                        float32 staged chain at the given chunk (M2 -> M3 ->
+                        M4, MB1 + MB3 -> MB4; the stage entries' arithmetic,
+                        state0 always sanitised), REUSE is not checked (the
+                        backward re-runs the forward) and diag must be NULL */
   int32_t dy_dtype;  /* upstream gradient dy: ATOMIC_F32 / ATOMIC_BF16     */
   int32_t flags;     /* ATOMIC_MAMBA2_*                                    */
   atomic_profile* profile;  /* optional per-kernel event timing, or NULL */
@@ -450,7 +455,8 @@ int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, const void* x
  * M3 sums over the reference's two 128-row sub-blocks, sanitising each
  * sub-block's part before the next is added (kernel_mamba2_b_intra.py:61-62,
  * 86-108), and M4 keeps the states entering each chunk in float32.  dt, x,
- * B, C bf16; the arrays fp32:
+ * B, C bf16 or fp32 (args.dtype; the backward stage entries too); the arrays
+ * fp32:
  *   cumdecay : [B][H][NT][C][P]     state_end : [B][H][NT][P][N]
  *   y_diag, y : [B][T][H][P]        state0, state_final : [B][H][P][N]
  * The arithmetic is that of the stage kernels, which differ from the whole

@@ -93,7 +93,9 @@ def test_workspace_size_rejects_bad_shapes_without_a_gpu():
     assert lib.atomic_mamba2_workspace_size(ctypes.byref(m_ok)) == 0
     m_ok.row_stride[2] = 136
     assert lib.atomic_mamba2_workspace_size(ctypes.byref(m_ok)) > 0
-    m_bad = _lib.Mamba2Args(1, 256, 2, 64, 128, 128, _lib.ATOMIC_F32, _lib.ATOMIC_BF16, 0, None)
+    m_f32 = _lib.Mamba2Args(1, 256, 2, 64, 128, 128, _lib.ATOMIC_F32, _lib.ATOMIC_BF16, 0, None)
+    assert lib.atomic_mamba2_workspace_size(ctypes.byref(m_f32)) > 0
+    m_bad = _lib.Mamba2Args(1, 256, 2, 64, 128, 128, 2, _lib.ATOMIC_BF16, 0, None)   # no such dtype
     assert lib.atomic_mamba2_workspace_size(ctypes.byref(m_bad)) == 0
 
     p_ok = _lib.Mamba2ProjArgs(1, 128, 4, 128, 64, 4, 1024, None)
