@@ -59,23 +59,15 @@ struct Mamba2Grads {
 // the high part and then of the low part, so hi and lo are summed in the MFMA.
 // The A fragments come from the chunk's CB staged in LDS (row pitch ld):
 // CB(m0.., k0..) for the row side, CB^T(m0.., k0..) by a transposed read for
-// the column side.  mask 1 keeps columns <= row (lower triangle), mask 2
-// columns >= row.
+// the column side.  The staged CB has its strict upper triangle zeroed, so a
+// diagonal block reads as its lower triangle (row side) and the transpose of
+// it (column side) with no per-element masks.
 template <typename T>
-__device__ __forceinline__ typename Mma<T>::frag cb_lds_dup(const T* s, int ld, int m0, int k0, int mask,
-                                                            bool transposed) {
+__device__ __forceinline__ typename Mma<T>::frag cb_lds_dup(const T* s, int ld, int m0, int k0, bool transposed) {
   typedef typename Mma<T>::frag frag;
   const int l = lane_id(), m = l & 15, g2 = l >> 5, kb = 8 * ((l >> 4) & 1);
-  frag a = transposed ? Mma<T>::ld_t(s, ld, m0, k0 - 16 * g2)
-                      : *reinterpret_cast<const frag*>(s + (m0 + m) * ld + k0 + kb);
-  if (mask) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const bool keep = mask == 1 ? (kb + e <= m) : (kb + e >= m);
-      if (!keep) a[e] = (T)0.f;
-    }
-  }
-  return a;
+  return transposed ? Mma<T>::ld_t(s, ld, m0, k0 - 16 * g2)
+                    : *reinterpret_cast<const frag*>(s + (m0 + m) * ld + k0 + kb);
 }
 template <typename T>
 __device__ __forceinline__ typename Mma<T>::frag ld_t_hilo(const T* hi, const T* lo, int ld, int i0, int k0) {
@@ -243,8 +235,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (tid < PT) nla = gr.lasta[bnhn * P + pn + tid];
   };
   load_slice(g * HG, 0, row0);
-  // the chunk's CB, shared by every head and slice of this workgroup
-  stage_rows<T, C, C, NTH>(sCB, L::LCB, cb0, C);
+  // the chunk's CB, shared by every head and slice of this workgroup, with its
+  // strict upper triangle (j > i) zeroed: the pair sums read only the blocks
+  // at and below the diagonal, and of a diagonal block its lower triangle, so
+  // the zeros are the triangle masks of those blocks
+  {
+    static_assert(sizeof(T) == 2, "two elements per dword");
+    constexpr int VEC = 8, PR = C / VEC, NP = C * PR, IT = (NP + NTH - 1) / NTH;
+    u32x4 tmp[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int e = tid + NTH * it;
+      if (NP % NTH == 0 || e < NP) tmp[it] = *reinterpret_cast<const u32x4*>(cb0 + (size_t)(e / PR) * C + (e % PR) * VEC);
+    }
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int e = tid + NTH * it;
+      if (NP % NTH == 0 || e < NP) {
+        const int r = e / PR, c0 = (e % PR) * VEC;
+        u32x4 v = tmp[it];
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          v[d] &= (c0 + 2 * d <= r ? 0xffffu : 0u) | (c0 + 2 * d + 1 <= r ? 0xffff0000u : 0u);
+        *reinterpret_cast<u32x4*>(sCB + r * L::LCB + c0) = v;
+      }
+    }
+  }
   for (int hh = 0; hh < HG; ++hh) {
     const int h = g * HG + hh;
     const float Ah = A[h];
@@ -427,7 +443,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             constexpr int IS = decltype(Ic)::value;
 #pragma unroll
             for (int J = 0; J <= IS; ++J) {  // sources at or below the block (row side)
-              const frag fa = cb_lds_dup<T>(sCB, L::LCB, 16 * IS, 16 * J, J == IS ? 1 : 0, false);
+              const frag fa = cb_lds_dup<T>(sCB, L::LCB, 16 * IS, 16 * J, false);
               const float* mr = sM + (IS * (IS + 1) / 2 + J) * PT;
 #pragma unroll
               for (int q = 0; q < NIW; ++q) {
@@ -440,7 +456,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
 #pragma unroll
             for (int J = IS; J < NB; ++J) {  // targets at or above the block (column side)
-              const frag fa = cb_lds_dup<T>(sCB, L::LCB, 16 * IS, 16 * J, J == IS ? 2 : 0, true);
+              const frag fa = cb_lds_dup<T>(sCB, L::LCB, 16 * IS, 16 * J, true);
               const float* mc = sM + (J * (J + 1) / 2 + IS) * PT;
 #pragma unroll
               for (int q = 0; q < NIW; ++q) {
