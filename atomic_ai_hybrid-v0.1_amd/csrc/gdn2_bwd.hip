@@ -296,7 +296,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 template <typename T, int C, int KQ, int V>
 struct HgLds {
   static constexpr int PAD = Pad<T>::v;
-  static constexpr int LK = KQ + PAD, LV = V + PAD, LC = C + PAD;
+  // bf16 h_pre / dh_next quarter rows unpadded (64 bytes): they are read only
+  // by transposed fragment reads (4 rows of 32 bytes per 16 lanes, on
+  // distinct banks at this pitch, not at 80 bytes) and by the row term
+  static constexpr int LK = KQ + (sizeof(T) == 2 ? 0 : PAD), LV = V + PAD, LC = C + PAD;
   static constexpr int off_do = 0;
   static constexpr int off_dv = off_do + C * LV * (int)sizeof(T);
   static constexpr int off_vn = off_dv + C * LV * (int)sizeof(T);
@@ -363,8 +366,9 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
   // dqg = scale dO h_pre^T ; dwt = -dv_new h_pre^T ; dkg = v_new dh_next^T, per quarter
   constexpr int NTQ = KQ / 16, TPW = MT * NTQ / 4;
   static_assert((MT * NTQ) % 4 == 0, "tiles must split evenly over 4 waves");
-  // gc_last row term: a thread takes a column pair and every SPL-th row, so
-  // a wave's 4-byte reads cover consecutive rows
+  // gc_last row term: a thread takes a column pair and every SPL-th row;
+  // consecutive lanes take consecutive column pairs, so a wave's 4-byte
+  // reads cover four whole rows
   constexpr int CPQ = KQ / 2, SPL = 256 / CPQ, VS = V / SPL;
   static_assert(SPL * KQ <= 512 && V % SPL == 0, "row-term partials fit their LDS");
   for (int c0 = 0; c0 < K; c0 += KQ) {
@@ -390,7 +394,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
     // exp(gc_last) * sum_v dh_next * h_pre   (kernel_bwd_b3_wy_dqkg.py:200-201)
     {
       typedef T T2 __attribute__((ext_vector_type(2)));
-      const int sp = threadIdx.x % SPL, d = 2 * (threadIdx.x / SPL);
+      const int sp = threadIdx.x / CPQ, d = 2 * (threadIdx.x % CPQ);
       float s0 = 0.f, s1 = 0.f;
 #pragma unroll
       for (int t = 0; t < VS; ++t) {
