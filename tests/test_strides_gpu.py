@@ -87,15 +87,17 @@ def test_gdn2_strided_noalloc_and_wrapper():
     assert torch.equal(gbig.grad[..., :HK].reshape(B, T, H, K), leaves[5].grad)
 
 
-def test_mamba2_strided_inputs_equal_dense():
+@pytest.mark.parametrize("dtype,C", [(BF16, 128), (F32, 64), (F32, 256)])
+def test_mamba2_strided_inputs_equal_dense(dtype, C):
     """dt, x as slices of one [B, T, 2 H P + 8] tensor and B, C of one
     [B, T, 2 N + 8] tensor (the in_proj / projection outputs of a fused
-    layer), dy a slice too: outputs and gradients bit-identical to dense."""
+    layer), dy a slice too: outputs and gradients bit-identical to dense
+    (float32 operands: the float32 staged chain)."""
     from atomic_ops import mamba2 as M
     from atomic_ops import kernel_mamba2_trainable_B6 as KM
-    B, T, H, P, N, C = 2, 256, 4, 64, 128, 128
-    banner("mamba2 row-strided inputs")
-    d = inputs.mamba2_inputs(B, T, H, P, N, seed=31, dO=True)
+    B, T, H, P, N = 2, 512, 4, 64, 128
+    banner(f"mamba2 row-strided inputs {dtype} chunk {C}")
+    d = inputs.mamba2_inputs(B, T, H, P, N, seed=31, dtype=dtype, dO=True)
     dt, x = _slices([d["dt"], d["x"]], 8)
     Bm, Cm = (t.view(B, T, N) for t in _slices([d["Bm"].view(B, T, 1, N), d["Cm"].view(B, T, 1, N)], 8))
     (dy,) = _slices([d["dy"]], 8)
