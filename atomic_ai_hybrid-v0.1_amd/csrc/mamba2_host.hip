@@ -529,9 +529,12 @@ using namespace ah;
 // fp32 operands run the float32 staged chain (csrc/stage256_bwd.hip) at the
 // caller's chunk: the reference's trainable op composes the same stages
 // (kernel_mamba2_trainable_B6.py:72-131).  Its workspace holds the larger of
-// the forward's and the backward's arrays.
+// the forward's and the backward's arrays; the backward's are followed by
+// room for dstate0 when the caller passes none.
 static size_t mamba2_f32_ws(const Mamba2Plan& p) {
-  const size_t f = m_f32_fwd_ws(p.f32dm), b = m_f32_bwd_ws(p.f32dm);
+  const Mamba2Dims& d = p.f32dm;
+  const size_t f = m_f32_fwd_ws(d);
+  const size_t b = m2_align(m_f32_bwd_ws(d)) + (size_t)d.B * d.H * d.P * d.N * sizeof(float);
   return m2_align(f > b ? f : b);
 }
 
@@ -592,12 +595,14 @@ extern "C" int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, co
   if (!dt || !x || !B || !C || !A || !dy || !ddt || !dx || !dB || !dC || !dA) return ATOMIC_ERR_NULL;
   if (p.f32) {  // the float32 staged backward, which always re-runs the forward (REUSE is not checked)
     if (a->diag) return ATOMIC_ERR_DTYPE;
-    if (!dstate0) return ATOMIC_ERR_NULL;
     if (!workspace || workspace_bytes < mamba2_f32_ws(p)) return ATOMIC_ERR_WORKSPACE;
     ws_tag_clobber(workspace, workspace_bytes);
     Launch L{a->profile, (hipStream_t)stream};
+    float* ws = static_cast<float*>(workspace);
+    // the scan always writes dstate0: into the workspace's tail when the caller wants none
+    float* ds0 = dstate0 ? dstate0 : ws + m2_align(m_f32_bwd_ws(p.f32dm)) / sizeof(float);
     return m_f32_bwd(p.f32dm, a->dy_dtype, dt, x, B, C, A, state0, dy, dstate_final, (float*)ddt, (float*)dx,
-                     (float*)dB, (float*)dC, dA, dstate0, static_cast<float*>(workspace), L);
+                     (float*)dB, (float*)dC, dA, ds0, ws, L);
   }
   if (!workspace || workspace_bytes < p.total) return ATOMIC_ERR_WORKSPACE;
   const bool reuse = (a->flags & ATOMIC_MAMBA2_REUSE) != 0;

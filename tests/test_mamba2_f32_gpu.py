@@ -157,3 +157,27 @@ def test_mamba2_f32_rejects_stage_reports():
         M.forward(*g, 128, diag=reports)
     args = M.make_args(g[0], g[2], 128)
     assert _lib.load().atomic_mamba2_workspace_size(ctypes.byref(args)) > 0
+
+
+def test_mamba2_f32_backward_without_dstate0():
+    """dstate0 may be NULL (atomic_mamba2_bwd): the float32 chain then keeps
+    it in the workspace, and every other gradient is bit-identical to the
+    call that asks for it."""
+    C, b, l, h, P, N = 128, 1, 512, 2, 64, 128
+    banner("mamba2 f32 backward, dstate0 NULL")
+    dt, x, Bm, Cm, A, dy, dsf, s0 = _inputs(b, l, h, P, N, 960)
+    g = [t.cuda() for t in (dt, x, Bm, Cm, A)]
+    ref = M.backward(*g, C, dy.cuda(), dsf.cuda(), state0=s0.cuda())
+    args = M.make_args(g[0], g[2], C, dy_dtype=F32)
+    lib = _lib.load()
+    ws = torch.empty(lib.atomic_mamba2_workspace_size(ctypes.byref(args)), dtype=torch.uint8, device="cuda")
+    out = [torch.empty_like(t) for t in (g[0], g[1], g[2], g[3])] + [torch.empty(h, device="cuda")]
+    p = M._ptr
+    dyc, dsfc, s0c = dy.cuda(), dsf.cuda(), s0.cuda()
+    rc = lib.atomic_mamba2_bwd(ctypes.byref(args), *(p(t) for t in g), p(s0c), p(dyc), p(dsfc),
+                               *(p(t) for t in out), p(None), p(ws), ctypes.c_size_t(ws.numel()),
+                               M._stream(g[0].device))
+    _lib.check(rc, "atomic_mamba2_bwd")
+    torch.cuda.synchronize()
+    for n, a_, r in zip(("ddt", "dx", "dB", "dC", "dA"), out, ref[:5]):
+        assert torch.equal(a_, r), n
