@@ -8,6 +8,10 @@
 //        B4  intra_backward_pallas         (kernel_bwd_b4_intra.py:57-165)
 //        B5  reverse_cumsum_bwd            (kernel_bwd_b5_reverse_cumsum.py:17-24)
 //   Mamba2 MB2 intra_chunk_ssd_bwd_pallas  (kernel_mamba2_bwd_b2_intra.py:32-180)
+//          MB1 + MB3 mamba2_bwd_scan       (kernel_mamba2_bwd_b1_state.py:132-254)
+//          MB4 mamba2_dA_backward          (mamba2_bwd_a_dA_reference.py:60-115)
+// and, composed from them and the forward stage kernels, the float32 whole
+// path that fp32 Mamba2 operands run (m_f32_fwd, m_f32_bwd).
 // The whole path fuses these into its own kernels at 64 / 128-row chunks;
 // the kernels here give each staged function with its own inputs, outputs
 // and clip / nan_to_num placement.  Every value is float32 (the reference
