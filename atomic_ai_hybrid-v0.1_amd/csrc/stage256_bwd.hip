@@ -722,8 +722,11 @@ __global__ __launch_bounds__(256) void m2s_bwd_k(Mamba2Dims d, In Cm, In dy, con
         for (int s = 0; s < N; ++s) y = fmaf(sC[r][s], sSp[c][s], y);                     // y_off_raw (:105)
         const size_t row = (size_t)b * d.T + (size_t)n * C + r0 + r, col = (size_t)h * P + p0 + c;
         const float cv = cz[(size_t)(r0 + r) * P + p0 + c];
-        const float dh = __expf(fminf(fmaxf(cv, -kClipDecay), 0.f));
-        const float m = (cv >= -kClipDecay && cv <= 0.f) ? 1.f : 0.f;
+        const float dhr = fminf(fmaxf(cv, -kClipDecay), 0.f);
+        const float dh = __expf(dhr);
+        // the reference masks on the clipped exponent (:123-124), not on cum
+        // as MB0 does (mamba2_bwd_reference.py:131), so every cum passes
+        const float m = (dhr >= -kClipDecay && dhr <= 0.f) ? 1.f : 0.f;
         float v = ld(dy, row * d.rdy + col) * y * dh * m;
         if (r0 + r == C - 1) v = v + sLa[c];
         dcum_s[(z * C + r0 + r) * P + p0 + c] = sanitize(v);                               // :131

@@ -512,7 +512,9 @@ size_t atomic_mamba2_bwd_scan_workspace_size(const atomic_mamba2_args* a);
  * state0) (kernel_mamba2_bwd_b1_state.py:132-254) at args.chunk (64, 128 or
  * 256; P a multiple of 32): M2's cumdecay, the reference chunk's forward
  * re-run for the state entering each chunk (state0 sanitised, NULL = zeros),
- * the state-only reverse scan (mamba2_bwd_state_reference.py:87-137) whose
+ * the state-only reverse scan (mamba2_bwd_state_reference.py:87-137; its
+ * y_off decay term is masked on the clipped exponent as there, :123-124, so
+ * every cum passes, where MB0 masks on cum) whose
  * sanitised carries are MB2's dstate_end_grad, MB2, and the sanitised sums
  * of the two halves.  dstate_final [B][H][P][N] or NULL.  Outputs float32:
  * ddt (the dt x part only, as the reference's), dx [B][T][H][P], dB, dC

@@ -181,3 +181,33 @@ def test_mamba2_f32_backward_without_dstate0():
     torch.cuda.synchronize()
     for n, a_, r in zip(("ddt", "dx", "dB", "dC", "dA"), out, ref[:5]):
         assert torch.equal(a_, r), n
+
+
+def test_mamba2_f32_positive_exponent_follows_the_stage_kernels():
+    """A head with A > 0 (every step exponent dt A positive), where the
+    reference's stage kernels and mamba2_ssd_reference part ways (no 1e6
+    caps in the former): the float32 whole path follows the staged chain,
+    forward against the oracle's M2 -> M3 -> M4 and backward against the
+    oracle's MB1 + MB3 and MB4 composed as the trainable op."""
+    from atomic_ops import mamba2_bwd_a_dA_reference as MB4
+    C, b, l, h, P, N = 64, 1, 256, 2, 64, 64
+    banner("mamba2 f32 positive step exponent")
+    dt, x, Bm, Cm, A, dy, dsf, s0 = _inputs(b, l, h, P, N, 970)
+    A = A.clone()
+    A[0] = 0.05
+    cum_r = om.build_chunk_cumdecay(dt, A, C)
+    assert (cum_r[:, 0] > 0).any(), "the exponent must be positive"
+    yd_r, se_r = om.intra_chunk_ssd(dt, x, Bm, Cm, cum_r, C)
+    y_r, sf_r = om.mamba2_inter_chunk_combine(yd_r, se_r, cum_r, Cm, C, state0=s0)
+    sc = om.mamba2_bwd_scan(dt, A, Bm, Cm, x, C, dy.double(), dsf.double(), s0.double())
+    ddt2, dA_r = om.mamba2_dA_backward(MB4.reshape_dt_to_pallas(dt, C), A, sc[5], C)
+    fin = om.final_sanitize
+    ref = (fin(sc[0] + MB4.unreshape_dt_from_pallas(ddt2)), fin(sc[3]), fin(sc[1]), fin(sc[2]), fin(dA_r), fin(sc[4]))
+    g = [t.cuda() for t in (dt, x, Bm, Cm, A)]
+    y, sf, ws = M.forward(*g, C, state0=s0.cuda())
+    grads = M.backward(*g, C, dy.cuda(), dsf.cuda(), state0=s0.cuda(), workspace=ws)
+    torch.cuda.synchronize()
+    _check("y", y, y_r)
+    _check("state_final", sf, sf_r)
+    for n, g_, r in zip(("ddt", "dx", "dB", "dC", "dA", "dstate0"), grads, ref):
+        _check(f"staged {n}", g_, r)

@@ -196,3 +196,22 @@ def test_mamba2_backward_stage_mistakes_are_caught(monkeypatch):
         return om.sanitize(d * A_.to(f)[None, :, None, None, None]), om.sanitize((d * dt_p.to(f)).sum((0, 2, 3, 4)))
     monkeypatch.setattr(om, "mamba2_dA_backward", forward_cumsum)
     assert worst() > 1e-6
+
+
+def test_mamba2_state_only_backward_masks_on_the_clipped_exponent():
+    """MB1's state-only step masks the y_off decay term on the clipped
+    exponent clip(cum, -20, 0) (mamba2_bwd_state_reference.py:123-124), which
+    every cum passes; MB0 masks on cum itself (mamba2_bwd_reference.py:131).
+    With every cum >= 0 the decay is exp(0) = 1, so the step's dcum is
+    exactly dy * (C state^T) on every row but the last (whose extra term is
+    masked off on cum > 0), a closed form MB0's mask (all zeros there) fails."""
+    gen = torch.Generator().manual_seed(23)
+    b, Cs, h, p, n = 1, 16, 2, 8, 4
+    sp = torch.randn(b, h, p, n, generator=gen, dtype=F64)
+    Cc = torch.randn(b, Cs, n, generator=gen, dtype=F64)
+    cum = torch.rand(b, Cs, h, p, generator=gen, dtype=F64).cumsum(1)       # > 0
+    dy = torch.randn(b, Cs, h, p, generator=gen, dtype=F64)
+    carry = torch.randn(b, h, p, n, generator=gen, dtype=F64)
+    _, _, dcum = om.state_only_bwd(sp, Cc, cum, dy, carry)
+    y_off = torch.einsum("bis,bhds->bihd", Cc, sp)
+    assert torch.allclose(dcum, dy * y_off, rtol=0, atol=1e-12)
