@@ -44,9 +44,20 @@ def _r(t):
     return t.float().double()
 
 
-def _case(B, T, H, K, dtype, seed, scale=0.8):
+def _positive_gates(g):
+    """Head 0's gates made positive (0.02 |g|, so gc grows along a block and
+    the pair decays exceed 1): the stage kernels' clips then act where the
+    model's gates (g <= 0) never take them."""
+    g = g.clone()
+    g[:, :, 0] = 0.02 * g[:, :, 0].abs()
+    return g
+
+
+def _case(B, T, H, K, dtype, seed, scale=0.8, positive=False):
     d = inputs.gdn2_inputs(B, T, H, K, K, seed=seed, dtype=dtype)
     q, k, v, w, b, g = (d[n] for n in ("q", "k", "v", "w", "b", "g"))
+    if positive:
+        g = _positive_gates(g)
     gen = torch.Generator().manual_seed(seed + 1)
     do = torch.randn(B, T, H, K, generator=gen).to(dtype)
     dht = 0.3 * torch.randn(B, H, K, K, generator=gen)
@@ -65,11 +76,12 @@ def _dev(t, dtype=F32):
     return t.to(dtype).contiguous().cuda()
 
 
-@pytest.mark.parametrize("dtype,K", [(F32, 128), (BF16, 128), (F32, 64), (BF16, 64)])
-def test_gdn2_backward_block_kernels_match_the_oracle(dtype, K):
+@pytest.mark.parametrize("dtype,K,positive", [(F32, 128, False), (BF16, 128, False), (F32, 64, False),
+                                              (BF16, 64, False), (F32, 128, True)])
+def test_gdn2_backward_block_kernels_match_the_oracle(dtype, K, positive):
     B, T, H = 1, 512, 2
-    banner(f"gdn2 backward stage kernels at BT 256 {dtype} K{K}")
-    c = _case(B, T, H, K, dtype, seed=301 + K)
+    banner(f"gdn2 backward stage kernels at BT 256 {dtype} K{K}{' positive gates' if positive else ''}")
+    c = _case(B, T, H, K, dtype, seed=301 + K, positive=positive)
     s = c["scale"]
     blk = c["blk"]
     do_b = blk(c["do"])
@@ -163,14 +175,17 @@ def test_gdn2_backward_stages_sanitise_like_the_reference():
     assert inside > 0
 
 
-@pytest.mark.parametrize("dtype", [F32, BF16])
-def test_gdn2_backward_stage_chain_matches_the_staged_oracle(dtype):
+@pytest.mark.parametrize("dtype,positive", [(F32, False), (BF16, False), (F32, True)])
+def test_gdn2_backward_stage_chain_matches_the_staged_oracle(dtype, positive):
     """Kernels A, B, C, D-with-state, then B2, B1, B3, B4, B5 through the
-    stage entries, composed as _gdn2_core_bwd (kernel_trainable_B6.py:97-181)."""
+    stage entries, composed as _gdn2_core_bwd (kernel_trainable_B6.py:97-181);
+    also with head 0's gates positive."""
     B, T, H, K = 1, 512, 2, 128
-    banner(f"gdn2 backward stage chain {dtype}")
+    banner(f"gdn2 backward stage chain {dtype}{' positive gates' if positive else ''}")
     d = inputs.gdn2_inputs(B, T, H, K, K, seed=55, dtype=dtype)
     q, k, v, w, b, g = (d[n] for n in ("q", "k", "v", "w", "b", "g"))
+    if positive:
+        g = _positive_gates(g)
     gen = torch.Generator().manual_seed(56)
     do = torch.randn(B, T, H, K, generator=gen).to(dtype)
     dhf = 0.3 * torch.randn(B, H, K, K, generator=gen)
