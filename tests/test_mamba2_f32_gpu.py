@@ -186,17 +186,20 @@ def test_mamba2_f32_backward_without_dstate0():
 def test_mamba2_f32_positive_exponent_follows_the_stage_kernels():
     """A head with A > 0 (every step exponent dt A positive), where the
     reference's stage kernels and mamba2_ssd_reference part ways (no 1e6
-    caps in the former): the float32 whole path follows the staged chain,
-    forward against the oracle's M2 -> M3 -> M4 and backward against the
-    oracle's MB1 + MB3 and MB4 composed as the trainable op."""
+    caps in the former), and a head with A = -200 (step exponents past the
+    -20 clip, so M2's and MB4's clip masks act): the float32 whole path
+    follows the staged chain, forward against the oracle's M2 -> M3 -> M4
+    and backward against the oracle's MB1 + MB3 and MB4 composed as the
+    trainable op."""
     from atomic_ops import mamba2_bwd_a_dA_reference as MB4
     C, b, l, h, P, N = 64, 1, 256, 2, 64, 64
     banner("mamba2 f32 positive step exponent")
     dt, x, Bm, Cm, A, dy, dsf, s0 = _inputs(b, l, h, P, N, 970)
     A = A.clone()
-    A[0] = 0.05
+    A[0], A[1] = 0.05, -200.0
     cum_r = om.build_chunk_cumdecay(dt, A, C)
     assert (cum_r[:, 0] > 0).any(), "the exponent must be positive"
+    assert ((dt[..., 1, :].double() * A[1]) < -20).any(), "some steps must pass the clip"
     yd_r, se_r = om.intra_chunk_ssd(dt, x, Bm, Cm, cum_r, C)
     y_r, sf_r = om.mamba2_inter_chunk_combine(yd_r, se_r, cum_r, Cm, C, state0=s0)
     sc = om.mamba2_bwd_scan(dt, A, Bm, Cm, x, C, dy.double(), dsf.double(), s0.double())
