@@ -112,6 +112,22 @@ def test_backward_positive_step_exponent_takes_exact_path():
     assert abs(dA[1] - dA_ref[1]) < 0.05 * abs(dA_ref[1])
 
 
+def test_backward_steep_decay_takes_exact_path():
+    """A = -200 for one head: step exponents past the -20 clip (their MB0
+    straight-through masks are zero) and block ranges beyond the
+    factorisation bound, so that head runs the pairwise path."""
+    banner("mamba2 bwd steep decay")
+
+    def mutate(inp):
+        inp["A"][1] = -200.0
+    args, ref = _case(1, 256, 3, 64, 128, 128, seed=23, state=True, mutate=mutate)
+    out = _gpu(args, 128, reuse=False)
+    errs = {n: rel_err(g, w) for n, g, w in zip(NAMES, out, ref)}
+    print("  rel_err " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+    for name, e in errs.items():
+        assert e < tol_for(BF16), (name, e)
+
+
 def test_trainable_wrapper_second_backward_recomputes():
     """A second backward through a retained graph no longer holds the
     forward's saved states; it recomputes them and gives the same

@@ -56,6 +56,20 @@ def test_positive_step_exponent_takes_exact_path():
     assert ey < tol_for(BF16) and es < tol_for(BF16)
 
 
+def test_steep_decay_takes_exact_path():
+    """A = -200 for one head: step exponents past the -20 clip and 16-row
+    block ranges far beyond the factorisation bound, so that head's slices
+    are evaluated pairwise with the reference's clips."""
+    banner("mamba2 fwd steep decay")
+
+    def mutate(inp):
+        inp["A"][1] = -200.0
+    (y, s), (y_ref, s_ref) = _run(1, 256, 3, 64, 128, 128, seed=7, mutate=mutate)
+    ey, es = rel_err(y, y_ref), rel_err(s, s_ref)
+    print(f"  rel_err y={ey:.3e} state={es:.3e}")
+    assert ey < tol_for(BF16) and es < tol_for(BF16)
+
+
 def test_decay_weight_cap():
     """A positive step exponent (A = +1) drives exp(clip(cum_i - cum_j, +-20))
     past the reference's 1e6 cap on L (mamba2_ssd_reference.py:120) for the
