@@ -613,7 +613,9 @@ __global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, StageIn dt, St
       // sources of an earlier sub-block feed this sub-block's rows through
       // their own sanitised sub-block sum (acc0); C <= 256 gives at most two
       const bool cross = si > 0 && J / srb < si;
-      for (int jj = 0; jj < RB; ++jj) {
+      // on the diagonal block, sources past this wave's last row add nothing
+      const int jend = J == I ? rg + 16 : RB;
+      for (int jj = 0; jj < jend; ++jj) {
         const int j = RB * J + jj;
         const float cj = sCum[jj * L::LP + p], xb = sDbx[jj * L::LP + p];
 #pragma unroll

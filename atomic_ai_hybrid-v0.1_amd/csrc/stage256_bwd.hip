@@ -521,12 +521,19 @@ __global__ __launch_bounds__(256) void m2b_pair_k(Mamba2Dims d, In dt, In x, In 
     for (int si = 0; si < C / bc; ++si) {
       for (int sj = 0; sj <= si; ++sj) {
         const bool diag = si == sj;
-        if (sj == rb) {  // r as the column j: d_dBx_2 (:95,109)
+        // r as the column j: d_dBx_2 (:95,109) and dcum_j (:107,113) share
+        // the pair weights, so both sums run in one pass (each in its own
+        // order, i ascending); dcum_j joins ac after the row part below
+        float sj_ = 0.f;
+        if (sj == rb) {
           float s2 = 0.f;
           for (int i = si * bc; i < (si + 1) * bc; ++i) {
             const float bl = (diag && i < r) ? 0.f : bcz[(size_t)i * C + r];
-            const float e = __expf(fminf(fmaxf(sCum[i][c] - cr, -kClipDecay), kClipDecay));
+            const float dd = sCum[i][c] - cr;
+            const float e = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
+            const float m = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
             s2 += e * bl * sDy[i][c];
+            sj_ += sDy[i][c] * bxr * bl * e * m;
           }
           a2 = sanitize(a2 + s2);
         }
@@ -541,17 +548,7 @@ __global__ __launch_bounds__(256) void m2b_pair_k(Mamba2Dims d, In dt, In x, In 
           }
           ac = sanitize(ac + si_);
         }
-        if (sj == rb) {  // r as the column j: dcum_j (:107,113)
-          float sj_ = 0.f;
-          for (int i = si * bc; i < (si + 1) * bc; ++i) {
-            const float bl = (diag && i < r) ? 0.f : bcz[(size_t)i * C + r];
-            const float dd = sCum[i][c] - cr;
-            const float e = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
-            const float m = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
-            sj_ += sDy[i][c] * bxr * bl * e * m;
-          }
-          ac = sanitize(ac + (-sj_));
-        }
+        if (sj == rb) ac = sanitize(ac + (-sj_));  // dcum_j (:107,113)
       }
     }
     const size_t o = (zr + r) * P + p0 + c;
