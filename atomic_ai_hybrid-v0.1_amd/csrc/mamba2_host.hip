@@ -398,9 +398,13 @@ static int mamba2_stage_plan(const atomic_mamba2_args* a, Mamba2Plan* p) {
 
 // M3 keeps CB ([B][NT][C][C] bf16) and M4 the states entering each chunk
 // ([B][NT][H][P][N] bf16) in the caller's workspace.
+static size_t m256_stage_ws(const Mamba2Dims& d) {  // M3's CB, or M4's fp32 states entering each chunk
+  const size_t cb = m_cb_ws(d), st = m256_combine_ws(d);
+  return m2_align(cb > st ? cb : st);
+}
 static size_t mamba2_stage_ws(const Mamba2Plan& p) {
   const Mamba2Dims& d = p.dm;
-  if (d.C == kStageBlock) return m2_align(m256_combine_ws(d));   // fp32 states entering each chunk
+  if (d.C == kStageBlock) return m256_stage_ws(d);
   const size_t cb = (size_t)d.B * d.NT * d.C * d.C * 2;
   const size_t st = (size_t)d.B * d.NT * d.H * d.P * d.N * 2;
   return m2_align(cb > st ? cb : st);
@@ -509,7 +513,8 @@ static int mamba2_cumdecay_stage(const Mamba2Plan& p, const void* dt, const floa
 
 static int mamba2_intra_stage(const Mamba2Plan& p, const void* dt, const void* x, const void* Bm, const void* Cm,
                               const float* cum, float* y_diag, float* state_end, void* ws, Launch& L) {
-  if (p.dm.C == kStageBlock) return m256_intra(p.dm, ATOMIC_BF16, dt, x, Bm, Cm, cum, y_diag, state_end, L);
+  if (p.dm.C == kStageBlock)
+    return m256_intra(p.dm, ATOMIC_BF16, dt, x, Bm, Cm, cum, y_diag, state_end, static_cast<float*>(ws), L);
   AH_M2_DISPATCH(mamba2_intra_stage_impl, p, dt, x, Bm, Cm, cum, y_diag, state_end, ws, L);
 }
 
@@ -622,7 +627,7 @@ extern "C" int atomic_mamba2_bwd(const atomic_mamba2_args* a, const void* dt, co
 extern "C" size_t atomic_mamba2_stage_workspace_size(const atomic_mamba2_args* a) {
   Mamba2Plan p;
   if (mamba2_stage_plan(a, &p) != ATOMIC_OK) return 0;
-  return p.f32 ? m2_align(m256_combine_ws(p.f32dm)) : mamba2_stage_ws(p);
+  return p.f32 ? m256_stage_ws(p.f32dm) : mamba2_stage_ws(p);
 }
 
 extern "C" int atomic_mamba2_chunk_cumdecay(const atomic_mamba2_args* a, const void* dt, const float* A,
@@ -645,8 +650,11 @@ extern "C" int atomic_mamba2_intra_chunk_ssd(const atomic_mamba2_args* a, const 
   if (rc != ATOMIC_OK) return rc;
   if (!dt || !x || !B || !C || !cumdecay || !y_diag || !state_end) return ATOMIC_ERR_NULL;
   if (p.f32) {
+    if (!workspace || workspace_bytes < m256_stage_ws(p.f32dm)) return ATOMIC_ERR_WORKSPACE;
+    ws_tag_clobber(workspace, workspace_bytes);
     Launch L{a->profile, (hipStream_t)stream};
-    return m256_intra(p.f32dm, ATOMIC_F32, dt, x, B, C, cumdecay, y_diag, state_end, L);
+    return m256_intra(p.f32dm, ATOMIC_F32, dt, x, B, C, cumdecay, y_diag, state_end, static_cast<float*>(workspace),
+                      L);
   }
   if (!workspace || workspace_bytes < mamba2_stage_ws(p)) return ATOMIC_ERR_WORKSPACE;
   ws_tag_clobber(workspace, workspace_bytes);

@@ -523,26 +523,20 @@ __global__ __launch_bounds__(256) void g256_combine_k(Gdn2Dims d, const float* _
 // (kernel_mamba2_b_intra.py:86-108), CB = sanitize(C B^T) (:83-84),
 // dBx = sanitize(dt x) (:81).  Thread (p = t % 64 of a 64-channel group,
 // rows 16 (t / 64) ..  + 15).
-template <int N>
 struct M3Lds {
-  static constexpr int LN = N + 1, LB = BT + 1, LP = 65;
+  static constexpr int LB = BT + 1, LP = 65;
   static constexpr int off_cb = 0;                  // [64][LB]  CB rows of block I
-  static constexpr int off_c = off_cb + RB * LB;    // [64][LN]  C rows of block I (fp32)
-  static constexpr int off_b = off_c + RB * LN;     // [64][LN]  B rows of one source block
-  static constexpr int off_cum = off_c;             // after CB: [64][LP] cum_j, [64][LP] dBx_j
-  static constexpr int off_dbx = off_cum + RB * LP;
-  static constexpr int floats = off_b + RB * LN;
-  static_assert(2 * RB * LP <= 2 * RB * LN, "the source tiles fit where C and B were");
+  static constexpr int off_cum = off_cb + RB * LB;  // [64][LP]  cum_j of one source block
+  static constexpr int off_dbx = off_cum + RB * LP; // [64][LP]  dBx_j
+  static constexpr int floats = off_dbx + RB * LP;
 };
 
 template <int P, int N>
-__global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, StageIn dt, StageIn x, StageIn Bm, StageIn Cm,
+__global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, StageIn dt, StageIn x, const float* __restrict__ cbg,
                                                     const float* __restrict__ cum, float* __restrict__ y_diag) {
-  typedef M3Lds<N> L;
+  typedef M3Lds L;
   __shared__ float smem[L::floats];
   float* sCB = smem + L::off_cb;
-  float* sC = smem + L::off_c;
-  float* sB = smem + L::off_b;
   float* sCum = smem + L::off_cum;
   float* sDbx = smem + L::off_dbx;
   const int C = d.C, nrb = C / RB;
@@ -553,42 +547,11 @@ __global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, StageIn dt, St
   // row blocks per sub-block, and block I's sub-block
   const int srb = (C < 128 ? C : 128) / RB, si = I / srb;
   const int jmax = (si + 1) * srb * RB;   // source rows: this sub-block and the ones before
-  // CB rows of block I against source rows [0, jmax)
-  for (int e = t; e < RB * N; e += 256) {
-    const int rr = e / N, s = e % N;
-    sC[rr * L::LN + s] = ld(Cm, (row0 + RB * I + rr) * d.rC + s);
-  }
-  {
-    const int ti = t >> 4, tj = t & 15;   // rows ti + 16 a, columns tj + 16 c of a 64 x 64 tile
-    for (int J = 0; J < jmax / RB; ++J) {
-      __syncthreads();
-      for (int e = t; e < RB * N; e += 256) {
-        const int rr = e / N, s = e % N;
-        sB[rr * L::LN + s] = ld(Bm, (row0 + RB * J + rr) * d.rB + s);
-      }
-      __syncthreads();
-      float acc[4][4];
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[a][c] = 0.f;
-      for (int s = 0; s < N; ++s) {
-        float cv[4], bv[4];
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          cv[a] = sC[(ti + 16 * a) * L::LN + s];
-          bv[a] = sB[(tj + 16 * a) * L::LN + s];
-        }
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) acc[a][c] += cv[a] * bv[c];
-      }
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) sCB[(ti + 16 * a) * L::LB + RB * J + tj + 16 * c] = sanitize(acc[a][c]);
-    }
+  // CB rows of block I against source rows [0, jmax), from the chunk's CB
+  const float* cbz = cbg + (((size_t)bb * d.NT + n) * C + (size_t)RB * I) * C;
+  for (int e = t; e < RB * jmax; e += 256) {
+    const int rr = e / jmax, j = e % jmax;
+    sCB[rr * L::LB + j] = cbz[(size_t)rr * C + j];
   }
   const int p = t & 63, rg = 16 * (t >> 6);
   for (int p0 = 0; p0 < P; p0 += 64) {
@@ -823,15 +786,17 @@ int g256_combine(const Gdn2Dims& d, const float* aqk, const float* wt, const flo
 
 template <int P, int N>
 static int m256_intra_t(const Mamba2Dims& d, int dtype, const void* dt, const void* x, const void* Bm,
-                        const void* Cm, const float* cum, float* y_diag, float* state_end, Launch& L) {
+                        const void* Cm, const float* cum, float* y_diag, float* state_end, float* cb, Launch& L) {
   const size_t bhn = (size_t)d.B * d.H * d.NT;
-  static_assert(M3Lds<N>::floats * sizeof(float) <= 160 * 1024, "M3 tiles fit the LDS");
+  static_assert(M3Lds::floats * sizeof(float) <= 160 * 1024, "M3 tiles fit the LDS");
   if (d.C != 64 && d.C != 128 && d.C != 256) return ATOMIC_ERR_SHAPE;
   const int bf = dtype == ATOMIC_BF16;
-  const StageIn idt{dt, bf}, ix{x, bf}, iB{Bm, bf}, iC{Cm, bf};
-  int rc = L("mamba2_intra_bt256", [&] {
+  const StageIn idt{dt, bf}, ix{x, bf}, iB{Bm, bf};
+  int rc = m_cb(d, dtype, Bm, Cm, cb, L);
+  if (rc) return rc;
+  rc = L("mamba2_intra_bt256", [&] {
     hipLaunchKernelGGL((m256_ydiag_k<P, N>), dim3((unsigned)(bhn * (d.C / RB))), dim3(256), 0, L.st, d, idt, ix,
-                       iB, iC, cum, y_diag);
+                       cb, cum, y_diag);
   });
   if (rc) return rc;
   return L("mamba2_state_end_bt256", [&] {
@@ -869,8 +834,8 @@ static int m256_combine_t(const Mamba2Dims& d, int dtype, const float* y_diag, c
   } while (0)
 
 int m256_intra(const Mamba2Dims& d, int dtype, const void* dt, const void* x, const void* Bm, const void* Cm,
-               const float* cum, float* y_diag, float* state_end, Launch& L) {
-  AH_M256_DISPATCH(m256_intra_t, d, dtype, dt, x, Bm, Cm, cum, y_diag, state_end, L);
+               const float* cum, float* y_diag, float* state_end, float* cb, Launch& L) {
+  AH_M256_DISPATCH(m256_intra_t, d, dtype, dt, x, Bm, Cm, cum, y_diag, state_end, cb, L);
 }
 
 int m256_combine(const Mamba2Dims& d, int dtype, const float* y_diag, const float* state_end, const float* cum,

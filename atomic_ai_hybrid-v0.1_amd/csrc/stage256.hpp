@@ -37,10 +37,15 @@ int g256_combine(const Gdn2Dims& d, const float* aqk, const float* wt, const flo
 
 // Mamba2 (dims with C = 64, 128 or 256; dt, x, B, C of dtype, bf16 or
 // fp32): M3 (y_diag [B][T][H][P], state_end [B][H][NT][P][N]) over the
-// reference's min(128, C)-row sub-blocks and M4 (y, state_final; the states
-// entering each chunk go to ws, [B][NT][H][P][N] fp32).
+// reference's min(128, C)-row sub-blocks, with the chunks' CB = sanitize(C
+// B^T) formed once per (batch, chunk) into cb ([B][NT][C][C] fp32, m_cb_ws
+// bytes), and M4 (y, state_final; the states entering each chunk go to ws,
+// [B][NT][H][P][N] fp32).
 int m256_intra(const Mamba2Dims& d, int dtype, const void* dt, const void* x, const void* Bm, const void* Cm,
-               const float* cum, float* y_diag, float* state_end, Launch& L);
+               const float* cum, float* y_diag, float* state_end, float* cb, Launch& L);
+// CB = sanitize(C B^T) per (batch, chunk) on the float32 GEMM (stage256_bwd.hip)
+int m_cb(const Mamba2Dims& d, int dtype, const void* Bm, const void* Cm, float* cb, Launch& L);
+size_t m_cb_ws(const Mamba2Dims& d);
 int m256_combine(const Mamba2Dims& d, int dtype, const float* y_diag, const float* state_end, const float* cum,
                  const void* Cm, const float* state0, float* y, float* state_final, float* ws, Launch& L);
 size_t m256_combine_ws(const Mamba2Dims& d);

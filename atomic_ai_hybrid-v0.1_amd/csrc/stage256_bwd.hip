@@ -1008,14 +1008,9 @@ int m_intra_bwd(const Mamba2Dims& d, int dtype, int dy_dtype, const void* dt, co
   auto dense3 = [&](long long S) { return Bat{(long long)H * NT * S, (long long)NT * S, S}; };
   auto rows3 = [&](long long r) { return Bat{(long long)d.T * r, 0, (long long)C * r}; };
   // CB = sanitize(C B^T) per (batch, chunk)   (:48)
-  GemmOp g = gemm_op(C, C, N, d.B * NT);
-  g.Z1 = 1; g.Z0 = NT;
-  g.A = In{Cp, bf}; g.lda = d.rC; g.sa = Bat{(long long)d.T * d.rC, 0, (long long)C * d.rC};
-  g.B = In{Bp, bf}; g.ldb = d.rB; g.sb = Bat{(long long)d.T * d.rB, 0, (long long)C * d.rB}; g.tb = 1;
-  g.C = bcin; g.ldc = C; g.sc = Bat{(long long)NT * C * C, 0, (long long)C * C};
-  g.post = 2;
-  int rc = gemm(g, d.B * NT, "m2b_cb", L);
+  int rc = m_cb(d, dtype, Bm, Cm, bcin, L);
   if (rc != ATOMIC_OK) return rc;
+  GemmOp g;
   // dwrite = sanitize(B dstate_end^T)   (:56)
   g = gemm_op(C, P, N, Z);
   g.Z1 = H; g.Z0 = NT;
@@ -1160,6 +1155,19 @@ int m_da_bwd(const Mamba2Dims& d, int dt_dtype, int tok, const void* dtp, const 
 }
 
 
+size_t m_cb_ws(const Mamba2Dims& d) { return (size_t)d.B * d.NT * d.C * d.C * sizeof(float); }
+
+int m_cb(const Mamba2Dims& d, int dtype, const void* Bm, const void* Cm, float* cb, Launch& L) {
+  const int C = d.C, N = d.N, NT = d.NT, bf = dtype == ATOMIC_BF16;
+  GemmOp g = gemm_op(C, C, N, d.B * NT);
+  g.Z1 = 1; g.Z0 = NT;
+  g.A = In{Cm, bf}; g.lda = d.rC; g.sa = Bat{(long long)d.T * d.rC, 0, (long long)C * d.rC};
+  g.B = In{Bm, bf}; g.ldb = d.rB; g.sb = Bat{(long long)d.T * d.rB, 0, (long long)C * d.rB}; g.tb = 1;
+  g.C = cb; g.ldc = C; g.sc = Bat{(long long)NT * C * C, 0, (long long)C * C};
+  g.post = 2;
+  return gemm(g, d.B * NT, "mamba2_cb_f32", L);
+}
+
 int m_cumdecay(const Mamba2Dims& d, int dtype, const void* dt, const float* A, float* cum, Launch& L) {
   const size_t n = (size_t)d.B * d.H * d.NT * d.P;
   const In idt{dt, dtype == ATOMIC_BF16};
@@ -1168,9 +1176,10 @@ int m_cumdecay(const Mamba2Dims& d, int dtype, const void* dt, const float* A, f
   });
 }
 
-size_t m_f32_fwd_ws(const Mamba2Dims& d) {
+size_t m_f32_fwd_ws(const Mamba2Dims& d) {  // cum, y_diag, state_end, then M3's CB or M4's states
   const size_t Z = (size_t)d.B * d.H * d.NT;
-  return (Z * d.C * d.P + (size_t)d.B * d.T * d.H * d.P + Z * d.P * d.N) * sizeof(float) + m256_combine_ws(d);
+  const size_t cb = m_cb_ws(d), st = m256_combine_ws(d);
+  return (Z * d.C * d.P + (size_t)d.B * d.T * d.H * d.P + Z * d.P * d.N) * sizeof(float) + (cb > st ? cb : st);
 }
 
 int m_f32_fwd(const Mamba2Dims& d, const void* dt, const void* x, const void* Bm, const void* Cm, const float* A,
@@ -1182,7 +1191,7 @@ int m_f32_fwd(const Mamba2Dims& d, const void* dt, const void* x, const void* Bm
   float* pre = state_end + Z * d.P * d.N;
   int rc = m_cumdecay(d, ATOMIC_F32, dt, A, cum, L);
   if (rc) return rc;
-  if ((rc = m256_intra(d, ATOMIC_F32, dt, x, Bm, Cm, cum, y_diag, state_end, L))) return rc;
+  if ((rc = m256_intra(d, ATOMIC_F32, dt, x, Bm, Cm, cum, y_diag, state_end, pre, L))) return rc;
   return m256_combine(d, ATOMIC_F32, y_diag, state_end, cum, Cm, state0, y, state_final, pre, L);
 }
 
