@@ -523,23 +523,23 @@ __global__ __launch_bounds__(256) void g256_combine_k(Gdn2Dims d, const float* _
 // (kernel_mamba2_b_intra.py:86-108), CB = sanitize(C B^T) (:83-84),
 // dBx = sanitize(dt x) (:81).  Thread (p = t % 64 of a 64-channel group,
 // rows 16 (t / 64) ..  + 15).
+// Dynamic LDS sized by the chunk, so that chunks of 64 / 128 rows run
+// three / two workgroups per CU: CB rows of block I [64][C + 1], then the
+// cum_j and dBx_j of one source block [64][LP] each.
 struct M3Lds {
-  static constexpr int LB = BT + 1, LP = 65;
-  static constexpr int off_cb = 0;                  // [64][LB]  CB rows of block I
-  static constexpr int off_cum = off_cb + RB * LB;  // [64][LP]  cum_j of one source block
-  static constexpr int off_dbx = off_cum + RB * LP; // [64][LP]  dBx_j
-  static constexpr int floats = off_dbx + RB * LP;
+  static constexpr int LP = 65;
+  static int floats(int C) { return RB * (C + 1) + 2 * RB * LP; }
 };
 
 template <int P, int N>
 __global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, StageIn dt, StageIn x, const float* __restrict__ cbg,
                                                     const float* __restrict__ cum, float* __restrict__ y_diag) {
   typedef M3Lds L;
-  __shared__ float smem[L::floats];
-  float* sCB = smem + L::off_cb;
-  float* sCum = smem + L::off_cum;
-  float* sDbx = smem + L::off_dbx;
-  const int C = d.C, nrb = C / RB;
+  extern __shared__ float smem[];
+  const int C = d.C, nrb = C / RB, LB = C + 1;
+  float* sCB = smem;
+  float* sCum = smem + RB * LB;
+  float* sDbx = sCum + RB * L::LP;
   const int bhn = blockIdx.x / nrb, I = nrb - 1 - (int)(blockIdx.x % nrb);
   const int bh = bhn / d.NT, n = bhn % d.NT, bb = bh / d.H, h = bh % d.H;
   const size_t row0 = (size_t)bb * d.T + (size_t)n * C;
@@ -551,7 +551,7 @@ __global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, StageIn dt, St
   const float* cbz = cbg + (((size_t)bb * d.NT + n) * C + (size_t)RB * I) * C;
   for (int e = t; e < RB * jmax; e += 256) {
     const int rr = e / jmax, j = e % jmax;
-    sCB[rr * L::LB + j] = cbz[(size_t)rr * C + j];
+    sCB[rr * LB + j] = cbz[(size_t)rr * C + j];
   }
   const int p = t & 63, rg = 16 * (t >> 6);
   for (int p0 = 0; p0 < P; p0 += 64) {
@@ -585,7 +585,7 @@ __global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, StageIn dt, St
         for (int a = 0; a < 16; ++a) {
           const int i = RB * I + rg + a;
           const float wgt = j <= i ? __expf(fminf(fmaxf(ci[a] - cj, -kClipDecay), kClipDecay)) *
-                                         sCB[(rg + a) * L::LB + j]
+                                         sCB[(rg + a) * LB + j]
                                    : 0.f;
           if (cross) acc0[a] += wgt * xb;
           else acc1[a] += wgt * xb;
@@ -788,14 +788,17 @@ template <int P, int N>
 static int m256_intra_t(const Mamba2Dims& d, int dtype, const void* dt, const void* x, const void* Bm,
                         const void* Cm, const float* cum, float* y_diag, float* state_end, float* cb, Launch& L) {
   const size_t bhn = (size_t)d.B * d.H * d.NT;
-  static_assert(M3Lds::floats * sizeof(float) <= 160 * 1024, "M3 tiles fit the LDS");
   if (d.C != 64 && d.C != 128 && d.C != 256) return ATOMIC_ERR_SHAPE;
+  const size_t lds = (size_t)M3Lds::floats(d.C) * sizeof(float);  // <= 99 KB at C = 256
+  if (hipFuncSetAttribute((const void*)m256_ydiag_k<P, N>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+      hipSuccess)
+    return ATOMIC_ERR_LAUNCH;
   const int bf = dtype == ATOMIC_BF16;
   const StageIn idt{dt, bf}, ix{x, bf}, iB{Bm, bf};
   int rc = m_cb(d, dtype, Bm, Cm, cb, L);
   if (rc) return rc;
   rc = L("mamba2_intra_bt256", [&] {
-    hipLaunchKernelGGL((m256_ydiag_k<P, N>), dim3((unsigned)(bhn * (d.C / RB))), dim3(256), 0, L.st, d, idt, ix,
+    hipLaunchKernelGGL((m256_ydiag_k<P, N>), dim3((unsigned)(bhn * (d.C / RB))), dim3(256), lds, L.st, d, idt, ix,
                        cb, cum, y_diag);
   });
   if (rc) return rc;
