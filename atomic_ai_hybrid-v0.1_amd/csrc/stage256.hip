@@ -523,36 +523,30 @@ __global__ __launch_bounds__(256) void g256_combine_k(Gdn2Dims d, const float* _
 // (kernel_mamba2_b_intra.py:86-108), CB = sanitize(C B^T) (:83-84),
 // dBx = sanitize(dt x) (:81).  Thread (p = t % 64 of a 64-channel group,
 // rows 16 (t / 64) ..  + 15).
-// Dynamic LDS sized by the chunk, so that chunks of 64 / 128 rows run
-// three / two workgroups per CU: CB rows of block I [64][C + 1], then the
-// cum_j and dBx_j of one source block [64][LP] each.
+// One source block at a time (50 KB, three workgroups per CU): the CB tile
+// of block I against it, then its cum_j and dBx_j, [64][LP] each.
 struct M3Lds {
   static constexpr int LP = 65;
-  static int floats(int C) { return RB * (C + 1) + 2 * RB * LP; }
+  static constexpr int off_cb = 0, off_cum = RB * LP, off_dbx = 2 * RB * LP, floats = 3 * RB * LP;
 };
 
 template <int P, int N>
 __global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, StageIn dt, StageIn x, const float* __restrict__ cbg,
                                                     const float* __restrict__ cum, float* __restrict__ y_diag) {
   typedef M3Lds L;
-  extern __shared__ float smem[];
-  const int C = d.C, nrb = C / RB, LB = C + 1;
-  float* sCB = smem;
-  float* sCum = smem + RB * LB;
-  float* sDbx = sCum + RB * L::LP;
+  __shared__ float smem[L::floats];
+  const int C = d.C, nrb = C / RB;
+  float* sCB = smem + L::off_cb;
+  float* sCum = smem + L::off_cum;
+  float* sDbx = smem + L::off_dbx;
   const int bhn = blockIdx.x / nrb, I = nrb - 1 - (int)(blockIdx.x % nrb);
   const int bh = bhn / d.NT, n = bhn % d.NT, bb = bh / d.H, h = bh % d.H;
   const size_t row0 = (size_t)bb * d.T + (size_t)n * C;
   const int t = threadIdx.x;
   // row blocks per sub-block, and block I's sub-block
   const int srb = (C < 128 ? C : 128) / RB, si = I / srb;
-  const int jmax = (si + 1) * srb * RB;   // source rows: this sub-block and the ones before
-  // CB rows of block I against source rows [0, jmax), from the chunk's CB
+  // CB rows of block I in the chunk's CB
   const float* cbz = cbg + (((size_t)bb * d.NT + n) * C + (size_t)RB * I) * C;
-  for (int e = t; e < RB * jmax; e += 256) {
-    const int rr = e / jmax, j = e % jmax;
-    sCB[rr * LB + j] = cbz[(size_t)rr * C + j];
-  }
   const int p = t & 63, rg = 16 * (t >> 6);
   for (int p0 = 0; p0 < P; p0 += 64) {
     const size_t hp = (size_t)h * P + p0 + p;
@@ -571,6 +565,7 @@ __global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, StageIn dt, St
         sCum[rr * L::LP + pp] = cum[((size_t)bhn * C + RB * J + rr) * P + p0 + pp];
         sDbx[rr * L::LP + pp] = sanitize(ld(dt, row * d.rdt + (size_t)h * P + p0 + pp) *
                                          ld(x, row * d.rx + (size_t)h * P + p0 + pp));
+        sCB[rr * L::LP + pp] = cbz[(size_t)rr * C + RB * J + pp];   // CB(row 64 I + rr, source 64 J + pp)
       }
       __syncthreads();
       // sources of an earlier sub-block feed this sub-block's rows through
@@ -585,7 +580,7 @@ __global__ __launch_bounds__(256) void m256_ydiag_k(Mamba2Dims d, StageIn dt, St
         for (int a = 0; a < 16; ++a) {
           const int i = RB * I + rg + a;
           const float wgt = j <= i ? __expf(fminf(fmaxf(ci[a] - cj, -kClipDecay), kClipDecay)) *
-                                         sCB[(rg + a) * LB + j]
+                                         sCB[(rg + a) * L::LP + jj]
                                    : 0.f;
           if (cross) acc0[a] += wgt * xb;
           else acc1[a] += wgt * xb;
@@ -789,16 +784,12 @@ static int m256_intra_t(const Mamba2Dims& d, int dtype, const void* dt, const vo
                         const void* Cm, const float* cum, float* y_diag, float* state_end, float* cb, Launch& L) {
   const size_t bhn = (size_t)d.B * d.H * d.NT;
   if (d.C != 64 && d.C != 128 && d.C != 256) return ATOMIC_ERR_SHAPE;
-  const size_t lds = (size_t)M3Lds::floats(d.C) * sizeof(float);  // <= 99 KB at C = 256
-  if (hipFuncSetAttribute((const void*)m256_ydiag_k<P, N>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
-      hipSuccess)
-    return ATOMIC_ERR_LAUNCH;
   const int bf = dtype == ATOMIC_BF16;
   const StageIn idt{dt, bf}, ix{x, bf}, iB{Bm, bf};
   int rc = m_cb(d, dtype, Bm, Cm, cb, L);
   if (rc) return rc;
   rc = L("mamba2_intra_bt256", [&] {
-    hipLaunchKernelGGL((m256_ydiag_k<P, N>), dim3((unsigned)(bhn * (d.C / RB))), dim3(256), lds, L.st, d, idt, ix,
+    hipLaunchKernelGGL((m256_ydiag_k<P, N>), dim3((unsigned)(bhn * (d.C / RB))), dim3(256), 0, L.st, d, idt, ix,
                        cb, cum, y_diag);
   });
   if (rc) return rc;
