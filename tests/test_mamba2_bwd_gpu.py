@@ -190,3 +190,43 @@ def test_reuse_requires_the_matching_forward():
         if a is None:
             continue
         assert torch.equal(a, b_) and torch.equal(a, c)
+
+
+def test_nonfinite_x_is_absorbed_like_mb0():
+    """NaN and inf in x: dBx = sanitize(dt x) absorbs them where MB0 does
+    (mamba2_bwd_reference.py:93); every gradient is finite and equals the
+    oracle's after the final sanitise."""
+    banner("mamba2 bwd non-finite x")
+
+    def mutate(inp):
+        inp["x"][0, 50, 1, 2] = float("nan")
+        inp["x"][0, 130, 0, 9] = float("inf")
+    args, ref = _case(1, 256, 2, 64, 128, 128, seed=29, state=True, mutate=mutate)
+    out = _gpu(args, 128, reuse=False)
+    errs = {}
+    for name, got, want in zip(NAMES, out, ref):
+        assert torch.isfinite(got).all(), name
+        errs[name] = rel_err(got, om.final_sanitize(want))
+    print("  rel_err " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+    for name, e in errs.items():
+        assert e < tol_for(BF16), (name, e)
+
+
+def test_nonfinite_dy_gives_finite_gradients():
+    """A NaN and an inf in dy: every gradient is finite.  MB0 multiplies its
+    causal masks in (mamba2_bwd_reference.py:147-156), so a non-finite dy_i
+    turns the masked pairs (j > i) into NaN (NaN x 0) and its sanitise then
+    zeroes every dB of that chunk and the whole dBx column of that channel;
+    the kernels skip the masked pairs, so those entries keep their values and
+    are not compared (the model's gradient sanitiser, model.py:192-217, keeps
+    dy finite)."""
+    banner("mamba2 bwd non-finite dy")
+
+    def mutate(inp):
+        inp["dy"][0, 5, 1, 3] = float("nan")
+        inp["dy"][0, 100, 0, 7] = float("inf")
+    args, _ = _case(1, 256, 2, 64, 128, 128, seed=29, state=True, mutate=mutate)
+    out = _gpu(args, 128, reuse=False)
+    for name, got in zip(NAMES, out):
+        assert torch.isfinite(got).all(), name
+        assert got.abs().max().item() <= 1e4, name
