@@ -206,3 +206,22 @@ def test_reuse_requires_the_matching_forward():
     torch.cuda.synchronize()
     for a, r in zip(got, ref):
         assert torch.equal(a, r)
+
+
+def test_nonfinite_do_gives_finite_gradients():
+    """A NaN and an inf in dO: every gradient is finite and inside the final
+    clip (kernel_trainable_B6.py:173-179).  The autodiff oracle multiplies
+    its causal masks in, so a non-finite dO row also poisons the masked pairs
+    (NaN x 0) before the sanitising clips; the kernels skip those pairs, so
+    the values are not compared (the model's gradient sanitiser,
+    model.py:192-217, keeps dO finite)."""
+    banner("gdn2 bwd non-finite dO")
+
+    def mutate(inp):
+        inp["do"][0, 10, 1, 5] = float("nan")
+        inp["do"][0, 70, 0, 3] = float("inf")
+    args, _ = _case(1, 128, 2, 128, BF16, seed=41, with_state=True, mutate=mutate)
+    out = _gpu(args, 1.0, reuse=True)
+    for name, got in zip(NAMES, out):
+        assert torch.isfinite(got).all(), name
+        assert got.abs().max().item() <= 1e4, name
