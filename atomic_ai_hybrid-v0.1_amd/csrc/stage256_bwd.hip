@@ -489,77 +489,141 @@ __global__ __launch_bounds__(256) void m2b_dbc_k(Mamba2Dims d, In dy, const floa
 }
 
 // d_dBx_2 and dcum over the sub-block pairs, then ddt, dx and dcum
-// (:74-128).  One workgroup per (item, 16-channel slice); thread (row group,
-// channel): rows rg + 16 m.
+// (:74-128).  One workgroup per (item, 64-row block R, 32 channels); thread
+// (channel p = t % 32, rows 64 R + rg .. + 7, rg = 8 (t / 32)).  For each
+// sub-block pair the partner rows are staged 64 at a time with the CB tile
+// between them and block R; every row sums its partners in ascending order,
+// masked pairs included (their zero weight multiplies in, as the reference's
+// causal mask does).
 __global__ __launch_bounds__(256) void m2b_pair_k(Mamba2Dims d, In dt, In x, In dy, const float* __restrict__ cum,
                                                   const float* __restrict__ bcin, const float* __restrict__ dbx,
                                                   const float* __restrict__ d1, const float* __restrict__ ddd,
                                                   float* __restrict__ ddt, float* __restrict__ dx,
                                                   float* __restrict__ dcum) {
-  constexpr int MAXC = 256;
-  __shared__ float sCum[MAXC][17], sDy[MAXC][17], sBx[MAXC][17];
-  __shared__ float sLast[16][17];
-  const int C = d.C, P = d.P, bc = C < 128 ? C : 128, nps = P / 16;
-  const int z = blockIdx.x / nps, p0 = (blockIdx.x % nps) * 16;
+  constexpr int NR = 8, PC = 32, LP = PC + 1, LB = 65;
+  __shared__ float sCum[64 * LP], sVal[64 * LP], sCB[64 * LB];
+  __shared__ float sLast[16][PC];
+  const int C = d.C, P = d.P, bc = C < 128 ? C : 128, nrb = C / 64, npg = P / PC;
+  const int z = blockIdx.x / (nrb * npg), rem = blockIdx.x % (nrb * npg);
+  const int R = rem / npg, p0 = (rem % npg) * PC;
   const int n = z % d.NT, h = z / d.NT % d.H, b = z / (d.NT * d.H);
-  const int t = threadIdx.x, c = t % 16, rg = t / 16;
+  const int t = threadIdx.x, p = t % PC, rg = NR * (t / PC);
   const size_t zr = (size_t)z * C, row0 = (size_t)b * d.T + (size_t)n * C;
+  const size_t hp = (size_t)h * P + p0;
   const float* bcz = bcin + ((size_t)b * d.NT + n) * C * C;   // sanitize(C B^T) of (b, n)
-  float lastp = 0.f;
-  for (int r = rg; r < C; r += 16) {
-    sCum[r][c] = cum[(zr + r) * P + p0 + c];
-    sDy[r][c] = ld(dy, (row0 + r) * d.rdy + (size_t)h * P + p0 + c);
-    sBx[r][c] = dbx[(zr + r) * P + p0 + c];
-    lastp += ddd[(zr + r) * P + p0 + c];
+  const int rb = 64 * R / bc, nsub = C / bc, bpb = bc / 64;  // R's sub-block; 64-row blocks per sub-block
+  float cr[NR], dyr[NR], bxr[NR], a2[NR], ac[NR];
+#pragma unroll
+  for (int a = 0; a < NR; ++a) {
+    const int r = 64 * R + rg + a;
+    cr[a] = cum[(zr + r) * P + p0 + p];
+    dyr[a] = ld(dy, (row0 + r) * d.rdy + hp + p);
+    bxr[a] = dbx[(zr + r) * P + p0 + p];
+    a2[a] = 0.f;
+    ac[a] = 0.f;
   }
-  sLast[rg][c] = lastp;
-  __syncthreads();
-  for (int r = rg; r < C; r += 16) {
-    const int rb = r / bc;
-    const float cr = sCum[r][c], dyr = sDy[r][c], bxr = sBx[r][c];
-    float a2 = 0.f, ac = 0.f;
-    for (int si = 0; si < C / bc; ++si) {
-      for (int sj = 0; sj <= si; ++sj) {
-        const bool diag = si == sj;
-        // r as the column j: d_dBx_2 (:95,109) and dcum_j (:107,113) share
-        // the pair weights, so both sums run in one pass (each in its own
-        // order, i ascending); dcum_j joins ac after the row part below
-        float sj_ = 0.f;
-        if (sj == rb) {
-          float s2 = 0.f;
-          for (int i = si * bc; i < (si + 1) * bc; ++i) {
-            const float bl = (diag && i < r) ? 0.f : bcz[(size_t)i * C + r];
-            const float dd = sCum[i][c] - cr;
-            const float e = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
-            const float m = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
-            s2 += e * bl * sDy[i][c];
-            sj_ += sDy[i][c] * bxr * bl * e * m;
+  for (int si = 0; si < nsub; ++si) {
+    for (int sj = 0; sj <= si; ++sj) {
+      const bool diag = si == sj;
+      float sjs[NR];
+#pragma unroll
+      for (int a = 0; a < NR; ++a) sjs[a] = 0.f;
+      if (sj == rb) {  // R's rows as the column j: d_dBx_2 (:95,109) and dcum_j (:107,113), one pass
+        float s2[NR];
+#pragma unroll
+        for (int a = 0; a < NR; ++a) s2[a] = 0.f;
+        for (int Q = si * bpb; Q < (si + 1) * bpb; ++Q) {
+          __syncthreads();
+          for (int e = t; e < 64 * PC; e += 256) {
+            const int rr = e / PC, pp = e % PC;
+            sCum[rr * LP + pp] = cum[(zr + 64 * Q + rr) * P + p0 + pp];
+            sVal[rr * LP + pp] = ld(dy, (row0 + 64 * Q + rr) * d.rdy + hp + pp);
           }
-          a2 = sanitize(a2 + s2);
-        }
-        if (si == rb) {  // r as the row i: dcum_i (:105-106,112)
-          float si_ = 0.f;
-          for (int j = sj * bc; j < (sj + 1) * bc; ++j) {
-            const float bl = (diag && j > r) ? 0.f : bcz[(size_t)r * C + j];
-            const float dd = cr - sCum[j][c];
-            const float e = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
-            const float m = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
-            si_ += dyr * sBx[j][c] * bl * e * m;
+          for (int e = t; e < 64 * 64; e += 256) {
+            const int rr = e >> 6, cc = e & 63;
+            sCB[rr * LB + cc] = bcz[(size_t)(64 * Q + rr) * C + 64 * R + cc];   // CB(i, j), i in Q, j in R
           }
-          ac = sanitize(ac + si_);
+          __syncthreads();
+          for (int ii = 0; ii < 64; ++ii) {
+            const int i = 64 * Q + ii;
+            const float ci = sCum[ii * LP + p], dyi = sVal[ii * LP + p];
+#pragma unroll
+            for (int a = 0; a < NR; ++a) {
+              const float bl = (diag && i < 64 * R + rg + a) ? 0.f : sCB[ii * LB + rg + a];
+              const float dd = ci - cr[a];
+              const float e = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
+              const float m = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
+              s2[a] += e * bl * dyi;
+              sjs[a] += dyi * bxr[a] * bl * e * m;
+            }
+          }
         }
-        if (sj == rb) ac = sanitize(ac + (-sj_));  // dcum_j (:107,113)
+#pragma unroll
+        for (int a = 0; a < NR; ++a) a2[a] = sanitize(a2[a] + s2[a]);
+      }
+      if (si == rb) {  // R's rows as the row i: dcum_i (:105-106,112)
+        float sis[NR];
+#pragma unroll
+        for (int a = 0; a < NR; ++a) sis[a] = 0.f;
+        for (int Q = sj * bpb; Q < (sj + 1) * bpb; ++Q) {
+          __syncthreads();
+          for (int e = t; e < 64 * PC; e += 256) {
+            const int rr = e / PC, pp = e % PC;
+            sCum[rr * LP + pp] = cum[(zr + 64 * Q + rr) * P + p0 + pp];
+            sVal[rr * LP + pp] = dbx[(zr + 64 * Q + rr) * P + p0 + pp];
+          }
+          for (int e = t; e < 64 * 64; e += 256) {
+            const int rr = e >> 6, cc = e & 63;
+            sCB[rr * LB + cc] = bcz[(size_t)(64 * R + rr) * C + 64 * Q + cc];   // CB(i, j), i in R, j in Q
+          }
+          __syncthreads();
+          for (int jj = 0; jj < 64; ++jj) {
+            const int j = 64 * Q + jj;
+            const float cj = sCum[jj * LP + p], bxj = sVal[jj * LP + p];
+#pragma unroll
+            for (int a = 0; a < NR; ++a) {
+              const float bl = (diag && j > 64 * R + rg + a) ? 0.f : sCB[(rg + a) * LB + jj];
+              const float dd = cr[a] - cj;
+              const float e = __expf(fminf(fmaxf(dd, -kClipDecay), kClipDecay));
+              const float m = (dd >= -kClipDecay && dd <= kClipDecay) ? 1.f : 0.f;
+              sis[a] += dyr[a] * bxj * bl * e * m;
+            }
+          }
+        }
+#pragma unroll
+        for (int a = 0; a < NR; ++a) ac[a] = sanitize(ac[a] + sis[a]);
+      }
+      if (sj == rb) {
+#pragma unroll
+        for (int a = 0; a < NR; ++a) ac[a] = sanitize(ac[a] + (-sjs[a]));   // dcum_j (:107,113)
       }
     }
-    const size_t o = (zr + r) * P + p0 + c;
-    const float dtot = sanitize(d1[o] + a2);                                      // :116
-    const size_t io = (row0 + r) * (size_t)d.H * P + (size_t)h * P + p0 + c;
-    ddt[io] = sanitize(dtot * ld(x, (row0 + r) * d.rx + (size_t)h * P + p0 + c));  // :118,126
-    dx[io] = sanitize(dtot * ld(dt, (row0 + r) * d.rdt + (size_t)h * P + p0 + c)); // :119,127
-    float dc = ac + (-ddd[o]);                                                    // :64,121
+  }
+  // the last row's d_cum_last_b: ddd summed over the chunk's rows, per row
+  // group g (rows g, g + 16, ..) and then over the groups (:64-65,122-123)
+  const bool last = R == nrb - 1;
+  if (last) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int g = 2 * (t / PC) + u;
+      float lp = 0.f;
+      for (int r = g; r < C; r += 16) lp += ddd[(zr + r) * P + p0 + p];
+      sLast[g][p] = lp;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int a = 0; a < NR; ++a) {
+    const int r = 64 * R + rg + a;
+    const size_t o = (zr + r) * P + p0 + p;
+    const float dtot = sanitize(d1[o] + a2[a]);                                   // :116
+    const size_t io = (row0 + r) * (size_t)d.H * P + hp + p;
+    ddt[io] = sanitize(dtot * ld(x, (row0 + r) * d.rx + hp + p));                  // :118,126
+    dx[io] = sanitize(dtot * ld(dt, (row0 + r) * d.rdt + hp + p));                 // :119,127
+    float dc = ac[a] + (-ddd[o]);                                                 // :64,121
     if (r == C - 1) {                                                             // :65,122-123
       float lb = 0.f;
-      for (int g2 = 0; g2 < 16; ++g2) lb += sLast[g2][c];
+      for (int g2 = 0; g2 < 16; ++g2) lb += sLast[g2][p];
       dc = dc + lb;
     }
     dcum[o] = sanitize(dc);                                                       // :128
@@ -1063,7 +1127,7 @@ int m_intra_bwd(const Mamba2Dims& d, int dtype, int dy_dtype, const void* dt, co
     }
   }
   rc = L("m2b_pair", [&] {
-    hipLaunchKernelGGL(m2b_pair_k, dim3(Z * (P / 16)), dim3(256), 0, L.st, d, idt, ix, idy, cum, bcin, dbx, d1,
+    hipLaunchKernelGGL(m2b_pair_k, dim3(Z * (C / 64) * (P / 32)), dim3(256), 0, L.st, d, idt, ix, idy, cum, bcin, dbx, d1,
                        ddd, ddt, dx, dcum);
   });
   if (rc != ATOMIC_OK) return rc;
