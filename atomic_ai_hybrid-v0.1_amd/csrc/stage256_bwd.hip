@@ -668,53 +668,70 @@ constexpr int MS_PT = 32, MS_RB = 32;
 // The reference chunk's state recurrence (mamba2_ssd_reference.py:125-146):
 // state_end = sanitize(B^T (dBx sanitize(e^{clip(cl - cum, +-20)}, 1e6))),
 // state = sanitize(state e^{clip(cl, -20, 0)} + state_end); the state entering
-// each chunk goes to sprev [B][NT][H][P][N].
+// each chunk goes to sprev [B][NT][H][P][N].  Every chunk's product at once
+// (one workgroup per (batch, head, chunk, 32 channels); thread (channel dd,
+// column group sg) owns state columns sg + 8 k and sums the chunk's rows in
+// order), left unsanitised in sprev; m2s_fwd_pass_k then walks the chunks.
 template <int N>
-__global__ __launch_bounds__(256) void m2s_fwd_k(Mamba2Dims d, In dt, In x, In Bm, const float* __restrict__ cum,
-                                                 const float* __restrict__ state0, float* __restrict__ sprev) {
+__global__ __launch_bounds__(256) void m2s_fwd_se_k(Mamba2Dims d, In dt, In x, In Bm, const float* __restrict__ cum,
+                                                    float* __restrict__ sprev) {
   constexpr int NK = N / 8;
   __shared__ float sW[MS_RB][MS_PT + 1];
   __shared__ float sB[MS_RB][N + 1];
   const int C = d.C, P = d.P, npt = P / MS_PT;
-  const int bh = blockIdx.x / npt, p0 = (blockIdx.x % npt) * MS_PT;
-  const int h = bh % d.H, b = bh / d.H;
+  const size_t z = blockIdx.x / npt;   // (b H + h) NT + n
+  const int p0 = (blockIdx.x % npt) * MS_PT;
+  const int n = (int)(z % d.NT), bh = (int)(z / d.NT), h = bh % d.H, b = bh / d.H;
   const int t = threadIdx.x, dd = t % MS_PT, sg = t / MS_PT;
-  float st[NK];
+  const float* cz = cum + z * C * P;
+  float acc[NK];
 #pragma unroll
-  for (int k = 0; k < NK; ++k)
-    st[k] = state0 ? sanitize(state0[((size_t)bh * P + p0 + dd) * N + sg + 8 * k]) : 0.f;   // :168-170
-  for (int n = 0; n < d.NT; ++n) {
-    const float* cz = cum + ((size_t)bh * d.NT + n) * C * P;
-    float* sp = sprev + ((((size_t)b * d.NT + n) * d.H + h) * P + p0 + dd) * N;
-#pragma unroll
-    for (int k = 0; k < NK; ++k) sp[sg + 8 * k] = st[k];
-    float acc[NK];
-#pragma unroll
-    for (int k = 0; k < NK; ++k) acc[k] = 0.f;
-    for (int r0 = 0; r0 < C; r0 += MS_RB) {
-      for (int e = t; e < MS_RB * MS_PT; e += 256) {
-        const int r = e / MS_PT, c = e % MS_PT;
-        const size_t row = (size_t)b * d.T + (size_t)n * C + r0 + r, col = (size_t)h * P + p0 + c;
-        const float bx = sanitize(ld(dt, row * d.rdt + col) * ld(x, row * d.rx + col));          // :125-126
-        const float raw = cz[(size_t)(C - 1) * P + p0 + c] - cz[(size_t)(r0 + r) * P + p0 + c];
-        const float dte = sanitize(__expf(fminf(fmaxf(raw, -kClipDecay), kClipDecay)), 1e6f);  // :133-134
-        sW[r][c] = bx * dte;                                                                     // :135
-      }
-      for (int e = t; e < MS_RB * N; e += 256) {
-        const int r = e / N, s = e % N;
-        sB[r][s] = ld(Bm, ((size_t)b * d.T + (size_t)n * C + r0 + r) * d.rB + s);
-      }
-      __syncthreads();
-      for (int r = 0; r < MS_RB; ++r) {
-        const float w = sW[r][dd];
-#pragma unroll
-        for (int k = 0; k < NK; ++k) acc[k] = fmaf(w, sB[r][sg + 8 * k], acc[k]);
-      }
-      __syncthreads();
+  for (int k = 0; k < NK; ++k) acc[k] = 0.f;
+  for (int r0 = 0; r0 < C; r0 += MS_RB) {
+    __syncthreads();
+    for (int e = t; e < MS_RB * MS_PT; e += 256) {
+      const int r = e / MS_PT, c = e % MS_PT;
+      const size_t row = (size_t)b * d.T + (size_t)n * C + r0 + r, col = (size_t)h * P + p0 + c;
+      const float bx = sanitize(ld(dt, row * d.rdt + col) * ld(x, row * d.rx + col));          // :125-126
+      const float raw = cz[(size_t)(C - 1) * P + p0 + c] - cz[(size_t)(r0 + r) * P + p0 + c];
+      const float dte = sanitize(__expf(fminf(fmaxf(raw, -kClipDecay), kClipDecay)), 1e6f);  // :133-134
+      sW[r][c] = bx * dte;                                                                     // :135
     }
-    const float dce = __expf(fminf(fmaxf(cz[(size_t)(C - 1) * P + p0 + dd], -kClipDecay), 0.f));   // :144
+    for (int e = t; e < MS_RB * N; e += 256) {
+      const int r = e / N, s = e % N;
+      sB[r][s] = ld(Bm, ((size_t)b * d.T + (size_t)n * C + r0 + r) * d.rB + s);
+    }
+    __syncthreads();
+    for (int r = 0; r < MS_RB; ++r) {
+      const float w = sW[r][dd];
 #pragma unroll
-    for (int k = 0; k < NK; ++k) st[k] = sanitize(st[k] * dce + sanitize(acc[k]));              // :136-137,145-146
+      for (int k = 0; k < NK; ++k) acc[k] = fmaf(w, sB[r][sg + 8 * k], acc[k]);
+    }
+  }
+  float* sp = sprev + ((((size_t)b * d.NT + n) * d.H + h) * P + p0 + dd) * N;
+#pragma unroll
+  for (int k = 0; k < NK; ++k) sp[sg + 8 * k] = acc[k];
+}
+
+// The recurrence itself, one thread per (batch, head, channel, state column),
+// in place: each chunk's product is replaced by the state entering the chunk
+// (state0 sanitised, :168-170).
+__global__ __launch_bounds__(256) void m2s_fwd_pass_k(Mamba2Dims d, const float* __restrict__ cum,
+                                                      const float* __restrict__ state0, float* __restrict__ sprev) {
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t total = (size_t)d.B * d.H * d.P * d.N;
+  if (e >= total) return;
+  const int s = (int)(e % d.N), p = (int)((e / d.N) % d.P);
+  const size_t bh = e / ((size_t)d.P * d.N);
+  const int h = (int)(bh % d.H), b = (int)(bh / d.H);
+  float st = state0 ? sanitize(state0[e]) : 0.f;
+  for (int n = 0; n < d.NT; ++n) {
+    const size_t o = ((((size_t)b * d.NT + n) * d.H + h) * d.P + p) * d.N + s;
+    const float se = sprev[o];
+    sprev[o] = st;
+    const float cl = cum[((bh * d.NT + n) * d.C + d.C - 1) * d.P + p];
+    const float dce = __expf(fminf(fmaxf(cl, -kClipDecay), 0.f));                                  // :144
+    st = sanitize(st * dce + sanitize(se));                                                        // :136-137,145-146
   }
 }
 
@@ -722,94 +739,119 @@ __global__ __launch_bounds__(256) void m2s_fwd_k(Mamba2Dims d, In dt, In x, In B
 // mamba2_bwd_state_reference.py:87-137): per chunk the sanitised carry (MB2's
 // dstate_end_grad, dse [B][H][NT][P][N]), dcum_state [B][H][NT][C][P],
 // dy_off_raw = dy e^{clip(cum, -20, 0)} ([B][T][H][P], for dC), and the next
-// carry sanitize(carry e^{clip(cl, -20, 0)} + dy_off_raw^T C).
+// carry sanitize(carry e^{clip(cl, -20, 0)} + dy_off_raw^T C).  The parts that
+// do not depend on the carry run for every chunk at once (this kernel: dy_off_raw,
+// dcum_state but the last row's carry term, and dy_off_raw^T C unsanitised in
+// dse); m2s_bwd_pass_k walks the chunks and m2s_bwd_last_k adds the last rows'
+// carry term.
 template <int N>
-__global__ __launch_bounds__(256) void m2s_bwd_k(Mamba2Dims d, In Cm, In dy, const float* __restrict__ cum,
-                                                 const float* __restrict__ sprev, const float* __restrict__ dsf,
-                                                 float* __restrict__ dyoff, float* __restrict__ dcum_s,
-                                                 float* __restrict__ dse, float* __restrict__ ds0) {
+__global__ __launch_bounds__(256) void m2s_bwd_par_k(Mamba2Dims d, In Cm, In dy, const float* __restrict__ cum,
+                                                     const float* __restrict__ sprev, float* __restrict__ dyoff,
+                                                     float* __restrict__ dcum_s, float* __restrict__ dse) {
   constexpr int NK = N / 8;
-  __shared__ float sCar[MS_PT][N + 1];
   __shared__ float sSp[MS_PT][N + 1];
   __shared__ float sC[MS_RB][N + 1];
   __shared__ float sDo[MS_RB][MS_PT + 1];
-  __shared__ float sLa[MS_PT];
   const int C = d.C, P = d.P, npt = P / MS_PT;
-  const int bh = blockIdx.x / npt, p0 = (blockIdx.x % npt) * MS_PT;
-  const int h = bh % d.H, b = bh / d.H;
+  const size_t z = blockIdx.x / npt;   // (b H + h) NT + n
+  const int p0 = (blockIdx.x % npt) * MS_PT;
+  const int n = (int)(z % d.NT), bh = (int)(z / d.NT), h = bh % d.H, b = bh / d.H;
   const int t = threadIdx.x, dd = t % MS_PT, sg = t / MS_PT;
+  const float* cz = cum + z * C * P;
 #pragma unroll
-  for (int k = 0; k < NK; ++k)
-    sCar[dd][sg + 8 * k] = dsf ? dsf[((size_t)bh * P + p0 + dd) * N + sg + 8 * k] : 0.f;
-  for (int n = d.NT - 1; n >= 0; --n) {
-    const size_t z = (size_t)bh * d.NT + n;
-    const float* cz = cum + z * C * P;
+  for (int k = 0; k < NK; ++k) {
+    const int s = sg + 8 * k;
+    sSp[dd][s] = sprev[((((size_t)b * d.NT + n) * d.H + h) * P + p0 + dd) * N + s];
+  }
+  float acc[NK];
 #pragma unroll
-    for (int k = 0; k < NK; ++k) {
-      const int s = sg + 8 * k;
-      const float c = sanitize(sCar[dd][s]);                                              // :208
-      sCar[dd][s] = c;
-      dse[(z * P + p0 + dd) * N + s] = c;                                                 // :216,230-231
-      sSp[dd][s] = sprev[((((size_t)b * d.NT + n) * d.H + h) * P + p0 + dd) * N + s];
+  for (int k = 0; k < NK; ++k) acc[k] = 0.f;
+  for (int r0 = 0; r0 < C; r0 += MS_RB) {
+    __syncthreads();
+    for (int e = t; e < MS_RB * N; e += 256) {
+      const int r = e / N, s = e % N;
+      sC[r][s] = ld(Cm, ((size_t)b * d.T + (size_t)n * C + r0 + r) * d.rC + s);
+    }
+    for (int e = t; e < MS_RB * MS_PT; e += 256) {
+      const int r = e / MS_PT, c = e % MS_PT;
+      const size_t row = (size_t)b * d.T + (size_t)n * C + r0 + r, col = (size_t)h * P + p0 + c;
+      const float dh = __expf(fminf(fmaxf(cz[(size_t)(r0 + r) * P + p0 + c], -kClipDecay), 0.f));   // :103-104
+      const float v = ld(dy, row * d.rdy + col) * dh;                                   // :117
+      sDo[r][c] = v;
+      dyoff[row * (size_t)d.H * P + col] = v;
     }
     __syncthreads();
-    if (t < MS_PT) {  // d_cumdecay_last_a (:113-114)
-      float a = 0.f;
-      for (int s = 0; s < N; ++s) a = fmaf(sCar[t][s], sSp[t][s], a);
-      const float cl = cz[(size_t)(C - 1) * P + p0 + t];
-      const float dce = __expf(fminf(fmaxf(cl, -kClipDecay), 0.f));
-      sLa[t] = a * dce * ((cl >= -kClipDecay && cl <= 0.f) ? 1.f : 0.f);
+    for (int e = t; e < MS_RB * MS_PT; e += 256) {  // dcum_state of the piece (:118,123-127)
+      const int r = e / MS_PT, c = e % MS_PT;
+      float y = 0.f;
+      for (int s = 0; s < N; ++s) y = fmaf(sC[r][s], sSp[c][s], y);                     // y_off_raw (:105)
+      const size_t row = (size_t)b * d.T + (size_t)n * C + r0 + r, col = (size_t)h * P + p0 + c;
+      const float cv = cz[(size_t)(r0 + r) * P + p0 + c];
+      const float dhr = fminf(fmaxf(cv, -kClipDecay), 0.f);
+      const float dh = __expf(dhr);
+      // the reference masks on the clipped exponent (:123-124), not on cum
+      // as MB0 does (mamba2_bwd_reference.py:131), so every cum passes
+      const float m = (dhr >= -kClipDecay && dhr <= 0.f) ? 1.f : 0.f;
+      const float v = ld(dy, row * d.rdy + col) * y * dh * m;
+      // the last row waits for its carry term (m2s_bwd_last_k)
+      dcum_s[(z * C + r0 + r) * P + p0 + c] = r0 + r == C - 1 ? v : sanitize(v);          // :131
     }
-    float acc[NK];
+    for (int r = 0; r < MS_RB; ++r) {  // dy_off_raw^T C (:120)
+      const float v = sDo[r][dd];
 #pragma unroll
-    for (int k = 0; k < NK; ++k) acc[k] = 0.f;
-    for (int r0 = 0; r0 < C; r0 += MS_RB) {
-      for (int e = t; e < MS_RB * N; e += 256) {
-        const int r = e / N, s = e % N;
-        sC[r][s] = ld(Cm, ((size_t)b * d.T + (size_t)n * C + r0 + r) * d.rC + s);
-      }
-      for (int e = t; e < MS_RB * MS_PT; e += 256) {
-        const int r = e / MS_PT, c = e % MS_PT;
-        const size_t row = (size_t)b * d.T + (size_t)n * C + r0 + r, col = (size_t)h * P + p0 + c;
-        const float dh = __expf(fminf(fmaxf(cz[(size_t)(r0 + r) * P + p0 + c], -kClipDecay), 0.f));   // :103-104
-        const float v = ld(dy, row * d.rdy + col) * dh;                                   // :117
-        sDo[r][c] = v;
-        dyoff[row * (size_t)d.H * P + col] = v;
-      }
-      __syncthreads();
-      for (int e = t; e < MS_RB * MS_PT; e += 256) {  // dcum_state of the piece (:118,123-127)
-        const int r = e / MS_PT, c = e % MS_PT;
-        float y = 0.f;
-        for (int s = 0; s < N; ++s) y = fmaf(sC[r][s], sSp[c][s], y);                     // y_off_raw (:105)
-        const size_t row = (size_t)b * d.T + (size_t)n * C + r0 + r, col = (size_t)h * P + p0 + c;
-        const float cv = cz[(size_t)(r0 + r) * P + p0 + c];
-        const float dhr = fminf(fmaxf(cv, -kClipDecay), 0.f);
-        const float dh = __expf(dhr);
-        // the reference masks on the clipped exponent (:123-124), not on cum
-        // as MB0 does (mamba2_bwd_reference.py:131), so every cum passes
-        const float m = (dhr >= -kClipDecay && dhr <= 0.f) ? 1.f : 0.f;
-        float v = ld(dy, row * d.rdy + col) * y * dh * m;
-        if (r0 + r == C - 1) v = v + sLa[c];
-        dcum_s[(z * C + r0 + r) * P + p0 + c] = sanitize(v);                               // :131
-      }
-      for (int r = 0; r < MS_RB; ++r) {  // dy_off_raw^T C (:120)
-        const float v = sDo[r][dd];
-#pragma unroll
-        for (int k = 0; k < NK; ++k) acc[k] = fmaf(v, sC[r][sg + 8 * k], acc[k]);
-      }
-      __syncthreads();
+      for (int k = 0; k < NK; ++k) acc[k] = fmaf(v, sC[r][sg + 8 * k], acc[k]);
     }
-    const float dce = __expf(fminf(fmaxf(cz[(size_t)(C - 1) * P + p0 + dd], -kClipDecay), 0.f));
-#pragma unroll
-    for (int k = 0; k < NK; ++k) {
-      const int s = sg + 8 * k;
-      sCar[dd][s] = sanitize(sCar[dd][s] * dce + acc[k]);                                 // :112,120,130
-    }
-    __syncthreads();
   }
 #pragma unroll
-  for (int k = 0; k < NK; ++k)
-    ds0[((size_t)bh * P + p0 + dd) * N + sg + 8 * k] = sanitize(sCar[dd][sg + 8 * k]);    // :219
+  for (int k = 0; k < NK; ++k) dse[(z * P + p0 + dd) * N + sg + 8 * k] = acc[k];
+}
+
+// The carries, one thread per (batch, head, channel, state column), reverse
+// over the chunks and in place: each chunk's dy_off_raw^T C is replaced by the
+// sanitised carry entering its backward (:208,216), and the carry becomes
+// sanitize(carry e^{clip(cl, -20, 0)} + dy_off_raw^T C) (:112,120,130).
+__global__ __launch_bounds__(256) void m2s_bwd_pass_k(Mamba2Dims d, const float* __restrict__ cum,
+                                                      const float* __restrict__ dsf, float* __restrict__ dse,
+                                                      float* __restrict__ ds0) {
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t total = (size_t)d.B * d.H * d.P * d.N;
+  if (e >= total) return;
+  const int s = (int)(e % d.N), p = (int)((e / d.N) % d.P);
+  const size_t bh = e / ((size_t)d.P * d.N);
+  float car = dsf ? dsf[e] : 0.f;
+  for (int n = d.NT - 1; n >= 0; --n) {
+    const size_t z = bh * d.NT + n;
+    const size_t o = (z * d.P + p) * d.N + s;
+    const float acc = dse[o];
+    const float c = sanitize(car);
+    dse[o] = c;
+    const float dce = __expf(fminf(fmaxf(cum[(z * d.C + d.C - 1) * d.P + p], -kClipDecay), 0.f));
+    car = sanitize(c * dce + acc);
+  }
+  ds0[e] = sanitize(car);                                                                 // :219
+}
+
+// The last row's carry term d_cumdecay_last_a = (carry . state_prev) e^{cl}
+// masked on cl (:113-114), one thread per (batch, head, chunk, channel).
+__global__ __launch_bounds__(256) void m2s_bwd_last_k(Mamba2Dims d, const float* __restrict__ cum,
+                                                      const float* __restrict__ sprev, const float* __restrict__ dse,
+                                                      float* __restrict__ dcum_s) {
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t total = (size_t)d.B * d.H * d.NT * d.P;
+  if (e >= total) return;
+  const int p = (int)(e % d.P);
+  const size_t z = e / d.P;
+  const int n = (int)(z % d.NT);
+  const size_t bh = z / d.NT;
+  const int h = (int)(bh % d.H), b = (int)(bh / d.H);
+  const float* car = dse + (z * d.P + p) * d.N;
+  const float* sp = sprev + ((((size_t)b * d.NT + n) * d.H + h) * d.P + p) * d.N;
+  float a = 0.f;
+  for (int s = 0; s < d.N; ++s) a = fmaf(car[s], sp[s], a);
+  const size_t o = (z * d.C + d.C - 1) * d.P + p;
+  const float cl = cum[o];
+  const float dce = __expf(fminf(fmaxf(cl, -kClipDecay), 0.f));
+  dcum_s[o] = sanitize(dcum_s[o] + a * dce * ((cl >= -kClipDecay && cl <= 0.f) ? 1.f : 0.f));
 }
 
 // MB3's sums (kernel_mamba2_bwd_b1_state.py:249-256), in place on MB2's outputs.
@@ -1163,21 +1205,33 @@ int m_bwd_scan(const Mamba2Dims& d, int dtype, int dy_dtype, const void* dt, con
   float* wmb2 = dse + Z * P * N;
   const int bf = dtype == ATOMIC_BF16;
   const In idt{dt, bf}, ix{x, bf}, iB{Bm, bf}, iC{Cm, bf}, idy{dy, dy_dtype == ATOMIC_BF16};
-  const dim3 grid((unsigned)(d.B * d.H * (P / MS_PT)));
+  const dim3 grid((unsigned)(Z * (P / MS_PT)));
+  const size_t nst = (size_t)d.B * d.H * P * N, nlast = Z * P;
+  const dim3 gst((unsigned)((nst + 255) / 256)), glast((unsigned)((nlast + 255) / 256));
   int rc = L("m2s_fwd", [&] {
     if (N == 128)
-      hipLaunchKernelGGL((m2s_fwd_k<128>), grid, dim3(256), 0, L.st, d, idt, ix, iB, cum, state0, sprev);
+      hipLaunchKernelGGL((m2s_fwd_se_k<128>), grid, dim3(256), 0, L.st, d, idt, ix, iB, cum, sprev);
     else
-      hipLaunchKernelGGL((m2s_fwd_k<64>), grid, dim3(256), 0, L.st, d, idt, ix, iB, cum, state0, sprev);
+      hipLaunchKernelGGL((m2s_fwd_se_k<64>), grid, dim3(256), 0, L.st, d, idt, ix, iB, cum, sprev);
+  });
+  if (rc != ATOMIC_OK) return rc;
+  rc = L("m2s_fwd_pass", [&] {
+    hipLaunchKernelGGL(m2s_fwd_pass_k, gst, dim3(256), 0, L.st, d, cum, state0, sprev);
   });
   if (rc != ATOMIC_OK) return rc;
   rc = L("m2s_bwd", [&] {
     if (N == 128)
-      hipLaunchKernelGGL((m2s_bwd_k<128>), grid, dim3(256), 0, L.st, d, iC, idy, cum, sprev, dsf, dyoff, dcum_s,
-                         dse, ds0);
+      hipLaunchKernelGGL((m2s_bwd_par_k<128>), grid, dim3(256), 0, L.st, d, iC, idy, cum, sprev, dyoff, dcum_s, dse);
     else
-      hipLaunchKernelGGL((m2s_bwd_k<64>), grid, dim3(256), 0, L.st, d, iC, idy, cum, sprev, dsf, dyoff, dcum_s, dse,
-                         ds0);
+      hipLaunchKernelGGL((m2s_bwd_par_k<64>), grid, dim3(256), 0, L.st, d, iC, idy, cum, sprev, dyoff, dcum_s, dse);
+  });
+  if (rc != ATOMIC_OK) return rc;
+  rc = L("m2s_bwd_pass", [&] {
+    hipLaunchKernelGGL(m2s_bwd_pass_k, gst, dim3(256), 0, L.st, d, cum, dsf, dse, ds0);
+  });
+  if (rc != ATOMIC_OK) return rc;
+  rc = L("m2s_bwd_last", [&] {
+    hipLaunchKernelGGL(m2s_bwd_last_k, glast, dim3(256), 0, L.st, d, cum, sprev, dse, dcum_s);
   });
   if (rc != ATOMIC_OK) return rc;
   // dC_state = sanitize(dy_off_raw C-rows x state_prev over (head, channel)) per (batch, chunk)   (:119,129)
