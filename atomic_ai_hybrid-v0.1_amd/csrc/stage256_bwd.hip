@@ -832,22 +832,38 @@ __global__ __launch_bounds__(256) void m2s_bwd_pass_k(Mamba2Dims d, const float*
 }
 
 // The last row's carry term d_cumdecay_last_a = (carry . state_prev) e^{cl}
-// masked on cl (:113-114), one thread per (batch, head, chunk, channel).
+// masked on cl (:113-114), for 32 (batch, head, chunk, channel) rows per
+// workgroup: their carry and state rows are staged through LDS (coalesced)
+// and each row's dot product runs in state-column order.
 __global__ __launch_bounds__(256) void m2s_bwd_last_k(Mamba2Dims d, const float* __restrict__ cum,
                                                       const float* __restrict__ sprev, const float* __restrict__ dse,
                                                       float* __restrict__ dcum_s) {
-  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  constexpr int RW = 32, MAXN = 128;
+  __shared__ float sA[RW][MAXN + 1], sS[RW][MAXN + 1];
   const size_t total = (size_t)d.B * d.H * d.NT * d.P;
-  if (e >= total) return;
-  const int p = (int)(e % d.P);
-  const size_t z = e / d.P;
-  const int n = (int)(z % d.NT);
-  const size_t bh = z / d.NT;
-  const int h = (int)(bh % d.H), b = (int)(bh / d.H);
-  const float* car = dse + (z * d.P + p) * d.N;
-  const float* sp = sprev + ((((size_t)b * d.NT + n) * d.H + h) * d.P + p) * d.N;
+  const size_t e0 = (size_t)blockIdx.x * RW;
+  const int N = d.N;
+  for (int e = threadIdx.x; e < RW * N; e += 256) {
+    const int rr = e / N, s = e % N;
+    const size_t er = e0 + rr;
+    if (er < total) {
+      const int p = (int)(er % d.P);
+      const size_t z = er / d.P;
+      const int n = (int)(z % d.NT);
+      const size_t bh = z / d.NT;
+      const int h = (int)(bh % d.H), b = (int)(bh / d.H);
+      sA[rr][s] = dse[(z * d.P + p) * N + s];
+      sS[rr][s] = sprev[((((size_t)b * d.NT + n) * d.H + h) * d.P + p) * N + s];
+    }
+  }
+  __syncthreads();
+  const int rr = threadIdx.x;
+  if (rr >= RW || e0 + rr >= total) return;
+  const size_t er = e0 + rr;
+  const int p = (int)(er % d.P);
+  const size_t z = er / d.P;
   float a = 0.f;
-  for (int s = 0; s < d.N; ++s) a = fmaf(car[s], sp[s], a);
+  for (int s = 0; s < N; ++s) a = fmaf(sA[rr][s], sS[rr][s], a);
   const size_t o = (z * d.C + d.C - 1) * d.P + p;
   const float cl = cum[o];
   const float dce = __expf(fminf(fmaxf(cl, -kClipDecay), 0.f));
@@ -1207,7 +1223,7 @@ int m_bwd_scan(const Mamba2Dims& d, int dtype, int dy_dtype, const void* dt, con
   const In idt{dt, bf}, ix{x, bf}, iB{Bm, bf}, iC{Cm, bf}, idy{dy, dy_dtype == ATOMIC_BF16};
   const dim3 grid((unsigned)(Z * (P / MS_PT)));
   const size_t nst = (size_t)d.B * d.H * P * N, nlast = Z * P;
-  const dim3 gst((unsigned)((nst + 255) / 256)), glast((unsigned)((nlast + 255) / 256));
+  const dim3 gst((unsigned)((nst + 255) / 256)), glast((unsigned)((nlast + 31) / 32));
   int rc = L("m2s_fwd", [&] {
     if (N == 128)
       hipLaunchKernelGGL((m2s_fwd_se_k<128>), grid, dim3(256), 0, L.st, d, idt, ix, iB, cum, sprev);
