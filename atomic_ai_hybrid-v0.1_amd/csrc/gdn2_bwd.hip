@@ -290,30 +290,34 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
 // ------------------------------------------------------------------ B2/B3 state terms
 // One workgroup per (batch, head, chunk).  dO, dv_new and v_new stay in LDS;
-// h_pre and dh_next pass through in KQ-column quarters (the next quarter is
-// loaded into registers while the current one computes), which keeps the LDS
-// at two workgroups per CU.
-template <typename T, int C, int KQ, int V>
+// h_pre and dh_next ([V][K] per chunk) pass through in quarters of VQ whole
+// rows (contiguous blocks, so every cache line is fetched once), the next
+// quarter loaded into registers while the current one computes.  dqg, dw~ and
+// dkg accumulate over the quarters in MFMA registers (wave w owns row blocks
+// w, w + 4, ...) and are written once, whole rows at a time.
+template <typename T, int C, int VQ, int K, int V>
 struct HgLds {
   static constexpr int PAD = Pad<T>::v;
-  // bf16 h_pre / dh_next quarter rows unpadded (64 bytes): they are read only
-  // by transposed fragment reads (4 rows of 32 bytes per 16 lanes, on
-  // distinct banks at this pitch, not at 80 bytes) and by the row term
-  static constexpr int LK = KQ + (sizeof(T) == 2 ? 0 : PAD), LV = V + PAD, LC = C + PAD;
+  // quarter rows padded by 16 elements: the transposed fragment reads of 16
+  // lanes (4 rows, 32 bytes each at bf16) then land on distinct banks
+  static constexpr int LK = K + 16, LV = V + PAD, LC = C + PAD;
   static constexpr int off_do = 0;
   static constexpr int off_dv = off_do + C * LV * (int)sizeof(T);
   static constexpr int off_vn = off_dv + C * LV * (int)sizeof(T);
   static constexpr int off_h = off_vn + V * LC * (int)sizeof(T);
-  static constexpr int off_dh = off_h + V * LK * (int)sizeof(T);
-  static constexpr int off_red = off_dh + V * LK * (int)sizeof(T);
-  static constexpr int total = off_red + 512 * 4;  // row-term partials [16][KQ]
+  static constexpr int off_dh = off_h + VQ * LK * (int)sizeof(T);
+  static constexpr int total = off_dh + VQ * LK * (int)sizeof(T);
+  // row-term partials [16][K] over the quarter buffers, after the last quarter
+  static constexpr int off_red = off_h;
+  static_assert(16 * K * 4 <= 2 * VQ * LK * (int)sizeof(T), "row-term partials fit the quarter buffers");
 };
 
 template <typename T, typename TD, int C, int K, int V>
 __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T> ck, Gdn2Grads<T> gr,
                                                      const TD* __restrict__ dO) {
-  constexpr int KQ = 32;
-  typedef HgLds<T, C, KQ, V> L;
+  constexpr int VQ = 32, NQ = V / VQ;
+  static_assert(V % VQ == 0 && VQ % Mma<T>::KS == 0, "V splits into whole quarters");
+  typedef HgLds<T, C, VQ, K, V> L;
   __shared__ __attribute__((aligned(16))) unsigned char lds[L::total];
   T* sDO = reinterpret_cast<T*>(lds + L::off_do);
   T* sDV = reinterpret_cast<T*>(lds + L::off_dv);
@@ -332,7 +336,7 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
   const T* dhg = gr.dhT + blk * V * K;
 
   // every operand is requested before the first LDS store
-  RegStage<T, V, KQ> ph, pdh;
+  RegStage<T, VQ, K> ph, pdh;
   RegStage<TD, C, V> pdo;
   RegStage<T, C, V> pdv;
   RegStage<T, V, C> pvn;
@@ -363,63 +367,97 @@ __global__ __launch_bounds__(256) void gdn2_bwd_hgrad(Gdn2Dims dm, Gdn2Chunks<T>
     store_tile_n(g_daqk, C, 16 * mi, 16 * nj, acc);
   }
 
-  // dqg = scale dO h_pre^T ; dwt = -dv_new h_pre^T ; dkg = v_new dh_next^T, per quarter
-  constexpr int NTQ = KQ / 16, TPW = MT * NTQ / 4;
-  static_assert((MT * NTQ) % 4 == 0, "tiles must split evenly over 4 waves");
-  // gc_last row term: a thread takes a column pair and every SPL-th row;
-  // consecutive lanes take consecutive column pairs, so a wave's 4-byte
-  // reads cover four whole rows
-  constexpr int CPQ = KQ / 2, SPL = 256 / CPQ, VS = V / SPL;
-  static_assert(SPL * KQ <= 512 && V % SPL == 0, "row-term partials fit their LDS");
-  for (int c0 = 0; c0 < K; c0 += KQ) {
-    if (c0 + KQ < K) {
-      ph.load(hg + c0 + KQ, K);
-      pdh.load(dhg + c0 + KQ, K);
-    }
-    T* g_dqg = gr.dqg + blk * C * K + c0;
-    T* g_dwt = gr.dwt + blk * C * K + c0;
-    T* g_dkg = gr.dkg + blk * C * K + c0;
+  // dqg = scale dO h_pre^T ; dwt = -dv_new h_pre^T ; dkg = v_new dh_next^T:
+  // each sum over v runs quarter by quarter in ascending v, as one sum would
+  constexpr int RB = MT / 4, NT = K / 16;
+  static_assert(MT % 4 == 0, "row blocks split evenly over 4 waves");
+  f32x4 aq[RB][NT], aw[RB][NT], ak[RB][NT];
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-      const int tile = wv_id * TPW + t, mi = tile % MT, ni = tile / MT;
-      f32x4 a = tile_mma<T, false, true>(zero4(), sDO, L::LV, sH, L::LK, 16 * mi, 16 * ni, V);
-      f32x4 b = tile_mma<T, false, true>(zero4(), sDV, L::LV, sH, L::LK, 16 * mi, 16 * ni, V);
-      f32x4 c = tile_mma<T, true, true>(zero4(), sVn, L::LC, sDh, L::LK, 16 * mi, 16 * ni, V);
+  for (int r = 0; r < RB; ++r)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) { a[i] *= dm.scale; b[i] = -b[i]; }
-      store_tile_n(g_dqg, K, 16 * mi, 16 * ni, a);
-      store_tile_n(g_dwt, K, 16 * mi, 16 * ni, b);
-      store_tile_n(g_dkg, K, 16 * mi, 16 * ni, c);
+    for (int t = 0; t < NT; ++t) aq[r][t] = aw[r][t] = ak[r][t] = zero4();
+  // gc_last row term sum_v dh_next * h_pre: partial sums over the rows
+  // v = j (mod 16), j = 0..15, each in ascending v, then summed over j.  A
+  // thread takes a column pair and GPT of the residues j; consecutive lanes
+  // take consecutive column pairs.
+  constexpr int CP = K / 2, TG = 256 / CP, GPT = 16 / TG;
+  static_assert(256 % CP == 0 && 16 % TG == 0 && VQ % 16 == 0, "row-term split");
+  const int d = 2 * (threadIdx.x % CP), tg = threadIdx.x / CP;
+  float rs[GPT][2];
+#pragma unroll
+  for (int j = 0; j < GPT; ++j) rs[j][0] = rs[j][1] = 0.f;
+  for (int q = 0; q < NQ; ++q) {
+    if (q + 1 < NQ) {
+      ph.load(hg + (size_t)(q + 1) * VQ * K, K);
+      pdh.load(dhg + (size_t)(q + 1) * VQ * K, K);
     }
-    // exp(gc_last) * sum_v dh_next * h_pre   (kernel_bwd_b3_wy_dqkg.py:200-201)
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int m0 = 16 * (wv_id + 4 * r);
+#pragma unroll
+      for (int k0 = 0; k0 < VQ; k0 += Mma<T>::KS) {
+        const typename Mma<T>::frag fo = Mma<T>::ld_c(sDO, L::LV, m0, q * VQ + k0);
+        const typename Mma<T>::frag fv = Mma<T>::ld_c(sDV, L::LV, m0, q * VQ + k0);
+        const typename Mma<T>::frag fn = Mma<T>::ld_t(sVn, L::LC, m0, q * VQ + k0);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const typename Mma<T>::frag bh_ = Mma<T>::ld_t(sH, L::LK, 16 * t, k0);
+          const typename Mma<T>::frag bd = Mma<T>::ld_t(sDh, L::LK, 16 * t, k0);
+          aq[r][t] = Mma<T>::mma(fo, bh_, aq[r][t]);
+          aw[r][t] = Mma<T>::mma(fv, bh_, aw[r][t]);
+          ak[r][t] = Mma<T>::mma(fn, bd, ak[r][t]);
+        }
+      }
+    }
     {
       typedef T T2 __attribute__((ext_vector_type(2)));
-      const int sp = threadIdx.x / CPQ, d = 2 * (threadIdx.x % CPQ);
-      float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-      for (int t = 0; t < VS; ++t) {
-        const int v = sp + SPL * t;
-        const T2 a = *reinterpret_cast<const T2*>(sDh + v * L::LK + d);
-        const T2 c = *reinterpret_cast<const T2*>(sH + v * L::LK + d);
-        s0 += to_f(a[0]) * to_f(c[0]);
-        s1 += to_f(a[1]) * to_f(c[1]);
+      for (int jj = 0; jj < GPT; ++jj) {
+#pragma unroll
+        for (int u = 0; u < VQ / 16; ++u) {
+          const int v = tg * GPT + jj + 16 * u;
+          const T2 a = *reinterpret_cast<const T2*>(sDh + v * L::LK + d);
+          const T2 c = *reinterpret_cast<const T2*>(sH + v * L::LK + d);
+          rs[jj][0] += to_f(a[0]) * to_f(c[0]);
+          rs[jj][1] += to_f(a[1]) * to_f(c[1]);
+        }
       }
-      red[sp * KQ + d] = s0;
-      red[sp * KQ + d + 1] = s1;
     }
-    __syncthreads();  // quarter done: its h / dh and the partial sums are read
-    if (threadIdx.x < KQ) {
-      const int d = threadIdx.x;
-      float s = 0.f;
-#pragma unroll
-      for (int j = 0; j < SPL; ++j) s += red[j * KQ + d];
-      gr.rlast[blk * K + c0 + d] = __expf(ck.gcl[blk * K + c0 + d]) * s;
-    }
-    if (c0 + KQ < K) {
+    __syncthreads();  // the quarter's h / dh are read
+    if (q + 1 < NQ) {
       ph.store(sH, L::LK);
       pdh.store(sDh, L::LK);
+      __syncthreads();
     }
-    __syncthreads();
+  }
+  T* g_dqg = gr.dqg + blk * C * K;
+  T* g_dwt = gr.dwt + blk * C * K;
+  T* g_dkg = gr.dkg + blk * C * K;
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const int m0 = 16 * (wv_id + 4 * r);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 a = aq[r][t], b = aw[r][t];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { a[i] *= dm.scale; b[i] = -b[i]; }
+      store_tile_n(g_dqg, K, m0, 16 * t, a);
+      store_tile_n(g_dwt, K, m0, 16 * t, b);
+      store_tile_n(g_dkg, K, m0, 16 * t, ak[r][t]);
+    }
+  }
+  // exp(gc_last) * sum_v dh_next * h_pre   (kernel_bwd_b3_wy_dqkg.py:200-201)
+#pragma unroll
+  for (int jj = 0; jj < GPT; ++jj) {
+    red[(tg * GPT + jj) * K + d] = rs[jj][0];
+    red[(tg * GPT + jj) * K + d + 1] = rs[jj][1];
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < K; c += 256) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s += red[j * K + c];
+    gr.rlast[blk * K + c] = __expf(ck.gcl[blk * K + c]) * s;
   }
 }
 

@@ -310,7 +310,7 @@ int gdn2_backward(const Gdn2Plan& p, int dtype, int do_dtype, const void* q, con
     AH_GDN2_BWD(bf16, float, 64);
   }
   // fp32 operands: at K = 128 every backward kernel fits the LDS at one
-  // workgroup per CU (gdn2_bwd_dh 160 KB, gdn2_bwd_hgrad 138 KB)
+  // workgroup per CU (gdn2_bwd_dh 160 KB, gdn2_bwd_hgrad 136 KB)
   if (p.dm.K == 128) {
     if (do_dtype == ATOMIC_BF16) AH_GDN2_BWD(float, bf16, 128);
     AH_GDN2_BWD(float, float, 128);
