@@ -875,7 +875,9 @@ __global__ __launch_bounds__(256) void m2s_comb_k(size_t nhp, size_t nn, size_t 
                                                   float* __restrict__ dx, float* __restrict__ dB,
                                                   float* __restrict__ dC, const float* __restrict__ dC_s,
                                                   float* __restrict__ dcum, const float* __restrict__ dcum_s) {
-  const size_t top = nhp > ncum ? nhp : ncum;
+  // the loop covers the longest of the three ranges (dB / dC is the longest
+  // when the state size exceeds heads x channels)
+  const size_t top = nhp > ncum ? (nhp > nn ? nhp : nn) : (ncum > nn ? ncum : nn);
   for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < top; e += (size_t)gridDim.x * 256) {
     if (e < nhp) {
       ddt[e] = sanitize(ddt[e]);
@@ -1262,7 +1264,7 @@ int m_bwd_scan(const Mamba2Dims& d, int dtype, int dy_dtype, const void* dt, con
   // MB2 with the carries as dstate_end_grad (:240-243)
   if ((rc = m_intra_bwd(d, dtype, dy_dtype, dt, x, Bm, Cm, cum, dy, dse, ddt, dx, dB, dC, dcum, wmb2, L))) return rc;
   const size_t nhp = (size_t)d.B * d.T * d.H * P, nn = (size_t)d.B * d.T * N, ncum = Z * C * P;
-  const size_t top = nhp > ncum ? nhp : ncum;
+  const size_t top = nhp > ncum ? (nhp > nn ? nhp : nn) : (ncum > nn ? ncum : nn);
   const int eb = (int)((top + 255) / 256 < 65536 ? (top + 255) / 256 : 65536);
   return L("m2s_comb", [&] {
     hipLaunchKernelGGL(m2s_comb_k, dim3(eb), dim3(256), 0, L.st, nhp, nn, ncum, ddt, dx, dB, dC, dC_s, dcum, dcum_s);

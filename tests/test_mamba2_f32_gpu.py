@@ -56,7 +56,10 @@ def _mb0_order(mb0):
 
 
 CASES = [(64, 2, 512, 2, 64, 128), (128, 1, 512, 3, 128, 64), (256, 1, 768, 2, 64, 128),
-         (256, 1, 512, 2, 192, 128)]
+         (256, 1, 512, 2, 192, 128),
+         # a state size above heads x channels (N > H P): the dC / dB arrays are
+         # the longest of the backward's final element-wise pass
+         (128, 2, 512, 1, 64, 128), (256, 2, 512, 1, 64, 128)]
 
 
 @pytest.mark.parametrize("C,b,l,h,P,N", CASES)
