@@ -234,12 +234,14 @@ def intra_chunk_ssd_loops(dt, x, Bm, Cm, cumdecay, chunk_size):
     return y, se
 
 
-def chunk_ssd_bwd(dt_c, A, B_c, C_c, x_c, state_prev, dy_c, dstate_new, dtype=torch.float64):
+def chunk_ssd_bwd(dt_c, A, B_c, C_c, x_c, state_prev, dy_c, dstate_new, dtype=torch.float64, cb_round=None):
     """Hand-derived backward of one chunk: MB0 ``_chunk_ssd_bwd``
     (mamba2_bwd_reference.py:55-197).  Returns
     ``(ddt_c, dB_c, dC_c, dx_c, dA, dstate_prev, dcum_total)``; the last one
     (the combined cumdecay cotangent after the last-row terms) is exposed for
-    kernel-level tests."""
+    kernel-level tests.  ``cb_round`` (a torch dtype; tests only) rounds the
+    C.B^T scores to that type, which emulates a kernel that stages them at
+    that precision; the reference keeps them float32."""
     f = dtype
     dt_c, B_c, C_c, x_c, state_prev = (t.to(f) for t in (dt_c, B_c, C_c, x_c, state_prev))
     dy_c = dy_c.to(f)
@@ -257,6 +259,8 @@ def chunk_ssd_bwd(dt_c, A, B_c, C_c, x_c, state_prev, dy_c, dstate_new, dtype=to
     causal = (idx[:, None] >= idx[None, :]).to(f)[None, :, :, None, None]
     L = sanitize(torch.exp(torch.clamp(decay_diff_raw, -CLIP_STEP, CLIP_STEP)) * causal, 1e6)
     BC_inner = sanitize(torch.einsum("bis,bjs->bij", C_c, B_c))
+    if cb_round is not None:
+        BC_inner = BC_inner.to(cb_round).to(f)
     dBx = sanitize(dt_c * x_c)
     weight = L * BC_inner[:, :, :, None, None]
     decay_to_end_raw = cumdecay[:, -1:] - cumdecay
@@ -315,10 +319,10 @@ def chunk_ssd_bwd(dt_c, A, B_c, C_c, x_c, state_prev, dy_c, dstate_new, dtype=to
 
 
 def chunk_ssd_bwd_scan(dt, A, Bm, Cm, x, chunk_size, do, dstate_final=None, state0=None,
-                       dtype=torch.float64):
+                       dtype=torch.float64, cb_round=None):
     """Full-sequence MB0 backward (mamba2_bwd_reference.py:200-266): forward
     re-run for ``state_prev`` per chunk, then a reverse scan.  Returns
-    ``(ddt, dB, dC, dx, dA, dstate0)``."""
+    ``(ddt, dB, dC, dx, dA, dstate0)``.  ``cb_round``: see chunk_ssd_bwd."""
     f = dtype
     b, l, h, p = dt.shape
     n = Bm.shape[-1]
@@ -334,7 +338,7 @@ def chunk_ssd_bwd_scan(dt, A, Bm, Cm, x, chunk_size, do, dstate_final=None, stat
     dA = torch.zeros(h, dtype=f)
     for c in reversed(range(nc)):                                                     # :236-247
         ddt_c, dB_c, dC_c, dx_c, dA_c, dstate, _ = chunk_ssd_bwd(
-            dtc[c], A, Bc[c], Cc[c], xc[c], prevs[c], doc[c], dstate, dtype=f)
+            dtc[c], A, Bc[c], Cc[c], xc[c], prevs[c], doc[c], dstate, dtype=f, cb_round=cb_round)
         outs[c] = (ddt_c, dB_c, dC_c, dx_c)
         dA = dA + dA_c                                                                # :263
     ddt, dB, dC, dx = (_from_chunks(torch.stack([o[i] for o in outs], 0)) for i in range(4))
