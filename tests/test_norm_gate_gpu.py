@@ -31,6 +31,8 @@ def _inputs(rows, d, seed, gate_scale):
     (9, 8192, 3.0),      # the largest supported dimension (a workgroup per row in the backward)
     (1100, 4096, 3.0),   # the smallest workgroup-per-row width; rows beyond the 512 partial rows
     (13, 6144, 60.0),    # twelve pieces per row: three per wave
+    (300, 1024, 3.0),    # two pieces per lane
+    (129, 3072, 60.0),   # six pieces per lane, one row past a workgroup of four
 ])
 def test_epilogue_matches_oracle(variant, ovar, rows, d, gate_scale):
     banner(f"norm_gate {ovar} rows={rows} d={d} gate_scale={gate_scale}")
