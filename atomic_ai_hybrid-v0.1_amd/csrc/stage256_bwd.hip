@@ -834,7 +834,8 @@ __global__ __launch_bounds__(256) void m2s_bwd_pass_k(Mamba2Dims d, const float*
 // The last row's carry term d_cumdecay_last_a = (carry . state_prev) e^{cl}
 // masked on cl (:113-114), for 32 (batch, head, chunk, channel) rows per
 // workgroup: their carry and state rows are staged through LDS (coalesced)
-// and each row's dot product runs in state-column order.
+// and each row's dot product runs in state-column order.  The rows hold up to
+// MAXN state columns; m_bwd_scan admits N = 64 or 128 only.
 __global__ __launch_bounds__(256) void m2s_bwd_last_k(Mamba2Dims d, const float* __restrict__ cum,
                                                       const float* __restrict__ sprev, const float* __restrict__ dse,
                                                       float* __restrict__ dcum_s) {
